@@ -1,0 +1,347 @@
+/*
+ * lemoq_hip.h — C-ABI of the MI355X (gfx950) kernels behind the lemoq batch-1
+ * OLMoE decode path: w8a16 grouped MoE, w8 dense GEMV, split-KV attention
+ * (fp16 and KV-INT8) with its log-sum-exp merge, RMSNorm, RoPE, router top-k
+ * and the KV write kernels.
+ *
+ * Conventions shared by every entry point:
+ *   - Plain pointers and sizes only.  fp16 data is passed as uint16_t (IEEE
+ *     binary16 bit patterns); int8 codes as int8_t; device scalars that the
+ *     kernels read at run time (positions, filled lengths, expert ids, token
+ *     ids) are device pointers, never host integers, so a captured hipGraph
+ *     stays valid while they change.
+ *   - `stream` is a hipStream_t passed as an opaque pointer (NULL = the null
+ *     stream).  Every call only enqueues work: no host synchronisation, no
+ *     device->host reads, no allocation or free of any memory.  Outputs and
+ *     workspaces are caller-owned.
+ *   - Return value: 0 on success; a negative LEMOQ_ERR_* code when the
+ *     arguments are rejected before anything is launched; a positive value is
+ *     the hipError_t reported by the launch.  lemoq_status_string() names it.
+ *   - All entry points are stateless and reentrant.
+ *
+ * Reference interfaces replaced are cited as path:line into LeanMoE-Quant.
+ */
+#ifndef LEMOQ_HIP_H
+#define LEMOQ_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LEMOQ_ABI_VERSION 1
+
+enum {
+  LEMOQ_OK = 0,
+  LEMOQ_ERR_NULL = -1,        /* a required pointer is NULL                  */
+  LEMOQ_ERR_SHAPE = -2,       /* a size is out of range or inconsistent      */
+  LEMOQ_ERR_UNSUPPORTED = -3, /* a valid request this build does not cover   */
+  LEMOQ_ERR_ALIGN = -4        /* a pointer is not 16-byte aligned            */
+};
+
+/* Human-readable name of a status returned by any lemoq_* call. */
+const char* lemoq_status_string(int status);
+/* LEMOQ_ABI_VERSION of the loaded library. */
+int lemoq_abi_version(void);
+
+/* ---------------------------------------------------------------------------
+ * A2 — per-group symmetric RTN, 8-bit.
+ * Replaces lemoq.quant.rtn.quantize_rtn (src/lemoq/quant/rtn.py:38-99) for
+ * bits=8, symmetric=True, and the fp16 scale cast done by
+ * quantize_fused_experts (src/lemoq/kernels/moe_grouped_quant.py:222-233) and
+ * QuantLinear (src/lemoq/quant/linear.py:332).
+ * w (rows, cols) fp32 row-major; groups of `group` along cols, the last group
+ * zero-padded to padded = ceil(cols/group)*group.  Writes codes (rows, padded)
+ * int8 and, per (row, group), scale_f16 (fp16 of the fp32 scale) and, when
+ * non-NULL, scale_f32.  scale = absmax/127 (1.0 when absmax == 0), codes =
+ * round-half-even(w/scale) clamped to [-128, 127], both in fp32.
+ * ------------------------------------------------------------------------- */
+int lemoq_rtn_quantize_w8(const float* w, int64_t rows, int64_t cols, int64_t group,
+                          int8_t* codes, uint16_t* scale_f16, float* scale_f32,
+                          void* stream);
+
+/* ---------------------------------------------------------------------------
+ * A7/A8/A9 — w8 symmetric dense GEMV (dequant in registers, fp32 accumulate).
+ * Replaces dequant_gemm_fused(x, qweight, scale, None, group_size=g, bits=8,
+ * symmetric=True, out_dtype=...) (src/lemoq/kernels/_dequant_triton.py:155-293,
+ * kernel :313-463), the operator used by QuantLinear._fused_forward
+ * (src/lemoq/quant/linear.py:446-469) and PackedQKV.project
+ * (src/lemoq/kernels/packed_qkv.py:78-96).
+ * x (M, K) fp16 contiguous; codes (N, padded_k) int8; scale (N, padded_k/group)
+ * fp16; y (M, N) fp16 when y_is_f16 else fp32.  K <= padded_k <= 8192,
+ * padded_k % 16 == 0, group % 16 == 0, padded_k % group == 0.
+ * ------------------------------------------------------------------------- */
+int lemoq_gemv_w8(const uint16_t* x, int64_t M, int64_t K,
+                  const int8_t* codes, const uint16_t* scale, int64_t N,
+                  int64_t padded_k, int64_t group, void* y, int y_is_f16,
+                  void* stream);
+
+/* Fused single-token form used by the decode step (no reference counterpart
+ * as one call: it fuses rms_norm_fused (src/lemoq/kernels/rmsnorm.py:102-163)
+ * into the GEMV prologue and the fp16 residual add of the HF decoder layer
+ * (transformers OlmoeDecoderLayer.forward, call site
+ * src/lemoq/kernels/attn_decode.py:1013-1016) into its epilogue).
+ *   x_src:   the input row, or with x_row_index != NULL row *x_row_index of
+ *            the (x_rows, K) table x_src (embedding gather; an index outside
+ *            [0, x_rows) reads as a zero row).
+ *   norm_w:  when non-NULL, x := fp16(fp16(x*rsqrt(mean(x^2)+eps)) * norm_w).
+ *   x_copy:  when non-NULL, block 0 writes the raw (un-normed) input row here.
+ *   residual: when non-NULL, y = fp16(fp16(acc) + residual) (may alias y).
+ * K == padded_k here. */
+int lemoq_gemv_w8_fused(const uint16_t* x_src, const int64_t* x_row_index,
+                        int64_t x_rows, const uint16_t* norm_w, float eps,
+                        uint16_t* x_copy,
+                        const int8_t* codes, const uint16_t* scale, int64_t N,
+                        int64_t K, int64_t group, const uint16_t* residual,
+                        uint16_t* y, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * A4 — grouped MoE gate/up + SiLU, w8.
+ * Replaces _gate_up_act_kernel_q (src/lemoq/kernels/_grouped_triton.py:249-332)
+ * as launched by grouped_moe_forward_quant
+ * (src/lemoq/kernels/moe_grouped_quant.py:473-515).
+ * x (H,) fp16; codes (E, 2F, H) int8 (gate rows [0,F), up rows [F,2F));
+ * scale (E, 2F, H/group) fp16; ids (top_k,) int64 device;
+ * act (top_k, F) fp16 = fp16(silu(gate) * up), fp32 accumulation.
+ * An id outside [0, E) yields a zero row (no out-of-bounds read).
+ * ------------------------------------------------------------------------- */
+int lemoq_moe_gate_up_w8(const uint16_t* x, const int8_t* codes,
+                         const uint16_t* scale, const int64_t* ids,
+                         int64_t top_k, int64_t num_experts, int64_t ffn,
+                         int64_t hidden, int64_t group, uint16_t* act,
+                         void* stream);
+
+/* A5 — grouped MoE down projection x routing weight, summed over the top_k
+ * slots in a fixed order, fp32 accumulation, fp16 output.  Replaces
+ * _down_sum_kernel_q + _out_reduce_kernel
+ * (src/lemoq/kernels/_grouped_triton.py:335-398, :197-211) as launched at
+ * src/lemoq/kernels/moe_grouped_quant.py:517-558.
+ * act (top_k, F) fp16; codes (E, H, F) int8; scale (E, H, F/group) fp16;
+ * ids (top_k,) int64; top_w (top_k,) fp16; out (H,) fp16.
+ * residual (nullable, may alias out): out = fp16(fp16(sum) + residual). */
+int lemoq_moe_down_w8(const uint16_t* act, const int8_t* codes,
+                      const uint16_t* scale, const int64_t* ids,
+                      const uint16_t* top_w, int64_t top_k, int64_t num_experts,
+                      int64_t hidden, int64_t ffn, int64_t group,
+                      const uint16_t* residual, uint16_t* out, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * A14/A15 — split-KV decode attention (flash-decoding), batch 1, q_len 1.
+ * Partials: m, l (heads, num_splits) fp32 and acc (heads, num_splits, D) fp32;
+ * split s of head h covers [s*c, min((s+1)*c, filled)) with
+ * c = ceil(filled/num_splits), filled read from the device int32 *filled.
+ * Scores use exp2 with qk_scale = scale*log2(e); an empty split writes
+ * (m=-inf, l=0, acc=0).  D in {64, 128, 256}.
+ *
+ * fp16 K/V: replaces _attn_split_kernel (src/lemoq/kernels/_attn_triton.py:46-99)
+ * launched by attn_decode_forward (src/lemoq/kernels/attn_decode.py:496-624).
+ * q (heads, D) fp16; k, v: head h, token t at k + h*head_stride + t*D. */
+int lemoq_attn_split_f16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                         int64_t head_stride, const int32_t* filled,
+                         int64_t heads, int64_t head_dim, int64_t num_splits,
+                         float qk_scale, float* m, float* l, float* acc,
+                         void* stream);
+
+/* KV-INT8: replaces _attn_split_kernel_int8 (src/lemoq/kernels/_attn_triton.py:102-165)
+ * launched by attn_decode_forward_int8 (src/lemoq/kernels/attn_decode.py:627-730).
+ * score_t = ((q . c_t) * qk_scale) * ks_t;  acc += sum_t (p_t * vs_t) * cv_t;
+ * l = sum_t p_t (the V scale is not in l).  Codes: kc + h*head_stride + t*D;
+ * scales: ks + h*s_len + t. */
+int lemoq_attn_split_i8(const uint16_t* q, const int8_t* kc, const uint16_t* ks,
+                        const int8_t* vc, const uint16_t* vs, int64_t head_stride,
+                        int64_t s_len, const int32_t* filled, int64_t heads,
+                        int64_t head_dim, int64_t num_splits, float qk_scale,
+                        float* m, float* l, float* acc, void* stream);
+
+/* LSE merge, fixed split order: out = sum_j acc_j 2^(m_j-M) / sum_j l_j 2^(m_j-M),
+ * M = max_j m_j (0 when every split is empty, giving out = 0).  Replaces
+ * _attn_combine_kernel (src/lemoq/kernels/_attn_triton.py:168-206).
+ * out (heads, D) fp16. */
+int lemoq_attn_merge(const float* m, const float* l, const float* acc,
+                     int64_t heads, int64_t num_splits, int64_t head_dim,
+                     uint16_t* out, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * A10 — RMSNorm, HF rounding points: y = fp16(fp16(x*rsqrt(mean(x^2)+eps)) * w).
+ * Replaces rms_norm_fused (src/lemoq/kernels/rmsnorm.py:102-163, kernel
+ * :173-202).  x, y (rows, hidden) fp16 contiguous; w (hidden,) fp16;
+ * hidden <= 8192.
+ * ------------------------------------------------------------------------- */
+int lemoq_rmsnorm(const uint16_t* x, int64_t rows, int64_t hidden,
+                  const uint16_t* w, float eps, uint16_t* y, void* stream);
+
+/* A11 — rotary embedding on one (1, heads, 1, D) tensor, strided:
+ * out = x*cos + rotate_half(x)*sin in fp32, rounded to fp16.  Replaces
+ * _rope_one_kernel (src/lemoq/kernels/rope.py:86-123) as launched by
+ * apply_rotary_pos_emb_fused (src/lemoq/kernels/rope.py:154-203).
+ * Element (h, d) of x at x + h*x_sh + d*x_sd; cos/sin element d at
+ * cos + d*cs_sd; out element at out + h*o_sh + d*o_sd.  D even, D <= 1024. */
+int lemoq_rope(const uint16_t* x, int64_t x_sh, int64_t x_sd, int64_t heads,
+               int64_t head_dim, const uint16_t* cos, const uint16_t* sin,
+               int64_t cs_sd, uint16_t* out, int64_t o_sh, int64_t o_sd,
+               void* stream);
+
+/* ---------------------------------------------------------------------------
+ * A12 — bitwise copy of the new k/v rows (heads, D) fp16 to slot *pos of the
+ * fp16 cache.  Replaces _kv_direct_write_kernel / kv_direct_write
+ * (src/lemoq/kernels/kv_direct.py:78-137; contract kv_write.py:26-50).
+ * Source head h at k + h*src_head_stride; destination at
+ * k_cache + h*dst_head_stride + (*pos)*D.  pos is a device int64.
+ * ------------------------------------------------------------------------- */
+int lemoq_kv_write_f16(const uint16_t* k, const uint16_t* v,
+                       int64_t src_head_stride, uint16_t* k_cache,
+                       uint16_t* v_cache, int64_t dst_head_stride,
+                       const int64_t* pos, int64_t heads, int64_t head_dim,
+                       void* stream);
+
+/* A13 — KV direct-write quantisation.  Per (head) row of the new k and v:
+ * s = fp32(amax)/127 (1.0 when amax == 0), code = round-half-even(x/s)
+ * clamped to [-127, 127], scale stored as fp16(s).  Codes of head h go to
+ * kc + h*code_head_stride + slot*D, the scale to ks + h*s_len + slot, with
+ * slot = *pos (device int64) or 0 when pos is NULL.  Replaces
+ * _kv_int8_cache_write_kernel / kv_int8_cache_write
+ * (src/lemoq/kernels/kv_int8.py:182-257) and, with pos == NULL,
+ * code_head_stride == D and s_len == 1, kv_int8_write (:276-355). */
+int lemoq_kv_write_i8(const uint16_t* k, const uint16_t* v, int64_t heads,
+                      int64_t head_dim, int8_t* kc, uint16_t* ks, int8_t* vc,
+                      uint16_t* vs, int64_t code_head_stride, int64_t s_len,
+                      const int64_t* pos, void* stream);
+
+/* Bulk per-token quantisation of `rows` contiguous rows of D fp16 (same
+ * arithmetic as lemoq_kv_write_i8).  Replaces kv_int8_bulk_quantize
+ * (src/lemoq/kernels/kv_int8.py:127-163). */
+int lemoq_kv_quantize_rows(const uint16_t* x, int64_t rows, int64_t head_dim,
+                           int8_t* codes, uint16_t* scales, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * A3 — routing: fp32 softmax over E logits, top_k by value (ties -> lowest
+ * index), optional renormalisation over the selected k.  Replaces
+ * _routing_softmax_topk_kernel / routing_softmax_topk
+ * (src/lemoq/kernels/_routing_triton.py:43-130).
+ * logits (T, E) with row stride `row_stride` elements, fp16 when
+ * logits_is_f16 else fp32; top_w (T, top_k) fp32; top_i (T, top_k) int64.
+ * E <= 1024, top_k <= E.
+ * ------------------------------------------------------------------------- */
+int lemoq_route_topk(const void* logits, int logits_is_f16, int64_t T, int64_t E,
+                     int64_t row_stride, int64_t top_k, int norm_topk_prob,
+                     float* top_w, int64_t* top_i, void* stream);
+
+/* Router of one token, fused: xn = rmsnorm(h, norm_w) (written to xn_out),
+ * logits = fp16(xn @ router_w^T) with fp32 accumulation (the F.linear of
+ * moe_static._route, src/lemoq/kernels/moe_static.py:262-283), then the
+ * routing above; top_w_f16 = fp16(top_w) (the `.to(x.dtype)` of _route).
+ * router_w (E, hidden) fp16.  norm_w may be NULL (no norm: xn = h).
+ * logits_out and top_w_f32 may be NULL. */
+int lemoq_router_topk_fused(const uint16_t* h, const uint16_t* norm_w, float eps,
+                            int64_t hidden, const uint16_t* router_w, int64_t E,
+                            int64_t top_k, int norm_topk_prob, uint16_t* xn_out,
+                            uint16_t* logits_out, float* top_w_f32,
+                            uint16_t* top_w_f16, int64_t* top_i, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * A16 — per-layer attention prologue of the decode step, fused: from the
+ * packed q|k|v row (3*heads*D fp16) computes q_norm and k_norm (RMSNorm over
+ * heads*D, HF rounding), RoPE with the cos/sin row (*pos) of the tables
+ * cos_tab/sin_tab (max_pos, D) fp16, writes q_out (heads, D) fp16, and writes
+ * the new k and v rows KV-INT8-quantised to slot *pos (same arithmetic as
+ * lemoq_kv_write_i8).  k_f16/v_f16 (nullable): also copy the fp16 rows into an
+ * fp16 cache at h*f16_head_stride + (*pos)*D.  k_rot_out (nullable): the
+ * fp16 rotated k row, for tests.  Replaces the sequence at
+ * src/lemoq/kernels/attn_decode.py:882-987.
+ * ------------------------------------------------------------------------- */
+int lemoq_qk_norm_rope_kv_i8(const uint16_t* qkv, int64_t heads, int64_t head_dim,
+                             const uint16_t* q_norm_w, const uint16_t* k_norm_w,
+                             float eps, const uint16_t* cos_tab,
+                             const uint16_t* sin_tab, const int64_t* pos,
+                             uint16_t* q_out, int8_t* kc, uint16_t* ks, int8_t* vc,
+                             uint16_t* vs, int64_t code_head_stride, int64_t s_len,
+                             uint16_t* k_f16, uint16_t* v_f16,
+                             int64_t f16_head_stride, uint16_t* k_rot_out,
+                             void* stream);
+
+/* ---------------------------------------------------------------------------
+ * A17 — greedy selection and step advance on the device (replaces the host
+ * `logits.argmax().item()` of StaticCacheDecodeSession.replay,
+ * benchmarks/cudagraph.py:751-766, and the per-step fills of
+ * _set_step_inputs, :655-678).  next = argmax(logits[0:n]) (first index on
+ * ties), or prompt[*pos + 1] while *pos + 1 < prompt_len; then
+ * *token = next, history[*pos + 1] = next (when *pos + 1 < history_len),
+ * *pos += 1, *filled = *pos + 1.
+ * ------------------------------------------------------------------------- */
+int lemoq_argmax_advance(const uint16_t* logits, int64_t n, int64_t* token,
+                         int64_t* pos, int32_t* filled, const int64_t* prompt,
+                         int64_t prompt_len, int64_t* history, int64_t history_len,
+                         void* stream);
+
+/* ---------------------------------------------------------------------------
+ * A17/A18 — one whole OLMoE decode step (embedding -> 16 x [attention, MoE]
+ * -> final norm -> lm_head -> greedy advance) enqueued on `stream`; the
+ * caller captures it into a hipGraph.  Replaces the captured
+ * model(token, ...) forward of StaticCacheDecodeSession.capture
+ * (benchmarks/cudagraph.py:680-737) for the canonical w8a16 + W8 lm_head +
+ * KV-INT8 cell.  All buffers are caller-owned; see LemoqOlmoeStep.
+ * ------------------------------------------------------------------------- */
+typedef struct LemoqOlmoeLayer {
+  const uint16_t* ln_in;     /* (H)                */
+  const uint16_t* ln_post;   /* (H)                */
+  const uint16_t* q_norm;    /* (heads*D)          */
+  const uint16_t* k_norm;    /* (heads*D)          */
+  const int8_t* qkv_codes;   /* (3*heads*D, H)     */
+  const uint16_t* qkv_scale; /* (3*heads*D, H/g)   */
+  const int8_t* o_codes;     /* (H, heads*D)       */
+  const uint16_t* o_scale;   /* (H, heads*D/g)     */
+  const uint16_t* router;    /* (E, H) fp16        */
+  const int8_t* gu_codes;    /* (E, 2F, H)         */
+  const uint16_t* gu_scale;  /* (E, 2F, H/g)       */
+  const int8_t* dn_codes;    /* (E, H, F)          */
+  const uint16_t* dn_scale;  /* (E, H, F/g)        */
+  int8_t* kc;                /* (heads, S, D)      */
+  uint16_t* ks;              /* (heads, S)         */
+  int8_t* vc;                /* (heads, S, D)      */
+  uint16_t* vs;              /* (heads, S)         */
+} LemoqOlmoeLayer;
+
+typedef struct LemoqOlmoeStep {
+  /* shapes */
+  int64_t hidden, heads, head_dim, ffn, num_experts, top_k, vocab, group;
+  int64_t num_layers, max_seq, num_splits, norm_topk_prob;
+  float eps, qk_scale;
+  /* weights */
+  const LemoqOlmoeLayer* layers; /* host array of num_layers entries */
+  const uint16_t* embed;         /* (vocab, H) fp16 */
+  const uint16_t* final_norm;    /* (H) */
+  const int8_t* lm_codes;        /* (vocab, H) */
+  const uint16_t* lm_scale;      /* (vocab, H/g) */
+  const uint16_t* cos_tab;       /* (max_seq, D) fp16 */
+  const uint16_t* sin_tab;       /* (max_seq, D) fp16 */
+  /* device scalars and per-step buffers */
+  int64_t* token;                /* (1) current token id */
+  int64_t* pos;                  /* (1) position of `token` */
+  int32_t* filled;               /* (1) == *pos + 1 during the step */
+  const int64_t* prompt;         /* (prompt_len) */
+  int64_t prompt_len;
+  int64_t* history;              /* (history_len) token at each position */
+  int64_t history_len;
+  uint16_t* h;                   /* (H) residual stream */
+  uint16_t* xn;                  /* (H) normed input of the MoE */
+  uint16_t* qkv;                 /* (3*heads*D) */
+  uint16_t* q_rot;               /* (heads*D) */
+  uint16_t* attn;                /* (heads*D) */
+  float* part_m;                 /* (heads*num_splits) */
+  float* part_l;                 /* (heads*num_splits) */
+  float* part_acc;               /* (heads*num_splits*D) */
+  uint16_t* router_logits;       /* (E) */
+  uint16_t* top_w;               /* (top_k) fp16 */
+  int64_t* top_i;                /* (top_k) */
+  uint16_t* act;                 /* (top_k, F) */
+  uint16_t* logits;              /* (vocab) fp16 */
+} LemoqOlmoeStep;
+
+int lemoq_olmoe_decode_step(const LemoqOlmoeStep* step, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LEMOQ_HIP_H */

@@ -1,0 +1,286 @@
+// Split-KV decode attention (flash-decoding) for batch 1, q_len 1, over fp16
+// or KV-INT8 caches, and the log-sum-exp merge of the splits.
+//
+// Split kernel: grid (num_splits, heads), 4 waves.  Every lane reads 16 bytes
+// of a K/V row, so a token row is LPT = D*bytes/16 lanes and a wave covers
+// TPW = 64/LPT tokens per load.  Each wave walks its interleaved blocks of
+// U*TPW tokens of the split with an online softmax whose running max is
+// wave-uniform: scores are reduced inside the LPT-lane group, the block max
+// with one wave butterfly, then p = exp2(s - m) weights the V rows that the
+// same lanes load.  The four wave states (m, l, acc[D]) are merged through
+// LDS in a fixed order.  Tokens at or beyond the filled length are never
+// loaded, so whatever the cache holds there (NaN included) cannot leak in.
+// INT8 rows fold the per-token scales: score = ((q.c) * qk_scale) * ks,
+// acc += (p * vs) * c, l += p.
+#include "common.h"
+
+namespace {
+
+template <int D, bool I8>
+struct AttnShape {
+  static constexpr int EB = I8 ? 1 : 2;    // bytes per cached element
+  static constexpr int EPL = 16 / EB;      // elements per lane
+  static constexpr int LPT = D / EPL;      // lanes per token row
+  static constexpr int TPW = 64 / LPT;     // tokens per wave load
+  static constexpr int U = I8 ? 2 : 4;     // loads per softmax update
+  static_assert(LPT >= 1 && LPT <= 64 && (64 % LPT) == 0, "unsupported head_dim");
+};
+
+// q . k for one 16-byte slice (fp16 K: 8 values; int8 K: 16 codes).
+__device__ __forceinline__ float qk_dot_f16(const u32x4 k, const u32x4 q) {
+  const uint32_t kw[4] = {k.x, k.y, k.z, k.w};
+  const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+  float a = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) a = __builtin_amdgcn_fdot2(as_h2(kw[i]), as_h2(qw[i]), a, false);
+  return a;
+}
+
+__device__ __forceinline__ void unpack_f16x8(const u32x4 v, float (&o)[8]) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    o[2 * i] = h2f((uint16_t)(w[i] & 0xFFFFu));
+    o[2 * i + 1] = h2f((uint16_t)(w[i] >> 16));
+  }
+}
+
+__device__ __forceinline__ void unpack_i8x16(const u32x4 v, float (&o)[16]) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int b = 0; b < 4; ++b) o[4 * i + b] = (float)(int8_t)((w[i] >> (8 * b)) & 0xFFu);
+  }
+}
+
+template <int D, bool I8>
+__global__ __launch_bounds__(256) void attn_split_kernel(
+    const uint16_t* __restrict__ q, const void* __restrict__ kp, const uint16_t* __restrict__ ks,
+    const void* __restrict__ vp, const uint16_t* __restrict__ vs, int64_t head_stride,
+    int64_t s_len, int64_t max_len, const int32_t* __restrict__ filled, int NS, float qk_scale,
+    float* __restrict__ m_out, float* __restrict__ l_out, float* __restrict__ acc_out) {
+  using S = AttnShape<D, I8>;
+  constexpr int EPL = S::EPL, LPT = S::LPT, TPW = S::TPW, U = S::U;
+  __shared__ float wm[4], wl[4];
+  __shared__ float wacc[4][D];
+
+  const int sp = blockIdx.x, h = blockIdx.y;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int dl = lane % LPT;  // which 16-byte slice of the row
+  const int tl = lane / LPT;  // which token of the wave load
+
+  int64_t n = filled[0];
+  n = n < 0 ? 0 : (n > max_len ? max_len : n);
+  const int64_t chunk = (n + NS - 1) / NS;
+  const int64_t start = (int64_t)sp * chunk;
+  const int64_t end = start + chunk < n ? start + chunk : n;
+
+  const uint8_t* kb = reinterpret_cast<const uint8_t*>(kp) + (int64_t)h * head_stride * S::EB;
+  const uint8_t* vb = reinterpret_cast<const uint8_t*>(vp) + (int64_t)h * head_stride * S::EB;
+  const uint16_t* ksh = I8 ? ks + (int64_t)h * s_len : nullptr;
+  const uint16_t* vsh = I8 ? vs + (int64_t)h * s_len : nullptr;
+
+  // This lane's slice of q.
+  XChunk qx;            // int8 path: 16 q values in dot order
+  u32x4 qv = {0u, 0u, 0u, 0u};  // fp16 path: 8 q values
+  if (I8) {
+    load_xchunk(q + (int64_t)h * D + dl * EPL, qx);
+  } else {
+    qv = *reinterpret_cast<const u32x4*>(q + (int64_t)h * D + dl * EPL);
+  }
+
+  float m = -INFINITY, l = 0.0f;
+  float acc[EPL];
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) acc[e] = 0.0f;
+
+  constexpr int BLK = TPW * U;  // tokens per wave step
+  for (int64_t base = start + (int64_t)wave * BLK; base < end; base += 4 * BLK) {
+    float sc[U];
+    bool valid[U];
+    u32x4 kr[U], vr[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t t = base + u * TPW + tl;
+      valid[u] = t < end;
+      const int64_t off = (t * D + dl * EPL) * S::EB;
+      kr[u] = valid[u] ? *reinterpret_cast<const u32x4*>(kb + off) : (u32x4){0u, 0u, 0u, 0u};
+      vr[u] = valid[u] ? *reinterpret_cast<const u32x4*>(vb + off) : (u32x4){0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float d = I8 ? dot16_i8(kr[u], qx, 0.0f) : qk_dot_f16(kr[u], qv);
+      d = group_sum<LPT>(d);
+      const int64_t t = base + u * TPW + tl;
+      float s = d * qk_scale;
+      if (I8) s = s * (valid[u] ? h2f(ksh[t]) : 0.0f);
+      sc[u] = valid[u] ? s : -INFINITY;
+    }
+    float mx = sc[0];
+#pragma unroll
+    for (int u = 1; u < U; ++u) mx = fmaxf(mx, sc[u]);
+    mx = wave_max(mx);
+    const float m_new = fmaxf(m, mx);
+    if (m_new == -INFINITY) continue;  // no valid token yet (cannot happen for finite scores)
+    const float alpha = exp2f(m - m_new);
+    float psum = 0.0f;
+    float pw[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const float p = valid[u] ? exp2f(sc[u] - m_new) : 0.0f;
+      psum += p;
+      const int64_t t = base + u * TPW + tl;
+      pw[u] = I8 ? (valid[u] ? p * h2f(vsh[t]) : 0.0f) : p;
+    }
+    l = l * alpha + psum;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) acc[e] *= alpha;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (I8) {
+        float vf[16];
+        unpack_i8x16(vr[u], vf);
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) acc[e] = fmaf(pw[u], vf[e], acc[e]);
+      } else {
+        float vf[8];
+        unpack_f16x8(vr[u], vf);
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) acc[e] = fmaf(pw[u], vf[e], acc[e]);
+      }
+    }
+    m = m_new;
+  }
+  // Sum the token groups of the wave (lanes with the same slice dl).
+#pragma unroll
+  for (int o = LPT; o < 64; o <<= 1) {
+    l += __shfl_xor(l, o, 64);
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) acc[e] += __shfl_xor(acc[e], o, 64);
+  }
+  if (lane == 0) {
+    wm[wave] = m;
+    wl[wave] = l;
+  }
+  if (tl == 0) {
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) wacc[wave][dl * EPL + e] = acc[e];
+  }
+  __syncthreads();
+  const int64_t pidx = (int64_t)h * NS + sp;
+  for (int t = threadIdx.x; t < D; t += 256) {
+    float M = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
+    float a = 0.0f, L = 0.0f;
+    if (M != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float f = exp2f(wm[w] - M);
+        a += wacc[w][t] * f;
+        L += wl[w] * f;
+      }
+    }
+    acc_out[pidx * D + t] = a;
+    if (t == 0) {
+      m_out[pidx] = M;
+      l_out[pidx] = L;
+    }
+  }
+}
+
+__global__ void attn_merge_kernel(const float* __restrict__ m, const float* __restrict__ l,
+                                  const float* __restrict__ acc, int NS, int D,
+                                  uint16_t* __restrict__ out) {
+  const int h = blockIdx.x;
+  const float* mh = m + (int64_t)h * NS;
+  const float* lh = l + (int64_t)h * NS;
+  float M = -INFINITY;
+  for (int j = 0; j < NS; ++j) M = fmaxf(M, mh[j]);
+  if (!(M > -INFINITY)) M = 0.0f;
+  for (int t = threadIdx.x; t < D; t += blockDim.x) {
+    float num = 0.0f, den = 0.0f;
+    for (int j = 0; j < NS; ++j) {
+      const float w = exp2f(mh[j] - M);
+      num += acc[((int64_t)h * NS + j) * D + t] * w;
+      den += lh[j] * w;
+    }
+    out[(int64_t)h * D + t] = f2h(den > 0.0f ? num / den : num);
+  }
+}
+
+template <bool I8>
+int launch_split(hipStream_t st, const uint16_t* q, const void* k, const uint16_t* ks,
+                 const void* v, const uint16_t* vs, int64_t head_stride, int64_t s_len,
+                 int64_t max_len, const int32_t* filled, int64_t heads, int64_t D, int64_t NS,
+                 float qk_scale, float* m, float* l, float* acc) {
+  dim3 grid((unsigned)NS, (unsigned)heads);
+#define LEMOQ_SPLIT_CASE(DD)                                                                   \
+  case DD:                                                                                     \
+    hipLaunchKernelGGL((attn_split_kernel<DD, I8>), grid, dim3(256), 0, st, q, k, ks, v, vs,  \
+                       head_stride, s_len, max_len, filled, (int)NS, qk_scale, m, l, acc);    \
+    break;
+  switch (D) {
+    LEMOQ_SPLIT_CASE(64)
+    LEMOQ_SPLIT_CASE(128)
+    LEMOQ_SPLIT_CASE(256)
+    default: return LEMOQ_ERR_UNSUPPORTED;
+  }
+#undef LEMOQ_SPLIT_CASE
+  LEMOQ_CHECK_LAUNCH();
+}
+
+int check_split_args(const void* q, const void* k, const void* v, const int32_t* filled,
+                     const float* m, const float* l, const float* acc, int64_t heads, int64_t D,
+                     int64_t NS, int64_t head_stride, int64_t max_len) {
+  if (!q || !k || !v || !filled || !m || !l || !acc) return LEMOQ_ERR_NULL;
+  if (heads <= 0 || heads > 65535 || NS <= 0 || NS > 65535) return LEMOQ_ERR_SHAPE;
+  if (D != 64 && D != 128 && D != 256) return LEMOQ_ERR_UNSUPPORTED;
+  if (max_len <= 0 || head_stride < max_len * D) return LEMOQ_ERR_SHAPE;
+  if (!lemoq_aligned16(q) || !lemoq_aligned16(k) || !lemoq_aligned16(v)) return LEMOQ_ERR_ALIGN;
+  return LEMOQ_OK;
+}
+
+}  // namespace
+
+// The f16 entry point has no separate capacity argument; the cache capacity
+// is head_stride / D (the reference requires a non-overlapping head stride
+// of at least S*D, src/lemoq/kernels/attn_decode.py:548-549).
+extern "C" int lemoq_attn_split_f16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                    int64_t head_stride, const int32_t* filled, int64_t heads,
+                                    int64_t head_dim, int64_t num_splits, float qk_scale,
+                                    float* m, float* l, float* acc, void* stream) {
+  if (head_dim <= 0) return LEMOQ_ERR_SHAPE;
+  const int64_t max_len = head_stride / head_dim;
+  int rc = check_split_args(q, k, v, filled, m, l, acc, heads, head_dim, num_splits, head_stride,
+                            max_len);
+  if (rc) return rc;
+  if ((head_stride * 2) % 16 != 0) return LEMOQ_ERR_ALIGN;
+  return launch_split<false>(lemoq_stream(stream), q, k, nullptr, v, nullptr, head_stride, 0,
+                             max_len, filled, heads, head_dim, num_splits, qk_scale, m, l, acc);
+}
+
+extern "C" int lemoq_attn_split_i8(const uint16_t* q, const int8_t* kc, const uint16_t* ks,
+                                   const int8_t* vc, const uint16_t* vs, int64_t head_stride,
+                                   int64_t s_len, const int32_t* filled, int64_t heads,
+                                   int64_t head_dim, int64_t num_splits, float qk_scale, float* m,
+                                   float* l, float* acc, void* stream) {
+  if (!ks || !vs) return LEMOQ_ERR_NULL;
+  int rc = check_split_args(q, kc, vc, filled, m, l, acc, heads, head_dim, num_splits,
+                            head_stride, s_len);
+  if (rc) return rc;
+  if (head_stride % 16 != 0) return LEMOQ_ERR_ALIGN;
+  return launch_split<true>(lemoq_stream(stream), q, kc, ks, vc, vs, head_stride, s_len, s_len,
+                            filled, heads, head_dim, num_splits, qk_scale, m, l, acc);
+}
+
+extern "C" int lemoq_attn_merge(const float* m, const float* l, const float* acc, int64_t heads,
+                                int64_t num_splits, int64_t head_dim, uint16_t* out,
+                                void* stream) {
+  if (!m || !l || !acc || !out) return LEMOQ_ERR_NULL;
+  if (heads <= 0 || heads > 65535 || num_splits <= 0 || head_dim <= 0 || head_dim > 1024)
+    return LEMOQ_ERR_SHAPE;
+  const int threads = head_dim <= 64 ? 64 : (head_dim <= 128 ? 128 : 256);
+  hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)heads), dim3(threads), 0,
+                     lemoq_stream(stream), m, l, acc, (int)num_splits, (int)head_dim, out);
+  LEMOQ_CHECK_LAUNCH();
+}

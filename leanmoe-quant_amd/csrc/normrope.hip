@@ -1,0 +1,208 @@
+// RMSNorm, RoPE, and the fused per-layer attention prologue of the decode
+// step (q_norm/k_norm -> RoPE -> KV-INT8 write).
+//
+// RMSNorm rounding points follow HF OlmoeRMSNorm.forward as restated by the
+// reference kernel (src/lemoq/kernels/rmsnorm.py:184-202): fp32 mean of
+// squares, x*rstd rounded to fp16, then the fp16 product with the fp16 weight
+// (exact in fp32, rounded once).  RoPE follows _rope_one_kernel
+// (src/lemoq/kernels/rope.py:101-123): y = x*cos + sign*x[shift]*sin in fp32
+// with rotate_half's halves, rounded to fp16.
+#include "common.h"
+
+namespace {
+
+// Block-wide sum over 256 threads (4 waves).
+__device__ __forceinline__ float block_sum_256(float v, float* red) {
+  v = wave_sum(v);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  const float t = red[0] + red[1] + red[2] + red[3];
+  __syncthreads();
+  return t;
+}
+
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict__ x, int H,
+                                                      const uint16_t* __restrict__ w, float eps,
+                                                      uint16_t* __restrict__ y) {
+  __shared__ float red[4];
+  const int64_t r = blockIdx.x;
+  const uint16_t* xr = x + r * H;
+  uint16_t* yr = y + r * H;
+  float ssq = 0.0f;
+  for (int i = threadIdx.x; i < H; i += 256) {
+    const float a = h2f(xr[i]);
+    ssq += a * a;
+  }
+  const float tot = block_sum_256(ssq, red);
+  const float rstd = 1.0f / sqrtf(tot / (float)H + eps);
+  for (int i = threadIdx.x; i < H; i += 256) {
+    const uint16_t nh = f2h(h2f(xr[i]) * rstd);
+    yr[i] = f2h(h2f(nh) * h2f(w[i]));
+  }
+}
+
+__device__ __forceinline__ float rope_elem(float x, float xs, float c, float s, bool first_half) {
+  return first_half ? x * c + (-xs) * s : x * c + xs * s;
+}
+
+__global__ __launch_bounds__(128) void rope_kernel(const uint16_t* __restrict__ x, int64_t x_sh,
+                                                   int64_t x_sd, int D,
+                                                   const uint16_t* __restrict__ cs,
+                                                   const uint16_t* __restrict__ sn, int64_t cs_sd,
+                                                   uint16_t* __restrict__ out, int64_t o_sh,
+                                                   int64_t o_sd) {
+  const int h = blockIdx.x;
+  const int half = D / 2;
+  for (int d = threadIdx.x; d < D; d += 128) {
+    const bool first = d < half;
+    const int sh = first ? d + half : d - half;
+    const float xv = h2f(x[h * x_sh + d * x_sd]);
+    const float xs = h2f(x[h * x_sh + sh * x_sd]);
+    const float c = h2f(cs[d * cs_sd]);
+    const float s = h2f(sn[d * cs_sd]);
+    out[h * o_sh + d * o_sd] = f2h(rope_elem(xv, xs, c, s, first));
+  }
+}
+
+// Fused attention prologue.  Block 0: q; block 1: k; block 2: v.
+// LDS holds the normed (then rotated) row of heads*D <= 8192 fp16.
+__global__ __launch_bounds__(256) void qk_norm_rope_kv_kernel(
+    const uint16_t* __restrict__ qkv, int heads, int D, const uint16_t* __restrict__ qn_w,
+    const uint16_t* __restrict__ kn_w, float eps, const uint16_t* __restrict__ cos_tab,
+    const uint16_t* __restrict__ sin_tab, const int64_t* __restrict__ pos_ptr,
+    uint16_t* __restrict__ q_out, int8_t* __restrict__ kc, uint16_t* __restrict__ ks,
+    int8_t* __restrict__ vc, uint16_t* __restrict__ vs, int64_t code_head_stride, int64_t s_len,
+    uint16_t* __restrict__ k_f16, uint16_t* __restrict__ v_f16, int64_t f16_head_stride,
+    uint16_t* __restrict__ k_rot_out) {
+  __shared__ __align__(16) uint16_t nrm[8192];
+  __shared__ __align__(16) uint16_t rot[8192];
+  __shared__ float red[4];
+  const int which = blockIdx.x;  // 0 q, 1 k, 2 v
+  const int HD = heads * D;
+  const int64_t pos = pos_ptr[0];
+  const bool pos_ok = pos >= 0 && pos < s_len;
+  const uint16_t* src = qkv + (int64_t)which * HD;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+
+  if (which == 2) {  // v: quantise the raw rows
+    if (!pos_ok) return;
+    for (int h = wave; h < heads; h += 4) {
+      const uint16_t* row = src + (int64_t)h * D;
+      int8_t* dst = vc + (int64_t)h * code_head_stride + pos * D;
+      // amax / scale / codes, same arithmetic as quant_row_wave (quant.hip)
+      float amax = 0.0f;
+      for (int d = lane; d < D; d += 64) amax = fmaxf(amax, fabsf(h2f(row[d])));
+      amax = wave_max(amax);
+      const float s = amax > 0.0f ? amax / 127.0f : 1.0f;
+      for (int d = lane; d < D; d += 64) {
+        float qv = rintf(h2f(row[d]) / s);
+        qv = fminf(fmaxf(qv, -127.0f), 127.0f);
+        dst[d] = (int8_t)(int)qv;
+        if (v_f16) v_f16[(int64_t)h * f16_head_stride + pos * D + d] = row[d];
+      }
+      if (lane == 0) vs[(int64_t)h * s_len + pos] = f2h(s);
+    }
+    return;
+  }
+
+  // q or k: RMSNorm over the whole heads*D row.
+  const uint16_t* nw = which == 0 ? qn_w : kn_w;
+  float ssq = 0.0f;
+  for (int i = threadIdx.x; i < HD; i += 256) {
+    const uint16_t v = src[i];
+    nrm[i] = v;
+    const float a = h2f(v);
+    ssq += a * a;
+  }
+  const float tot = block_sum_256(ssq, red);
+  const float rstd = 1.0f / sqrtf(tot / (float)HD + eps);
+  for (int i = threadIdx.x; i < HD; i += 256) {
+    const uint16_t nh = f2h(h2f(nrm[i]) * rstd);
+    nrm[i] = f2h(h2f(nh) * h2f(nw[i]));
+  }
+  __syncthreads();
+  // RoPE with the table row of this position (clamped read; writes need pos_ok).
+  const int64_t prow = pos_ok ? pos : 0;
+  const uint16_t* cr = cos_tab + prow * D;
+  const uint16_t* sr = sin_tab + prow * D;
+  const int half = D / 2;
+  for (int i = threadIdx.x; i < HD; i += 256) {
+    const int h = i / D, d = i - h * D;
+    const bool first = d < half;
+    const int sh = first ? d + half : d - half;
+    const float xv = h2f(nrm[i]);
+    const float xs = h2f(nrm[h * D + sh]);
+    const uint16_t o = f2h(rope_elem(xv, xs, h2f(cr[d]), h2f(sr[d]), first));
+    if (which == 0) {
+      q_out[i] = o;
+    } else {
+      rot[i] = o;
+      if (k_rot_out) k_rot_out[i] = o;
+    }
+  }
+  if (which == 0 || !pos_ok) return;
+  __syncthreads();
+  for (int h = wave; h < heads; h += 4) {
+    const uint16_t* row = rot + h * D;
+    int8_t* dst = kc + (int64_t)h * code_head_stride + pos * D;
+    float amax = 0.0f;
+    for (int d = lane; d < D; d += 64) amax = fmaxf(amax, fabsf(h2f(row[d])));
+    amax = wave_max(amax);
+    const float s = amax > 0.0f ? amax / 127.0f : 1.0f;
+    for (int d = lane; d < D; d += 64) {
+      float qv = rintf(h2f(row[d]) / s);
+      qv = fminf(fmaxf(qv, -127.0f), 127.0f);
+      dst[d] = (int8_t)(int)qv;
+      if (k_f16) k_f16[(int64_t)h * f16_head_stride + pos * D + d] = row[d];
+    }
+    if (lane == 0) ks[(int64_t)h * s_len + pos] = f2h(s);
+  }
+}
+
+}  // namespace
+
+extern "C" int lemoq_rmsnorm(const uint16_t* x, int64_t rows, int64_t hidden, const uint16_t* w,
+                             float eps, uint16_t* y, void* stream) {
+  if (!x || !w || !y) return LEMOQ_ERR_NULL;
+  if (rows < 0 || hidden <= 0 || hidden > 8192) return LEMOQ_ERR_SHAPE;
+  if (rows == 0) return LEMOQ_OK;
+  if (rows > 0x7fffffffLL) return LEMOQ_ERR_SHAPE;
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)rows), dim3(256), 0, lemoq_stream(stream), x,
+                     (int)hidden, w, eps, y);
+  LEMOQ_CHECK_LAUNCH();
+}
+
+extern "C" int lemoq_rope(const uint16_t* x, int64_t x_sh, int64_t x_sd, int64_t heads,
+                          int64_t head_dim, const uint16_t* cos, const uint16_t* sin,
+                          int64_t cs_sd, uint16_t* out, int64_t o_sh, int64_t o_sd,
+                          void* stream) {
+  if (!x || !cos || !sin || !out) return LEMOQ_ERR_NULL;
+  if (heads <= 0 || heads > 65535 || head_dim < 2 || head_dim % 2 != 0 || head_dim > 1024)
+    return LEMOQ_ERR_SHAPE;
+  hipLaunchKernelGGL(rope_kernel, dim3((unsigned)heads), dim3(128), 0, lemoq_stream(stream), x,
+                     x_sh, x_sd, (int)head_dim, cos, sin, cs_sd, out, o_sh, o_sd);
+  LEMOQ_CHECK_LAUNCH();
+}
+
+extern "C" int lemoq_qk_norm_rope_kv_i8(const uint16_t* qkv, int64_t heads, int64_t head_dim,
+                                        const uint16_t* q_norm_w, const uint16_t* k_norm_w,
+                                        float eps, const uint16_t* cos_tab,
+                                        const uint16_t* sin_tab, const int64_t* pos,
+                                        uint16_t* q_out, int8_t* kc, uint16_t* ks, int8_t* vc,
+                                        uint16_t* vs, int64_t code_head_stride, int64_t s_len,
+                                        uint16_t* k_f16, uint16_t* v_f16,
+                                        int64_t f16_head_stride, uint16_t* k_rot_out,
+                                        void* stream) {
+  if (!qkv || !q_norm_w || !k_norm_w || !cos_tab || !sin_tab || !pos || !q_out || !kc || !ks ||
+      !vc || !vs)
+    return LEMOQ_ERR_NULL;
+  if (heads <= 0 || head_dim < 2 || head_dim % 2 != 0 || heads * head_dim > 8192)
+    return LEMOQ_ERR_SHAPE;
+  if (s_len <= 0 || code_head_stride < s_len * head_dim) return LEMOQ_ERR_SHAPE;
+  if ((k_f16 || v_f16) && f16_head_stride < s_len * head_dim) return LEMOQ_ERR_SHAPE;
+  hipLaunchKernelGGL(qk_norm_rope_kv_kernel, dim3(3), dim3(256), 0, lemoq_stream(stream), qkv,
+                     (int)heads, (int)head_dim, q_norm_w, k_norm_w, eps, cos_tab, sin_tab, pos,
+                     q_out, kc, ks, vc, vs, code_head_stride, s_len, k_f16, v_f16,
+                     f16_head_stride, k_rot_out);
+  LEMOQ_CHECK_LAUNCH();
+}

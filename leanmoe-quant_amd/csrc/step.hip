@@ -1,0 +1,80 @@
+// Native decode-step executor: enqueues one whole OLMoE decode step of the
+// canonical cell (w8a16 attention + experts, W8 lm_head, KV-INT8 cache) on a
+// stream, ready to be captured into a hipGraph by the caller.
+//
+// Per layer (8 launches):
+//   1 gemv_w8_fused   input RMSNorm (+ embedding gather on layer 0) -> packed q|k|v
+//   2 qk_norm_rope_kv q_norm/k_norm, RoPE at *pos, KV-INT8 write of slot *pos
+//   3 attn_split_i8   split-KV partials over [0, *filled)
+//   4 attn_merge      LSE merge -> attention output
+//   5 gemv_w8_fused   o_proj with the residual add folded into the epilogue
+//   6 router_fused    post-attention RMSNorm, router GEMV, softmax, top-k
+//   7 moe_gate_up_w8  gate/up + SiLU of the 8 selected experts
+//   8 moe_down_w8     down projection x routing weight + residual add
+// then final RMSNorm + lm_head GEMV, and the on-device greedy argmax that
+// writes the next token and advances *pos / *filled.
+//
+// The layer order and rounding points restate the HF OLMoE decoder layer
+// (transformers OlmoeDecoderLayer/OlmoeModel, called by the reference through
+// StaticCacheDecodeSession, benchmarks/cudagraph.py:720-737) with the
+// reference's patched operators (attn_decode.py:836-1017,
+// moe_grouped_quant.py:562-601, rmsnorm.py:205-212).
+#include "common.h"
+
+#define LEMOQ_TRY(expr)       \
+  do {                        \
+    const int rc__ = (expr);  \
+    if (rc__) return rc__;    \
+  } while (0)
+
+extern "C" int lemoq_olmoe_decode_step(const LemoqOlmoeStep* p, void* stream) {
+  if (!p || !p->layers) return LEMOQ_ERR_NULL;
+  if (!p->embed || !p->final_norm || !p->lm_codes || !p->lm_scale || !p->cos_tab ||
+      !p->sin_tab || !p->token || !p->pos || !p->filled || !p->h || !p->xn || !p->qkv ||
+      !p->q_rot || !p->attn || !p->part_m || !p->part_l || !p->part_acc || !p->top_w ||
+      !p->top_i || !p->act || !p->logits)
+    return LEMOQ_ERR_NULL;
+  const int64_t H = p->hidden, HD = p->heads * p->head_dim, D = p->head_dim;
+  if (H <= 0 || p->heads <= 0 || D <= 0 || p->num_layers <= 0 || p->max_seq <= 0 ||
+      p->num_splits <= 0 || p->vocab <= 0)
+    return LEMOQ_ERR_SHAPE;
+  const int64_t S = p->max_seq;
+  for (int64_t L = 0; L < p->num_layers; ++L) {
+    const LemoqOlmoeLayer& w = p->layers[L];
+    const bool first = L == 0;
+    // 1. input RMSNorm + packed qkv projection.  Layer 0 gathers the
+    //    embedding row of *token and block 0 stores it as the residual.
+    LEMOQ_TRY(lemoq_gemv_w8_fused(first ? p->embed : p->h, first ? p->token : nullptr, p->vocab,
+                                  w.ln_in, p->eps, first ? p->h : nullptr, w.qkv_codes,
+                                  w.qkv_scale, 3 * HD, H, p->group, nullptr, p->qkv, stream));
+    // 2. q/k norm, RoPE, KV-INT8 write at slot *pos.
+    LEMOQ_TRY(lemoq_qk_norm_rope_kv_i8(p->qkv, p->heads, D, w.q_norm, w.k_norm, p->eps,
+                                       p->cos_tab, p->sin_tab, p->pos, p->q_rot, w.kc, w.ks,
+                                       w.vc, w.vs, S * D, S, nullptr, nullptr, 0, nullptr,
+                                       stream));
+    // 3-4. split-KV attention over [0, *filled) and the LSE merge.
+    LEMOQ_TRY(lemoq_attn_split_i8(p->q_rot, w.kc, w.ks, w.vc, w.vs, S * D, S, p->filled,
+                                  p->heads, D, p->num_splits, p->qk_scale, p->part_m, p->part_l,
+                                  p->part_acc, stream));
+    LEMOQ_TRY(lemoq_attn_merge(p->part_m, p->part_l, p->part_acc, p->heads, p->num_splits, D,
+                               p->attn, stream));
+    // 5. o_proj; h = fp16(fp16(o) + h).
+    LEMOQ_TRY(lemoq_gemv_w8_fused(p->attn, nullptr, 0, nullptr, p->eps, nullptr, w.o_codes,
+                                  w.o_scale, H, HD, p->group, p->h, p->h, stream));
+    // 6. post-attention RMSNorm + router + top-k.
+    LEMOQ_TRY(lemoq_router_topk_fused(p->h, w.ln_post, p->eps, H, w.router, p->num_experts,
+                                      p->top_k, (int)p->norm_topk_prob, p->xn,
+                                      p->router_logits, nullptr, p->top_w, p->top_i, stream));
+    // 7-8. grouped MoE; h = fp16(fp16(moe) + h).
+    LEMOQ_TRY(lemoq_moe_gate_up_w8(p->xn, w.gu_codes, w.gu_scale, p->top_i, p->top_k,
+                                   p->num_experts, p->ffn, H, p->group, p->act, stream));
+    LEMOQ_TRY(lemoq_moe_down_w8(p->act, w.dn_codes, w.dn_scale, p->top_i, p->top_w, p->top_k,
+                                p->num_experts, H, p->ffn, p->group, p->h, p->h, stream));
+  }
+  // Final norm + W8 lm_head, then greedy selection and step advance.
+  LEMOQ_TRY(lemoq_gemv_w8_fused(p->h, nullptr, 0, p->final_norm, p->eps, nullptr, p->lm_codes,
+                                p->lm_scale, p->vocab, H, p->group, nullptr, p->logits, stream));
+  LEMOQ_TRY(lemoq_argmax_advance(p->logits, p->vocab, p->token, p->pos, p->filled, p->prompt,
+                                 p->prompt_len, p->history, p->history_len, stream));
+  return LEMOQ_OK;
+}

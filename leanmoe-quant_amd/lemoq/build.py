@@ -1,0 +1,70 @@
+"""In-tree build of ``liblemoq_hip.so`` for gfx950 with hipcc.
+
+``python -m lemoq.build`` (with ``leanmoe-quant_amd`` on ``sys.path``) or
+``build_library()`` compiles every ``csrc/*.hip`` into one shared library next
+to the package (``lemoq/_lib``), which is what the ctypes loader opens.  It
+always recompiles; the result is written atomically.
+"""
+
+from __future__ import annotations
+
+import glob
+import os
+import subprocess
+import sys
+
+from lemoq._hip import LIB_DIR, LIB_PATH
+
+PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))  # leanmoe-quant_amd/
+REPO_ROOT = os.path.dirname(PKG_ROOT)
+CSRC = os.path.join(PKG_ROOT, "csrc")
+INCLUDE = os.path.join(REPO_ROOT, "include")
+
+OFFLOAD_ARCH = "gfx950"
+
+HIPCC_FLAGS = [
+    "--offload-arch=" + OFFLOAD_ARCH,
+    "-O3",
+    "-std=c++17",
+    "-shared",
+    "-fPIC",
+    "-mcode-object-version=5",
+    # Never emit packed-FP32 VALU ops (v_pk_{add,mul,fma}_f32).
+    "-Xclang",
+    "-target-feature",
+    "-Xclang",
+    "-packed-fp32-ops",
+]
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc"):
+        if cand and os.path.exists(cand):
+            return cand
+    return "hipcc"
+
+
+def sources() -> list[str]:
+    return sorted(glob.glob(os.path.join(CSRC, "*.hip")))
+
+
+def build_library(verbose: bool = False) -> str:
+    """Compile csrc/*.hip -> lemoq/_lib/liblemoq_hip.so; returns the path."""
+    os.makedirs(LIB_DIR, exist_ok=True)
+    tmp = LIB_PATH + ".tmp%d" % os.getpid()
+    cmd = [hipcc(), *HIPCC_FLAGS, "-I" + INCLUDE, "-I" + CSRC, *sources(), "-o", tmp]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    noise = "is not a recognized feature for this target"
+    err = "\n".join(line for line in proc.stderr.splitlines() if noise not in line)
+    if proc.returncode != 0:
+        if os.path.exists(tmp):
+            os.remove(tmp)
+        raise RuntimeError("hipcc failed (%d):\n%s\n%s" % (proc.returncode, " ".join(cmd), err))
+    if verbose and err.strip():
+        sys.stderr.write(err + "\n")
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    print(build_library(verbose=True))

@@ -1,0 +1,332 @@
+"""Split-KV decode attention (flash-decoding) over fp16 or KV-INT8 caches.
+
+Operator surface of the reference's ``src/lemoq/kernels/attn_decode.py``:
+``attn_decode_forward`` (``:496-624``), ``attn_decode_forward_int8``
+(``:627-730``), ``launch_plan`` (``:208-265``), ``resolve_num_splits``
+(``:172-201``), ``merged_config``, ``judge_length_change`` (``:427-468``),
+the frozen gates and ``warm``.  Two HIP launches per call
+(``lemoq_attn_split_{f16,i8}`` then ``lemoq_attn_merge``); the filled length
+is read on the device from a ``(1,) int32`` tensor, so a captured graph
+replays correctly when the length changes; only ``[0, filled)`` is read.
+
+Semantics: split ``s`` covers ``[s*c, min((s+1)*c, filled))`` with
+``c = ceil(filled/num_splits)``; online softmax with exp2 and
+``QK_SCALE = scale*log2(e)``; empty splits contribute nothing; the merge runs
+in a fixed split order; ``filled == 0`` yields zeros, never NaN.  INT8 folds
+the per-token scales: ``score = ((q.c_k)*QK_SCALE)*ks``,
+``acc += (p*vs)*c_v``, ``l = sum p``.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Any
+
+from lemoq import _hip
+
+__all__ = [
+    "ATTN_CONFIGS",
+    "LENGTH_CHANGE_GATE",
+    "LOG2E",
+    "PARITY_GATE",
+    "attn_decode_available",
+    "attn_decode_forward",
+    "attn_decode_forward_int8",
+    "judge_length_change",
+    "launch_plan",
+    "merged_config",
+    "resolve_num_splits",
+    "warm",
+]
+
+LOG2E = 1.4426950408889634
+
+PARITY_GATE = {
+    "tol_atol": 1e-3,
+    "tol_rtol": 1e-3,
+    "tol_slack": 1.5,
+    "note": "err_kernel <= err_baseline * tol_slack and allclose(atol, rtol); errors vs an fp64 oracle",
+}
+
+LENGTH_CHANGE_GATE = {
+    "correct_err_max": 1e-2,
+    "discriminant_min": 1.0,
+    "note": "captured at length N, replayed at M: must give M's answer while N's answer is far from it",
+}
+
+# num_splits=None -> ceil(CUs / heads) on the running device (256 CUs / 16 heads
+# = 16 on MI355X).  The answer does not depend on the split count.
+ATTN_CONFIGS: dict[str, Any] = {"num_splits": None}
+
+SUPPORTED_HEAD_DIMS = (64, 128, 256)
+
+
+def attn_decode_available() -> bool:
+    try:
+        import torch  # noqa: PLC0415
+
+        return _hip.library_available() and bool(torch.cuda.is_available())
+    except Exception:  # noqa: BLE001
+        return False
+
+
+def merged_config(config: dict[str, Any] | None = None) -> dict[str, Any]:
+    cfg = {k: dict(v) if isinstance(v, dict) else v for k, v in ATTN_CONFIGS.items()}
+    for key, value in (config or {}).items():
+        if isinstance(value, dict) and isinstance(cfg.get(key), dict):
+            cfg[key].update(value)
+        else:
+            cfg[key] = value
+    return cfg
+
+
+def resolve_num_splits(num_splits: int | None, *, heads: int, device: Any = None) -> int:
+    """``None`` -> ``ceil(CUs / heads)`` of the device (1 when no device is visible)."""
+    if num_splits is not None:
+        if int(num_splits) < 1:
+            raise ValueError("num_splits must be >= 1")
+        return int(num_splits)
+    cus = None
+    try:
+        import torch  # noqa: PLC0415
+
+        if torch.cuda.is_available():
+            idx = device if device is not None else 0
+            cus = int(torch.cuda.get_device_properties(idx).multi_processor_count)
+    except Exception:  # noqa: BLE001
+        cus = None
+    if not cus:
+        return 1
+    return max(1, -(-cus // max(1, int(heads))))
+
+
+def launch_plan(*, heads: int, head_dim: int, num_splits: int, **_: Any) -> dict[str, Any]:
+    """Grid and partial-buffer shapes (pure host arithmetic)."""
+    if heads < 1 or head_dim < 1:
+        raise ValueError("heads and head_dim must be positive")
+    if head_dim & (head_dim - 1):
+        raise ValueError("head_dim must be a power of two, got %r" % (head_dim,))
+    if num_splits < 1:
+        raise ValueError("num_splits must be >= 1")
+    return {
+        "heads": int(heads),
+        "head_dim": int(head_dim),
+        "num_splits": int(num_splits),
+        "kernel_count": 2,
+        "split": {
+            "grid": (int(num_splits), int(heads)),
+            "block": 256,
+            "m_shape": (int(heads), int(num_splits)),
+            "l_shape": (int(heads), int(num_splits)),
+            "acc_shape": (int(heads), int(num_splits), int(head_dim)),
+            "dtype": "float32",
+        },
+        "combine": {"grid": (int(heads),), "out_shape": (1, int(heads), 1, int(head_dim))},
+    }
+
+
+def judge_length_change(
+    *, correct_err: float, stale_err: float, gate: dict[str, Any] | None = None
+) -> dict[str, Any]:
+    """K4 verdict: PASS/FAIL only when the stale answer is far from the correct one."""
+    gate = LENGTH_CHANGE_GATE if gate is None else gate
+    correct_err = float(correct_err)
+    stale_err = float(stale_err)
+    discriminating = stale_err >= float(gate["discriminant_min"])
+    correct = correct_err < float(gate["correct_err_max"])
+    verdict = "INCONCLUSIVE" if not discriminating else ("PASS" if correct else "FAIL")
+    return {
+        "verdict": verdict,
+        "correct_err": correct_err,
+        "stale_err": stale_err,
+        "discriminating": bool(discriminating),
+        "gate": dict(gate),
+    }
+
+
+def _filled_tensor(filled_len: Any, *, device: Any, seq_len: int) -> Any:
+    """Host int or (1,) int32 device tensor -> (1,) int32 device tensor."""
+    import torch  # noqa: PLC0415
+
+    if torch.is_tensor(filled_len):
+        if filled_len.numel() != 1:
+            raise ValueError("filled_len tensor must have one element, got %d" % filled_len.numel())
+        if filled_len.dtype != torch.int32:
+            raise ValueError("filled_len tensor must be int32, got %s" % filled_len.dtype)
+        if filled_len.device != device:
+            raise ValueError("filled_len and k/v are on different devices: %s vs %s" % (filled_len.device, device))
+        return filled_len.reshape(1)
+    if type(filled_len) is not int:
+        raise ValueError("filled_len must be an int or a one-element int32 tensor")
+    n = int(filled_len)
+    if n < 0 or n > seq_len:
+        raise ValueError("filled_len=%d must lie in [0, %d]" % (n, seq_len))
+    return torch.full((1,), n, dtype=torch.int32, device=device)
+
+
+def _partials(heads: int, num_splits: int, head_dim: int, device: Any):
+    import torch  # noqa: PLC0415
+
+    m = torch.empty((heads, num_splits), dtype=torch.float32, device=device)
+    l = torch.empty((heads, num_splits), dtype=torch.float32, device=device)
+    acc = torch.empty((heads, num_splits, head_dim), dtype=torch.float32, device=device)
+    return m, l, acc
+
+
+def attn_decode_forward(
+    q: Any,
+    k: Any,
+    v: Any,
+    filled_len: Any,
+    *,
+    config: dict[str, Any] | None = None,
+    backend: str = "auto",
+    scale: float | None = None,
+) -> Any:
+    """``q (1,H,1,D)`` + whole static fp16 cache ``k, v (1,H,S,D)`` -> ``(1,H,1,D)`` fp16."""
+    import torch  # noqa: PLC0415
+
+    cfg = merged_config(config)
+    if backend not in ("auto", "hip", "triton", "oracle"):
+        raise ValueError("unknown backend %r" % (backend,))
+    if backend == "oracle":
+        raise NotImplementedError(
+            "backend='oracle' is the CPU restatement kept with the tests; no CPU path here"
+        )
+    for name, tensor in (("q", q), ("k", k), ("v", v)):
+        if not torch.is_tensor(tensor):
+            raise TypeError("%s must be a tensor" % name)
+        if tensor.dim() != 4:
+            raise ValueError("%s must be 4-D, got %s" % (name, tuple(tensor.shape)))
+        if tensor.stride(-1) != 1:
+            raise ValueError("%s must be contiguous in the last dimension" % name)
+    if int(q.shape[2]) != 1 or int(q.shape[0]) != 1:
+        raise NotImplementedError("attn_decode handles batch=1 / q_len=1 only")
+    if tuple(k.shape) != tuple(v.shape):
+        raise ValueError("k and v must have the same shape")
+    if int(k.shape[0]) != 1 or int(k.shape[3]) != int(q.shape[3]):
+        raise ValueError("k/v must be batch 1 with the head_dim of q")
+    if q.device != k.device or q.device != v.device:
+        raise ValueError("q/k/v must be on one device")
+    if int(q.shape[1]) < 1 or int(k.shape[2]) < 1:
+        raise ValueError("heads and cache capacity must be positive")
+    if k.stride(2) != k.shape[3] or v.stride(2) != v.shape[3]:
+        raise ValueError("the k/v sequence stride must equal head_dim")
+    if k.stride(1) != v.stride(1) or k.stride(1) < k.shape[2] * k.shape[3]:
+        raise ValueError("k/v need one non-overlapping head stride")
+    if int(k.shape[1]) != int(q.shape[1]):
+        raise NotImplementedError("attn_decode does not do GQA")
+    if k.dtype != v.dtype:
+        raise ValueError("k/v dtypes differ")
+    if q.dtype != k.dtype:
+        raise ValueError("q and k/v dtypes differ (%s vs %s)" % (q.dtype, k.dtype))
+    if q.dtype != torch.float16:
+        raise ValueError("the HIP attention supports fp16 only")
+    heads, head_dim, seq_len = int(q.shape[1]), int(q.shape[3]), int(k.shape[2])
+    if head_dim not in SUPPORTED_HEAD_DIMS:
+        raise NotImplementedError("head_dim must be one of %s" % (SUPPORTED_HEAD_DIMS,))
+    filled = _filled_tensor(filled_len, device=q.device, seq_len=seq_len)
+    _hip.require_rocm(q, k, v, filled, what="attn_decode_forward")
+    num_splits = resolve_num_splits(cfg.get("num_splits"), heads=heads, device=q.device)
+    plan = launch_plan(heads=heads, head_dim=head_dim, num_splits=num_splits)
+    qc = q.reshape(heads, head_dim).contiguous()
+    m, l, acc = _partials(heads, num_splits, head_dim, q.device)
+    out = torch.empty(plan["combine"]["out_shape"], dtype=torch.float16, device=q.device)
+    qk_scale = (scale if scale is not None else 1.0 / math.sqrt(head_dim)) * LOG2E
+    st = _hip.stream_of(q.device)
+    # The capacity the kernel clamps `filled` to is head_stride / D >= S.
+    _hip.call(
+        "lemoq_attn_split_f16",
+        _hip.ptr(qc), _hip.ptr(k), _hip.ptr(v), int(k.stride(1)), _hip.ptr(filled),
+        heads, head_dim, num_splits, float(qk_scale),
+        _hip.ptr(m), _hip.ptr(l), _hip.ptr(acc), st,
+    )
+    _hip.call(
+        "lemoq_attn_merge",
+        _hip.ptr(m), _hip.ptr(l), _hip.ptr(acc), heads, num_splits, head_dim, _hip.ptr(out), st,
+    )
+    return out
+
+
+def attn_decode_forward_int8(
+    q: Any,
+    k_codes: Any,
+    k_scale: Any,
+    v_codes: Any,
+    v_scale: Any,
+    filled_len: Any,
+    *,
+    config: dict[str, Any] | None = None,
+    scale: float | None = None,
+) -> Any:
+    """``q (1,H,1,D)`` + int8 cache ``(1,H,S,D)`` with fp16 per-token scales ``(1,H,S)``."""
+    import torch  # noqa: PLC0415
+
+    cfg = merged_config(config)
+    for name, tensor in (("q", q), ("k_codes", k_codes), ("v_codes", v_codes)):
+        if not torch.is_tensor(tensor) or tensor.dim() != 4:
+            raise ValueError("%s must be a 4-D tensor" % name)
+        if tensor.stride(-1) != 1:
+            raise ValueError("%s must be contiguous in the last dimension" % name)
+    for name, tensor in (("k_scale", k_scale), ("v_scale", v_scale)):
+        if not torch.is_tensor(tensor) or tensor.dim() != 3:
+            raise ValueError("%s must be 3-D (1,H,S)" % name)
+    if k_codes.dtype != torch.int8 or v_codes.dtype != torch.int8:
+        raise ValueError("codes must be int8")
+    if k_scale.dtype != torch.float16 or v_scale.dtype != torch.float16:
+        raise ValueError("scales must be fp16")
+    if int(q.shape[2]) != 1 or int(q.shape[0]) != 1:
+        raise NotImplementedError("int8 attention handles batch=1 / q_len=1 only")
+    heads, seq_len, head_dim = int(k_codes.shape[1]), int(k_codes.shape[2]), int(k_codes.shape[3])
+    if tuple(k_codes.shape) != tuple(v_codes.shape) or int(q.shape[1]) != heads:
+        raise ValueError("k/v codes must match and have q's head count")
+    if tuple(k_scale.shape) != (1, heads, seq_len) or tuple(v_scale.shape) != (1, heads, seq_len):
+        raise ValueError("scales must be (1,H,S)")
+    if q.dtype != torch.float16:
+        raise ValueError("q must be fp16")
+    if head_dim not in SUPPORTED_HEAD_DIMS:
+        raise NotImplementedError("head_dim must be one of %s" % (SUPPORTED_HEAD_DIMS,))
+    for name, t in (("k_codes", k_codes), ("v_codes", v_codes), ("k_scale", k_scale), ("v_scale", v_scale)):
+        if not t.is_contiguous():
+            raise ValueError("%s must be contiguous" % name)
+    _hip.require_rocm(q, k_codes, k_scale, v_codes, v_scale, what="attn_decode_forward_int8")
+    filled = _filled_tensor(filled_len, device=q.device, seq_len=seq_len)
+    num_splits = resolve_num_splits(cfg.get("num_splits"), heads=heads, device=q.device)
+    plan = launch_plan(heads=heads, head_dim=head_dim, num_splits=num_splits)
+    qc = q.reshape(heads, head_dim).contiguous()
+    m, l, acc = _partials(heads, num_splits, head_dim, q.device)
+    out = torch.empty(plan["combine"]["out_shape"], dtype=torch.float16, device=q.device)
+    qk_scale = (scale if scale is not None else 1.0 / math.sqrt(head_dim)) * LOG2E
+    st = _hip.stream_of(q.device)
+    _hip.call(
+        "lemoq_attn_split_i8",
+        _hip.ptr(qc), _hip.ptr(k_codes), _hip.ptr(k_scale), _hip.ptr(v_codes), _hip.ptr(v_scale),
+        int(k_codes.stride(1)), seq_len, _hip.ptr(filled), heads, head_dim, num_splits,
+        float(qk_scale), _hip.ptr(m), _hip.ptr(l), _hip.ptr(acc), st,
+    )
+    _hip.call(
+        "lemoq_attn_merge",
+        _hip.ptr(m), _hip.ptr(l), _hip.ptr(acc), heads, num_splits, head_dim, _hip.ptr(out), st,
+    )
+    return out
+
+
+def warm(*, heads: int, head_dim: int, kv_len: int, filled: int | None = None, device: Any = None,
+         config: dict[str, Any] | None = None, **_: Any) -> dict[str, Any]:
+    """One real launch before capture (HIP code needs no JIT; kept for compatibility)."""
+    import torch  # noqa: PLC0415
+
+    dev = torch.device(device if device is not None else "cuda")
+    q = torch.zeros((1, heads, 1, head_dim), dtype=torch.float16, device=dev)
+    k = torch.zeros((1, heads, kv_len, head_dim), dtype=torch.float16, device=dev)
+    n = int(filled if filled is not None else kv_len)
+    attn_decode_forward(q, k, k.clone(), torch.full((1,), n, dtype=torch.int32, device=dev), config=config)
+    torch.cuda.synchronize(dev)
+    cfg = merged_config(config)
+    return {
+        "heads": int(heads),
+        "head_dim": int(head_dim),
+        "kv_len": int(kv_len),
+        "filled": n,
+        "num_splits": resolve_num_splits(cfg.get("num_splits"), heads=int(heads), device=dev),
+    }

@@ -1,0 +1,371 @@
+"""OLMoE decode-step module on the HIP kernels: weights, KV-INT8 cache, session.
+
+This replaces the reference's HF-patched model + ``StaticCacheDecodeSession``
+(``benchmarks/cudagraph.py:511-820``) for the canonical cell
+``--moe grouped --dequant fused --attn kernel --execution cudagraph
+--bit-width w8a16`` with W8 lm_head and KV-INT8 (``runner.py:2447-2521``,
+``fusion_switches.py:49-57``):
+
+* ``OlmoeShape`` — the model shape (OLMoE-1B-7B by default: H 2048, 16 layers,
+  16 heads x 128, 64 experts top-8, F 1024, vocab 50304).
+* ``OlmoeW8Weights.random(shape, seed)`` — seeded random init generated and
+  RTN-w8-quantized on the device (attention q|k|v packed row-wise, o_proj,
+  experts, lm_head); router, embedding and norm weights stay fp16.
+* ``DecodeSession`` — fixed-address KV-INT8 cache and step buffers, the step
+  enqueued by one native call (``lemoq_olmoe_decode_step``), captured once
+  into a hipGraph (``torch.cuda.CUDAGraph``) and replayed.  Greedy selection
+  and the position advance run on the device, so consecutive replays need no
+  host round trip; prompt tokens are fed by the same step (prefill = one
+  replay per prompt position).
+
+Layout in HBM (per layer): ``qkv_codes`` (3*heads*D, H) int8 with fp16 scales
+(3*heads*D, H/g); ``o_codes`` (H, heads*D); ``gu_codes`` (E, 2F, H) and
+``dn_codes`` (E, H, F) int8 with per-group fp16 scales; ``kc``/``vc`` (heads, S, D)
+int8 and ``ks``/``vs`` (heads, S) fp16 for S = max_seq cache slots.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from dataclasses import dataclass, field, fields
+from typing import Any
+
+import torch
+
+from lemoq import _hip
+
+__all__ = ["OlmoeShape", "OLMOE_1B_7B", "OlmoeW8Weights", "LayerW8", "DecodeSession"]
+
+LOG2E = 1.4426950408889634
+
+
+@dataclass(frozen=True)
+class OlmoeShape:
+    hidden: int = 2048
+    heads: int = 16
+    head_dim: int = 128
+    layers: int = 16
+    num_experts: int = 64
+    top_k: int = 8
+    ffn: int = 1024
+    vocab: int = 50304
+    eps: float = 1e-5
+    rope_theta: float = 10000.0
+    norm_topk_prob: bool = False
+    group_size: int = 128
+    init_std: float = 0.02
+
+    @property
+    def qkv_rows(self) -> int:
+        return 3 * self.heads * self.head_dim
+
+    def weight_bytes_per_token(self) -> int:
+        """Bytes of weights one decode step streams (w8 codes + fp16 scales, fp16 rest)."""
+        H, HD, F, g = self.hidden, self.heads * self.head_dim, self.ffn, self.group_size
+        w8 = lambda rows, cols: rows * cols + rows * (cols // g) * 2  # noqa: E731
+        per_layer = (
+            w8(3 * HD, H)
+            + w8(H, HD)
+            + self.top_k * (w8(2 * F, H) + w8(H, F))
+            + self.num_experts * H * 2  # fp16 router
+            + 4 * H * 2  # ln_in, ln_post (H) and q_norm, k_norm (HD == H for OLMoE)
+        )
+        return self.layers * per_layer + w8(self.vocab, H) + H * 2 + H * 2
+
+
+OLMOE_1B_7B = OlmoeShape()
+
+
+@dataclass
+class LayerW8:
+    ln_in: Any
+    ln_post: Any
+    q_norm: Any
+    k_norm: Any
+    qkv_codes: Any
+    qkv_scale: Any
+    o_codes: Any
+    o_scale: Any
+    router: Any
+    gu_codes: Any
+    gu_scale: Any
+    dn_codes: Any
+    dn_scale: Any
+
+
+@dataclass
+class OlmoeW8Weights:
+    shape: OlmoeShape
+    embed: Any
+    final_norm: Any
+    lm_codes: Any
+    lm_scale: Any
+    layers: list[LayerW8] = field(default_factory=list)
+
+    @property
+    def device(self) -> Any:
+        return self.embed.device
+
+    def to_host(self) -> "OlmoeW8Weights":
+        """Copy every tensor to the CPU (the form the CPU oracle consumes)."""
+        cpu = lambda t: t.detach().to("cpu")  # noqa: E731
+        return OlmoeW8Weights(
+            shape=self.shape,
+            embed=cpu(self.embed),
+            final_norm=cpu(self.final_norm),
+            lm_codes=cpu(self.lm_codes),
+            lm_scale=cpu(self.lm_scale),
+            layers=[LayerW8(**{f.name: cpu(getattr(L, f.name)) for f in fields(LayerW8)}) for L in self.layers],
+        )
+
+    @classmethod
+    def random(cls, shape: OlmoeShape = OLMOE_1B_7B, *, seed: int = 0, device: Any = "cuda") -> "OlmoeW8Weights":
+        """Seeded random init on the device, RTN-w8-quantized by the HIP kernel.
+
+        Linear, expert, router and embedding weights ~ N(0, init_std) (the HF
+        ``_init_weights`` distribution); norm weights ~ U(0.5, 1.5) so that a
+        mixed-up norm weight changes the answer.  Generation order is fixed:
+        embedding, then per layer (ln_in, ln_post, q_norm, k_norm, q|k|v, o,
+        router, gate_up, down), then final norm, lm_head.
+        """
+        from lemoq.quant import rtn  # noqa: PLC0415
+
+        dev = torch.device(device)
+        _hip.require_rocm(torch.empty(0, device=dev), what="OlmoeW8Weights.random")
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(int(seed))
+        s = shape
+        g = s.group_size
+        HD = s.heads * s.head_dim
+
+        def normal(*size: int) -> Any:
+            return torch.randn(size, generator=gen, device=dev, dtype=torch.float32) * s.init_std
+
+        def gamma(n: int) -> Any:
+            return (torch.rand((n,), generator=gen, device=dev, dtype=torch.float32) + 0.5).to(torch.float16)
+
+        def q8(w: Any) -> tuple[Any, Any]:
+            q = rtn.quantize_rtn(w, bits=8, group_size=g)
+            return q["codes_padded"], q["scale_f16"]
+
+        embed = normal(s.vocab, s.hidden).to(torch.float16)
+        layers = []
+        for _ in range(s.layers):
+            ln_in, ln_post, qn, kn = gamma(s.hidden), gamma(s.hidden), gamma(HD), gamma(HD)
+            qkv_c, qkv_s = q8(normal(3 * HD, s.hidden))
+            o_c, o_s = q8(normal(s.hidden, HD))
+            router = normal(s.num_experts, s.hidden).to(torch.float16)
+            gu = normal(s.num_experts * 2 * s.ffn, s.hidden)
+            gu_c, gu_s = q8(gu)
+            del gu
+            dn = normal(s.num_experts * s.hidden, s.ffn)
+            dn_c, dn_s = q8(dn)
+            del dn
+            layers.append(
+                LayerW8(
+                    ln_in=ln_in, ln_post=ln_post, q_norm=qn, k_norm=kn,
+                    qkv_codes=qkv_c, qkv_scale=qkv_s, o_codes=o_c, o_scale=o_s, router=router,
+                    gu_codes=gu_c.reshape(s.num_experts, 2 * s.ffn, s.hidden),
+                    gu_scale=gu_s.reshape(s.num_experts, 2 * s.ffn, s.hidden // g),
+                    dn_codes=dn_c.reshape(s.num_experts, s.hidden, s.ffn),
+                    dn_scale=dn_s.reshape(s.num_experts, s.hidden, s.ffn // g),
+                )
+            )
+        final_norm = gamma(s.hidden)
+        lm_c, lm_s = q8(normal(s.vocab, s.hidden))
+        return cls(shape=s, embed=embed, final_norm=final_norm, lm_codes=lm_c, lm_scale=lm_s, layers=layers)
+
+
+class DecodeSession:
+    """Static-shape decode session over a KV-INT8 cache, captured as one hipGraph step.
+
+    Mirrors ``StaticCacheDecodeSession`` (``benchmarks/cudagraph.py:511-820``):
+    ``prefill()``, ``capture()``, ``replay()``, ``decode_eager()``,
+    ``set_position()``, ``logits_cpu()``, ``reset()``.  ``prompt_ids`` is a 1-D
+    sequence of token ids (the canonical prompt is ``ctx`` ones); the cache has
+    ``ctx + max_new_tokens`` slots.
+    """
+
+    def __init__(
+        self,
+        weights: OlmoeW8Weights,
+        prompt_ids: Any,
+        *,
+        max_new_tokens: int,
+        num_splits: int | None = None,
+    ) -> None:
+        from lemoq.kernels.attn_decode import resolve_num_splits  # noqa: PLC0415
+        from lemoq.kernels.rope import rotary_cos_sin  # noqa: PLC0415
+
+        s = weights.shape
+        dev = weights.device
+        _hip.require_rocm(weights.embed, what="DecodeSession")
+        prompt = torch.as_tensor(prompt_ids, dtype=torch.int64).reshape(-1)
+        if prompt.numel() < 1:
+            raise ValueError("prompt must hold at least one token")
+        if int(prompt.min()) < 0 or int(prompt.max()) >= s.vocab:
+            raise ValueError("prompt token ids must lie in [0, vocab)")
+        if max_new_tokens < 1:
+            raise ValueError("max_new_tokens must be >= 1")
+        self.weights = weights
+        self.shape = s
+        self.device = dev
+        self.ctx = int(prompt.numel())
+        self.max_new_tokens = int(max_new_tokens)
+        self.max_seq = self.ctx + self.max_new_tokens
+        self.num_splits = resolve_num_splits(num_splits, heads=s.heads, device=dev)
+        S, D, HD = self.max_seq, s.head_dim, s.heads * s.head_dim
+
+        i8 = dict(dtype=torch.int8, device=dev)
+        f16 = dict(dtype=torch.float16, device=dev)
+        self.kv = []
+        for _ in range(s.layers):
+            self.kv.append(
+                {
+                    "kc": torch.zeros((s.heads, S, D), **i8),
+                    "ks": torch.ones((s.heads, S), **f16),
+                    "vc": torch.zeros((s.heads, S, D), **i8),
+                    "vs": torch.ones((s.heads, S), **f16),
+                }
+            )
+        cos, sin = rotary_cos_sin(torch.arange(S), D, s.rope_theta)
+        self.cos_tab = cos.to(dev).contiguous()
+        self.sin_tab = sin.to(dev).contiguous()
+        self.prompt = prompt.to(dev)
+        self.token = torch.zeros((1,), dtype=torch.int64, device=dev)
+        self.pos = torch.zeros((1,), dtype=torch.int64, device=dev)
+        self.filled = torch.zeros((1,), dtype=torch.int32, device=dev)
+        self.history = torch.zeros((S + 1,), dtype=torch.int64, device=dev)
+        self.h = torch.zeros((s.hidden,), **f16)
+        self.xn = torch.zeros((s.hidden,), **f16)
+        self.qkv = torch.zeros((3 * HD,), **f16)
+        self.q_rot = torch.zeros((HD,), **f16)
+        self.attn = torch.zeros((HD,), **f16)
+        self.part_m = torch.zeros((s.heads * self.num_splits,), dtype=torch.float32, device=dev)
+        self.part_l = torch.zeros_like(self.part_m)
+        self.part_acc = torch.zeros((s.heads * self.num_splits * D,), dtype=torch.float32, device=dev)
+        self.router_logits = torch.zeros((s.num_experts,), **f16)
+        self.top_w = torch.zeros((s.top_k,), **f16)
+        self.top_i = torch.zeros((s.top_k,), dtype=torch.int64, device=dev)
+        self.act = torch.zeros((s.top_k, s.ffn), **f16)
+        self.logits = torch.zeros((s.vocab,), **f16)
+
+        P = _hip.ptr
+        self._layer_structs = (_hip.LemoqOlmoeLayer * s.layers)()
+        for i, (L, kv) in enumerate(zip(weights.layers, self.kv)):
+            ls = self._layer_structs[i]
+            for name in (
+                "ln_in", "ln_post", "q_norm", "k_norm", "qkv_codes", "qkv_scale", "o_codes",
+                "o_scale", "router", "gu_codes", "gu_scale", "dn_codes", "dn_scale",
+            ):
+                t = getattr(L, name)
+                if not t.is_contiguous() or t.device != dev:
+                    raise ValueError("layer %d weight %s must be contiguous on %s" % (i, name, dev))
+                setattr(ls, name, P(t))
+            for name in ("kc", "ks", "vc", "vs"):
+                setattr(ls, name, P(kv[name]))
+        st = _hip.LemoqOlmoeStep()
+        st.hidden, st.heads, st.head_dim = s.hidden, s.heads, s.head_dim
+        st.ffn, st.num_experts, st.top_k = s.ffn, s.num_experts, s.top_k
+        st.vocab, st.group, st.num_layers = s.vocab, s.group_size, s.layers
+        st.max_seq, st.num_splits, st.norm_topk_prob = S, self.num_splits, int(bool(s.norm_topk_prob))
+        st.eps = float(s.eps)
+        st.qk_scale = float((1.0 / math.sqrt(D)) * LOG2E)
+        st.layers = ctypes.cast(self._layer_structs, ctypes.POINTER(_hip.LemoqOlmoeLayer))
+        st.embed, st.final_norm = P(weights.embed), P(weights.final_norm)
+        st.lm_codes, st.lm_scale = P(weights.lm_codes), P(weights.lm_scale)
+        st.cos_tab, st.sin_tab = P(self.cos_tab), P(self.sin_tab)
+        st.token, st.pos, st.filled = P(self.token), P(self.pos), P(self.filled)
+        st.prompt, st.prompt_len = P(self.prompt), self.ctx
+        st.history, st.history_len = P(self.history), int(self.history.numel())
+        for name in ("h", "xn", "qkv", "q_rot", "attn", "part_m", "part_l", "part_acc",
+                     "router_logits", "top_w", "top_i", "act", "logits"):
+            setattr(st, name, P(getattr(self, name)))
+        self._step = st
+        self.graph: Any = None
+        self.stream: Any = None
+        self.reset()
+
+    # ------------------------------------------------------------------ state
+    def reset(self) -> None:
+        """Back to position 0 with the first prompt token (cache slots are overwritten as it runs)."""
+        self.token.copy_(self.prompt[:1])
+        self.pos.zero_()
+        self.filled.fill_(1)
+        self.history.zero_()
+        self.history[:1].copy_(self.prompt[:1])
+        torch.cuda.synchronize(self.device)
+
+    def set_position(self, position: int, token: int | None = None) -> None:
+        """Move the decode position (graph-safe: only device scalars change)."""
+        if position < 0 or position >= self.max_seq:
+            raise RuntimeError("position %d outside the cache capacity %d" % (position, self.max_seq))
+        self.pos.fill_(int(position))
+        self.filled.fill_(int(position) + 1)
+        if token is not None:
+            self.token.fill_(int(token))
+
+    @property
+    def position(self) -> int:
+        return int(self.pos.item())
+
+    # ------------------------------------------------------------------ steps
+    def _enqueue_step(self) -> None:
+        _hip.call("lemoq_olmoe_decode_step", ctypes.byref(self._step), _hip.stream_of(self.device))
+
+    def _check_room(self, n: int) -> None:
+        if self.position + n > self.max_seq:
+            raise RuntimeError("decode position would exceed the cache capacity %d" % self.max_seq)
+
+    def decode_eager(self) -> Any:
+        """One step without the graph; returns the step's fp16 logits (device)."""
+        self._check_room(1)
+        self._enqueue_step()
+        return self.logits
+
+    def capture(self) -> dict[str, Any]:
+        """Capture one decode step into a hipGraph (state is untouched by the capture)."""
+        if self.graph is not None:
+            return {"capture_success": True}
+        self.stream = torch.cuda.Stream(device=self.device)
+        self.stream.wait_stream(torch.cuda.current_stream(self.device))
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=self.stream):
+            self._enqueue_step()
+        torch.cuda.synchronize(self.device)
+        self.graph = graph
+        return {"capture_success": True, "launches_per_step": 8 * self.shape.layers + 2}
+
+    def replay(self, n: int = 1, *, synchronize: bool = True) -> Any:
+        """Replay the captured step ``n`` times back to back; returns the last logits."""
+        if self.graph is None:
+            raise RuntimeError("capture() must succeed before replay()")
+        self._check_room(n) if synchronize else None
+        for _ in range(int(n)):
+            self.graph.replay()
+        if synchronize:
+            torch.cuda.synchronize(self.device)
+        return self.logits
+
+    def prefill(self) -> int:
+        """Run the prompt through the step (one replay per position); returns the seed token."""
+        if self.graph is None:
+            self.capture()
+        self.reset()
+        self.replay(self.ctx)
+        return int(self.token.item())
+
+    def generated(self) -> list[int]:
+        """Tokens chosen after the prompt so far (device history -> host)."""
+        p = self.position
+        return [int(t) for t in self.history[self.ctx : p + 1].tolist()]
+
+    def logits_cpu(self) -> Any:
+        torch.cuda.synchronize(self.device)
+        return self.logits.detach().to("cpu").clone()
+
+    def kv_cpu(self) -> list[dict[str, Any]]:
+        """Host copy of every layer's KV-INT8 cache (for the CPU oracle)."""
+        torch.cuda.synchronize(self.device)
+        return [{k: v.detach().to("cpu").clone() for k, v in kv.items()} for kv in self.kv]

@@ -1,0 +1,24 @@
+"""CPU oracle of the lemoq batch-1 OLMoE decode path — TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
+``bench.py`` may import anything under ``oracle/``, and only as the checker
+(or the timed CPU baseline), never as a product path.  The package
+``lemoq`` (``leanmoe-quant_amd/lemoq``) must not import it.
+
+Contents (each function cites the reference file:line it restates):
+
+* ``oracle.quant``  — numpy: per-group RTN w8 (``src/lemoq/quant/numpy_oracle.py``),
+  per-token KV-INT8 (``src/lemoq/kernels/kv_int8.py``), the routing order
+  (``tests/test_routing_fusion.py:24-35``).  Bit-exact targets.
+* ``oracle.cref``   — ctypes binding of ``oracle/c/quant_ref.c``, a second,
+  independent plain-C restatement of the two bit-exact quantisers.
+* ``oracle.ops``    — torch-CPU restatements of the floating-point operators
+  (dequant GEMV, grouped MoE, split-KV attention fp16/int8 + merge, dense
+  attention, RMSNorm, RoPE, router), in the reference's op order.
+* ``oracle.olmoe``  — the full decode step on the CPU (HF OLMoE decoder math
+  with the reference's patched operators), and a seeded tiny-model init.
+
+How each function is pinned (golden vectors, closed forms, brute force,
+independent restatements, HF transformers) is listed per function in
+DESIGN.md and exercised by ``tests/test_oracle_*.py``.
+"""

@@ -1,0 +1,216 @@
+"""CPU decode step of the OLMoE w8a16 + W8 lm_head + KV-INT8 cell.
+
+Test infrastructure (see ``oracle/__init__.py``).  ``OracleDecoder.step``
+restates, on CPU tensors, the HF OLMoE decoder (transformers
+``OlmoeModel``/``OlmoeDecoderLayer``/``OlmoeAttention``/``OlmoeSparseMoeBlock``)
+as patched by the reference's canonical cell:
+
+* packed q|k|v via the fused w8 GEMV (``src/lemoq/kernels/packed_qkv.py:78-96``);
+  q_norm/k_norm over heads*D, fused RoPE (``rope.py:154-203``);
+* KV-INT8 write of the new row then split-KV INT8 attention over
+  ``[0, pos+1)`` (``attn_decode.py:952-1000``, ``kv_int8.py:223-257``);
+* o_proj, fp16 residual add; post-attention norm; ``_route``; grouped w8 MoE
+  (``moe_grouped_quant.py:562-601``); fp16 residual add;
+* final norm, W8 lm_head; greedy argmax (first index on ties).
+
+Weights come as plain CPU tensors with the same field names as
+``lemoq.model.olmoe.OlmoeW8Weights``.  Static weights (q|k|v, o, lm_head) are
+dequantised once; experts are dequantised when selected.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+from typing import Any
+
+import numpy as np
+import torch
+
+from oracle import ops
+from oracle import quant as oq
+
+LOG2E = 1.4426950408889634
+
+
+@dataclass(frozen=True)
+class Shape:
+    hidden: int = 2048
+    heads: int = 16
+    head_dim: int = 128
+    layers: int = 16
+    num_experts: int = 64
+    top_k: int = 8
+    ffn: int = 1024
+    vocab: int = 50304
+    eps: float = 1e-5
+    rope_theta: float = 10000.0
+    norm_topk_prob: bool = False
+    group_size: int = 128
+    init_std: float = 0.02
+
+
+@dataclass
+class HostLayer:
+    ln_in: Any
+    ln_post: Any
+    q_norm: Any
+    k_norm: Any
+    qkv_codes: Any
+    qkv_scale: Any
+    o_codes: Any
+    o_scale: Any
+    router: Any
+    gu_codes: Any
+    gu_scale: Any
+    dn_codes: Any
+    dn_scale: Any
+
+
+@dataclass
+class HostWeights:
+    shape: Any
+    embed: Any
+    final_norm: Any
+    lm_codes: Any
+    lm_scale: Any
+    layers: list = field(default_factory=list)
+
+
+def random_host_weights(shape: Shape, seed: int = 0) -> HostWeights:
+    """Seeded CPU init for tiny CPU-only oracle tests (numpy RTN; not the device generator)."""
+    g = torch.Generator().manual_seed(seed)
+    s = shape
+    HD = s.heads * s.head_dim
+
+    def normal(*size: int) -> Any:
+        return torch.randn(size, generator=g, dtype=torch.float32) * s.init_std
+
+    def gamma(n: int) -> Any:
+        return (torch.rand((n,), generator=g, dtype=torch.float32) + 0.5).to(torch.float16)
+
+    def q8(w: Any):
+        q = oq.rtn_quantize_w8(w.numpy(), s.group_size)
+        return torch.from_numpy(q["codes_padded"]), torch.from_numpy(q["scale_f16"])
+
+    embed = normal(s.vocab, s.hidden).to(torch.float16)
+    layers = []
+    for _ in range(s.layers):
+        ln_in, ln_post, qn, kn = gamma(s.hidden), gamma(s.hidden), gamma(HD), gamma(HD)
+        qkv_c, qkv_s = q8(normal(3 * HD, s.hidden))
+        o_c, o_s = q8(normal(s.hidden, HD))
+        router = normal(s.num_experts, s.hidden).to(torch.float16)
+        gu_c, gu_s = q8(normal(s.num_experts * 2 * s.ffn, s.hidden))
+        dn_c, dn_s = q8(normal(s.num_experts * s.hidden, s.ffn))
+        layers.append(HostLayer(
+            ln_in=ln_in, ln_post=ln_post, q_norm=qn, k_norm=kn, qkv_codes=qkv_c, qkv_scale=qkv_s,
+            o_codes=o_c, o_scale=o_s, router=router,
+            gu_codes=gu_c.reshape(s.num_experts, 2 * s.ffn, s.hidden),
+            gu_scale=gu_s.reshape(s.num_experts, 2 * s.ffn, s.hidden // s.group_size),
+            dn_codes=dn_c.reshape(s.num_experts, s.hidden, s.ffn),
+            dn_scale=dn_s.reshape(s.num_experts, s.hidden, s.ffn // s.group_size),
+        ))
+    final_norm = gamma(s.hidden)
+    lm_c, lm_s = q8(normal(s.vocab, s.hidden))
+    return HostWeights(shape=s, embed=embed, final_norm=final_norm, lm_codes=lm_c, lm_scale=lm_s, layers=layers)
+
+
+class OracleDecoder:
+    """CPU decode step with its own KV-INT8 cache of ``max_seq`` slots."""
+
+    def __init__(self, weights: Any, max_seq: int, *, kv: list | None = None) -> None:
+        self.w = weights
+        s = weights.shape
+        self.s = s
+        self.max_seq = int(max_seq)
+        g = s.group_size
+        self.qkv_w = [ops.dequant_w8(L.qkv_codes, L.qkv_scale, g) for L in weights.layers]
+        self.o_w = [ops.dequant_w8(L.o_codes, L.o_scale, g) for L in weights.layers]
+        self.lm_w = ops.dequant_w8(weights.lm_codes, weights.lm_scale, g)
+        cos, sin = ops.rotary_cos_sin(torch.arange(self.max_seq), s.head_dim, s.rope_theta)
+        self.cos, self.sin = cos, sin
+        if kv is None:
+            kv = [
+                {
+                    "kc": torch.zeros((s.heads, self.max_seq, s.head_dim), dtype=torch.int8),
+                    "ks": torch.ones((s.heads, self.max_seq), dtype=torch.float16),
+                    "vc": torch.zeros((s.heads, self.max_seq, s.head_dim), dtype=torch.int8),
+                    "vs": torch.ones((s.heads, self.max_seq), dtype=torch.float16),
+                }
+                for _ in range(s.layers)
+            ]
+        self.kv = kv
+        self.trace: dict[str, Any] = {}
+
+    @staticmethod
+    def _linear(x16: Any, w32: Any) -> Any:
+        """fused w8 GEMV numerics: fp32 accumulate, one fp16 rounding."""
+        return (x16.to(torch.float32).reshape(1, -1) @ w32.t()).reshape(-1).to(torch.float16)
+
+    def _quant_into(self, cache_c: Any, cache_s: Any, pos: int, rows16: Any) -> None:
+        codes, scales = oq.kv_quantize_rows(rows16.numpy())
+        cache_c[:, pos, :] = torch.from_numpy(codes)
+        cache_s[:, pos] = torch.from_numpy(scales)
+
+    def step(self, token: int, pos: int, *, keep_trace: bool = False) -> Any:
+        """Process ``token`` at position ``pos``; returns the fp16 logits (vocab,)."""
+        s, w = self.s, self.w
+        H, NH, D = s.hidden, s.heads, s.head_dim
+        HD = NH * D
+        if not (0 <= pos < self.max_seq):
+            raise ValueError("pos outside the cache")
+        qk_scale = (1.0 / math.sqrt(D))
+        h = w.embed[int(token)].clone()
+        cos, sin = self.cos[pos], self.sin[pos]
+        for li, L in enumerate(w.layers):
+            kv = self.kv[li]
+            r = h
+            xn = ops.rms_norm(h, L.ln_in, s.eps)
+            qkv = self._linear(xn, self.qkv_w[li])
+            q, k, v = qkv[:HD], qkv[HD : 2 * HD], qkv[2 * HD :]
+            q = ops.rms_norm(q, L.q_norm, s.eps)
+            k = ops.rms_norm(k, L.k_norm, s.eps)
+            q = ops.rope_fused(q.reshape(NH, D), cos, sin)
+            k = ops.rope_fused(k.reshape(NH, D), cos, sin)
+            self._quant_into(kv["kc"], kv["ks"], pos, k)
+            self._quant_into(kv["vc"], kv["vs"], pos, v.reshape(NH, D))
+            attn = ops.int8_attention_folded(q, kv["kc"], kv["ks"], kv["vc"], kv["vs"], pos + 1,
+                                             scale=qk_scale).to(torch.float16).reshape(-1)
+            o = self._linear(attn, self.o_w[li])
+            h = r + o
+            r = h
+            xn = ops.rms_norm(h, L.ln_post, s.eps)
+            logits_r, top_w, top_i = ops.route(xn.reshape(1, -1), L.router, s.top_k, s.norm_topk_prob)
+            moe, act = ops.grouped_moe_w8(xn, L.gu_codes, L.gu_scale, L.dn_codes, L.dn_scale,
+                                          s.group_size, top_i.reshape(-1), top_w.reshape(-1))
+            h = r + moe
+            if keep_trace:
+                self.trace.setdefault("top_i", []).append(top_i.reshape(-1).clone())
+                self.trace.setdefault("h", []).append(h.clone())
+        hn = ops.rms_norm(h, w.final_norm, s.eps)
+        return self._linear(hn, self.lm_w)
+
+    def greedy(self, logits: Any) -> int:
+        """First index of the maximum (``torch.argmax``/``.item()`` of the reference session)."""
+        lf = logits.to(torch.float32).numpy()
+        return int(np.argmax(lf))
+
+    def run(self, prompt: list[int], new_tokens: int, *, start_pos: int = 0, seed_token: int | None = None):
+        """Prefill ``prompt`` by stepping it (positions start_pos..), then ``new_tokens`` greedy steps.
+
+        Returns ``(tokens, logits_per_decode_step)``; ``tokens[0]`` is the seed token.
+        """
+        pos = start_pos
+        logits = None
+        for t in prompt:
+            logits = self.step(int(t), pos)
+            pos += 1
+        tok = self.greedy(logits) if seed_token is None else int(seed_token)
+        tokens, all_logits = [tok], []
+        for _ in range(new_tokens):
+            logits = self.step(tok, pos)
+            all_logits.append(logits)
+            pos += 1
+            tok = self.greedy(logits)
+            tokens.append(tok)
+        return tokens, all_logits

@@ -1,0 +1,64 @@
+"""CPU checks of the C-ABI library: it loads without a GPU and exports every
+symbol include/lemoq_hip.h declares, with the status strings of the header."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "lemoq_hip.h")
+
+
+def _declared_functions() -> list[str]:
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(lemoq_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_expected_entry_points():
+    names = _declared_functions()
+    assert "lemoq_olmoe_decode_step" in names and "lemoq_gemv_w8" in names
+    assert len(names) >= 19
+
+
+def test_library_exports_every_declared_symbol():
+    from lemoq import _hip
+
+    if not _hip.library_available():
+        pytest.fail("liblemoq_hip.so is not built; run __graft_entry__.build()")
+    lib = ctypes.CDLL(_hip.LIB_PATH)
+    missing = [n for n in _declared_functions() if not hasattr(lib, n)]
+    assert not missing, missing
+    # every declared function has a typed ctypes signature
+    assert sorted(_hip.SIGNATURES) == _declared_functions()
+
+
+def test_status_strings_and_abi():
+    from lemoq import _hip
+
+    lib = _hip.load()
+    assert lib.lemoq_abi_version() == _hip.ABI_VERSION
+    assert lib.lemoq_status_string(0) == b"ok"
+    assert b"NULL" in lib.lemoq_status_string(-1)
+    assert b"unknown" in lib.lemoq_status_string(-99)
+
+
+def test_argument_rejection_happens_before_any_launch():
+    """Invalid arguments return a negative status without touching a device."""
+    from lemoq import _hip
+
+    lib = _hip.load()
+    assert lib.lemoq_gemv_w8(None, 1, 16, None, None, 16, 16, 16, None, 1, None) == -1
+    # aligned non-null fake pointers, bad group (not a multiple of 16): rejected as unsupported
+    fake = 4096
+    assert lib.lemoq_gemv_w8(fake, 1, 128, fake, fake, 8, 128, 8, fake, 1, None) == -3
+    assert lib.lemoq_gemv_w8(fake, 1, 128, fake + 1, fake, 8, 128, 128, fake, 1, None) == -4
+    assert lib.lemoq_attn_split_i8(fake, fake, fake, fake, fake, 128 * 10, 10, fake, 16, 96, 4, 1.0,
+                                   fake, fake, fake, None) == -3
+    assert lib.lemoq_route_topk(fake, 1, 1, 2000, 2000, 8, 0, fake, fake, None) == -2
+    with pytest.raises(ValueError):
+        _hip.call("lemoq_gemv_w8", None, 1, 16, None, None, 16, 16, 16, None, 1, None)

@@ -1,0 +1,427 @@
+"""GPU parity of the floating-point operators against the CPU oracle.
+
+Cases mirror the reference's K1 gates: tests/test_kernel_parity.py:134-282
+(dequant GEMV m in {1,4}, k in {2048,256,500,512,1024}; grouped MoE vs fp64),
+tests/test_attn_decode.py:421-494 and tests/test_fusion_adversarial.py:72-85
+(split-KV vs fp64, filled in {0,1,17}, NaN tail, length change),
+tests/test_kv_int8_read_gpu.py:90-146 (int8 attention vs dequant fp64),
+tests/test_rmsnorm_parity.py:31-58, tests/test_fused_rope.py:114-143,
+tests/test_routing_fusion.py:72-119, tests/test_packed_qkv.py:152-174.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import ATOL, RTOL, assert_close, assert_gate, max_abs, randn
+from oracle import ops
+from oracle import quant as oq
+
+pytestmark = pytest.mark.gpu
+
+
+def _q8(w: torch.Tensor, group: int):
+    q = oq.rtn_quantize_w8(w.numpy(), group)
+    return torch.from_numpy(q["codes_padded"]), torch.from_numpy(q["scale_f16"])
+
+
+# ---------------------------------------------------------------------------
+# dense w8 GEMV
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("m", [1, 4])
+@pytest.mark.parametrize("k", [2048, 256, 500, 512, 1024])
+def test_dequant_gemm_fused_vs_fp64(m, k, dev):
+    from lemoq.kernels.dequant_gemm import dequant_gemm_fused
+
+    n = 384
+    group = 128
+    w = randn(n, k, seed=k + m, std=0.02)
+    codes, scale = _q8(w, group)
+    x = (randn(m, k, seed=7 * k + m) * 0.5).to(torch.float16)
+    w64 = ops.dequant_w8(codes, scale, group)[:, :k].double()
+    ref64 = x.double() @ w64.t()
+    # fp32 output: the reference's K1 gate against the separate (dequantise-then-GEMM) arm
+    got32 = dequant_gemm_fused(x.to(dev), codes.to(dev), scale.to(dev), None, group_size=group, bits=8)
+    assert got32.dtype == torch.float32
+    baseline = ops.dequant_gemm_separate(x, codes, scale, group)
+    assert_gate(got32.cpu(), ref64, baseline, what="gemv fp32 m=%d k=%d" % (m, k))
+    # fp16 output (the decode path): BASELINE tolerance against fp64
+    got = dequant_gemm_fused(x.to(dev), codes.to(dev), scale.to(dev), None, group_size=group,
+                             bits=8, out_dtype=torch.float16)
+    assert_close(got.cpu(), ref64, what="gemv fp16 m=%d k=%d" % (m, k))
+    assert torch.equal(got.cpu(), got32.cpu().to(torch.float16))
+
+
+@pytest.mark.parametrize("n", [6144, 2048, 50304])
+def test_dequant_gemm_olmoe_shapes(n, dev):
+    from lemoq.kernels.dequant_gemm import dequant_gemm_fused
+
+    k = 2048
+    w = randn(n, k, seed=n, std=0.02)
+    codes, scale = _q8(w, 128)
+    x = randn(1, k, seed=n + 1).to(torch.float16)
+    got = dequant_gemm_fused(x.to(dev), codes.to(dev), scale.to(dev), None, group_size=128,
+                             bits=8, out_dtype=torch.float16).cpu()
+    ref = ops.dequant_gemm_fused_tiles(x, codes, scale, 128)
+    assert_close(got, ref, what="gemv N=%d" % n)
+
+
+def test_packed_qkv_bitwise_equals_three_calls(dev):
+    from lemoq.kernels.packed_qkv import pack_qkv
+    from lemoq.quant.linear import QuantLinear
+
+    projs = [QuantLinear(randn(2048, 2048, seed=s, std=0.02).to(dev)) for s in (1, 2, 3)]
+    packed = pack_qkv(*projs)
+    x = randn(1, 1, 2048, seed=9).to(torch.float16).to(dev)
+    q, k, v = packed.project(x)
+    for got, proj in zip((q, k, v), projs):
+        assert torch.equal(got, proj(x))
+
+
+def test_gemv_fused_norm_and_residual(dev):
+    from lemoq import _hip
+
+    H, N = 2048, 2048
+    w = randn(N, H, seed=21, std=0.02)
+    codes, scale = _q8(w, 128)
+    x = randn(H, seed=22).to(torch.float16)
+    gamma = (torch.rand(H, generator=torch.Generator().manual_seed(23)) + 0.5).to(torch.float16)
+    resid = randn(N, seed=24).to(torch.float16)
+    y = resid.clone().to(dev)
+    # keep every device tensor referenced until the kernel has run
+    xd, gd, cd, sd = x.to(dev), gamma.to(dev), codes.to(dev), scale.to(dev)
+    _hip.call("lemoq_gemv_w8_fused", _hip.ptr(xd), None, 0, _hip.ptr(gd), 1e-5, None,
+              _hip.ptr(cd), _hip.ptr(sd), N, H, 128, _hip.ptr(y), _hip.ptr(y), _hip.stream_of(dev))
+    torch.cuda.synchronize()
+    xn = ops.rms_norm(x, gamma, 1e-5)
+    ref = (ops.dequant_gemm_separate(xn.reshape(1, -1), codes, scale, 128).reshape(-1)
+           .to(torch.float16) + resid)
+    assert_close(y.cpu(), ref, what="norm+gemv+residual")
+
+
+# ---------------------------------------------------------------------------
+# routing
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("norm", [False, True])
+@pytest.mark.parametrize("e,k", [(64, 8), (12, 3), (8, 8), (100, 5)])
+def test_routing_softmax_topk_vs_oracle(norm, e, k, dev):
+    from lemoq.kernels.routing import routing_softmax_topk
+
+    logits = randn(7, e, seed=e * 10 + k)
+    ref_w, ref_i = oq.route_order(logits.numpy(), k, norm)
+    got_w, got_i = routing_softmax_topk(logits.to(dev), top_k=k, norm_topk_prob=norm)
+    assert np.array_equal(got_i.cpu().numpy(), ref_i)
+    assert np.allclose(got_w.cpu().numpy(), ref_w, atol=1e-6, rtol=1e-5)
+
+
+@pytest.mark.parametrize("case", ["all_equal", "kth_boundary", "fp16_rounding"])
+def test_routing_ties_lowest_index(case, dev):
+    from lemoq.kernels.routing import routing_softmax_topk
+
+    logits = torch.zeros(1, 64)
+    if case == "kth_boundary":
+        logits[:, :7] = torch.arange(8, 1, -1).float()
+    elif case == "fp16_rounding":
+        logits = (torch.ones_like(logits) + torch.arange(64) * 1e-6).half().float()
+    ref_w, ref_i = oq.route_order(logits.numpy(), 8, False)
+    got_w, got_i = routing_softmax_topk(logits.to(dev), top_k=8)
+    assert np.array_equal(got_i.cpu().numpy(), ref_i), (case, got_i, ref_i)
+    assert np.allclose(got_w.cpu().numpy(), ref_w, atol=1e-6)
+
+
+@pytest.mark.parametrize("norm", [False, True])
+def test_fused_router_vs_oracle(norm, dev):
+    from lemoq.kernels.moe_static import _route
+
+    for seed in range(8):
+        x = randn(1, 2048, seed=100 + seed).to(torch.float16)
+        rw = randn(64, 2048, seed=200 + seed, std=0.02).to(torch.float16)
+        lg, tw, ti = _route(x.to(dev), rw.to(dev), top_k=8, norm_topk_prob=norm)
+        rlg, rtw, rti = ops.route(x, rw, 8, norm)
+        # logits: one fp16 rounding of an fp32 dot; summation order may move a value by 1 ulp
+        assert max_abs(lg.cpu(), rlg) <= 2e-3
+        assert np.array_equal(ti.cpu().numpy(), rti.numpy()), seed
+        assert torch.allclose(tw.cpu().float(), rtw.float(), atol=1e-3, rtol=0)
+        assert tw.dtype == torch.float16 and ti.dtype == torch.int64
+
+
+# ---------------------------------------------------------------------------
+# grouped MoE
+# ---------------------------------------------------------------------------
+def _experts(E, F, H, group, seed):
+    gu = randn(E * 2 * F, H, seed=seed, std=0.02)
+    dn = randn(E * H, F, seed=seed + 1, std=0.02)
+    gc, gs = _q8(gu, group)
+    dc, ds = _q8(dn, group)
+    return (gc.reshape(E, 2 * F, H), gs.reshape(E, 2 * F, H // group),
+            dc.reshape(E, H, F), ds.reshape(E, H, F // group))
+
+
+@pytest.mark.parametrize("E,F,H,K", [(64, 1024, 2048, 8), (8, 256, 512, 2), (16, 128, 1024, 4)])
+def test_grouped_moe_vs_fp64(E, F, H, K, dev):
+    from lemoq.kernels.moe_grouped_quant import QuantFusedExperts, grouped_moe_forward_quant
+
+    gc, gs, dc, ds = _experts(E, F, H, 128, seed=E + F)
+    q = QuantFusedExperts(gc.to(dev), gs.to(dev), dc.to(dev), ds.to(dev), bits=8, group_size=128)
+    x = randn(H, seed=3).to(torch.float16)
+    ids = torch.randperm(E, generator=torch.Generator().manual_seed(4))[:K]
+    w = torch.softmax(randn(K, seed=5), 0).to(torch.float16)
+    got = grouped_moe_forward_quant(x.to(dev), q, ids.to(dev), w.to(dev)).cpu()
+    ref, act_ref = ops.grouped_moe_w8(x, gc, gs, dc, ds, 128, ids, w)
+    # fp64 closed form on the dequantised weights with the fp16 act rounding point
+    gu64 = torch.stack([ops.dequant_w8(gc[e], gs[e], 128) for e in ids.tolist()]).double()
+    g = gu64[:, :F] @ x.double()
+    u = gu64[:, F:] @ x.double()
+    act64 = (g * torch.sigmoid(g) * u).to(torch.float16).double()
+    dn64 = torch.stack([ops.dequant_w8(dc[e], ds[e], 128) for e in ids.tolist()]).double()
+    out64 = ((dn64 @ act64.unsqueeze(-1)).squeeze(-1) * w.double().unsqueeze(1)).sum(0)
+    assert_close(got, out64, what="moe vs fp64")
+    assert_close(got, ref, what="moe vs oracle")
+
+
+def test_grouped_moe_linear_in_weights_and_residual(dev):
+    from lemoq.kernels.moe_grouped_quant import QuantFusedExperts, grouped_moe_forward_quant
+
+    E, F, H, K = 8, 256, 512, 2
+    gc, gs, dc, ds = _experts(E, F, H, 128, seed=77)
+    q = QuantFusedExperts(gc.to(dev), gs.to(dev), dc.to(dev), ds.to(dev), bits=8, group_size=128)
+    x = randn(H, seed=8).to(torch.float16).to(dev)
+    ids = torch.tensor([5, 2], device=dev)
+    w1 = torch.tensor([0.25, 0.5], dtype=torch.float16, device=dev)
+    y1 = grouped_moe_forward_quant(x, q, ids, w1).float()
+    y2 = grouped_moe_forward_quant(x, q, ids, w1 * 2).float()
+    assert_close(y2.cpu(), 2 * y1.cpu(), rtol=2e-3, atol=1e-4, what="linearity")
+    zero = grouped_moe_forward_quant(x, q, ids, torch.zeros_like(w1))
+    assert (zero == 0).all()
+    resid = randn(H, seed=9).to(torch.float16).to(dev)
+    yr = grouped_moe_forward_quant(x, q, ids, w1, residual=resid)
+    assert torch.equal(yr, (grouped_moe_forward_quant(x, q, ids, w1) + resid))
+
+
+def test_static_moe_forward_block(dev):
+    from lemoq.kernels.moe_grouped_quant import QuantFusedExperts, static_moe_forward_grouped_quant
+
+    E, F, H = 64, 1024, 2048
+    gc, gs, dc, ds = _experts(E, F, H, 128, seed=31)
+    q = QuantFusedExperts(gc.to(dev), gs.to(dev), dc.to(dev), ds.to(dev), bits=8, group_size=128)
+    x = randn(1, 1, H, seed=32).to(torch.float16)
+    rw = randn(E, H, seed=33, std=0.02).to(torch.float16)
+    for norm in (False, True):
+        out, logits = static_moe_forward_grouped_quant(x.to(dev), rw.to(dev), q, top_k=8,
+                                                      norm_topk_prob=norm, act_fn=torch.nn.functional.silu)
+        rl, rw8, ri = ops.route(x.reshape(1, H), rw, 8, norm)
+        ref, _ = ops.grouped_moe_w8(x.reshape(-1), gc, gs, dc, ds, 128, ri, rw8)
+        assert out.shape == (1, 1, H)
+        assert_close(out.cpu().reshape(-1), ref, what="static block norm=%s" % norm)
+
+
+# ---------------------------------------------------------------------------
+# attention
+# ---------------------------------------------------------------------------
+def _qkv(H, S, D, seed, qs=1.0):
+    q = randn(1, H, 1, D, seed=seed, std=qs).to(torch.float16)
+    k = randn(1, H, S, D, seed=seed + 1).to(torch.float16)
+    v = randn(1, H, S, D, seed=seed + 2).to(torch.float16)
+    return q, k, v
+
+
+@pytest.mark.parametrize("ctx", [1024, 4096])
+def test_attn_fp16_vs_fp64(ctx, dev):
+    from lemoq.kernels.attn_decode import attn_decode_forward
+
+    q, k, v = _qkv(16, ctx, 128, seed=ctx)
+    n = torch.tensor([ctx], dtype=torch.int32, device=dev)
+    got = attn_decode_forward(q.to(dev), k.to(dev), v.to(dev), n).cpu().reshape(16, 128)
+    ref64 = ops.dense_attention(q.reshape(16, 128), k[0], v[0], ctx)
+    base = ops.split_kv_oracle(q.reshape(16, 128), k[0], v[0], ctx, num_splits=11).to(torch.float16)
+    assert_gate(got, ref64, base, what="attn fp16 ctx=%d" % ctx)
+
+
+@pytest.mark.parametrize("splits", [1, 2, 3, 8, 17, 64])
+def test_attn_split_count_invariance(splits, dev):
+    from lemoq.kernels.attn_decode import attn_decode_forward
+
+    q, k, v = _qkv(4, 700, 128, seed=50)
+    n = torch.tensor([613], dtype=torch.int32, device=dev)
+    got = attn_decode_forward(q.to(dev), k.to(dev), v.to(dev), n, config={"num_splits": splits})
+    ref = ops.dense_attention(q.reshape(4, 128), k[0], v[0], 613)
+    assert_close(got.cpu().reshape(4, 128), ref, rtol=1e-3, atol=1e-3, what="splits=%d" % splits)
+
+
+@pytest.mark.parametrize("filled", [0, 1, 17])
+@pytest.mark.parametrize("D", [64, 128, 256])
+def test_attn_length_boundaries(filled, D, dev):
+    from lemoq.kernels.attn_decode import attn_decode_forward
+
+    q, k, v = _qkv(2, 17, D, seed=60 + D, qs=0.1)
+    n = torch.tensor([filled], dtype=torch.int32, device=dev)
+    got = attn_decode_forward(q.to(dev), k.to(dev), v.to(dev), n, config={"num_splits": 4})
+    ref = ops.dense_attention(q.reshape(2, D), k[0], v[0], filled).to(torch.float16)
+    assert torch.isfinite(got).all()
+    assert_close(got.cpu().reshape(2, D), ref, rtol=1e-3, atol=1e-3, what="filled=%d" % filled)
+    if filled == 0:
+        assert (got == 0).all()
+
+
+def test_attn_nan_tail_never_read(dev):
+    from lemoq.kernels.attn_decode import attn_decode_forward, attn_decode_forward_int8
+    from lemoq.kernels.kv_int8 import kv_int8_bulk_quantize
+
+    q, k, v = _qkv(16, 256, 128, seed=70)
+    k[:, :, 100:] = float("nan")
+    v[:, :, 100:] = float("nan")
+    n = torch.tensor([100], dtype=torch.int32, device=dev)
+    got = attn_decode_forward(q.to(dev), k.to(dev), v.to(dev), n)
+    assert torch.isfinite(got).all()
+    ref = ops.dense_attention(q.reshape(16, 128), k[0], v[0], 100)
+    assert_close(got.cpu().reshape(16, 128), ref, what="nan tail fp16")
+    bufs = kv_int8_bulk_quantize(k.to(dev), v.to(dev), filled=100)
+    bufs["ks"][0, :, 100:] = float("nan")
+    bufs["vs"][0, :, 100:] = float("nan")
+    got8 = attn_decode_forward_int8(q.to(dev), bufs["kc"], bufs["ks"], bufs["vc"], bufs["vs"], n)
+    assert torch.isfinite(got8).all()
+
+
+def test_attn_length_change_is_read_on_device(dev):
+    from lemoq.kernels.attn_decode import attn_decode_forward, judge_length_change
+
+    q, k, v = _qkv(16, 2048, 128, seed=80)
+    k[:, :, 1500:] *= 3.0  # make the late keys matter
+    v[:, :, 1500:] += 4.0
+    n = torch.tensor([1000], dtype=torch.int32, device=dev)
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    out = attn_decode_forward(qd, kd, vd, n)  # warm
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = attn_decode_forward(qd, kd, vd, n)
+    n.fill_(2000)
+    g.replay()
+    torch.cuda.synchronize()
+    ref_new = ops.dense_attention(q.reshape(16, 128), k[0], v[0], 2000)
+    ref_old = ops.dense_attention(q.reshape(16, 128), k[0], v[0], 1000)
+    verdict = judge_length_change(correct_err=max_abs(out.cpu().reshape(16, 128), ref_new),
+                                  stale_err=max_abs(ref_old, ref_new))
+    assert verdict["verdict"] == "PASS", verdict
+
+
+@pytest.mark.parametrize("ctx", [4096, 16384])
+def test_attn_int8_vs_fp64_dequant(ctx, dev):
+    from lemoq.kernels.attn_decode import attn_decode_forward_int8
+    from lemoq.kernels.kv_int8 import kv_int8_bulk_quantize
+
+    q, k, v = _qkv(16, ctx, 128, seed=ctx + 1)
+    bufs = kv_int8_bulk_quantize(k.to(dev), v.to(dev))
+    n = torch.tensor([ctx], dtype=torch.int32, device=dev)
+    got = attn_decode_forward_int8(q.to(dev), bufs["kc"], bufs["ks"], bufs["vc"], bufs["vs"], n)
+    kc, ks, vc, vs = (bufs[x][0].cpu() for x in ("kc", "ks", "vc", "vs"))
+    ref64 = ops.int8_attention_dequant(q.reshape(16, 128), kc, ks, vc, vs, ctx)
+    base = ops.int8_attention_folded(q.reshape(16, 128), kc, ks, vc, vs, ctx).to(torch.float16)
+    assert_gate(got.cpu().reshape(16, 128), ref64, base, what="attn int8 ctx=%d" % ctx)
+
+
+def test_attn_int8_partial_fill(dev):
+    from lemoq.kernels.attn_decode import attn_decode_forward_int8
+    from lemoq.kernels.kv_int8 import kv_int8_bulk_quantize
+
+    q, k, v = _qkv(16, 512, 128, seed=91)
+    bufs = kv_int8_bulk_quantize(k.to(dev), v.to(dev))
+    for filled in (1, 33, 300):
+        n = torch.tensor([filled], dtype=torch.int32, device=dev)
+        got = attn_decode_forward_int8(q.to(dev), bufs["kc"], bufs["ks"], bufs["vc"], bufs["vs"], n)
+        kc, ks, vc, vs = (bufs[x][0].cpu() for x in ("kc", "ks", "vc", "vs"))
+        ref = ops.int8_attention_dequant(q.reshape(16, 128), kc, ks, vc, vs, filled)
+        assert_close(got.cpu().reshape(16, 128), ref, rtol=1e-3, atol=1e-3, what="filled=%d" % filled)
+
+
+# ---------------------------------------------------------------------------
+# RMSNorm / RoPE
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("rows,H", [(1, 2048), (16, 128), (3, 1000)])
+def test_rmsnorm_vs_hf_formula(rows, H, dev):
+    from lemoq.kernels.rmsnorm import rms_norm_fused
+
+    x = randn(rows, H, seed=H).to(torch.float16)
+    w = (torch.rand(H, generator=torch.Generator().manual_seed(H + 1)) + 0.5).to(torch.float16)
+    got = rms_norm_fused(x.to(dev), w.to(dev), 1e-5).cpu()
+    ref = ops.rms_norm(x, w, 1e-5)
+    # fp16 rounding points are shared; the fp32 reduction order may move an element by 1 ulp
+    assert_close(got, ref, rtol=1e-3, atol=1e-3, what="rmsnorm")
+    assert (got.double() - ref.double()).abs().gt(0).float().mean() < 0.01
+
+
+@pytest.mark.parametrize("pos", [0, 1, 1024, 4096])
+def test_rope_fused_vs_oracle(pos, dev):
+    from lemoq.kernels.rope import apply_rotary_pos_emb_fused, rotary_cos_sin
+
+    q = randn(1, 16, 1, 128, seed=pos).to(torch.float16)
+    k = randn(1, 16, 1, 128, seed=pos + 1).to(torch.float16)
+    cos, sin = rotary_cos_sin([pos], 128)
+    qo, ko = apply_rotary_pos_emb_fused(q.to(dev), k.to(dev), cos.reshape(1, 1, 128).to(dev),
+                                        sin.reshape(1, 1, 128).to(dev))
+    rq = ops.rope_fused(q, cos[0], sin[0])
+    rk = ops.rope_fused(k, cos[0], sin[0])
+    assert_close(qo.cpu(), rq, rtol=1e-3, atol=1e-3, what="rope q")
+    assert_close(ko.cpu(), rk, rtol=1e-3, atol=1e-3, what="rope k")
+    hq, hk = ops.rope_hf(q.float(), k.float(), cos[0].float(), sin[0].float())
+    assert_close(qo.cpu(), hq, what="rope vs hf")
+
+
+def test_rope_strided_views(dev):
+    from lemoq.kernels.rope import apply_rotary_pos_emb_fused, rotary_cos_sin
+
+    base = randn(1, 1, 16, 128, seed=5).to(torch.float16).to(dev)
+    q = base.transpose(1, 2)  # (1,16,1,128) non-contiguous view
+    k = base.transpose(1, 2)[:, :8]
+    cos, sin = rotary_cos_sin([77], 128)
+    qo, ko = apply_rotary_pos_emb_fused(q, k, cos.reshape(1, 1, 128).to(dev), sin.reshape(1, 1, 128).to(dev))
+    rq = ops.rope_fused(q.cpu(), cos[0], sin[0])
+    assert_close(qo.cpu(), rq, rtol=1e-3, atol=1e-3, what="strided rope")
+    assert ko.shape == (1, 8, 1, 128)
+
+
+def test_qk_norm_rope_kv_fused_prologue(dev):
+    """The fused step prologue == rmsnorm -> rope -> per-token quant, codes bit-exact on its own k row."""
+    from lemoq import _hip
+    from lemoq.kernels.rope import rotary_cos_sin
+
+    NH, D, S, pos = 16, 128, 64, 37
+    HD = NH * D
+    qkv = randn(3 * HD, seed=1).to(torch.float16)
+    qn = (torch.rand(HD, generator=torch.Generator().manual_seed(2)) + 0.5).to(torch.float16)
+    kn = (torch.rand(HD, generator=torch.Generator().manual_seed(3)) + 0.5).to(torch.float16)
+    cos, sin = rotary_cos_sin(torch.arange(S), D)
+    kc = torch.zeros((NH, S, D), dtype=torch.int8, device=dev)
+    vc = torch.zeros_like(kc)
+    ks = torch.ones((NH, S), dtype=torch.float16, device=dev)
+    vs = torch.ones_like(ks)
+    q_out = torch.empty(HD, dtype=torch.float16, device=dev)
+    k_rot = torch.empty(HD, dtype=torch.float16, device=dev)
+    kf = torch.zeros((NH, S, D), dtype=torch.float16, device=dev)
+    vf = torch.zeros_like(kf)
+    P = _hip.ptr
+    # keep every device tensor referenced until the kernel has run
+    qkv_d, qn_d, kn_d, cos_d, sin_d = (t.to(dev) for t in (qkv, qn, kn, cos, sin))
+    pos_d = torch.tensor([pos], device=dev)
+    _hip.call("lemoq_qk_norm_rope_kv_i8", P(qkv_d), NH, D, P(qn_d), P(kn_d), 1e-5, P(cos_d), P(sin_d),
+              P(pos_d), P(q_out), P(kc), P(ks), P(vc), P(vs), S * D, S, P(kf), P(vf), S * D, P(k_rot),
+              _hip.stream_of(dev))
+    torch.cuda.synchronize()
+    q_ref = ops.rope_fused(ops.rms_norm(qkv[:HD], qn, 1e-5).reshape(NH, D), cos[pos], sin[pos])
+    k_ref = ops.rope_fused(ops.rms_norm(qkv[HD:2 * HD], kn, 1e-5).reshape(NH, D), cos[pos], sin[pos])
+    assert_close(q_out.cpu().reshape(NH, D), q_ref, rtol=1e-3, atol=1e-3, what="q")
+    assert_close(k_rot.cpu().reshape(NH, D), k_ref, rtol=1e-3, atol=1e-3, what="k")
+    rc, rs = oq.kv_quantize_rows(k_rot.cpu().reshape(NH, D).numpy())
+    assert np.array_equal(kc[:, pos].cpu().numpy(), rc)
+    assert np.array_equal(ks[:, pos].cpu().numpy().view(np.uint16), rs.view(np.uint16))
+    vrc, vrs = oq.kv_quantize_rows(qkv[2 * HD:].reshape(NH, D).numpy())
+    assert np.array_equal(vc[:, pos].cpu().numpy(), vrc)
+    assert np.array_equal(vs[:, pos].cpu().numpy().view(np.uint16), vrs.view(np.uint16))
+    assert torch.equal(kf[:, pos].cpu(), k_rot.cpu().reshape(NH, D))
+    assert torch.equal(vf[:, pos].cpu(), qkv[2 * HD:].reshape(NH, D))
+    other = torch.ones(S, dtype=torch.bool)
+    other[pos] = False
+    assert (kc[:, other] == 0).all() and (ks[:, other] == 1).all()
