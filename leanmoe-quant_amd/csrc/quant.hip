@@ -97,6 +97,7 @@ __global__ __launch_bounds__(256) void kv_write_i8_kernel(
   const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (r >= 2 * heads) return;
   const int64_t slot = pos ? pos[0] : 0;
+  if (slot < 0 || slot >= s_len) return;  // a position outside the cache writes nothing
   const bool is_k = r < heads;
   const int h = is_k ? r : r - heads;
   const uint16_t* src = (is_k ? k : v) + (int64_t)h * D;
@@ -112,6 +113,7 @@ extern "C" int lemoq_kv_write_i8(const uint16_t* k, const uint16_t* v, int64_t h
   if (!k || !v || !kc || !ks || !vc || !vs) return LEMOQ_ERR_NULL;
   if (heads <= 0 || head_dim <= 0 || head_dim > 4096 || heads > 65536) return LEMOQ_ERR_SHAPE;
   if (code_head_stride < head_dim || s_len < 1) return LEMOQ_ERR_SHAPE;
+  if (pos && code_head_stride < s_len * head_dim) return LEMOQ_ERR_SHAPE;
   const int rows = (int)(2 * heads);
   hipLaunchKernelGGL(kv_write_i8_kernel, dim3((rows + 3) / 4), dim3(256), 0, lemoq_stream(stream),
                      k, v, (int)heads, (int)head_dim, kc, ks, vc, vs, code_head_stride, s_len, pos);
@@ -150,6 +152,7 @@ __global__ __launch_bounds__(64) void kv_write_f16_kernel(
   const bool is_k = r < heads;
   const int h = is_k ? r : r - heads;
   const int64_t slot = pos[0];
+  if (slot < 0 || (slot + 1) * D > dst_head_stride) return;  // outside the cache: no write
   const uint16_t* src = (is_k ? k : v) + (int64_t)h * src_head_stride;
   uint16_t* dst = (is_k ? k_cache : v_cache) + (int64_t)h * dst_head_stride + slot * D;
   for (int d = threadIdx.x; d < D; d += 64) dst[d] = src[d];
