@@ -1,0 +1,404 @@
+#!/usr/bin/env python3
+"""Decode-step benchmark of the lemoq MI355X build (one GPU).
+
+Workload: the OLMoE-1B-7B-shaped batch-1 decode step of the reference's
+canonical cell (w8a16 g128 attention + experts, W8 lm_head, KV-INT8 cache,
+split-KV attention, one graph per step): seeded random weights, prompt of
+``ctx`` copies of token id 1, then greedy decode steps replayed from one
+captured hipGraph.  The reference quotes this as ms/token at ctx 1024 and 4096
+(README_EN.md:66-71 of LeanMoE-Quant, RTX 5090).
+
+Printed: ONE JSON line on stdout.  ``value`` is ms/token at ``--ctx`` (wall
+clock over exactly ``--steps`` replays, synchronised on both sides, after
+``--warmup`` replays); the line also carries the second context, the step's
+HBM roofline fraction, per-kernel cold timings, the dominant kernel's roofline
+(``roofline``) and the CPU oracle's ms/token on this host (``cpu_baseline``).
+Progress goes to stderr.
+
+``--mode kernels`` runs only the weights + isolated kernel timings (short; the
+form used under ``rocprofv3 --pmc``).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(REPO, "leanmoe-quant_amd")
+for _p in (REPO, PKG):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "ms/token decode step, OLMoE-shape w8a16+KV-INT8 @ctx1024/4096; % HBM roofline"
+HBM_PEAK_GBS = 8000.0  # MI355X published HBM3E bandwidth
+REFERENCE_RTX5090_MS = {"1024": 1.4602, "4096": 1.6075}  # README_EN.md:71 (not this hardware)
+KV_BYTES_PER_TOKEN_LAYER = 16 * (128 + 2) * 2  # 16 heads x (128 codes + fp16 scale) x (K, V)
+
+
+def log(msg: str) -> None:
+    sys.stderr.write("[bench %7.1fs] %s\n" % (time.time() - _T0, msg))
+    sys.stderr.flush()
+
+
+_T0 = time.time()
+
+
+def parse_args(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=32)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--ctx", type=int, default=1024)
+    ap.add_argument("--ctx2", type=int, default=4096, help="second context (0: skip)")
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--kernel-reps", type=int, default=32)
+    ap.add_argument("--cpu-budget-s", type=float, default=20.0)
+    ap.add_argument("--cpu-check-steps", type=int, default=4)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--mode", choices=("full", "kernels"), default="full")
+    return ap.parse_args(argv)
+
+
+# ---------------------------------------------------------------------------
+# timing helpers
+# ---------------------------------------------------------------------------
+class Flusher:
+    """Reads a buffer larger than the 256 MB Infinity Cache + L2 (evicts them) and
+    measures the read bandwidth of that stream (the roofline denominator)."""
+
+    def __init__(self, torch, hip, dev, nbytes: int = 1 << 30):
+        self.torch, self.hip = torch, hip
+        self.buf = torch.empty((nbytes,), dtype=torch.uint8, device=dev)
+        self.buf.fill_(1)
+        self.nbytes = nbytes
+        self.blocks = 8192
+        self.out = torch.empty((self.blocks,), dtype=torch.int32, device=dev)
+
+    def flush(self) -> None:
+        self.hip.call("lemoq_read_probe", self.hip.ptr(self.buf), self.nbytes, self.hip.ptr(self.out),
+                      self.blocks, self.hip.stream_of())
+
+    def read_bandwidth_gbs(self, reps: int = 10) -> float:
+        torch = self.torch
+        self.flush()
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+        for a, b in evs:
+            a.record()
+            self.flush()
+            b.record()
+        torch.cuda.synchronize()
+        ms = sorted(a.elapsed_time(b) for a, b in evs)
+        return self.nbytes / (ms[len(ms) // 2] * 1e-3) / 1e9
+
+
+def time_cold(torch, flusher, launches, reps: int) -> dict:
+    """Cold per-launch duration: cache flush, then event/kernel/event, ``reps`` times
+    cycling through ``launches`` (callables enqueueing one kernel on the current stream)."""
+    evs = []
+    for r in range(reps):
+        flusher.flush()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        launches[r % len(launches)]()
+        b.record()
+        evs.append((a, b))
+    torch.cuda.synchronize()
+    us = sorted(a.elapsed_time(b) * 1e3 for a, b in evs)
+    return {"avg_us": sum(us) / len(us), "p50_us": us[len(us) // 2], "min_us": us[0], "reps": reps}
+
+
+# ---------------------------------------------------------------------------
+# isolated kernels of the step (the same entry points the step executor calls)
+# ---------------------------------------------------------------------------
+def kernel_table(torch, hip, w, sess, flusher, reps: int) -> dict:
+    s = w.shape
+    H, HD, D, F, E, K, g = s.hidden, s.heads * s.head_dim, s.head_dim, s.ffn, s.num_experts, s.top_k, s.group_size
+    P, st = hip.ptr, hip.stream_of
+    L = w.layers
+    nl = len(L)
+    filled = int(sess.filled.item())
+    S = sess.max_seq
+    w8 = lambda rows, cols: rows * cols + rows * (cols // g) * 2  # noqa: E731
+    scratch = {
+        "h": torch.randn((H,), device=sess.device).to(torch.float16),
+        "y": torch.empty((max(s.vocab, 3 * HD),), dtype=torch.float16, device=sess.device),
+        "ids": sess.top_i.clone(),
+        "tw": sess.top_w.clone(),
+        "act": sess.act.clone(),
+    }
+    qk_scale = (1.0 / math.sqrt(D)) * 1.4426950408889634
+    specs = {}
+
+    def add(name, nbytes, launches):
+        specs[name] = (nbytes, launches)
+
+    add("moe_gate_up_w8", K * w8(2 * F, H) + H * 2 + K * F * 2,
+        [lambda i=i: hip.call("lemoq_moe_gate_up_w8", P(scratch["h"]), P(L[i].gu_codes), P(L[i].gu_scale),
+                               P(scratch["ids"]), K, E, F, H, g, P(scratch["act"]), st()) for i in range(nl)])
+    add("moe_down_w8", K * w8(H, F) + K * F * 2 + 3 * H * 2,
+        [lambda i=i: hip.call("lemoq_moe_down_w8", P(scratch["act"]), P(L[i].dn_codes), P(L[i].dn_scale),
+                               P(scratch["ids"]), P(scratch["tw"]), K, E, H, F, g, P(scratch["h"]),
+                               P(scratch["y"]), st()) for i in range(nl)])
+    add("gemv_w8 qkv (+input RMSNorm)", w8(3 * HD, H) + 2 * H * 2 + 3 * HD * 2,
+        [lambda i=i: hip.call("lemoq_gemv_w8_fused", P(scratch["h"]), None, 0, P(L[i].ln_in), s.eps, None,
+                               P(L[i].qkv_codes), P(L[i].qkv_scale), 3 * HD, H, g, None, P(scratch["y"]), st())
+         for i in range(nl)])
+    add("gemv_w8 o_proj (+residual)", w8(H, HD) + HD * 2 + 2 * H * 2,
+        [lambda i=i: hip.call("lemoq_gemv_w8_fused", P(sess.attn), None, 0, None, s.eps, None,
+                               P(L[i].o_codes), P(L[i].o_scale), H, HD, g, P(scratch["h"]), P(scratch["y"]), st())
+         for i in range(nl)])
+    add("gemv_w8 lm_head (+final RMSNorm)", w8(s.vocab, H) + 2 * H * 2 + s.vocab * 2,
+        [lambda: hip.call("lemoq_gemv_w8_fused", P(scratch["h"]), None, 0, P(w.final_norm), s.eps, None,
+                          P(w.lm_codes), P(w.lm_scale), s.vocab, H, g, None, P(scratch["y"]), st())])
+    add("router_topk_fused", E * H * 2 + 3 * H * 2,
+        [lambda i=i: hip.call("lemoq_router_topk_fused", P(scratch["h"]), P(L[i].ln_post), s.eps, H,
+                               P(L[i].router), E, K, int(s.norm_topk_prob), P(sess.xn), None, None,
+                               P(scratch["tw"]), P(scratch["ids"]), st()) for i in range(nl)])
+    kv = sess.kv
+    add("attn_split_i8 (filled=%d)" % filled,
+        KV_BYTES_PER_TOKEN_LAYER * filled + HD * 2 + s.heads * sess.num_splits * (D + 2) * 4,
+        [lambda i=i: hip.call("lemoq_attn_split_i8", P(sess.q_rot), P(kv[i]["kc"]), P(kv[i]["ks"]), P(kv[i]["vc"]),
+                               P(kv[i]["vs"]), S * D, S, P(sess.filled), s.heads, D, sess.num_splits, qk_scale,
+                               P(sess.part_m), P(sess.part_l), P(sess.part_acc), st()) for i in range(nl)])
+    add("attn_merge", s.heads * sess.num_splits * (D + 2) * 4 + HD * 2,
+        [lambda: hip.call("lemoq_attn_merge", P(sess.part_m), P(sess.part_l), P(sess.part_acc), s.heads,
+                          sess.num_splits, D, P(sess.attn), st())])
+    out = {}
+    for name, (nbytes, launches) in specs.items():
+        r = time_cold(torch, flusher, launches, reps)
+        r["bytes"] = int(nbytes)
+        r["gbs"] = nbytes / (r["avg_us"] * 1e-6) / 1e9
+        r["frac_of_peak"] = r["gbs"] / HBM_PEAK_GBS
+        out[name] = r
+        log("kernel %-36s %8.2f us avg  %7.1f GB/s" % (name, r["avg_us"], r["gbs"]))
+    return out
+
+
+# ---------------------------------------------------------------------------
+# decode timing
+# ---------------------------------------------------------------------------
+def time_decode(torch, w, ctx: int, steps: int, warmup: int, extra: int):
+    from lemoq.model.olmoe import DecodeSession
+
+    sess = DecodeSession(w, [1] * ctx, max_new_tokens=warmup + steps + extra + 1)
+    sess.capture()
+    t = time.time()
+    sess.prefill()
+    log("ctx %d: prefill (%d graph replays) %.2fs" % (ctx, ctx, time.time() - t))
+    for _ in range(warmup):
+        sess.graph.replay()
+    torch.cuda.synchronize()
+    filled0 = int(sess.filled.item())
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(steps):
+        sess.graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3
+    dev_ms = e0.elapsed_time(e1)
+    filled_avg = filled0 + (steps - 1) / 2.0
+    step_bytes = w.shape.weight_bytes_per_token() + KV_BYTES_PER_TOKEN_LAYER * w.shape.layers * filled_avg
+    res = {
+        "ctx": ctx,
+        "ms_per_token": wall_ms / steps,
+        "device_ms_per_token": dev_ms / steps,
+        "tokens_per_s": steps / (wall_ms * 1e-3),
+        "host_share": max(0.0, (wall_ms - dev_ms) / wall_ms),
+        "filled_first": filled0,
+        "step_bytes": int(step_bytes),
+        "launches_per_step": 8 * w.shape.layers + 2,
+    }
+    log("ctx %d: %.4f ms/token wall, %.4f device, %d steps" % (ctx, res["ms_per_token"], res["device_ms_per_token"], steps))
+    return sess, res
+
+
+def cpu_baseline(torch, w, sess, check_tokens, budget_s: float, max_steps: int, snap) -> dict:
+    """The CPU oracle (torch, this host's cores) decoding from the GPU's KV snapshot."""
+    from oracle.olmoe import OracleDecoder
+
+    kv, token, pos = snap
+    t = time.time()
+    host = w.to_host()
+    od = OracleDecoder(host, sess.max_seq, kv=kv)
+    log("cpu oracle ready in %.1fs (%d threads)" % (time.time() - t, torch.get_num_threads()))
+    tokens, times, logits0 = [], [], None
+    tok = token
+    for i in range(max_steps):
+        t = time.perf_counter()
+        lg = od.step(tok, pos + i)
+        times.append(time.perf_counter() - t)
+        if logits0 is None:
+            logits0 = lg
+        tok = od.greedy(lg)
+        tokens.append(tok)
+        if sum(times) > budget_s:
+            break
+    timed = times[1:] if len(times) > 1 else times  # first step warms the allocator
+    ms = 1e3 * sum(timed) / len(timed)
+    n = len(tokens)
+    return {
+        "value": ms,
+        "unit": "ms/token",
+        "cores": int(torch.get_num_threads()),
+        "kind": "port",
+        "sample": "%d greedy decode steps of the full OLMoE-1B-7B-shaped w8a16+KV-INT8 model by the torch-CPU "
+                  "oracle from the GPU's KV snapshot at position %d (first step untimed)" % (n, pos),
+        "host_cpu_count": os.cpu_count(),
+        "tokens_match_gpu": tokens == check_tokens[:n],
+        "cpu_tokens": tokens,
+        "gpu_tokens": check_tokens[:n],
+        "_logits0": logits0,
+    }
+
+
+def main(argv=None) -> int:
+    args = parse_args(argv)
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path (the batch-1 decode "
+              "step runs on one MI355X); run with --gpus 1", file=sys.stderr)
+        return 2
+    import torch
+
+    from lemoq import _hip
+    from lemoq.model.olmoe import OLMOE_1B_7B, OlmoeW8Weights
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 2
+    _hip.load()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    log("device %s, %d CUs" % (torch.cuda.get_device_name(dev), torch.cuda.get_device_properties(dev).multi_processor_count))
+    t = time.time()
+    w = OlmoeW8Weights.random(OLMOE_1B_7B, seed=args.seed, device=dev)
+    torch.cuda.synchronize()
+    log("weights ready %.1fs (%.1f MB streamed per token)" % (time.time() - t, w.shape.weight_bytes_per_token() / 1e6))
+    flusher = Flusher(torch, _hip, dev)
+    read_bw = flusher.read_bandwidth_gbs()
+    log("measured read bandwidth %.1f GB/s" % read_bw)
+
+    if args.mode == "kernels":
+        from lemoq.model.olmoe import DecodeSession
+
+        sess = DecodeSession(w, [1] * args.ctx, max_new_tokens=2)
+        sess.capture()
+        sess.prefill()
+        kt = kernel_table(torch, _hip, w, sess, flusher, args.kernel_reps)
+        print(json.dumps({"mode": "kernels", "read_bw_gbs": read_bw, "kernels": kt}))
+        return 0
+
+    check_n = 0 if args.no_cpu else max(1, args.cpu_check_steps)
+    sess, r1 = time_decode(torch, w, args.ctx, args.steps, args.warmup, check_n)
+    snap = None
+    check_tokens: list[int] = []
+    gpu_logits0 = None
+    if check_n:
+        snap = (sess.kv_cpu(), int(sess.token.item()), sess.position)
+        p0 = sess.position
+        sess.replay(1)
+        gpu_logits0 = sess.logits_cpu()
+        if check_n > 1:
+            sess.replay(check_n - 1)
+        check_tokens = [int(t) for t in sess.history[p0 + 1: p0 + 1 + check_n].tolist()]
+    kt = kernel_table(torch, _hip, w, sess, flusher, args.kernel_reps)
+    cap = _Cap(sess.max_seq)
+    del sess
+    r2 = None
+    if args.ctx2:
+        s2, r2 = time_decode(torch, w, args.ctx2, args.steps, args.warmup, 0)
+        del s2
+    torch.cuda.synchronize()
+
+    cpu = None
+    if check_n:
+        cpu = cpu_baseline(torch, w, cap, check_tokens,
+                           args.cpu_budget_s, check_n, snap)
+        lg0 = cpu.pop("_logits0")
+        cpu["logits_max_abs_diff_step0"] = float((lg0.float() - gpu_logits0.float()).abs().max())
+
+    dom_name = "moe_gate_up_w8"
+    dom = kt[dom_name]
+    traffic = _traffic_from_profiles(dom_name)
+    line = {
+        "metric": METRIC,
+        "value": r1["ms_per_token"],
+        "unit": "ms/token",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": r1["ms_per_token"],
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic",
+        "config": {
+            "workload": "OLMoE-1B-7B-shaped batch-1 greedy decode step (16 layers, hidden 2048, 16x128 heads, "
+                        "64 experts top-8, ffn 1024, vocab 50304), w8a16 g128 + W8 lm_head + KV-INT8, "
+                        "prompt %d x token 1, seeded random init, one hipGraph replay per token" % args.ctx,
+            "ctx": args.ctx,
+            "weights": "int8 per-group-128 codes, fp16 scales; fp32 accumulation",
+        },
+        "tokens_per_s": r1["tokens_per_s"],
+        "device_ms_per_token": r1["device_ms_per_token"],
+        "host_share": r1["host_share"],
+        "launches_per_step": r1["launches_per_step"],
+        "step_bytes": r1["step_bytes"],
+        "step_hbm_frac_of_peak": r1["step_bytes"] / (r1["device_ms_per_token"] * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "step_hbm_frac_of_measured": r1["step_bytes"] / (r1["device_ms_per_token"] * 1e-3) / 1e9 / read_bw,
+        "measured_read_bw_gbs": read_bw,
+        "reference_rtx5090_ms_per_token": REFERENCE_RTX5090_MS,
+        "roofline": {
+            "kernel": dom_name,
+            "bound": "hbm",
+            "achieved": dom["gbs"],
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": dom["gbs"] / HBM_PEAK_GBS,
+            "traffic": traffic,
+            "bytes_per_launch": dom["bytes"],
+            "avg_us": dom["avg_us"],
+        },
+        "kernels": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()} for k, v in kt.items()},
+    }
+    if r2 is not None:
+        line["ctx2"] = r2
+        line["ms_per_token_ctx%d" % args.ctx2] = r2["ms_per_token"]
+        line["step_hbm_frac_of_peak_ctx%d" % args.ctx2] = (
+            r2["step_bytes"] / (r2["device_ms_per_token"] * 1e-3) / 1e9 / HBM_PEAK_GBS)
+    if cpu is not None:
+        line["cpu_baseline"] = cpu
+    print(json.dumps(line))
+    sys.stdout.flush()
+    return 0
+
+
+class _Cap:
+    """Stand-in carrying the cache capacity the CPU oracle needs."""
+
+    def __init__(self, max_seq: int) -> None:
+        self.max_seq = max_seq
+
+
+def _traffic_from_profiles(kernel: str):
+    """HBM bytes per launch of ``kernel`` from the committed rocprofv3 --pmc summary, if present."""
+    path = os.path.join(REPO, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            data = json.load(f)
+        return data.get(kernel, {}).get("traffic_bytes")
+    except (OSError, ValueError):
+        return None
+
+
+if __name__ == "__main__":
+    sys.exit(main())

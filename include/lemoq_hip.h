@@ -340,6 +340,16 @@ typedef struct LemoqOlmoeStep {
 
 int lemoq_olmoe_decode_step(const LemoqOlmoeStep* step, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Measurement: read n_bytes (multiple of 16, 16-byte aligned) once with
+ * nontemporal 16-byte loads over `blocks` 256-thread blocks; block b writes a
+ * fold of what it read to out[b].  The roofline denominator (measured read
+ * bandwidth) and the cache flush before cold kernel timings.  Restates the
+ * method of the reference's read probe (tools/probe_machine.py:392-505).
+ * ------------------------------------------------------------------------- */
+int lemoq_read_probe(const void* src, int64_t n_bytes, uint32_t* out, int64_t blocks,
+                     void* stream);
+
 #ifdef __cplusplus
 }
 #endif

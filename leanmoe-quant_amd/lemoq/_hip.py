@@ -148,6 +148,7 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     ),
     "lemoq_argmax_advance": (_I, [_P, _I64, _P, _P, _P, _P, _I64, _P, _I64, _P]),
     "lemoq_olmoe_decode_step": (_I, [ctypes.POINTER(LemoqOlmoeStep), _P]),
+    "lemoq_read_probe": (_I, [_P, _I64, _P, _I64, _P]),
 }
 
 
