@@ -56,9 +56,9 @@ def parse_args(argv=None):
     ap.add_argument("--ctx", type=int, default=1024)
     ap.add_argument("--ctx2", type=int, default=4096, help="second context (0: skip)")
     ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--kernel-reps", type=int, default=32)
+    ap.add_argument("--kernel-reps", type=int, default=4)
     ap.add_argument("--cpu-budget-s", type=float, default=20.0)
-    ap.add_argument("--cpu-check-steps", type=int, default=4)
+    ap.add_argument("--cpu-check-steps", type=int, default=32)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--mode", choices=("full", "kernels"), default="full")
     return ap.parse_args(argv)
@@ -97,19 +97,24 @@ class Flusher:
 
 
 def time_cold(torch, flusher, launches, reps: int) -> dict:
-    """Cold per-launch duration: cache flush, then event/kernel/event, ``reps`` times
-    cycling through ``launches`` (callables enqueueing one kernel on the current stream)."""
+    """Per-launch duration of back-to-back launches: flush the caches, then time
+    one pass over ``launches`` (callables enqueueing one kernel each on the
+    current stream, one per layer so every launch reads cold weights) between
+    two events; ``reps`` passes.  No event sits between the kernels, so the
+    average is comparable with the profiler's per-kernel duration."""
     evs = []
-    for r in range(reps):
+    for _ in range(reps):
         flusher.flush()
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record()
-        launches[r % len(launches)]()
+        for fn in launches:
+            fn()
         b.record()
         evs.append((a, b))
     torch.cuda.synchronize()
-    us = sorted(a.elapsed_time(b) * 1e3 for a, b in evs)
-    return {"avg_us": sum(us) / len(us), "p50_us": us[len(us) // 2], "min_us": us[0], "reps": reps}
+    us = sorted(a.elapsed_time(b) * 1e3 / len(launches) for a, b in evs)
+    return {"avg_us": sum(us) / len(us), "p50_us": us[len(us) // 2], "min_us": us[0],
+            "launches": reps * len(launches)}
 
 
 # ---------------------------------------------------------------------------
@@ -124,20 +129,29 @@ def kernel_table(torch, hip, w, sess, flusher, reps: int) -> dict:
     filled = int(sess.filled.item())
     S = sess.max_seq
     w8 = lambda rows, cols: rows * cols + rows * (cols // g) * 2  # noqa: E731
+    dev = sess.device
     scratch = {
-        "h": torch.randn((H,), device=sess.device).to(torch.float16),
-        "y": torch.empty((max(s.vocab, 3 * HD),), dtype=torch.float16, device=sess.device),
+        "h": torch.randn((H,), device=dev).to(torch.float16),
+        "y": torch.empty((max(s.vocab, 3 * HD),), dtype=torch.float16, device=dev),
         "ids": sess.top_i.clone(),
         "tw": sess.top_w.clone(),
         "act": sess.act.clone(),
+        "xn": torch.empty((H,), dtype=torch.float16, device=dev),
+        "lg": torch.empty((E,), dtype=torch.float16, device=dev),
+        "tok": torch.zeros((1,), dtype=torch.int64, device=dev),
+        "pos": torch.zeros((1,), dtype=torch.int64, device=dev),
+        "fill": torch.zeros((1,), dtype=torch.int32, device=dev),
+        "ids2": sess.top_i.clone(),
+        "tw2": sess.top_w.clone(),
     }
+    kv = sess.kv
     qk_scale = (1.0 / math.sqrt(D)) * 1.4426950408889634
     specs = {}
 
     def add(name, nbytes, launches):
         specs[name] = (nbytes, launches)
 
-    add("moe_gate_up_w8", K * w8(2 * F, H) + H * 2 + K * F * 2,
+    add("moe_gate_up_w8", K * w8(2 * F, H) + H * 2 + K * 8 + K * F * 2,
         [lambda i=i: hip.call("lemoq_moe_gate_up_w8", P(scratch["h"]), P(L[i].gu_codes), P(L[i].gu_scale),
                                P(scratch["ids"]), K, E, F, H, g, P(scratch["act"]), st()) for i in range(nl)])
     add("moe_down_w8", K * w8(H, F) + K * F * 2 + 3 * H * 2,
@@ -148,18 +162,11 @@ def kernel_table(torch, hip, w, sess, flusher, reps: int) -> dict:
         [lambda i=i: hip.call("lemoq_gemv_w8_fused", P(scratch["h"]), None, 0, P(L[i].ln_in), s.eps, None,
                                P(L[i].qkv_codes), P(L[i].qkv_scale), 3 * HD, H, g, None, P(scratch["y"]), st())
          for i in range(nl)])
-    add("gemv_w8 o_proj (+residual)", w8(H, HD) + HD * 2 + 2 * H * 2,
-        [lambda i=i: hip.call("lemoq_gemv_w8_fused", P(sess.attn), None, 0, None, s.eps, None,
-                               P(L[i].o_codes), P(L[i].o_scale), H, HD, g, P(scratch["h"]), P(scratch["y"]), st())
-         for i in range(nl)])
-    add("gemv_w8 lm_head (+final RMSNorm)", w8(s.vocab, H) + 2 * H * 2 + s.vocab * 2,
-        [lambda: hip.call("lemoq_gemv_w8_fused", P(scratch["h"]), None, 0, P(w.final_norm), s.eps, None,
-                          P(w.lm_codes), P(w.lm_scale), s.vocab, H, g, None, P(scratch["y"]), st())])
-    add("router_topk_fused", E * H * 2 + 3 * H * 2,
-        [lambda i=i: hip.call("lemoq_router_topk_fused", P(scratch["h"]), P(L[i].ln_post), s.eps, H,
-                               P(L[i].router), E, K, int(s.norm_topk_prob), P(sess.xn), None, None,
-                               P(scratch["tw"]), P(scratch["ids"]), st()) for i in range(nl)])
-    kv = sess.kv
+    add("qk_norm_rope_kv_i8", 3 * HD * 2 + 2 * HD * 2 + 2 * D * 2 + HD * 2 + 2 * (HD + 2 * s.heads),
+        [lambda i=i: hip.call("lemoq_qk_norm_rope_kv_i8", P(sess.qkv), s.heads, D, P(L[i].q_norm), P(L[i].k_norm),
+                               s.eps, P(sess.cos_tab), P(sess.sin_tab), P(sess.pos), P(sess.q_rot),
+                               P(kv[i]["kc"]), P(kv[i]["ks"]), P(kv[i]["vc"]), P(kv[i]["vs"]), S * D, S,
+                               None, None, 0, None, st()) for i in range(nl)])
     add("attn_split_i8 (filled=%d)" % filled,
         KV_BYTES_PER_TOKEN_LAYER * filled + HD * 2 + s.heads * sess.num_splits * (D + 2) * 4,
         [lambda i=i: hip.call("lemoq_attn_split_i8", P(sess.q_rot), P(kv[i]["kc"]), P(kv[i]["ks"]), P(kv[i]["vc"]),
@@ -167,7 +174,20 @@ def kernel_table(torch, hip, w, sess, flusher, reps: int) -> dict:
                                P(sess.part_m), P(sess.part_l), P(sess.part_acc), st()) for i in range(nl)])
     add("attn_merge", s.heads * sess.num_splits * (D + 2) * 4 + HD * 2,
         [lambda: hip.call("lemoq_attn_merge", P(sess.part_m), P(sess.part_l), P(sess.part_acc), s.heads,
-                          sess.num_splits, D, P(sess.attn), st())])
+                          sess.num_splits, D, P(sess.attn), st())] * nl)
+    add("gemv_w8 o_proj (+residual)", w8(H, HD) + HD * 2 + 2 * H * 2,
+        [lambda i=i: hip.call("lemoq_gemv_w8_fused", P(sess.attn), None, 0, None, s.eps, None,
+                               P(L[i].o_codes), P(L[i].o_scale), H, HD, g, P(scratch["h"]), P(scratch["y"]), st())
+         for i in range(nl)])
+    add("router_topk_fused", E * H * 2 + 3 * H * 2 + E * 2 + K * 10,
+        [lambda i=i: hip.call("lemoq_router_topk_fused", P(scratch["h"]), P(L[i].ln_post), s.eps, H, P(L[i].router),
+                               E, K, int(s.norm_topk_prob), P(scratch["xn"]), P(scratch["lg"]), None,
+                               P(scratch["tw2"]), P(scratch["ids2"]), st()) for i in range(nl)])
+    add("gemv_w8 lm_head + argmax (2 launches)", w8(s.vocab, H) + 2 * H * 2 + s.vocab * 2,
+        [lambda: hip.call("lemoq_lm_head_argmax_w8", P(scratch["h"]), P(w.final_norm), s.eps, P(w.lm_codes),
+                          P(w.lm_scale), s.vocab, H, g, P(scratch["y"]), P(sess.am_val), P(sess.am_idx),
+                          int(sess.am_val.numel()), P(scratch["tok"]), P(scratch["pos"]), P(scratch["fill"]),
+                          None, 0, None, 0, st())])
     out = {}
     for name, (nbytes, launches) in specs.items():
         r = time_cold(torch, flusher, launches, reps)

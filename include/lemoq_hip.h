@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define LEMOQ_ABI_VERSION 1
+#define LEMOQ_ABI_VERSION 2
 
 enum {
   LEMOQ_OK = 0,
@@ -95,6 +95,24 @@ int lemoq_gemv_w8_fused(const uint16_t* x_src, const int64_t* x_row_index,
                         const int8_t* codes, const uint16_t* scale, int64_t N,
                         int64_t K, int64_t group, const uint16_t* residual,
                         uint16_t* y, void* stream);
+
+/* Fused final step of the decode graph (no single reference counterpart: it
+ * joins the lm_head QuantLinear GEMV, src/lemoq/quant/linear.py:446-469, with
+ * the greedy `logits.argmax()` of StaticCacheDecodeSession.replay,
+ * benchmarks/cudagraph.py:759-762, moved onto the device).
+ * logits (N) fp16 = W8 GEMV of x (optionally RMSNormed with norm_w); each
+ * GEMV block writes its best (fp16 value, lowest row) to part_val/part_idx
+ * (part_len >= lemoq_lm_head_argmax_parts(N)), then one block reduces them
+ * (ties -> lowest row) and advances the step exactly like
+ * lemoq_argmax_advance.  Two launches. */
+int lemoq_lm_head_argmax_w8(const uint16_t* x, const uint16_t* norm_w, float eps,
+                            const int8_t* codes, const uint16_t* scale, int64_t N, int64_t K,
+                            int64_t group, uint16_t* logits, float* part_val,
+                            int32_t* part_idx, int64_t part_len, int64_t* token, int64_t* pos,
+                            int32_t* filled, const int64_t* prompt, int64_t prompt_len,
+                            int64_t* history, int64_t history_len, void* stream);
+/* Number of argmax partials lemoq_lm_head_argmax_w8 writes for N rows. */
+int64_t lemoq_lm_head_argmax_parts(int64_t N);
 
 /* ---------------------------------------------------------------------------
  * A4 — grouped MoE gate/up + SiLU, w8.
@@ -232,7 +250,8 @@ int lemoq_route_topk(const void* logits, int logits_is_f16, int64_t T, int64_t E
  * moe_static._route, src/lemoq/kernels/moe_static.py:262-283), then the
  * routing above; top_w_f16 = fp16(top_w) (the `.to(x.dtype)` of _route).
  * router_w (E, hidden) fp16.  norm_w may be NULL (no norm: xn = h).
- * logits_out and top_w_f32 may be NULL. */
+ * logits_out, top_w_f32 and top_w_f16 may be NULL.  One 1024-thread block
+ * (the 64 x 2048 router is 256 KB; one wave per row, then one wave routes). */
 int lemoq_router_topk_fused(const uint16_t* h, const uint16_t* norm_w, float eps,
                             int64_t hidden, const uint16_t* router_w, int64_t E,
                             int64_t top_k, int norm_topk_prob, uint16_t* xn_out,
@@ -336,6 +355,9 @@ typedef struct LemoqOlmoeStep {
   int64_t* top_i;                /* (top_k) */
   uint16_t* act;                 /* (top_k, F) */
   uint16_t* logits;              /* (vocab) fp16 */
+  float* am_val;                 /* (am_len) argmax partials */
+  int32_t* am_idx;               /* (am_len) */
+  int64_t am_len;                /* >= lemoq_lm_head_argmax_parts(vocab) */
 } LemoqOlmoeStep;
 
 int lemoq_olmoe_decode_step(const LemoqOlmoeStep* step, void* stream);

@@ -188,22 +188,50 @@ __global__ __launch_bounds__(256) void attn_split_kernel(
   }
 }
 
-__global__ void attn_merge_kernel(const float* __restrict__ m, const float* __restrict__ l,
-                                  const float* __restrict__ acc, int NS, int D,
-                                  uint16_t* __restrict__ out) {
+// LSE merge of one head per block: the split weights 2^(m_j - M) and the
+// denominator are formed once in LDS, then thread t streams acc[j][t] for all
+// splits (independent loads, fixed split order).
+__global__ __launch_bounds__(256) void attn_merge_kernel(const float* __restrict__ m,
+                                                         const float* __restrict__ l,
+                                                         const float* __restrict__ acc, int NS,
+                                                         int D, uint16_t* __restrict__ out) {
+  __shared__ float wj[1024];
+  __shared__ float red[2];
   const int h = blockIdx.x;
   const float* mh = m + (int64_t)h * NS;
   const float* lh = l + (int64_t)h * NS;
-  float M = -INFINITY;
-  for (int j = 0; j < NS; ++j) M = fmaxf(M, mh[j]);
-  if (!(M > -INFINITY)) M = 0.0f;
+  const float* ah = acc + (int64_t)h * NS * D;
+  for (int j = threadIdx.x; j < NS; j += blockDim.x) wj[j] = mh[j];
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float M = -INFINITY;
+    for (int j = 0; j < NS; ++j) M = fmaxf(M, wj[j]);
+    if (!(M > -INFINITY)) M = 0.0f;  // every split empty: out = 0
+    red[0] = M;
+  }
+  __syncthreads();
+  const float M = red[0];
+  for (int j = threadIdx.x; j < NS; j += blockDim.x) wj[j] = exp2f(wj[j] - M);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float den = 0.0f;
+    for (int j = 0; j < NS; ++j) den += lh[j] * wj[j];
+    red[1] = den;
+  }
+  __syncthreads();
+  const float den = red[1];
   for (int t = threadIdx.x; t < D; t += blockDim.x) {
-    float num = 0.0f, den = 0.0f;
-    for (int j = 0; j < NS; ++j) {
-      const float w = exp2f(mh[j] - M);
-      num += acc[((int64_t)h * NS + j) * D + t] * w;
-      den += lh[j] * w;
+    float num = 0.0f;
+    int j = 0;
+    for (; j + 4 <= NS; j += 4) {
+      const float a0 = ah[(int64_t)j * D + t], a1 = ah[(int64_t)(j + 1) * D + t];
+      const float a2 = ah[(int64_t)(j + 2) * D + t], a3 = ah[(int64_t)(j + 3) * D + t];
+      num += a0 * wj[j];
+      num += a1 * wj[j + 1];
+      num += a2 * wj[j + 2];
+      num += a3 * wj[j + 3];
     }
+    for (; j < NS; ++j) num += ah[(int64_t)j * D + t] * wj[j];
     out[(int64_t)h * D + t] = f2h(den > 0.0f ? num / den : num);
   }
 }
@@ -277,7 +305,8 @@ extern "C" int lemoq_attn_merge(const float* m, const float* l, const float* acc
                                 int64_t num_splits, int64_t head_dim, uint16_t* out,
                                 void* stream) {
   if (!m || !l || !acc || !out) return LEMOQ_ERR_NULL;
-  if (heads <= 0 || heads > 65535 || num_splits <= 0 || head_dim <= 0 || head_dim > 1024)
+  if (heads <= 0 || heads > 65535 || num_splits <= 0 || num_splits > 1024 || head_dim <= 0 ||
+      head_dim > 256)
     return LEMOQ_ERR_SHAPE;
   const int threads = head_dim <= 64 ? 64 : (head_dim <= 128 ? 128 : 256);
   hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)heads), dim3(threads), 0,

@@ -31,17 +31,40 @@ __device__ __forceinline__ uint16_t hadd_round(float a_f16_exact, uint16_t b) {
 __device__ __forceinline__ f16x2 as_h2(uint32_t v) { return __builtin_bit_cast(f16x2, v); }
 
 // ---------------------------------------------------------------------------
-// Wave-level reductions (fixed butterfly order => deterministic).
+// Wave-level reductions, deterministic (fixed combination order).
+// Within each row of 16 lanes: DPP quad_perm [1,0,3,2], quad_perm [2,3,0,1],
+// row_half_mirror, row_mirror leave the row's total in every lane of the row;
+// the four row totals are then combined through v_readlane in row order, so
+// the result is wave-uniform.  No LDS traffic (a ds_bpermute butterfly costs
+// an LDS round trip per step).
 // ---------------------------------------------------------------------------
+#define LEMOQ_DPP_QUAD_1032 0xB1
+#define LEMOQ_DPP_QUAD_2301 0x4E
+#define LEMOQ_DPP_ROW_HALF_MIRROR 0x141
+#define LEMOQ_DPP_ROW_MIRROR 0x140
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                                0xF, 0xF, false));
+}
+__device__ __forceinline__ float lane_f(float v, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, LEMOQ_WAVE);
-  return v;
+  v += dpp_f<LEMOQ_DPP_QUAD_1032>(v);
+  v += dpp_f<LEMOQ_DPP_QUAD_2301>(v);
+  v += dpp_f<LEMOQ_DPP_ROW_HALF_MIRROR>(v);
+  v += dpp_f<LEMOQ_DPP_ROW_MIRROR>(v);
+  return (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48));
 }
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, LEMOQ_WAVE));
-  return v;
+  v = fmaxf(v, dpp_f<LEMOQ_DPP_QUAD_1032>(v));
+  v = fmaxf(v, dpp_f<LEMOQ_DPP_QUAD_2301>(v));
+  v = fmaxf(v, dpp_f<LEMOQ_DPP_ROW_HALF_MIRROR>(v));
+  v = fmaxf(v, dpp_f<LEMOQ_DPP_ROW_MIRROR>(v));
+  return fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(lane_f(v, 32), lane_f(v, 48)));
 }
 // Sum over aligned groups of G lanes (G a power of two <= 64).
 template <int G>
@@ -108,9 +131,255 @@ __device__ __forceinline__ float dot16_i8(const u32x4 c, const XChunk& xc, float
   return acc;
 }
 
+// Build the dot-order chunk from 16 consecutive fp16 values held in two
+// dwordx4 registers (same permutation as load_xchunk).
+__device__ __forceinline__ void make_xchunk(const u32x4 p0, const u32x4 p1, XChunk& xc) {
+  const uint32_t w[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t lo = w[2 * i], hi = w[2 * i + 1];
+    xc.a[i] = as_h2((lo & 0xFFFFu) | (hi << 16));
+    xc.b[i] = as_h2((lo >> 16) | (hi & 0xFFFF0000u));
+  }
+}
+
 // 16-byte global load of weights that are streamed once per step.
 __device__ __forceinline__ u32x4 load_stream16(const int8_t* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+
+// ---------------------------------------------------------------------------
+// Loads-first streaming of int8 weight rows.
+//
+// A row of Kp int8 codes is read as ceil(Kp/1024) chunks of 1 KB; lane l owns
+// bytes [1024*j + 16*l, +16) of chunk j, so its 16 codes lie inside one
+// quantisation group (group % 16 == 0) and need one fp16 scale.  w8_issue
+// only issues the loads (codes and scales of R rows); callers issue every
+// other independent load next and only then start arithmetic, so each lane
+// keeps R*KCH 16-byte loads in flight from the first cycles of the kernel.
+// ---------------------------------------------------------------------------
+template <int R, int KCH>
+struct W8Tile {
+  u32x4 c[R][KCH];
+  uint16_t s[R][KCH];
+  uint32_t ok;  // bit r*KCH + j: slice (r, j) lies inside the matrix
+};
+
+// EXACT: every row of the tile exists and Kp == 1024*KCH, so the loads are
+// straight-line code.  Otherwise addresses are clamped into the matrix (no
+// branch around a load, which would make the compiler wait on each one) and
+// the slices outside it are zeroed through `ok` when they are used.
+template <int R, int KCH, bool EXACT>
+__device__ __forceinline__ void w8_issue(W8Tile<R, KCH>& t, const int8_t* __restrict__ codes,
+                                         const uint16_t* __restrict__ scale, int64_t row0,
+                                         int64_t nrows, int Kp, int ngroups, int group,
+                                         int lane) {
+  t.ok = 0u;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int64_t row = row0 + r;
+#pragma unroll
+    for (int j = 0; j < KCH; ++j) {
+      const int off = 1024 * j + 16 * lane;
+      if constexpr (EXACT) {
+        t.c[r][j] = load_stream16(codes + row * Kp + off);
+        t.s[r][j] = scale[row * ngroups + off / group];
+        t.ok |= 1u << (r * KCH + j);
+      } else {
+        const bool in = row < nrows && off < Kp;
+        const int64_t rr = in ? row : 0;
+        const int oo = in ? off : 0;
+        t.c[r][j] = load_stream16(codes + rr * Kp + oo);
+        t.s[r][j] = scale[rr * ngroups + oo / group];
+        t.ok |= (in ? 1u : 0u) << (r * KCH + j);
+      }
+    }
+  }
+}
+
+// sum_j scale_j * (codes_j . x_j) for row r of the tile.
+template <int R, int KCH>
+__device__ __forceinline__ float w8_row_dot(const W8Tile<R, KCH>& t, int r, const XChunk (&xc)[KCH]) {
+  float a = 0.0f;
+#pragma unroll
+  for (int j = 0; j < KCH; ++j) {
+    const float sc = ((t.ok >> (r * KCH + j)) & 1u) ? h2f(t.s[r][j]) : 0.0f;
+    a = fmaf(sc, dot16_i8(t.c[r][j], xc[j], 0.0f), a);
+  }
+  return a;
+}
+
+// The activation slice of one lane: 16 fp16 values per 1 KB chunk, raw bits.
+template <int KCH>
+struct XRaw {
+  u32x4 v[KCH][2];
+};
+
+// Issue the loads of src[1024*j + 16*lane, +16) for every chunk.
+// EXACT: n == 1024*KCH and src 16-byte aligned (straight-line vector loads).
+// Otherwise elements at or beyond n read as 0; `vec` (uniform) says src is
+// 16-byte aligned and n % 8 == 0, so whole in-range slices use vector loads.
+template <int KCH, bool EXACT>
+__device__ __forceinline__ void x_issue(XRaw<KCH>& x, const uint16_t* __restrict__ src, int n,
+                                        bool vec, int lane) {
+#pragma unroll
+  for (int j = 0; j < KCH; ++j) {
+    const int off = 1024 * j + 16 * lane;
+    if (EXACT || (vec && off + 16 <= n)) {
+      x.v[j][0] = *reinterpret_cast<const u32x4*>(src + off);
+      x.v[j][1] = *reinterpret_cast<const u32x4*>(src + off + 8);
+    } else {
+      uint32_t w[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int e = off + 2 * i;
+        const uint32_t lo = e < n ? src[e] : 0u;
+        const uint32_t hi = e + 1 < n ? src[e + 1] : 0u;
+        w[i] = lo | (hi << 16);
+      }
+      x.v[j][0] = (u32x4){w[0], w[1], w[2], w[3]};
+      x.v[j][1] = (u32x4){w[4], w[5], w[6], w[7]};
+    }
+  }
+}
+
+// HF RMSNorm of the whole row held by the wave (lane slices of x), in place:
+// x := fp16(fp16(x * rsqrt(mean(x^2) + eps)) * w), fp32 mean over n values.
+template <int KCH>
+__device__ __forceinline__ void x_rmsnorm(XRaw<KCH>& x, const XRaw<KCH>& w, int n, float eps) {
+  float ssq = 0.0f;
+#pragma unroll
+  for (int j = 0; j < KCH; ++j)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t q[4] = {x.v[j][h].x, x.v[j][h].y, x.v[j][h].z, x.v[j][h].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float a = h2f((uint16_t)(q[i] & 0xFFFFu)), b = h2f((uint16_t)(q[i] >> 16));
+        ssq = fmaf(a, a, ssq);
+        ssq = fmaf(b, b, ssq);
+      }
+    }
+  const float rstd = 1.0f / sqrtf(wave_sum(ssq) / (float)n + eps);
+#pragma unroll
+  for (int j = 0; j < KCH; ++j)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t q[4] = {x.v[j][h].x, x.v[j][h].y, x.v[j][h].z, x.v[j][h].w};
+      const uint32_t g[4] = {w.v[j][h].x, w.v[j][h].y, w.v[j][h].z, w.v[j][h].w};
+      uint32_t o[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint16_t a = f2h(h2f((uint16_t)(q[i] & 0xFFFFu)) * rstd);
+        const uint16_t b = f2h(h2f((uint16_t)(q[i] >> 16)) * rstd);
+        const uint16_t ya = f2h(h2f(a) * h2f((uint16_t)(g[i] & 0xFFFFu)));
+        const uint16_t yb = f2h(h2f(b) * h2f((uint16_t)(g[i] >> 16)));
+        o[i] = (uint32_t)ya | ((uint32_t)yb << 16);
+      }
+      x.v[j][h] = (u32x4){o[0], o[1], o[2], o[3]};
+    }
+}
+
+template <int KCH>
+__device__ __forceinline__ void x_chunks(const XRaw<KCH>& x, XChunk (&xc)[KCH]) {
+#pragma unroll
+  for (int j = 0; j < KCH; ++j) make_xchunk(x.v[j][0], x.v[j][1], xc[j]);
+}
+
+// Keep the scheduler from moving arithmetic above the loads issued so far.
+#define LEMOQ_LOADS_ISSUED() __builtin_amdgcn_sched_barrier(0)
+
+// ---------------------------------------------------------------------------
+// Routing of one token inside one wave (the arithmetic of
+// src/lemoq/kernels/_routing_triton.py:55-80 and moe_static._route,
+// src/lemoq/kernels/moe_static.py:276-283): p = exp(z - max) / sum exp(z - max)
+// in fp32 over E <= 64*PL values (lane l holds elements l + 64*i), then top_k
+// rounds of argmax (ties -> lowest index), optional renormalisation over the
+// selected k.  Lane k < top_k returns the k-th selection (id, weight).
+// ---------------------------------------------------------------------------
+template <int PL>
+__device__ __forceinline__ void wave_route(const float (&z)[PL], int E, int top_k, bool norm,
+                                           int& my_id, float& my_w) {
+  const int lane = threadIdx.x & 63;
+  float mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < PL; ++i)
+    if (lane + 64 * i < E) mx = fmaxf(mx, z[i]);
+  mx = wave_max(mx);
+  float p[PL];
+  float sum = 0.0f;
+#pragma unroll
+  for (int i = 0; i < PL; ++i) {
+    p[i] = (lane + 64 * i < E) ? expf(z[i] - mx) : 0.0f;
+    sum += p[i];
+  }
+  sum = wave_sum(sum);
+#pragma unroll
+  for (int i = 0; i < PL; ++i) p[i] = (lane + 64 * i < E) ? p[i] / sum : -1.0f;
+  my_id = 0;
+  my_w = 0.0f;
+  float wsum = 0.0f;
+  if constexpr (PL == 1) {
+    // Rank of this lane's probability among the wave's 64 (larger first, ties
+    // -> lower index: the order K rounds of argmax produce; lanes >= E hold
+    // -1), read back as broadcasts from a per-wave LDS copy; then the k-th
+    // selection is the lane of rank k (one ballot per k).
+    __shared__ __align__(16) float route_p[16][64];
+    float* sp = route_p[(threadIdx.x >> 6) & 15];
+    sp[lane] = p[0];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    int rank = 0;
+#pragma unroll
+    for (int j = 0; j < 64; j += 4) {
+      const float4 v = *reinterpret_cast<const float4*>(sp + j);
+      rank += (v.x > p[0] || (v.x == p[0] && j < lane)) ? 1 : 0;
+      rank += (v.y > p[0] || (v.y == p[0] && j + 1 < lane)) ? 1 : 0;
+      rank += (v.z > p[0] || (v.z == p[0] && j + 2 < lane)) ? 1 : 0;
+      rank += (v.w > p[0] || (v.w == p[0] && j + 3 < lane)) ? 1 : 0;
+    }
+    for (int k = 0; k < top_k; ++k) {
+      const uint64_t b = __ballot(rank == k);
+      const int id = (int)__builtin_ctzll(b);
+      const float w = sp[id];
+      if (lane == k) {
+        my_id = id;
+        my_w = w;
+      }
+      wsum += w;
+    }
+  } else {
+    uint32_t taken = 0u;
+    for (int k = 0; k < top_k; ++k) {
+      float bv = -2.0f;
+      int bi = 0x7fffffff;
+#pragma unroll
+      for (int i = 0; i < PL; ++i) {
+        const int idx = lane + 64 * i;
+        if (!((taken >> i) & 1u) && idx < E && p[i] > bv) {
+          bv = p[i];
+          bi = idx;
+        }
+      }
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(bv, o, 64);
+        const int oi = __shfl_xor(bi, o, 64);
+        if (ov > bv || (ov == bv && oi < bi)) {
+          bv = ov;
+          bi = oi;
+        }
+      }
+      if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
+      if (lane == k) {
+        my_id = bi;
+        my_w = bv;
+      }
+      wsum += bv;
+    }
+  }
+  if (norm) my_w = my_w / wsum;
 }
 
 // ---------------------------------------------------------------------------

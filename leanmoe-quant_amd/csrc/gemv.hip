@@ -1,164 +1,164 @@
-// w8a16 dense GEMV (dequantisation in registers), the fused router
-// (RMSNorm + fp16 GEMV + softmax/top-k), routing top-k and the greedy argmax
-// that advances the decode position on the device.
+// w8a16 dense GEMV (dequantisation in registers), the router (RMSNorm + fp16
+// GEMV + softmax/top-k), routing top-k, and the greedy argmax that advances
+// the decode position on the device.
 //
-// GEMV layout.  A 256-thread block is 4 waves; each wave owns R consecutive
-// output rows.  A row of K int8 codes is read as K/1024 chunks of 1 KB: lane l
-// loads the 16 bytes at 1024*j + 16*l (one global_load_dwordx4, fully
-// coalesced), so a lane's 16 codes always sit inside one quantisation group
-// (group % 16 == 0) and it needs exactly one fp16 scale per chunk.  The
-// activation row is staged once per block in LDS (with the RMSNorm prologue
-// applied there when requested) and each lane keeps its own 16*K/1024 values
-// in registers, pre-permuted for v_dot2_f32_f16.  After the loads of all R
-// rows are issued, each lane forms s * sum(c*x) per chunk and a wave
-// butterfly reduces the row.  No MFMA: at batch 1 this is ~1 flop/byte and
-// HBM bound.
+// GEMV layout.  A 256-thread block is 4 independent waves; wave w of block b
+// owns the R consecutive output rows (4b + w)*R ... and never synchronises
+// with the other waves.  Each lane first issues every load it will need: the
+// 16-byte code slices of its R rows (lane l reads bytes [1024j + 16l, +16) of
+// chunk j of a row, fully coalesced) with their fp16 scales, then its slice
+// of the activation row (and of the RMSNorm weight).  Only then does any
+// arithmetic start: the RMSNorm of the prologue is a wave reduction over the
+// slices (the wave holds the whole row), codes are turned into exact fp16
+// pairs and reduced with v_dot2_f32_f16 in fp32, and a butterfly sums each
+// row.  No LDS and no barrier stand between kernel entry and the weight
+// stream.  No MFMA: at batch 1 this is ~1 flop per weight byte, HBM bound.
 #include "common.h"
 
 namespace {
 
-// Stage x[0:K) (fp16) into LDS xs[0:KCH*1024), zero padded; optionally apply
-// the HF RMSNorm (fp32 mean of squares, x*rstd rounded to fp16, times the
-// fp16 weight with one rounding).  Returns after a block barrier.
-template <int KCH>
-__device__ __forceinline__ void stage_x(const uint16_t* __restrict__ xr, int K,
-                                        const uint16_t* __restrict__ norm_w, float eps,
-                                        uint16_t* __restrict__ x_copy, bool write_copy,
-                                        uint16_t* __restrict__ xs, float* __restrict__ red) {
-  const int tid = threadIdx.x;
-  constexpr int KP = KCH * 1024;
-  const bool vec = ((K & 7) == 0) && ((reinterpret_cast<uintptr_t>(xr) & 15u) == 0);
-  float ssq = 0.0f;
-  if (vec) {
-    for (int i = tid * 8; i < KP; i += 256 * 8) {
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (i < K) v = *reinterpret_cast<const u32x4*>(xr + i);
-      *reinterpret_cast<u32x4*>(xs + i) = v;
-      if (norm_w) {
-        const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float a = h2f((uint16_t)(w4[q] & 0xFFFFu));
-          const float b = h2f((uint16_t)(w4[q] >> 16));
-          ssq += a * a;
-          ssq += b * b;
-        }
-      }
-      if (write_copy && i < K) *reinterpret_cast<u32x4*>(x_copy + i) = v;
-    }
-  } else {
-    for (int i = tid; i < KP; i += 256) {
-      const uint16_t v = i < K ? xr[i] : (uint16_t)0;
-      xs[i] = v;
-      if (norm_w) {
-        const float a = h2f(v);
-        ssq += a * a;
-      }
-      if (write_copy && i < K) x_copy[i] = v;
-    }
-  }
-  if (norm_w) {
-    ssq = wave_sum(ssq);
-    if ((tid & 63) == 0) red[tid >> 6] = ssq;
-    __syncthreads();
-    const float tot = red[0] + red[1] + red[2] + red[3];
-    const float rstd = 1.0f / sqrtf(tot / (float)K + eps);
-    for (int i = tid; i < K; i += 256) {
-      const uint16_t nh = f2h(h2f(xs[i]) * rstd);
-      xs[i] = f2h(h2f(nh) * h2f(norm_w[i]));
-    }
-  }
-  __syncthreads();
-}
+struct GemvArgs {
+  const uint16_t* x;
+  int64_t x_ld;
+  const int64_t* x_row_index;  // embedding gather: row *x_row_index of x
+  int64_t x_rows;
+  int K;
+  const uint16_t* norm_w;  // RMSNorm prologue when non-null
+  float eps;
+  uint16_t* x_copy;  // block 0 / wave 0 stores the raw input row here
+  const int8_t* codes;
+  const uint16_t* scale;
+  int64_t N;
+  int Kp;
+  int group;
+  const uint16_t* resid;  // y = fp16(fp16(acc) + resid) when non-null
+  void* y;
+  int64_t y_ld;
+  int y_f16;
+  // argmax epilogue: per-block best (fp16-rounded value, lowest row)
+  float* am_val;
+  int32_t* am_idx;
+};
 
-template <int KCH, int R>
-__global__ __launch_bounds__(256) void gemv_w8_kernel(
-    const uint16_t* __restrict__ x, int64_t x_ld, const int64_t* __restrict__ x_row_index,
-    int64_t x_rows, int K, const uint16_t* __restrict__ norm_w, float eps,
-    uint16_t* __restrict__ x_copy, const int8_t* __restrict__ codes,
-    const uint16_t* __restrict__ scale, int64_t N, int Kp, int group,
-    const uint16_t* __restrict__ resid, void* __restrict__ y, int64_t y_ld, int y_f16) {
-  __shared__ __align__(16) uint16_t xs[KCH * 1024];
-  __shared__ float red[4];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+constexpr int kArgmaxPlain = 0;
+constexpr int kArgmaxPartials = 1;
+
+template <int KCH, int R, int MODE, bool EXACT>
+__global__ __launch_bounds__(256) void gemv_w8_kernel(const GemvArgs a) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t m = blockIdx.y;
+  const int64_t row0 = ((int64_t)blockIdx.x * 4 + wave) * R;
+
+  W8Tile<R, KCH> t;
+  w8_issue<R, KCH, EXACT>(t, a.codes, a.scale, row0, a.N, a.Kp, a.Kp / a.group, a.group, lane);
 
   const uint16_t* xr;
-  bool x_valid = true;
-  if (x_row_index) {
-    const int64_t r = x_row_index[0];
-    x_valid = r >= 0 && r < x_rows;
-    xr = x + (x_valid ? r : 0) * x_ld;
+  bool x_ok = true;
+  if (a.x_row_index) {
+    const int64_t r = a.x_row_index[0];
+    x_ok = r >= 0 && r < a.x_rows;  // an index outside the table reads as a zero row
+    xr = a.x + (x_ok ? r : 0) * a.x_ld;
   } else {
-    xr = x + m * x_ld;
+    xr = a.x + m * a.x_ld;
   }
-  stage_x<KCH>(xr, x_valid ? K : 0, norm_w, eps, x_copy, x_copy != nullptr && blockIdx.x == 0,
-               xs, red);
-
-  XChunk xc[KCH];
+  const bool vec = ((reinterpret_cast<uintptr_t>(xr) & 15u) == 0) && ((a.K & 7) == 0);
+  XRaw<KCH> xv;
+  x_issue<KCH, EXACT>(xv, xr, a.K, vec, lane);
+  XRaw<KCH> nw;
+  if (a.norm_w) {
+    const bool nvec = ((reinterpret_cast<uintptr_t>(a.norm_w) & 15u) == 0) && ((a.K & 7) == 0);
+    x_issue<KCH, EXACT>(nw, a.norm_w, a.K, nvec, lane);
+  }
+  LEMOQ_LOADS_ISSUED();
+  if (!x_ok) {
 #pragma unroll
-  for (int j = 0; j < KCH; ++j) load_xchunk(xs + 1024 * j + 16 * lane, xc[j]);
+    for (int j = 0; j < KCH; ++j) xv.v[j][0] = xv.v[j][1] = (u32x4){0u, 0u, 0u, 0u};
+  }
 
-  const int ngroups = Kp / group;
-  int gidx[KCH];
-#pragma unroll
-  for (int j = 0; j < KCH; ++j) gidx[j] = (1024 * j + 16 * lane) / group;
-
-  const int64_t row0 = ((int64_t)blockIdx.x * 4 + wave) * R;
-  u32x4 c[R][KCH];
-  float s[R][KCH];
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int64_t n = row0 + r;
+  if (a.x_copy && blockIdx.x == 0 && wave == 0) {
 #pragma unroll
     for (int j = 0; j < KCH; ++j) {
       const int off = 1024 * j + 16 * lane;
-      if (n < N && off < Kp) {
-        c[r][j] = load_stream16(codes + n * Kp + off);
-        s[r][j] = h2f(scale[n * ngroups + gidx[j]]);
-      } else {
-        c[r][j] = (u32x4){0u, 0u, 0u, 0u};
-        s[r][j] = 0.0f;
-      }
+      const uint32_t w[8] = {xv.v[j][0].x, xv.v[j][0].y, xv.v[j][0].z, xv.v[j][0].w,
+                             xv.v[j][1].x, xv.v[j][1].y, xv.v[j][1].z, xv.v[j][1].w};
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        if (off + i < a.K) a.x_copy[off + i] = (uint16_t)(w[i >> 1] >> (16 * (i & 1)));
     }
   }
+  if (a.norm_w) x_rmsnorm<KCH>(xv, nw, a.K, a.eps);
+  XChunk xc[KCH];
+  x_chunks<KCH>(xv, xc);
+
   float acc[R];
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    float a = 0.0f;
+  for (int r = 0; r < R; ++r) acc[r] = wave_sum(w8_row_dot<R, KCH>(t, r, xc));
+
+  if (MODE == kArgmaxPlain) {
+    if (lane < R) {
+      float v = acc[0];
 #pragma unroll
-    for (int j = 0; j < KCH; ++j) a = fmaf(s[r][j], dot16_i8(c[r][j], xc[j], 0.0f), a);
-    acc[r] = wave_sum(a);
-  }
-  if (lane < R) {
-    float v = acc[0];
-#pragma unroll
-    for (int r = 1; r < R; ++r)
-      if (lane == r) v = acc[r];
-    const int64_t n = row0 + lane;
-    if (n < N) {
-      if (y_f16) {
-        uint16_t o = f2h(v);
-        if (resid) o = hadd_round(h2f(o), resid[n]);
-        reinterpret_cast<uint16_t*>(y)[m * y_ld + n] = o;
-      } else {
-        reinterpret_cast<float*>(y)[m * y_ld + n] = v;
+      for (int r = 1; r < R; ++r)
+        if (lane == r) v = acc[r];
+      const int64_t n = row0 + lane;
+      if (n < a.N) {
+        if (a.y_f16) {
+          uint16_t o = f2h(v);
+          if (a.resid) o = hadd_round(h2f(o), a.resid[n]);
+          reinterpret_cast<uint16_t*>(a.y)[m * a.y_ld + n] = o;
+        } else {
+          reinterpret_cast<float*>(a.y)[m * a.y_ld + n] = v;
+        }
       }
+    }
+  } else {
+    // fp16 logits out, plus this block's best (value, lowest row).
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t n = row0 + r;
+      const uint16_t o = f2h(acc[r]);
+      if (n < a.N) {
+        if (lane == r) reinterpret_cast<uint16_t*>(a.y)[n] = o;
+        const float v = h2f(o);
+        if (v > bv) {  // rows ascend: strict > keeps the lowest row on ties
+          bv = v;
+          bi = (int)n;
+        }
+      }
+    }
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    if (lane == 0) {
+      sv[wave] = bv;
+      si[wave] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float v = sv[0];
+      int i = si[0];
+#pragma unroll
+      for (int w = 1; w < 4; ++w)
+        if (sv[w] > v || (sv[w] == v && si[w] < i)) {
+          v = sv[w];
+          i = si[w];
+        }
+      const bool none = i == 0x7fffffff;  // no valid row in this block
+      a.am_val[blockIdx.x] = none ? -INFINITY : v;
+      a.am_idx[blockIdx.x] = none ? -1 : i;
     }
   }
 }
 
-template <int KCH>
-int launch_gemv(int R, dim3 grid, hipStream_t st, const uint16_t* x, int64_t x_ld,
-                const int64_t* x_row_index, int64_t x_rows, int K, const uint16_t* norm_w,
-                float eps, uint16_t* x_copy, const int8_t* codes, const uint16_t* scale,
-                int64_t N, int Kp, int group, const uint16_t* resid, void* y, int64_t y_ld,
-                int y_f16) {
-#define LEMOQ_GEMV_CASE(RR)                                                                      \
-  case RR:                                                                                       \
-    hipLaunchKernelGGL((gemv_w8_kernel<KCH, RR>), grid, dim3(256), 0, st, x, x_ld, x_row_index, \
-                       x_rows, K, norm_w, eps, x_copy, codes, scale, N, Kp, group, resid, y,    \
-                       y_ld, y_f16);                                                             \
+template <int KCH, int MODE>
+int launch_gemv(int R, bool exact, dim3 grid, hipStream_t st, const GemvArgs& a) {
+#define LEMOQ_GEMV_CASE(RR)                                                                     \
+  case RR:                                                                                      \
+    if (exact)                                                                                  \
+      hipLaunchKernelGGL((gemv_w8_kernel<KCH, RR, MODE, true>), grid, dim3(256), 0, st, a);    \
+    else                                                                                        \
+      hipLaunchKernelGGL((gemv_w8_kernel<KCH, RR, MODE, false>), grid, dim3(256), 0, st, a);   \
     break;
   switch (R) {
     LEMOQ_GEMV_CASE(1)
@@ -170,224 +170,94 @@ int launch_gemv(int R, dim3 grid, hipStream_t st, const uint16_t* x, int64_t x_l
   LEMOQ_CHECK_LAUNCH();
 }
 
+// Rows per wave: enough waves to cover the 256 CUs several times over for the
+// small matrices, fewer redundant activation reads for the large ones.
 int rows_per_wave(int64_t N) { return N <= 4096 ? 1 : (N <= 16384 ? 2 : 4); }
 
-int gemv_dispatch(hipStream_t st, const uint16_t* x, int64_t x_ld, const int64_t* x_row_index,
-                  int64_t x_rows, int64_t M, int64_t K, const uint16_t* norm_w, float eps,
-                  uint16_t* x_copy, const int8_t* codes, const uint16_t* scale, int64_t N,
-                  int64_t Kp, int64_t group, const uint16_t* resid, void* y, int64_t y_ld,
-                  int y_f16) {
-  if (N <= 0 || M <= 0 || K <= 0) return LEMOQ_ERR_SHAPE;
-  if (Kp > 8192 || Kp % 16 != 0 || group <= 0 || group % 16 != 0 || Kp % group != 0 || K > Kp)
+int kch_pow2(int64_t Kp) {
+  const int64_t kch = (Kp + 1023) / 1024;
+  return kch <= 1 ? 1 : (kch <= 2 ? 2 : (kch <= 4 ? 4 : 8));
+}
+
+template <int MODE>
+int gemv_dispatch(hipStream_t st, GemvArgs a, int64_t M) {
+  if (a.N <= 0 || M <= 0 || a.K <= 0) return LEMOQ_ERR_SHAPE;
+  if (a.Kp > 8192 || a.Kp % 16 != 0 || a.group <= 0 || a.group % 16 != 0 || a.Kp % a.group != 0 ||
+      a.K > a.Kp)
     return LEMOQ_ERR_UNSUPPORTED;
   if (M > 65535) return LEMOQ_ERR_SHAPE;
-  if (!lemoq_aligned16(codes)) return LEMOQ_ERR_ALIGN;
-  const int R = rows_per_wave(N);
-  const int64_t blocks = (N + 4 * R - 1) / (4 * R);
+  if (!lemoq_aligned16(a.codes)) return LEMOQ_ERR_ALIGN;
+  const int R = rows_per_wave(a.N);
+  const int64_t blocks = (a.N + 4 * R - 1) / (4 * R);
   if (blocks > 0x7fffffffLL) return LEMOQ_ERR_SHAPE;
   dim3 grid((unsigned)blocks, (unsigned)M);
-  const int kch = (int)((Kp + 1023) / 1024);
-  const int kch_pow2 = kch <= 1 ? 1 : (kch <= 2 ? 2 : (kch <= 4 ? 4 : 8));
-  switch (kch_pow2) {
-    case 1:
-      return launch_gemv<1>(R, grid, st, x, x_ld, x_row_index, x_rows, (int)K, norm_w, eps,
-                            x_copy, codes, scale, N, (int)Kp, (int)group, resid, y, y_ld, y_f16);
-    case 2:
-      return launch_gemv<2>(R, grid, st, x, x_ld, x_row_index, x_rows, (int)K, norm_w, eps,
-                            x_copy, codes, scale, N, (int)Kp, (int)group, resid, y, y_ld, y_f16);
-    case 4:
-      return launch_gemv<4>(R, grid, st, x, x_ld, x_row_index, x_rows, (int)K, norm_w, eps,
-                            x_copy, codes, scale, N, (int)Kp, (int)group, resid, y, y_ld, y_f16);
-    default:
-      return launch_gemv<8>(R, grid, st, x, x_ld, x_row_index, x_rows, (int)K, norm_w, eps,
-                            x_copy, codes, scale, N, (int)Kp, (int)group, resid, y, y_ld, y_f16);
+  const int kch = kch_pow2(a.Kp);
+  // Straight-line loads when the tile never leaves the matrix and the
+  // activation rows are whole aligned 1 KB chunks.
+  const bool exact = a.K == a.Kp && a.Kp == 1024 * kch && a.N % (4 * R) == 0 &&
+                     lemoq_aligned16(a.x) && (M == 1 || a.x_ld % 8 == 0) &&
+                     (a.x_row_index == nullptr || a.x_ld % 8 == 0) &&
+                     (a.norm_w == nullptr || lemoq_aligned16(a.norm_w));
+  switch (kch) {
+    case 1: return launch_gemv<1, MODE>(R, exact, grid, st, a);
+    case 2: return launch_gemv<2, MODE>(R, exact, grid, st, a);
+    case 4: return launch_gemv<4, MODE>(R, exact, grid, st, a);
+    default: return launch_gemv<8, MODE>(R, exact, grid, st, a);
   }
 }
 
-}  // namespace
-
-extern "C" int lemoq_gemv_w8(const uint16_t* x, int64_t M, int64_t K, const int8_t* codes,
-                             const uint16_t* scale, int64_t N, int64_t padded_k, int64_t group,
-                             void* y, int y_is_f16, void* stream) {
-  if (!x || !codes || !scale || !y) return LEMOQ_ERR_NULL;
-  return gemv_dispatch(lemoq_stream(stream), x, K, nullptr, 0, M, K, nullptr, 0.0f, nullptr,
-                       codes, scale, N, padded_k, group, nullptr, y, N, y_is_f16 ? 1 : 0);
-}
-
-extern "C" int lemoq_gemv_w8_fused(const uint16_t* x_src, const int64_t* x_row_index,
-                                   int64_t x_rows, const uint16_t* norm_w, float eps,
-                                   uint16_t* x_copy, const int8_t* codes, const uint16_t* scale,
-                                   int64_t N, int64_t K, int64_t group, const uint16_t* residual,
-                                   uint16_t* y, void* stream) {
-  if (!x_src || !codes || !scale || !y) return LEMOQ_ERR_NULL;
-  if (x_row_index && x_rows <= 0) return LEMOQ_ERR_SHAPE;
-  return gemv_dispatch(lemoq_stream(stream), x_src, K, x_row_index, x_rows, 1, K, norm_w, eps,
-                       x_copy, codes, scale, N, K, group, residual, y, N, 1);
+GemvArgs make_args(const uint16_t* x, int64_t x_ld, const int64_t* x_row_index, int64_t x_rows,
+                   int64_t K, const uint16_t* norm_w, float eps, uint16_t* x_copy,
+                   const int8_t* codes, const uint16_t* scale, int64_t N, int64_t Kp,
+                   int64_t group, const uint16_t* resid, void* y, int64_t y_ld, int y_f16) {
+  GemvArgs a;
+  a.x = x;
+  a.x_ld = x_ld;
+  a.x_row_index = x_row_index;
+  a.x_rows = x_rows;
+  a.K = (int)K;
+  a.norm_w = norm_w;
+  a.eps = eps;
+  a.x_copy = x_copy;
+  a.codes = codes;
+  a.scale = scale;
+  a.N = N;
+  a.Kp = (int)Kp;
+  a.group = (int)group;
+  a.resid = resid;
+  a.y = y;
+  a.y_ld = y_ld;
+  a.y_f16 = y_f16;
+  a.am_val = nullptr;
+  a.am_idx = nullptr;
+  return a;
 }
 
 // ---------------------------------------------------------------------------
-// Routing: softmax over E values then top_k by probability (ties -> lowest
-// index), optional renormalisation.  One wave handles one token; lane l holds
-// values l, l+64, ... (E <= 1024).  Arithmetic follows
-// src/lemoq/kernels/_routing_triton.py:55-80 and moe_static._route
-// (src/lemoq/kernels/moe_static.py:276-283): p = exp(z - max) / sum(exp(z - max)).
+// Greedy selection + step advance (one 1024-thread block) over either the
+// fp16 logits themselves (PARTIALS == false: candidate i has value logits[i])
+// or the per-block partials of the lm_head GEMV (value val[i], row idx[i]).
+// Ties resolve to the lowest row; NaN never wins; all -inf/NaN -> row 0.
+// Then: next = argmax, or prompt[*pos + 1] while *pos + 1 < prompt_len;
+// *token = next, history[*pos + 1] = next, *pos += 1, *filled = *pos + 1.
 // ---------------------------------------------------------------------------
-namespace {
-constexpr int kMaxPerLane = 16;  // E <= 1024
-
-__device__ void wave_route_topk(const float (&z)[kMaxPerLane], int E, int top_k, bool norm,
-                                float* __restrict__ out_w32, uint16_t* __restrict__ out_w16,
-                                int64_t* __restrict__ out_i) {
-  const int lane = threadIdx.x & 63;
-  float mx = -INFINITY;
-#pragma unroll
-  for (int i = 0; i < kMaxPerLane; ++i)
-    if (lane + 64 * i < E) mx = fmaxf(mx, z[i]);
-  mx = wave_max(mx);
-  float p[kMaxPerLane];
-  float sum = 0.0f;
-#pragma unroll
-  for (int i = 0; i < kMaxPerLane; ++i) {
-    p[i] = (lane + 64 * i < E) ? expf(z[i] - mx) : 0.0f;
-    sum += p[i];
-  }
-  sum = wave_sum(sum);
-  uint32_t taken = 0u;  // bit i: element lane+64*i already selected
-#pragma unroll
-  for (int i = 0; i < kMaxPerLane; ++i) p[i] = (lane + 64 * i < E) ? p[i] / sum : -1.0f;
-  float wsel = 0.0f;  // lane k < top_k keeps the k-th selected probability
-  float wsum = 0.0f;
-  for (int k = 0; k < top_k; ++k) {
-    float bv = -2.0f;
-    int bi = 0x7fffffff;
-#pragma unroll
-    for (int i = 0; i < kMaxPerLane; ++i) {
-      const int idx = lane + 64 * i;
-      if (!((taken >> i) & 1u) && idx < E && p[i] > bv) {
-        bv = p[i];
-        bi = idx;
-      }
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const float ov = __shfl_xor(bv, o, 64);
-      const int oi = __shfl_xor(bi, o, 64);
-      if (ov > bv || (ov == bv && oi < bi)) {
-        bv = ov;
-        bi = oi;
-      }
-    }
-    if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
-    if (lane == k) wsel = bv;
-    wsum += bv;
-    if (lane == 0) out_i[k] = (int64_t)bi;
-  }
-  if (lane < top_k) {
-    const float w = norm ? wsel / wsum : wsel;
-    if (out_w32) out_w32[lane] = w;
-    if (out_w16) out_w16[lane] = f2h(w);
-  }
-}
-
-__global__ __launch_bounds__(256) void route_topk_kernel(const void* __restrict__ logits, int f16,
-                                                         int64_t T, int E, int64_t stride,
-                                                         int top_k, int norm,
-                                                         float* __restrict__ top_w,
-                                                         int64_t* __restrict__ top_i) {
-  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (t >= T) return;
-  const int lane = threadIdx.x & 63;
-  float z[kMaxPerLane];
-#pragma unroll
-  for (int i = 0; i < kMaxPerLane; ++i) {
-    const int idx = lane + 64 * i;
-    if (idx < E) {
-      z[i] = f16 ? h2f(reinterpret_cast<const uint16_t*>(logits)[t * stride + idx])
-                 : reinterpret_cast<const float*>(logits)[t * stride + idx];
-    } else {
-      z[i] = -INFINITY;
-    }
-  }
-  wave_route_topk(z, E, top_k, norm != 0, top_w + t * top_k, nullptr, top_i + t * top_k);
-}
-
-// Fused router of one token: 16 waves.  RMSNorm of h into LDS (and xn_out),
-// fp16 GEMV over E rows (lane l reads 8 fp16 at 8*l + 512*i: 16-byte loads),
-// logits rounded once to fp16, then wave 0 routes.
-__global__ __launch_bounds__(1024) void router_fused_kernel(
-    const uint16_t* __restrict__ h, const uint16_t* __restrict__ norm_w, float eps, int H,
-    const uint16_t* __restrict__ rw, int E, int top_k, int norm, uint16_t* __restrict__ xn_out,
-    uint16_t* __restrict__ logits_out, float* __restrict__ top_w32,
-    uint16_t* __restrict__ top_w16, int64_t* __restrict__ top_i) {
-  __shared__ __align__(16) uint16_t xs[8192];
-  __shared__ float red[16];
-  __shared__ float lg[1024];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  float ssq = 0.0f;
-  for (int i = tid; i < H; i += 1024) {
-    const uint16_t v = h[i];
-    xs[i] = v;
-    const float a = h2f(v);
-    ssq += a * a;
-  }
-  if (norm_w) {
-    ssq = wave_sum(ssq);
-    if (lane == 0) red[wave] = ssq;
-    __syncthreads();
-    float tot = 0.0f;
-#pragma unroll
-    for (int w = 0; w < 16; ++w) tot += red[w];
-    const float rstd = 1.0f / sqrtf(tot / (float)H + eps);
-    for (int i = tid; i < H; i += 1024) {
-      const uint16_t nh = f2h(h2f(xs[i]) * rstd);
-      xs[i] = f2h(h2f(nh) * h2f(norm_w[i]));
-    }
-  }
-  __syncthreads();
-  if (xn_out)
-    for (int i = tid; i < H; i += 1024) xn_out[i] = xs[i];
-  for (int e = wave; e < E; e += 16) {
-    const uint16_t* wr = rw + (int64_t)e * H;
-    float a = 0.0f;
-    for (int k = 8 * lane; k < H; k += 512) {
-      const u32x4 wv = *reinterpret_cast<const u32x4*>(wr + k);
-      const u32x4 xv = *reinterpret_cast<const u32x4*>(xs + k);
-      const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
-      const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) a = __builtin_amdgcn_fdot2(as_h2(ww[i]), as_h2(xw[i]), a, false);
-    }
-    a = wave_sum(a);
-    if (lane == 0) {
-      const uint16_t lh = f2h(a);
-      lg[e] = h2f(lh);
-      if (logits_out) logits_out[e] = lh;
-    }
-  }
-  __syncthreads();
-  if (wave == 0) {
-    float z[kMaxPerLane];
-#pragma unroll
-    for (int i = 0; i < kMaxPerLane; ++i) z[i] = (lane + 64 * i < E) ? lg[lane + 64 * i] : -INFINITY;
-    wave_route_topk(z, E, top_k, norm != 0, top_w32, top_w16, top_i);
-  }
-}
-
-// Greedy argmax (first index on ties) + step advance, one 1024-thread block.
+template <bool PARTIALS>
 __global__ __launch_bounds__(1024) void argmax_advance_kernel(
-    const uint16_t* __restrict__ logits, int64_t n, int64_t* __restrict__ token,
+    const uint16_t* __restrict__ logits, const float* __restrict__ pv,
+    const int32_t* __restrict__ pi, int64_t n, int64_t* __restrict__ token,
     int64_t* __restrict__ pos, int32_t* __restrict__ filled, const int64_t* __restrict__ prompt,
     int64_t prompt_len, int64_t* __restrict__ history, int64_t history_len) {
   __shared__ float bvs[16];
   __shared__ int64_t bis[16];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   float bv = -INFINITY;
-  int64_t bi = n;  // sentinel larger than every index
+  int64_t bi = INT64_MAX;
   for (int64_t i = tid; i < n; i += 1024) {
-    const float v = h2f(logits[i]);
-    if (v > bv) {  // ascending scan: strict > keeps the first index
+    const float v = PARTIALS ? pv[i] : h2f(logits[i]);
+    const int64_t idx = PARTIALS ? (int64_t)pi[i] : i;
+    if (idx >= 0 && (v > bv || (v == bv && idx < bi))) {
       bv = v;
-      bi = i;
+      bi = idx;
     }
   }
 #pragma unroll
@@ -413,10 +283,10 @@ __global__ __launch_bounds__(1024) void argmax_advance_kernel(
         idx = bis[w];
       }
     }
-    if (idx >= n) idx = 0;  // every logit was -inf or NaN
+    if (idx == INT64_MAX || idx < 0) idx = 0;  // every logit was -inf or NaN
     const int64_t p = pos[0];
     int64_t next = idx;
-    if (prompt && p + 1 < prompt_len) next = prompt[p + 1];
+    if (prompt && p + 1 >= 0 && p + 1 < prompt_len) next = prompt[p + 1];
     token[0] = next;
     if (history && p + 1 >= 0 && p + 1 < history_len) history[p + 1] = next;
     pos[0] = p + 1;
@@ -424,7 +294,226 @@ __global__ __launch_bounds__(1024) void argmax_advance_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Router of one token in one 1024-thread block: xn = RMSNorm(h) and
+// logits[e] = fp16(xn . W[e]) with fp32 accumulation (the F.linear of
+// moe_static._route, src/lemoq/kernels/moe_static.py:262-283, on the
+// post-attention norm's output), then wave 0 routes (softmax, top_k, optional
+// renorm) and writes ids and weights.  Wave w streams rows w*4 .. w*4+3 of
+// each 64-row pass, issuing all of its loads (rows, h, norm weight) first; it
+// recomputes the norm from its own slices (the wave holds the whole row).
+// ---------------------------------------------------------------------------
+template <int KCH, bool EXACT>
+__global__ __launch_bounds__(1024) void router_kernel(
+    const uint16_t* __restrict__ h, const uint16_t* __restrict__ norm_w, float eps, int H,
+    const uint16_t* __restrict__ rw, int E, int top_k, int norm, uint16_t* __restrict__ xn_out,
+    uint16_t* __restrict__ logits_out, float* __restrict__ top_w32,
+    uint16_t* __restrict__ top_w16, int64_t* __restrict__ top_i) {
+  __shared__ float lg[1024];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  XRaw<KCH> xv, nw;
+  bool normed = false;
+  for (int e0 = wave * 4; e0 < E; e0 += 64) {
+    XRaw<KCH> wr[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int e = e0 + r < E ? e0 + r : E - 1;
+      x_issue<KCH, EXACT>(wr[r], rw + (int64_t)e * H, H, true, lane);
+    }
+    if (!normed) {
+      x_issue<KCH, EXACT>(xv, h, H, true, lane);
+      if (norm_w) x_issue<KCH, EXACT>(nw, norm_w, H, true, lane);
+    }
+    LEMOQ_LOADS_ISSUED();
+    if (!normed) {
+      if (norm_w) x_rmsnorm<KCH>(xv, nw, H, eps);
+      normed = true;
+      if (xn_out && wave == 0) {
+#pragma unroll
+        for (int j = 0; j < KCH; ++j) {
+          const int off = 1024 * j + 16 * lane;
+          if (off + 16 <= H) {
+            *reinterpret_cast<u32x4*>(xn_out + off) = xv.v[j][0];
+            *reinterpret_cast<u32x4*>(xn_out + off + 8) = xv.v[j][1];
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int j = 0; j < KCH; ++j)
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const uint32_t ww[4] = {wr[r].v[j][q].x, wr[r].v[j][q].y, wr[r].v[j][q].z, wr[r].v[j][q].w};
+          const uint32_t xw[4] = {xv.v[j][q].x, xv.v[j][q].y, xv.v[j][q].z, xv.v[j][q].w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            acc = __builtin_amdgcn_fdot2(as_h2(ww[i]), as_h2(xw[i]), acc, false);
+        }
+      acc = wave_sum(acc);
+      const int e = e0 + r;
+      if (lane == 0 && e < E) {
+        const uint16_t o = f2h(acc);
+        lg[e] = h2f(o);
+        if (logits_out) logits_out[e] = o;
+      }
+    }
+  }
+  __syncthreads();
+  if (wave == 0) {
+    int id;
+    float w;
+    if (E <= 64) {
+      float z[1] = {lane < E ? lg[lane] : -INFINITY};
+      wave_route<1>(z, E, top_k, norm != 0, id, w);
+    } else {
+      float z[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) z[i] = lane + 64 * i < E ? lg[lane + 64 * i] : -INFINITY;
+      wave_route<16>(z, E, top_k, norm != 0, id, w);
+    }
+    if (lane < top_k) {
+      top_i[lane] = (int64_t)id;
+      if (top_w32) top_w32[lane] = w;
+      if (top_w16) top_w16[lane] = f2h(w);
+    }
+  }
+}
+
+// Routing of T tokens, one wave per token (values per lane PL = ceil(E/64)).
+template <int PL>
+__global__ __launch_bounds__(256) void route_topk_kernel(const void* __restrict__ logits, int f16,
+                                                         int64_t T, int E, int64_t stride,
+                                                         int top_k, int norm,
+                                                         float* __restrict__ top_w32,
+                                                         uint16_t* __restrict__ top_w16,
+                                                         int64_t* __restrict__ top_i) {
+  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const int lane = threadIdx.x & 63;
+  float z[PL];
+#pragma unroll
+  for (int i = 0; i < PL; ++i) {
+    const int idx = lane + 64 * i;
+    if (idx < E) {
+      z[i] = f16 ? h2f(reinterpret_cast<const uint16_t*>(logits)[t * stride + idx])
+                 : reinterpret_cast<const float*>(logits)[t * stride + idx];
+    } else {
+      z[i] = -INFINITY;
+    }
+  }
+  int id;
+  float w;
+  wave_route<PL>(z, E, top_k, norm != 0, id, w);
+  if (lane < top_k) {
+    top_i[t * top_k + lane] = (int64_t)id;
+    if (top_w32) top_w32[t * top_k + lane] = w;
+    if (top_w16) top_w16[t * top_k + lane] = f2h(w);
+  }
+}
+
+int launch_route(hipStream_t st, const void* logits, int f16, int64_t T, int64_t E,
+                 int64_t stride, int64_t top_k, int norm, float* w32, uint16_t* w16,
+                 int64_t* ids) {
+  const int64_t blocks = (T + 3) / 4;
+  if (blocks > 0x7fffffffLL) return LEMOQ_ERR_SHAPE;
+  const int pl = (int)((E + 63) / 64);
+#define LEMOQ_ROUTE_CASE(PP)                                                                    \
+  if (pl <= PP) {                                                                               \
+    hipLaunchKernelGGL((route_topk_kernel<PP>), dim3((unsigned)blocks), dim3(256), 0, st,      \
+                       logits, f16, T, (int)E, stride, (int)top_k, norm, w32, w16, ids);        \
+    LEMOQ_CHECK_LAUNCH();                                                                       \
+  }
+  LEMOQ_ROUTE_CASE(1)
+  LEMOQ_ROUTE_CASE(4)
+  LEMOQ_ROUTE_CASE(16)
+#undef LEMOQ_ROUTE_CASE
+  return LEMOQ_ERR_UNSUPPORTED;
+}
+
+int launch_router(hipStream_t st, const uint16_t* h, const uint16_t* norm_w, float eps, int64_t H,
+                  const uint16_t* rw, int64_t E, int64_t top_k, int norm, uint16_t* xn_out,
+                  uint16_t* logits, float* w32, uint16_t* w16, int64_t* ids) {
+  const int kch = kch_pow2(H);
+  const bool exact = H == 1024 * kch;
+#define LEMOQ_ROUTER_CASE(KK)                                                                    \
+  case KK:                                                                                       \
+    if (exact)                                                                                   \
+      hipLaunchKernelGGL((router_kernel<KK, true>), dim3(1), dim3(1024), 0, st, h, norm_w, eps,  \
+                         (int)H, rw, (int)E, (int)top_k, norm, xn_out, logits, w32, w16, ids);   \
+    else                                                                                         \
+      hipLaunchKernelGGL((router_kernel<KK, false>), dim3(1), dim3(1024), 0, st, h, norm_w, eps, \
+                         (int)H, rw, (int)E, (int)top_k, norm, xn_out, logits, w32, w16, ids);   \
+    break;
+  switch (kch) {
+    LEMOQ_ROUTER_CASE(1)
+    LEMOQ_ROUTER_CASE(2)
+    LEMOQ_ROUTER_CASE(4)
+    LEMOQ_ROUTER_CASE(8)
+    default: return LEMOQ_ERR_UNSUPPORTED;
+  }
+#undef LEMOQ_ROUTER_CASE
+  LEMOQ_CHECK_LAUNCH();
+}
+
 }  // namespace
+
+extern "C" int lemoq_gemv_w8(const uint16_t* x, int64_t M, int64_t K, const int8_t* codes,
+                             const uint16_t* scale, int64_t N, int64_t padded_k, int64_t group,
+                             void* y, int y_is_f16, void* stream) {
+  if (!x || !codes || !scale || !y) return LEMOQ_ERR_NULL;
+  return gemv_dispatch<kArgmaxPlain>(
+      lemoq_stream(stream),
+      make_args(x, K, nullptr, 0, K, nullptr, 0.0f, nullptr, codes, scale, N, padded_k, group,
+                nullptr, y, N, y_is_f16 ? 1 : 0),
+      M);
+}
+
+extern "C" int lemoq_gemv_w8_fused(const uint16_t* x_src, const int64_t* x_row_index,
+                                   int64_t x_rows, const uint16_t* norm_w, float eps,
+                                   uint16_t* x_copy, const int8_t* codes, const uint16_t* scale,
+                                   int64_t N, int64_t K, int64_t group, const uint16_t* residual,
+                                   uint16_t* y, void* stream) {
+  if (!x_src || !codes || !scale || !y) return LEMOQ_ERR_NULL;
+  if (x_row_index && x_rows <= 0) return LEMOQ_ERR_SHAPE;
+  return gemv_dispatch<kArgmaxPlain>(
+      lemoq_stream(stream),
+      make_args(x_src, K, x_row_index, x_rows, K, norm_w, eps, x_copy, codes, scale, N, K, group,
+                residual, y, N, 1),
+      1);
+}
+
+extern "C" int lemoq_lm_head_argmax_w8(const uint16_t* x, const uint16_t* norm_w, float eps,
+                                       const int8_t* codes, const uint16_t* scale, int64_t N,
+                                       int64_t K, int64_t group, uint16_t* logits,
+                                       float* part_val, int32_t* part_idx, int64_t part_len,
+                                       int64_t* token, int64_t* pos, int32_t* filled,
+                                       const int64_t* prompt, int64_t prompt_len,
+                                       int64_t* history, int64_t history_len, void* stream) {
+  if (!x || !codes || !scale || !logits || !part_val || !part_idx || !token || !pos || !filled)
+    return LEMOQ_ERR_NULL;
+  if (N <= 0 || N > 0x7ffffffeLL) return LEMOQ_ERR_SHAPE;
+  const int64_t blocks = (N + 4 * rows_per_wave(N) - 1) / (4 * rows_per_wave(N));
+  if (part_len < blocks) return LEMOQ_ERR_SHAPE;
+  GemvArgs a = make_args(x, K, nullptr, 0, K, norm_w, eps, nullptr, codes, scale, N, K, group,
+                         nullptr, logits, N, 1);
+  a.am_val = part_val;
+  a.am_idx = part_idx;
+  hipStream_t st = lemoq_stream(stream);
+  const int rc = gemv_dispatch<kArgmaxPartials>(st, a, 1);
+  if (rc) return rc;
+  hipLaunchKernelGGL((argmax_advance_kernel<true>), dim3(1), dim3(1024), 0, st, nullptr, part_val,
+                     part_idx, blocks, token, pos, filled, prompt, prompt_len, history,
+                     history_len);
+  LEMOQ_CHECK_LAUNCH();
+}
+
+extern "C" int64_t lemoq_lm_head_argmax_parts(int64_t N) {
+  if (N <= 0) return 0;
+  return (N + 4 * rows_per_wave(N) - 1) / (4 * rows_per_wave(N));
+}
 
 extern "C" int lemoq_route_topk(const void* logits, int logits_is_f16, int64_t T, int64_t E,
                                 int64_t row_stride, int64_t top_k, int norm_topk_prob,
@@ -433,12 +522,8 @@ extern "C" int lemoq_route_topk(const void* logits, int logits_is_f16, int64_t T
   if (T < 0 || E <= 0 || E > 1024 || top_k <= 0 || top_k > E || top_k > 64 || row_stride < E)
     return LEMOQ_ERR_SHAPE;
   if (T == 0) return LEMOQ_OK;
-  const int64_t blocks = (T + 3) / 4;
-  if (blocks > 0x7fffffffLL) return LEMOQ_ERR_SHAPE;
-  hipLaunchKernelGGL(route_topk_kernel, dim3((unsigned)blocks), dim3(256), 0, lemoq_stream(stream),
-                     logits, logits_is_f16 ? 1 : 0, T, (int)E, row_stride, (int)top_k,
-                     norm_topk_prob ? 1 : 0, top_w, top_i);
-  LEMOQ_CHECK_LAUNCH();
+  return launch_route(lemoq_stream(stream), logits, logits_is_f16 ? 1 : 0, T, E, row_stride, top_k,
+                      norm_topk_prob ? 1 : 0, top_w, nullptr, top_i);
 }
 
 extern "C" int lemoq_router_topk_fused(const uint16_t* h, const uint16_t* norm_w, float eps,
@@ -447,13 +532,13 @@ extern "C" int lemoq_router_topk_fused(const uint16_t* h, const uint16_t* norm_w
                                        uint16_t* logits_out, float* top_w_f32,
                                        uint16_t* top_w_f16, int64_t* top_i, void* stream) {
   if (!h || !router_w || !top_i) return LEMOQ_ERR_NULL;
-  if (hidden <= 0 || hidden > 8192 || hidden % 8 != 0) return LEMOQ_ERR_UNSUPPORTED;
+  if (hidden <= 0 || hidden > 8192 || hidden % 16 != 0) return LEMOQ_ERR_UNSUPPORTED;
   if (E <= 0 || E > 1024 || top_k <= 0 || top_k > E || top_k > 64) return LEMOQ_ERR_SHAPE;
-  if (!lemoq_aligned16(router_w)) return LEMOQ_ERR_ALIGN;
-  hipLaunchKernelGGL(router_fused_kernel, dim3(1), dim3(1024), 0, lemoq_stream(stream), h, norm_w,
-                     eps, (int)hidden, router_w, (int)E, (int)top_k, norm_topk_prob ? 1 : 0,
-                     xn_out, logits_out, top_w_f32, top_w_f16, top_i);
-  LEMOQ_CHECK_LAUNCH();
+  if (!lemoq_aligned16(router_w) || !lemoq_aligned16(h) || (norm_w && !lemoq_aligned16(norm_w)) ||
+      (xn_out && !lemoq_aligned16(xn_out)))
+    return LEMOQ_ERR_ALIGN;
+  return launch_router(lemoq_stream(stream), h, norm_w, eps, hidden, router_w, E, top_k,
+                       norm_topk_prob ? 1 : 0, xn_out, logits_out, top_w_f32, top_w_f16, top_i);
 }
 
 extern "C" int lemoq_argmax_advance(const uint16_t* logits, int64_t n, int64_t* token,
@@ -462,7 +547,8 @@ extern "C" int lemoq_argmax_advance(const uint16_t* logits, int64_t n, int64_t* 
                                     void* stream) {
   if (!logits || !token || !pos || !filled) return LEMOQ_ERR_NULL;
   if (n <= 0) return LEMOQ_ERR_SHAPE;
-  hipLaunchKernelGGL(argmax_advance_kernel, dim3(1), dim3(1024), 0, lemoq_stream(stream), logits,
-                     n, token, pos, filled, prompt, prompt_len, history, history_len);
+  hipLaunchKernelGGL((argmax_advance_kernel<false>), dim3(1), dim3(1024), 0, lemoq_stream(stream),
+                     logits, nullptr, nullptr, n, token, pos, filled, prompt, prompt_len, history,
+                     history_len);
   LEMOQ_CHECK_LAUNCH();
 }

@@ -64,99 +64,101 @@ __global__ __launch_bounds__(128) void rope_kernel(const uint16_t* __restrict__ 
   }
 }
 
-// Fused attention prologue.  Block 0: q; block 1: k; block 2: v.
-// LDS holds the normed (then rotated) row of heads*D <= 8192 fp16.
-__global__ __launch_bounds__(256) void qk_norm_rope_kv_kernel(
-    const uint16_t* __restrict__ qkv, int heads, int D, const uint16_t* __restrict__ qn_w,
+// Fused attention prologue, one wave per (row kind, head): blocks
+// [0, heads) take the q heads, [heads, 2*heads) the k heads, [2*heads,
+// 3*heads) the v heads.  A q/k wave reads the whole heads*D row (the RMSNorm
+// is over all heads, as HF's q_norm/k_norm over hidden_size) to form the sum
+// of squares, then normalises and rotates only its own head: lane l holds
+// elements d = l*EPL + i (EPL = D/64) and the rotate_half partner d +- D/2
+// sits in lane l ^ 32.  k and v heads are quantised to KV-INT8 at slot *pos
+// (amax / 127 scale, round-half-even codes; the arithmetic of
+// src/lemoq/kernels/kv_int8.py:196-216).
+template <int EPL>
+__global__ __launch_bounds__(64) void qk_norm_rope_kv_kernel(
+    const uint16_t* __restrict__ qkv, int heads, const uint16_t* __restrict__ qn_w,
     const uint16_t* __restrict__ kn_w, float eps, const uint16_t* __restrict__ cos_tab,
     const uint16_t* __restrict__ sin_tab, const int64_t* __restrict__ pos_ptr,
     uint16_t* __restrict__ q_out, int8_t* __restrict__ kc, uint16_t* __restrict__ ks,
     int8_t* __restrict__ vc, uint16_t* __restrict__ vs, int64_t code_head_stride, int64_t s_len,
     uint16_t* __restrict__ k_f16, uint16_t* __restrict__ v_f16, int64_t f16_head_stride,
     uint16_t* __restrict__ k_rot_out) {
-  __shared__ __align__(16) uint16_t nrm[8192];
-  __shared__ __align__(16) uint16_t rot[8192];
-  __shared__ float red[4];
-  const int which = blockIdx.x;  // 0 q, 1 k, 2 v
+  constexpr int D = 64 * EPL;
+  const int lane = threadIdx.x;
+  const int which = blockIdx.x / heads;  // 0 q, 1 k, 2 v
+  const int h = blockIdx.x - which * heads;
   const int HD = heads * D;
   const int64_t pos = pos_ptr[0];
   const bool pos_ok = pos >= 0 && pos < s_len;
   const uint16_t* src = qkv + (int64_t)which * HD;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int d0 = lane * EPL;
 
-  if (which == 2) {  // v: quantise the raw rows
-    if (!pos_ok) return;
-    for (int h = wave; h < heads; h += 4) {
-      const uint16_t* row = src + (int64_t)h * D;
-      int8_t* dst = vc + (int64_t)h * code_head_stride + pos * D;
-      // amax / scale / codes, same arithmetic as quant_row_wave (quant.hip)
-      float amax = 0.0f;
-      for (int d = lane; d < D; d += 64) amax = fmaxf(amax, fabsf(h2f(row[d])));
-      amax = wave_max(amax);
-      const float s = amax > 0.0f ? amax / 127.0f : 1.0f;
-      for (int d = lane; d < D; d += 64) {
-        float qv = rintf(h2f(row[d]) / s);
-        qv = fminf(fmaxf(qv, -127.0f), 127.0f);
-        dst[d] = (int8_t)(int)qv;
-        if (v_f16) v_f16[(int64_t)h * f16_head_stride + pos * D + d] = row[d];
+  // own head's elements, raw
+  float xv[EPL];
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) xv[i] = h2f(src[h * D + d0 + i]);
+
+  float o[EPL];
+  if (which < 2) {
+    const uint16_t* nw = which == 0 ? qn_w : kn_w;
+    float wv[EPL], cv[EPL], sv[EPL];
+    const int64_t prow = pos_ok ? pos : 0;  // clamped table read; writes need pos_ok
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      wv[i] = h2f(nw[h * D + d0 + i]);
+      cv[i] = h2f(cos_tab[prow * D + d0 + i]);
+      sv[i] = h2f(sin_tab[prow * D + d0 + i]);
+    }
+    float ssq = 0.0f;
+    for (int i = lane * 8; i < HD; i += 64 * 8) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(src + i);
+      const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float a = h2f((uint16_t)(w4[q] & 0xFFFFu)), b = h2f((uint16_t)(w4[q] >> 16));
+        ssq = fmaf(a, a, ssq);
+        ssq = fmaf(b, b, ssq);
       }
-      if (lane == 0) vs[(int64_t)h * s_len + pos] = f2h(s);
     }
-    return;
-  }
-
-  // q or k: RMSNorm over the whole heads*D row.
-  const uint16_t* nw = which == 0 ? qn_w : kn_w;
-  float ssq = 0.0f;
-  for (int i = threadIdx.x; i < HD; i += 256) {
-    const uint16_t v = src[i];
-    nrm[i] = v;
-    const float a = h2f(v);
-    ssq += a * a;
-  }
-  const float tot = block_sum_256(ssq, red);
-  const float rstd = 1.0f / sqrtf(tot / (float)HD + eps);
-  for (int i = threadIdx.x; i < HD; i += 256) {
-    const uint16_t nh = f2h(h2f(nrm[i]) * rstd);
-    nrm[i] = f2h(h2f(nh) * h2f(nw[i]));
-  }
-  __syncthreads();
-  // RoPE with the table row of this position (clamped read; writes need pos_ok).
-  const int64_t prow = pos_ok ? pos : 0;
-  const uint16_t* cr = cos_tab + prow * D;
-  const uint16_t* sr = sin_tab + prow * D;
-  const int half = D / 2;
-  for (int i = threadIdx.x; i < HD; i += 256) {
-    const int h = i / D, d = i - h * D;
-    const bool first = d < half;
-    const int sh = first ? d + half : d - half;
-    const float xv = h2f(nrm[i]);
-    const float xs = h2f(nrm[h * D + sh]);
-    const uint16_t o = f2h(rope_elem(xv, xs, h2f(cr[d]), h2f(sr[d]), first));
+    const float rstd = 1.0f / sqrtf(wave_sum(ssq) / (float)HD + eps);
+    float xn[EPL];
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) xn[i] = h2f(f2h(h2f(f2h(xv[i] * rstd)) * wv[i]));
+    const bool first = lane < 32;  // d < D/2
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      const float xs = __shfl_xor(xn[i], 32, 64);
+      o[i] = h2f(f2h(first ? xn[i] * cv[i] + (-xs) * sv[i] : xn[i] * cv[i] + xs * sv[i]));
+    }
     if (which == 0) {
-      q_out[i] = o;
-    } else {
-      rot[i] = o;
-      if (k_rot_out) k_rot_out[i] = o;
+#pragma unroll
+      for (int i = 0; i < EPL; ++i) q_out[h * D + d0 + i] = f2h(o[i]);
+      return;
     }
-  }
-  if (which == 0 || !pos_ok) return;
-  __syncthreads();
-  for (int h = wave; h < heads; h += 4) {
-    const uint16_t* row = rot + h * D;
-    int8_t* dst = kc + (int64_t)h * code_head_stride + pos * D;
-    float amax = 0.0f;
-    for (int d = lane; d < D; d += 64) amax = fmaxf(amax, fabsf(h2f(row[d])));
-    amax = wave_max(amax);
-    const float s = amax > 0.0f ? amax / 127.0f : 1.0f;
-    for (int d = lane; d < D; d += 64) {
-      float qv = rintf(h2f(row[d]) / s);
-      qv = fminf(fmaxf(qv, -127.0f), 127.0f);
-      dst[d] = (int8_t)(int)qv;
-      if (k_f16) k_f16[(int64_t)h * f16_head_stride + pos * D + d] = row[d];
+    if (k_rot_out) {
+#pragma unroll
+      for (int i = 0; i < EPL; ++i) k_rot_out[h * D + d0 + i] = f2h(o[i]);
     }
-    if (lane == 0) ks[(int64_t)h * s_len + pos] = f2h(s);
+  } else {
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) o[i] = xv[i];
   }
+  if (!pos_ok) return;
+  // KV-INT8 quantisation of this head's row.
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) amax = fmaxf(amax, fabsf(o[i]));
+  amax = wave_max(amax);
+  const float s = amax > 0.0f ? amax / 127.0f : 1.0f;
+  int8_t* dst = (which == 1 ? kc : vc) + (int64_t)h * code_head_stride + pos * D;
+  uint16_t* f16dst = which == 1 ? k_f16 : v_f16;
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    float qv = rintf(o[i] / s);
+    qv = fminf(fmaxf(qv, -127.0f), 127.0f);
+    dst[d0 + i] = (int8_t)(int)qv;
+    if (f16dst) f16dst[(int64_t)h * f16_head_stride + pos * D + d0 + i] = f2h(o[i]);
+  }
+  if (lane == 0) (which == 1 ? ks : vs)[(int64_t)h * s_len + pos] = f2h(s);
 }
 
 }  // namespace
@@ -196,13 +198,22 @@ extern "C" int lemoq_qk_norm_rope_kv_i8(const uint16_t* qkv, int64_t heads, int6
   if (!qkv || !q_norm_w || !k_norm_w || !cos_tab || !sin_tab || !pos || !q_out || !kc || !ks ||
       !vc || !vs)
     return LEMOQ_ERR_NULL;
-  if (heads <= 0 || head_dim < 2 || head_dim % 2 != 0 || heads * head_dim > 8192)
-    return LEMOQ_ERR_SHAPE;
+  if (heads <= 0 || heads > 4096 || heads * head_dim > 65536) return LEMOQ_ERR_SHAPE;
+  if (head_dim != 64 && head_dim != 128 && head_dim != 256) return LEMOQ_ERR_UNSUPPORTED;
+  if (!lemoq_aligned16(qkv)) return LEMOQ_ERR_ALIGN;
   if (s_len <= 0 || code_head_stride < s_len * head_dim) return LEMOQ_ERR_SHAPE;
   if ((k_f16 || v_f16) && f16_head_stride < s_len * head_dim) return LEMOQ_ERR_SHAPE;
-  hipLaunchKernelGGL(qk_norm_rope_kv_kernel, dim3(3), dim3(256), 0, lemoq_stream(stream), qkv,
-                     (int)heads, (int)head_dim, q_norm_w, k_norm_w, eps, cos_tab, sin_tab, pos,
-                     q_out, kc, ks, vc, vs, code_head_stride, s_len, k_f16, v_f16,
-                     f16_head_stride, k_rot_out);
+  const dim3 grid((unsigned)(3 * heads));
+  hipStream_t st = lemoq_stream(stream);
+#define LEMOQ_QK_CASE(EE)                                                                       \
+  hipLaunchKernelGGL((qk_norm_rope_kv_kernel<EE>), grid, dim3(64), 0, st, qkv, (int)heads,      \
+                     q_norm_w, k_norm_w, eps, cos_tab, sin_tab, pos, q_out, kc, ks, vc, vs,    \
+                     code_head_stride, s_len, k_f16, v_f16, f16_head_stride, k_rot_out);
+  switch (head_dim) {
+    case 64: LEMOQ_QK_CASE(1) break;
+    case 128: LEMOQ_QK_CASE(2) break;
+    default: LEMOQ_QK_CASE(4) break;
+  }
+#undef LEMOQ_QK_CASE
   LEMOQ_CHECK_LAUNCH();
 }

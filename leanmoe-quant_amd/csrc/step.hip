@@ -11,8 +11,8 @@
 //   6 router_fused    post-attention RMSNorm, router GEMV, softmax, top-k
 //   7 moe_gate_up_w8  gate/up + SiLU of the 8 selected experts
 //   8 moe_down_w8     down projection x routing weight + residual add
-// then final RMSNorm + lm_head GEMV, and the on-device greedy argmax that
-// writes the next token and advances *pos / *filled.
+// then final RMSNorm + lm_head GEMV with per-block argmax partials, and the
+// greedy selection that writes the next token and advances *pos / *filled.
 //
 // The layer order and rounding points restate the HF OLMoE decoder layer
 // (transformers OlmoeDecoderLayer/OlmoeModel, called by the reference through
@@ -32,7 +32,7 @@ extern "C" int lemoq_olmoe_decode_step(const LemoqOlmoeStep* p, void* stream) {
   if (!p->embed || !p->final_norm || !p->lm_codes || !p->lm_scale || !p->cos_tab ||
       !p->sin_tab || !p->token || !p->pos || !p->filled || !p->h || !p->xn || !p->qkv ||
       !p->q_rot || !p->attn || !p->part_m || !p->part_l || !p->part_acc || !p->top_w ||
-      !p->top_i || !p->act || !p->logits)
+      !p->top_i || !p->act || !p->logits || !p->router_logits || !p->am_val || !p->am_idx)
     return LEMOQ_ERR_NULL;
   const int64_t H = p->hidden, HD = p->heads * p->head_dim, D = p->head_dim;
   if (H <= 0 || p->heads <= 0 || D <= 0 || p->num_layers <= 0 || p->max_seq <= 0 ||
@@ -71,10 +71,9 @@ extern "C" int lemoq_olmoe_decode_step(const LemoqOlmoeStep* p, void* stream) {
     LEMOQ_TRY(lemoq_moe_down_w8(p->act, w.dn_codes, w.dn_scale, p->top_i, p->top_w, p->top_k,
                                 p->num_experts, H, p->ffn, p->group, p->h, p->h, stream));
   }
-  // Final norm + W8 lm_head, then greedy selection and step advance.
-  LEMOQ_TRY(lemoq_gemv_w8_fused(p->h, nullptr, 0, p->final_norm, p->eps, nullptr, p->lm_codes,
-                                p->lm_scale, p->vocab, H, p->group, nullptr, p->logits, stream));
-  LEMOQ_TRY(lemoq_argmax_advance(p->logits, p->vocab, p->token, p->pos, p->filled, p->prompt,
-                                 p->prompt_len, p->history, p->history_len, stream));
-  return LEMOQ_OK;
+  // Final norm + W8 lm_head with argmax partials, then greedy selection and step advance.
+  return lemoq_lm_head_argmax_w8(p->h, p->final_norm, p->eps, p->lm_codes, p->lm_scale, p->vocab,
+                                 H, p->group, p->logits, p->am_val, p->am_idx, p->am_len,
+                                 p->token, p->pos, p->filled, p->prompt, p->prompt_len,
+                                 p->history, p->history_len, stream);
 }

@@ -19,7 +19,7 @@ LIB_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib")
 LIB_NAME = "liblemoq_hip.so"
 LIB_PATH = os.path.join(LIB_DIR, LIB_NAME)
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -99,6 +99,9 @@ class LemoqOlmoeStep(ctypes.Structure):
         ("top_i", _P),
         ("act", _P),
         ("logits", _P),
+        ("am_val", _P),
+        ("am_idx", _P),
+        ("am_len", _I64),
     ]
 
 
@@ -149,6 +152,11 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "lemoq_argmax_advance": (_I, [_P, _I64, _P, _P, _P, _P, _I64, _P, _I64, _P]),
     "lemoq_olmoe_decode_step": (_I, [ctypes.POINTER(LemoqOlmoeStep), _P]),
     "lemoq_read_probe": (_I, [_P, _I64, _P, _I64, _P]),
+    "lemoq_lm_head_argmax_w8": (
+        _I,
+        [_P, _P, _F, _P, _P, _I64, _I64, _I64, _P, _P, _P, _I64, _P, _P, _P, _P, _I64, _P, _I64, _P],
+    ),
+    "lemoq_lm_head_argmax_parts": (_I64, [_I64]),
 }
 
 

@@ -40,7 +40,7 @@ def _route(x: Any, router_weight: Any, *, top_k: int, norm_topk_prob: bool):
         t_tokens == 1
         and x.dtype == torch.float16
         and router_weight.dtype == torch.float16
-        and hidden % 8 == 0
+        and hidden % 16 == 0
         and hidden <= 8192
         and e <= 1024
         and top_k <= 64
@@ -48,6 +48,10 @@ def _route(x: Any, router_weight: Any, *, top_k: int, norm_topk_prob: bool):
     if fused_ok:
         xc = x.contiguous()
         wc = router_weight.contiguous()
+        if xc.data_ptr() % 16:
+            xc = xc.clone()
+        if wc.data_ptr() % 16:
+            wc = wc.clone()
         logits = torch.empty((1, e), dtype=torch.float16, device=x.device)
         top_w = torch.empty((1, top_k), dtype=torch.float16, device=x.device)
         top_i = torch.empty((1, top_k), dtype=torch.int64, device=x.device)

@@ -250,6 +250,9 @@ class DecodeSession:
         self.top_i = torch.zeros((s.top_k,), dtype=torch.int64, device=dev)
         self.act = torch.zeros((s.top_k, s.ffn), **f16)
         self.logits = torch.zeros((s.vocab,), **f16)
+        n_parts = int(_hip.load().lemoq_lm_head_argmax_parts(s.vocab))
+        self.am_val = torch.zeros((n_parts,), dtype=torch.float32, device=dev)
+        self.am_idx = torch.zeros((n_parts,), dtype=torch.int32, device=dev)
 
         P = _hip.ptr
         self._layer_structs = (_hip.LemoqOlmoeLayer * s.layers)()
@@ -280,8 +283,9 @@ class DecodeSession:
         st.prompt, st.prompt_len = P(self.prompt), self.ctx
         st.history, st.history_len = P(self.history), int(self.history.numel())
         for name in ("h", "xn", "qkv", "q_rot", "attn", "part_m", "part_l", "part_acc",
-                     "router_logits", "top_w", "top_i", "act", "logits"):
+                     "router_logits", "top_w", "top_i", "act", "logits", "am_val", "am_idx"):
             setattr(st, name, P(getattr(self, name)))
+        st.am_len = n_parts
         self._step = st
         self.graph: Any = None
         self.stream: Any = None
