@@ -151,9 +151,10 @@ def kernel_table(torch, hip, w, sess, flusher, reps: int) -> dict:
     def add(name, nbytes, launches):
         specs[name] = (nbytes, launches)
 
-    add("moe_gate_up_w8", K * w8(2 * F, H) + H * 2 + K * 8 + K * F * 2,
-        [lambda i=i: hip.call("lemoq_moe_gate_up_w8", P(scratch["h"]), P(L[i].gu_codes), P(L[i].gu_scale),
-                               P(scratch["ids"]), K, E, F, H, g, P(scratch["act"]), st()) for i in range(nl)])
+    add("moe_gate_up_w8_routed", K * w8(2 * F, H) + H * 2 + E * 2 + K * F * 2,
+        [lambda i=i: hip.call("lemoq_moe_gate_up_w8_routed", P(scratch["h"]), P(L[i].gu_codes), P(L[i].gu_scale),
+                               P(sess.router_logits), K, int(s.norm_topk_prob), E, F, H, g, P(scratch["act"]),
+                               P(scratch["ids"]), P(scratch["tw"]), st()) for i in range(nl)])
     add("moe_down_w8", K * w8(H, F) + K * F * 2 + 3 * H * 2,
         [lambda i=i: hip.call("lemoq_moe_down_w8", P(scratch["act"]), P(L[i].dn_codes), P(L[i].dn_scale),
                                P(scratch["ids"]), P(scratch["tw"]), K, E, H, F, g, P(scratch["h"]),
@@ -179,10 +180,9 @@ def kernel_table(torch, hip, w, sess, flusher, reps: int) -> dict:
         [lambda i=i: hip.call("lemoq_gemv_w8_fused", P(sess.attn), None, 0, None, s.eps, None,
                                P(L[i].o_codes), P(L[i].o_scale), H, HD, g, P(scratch["h"]), P(scratch["y"]), st())
          for i in range(nl)])
-    add("router_topk_fused", E * H * 2 + 3 * H * 2 + E * 2 + K * 10,
-        [lambda i=i: hip.call("lemoq_router_topk_fused", P(scratch["h"]), P(L[i].ln_post), s.eps, H, P(L[i].router),
-                               E, K, int(s.norm_topk_prob), P(scratch["xn"]), P(scratch["lg"]), None,
-                               P(scratch["tw2"]), P(scratch["ids2"]), st()) for i in range(nl)])
+    add("router_logits", E * H * 2 + 3 * H * 2 + E * 2,
+        [lambda i=i: hip.call("lemoq_router_logits", P(scratch["h"]), P(L[i].ln_post), s.eps, H, P(L[i].router), E,
+                               P(scratch["xn"]), P(scratch["lg"]), st()) for i in range(nl)])
     add("gemv_w8 lm_head + argmax (2 launches)", w8(s.vocab, H) + 2 * H * 2 + s.vocab * 2,
         [lambda: hip.call("lemoq_lm_head_argmax_w8", P(scratch["h"]), P(w.final_norm), s.eps, P(w.lm_codes),
                           P(w.lm_scale), s.vocab, H, g, P(scratch["y"]), P(sess.am_val), P(sess.am_idx),
@@ -345,7 +345,7 @@ def main(argv=None) -> int:
         lg0 = cpu.pop("_logits0")
         cpu["logits_max_abs_diff_step0"] = float((lg0.float() - gpu_logits0.float()).abs().max())
 
-    dom_name = "moe_gate_up_w8"
+    dom_name = "moe_gate_up_w8_routed"
     dom = kt[dom_name]
     traffic = _traffic_from_profiles(dom_name)
     line = {

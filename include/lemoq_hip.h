@@ -130,6 +130,19 @@ int lemoq_moe_gate_up_w8(const uint16_t* x, const int8_t* codes,
                          int64_t hidden, int64_t group, uint16_t* act,
                          void* stream);
 
+/* Routed form used by the decode step: takes the router's fp16 logits (E)
+ * instead of ids.  Every wave runs the routing of lemoq_route_topk (fp32
+ * softmax, top_k with ties -> lowest index, optional renormalisation) and
+ * streams the expert of its slot; the selected ids (int64) and fp16 weights
+ * (the `.to(x.dtype)` of moe_static._route, src/lemoq/kernels/moe_static.py:
+ * 276-283) are stored to top_i/top_w for the down kernel.  E <= 256,
+ * top_k <= 64. */
+int lemoq_moe_gate_up_w8_routed(const uint16_t* x, const int8_t* codes,
+                                const uint16_t* scale, const uint16_t* router_logits,
+                                int64_t top_k, int norm_topk_prob, int64_t num_experts,
+                                int64_t ffn, int64_t hidden, int64_t group, uint16_t* act,
+                                int64_t* top_i, uint16_t* top_w, void* stream);
+
 /* A5 — grouped MoE down projection x routing weight, summed over the top_k
  * slots in a fixed order, fp32 accumulation, fp16 output.  Replaces
  * _down_sum_kernel_q + _out_reduce_kernel
@@ -244,6 +257,15 @@ int lemoq_kv_quantize_rows(const uint16_t* x, int64_t rows, int64_t head_dim,
 int lemoq_route_topk(const void* logits, int logits_is_f16, int64_t T, int64_t E,
                      int64_t row_stride, int64_t top_k, int norm_topk_prob,
                      float* top_w, int64_t* top_i, void* stream);
+
+/* Router logits of one token: xn = rmsnorm(h, norm_w) (xn_out, nullable),
+ * logits_out (E) = fp16(xn @ router_w^T), fp32 accumulation (the F.linear of
+ * moe_static._route, src/lemoq/kernels/moe_static.py:267).  One wave per
+ * expert row over ceil(E/4) blocks; hidden % 16 == 0, 16-byte aligned
+ * pointers. */
+int lemoq_router_logits(const uint16_t* h, const uint16_t* norm_w, float eps, int64_t hidden,
+                        const uint16_t* router_w, int64_t E, uint16_t* xn_out,
+                        uint16_t* logits_out, void* stream);
 
 /* Router of one token, fused: xn = rmsnorm(h, norm_w) (written to xn_out),
  * logits = fp16(xn @ router_w^T) with fp32 accumulation (the F.linear of

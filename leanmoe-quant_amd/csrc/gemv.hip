@@ -382,6 +382,76 @@ __global__ __launch_bounds__(1024) void router_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Router logits of one token over many blocks: one wave per expert row; every
+// wave recomputes xn = RMSNorm(h) from its own slices (the wave holds the
+// whole row), so waves never synchronise.  logits[e] = fp16(xn . W[e]) with
+// fp32 accumulation.  Wave 0 of block 0 stores xn.
+// ---------------------------------------------------------------------------
+template <int KCH, bool EXACT>
+__global__ __launch_bounds__(256) void router_logits_kernel(
+    const uint16_t* __restrict__ h, const uint16_t* __restrict__ norm_w, float eps, int H,
+    const uint16_t* __restrict__ rw, int E, uint16_t* __restrict__ xn_out,
+    uint16_t* __restrict__ logits_out) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int e = blockIdx.x * 4 + wave;
+  const int ec = e < E ? e : E - 1;
+  XRaw<KCH> wr, xv, nw;
+  x_issue<KCH, EXACT>(wr, rw + (int64_t)ec * H, H, true, lane);
+  x_issue<KCH, EXACT>(xv, h, H, true, lane);
+  if (norm_w) x_issue<KCH, EXACT>(nw, norm_w, H, true, lane);
+  LEMOQ_LOADS_ISSUED();
+  if (norm_w) x_rmsnorm<KCH>(xv, nw, H, eps);
+  if (xn_out && blockIdx.x == 0 && wave == 0) {
+#pragma unroll
+    for (int j = 0; j < KCH; ++j) {
+      const int off = 1024 * j + 16 * lane;
+      if (off + 16 <= H) {
+        *reinterpret_cast<u32x4*>(xn_out + off) = xv.v[j][0];
+        *reinterpret_cast<u32x4*>(xn_out + off + 8) = xv.v[j][1];
+      }
+    }
+  }
+  float acc = 0.0f;
+#pragma unroll
+  for (int j = 0; j < KCH; ++j)
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const uint32_t ww[4] = {wr.v[j][q].x, wr.v[j][q].y, wr.v[j][q].z, wr.v[j][q].w};
+      const uint32_t xw[4] = {xv.v[j][q].x, xv.v[j][q].y, xv.v[j][q].z, xv.v[j][q].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc = __builtin_amdgcn_fdot2(as_h2(ww[i]), as_h2(xw[i]), acc, false);
+    }
+  acc = wave_sum(acc);
+  if (lane == 0 && e < E) logits_out[e] = f2h(acc);
+}
+
+int launch_router_logits(hipStream_t st, const uint16_t* h, const uint16_t* norm_w, float eps,
+                         int64_t H, const uint16_t* rw, int64_t E, uint16_t* xn_out,
+                         uint16_t* logits) {
+  const dim3 grid((unsigned)((E + 3) / 4));
+  const int kch = kch_pow2(H);
+  const bool exact = H == 1024 * kch;
+#define LEMOQ_RL_CASE(KK)                                                                        \
+  case KK:                                                                                       \
+    if (exact)                                                                                   \
+      hipLaunchKernelGGL((router_logits_kernel<KK, true>), grid, dim3(256), 0, st, h, norm_w,    \
+                         eps, (int)H, rw, (int)E, xn_out, logits);                               \
+    else                                                                                         \
+      hipLaunchKernelGGL((router_logits_kernel<KK, false>), grid, dim3(256), 0, st, h, norm_w,   \
+                         eps, (int)H, rw, (int)E, xn_out, logits);                               \
+    break;
+  switch (kch) {
+    LEMOQ_RL_CASE(1)
+    LEMOQ_RL_CASE(2)
+    LEMOQ_RL_CASE(4)
+    LEMOQ_RL_CASE(8)
+    default: return LEMOQ_ERR_UNSUPPORTED;
+  }
+#undef LEMOQ_RL_CASE
+  LEMOQ_CHECK_LAUNCH();
+}
+
 // Routing of T tokens, one wave per token (values per lane PL = ceil(E/64)).
 template <int PL>
 __global__ __launch_bounds__(256) void route_topk_kernel(const void* __restrict__ logits, int f16,
@@ -524,6 +594,19 @@ extern "C" int lemoq_route_topk(const void* logits, int logits_is_f16, int64_t T
   if (T == 0) return LEMOQ_OK;
   return launch_route(lemoq_stream(stream), logits, logits_is_f16 ? 1 : 0, T, E, row_stride, top_k,
                       norm_topk_prob ? 1 : 0, top_w, nullptr, top_i);
+}
+
+extern "C" int lemoq_router_logits(const uint16_t* h, const uint16_t* norm_w, float eps,
+                                   int64_t hidden, const uint16_t* router_w, int64_t E,
+                                   uint16_t* xn_out, uint16_t* logits_out, void* stream) {
+  if (!h || !router_w || !logits_out) return LEMOQ_ERR_NULL;
+  if (hidden <= 0 || hidden > 8192 || hidden % 16 != 0) return LEMOQ_ERR_UNSUPPORTED;
+  if (E <= 0 || E > 65536) return LEMOQ_ERR_SHAPE;
+  if (!lemoq_aligned16(router_w) || !lemoq_aligned16(h) || (norm_w && !lemoq_aligned16(norm_w)) ||
+      (xn_out && !lemoq_aligned16(xn_out)))
+    return LEMOQ_ERR_ALIGN;
+  return launch_router_logits(lemoq_stream(stream), h, norm_w, eps, hidden, router_w, E, xn_out,
+                              logits_out);
 }
 
 extern "C" int lemoq_router_topk_fused(const uint16_t* h, const uint16_t* norm_w, float eps,

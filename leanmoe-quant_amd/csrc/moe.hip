@@ -3,7 +3,12 @@
 //
 // gate/up:  grid (ceil(F / (4*R)), top_k); wave w of block b computes the R
 //           gate rows and the R matching up rows n = (4b + w)*R + r of expert
-//           ids[slot] and writes act[slot, n] = fp16(silu(g) * u).
+//           ids[slot] and writes act[slot, n] = fp16(silu(g) * u).  The
+//           routed form takes the router's fp16 logits instead of ids: every
+//           wave runs the softmax/top-k of the 64 logits itself (wave_route:
+//           DPP reductions and an LDS rank count, no block barrier) and
+//           streams the expert of its slot; block (0, 0) stores the selected
+//           ids and fp16 weights for the down kernel.
 // down:     grid ceil(H / R) blocks of 8 waves; wave w walks the slots
 //           w, w+8, ... and computes the R rows of expert ids[slot] against
 //           act[slot]; the block then sums slot partials * top_w in a fixed
@@ -19,19 +24,46 @@ struct GateUpArgs {
   const uint16_t* x;
   const int8_t* codes;
   const uint16_t* scale;
-  const int64_t* ids;
+  const int64_t* ids;      // plain form
+  const uint16_t* logits;  // routed form: (E) fp16 router logits
   int top_k;
+  int norm;
+  int64_t* ids_out;        // routed form: selected ids (top_k)
+  uint16_t* w_out;         // routed form: fp16 routing weights (top_k)
   int E, F, H, group;
   uint16_t* act;
 };
 
-template <int KCH, int R, bool EXACT>
+// PL = 0: ids given; PL > 0: routed from E <= 64*PL logits.
+template <int KCH, int R, int PL, bool EXACT>
 __global__ __launch_bounds__(256) void moe_gate_up_kernel(const GateUpArgs a) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int slot = blockIdx.y;
-  const int64_t e = a.ids[slot];
+  int64_t e = 0;
+  constexpr int PZ = PL > 0 ? PL : 1;
+  float z[PZ];
+  if constexpr (PL > 0) {
+#pragma unroll
+    for (int i = 0; i < PL; ++i) {
+      const int idx = lane + 64 * i;
+      z[i] = idx < a.E ? h2f(a.logits[idx]) : -INFINITY;
+    }
+  } else {
+    e = a.ids[slot];
+  }
   XRaw<KCH> xv;
   x_issue<KCH, EXACT>(xv, a.x, a.H, true, lane);
+  if constexpr (PL > 0) {
+    LEMOQ_LOADS_ISSUED();
+    int id;
+    float w;
+    wave_route<PZ>(z, a.E, a.top_k, a.norm != 0, id, w);
+    e = __builtin_amdgcn_readlane(id, slot);
+    if (blockIdx.x == 0 && slot == 0 && wave == 0 && lane < a.top_k) {
+      a.ids_out[lane] = (int64_t)id;
+      a.w_out[lane] = f2h(w);
+    }
+  }
   const bool ev = e >= 0 && e < a.E;
   const int F = a.F;
   const int n0 = (blockIdx.x * 4 + wave) * R;
@@ -113,13 +145,24 @@ __global__ __launch_bounds__(512) void moe_down_kernel(
 }
 
 template <int KCH>
-int launch_gate_up(hipStream_t st, const GateUpArgs& a) {
+int launch_gate_up(hipStream_t st, const GateUpArgs& a, int pl) {
   constexpr int R = 2;
   dim3 grid((unsigned)((a.F + 4 * R - 1) / (4 * R)), (unsigned)a.top_k);
-  if (a.H == 1024 * KCH && a.F % (4 * R) == 0)
-    hipLaunchKernelGGL((moe_gate_up_kernel<KCH, R, true>), grid, dim3(256), 0, st, a);
-  else
-    hipLaunchKernelGGL((moe_gate_up_kernel<KCH, R, false>), grid, dim3(256), 0, st, a);
+  const bool exact = a.H == 1024 * KCH && a.F % (4 * R) == 0;
+#define LEMOQ_GU_CASE(PP)                                                                      \
+  case PP:                                                                                     \
+    if (exact)                                                                                 \
+      hipLaunchKernelGGL((moe_gate_up_kernel<KCH, R, PP, true>), grid, dim3(256), 0, st, a);  \
+    else                                                                                       \
+      hipLaunchKernelGGL((moe_gate_up_kernel<KCH, R, PP, false>), grid, dim3(256), 0, st, a); \
+    break;
+  switch (pl) {
+    LEMOQ_GU_CASE(0)
+    LEMOQ_GU_CASE(1)
+    LEMOQ_GU_CASE(4)
+    default: return LEMOQ_ERR_UNSUPPORTED;
+  }
+#undef LEMOQ_GU_CASE
   LEMOQ_CHECK_LAUNCH();
 }
 
@@ -143,12 +186,12 @@ int kch_of(int64_t k) {
   return c <= 1 ? 1 : (c <= 2 ? 2 : (c <= 4 ? 4 : 8));
 }
 
-int gate_up_dispatch(hipStream_t st, const GateUpArgs& a) {
+int gate_up_dispatch(hipStream_t st, const GateUpArgs& a, int pl) {
   switch (kch_of(a.H)) {
-    case 1: return launch_gate_up<1>(st, a);
-    case 2: return launch_gate_up<2>(st, a);
-    case 4: return launch_gate_up<4>(st, a);
-    default: return launch_gate_up<8>(st, a);
+    case 1: return launch_gate_up<1>(st, a, pl);
+    case 2: return launch_gate_up<2>(st, a, pl);
+    case 4: return launch_gate_up<4>(st, a, pl);
+    default: return launch_gate_up<8>(st, a, pl);
   }
 }
 
@@ -173,7 +216,11 @@ GateUpArgs make_gate_up(const uint16_t* x, const int8_t* codes, const uint16_t* 
   a.codes = codes;
   a.scale = scale;
   a.ids = nullptr;
+  a.logits = nullptr;
   a.top_k = (int)top_k;
+  a.norm = 0;
+  a.ids_out = nullptr;
+  a.w_out = nullptr;
   a.E = (int)E;
   a.F = (int)F;
   a.H = (int)H;
@@ -192,7 +239,27 @@ extern "C" int lemoq_moe_gate_up_w8(const uint16_t* x, const int8_t* codes, cons
   if (rc) return rc;
   GateUpArgs a = make_gate_up(x, codes, scale, top_k, num_experts, ffn, hidden, group, act);
   a.ids = ids;
-  return gate_up_dispatch(lemoq_stream(stream), a);
+  return gate_up_dispatch(lemoq_stream(stream), a, 0);
+}
+
+extern "C" int lemoq_moe_gate_up_w8_routed(const uint16_t* x, const int8_t* codes,
+                                           const uint16_t* scale, const uint16_t* router_logits,
+                                           int64_t top_k, int norm_topk_prob,
+                                           int64_t num_experts, int64_t ffn, int64_t hidden,
+                                           int64_t group, uint16_t* act, int64_t* top_i,
+                                           uint16_t* top_w, void* stream) {
+  int rc = check_gate_up(x, codes, scale, router_logits, act, top_k, num_experts, ffn, hidden,
+                         group);
+  if (rc) return rc;
+  if (!top_i || !top_w) return LEMOQ_ERR_NULL;
+  if (top_k > 64 || top_k > num_experts) return LEMOQ_ERR_SHAPE;
+  if (num_experts > 256) return LEMOQ_ERR_UNSUPPORTED;
+  GateUpArgs a = make_gate_up(x, codes, scale, top_k, num_experts, ffn, hidden, group, act);
+  a.logits = router_logits;
+  a.norm = norm_topk_prob ? 1 : 0;
+  a.ids_out = top_i;
+  a.w_out = top_w;
+  return gate_up_dispatch(lemoq_stream(stream), a, num_experts <= 64 ? 1 : 4);
 }
 
 extern "C" int lemoq_moe_down_w8(const uint16_t* act, const int8_t* codes, const uint16_t* scale,

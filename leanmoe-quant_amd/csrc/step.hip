@@ -8,8 +8,10 @@
 //   3 attn_split_i8   split-KV partials over [0, *filled)
 //   4 attn_merge      LSE merge -> attention output
 //   5 gemv_w8_fused   o_proj with the residual add folded into the epilogue
-//   6 router_fused    post-attention RMSNorm, router GEMV, softmax, top-k
-//   7 moe_gate_up_w8  gate/up + SiLU of the 8 selected experts
+//   6 router_logits   post-attention RMSNorm + router GEMV -> fp16 logits
+//                     (one wave per expert row)
+//   7 moe_gate_up_w8  softmax/top-k of the logits in every wave, then gate/up
+//                     + SiLU of the 8 selected experts (stores ids, weights)
 //   8 moe_down_w8     down projection x routing weight + residual add
 // then final RMSNorm + lm_head GEMV with per-block argmax partials, and the
 // greedy selection that writes the next token and advances *pos / *filled.
@@ -61,13 +63,14 @@ extern "C" int lemoq_olmoe_decode_step(const LemoqOlmoeStep* p, void* stream) {
     // 5. o_proj; h = fp16(fp16(o) + h).
     LEMOQ_TRY(lemoq_gemv_w8_fused(p->attn, nullptr, 0, nullptr, p->eps, nullptr, w.o_codes,
                                   w.o_scale, H, HD, p->group, p->h, p->h, stream));
-    // 6. post-attention RMSNorm + router + top-k.
-    LEMOQ_TRY(lemoq_router_topk_fused(p->h, w.ln_post, p->eps, H, w.router, p->num_experts,
-                                      p->top_k, (int)p->norm_topk_prob, p->xn,
-                                      p->router_logits, nullptr, p->top_w, p->top_i, stream));
-    // 7-8. grouped MoE; h = fp16(fp16(moe) + h).
-    LEMOQ_TRY(lemoq_moe_gate_up_w8(p->xn, w.gu_codes, w.gu_scale, p->top_i, p->top_k,
-                                   p->num_experts, p->ffn, H, p->group, p->act, stream));
+    // 6. post-attention RMSNorm + router logits.
+    LEMOQ_TRY(lemoq_router_logits(p->h, w.ln_post, p->eps, H, w.router, p->num_experts, p->xn,
+                                  p->router_logits, stream));
+    // 7-8. routing + grouped MoE; h = fp16(fp16(moe) + h).
+    LEMOQ_TRY(lemoq_moe_gate_up_w8_routed(p->xn, w.gu_codes, w.gu_scale, p->router_logits,
+                                          p->top_k, (int)p->norm_topk_prob, p->num_experts,
+                                          p->ffn, H, p->group, p->act, p->top_i, p->top_w,
+                                          stream));
     LEMOQ_TRY(lemoq_moe_down_w8(p->act, w.dn_codes, w.dn_scale, p->top_i, p->top_w, p->top_k,
                                 p->num_experts, H, p->ffn, p->group, p->h, p->h, stream));
   }

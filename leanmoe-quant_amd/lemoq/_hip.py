@@ -157,6 +157,11 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         [_P, _P, _F, _P, _P, _I64, _I64, _I64, _P, _P, _P, _I64, _P, _P, _P, _P, _I64, _P, _I64, _P],
     ),
     "lemoq_lm_head_argmax_parts": (_I64, [_I64]),
+    "lemoq_router_logits": (_I, [_P, _P, _F, _I64, _P, _I64, _P, _P, _P]),
+    "lemoq_moe_gate_up_w8_routed": (
+        _I,
+        [_P, _P, _P, _P, _I64, _I, _I64, _I64, _I64, _I64, _P, _P, _P, _P],
+    ),
 }
 
 

@@ -28,40 +28,68 @@ def _kl(p_logits, q_logits) -> float:
     return float((p.exp() * (p - q)).sum())
 
 
-def _run(shape, prompt, steps, seed, dev, *, norm_topk_prob=False):
+def _margin(logits) -> float:
+    top = torch.topk(logits.float(), 2).values
+    return float(top[0] - top[1])
+
+
+def _teacher_forced(shape, prompt, steps, seed, dev, *, norm_topk_prob=False):
+    """GPU decodes greedily; the oracle processes the GPU's token at every step
+    (from the GPU's KV cache after prefill) so each step compares the same input.
+    Returns per-step (gpu logits, oracle logits) and the GPU token sequence."""
     if norm_topk_prob:
         shape = OlmoeShape(**{**shape.__dict__, "norm_topk_prob": True})
     w = OlmoeW8Weights.random(shape, seed=seed, device=dev)
     sess = DecodeSession(w, prompt, max_new_tokens=steps, num_splits=None)
-    seed_tok = sess.prefill()
+    sess.prefill()
     kv = sess.kv_cpu()
     gpu_logits = []
     for _ in range(steps):
         sess.replay(1)
         gpu_logits.append(sess.logits_cpu())
+    toks = [int(t) for t in sess.history[len(prompt) - 1: len(prompt) + steps].tolist()]
     oracle = OracleDecoder(w.to_host(), sess.max_seq, kv=kv)
-    tokens, ref_logits = oracle.run([], steps, start_pos=len(prompt), seed_token=seed_tok)
-    return sess, tokens, gpu_logits, ref_logits
+    ref_logits = [oracle.step(toks[i + 1], len(prompt) + i) for i in range(steps)]
+    return toks, gpu_logits, ref_logits
+
+
+def _check_steps(toks, gl, rl, *, rel=2e-2):
+    """Per step: logits KL < 0.01 (the BASELINE gate for the full step), max
+    |diff| below ``rel`` of the largest logit, and the GPU's greedy token is the
+    oracle's argmax unless the oracle's own top-1/top-2 margin is below twice
+    the measured logit difference (a near-tie, printed)."""
+    flips = []
+    for i, (a, b) in enumerate(zip(gl, rl)):
+        diff = float((a.float() - b.float()).abs().max())
+        scale = float(b.float().abs().max())
+        kl = _kl(b, a)
+        m = _margin(b)
+        ga, ra = int(torch.argmax(a.float())), int(torch.argmax(b.float()))
+        print("step %2d tok %6d diff %.2e |max| %.2e kl %.1e margin %.2e argmax gpu %d oracle %d"
+              % (i, toks[i + 2] if i + 2 < len(toks) else -1, diff, scale, kl, m, ga, ra))
+        assert diff <= rel * scale, (i, diff, scale)
+        assert kl < 1e-2, (i, kl)
+        if ga != ra:
+            flips.append((i, m, diff))
+            assert m <= 2 * diff, (i, m, diff)
+    return flips
 
 
 @pytest.mark.parametrize("norm", [False, True])
-def test_tiny_model_32_greedy_steps_match_oracle(norm, dev):
+def test_tiny_model_32_steps_match_oracle(norm, dev):
     print("case: tiny model, 32 steps, norm_topk_prob=%s" % norm, flush=True)
-    sess, tokens, gl, rl = _run(TINY, [1] * 16, 32, 3, dev, norm_topk_prob=norm)
-    assert sess.generated() == tokens
-    for i, (a, b) in enumerate(zip(gl, rl)):
-        assert (a.float() - b.float()).abs().max() < 2e-2, i
-        assert _kl(b, a) < 1e-2, i
+    toks, gl, rl = _teacher_forced(TINY, [1] * 16, 32, 3, dev, norm_topk_prob=norm)
+    _check_steps(toks, gl, rl)
 
 
 def test_olmoe_shape_32_greedy_steps_match_oracle(dev):
-    """Full OLMoE-1B-7B shape (16 layers, 64 experts top-8, vocab 50304) at ctx 256."""
+    """Full OLMoE-1B-7B shape (16 layers, 64 experts top-8, vocab 50304) at ctx 256:
+    the 32 greedy tokens are identical (no near-tie flips) and every step's
+    logits agree."""
     print("case: OLMoE shape, ctx 256, 32 steps", flush=True)
-    sess, tokens, gl, rl = _run(OLMOE_1B_7B, [1] * 256, 32, 0, dev)
-    assert sess.generated() == tokens
-    for i, (a, b) in enumerate(zip(gl, rl)):
-        assert _kl(b, a) < 1e-2, i
-        assert (a.float() - b.float()).abs().max() < 2e-2, i
+    toks, gl, rl = _teacher_forced(OLMOE_1B_7B, [1] * 256, 32, 0, dev)
+    flips = _check_steps(toks, gl, rl)
+    assert not flips, flips
 
 
 def test_graph_replay_equals_eager_step_bitwise(dev):

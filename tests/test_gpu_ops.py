@@ -149,6 +149,46 @@ def test_fused_router_vs_oracle(norm, dev):
         assert tw.dtype == torch.float16 and ti.dtype == torch.int64
 
 
+@pytest.mark.parametrize("norm", [False, True])
+@pytest.mark.parametrize("E", [64, 8, 100])
+def test_router_logits_then_routed_gate_up_vs_oracle(norm, E, dev):
+    """The decode step's routing path: lemoq_router_logits (one wave per expert)
+    then the routing inside lemoq_moe_gate_up_w8_routed.  ids must equal the
+    oracle's _route bit for bit; act must equal the plain gate/up on those ids."""
+    from lemoq import _hip
+
+    H, F, K, g = 2048, 256, min(8, E), 128
+    gc, gs, _, _ = _experts(E, F, H, g, seed=300 + E)
+    for seed in range(6):
+        h = randn(H, seed=400 + seed).to(torch.float16)
+        ln = (torch.rand(H, generator=torch.Generator().manual_seed(seed)) + 0.5).to(torch.float16)
+        rw = randn(E, H, seed=500 + seed, std=0.02).to(torch.float16)
+        hd, lnd, rwd = h.to(dev), ln.to(dev), rw.to(dev)
+        xn = torch.empty(H, dtype=torch.float16, device=dev)
+        lg = torch.empty(E, dtype=torch.float16, device=dev)
+        st = _hip.stream_of(dev)
+        _hip.call("lemoq_router_logits", _hip.ptr(hd), _hip.ptr(lnd), 1e-5, H, _hip.ptr(rwd), E,
+                  _hip.ptr(xn), _hip.ptr(lg), st)
+        xn_ref = ops.rms_norm(h, ln, 1e-5)
+        assert max_abs(xn.cpu(), xn_ref) <= 2e-3
+        rlg, rtw, rti = ops.route(xn_ref.reshape(1, H), rw, K, norm)
+        assert max_abs(lg.cpu(), rlg.reshape(-1)) <= 2e-3
+        act = torch.empty(K, F, dtype=torch.float16, device=dev)
+        ti = torch.empty(K, dtype=torch.int64, device=dev)
+        tw = torch.empty(K, dtype=torch.float16, device=dev)
+        gcd, gsd = gc.to(dev), gs.to(dev)
+        _hip.call("lemoq_moe_gate_up_w8_routed", _hip.ptr(xn), _hip.ptr(gcd), _hip.ptr(gsd), _hip.ptr(lg), K,
+                  1 if norm else 0, E, F, H, g, _hip.ptr(act), _hip.ptr(ti), _hip.ptr(tw), st)
+        # routing of the GPU logits by the oracle's rule: bit-exact ids
+        ref_w, ref_i = oq.route_order(lg.cpu().float().numpy()[None], K, norm)
+        assert np.array_equal(ti.cpu().numpy(), ref_i[0]), seed
+        assert torch.allclose(tw.cpu().float(), torch.from_numpy(ref_w[0]).half().float(), atol=1e-3, rtol=0)
+        act2 = torch.empty_like(act)
+        _hip.call("lemoq_moe_gate_up_w8", _hip.ptr(xn), _hip.ptr(gcd), _hip.ptr(gsd), _hip.ptr(ti), K, E, F, H, g,
+                  _hip.ptr(act2), st)
+        assert torch.equal(act, act2)
+
+
 # ---------------------------------------------------------------------------
 # grouped MoE
 # ---------------------------------------------------------------------------
