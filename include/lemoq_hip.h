@@ -301,6 +301,22 @@ int lemoq_qk_norm_rope_kv_i8(const uint16_t* qkv, int64_t heads, int64_t head_di
                              int64_t f16_head_stride, uint16_t* k_rot_out,
                              void* stream);
 
+/* A16 fused, one block per head (no reference counterpart as one call: it
+ * joins the q_norm/k_norm, RoPE, KV-INT8 write and int8 attention sequence of
+ * src/lemoq/kernels/attn_decode.py:882-1000 for one decode token).  From the
+ * packed q|k|v row: q and the new k are RMS-normed over heads*D and rotated
+ * at *pos, the new k and v are quantised to KV-INT8 and written to slot *pos
+ * (same arithmetic and bytes as lemoq_qk_norm_rope_kv_i8), and out (heads, D)
+ * fp16 = softmax attention of q over tokens [0, *pos] with the scales folded
+ * in (as lemoq_attn_split_i8 + lemoq_attn_merge).  One launch of `heads`
+ * blocks; the step uses it while s_len <= 8192.  D in {64, 128, 256}. */
+int lemoq_attn_decode_fused_i8(const uint16_t* qkv, int64_t heads, int64_t head_dim,
+                               const uint16_t* q_norm_w, const uint16_t* k_norm_w, float eps,
+                               const uint16_t* cos_tab, const uint16_t* sin_tab,
+                               const int64_t* pos, int8_t* kc, uint16_t* ks, int8_t* vc,
+                               uint16_t* vs, int64_t code_head_stride, int64_t s_len,
+                               float qk_scale, uint16_t* out, void* stream);
+
 /* ---------------------------------------------------------------------------
  * A17 — greedy selection and step advance on the device (replaces the host
  * `logits.argmax().item()` of StaticCacheDecodeSession.replay,

@@ -38,6 +38,9 @@ from lemoq import _hip
 __all__ = ["OlmoeShape", "OLMOE_1B_7B", "OlmoeW8Weights", "LayerW8", "DecodeSession"]
 
 LOG2E = 1.4426950408889634
+# Cache capacity up to which the step runs the one-block-per-head fused
+# attention (kFusedAttnMaxSeq in csrc/step.hip).
+FUSED_ATTN_MAX_SEQ = 0
 
 
 @dataclass(frozen=True)
@@ -328,10 +331,16 @@ class DecodeSession:
         self._enqueue_step()
         return self.logits
 
+    @property
+    def launches_per_step(self) -> int:
+        """Kernel launches in one captured step (see csrc/step.hip)."""
+        per_layer = 6 if self.max_seq <= FUSED_ATTN_MAX_SEQ else 8
+        return per_layer * self.shape.layers + 2
+
     def capture(self) -> dict[str, Any]:
         """Capture one decode step into a hipGraph (state is untouched by the capture)."""
         if self.graph is not None:
-            return {"capture_success": True}
+            return {"capture_success": True, "launches_per_step": self.launches_per_step}
         self.stream = torch.cuda.Stream(device=self.device)
         self.stream.wait_stream(torch.cuda.current_stream(self.device))
         graph = torch.cuda.CUDAGraph()
@@ -339,7 +348,7 @@ class DecodeSession:
             self._enqueue_step()
         torch.cuda.synchronize(self.device)
         self.graph = graph
-        return {"capture_success": True, "launches_per_step": 8 * self.shape.layers + 2}
+        return {"capture_success": True, "launches_per_step": self.launches_per_step}
 
     def replay(self, n: int = 1, *, synchronize: bool = True) -> Any:
         """Replay the captured step ``n`` times back to back; returns the last logits."""

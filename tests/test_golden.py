@@ -1,0 +1,142 @@
+"""Golden fixtures (tests/golden/*.npz, written by tests/golden/make_golden.py).
+
+CPU: the oracle still reproduces every fixture exactly, and the plain-C
+restatement agrees on the bit-exact ones.  GPU (through the C-ABI): RTN codes
+and scales, KV-INT8 bytes and routing ids are bit-exact; the tiny model's
+greedy decode (its top-1/top-2 margins are >= 0.017, far above the fp16
+logit error) gives the same 9 tokens and logits within KL 1e-4.
+"""
+
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import cref
+from oracle import quant as oq
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def _load(name):
+    with np.load(os.path.join(GOLDEN, name + ".npz"), allow_pickle=False) as d:
+        return {k: d[k] for k in d.files}
+
+
+def _make():
+    import importlib.util
+
+    spec = importlib.util.spec_from_file_location("make_golden", os.path.join(GOLDEN, "make_golden.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+# ---------------------------------------------------------------------------
+# CPU
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("name", ["rtn_w8", "kv_int8", "routing"])
+def test_oracle_reproduces_fixture(name):
+    mk = _make()
+    fresh = {"rtn_w8": mk.rtn_fixture, "kv_int8": mk.kv_fixture, "routing": mk.route_fixture}[name]()
+    stored = _load(name)
+    assert sorted(fresh) == sorted(stored)
+    for k in stored:
+        assert np.array_equal(np.asarray(fresh[k]).view(np.uint8), stored[k].view(np.uint8)), (name, k)
+
+
+def test_oracle_reproduces_tiny_decode():
+    mk = _make()
+    fresh = mk.tiny_decode_fixture()
+    stored = _load("tiny_decode")
+    assert np.array_equal(fresh["tokens"], stored["tokens"])
+    assert np.array_equal(fresh["logits"].view(np.uint16), stored["logits"].view(np.uint16))
+
+
+def test_c_restatement_matches_fixtures():
+    cref.build()
+    r = _load("rtn_w8")
+    codes, s32, s16 = cref.rtn_w8(r["w"], 128)
+    assert np.array_equal(codes, r["codes"]) and np.array_equal(s32, r["scale32"])
+    assert np.array_equal(s16.view(np.uint16), r["scale16"].view(np.uint16))
+    k = _load("kv_int8")
+    c, s = cref.kv_quant_rows(k["x"])
+    assert np.array_equal(c, k["codes"]) and np.array_equal(s.view(np.uint16), k["scales"].view(np.uint16))
+    assert k["codes"][5, :8].tolist() == [127, 64, 32, -64, -127, 16, 0, 0]
+    assert k["scales"][3] == 1.0 and (k["codes"][3] == 0).all()
+
+
+# ---------------------------------------------------------------------------
+# GPU
+# ---------------------------------------------------------------------------
+@pytest.mark.gpu
+def test_gpu_rtn_matches_fixture(dev):
+    from lemoq.quant import rtn
+
+    r = _load("rtn_w8")
+    q = rtn.quantize_rtn(torch.from_numpy(r["w"]).to(dev), bits=8, group_size=128)
+    assert np.array_equal(q["codes_padded"].cpu().numpy(), r["codes"])
+    assert np.array_equal(q["scale_f16"].cpu().numpy().view(np.uint16), r["scale16"].view(np.uint16))
+    q2 = rtn.quantize_rtn(torch.from_numpy(r["w_pad"]).to(dev), bits=8, group_size=128)
+    assert np.array_equal(q2["codes_padded"].cpu().numpy(), r["codes_pad"])
+    assert np.array_equal(q2["scale_f16"].cpu().numpy().view(np.uint16), r["scale16_pad"].view(np.uint16))
+
+
+@pytest.mark.gpu
+def test_gpu_kv_int8_matches_fixture(dev):
+    from lemoq import _hip
+
+    k = _load("kv_int8")
+    x = torch.from_numpy(k["x"]).to(dev)
+    codes = torch.empty((16, 128), dtype=torch.int8, device=dev)
+    scales = torch.empty((16,), dtype=torch.float16, device=dev)
+    _hip.call("lemoq_kv_quantize_rows", _hip.ptr(x), 16, 128, _hip.ptr(codes), _hip.ptr(scales), _hip.stream_of(dev))
+    assert np.array_equal(codes.cpu().numpy(), k["codes"])
+    assert np.array_equal(scales.cpu().numpy().view(np.uint16), k["scales"].view(np.uint16))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("norm", [False, True])
+def test_gpu_routing_matches_fixture(norm, dev):
+    from lemoq.kernels.routing import routing_softmax_topk
+
+    r = _load("routing")
+    w, i = routing_softmax_topk(torch.from_numpy(r["logits"]).to(dev), top_k=8, norm_topk_prob=norm)
+    assert np.array_equal(i.cpu().numpy(), r["ids_norm%d" % norm])
+    assert np.allclose(w.cpu().numpy(), r["w_norm%d" % norm], atol=1e-6, rtol=1e-5)
+
+
+@pytest.mark.gpu
+def test_gpu_tiny_decode_matches_fixture(dev):
+    from dataclasses import fields
+
+    from lemoq.model.olmoe import DecodeSession, LayerW8, OlmoeShape, OlmoeW8Weights
+    from oracle.olmoe import random_host_weights
+
+    mk = _make()
+    g = _load("tiny_decode")
+    hw = random_host_weights(mk.TINY, seed=int(g["seed"]))
+    s = mk.TINY
+    shape = OlmoeShape(hidden=s.hidden, heads=s.heads, head_dim=s.head_dim, layers=s.layers,
+                       num_experts=s.num_experts, top_k=s.top_k, ffn=s.ffn, vocab=s.vocab)
+    on = lambda t: t.contiguous().to(dev)  # noqa: E731
+    w = OlmoeW8Weights(shape=shape, embed=on(hw.embed), final_norm=on(hw.final_norm), lm_codes=on(hw.lm_codes),
+                       lm_scale=on(hw.lm_scale),
+                       layers=[LayerW8(**{f.name: on(getattr(L, f.name)) for f in fields(LayerW8)}) for L in hw.layers])
+    prompt = g["prompt"].tolist()
+    steps = len(g["tokens"]) - 1
+    sess = DecodeSession(w, prompt, max_new_tokens=steps, num_splits=4)
+    sess.prefill()
+    logits = []
+    for _ in range(steps):
+        sess.replay(1)
+        logits.append(sess.logits_cpu())
+    assert sess.generated() == g["tokens"].tolist()
+    for a, b in zip(logits, g["logits"]):
+        ref = torch.from_numpy(b).double()
+        p, q = torch.log_softmax(ref, -1), torch.log_softmax(a.double(), -1)
+        assert float((p.exp() * (p - q)).sum()) < 1e-4
+        assert float((a.double() - ref).abs().max()) < 2e-2

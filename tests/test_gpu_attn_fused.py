@@ -1,0 +1,127 @@
+"""GPU parity of the one-block-per-head fused attention (lemoq_attn_decode_fused_i8)
+against the three-launch split path (lemoq_qk_norm_rope_kv_i8 +
+lemoq_attn_split_i8 + lemoq_attn_merge) and against the CPU oracle.
+
+The KV-INT8 bytes it writes must equal the split path's bit for bit (both are
+pinned to the oracle's per-token quantiser); the attention output must match
+within the BASELINE fp16 tolerance (rtol 2e-2 / atol 2e-3).  Cases mirror the
+reference's length boundaries (tests/test_fusion_adversarial.py:72-85,
+tests/test_attn_decode.py:111-149 of LeanMoE-Quant): first token, block edges,
+long caches, a NaN-poisoned tail that must never be read.
+"""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from helpers import assert_close, randn
+from oracle import ops
+from oracle import quant as oq
+
+pytestmark = pytest.mark.gpu
+
+LOG2E = 1.4426950408889634
+
+
+def _state(heads, D, S, filled, seed):
+    HD = heads * D
+    g = torch.Generator().manual_seed(seed)
+    qkv = (torch.randn((3 * HD,), generator=g) * 2).to(torch.float16)
+    qn = (torch.rand((HD,), generator=g) + 0.5).to(torch.float16)
+    kn = (torch.rand((HD,), generator=g) + 0.5).to(torch.float16)
+    k = torch.randn((heads, S, D), generator=g).to(torch.float16)
+    v = torch.randn((heads, S, D), generator=g).to(torch.float16)
+    kc, ks = oq.kv_quantize_rows(k.numpy())
+    vc, vs = oq.kv_quantize_rows(v.numpy())
+    cache = {n: torch.from_numpy(a) for n, a in (("kc", kc), ("ks", ks), ("vc", vc), ("vs", vs))}
+    cos, sin = ops.rotary_cos_sin(torch.arange(S), D, 1e4)
+    return qkv, qn, kn, cache, cos.contiguous(), sin.contiguous()
+
+
+def _to(dev, cache):
+    return {n: t.clone().to(dev) for n, t in cache.items()}
+
+
+def _split_path(hip, dev, qkv, qn, kn, cache, cos, sin, pos, heads, D, S, ns):
+    c = _to(dev, cache)
+    q_rot = torch.empty((heads * D,), dtype=torch.float16, device=dev)
+    posd = torch.tensor([pos], dtype=torch.int64, device=dev)
+    filled = torch.tensor([pos + 1], dtype=torch.int32, device=dev)
+    m = torch.empty((heads * ns,), dtype=torch.float32, device=dev)
+    l = torch.empty_like(m)
+    acc = torch.empty((heads * ns * D,), dtype=torch.float32, device=dev)
+    out = torch.empty((heads * D,), dtype=torch.float16, device=dev)
+    P, st = hip.ptr, hip.stream_of(dev)
+    qkvd, qnd, knd, cosd, sind = (t.to(dev) for t in (qkv, qn, kn, cos, sin))
+    hip.call("lemoq_qk_norm_rope_kv_i8", P(qkvd), heads, D, P(qnd), P(knd), 1e-5, P(cosd), P(sind), P(posd),
+             P(q_rot), P(c["kc"]), P(c["ks"]), P(c["vc"]), P(c["vs"]), S * D, S, None, None, 0, None, st)
+    qk_scale = (1.0 / math.sqrt(D)) * LOG2E
+    hip.call("lemoq_attn_split_i8", P(q_rot), P(c["kc"]), P(c["ks"]), P(c["vc"]), P(c["vs"]), S * D, S,
+             P(filled), heads, D, ns, qk_scale, P(m), P(l), P(acc), st)
+    hip.call("lemoq_attn_merge", P(m), P(l), P(acc), heads, ns, D, P(out), st)
+    return out.cpu(), {n: t.cpu() for n, t in c.items()}, q_rot.cpu()
+
+
+def _fused_path(hip, dev, qkv, qn, kn, cache, cos, sin, pos, heads, D, S):
+    c = _to(dev, cache)
+    posd = torch.tensor([pos], dtype=torch.int64, device=dev)
+    out = torch.full((heads * D,), float("nan"), dtype=torch.float16, device=dev)
+    P, st = hip.ptr, hip.stream_of(dev)
+    qkvd, qnd, knd, cosd, sind = (t.to(dev) for t in (qkv, qn, kn, cos, sin))
+    qk_scale = (1.0 / math.sqrt(D)) * LOG2E
+    hip.call("lemoq_attn_decode_fused_i8", P(qkvd), heads, D, P(qnd), P(knd), 1e-5, P(cosd), P(sind), P(posd),
+             P(c["kc"]), P(c["ks"]), P(c["vc"]), P(c["vs"]), S * D, S, qk_scale, P(out), st)
+    return out.cpu(), {n: t.cpu() for n, t in c.items()}
+
+
+@pytest.mark.parametrize("heads,D,S,pos", [
+    (16, 128, 1100, 0), (16, 128, 1100, 1), (16, 128, 1100, 63), (16, 128, 1100, 64),
+    (16, 128, 1100, 1024), (16, 128, 4200, 4095), (8, 64, 700, 511), (4, 256, 300, 257),
+])
+def test_fused_attention_equals_split_path_and_oracle(heads, D, S, pos, dev):
+    from lemoq import _hip
+
+    print("case: heads=%d D=%d S=%d pos=%d" % (heads, D, S, pos), flush=True)
+    qkv, qn, kn, cache, cos, sin = _state(heads, D, S, pos + 1, seed=pos + D)
+    out_s, cache_s, q_rot = _split_path(_hip, dev, qkv, qn, kn, cache, cos, sin, pos, heads, D, S, ns=16)
+    out_f, cache_f = _fused_path(_hip, dev, qkv, qn, kn, cache, cos, sin, pos, heads, D, S)
+    for n in ("kc", "ks", "vc", "vs"):
+        assert torch.equal(cache_f[n], cache_s[n]), n  # identical KV-INT8 bytes at slot pos, rest untouched
+    assert torch.isfinite(out_f).all()
+    assert_close(out_f, out_s, what="fused vs split")
+    # oracle: q/k norm + RoPE then int8 attention over [0, pos] of the written cache
+    q = ops.rope_fused(ops.rms_norm(qkv[: heads * D], qn, 1e-5).reshape(heads, D), cos[pos], sin[pos])
+    # GPU and CPU sum the squares in different orders: rstd may differ by an ulp
+    assert_close(q_rot, q.reshape(-1), rtol=2e-3, atol=2e-3, what="q_norm+rope")
+    ref = ops.int8_attention_folded(q, cache_s["kc"], cache_s["ks"], cache_s["vc"], cache_s["vs"], pos + 1)
+    assert_close(out_f.reshape(heads, D), ref, what="fused vs oracle")
+    deq = ops.int8_attention_dequant(q, cache_s["kc"], cache_s["ks"], cache_s["vc"], cache_s["vs"], pos + 1)
+    assert (out_f.reshape(heads, D).double() - deq).abs().max() < 2e-3
+
+
+def test_fused_attention_never_reads_beyond_pos(dev):
+    """NaN-poisoned slots after pos (codes cannot be NaN, scales can) never leak in."""
+    from lemoq import _hip
+
+    heads, D, S, pos = 16, 128, 600, 300
+    qkv, qn, kn, cache, cos, sin = _state(heads, D, S, pos + 1, seed=11)
+    clean, _ = _fused_path(_hip, dev, qkv, qn, kn, cache, cos, sin, pos, heads, D, S)
+    poisoned = {n: t.clone() for n, t in cache.items()}
+    poisoned["ks"][:, pos + 1:] = float("nan")
+    poisoned["vs"][:, pos + 1:] = float("nan")
+    out, _ = _fused_path(_hip, dev, qkv, qn, kn, poisoned, cos, sin, pos, heads, D, S)
+    assert torch.isfinite(out).all() and torch.equal(out, clean)
+
+
+def test_fused_attention_position_outside_cache_writes_nothing(dev):
+    from lemoq import _hip
+
+    heads, D, S = 4, 128, 64
+    qkv, qn, kn, cache, cos, sin = _state(heads, D, S, 1, seed=12)
+    out, after = _fused_path(_hip, dev, qkv, qn, kn, cache, cos, sin, S, heads, D, S)
+    for n in ("kc", "ks", "vc", "vs"):
+        assert torch.equal(after[n], cache[n]), n
+    assert (out == 0).all()
