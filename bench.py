@@ -163,12 +163,17 @@ def kernel_table(torch, hip, w, sess, flusher, reps: int) -> dict:
         [lambda i=i: hip.call("lemoq_gemv_w8_fused", P(scratch["h"]), None, 0, P(L[i].ln_in), s.eps, None,
                                P(L[i].qkv_codes), P(L[i].qkv_scale), 3 * HD, H, g, None, P(scratch["y"]), st())
          for i in range(nl)])
-    add("attn_decode_fused_i8 (filled=%d)" % filled,
-        KV_BYTES_PER_TOKEN_LAYER * filled + 3 * HD * 2 + 2 * HD * 2 + 2 * D * 2 + HD * 2,
-        [lambda i=i: hip.call("lemoq_attn_decode_fused_i8", P(sess.qkv), s.heads, D, P(L[i].q_norm),
+    ns = sess.num_splits
+    add("attn_split_fused_i8 (filled=%d)" % filled,
+        KV_BYTES_PER_TOKEN_LAYER * filled + 3 * HD * 2 + 2 * HD * 2 + 2 * D * 2 + s.heads * ns * (D + 2) * 4,
+        [lambda i=i: hip.call("lemoq_attn_split_fused_i8", P(sess.qkv), s.heads, D, P(L[i].q_norm),
                                P(L[i].k_norm), s.eps, P(sess.cos_tab), P(sess.sin_tab), P(sess.pos),
-                               P(kv[i]["kc"]), P(kv[i]["ks"]), P(kv[i]["vc"]), P(kv[i]["vs"]), S * D, S,
-                               qk_scale, P(sess.attn), st()) for i in range(nl)])
+                               P(kv[i]["kc"]), P(kv[i]["ks"]), P(kv[i]["vc"]), P(kv[i]["vs"]), S * D, S, ns,
+                               qk_scale, P(sess.part_m), P(sess.part_l), P(sess.part_acc), st())
+         for i in range(nl)])
+    add("attn_merge", s.heads * ns * (D + 2) * 4 + HD * 2,
+        [lambda: hip.call("lemoq_attn_merge", P(sess.part_m), P(sess.part_l), P(sess.part_acc), s.heads, ns, D,
+                          P(sess.attn), st())] * nl)
     add("gemv_w8 o_proj (+residual)", w8(H, HD) + HD * 2 + 2 * H * 2,
         [lambda i=i: hip.call("lemoq_gemv_w8_fused", P(sess.attn), None, 0, None, s.eps, None,
                                P(L[i].o_codes), P(L[i].o_scale), H, HD, g, P(scratch["h"]), P(scratch["y"]), st())

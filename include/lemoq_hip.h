@@ -301,21 +301,24 @@ int lemoq_qk_norm_rope_kv_i8(const uint16_t* qkv, int64_t heads, int64_t head_di
                              int64_t f16_head_stride, uint16_t* k_rot_out,
                              void* stream);
 
-/* A16 fused, one block per head (no reference counterpart as one call: it
- * joins the q_norm/k_norm, RoPE, KV-INT8 write and int8 attention sequence of
- * src/lemoq/kernels/attn_decode.py:882-1000 for one decode token).  From the
- * packed q|k|v row: q and the new k are RMS-normed over heads*D and rotated
- * at *pos, the new k and v are quantised to KV-INT8 and written to slot *pos
- * (same arithmetic and bytes as lemoq_qk_norm_rope_kv_i8), and out (heads, D)
- * fp16 = softmax attention of q over tokens [0, *pos] with the scales folded
- * in (as lemoq_attn_split_i8 + lemoq_attn_merge).  One launch of `heads`
- * blocks; the step uses it while s_len <= 8192.  D in {64, 128, 256}. */
-int lemoq_attn_decode_fused_i8(const uint16_t* qkv, int64_t heads, int64_t head_dim,
-                               const uint16_t* q_norm_w, const uint16_t* k_norm_w, float eps,
-                               const uint16_t* cos_tab, const uint16_t* sin_tab,
-                               const int64_t* pos, int8_t* kc, uint16_t* ks, int8_t* vc,
-                               uint16_t* vs, int64_t code_head_stride, int64_t s_len,
-                               float qk_scale, uint16_t* out, void* stream);
+/* A16 fused (no reference counterpart as one call: it joins the q_norm/k_norm,
+ * RoPE, KV-INT8 write and split-KV int8 attention sequence of
+ * src/lemoq/kernels/attn_decode.py:882-1000 for one decode token).  Grid
+ * (num_splits, heads): split s of head h covers [s*c, min((s+1)*c, n)) with
+ * n = *pos + 1, c = ceil(n/num_splits).  From the packed q|k|v row, q and the
+ * new k are RMS-normed over heads*D and rotated at *pos; the block holding
+ * *pos quantises the new k and v to KV-INT8 and writes them to slot *pos
+ * (same arithmetic and bytes as lemoq_qk_norm_rope_kv_i8).  Writes the
+ * partials m, l (heads, num_splits) and acc (heads, num_splits, D) of
+ * lemoq_attn_split_i8 over tokens [0, *pos]; merge them with
+ * lemoq_attn_merge.  D in {64, 128, 256}. */
+int lemoq_attn_split_fused_i8(const uint16_t* qkv, int64_t heads, int64_t head_dim,
+                              const uint16_t* q_norm_w, const uint16_t* k_norm_w, float eps,
+                              const uint16_t* cos_tab, const uint16_t* sin_tab,
+                              const int64_t* pos, int8_t* kc, uint16_t* ks, int8_t* vc,
+                              uint16_t* vs, int64_t code_head_stride, int64_t s_len,
+                              int64_t num_splits, float qk_scale, float* m, float* l, float* acc,
+                              void* stream);
 
 /* ---------------------------------------------------------------------------
  * A17 — greedy selection and step advance on the device (replaces the host

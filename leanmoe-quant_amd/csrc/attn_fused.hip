@@ -1,35 +1,32 @@
-// Fused per-layer attention of the decode step over the KV-INT8 cache: one
-// 1024-thread block (16 waves) per head does
-//   q_norm / k_norm (RMSNorm over all heads*D values, HF rounding points),
-//   RoPE at *pos, the KV-INT8 write of the new k/v row to slot *pos, and the
-//   softmax attention of q over tokens [0, *pos] with the per-token scales
-//   folded in (score = ((q.c) * qk_scale) * ks, acc += (p * vs) * c, l += p),
-// and writes the head's fp16 output.  One block per head needs no split merge
-// (a cross-block reduction would need another launch: on MI355X a kernel
-// boundary inside a graph costs ~1.6 us, a grid barrier or "last block"
-// atomic more), so it replaces three launches of the split path
-// (qk_norm_rope_kv_i8, attn_split_i8, attn_merge) while the cache fits the
-// per-CU bandwidth (the step uses it up to 8192 cache slots).
+// Fused per-layer attention of the decode step over the KV-INT8 cache.
 //
-// Waves 0-2 compute the q row, the new k row (quantised: written to the cache
-// and kept in LDS) and the new v row while waves 3-15 already stream their
-// first 64 cached tokens; the first block of cache loads of every wave is
-// issued before *pos is known (addresses clamped to the capacity, validity
-// decided afterwards), so one memory round trip starts everything.  Cached
-// tokens [0, pos) are read from memory; the new token is folded in by wave 0
-// from LDS (the same int8 codes and fp16 scale the cache now holds), never
-// read back from the cache it just wrote.
+// attn_split_fused_i8: grid (num_splits, heads), 8 waves per block.  Block
+// (s, h) covers tokens [s*c, min((s+1)*c, n)) of head h with n = *pos + 1 and
+// c = ceil(n / num_splits) (the reference's split rule,
+// src/lemoq/kernels/attn_decode.py:295-354), and does in one launch what the
+// reference does in four (attn_decode.py:882-1000):
+//   - q_norm over all heads*D values of q (HF rounding points) and RoPE at
+//     *pos for head h (wave 0, every block: the 4 KB row is L2-resident);
+//   - in the one block whose range holds *pos: k_norm + RoPE of the new k and
+//     the KV-INT8 quantisation of the new k and v rows (waves 1 and 2),
+//     written to slot *pos of the cache and kept in LDS;
+//   - the online softmax over its cached tokens with the per-token scales
+//     folded in (score = ((q.c) * qk_scale) * ks, acc += (p * vs) * c,
+//     l += p), the new token folded from LDS (never read back from the slot
+//     just written), and the block's (m, l, acc[D]) partial.
+// The LSE merge of the partials is done by the consumer (lemoq_attn_merge, or
+// the o_proj GEMV prologue of the decode step).  Each wave keeps two blocks
+// of token loads in flight (double buffering).
 //
-// Arithmetic restates the reference's patched attention
-// (src/lemoq/kernels/attn_decode.py:882-1000), _attn_split_kernel_int8
+// Arithmetic restates _attn_split_kernel_int8
 // (src/lemoq/kernels/_attn_triton.py:102-165), the KV write
-// (src/lemoq/kernels/kv_int8.py:196-216) and _rope_one_kernel
-// (src/lemoq/kernels/rope.py:101-123).
+// (src/lemoq/kernels/kv_int8.py:196-216), _rope_one_kernel
+// (src/lemoq/kernels/rope.py:101-123) and the HF q_norm/k_norm RMSNorm.
 #include "common.h"
 
 namespace {
 
-struct AttnHeadArgs {
+struct AttnSplitArgs {
   const uint16_t* qkv;    // (3 * heads * D) fp16: q | k | v
   const uint16_t* qn_w;   // (heads * D) fp16
   const uint16_t* kn_w;   // (heads * D) fp16
@@ -44,8 +41,11 @@ struct AttnHeadArgs {
   int64_t code_head_stride;  // >= s_len * D
   int64_t s_len;
   int heads;
+  int ns;
   float qk_scale;  // softmax scale * log2(e)
-  uint16_t* out;   // (heads * D) fp16
+  float* m_out;    // (heads, ns)
+  float* l_out;    // (heads, ns)
+  float* acc_out;  // (heads, ns, D)
 };
 
 // Sum over aligned groups of G lanes (G in {4, 8, 16}) with DPP row ops.
@@ -62,8 +62,8 @@ template <int D>
 struct HeadShape {
   static constexpr int LPT = D / 16;    // lanes per cached token row (16 codes per lane)
   static constexpr int TPW = 64 / LPT;  // tokens per wave load
-  static constexpr int U = 8;           // wave loads per iteration
-  static constexpr int BLK = TPW * U;   // tokens per wave iteration
+  static constexpr int U = 4;           // wave loads per token block
+  static constexpr int BLK = TPW * U;   // tokens per wave token block
   static constexpr int NW = 8;          // waves per block
   static constexpr int EPL = D / 64;    // prologue elements per lane
   static_assert(LPT == 4 || LPT == 8 || LPT == 16, "head_dim must be 64, 128 or 256");
@@ -75,17 +75,20 @@ struct TokBlock {
   uint16_t ks[HeadShape<D>::U], vs[HeadShape<D>::U];
 };
 
+// Loads of the token block at `base` (token base + u*TPW + tl for slice u);
+// slots at or beyond `lim` are clamped to lim - 1 (a valid slot) and masked
+// when folded.
 template <int D>
 __device__ __forceinline__ void issue_tokens(TokBlock<D>& b, const int8_t* __restrict__ kb,
                                              const int8_t* __restrict__ vb,
                                              const uint16_t* __restrict__ ksh,
                                              const uint16_t* __restrict__ vsh, int64_t base,
-                                             int64_t cap, int tl, int dl) {
+                                             int64_t lim, int tl, int dl) {
   using S = HeadShape<D>;
 #pragma unroll
   for (int u = 0; u < S::U; ++u) {
     int64_t t = base + u * S::TPW + tl;
-    t = t < cap ? t : cap - 1;  // clamped: always a valid slot; validity is decided later
+    t = t < lim ? t : lim - 1;
     b.k[u] = load_stream16(kb + t * D + dl * 16);
     b.v[u] = load_stream16(vb + t * D + dl * 16);
     b.ks[u] = ksh[t];
@@ -98,8 +101,8 @@ struct SoftmaxState {
   float acc[16];
 };
 
-// Online-softmax update with U token slices per lane (token base + u*TPW + tl),
-// valid when below n; wave-uniform running max.
+// Online-softmax update with the token block at `base`; slices at or beyond
+// `n` are masked.  The running max is wave-uniform.
 template <int D>
 __device__ __forceinline__ void fold_tokens(SoftmaxState& st, const TokBlock<D>& b, const XChunk& qx,
                                             int64_t base, int64_t n, int tl, float qk_scale) {
@@ -125,10 +128,10 @@ __device__ __forceinline__ void fold_tokens(SoftmaxState& st, const TokBlock<D>&
   for (int e = 0; e < 16; ++e) st.acc[e] *= alpha;
 #pragma unroll
   for (int u = 0; u < S::U; ++u) {
-    const float p = exp2f(sc[u] - m_new);  // 0 for invalid slices (sc = -inf)
+    const float p = exp2f(sc[u] - m_new);  // 0 for masked slices (sc = -inf)
     st.l += p;
-    // an invalid slice may hold anything (its slot was read speculatively):
-    // select, never multiply, so a NaN scale there cannot reach acc
+    // a masked slice may hold anything (clamped slot): select, never multiply,
+    // so a NaN scale there cannot reach acc
     const float pw = valid[u] ? p * h2f(b.vs[u]) : 0.0f;
     const uint32_t w[4] = {b.v[u].x, b.v[u].y, b.v[u].z, b.v[u].w};
 #pragma unroll
@@ -141,9 +144,10 @@ __device__ __forceinline__ void fold_tokens(SoftmaxState& st, const TokBlock<D>&
 }
 
 template <int D>
-__global__ __launch_bounds__(512) void attn_head_i8_kernel(const AttnHeadArgs a) {
+__global__ __launch_bounds__(512) void attn_split_fused_i8_kernel(const AttnSplitArgs a) {
   using S = HeadShape<D>;
-  constexpr int LPT = S::LPT, TPW = S::TPW, BLK = S::BLK, NW = S::NW, EPL = S::EPL;
+  constexpr int LPT = S::LPT, BLK = S::BLK, NW = S::NW, EPL = S::EPL;
+  constexpr int STRIDE = NW * BLK;
   __shared__ __align__(16) uint16_t q_s[D];
   __shared__ __align__(16) int8_t knew_s[D];
   __shared__ __align__(16) int8_t vnew_s[D];
@@ -151,7 +155,7 @@ __global__ __launch_bounds__(512) void attn_head_i8_kernel(const AttnHeadArgs a)
   __shared__ float wm[NW], wl[NW];
   __shared__ float wacc[NW][D];
 
-  const int h = blockIdx.x;
+  const int sp = blockIdx.x, h = blockIdx.y;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int dl = lane % LPT, tl = lane / LPT;
   const int HD = a.heads * D;
@@ -161,18 +165,22 @@ __global__ __launch_bounds__(512) void attn_head_i8_kernel(const AttnHeadArgs a)
   const uint16_t* ksh = a.ks + (int64_t)h * cap;
   const uint16_t* vsh = a.vs + (int64_t)h * cap;
 
-  // First block of cached tokens: issued before *pos arrives.
-  TokBlock<D> tb;
-  int64_t base = (int64_t)wave * BLK;
-  issue_tokens<D>(tb, kb, vb, ksh, vsh, base, cap, tl, dl);
-
   const int64_t pos = a.pos[0];
   const bool pos_ok = pos >= 0 && pos < cap;
-  const int64_t n_cache = pos_ok ? pos : 0;  // tokens [0, pos) come from the cache
+  const int64_t n_tot = pos_ok ? pos + 1 : 0;  // attention over tokens [0, pos]
+  const int64_t chunk = (n_tot + a.ns - 1) / a.ns;
+  const int64_t start = (int64_t)sp * chunk;
+  const int64_t end = start + chunk < n_tot ? start + chunk : n_tot;
+  const bool owns_new = pos_ok && start <= pos && pos < end;
+  const int64_t cend = owns_new ? pos : end;  // cached tokens [start, cend)
 
-  if (wave < 3) {
-    // Prologue: wave 0 -> q, wave 1 -> new k (normed, rotated, quantised),
-    // wave 2 -> new v (quantised).  Lane holds elements d0 .. d0+EPL-1 of head h.
+  TokBlock<D> ta, tb;
+  int64_t base = start + (int64_t)wave * BLK;
+  if (base < cend) issue_tokens<D>(ta, kb, vb, ksh, vsh, base, cend, tl, dl);
+
+  if (wave == 0 || (owns_new && wave < 3)) {
+    // Prologue: wave 0 -> q (every block), wave 1 -> new k (normed, rotated,
+    // quantised), wave 2 -> new v (quantised).  Lane holds d0 .. d0+EPL-1.
     const int which = wave;
     const uint16_t* src = a.qkv + (int64_t)which * HD;
     const int d0 = lane * EPL;
@@ -220,18 +228,18 @@ __global__ __launch_bounds__(512) void attn_head_i8_kernel(const AttnHeadArgs a)
       const float s = amax > 0.0f ? amax / 127.0f : 1.0f;
       const uint16_t s16 = f2h(s);
       int8_t* lds = which == 1 ? knew_s : vnew_s;
-      int8_t* dst = (which == 1 ? a.kc : a.vc) + (int64_t)h * a.code_head_stride + (pos_ok ? pos : 0) * D;
+      int8_t* dst = (which == 1 ? a.kc : a.vc) + (int64_t)h * a.code_head_stride + pos * D;
 #pragma unroll
       for (int i = 0; i < EPL; ++i) {
         float qv = rintf(o[i] / s);
         qv = fminf(fmaxf(qv, -127.0f), 127.0f);
         const int8_t c = (int8_t)(int)qv;
         lds[d0 + i] = c;
-        if (pos_ok) dst[d0 + i] = c;
+        dst[d0 + i] = c;
       }
       if (lane == 0) {
         kvs_s[which - 1] = h2f(s16);
-        if (pos_ok) (which == 1 ? a.ks : a.vs)[(int64_t)h * cap + pos] = s16;
+        (which == 1 ? a.ks : a.vs)[(int64_t)h * cap + pos] = s16;
       }
     }
   }
@@ -245,23 +253,31 @@ __global__ __launch_bounds__(512) void attn_head_i8_kernel(const AttnHeadArgs a)
 #pragma unroll
   for (int e = 0; e < 16; ++e) st.acc[e] = 0.0f;
 
-  for (bool first = true; base < n_cache; base += NW * BLK, first = false) {
-    if (!first) issue_tokens<D>(tb, kb, vb, ksh, vsh, base, cap, tl, dl);
+  // Two token blocks in flight: fold one while the next one loads.
+  while (base < cend) {
+    int64_t nb = base + STRIDE;
+    if (nb < cend) issue_tokens<D>(tb, kb, vb, ksh, vsh, nb, cend, tl, dl);
     LEMOQ_LOADS_ISSUED();
-    fold_tokens<D>(st, tb, qx, base, n_cache, tl, a.qk_scale);
+    fold_tokens<D>(st, ta, qx, base, cend, tl, a.qk_scale);
+    base = nb;
+    if (base >= cend) break;
+    nb = base + STRIDE;
+    if (nb < cend) issue_tokens<D>(ta, kb, vb, ksh, vsh, nb, cend, tl, dl);
+    LEMOQ_LOADS_ISSUED();
+    fold_tokens<D>(st, tb, qx, base, cend, tl, a.qk_scale);
+    base = nb;
   }
-  if (wave == 0 && pos_ok) {
-    // The new token at slot pos, from LDS: only the lanes of token group 0 are valid.
-    TokBlock<D> nb;
+  if (wave == 0 && owns_new) {
+    // The new token at slot pos, from LDS: only slice (u = 0, tl = 0) is valid.
+    TokBlock<D> nbk;
 #pragma unroll
     for (int u = 0; u < S::U; ++u) {
-      nb.k[u] = *reinterpret_cast<const u32x4*>(knew_s + dl * 16);
-      nb.v[u] = *reinterpret_cast<const u32x4*>(vnew_s + dl * 16);
-      nb.ks[u] = f2h(kvs_s[0]);
-      nb.vs[u] = f2h(kvs_s[1]);
+      nbk.k[u] = *reinterpret_cast<const u32x4*>(knew_s + dl * 16);
+      nbk.v[u] = *reinterpret_cast<const u32x4*>(vnew_s + dl * 16);
+      nbk.ks[u] = f2h(kvs_s[0]);
+      nbk.vs[u] = f2h(kvs_s[1]);
     }
-    // token index of slice (u, tl) is u*TPW + tl: only (0, 0) is below 1.
-    fold_tokens<D>(st, nb, qx, 0, 1, tl, a.qk_scale);
+    fold_tokens<D>(st, nbk, qx, 0, 1, tl, a.qk_scale);
   }
 
   // Sum the token groups of the wave (lanes with the same slice dl).
@@ -280,6 +296,7 @@ __global__ __launch_bounds__(512) void attn_head_i8_kernel(const AttnHeadArgs a)
     for (int e = 0; e < 16; ++e) wacc[wave][dl * 16 + e] = st.acc[e];
   }
   __syncthreads();
+  const int64_t pidx = (int64_t)h * a.ns + sp;
   for (int t = threadIdx.x; t < D; t += 64 * NW) {
     float M = -INFINITY;
 #pragma unroll
@@ -293,29 +310,35 @@ __global__ __launch_bounds__(512) void attn_head_i8_kernel(const AttnHeadArgs a)
         den += wl[w] * f;
       }
     }
-    a.out[(int64_t)h * D + t] = f2h(den > 0.0f ? num / den : num);
+    a.acc_out[pidx * D + t] = num;
+    if (t == 0) {
+      a.m_out[pidx] = M;  // -inf for an empty split (l = 0, acc = 0)
+      a.l_out[pidx] = den;
+    }
   }
 }
 
 }  // namespace
 
-extern "C" int lemoq_attn_decode_fused_i8(const uint16_t* qkv, int64_t heads, int64_t head_dim,
-                                          const uint16_t* q_norm_w, const uint16_t* k_norm_w,
-                                          float eps, const uint16_t* cos_tab,
-                                          const uint16_t* sin_tab, const int64_t* pos,
-                                          int8_t* kc, uint16_t* ks, int8_t* vc, uint16_t* vs,
-                                          int64_t code_head_stride, int64_t s_len, float qk_scale,
-                                          uint16_t* out, void* stream) {
+extern "C" int lemoq_attn_split_fused_i8(const uint16_t* qkv, int64_t heads, int64_t head_dim,
+                                         const uint16_t* q_norm_w, const uint16_t* k_norm_w,
+                                         float eps, const uint16_t* cos_tab,
+                                         const uint16_t* sin_tab, const int64_t* pos, int8_t* kc,
+                                         uint16_t* ks, int8_t* vc, uint16_t* vs,
+                                         int64_t code_head_stride, int64_t s_len,
+                                         int64_t num_splits, float qk_scale, float* m, float* l,
+                                         float* acc, void* stream) {
   if (!qkv || !q_norm_w || !k_norm_w || !cos_tab || !sin_tab || !pos || !kc || !ks || !vc || !vs ||
-      !out)
+      !m || !l || !acc)
     return LEMOQ_ERR_NULL;
   if (head_dim != 64 && head_dim != 128 && head_dim != 256) return LEMOQ_ERR_UNSUPPORTED;
   if (heads <= 0 || heads > 65535 || heads * head_dim > 65536) return LEMOQ_ERR_SHAPE;
+  if (num_splits <= 0 || num_splits > 65535) return LEMOQ_ERR_SHAPE;
   if (s_len <= 0 || code_head_stride < s_len * head_dim) return LEMOQ_ERR_SHAPE;
   if (!lemoq_aligned16(qkv) || !lemoq_aligned16(kc) || !lemoq_aligned16(vc) ||
       code_head_stride % 16 != 0)
     return LEMOQ_ERR_ALIGN;
-  AttnHeadArgs a;
+  AttnSplitArgs a;
   a.qkv = qkv;
   a.qn_w = q_norm_w;
   a.kn_w = k_norm_w;
@@ -330,13 +353,18 @@ extern "C" int lemoq_attn_decode_fused_i8(const uint16_t* qkv, int64_t heads, in
   a.code_head_stride = code_head_stride;
   a.s_len = s_len;
   a.heads = (int)heads;
+  a.ns = (int)num_splits;
   a.qk_scale = qk_scale;
-  a.out = out;
+  a.m_out = m;
+  a.l_out = l;
+  a.acc_out = acc;
   hipStream_t st = lemoq_stream(stream);
+  const dim3 grid((unsigned)num_splits, (unsigned)heads);
+  const dim3 block(64 * HeadShape<128>::NW);
   switch (head_dim) {
-    case 64: hipLaunchKernelGGL((attn_head_i8_kernel<64>), dim3((unsigned)heads), dim3(64 * HeadShape<64>::NW), 0, st, a); break;
-    case 128: hipLaunchKernelGGL((attn_head_i8_kernel<128>), dim3((unsigned)heads), dim3(64 * HeadShape<64>::NW), 0, st, a); break;
-    default: hipLaunchKernelGGL((attn_head_i8_kernel<256>), dim3((unsigned)heads), dim3(64 * HeadShape<64>::NW), 0, st, a); break;
+    case 64: hipLaunchKernelGGL((attn_split_fused_i8_kernel<64>), grid, block, 0, st, a); break;
+    case 128: hipLaunchKernelGGL((attn_split_fused_i8_kernel<128>), grid, block, 0, st, a); break;
+    default: hipLaunchKernelGGL((attn_split_fused_i8_kernel<256>), grid, block, 0, st, a); break;
   }
   LEMOQ_CHECK_LAUNCH();
 }

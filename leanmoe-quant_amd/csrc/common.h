@@ -84,10 +84,10 @@ __device__ __forceinline__ float group_max(float v) {
 // int8 x fp16 dot product of 16 codes.
 //
 // Four int8 codes c0..c3 packed in a dword become two exact fp16 pairs with
-// three bit operations and one packed fp16 subtract:
+// one xor, two byte permutes and two packed fp16 subtracts:
 //   t = c ^ 0x80808080            -> offset-binary bytes u = c + 128
-//   (t & 0x00FF00FF) | 0x64006400 -> fp16 pair (1024+u0, 1024+u2)
-//   ((t>>8) & 0x00FF00FF) | ...   -> fp16 pair (1024+u1, 1024+u3)
+//   perm(0x64.., t) bytes (u0,0x64,u2,0x64) -> fp16 pair (1024+u0, 1024+u2)
+//   perm(0x64.., t) bytes (u1,0x64,u3,0x64) -> fp16 pair (1024+u1, 1024+u3)
 //   pair - 1152                   -> (c0, c2), (c1, c3)   (exact in fp16)
 // v_dot2_f32_f16 then forms c*x products exactly in fp32 and accumulates in
 // fp32, so the result is the fp32 sum of exact products, as in the
@@ -120,9 +120,11 @@ __device__ __forceinline__ float dot16_i8(const u32x4 c, const XChunk& xc, float
   const f16x2 bias = {(f16)1152.0f, (f16)1152.0f};
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const uint32_t t = cw[i] ^ 0x80808080u;
-    const uint32_t lo = (t & 0x00FF00FFu) | 0x64006400u;
-    const uint32_t hi = ((t >> 8) & 0x00FF00FFu) | 0x64006400u;
+    const uint32_t t = cw[i] ^ 0x80808080u;  // offset-binary bytes u = c + 128
+    // v_perm_b32 byte select over {0x64646464 (bytes 4-7), t (bytes 0-3)}:
+    // lo = bytes (u0, 0x64, u2, 0x64), hi = bytes (u1, 0x64, u3, 0x64)
+    const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, t, 0x04020400u);
+    const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, t, 0x04030401u);
     const f16x2 clo = as_h2(lo) - bias;
     const f16x2 chi = as_h2(hi) - bias;
     acc = __builtin_amdgcn_fdot2(clo, xc.a[i], acc, false);

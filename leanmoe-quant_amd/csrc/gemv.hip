@@ -42,16 +42,15 @@ struct GemvArgs {
 
 constexpr int kArgmaxPlain = 0;
 constexpr int kArgmaxPartials = 1;
-
 template <int KCH, int R, int MODE, bool EXACT>
 __global__ __launch_bounds__(256) void gemv_w8_kernel(const GemvArgs a) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t m = blockIdx.y;
   const int64_t row0 = ((int64_t)blockIdx.x * 4 + wave) * R;
 
+  // Activation loads go first: the load counter retires in order, so the
+  // prologue (RMSNorm) then waits only for them while the weights stream in.
   W8Tile<R, KCH> t;
-  w8_issue<R, KCH, EXACT>(t, a.codes, a.scale, row0, a.N, a.Kp, a.Kp / a.group, a.group, lane);
-
   const uint16_t* xr;
   bool x_ok = true;
   if (a.x_row_index) {
@@ -61,32 +60,89 @@ __global__ __launch_bounds__(256) void gemv_w8_kernel(const GemvArgs a) {
   } else {
     xr = a.x + m * a.x_ld;
   }
-  const bool vec = ((reinterpret_cast<uintptr_t>(xr) & 15u) == 0) && ((a.K & 7) == 0);
   XRaw<KCH> xv;
-  x_issue<KCH, EXACT>(xv, xr, a.K, vec, lane);
-  XRaw<KCH> nw;
-  if (a.norm_w) {
-    const bool nvec = ((reinterpret_cast<uintptr_t>(a.norm_w) & 15u) == 0) && ((a.K & 7) == 0);
-    x_issue<KCH, EXACT>(nw, a.norm_w, a.K, nvec, lane);
-  }
-  LEMOQ_LOADS_ISSUED();
-  if (!x_ok) {
+  // Exact shapes with K >= 2048: the RMSNorm prologue runs once per block
+  // (8 values per thread, LDS), not once per wave, after the weight loads.
+  constexpr bool kBlockNorm = EXACT && KCH >= 2;
+  if (kBlockNorm && a.norm_w) {
+    __shared__ __align__(16) uint16_t xs[KCH * 1024];
+    __shared__ float red[4];
+    constexpr int NV = KCH >= 2 ? KCH / 2 : 1;  // u32x4 (8 values) per thread
+    u32x4 rv[NV], wv[NV];
 #pragma unroll
-    for (int j = 0; j < KCH; ++j) xv.v[j][0] = xv.v[j][1] = (u32x4){0u, 0u, 0u, 0u};
-  }
-
-  if (a.x_copy && blockIdx.x == 0 && wave == 0) {
+    for (int i = 0; i < NV; ++i) {
+      const int off = (i * 256 + threadIdx.x) * 8;
+      rv[i] = *reinterpret_cast<const u32x4*>(xr + off);
+      wv[i] = *reinterpret_cast<const u32x4*>(a.norm_w + off);
+    }
+    w8_issue<R, KCH, EXACT>(t, a.codes, a.scale, row0, a.N, a.Kp, a.Kp / a.group, a.group, lane);
+    LEMOQ_LOADS_ISSUED();
+    float ssq = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      if (!x_ok) rv[i] = (u32x4){0u, 0u, 0u, 0u};
+      const uint32_t q[4] = {rv[i].x, rv[i].y, rv[i].z, rv[i].w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float x0 = h2f((uint16_t)(q[k] & 0xFFFFu)), x1 = h2f((uint16_t)(q[k] >> 16));
+        ssq = fmaf(x0, x0, ssq);
+        ssq = fmaf(x1, x1, ssq);
+      }
+      if (a.x_copy && blockIdx.x == 0)
+        *reinterpret_cast<u32x4*>(a.x_copy + (i * 256 + threadIdx.x) * 8) = rv[i];
+    }
+    ssq = wave_sum(ssq);
+    if (lane == 0) red[wave] = ssq;
+    __syncthreads();
+    const float rstd = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)a.K + a.eps);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const uint32_t q[4] = {rv[i].x, rv[i].y, rv[i].z, rv[i].w};
+      const uint32_t g[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
+      uint32_t o[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint16_t n0 = f2h(h2f((uint16_t)(q[k] & 0xFFFFu)) * rstd);
+        const uint16_t n1 = f2h(h2f((uint16_t)(q[k] >> 16)) * rstd);
+        const uint16_t y0 = f2h(h2f(n0) * h2f((uint16_t)(g[k] & 0xFFFFu)));
+        const uint16_t y1 = f2h(h2f(n1) * h2f((uint16_t)(g[k] >> 16)));
+        o[k] = (uint32_t)y0 | ((uint32_t)y1 << 16);
+      }
+      *reinterpret_cast<u32x4*>(xs + (i * 256 + threadIdx.x) * 8) = (u32x4){o[0], o[1], o[2], o[3]};
+    }
+    __syncthreads();
 #pragma unroll
     for (int j = 0; j < KCH; ++j) {
-      const int off = 1024 * j + 16 * lane;
-      const uint32_t w[8] = {xv.v[j][0].x, xv.v[j][0].y, xv.v[j][0].z, xv.v[j][0].w,
-                             xv.v[j][1].x, xv.v[j][1].y, xv.v[j][1].z, xv.v[j][1].w};
-#pragma unroll
-      for (int i = 0; i < 16; ++i)
-        if (off + i < a.K) a.x_copy[off + i] = (uint16_t)(w[i >> 1] >> (16 * (i & 1)));
+      xv.v[j][0] = *reinterpret_cast<const u32x4*>(xs + 1024 * j + 16 * lane);
+      xv.v[j][1] = *reinterpret_cast<const u32x4*>(xs + 1024 * j + 16 * lane + 8);
     }
+  } else {
+    const bool vec = ((reinterpret_cast<uintptr_t>(xr) & 15u) == 0) && ((a.K & 7) == 0);
+    x_issue<KCH, EXACT>(xv, xr, a.K, vec, lane);
+    XRaw<KCH> nw;
+    if (a.norm_w) {
+      const bool nvec = ((reinterpret_cast<uintptr_t>(a.norm_w) & 15u) == 0) && ((a.K & 7) == 0);
+      x_issue<KCH, EXACT>(nw, a.norm_w, a.K, nvec, lane);
+    }
+    w8_issue<R, KCH, EXACT>(t, a.codes, a.scale, row0, a.N, a.Kp, a.Kp / a.group, a.group, lane);
+    LEMOQ_LOADS_ISSUED();
+    if (!x_ok) {
+#pragma unroll
+      for (int j = 0; j < KCH; ++j) xv.v[j][0] = xv.v[j][1] = (u32x4){0u, 0u, 0u, 0u};
+    }
+    if (a.x_copy && blockIdx.x == 0 && wave == 0) {
+#pragma unroll
+      for (int j = 0; j < KCH; ++j) {
+        const int off = 1024 * j + 16 * lane;
+        const uint32_t w[8] = {xv.v[j][0].x, xv.v[j][0].y, xv.v[j][0].z, xv.v[j][0].w,
+                               xv.v[j][1].x, xv.v[j][1].y, xv.v[j][1].z, xv.v[j][1].w};
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (off + i < a.K) a.x_copy[off + i] = (uint16_t)(w[i >> 1] >> (16 * (i & 1)));
+      }
+    }
+    if (a.norm_w) x_rmsnorm<KCH>(xv, nw, a.K, a.eps);
   }
-  if (a.norm_w) x_rmsnorm<KCH>(xv, nw, a.K, a.eps);
   XChunk xc[KCH];
   x_chunks<KCH>(xv, xc);
 
@@ -170,9 +226,10 @@ int launch_gemv(int R, bool exact, dim3 grid, hipStream_t st, const GemvArgs& a)
   LEMOQ_CHECK_LAUNCH();
 }
 
-// Rows per wave: enough waves to cover the 256 CUs several times over for the
-// small matrices, fewer redundant activation reads for the large ones.
-int rows_per_wave(int64_t N) { return N <= 4096 ? 1 : (N <= 16384 ? 2 : 4); }
+// Rows per wave: 2 (swept on MI355X at the OLMoE shapes with cold weights:
+// R = 1, 2, 4 for the 2048-, 6144- and 50304-row projections; 2 is best or
+// within 2% everywhere).
+int rows_per_wave(int64_t) { return 2; }
 
 int kch_pow2(int64_t Kp) {
   const int64_t kch = (Kp + 1023) / 1024;
@@ -397,9 +454,9 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
   const int e = blockIdx.x * 4 + wave;
   const int ec = e < E ? e : E - 1;
   XRaw<KCH> wr, xv, nw;
-  x_issue<KCH, EXACT>(wr, rw + (int64_t)ec * H, H, true, lane);
   x_issue<KCH, EXACT>(xv, h, H, true, lane);
   if (norm_w) x_issue<KCH, EXACT>(nw, norm_w, H, true, lane);
+  x_issue<KCH, EXACT>(wr, rw + (int64_t)ec * H, H, true, lane);
   LEMOQ_LOADS_ISSUED();
   if (norm_w) x_rmsnorm<KCH>(xv, nw, H, eps);
   if (xn_out && blockIdx.x == 0 && wave == 0) {

@@ -4,11 +4,11 @@
 // gate/up:  grid (ceil(F / (4*R)), top_k); wave w of block b computes the R
 //           gate rows and the R matching up rows n = (4b + w)*R + r of expert
 //           ids[slot] and writes act[slot, n] = fp16(silu(g) * u).  The
-//           routed form takes the router's fp16 logits instead of ids: every
-//           wave runs the softmax/top-k of the 64 logits itself (wave_route:
-//           DPP reductions and an LDS rank count, no block barrier) and
-//           streams the expert of its slot; block (0, 0) stores the selected
-//           ids and fp16 weights for the down kernel.
+//           routed form takes the router's fp16 logits instead of ids: wave 0
+//           of every block runs the softmax/top-k of the logits (wave_route:
+//           DPP reductions and an LDS rank count) and the block streams the
+//           expert of its slot; block (0, 0) stores the selected ids and fp16
+//           weights for the down kernel.
 // down:     grid ceil(H / R) blocks of 8 waves; wave w walks the slots
 //           w, w+8, ... and computes the R rows of expert ids[slot] against
 //           act[slot]; the block then sums slot partials * top_w in a fixed
@@ -54,15 +54,23 @@ __global__ __launch_bounds__(256) void moe_gate_up_kernel(const GateUpArgs a) {
   XRaw<KCH> xv;
   x_issue<KCH, EXACT>(xv, a.x, a.H, true, lane);
   if constexpr (PL > 0) {
-    LEMOQ_LOADS_ISSUED();
-    int id;
-    float w;
-    wave_route<PZ>(z, a.E, a.top_k, a.norm != 0, id, w);
-    e = __builtin_amdgcn_readlane(id, slot);
-    if (blockIdx.x == 0 && slot == 0 && wave == 0 && lane < a.top_k) {
-      a.ids_out[lane] = (int64_t)id;
-      a.w_out[lane] = f2h(w);
+    // Routing once per block: wave 0 ranks the logits, the block reads its id
+    // from LDS (the other waves' x loads are in flight meanwhile).
+    __shared__ int sel_id[64];
+    if (wave == 0) {
+      int id;
+      float w;
+      wave_route<PZ>(z, a.E, a.top_k, a.norm != 0, id, w);
+      if (lane < a.top_k) {
+        sel_id[lane] = id;
+        if (blockIdx.x == 0 && slot == 0) {
+          a.ids_out[lane] = (int64_t)id;
+          a.w_out[lane] = f2h(w);
+        }
+      }
     }
+    __syncthreads();
+    e = sel_id[slot];
   }
   const bool ev = e >= 0 && e < a.E;
   const int F = a.F;

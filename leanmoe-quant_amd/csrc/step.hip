@@ -2,17 +2,17 @@
 // canonical cell (w8a16 attention + experts, W8 lm_head, KV-INT8 cache) on a
 // stream, ready to be captured into a hipGraph by the caller.
 //
-// Per layer (6 launches while max_seq <= kFusedAttnMaxSeq, else 8):
+// Per layer (7 launches):
 //   1 gemv_w8_fused   input RMSNorm (+ embedding gather on layer 0) -> packed q|k|v
-//   2 attn fused      one block per head: q_norm/k_norm, RoPE at *pos, KV-INT8
-//                     write of slot *pos, attention over [0, *pos]
-//     (long caches:   qk_norm_rope_kv, attn_split_i8 over [0, *filled), attn_merge)
-//   5 gemv_w8_fused   o_proj with the residual add folded into the epilogue
-//   6 router_logits   post-attention RMSNorm + router GEMV -> fp16 logits
+//   2 attn_split_fused q_norm/k_norm, RoPE at *pos, KV-INT8 write of slot *pos,
+//                     split-KV partials over [0, *pos]
+//   3 attn_merge      LSE merge of the partials
+//   4 gemv_w8_fused   o_proj, residual add in the epilogue
+//   5 router_logits   post-attention RMSNorm + router GEMV -> fp16 logits
 //                     (one wave per expert row)
-//   7 moe_gate_up_w8  softmax/top-k of the logits in every wave, then gate/up
+//   6 moe_gate_up_w8  softmax/top-k of the logits in every wave, then gate/up
 //                     + SiLU of the 8 selected experts (stores ids, weights)
-//   8 moe_down_w8     down projection x routing weight + residual add
+//   7 moe_down_w8     down projection x routing weight + residual add
 // then final RMSNorm + lm_head GEMV with per-block argmax partials, and the
 // greedy selection that writes the next token and advances *pos / *filled.
 //
@@ -28,10 +28,6 @@
     const int rc__ = (expr);  \
     if (rc__) return rc__;    \
   } while (0)
-
-// One block per head streams the whole cache of its head; past this many
-// slots the split-KV path (more blocks per head, one merge launch) is faster.
-static constexpr int64_t kFusedAttnMaxSeq = 0;
 
 extern "C" int lemoq_olmoe_decode_step(const LemoqOlmoeStep* p, void* stream) {
   if (!p || !p->layers) return LEMOQ_ERR_NULL;
@@ -53,31 +49,21 @@ extern "C" int lemoq_olmoe_decode_step(const LemoqOlmoeStep* p, void* stream) {
     LEMOQ_TRY(lemoq_gemv_w8_fused(first ? p->embed : p->h, first ? p->token : nullptr, p->vocab,
                                   w.ln_in, p->eps, first ? p->h : nullptr, w.qkv_codes,
                                   w.qkv_scale, 3 * HD, H, p->group, nullptr, p->qkv, stream));
-    if (S <= kFusedAttnMaxSeq) {
-      // 2. q/k norm, RoPE, KV-INT8 write at slot *pos, attention: one block per head.
-      LEMOQ_TRY(lemoq_attn_decode_fused_i8(p->qkv, p->heads, D, w.q_norm, w.k_norm, p->eps,
-                                           p->cos_tab, p->sin_tab, p->pos, w.kc, w.ks, w.vc,
-                                           w.vs, S * D, S, p->qk_scale, p->attn, stream));
-    } else {
-      // 2. q/k norm, RoPE, KV-INT8 write at slot *pos.
-      LEMOQ_TRY(lemoq_qk_norm_rope_kv_i8(p->qkv, p->heads, D, w.q_norm, w.k_norm, p->eps,
-                                         p->cos_tab, p->sin_tab, p->pos, p->q_rot, w.kc, w.ks,
-                                         w.vc, w.vs, S * D, S, nullptr, nullptr, 0, nullptr,
-                                         stream));
-      // 3-4. split-KV attention over [0, *filled) and the LSE merge.
-      LEMOQ_TRY(lemoq_attn_split_i8(p->q_rot, w.kc, w.ks, w.vc, w.vs, S * D, S, p->filled,
-                                    p->heads, D, p->num_splits, p->qk_scale, p->part_m,
-                                    p->part_l, p->part_acc, stream));
-      LEMOQ_TRY(lemoq_attn_merge(p->part_m, p->part_l, p->part_acc, p->heads, p->num_splits, D,
-                                 p->attn, stream));
-    }
-    // 5. o_proj; h = fp16(fp16(o) + h).
+    // 2. q/k norm, RoPE, KV-INT8 write at slot *pos, split-KV partials.
+    LEMOQ_TRY(lemoq_attn_split_fused_i8(p->qkv, p->heads, D, w.q_norm, w.k_norm, p->eps,
+                                        p->cos_tab, p->sin_tab, p->pos, w.kc, w.ks, w.vc, w.vs,
+                                        S * D, S, p->num_splits, p->qk_scale, p->part_m,
+                                        p->part_l, p->part_acc, stream));
+    // 3. LSE merge of the partials.
+    LEMOQ_TRY(lemoq_attn_merge(p->part_m, p->part_l, p->part_acc, p->heads, p->num_splits, D,
+                               p->attn, stream));
+    // 4. o_proj; h = fp16(fp16(o) + h).
     LEMOQ_TRY(lemoq_gemv_w8_fused(p->attn, nullptr, 0, nullptr, p->eps, nullptr, w.o_codes,
                                   w.o_scale, H, HD, p->group, p->h, p->h, stream));
-    // 6. post-attention RMSNorm + router logits.
+    // 5. post-attention RMSNorm + router logits.
     LEMOQ_TRY(lemoq_router_logits(p->h, w.ln_post, p->eps, H, w.router, p->num_experts, p->xn,
                                   p->router_logits, stream));
-    // 7-8. routing + grouped MoE; h = fp16(fp16(moe) + h).
+    // 6-7. routing + grouped MoE; h = fp16(fp16(moe) + h).
     LEMOQ_TRY(lemoq_moe_gate_up_w8_routed(p->xn, w.gu_codes, w.gu_scale, p->router_logits,
                                           p->top_k, (int)p->norm_topk_prob, p->num_experts,
                                           p->ffn, H, p->group, p->act, p->top_i, p->top_w,

@@ -158,10 +158,11 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     ),
     "lemoq_lm_head_argmax_parts": (_I64, [_I64]),
     "lemoq_router_logits": (_I, [_P, _P, _F, _I64, _P, _I64, _P, _P, _P]),
-    "lemoq_attn_decode_fused_i8": (
+    "lemoq_attn_split_fused_i8": (
         _I,
-        [_P, _I64, _I64, _P, _P, _F, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _F, _P, _P],
+        [_P, _I64, _I64, _P, _P, _F, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _F, _P, _P, _P, _P],
     ),
+
     "lemoq_moe_gate_up_w8_routed": (
         _I,
         [_P, _P, _P, _P, _I64, _I, _I64, _I64, _I64, _I64, _P, _P, _P, _P],

@@ -38,9 +38,17 @@ from lemoq import _hip
 __all__ = ["OlmoeShape", "OLMOE_1B_7B", "OlmoeW8Weights", "LayerW8", "DecodeSession"]
 
 LOG2E = 1.4426950408889634
-# Cache capacity up to which the step runs the one-block-per-head fused
-# attention (kFusedAttnMaxSeq in csrc/step.hip).
-FUSED_ATTN_MAX_SEQ = 0
+# Split-KV blocks per head of the step's attention: about 512 cache slots per
+# 8-wave block (two token blocks of 256 in flight per wave pass), between 2 and
+# 8 splits.
+STEP_SLOTS_PER_SPLIT = 512
+STEP_MAX_SPLITS = 8
+
+
+def step_num_splits(max_seq: int, heads: int) -> int:
+    ns = -(-int(max_seq) // STEP_SLOTS_PER_SPLIT)
+    ns = max(2, min(STEP_MAX_SPLITS, ns))
+    return max(1, min(ns, 1024 // max(1, int(heads))))
 
 
 @dataclass(frozen=True)
@@ -217,7 +225,8 @@ class DecodeSession:
         self.ctx = int(prompt.numel())
         self.max_new_tokens = int(max_new_tokens)
         self.max_seq = self.ctx + self.max_new_tokens
-        self.num_splits = resolve_num_splits(num_splits, heads=s.heads, device=dev)
+        self.num_splits = (step_num_splits(self.max_seq, s.heads) if num_splits is None
+                           else resolve_num_splits(num_splits, heads=s.heads, device=dev))
         S, D, HD = self.max_seq, s.head_dim, s.heads * s.head_dim
 
         i8 = dict(dtype=torch.int8, device=dev)
@@ -334,8 +343,7 @@ class DecodeSession:
     @property
     def launches_per_step(self) -> int:
         """Kernel launches in one captured step (see csrc/step.hip)."""
-        per_layer = 6 if self.max_seq <= FUSED_ATTN_MAX_SEQ else 8
-        return per_layer * self.shape.layers + 2
+        return 7 * self.shape.layers + 2
 
     def capture(self) -> dict[str, Any]:
         """Capture one decode step into a hipGraph (state is untouched by the capture)."""

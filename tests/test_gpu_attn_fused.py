@@ -1,13 +1,16 @@
-"""GPU parity of the one-block-per-head fused attention (lemoq_attn_decode_fused_i8)
-against the three-launch split path (lemoq_qk_norm_rope_kv_i8 +
-lemoq_attn_split_i8 + lemoq_attn_merge) and against the CPU oracle.
+"""GPU parity of the decode step's fused attention against the unfused operators
+and the CPU oracle:
 
-The KV-INT8 bytes it writes must equal the split path's bit for bit (both are
-pinned to the oracle's per-token quantiser); the attention output must match
+* lemoq_attn_split_fused_i8 (q/k norm + RoPE + KV-INT8 write + split-KV
+  partials in one launch) vs lemoq_qk_norm_rope_kv_i8 + lemoq_attn_split_i8,
+  both merged by lemoq_attn_merge;
+
+The KV-INT8 bytes written must equal the unfused path's bit for bit (both are
+pinned to the oracle's per-token quantiser); attention outputs must match
 within the BASELINE fp16 tolerance (rtol 2e-2 / atol 2e-3).  Cases mirror the
 reference's length boundaries (tests/test_fusion_adversarial.py:72-85,
-tests/test_attn_decode.py:111-149 of LeanMoE-Quant): first token, block edges,
-long caches, a NaN-poisoned tail that must never be read.
+tests/test_attn_decode.py:83-149 of LeanMoE-Quant): first token, block edges,
+several split counts, long caches, a NaN-poisoned tail that must never be read.
 """
 
 from __future__ import annotations
@@ -65,29 +68,41 @@ def _split_path(hip, dev, qkv, qn, kn, cache, cos, sin, pos, heads, D, S, ns):
     return out.cpu(), {n: t.cpu() for n, t in c.items()}, q_rot.cpu()
 
 
-def _fused_path(hip, dev, qkv, qn, kn, cache, cos, sin, pos, heads, D, S):
+def _merge(hip, dev, m, l, acc, heads, ns, D):
+    out = torch.empty((heads * D,), dtype=torch.float16, device=dev)
+    hip.call("lemoq_attn_merge", hip.ptr(m), hip.ptr(l), hip.ptr(acc), heads, ns, D, hip.ptr(out), hip.stream_of(dev))
+    return out
+
+
+def _fused_path(hip, dev, qkv, qn, kn, cache, cos, sin, pos, heads, D, S, ns=4, raw=False):
     c = _to(dev, cache)
     posd = torch.tensor([pos], dtype=torch.int64, device=dev)
-    out = torch.full((heads * D,), float("nan"), dtype=torch.float16, device=dev)
+    m = torch.full((heads * ns,), float("nan"), dtype=torch.float32, device=dev)
+    l = torch.full_like(m, float("nan"))
+    acc = torch.full((heads * ns * D,), float("nan"), dtype=torch.float32, device=dev)
     P, st = hip.ptr, hip.stream_of(dev)
     qkvd, qnd, knd, cosd, sind = (t.to(dev) for t in (qkv, qn, kn, cos, sin))
     qk_scale = (1.0 / math.sqrt(D)) * LOG2E
-    hip.call("lemoq_attn_decode_fused_i8", P(qkvd), heads, D, P(qnd), P(knd), 1e-5, P(cosd), P(sind), P(posd),
-             P(c["kc"]), P(c["ks"]), P(c["vc"]), P(c["vs"]), S * D, S, qk_scale, P(out), st)
+    hip.call("lemoq_attn_split_fused_i8", P(qkvd), heads, D, P(qnd), P(knd), 1e-5, P(cosd), P(sind), P(posd),
+             P(c["kc"]), P(c["ks"]), P(c["vc"]), P(c["vs"]), S * D, S, ns, qk_scale, P(m), P(l), P(acc), st)
+    if raw:
+        return m, l, acc, {n: t.cpu() for n, t in c.items()}
+    out = _merge(hip, dev, m, l, acc, heads, ns, D)
     return out.cpu(), {n: t.cpu() for n, t in c.items()}
 
 
-@pytest.mark.parametrize("heads,D,S,pos", [
-    (16, 128, 1100, 0), (16, 128, 1100, 1), (16, 128, 1100, 63), (16, 128, 1100, 64),
-    (16, 128, 1100, 1024), (16, 128, 4200, 4095), (8, 64, 700, 511), (4, 256, 300, 257),
+@pytest.mark.parametrize("heads,D,S,pos,ns", [
+    (16, 128, 1100, 0, 3), (16, 128, 1100, 1, 3), (16, 128, 1100, 63, 3), (16, 128, 1100, 64, 8),
+    (16, 128, 1100, 1024, 3), (16, 128, 1100, 1024, 1), (16, 128, 4200, 4095, 8), (8, 64, 700, 511, 2),
+    (4, 256, 300, 257, 5), (16, 128, 1100, 5, 8),
 ])
-def test_fused_attention_equals_split_path_and_oracle(heads, D, S, pos, dev):
+def test_fused_attention_equals_split_path_and_oracle(heads, D, S, pos, ns, dev):
     from lemoq import _hip
 
-    print("case: heads=%d D=%d S=%d pos=%d" % (heads, D, S, pos), flush=True)
+    print("case: heads=%d D=%d S=%d pos=%d ns=%d" % (heads, D, S, pos, ns), flush=True)
     qkv, qn, kn, cache, cos, sin = _state(heads, D, S, pos + 1, seed=pos + D)
     out_s, cache_s, q_rot = _split_path(_hip, dev, qkv, qn, kn, cache, cos, sin, pos, heads, D, S, ns=16)
-    out_f, cache_f = _fused_path(_hip, dev, qkv, qn, kn, cache, cos, sin, pos, heads, D, S)
+    out_f, cache_f = _fused_path(_hip, dev, qkv, qn, kn, cache, cos, sin, pos, heads, D, S, ns=ns)
     for n in ("kc", "ks", "vc", "vs"):
         assert torch.equal(cache_f[n], cache_s[n]), n  # identical KV-INT8 bytes at slot pos, rest untouched
     assert torch.isfinite(out_f).all()
@@ -125,3 +140,5 @@ def test_fused_attention_position_outside_cache_writes_nothing(dev):
     for n in ("kc", "ks", "vc", "vs"):
         assert torch.equal(after[n], cache[n]), n
     assert (out == 0).all()
+
+
