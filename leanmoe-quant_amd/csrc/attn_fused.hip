@@ -1,6 +1,6 @@
 // Fused per-layer attention of the decode step over the KV-INT8 cache.
 //
-// attn_split_fused_i8: grid (num_splits, heads), 8 waves per block.  Block
+// attn_split_fused_i8: grid (num_splits, heads), 4 or 8 waves per block.  Block
 // (s, h) covers tokens [s*c, min((s+1)*c, n)) of head h with n = *pos + 1 and
 // c = ceil(n / num_splits) (the reference's split rule,
 // src/lemoq/kernels/attn_decode.py:295-354), and does in one launch what the
@@ -58,33 +58,33 @@ __device__ __forceinline__ float group_sum_dpp(float v) {
   return v;
 }
 
-template <int D>
+template <int D, int NW_ = 8, int U_ = 4>
 struct HeadShape {
   static constexpr int LPT = D / 16;    // lanes per cached token row (16 codes per lane)
   static constexpr int TPW = 64 / LPT;  // tokens per wave load
-  static constexpr int U = 4;           // wave loads per token block
+  static constexpr int U = U_;          // wave loads per token block
   static constexpr int BLK = TPW * U;   // tokens per wave token block
-  static constexpr int NW = 8;          // waves per block
+  static constexpr int NW = NW_;        // waves per block
   static constexpr int EPL = D / 64;    // prologue elements per lane
   static_assert(LPT == 4 || LPT == 8 || LPT == 16, "head_dim must be 64, 128 or 256");
+  static_assert(NW >= 3, "waves 0..2 carry the q and new k/v prologue");
 };
 
-template <int D>
+template <class S>
 struct TokBlock {
-  u32x4 k[HeadShape<D>::U], v[HeadShape<D>::U];
-  uint16_t ks[HeadShape<D>::U], vs[HeadShape<D>::U];
+  u32x4 k[S::U], v[S::U];
+  uint16_t ks[S::U], vs[S::U];
 };
 
 // Loads of the token block at `base` (token base + u*TPW + tl for slice u);
 // slots at or beyond `lim` are clamped to lim - 1 (a valid slot) and masked
 // when folded.
-template <int D>
-__device__ __forceinline__ void issue_tokens(TokBlock<D>& b, const int8_t* __restrict__ kb,
+template <int D, class S>
+__device__ __forceinline__ void issue_tokens(TokBlock<S>& b, const int8_t* __restrict__ kb,
                                              const int8_t* __restrict__ vb,
                                              const uint16_t* __restrict__ ksh,
                                              const uint16_t* __restrict__ vsh, int64_t base,
                                              int64_t lim, int tl, int dl) {
-  using S = HeadShape<D>;
 #pragma unroll
   for (int u = 0; u < S::U; ++u) {
     int64_t t = base + u * S::TPW + tl;
@@ -103,10 +103,9 @@ struct SoftmaxState {
 
 // Online-softmax update with the token block at `base`; slices at or beyond
 // `n` are masked.  The running max is wave-uniform.
-template <int D>
-__device__ __forceinline__ void fold_tokens(SoftmaxState& st, const TokBlock<D>& b, const XChunk& qx,
+template <class S>
+__device__ __forceinline__ void fold_tokens(SoftmaxState& st, const TokBlock<S>& b, const XChunk& qx,
                                             int64_t base, int64_t n, int tl, float qk_scale) {
-  using S = HeadShape<D>;
   float sc[S::U];
   bool valid[S::U];
 #pragma unroll
@@ -143,9 +142,9 @@ __device__ __forceinline__ void fold_tokens(SoftmaxState& st, const TokBlock<D>&
   st.m = m_new;
 }
 
-template <int D>
-__global__ __launch_bounds__(512) void attn_split_fused_i8_kernel(const AttnSplitArgs a) {
-  using S = HeadShape<D>;
+template <int D, int NW_ = 8, int U_ = 4>
+__global__ __launch_bounds__(64 * NW_) void attn_split_fused_i8_kernel(const AttnSplitArgs a) {
+  using S = HeadShape<D, NW_, U_>;
   constexpr int LPT = S::LPT, BLK = S::BLK, NW = S::NW, EPL = S::EPL;
   constexpr int STRIDE = NW * BLK;
   __shared__ __align__(16) uint16_t q_s[D];
@@ -174,9 +173,9 @@ __global__ __launch_bounds__(512) void attn_split_fused_i8_kernel(const AttnSpli
   const bool owns_new = pos_ok && start <= pos && pos < end;
   const int64_t cend = owns_new ? pos : end;  // cached tokens [start, cend)
 
-  TokBlock<D> ta, tb;
+  TokBlock<S> ta, tb;
   int64_t base = start + (int64_t)wave * BLK;
-  if (base < cend) issue_tokens<D>(ta, kb, vb, ksh, vsh, base, cend, tl, dl);
+  if (base < cend) issue_tokens<D, S>(ta, kb, vb, ksh, vsh, base, cend, tl, dl);
 
   if (wave == 0 || (owns_new && wave < 3)) {
     // Prologue: wave 0 -> q (every block), wave 1 -> new k (normed, rotated,
@@ -256,20 +255,20 @@ __global__ __launch_bounds__(512) void attn_split_fused_i8_kernel(const AttnSpli
   // Two token blocks in flight: fold one while the next one loads.
   while (base < cend) {
     int64_t nb = base + STRIDE;
-    if (nb < cend) issue_tokens<D>(tb, kb, vb, ksh, vsh, nb, cend, tl, dl);
+    if (nb < cend) issue_tokens<D, S>(tb, kb, vb, ksh, vsh, nb, cend, tl, dl);
     LEMOQ_LOADS_ISSUED();
-    fold_tokens<D>(st, ta, qx, base, cend, tl, a.qk_scale);
+    fold_tokens<S>(st, ta, qx, base, cend, tl, a.qk_scale);
     base = nb;
     if (base >= cend) break;
     nb = base + STRIDE;
-    if (nb < cend) issue_tokens<D>(ta, kb, vb, ksh, vsh, nb, cend, tl, dl);
+    if (nb < cend) issue_tokens<D, S>(ta, kb, vb, ksh, vsh, nb, cend, tl, dl);
     LEMOQ_LOADS_ISSUED();
-    fold_tokens<D>(st, tb, qx, base, cend, tl, a.qk_scale);
+    fold_tokens<S>(st, tb, qx, base, cend, tl, a.qk_scale);
     base = nb;
   }
   if (wave == 0 && owns_new) {
     // The new token at slot pos, from LDS: only slice (u = 0, tl = 0) is valid.
-    TokBlock<D> nbk;
+    TokBlock<S> nbk;
 #pragma unroll
     for (int u = 0; u < S::U; ++u) {
       nbk.k[u] = *reinterpret_cast<const u32x4*>(knew_s + dl * 16);
@@ -277,7 +276,7 @@ __global__ __launch_bounds__(512) void attn_split_fused_i8_kernel(const AttnSpli
       nbk.ks[u] = f2h(kvs_s[0]);
       nbk.vs[u] = f2h(kvs_s[1]);
     }
-    fold_tokens<D>(st, nbk, qx, 0, 1, tl, a.qk_scale);
+    fold_tokens<S>(st, nbk, qx, 0, 1, tl, a.qk_scale);
   }
 
   // Sum the token groups of the wave (lanes with the same slice dl).
@@ -360,11 +359,25 @@ extern "C" int lemoq_attn_split_fused_i8(const uint16_t* qkv, int64_t heads, int
   a.acc_out = acc;
   hipStream_t st = lemoq_stream(stream);
   const dim3 grid((unsigned)num_splits, (unsigned)heads);
-  const dim3 block(64 * HeadShape<128>::NW);
-  switch (head_dim) {
-    case 64: hipLaunchKernelGGL((attn_split_fused_i8_kernel<64>), grid, block, 0, st, a); break;
-    case 128: hipLaunchKernelGGL((attn_split_fused_i8_kernel<128>), grid, block, 0, st, a); break;
-    default: hipLaunchKernelGGL((attn_split_fused_i8_kernel<256>), grid, block, 0, st, a); break;
+  // Short splits (at most 128 slots per block over the cache's capacity) run
+  // 4 waves per block, so two blocks share a CU and their prologues overlap;
+  // longer splits run 8 waves, whose double-buffered token blocks keep more
+  // loads in flight per block.
+  const bool short_split = (s_len + num_splits - 1) / num_splits <= 128;
+  if (short_split) {
+    const dim3 block(64 * 4);
+    switch (head_dim) {
+      case 64: hipLaunchKernelGGL((attn_split_fused_i8_kernel<64, 4>), grid, block, 0, st, a); break;
+      case 128: hipLaunchKernelGGL((attn_split_fused_i8_kernel<128, 4>), grid, block, 0, st, a); break;
+      default: hipLaunchKernelGGL((attn_split_fused_i8_kernel<256, 4>), grid, block, 0, st, a); break;
+    }
+  } else {
+    const dim3 block(64 * 8);
+    switch (head_dim) {
+      case 64: hipLaunchKernelGGL((attn_split_fused_i8_kernel<64, 8>), grid, block, 0, st, a); break;
+      case 128: hipLaunchKernelGGL((attn_split_fused_i8_kernel<128, 8>), grid, block, 0, st, a); break;
+      default: hipLaunchKernelGGL((attn_split_fused_i8_kernel<256, 8>), grid, block, 0, st, a); break;
+    }
   }
   LEMOQ_CHECK_LAUNCH();
 }

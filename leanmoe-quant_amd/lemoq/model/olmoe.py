@@ -38,17 +38,20 @@ from lemoq import _hip
 __all__ = ["OlmoeShape", "OLMOE_1B_7B", "OlmoeW8Weights", "LayerW8", "DecodeSession"]
 
 LOG2E = 1.4426950408889634
-# Split-KV blocks per head of the step's attention: about 512 cache slots per
-# 8-wave block (two token blocks of 256 in flight per wave pass), between 2 and
-# 8 splits.
-STEP_SLOTS_PER_SPLIT = 512
-STEP_MAX_SPLITS = 8
+# Split-KV blocks per head of the step's attention: one block per 64 cache
+# slots, at least 2, and at most one wave of blocks over the chip
+# (heads * splits <= compute units; 16 splits per head for OLMoE's 16 heads on
+# a 256-CU MI355X).  A grid larger than one block per CU runs a second round
+# of blocks, which costs more than the longer splits save; the LSE merge grows
+# with the split count (2.5 us at 8 splits, 2.9 at 16, 3.6 at 32).
+STEP_SLOTS_PER_SPLIT = 64
+STEP_MAX_SPLITS = 64
 
 
-def step_num_splits(max_seq: int, heads: int) -> int:
+def step_num_splits(max_seq: int, heads: int, compute_units: int = 256) -> int:
     ns = -(-int(max_seq) // STEP_SLOTS_PER_SPLIT)
-    ns = max(2, min(STEP_MAX_SPLITS, ns))
-    return max(1, min(ns, 1024 // max(1, int(heads))))
+    cap = max(1, min(STEP_MAX_SPLITS, int(compute_units) // max(1, int(heads))))
+    return max(1, min(max(2, ns), cap))
 
 
 @dataclass(frozen=True)
@@ -225,7 +228,8 @@ class DecodeSession:
         self.ctx = int(prompt.numel())
         self.max_new_tokens = int(max_new_tokens)
         self.max_seq = self.ctx + self.max_new_tokens
-        self.num_splits = (step_num_splits(self.max_seq, s.heads) if num_splits is None
+        cus = torch.cuda.get_device_properties(dev).multi_processor_count
+        self.num_splits = (step_num_splits(self.max_seq, s.heads, cus) if num_splits is None
                            else resolve_num_splits(num_splits, heads=s.heads, device=dev))
         S, D, HD = self.max_seq, s.head_dim, s.heads * s.head_dim
 

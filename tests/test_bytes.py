@@ -62,3 +62,17 @@ def test_step_bytes_and_attainment():
         attainment(1.0, 0.0, 1.0)
     with pytest.raises(ValueError):
         kv_read_bytes(OLMOE_1B_7B, 10, kv="fp8")
+
+
+def test_step_split_rule():
+    """One split per 64 cache slots, at least 2, and heads * splits within one
+    block per compute unit (a second round of blocks costs more than it saves)."""
+    from lemoq.model.olmoe import step_num_splits
+
+    assert step_num_splits(1061, 16, 256) == 16 and step_num_splits(4133, 16, 256) == 16
+    assert step_num_splits(20, 2, 256) == 2 and step_num_splits(300, 2, 256) == 5
+    assert step_num_splits(100000, 4, 256) == 64 and step_num_splits(5000, 16, 128) == 8
+    for S in (1, 63, 64, 65, 1000, 5000):
+        for heads in (1, 2, 16, 64, 300):
+            ns = step_num_splits(S, heads, 256)
+            assert ns >= 1 and (heads * ns <= 256 or ns == 1)
