@@ -15,8 +15,13 @@ HBM roofline fraction, per-kernel cold timings, the dominant kernel's roofline
 (``roofline``) and the CPU oracle's ms/token on this host (``cpu_baseline``).
 Progress goes to stderr.
 
-``--mode kernels`` runs only the weights + isolated kernel timings (short; the
-form used under ``rocprofv3 --pmc``).
+``--mode kernels`` runs only the weights + isolated kernel timings.
+``--mode traffic`` is the short form profiled under ``rocprofv3 --pmc``: a
+copy of known size (the counter calibration), then the isolated kernels over
+a synthetic KV cache at ``--ctx`` (no prefill); it prints the dispatch plan.
+``--summarize-pmc FETCH_CSV WRITE_CSV PLAN_JSON`` (CPU only) turns the two
+counter passes into per-kernel HBM bytes per launch: profiles/traffic.json,
+which fills ``roofline.traffic``, and a markdown table beside it.
 """
 
 from __future__ import annotations
@@ -60,7 +65,9 @@ def parse_args(argv=None):
     ap.add_argument("--cpu-budget-s", type=float, default=20.0)
     ap.add_argument("--cpu-check-steps", type=int, default=32)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--mode", choices=("full", "kernels"), default="full")
+    ap.add_argument("--mode", choices=("full", "kernels", "traffic"), default="full")
+    ap.add_argument("--summarize-pmc", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "PLAN_JSON"))
+    ap.add_argument("--profiles-dir", default=os.path.join(REPO, "profiles"))
     return ap.parse_args(argv)
 
 
@@ -148,21 +155,24 @@ def kernel_table(torch, hip, w, sess, flusher, reps: int) -> dict:
     qk_scale = (1.0 / math.sqrt(D)) * 1.4426950408889634
     specs = {}
 
-    def add(name, nbytes, launches):
-        specs[name] = (nbytes, launches)
+    def add(name, nbytes, launches, kernels):
+        specs[name] = (nbytes, launches, kernels)
 
     add("moe_gate_up_w8_routed", K * w8(2 * F, H) + H * 2 + E * 2 + K * F * 2,
         [lambda i=i: hip.call("lemoq_moe_gate_up_w8_routed", P(scratch["h"]), P(L[i].gu_codes), P(L[i].gu_scale),
                                P(sess.router_logits), K, int(s.norm_topk_prob), E, F, H, g, P(scratch["act"]),
-                               P(scratch["ids"]), P(scratch["tw"]), st()) for i in range(nl)])
+                               P(scratch["ids"]), P(scratch["tw"]), st()) for i in range(nl)],
+        ["moe_gate_up_kernel"])
     add("moe_down_w8", K * w8(H, F) + K * F * 2 + 3 * H * 2,
         [lambda i=i: hip.call("lemoq_moe_down_w8", P(scratch["act"]), P(L[i].dn_codes), P(L[i].dn_scale),
                                P(scratch["ids"]), P(scratch["tw"]), K, E, H, F, g, P(scratch["h"]),
-                               P(scratch["y"]), st()) for i in range(nl)])
+                               P(scratch["y"]), st()) for i in range(nl)],
+        ["moe_down_kernel"])
     add("gemv_w8 qkv (+input RMSNorm)", w8(3 * HD, H) + 2 * H * 2 + 3 * HD * 2,
         [lambda i=i: hip.call("lemoq_gemv_w8_fused", P(scratch["h"]), None, 0, P(L[i].ln_in), s.eps, None,
                                P(L[i].qkv_codes), P(L[i].qkv_scale), 3 * HD, H, g, None, P(scratch["y"]), st())
-         for i in range(nl)])
+         for i in range(nl)],
+        ["gemv_w8_kernel"])
     ns = sess.num_splits
     add("attn_split_fused_i8 (filled=%d)" % filled,
         KV_BYTES_PER_TOKEN_LAYER * filled + 3 * HD * 2 + 2 * HD * 2 + 2 * D * 2 + s.heads * ns * (D + 2) * 4,
@@ -170,26 +180,32 @@ def kernel_table(torch, hip, w, sess, flusher, reps: int) -> dict:
                                P(L[i].k_norm), s.eps, P(sess.cos_tab), P(sess.sin_tab), P(sess.pos),
                                P(kv[i]["kc"]), P(kv[i]["ks"]), P(kv[i]["vc"]), P(kv[i]["vs"]), S * D, S, ns,
                                qk_scale, P(sess.part_m), P(sess.part_l), P(sess.part_acc), st())
-         for i in range(nl)])
+         for i in range(nl)],
+        ["attn_split_fused_i8_kernel"])
     add("attn_merge", s.heads * ns * (D + 2) * 4 + HD * 2,
         [lambda: hip.call("lemoq_attn_merge", P(sess.part_m), P(sess.part_l), P(sess.part_acc), s.heads, ns, D,
-                          P(sess.attn), st())] * nl)
+                          P(sess.attn), st())] * nl,
+        ["attn_merge_kernel"])
     add("gemv_w8 o_proj (+residual)", w8(H, HD) + HD * 2 + 2 * H * 2,
         [lambda i=i: hip.call("lemoq_gemv_w8_fused", P(sess.attn), None, 0, None, s.eps, None,
                                P(L[i].o_codes), P(L[i].o_scale), H, HD, g, P(scratch["h"]), P(scratch["y"]), st())
-         for i in range(nl)])
+         for i in range(nl)],
+        ["gemv_w8_kernel"])
     add("router_logits", E * H * 2 + 3 * H * 2 + E * 2,
         [lambda i=i: hip.call("lemoq_router_logits", P(scratch["h"]), P(L[i].ln_post), s.eps, H, P(L[i].router), E,
-                               P(scratch["xn"]), P(scratch["lg"]), st()) for i in range(nl)])
+                               P(scratch["xn"]), P(scratch["lg"]), st()) for i in range(nl)],
+        ["router_logits_kernel"])
     add("gemv_w8 lm_head + argmax (2 launches)", w8(s.vocab, H) + 2 * H * 2 + s.vocab * 2,
         [lambda: hip.call("lemoq_lm_head_argmax_w8", P(scratch["h"]), P(w.final_norm), s.eps, P(w.lm_codes),
                           P(w.lm_scale), s.vocab, H, g, P(scratch["y"]), P(sess.am_val), P(sess.am_idx),
                           int(sess.am_val.numel()), P(scratch["tok"]), P(scratch["pos"]), P(scratch["fill"]),
-                          None, 0, None, 0, st())])
+                          None, 0, None, 0, st())],
+        ["gemv_w8_kernel", "argmax_advance_kernel"])
     out = {}
-    for name, (nbytes, launches) in specs.items():
+    for name, (nbytes, launches, kernels) in specs.items():
         r = time_cold(torch, flusher, launches, reps)
         r["bytes"] = int(nbytes)
+        r["dispatch_kernels"] = kernels
         r["gbs"] = nbytes / (r["avg_us"] * 1e-6) / 1e9
         r["frac_of_peak"] = r["gbs"] / HBM_PEAK_GBS
         out[name] = r
@@ -285,8 +301,116 @@ def cpu_baseline(torch, w, cap, gpu_tokens, gpu_logits, budget_s: float, max_ste
     }
 
 
+# ---------------------------------------------------------------------------
+# HBM traffic from two rocprofv3 --pmc passes
+# ---------------------------------------------------------------------------
+COPY_BYTES = 512 << 20  # calibration copy: larger than the 256 MB Infinity Cache
+
+
+def synthetic_cache(torch, sess, filled: int, seed: int = 7) -> None:
+    """Random KV-INT8 contents (codes in [-127, 127], scales in [0.01, 0.02)) and
+    the decode position at ``filled`` - 1, in place of a prefill: the isolated
+    kernels' bytes and times depend on the filled length, not on the values."""
+    g = torch.Generator(device=sess.device).manual_seed(seed)
+    for kv in sess.kv:
+        for n in ("kc", "vc"):
+            kv[n].random_(-127, 128, generator=g)
+        for n in ("ks", "vs"):
+            kv[n].uniform_(0.01, 0.02, generator=g)
+    sess.set_position(filled - 1, token=1)
+    torch.cuda.synchronize()
+
+
+def copy_calibration(torch, hip, flusher, reps: int = 2) -> dict:
+    """``reps`` cold copies of COPY_BYTES with lemoq_copy_probe (each byte read once and
+    written once): the profiler's FETCH_SIZE / WRITE_SIZE of these dispatches
+    calibrate the same counters on the step's kernels."""
+    dst = torch.empty((COPY_BYTES,), dtype=torch.uint8, device=flusher.buf.device)
+    for _ in range(reps):
+        flusher.flush()
+        hip.call("lemoq_copy_probe", hip.ptr(flusher.buf), hip.ptr(dst), COPY_BYTES, 4096, hip.stream_of())
+    torch.cuda.synchronize()
+    return {"copy_bytes": COPY_BYTES, "copies": reps, "flush_bytes": flusher.nbytes}
+
+
+def _pmc_rows(path: str, counter: str) -> list:
+    """(dispatch id, kernel name, value) of one counter from a rocprofv3 counter_collection csv, in dispatch order."""
+    import csv
+
+    rows = []
+    with open(path, newline="") as f:
+        for r in csv.DictReader(f):
+            if r.get("Counter_Name") != counter:
+                continue
+            rows.append((int(r["Dispatch_Id"]), r["Kernel_Name"], float(r["Counter_Value"])))
+    rows.sort()
+    return rows
+
+
+def summarize_pmc(fetch_csv: str, write_csv: str, plan_json: str, out_dir: str) -> dict:
+    """Per-kernel HBM bytes per launch from a FETCH_SIZE pass and a WRITE_SIZE pass
+    (KiB per dispatch) of ``bench.py --mode traffic``.  Each counter is scaled
+    by bytes / counter of the calibration copy (read COPY_BYTES, wrote
+    COPY_BYTES).  The traffic-mode dispatches of the plan's kernels are matched
+    to its kernel table in order (cache flushes and torch's own copies and
+    fills in between are skipped), and every matched kernel name is checked
+    against the plan."""
+    with open(plan_json) as f:
+        plan = json.loads(f.read().strip().splitlines()[-1])
+    passes = {}
+    for counter, path in (("FETCH_SIZE", fetch_csv), ("WRITE_SIZE", write_csv)):
+        rows = _pmc_rows(path, counter)
+        copies = [v for _, n, v in rows if "copy_probe_kernel" in n]
+        flushes = [v for _, n, v in rows if "read_probe_kernel" in n]
+        if len(copies) < 1:
+            raise SystemExit("%s: no copy_probe_kernel dispatch in %s" % (counter, path))
+        kib = sum(copies) / len(copies)
+        factor = plan["calibration"]["copy_bytes"] / (kib * 1024.0)
+        first_copy = next(i for i, (_, n, _) in enumerate(rows) if "copy_probe_kernel" in n)
+        known = {kn for k in plan["kernels"].values() for kn in k["dispatch_kernels"]}
+        seq = [(n, v) for _, n, v in rows[first_copy:] if any(kn in n for kn in known)]
+        per = {}
+        i = 0
+        for name, k in plan["kernels"].items():
+            calls = k["launches"]
+            vals = []
+            for _ in range(calls):
+                tot = 0.0
+                for kn in k["dispatch_kernels"]:
+                    if i >= len(seq) or kn not in seq[i][0]:
+                        got = seq[i][0] if i < len(seq) else "end of trace"
+                        raise SystemExit("%s: dispatch %d is %r, the plan expects %s" % (counter, i, got, kn))
+                    tot += seq[i][1]
+                    i += 1
+                vals.append(tot)
+            per[name] = sum(vals) / len(vals) * 1024.0 * factor
+        passes[counter] = {"factor": factor, "copy_kib": kib,
+                           "flush_kib": sum(flushes) / len(flushes) if flushes else None, "per": per}
+    out = {"calibration": {
+        "copy_bytes": plan["calibration"]["copy_bytes"],
+        "fetch_factor": passes["FETCH_SIZE"]["factor"], "write_factor": passes["WRITE_SIZE"]["factor"],
+        "copy_fetch_kib": passes["FETCH_SIZE"]["copy_kib"], "copy_write_kib": passes["WRITE_SIZE"]["copy_kib"],
+        "flush_fetch_kib": passes["FETCH_SIZE"]["flush_kib"], "flush_bytes": plan["calibration"]["flush_bytes"],
+    }, "ctx": plan["ctx"]}
+    lines = ["| kernel | algorithmic B/launch | HBM read B | HBM write B | traffic / algorithmic |", "|---|---|---|---|---|"]
+    for name, k in plan["kernels"].items():
+        rd, wr = passes["FETCH_SIZE"]["per"][name], passes["WRITE_SIZE"]["per"][name]
+        out[name] = {"traffic_bytes": int(round(rd + wr)), "read_bytes": int(round(rd)), "write_bytes": int(round(wr)),
+                     "algorithmic_bytes": k["bytes"], "launches": k["launches"]}
+        lines.append("| %s | %d | %d | %d | %.3f |" % (name, k["bytes"], rd, wr, (rd + wr) / k["bytes"]))
+    os.makedirs(out_dir, exist_ok=True)
+    with open(os.path.join(out_dir, "traffic.json"), "w") as f:
+        json.dump(out, f, indent=1, sort_keys=True)
+        f.write("\n")
+    return {"table": "\n".join(lines), "data": out}
+
+
 def main(argv=None) -> int:
     args = parse_args(argv)
+    if args.summarize_pmc:
+        r = summarize_pmc(*args.summarize_pmc, out_dir=args.profiles_dir)
+        print(r["table"])
+        return 0
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (the batch-1 decode "
@@ -311,6 +435,16 @@ def main(argv=None) -> int:
     flusher = Flusher(torch, _hip, dev)
     read_bw = flusher.read_bandwidth_gbs()
     log("measured read bandwidth %.1f GB/s" % read_bw)
+
+    if args.mode == "traffic":
+        from lemoq.model.olmoe import DecodeSession
+
+        sess = DecodeSession(w, [1] * args.ctx, max_new_tokens=2)
+        synthetic_cache(torch, sess, sess.ctx + 1)
+        cal = copy_calibration(torch, _hip, flusher)
+        kt = kernel_table(torch, _hip, w, sess, flusher, args.kernel_reps)
+        print(json.dumps({"mode": "traffic", "ctx": args.ctx, "calibration": cal, "kernels": kt}))
+        return 0
 
     if args.mode == "kernels":
         from lemoq.model.olmoe import DecodeSession
@@ -390,7 +524,8 @@ def main(argv=None) -> int:
             "bytes_per_launch": dom["bytes"],
             "avg_us": dom["avg_us"],
         },
-        "kernels": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()} for k, v in kt.items()},
+        "kernels": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()
+                        if kk != "dispatch_kernels"} for k, v in kt.items()},
     }
     if r2 is not None:
         line["ctx2"] = r2

@@ -413,6 +413,15 @@ int lemoq_olmoe_decode_step(const LemoqOlmoeStep* step, void* stream);
 int lemoq_read_probe(const void* src, int64_t n_bytes, uint32_t* out, int64_t blocks,
                      void* stream);
 
+/* Measurement: copy n_bytes (multiple of 16, both pointers 16-byte aligned,
+ * no overlap) from src to dst with 16-byte loads and stores over `blocks`
+ * 256-thread blocks.  A kernel of known traffic (n_bytes read, n_bytes
+ * written) that calibrates the profiler's FETCH_SIZE and WRITE_SIZE counters
+ * before they are read as HBM bytes of the step's kernels.  No counterpart in
+ * the reference (its profiling reads wall time only).
+ * ------------------------------------------------------------------------- */
+int lemoq_copy_probe(const void* src, void* dst, int64_t n_bytes, int64_t blocks, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

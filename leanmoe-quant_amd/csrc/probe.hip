@@ -35,6 +35,15 @@ __global__ __launch_bounds__(256) void read_probe_kernel(const u32x4* __restrict
   if (threadIdx.x == 0) out[blockIdx.x] = red[0] ^ red[1] ^ red[2] ^ red[3];
 }
 
+// Plain copy with 16-byte loads and stores: each byte is read once and
+// written once, so its profiler counters calibrate FETCH_SIZE / WRITE_SIZE.
+__global__ __launch_bounds__(256) void copy_probe_kernel(const u32x4* __restrict__ src,
+                                                         u32x4* __restrict__ dst, int64_t n16) {
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += stride)
+    dst[i] = __builtin_nontemporal_load(src + i);
+}
+
 }  // namespace
 
 extern "C" int lemoq_read_probe(const void* src, int64_t n_bytes, uint32_t* out, int64_t blocks,
@@ -44,5 +53,18 @@ extern "C" int lemoq_read_probe(const void* src, int64_t n_bytes, uint32_t* out,
   if (!lemoq_aligned16(src)) return LEMOQ_ERR_ALIGN;
   hipLaunchKernelGGL(read_probe_kernel, dim3((unsigned)blocks), dim3(256), 0, lemoq_stream(stream),
                      reinterpret_cast<const u32x4*>(src), n_bytes / 16, out);
+  LEMOQ_CHECK_LAUNCH();
+}
+
+extern "C" int lemoq_copy_probe(const void* src, void* dst, int64_t n_bytes, int64_t blocks,
+                                void* stream) {
+  if (!src || !dst) return LEMOQ_ERR_NULL;
+  if (n_bytes <= 0 || n_bytes % 16 != 0 || blocks <= 0 || blocks > 65536) return LEMOQ_ERR_SHAPE;
+  if (!lemoq_aligned16(src) || !lemoq_aligned16(dst)) return LEMOQ_ERR_ALIGN;
+  const char* s = static_cast<const char*>(src);
+  const char* d = static_cast<const char*>(dst);
+  if (s < d + n_bytes && d < s + n_bytes) return LEMOQ_ERR_SHAPE;
+  hipLaunchKernelGGL(copy_probe_kernel, dim3((unsigned)blocks), dim3(256), 0, lemoq_stream(stream),
+                     reinterpret_cast<const u32x4*>(src), reinterpret_cast<u32x4*>(dst), n_bytes / 16);
   LEMOQ_CHECK_LAUNCH();
 }

@@ -152,6 +152,7 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "lemoq_argmax_advance": (_I, [_P, _I64, _P, _P, _P, _P, _I64, _P, _I64, _P]),
     "lemoq_olmoe_decode_step": (_I, [ctypes.POINTER(LemoqOlmoeStep), _P]),
     "lemoq_read_probe": (_I, [_P, _I64, _P, _I64, _P]),
+    "lemoq_copy_probe": (_I, [_P, _P, _I64, _I64, _P]),
     "lemoq_lm_head_argmax_w8": (
         _I,
         [_P, _P, _F, _P, _P, _I64, _I64, _I64, _P, _P, _P, _I64, _P, _P, _P, _P, _I64, _P, _I64, _P],

@@ -1,0 +1,76 @@
+"""bench.py's counter summary (CPU): two synthetic rocprofv3 counter_collection
+files with known per-dispatch KiB must give back the bytes they were built
+from, scaled by the calibration copy, and a dispatch order that does not follow
+the plan must be rejected."""
+
+from __future__ import annotations
+
+import csv
+import json
+
+import pytest
+
+import bench
+
+COLS = ["Correlation_Id", "Dispatch_Id", "Agent_Id", "Queue_Id", "Process_Id", "Thread_Id", "Grid_Size",
+        "Kernel_Id", "Kernel_Name", "Workgroup_Size", "LDS_Block_Size", "Scratch_Size", "VGPR_Count",
+        "Accum_VGPR_Count", "SGPR_Count", "Counter_Name", "Counter_Value", "Start_Timestamp", "End_Timestamp"]
+
+PLAN = {
+    "mode": "traffic", "ctx": 64,
+    "calibration": {"copy_bytes": 1 << 20, "copies": 2, "flush_bytes": 4 << 20},
+    "kernels": {
+        "a": {"bytes": 1000, "launches": 2, "dispatch_kernels": ["moe_gate_up_kernel"]},
+        "b": {"bytes": 500, "launches": 2, "dispatch_kernels": ["gemv_w8_kernel", "argmax_advance_kernel"]},
+    },
+}
+
+
+def _write(path, counter, seq):
+    with open(path, "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=COLS)
+        w.writeheader()
+        for i, (name, kib) in enumerate(seq):
+            row = {c: 0 for c in COLS}
+            row.update({"Dispatch_Id": i + 1, "Kernel_Name": "void (anonymous namespace)::%s<1>(Args)" % name,
+                        "Counter_Name": counter, "Counter_Value": kib})
+            w.writerow(row)
+
+
+def _seq(copy_kib, a_kib, b_kib, c_kib):
+    seq = [("rtn_w8_kernel", 99.0), ("read_probe_kernel", 4096.0), ("copy_probe_kernel", copy_kib),
+           ("read_probe_kernel", 4096.0), ("copy_probe_kernel", copy_kib), ("__amd_rocclr_copyBuffer", 7.0)]
+    for _ in range(2):  # one flush, then the launches of one pass
+        seq.append(("read_probe_kernel", 4096.0))
+        seq.append(("moe_gate_up_kernel", a_kib))
+    for _ in range(2):
+        seq.append(("read_probe_kernel", 4096.0))
+        seq += [("gemv_w8_kernel", b_kib), ("argmax_advance_kernel", c_kib)]
+    return seq
+
+
+def test_summary_recovers_calibrated_bytes(tmp_path):
+    # fetch counter reads 2x the true bytes (factor 0.5), write counter 1x
+    _write(tmp_path / "f.csv", "FETCH_SIZE", _seq(2048.0, 8.0, 4.0, 1.0))
+    _write(tmp_path / "w.csv", "WRITE_SIZE", _seq(1024.0, 1.0, 0.5, 0.25))
+    (tmp_path / "plan.json").write_text("progress line\n" + json.dumps(PLAN) + "\n")
+    r = bench.summarize_pmc(str(tmp_path / "f.csv"), str(tmp_path / "w.csv"), str(tmp_path / "plan.json"),
+                            str(tmp_path / "out"))
+    d = json.loads((tmp_path / "out" / "traffic.json").read_text())
+    assert d["calibration"]["fetch_factor"] == pytest.approx(0.5)
+    assert d["calibration"]["write_factor"] == pytest.approx(1.0)
+    assert d["a"]["read_bytes"] == 4096 and d["a"]["write_bytes"] == 1024 and d["a"]["traffic_bytes"] == 5120
+    assert d["b"]["read_bytes"] == 2560 and d["b"]["write_bytes"] == 768
+    assert d["b"]["algorithmic_bytes"] == 500 and "| b | 500 |" in r["table"]
+
+
+def test_summary_rejects_dispatches_out_of_plan(tmp_path):
+    seq = _seq(1024.0, 1.0, 1.0, 1.0)
+    seq[7] = ("gemv_w8_kernel", 1.0)  # the plan expects moe_gate_up_kernel there
+    seq.insert(3, ("__amd_rocclr_copyBuffer", 5.0))  # not a plan kernel: skipped
+    _write(tmp_path / "f.csv", "FETCH_SIZE", seq)
+    _write(tmp_path / "w.csv", "WRITE_SIZE", _seq(1024.0, 1.0, 1.0, 1.0))
+    (tmp_path / "plan.json").write_text(json.dumps(PLAN))
+    with pytest.raises(SystemExit, match="gemv_w8_kernel.*expects moe_gate_up_kernel"):
+        bench.summarize_pmc(str(tmp_path / "f.csv"), str(tmp_path / "w.csv"), str(tmp_path / "plan.json"),
+                            str(tmp_path / "out"))
