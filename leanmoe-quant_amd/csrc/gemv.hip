@@ -309,12 +309,27 @@ __global__ __launch_bounds__(1024) void argmax_advance_kernel(
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   float bv = -INFINITY;
   int64_t bi = INT64_MAX;
-  for (int64_t i = tid; i < n; i += 1024) {
-    const float v = PARTIALS ? pv[i] : h2f(logits[i]);
-    const int64_t idx = PARTIALS ? (int64_t)pi[i] : i;
-    if (idx >= 0 && (v > bv || (v == bv && idx < bi))) {
-      bv = v;
-      bi = idx;
+  // Passes of 8 loads per thread, all issued (addresses clamped into [0, n))
+  // before any comparison, so a pass waits on memory once.  The result does
+  // not depend on the visiting order: ties go to the lowest index.
+  constexpr int B = 8;
+  for (int64_t base = 0; base < n; base += (int64_t)B * 1024) {
+    float v[B];
+    int64_t ix[B];
+#pragma unroll
+    for (int j = 0; j < B; ++j) {
+      const int64_t i = base + (int64_t)j * 1024 + tid;
+      const int64_t ic = i < n ? i : n - 1;
+      v[j] = PARTIALS ? pv[ic] : h2f(logits[ic]);
+      ix[j] = PARTIALS ? (int64_t)pi[ic] : ic;
+      if (i >= n) ix[j] = -1;
+    }
+#pragma unroll
+    for (int j = 0; j < B; ++j) {
+      if (ix[j] >= 0 && (v[j] > bv || (v[j] == bv && ix[j] < bi))) {
+        bv = v[j];
+        bi = ix[j];
+      }
     }
   }
 #pragma unroll
