@@ -236,6 +236,42 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float* __restrict
   }
 }
 
+// LSE merge with one wave per (head, 64 dims) and at most NSMAX splits: every
+// load (lane j's m[j] and l[j], and acc[j][dims] of all splits) is issued at
+// entry, so the merge waits on memory once; the wave forms M = max m_j,
+// w_j = 2^(m_j - M) and den = sum l_j w_j with DPP reductions and broadcasts
+// w_j with readlane.  No LDS, no barrier.  num = sum_j acc_j w_j in split
+// order.  Slots j >= NS read a valid split (clamped) with weight 0.
+template <int NSMAX>
+__global__ __launch_bounds__(64) void attn_merge_wave_kernel(const float* __restrict__ m,
+                                                             const float* __restrict__ l,
+                                                             const float* __restrict__ acc,
+                                                             int NS, int D,
+                                                             uint16_t* __restrict__ out) {
+  const int h = blockIdx.x, lane = threadIdx.x;
+  const int t = blockIdx.y * 64 + lane;
+  const int tc = t < D ? t : D - 1;
+  const float* ah = acc + (int64_t)h * NS * D + tc;
+  const int jl = lane < NS ? lane : NS - 1;
+  float mj = m[(int64_t)h * NS + jl];
+  float lj = l[(int64_t)h * NS + jl];
+  float a[NSMAX];
+#pragma unroll
+  for (int j = 0; j < NSMAX; ++j) a[j] = ah[(int64_t)(j < NS ? j : NS - 1) * D];
+  if (lane >= NS) {
+    mj = -INFINITY;
+    lj = 0.0f;
+  }
+  float M = wave_max(mj);
+  if (!(M > -INFINITY)) M = 0.0f;  // every split empty: out = 0
+  const float wj = exp2f(mj - M);
+  const float den = wave_sum(lj * wj);
+  float num = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NSMAX; ++j) num += a[j] * lane_f(wj, j);
+  if (t < D) out[(int64_t)h * D + t] = f2h(den > 0.0f ? num / den : num);
+}
+
 template <bool I8>
 int launch_split(hipStream_t st, const uint16_t* q, const void* k, const uint16_t* ks,
                  const void* v, const uint16_t* vs, int64_t head_stride, int64_t s_len,
@@ -308,8 +344,19 @@ extern "C" int lemoq_attn_merge(const float* m, const float* l, const float* acc
   if (heads <= 0 || heads > 65535 || num_splits <= 0 || num_splits > 1024 || head_dim <= 0 ||
       head_dim > 256)
     return LEMOQ_ERR_SHAPE;
+  hipStream_t st = lemoq_stream(stream);
+  if (num_splits <= 64) {
+    const dim3 grid((unsigned)heads, (unsigned)((head_dim + 63) / 64));
+    if (num_splits <= 16)
+      hipLaunchKernelGGL((attn_merge_wave_kernel<16>), grid, dim3(64), 0, st, m, l, acc,
+                         (int)num_splits, (int)head_dim, out);
+    else
+      hipLaunchKernelGGL((attn_merge_wave_kernel<64>), grid, dim3(64), 0, st, m, l, acc,
+                         (int)num_splits, (int)head_dim, out);
+    LEMOQ_CHECK_LAUNCH();
+  }
   const int threads = head_dim <= 64 ? 64 : (head_dim <= 128 ? 128 : 256);
-  hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)heads), dim3(threads), 0,
-                     lemoq_stream(stream), m, l, acc, (int)num_splits, (int)head_dim, out);
+  hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)heads), dim3(threads), 0, st, m, l, acc,
+                     (int)num_splits, (int)head_dim, out);
   LEMOQ_CHECK_LAUNCH();
 }

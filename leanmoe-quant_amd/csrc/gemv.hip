@@ -60,6 +60,13 @@ __global__ __launch_bounds__(256) void gemv_w8_kernel(const GemvArgs a) {
   } else {
     xr = a.x + m * a.x_ld;
   }
+  // The residual of this wave's rows is loaded now, not in the epilogue, so
+  // the epilogue does not wait on memory (lane r < R holds row row0 + r).
+  uint16_t res = 0;
+  if (MODE == kArgmaxPlain && a.resid) {
+    const int64_t nr = row0 + (lane & (R - 1));
+    res = a.resid[nr < a.N ? nr : a.N - 1];
+  }
   XRaw<KCH> xv;
   // Exact shapes with K >= 2048: the RMSNorm prologue runs once per block
   // (8 values per thread, LDS), not once per wave, after the weight loads.
@@ -160,7 +167,7 @@ __global__ __launch_bounds__(256) void gemv_w8_kernel(const GemvArgs a) {
       if (n < a.N) {
         if (a.y_f16) {
           uint16_t o = f2h(v);
-          if (a.resid) o = hadd_round(h2f(o), a.resid[n]);
+          if (a.resid) o = hadd_round(h2f(o), res);
           reinterpret_cast<uint16_t*>(a.y)[m * a.y_ld + n] = o;
         } else {
           reinterpret_cast<float*>(a.y)[m * a.y_ld + n] = v;

@@ -119,9 +119,14 @@ __global__ __launch_bounds__(512) void moe_down_kernel(
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n0 = blockIdx.x * R;
   const int ng = F / group;
+  // Epilogue operands (residual of this block's rows) are loaded up front.
+  const int t = threadIdx.x;
+  uint16_t res = 0;
+  if (resid && t < R) res = resid[n0 + t < H ? n0 + t : H - 1];
 
   for (int slot = wave; slot < top_k; slot += 8) {
     const int64_t e = ids[slot];
+    const float wslot = h2f(top_w[slot]);
     XRaw<KCH> av;
     x_issue<KCH, EXACT>(av, act + (int64_t)slot * F, F, true, lane);
     const bool ev = e >= 0 && e < E;
@@ -135,18 +140,17 @@ __global__ __launch_bounds__(512) void moe_down_kernel(
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const float v = wave_sum(w8_row_dot<R, KCH>(t, r, xc));
-      if (lane == 0) part[slot][r] = ev ? v : 0.0f;
+      if (lane == 0) part[slot][r] = ev ? v * wslot : 0.0f;
     }
   }
   __syncthreads();
-  const int t = threadIdx.x;
   if (t < R) {
     const int n = n0 + t;
     if (n < H) {
       float v = 0.0f;
-      for (int i = 0; i < top_k; ++i) v += part[i][t] * h2f(top_w[i]);
+      for (int i = 0; i < top_k; ++i) v += part[i][t];
       uint16_t o = f2h(v);
-      if (resid) o = hadd_round(h2f(o), resid[n]);
+      if (resid) o = hadd_round(h2f(o), res);
       out[n] = o;
     }
   }

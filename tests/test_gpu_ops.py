@@ -281,7 +281,7 @@ def test_attn_fp16_vs_fp64(ctx, dev):
     assert_gate(got, ref64, base, what="attn fp16 ctx=%d" % ctx)
 
 
-@pytest.mark.parametrize("splits", [1, 2, 3, 8, 17, 64])
+@pytest.mark.parametrize("splits", [1, 2, 3, 8, 17, 64, 65, 100])
 def test_attn_split_count_invariance(splits, dev):
     from lemoq.kernels.attn_decode import attn_decode_forward
 
@@ -465,3 +465,29 @@ def test_qk_norm_rope_kv_fused_prologue(dev):
     other = torch.ones(S, dtype=torch.bool)
     other[pos] = False
     assert (kc[:, other] == 0).all() and (ks[:, other] == 1).all()
+
+
+@pytest.mark.parametrize("ns", [1, 5, 16, 17, 64, 65, 200])
+@pytest.mark.parametrize("D", [64, 128, 256])
+def test_attn_merge_vs_oracle(ns, D, dev):
+    """lemoq_attn_merge (one wave per 64 dims up to 64 splits, the LDS kernel beyond)
+    against the oracle's LSE merge: empty splits (m = -inf, l = 0, acc = 0), a head
+    whose splits are all empty (-> 0), and m spread over 40 binades."""
+    from lemoq import _hip
+
+    heads = 3
+    g = torch.Generator().manual_seed(ns * 1000 + D)
+    m = (torch.rand((heads, ns), generator=g) * 40 - 20).float()
+    l = torch.rand((heads, ns), generator=g).float() * 10 + 0.1
+    acc = torch.randn((heads, ns, D), generator=g).float() * l.unsqueeze(-1)
+    empty = torch.rand((heads, ns), generator=g) < 0.3
+    empty[2] = True
+    m[empty], l[empty], acc[empty] = float("-inf"), 0.0, 0.0
+    out = torch.empty((heads * D,), dtype=torch.float16, device=dev)
+    md, ld, ad = m.to(dev), l.to(dev), acc.to(dev)
+    _hip.call("lemoq_attn_merge", _hip.ptr(md), _hip.ptr(ld), _hip.ptr(ad), heads, ns, D, _hip.ptr(out),
+              _hip.stream_of(dev))
+    ref = ops.merge_splits(m.double(), l.double(), acc.double())
+    got = out.cpu().reshape(heads, D)
+    assert torch.isfinite(got).all() and (got[2] == 0).all()
+    assert_close(got, ref, what="merge ns=%d D=%d" % (ns, D))
