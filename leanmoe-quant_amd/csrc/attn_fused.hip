@@ -1,6 +1,6 @@
 // Fused per-layer attention of the decode step over the KV-INT8 cache.
 //
-// attn_split_fused_i8: grid (num_splits, heads), 4 or 8 waves per block.  Block
+// attn_split_fused_i8: grid (num_splits, heads), 4 waves per block.  Block
 // (s, h) covers tokens [s*c, min((s+1)*c, n)) of head h with n = *pos + 1 and
 // c = ceil(n / num_splits) (the reference's split rule,
 // src/lemoq/kernels/attn_decode.py:295-354), and does in one launch what the
@@ -14,9 +14,9 @@
 //     folded in (score = ((q.c) * qk_scale) * ks, acc += (p * vs) * c,
 //     l += p), the new token folded from LDS (never read back from the slot
 //     just written), and the block's (m, l, acc[D]) partial.
-// The LSE merge of the partials is done by the consumer (lemoq_attn_merge, or
-// the o_proj GEMV prologue of the decode step).  Each wave keeps two blocks
-// of token loads in flight (double buffering).
+// The LSE merge of the partials is lemoq_attn_merge.  Each wave keeps two
+// blocks of token loads in flight (double buffering); the token groups of a
+// wave are summed with DPP row rotations and the gfx950 cross-row swaps.
 //
 // Arithmetic restates _attn_split_kernel_int8
 // (src/lemoq/kernels/_attn_triton.py:102-165), the KV write
@@ -173,52 +173,74 @@ __global__ __launch_bounds__(64 * NW_) void attn_split_fused_i8_kernel(const Att
   const bool owns_new = pos_ok && start <= pos && pos < end;
   const int64_t cend = owns_new ? pos : end;  // cached tokens [start, cend)
 
+  // The first token block is issued unconditionally (slots clamped into
+  // [0, max(cend, 1)), folds masked by cend): a load under a branch lets the
+  // compiler unpack its bytes right after the issue, which waits on it before
+  // the prologue below could overlap it.
   TokBlock<S> ta, tb;
   int64_t base = start + (int64_t)wave * BLK;
-  if (base < cend) issue_tokens<D, S>(ta, kb, vb, ksh, vsh, base, cend, tl, dl);
+  const int64_t lim = cend > 0 ? cend : 1;
+  issue_tokens<D, S>(ta, kb, vb, ksh, vsh, base, lim, tl, dl);
 
   if (wave == 0 || (owns_new && wave < 3)) {
     // Prologue: wave 0 -> q (every block), wave 1 -> new k (normed, rotated,
-    // quantised), wave 2 -> new v (quantised).  Lane holds d0 .. d0+EPL-1.
+    // quantised), wave 2 -> new v (quantised).  Element i of a lane is
+    // d = lane + 64 i, so for D >= 128 a lane holds both rotate_half partners
+    // (d and d + D/2) and RoPE needs no cross-lane exchange; for D = 64 the
+    // partner is lane ^ 32.  Every prologue load (the lane's values, norm
+    // weight, cos/sin row, and the whole q or k row for the sum of squares)
+    // is issued as raw bits before any of them is used, so the prologue waits
+    // on memory once.
+    constexpr int QV = 8;  // 16-byte row slices per lane held in registers (rows <= 4096)
     const int which = wave;
     const uint16_t* src = a.qkv + (int64_t)which * HD;
-    const int d0 = lane * EPL;
-    float o[EPL];
+    uint16_t ob[EPL], wb[EPL], cb[EPL], sb[EPL];
+    u32x4 qrow[QV];
 #pragma unroll
-    for (int i = 0; i < EPL; ++i) o[i] = h2f(src[h * D + d0 + i]);
+    for (int i = 0; i < EPL; ++i) ob[i] = src[h * D + lane + 64 * i];
     if (which < 2) {
       const uint16_t* nw = which == 0 ? a.qn_w : a.kn_w;
       const int64_t prow = pos_ok ? pos : 0;
-      float wv[EPL], cv[EPL], sv[EPL];
+#pragma unroll
+      for (int j = 0; j < QV; ++j) {
+        const int i = lane * 8 + j * 64 * 8;
+        qrow[j] = *reinterpret_cast<const u32x4*>(src + (i < HD ? i : 0));  // masked below
+      }
 #pragma unroll
       for (int i = 0; i < EPL; ++i) {
-        wv[i] = h2f(nw[h * D + d0 + i]);
-        cv[i] = h2f(a.cos_tab[prow * D + d0 + i]);
-        sv[i] = h2f(a.sin_tab[prow * D + d0 + i]);
+        wb[i] = nw[h * D + lane + 64 * i];
+        cb[i] = a.cos_tab[prow * D + lane + 64 * i];
+        sb[i] = a.sin_tab[prow * D + lane + 64 * i];
       }
+    }
+    LEMOQ_LOADS_ISSUED();
+    float o[EPL];
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) o[i] = h2f(ob[i]);
+    if (which < 2) {
+      // Same sum-of-squares order as lemoq_qk_norm_rope_kv_i8 (slices
+      // lane*8 + 512 j, ssq_f16x8), so both write identical KV bytes.
       float ssq = 0.0f;
-      for (int i = lane * 8; i < HD; i += 64 * 8) {
-        const u32x4 v = *reinterpret_cast<const u32x4*>(src + i);
-        const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float x0 = h2f((uint16_t)(w4[q] & 0xFFFFu)), x1 = h2f((uint16_t)(w4[q] >> 16));
-          ssq = fmaf(x0, x0, ssq);
-          ssq = fmaf(x1, x1, ssq);
-        }
-      }
+      for (int j = 0; j < QV; ++j)
+        if (lane * 8 + j * 64 * 8 < HD) ssq = ssq_f16x8(qrow[j], ssq);
+      for (int i = lane * 8 + QV * 64 * 8; i < HD; i += 64 * 8)  // rows beyond 4096 values
+        ssq = ssq_f16x8(*reinterpret_cast<const u32x4*>(src + i), ssq);
       const float rstd = 1.0f / sqrtf(wave_sum(ssq) / (float)HD + a.eps);
-      const bool first = lane < 32;  // d < D/2; the rotate_half partner is lane ^ 32
+      float xn[EPL];
+#pragma unroll
+      for (int i = 0; i < EPL; ++i) xn[i] = h2f(f2h(h2f(f2h(o[i] * rstd)) * h2f(wb[i])));
 #pragma unroll
       for (int i = 0; i < EPL; ++i) {
-        const float xn = h2f(f2h(h2f(f2h(o[i] * rstd)) * wv[i]));
-        const float xs = __shfl_xor(xn, 32, 64);
-        o[i] = h2f(f2h(first ? xn * cv[i] + (-xs) * sv[i] : xn * cv[i] + xs * sv[i]));
+        const bool first = EPL == 1 ? lane < 32 : i < EPL / 2;  // d < D/2
+        const float xs = EPL == 1 ? xor32_get(xn[i], lane) : xn[i ^ (EPL / 2)];
+        const float cv = h2f(cb[i]), sv = h2f(sb[i]);
+        o[i] = h2f(f2h(first ? xn[i] * cv + (-xs) * sv : xn[i] * cv + xs * sv));
       }
     }
     if (which == 0) {
 #pragma unroll
-      for (int i = 0; i < EPL; ++i) q_s[d0 + i] = f2h(o[i]);
+      for (int i = 0; i < EPL; ++i) q_s[lane + 64 * i] = f2h(o[i]);
     } else {
       float amax = 0.0f;
 #pragma unroll
@@ -233,8 +255,8 @@ __global__ __launch_bounds__(64 * NW_) void attn_split_fused_i8_kernel(const Att
         float qv = rintf(o[i] / s);
         qv = fminf(fmaxf(qv, -127.0f), 127.0f);
         const int8_t c = (int8_t)(int)qv;
-        lds[d0 + i] = c;
-        dst[d0 + i] = c;
+        lds[lane + 64 * i] = c;
+        dst[lane + 64 * i] = c;
       }
       if (lane == 0) {
         kvs_s[which - 1] = h2f(s16);
@@ -252,22 +274,25 @@ __global__ __launch_bounds__(64 * NW_) void attn_split_fused_i8_kernel(const Att
 #pragma unroll
   for (int e = 0; e < 16; ++e) st.acc[e] = 0.0f;
 
-  // Two token blocks in flight: fold one while the next one loads.
+  // Two token blocks in flight: fold one while the next one loads.  The
+  // next block is issued unconditionally (clamped; at the end it re-reads
+  // the split's last slot, an L2 hit) for the reason given above.
   while (base < cend) {
     int64_t nb = base + STRIDE;
-    if (nb < cend) issue_tokens<D, S>(tb, kb, vb, ksh, vsh, nb, cend, tl, dl);
+    issue_tokens<D, S>(tb, kb, vb, ksh, vsh, nb, lim, tl, dl);
     LEMOQ_LOADS_ISSUED();
     fold_tokens<S>(st, ta, qx, base, cend, tl, a.qk_scale);
     base = nb;
     if (base >= cend) break;
     nb = base + STRIDE;
-    if (nb < cend) issue_tokens<D, S>(ta, kb, vb, ksh, vsh, nb, cend, tl, dl);
+    issue_tokens<D, S>(ta, kb, vb, ksh, vsh, nb, lim, tl, dl);
     LEMOQ_LOADS_ISSUED();
     fold_tokens<S>(st, tb, qx, base, cend, tl, a.qk_scale);
     base = nb;
   }
-  if (wave == 0 && owns_new) {
-    // The new token at slot pos, from LDS: only slice (u = 0, tl = 0) is valid.
+  if (wave == NW - 1 && owns_new) {
+    // The new token at slot pos, from LDS: only slice (u = 0, tl = 0) is
+    // valid.  The last wave holds the fewest cached tokens of the split.
     TokBlock<S> nbk;
 #pragma unroll
     for (int u = 0; u < S::U; ++u) {
@@ -279,13 +304,11 @@ __global__ __launch_bounds__(64 * NW_) void attn_split_fused_i8_kernel(const Att
     fold_tokens<S>(st, nbk, qx, 0, 1, tl, a.qk_scale);
   }
 
-  // Sum the token groups of the wave (lanes with the same slice dl).
+  // Sum the token groups of the wave (lanes with the same slice dl); the
+  // running max is wave-uniform, so no rescale is needed.
+  st.l = group_total<LPT>(st.l, lane);
 #pragma unroll
-  for (int o = LPT; o < 64; o <<= 1) {
-    st.l += __shfl_xor(st.l, o, 64);
-#pragma unroll
-    for (int e = 0; e < 16; ++e) st.acc[e] += __shfl_xor(st.acc[e], o, 64);
-  }
+  for (int e = 0; e < 16; ++e) st.acc[e] = group_total<LPT>(st.acc[e], lane);
   if (lane == 0) {
     wm[wave] = st.m;
     wl[wave] = st.l;
@@ -359,25 +382,14 @@ extern "C" int lemoq_attn_split_fused_i8(const uint16_t* qkv, int64_t heads, int
   a.acc_out = acc;
   hipStream_t st = lemoq_stream(stream);
   const dim3 grid((unsigned)num_splits, (unsigned)heads);
-  // Short splits (at most 128 slots per block over the cache's capacity) run
-  // 4 waves per block, so two blocks share a CU and their prologues overlap;
-  // longer splits run 8 waves, whose double-buffered token blocks keep more
-  // loads in flight per block.
-  const bool short_split = (s_len + num_splits - 1) / num_splits <= 128;
-  if (short_split) {
-    const dim3 block(64 * 4);
-    switch (head_dim) {
-      case 64: hipLaunchKernelGGL((attn_split_fused_i8_kernel<64, 4>), grid, block, 0, st, a); break;
-      case 128: hipLaunchKernelGGL((attn_split_fused_i8_kernel<128, 4>), grid, block, 0, st, a); break;
-      default: hipLaunchKernelGGL((attn_split_fused_i8_kernel<256, 4>), grid, block, 0, st, a); break;
-    }
-  } else {
-    const dim3 block(64 * 8);
-    switch (head_dim) {
-      case 64: hipLaunchKernelGGL((attn_split_fused_i8_kernel<64, 8>), grid, block, 0, st, a); break;
-      case 128: hipLaunchKernelGGL((attn_split_fused_i8_kernel<128, 8>), grid, block, 0, st, a); break;
-      default: hipLaunchKernelGGL((attn_split_fused_i8_kernel<256, 8>), grid, block, 0, st, a); break;
-    }
+  // 4 waves per block (two blocks share a CU), 2 token loads per wave in
+  // flight per token block: the fastest shape measured at 1 100 and 4 200
+  // cache slots with 16 splits (against 8 and 16 waves, 1 and 4 loads).
+  const dim3 block(64 * 4);
+  switch (head_dim) {
+    case 64: hipLaunchKernelGGL((attn_split_fused_i8_kernel<64, 4, 2>), grid, block, 0, st, a); break;
+    case 128: hipLaunchKernelGGL((attn_split_fused_i8_kernel<128, 4, 2>), grid, block, 0, st, a); break;
+    default: hipLaunchKernelGGL((attn_split_fused_i8_kernel<256, 4, 2>), grid, block, 0, st, a); break;
   }
   LEMOQ_CHECK_LAUNCH();
 }

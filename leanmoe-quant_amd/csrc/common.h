@@ -66,6 +66,47 @@ __device__ __forceinline__ float wave_max(float v) {
   v = fmaxf(v, dpp_f<LEMOQ_DPP_ROW_MIRROR>(v));
   return fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(lane_f(v, 32), lane_f(v, 48)));
 }
+// Cross-row exchanges of gfx950 (v_permlane16_swap / v_permlane32_swap, no
+// LDS): the value of lane ^ 16 or lane ^ 32.  The swap returns both halves;
+// the partner is selected by lane.  (Adding the two returned halves directly
+// is miscompiled when both operands are the same value: the compiler adds
+// one half to itself.  Selecting the partner and adding it to the lane's own
+// value is exact and symmetric: both lanes of a pair hold the same sum.)
+__device__ __forceinline__ float xor16_get(float v, int lane) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, v),
+                                                  __builtin_bit_cast(uint32_t, v), false, false);
+  return __builtin_bit_cast(float, (lane & 16) ? r[0] : r[1]);
+}
+__device__ __forceinline__ float xor32_get(float v, int lane) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v),
+                                                  __builtin_bit_cast(uint32_t, v), false, false);
+  return __builtin_bit_cast(float, lane < 32 ? r[1] : r[0]);
+}
+
+#define LEMOQ_DPP_ROW_ROR4 0x124
+#define LEMOQ_DPP_ROW_ROR8 0x128
+
+// Sum over the lanes that share lane % G (G in {4, 8, 16}): the total of the
+// 64 / G groups of G lanes, in every lane.  Row rotations by 4 and 8 (DPP),
+// then the two cross-row swaps; no LDS.
+template <int G>
+__device__ __forceinline__ float group_total(float v, int lane) {
+  static_assert(G == 4 || G == 8 || G == 16, "G must be 4, 8 or 16");
+  if (G == 4) v += dpp_f<LEMOQ_DPP_ROW_ROR4>(v);
+  if (G <= 8) v += dpp_f<LEMOQ_DPP_ROW_ROR8>(v);
+  v += xor16_get(v, lane);
+  return v + xor32_get(v, lane);
+}
+
+// Sum of squares of 8 fp16 values (16 bytes) added to acc: four v_dot2_f32_f16
+// (x.lo^2 + x.hi^2 + acc, products exact in fp32) in word order.
+__device__ __forceinline__ float ssq_f16x8(u32x4 v, float acc) {
+  acc = __builtin_amdgcn_fdot2(as_h2(v.x), as_h2(v.x), acc, false);
+  acc = __builtin_amdgcn_fdot2(as_h2(v.y), as_h2(v.y), acc, false);
+  acc = __builtin_amdgcn_fdot2(as_h2(v.z), as_h2(v.z), acc, false);
+  return __builtin_amdgcn_fdot2(as_h2(v.w), as_h2(v.w), acc, false);
+}
+
 // Sum over aligned groups of G lanes (G a power of two <= 64).
 template <int G>
 __device__ __forceinline__ float group_sum(float v) {

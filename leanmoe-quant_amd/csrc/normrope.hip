@@ -108,17 +108,11 @@ __global__ __launch_bounds__(64) void qk_norm_rope_kv_kernel(
       cv[i] = h2f(cos_tab[prow * D + d0 + i]);
       sv[i] = h2f(sin_tab[prow * D + d0 + i]);
     }
+    // Slices lane*8 + 512 j in order, four v_dot2 each (ssq_f16x8): the
+    // order the fused attention prologue uses, so both write the same bytes.
     float ssq = 0.0f;
-    for (int i = lane * 8; i < HD; i += 64 * 8) {
-      const u32x4 v = *reinterpret_cast<const u32x4*>(src + i);
-      const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const float a = h2f((uint16_t)(w4[q] & 0xFFFFu)), b = h2f((uint16_t)(w4[q] >> 16));
-        ssq = fmaf(a, a, ssq);
-        ssq = fmaf(b, b, ssq);
-      }
-    }
+    for (int i = lane * 8; i < HD; i += 64 * 8)
+      ssq = ssq_f16x8(*reinterpret_cast<const u32x4*>(src + i), ssq);
     const float rstd = 1.0f / sqrtf(wave_sum(ssq) / (float)HD + eps);
     float xn[EPL];
 #pragma unroll
