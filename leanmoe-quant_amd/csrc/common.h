@@ -336,14 +336,22 @@ __device__ __forceinline__ void x_chunks(const XRaw<KCH>& x, XChunk (&xc)[KCH]) 
 // Routing of one token inside one wave (the arithmetic of
 // src/lemoq/kernels/_routing_triton.py:55-80 and moe_static._route,
 // src/lemoq/kernels/moe_static.py:276-283): p = exp(z - max) / sum exp(z - max)
-// in fp32 over E <= 64*PL values (lane l holds elements l + 64*i), then top_k
+// in fp32 over E <= 64*PL values (lane l holds elements l + 64*i), then
 // rounds of argmax (ties -> lowest index), optional renormalisation over the
-// selected k.  Lane k < top_k returns the k-th selection (id, weight).
+// selected top_k.  Lane k < rounds returns the k-th selection (id, weight).
+// `rounds` (1 .. top_k) stops the selection early for a caller that needs
+// only the first few ranks; the renormalised weight is exact only when
+// rounds == top_k (the sum covers the selected weights).
+//
+// PL == 1: each round is a DPP wave max of the remaining probabilities, a
+// ballot of the lanes equal to it (the lowest such lane wins) and a readlane
+// of the winner's weight; no LDS.
 // ---------------------------------------------------------------------------
 template <int PL>
 __device__ __forceinline__ void wave_route(const float (&z)[PL], int E, int top_k, bool norm,
-                                           int& my_id, float& my_w) {
+                                           int& my_id, float& my_w, int rounds = -1) {
   const int lane = threadIdx.x & 63;
+  if (rounds < 0 || rounds > top_k) rounds = top_k;
   float mx = -INFINITY;
 #pragma unroll
   for (int i = 0; i < PL; ++i)
@@ -363,38 +371,21 @@ __device__ __forceinline__ void wave_route(const float (&z)[PL], int E, int top_
   my_w = 0.0f;
   float wsum = 0.0f;
   if constexpr (PL == 1) {
-    // Rank of this lane's probability among the wave's 64 (larger first, ties
-    // -> lower index: the order K rounds of argmax produce; lanes >= E hold
-    // -1), read back as broadcasts from a per-wave LDS copy; then the k-th
-    // selection is the lane of rank k (one ballot per k).
-    __shared__ __align__(16) float route_p[16][64];
-    float* sp = route_p[(threadIdx.x >> 6) & 15];
-    sp[lane] = p[0];
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    int rank = 0;
-#pragma unroll
-    for (int j = 0; j < 64; j += 4) {
-      const float4 v = *reinterpret_cast<const float4*>(sp + j);
-      rank += (v.x > p[0] || (v.x == p[0] && j < lane)) ? 1 : 0;
-      rank += (v.y > p[0] || (v.y == p[0] && j + 1 < lane)) ? 1 : 0;
-      rank += (v.z > p[0] || (v.z == p[0] && j + 2 < lane)) ? 1 : 0;
-      rank += (v.w > p[0] || (v.w == p[0] && j + 3 < lane)) ? 1 : 0;
-    }
-    for (int k = 0; k < top_k; ++k) {
-      const uint64_t b = __ballot(rank == k);
-      const int id = (int)__builtin_ctzll(b);
-      const float w = sp[id];
+    float q = p[0];  // remaining candidates; selected lanes drop to -2
+    for (int k = 0; k < rounds; ++k) {
+      const float m = wave_max(q);
+      const int id = (int)__builtin_ctzll(__ballot(q == m));
+      const float w = lane_f(p[0], id);
       if (lane == k) {
         my_id = id;
         my_w = w;
       }
       wsum += w;
+      if (lane == id) q = -2.0f;
     }
   } else {
     uint32_t taken = 0u;
-    for (int k = 0; k < top_k; ++k) {
+    for (int k = 0; k < rounds; ++k) {
       float bv = -2.0f;
       int bi = 0x7fffffff;
 #pragma unroll

@@ -5,10 +5,11 @@
 //           gate rows and the R matching up rows n = (4b + w)*R + r of expert
 //           ids[slot] and writes act[slot, n] = fp16(silu(g) * u).  The
 //           routed form takes the router's fp16 logits instead of ids: wave 0
-//           of every block runs the softmax/top-k of the logits (wave_route:
-//           DPP reductions and an LDS rank count) and the block streams the
-//           expert of its slot; block (0, 0) stores the selected ids and fp16
-//           weights for the down kernel.
+//           of every block runs the softmax of the logits and as many argmax
+//           rounds as its slot needs (wave_route: DPP max, ballot, readlane)
+//           and the block streams the expert of its slot; block (0, 0) runs
+//           all top_k rounds and stores the selected ids and fp16 weights for
+//           the down kernel.
 // down:     grid ceil(H / R) blocks of 8 waves; wave w walks the slots
 //           w, w+8, ... and computes the R rows of expert ids[slot] against
 //           act[slot]; the block then sums slot partials * top_w in a fixed
@@ -58,12 +59,16 @@ __global__ __launch_bounds__(256) void moe_gate_up_kernel(const GateUpArgs a) {
     // from LDS (the other waves' x loads are in flight meanwhile).
     __shared__ int sel_id[64];
     if (wave == 0) {
+      // Block (0, 0) selects all top_k (ids and weights for the down
+      // kernel); every other block stops at its own slot's rank.
+      const bool publish = blockIdx.x == 0 && slot == 0;
+      const int rounds = publish ? a.top_k : slot + 1;
       int id;
       float w;
-      wave_route<PZ>(z, a.E, a.top_k, a.norm != 0, id, w);
-      if (lane < a.top_k) {
+      wave_route<PZ>(z, a.E, a.top_k, a.norm != 0, id, w, rounds);
+      if (lane < rounds) {
         sel_id[lane] = id;
-        if (blockIdx.x == 0 && slot == 0) {
+        if (publish) {
           a.ids_out[lane] = (int64_t)id;
           a.w_out[lane] = f2h(w);
         }

@@ -189,6 +189,47 @@ def test_router_logits_then_routed_gate_up_vs_oracle(norm, E, dev):
         assert torch.equal(act, act2)
 
 
+@pytest.mark.parametrize("case", ["ties_inside", "ties_at_boundary", "all_equal", "descending"])
+@pytest.mark.parametrize("norm", [False, True])
+def test_routed_gate_up_with_tied_logits(case, norm, dev):
+    """Every block of lemoq_moe_gate_up_w8_routed selects its own slot's expert
+    (argmax rounds up to its rank): with tied logits the ids must follow the
+    oracle's order (larger first, ties -> lower index) for every slot, and act
+    must equal the plain gate/up on the oracle's ids."""
+    from lemoq import _hip
+
+    E, K, H, F, g = 64, 8, 2048, 256, 128
+    gc, gs, _, _ = _experts(E, F, H, g, seed=910)
+    z = torch.linspace(-2.0, 1.0, E)[torch.randperm(E, generator=torch.Generator().manual_seed(3))]
+    if case == "ties_inside":
+        z[[5, 9, 40]] = 3.0   # three-way tie at the top
+        z[[2, 33]] = 2.5
+    elif case == "ties_at_boundary":
+        z[:6] = torch.tensor([4.0, 3.9, 3.8, 3.7, 3.6, 3.5])
+        z[[10, 20, 30, 50]] = 3.0  # ranks 6..9 tie: only 10 and 20 are selected
+    elif case == "all_equal":
+        z[:] = 0.5
+    else:
+        z = torch.linspace(2.0, -2.0, E)
+    lg = z.to(torch.float16)
+    x = randn(H, seed=911).to(torch.float16)
+    st = _hip.stream_of(dev)
+    gcd, gsd, xd, lgd = gc.to(dev), gs.to(dev), x.to(dev), lg.to(dev)
+    act = torch.empty(K, F, dtype=torch.float16, device=dev)
+    ti = torch.empty(K, dtype=torch.int64, device=dev)
+    tw = torch.empty(K, dtype=torch.float16, device=dev)
+    _hip.call("lemoq_moe_gate_up_w8_routed", _hip.ptr(xd), _hip.ptr(gcd), _hip.ptr(gsd), _hip.ptr(lgd), K,
+              1 if norm else 0, E, F, H, g, _hip.ptr(act), _hip.ptr(ti), _hip.ptr(tw), st)
+    ref_w, ref_i = oq.route_order(lg.float().numpy()[None], K, norm)
+    assert np.array_equal(ti.cpu().numpy(), ref_i[0]), (case, ti.cpu().tolist(), ref_i[0].tolist())
+    assert torch.allclose(tw.cpu().float(), torch.from_numpy(ref_w[0]).half().float(), atol=1e-3, rtol=0)
+    ids = torch.from_numpy(ref_i[0].astype(np.int64)).to(dev)
+    act2 = torch.empty_like(act)
+    _hip.call("lemoq_moe_gate_up_w8", _hip.ptr(xd), _hip.ptr(gcd), _hip.ptr(gsd), _hip.ptr(ids), K, E, F, H, g,
+              _hip.ptr(act2), st)
+    assert torch.equal(act, act2), case
+
+
 # ---------------------------------------------------------------------------
 # grouped MoE
 # ---------------------------------------------------------------------------
