@@ -253,15 +253,14 @@ __global__ __launch_bounds__(64) void attn_merge_wave_kernel(const float* __rest
   const int tc = t < D ? t : D - 1;
   const float* ah = acc + (int64_t)h * NS * D + tc;
   const int jl = lane < NS ? lane : NS - 1;
-  float mj = m[(int64_t)h * NS + jl];
-  float lj = l[(int64_t)h * NS + jl];
+  const float mraw = m[(int64_t)h * NS + jl];
+  const float lraw = l[(int64_t)h * NS + jl];
   float a[NSMAX];
 #pragma unroll
   for (int j = 0; j < NSMAX; ++j) a[j] = ah[(int64_t)(j < NS ? j : NS - 1) * D];
-  if (lane >= NS) {
-    mj = -INFINITY;
-    lj = 0.0f;
-  }
+  LEMOQ_LOADS_ISSUED();
+  const float mj = lane < NS ? mraw : -INFINITY;  // selects, not branches
+  const float lj = lane < NS ? lraw : 0.0f;
   float M = wave_max(mj);
   if (!(M > -INFINITY)) M = 0.0f;  // every split empty: out = 0
   const float wj = exp2f(mj - M);
@@ -269,7 +268,11 @@ __global__ __launch_bounds__(64) void attn_merge_wave_kernel(const float* __rest
   float num = 0.0f;
 #pragma unroll
   for (int j = 0; j < NSMAX; ++j) num += a[j] * lane_f(wj, j);
-  if (t < D) out[(int64_t)h * D + t] = f2h(den > 0.0f ? num / den : num);
+  // Unconditional store: a lane with t >= D read the clamped column D - 1,
+  // so it writes lane D-1's value to out[D-1] (identical bits).  A store
+  // under `t < D` would let the compiler sink the acc loads and the sum into
+  // the branch, after the reductions, costing a second memory round trip.
+  out[(int64_t)h * D + tc] = f2h(den > 0.0f ? num / den : num);
 }
 
 template <bool I8>

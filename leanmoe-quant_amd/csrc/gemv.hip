@@ -62,10 +62,14 @@ __global__ __launch_bounds__(256) void gemv_w8_kernel(const GemvArgs a) {
   }
   // The residual of this wave's rows is loaded now, not in the epilogue, so
   // the epilogue does not wait on memory (lane r < R holds row row0 + r).
+  // The load is unconditional (a valid address when there is no residual):
+  // a load under a branch is waited on right away, before the loads below
+  // are issued.
   uint16_t res = 0;
-  if (MODE == kArgmaxPlain && a.resid) {
+  if (MODE == kArgmaxPlain) {
     const int64_t nr = row0 + (lane & (R - 1));
-    res = a.resid[nr < a.N ? nr : a.N - 1];
+    const uint16_t* rp = a.resid ? a.resid + (nr < a.N ? nr : a.N - 1) : a.x;
+    res = *rp;
   }
   XRaw<KCH> xv;
   // Exact shapes with K >= 2048: the RMSNorm prologue runs once per block

@@ -44,10 +44,13 @@ __global__ __launch_bounds__(256) void moe_gate_up_kernel(const GateUpArgs a) {
   constexpr int PZ = PL > 0 ? PL : 1;
   float z[PZ];
   if constexpr (PL > 0) {
+    // Unconditional loads (index clamped, value masked after the load): a
+    // load under a branch is waited on before the x loads below are issued.
 #pragma unroll
     for (int i = 0; i < PL; ++i) {
       const int idx = lane + 64 * i;
-      z[i] = idx < a.E ? h2f(a.logits[idx]) : -INFINITY;
+      const float v = h2f(a.logits[idx < a.E ? idx : a.E - 1]);
+      z[i] = idx < a.E ? v : -INFINITY;
     }
   } else {
     e = a.ids[slot];
@@ -124,10 +127,11 @@ __global__ __launch_bounds__(512) void moe_down_kernel(
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n0 = blockIdx.x * R;
   const int ng = F / group;
-  // Epilogue operands (residual of this block's rows) are loaded up front.
+  // Epilogue operands (residual of this block's rows) are loaded up front,
+  // unconditionally (a load under a branch is waited on right away).
   const int t = threadIdx.x;
-  uint16_t res = 0;
-  if (resid && t < R) res = resid[n0 + t < H ? n0 + t : H - 1];
+  const int nres = n0 + (t & (R - 1));
+  const uint16_t res = *(resid ? resid + (nres < H ? nres : H - 1) : act);
 
   for (int slot = wave; slot < top_k; slot += 8) {
     const int64_t e = ids[slot];
