@@ -86,12 +86,18 @@ def test_olmoe_shape_32_greedy_steps_match_oracle(dev):
     """Full OLMoE-1B-7B shape (16 layers, 64 experts top-8, vocab 50304) at ctx 256:
     every step's logits agree (KL < 0.01) and the greedy token equals the
     oracle's argmax except at near-ties (random-init logits have top-1/top-2
-    margins down to one fp16 ulp; such steps are printed and counted)."""
+    margins down to one fp16 ulp; such steps are printed).  A step where the
+    oracle's top two fp16 logits are exactly equal (margin 0) is decided by
+    index order alone, so the reference is indifferent between the two tokens:
+    such flips are listed but not counted.  At most 2 flips at a non-zero
+    margin are allowed, each within twice the measured logit difference."""
     print("case: OLMoE shape, ctx 256, 32 steps", flush=True)
     toks, gl, rl = _teacher_forced(OLMOE_1B_7B, [1] * 256, 32, 0, dev)
     flips = _check_steps(toks, gl, rl)
-    print("near-tie flips:", flips)
-    assert len(flips) <= 2, flips
+    exact_ties = [f for f in flips if f[1] == 0.0]
+    counted = [f for f in flips if f[1] != 0.0]
+    print("near-tie flips:", counted, "flips at exact fp16 ties:", exact_ties)
+    assert len(counted) <= 2, flips
 
 
 def test_graph_replay_equals_eager_step_bitwise(dev):
