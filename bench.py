@@ -219,7 +219,7 @@ def kernel_table(torch, hip, w, sess, flusher, reps: int) -> dict:
 def time_decode(torch, w, ctx: int, steps: int, warmup: int, extra: int):
     from lemoq.model.olmoe import DecodeSession
 
-    sess = DecodeSession(w, [1] * ctx, max_new_tokens=warmup + steps + extra + 1)
+    sess = DecodeSession(w, [1] * ctx, max_new_tokens=warmup + 2 * steps + extra + 4)
     sess.capture()
     t = time.time()
     sess.prefill()
@@ -238,6 +238,15 @@ def time_decode(torch, w, ctx: int, steps: int, warmup: int, extra: int):
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3
     dev_ms = e0.elapsed_time(e1)
+    # Per-step latency distribution: a second pass with an event between replays.
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    evs[0].record()
+    for i in range(steps):
+        sess.graph.replay()
+        evs[i + 1].record()
+    torch.cuda.synchronize()
+    per = sorted(evs[i].elapsed_time(evs[i + 1]) for i in range(steps))
+    p50, p99 = per[len(per) // 2], per[min(len(per) - 1, int(round(0.99 * (len(per) - 1))))]
     filled_avg = filled0 + (steps - 1) / 2.0
     step_bytes = w.shape.weight_bytes_per_token() + KV_BYTES_PER_TOKEN_LAYER * w.shape.layers * filled_avg
     res = {
@@ -249,8 +258,11 @@ def time_decode(torch, w, ctx: int, steps: int, warmup: int, extra: int):
         "filled_first": filled0,
         "step_bytes": int(step_bytes),
         "launches_per_step": sess.launches_per_step,
+        "step_ms_p50": p50,
+        "step_ms_p99": p99,
     }
-    log("ctx %d: %.4f ms/token wall, %.4f device, %d steps" % (ctx, res["ms_per_token"], res["device_ms_per_token"], steps))
+    log("ctx %d: %.4f ms/token wall, %.4f device, %d steps; per-step p50 %.4f p99 %.4f ms"
+        % (ctx, res["ms_per_token"], res["device_ms_per_token"], steps, p50, p99))
     return sess, res
 
 
@@ -287,10 +299,23 @@ def cpu_baseline(torch, w, cap, gpu_tokens, gpu_logits, budget_s: float, max_ste
             break
     timed = times[1:] if len(times) > 1 else times  # first step warms the allocator
     ms = 1e3 * sum(timed) / len(timed)
+    # One thread: two more steps (the second timed), the same oracle state.
+    threads = torch.get_num_threads()
+    torch.set_num_threads(1)
+    try:
+        od.step(seq[n], pos + n)
+        t = time.perf_counter()
+        od.step(seq[n + 1] if n + 1 < len(seq) else seq[n], pos + n + 1)
+        ms_1t = 1e3 * (time.perf_counter() - t)
+    finally:
+        torch.set_num_threads(threads)
+    log("cpu oracle: %.1f ms/token on %d threads, %.1f ms/token on 1 thread" % (ms, threads, ms_1t))
     return {
         "value": ms,
         "unit": "ms/token",
-        "cores": int(torch.get_num_threads()),
+        "cores": int(threads),
+        "value_1thread": ms_1t,
+        "cpu_model": _cpu_model(),
         "kind": "port",
         "sample": "%d decode steps of the full OLMoE-1B-7B-shaped w8a16+KV-INT8 model by the torch-CPU oracle "
                   "from the GPU's KV snapshot at position %d, fed the GPU's greedy tokens (first step untimed)"
@@ -302,6 +327,69 @@ def cpu_baseline(torch, w, cap, gpu_tokens, gpu_logits, budget_s: float, max_ste
 
 
 # ---------------------------------------------------------------------------
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+# ---------------------------------------------------------------------------
+# BASELINE attention configs as isolated kernels (fp16 and KV-INT8 split-KV)
+# ---------------------------------------------------------------------------
+def attention_configs(torch, hip, flusher, reps: int) -> dict:
+    """Split-KV decode attention at the BASELINE shapes, cold, 16 layers' worth of
+    caches per pass (split kernel + LSE merge, chunks of 256 cache slots):
+    fp16 K/V at ctx 1024 and 4096, KV-INT8 at 4096 and 16384.  Algorithmic
+    bytes: fp16 4 * 16 * ctx * 128; int8 4160 * ctx; plus q and partials."""
+    dev = flusher.buf.device
+    heads, D, copies = 16, 128, 16
+    qk_scale = (1.0 / math.sqrt(D)) * 1.4426950408889634
+    out = {}
+    for kind, ctx in (("f16", 1024), ("f16", 4096), ("i8", 4096), ("i8", 16384)):
+        ns = ctx // 256
+        q = torch.randn((heads * D,), device=dev).to(torch.float16)
+        filled = torch.tensor([ctx], dtype=torch.int32, device=dev)
+        m = torch.empty((heads * ns,), dtype=torch.float32, device=dev)
+        l = torch.empty_like(m)
+        acc = torch.empty((heads * ns * D,), dtype=torch.float32, device=dev)
+        o = torch.empty((heads * D,), dtype=torch.float16, device=dev)
+        P, st = hip.ptr, hip.stream_of
+        caches = []
+        for _ in range(copies):
+            if kind == "f16":
+                caches.append([torch.randn((heads * ctx * D,), device=dev).to(torch.float16) for _ in range(2)])
+            else:
+                c = [torch.randint(-127, 128, (heads * ctx * D,), dtype=torch.int8, device=dev) for _ in range(2)]
+                sc = [torch.full((heads * ctx,), 0.01, dtype=torch.float16, device=dev) for _ in range(2)]
+                caches.append(c + sc)
+        if kind == "f16":
+            nbytes = 4 * heads * ctx * D + heads * D * 2 + heads * ns * (D + 2) * 4
+            fns = [lambda c=c: (hip.call("lemoq_attn_split_f16", P(q), P(c[0]), P(c[1]), ctx * D, P(filled), heads, D,
+                                         ns, qk_scale, P(m), P(l), P(acc), st()),
+                                hip.call("lemoq_attn_merge", P(m), P(l), P(acc), heads, ns, D, P(o), st()))
+                   for c in caches]
+        else:
+            nbytes = KV_BYTES_PER_TOKEN_LAYER * ctx + heads * D * 2 + heads * ns * (D + 2) * 4
+            fns = [lambda c=c: (hip.call("lemoq_attn_split_i8", P(q), P(c[0]), P(c[2]), P(c[1]), P(c[3]), ctx * D, ctx,
+                                         P(filled), heads, D, ns, qk_scale, P(m), P(l), P(acc), st()),
+                                hip.call("lemoq_attn_merge", P(m), P(l), P(acc), heads, ns, D, P(o), st()))
+                   for c in caches]
+        r = time_cold(torch, flusher, fns, reps)
+        name = "attn_%s ctx %d (split + merge, %d splits)" % (kind, ctx, ns)
+        r["bytes"] = int(nbytes)
+        r["gbs"] = nbytes / (r["avg_us"] * 1e-6) / 1e9
+        out[name] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in r.items()}
+        log("config %-44s %8.2f us avg  %7.1f GB/s" % (name, r["avg_us"], r["gbs"]))
+        del caches, fns
+        torch.cuda.synchronize()
+    return out
+
+
 # HBM traffic from two rocprofv3 --pmc passes
 # ---------------------------------------------------------------------------
 COPY_BYTES = 512 << 20  # calibration copy: larger than the 256 MB Infinity Cache
@@ -469,6 +557,7 @@ def main(argv=None) -> int:
             check_logits.append(sess.logits_cpu())
         check_tokens = [int(t) for t in sess.history[p0 + 1: p0 + 1 + check_n].tolist()]
     kt = kernel_table(torch, _hip, w, sess, flusher, args.kernel_reps)
+    cfg = attention_configs(torch, _hip, flusher, args.kernel_reps)
     cap = _Cap(sess.max_seq)
     del sess
     r2 = None
@@ -527,6 +616,8 @@ def main(argv=None) -> int:
         "kernels": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()
                         if kk != "dispatch_kernels"} for k, v in kt.items()},
     }
+    line["attention_configs"] = cfg
+    line["step_ms_p50"], line["step_ms_p99"] = r1["step_ms_p50"], r1["step_ms_p99"]
     if r2 is not None:
         line["ctx2"] = r2
         line["ms_per_token_ctx%d" % args.ctx2] = r2["ms_per_token"]
