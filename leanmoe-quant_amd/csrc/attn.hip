@@ -1,58 +1,24 @@
 // Split-KV decode attention (flash-decoding) for batch 1, q_len 1, over fp16
 // or KV-INT8 caches, and the log-sum-exp merge of the splits.
 //
-// Split kernel: grid (num_splits, heads), 4 waves.  Every lane reads 16 bytes
-// of a K/V row, so a token row is LPT = D*bytes/16 lanes and a wave covers
-// TPW = 64/LPT tokens per load.  Each wave walks its interleaved blocks of
-// U*TPW tokens of the split with an online softmax whose running max is
-// wave-uniform: scores are reduced inside the LPT-lane group, the block max
-// with one wave butterfly, then p = exp2(s - m) weights the V rows that the
-// same lanes load.  The four wave states (m, l, acc[D]) are merged through
-// LDS in a fixed order.  Tokens at or beyond the filled length are never
-// loaded, so whatever the cache holds there (NaN included) cannot leak in.
-// INT8 rows fold the per-token scales: score = ((q.c) * qk_scale) * ks,
-// acc += (p * vs) * c, l += p.
-#include "common.h"
+// Split kernel: grid (num_splits, heads), 4 waves.  Block (s, h) covers
+// tokens [s*c, min((s+1)*c, n)) of head h with n = *filled (clamped to the
+// cache) and c = ceil(n / num_splits) (the reference's split rule,
+// src/lemoq/kernels/attn_decode.py:295-354).  Each wave walks its
+// interleaved token blocks with two blocks of loads in flight, an online
+// softmax with a wave-uniform running max, and KV-INT8 scales folded in
+// (attn_common.h); the four wave states are merged through LDS in a fixed
+// order.  Tokens at or beyond the filled length are never loaded, so
+// whatever the cache holds there (NaN included) cannot leak in.
+#include "attn_common.h"
 
 namespace {
 
 template <int D, bool I8>
-struct AttnShape {
-  static constexpr int EB = I8 ? 1 : 2;    // bytes per cached element
-  static constexpr int EPL = 16 / EB;      // elements per lane
-  static constexpr int LPT = D / EPL;      // lanes per token row
-  static constexpr int TPW = 64 / LPT;     // tokens per wave load
-  static constexpr int U = I8 ? 2 : 4;     // loads per softmax update
-  static_assert(LPT >= 1 && LPT <= 64 && (64 % LPT) == 0, "unsupported head_dim");
+struct SplitShape {
+  static constexpr int NW = 4;             // waves per block
+  using T = lemoq_attn::TokShape<D, I8, I8 ? 2 : 4>;  // 16 tokens per wave block at D = 128
 };
-
-// q . k for one 16-byte slice (fp16 K: 8 values; int8 K: 16 codes).
-__device__ __forceinline__ float qk_dot_f16(const u32x4 k, const u32x4 q) {
-  const uint32_t kw[4] = {k.x, k.y, k.z, k.w};
-  const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
-  float a = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) a = __builtin_amdgcn_fdot2(as_h2(kw[i]), as_h2(qw[i]), a, false);
-  return a;
-}
-
-__device__ __forceinline__ void unpack_f16x8(const u32x4 v, float (&o)[8]) {
-  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    o[2 * i] = h2f((uint16_t)(w[i] & 0xFFFFu));
-    o[2 * i + 1] = h2f((uint16_t)(w[i] >> 16));
-  }
-}
-
-__device__ __forceinline__ void unpack_i8x16(const u32x4 v, float (&o)[16]) {
-  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-#pragma unroll
-    for (int b = 0; b < 4; ++b) o[4 * i + b] = (float)(int8_t)((w[i] >> (8 * b)) & 0xFFu);
-  }
-}
 
 template <int D, bool I8>
 __global__ __launch_bounds__(256) void attn_split_kernel(
@@ -60,15 +26,20 @@ __global__ __launch_bounds__(256) void attn_split_kernel(
     const void* __restrict__ vp, const uint16_t* __restrict__ vs, int64_t head_stride,
     int64_t s_len, int64_t max_len, const int32_t* __restrict__ filled, int NS, float qk_scale,
     float* __restrict__ m_out, float* __restrict__ l_out, float* __restrict__ acc_out) {
-  using S = AttnShape<D, I8>;
-  constexpr int EPL = S::EPL, LPT = S::LPT, TPW = S::TPW, U = S::U;
-  __shared__ float wm[4], wl[4];
-  __shared__ float wacc[4][D];
+  using T = typename SplitShape<D, I8>::T;
+  constexpr int NW = SplitShape<D, I8>::NW;
+  constexpr int STRIDE = NW * T::BLK;
+  __shared__ float wm[NW], wl[NW];
+  __shared__ float wacc[NW * D];
 
   const int sp = blockIdx.x, h = blockIdx.y;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int dl = lane % LPT;  // which 16-byte slice of the row
-  const int tl = lane / LPT;  // which token of the wave load
+  const int dl = lane % T::LPT;  // which 16-byte slice of the row
+  const int tl = lane / T::LPT;  // which token of the wave load
+
+  // This lane's slice of q first: the load counter retires in order.
+  lemoq_attn::QSlice<I8> qx;
+  lemoq_attn::load_q<T>(qx, q + (int64_t)h * D, dl);
 
   int64_t n = filled[0];
   n = n < 0 ? 0 : (n > max_len ? max_len : n);
@@ -76,116 +47,32 @@ __global__ __launch_bounds__(256) void attn_split_kernel(
   const int64_t start = (int64_t)sp * chunk;
   const int64_t end = start + chunk < n ? start + chunk : n;
 
-  const uint8_t* kb = reinterpret_cast<const uint8_t*>(kp) + (int64_t)h * head_stride * S::EB;
-  const uint8_t* vb = reinterpret_cast<const uint8_t*>(vp) + (int64_t)h * head_stride * S::EB;
+  const uint8_t* kb = reinterpret_cast<const uint8_t*>(kp) + (int64_t)h * head_stride * T::EB;
+  const uint8_t* vb = reinterpret_cast<const uint8_t*>(vp) + (int64_t)h * head_stride * T::EB;
   const uint16_t* ksh = I8 ? ks + (int64_t)h * s_len : nullptr;
   const uint16_t* vsh = I8 ? vs + (int64_t)h * s_len : nullptr;
 
-  // This lane's slice of q.
-  XChunk qx;            // int8 path: 16 q values in dot order
-  u32x4 qv = {0u, 0u, 0u, 0u};  // fp16 path: 8 q values
-  if (I8) {
-    load_xchunk(q + (int64_t)h * D + dl * EPL, qx);
-  } else {
-    qv = *reinterpret_cast<const u32x4*>(q + (int64_t)h * D + dl * EPL);
+  lemoq_attn::TokBlock<T> ta, tb;
+  int64_t base = start + (int64_t)wave * T::BLK;
+  const int64_t lim = end > 0 ? end : 1;  // clamp target: slot lim - 1 is always valid
+  lemoq_attn::issue_tokens<T>(ta, kb, vb, ksh, vsh, base, lim, tl, dl, D);
+  lemoq_attn::SoftmaxState<T::EPL> st;
+  lemoq_attn::softmax_init(st);
+  while (base < end) {
+    int64_t nb = base + STRIDE;
+    lemoq_attn::issue_tokens<T>(tb, kb, vb, ksh, vsh, nb, lim, tl, dl, D);
+    LEMOQ_LOADS_ISSUED();
+    lemoq_attn::fold_tokens<T>(st, ta, qx, base, end, tl, lane, qk_scale);
+    base = nb;
+    if (base >= end) break;
+    nb = base + STRIDE;
+    lemoq_attn::issue_tokens<T>(ta, kb, vb, ksh, vsh, nb, lim, tl, dl, D);
+    LEMOQ_LOADS_ISSUED();
+    lemoq_attn::fold_tokens<T>(st, tb, qx, base, end, tl, lane, qk_scale);
+    base = nb;
   }
-
-  float m = -INFINITY, l = 0.0f;
-  float acc[EPL];
-#pragma unroll
-  for (int e = 0; e < EPL; ++e) acc[e] = 0.0f;
-
-  constexpr int BLK = TPW * U;  // tokens per wave step
-  for (int64_t base = start + (int64_t)wave * BLK; base < end; base += 4 * BLK) {
-    float sc[U];
-    bool valid[U];
-    u32x4 kr[U], vr[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t t = base + u * TPW + tl;
-      valid[u] = t < end;
-      const int64_t off = (t * D + dl * EPL) * S::EB;
-      kr[u] = valid[u] ? *reinterpret_cast<const u32x4*>(kb + off) : (u32x4){0u, 0u, 0u, 0u};
-      vr[u] = valid[u] ? *reinterpret_cast<const u32x4*>(vb + off) : (u32x4){0u, 0u, 0u, 0u};
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      float d = I8 ? dot16_i8(kr[u], qx, 0.0f) : qk_dot_f16(kr[u], qv);
-      d = group_sum<LPT>(d);
-      const int64_t t = base + u * TPW + tl;
-      float s = d * qk_scale;
-      if (I8) s = s * (valid[u] ? h2f(ksh[t]) : 0.0f);
-      sc[u] = valid[u] ? s : -INFINITY;
-    }
-    float mx = sc[0];
-#pragma unroll
-    for (int u = 1; u < U; ++u) mx = fmaxf(mx, sc[u]);
-    mx = wave_max(mx);
-    const float m_new = fmaxf(m, mx);
-    if (m_new == -INFINITY) continue;  // no valid token yet (cannot happen for finite scores)
-    const float alpha = exp2f(m - m_new);
-    float psum = 0.0f;
-    float pw[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const float p = valid[u] ? exp2f(sc[u] - m_new) : 0.0f;
-      psum += p;
-      const int64_t t = base + u * TPW + tl;
-      pw[u] = I8 ? (valid[u] ? p * h2f(vsh[t]) : 0.0f) : p;
-    }
-    l = l * alpha + psum;
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) acc[e] *= alpha;
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if (I8) {
-        float vf[16];
-        unpack_i8x16(vr[u], vf);
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) acc[e] = fmaf(pw[u], vf[e], acc[e]);
-      } else {
-        float vf[8];
-        unpack_f16x8(vr[u], vf);
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) acc[e] = fmaf(pw[u], vf[e], acc[e]);
-      }
-    }
-    m = m_new;
-  }
-  // Sum the token groups of the wave (lanes with the same slice dl).
-#pragma unroll
-  for (int o = LPT; o < 64; o <<= 1) {
-    l += __shfl_xor(l, o, 64);
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) acc[e] += __shfl_xor(acc[e], o, 64);
-  }
-  if (lane == 0) {
-    wm[wave] = m;
-    wl[wave] = l;
-  }
-  if (tl == 0) {
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) wacc[wave][dl * EPL + e] = acc[e];
-  }
-  __syncthreads();
-  const int64_t pidx = (int64_t)h * NS + sp;
-  for (int t = threadIdx.x; t < D; t += 256) {
-    float M = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
-    float a = 0.0f, L = 0.0f;
-    if (M != -INFINITY) {
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const float f = exp2f(wm[w] - M);
-        a += wacc[w][t] * f;
-        L += wl[w] * f;
-      }
-    }
-    acc_out[pidx * D + t] = a;
-    if (t == 0) {
-      m_out[pidx] = M;
-      l_out[pidx] = L;
-    }
-  }
+  lemoq_attn::finish_split<T, NW, D>(st, wm, wl, wacc, lane, wave, tl, dl, (int64_t)h * NS + sp,
+                                     m_out, l_out, acc_out);
 }
 
 // LSE merge of one head per block: the split weights 2^(m_j - M) and the

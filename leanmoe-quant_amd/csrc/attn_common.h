@@ -1,0 +1,226 @@
+// Split-KV decode attention building blocks shared by the fused per-layer
+// kernel (attn_fused.hip) and the standalone split kernels (attn.hip).
+//
+// A lane reads 16 bytes of a cached K or V row: 16 int8 codes (KV-INT8) or 8
+// fp16 values.  A token row is LPT = D * bytes / 16 lanes, a wave load covers
+// TPW = 64 / LPT tokens, and a wave token block is U loads (BLK = TPW * U
+// tokens).  Token blocks are issued unconditionally, with slots at or beyond
+// the split's end clamped to a valid slot and masked when folded, so a load
+// never sits under a branch (the compiler would wait on it right away) and a
+// slot past the filled length is never read.  The online softmax keeps a
+// wave-uniform running max; INT8 rows fold the per-token scales
+// (score = ((q.c) * qk_scale) * ks, acc += (p * vs) * c, l += p), which is
+// the arithmetic of _attn_split_kernel_int8 / _attn_split_kernel
+// (src/lemoq/kernels/_attn_triton.py:30-165 of the reference).
+#pragma once
+
+#include "common.h"
+
+namespace lemoq_attn {
+
+// Sum over aligned groups of G lanes (G in {4, 8, 16, 32}): DPP row ops, then
+// the cross-row exchange for 32.
+template <int G>
+__device__ __forceinline__ float group_sum_lanes(float v, int lane) {
+  static_assert(G == 4 || G == 8 || G == 16 || G == 32, "group of 4, 8, 16 or 32 lanes");
+  v += dpp_f<LEMOQ_DPP_QUAD_1032>(v);
+  v += dpp_f<LEMOQ_DPP_QUAD_2301>(v);
+  if (G >= 8) v += dpp_f<LEMOQ_DPP_ROW_HALF_MIRROR>(v);
+  if (G >= 16) v += dpp_f<LEMOQ_DPP_ROW_MIRROR>(v);
+  if (G >= 32) v += xor16_get(v, lane);
+  return v;
+}
+
+// Sum over the lanes that share lane % G (the 64 / G token groups of a wave).
+template <int G>
+__device__ __forceinline__ float groups_total(float v, int lane) {
+  if constexpr (G == 32) {
+    return v + xor32_get(v, lane);
+  } else {
+    return group_total<G>(v, lane);
+  }
+}
+
+template <int D, bool I8, int U_>
+struct TokShape {
+  static constexpr bool INT8 = I8;
+  static constexpr int EB = I8 ? 1 : 2;    // bytes per cached element
+  static constexpr int EPL = 16 / EB;      // cached elements per lane load
+  static constexpr int LPT = D / EPL;      // lanes per token row
+  static constexpr int TPW = 64 / LPT;     // tokens per wave load
+  static constexpr int U = U_;             // wave loads per token block
+  static constexpr int BLK = TPW * U;      // tokens per wave token block
+  static_assert(LPT == 4 || LPT == 8 || LPT == 16 || LPT == 32, "head_dim must be 64, 128 or 256");
+};
+
+template <class S>
+struct TokBlock {
+  u32x4 k[S::U], v[S::U];
+  uint16_t ks[S::U], vs[S::U];  // per-token scales (KV-INT8 only)
+};
+
+// The lane's slice of q: 16 values in dot16_i8 order (int8 K) or 8 packed
+// fp16 values (fp16 K).
+template <bool I8>
+struct QSlice;
+template <>
+struct QSlice<true> {
+  XChunk x;
+};
+template <>
+struct QSlice<false> {
+  u32x4 x;
+};
+
+template <class S>
+__device__ __forceinline__ void load_q(QSlice<S::INT8>& q, const uint16_t* qh, int dl) {
+  if constexpr (S::INT8) {
+    load_xchunk(qh + dl * 16, q.x);
+  } else {
+    q.x = *reinterpret_cast<const u32x4*>(qh + dl * 8);
+  }
+}
+
+// Loads of the token block at `base` (token base + u*TPW + tl for load u);
+// slots at or beyond `lim` are clamped to lim - 1 (a valid slot).
+template <class S>
+__device__ __forceinline__ void issue_tokens(TokBlock<S>& b, const uint8_t* __restrict__ kb,
+                                             const uint8_t* __restrict__ vb,
+                                             const uint16_t* __restrict__ ksh,
+                                             const uint16_t* __restrict__ vsh, int64_t base,
+                                             int64_t lim, int tl, int dl, int D) {
+#pragma unroll
+  for (int u = 0; u < S::U; ++u) {
+    int64_t t = base + u * S::TPW + tl;
+    t = t < lim ? t : lim - 1;
+    const int64_t off = t * D * S::EB + dl * 16;
+    b.k[u] = load_stream16(reinterpret_cast<const int8_t*>(kb + off));
+    b.v[u] = load_stream16(reinterpret_cast<const int8_t*>(vb + off));
+    if constexpr (S::INT8) {
+      b.ks[u] = ksh[t];
+      b.vs[u] = vsh[t];
+    }
+  }
+}
+
+template <int EPL>
+struct SoftmaxState {
+  float m, l;
+  float acc[EPL];
+};
+
+template <int EPL>
+__device__ __forceinline__ void softmax_init(SoftmaxState<EPL>& st) {
+  st.m = -INFINITY;
+  st.l = 0.0f;
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) st.acc[e] = 0.0f;
+}
+
+__device__ __forceinline__ float qk_dot_f16(const u32x4 k, const u32x4 q) {
+  float a = __builtin_amdgcn_fdot2(as_h2(k.x), as_h2(q.x), 0.0f, false);
+  a = __builtin_amdgcn_fdot2(as_h2(k.y), as_h2(q.y), a, false);
+  a = __builtin_amdgcn_fdot2(as_h2(k.z), as_h2(q.z), a, false);
+  return __builtin_amdgcn_fdot2(as_h2(k.w), as_h2(q.w), a, false);
+}
+
+// Online-softmax update with the token block at `base`; loads at or beyond
+// `n` are masked (a masked slot may hold anything: its weight is selected to
+// zero, never multiplied, so a NaN scale or value there cannot reach acc).
+template <class S>
+__device__ __forceinline__ void fold_tokens(SoftmaxState<S::EPL>& st, const TokBlock<S>& b,
+                                            const QSlice<S::INT8>& q, int64_t base, int64_t n,
+                                            int tl, int lane, float qk_scale) {
+  float sc[S::U];
+  bool valid[S::U];
+#pragma unroll
+  for (int u = 0; u < S::U; ++u) {
+    const int64_t t = base + u * S::TPW + tl;
+    valid[u] = t < n;
+    float d;
+    if constexpr (S::INT8) {
+      d = group_sum_lanes<S::LPT>(dot16_i8(b.k[u], q.x, 0.0f), lane);
+      sc[u] = valid[u] ? (d * qk_scale) * h2f(b.ks[u]) : -INFINITY;
+    } else {
+      d = group_sum_lanes<S::LPT>(qk_dot_f16(b.k[u], q.x), lane);
+      sc[u] = valid[u] ? d * qk_scale : -INFINITY;
+    }
+  }
+  float mx = sc[0];
+#pragma unroll
+  for (int u = 1; u < S::U; ++u) mx = fmaxf(mx, sc[u]);
+  mx = wave_max(mx);
+  const float m_new = fmaxf(st.m, mx);
+  if (m_new == -INFINITY) return;  // no valid token in this block (wave-uniform)
+  const float alpha = exp2f(st.m - m_new);
+  st.l *= alpha;
+#pragma unroll
+  for (int e = 0; e < S::EPL; ++e) st.acc[e] *= alpha;
+#pragma unroll
+  for (int u = 0; u < S::U; ++u) {
+    const float p = exp2f(sc[u] - m_new);  // 0 for masked loads (sc = -inf)
+    st.l += p;
+    const uint32_t w[4] = {b.v[u].x, b.v[u].y, b.v[u].z, b.v[u].w};
+    if constexpr (S::INT8) {
+      const float pw = valid[u] ? p * h2f(b.vs[u]) : 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          st.acc[4 * i + k] = fmaf(pw, (float)(int8_t)((w[i] >> (8 * k)) & 0xFFu), st.acc[4 * i + k]);
+    } else {
+      const float pw = valid[u] ? p : 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        st.acc[2 * i] = fmaf(pw, valid[u] ? h2f((uint16_t)(w[i] & 0xFFFFu)) : 0.0f, st.acc[2 * i]);
+        st.acc[2 * i + 1] = fmaf(pw, valid[u] ? h2f((uint16_t)(w[i] >> 16)) : 0.0f, st.acc[2 * i + 1]);
+      }
+    }
+  }
+  st.m = m_new;
+}
+
+// End of a split block: sum the token groups of each wave (the running max is
+// wave-uniform), merge the NW wave states through LDS in wave order, and
+// write the block's (m, l, acc[D]) partial; m = -inf for an empty split
+// (l = 0, acc = 0).  wm/wl hold NW floats, wacc NW * D.
+template <class S, int NW, int D>
+__device__ __forceinline__ void finish_split(SoftmaxState<S::EPL>& st, float* wm, float* wl,
+                                             float* wacc, int lane, int wave, int tl, int dl,
+                                             int64_t pidx, float* __restrict__ m_out,
+                                             float* __restrict__ l_out,
+                                             float* __restrict__ acc_out) {
+  st.l = groups_total<S::LPT>(st.l, lane);
+#pragma unroll
+  for (int e = 0; e < S::EPL; ++e) st.acc[e] = groups_total<S::LPT>(st.acc[e], lane);
+  if (lane == 0) {
+    wm[wave] = st.m;
+    wl[wave] = st.l;
+  }
+  if (tl == 0) {
+#pragma unroll
+    for (int e = 0; e < S::EPL; ++e) wacc[wave * D + dl * S::EPL + e] = st.acc[e];
+  }
+  __syncthreads();
+  for (int t = threadIdx.x; t < D; t += 64 * NW) {
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, wm[w]);
+    float num = 0.0f, den = 0.0f;
+    if (M != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        const float f = exp2f(wm[w] - M);
+        num += wacc[w * D + t] * f;
+        den += wl[w] * f;
+      }
+    }
+    acc_out[pidx * D + t] = num;
+    if (t == 0) {
+      m_out[pidx] = M;
+      l_out[pidx] = den;
+    }
+  }
+}
+
+}  // namespace lemoq_attn

@@ -22,7 +22,7 @@
 // (src/lemoq/kernels/_attn_triton.py:102-165), the KV write
 // (src/lemoq/kernels/kv_int8.py:196-216), _rope_one_kernel
 // (src/lemoq/kernels/rope.py:101-123) and the HF q_norm/k_norm RMSNorm.
-#include "common.h"
+#include "attn_common.h"
 
 namespace {
 
@@ -48,119 +48,36 @@ struct AttnSplitArgs {
   float* acc_out;  // (heads, ns, D)
 };
 
-// Sum over aligned groups of G lanes (G in {4, 8, 16}) with DPP row ops.
-template <int G>
-__device__ __forceinline__ float group_sum_dpp(float v) {
-  v += dpp_f<LEMOQ_DPP_QUAD_1032>(v);
-  v += dpp_f<LEMOQ_DPP_QUAD_2301>(v);
-  if (G >= 8) v += dpp_f<LEMOQ_DPP_ROW_HALF_MIRROR>(v);
-  if (G >= 16) v += dpp_f<LEMOQ_DPP_ROW_MIRROR>(v);
-  return v;
-}
-
 template <int D, int NW_ = 8, int U_ = 4>
 struct HeadShape {
-  static constexpr int LPT = D / 16;    // lanes per cached token row (16 codes per lane)
-  static constexpr int TPW = 64 / LPT;  // tokens per wave load
-  static constexpr int U = U_;          // wave loads per token block
-  static constexpr int BLK = TPW * U;   // tokens per wave token block
+  using T = lemoq_attn::TokShape<D, true, U_>;  // KV-INT8 token rows
+  static constexpr int LPT = T::LPT;    // lanes per cached token row (16 codes per lane)
+  static constexpr int BLK = T::BLK;    // tokens per wave token block
   static constexpr int NW = NW_;        // waves per block
   static constexpr int EPL = D / 64;    // prologue elements per lane
-  static_assert(LPT == 4 || LPT == 8 || LPT == 16, "head_dim must be 64, 128 or 256");
   static_assert(NW >= 3, "waves 0..2 carry the q and new k/v prologue");
 };
-
-template <class S>
-struct TokBlock {
-  u32x4 k[S::U], v[S::U];
-  uint16_t ks[S::U], vs[S::U];
-};
-
-// Loads of the token block at `base` (token base + u*TPW + tl for slice u);
-// slots at or beyond `lim` are clamped to lim - 1 (a valid slot) and masked
-// when folded.
-template <int D, class S>
-__device__ __forceinline__ void issue_tokens(TokBlock<S>& b, const int8_t* __restrict__ kb,
-                                             const int8_t* __restrict__ vb,
-                                             const uint16_t* __restrict__ ksh,
-                                             const uint16_t* __restrict__ vsh, int64_t base,
-                                             int64_t lim, int tl, int dl) {
-#pragma unroll
-  for (int u = 0; u < S::U; ++u) {
-    int64_t t = base + u * S::TPW + tl;
-    t = t < lim ? t : lim - 1;
-    b.k[u] = load_stream16(kb + t * D + dl * 16);
-    b.v[u] = load_stream16(vb + t * D + dl * 16);
-    b.ks[u] = ksh[t];
-    b.vs[u] = vsh[t];
-  }
-}
-
-struct SoftmaxState {
-  float m, l;
-  float acc[16];
-};
-
-// Online-softmax update with the token block at `base`; slices at or beyond
-// `n` are masked.  The running max is wave-uniform.
-template <class S>
-__device__ __forceinline__ void fold_tokens(SoftmaxState& st, const TokBlock<S>& b, const XChunk& qx,
-                                            int64_t base, int64_t n, int tl, float qk_scale) {
-  float sc[S::U];
-  bool valid[S::U];
-#pragma unroll
-  for (int u = 0; u < S::U; ++u) {
-    const int64_t t = base + u * S::TPW + tl;
-    valid[u] = t < n;
-    const float d = group_sum_dpp<S::LPT>(dot16_i8(b.k[u], qx, 0.0f));
-    sc[u] = valid[u] ? (d * qk_scale) * h2f(b.ks[u]) : -INFINITY;
-  }
-  float mx = sc[0];
-#pragma unroll
-  for (int u = 1; u < S::U; ++u) mx = fmaxf(mx, sc[u]);
-  mx = wave_max(mx);
-  const float m_new = fmaxf(st.m, mx);
-  if (m_new == -INFINITY) return;  // no valid token in this block (wave-uniform)
-  const float alpha = exp2f(st.m - m_new);
-  st.l *= alpha;
-#pragma unroll
-  for (int e = 0; e < 16; ++e) st.acc[e] *= alpha;
-#pragma unroll
-  for (int u = 0; u < S::U; ++u) {
-    const float p = exp2f(sc[u] - m_new);  // 0 for masked slices (sc = -inf)
-    st.l += p;
-    // a masked slice may hold anything (clamped slot): select, never multiply,
-    // so a NaN scale there cannot reach acc
-    const float pw = valid[u] ? p * h2f(b.vs[u]) : 0.0f;
-    const uint32_t w[4] = {b.v[u].x, b.v[u].y, b.v[u].z, b.v[u].w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        st.acc[4 * i + q] = fmaf(pw, (float)(int8_t)((w[i] >> (8 * q)) & 0xFFu), st.acc[4 * i + q]);
-  }
-  st.m = m_new;
-}
 
 template <int D, int NW_ = 8, int U_ = 4>
 __global__ __launch_bounds__(64 * NW_) void attn_split_fused_i8_kernel(const AttnSplitArgs a) {
   using S = HeadShape<D, NW_, U_>;
-  constexpr int LPT = S::LPT, BLK = S::BLK, NW = S::NW, EPL = S::EPL;
+  using T = typename S::T;
+  constexpr int BLK = S::BLK, NW = S::NW, EPL = S::EPL;
   constexpr int STRIDE = NW * BLK;
   __shared__ __align__(16) uint16_t q_s[D];
   __shared__ __align__(16) int8_t knew_s[D];
   __shared__ __align__(16) int8_t vnew_s[D];
   __shared__ float kvs_s[2];
   __shared__ float wm[NW], wl[NW];
-  __shared__ float wacc[NW][D];
+  __shared__ float wacc[NW * D];
 
   const int sp = blockIdx.x, h = blockIdx.y;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int dl = lane % LPT, tl = lane / LPT;
+  const int dl = lane % T::LPT, tl = lane / T::LPT;
   const int HD = a.heads * D;
   const int64_t cap = a.s_len;
-  const int8_t* kb = a.kc + (int64_t)h * a.code_head_stride;
-  const int8_t* vb = a.vc + (int64_t)h * a.code_head_stride;
+  const uint8_t* kb = reinterpret_cast<const uint8_t*>(a.kc + (int64_t)h * a.code_head_stride);
+  const uint8_t* vb = reinterpret_cast<const uint8_t*>(a.vc + (int64_t)h * a.code_head_stride);
   const uint16_t* ksh = a.ks + (int64_t)h * cap;
   const uint16_t* vsh = a.vs + (int64_t)h * cap;
 
@@ -177,10 +94,10 @@ __global__ __launch_bounds__(64 * NW_) void attn_split_fused_i8_kernel(const Att
   // [0, max(cend, 1)), folds masked by cend): a load under a branch lets the
   // compiler unpack its bytes right after the issue, which waits on it before
   // the prologue below could overlap it.
-  TokBlock<S> ta, tb;
+  lemoq_attn::TokBlock<T> ta, tb;
   int64_t base = start + (int64_t)wave * BLK;
   const int64_t lim = cend > 0 ? cend : 1;
-  issue_tokens<D, S>(ta, kb, vb, ksh, vsh, base, lim, tl, dl);
+  lemoq_attn::issue_tokens<T>(ta, kb, vb, ksh, vsh, base, lim, tl, dl, D);
 
   if (wave == 0 || (owns_new && wave < 3)) {
     // Prologue: wave 0 -> q (every block), wave 1 -> new k (normed, rotated,
@@ -266,78 +183,42 @@ __global__ __launch_bounds__(64 * NW_) void attn_split_fused_i8_kernel(const Att
   }
   __syncthreads();
 
-  XChunk qx;
-  load_xchunk(q_s + dl * 16, qx);
-  SoftmaxState st;
-  st.m = -INFINITY;
-  st.l = 0.0f;
-#pragma unroll
-  for (int e = 0; e < 16; ++e) st.acc[e] = 0.0f;
+  lemoq_attn::QSlice<true> qx;
+  load_xchunk(q_s + dl * 16, qx.x);
+  lemoq_attn::SoftmaxState<T::EPL> st;
+  lemoq_attn::softmax_init(st);
 
   // Two token blocks in flight: fold one while the next one loads.  The
   // next block is issued unconditionally (clamped; at the end it re-reads
   // the split's last slot, an L2 hit) for the reason given above.
   while (base < cend) {
     int64_t nb = base + STRIDE;
-    issue_tokens<D, S>(tb, kb, vb, ksh, vsh, nb, lim, tl, dl);
+    lemoq_attn::issue_tokens<T>(tb, kb, vb, ksh, vsh, nb, lim, tl, dl, D);
     LEMOQ_LOADS_ISSUED();
-    fold_tokens<S>(st, ta, qx, base, cend, tl, a.qk_scale);
+    lemoq_attn::fold_tokens<T>(st, ta, qx, base, cend, tl, lane, a.qk_scale);
     base = nb;
     if (base >= cend) break;
     nb = base + STRIDE;
-    issue_tokens<D, S>(ta, kb, vb, ksh, vsh, nb, lim, tl, dl);
+    lemoq_attn::issue_tokens<T>(ta, kb, vb, ksh, vsh, nb, lim, tl, dl, D);
     LEMOQ_LOADS_ISSUED();
-    fold_tokens<S>(st, tb, qx, base, cend, tl, a.qk_scale);
+    lemoq_attn::fold_tokens<T>(st, tb, qx, base, cend, tl, lane, a.qk_scale);
     base = nb;
   }
   if (wave == NW - 1 && owns_new) {
     // The new token at slot pos, from LDS: only slice (u = 0, tl = 0) is
     // valid.  The last wave holds the fewest cached tokens of the split.
-    TokBlock<S> nbk;
+    lemoq_attn::TokBlock<T> nbk;
 #pragma unroll
-    for (int u = 0; u < S::U; ++u) {
+    for (int u = 0; u < T::U; ++u) {
       nbk.k[u] = *reinterpret_cast<const u32x4*>(knew_s + dl * 16);
       nbk.v[u] = *reinterpret_cast<const u32x4*>(vnew_s + dl * 16);
       nbk.ks[u] = f2h(kvs_s[0]);
       nbk.vs[u] = f2h(kvs_s[1]);
     }
-    fold_tokens<S>(st, nbk, qx, 0, 1, tl, a.qk_scale);
+    lemoq_attn::fold_tokens<T>(st, nbk, qx, 0, 1, tl, lane, a.qk_scale);
   }
-
-  // Sum the token groups of the wave (lanes with the same slice dl); the
-  // running max is wave-uniform, so no rescale is needed.
-  st.l = group_total<LPT>(st.l, lane);
-#pragma unroll
-  for (int e = 0; e < 16; ++e) st.acc[e] = group_total<LPT>(st.acc[e], lane);
-  if (lane == 0) {
-    wm[wave] = st.m;
-    wl[wave] = st.l;
-  }
-  if (tl == 0) {
-#pragma unroll
-    for (int e = 0; e < 16; ++e) wacc[wave][dl * 16 + e] = st.acc[e];
-  }
-  __syncthreads();
-  const int64_t pidx = (int64_t)h * a.ns + sp;
-  for (int t = threadIdx.x; t < D; t += 64 * NW) {
-    float M = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) M = fmaxf(M, wm[w]);
-    float num = 0.0f, den = 0.0f;
-    if (M != -INFINITY) {
-#pragma unroll
-      for (int w = 0; w < NW; ++w) {
-        const float f = exp2f(wm[w] - M);
-        num += wacc[w][t] * f;
-        den += wl[w] * f;
-      }
-    }
-    a.acc_out[pidx * D + t] = num;
-    if (t == 0) {
-      a.m_out[pidx] = M;  // -inf for an empty split (l = 0, acc = 0)
-      a.l_out[pidx] = den;
-    }
-  }
+  lemoq_attn::finish_split<T, NW, D>(st, wm, wl, wacc, lane, wave, tl, dl,
+                                     (int64_t)h * a.ns + sp, a.m_out, a.l_out, a.acc_out);
 }
 
 }  // namespace

@@ -83,3 +83,19 @@ def apply_rotary_pos_emb_fused(
             _hip.ptr(out), int(out.stride(1)), int(out.stride(3)), st,
         )
     return qo, ko
+
+
+def warm(*, heads: int = 16, kv_heads: int = 4, head_dim: int = 128, device: Any = None) -> None:
+    """One real launch before graph capture (same signature and defaults as the
+    reference's ``rope.warm``, src/lemoq/kernels/rope.py:206): loads the HIP
+    library and runs ``apply_rotary_pos_emb_fused`` on (1, heads, 1, head_dim) q
+    and (1, kv_heads, 1, head_dim) k with (1, 1, head_dim) cos/sin, then syncs."""
+    import torch  # noqa: PLC0415
+
+    dev = device if device is not None else torch.device("cuda")
+    q = torch.randn(1, heads, 1, head_dim, dtype=torch.float16, device=dev)
+    k = torch.randn(1, kv_heads, 1, head_dim, dtype=torch.float16, device=dev)
+    cos = torch.randn(1, 1, head_dim, dtype=torch.float16, device=dev)
+    sin = torch.randn(1, 1, head_dim, dtype=torch.float16, device=dev)
+    apply_rotary_pos_emb_fused(q, k, cos, sin)
+    torch.cuda.synchronize(dev)

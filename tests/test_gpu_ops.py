@@ -532,3 +532,17 @@ def test_attn_merge_vs_oracle(ns, D, dev):
     got = out.cpu().reshape(heads, D)
     assert torch.isfinite(got).all() and (got[2] == 0).all()
     assert_close(got, ref, what="merge ns=%d D=%d" % (ns, D))
+
+
+def test_warm_entry_points_run_before_capture(dev):
+    """The reference's warm() hooks (one real launch, then sync) exist with the
+    same signatures and run on the device."""
+    from lemoq.kernels import attn_decode, dequant_gemm, rmsnorm, rope
+
+    rope.warm(device=dev)
+    rope.warm(heads=16, kv_heads=16, head_dim=128, device=dev)
+    x = randn(1, 2048, seed=70).to(torch.float16).to(dev)
+    rmsnorm.warm(x, torch.ones(2048, dtype=torch.float16, device=dev), 1e-5)
+    codes, scale = _q8(randn(256, 2048, seed=71, std=0.02), 128)
+    dequant_gemm.warm(x, codes.to(dev), scale.to(dev), None, group_size=128, bits=8)
+    attn_decode.warm(heads=16, head_dim=128, kv_len=512, device=dev)
