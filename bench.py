@@ -83,7 +83,7 @@ class Flusher:
         self.buf = torch.empty((nbytes,), dtype=torch.uint8, device=dev)
         self.buf.fill_(1)
         self.nbytes = nbytes
-        self.blocks = 8192
+        self.blocks = max(1, min(65536, nbytes // 16384))  # 16 KB shares: one 4 KB chunk per wave
         self.out = torch.empty((self.blocks,), dtype=torch.int32, device=dev)
 
     def flush(self) -> None:

@@ -405,10 +405,14 @@ int lemoq_olmoe_decode_step(const LemoqOlmoeStep* step, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Measurement: read n_bytes (multiple of 16, 16-byte aligned) once with
- * nontemporal 16-byte loads over `blocks` 256-thread blocks; block b writes a
- * fold of what it read to out[b].  The roofline denominator (measured read
- * bandwidth) and the cache flush before cold kernel timings.  Restates the
- * method of the reference's read probe (tools/probe_machine.py:392-505).
+ * nontemporal 16-byte loads.  The buffer is cut into contiguous shares of
+ * per = ceil(n_bytes / blocks) bytes rounded up to 4 KB; block b (one per
+ * non-empty share, at most `blocks`) reads share b in 4 KB wave chunks and
+ * writes a fold of what it read to out[b] (out holds `blocks` entries; those
+ * past the last non-empty share are left untouched).  The roofline
+ * denominator (measured read bandwidth) and the cache flush before cold kernel
+ * timings.  Restates the method of the reference's read probe
+ * (tools/probe_machine.py:392-505).
  * ------------------------------------------------------------------------- */
 int lemoq_read_probe(const void* src, int64_t n_bytes, uint32_t* out, int64_t blocks,
                      void* stream);

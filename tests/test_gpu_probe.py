@@ -34,7 +34,7 @@ def test_copy_probe_rejects_overlap_and_misalignment(dev):
         _hip.call("lemoq_copy_probe", _hip.ptr(buf) + 8, _hip.ptr(buf) + 2048, 1024, 4, _hip.stream_of(dev))
 
 
-@pytest.mark.parametrize("n16,blocks", [(1, 1), (1000, 2), (70001, 16)])
+@pytest.mark.parametrize("n16,blocks", [(1, 1), (1000, 2), (70001, 16), (300, 4), (65536, 16)])
 def test_read_probe_folds_every_element(n16, blocks, dev):
     from lemoq import _hip
 
@@ -44,12 +44,14 @@ def test_read_probe_folds_every_element(n16, blocks, dev):
     out = torch.zeros((blocks,), dtype=torch.int32, device=dev)
     _hip.call("lemoq_read_probe", _hip.ptr(src), n16 * 16, _hip.ptr(out), blocks, _hip.stream_of(dev))
     torch.cuda.synchronize()
-    # element i is read by block (i mod (blocks*256)) // 256; a block folds the
-    # 32-bit word sums of its elements with xor
+    # contiguous shares of per16 elements (ceil(n16 / blocks) rounded up to 256);
+    # a block folds the 32-bit word sums of its share with xor; blocks past the
+    # last non-empty share are not launched (their entries stay 0)
+    per16 = -(-n16 // blocks)
+    per16 = -(-per16 // 256) * 256
     sums = words.astype(np.uint64).sum(axis=1).astype(np.uint32)
-    owner = (np.arange(n16) % (blocks * 256)) // 256
     want = np.zeros((blocks,), dtype=np.uint32)
     for b in range(blocks):
-        s = sums[owner == b]
+        s = sums[b * per16: (b + 1) * per16]
         want[b] = np.bitwise_xor.reduce(s) if s.size else 0
     assert np.array_equal(out.cpu().numpy().view(np.uint32), want)
