@@ -404,6 +404,107 @@ typedef struct LemoqOlmoeStep {
 int lemoq_olmoe_decode_step(const LemoqOlmoeStep* step, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * Prefill (several tokens per call) — batched GEMMs on the matrix cores.
+ *
+ * w8 linear over M rows with the numerics of the reference's multi-token
+ * QuantLinear arm ("separate": dequantised fp16 weight, then F.linear;
+ * src/lemoq/quant/linear.py:365-395,471-480, chosen for every input with more
+ * than one token, :431-434): w = fp16(code * scale), fp32 accumulation,
+ * y = fp16(x @ w^T); with residual != NULL, y = fp16(y + residual) (torch's
+ * fp16 add).  x row m is row x_rows[m] of x when x_rows != NULL.
+ *   x (rows, x_ld) fp16; codes (N, K) int8; scale (N, K/group) fp16;
+ *   y (M, y_ld) fp16; residual (M, residual_ld) fp16 (may alias y).
+ *   K % 32 == 0, group % 32 == 0, K % group == 0, x_ld % 8 == 0, x and codes
+ *   16-byte aligned.
+ * ------------------------------------------------------------------------- */
+int lemoq_gemm_w8(const uint16_t* x, int64_t M, int64_t K, int64_t x_ld, const int32_t* x_rows,
+                  const int8_t* codes, const uint16_t* scale, int64_t N, int64_t group,
+                  uint16_t* y, int64_t y_ld, const uint16_t* residual, int64_t residual_ld,
+                  void* stream);
+
+/* fp16 linear over M rows, y = fp16(x @ w^T) with fp32 accumulation: the
+ * router's F.linear for several tokens (src/lemoq/kernels/moe_static.py:267).
+ *   w (N, K) fp16; same shape rules as lemoq_gemm_w8. */
+int lemoq_gemm_f16(const uint16_t* x, int64_t M, int64_t K, int64_t x_ld, const uint16_t* w,
+                   int64_t N, uint16_t* y, int64_t y_ld, void* stream);
+
+/* Embedding lookup of several tokens (HF embed_tokens on the prompt):
+ * dst[r] = src[ids[r]] for r < rows, a zero row for an id outside
+ * [0, n_rows).  src (n_rows, H) fp16, dst (rows, H); H % 8 == 0, 16-byte
+ * aligned. */
+int lemoq_gather_rows(const uint16_t* src, int64_t n_rows, int64_t H, const int64_t* ids, int64_t rows,
+                      uint16_t* dst, void* stream);
+
+/* Attention prologue of several prompt rows: lemoq_qk_norm_rope_kv_i8 per row
+ * r of qkv (rows, 3*heads*D) at position pos0 + r, with the RoPE rounding of
+ * HF's apply_rotary_pos_emb (fp16(fp16(x*cos) + fp16(rotate_half(x)*sin))),
+ * which the reference's multi-token path uses (the fused RoPE guard takes
+ * q_len == 1 only, src/lemoq/kernels/rope.py:140-177).  q_out (rows, heads,
+ * D); KV-INT8 rows into slots pos0 .. pos0+rows-1 (the values
+ * kv_int8_bulk_quantize, src/lemoq/kernels/kv_int8.py:127-162, gives for the
+ * fp16 cache rows); k_f16/v_f16 (nullable) fp16 copies at
+ * h*f16_head_stride + pos*D for the prefill attention.  pos0 + rows <= s_len;
+ * cos_tab/sin_tab hold s_len rows. */
+int lemoq_qk_norm_rope_kv_i8_rows(const uint16_t* qkv, int64_t rows, int64_t heads,
+                                  int64_t head_dim, const uint16_t* q_norm_w,
+                                  const uint16_t* k_norm_w, float eps, const uint16_t* cos_tab,
+                                  const uint16_t* sin_tab, int64_t pos0, uint16_t* q_out,
+                                  int8_t* kc, uint16_t* ks, int8_t* vc, uint16_t* vs,
+                                  int64_t code_head_stride, int64_t s_len, uint16_t* k_f16,
+                                  uint16_t* v_f16, int64_t f16_head_stride, void* stream);
+
+/* Causal attention over T prompt rows (HF OlmoeAttention with sdpa, the
+ * reference's multi-token path, src/lemoq/kernels/attn_decode.py:836-1017):
+ * out[t, h, :] = softmax over keys j <= t of (q_t . k_j) * scale, times v_j;
+ * qk_scale = scale * log2(e); fp32 statistics, fp16 out.
+ *   q (T, q_ld) with head h at column h*D; k, v (heads, kv_head_stride) with
+ *   key j of head h at h*kv_head_stride + j*D; out (T, out_ld).
+ *   D in {64, 128, 256}; q, k, v 16-byte aligned, out 8-byte aligned. */
+int lemoq_attn_prefill_f16(const uint16_t* q, int64_t q_ld, const uint16_t* k, const uint16_t* v,
+                           int64_t kv_head_stride, int64_t T, int64_t heads, int64_t head_dim,
+                           float qk_scale, uint16_t* out, int64_t out_ld, void* stream);
+
+/* MoE block of several tokens (replaces _prefill_forward,
+ * src/lemoq/kernels/moe_static.py:329-371, for quantized experts: each
+ * expert's weights read once for all of its tokens).
+ * Tile table size for `pairs` = T*top_k (token, slot) pairs and E experts. */
+int64_t lemoq_moe_prefill_max_tiles(int64_t pairs, int64_t E);
+
+/* Stable sort of the pairs by expert: pair_tok/pair_src/pair_w (T*top_k)
+ * hold, in expert order and token order within an expert, the token, the
+ * pair index token*top_k + slot and fp16(top_w); expert_off (E+1) the run
+ * starts; tiles (max_tiles, 4) int32 rows (expert, begin, end, 0) of at most
+ * 128 pairs, unused rows with expert -1.  top_i (T, top_k) int64 in [0, E),
+ * top_w (T, top_k) fp32 (lemoq_route_topk's outputs).  E <= 255,
+ * top_k <= 8, T*top_k <= 32768. */
+int lemoq_moe_prefill_sort(const int64_t* top_i, const float* top_w, int64_t T, int64_t top_k,
+                           int64_t E, int32_t* pair_tok, int32_t* pair_src, uint16_t* pair_w,
+                           int32_t* expert_off, int32_t* tiles, int64_t max_tiles, void* stream);
+
+/* act (pairs, F) = fp16(fp16(silu(g)) * u), g and u the fp16 outputs of
+ * x[pair_tok] @ w^T for the expert's gate rows [0, F) and up rows [F, 2F)
+ * (w8, w = fp16(code * scale)).  x (T, H) fp16; gu_codes (E, 2F, H) int8;
+ * gu_scale (E, 2F, H/group) fp16.  H, F, group multiples of 32. */
+int lemoq_moe_prefill_gate_up(const uint16_t* x, int64_t H, const int32_t* pair_tok,
+                              const int32_t* tiles, int64_t max_tiles, const int8_t* gu_codes,
+                              const uint16_t* gu_scale, int64_t F, int64_t group, uint16_t* act,
+                              void* stream);
+
+/* y[pair_src] (H) = fp16(fp16(act @ w_down^T) * pair_w) for each sorted pair.
+ * dn_codes (E, H, F) int8; dn_scale (E, H, F/group) fp16; y (T*top_k, H). */
+int lemoq_moe_prefill_down(const uint16_t* act, int64_t F, const int32_t* pair_src,
+                           const uint16_t* pair_w, const int32_t* tiles, int64_t max_tiles,
+                           const int8_t* dn_codes, const uint16_t* dn_scale, int64_t H,
+                           int64_t group, uint16_t* y, void* stream);
+
+/* out[t] = fp16(residual[t] + s), s the fp16 running sum (from 0) of the
+ * token's y rows in ascending expert order (the order the reference's expert
+ * loop index_adds them); residual nullable (then out = s), may alias out.
+ * H % 8 == 0; y, out, residual 16-byte aligned. */
+int lemoq_moe_prefill_combine(const uint16_t* y, const int64_t* top_i, int64_t T, int64_t top_k,
+                              int64_t H, const uint16_t* residual, uint16_t* out, void* stream);
+
+/* ---------------------------------------------------------------------------
  * Measurement: read n_bytes (multiple of 16, 16-byte aligned) once with
  * nontemporal 16-byte loads.  The buffer is cut into contiguous shares of
  * per = ceil(n_bytes / blocks) bytes rounded up to 4 KB; block b (one per

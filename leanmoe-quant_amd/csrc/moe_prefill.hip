@@ -1,0 +1,353 @@
+// MoE block for several tokens (prefill) on the matrix cores.
+//
+// The reference's multi-token MoE (_prefill_forward,
+// src/lemoq/kernels/moe_static.py:329-371) loops over experts: for expert e it
+// gathers the tokens routed to it (nonzero of top_i == e, token order), runs
+// gu = x_e @ dequant(gate_up_e)^T and y = (silu(gate) * up) @ dequant(down_e)^T
+// as fp16 F.linear calls, and index_adds y * w into a zero fp16 output, one
+// expert after the other.  Here each expert's weights are read once by a
+// grouped GEMM over all of its tokens, in four launches:
+//
+//  1. moe_sort: stable counting sort of the (token, slot) pairs by expert
+//     (pairs of one expert stay in token order), the pairs' fp16 routing
+//     weights (top_w.to(fp16), moe_static.py:281-283), and a table of
+//     128-row tiles, each inside one expert's run of pairs.
+//  2. moe_gate_up: act = fp16(fp16(silu(g)) * u) with g, u the fp16 outputs of
+//     the gate and up rows (the reference's gu.chunk, act_fn(gate) * up);
+//     gate and up columns n sit in the same lane, so the product is formed in
+//     the GEMM epilogue.
+//  3. moe_down: y = fp16(act @ w_down^T), then fp16(y * w) (the `y * w` of
+//     the index_add), written to row token*top_k + slot.
+//  4. moe_combine: out = 0; out = fp16(out + y_slot) over the token's slots
+//     in ascending expert order (the order of the expert loop; a token meets
+//     each expert at most once, so index_add_ adds one term per expert), then
+//     fp16(residual + out) (HF's decoder-layer residual add).
+//
+// The weights dequantise to fp16(code * scale) as the reference's prefill
+// does (dequant_*_expert(e, dtype=x.dtype), moe_grouped_quant.py:173-188).
+#include "gemm_core.h"
+
+namespace {
+
+using namespace lemoq_gemm;
+
+constexpr int TILE_ROWS = 128;    // rows of a tile (2 waves of 64 along M)
+constexpr int MAX_PAIRS = 32768;  // T * top_k held as bytes in LDS by moe_sort
+constexpr int MAX_EXPERTS = 255;  // expert ids are bytes; 255 marks an invalid id
+
+// ---------------------------------------------------------------------------
+// 1. sort.  One block per expert; each block builds the full histogram (the
+// ids are staged in LDS as bytes), derives its expert's pair offset and tile
+// offset, writes its tiles, and places its pairs: each thread owns a
+// contiguous run of pairs, counts its matches, and an exclusive scan over the
+// threads gives the stable positions.  Block 0 writes expert_off and marks the
+// unused tail of the tile table (expert -1).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void moe_sort_kernel(const int64_t* __restrict__ top_i,
+                                                       const float* __restrict__ top_w, int P,
+                                                       int top_k, int E, int32_t* __restrict__ pair_tok,
+                                                       int32_t* __restrict__ pair_src,
+                                                       uint16_t* __restrict__ pair_w,
+                                                       int32_t* __restrict__ expert_off,
+                                                       int32_t* __restrict__ tiles, int max_tiles) {
+  __shared__ uint8_t ids[MAX_PAIRS];
+  __shared__ int hist[256];
+  __shared__ int wave_tot[4];
+  __shared__ int s_off, s_toff;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int me = blockIdx.x;
+  for (int i = tid; i < 256; i += 256) hist[i] = 0;
+  __syncthreads();
+  for (int p = tid; p < P; p += 256) {
+    const int64_t e = top_i[p];
+    const bool ok = e >= 0 && e < E;
+    ids[p] = ok ? (uint8_t)e : (uint8_t)255;
+    if (ok) atomicAdd(&hist[(int)e], 1);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int off = 0, toff = 0;
+    for (int e = 0; e < me; ++e) {
+      off += hist[e];
+      toff += (hist[e] + TILE_ROWS - 1) / TILE_ROWS;
+    }
+    s_off = off;
+    s_toff = toff;
+    if (me == 0) {
+      int o = 0, t = 0;
+      for (int e = 0; e < E; ++e) {
+        expert_off[e] = o;
+        o += hist[e];
+        t += (hist[e] + TILE_ROWS - 1) / TILE_ROWS;
+      }
+      expert_off[E] = o;
+      for (int i = t; i < max_tiles; ++i) tiles[4 * i] = -1;
+    }
+  }
+  __syncthreads();
+  const int cnt = hist[me], off = s_off;
+  const int ntiles = (cnt + TILE_ROWS - 1) / TILE_ROWS;
+  for (int i = tid; i < ntiles; i += 256) {
+    int32_t* t = tiles + 4 * (s_toff + i);
+    t[0] = me;
+    t[1] = off + i * TILE_ROWS;
+    t[2] = off + min(cnt, (i + 1) * TILE_ROWS);
+    t[3] = 0;
+  }
+  const int chunk = (P + 255) / 256;
+  const int beg = min(P, tid * chunk), end = min(P, beg + chunk);
+  int c = 0;
+  for (int p = beg; p < end; ++p) c += ids[p] == me;
+  // exclusive scan of c over the block: wave prefix, then wave totals
+  int incl = c;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int t = __shfl_up(incl, d, 64);
+    if (lane >= d) incl += t;
+  }
+  if (lane == 63) wave_tot[wave] = incl;
+  __syncthreads();
+  int pos = off + incl - c;
+  for (int w = 0; w < wave; ++w) pos += wave_tot[w];
+  for (int p = beg; p < end; ++p) {
+    if (ids[p] != me) continue;
+    pair_tok[pos] = p / top_k;
+    pair_src[pos] = p;
+    pair_w[pos] = f2h(top_w[p]);
+    ++pos;
+  }
+}
+
+struct GroupedArgs {
+  const uint16_t* x;        // gate_up: hidden rows (T, H); down: act rows (P, F)
+  const int32_t* pair_tok;  // gate_up: token of each sorted pair
+  const int32_t* pair_src;  // down: output row of each sorted pair
+  const uint16_t* pair_w;   // down: fp16 routing weight of each sorted pair
+  const int32_t* tiles;     // (max_tiles, 4): expert, row begin, row end, 0
+  const int8_t* codes;      // (E, rows_per_expert, K)
+  const uint16_t* scale;    // (E, rows_per_expert, K / group)
+  int64_t K;                // reduction width (H for gate_up, F for down)
+  int64_t N;                // output columns (F for gate_up, H for down)
+  int group;
+  uint16_t* y;              // gate_up: act (P, F); down: (T * top_k, H)
+};
+
+// 2. gate_up: wave tile 64 pairs x 64 act columns (fragments 0,1 gate rows,
+// 2,3 the matching up rows), block 2 x 2 waves.
+__global__ __launch_bounds__(256) void moe_gate_up_kernel(const GroupedArgs a) {
+  constexpr int FM = 2, FN = 4, NH = FN / 2;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int half = lane >> 5, l32 = lane & 31;
+  const int32_t* tl = a.tiles + 4 * (int64_t)blockIdx.y;
+  const int e = tl[0];
+  if (e < 0) return;
+  const int64_t rs = tl[1], re = tl[2];
+  const int64_t m0 = rs + 64 * (wave >> 1);
+  const int64_t n0 = ((int64_t)blockIdx.x * 2 + (wave & 1)) * 32 * NH;
+  if (m0 >= re || n0 >= a.N) return;  // wave-uniform
+  const int64_t F = a.N, rows_e = 2 * F;
+  const uint16_t* xr[FM];
+#pragma unroll
+  for (int f = 0; f < FM; ++f) {
+    int64_t m = m0 + 32 * f + l32;
+    m = m < re ? m : re - 1;
+    xr[f] = a.x + (int64_t)a.pair_tok[m] * a.K + 16 * half;
+  }
+  WRow wr[FN];
+  const int64_t ng = a.K / a.group;
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    int64_t n = n0 + 32 * (j % NH) + l32;
+    n = n < F ? n : F - 1;
+    const int64_t row = (int64_t)e * rows_e + (j < NH ? n : F + n);
+    wr[j].codes = a.codes + row * a.K + 16 * half;
+    wr[j].scale = a.scale + row * ng;
+    wr[j].w16 = nullptr;
+  }
+  Acc<FM, FN> acc;
+  acc_zero(acc);
+  mainloop<true>(acc, xr, wr, a.K, a.group);
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < NH; ++j) {
+      const int64_t n = n0 + 32 * j + l32;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t m = m0 + 32 * i + acc_row(r, half);
+        if (m >= re || n >= F) continue;
+        const float g = h2f(f2h(acc.v[i][j][r]));
+        const float u = h2f(f2h(acc.v[i][j + NH][r]));
+        const float sg = h2f(f2h(g / (1.0f + expf(-g))));
+        a.y[m * F + n] = f2h(sg * u);
+      }
+    }
+}
+
+// 3. down: wave tile 64 pairs x 64 hidden columns, block 2 x 2 waves.
+__global__ __launch_bounds__(256) void moe_down_kernel(const GroupedArgs a) {
+  constexpr int FM = 2, FN = 2;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int half = lane >> 5, l32 = lane & 31;
+  const int32_t* tl = a.tiles + 4 * (int64_t)blockIdx.y;
+  const int e = tl[0];
+  if (e < 0) return;
+  const int64_t rs = tl[1], re = tl[2];
+  const int64_t m0 = rs + 64 * (wave >> 1);
+  const int64_t n0 = ((int64_t)blockIdx.x * 2 + (wave & 1)) * 64;
+  if (m0 >= re || n0 >= a.N) return;  // wave-uniform
+  const int64_t H = a.N;
+  const uint16_t* xr[FM];
+#pragma unroll
+  for (int f = 0; f < FM; ++f) {
+    int64_t m = m0 + 32 * f + l32;
+    m = m < re ? m : re - 1;
+    xr[f] = a.x + m * a.K + 16 * half;
+  }
+  WRow wr[FN];
+  const int64_t ng = a.K / a.group;
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    int64_t n = n0 + 32 * j + l32;
+    n = n < H ? n : H - 1;
+    const int64_t row = (int64_t)e * H + n;
+    wr[j].codes = a.codes + row * a.K + 16 * half;
+    wr[j].scale = a.scale + row * ng;
+    wr[j].w16 = nullptr;
+  }
+  Acc<FM, FN> acc;
+  acc_zero(acc);
+  mainloop<true>(acc, xr, wr, a.K, a.group);
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int64_t m = m0 + 32 * i + acc_row(r, half);
+      if (m >= re) continue;
+      const float w = h2f(a.pair_w[m]);
+      uint16_t* dst = a.y + (int64_t)a.pair_src[m] * H;
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int64_t n = n0 + 32 * j + l32;
+        if (n >= H) continue;
+        dst[n] = f2h(h2f(f2h(acc.v[i][j][r])) * w);
+      }
+    }
+}
+
+// 4. combine: one block per token, 8 columns per thread.
+__global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __restrict__ y,
+                                                          const int64_t* __restrict__ top_i,
+                                                          int top_k, int64_t H,
+                                                          const uint16_t* __restrict__ resid,
+                                                          uint16_t* __restrict__ out) {
+  const int64_t t = blockIdx.x;
+  int64_t ids[8];
+  int order[8];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) ids[s] = s < top_k ? top_i[t * top_k + s] : INT64_MAX;
+  // ascending expert id (slot order among equal ids)
+  bool used[8] = {false, false, false, false, false, false, false, false};
+#pragma unroll
+  for (int o = 0; o < 8; ++o) {
+    int best = -1;
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+      if (s < top_k && !used[s] && (best < 0 || ids[s] < ids[best])) best = s;
+    order[o] = best < 0 ? 0 : best;
+    if (best >= 0) used[best] = true;
+  }
+  for (int64_t c = (int64_t)threadIdx.x * 8; c < H; c += 256 * 8) {
+    float acc[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+    for (int o = 0; o < top_k; ++o) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(y + (t * top_k + order[o]) * H + c);
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc[2 * i] = h2f(f2h(acc[2 * i] + h2f((uint16_t)(w[i] & 0xFFFFu))));
+        acc[2 * i + 1] = h2f(f2h(acc[2 * i + 1] + h2f((uint16_t)(w[i] >> 16))));
+      }
+    }
+    uint32_t o[4];
+    if (resid) {
+      const u32x4 r = *reinterpret_cast<const u32x4*>(resid + t * H + c);
+      const uint32_t rw[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        o[i] = (uint32_t)hadd_round(acc[2 * i], (uint16_t)(rw[i] & 0xFFFFu)) |
+               ((uint32_t)hadd_round(acc[2 * i + 1], (uint16_t)(rw[i] >> 16)) << 16);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        o[i] = (uint32_t)f2h(acc[2 * i]) | ((uint32_t)f2h(acc[2 * i + 1]) << 16);
+    }
+    *reinterpret_cast<u32x4*>(out + t * H + c) = (u32x4){o[0], o[1], o[2], o[3]};
+  }
+}
+
+bool grouped_shape_ok(int64_t K, int64_t N, int64_t group) {
+  return K > 0 && N > 0 && K % 32 == 0 && N % 32 == 0 && group > 0 && group % 32 == 0 && K % group == 0 &&
+         N <= 65535LL * 128;
+}
+
+}  // namespace
+
+extern "C" int64_t lemoq_moe_prefill_max_tiles(int64_t pairs, int64_t E) {
+  return pairs / TILE_ROWS + E;
+}
+
+extern "C" int lemoq_moe_prefill_sort(const int64_t* top_i, const float* top_w, int64_t T, int64_t top_k,
+                                      int64_t E, int32_t* pair_tok, int32_t* pair_src, uint16_t* pair_w,
+                                      int32_t* expert_off, int32_t* tiles, int64_t max_tiles, void* stream) {
+  if (!top_i || !top_w || !pair_tok || !pair_src || !pair_w || !expert_off || !tiles) return LEMOQ_ERR_NULL;
+  if (T <= 0 || top_k <= 0 || top_k > 8 || E <= 0 || E > MAX_EXPERTS || top_k > E) return LEMOQ_ERR_SHAPE;
+  if (T * top_k > MAX_PAIRS) return LEMOQ_ERR_UNSUPPORTED;
+  if (max_tiles < lemoq_moe_prefill_max_tiles(T * top_k, E) || max_tiles > 0x7fffffffLL) return LEMOQ_ERR_SHAPE;
+  hipLaunchKernelGGL(moe_sort_kernel, dim3((unsigned)E), dim3(256), 0, lemoq_stream(stream), top_i, top_w,
+                     (int)(T * top_k), (int)top_k, (int)E, pair_tok, pair_src, pair_w, expert_off, tiles,
+                     (int)max_tiles);
+  LEMOQ_CHECK_LAUNCH();
+}
+
+extern "C" int lemoq_moe_prefill_gate_up(const uint16_t* x, int64_t H, const int32_t* pair_tok,
+                                         const int32_t* tiles, int64_t max_tiles, const int8_t* gu_codes,
+                                         const uint16_t* gu_scale, int64_t F, int64_t group, uint16_t* act,
+                                         void* stream) {
+  if (!x || !pair_tok || !tiles || !gu_codes || !gu_scale || !act) return LEMOQ_ERR_NULL;
+  if (!grouped_shape_ok(H, F, group) || max_tiles <= 0 || max_tiles > 65535) return LEMOQ_ERR_SHAPE;
+  if (!lemoq_aligned16(x) || !lemoq_aligned16(gu_codes)) return LEMOQ_ERR_ALIGN;
+  GroupedArgs a{};
+  a.x = x; a.pair_tok = pair_tok; a.tiles = tiles; a.codes = gu_codes; a.scale = gu_scale;
+  a.K = H; a.N = F; a.group = (int)group; a.y = act;
+  const dim3 grid((unsigned)((F + 127) / 128), (unsigned)max_tiles);
+  hipLaunchKernelGGL(moe_gate_up_kernel, grid, dim3(256), 0, lemoq_stream(stream), a);
+  LEMOQ_CHECK_LAUNCH();
+}
+
+extern "C" int lemoq_moe_prefill_down(const uint16_t* act, int64_t F, const int32_t* pair_src,
+                                      const uint16_t* pair_w, const int32_t* tiles, int64_t max_tiles,
+                                      const int8_t* dn_codes, const uint16_t* dn_scale, int64_t H,
+                                      int64_t group, uint16_t* y, void* stream) {
+  if (!act || !pair_src || !pair_w || !tiles || !dn_codes || !dn_scale || !y) return LEMOQ_ERR_NULL;
+  if (!grouped_shape_ok(F, H, group) || max_tiles <= 0 || max_tiles > 65535) return LEMOQ_ERR_SHAPE;
+  if (!lemoq_aligned16(act) || !lemoq_aligned16(dn_codes)) return LEMOQ_ERR_ALIGN;
+  GroupedArgs a{};
+  a.x = act; a.pair_src = pair_src; a.pair_w = pair_w; a.tiles = tiles; a.codes = dn_codes;
+  a.scale = dn_scale; a.K = F; a.N = H; a.group = (int)group; a.y = y;
+  const dim3 grid((unsigned)((H + 127) / 128), (unsigned)max_tiles);
+  hipLaunchKernelGGL(moe_down_kernel, grid, dim3(256), 0, lemoq_stream(stream), a);
+  LEMOQ_CHECK_LAUNCH();
+}
+
+extern "C" int lemoq_moe_prefill_combine(const uint16_t* y, const int64_t* top_i, int64_t T, int64_t top_k,
+                                         int64_t H, const uint16_t* residual, uint16_t* out, void* stream) {
+  if (!y || !top_i || !out) return LEMOQ_ERR_NULL;
+  if (T <= 0 || T > 0x7fffffffLL || top_k <= 0 || top_k > 8 || H <= 0 || H % 8 != 0) return LEMOQ_ERR_SHAPE;
+  if (!lemoq_aligned16(y) || !lemoq_aligned16(out) || (residual && !lemoq_aligned16(residual)))
+    return LEMOQ_ERR_ALIGN;
+  hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)T), dim3(256), 0, lemoq_stream(stream), y, top_i,
+                     (int)top_k, H, residual, out);
+  LEMOQ_CHECK_LAUNCH();
+}

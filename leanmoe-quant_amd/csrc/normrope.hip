@@ -41,6 +41,23 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict
   }
 }
 
+// Embedding rows of several tokens: dst[r] = src[ids[r]] (a zero row for an
+// id outside [0, n_rows)), 16 bytes per thread.
+__global__ __launch_bounds__(256) void gather_rows_kernel(const uint16_t* __restrict__ src,
+                                                          int64_t n_rows, int64_t H,
+                                                          const int64_t* __restrict__ ids,
+                                                          uint16_t* __restrict__ dst) {
+  const int64_t r = blockIdx.x;
+  const int64_t id = ids[r];
+  const bool ok = id >= 0 && id < n_rows;
+  const uint16_t* s = src + (ok ? id : 0) * H;
+  for (int64_t c = (int64_t)threadIdx.x * 8; c < H; c += 256 * 8) {
+    u32x4 v = *reinterpret_cast<const u32x4*>(s + c);
+    if (!ok) v = (u32x4){0u, 0u, 0u, 0u};
+    *reinterpret_cast<u32x4*>(dst + r * H + c) = v;
+  }
+}
+
 __device__ __forceinline__ float rope_elem(float x, float xs, float c, float s, bool first_half) {
   return first_half ? x * c + (-xs) * s : x * c + xs * s;
 }
@@ -73,11 +90,18 @@ __global__ __launch_bounds__(128) void rope_kernel(const uint16_t* __restrict__ 
 // sits in lane l ^ 32.  k and v heads are quantised to KV-INT8 at slot *pos
 // (amax / 127 scale, round-half-even codes; the arithmetic of
 // src/lemoq/kernels/kv_int8.py:196-216).
-template <int EPL>
+//
+// Several rows (prefill): grid.y indexes the row; row r reads qkv row r,
+// writes q_out row r and cache slot pos0 + r (pos0 = *pos_ptr when pos_ptr is
+// non-NULL).  HF_ROPE selects the rounding of HF's apply_rotary_pos_emb,
+// which the reference's multi-token path takes (the fused RoPE only accepts
+// q_len == 1, src/lemoq/kernels/rope.py:140-177): fp16(fp16(x*cos) +
+// fp16(rotate_half(x)*sin)) instead of one rounding of the fp32 sum.
+template <int EPL, bool HF_ROPE>
 __global__ __launch_bounds__(64) void qk_norm_rope_kv_kernel(
     const uint16_t* __restrict__ qkv, int heads, const uint16_t* __restrict__ qn_w,
     const uint16_t* __restrict__ kn_w, float eps, const uint16_t* __restrict__ cos_tab,
-    const uint16_t* __restrict__ sin_tab, const int64_t* __restrict__ pos_ptr,
+    const uint16_t* __restrict__ sin_tab, const int64_t* __restrict__ pos_ptr, int64_t pos0,
     uint16_t* __restrict__ q_out, int8_t* __restrict__ kc, uint16_t* __restrict__ ks,
     int8_t* __restrict__ vc, uint16_t* __restrict__ vs, int64_t code_head_stride, int64_t s_len,
     uint16_t* __restrict__ k_f16, uint16_t* __restrict__ v_f16, int64_t f16_head_stride,
@@ -87,7 +111,11 @@ __global__ __launch_bounds__(64) void qk_norm_rope_kv_kernel(
   const int which = blockIdx.x / heads;  // 0 q, 1 k, 2 v
   const int h = blockIdx.x - which * heads;
   const int HD = heads * D;
-  const int64_t pos = pos_ptr[0];
+  const int64_t row = blockIdx.y;
+  const int64_t pos = (pos_ptr ? pos_ptr[0] : pos0) + row;
+  qkv += row * 3 * HD;
+  q_out += row * HD;
+  if (k_rot_out) k_rot_out += row * HD;
   const bool pos_ok = pos >= 0 && pos < s_len;
   const uint16_t* src = qkv + (int64_t)which * HD;
   const int d0 = lane * EPL;
@@ -121,7 +149,16 @@ __global__ __launch_bounds__(64) void qk_norm_rope_kv_kernel(
 #pragma unroll
     for (int i = 0; i < EPL; ++i) {
       const float xs = __shfl_xor(xn[i], 32, 64);
-      o[i] = h2f(f2h(first ? xn[i] * cv[i] + (-xs) * sv[i] : xn[i] * cv[i] + xs * sv[i]));
+      const float xr = first ? -xs : xs;
+      if constexpr (HF_ROPE) {
+        // Three roundings; without this pragma the compiler narrows the
+        // products to fp16 multiplies and contracts one of them with the add
+        // into a single-rounding fma.
+#pragma clang fp contract(off)
+        o[i] = h2f(f2h(h2f(f2h(xn[i] * cv[i])) + h2f(f2h(xr * sv[i]))));
+      } else {
+        o[i] = h2f(f2h(xn[i] * cv[i] + xr * sv[i]));
+      }
     }
     if (which == 0) {
 #pragma unroll
@@ -168,6 +205,17 @@ extern "C" int lemoq_rmsnorm(const uint16_t* x, int64_t rows, int64_t hidden, co
   LEMOQ_CHECK_LAUNCH();
 }
 
+extern "C" int lemoq_gather_rows(const uint16_t* src, int64_t n_rows, int64_t H, const int64_t* ids,
+                                 int64_t rows, uint16_t* dst, void* stream) {
+  if (!src || !ids || !dst) return LEMOQ_ERR_NULL;
+  if (n_rows <= 0 || H <= 0 || H % 8 != 0 || rows < 0 || rows > 0x7fffffffLL) return LEMOQ_ERR_SHAPE;
+  if (!lemoq_aligned16(src) || !lemoq_aligned16(dst)) return LEMOQ_ERR_ALIGN;
+  if (rows == 0) return LEMOQ_OK;
+  hipLaunchKernelGGL(gather_rows_kernel, dim3((unsigned)rows), dim3(256), 0, lemoq_stream(stream), src,
+                     n_rows, H, ids, dst);
+  LEMOQ_CHECK_LAUNCH();
+}
+
 extern "C" int lemoq_rope(const uint16_t* x, int64_t x_sh, int64_t x_sd, int64_t heads,
                           int64_t head_dim, const uint16_t* cos, const uint16_t* sin,
                           int64_t cs_sd, uint16_t* out, int64_t o_sh, int64_t o_sd,
@@ -200,14 +248,50 @@ extern "C" int lemoq_qk_norm_rope_kv_i8(const uint16_t* qkv, int64_t heads, int6
   const dim3 grid((unsigned)(3 * heads));
   hipStream_t st = lemoq_stream(stream);
 #define LEMOQ_QK_CASE(EE)                                                                       \
-  hipLaunchKernelGGL((qk_norm_rope_kv_kernel<EE>), grid, dim3(64), 0, st, qkv, (int)heads,      \
-                     q_norm_w, k_norm_w, eps, cos_tab, sin_tab, pos, q_out, kc, ks, vc, vs,    \
-                     code_head_stride, s_len, k_f16, v_f16, f16_head_stride, k_rot_out);
+  hipLaunchKernelGGL((qk_norm_rope_kv_kernel<EE, false>), grid, dim3(64), 0, st, qkv,           \
+                     (int)heads, q_norm_w, k_norm_w, eps, cos_tab, sin_tab, pos, (int64_t)0,   \
+                     q_out, kc, ks, vc, vs, code_head_stride, s_len, k_f16, v_f16,              \
+                     f16_head_stride, k_rot_out);
   switch (head_dim) {
     case 64: LEMOQ_QK_CASE(1) break;
     case 128: LEMOQ_QK_CASE(2) break;
     default: LEMOQ_QK_CASE(4) break;
   }
 #undef LEMOQ_QK_CASE
+  LEMOQ_CHECK_LAUNCH();
+}
+
+extern "C" int lemoq_qk_norm_rope_kv_i8_rows(const uint16_t* qkv, int64_t rows, int64_t heads,
+                                             int64_t head_dim, const uint16_t* q_norm_w,
+                                             const uint16_t* k_norm_w, float eps,
+                                             const uint16_t* cos_tab, const uint16_t* sin_tab,
+                                             int64_t pos0, uint16_t* q_out, int8_t* kc,
+                                             uint16_t* ks, int8_t* vc, uint16_t* vs,
+                                             int64_t code_head_stride, int64_t s_len,
+                                             uint16_t* k_f16, uint16_t* v_f16,
+                                             int64_t f16_head_stride, void* stream) {
+  if (!qkv || !q_norm_w || !k_norm_w || !cos_tab || !sin_tab || !q_out || !kc || !ks || !vc ||
+      !vs)
+    return LEMOQ_ERR_NULL;
+  if (heads <= 0 || heads > 4096 || heads * head_dim > 65536) return LEMOQ_ERR_SHAPE;
+  if (head_dim != 64 && head_dim != 128 && head_dim != 256) return LEMOQ_ERR_UNSUPPORTED;
+  if (!lemoq_aligned16(qkv)) return LEMOQ_ERR_ALIGN;
+  if (s_len <= 0 || code_head_stride < s_len * head_dim) return LEMOQ_ERR_SHAPE;
+  if ((k_f16 || v_f16) && f16_head_stride < s_len * head_dim) return LEMOQ_ERR_SHAPE;
+  // every row's slot must exist: the cos/sin tables and the caches hold s_len positions
+  if (rows <= 0 || rows > 65535 || pos0 < 0 || pos0 + rows > s_len) return LEMOQ_ERR_SHAPE;
+  const dim3 grid((unsigned)(3 * heads), (unsigned)rows);
+  hipStream_t st = lemoq_stream(stream);
+#define LEMOQ_QK_ROWS_CASE(EE)                                                                  \
+  hipLaunchKernelGGL((qk_norm_rope_kv_kernel<EE, true>), grid, dim3(64), 0, st, qkv,            \
+                     (int)heads, q_norm_w, k_norm_w, eps, cos_tab, sin_tab,                     \
+                     (const int64_t*)nullptr, pos0, q_out, kc, ks, vc, vs, code_head_stride,    \
+                     s_len, k_f16, v_f16, f16_head_stride, (uint16_t*)nullptr);
+  switch (head_dim) {
+    case 64: LEMOQ_QK_ROWS_CASE(1) break;
+    case 128: LEMOQ_QK_ROWS_CASE(2) break;
+    default: LEMOQ_QK_ROWS_CASE(4) break;
+  }
+#undef LEMOQ_QK_ROWS_CASE
   LEMOQ_CHECK_LAUNCH();
 }

@@ -168,6 +168,19 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         _I,
         [_P, _P, _P, _P, _I64, _I, _I64, _I64, _I64, _I64, _P, _P, _P, _P],
     ),
+    "lemoq_gemm_w8": (_I, [_P, _I64, _I64, _I64, _P, _P, _P, _I64, _I64, _P, _I64, _P, _I64, _P]),
+    "lemoq_gemm_f16": (_I, [_P, _I64, _I64, _I64, _P, _I64, _P, _I64, _P]),
+    "lemoq_gather_rows": (_I, [_P, _I64, _I64, _P, _I64, _P, _P]),
+    "lemoq_qk_norm_rope_kv_i8_rows": (
+        _I,
+        [_P, _I64, _I64, _I64, _P, _P, _F, _P, _P, _I64, _P, _P, _P, _P, _P, _I64, _I64, _P, _P, _I64, _P],
+    ),
+    "lemoq_attn_prefill_f16": (_I, [_P, _I64, _P, _P, _I64, _I64, _I64, _I64, _F, _P, _I64, _P]),
+    "lemoq_moe_prefill_max_tiles": (_I64, [_I64, _I64]),
+    "lemoq_moe_prefill_sort": (_I, [_P, _P, _I64, _I64, _I64, _P, _P, _P, _P, _P, _I64, _P]),
+    "lemoq_moe_prefill_gate_up": (_I, [_P, _I64, _P, _P, _I64, _P, _P, _I64, _I64, _P, _P]),
+    "lemoq_moe_prefill_down": (_I, [_P, _I64, _P, _P, _P, _I64, _P, _P, _I64, _I64, _P, _P]),
+    "lemoq_moe_prefill_combine": (_I, [_P, _P, _I64, _I64, _I64, _P, _P, _P]),
 }
 
 

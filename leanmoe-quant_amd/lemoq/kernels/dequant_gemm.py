@@ -1,4 +1,6 @@
-"""w8 dense GEMV with in-register dequantisation (``lemoq_gemv_w8``).
+"""w8 dense GEMV with in-register dequantisation (``lemoq_gemv_w8``), and the
+multi-token w8 / fp16 linears on the matrix cores (``lemoq_gemm_w8``,
+``lemoq_gemm_f16``).
 
 Replaces ``dequant_gemm_fused`` of the reference
 (``src/lemoq/kernels/_dequant_triton.py:155-293``) for the branch the decode
@@ -16,7 +18,8 @@ from typing import Any
 
 from lemoq import _hip
 
-__all__ = ["DEQUANT_GEMM_CONFIGS", "dequant_gemm_fused", "fused_available", "warm"]
+__all__ = ["DEQUANT_GEMM_CONFIGS", "dequant_gemm_fused", "dequant_gemm_separate", "linear_f16",
+           "fused_available", "warm"]
 
 # The HIP kernel's tiling is chosen inside the library from N (rows per wave)
 # and K (1 KB chunks per row); no tunables are exposed.  Kept for call-site
@@ -122,3 +125,82 @@ def dequant_gemm_fused(
 def warm(x: Any, qweight: Any, scale: Any, zero: Any = None, **kwargs: Any) -> None:
     """One real launch (kept for call-site compatibility; HIP code needs no JIT)."""
     dequant_gemm_fused(x, qweight, scale, zero, **kwargs)
+
+
+def _check_rows(x: Any, K: int, what: str) -> None:
+    import torch  # noqa: PLC0415
+
+    if x.dim() != 2 or int(x.shape[1]) != K:
+        raise ValueError("%s: x must be (M, %d), got %r" % (what, K, tuple(x.shape)))
+    if x.dtype != torch.float16:
+        raise NotImplementedError("%s: x must be fp16, got %s" % (what, x.dtype))
+    if not x.is_contiguous():
+        raise ValueError("%s: x must be contiguous" % what)
+
+
+def dequant_gemm_separate(
+    x: Any,
+    qweight: Any,
+    scale: Any,
+    zero: Any = None,
+    *,
+    group_size: int,
+    bits: int = 8,
+    symmetric: bool = True,
+    residual: Any = None,
+) -> Any:
+    """``y (M, N) = fp16(x @ fp16(dequant(qweight)).T)`` on the matrix cores.
+
+    The numerics of the reference's multi-token ``QuantLinear`` arm
+    (``dequantized_weight(dtype=fp16)`` then ``F.linear``,
+    ``src/lemoq/quant/linear.py:365-395,471-480``) without materialising the
+    weight: each code is dequantised to ``fp16(code * scale)`` in registers,
+    products accumulate in fp32, the output is rounded to fp16 once.  With
+    ``residual`` (M, N) fp16, ``y = fp16(y + residual)``.  K must equal the
+    padded width (a multiple of 32 and of ``group_size``).
+    """
+    import torch  # noqa: PLC0415
+
+    if bits != 8 or not symmetric or zero is not None:
+        raise NotImplementedError("the HIP build implements the 8-bit symmetric (zero=None) branch only")
+    if qweight.dim() != 2 or qweight.dtype != torch.int8 or not qweight.is_contiguous():
+        raise ValueError("qweight must be contiguous int8 (N, K)")
+    N, K = int(qweight.shape[0]), int(qweight.shape[1])
+    g = int(group_size)
+    if scale.dtype != torch.float16 or tuple(scale.shape) != (N, K // max(g, 1)) or not scale.is_contiguous():
+        raise ValueError("scale must be contiguous fp16 (N, K/group), got %r" % (tuple(scale.shape),))
+    if g <= 0 or g % 32 != 0 or K % g != 0:
+        raise NotImplementedError("the matrix-core GEMM needs group_size % 32 == 0 and K % group_size == 0")
+    _check_rows(x, K, "dequant_gemm_separate")
+    M = int(x.shape[0])
+    y = torch.empty((M, N), dtype=torch.float16, device=x.device)
+    if residual is not None and (tuple(residual.shape) != (M, N) or residual.dtype != torch.float16
+                                 or not residual.is_contiguous()):
+        raise ValueError("residual must be contiguous fp16 (M, N)")
+    _hip.require_rocm(x, qweight, scale, what="dequant_gemm_separate")
+    if M == 0 or N == 0:
+        return y
+    _hip.call("lemoq_gemm_w8", _hip.ptr(x), M, K, K, None, _hip.ptr(qweight), _hip.ptr(scale), N, g,
+              _hip.ptr(y), N, _hip.ptr(residual) if residual is not None else None, N,
+              _hip.stream_of(x.device))
+    return y
+
+
+def linear_f16(x: Any, weight: Any) -> Any:
+    """``fp16(x (M, K) @ weight (N, K).T)`` with fp32 accumulation (``F.linear`` in fp16)."""
+    import torch  # noqa: PLC0415
+
+    if weight.dim() != 2 or weight.dtype != torch.float16 or not weight.is_contiguous():
+        raise ValueError("weight must be contiguous fp16 (N, K)")
+    N, K = int(weight.shape[0]), int(weight.shape[1])
+    if K % 32 != 0:
+        raise NotImplementedError("linear_f16 needs K % 32 == 0, got %d" % K)
+    _check_rows(x, K, "linear_f16")
+    M = int(x.shape[0])
+    y = torch.empty((M, N), dtype=torch.float16, device=x.device)
+    _hip.require_rocm(x, weight, what="linear_f16")
+    if M == 0 or N == 0:
+        return y
+    _hip.call("lemoq_gemm_f16", _hip.ptr(x), M, K, K, _hip.ptr(weight), N, _hip.ptr(y), N,
+              _hip.stream_of(x.device))
+    return y

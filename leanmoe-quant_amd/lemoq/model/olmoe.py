@@ -15,8 +15,9 @@ This replaces the reference's HF-patched model + ``StaticCacheDecodeSession``
   enqueued by one native call (``lemoq_olmoe_decode_step``), captured once
   into a hipGraph (``torch.cuda.CUDAGraph``) and replayed.  Greedy selection
   and the position advance run on the device, so consecutive replays need no
-  host round trip; prompt tokens are fed by the same step (prefill = one
-  replay per prompt position).
+  host round trip.  ``prefill()`` runs the prompt as one batch on the matrix
+  cores (``lemoq.model.prefill``), as the reference's session does; the
+  prompt can also be fed through the step itself (one replay per position).
 
 Layout in HBM (per layer): ``qkv_codes`` (3*heads*D, H) int8 with fp16 scales
 (3*heads*D, H/g); ``o_codes`` (H, heads*D); ``gu_codes`` (E, 2F, H) and
@@ -373,12 +374,34 @@ class DecodeSession:
             torch.cuda.synchronize(self.device)
         return self.logits
 
-    def prefill(self) -> int:
-        """Run the prompt through the step (one replay per position); returns the seed token."""
+    def prefill(self, mode: str = "batched") -> int:
+        """Fill the KV-INT8 cache with the prompt and seed the first decode token; returns it.
+
+        ``mode="batched"`` (default) is the reference's prefill: one multi-token
+        forward (``lemoq.model.prefill.prefill_prompt``, the path of
+        ``StaticCacheDecodeSession.prefill``, ``benchmarks/cudagraph.py:578-599``),
+        then the greedy pick of the last position's logits (``lemoq_argmax_advance``).
+        ``mode="stepped"`` feeds the prompt through the captured decode step, one
+        replay per position (decode numerics for every prompt token).
+        """
         if self.graph is None:
             self.capture()
         self.reset()
-        self.replay(self.ctx)
+        if mode == "stepped":
+            self.replay(self.ctx)
+        elif mode == "batched":
+            from lemoq.model.prefill import prefill_prompt  # noqa: PLC0415
+
+            prefill_prompt(self.weights, self.prompt, self.kv, self.cos_tab, self.sin_tab, self.max_seq,
+                           self.logits)
+            self.history[: self.ctx].copy_(self.prompt)
+            self.pos.fill_(self.ctx - 1)
+            _hip.call("lemoq_argmax_advance", _hip.ptr(self.logits), self.shape.vocab, _hip.ptr(self.token),
+                      _hip.ptr(self.pos), _hip.ptr(self.filled), _hip.ptr(self.prompt), self.ctx,
+                      _hip.ptr(self.history), int(self.history.numel()), _hip.stream_of(self.device))
+            torch.cuda.synchronize(self.device)
+        else:
+            raise ValueError("prefill mode must be 'batched' or 'stepped', got %r" % (mode,))
         return int(self.token.item())
 
     def generated(self) -> list[int]:

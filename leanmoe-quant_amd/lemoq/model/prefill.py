@@ -1,0 +1,125 @@
+"""Batched prompt prefill of the OLMoE W8 model on the matrix cores.
+
+The reference's session prefills the whole prompt with one forward of the
+patched HF model (``StaticCacheDecodeSession.prefill``,
+``benchmarks/cudagraph.py:578-599``).  With more than one token every patched
+operator takes its multi-token branch, and this module runs exactly that path
+with the HIP kernels, one layer at a time:
+
+=====================  ==========================================================
+HF / reference         here (C-ABI entry point)
+=====================  ==========================================================
+embed_tokens           ``lemoq_gather_rows``
+input_layernorm        ``lemoq_rmsnorm`` (the fused RMSNorm, any row count)
+q/k/v_proj             ``lemoq_gemm_w8`` (QuantLinear separate arm, linear.py:471-480)
+q_norm, k_norm, RoPE,  ``lemoq_qk_norm_rope_kv_i8_rows`` (HF RoPE rounding; the
+KV cache + INT8 bulk   KV-INT8 rows are what kv_int8_bulk_quantize gives)
+sdpa causal attention  ``lemoq_attn_prefill_f16``
+o_proj + residual      ``lemoq_gemm_w8`` with the residual in its epilogue
+post_attention norm    ``lemoq_rmsnorm``
+router F.linear        ``lemoq_gemm_f16``; ``lemoq_route_topk``
+_prefill_forward       ``lemoq_moe_prefill_sort`` / ``_gate_up`` / ``_down`` /
+(moe_static.py:329)    ``_combine`` (the combine adds the residual)
+final norm, lm_head    ``lemoq_rmsnorm`` + ``lemoq_gemm_w8`` on the last row
+=====================  ==========================================================
+
+The KV-INT8 cache slots 0..T-1 of every layer are written; the logits of the
+last prompt position land in ``logits``.  All launches go on torch's current
+stream; scratch tensors are allocated per call (prefill is eager, as in the
+reference).
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Any
+
+import torch
+
+from lemoq import _hip
+
+__all__ = ["prefill_prompt", "PREFILL_MAX_PAIRS"]
+
+LOG2E = 1.4426950408889634
+# T * top_k pairs are sorted in one block's LDS (lemoq_moe_prefill_sort).
+PREFILL_MAX_PAIRS = 32768
+
+
+def prefill_prompt(weights: Any, tokens: Any, kv: list, cos_tab: Any, sin_tab: Any, max_seq: int,
+                   logits: Any) -> None:
+    """Prefill ``tokens`` (int64 (T,) on the device) at positions 0..T-1.
+
+    ``kv``: per layer the KV-INT8 cache dict (kc (heads, S, D) int8, ks (heads, S)
+    fp16, vc, vs) with S = ``max_seq``; ``cos_tab``/``sin_tab`` (S, D) fp16;
+    ``logits`` (vocab,) fp16 receives the last position's logits.
+    """
+    s = weights.shape
+    dev = weights.device
+    T = int(tokens.numel())
+    S = int(max_seq)
+    H, NH, D, E, K, F = s.hidden, s.heads, s.head_dim, s.num_experts, s.top_k, s.ffn
+    HD = NH * D
+    g = s.group_size
+    if T < 1 or T > S:
+        raise ValueError("prompt length %d outside [1, %d]" % (T, S))
+    if T * K > PREFILL_MAX_PAIRS:
+        raise NotImplementedError("prefill sorts at most %d (token, expert) pairs; T*top_k = %d"
+                                  % (PREFILL_MAX_PAIRS, T * K))
+    if tokens.dtype != torch.int64 or tokens.device != dev or not tokens.is_contiguous():
+        raise ValueError("tokens must be a contiguous int64 tensor on %s" % dev)
+    _hip.require_rocm(tokens, weights.embed, what="prefill_prompt")
+    lib = _hip.load()
+    P = _hip.ptr
+    st = _hip.stream_of(dev)
+    f16 = dict(dtype=torch.float16, device=dev)
+    i32 = dict(dtype=torch.int32, device=dev)
+
+    h = torch.empty((T, H), **f16)
+    xn = torch.empty((T, H), **f16)
+    qkv = torch.empty((T, 3 * HD), **f16)
+    q = torch.empty((T, HD), **f16)
+    k16 = torch.empty((NH, S, D), **f16)
+    v16 = torch.empty((NH, S, D), **f16)
+    attn = torch.empty((T, HD), **f16)
+    rlog = torch.empty((T, E), **f16)
+    top_w = torch.empty((T, K), dtype=torch.float32, device=dev)
+    top_i = torch.empty((T, K), dtype=torch.int64, device=dev)
+    pairs = T * K
+    max_tiles = int(lib.lemoq_moe_prefill_max_tiles(pairs, E))
+    pair_tok = torch.empty((pairs,), **i32)
+    pair_src = torch.empty((pairs,), **i32)
+    pair_w = torch.empty((pairs,), **f16)
+    expert_off = torch.empty((E + 1,), **i32)
+    tiles = torch.empty((max_tiles, 4), **i32)
+    act = torch.empty((pairs, F), **f16)
+    ybuf = torch.empty((pairs, H), **f16)
+    qk_scale = float((1.0 / math.sqrt(D)) * LOG2E)
+
+    _hip.call("lemoq_gather_rows", P(weights.embed), s.vocab, H, P(tokens), T, P(h), st)
+    for L, c in zip(weights.layers, kv):
+        _hip.call("lemoq_rmsnorm", P(h), T, H, P(L.ln_in), float(s.eps), P(xn), st)
+        _hip.call("lemoq_gemm_w8", P(xn), T, H, H, None, P(L.qkv_codes), P(L.qkv_scale), 3 * HD, g,
+                  P(qkv), 3 * HD, None, 0, st)
+        _hip.call("lemoq_qk_norm_rope_kv_i8_rows", P(qkv), T, NH, D, P(L.q_norm), P(L.k_norm), float(s.eps),
+                  P(cos_tab), P(sin_tab), 0, P(q), P(c["kc"]), P(c["ks"]), P(c["vc"]), P(c["vs"]), S * D, S,
+                  P(k16), P(v16), S * D, st)
+        _hip.call("lemoq_attn_prefill_f16", P(q), HD, P(k16), P(v16), S * D, T, NH, D, qk_scale, P(attn), HD, st)
+        _hip.call("lemoq_gemm_w8", P(attn), T, HD, HD, None, P(L.o_codes), P(L.o_scale), H, g, P(h), H, P(h), H,
+                  st)
+        _hip.call("lemoq_rmsnorm", P(h), T, H, P(L.ln_post), float(s.eps), P(xn), st)
+        _hip.call("lemoq_gemm_f16", P(xn), T, H, H, P(L.router), E, P(rlog), E, st)
+        _hip.call("lemoq_route_topk", P(rlog), 1, T, E, E, K, int(bool(s.norm_topk_prob)), P(top_w), P(top_i), st)
+        _hip.call("lemoq_moe_prefill_sort", P(top_i), P(top_w), T, K, E, P(pair_tok), P(pair_src), P(pair_w),
+                  P(expert_off), P(tiles), max_tiles, st)
+        _hip.call("lemoq_moe_prefill_gate_up", P(xn), H, P(pair_tok), P(tiles), max_tiles, P(L.gu_codes),
+                  P(L.gu_scale), F, g, P(act), st)
+        _hip.call("lemoq_moe_prefill_down", P(act), F, P(pair_src), P(pair_w), P(tiles), max_tiles,
+                  P(L.dn_codes), P(L.dn_scale), H, g, P(ybuf), st)
+        _hip.call("lemoq_moe_prefill_combine", P(ybuf), P(top_i), T, K, H, P(h), P(h), st)
+    last = h[T - 1:]
+    _hip.call("lemoq_rmsnorm", P(last), 1, H, P(weights.final_norm), float(s.eps), P(xn), st)
+    _hip.call("lemoq_gemm_w8", P(xn), 1, H, H, None, P(weights.lm_codes), P(weights.lm_scale), s.vocab, g,
+              P(logits), s.vocab, None, 0, st)
+    # The scratch tensors are released when this returns; the caching allocator
+    # hands their memory only to later work on this same stream, which runs
+    # after these kernels.

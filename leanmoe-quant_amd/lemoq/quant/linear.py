@@ -2,11 +2,14 @@
 
 Replaces the part of the reference's ``QuantLinear`` (``src/lemoq/quant/linear.py:245-488``)
 that the decode path uses: buffers ``packed`` int8 (out, padded_in), ``scale``
-fp16 (out, n_groups), ``zero=None``, ``bias`` (optional); ``forward`` is the
-fused dequant-GEMV (``_fused_forward``, ``:446-469``) for any number of rows
-(the kernel re-reads the weight per row; decode uses one).  Quantisation runs
-on the device (``lemoq.quant.rtn``).  There is no "separate" arm and no
-host-side dequantisation.
+fp16 (out, n_groups), ``zero=None``, ``bias`` (optional).  ``forward``
+dispatches as the reference does (``_fused_fallback_reason``, ``:420-444``):
+one token takes the fused dequant-GEMV (``_fused_forward``, ``:446-469``;
+fp32 dequantisation, one rounding), several tokens take the numerics of the
+"separate" arm (``dequantized_weight`` + ``F.linear``, ``:365-395,471-480``:
+fp16 weight, fp32 accumulation) on the matrix-core GEMM, which dequantises in
+registers instead of materialising the fp16 weight.  Quantisation runs on the
+device (``lemoq.quant.rtn``).
 """
 
 from __future__ import annotations
@@ -61,16 +64,21 @@ class QuantLinear(nn.Module):
         return obj
 
     def forward(self, x: Any) -> Any:
-        from lemoq.kernels.dequant_gemm import dequant_gemm_fused  # noqa: PLC0415
+        from lemoq.kernels.dequant_gemm import dequant_gemm_fused, dequant_gemm_separate  # noqa: PLC0415
 
         if x.shape[-1] != self.in_features:
             raise ValueError("input width %d != in_features %d" % (int(x.shape[-1]), self.in_features))
         flat = x.reshape(-1, self.in_features)
-        y = dequant_gemm_fused(
-            flat if flat.is_contiguous() else flat.contiguous(),
-            self.packed, self.scale, None, group_size=self.group_size, bits=8, symmetric=True,
-            out_dtype=x.dtype,
-        )
+        flat = flat if flat.is_contiguous() else flat.contiguous()
+        if int(flat.shape[0]) == 1:
+            y = dequant_gemm_fused(flat, self.packed, self.scale, None, group_size=self.group_size, bits=8,
+                                   symmetric=True, out_dtype=x.dtype)
+        else:
+            xs = flat
+            if self.padded_in != self.in_features:  # padded columns hold code 0: zero inputs add nothing
+                xs = torch.nn.functional.pad(xs, (0, self.padded_in - self.in_features))
+            y = dequant_gemm_separate(xs, self.packed, self.scale, None, group_size=self.group_size)
+            y = y if x.dtype == y.dtype else y.to(x.dtype)
         y = y.reshape(*x.shape[:-1], self.out_features)
         if self.bias is not None:
             y = y + self.bias.to(y.dtype)

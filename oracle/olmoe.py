@@ -214,3 +214,72 @@ class OracleDecoder:
             tok = self.greedy(logits)
             tokens.append(tok)
         return tokens, all_logits
+
+
+def oracle_prefill(weights: Any, tokens: Any, max_seq: int, *, all_logits: bool = False):
+    """The reference's prefill of the prompt ``tokens`` (positions 0..T-1) on the CPU.
+
+    ``StaticCacheDecodeSession.prefill`` (``benchmarks/cudagraph.py:578-599``) runs the
+    patched HF model over all T tokens at once; every patched operator takes its
+    multi-token branch there:
+
+    * linears: ``QuantLinear`` "separate" arm, fp16 weight then ``F.linear``
+      (``src/lemoq/quant/linear.py:365-395,420-434,471-480``) -> ``ops.linear_separate_w8``;
+    * RMSNorms (input, q/k over heads*D, post-attention, final): the fused kernel for any
+      row count (``rmsnorm.py:102-163``) -> ``ops.rms_norm``;
+    * RoPE: HF ``apply_rotary_pos_emb`` (the fused RoPE guard takes q_len == 1 only,
+      ``rope.py:140-177``) -> ``ops.rope_hf``;
+    * attention: HF's own forward with sdpa and a causal mask (the decode core is only
+      taken for q_len == 1, ``attn_decode.py:836-1017``) -> ``ops.causal_attention``;
+    * MoE: router ``F.linear`` in fp16, ``_route``, per-expert loop
+      (``moe_static.py:262-283,329-371``) -> ``ops.linear_f16``, ``ops.route_logits``,
+      ``ops.moe_prefill_w8``;
+    * the KV-INT8 cache is the bulk quantisation of the fp16 k/v rows
+      (``kv_int8.py:127-162``) -> ``oracle.quant.kv_quantize_rows``;
+    * logits: final norm and the W8 lm_head (separate arm: T > 1 rows reach it).
+
+    Returns ``(logits, kv)``: fp16 logits of the last position (``(T, vocab)`` with
+    ``all_logits``), and per layer the KV-INT8 cache dict (kc, ks, vc, vs) of ``max_seq``
+    slots with slots 0..T-1 filled (the rest codes 0, scales 1).
+    """
+    s, w = weights.shape, weights
+    toks = torch.as_tensor(tokens, dtype=torch.int64).reshape(-1)
+    T = int(toks.numel())
+    NH, D = s.heads, s.head_dim
+    HD = NH * D
+    g = s.group_size
+    if not (0 < T <= max_seq):
+        raise ValueError("prompt length outside the cache")
+    cos, sin = ops.rotary_cos_sin(torch.arange(T), D, s.rope_theta)
+    cos, sin = cos.unsqueeze(1), sin.unsqueeze(1)  # (T, 1, D) against (T, heads, D)
+    h = w.embed[toks].clone()
+    kv_out = []
+    for L in w.layers:
+        r = h
+        xn = ops.rms_norm(h, L.ln_in, s.eps)
+        qkv = ops.linear_separate_w8(xn, L.qkv_codes, L.qkv_scale, g)
+        q = ops.rms_norm(qkv[:, :HD], L.q_norm, s.eps).reshape(T, NH, D)
+        k = ops.rms_norm(qkv[:, HD:2 * HD], L.k_norm, s.eps).reshape(T, NH, D)
+        v = qkv[:, 2 * HD:].reshape(T, NH, D)
+        q, k = ops.rope_hf(q, k, cos, sin)
+        cache = {
+            "kc": torch.zeros((NH, max_seq, D), dtype=torch.int8),
+            "ks": torch.ones((NH, max_seq), dtype=torch.float16),
+            "vc": torch.zeros((NH, max_seq, D), dtype=torch.int8),
+            "vs": torch.ones((NH, max_seq), dtype=torch.float16),
+        }
+        for name, rows in (("k", k), ("v", v)):
+            codes, scales = oq.kv_quantize_rows(rows.reshape(T * NH, D).numpy())
+            cache[name + "c"][:, :T, :] = torch.from_numpy(codes).reshape(T, NH, D).transpose(0, 1)
+            cache[name + "s"][:, :T] = torch.from_numpy(scales).reshape(T, NH).transpose(0, 1)
+        kv_out.append(cache)
+        attn = ops.causal_attention(q, k, v).to(torch.float16).reshape(T, HD)
+        h = r + ops.linear_separate_w8(attn, L.o_codes, L.o_scale, g)
+        r = h
+        xn = ops.rms_norm(h, L.ln_post, s.eps)
+        top_w, top_i = ops.route_logits(ops.linear_f16(xn, L.router), s.top_k, s.norm_topk_prob)
+        h = r + ops.moe_prefill_w8(xn, L.gu_codes, L.gu_scale, L.dn_codes, L.dn_scale, g, top_i,
+                                   top_w.to(torch.float16))
+    rows = h if all_logits else h[-1:]
+    logits = ops.linear_separate_w8(ops.rms_norm(rows, w.final_norm, s.eps), w.lm_codes, w.lm_scale, g)
+    return (logits if all_logits else logits[0]), kv_out

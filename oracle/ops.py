@@ -38,6 +38,25 @@ def dequant_gemm_separate(x: Any, codes: Any, scale: Any, group: int, out_dtype:
     return y.to(out_dtype) if out_dtype is not None else y
 
 
+def dequant_weight_f16(codes: Any, scale: Any, group: int) -> torch.Tensor:
+    """``QuantLinear.dequantized_weight(dtype=fp16)`` (``src/lemoq/quant/linear.py:365-395``):
+    the exact fp32 product ``code * scale`` rounded once to fp16."""
+    return dequant_w8(codes, scale, group).to(torch.float16)
+
+
+def linear_separate_w8(x: Any, codes: Any, scale: Any, group: int) -> torch.Tensor:
+    """The multi-token ``QuantLinear`` arm (``src/lemoq/quant/linear.py:471-480``):
+    ``F.linear(x16, fp16 weight)`` -> fp16.  The product is formed in fp64 and
+    rounded once to fp16 (a GPU fp32-accumulating GEMM lands within an ulp)."""
+    w16 = dequant_weight_f16(codes, scale, group)[:, : int(x.shape[-1])]
+    return (x.to(torch.float64) @ w16.to(torch.float64).t()).to(torch.float16)
+
+
+def linear_f16(x: Any, weight: Any) -> torch.Tensor:
+    """``F.linear`` of fp16 operands -> fp16 (fp64 product, one rounding)."""
+    return (x.to(torch.float64) @ weight.to(torch.float64).t()).to(torch.float16)
+
+
 def dequant_gemm_fused_tiles(x: Any, codes: Any, scale: Any, group: int, out_dtype: Any = None) -> torch.Tensor:
     """Group-by-group accumulation (``src/lemoq/kernels/reference.py:63-112``)."""
     M, K = int(x.shape[0]), int(x.shape[1])
@@ -109,6 +128,12 @@ def route(x: Any, router_weight: Any, top_k: int, norm_topk_prob: bool):
     dtype, fp32 softmax, top-k by probability (ties -> lowest index, the rule of
     ``_routing_triton.py:11-14``), optional renorm, weights cast to x's dtype."""
     logits = F.linear(x, router_weight)
+    top_w, top_i = route_logits(logits, top_k, norm_topk_prob)
+    return logits, top_w.to(x.dtype), top_i
+
+
+def route_logits(logits: Any, top_k: int, norm_topk_prob: bool):
+    """The softmax/top-k tail of ``_route`` on given logits: ``(top_w fp32, top_i int64)``."""
     p = F.softmax(logits, dim=-1, dtype=torch.float32)
     pn = p.numpy()
     order = np.argsort(-pn, axis=-1, kind="stable")[..., :top_k]
@@ -116,7 +141,7 @@ def route(x: Any, router_weight: Any, top_k: int, norm_topk_prob: bool):
     top_w = torch.gather(p, -1, top_i)
     if norm_topk_prob:
         top_w = top_w / top_w.sum(dim=-1, keepdim=True)
-    return logits, top_w.to(x.dtype), top_i
+    return top_w, top_i
 
 
 def grouped_gate_up_act(x: Any, gate_up_sel: Any, ffn: int) -> torch.Tensor:
@@ -151,6 +176,40 @@ def grouped_moe_w8(x: Any, gu_codes: Any, gu_scale: Any, dn_codes: Any, dn_scale
     dn = torch.stack([dequant_w8(dn_codes[e], dn_scale[e], group) for e in ids])
     out = grouped_down_sum(act, dn, top_w.reshape(-1).to(torch.float16)).to(torch.float16)
     return out, act
+
+
+def moe_prefill_w8(x: Any, gu_codes: Any, gu_scale: Any, dn_codes: Any, dn_scale: Any, group: int,
+                   top_i: Any, top_w16: Any) -> torch.Tensor:
+    """``_prefill_forward`` with quantized experts (``src/lemoq/kernels/moe_static.py:329-371``):
+    experts in ascending order; the expert's tokens (``nonzero``, token order) go through
+    ``gu = F.linear(x_e, fp16 W_gu)``, ``act = silu(gate) * up`` and ``y = F.linear(act, fp16 W_dn)``
+    in fp16, and ``y * w`` is index_added into a zero fp16 output.  x (T, H) fp16;
+    top_i (T, k) int64; top_w16 (T, k) fp16 -> (T, H) fp16."""
+    out = torch.zeros_like(x)
+    ffn = int(gu_codes.shape[1]) // 2
+    for e in range(int(gu_codes.shape[0])):
+        tok, slot = (top_i == e).nonzero(as_tuple=True)
+        if tok.numel() == 0:
+            continue
+        w = top_w16[tok, slot].unsqueeze(-1)
+        gu = linear_separate_w8(x[tok], gu_codes[e], gu_scale[e], group)
+        act = F.silu(gu[:, :ffn]) * gu[:, ffn:]
+        y = linear_separate_w8(act, dn_codes[e], dn_scale[e], group)
+        out.index_add_(0, tok, y * w)
+    return out
+
+
+def causal_attention(q: Any, k: Any, v: Any, *, scale: float | None = None,
+                     dtype: Any = torch.float64) -> torch.Tensor:
+    """Causal softmax attention over the prompt (HF ``OlmoeAttention`` with sdpa and a causal
+    mask), in fp64 by default.  q, k, v (T, H, D) -> (T, H, D)."""
+    T, dim = int(q.shape[0]), int(q.shape[-1])
+    scale = (1.0 / math.sqrt(dim)) if scale is None else float(scale)
+    qq, kk, vv = (t.to(dtype).transpose(0, 1) for t in (q, k, v))
+    scores = torch.matmul(qq, kk.transpose(1, 2)) * scale
+    future = torch.ones((T, T), dtype=torch.bool).triu(1)
+    scores = scores.masked_fill(future, float("-inf"))
+    return torch.matmul(torch.softmax(scores, dim=-1), vv).transpose(0, 1)
 
 
 # ---------------------------------------------------------------------------

@@ -60,5 +60,10 @@ def test_argument_rejection_happens_before_any_launch():
     assert lib.lemoq_attn_split_i8(fake, fake, fake, fake, fake, 128 * 10, 10, fake, 16, 96, 4, 1.0,
                                    fake, fake, fake, None) == -3
     assert lib.lemoq_route_topk(fake, 1, 1, 2000, 2000, 8, 0, fake, fake, None) == -2
+    # prefill GEMMs: K not a multiple of 32, group not a multiple of 32, misaligned codes
+    assert lib.lemoq_gemm_w8(fake, 4, 48, 48, None, fake, fake, 64, 48, fake, 64, None, 0, None) == -2
+    assert lib.lemoq_gemm_w8(fake, 4, 128, 128, None, fake, fake, 64, 16, fake, 64, None, 0, None) == -3
+    assert lib.lemoq_gemm_w8(fake, 4, 128, 128, None, fake + 8, fake, 64, 128, fake, 64, None, 0, None) == -4
+    assert lib.lemoq_gemm_f16(fake, 4, 128, 64, fake, 64, fake, 64, None) == -2
     with pytest.raises(ValueError):
         _hip.call("lemoq_gemv_w8", None, 1, 16, None, None, 16, 16, 16, None, 1, None)

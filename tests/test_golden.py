@@ -129,7 +129,7 @@ def test_gpu_tiny_decode_matches_fixture(dev):
     prompt = g["prompt"].tolist()
     steps = len(g["tokens"]) - 1
     sess = DecodeSession(w, prompt, max_new_tokens=steps, num_splits=4)
-    sess.prefill()
+    sess.prefill(mode="stepped")  # the fixture's oracle stepped the prompt
     logits = []
     for _ in range(steps):
         sess.replay(1)

@@ -126,7 +126,7 @@ def test_prompt_tokens_are_fed_then_greedy_takes_over(dev):
     w = OlmoeW8Weights.random(TINY, seed=6, device=dev)
     prompt = [5, 17, 300, 2, 999, 42]
     sess = DecodeSession(w, prompt, max_new_tokens=3, num_splits=2)
-    sess.prefill()
+    sess.prefill(mode="stepped")  # the oracle's run() steps the prompt too
     hist = sess.history[: len(prompt)].tolist()
     assert hist == prompt
     oracle = OracleDecoder(w.to_host(), sess.max_seq)

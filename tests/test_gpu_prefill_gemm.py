@@ -1,0 +1,127 @@
+"""GPU parity of the multi-token linears on the matrix cores.
+
+``lemoq_gemm_w8`` follows the reference's multi-token ``QuantLinear`` arm
+(fp16 dequantised weight, ``F.linear``: src/lemoq/quant/linear.py:365-395,
+471-480) and ``lemoq_gemm_f16`` the router's fp16 ``F.linear`` for several
+tokens (src/lemoq/kernels/moe_static.py:267).  The oracle forms each product
+in fp64 from the same fp16 weight and rounds once to fp16; the kernel
+accumulates in fp32, so every output lies within one fp16 ulp of the oracle
+plus an fp32 accumulation allowance of 3e-5 * sum|x||w| (the worst case for
+K = 2048 is 2048 * 2^-24 = 1.2e-4; observed errors are far below the
+allowance).  The BASELINE tolerance (rtol 2e-2, atol 2e-3) is checked as well.
+Shapes: the OLMoE prefill linears (qkv 6144 x 2048, o_proj 2048 x 2048, one
+expert's gate_up 2048 x 2048 and down 2048 x 1024, router 64 x 2048, lm_head
+50304 x 2048 for the last row), ragged M and N, row gather and residual.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from helpers import assert_close, randn
+from oracle import ops
+from oracle import quant as oq
+
+pytestmark = pytest.mark.gpu
+
+
+def _q8(w: torch.Tensor, group: int):
+    q = oq.rtn_quantize_w8(w.numpy(), group)
+    return torch.from_numpy(q["codes_padded"]), torch.from_numpy(q["scale_f16"])
+
+
+def _ulp16(r: torch.Tensor) -> torch.Tensor:
+    a = r.double().abs().clamp_min(2.0 ** -14)
+    return torch.exp2(torch.floor(torch.log2(a)) - 10)
+
+
+def _assert_linear(got, ref16, absdot, what):
+    g, r = got.double().cpu(), ref16.double()
+    assert g.shape == r.shape, what
+    assert torch.isfinite(g).all(), what
+    bound = _ulp16(r) + 3e-5 * absdot
+    err = (g - r).abs()
+    assert bool((err <= bound).all()), "%s: max err %.3e, worst excess %.3e" % (
+        what, float(err.max()), float((err - bound).max()))
+    assert_close(got, ref16, what=what)
+
+
+SHAPES = [
+    (2, 384, 256),       # tiny
+    (16, 6144, 2048),    # qkv, short prompt
+    (100, 2048, 2048),   # o_proj, ragged M
+    (1024, 6144, 2048),  # qkv at ctx 1024
+    (37, 100, 128),      # ragged M and N, one group
+    (257, 2048, 1024),   # expert down width
+    (1, 50304, 2048),    # lm_head on the last prompt row
+]
+
+
+@pytest.mark.parametrize("m,n,k", SHAPES, ids=["%dx%dx%d" % s for s in SHAPES])
+def test_gemm_w8_vs_oracle(m, n, k, dev):
+    from lemoq.kernels.dequant_gemm import dequant_gemm_separate
+
+    print("case: gemm_w8 m=%d n=%d k=%d" % (m, n, k), flush=True)
+    codes, scale = _q8(randn(n, k, seed=n + k, std=0.02), 128)
+    x = randn(m, k, seed=3 * m + k).to(torch.float16)
+    got = dequant_gemm_separate(x.to(dev), codes.to(dev), scale.to(dev), group_size=128)
+    torch.cuda.synchronize()
+    ref = ops.linear_separate_w8(x, codes, scale, 128)
+    absdot = x.double().abs() @ ops.dequant_weight_f16(codes, scale, 128).double().abs().t()
+    _assert_linear(got, ref, absdot, "gemm_w8 %dx%dx%d" % (m, n, k))
+
+
+def test_gemm_w8_gather_and_residual(dev):
+    from lemoq import _hip
+
+    print("case: gemm_w8 gather + residual", flush=True)
+    rows, m, n, k = 300, 77, 512, 1024
+    codes, scale = _q8(randn(n, k, seed=41, std=0.02), 128)
+    x = randn(rows, k, seed=42).to(torch.float16)
+    idx = torch.randint(0, rows, (m,), generator=torch.Generator().manual_seed(43), dtype=torch.int32)
+    resid = randn(m, n, seed=44).to(torch.float16)
+    xd, cd, sd, idd = x.to(dev), codes.to(dev), scale.to(dev), idx.to(dev)
+    y = resid.clone().to(dev)  # residual aliases the output
+    _hip.call("lemoq_gemm_w8", _hip.ptr(xd), m, k, k, _hip.ptr(idd), _hip.ptr(cd), _hip.ptr(sd), n, 128,
+              _hip.ptr(y), n, _hip.ptr(y), n, _hip.stream_of(dev))
+    torch.cuda.synchronize()
+    xg = x[idx.long()]
+    lin = ops.linear_separate_w8(xg, codes, scale, 128)
+    ref = (lin.float() + resid.float()).to(torch.float16)
+    absdot = xg.double().abs() @ ops.dequant_weight_f16(codes, scale, 128).double().abs().t()
+    # one ulp of the linear output can move the sum by one more rounding step
+    err = (y.cpu().double() - ref.double()).abs()
+    bound = _ulp16(ref) + _ulp16(lin) + 3e-5 * absdot
+    assert bool((err <= bound).all()), float((err - bound).max())
+    assert_close(y.cpu(), ref, what="gather+residual")
+
+
+@pytest.mark.parametrize("m,n,k", [(1024, 64, 2048), (5, 64, 2048), (3, 50, 64)])
+def test_gemm_f16_vs_oracle(m, n, k, dev):
+    from lemoq.kernels.dequant_gemm import linear_f16
+
+    print("case: gemm_f16 m=%d n=%d k=%d" % (m, n, k), flush=True)
+    w = randn(n, k, seed=n * k, std=0.02).to(torch.float16)
+    x = randn(m, k, seed=m + 5).to(torch.float16)
+    got = linear_f16(x.to(dev), w.to(dev))
+    torch.cuda.synchronize()
+    ref = ops.linear_f16(x, w)
+    _assert_linear(got, ref, x.double().abs() @ w.double().abs().t(), "gemm_f16 %dx%dx%d" % (m, n, k))
+
+
+def test_quant_linear_dispatch(dev):
+    """One row takes the fused GEMV, several rows the separate-arm GEMM (as the reference's forward)."""
+    from lemoq.kernels.dequant_gemm import dequant_gemm_fused, dequant_gemm_separate
+    from lemoq.quant.linear import QuantLinear
+
+    print("case: QuantLinear dispatch", flush=True)
+    lin = QuantLinear(randn(1024, 2048, seed=61, std=0.02).to(dev))
+    x1 = randn(1, 2048, seed=62).to(torch.float16).to(dev)
+    x7 = randn(1, 7, 2048, seed=63).to(torch.float16).to(dev)
+    assert torch.equal(lin(x1), dequant_gemm_fused(x1, lin.packed, lin.scale, None, group_size=128,
+                                                   out_dtype=torch.float16))
+    y7 = lin(x7)
+    assert y7.shape == (1, 7, 1024)
+    assert torch.equal(y7.reshape(7, 1024), dequant_gemm_separate(x7.reshape(7, 2048), lin.packed, lin.scale,
+                                                                  group_size=128))
