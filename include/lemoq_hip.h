@@ -414,7 +414,7 @@ int lemoq_olmoe_decode_step(const LemoqOlmoeStep* step, void* stream);
  * fp16 add).  x row m is row x_rows[m] of x when x_rows != NULL.
  *   x (rows, x_ld) fp16; codes (N, K) int8; scale (N, K/group) fp16;
  *   y (M, y_ld) fp16; residual (M, residual_ld) fp16 (may alias y).
- *   K % 32 == 0, group % 32 == 0, K % group == 0, x_ld % 8 == 0, x and codes
+ *   K % 64 == 0, group % 64 == 0, K % group == 0, x_ld % 8 == 0, x and codes
  *   16-byte aligned.
  * ------------------------------------------------------------------------- */
 int lemoq_gemm_w8(const uint16_t* x, int64_t M, int64_t K, int64_t x_ld, const int32_t* x_rows,
@@ -484,7 +484,7 @@ int lemoq_moe_prefill_sort(const int64_t* top_i, const float* top_w, int64_t T, 
 /* act (pairs, F) = fp16(fp16(silu(g)) * u), g and u the fp16 outputs of
  * x[pair_tok] @ w^T for the expert's gate rows [0, F) and up rows [F, 2F)
  * (w8, w = fp16(code * scale)).  x (T, H) fp16; gu_codes (E, 2F, H) int8;
- * gu_scale (E, 2F, H/group) fp16.  H, F, group multiples of 32. */
+ * gu_scale (E, 2F, H/group) fp16.  H, F and group multiples of 64. */
 int lemoq_moe_prefill_gate_up(const uint16_t* x, int64_t H, const int32_t* pair_tok,
                               const int32_t* tiles, int64_t max_tiles, const int8_t* gu_codes,
                               const uint16_t* gu_scale, int64_t F, int64_t group, uint16_t* act,

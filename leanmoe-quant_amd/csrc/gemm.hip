@@ -8,8 +8,10 @@
 // code, converted to fp16, times the fp16 scale in one fp16 rounding
 // (v_pk_mul_f16).
 //
-// Tiling: 4 waves per block as 2 x 2 wave tiles of 64 x 64 (the main loop of
-// gemm_core.h), no LDS.
+// Tiling: 4 waves per block (2 x 2), block tiles of 128 x 128, or 64 x 128
+// when a grid of 128 x 128 tiles would leave compute units idle; the stage
+// pipeline of gemm_core.h.  Tiles are numbered n-major (consecutive tiles
+// share the weight tile) and each XCD takes a contiguous range of them.
 //
 // Rows: X row m may be gathered (x_rows[m]); the output is fp16 rows with an
 // optional fp16 residual added in one rounding (torch's fp16 add).  Rows and
@@ -35,45 +37,56 @@ struct GemmArgs {
   int64_t resid_ld;
 };
 
-template <bool W8, int FM, int FN>
+template <bool W8, int BM, int BN>
 __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  using TL = Tile<BM, BN>;
+  __shared__ __align__(16) uint16_t lds[TL::LDS_ELEMS];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int half = lane >> 5, l32 = lane & 31;
-  constexpr int TM = 32 * FM, TN = 32 * FN;
-  const int64_t m0 = ((int64_t)blockIdx.y * 2 + (wave >> 1)) * TM;
-  const int64_t n0 = ((int64_t)blockIdx.x * 2 + (wave & 1)) * TN;
-  if (m0 >= a.M || n0 >= a.N) return;  // wave-uniform: a whole wave tile outside the output
+  const int64_t nbm = (a.M + BM - 1) / BM, nbn = (a.N + BN - 1) / BN;
+  const int64_t tile = xcd_tile(blockIdx.x, nbm * nbn);
+  const int64_t m0 = (tile % nbm) * BM, n0 = (tile / nbm) * BN;
 
-  const uint16_t* xr[FM];
+  Sources<TL, W8> src;
 #pragma unroll
-  for (int f = 0; f < FM; ++f) {
-    int64_t m = m0 + 32 * f + l32;
+  for (int i = 0; i < TL::A_CH; ++i) {
+    int64_t m = m0 + TL::a_row(t, i);
     m = m < a.M ? m : a.M - 1;
-    const int64_t src = a.x_rows ? (int64_t)a.x_rows[m] : m;
-    xr[f] = a.x + src * a.x_ld + 16 * half;
+    const int64_t row = a.x_rows ? (int64_t)a.x_rows[m] : m;
+    src.a[i] = a.x + row * a.x_ld + TL::a_col(t, i);
   }
-  WRow wr[FN];
-  const int64_t ng = W8 ? a.K / a.group : 1;
+  if constexpr (W8) {
+    const int64_t ng = a.K / a.group;
 #pragma unroll
-  for (int f = 0; f < FN; ++f) {
-    int64_t n = n0 + 32 * f + l32;
-    n = n < a.N ? n : a.N - 1;
-    wr[f].codes = W8 ? a.codes + n * a.K + 16 * half : nullptr;
-    wr[f].scale = W8 ? a.scale + n * ng : nullptr;
-    wr[f].w16 = W8 ? nullptr : a.w16 + n * a.K + 16 * half;
+    for (int i = 0; i < TL::B8_CH; ++i) {
+      int64_t n = n0 + TL::b8_row(t, i);
+      n = n < a.N ? n : a.N - 1;
+      src.bc[i] = a.codes + n * a.K + TL::b8_col(t, i);
+      src.bs[i] = a.scale + n * ng;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < TL::B16_CH; ++i) {
+      int64_t n = n0 + TL::b16_row(t, i);
+      n = n < a.N ? n : a.N - 1;
+      src.bw[i] = a.w16 + n * a.K + TL::b16_col(t, i);
+    }
   }
-  Acc<FM, FN> acc;
-  acc_zero(acc);
-  mainloop<W8>(acc, xr, wr, a.K, a.group);
+  const int wm = wave >> 1, wn = wave & 1;
+  int b_row0[TL::FN];
+#pragma unroll
+  for (int j = 0; j < TL::FN; ++j) b_row0[j] = wn * (BN / 2) + 32 * j;
+  Acc<TL::FM, TL::FN> acc;
+  block_mainloop<TL, W8>(acc, src, a.K, a.group, lds, wm * (BM / 2), b_row0);
 
 #pragma unroll
-  for (int i = 0; i < FM; ++i)
+  for (int i = 0; i < TL::FM; ++i)
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      const int64_t n = n0 + 32 * j + l32;
+    for (int j = 0; j < TL::FN; ++j) {
+      const int64_t n = n0 + wn * (BN / 2) + 32 * j + l32;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int64_t m = m0 + 32 * i + acc_row(r, half);
+        const int64_t m = m0 + wm * (BM / 2) + 32 * i + acc_row(r, half);
         if (m >= a.M || n >= a.N) continue;
         uint16_t o = f2h(acc.v[i][j][r]);
         if (a.resid) o = hadd_round(h2f(o), a.resid[m * a.resid_ld + n]);
@@ -82,22 +95,28 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
     }
 }
 
-int launch_gemm(const GemmArgs& a, hipStream_t st) {
-  constexpr int FM = 2, FN = 2;
-  const dim3 grid((unsigned)((a.N + 2 * 32 * FN - 1) / (2 * 32 * FN)),
-                  (unsigned)((a.M + 2 * 32 * FM - 1) / (2 * 32 * FM)));
-  if (a.codes)
-    hipLaunchKernelGGL((gemm_kernel<true, FM, FN>), grid, dim3(256), 0, st, a);
-  else
-    hipLaunchKernelGGL((gemm_kernel<false, FM, FN>), grid, dim3(256), 0, st, a);
+template <bool W8>
+int launch_tiles(const GemmArgs& a, hipStream_t st) {
+  const int64_t big = ((a.M + 127) / 128) * ((a.N + 127) / 128);
+  if (big >= 256) {
+    hipLaunchKernelGGL((gemm_kernel<W8, 128, 128>), dim3((unsigned)big), dim3(256), 0, st, a);
+  } else {
+    const int64_t small = ((a.M + 63) / 64) * ((a.N + 127) / 128);
+    hipLaunchKernelGGL((gemm_kernel<W8, 64, 128>), dim3((unsigned)small), dim3(256), 0, st, a);
+  }
   LEMOQ_CHECK_LAUNCH();
+}
+
+int launch_gemm(const GemmArgs& a, hipStream_t st) {
+  return a.codes ? launch_tiles<true>(a, st) : launch_tiles<false>(a, st);
 }
 
 int check_gemm(const GemmArgs& a) {
   if (!a.x || (!a.codes && !a.w16) || (a.codes && !a.scale) || !a.y16) return LEMOQ_ERR_NULL;
-  if (a.M <= 0 || a.N <= 0 || a.K <= 0 || a.M > 65535LL * 128 || a.N > 65535LL * 128) return LEMOQ_ERR_SHAPE;
-  if (a.K % 32 != 0 || a.x_ld < a.K || a.x_ld % 8 != 0 || a.y_ld < a.N) return LEMOQ_ERR_SHAPE;
-  if (a.codes && (a.group <= 0 || a.group % 32 != 0 || a.K % a.group != 0)) return LEMOQ_ERR_UNSUPPORTED;
+  if (a.M <= 0 || a.N <= 0 || a.K <= 0 || a.M > (1LL << 24) || a.N > (1LL << 24)) return LEMOQ_ERR_SHAPE;
+  if (((a.M + 63) / 64) * ((a.N + 127) / 128) > 0x7fffffffLL) return LEMOQ_ERR_SHAPE;
+  if (a.K % 64 != 0 || a.x_ld < a.K || a.x_ld % 8 != 0 || a.y_ld < a.N) return LEMOQ_ERR_SHAPE;
+  if (a.codes && (a.group <= 0 || a.group % 64 != 0 || a.K % a.group != 0)) return LEMOQ_ERR_UNSUPPORTED;
   if (a.resid && a.resid_ld < a.N) return LEMOQ_ERR_SHAPE;
   if (!lemoq_aligned16(a.x) || (a.codes && !lemoq_aligned16(a.codes)) || (a.w16 && !lemoq_aligned16(a.w16)))
     return LEMOQ_ERR_ALIGN;

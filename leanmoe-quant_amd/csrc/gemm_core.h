@@ -1,17 +1,22 @@
-// Matrix-core main loop shared by the multi-token (prefill) GEMMs: a wave
-// accumulates a (32*FM) x (32*FN) tile of Y = X W^T with
-// v_mfma_f32_32x32x16_f16, X rows fp16 and W rows either w8 (int8 codes +
-// fp16 per-group scales, dequantised in registers to fp16(code * scale)) or
-// fp16.
+// Matrix-core main loop shared by the multi-token (prefill) GEMMs.
+//
+// A block of 4 waves (2 x 2) computes a BM x BN tile of Y = X W^T with
+// v_mfma_f32_32x32x16_f16; X rows fp16, W rows either w8 (int8 codes + fp16
+// per-group scales, dequantised to fp16(code * scale) once per block as the
+// tile is written to LDS) or fp16.  K advances in stages of 64: the global
+// loads of stage s+1 are issued into registers before the matrix ops of stage
+// s, then written to the other half of a double-buffered LDS tile; one
+// barrier per stage.  Loads are never under a branch: the prefetch of the
+// stage after the last re-reads the last stage (clamped k) into the unused
+// buffer.
 //
 // Operand layout of v_mfma_f32_32x32x16_f16 (verified on the device): lane l
 // holds row (A) / column (B) l % 32 and 8 k-values of the lane half l / 32;
 // accumulator register r of lane l is element (8*(r/4) + 4*(l/32) + r%4,
 // l % 32).  The sum over k does not depend on which k-values a lane half
-// holds as long as A and B agree, so each lane reads 16 consecutive k (one
-// 16-byte load of codes, two of fp16) and feeds two instructions: half h takes
-// k0 + 16h + [0, 8) in the first and k0 + 16h + [8, 16) in the second.  A
-// 32-wide k block lies inside one scale group (group % 32 == 0).
+// holds as long as A and B agree, so each lane reads 16 consecutive k of a
+// 32-wide chunk (two 16-byte LDS reads) and feeds two instructions: half h
+// takes 16h + [0, 8) in the first and 16h + [8, 16) in the second.
 #pragma once
 
 #include "common.h"
@@ -21,13 +26,16 @@ namespace lemoq_gemm {
 typedef _Float16 h8v __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
+constexpr int BK = 64;            // k per stage
+constexpr int LDS_PITCH = BK + 8; // fp16 per LDS row (16-byte pad)
+
 __device__ __forceinline__ h8v h8_of(const u32x4 v) { return __builtin_bit_cast(h8v, v); }
 
-// 16 int8 codes (k order) -> two h8v of fp16(code * s): the code becomes an
+// 16 int8 codes (k order) -> two u32x4 of fp16(code * s): the code becomes an
 // exact fp16 through (1024 + (code + 128)) - 1152, and one fp16 multiply
 // rounds the exact product once (the fp32 product code * scale is exact, so
 // this equals rounding it to fp16).
-__device__ __forceinline__ void dequant16(const u32x4 c, uint32_t s2, h8v& lo, h8v& hi) {
+__device__ __forceinline__ void dequant16(const u32x4 c, uint32_t s2, u32x4& lo, u32x4& hi) {
   const uint32_t w[4] = {c.x, c.y, c.z, c.w};
   const f16x2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
   const f16x2 sc = as_h2(s2);
@@ -40,15 +48,29 @@ __device__ __forceinline__ void dequant16(const u32x4 c, uint32_t s2, h8v& lo, h
     o[2 * i] = __builtin_bit_cast(uint32_t, (as_h2(p01) - bias) * sc);
     o[2 * i + 1] = __builtin_bit_cast(uint32_t, (as_h2(p23) - bias) * sc);
   }
-  lo = __builtin_bit_cast(h8v, (u32x4){o[0], o[1], o[2], o[3]});
-  hi = __builtin_bit_cast(h8v, (u32x4){o[4], o[5], o[6], o[7]});
+  lo = (u32x4){o[0], o[1], o[2], o[3]};
+  hi = (u32x4){o[4], o[5], o[6], o[7]};
 }
 
-// Weight-row source of one B fragment: w8 (codes row + scales row) or fp16.
-struct WRow {
-  const int8_t* codes;     // row start + 16*half (w8)
-  const uint16_t* scale;   // row's scales (w8)
-  const uint16_t* w16;     // row start + 16*half (fp16)
+// Tile geometry of a BM x BN block (BM, BN in {64, 128}).
+template <int BM_, int BN_>
+struct Tile {
+  static constexpr int BM = BM_, BN = BN_;
+  static constexpr int FM = BM / 64, FN = BN / 64;   // 32 x 32 fragments per wave
+  static constexpr int A_CH = BM * (BK / 8) / 256;   // 16-byte A chunks per thread per stage
+  static constexpr int B16_CH = BN * (BK / 8) / 256; // fp16 B chunks per thread
+  static constexpr int B8_CH = BN * (BK / 16) / 256; // w8 B chunks (16 codes) per thread
+  static constexpr int LDS_HALF = (BM + BN) * LDS_PITCH;  // fp16 per buffer
+  static constexpr int LDS_ELEMS = 2 * LDS_HALF;
+  static_assert(BM % 64 == 0 && BN % 64 == 0 && B8_CH >= 1, "tile sizes");
+  // Thread t's A chunk i: tile row (t + 256 i) / 8, column 8 * ((t + 256 i) % 8).
+  __device__ static int a_row(int t, int i) { return (t + 256 * i) >> 3; }
+  __device__ static int a_col(int t, int i) { return 8 * ((t + 256 * i) & 7); }
+  __device__ static int b16_row(int t, int i) { return (t + 256 * i) >> 3; }
+  __device__ static int b16_col(int t, int i) { return 8 * ((t + 256 * i) & 7); }
+  // w8 chunk: 16 codes; tile row (t + 256 i) / 4, column 16 * ((t + 256 i) % 4).
+  __device__ static int b8_row(int t, int i) { return (t + 256 * i) >> 2; }
+  __device__ static int b8_col(int t, int i) { return 16 * ((t + 256 * i) & 3); }
 };
 
 template <int FM, int FN>
@@ -56,54 +78,128 @@ struct Acc {
   f32x16 v[FM][FN];
 };
 
-template <int FM, int FN>
-__device__ __forceinline__ void acc_zero(Acc<FM, FN>& a) {
+// Per-thread sources of one block: A chunk pointers (row start + column) and
+// B chunk pointers (codes and the row's scales, or fp16 weights).
+template <class TL, bool W8>
+struct Sources {
+  const uint16_t* a[TL::A_CH];
+  const int8_t* bc[W8 ? TL::B8_CH : 1];
+  const uint16_t* bs[W8 ? TL::B8_CH : 1];
+  const uint16_t* bw[W8 ? 1 : TL::B16_CH];
+};
+
+template <class TL, bool W8>
+struct Staged {
+  u32x4 a[TL::A_CH];
+  u32x4 b[W8 ? TL::B8_CH : TL::B16_CH];
+  uint16_t s[W8 ? TL::B8_CH : 1];
+};
+
+template <class TL, bool W8>
+__device__ __forceinline__ void stage_load(Staged<TL, W8>& st, const Sources<TL, W8>& src, int64_t k0,
+                                           int group) {
 #pragma unroll
-  for (int i = 0; i < FM; ++i)
+  for (int i = 0; i < TL::A_CH; ++i) st.a[i] = *reinterpret_cast<const u32x4*>(src.a[i] + k0);
+  if constexpr (W8) {
 #pragma unroll
-    for (int j = 0; j < FN; ++j) a.v[i][j] = (f32x16){};
+    for (int i = 0; i < TL::B8_CH; ++i) {
+      st.b[i] = *reinterpret_cast<const u32x4*>(src.bc[i] + k0);
+      st.s[i] = src.bs[i][k0 / group];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < TL::B16_CH; ++i) st.b[i] = *reinterpret_cast<const u32x4*>(src.bw[i] + k0);
+  }
 }
 
-// xr[f]: start of the lane's X row for fragment f, already offset by 16*half.
-template <bool W8, int FM, int FN>
-__device__ __forceinline__ void mainloop(Acc<FM, FN>& acc, const uint16_t* const (&xr)[FM],
-                                         const WRow (&wr)[FN], int64_t K, int group) {
-  for (int64_t k0 = 0; k0 < K; k0 += 32) {
-    u32x4 xa[FM][2];
+template <class TL, bool W8>
+__device__ __forceinline__ void stage_store(const Staged<TL, W8>& st, uint16_t* buf, int t) {
+  uint16_t* As = buf;
+  uint16_t* Bs = buf + TL::BM * LDS_PITCH;
 #pragma unroll
-    for (int f = 0; f < FM; ++f) {
-      xa[f][0] = *reinterpret_cast<const u32x4*>(xr[f] + k0);
-      xa[f][1] = *reinterpret_cast<const u32x4*>(xr[f] + k0 + 8);
+  for (int i = 0; i < TL::A_CH; ++i)
+    *reinterpret_cast<u32x4*>(As + TL::a_row(t, i) * LDS_PITCH + TL::a_col(t, i)) = st.a[i];
+  if constexpr (W8) {
+#pragma unroll
+    for (int i = 0; i < TL::B8_CH; ++i) {
+      u32x4 lo, hi;
+      dequant16(st.b[i], (uint32_t)st.s[i] * 0x10001u, lo, hi);
+      uint16_t* d = Bs + TL::b8_row(t, i) * LDS_PITCH + TL::b8_col(t, i);
+      *reinterpret_cast<u32x4*>(d) = lo;
+      *reinterpret_cast<u32x4*>(d + 8) = hi;
     }
-    h8v blo[FN], bhi[FN];
-    if constexpr (W8) {
-      u32x4 wc[FN];
-      uint16_t ws[FN];
+  } else {
 #pragma unroll
-      for (int f = 0; f < FN; ++f) {
-        wc[f] = *reinterpret_cast<const u32x4*>(wr[f].codes + k0);
-        ws[f] = wr[f].scale[k0 / group];
-      }
+    for (int i = 0; i < TL::B16_CH; ++i)
+      *reinterpret_cast<u32x4*>(Bs + TL::b16_row(t, i) * LDS_PITCH + TL::b16_col(t, i)) = st.b[i];
+  }
+}
+
+// The matrix ops of one stage for a wave: A fragments at tile rows
+// a_row0 + 32 i, B fragments at tile rows b_row0[j].
+template <class TL>
+__device__ __forceinline__ void stage_mma(Acc<TL::FM, TL::FN>& acc, const uint16_t* buf, int a_row0,
+                                          const int (&b_row0)[TL::FN], int l32, int half) {
+  const uint16_t* As = buf;
+  const uint16_t* Bs = buf + TL::BM * LDS_PITCH;
 #pragma unroll
-      for (int f = 0; f < FN; ++f) dequant16(wc[f], (uint32_t)ws[f] * 0x10001u, blo[f], bhi[f]);
-    } else {
+  for (int c = 0; c < BK / 32; ++c) {
+    u32x4 a[TL::FM][2], b[TL::FN][2];
 #pragma unroll
-      for (int f = 0; f < FN; ++f) {
-        blo[f] = h8_of(*reinterpret_cast<const u32x4*>(wr[f].w16 + k0));
-        bhi[f] = h8_of(*reinterpret_cast<const u32x4*>(wr[f].w16 + k0 + 8));
-      }
+    for (int i = 0; i < TL::FM; ++i) {
+      const uint16_t* p = As + (a_row0 + 32 * i + l32) * LDS_PITCH + 32 * c + 16 * half;
+      a[i][0] = *reinterpret_cast<const u32x4*>(p);
+      a[i][1] = *reinterpret_cast<const u32x4*>(p + 8);
     }
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
+    for (int j = 0; j < TL::FN; ++j) {
+      const uint16_t* p = Bs + (b_row0[j] + l32) * LDS_PITCH + 32 * c + 16 * half;
+      b[j][0] = *reinterpret_cast<const u32x4*>(p);
+      b[j][1] = *reinterpret_cast<const u32x4*>(p + 8);
+    }
 #pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        acc.v[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(h8_of(xa[i][0]), blo[j], acc.v[i][j], 0, 0, 0);
-        acc.v[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(h8_of(xa[i][1]), bhi[j], acc.v[i][j], 0, 0, 0);
+    for (int i = 0; i < TL::FM; ++i)
+#pragma unroll
+      for (int j = 0; j < TL::FN; ++j) {
+        acc.v[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(h8_of(a[i][0]), h8_of(b[j][0]), acc.v[i][j], 0, 0, 0);
+        acc.v[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(h8_of(a[i][1]), h8_of(b[j][1]), acc.v[i][j], 0, 0, 0);
       }
+  }
+}
+
+// Whole K loop of a block.  K % 64 == 0; lds holds TL::LDS_ELEMS fp16.
+template <class TL, bool W8>
+__device__ __forceinline__ void block_mainloop(Acc<TL::FM, TL::FN>& acc, const Sources<TL, W8>& src,
+                                               int64_t K, int group, uint16_t* lds, int a_row0,
+                                               const int (&b_row0)[TL::FN]) {
+  const int t = threadIdx.x, lane = t & 63;
+  const int half = lane >> 5, l32 = lane & 31;
+#pragma unroll
+  for (int i = 0; i < TL::FM; ++i)
+#pragma unroll
+    for (int j = 0; j < TL::FN; ++j) acc.v[i][j] = (f32x16){};
+  Staged<TL, W8> st;
+  stage_load<TL, W8>(st, src, 0, group);
+  stage_store<TL, W8>(st, lds, t);
+  __syncthreads();
+  const int64_t nst = K / BK;
+  for (int64_t s = 0; s < nst; ++s) {
+    const int64_t kn = (s + 1 < nst ? s + 1 : s) * BK;  // clamped prefetch
+    stage_load<TL, W8>(st, src, kn, group);
+    stage_mma<TL>(acc, lds + (s & 1) * TL::LDS_HALF, a_row0, b_row0, l32, half);
+    stage_store<TL, W8>(st, lds + ((s + 1) & 1) * TL::LDS_HALF, t);
+    __syncthreads();
   }
 }
 
 // Row (within the 32-row fragment) of accumulator register r in lane half `half`.
 __device__ __forceinline__ int acc_row(int r, int half) { return 8 * (r / 4) + 4 * half + (r % 4); }
+
+// Block index -> tile index so that the blocks of one XCD (dispatched
+// round-robin over 8) take a contiguous range of tiles.
+__device__ __forceinline__ int64_t xcd_tile(int64_t b, int64_t nblocks) {
+  if (nblocks % 8 != 0) return b;
+  return (b % 8) * (nblocks / 8) + b / 8;
+}
 
 }  // namespace lemoq_gemm

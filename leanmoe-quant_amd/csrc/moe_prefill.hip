@@ -132,103 +132,112 @@ struct GroupedArgs {
   uint16_t* y;              // gate_up: act (P, F); down: (T * top_k, H)
 };
 
-// 2. gate_up: wave tile 64 pairs x 64 act columns (fragments 0,1 gate rows,
-// 2,3 the matching up rows), block 2 x 2 waves.
-__global__ __launch_bounds__(256) void moe_gate_up_kernel(const GroupedArgs a) {
-  constexpr int FM = 2, FN = 4, NH = FN / 2;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+// Grouped GEMM blocks: a 1-D grid over (column block nb, tile mt) numbered
+// nb-major, so consecutive blocks take consecutive tiles of the same column
+// block (usually the same expert, i.e. the same weight tile), and each XCD
+// takes a contiguous range of them.  Block tile 128 pairs x 128 weight rows
+// (the stage pipeline of gemm_core.h).
+using GTile = Tile<128, 128>;
+
+__device__ __forceinline__ bool grouped_tile(const GroupedArgs& a, int64_t ncol_blocks, int64_t max_tiles,
+                                             int64_t& nb, int& e, int64_t& rs, int64_t& re) {
+  const int64_t lin = xcd_tile(blockIdx.x, ncol_blocks * max_tiles);
+  nb = lin / max_tiles;
+  const int32_t* tl = a.tiles + 4 * (lin % max_tiles);
+  e = tl[0];
+  rs = tl[1];
+  re = tl[2];
+  return e >= 0;
+}
+
+// 2. gate_up: the block's 128 weight rows are 64 gate rows (act columns
+// n0 .. n0+63) and the 64 matching up rows, so wave (wm, wn) pairs gate rows
+// 32 wn .. 32 wn + 31 (fragment 0) with the same up rows (fragment 1).
+__global__ __launch_bounds__(256) void moe_gate_up_kernel(const GroupedArgs a, int64_t max_tiles) {
+  __shared__ __align__(16) uint16_t lds[GTile::LDS_ELEMS];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int half = lane >> 5, l32 = lane & 31;
-  const int32_t* tl = a.tiles + 4 * (int64_t)blockIdx.y;
-  const int e = tl[0];
-  if (e < 0) return;
-  const int64_t rs = tl[1], re = tl[2];
-  const int64_t m0 = rs + 64 * (wave >> 1);
-  const int64_t n0 = ((int64_t)blockIdx.x * 2 + (wave & 1)) * 32 * NH;
-  if (m0 >= re || n0 >= a.N) return;  // wave-uniform
-  const int64_t F = a.N, rows_e = 2 * F;
-  const uint16_t* xr[FM];
+  const int64_t F = a.N;
+  int64_t nb, rs, re;
+  int e;
+  if (!grouped_tile(a, (F + 63) / 64, max_tiles, nb, e, rs, re)) return;  // block-uniform
+  const int64_t n0 = nb * 64;
+  Sources<GTile, true> src;
 #pragma unroll
-  for (int f = 0; f < FM; ++f) {
-    int64_t m = m0 + 32 * f + l32;
+  for (int i = 0; i < GTile::A_CH; ++i) {
+    int64_t m = rs + GTile::a_row(t, i);
     m = m < re ? m : re - 1;
-    xr[f] = a.x + (int64_t)a.pair_tok[m] * a.K + 16 * half;
+    src.a[i] = a.x + (int64_t)a.pair_tok[m] * a.K + GTile::a_col(t, i);
   }
-  WRow wr[FN];
   const int64_t ng = a.K / a.group;
 #pragma unroll
-  for (int j = 0; j < FN; ++j) {
-    int64_t n = n0 + 32 * (j % NH) + l32;
+  for (int i = 0; i < GTile::B8_CH; ++i) {
+    const int r = GTile::b8_row(t, i);
+    int64_t n = n0 + (r & 63);
     n = n < F ? n : F - 1;
-    const int64_t row = (int64_t)e * rows_e + (j < NH ? n : F + n);
-    wr[j].codes = a.codes + row * a.K + 16 * half;
-    wr[j].scale = a.scale + row * ng;
-    wr[j].w16 = nullptr;
+    const int64_t row = (int64_t)e * 2 * F + (r < 64 ? n : F + n);
+    src.bc[i] = a.codes + row * a.K + GTile::b8_col(t, i);
+    src.bs[i] = a.scale + row * ng;
   }
-  Acc<FM, FN> acc;
-  acc_zero(acc);
-  mainloop<true>(acc, xr, wr, a.K, a.group);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int b_row0[2] = {32 * wn, 64 + 32 * wn};
+  Acc<2, 2> acc;
+  block_mainloop<GTile, true>(acc, src, a.K, a.group, lds, 64 * wm, b_row0);
+  const int64_t n = n0 + 32 * wn + l32;
 #pragma unroll
-  for (int i = 0; i < FM; ++i)
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < NH; ++j) {
-      const int64_t n = n0 + 32 * j + l32;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t m = m0 + 32 * i + acc_row(r, half);
-        if (m >= re || n >= F) continue;
-        const float g = h2f(f2h(acc.v[i][j][r]));
-        const float u = h2f(f2h(acc.v[i][j + NH][r]));
-        const float sg = h2f(f2h(g / (1.0f + expf(-g))));
-        a.y[m * F + n] = f2h(sg * u);
-      }
+    for (int r = 0; r < 16; ++r) {
+      const int64_t m = rs + 64 * wm + 32 * i + acc_row(r, half);
+      if (m >= re || n >= F) continue;
+      const float g = h2f(f2h(acc.v[i][0][r]));
+      const float u = h2f(f2h(acc.v[i][1][r]));
+      const float sg = h2f(f2h(g / (1.0f + expf(-g))));
+      a.y[m * F + n] = f2h(sg * u);
     }
 }
 
-// 3. down: wave tile 64 pairs x 64 hidden columns, block 2 x 2 waves.
-__global__ __launch_bounds__(256) void moe_down_kernel(const GroupedArgs a) {
-  constexpr int FM = 2, FN = 2;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+// 3. down: 128 pairs x 128 hidden columns per block.
+__global__ __launch_bounds__(256) void moe_down_kernel(const GroupedArgs a, int64_t max_tiles) {
+  __shared__ __align__(16) uint16_t lds[GTile::LDS_ELEMS];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int half = lane >> 5, l32 = lane & 31;
-  const int32_t* tl = a.tiles + 4 * (int64_t)blockIdx.y;
-  const int e = tl[0];
-  if (e < 0) return;
-  const int64_t rs = tl[1], re = tl[2];
-  const int64_t m0 = rs + 64 * (wave >> 1);
-  const int64_t n0 = ((int64_t)blockIdx.x * 2 + (wave & 1)) * 64;
-  if (m0 >= re || n0 >= a.N) return;  // wave-uniform
   const int64_t H = a.N;
-  const uint16_t* xr[FM];
+  int64_t nb, rs, re;
+  int e;
+  if (!grouped_tile(a, (H + 127) / 128, max_tiles, nb, e, rs, re)) return;  // block-uniform
+  const int64_t n0 = nb * 128;
+  Sources<GTile, true> src;
 #pragma unroll
-  for (int f = 0; f < FM; ++f) {
-    int64_t m = m0 + 32 * f + l32;
+  for (int i = 0; i < GTile::A_CH; ++i) {
+    int64_t m = rs + GTile::a_row(t, i);
     m = m < re ? m : re - 1;
-    xr[f] = a.x + m * a.K + 16 * half;
+    src.a[i] = a.x + m * a.K + GTile::a_col(t, i);
   }
-  WRow wr[FN];
   const int64_t ng = a.K / a.group;
 #pragma unroll
-  for (int j = 0; j < FN; ++j) {
-    int64_t n = n0 + 32 * j + l32;
+  for (int i = 0; i < GTile::B8_CH; ++i) {
+    int64_t n = n0 + GTile::b8_row(t, i);
     n = n < H ? n : H - 1;
     const int64_t row = (int64_t)e * H + n;
-    wr[j].codes = a.codes + row * a.K + 16 * half;
-    wr[j].scale = a.scale + row * ng;
-    wr[j].w16 = nullptr;
+    src.bc[i] = a.codes + row * a.K + GTile::b8_col(t, i);
+    src.bs[i] = a.scale + row * ng;
   }
-  Acc<FM, FN> acc;
-  acc_zero(acc);
-  mainloop<true>(acc, xr, wr, a.K, a.group);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int b_row0[2] = {64 * wn, 64 * wn + 32};
+  Acc<2, 2> acc;
+  block_mainloop<GTile, true>(acc, src, a.K, a.group, lds, 64 * wm, b_row0);
 #pragma unroll
-  for (int i = 0; i < FM; ++i)
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int64_t m = m0 + 32 * i + acc_row(r, half);
+      const int64_t m = rs + 64 * wm + 32 * i + acc_row(r, half);
       if (m >= re) continue;
       const float w = h2f(a.pair_w[m]);
       uint16_t* dst = a.y + (int64_t)a.pair_src[m] * H;
 #pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        const int64_t n = n0 + 32 * j + l32;
+      for (int j = 0; j < 2; ++j) {
+        const int64_t n = n0 + 64 * wn + 32 * j + l32;
         if (n >= H) continue;
         dst[n] = f2h(h2f(f2h(acc.v[i][j][r])) * w);
       }
@@ -288,8 +297,8 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __rest
 }
 
 bool grouped_shape_ok(int64_t K, int64_t N, int64_t group) {
-  return K > 0 && N > 0 && K % 32 == 0 && N % 32 == 0 && group > 0 && group % 32 == 0 && K % group == 0 &&
-         N <= 65535LL * 128;
+  return K > 0 && N > 0 && K % 64 == 0 && N % 32 == 0 && group > 0 && group % 64 == 0 && K % group == 0 &&
+         N <= (1LL << 24);
 }
 
 }  // namespace
@@ -316,13 +325,15 @@ extern "C" int lemoq_moe_prefill_gate_up(const uint16_t* x, int64_t H, const int
                                          const uint16_t* gu_scale, int64_t F, int64_t group, uint16_t* act,
                                          void* stream) {
   if (!x || !pair_tok || !tiles || !gu_codes || !gu_scale || !act) return LEMOQ_ERR_NULL;
-  if (!grouped_shape_ok(H, F, group) || max_tiles <= 0 || max_tiles > 65535) return LEMOQ_ERR_SHAPE;
+  if (!grouped_shape_ok(H, F, group) || max_tiles <= 0 || max_tiles > (1LL << 20)) return LEMOQ_ERR_SHAPE;
   if (!lemoq_aligned16(x) || !lemoq_aligned16(gu_codes)) return LEMOQ_ERR_ALIGN;
   GroupedArgs a{};
   a.x = x; a.pair_tok = pair_tok; a.tiles = tiles; a.codes = gu_codes; a.scale = gu_scale;
   a.K = H; a.N = F; a.group = (int)group; a.y = act;
-  const dim3 grid((unsigned)((F + 127) / 128), (unsigned)max_tiles);
-  hipLaunchKernelGGL(moe_gate_up_kernel, grid, dim3(256), 0, lemoq_stream(stream), a);
+  const int64_t blocks = ((F + 63) / 64) * max_tiles;
+  if (blocks > 0x7fffffffLL) return LEMOQ_ERR_SHAPE;
+  hipLaunchKernelGGL(moe_gate_up_kernel, dim3((unsigned)blocks), dim3(256), 0, lemoq_stream(stream), a,
+                     max_tiles);
   LEMOQ_CHECK_LAUNCH();
 }
 
@@ -331,13 +342,15 @@ extern "C" int lemoq_moe_prefill_down(const uint16_t* act, int64_t F, const int3
                                       const int8_t* dn_codes, const uint16_t* dn_scale, int64_t H,
                                       int64_t group, uint16_t* y, void* stream) {
   if (!act || !pair_src || !pair_w || !tiles || !dn_codes || !dn_scale || !y) return LEMOQ_ERR_NULL;
-  if (!grouped_shape_ok(F, H, group) || max_tiles <= 0 || max_tiles > 65535) return LEMOQ_ERR_SHAPE;
+  if (!grouped_shape_ok(F, H, group) || max_tiles <= 0 || max_tiles > (1LL << 20)) return LEMOQ_ERR_SHAPE;
   if (!lemoq_aligned16(act) || !lemoq_aligned16(dn_codes)) return LEMOQ_ERR_ALIGN;
   GroupedArgs a{};
   a.x = act; a.pair_src = pair_src; a.pair_w = pair_w; a.tiles = tiles; a.codes = dn_codes;
   a.scale = dn_scale; a.K = F; a.N = H; a.group = (int)group; a.y = y;
-  const dim3 grid((unsigned)((H + 127) / 128), (unsigned)max_tiles);
-  hipLaunchKernelGGL(moe_down_kernel, grid, dim3(256), 0, lemoq_stream(stream), a);
+  const int64_t blocks = ((H + 127) / 128) * max_tiles;
+  if (blocks > 0x7fffffffLL) return LEMOQ_ERR_SHAPE;
+  hipLaunchKernelGGL(moe_down_kernel, dim3((unsigned)blocks), dim3(256), 0, lemoq_stream(stream), a,
+                     max_tiles);
   LEMOQ_CHECK_LAUNCH();
 }
 

@@ -157,7 +157,7 @@ def dequant_gemm_separate(
     weight: each code is dequantised to ``fp16(code * scale)`` in registers,
     products accumulate in fp32, the output is rounded to fp16 once.  With
     ``residual`` (M, N) fp16, ``y = fp16(y + residual)``.  K must equal the
-    padded width (a multiple of 32 and of ``group_size``).
+    padded width (a multiple of 64 and of ``group_size``).
     """
     import torch  # noqa: PLC0415
 
@@ -169,8 +169,8 @@ def dequant_gemm_separate(
     g = int(group_size)
     if scale.dtype != torch.float16 or tuple(scale.shape) != (N, K // max(g, 1)) or not scale.is_contiguous():
         raise ValueError("scale must be contiguous fp16 (N, K/group), got %r" % (tuple(scale.shape),))
-    if g <= 0 or g % 32 != 0 or K % g != 0:
-        raise NotImplementedError("the matrix-core GEMM needs group_size % 32 == 0 and K % group_size == 0")
+    if g <= 0 or g % 64 != 0 or K % g != 0:
+        raise NotImplementedError("the matrix-core GEMM needs group_size % 64 == 0 and K % group_size == 0")
     _check_rows(x, K, "dequant_gemm_separate")
     M = int(x.shape[0])
     y = torch.empty((M, N), dtype=torch.float16, device=x.device)
@@ -193,8 +193,8 @@ def linear_f16(x: Any, weight: Any) -> Any:
     if weight.dim() != 2 or weight.dtype != torch.float16 or not weight.is_contiguous():
         raise ValueError("weight must be contiguous fp16 (N, K)")
     N, K = int(weight.shape[0]), int(weight.shape[1])
-    if K % 32 != 0:
-        raise NotImplementedError("linear_f16 needs K % 32 == 0, got %d" % K)
+    if K % 64 != 0:
+        raise NotImplementedError("linear_f16 needs K % 64 == 0, got %d" % K)
     _check_rows(x, K, "linear_f16")
     M = int(x.shape[0])
     y = torch.empty((M, N), dtype=torch.float16, device=x.device)
