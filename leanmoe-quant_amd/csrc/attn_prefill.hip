@@ -8,15 +8,19 @@
 // and accumulators; P is rounded to fp16 for the P V product (as flash
 // kernels do).
 //
-// Layout per wave: 32 queries; key tiles of 32.  S^T = K Q^T puts one query
-// per lane column (accumulator register r of lane l holds key
-// 8*(r/4) + 4*(l/32) + r%4, query l % 32), so the running max and sum of a
-// query are a lane-local reduction plus one exchange with lane l ^ 32, and
-// the probabilities are already the B operand of O^T = V^T P^T (with the key
-// order of that register layout used for the k index of both operands).  The
-// V tile is staged transposed in LDS (V^T rows of 32 keys); the K tile is
-// staged row-major.  A block of NW waves (32*NW queries) shares the tiles;
-// blocks are launched heaviest (latest queries) first.
+// Layout per wave: 32 queries.  S^T = K Q^T puts one query per lane column
+// (accumulator register r of lane l holds key 8*(r/4) + 4*(l/32) + r%4 of the
+// 32-key fragment, query l % 32), so the running max and sum of a query are a
+// lane-local reduction plus one exchange with lane l ^ 32, and the
+// probabilities are already the B operand of O^T = V^T P^T (with the key
+// order of that register layout used for the k index of both operands).
+//
+// A block of NW waves (32*NW queries) shares key tiles of KT = 8192 / D keys
+// staged in LDS: K row-major, V transposed (V^T rows of KT keys).  The tile
+// after the current one is loaded into registers before the current one is
+// used (V as 4-key x 8-dim sub-blocks, transposed in registers so the LDS
+// writes are 8 bytes wide) and written to the other half of a double buffer;
+// one barrier per tile.  Blocks are launched heaviest (latest queries) first.
 #include "common.h"
 
 namespace {
@@ -24,36 +28,106 @@ namespace {
 typedef _Float16 h8v __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int KT = 32;  // keys per tile
-
 __device__ __forceinline__ h8v h8_of(const u32x4 v) { return __builtin_bit_cast(h8v, v); }
 
 template <int D, int NW>
-__global__ __launch_bounds__(64 * NW) void attn_prefill_kernel(
+struct AttnGeom {
+  static constexpr int THREADS = 64 * NW;
+  static constexpr int QB = 32 * NW;               // queries per block
+  static constexpr int KT = 8192 / D;              // keys per tile
+  static constexpr int NS = KT / 32;               // S fragments per tile
+  static constexpr int DF = D / 32;                // output fragments
+  static constexpr int KP = D + 8;                 // K tile row pitch (fp16)
+  static constexpr int VP = KT + 8;                // V^T row pitch (fp16)
+  static constexpr int K_CH = KT * D / 8 / THREADS;        // 16-byte K chunks per thread
+  static constexpr int V_CH = (KT / 4) * (D / 8) / THREADS;  // 4 x 8 V sub-blocks per thread
+  static constexpr int HALF = KT * KP + D * VP;    // fp16 per LDS buffer
+  static_assert(K_CH >= 1 && V_CH >= 1, "tile split");
+};
+
+template <class G>
+struct AttnStage {
+  u32x4 k[G::K_CH];
+  u32x4 v[G::V_CH][4];
+};
+
+template <int D, int NW>
+__device__ __forceinline__ void attn_load(AttnStage<AttnGeom<D, NW>>& st, const uint16_t* __restrict__ kh,
+                                          const uint16_t* __restrict__ vh, int64_t k0, int64_t T, int t) {
+  using G = AttnGeom<D, NW>;
+#pragma unroll
+  for (int i = 0; i < G::K_CH; ++i) {
+    const int c = t + G::THREADS * i;
+    int64_t key = k0 + c / (D / 8);
+    key = key < T ? key : T - 1;
+    st.k[i] = *reinterpret_cast<const u32x4*>(kh + key * D + 8 * (c % (D / 8)));
+  }
+#pragma unroll
+  for (int i = 0; i < G::V_CH; ++i) {
+    const int c = t + G::THREADS * i;
+    const int kq = c / (D / 8), dq = c % (D / 8);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      int64_t key = k0 + 4 * kq + j;
+      key = key < T ? key : T - 1;
+      st.v[i][j] = *reinterpret_cast<const u32x4*>(vh + key * D + 8 * dq);
+    }
+  }
+}
+
+template <int D, int NW>
+__device__ __forceinline__ void attn_store(const AttnStage<AttnGeom<D, NW>>& st, uint16_t* buf, int t) {
+  using G = AttnGeom<D, NW>;
+  uint16_t* ks = buf;
+  uint16_t* vt = buf + G::KT * G::KP;
+#pragma unroll
+  for (int i = 0; i < G::K_CH; ++i) {
+    const int c = t + G::THREADS * i;
+    *reinterpret_cast<u32x4*>(ks + (c / (D / 8)) * G::KP + 8 * (c % (D / 8))) = st.k[i];
+  }
+#pragma unroll
+  for (int i = 0; i < G::V_CH; ++i) {
+    const int c = t + G::THREADS * i;
+    const int kq = c / (D / 8), dq = c % (D / 8);
+    const uint32_t v0[4] = {st.v[i][0].x, st.v[i][0].y, st.v[i][0].z, st.v[i][0].w};
+    const uint32_t v1[4] = {st.v[i][1].x, st.v[i][1].y, st.v[i][1].z, st.v[i][1].w};
+    const uint32_t v2[4] = {st.v[i][2].x, st.v[i][2].y, st.v[i][2].z, st.v[i][2].w};
+    const uint32_t v3[4] = {st.v[i][3].x, st.v[i][3].y, st.v[i][3].z, st.v[i][3].w};
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      // dims 2w and 2w+1 of keys 4kq .. 4kq+3
+      const uint2 lo = make_uint2(__builtin_amdgcn_perm(v1[w], v0[w], 0x05040100u),
+                                  __builtin_amdgcn_perm(v3[w], v2[w], 0x05040100u));
+      const uint2 hi = make_uint2(__builtin_amdgcn_perm(v1[w], v0[w], 0x07060302u),
+                                  __builtin_amdgcn_perm(v3[w], v2[w], 0x07060302u));
+      *reinterpret_cast<uint2*>(vt + (8 * dq + 2 * w) * G::VP + 4 * kq) = lo;
+      *reinterpret_cast<uint2*>(vt + (8 * dq + 2 * w + 1) * G::VP + 4 * kq) = hi;
+    }
+  }
+}
+
+template <int D, int NW>
+__device__ __forceinline__ void attn_prefill_body(
     const uint16_t* __restrict__ q, int64_t q_ld, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, int64_t kv_head_stride, int64_t T, float qk_scale,
     uint16_t* __restrict__ out, int64_t out_ld) {
-  constexpr int QB = 32 * NW;
-  constexpr int KP = D + 8;   // K tile row pitch (fp16): 16-byte pad
-  constexpr int VP = KT + 4;  // V^T row pitch (fp16): 8-byte pad
-  constexpr int DF = D / 32;  // output fragments (32 dims each)
-  __shared__ __align__(16) uint16_t ks[KT * KP];
-  __shared__ __align__(16) uint16_t vt[D * VP];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  using G = AttnGeom<D, NW>;
+  __shared__ __align__(16) uint16_t lds[2 * G::HALF];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int half = lane >> 5, l32 = lane & 31;
   const int h = blockIdx.y;
-  const int64_t nqb = (T + QB - 1) / QB;
-  const int64_t q0 = (nqb - 1 - (int64_t)blockIdx.x) * QB;
+  const int64_t nqb = (T + G::QB - 1) / G::QB;
+  const int64_t q0 = (nqb - 1 - (int64_t)blockIdx.x) * G::QB;
   const int64_t qw = q0 + 32 * wave;
   const int64_t qi = qw + l32;
   const int64_t qc = qi < T ? qi : T - 1;
 
   // Q^T operand: lane half h holds dims 32j + 16h + [0, 16) of its query.
-  h8v qf[DF][2];
+  h8v qf[G::DF][2];
   {
     const uint16_t* qp = q + qc * q_ld + (int64_t)h * D + 16 * half;
 #pragma unroll
-    for (int j = 0; j < DF; ++j) {
+    for (int j = 0; j < G::DF; ++j) {
       qf[j][0] = h8_of(*reinterpret_cast<const u32x4*>(qp + 32 * j));
       qf[j][1] = h8_of(*reinterpret_cast<const u32x4*>(qp + 32 * j + 8));
     }
@@ -62,75 +136,88 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_kernel(
   const uint16_t* vh = v + (int64_t)h * kv_head_stride;
 
   float m = -INFINITY, l = 0.0f;
-  f32x16 o[DF];
+  f32x16 o[G::DF];
 #pragma unroll
-  for (int f = 0; f < DF; ++f) o[f] = (f32x16){};
+  for (int f = 0; f < G::DF; ++f) o[f] = (f32x16){};
 
-  const int64_t kend = T < q0 + QB ? T : q0 + QB;
-  for (int64_t k0 = 0; k0 < kend; k0 += KT) {
-    __syncthreads();  // the previous tile has been read
-    for (int c = threadIdx.x; c < KT * D / 8; c += 64 * NW) {
-      const int kr = c / (D / 8), c8 = c - kr * (D / 8);
-      int64_t key = k0 + kr;
-      key = key < T ? key : T - 1;
-      const u32x4 kv = *reinterpret_cast<const u32x4*>(kh + key * D + c8 * 8);
-      const u32x4 vv = *reinterpret_cast<const u32x4*>(vh + key * D + c8 * 8);
-      *reinterpret_cast<u32x4*>(ks + kr * KP + c8 * 8) = kv;
-      const uint32_t w[4] = {vv.x, vv.y, vv.z, vv.w};
+  const int64_t kend = T < q0 + G::QB ? T : q0 + G::QB;
+  const int64_t ntile = (kend + G::KT - 1) / G::KT;
+  AttnStage<G> st;
+  attn_load<D, NW>(st, kh, vh, 0, T, t);
+  attn_store<D, NW>(st, lds, t);
+  __syncthreads();
+  for (int64_t it = 0; it < ntile; ++it) {
+    const int64_t k0 = it * G::KT;
+    const int64_t kn = (it + 1 < ntile ? it + 1 : it) * G::KT;  // clamped prefetch
+    attn_load<D, NW>(st, kh, vh, kn, T, t);
+    const uint16_t* ks = lds + (it & 1) * G::HALF;
+    const uint16_t* vt = ks + G::KT * G::KP;
+    if (k0 <= qw) {  // wave-uniform: the tile holds a key at or before every query of the wave
+      f32x16 s[G::NS];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        vt[(c8 * 8 + 2 * e) * VP + kr] = (uint16_t)(w[e] & 0xFFFFu);
-        vt[(c8 * 8 + 2 * e + 1) * VP + kr] = (uint16_t)(w[e] >> 16);
+      for (int sf = 0; sf < G::NS; ++sf) s[sf] = (f32x16){};
+      // the NS accumulation chains are interleaved (independent neighbours)
+#pragma unroll
+      for (int j = 0; j < G::DF; ++j)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+          for (int sf = 0; sf < G::NS; ++sf) {
+            const uint16_t* kp = ks + (32 * sf + l32) * G::KP + 32 * j + 16 * half + 8 * hh;
+            s[sf] = __builtin_amdgcn_mfma_f32_32x32x16_f16(h8_of(*reinterpret_cast<const u32x4*>(kp)), qf[j][hh],
+                                                           s[sf], 0, 0, 0);
+          }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int sf = 0; sf < G::NS; ++sf)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t key = k0 + 32 * sf + 8 * (r / 4) + 4 * half + (r % 4);
+          s[sf][r] = (key <= qi && key < T) ? s[sf][r] * qk_scale : -INFINITY;
+          mx = fmaxf(mx, s[sf][r]);
+        }
+      mx = fmaxf(mx, xor32_get(mx, lane));
+      // key k0 <= qw <= qi is valid for every query of the wave, so mn is finite
+      const float mn = fmaxf(m, mx);
+      const float alpha = exp2f(m - mn);
+      float ps = 0.0f;
+      h8v pb[2 * G::NS];
+#pragma unroll
+      for (int sf = 0; sf < G::NS; ++sf) {
+        uint32_t pk[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float p0 = exp2f(s[sf][2 * i] - mn), p1 = exp2f(s[sf][2 * i + 1] - mn);
+          ps += p0 + p1;
+          pk[i] = (uint32_t)f2h(p0) | ((uint32_t)f2h(p1) << 16);
+        }
+        pb[2 * sf] = h8_of((u32x4){pk[0], pk[1], pk[2], pk[3]});
+        pb[2 * sf + 1] = h8_of((u32x4){pk[4], pk[5], pk[6], pk[7]});
+      }
+      l = l * alpha + ps;
+      m = mn;
+      // rescale only when some query's running max moved (wave-uniform test)
+      if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
+#pragma unroll
+        for (int f = 0; f < G::DF; ++f)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o[f][r] *= alpha;
+      }
+#pragma unroll
+      for (int qq = 0; qq < 2 * G::NS; ++qq) {
+        const int kb = 32 * (qq / 2) + 16 * (qq % 2);
+#pragma unroll
+        for (int f = 0; f < G::DF; ++f) {
+          const uint16_t* vp = vt + (32 * f + l32) * G::VP + 4 * half + kb;
+          const uint2 a0 = *reinterpret_cast<const uint2*>(vp);
+          const uint2 a1 = *reinterpret_cast<const uint2*>(vp + 8);
+          o[f] = __builtin_amdgcn_mfma_f32_32x32x16_f16(h8_of((u32x4){a0.x, a0.y, a1.x, a1.y}), pb[qq], o[f], 0,
+                                                        0, 0);
+        }
       }
     }
+    attn_store<D, NW>(st, lds + ((it + 1) & 1) * G::HALF, t);
     __syncthreads();
-    if (k0 > qw) continue;  // wave-uniform: every key of the tile is after every query of the wave
-
-    // S^T (32 keys x 32 queries)
-    f32x16 s = (f32x16){};
-#pragma unroll
-    for (int j = 0; j < DF; ++j) {
-      const uint16_t* kp = ks + l32 * KP + 32 * j + 16 * half;
-      s = __builtin_amdgcn_mfma_f32_32x32x16_f16(h8_of(*reinterpret_cast<const u32x4*>(kp)), qf[j][0], s, 0, 0, 0);
-      s = __builtin_amdgcn_mfma_f32_32x32x16_f16(h8_of(*reinterpret_cast<const u32x4*>(kp + 8)), qf[j][1], s, 0,
-                                                 0, 0);
-    }
-    float x[16];
-    float mx = -INFINITY;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int64_t key = k0 + 8 * (r / 4) + 4 * half + (r % 4);
-      x[r] = (key <= qi && key < T) ? s[r] * qk_scale : -INFINITY;
-      mx = fmaxf(mx, x[r]);
-    }
-    mx = fmaxf(mx, xor32_get(mx, lane));
-    // key k0 <= qw <= qi is valid for every query, so mn is finite
-    const float mn = fmaxf(m, mx);
-    const float alpha = exp2f(m - mn);
-    float ps = 0.0f;
-    uint32_t pk[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float p0 = exp2f(x[2 * i] - mn), p1 = exp2f(x[2 * i + 1] - mn);
-      ps += p0 + p1;
-      pk[i] = (uint32_t)f2h(p0) | ((uint32_t)f2h(p1) << 16);
-    }
-    l = l * alpha + ps;
-    m = mn;
-    const h8v pb0 = h8_of((u32x4){pk[0], pk[1], pk[2], pk[3]});
-    const h8v pb1 = h8_of((u32x4){pk[4], pk[5], pk[6], pk[7]});
-#pragma unroll
-    for (int f = 0; f < DF; ++f) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[f][r] *= alpha;
-      const uint16_t* vp = vt + (32 * f + l32) * VP + 4 * half;
-      const uint2 a0 = *reinterpret_cast<const uint2*>(vp);
-      const uint2 a1 = *reinterpret_cast<const uint2*>(vp + 8);
-      const uint2 b0 = *reinterpret_cast<const uint2*>(vp + 16);
-      const uint2 b1 = *reinterpret_cast<const uint2*>(vp + 24);
-      o[f] = __builtin_amdgcn_mfma_f32_32x32x16_f16(h8_of((u32x4){a0.x, a0.y, a1.x, a1.y}), pb0, o[f], 0, 0, 0);
-      o[f] = __builtin_amdgcn_mfma_f32_32x32x16_f16(h8_of((u32x4){b0.x, b0.y, b1.x, b1.y}), pb1, o[f], 0, 0, 0);
-    }
   }
 
   const float lt = l + xor32_get(l, lane);
@@ -138,7 +225,7 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_kernel(
   if (qi >= T) return;
   uint16_t* op = out + qi * out_ld + (int64_t)h * D + 4 * half;
 #pragma unroll
-  for (int f = 0; f < DF; ++f)
+  for (int f = 0; f < G::DF; ++f)
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
       const uint32_t lo = (uint32_t)f2h(o[f][4 * b] * inv) | ((uint32_t)f2h(o[f][4 * b + 1] * inv) << 16);
@@ -147,13 +234,54 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_kernel(
     }
 }
 
+// Two waves per SIMD need at most 256 registers a lane: met without spills
+// for head_dim <= 128 with 4-wave blocks (two blocks fit the LDS of a CU).
+template <int D, int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) void attn_prefill_kernel_occ2(
+    const uint16_t* __restrict__ q, int64_t q_ld, const uint16_t* __restrict__ k,
+    const uint16_t* __restrict__ v, int64_t kv_head_stride, int64_t T, float qk_scale,
+    uint16_t* __restrict__ out, int64_t out_ld) {
+  attn_prefill_body<D, NW>(q, q_ld, k, v, kv_head_stride, T, qk_scale, out, out_ld);
+}
+
+template <int D, int NW>
+__global__ __launch_bounds__(64 * NW) void attn_prefill_kernel(
+    const uint16_t* __restrict__ q, int64_t q_ld, const uint16_t* __restrict__ k,
+    const uint16_t* __restrict__ v, int64_t kv_head_stride, int64_t T, float qk_scale,
+    uint16_t* __restrict__ out, int64_t out_ld) {
+  attn_prefill_body<D, NW>(q, q_ld, k, v, kv_head_stride, T, qk_scale, out, out_ld);
+}
+
+template <int D, int NW>
+void launch_attn(const uint16_t* q, int64_t q_ld, const uint16_t* k, const uint16_t* v, int64_t kv_head_stride,
+                 int64_t T, int64_t heads, float qk_scale, uint16_t* out, int64_t out_ld, hipStream_t st) {
+  const int64_t nqb = (T + 32 * NW - 1) / (32 * NW);
+  const dim3 grid((unsigned)nqb, (unsigned)heads);
+  if constexpr (D <= 128 && NW == 4)
+    hipLaunchKernelGGL((attn_prefill_kernel_occ2<D, NW>), grid, dim3(64 * NW), 0, st, q, q_ld, k, v,
+                       kv_head_stride, T, qk_scale, out, out_ld);
+  else
+    hipLaunchKernelGGL((attn_prefill_kernel<D, NW>), grid, dim3(64 * NW), 0, st, q, q_ld, k, v, kv_head_stride,
+                       T, qk_scale, out, out_ld);
+}
+
+template <int D>
+void launch_attn_d(const uint16_t* q, int64_t q_ld, const uint16_t* k, const uint16_t* v, int64_t kv_head_stride,
+                   int64_t T, int64_t heads, float qk_scale, uint16_t* out, int64_t out_ld, hipStream_t st) {
+  // 4 waves per block once that still gives a block per compute unit
+  if (((T + 127) / 128) * heads >= 256)
+    launch_attn<D, 4>(q, q_ld, k, v, kv_head_stride, T, heads, qk_scale, out, out_ld, st);
+  else
+    launch_attn<D, 2>(q, q_ld, k, v, kv_head_stride, T, heads, qk_scale, out, out_ld, st);
+}
+
 }  // namespace
 
 extern "C" int lemoq_attn_prefill_f16(const uint16_t* q, int64_t q_ld, const uint16_t* k, const uint16_t* v,
                                       int64_t kv_head_stride, int64_t T, int64_t heads, int64_t head_dim,
                                       float qk_scale, uint16_t* out, int64_t out_ld, void* stream) {
   if (!q || !k || !v || !out) return LEMOQ_ERR_NULL;
-  if (T <= 0 || heads <= 0 || heads > 65535) return LEMOQ_ERR_SHAPE;
+  if (T <= 0 || T > (1LL << 30) || heads <= 0 || heads > 65535) return LEMOQ_ERR_SHAPE;
   if (head_dim != 64 && head_dim != 128 && head_dim != 256) return LEMOQ_ERR_UNSUPPORTED;
   if (q_ld < heads * head_dim || out_ld < heads * head_dim || q_ld % 8 != 0 || out_ld % 4 != 0 ||
       kv_head_stride < T * head_dim || kv_head_stride % 8 != 0)
@@ -161,24 +289,11 @@ extern "C" int lemoq_attn_prefill_f16(const uint16_t* q, int64_t q_ld, const uin
   if (!lemoq_aligned16(q) || !lemoq_aligned16(k) || !lemoq_aligned16(v) ||
       (reinterpret_cast<uintptr_t>(out) & 7u) != 0)
     return LEMOQ_ERR_ALIGN;
-  constexpr int NW = 2;
-  const int64_t nqb = (T + 32 * NW - 1) / (32 * NW);
-  if (nqb > 0x7fffffffLL) return LEMOQ_ERR_SHAPE;
-  const dim3 grid((unsigned)nqb, (unsigned)heads);
   hipStream_t st = lemoq_stream(stream);
   switch (head_dim) {
-    case 64:
-      hipLaunchKernelGGL((attn_prefill_kernel<64, NW>), grid, dim3(64 * NW), 0, st, q, q_ld, k, v,
-                         kv_head_stride, T, qk_scale, out, out_ld);
-      break;
-    case 128:
-      hipLaunchKernelGGL((attn_prefill_kernel<128, NW>), grid, dim3(64 * NW), 0, st, q, q_ld, k, v,
-                         kv_head_stride, T, qk_scale, out, out_ld);
-      break;
-    default:
-      hipLaunchKernelGGL((attn_prefill_kernel<256, NW>), grid, dim3(64 * NW), 0, st, q, q_ld, k, v,
-                         kv_head_stride, T, qk_scale, out, out_ld);
-      break;
+    case 64: launch_attn_d<64>(q, q_ld, k, v, kv_head_stride, T, heads, qk_scale, out, out_ld, st); break;
+    case 128: launch_attn_d<128>(q, q_ld, k, v, kv_head_stride, T, heads, qk_scale, out, out_ld, st); break;
+    default: launch_attn_d<256>(q, q_ld, k, v, kv_head_stride, T, heads, qk_scale, out, out_ld, st); break;
   }
   LEMOQ_CHECK_LAUNCH();
 }

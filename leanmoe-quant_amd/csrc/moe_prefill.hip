@@ -36,33 +36,47 @@ constexpr int MAX_PAIRS = 32768;  // T * top_k held as bytes in LDS by moe_sort
 constexpr int MAX_EXPERTS = 255;  // expert ids are bytes; 255 marks an invalid id
 
 // ---------------------------------------------------------------------------
-// 1. sort.  One block per expert; each block builds the full histogram (the
-// ids are staged in LDS as bytes), derives its expert's pair offset and tile
-// offset, writes its tiles, and places its pairs: each thread owns a
-// contiguous run of pairs, counts its matches, and an exclusive scan over the
-// threads gives the stable positions.  Block 0 writes expert_off and marks the
-// unused tail of the tile table (expert -1).
+// 1. sort.  One block of 1024 threads per expert; each block stages the ids
+// in LDS as bytes and builds the full histogram (one private histogram per
+// wave, then summed), derives its expert's pair offset and tile offset, writes
+// its tiles, and places its pairs: each thread owns a contiguous run of
+// pairs (read 4 ids at a time), counts its matches, and an exclusive scan over
+// the threads gives the stable positions.  Block 0 writes expert_off and
+// marks the unused tail of the tile table (expert -1).
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void moe_sort_kernel(const int64_t* __restrict__ top_i,
-                                                       const float* __restrict__ top_w, int P,
-                                                       int top_k, int E, int32_t* __restrict__ pair_tok,
-                                                       int32_t* __restrict__ pair_src,
-                                                       uint16_t* __restrict__ pair_w,
-                                                       int32_t* __restrict__ expert_off,
-                                                       int32_t* __restrict__ tiles, int max_tiles) {
-  __shared__ uint8_t ids[MAX_PAIRS];
+constexpr int SORT_THREADS = 1024;
+constexpr int SORT_WAVES = SORT_THREADS / 64;
+
+__global__ __launch_bounds__(SORT_THREADS) void moe_sort_kernel(const int64_t* __restrict__ top_i,
+                                                                const float* __restrict__ top_w, int P,
+                                                                int top_k, int E, int32_t* __restrict__ pair_tok,
+                                                                int32_t* __restrict__ pair_src,
+                                                                uint16_t* __restrict__ pair_w,
+                                                                int32_t* __restrict__ expert_off,
+                                                                int32_t* __restrict__ tiles, int max_tiles) {
+  __shared__ __align__(16) uint8_t ids[MAX_PAIRS];
+  __shared__ int whist[SORT_WAVES][256];
   __shared__ int hist[256];
-  __shared__ int wave_tot[4];
+  __shared__ int wave_tot[SORT_WAVES];
   __shared__ int s_off, s_toff;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int me = blockIdx.x;
-  for (int i = tid; i < 256; i += 256) hist[i] = 0;
+  for (int i = lane; i < 256; i += 64) whist[wave][i] = 0;
   __syncthreads();
-  for (int p = tid; p < P; p += 256) {
+  for (int p = tid; p < P; p += SORT_THREADS) {
     const int64_t e = top_i[p];
     const bool ok = e >= 0 && e < E;
     ids[p] = ok ? (uint8_t)e : (uint8_t)255;
-    if (ok) atomicAdd(&hist[(int)e], 1);
+    if (ok) atomicAdd(&whist[wave][(int)e], 1);
+  }
+  // pad the byte array to a multiple of 4 with invalid ids
+  if (tid < 4 && P + tid < ((P + 3) & ~3)) ids[P + tid] = 255;
+  __syncthreads();
+  if (tid < 256) {
+    int c = 0;
+#pragma unroll
+    for (int w = 0; w < SORT_WAVES; ++w) c += whist[w][tid];
+    hist[tid] = c;
   }
   __syncthreads();
   if (tid == 0) {
@@ -87,18 +101,25 @@ __global__ __launch_bounds__(256) void moe_sort_kernel(const int64_t* __restrict
   __syncthreads();
   const int cnt = hist[me], off = s_off;
   const int ntiles = (cnt + TILE_ROWS - 1) / TILE_ROWS;
-  for (int i = tid; i < ntiles; i += 256) {
+  for (int i = tid; i < ntiles; i += SORT_THREADS) {
     int32_t* t = tiles + 4 * (s_toff + i);
     t[0] = me;
     t[1] = off + i * TILE_ROWS;
     t[2] = off + min(cnt, (i + 1) * TILE_ROWS);
     t[3] = 0;
   }
-  const int chunk = (P + 255) / 256;
-  const int beg = min(P, tid * chunk), end = min(P, beg + chunk);
+  // runs of a multiple of 4 pairs per thread
+  const int P4 = (P + 3) / 4;
+  const int chunk4 = (P4 + SORT_THREADS - 1) / SORT_THREADS;
+  const int beg4 = min(P4, tid * chunk4), end4 = min(P4, beg4 + chunk4);
+  const uint32_t* ids4 = reinterpret_cast<const uint32_t*>(ids);
+  const uint32_t mev = (uint32_t)me * 0x01010101u;
   int c = 0;
-  for (int p = beg; p < end; ++p) c += ids[p] == me;
-  // exclusive scan of c over the block: wave prefix, then wave totals
+  for (int i = beg4; i < end4; ++i) {
+    const uint32_t x = ids4[i] ^ mev;  // a zero byte marks a match
+#pragma unroll
+    for (int b = 0; b < 4; ++b) c += ((x >> (8 * b)) & 0xFFu) == 0u;
+  }
   int incl = c;
 #pragma unroll
   for (int d = 1; d < 64; d <<= 1) {
@@ -109,12 +130,17 @@ __global__ __launch_bounds__(256) void moe_sort_kernel(const int64_t* __restrict
   __syncthreads();
   int pos = off + incl - c;
   for (int w = 0; w < wave; ++w) pos += wave_tot[w];
-  for (int p = beg; p < end; ++p) {
-    if (ids[p] != me) continue;
-    pair_tok[pos] = p / top_k;
-    pair_src[pos] = p;
-    pair_w[pos] = f2h(top_w[p]);
-    ++pos;
+  for (int i = beg4; i < end4; ++i) {
+    const uint32_t x = ids4[i] ^ mev;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      if (((x >> (8 * b)) & 0xFFu) != 0u) continue;
+      const int p = 4 * i + b;
+      pair_tok[pos] = p / top_k;
+      pair_src[pos] = p;
+      pair_w[pos] = f2h(top_w[p]);
+      ++pos;
+    }
   }
 }
 
@@ -244,7 +270,9 @@ __global__ __launch_bounds__(256) void moe_down_kernel(const GroupedArgs a, int6
     }
 }
 
-// 4. combine: one block per token, 8 columns per thread.
+// 4. combine: one block per token, 8 columns per thread.  The slot loop has a
+// fixed trip count of 8 (slots past top_k read slot 0 and are not added), so
+// all of a thread's loads are issued before the first add.
 __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __restrict__ y,
                                                           const int64_t* __restrict__ top_i,
                                                           int top_k, int64_t H,
@@ -252,47 +280,56 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __rest
                                                           uint16_t* __restrict__ out) {
   const int64_t t = blockIdx.x;
   int64_t ids[8];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) ids[s] = top_i[t * top_k + (s < top_k ? s : 0)];
+  // slot of rank o in ascending expert id (slot order among equal ids), with
+  // static indexing only (a runtime index into ids would place it in scratch)
+  int rank[8];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    int r = 0;
+#pragma unroll
+    for (int s2 = 0; s2 < 8; ++s2) r += (s2 < top_k && (ids[s2] < ids[s] || (ids[s2] == ids[s] && s2 < s))) ? 1 : 0;
+    rank[s] = r;
+  }
   int order[8];
 #pragma unroll
-  for (int s = 0; s < 8; ++s) ids[s] = s < top_k ? top_i[t * top_k + s] : INT64_MAX;
-  // ascending expert id (slot order among equal ids)
-  bool used[8] = {false, false, false, false, false, false, false, false};
-#pragma unroll
   for (int o = 0; o < 8; ++o) {
-    int best = -1;
+    int slot = 0;
 #pragma unroll
-    for (int s = 0; s < 8; ++s)
-      if (s < top_k && !used[s] && (best < 0 || ids[s] < ids[best])) best = s;
-    order[o] = best < 0 ? 0 : best;
-    if (best >= 0) used[best] = true;
+    for (int s = 0; s < 8; ++s) slot = (s < top_k && rank[s] == o) ? s : slot;
+    order[o] = slot;
   }
   for (int64_t c = (int64_t)threadIdx.x * 8; c < H; c += 256 * 8) {
+    u32x4 v[8];
+#pragma unroll
+    for (int o = 0; o < 8; ++o) v[o] = *reinterpret_cast<const u32x4*>(y + (t * top_k + order[o]) * H + c);
+    u32x4 r = (u32x4){0u, 0u, 0u, 0u};
+    if (resid) r = *reinterpret_cast<const u32x4*>(resid + t * H + c);
+    LEMOQ_LOADS_ISSUED();
     float acc[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
-    for (int o = 0; o < top_k; ++o) {
-      const u32x4 v = *reinterpret_cast<const u32x4*>(y + (t * top_k + order[o]) * H + c);
-      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int o = 0; o < 8; ++o) {
+      const uint32_t w[4] = {v[o].x, v[o].y, v[o].z, v[o].w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        acc[2 * i] = h2f(f2h(acc[2 * i] + h2f((uint16_t)(w[i] & 0xFFFFu))));
-        acc[2 * i + 1] = h2f(f2h(acc[2 * i + 1] + h2f((uint16_t)(w[i] >> 16))));
+        const float lo = h2f(f2h(acc[2 * i] + h2f((uint16_t)(w[i] & 0xFFFFu))));
+        const float hi = h2f(f2h(acc[2 * i + 1] + h2f((uint16_t)(w[i] >> 16))));
+        acc[2 * i] = o < top_k ? lo : acc[2 * i];
+        acc[2 * i + 1] = o < top_k ? hi : acc[2 * i + 1];
       }
     }
-    uint32_t o[4];
-    if (resid) {
-      const u32x4 r = *reinterpret_cast<const u32x4*>(resid + t * H + c);
-      const uint32_t rw[4] = {r.x, r.y, r.z, r.w};
+    uint32_t ow[4];
+    const uint32_t rw[4] = {r.x, r.y, r.z, r.w};
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        o[i] = (uint32_t)hadd_round(acc[2 * i], (uint16_t)(rw[i] & 0xFFFFu)) |
-               ((uint32_t)hadd_round(acc[2 * i + 1], (uint16_t)(rw[i] >> 16)) << 16);
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        o[i] = (uint32_t)f2h(acc[2 * i]) | ((uint32_t)f2h(acc[2 * i + 1]) << 16);
+    for (int i = 0; i < 4; ++i) {
+      const uint16_t lo = resid ? hadd_round(acc[2 * i], (uint16_t)(rw[i] & 0xFFFFu)) : f2h(acc[2 * i]);
+      const uint16_t hi = resid ? hadd_round(acc[2 * i + 1], (uint16_t)(rw[i] >> 16)) : f2h(acc[2 * i + 1]);
+      ow[i] = (uint32_t)lo | ((uint32_t)hi << 16);
     }
-    *reinterpret_cast<u32x4*>(out + t * H + c) = (u32x4){o[0], o[1], o[2], o[3]};
+    *reinterpret_cast<u32x4*>(out + t * H + c) = (u32x4){ow[0], ow[1], ow[2], ow[3]};
   }
 }
 
@@ -314,7 +351,7 @@ extern "C" int lemoq_moe_prefill_sort(const int64_t* top_i, const float* top_w, 
   if (T <= 0 || top_k <= 0 || top_k > 8 || E <= 0 || E > MAX_EXPERTS || top_k > E) return LEMOQ_ERR_SHAPE;
   if (T * top_k > MAX_PAIRS) return LEMOQ_ERR_UNSUPPORTED;
   if (max_tiles < lemoq_moe_prefill_max_tiles(T * top_k, E) || max_tiles > 0x7fffffffLL) return LEMOQ_ERR_SHAPE;
-  hipLaunchKernelGGL(moe_sort_kernel, dim3((unsigned)E), dim3(256), 0, lemoq_stream(stream), top_i, top_w,
+  hipLaunchKernelGGL(moe_sort_kernel, dim3((unsigned)E), dim3(SORT_THREADS), 0, lemoq_stream(stream), top_i, top_w,
                      (int)(T * top_k), (int)top_k, (int)E, pair_tok, pair_src, pair_w, expert_off, tiles,
                      (int)max_tiles);
   LEMOQ_CHECK_LAUNCH();

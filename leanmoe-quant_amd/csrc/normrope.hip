@@ -90,18 +90,11 @@ __global__ __launch_bounds__(128) void rope_kernel(const uint16_t* __restrict__ 
 // sits in lane l ^ 32.  k and v heads are quantised to KV-INT8 at slot *pos
 // (amax / 127 scale, round-half-even codes; the arithmetic of
 // src/lemoq/kernels/kv_int8.py:196-216).
-//
-// Several rows (prefill): grid.y indexes the row; row r reads qkv row r,
-// writes q_out row r and cache slot pos0 + r (pos0 = *pos_ptr when pos_ptr is
-// non-NULL).  HF_ROPE selects the rounding of HF's apply_rotary_pos_emb,
-// which the reference's multi-token path takes (the fused RoPE only accepts
-// q_len == 1, src/lemoq/kernels/rope.py:140-177): fp16(fp16(x*cos) +
-// fp16(rotate_half(x)*sin)) instead of one rounding of the fp32 sum.
-template <int EPL, bool HF_ROPE>
+template <int EPL>
 __global__ __launch_bounds__(64) void qk_norm_rope_kv_kernel(
     const uint16_t* __restrict__ qkv, int heads, const uint16_t* __restrict__ qn_w,
     const uint16_t* __restrict__ kn_w, float eps, const uint16_t* __restrict__ cos_tab,
-    const uint16_t* __restrict__ sin_tab, const int64_t* __restrict__ pos_ptr, int64_t pos0,
+    const uint16_t* __restrict__ sin_tab, const int64_t* __restrict__ pos_ptr,
     uint16_t* __restrict__ q_out, int8_t* __restrict__ kc, uint16_t* __restrict__ ks,
     int8_t* __restrict__ vc, uint16_t* __restrict__ vs, int64_t code_head_stride, int64_t s_len,
     uint16_t* __restrict__ k_f16, uint16_t* __restrict__ v_f16, int64_t f16_head_stride,
@@ -111,11 +104,7 @@ __global__ __launch_bounds__(64) void qk_norm_rope_kv_kernel(
   const int which = blockIdx.x / heads;  // 0 q, 1 k, 2 v
   const int h = blockIdx.x - which * heads;
   const int HD = heads * D;
-  const int64_t row = blockIdx.y;
-  const int64_t pos = (pos_ptr ? pos_ptr[0] : pos0) + row;
-  qkv += row * 3 * HD;
-  q_out += row * HD;
-  if (k_rot_out) k_rot_out += row * HD;
+  const int64_t pos = pos_ptr[0];
   const bool pos_ok = pos >= 0 && pos < s_len;
   const uint16_t* src = qkv + (int64_t)which * HD;
   const int d0 = lane * EPL;
@@ -150,15 +139,7 @@ __global__ __launch_bounds__(64) void qk_norm_rope_kv_kernel(
     for (int i = 0; i < EPL; ++i) {
       const float xs = __shfl_xor(xn[i], 32, 64);
       const float xr = first ? -xs : xs;
-      if constexpr (HF_ROPE) {
-        // Three roundings; without this pragma the compiler narrows the
-        // products to fp16 multiplies and contracts one of them with the add
-        // into a single-rounding fma.
-#pragma clang fp contract(off)
-        o[i] = h2f(f2h(h2f(f2h(xn[i] * cv[i])) + h2f(f2h(xr * sv[i]))));
-      } else {
-        o[i] = h2f(f2h(xn[i] * cv[i] + xr * sv[i]));
-      }
+      o[i] = h2f(f2h(xn[i] * cv[i] + xr * sv[i]));
     }
     if (which == 0) {
 #pragma unroll
@@ -190,6 +171,102 @@ __global__ __launch_bounds__(64) void qk_norm_rope_kv_kernel(
     if (f16dst) f16dst[(int64_t)h * f16_head_stride + pos * D + d0 + i] = f2h(o[i]);
   }
   if (lane == 0) (which == 1 ? ks : vs)[(int64_t)h * s_len + pos] = f2h(s);
+}
+
+// Attention prologue of several prompt rows (prefill): one block per (row,
+// part) with part 0 q, 1 k, 2 v; thread t holds the 8 elements
+// [8t, 8t + 8) of the part's heads*D row (head 8t / D), so the RMSNorm over
+// heads*D is one block reduction and the RoPE partner d +- D/2 sits D/16
+// lanes away in the same wave.  q and k: q_norm/k_norm, then RoPE with HF's
+// rounding (fp16(fp16(x*cos) + fp16(rotate_half(x)*sin))); k and v: the fp16
+// row to the attention's cache and the KV-INT8 row (amax over the head's D/8
+// threads).  Threads past heads*D/8 (a block is whole waves) only take part
+// in the reductions, with zeros.
+template <int D>
+__global__ __launch_bounds__(1024) void qk_rows_kernel(
+    const uint16_t* __restrict__ qkv, int HD, const uint16_t* __restrict__ qn_w,
+    const uint16_t* __restrict__ kn_w, float eps, const uint16_t* __restrict__ cos_tab,
+    const uint16_t* __restrict__ sin_tab, int64_t pos0, uint16_t* __restrict__ q_out,
+    int8_t* __restrict__ kc, uint16_t* __restrict__ ks, int8_t* __restrict__ vc,
+    uint16_t* __restrict__ vs, int64_t code_head_stride, int64_t s_len, uint16_t* __restrict__ k_f16,
+    uint16_t* __restrict__ v_f16, int64_t f16_head_stride) {
+  __shared__ float red[16];
+  const int t = threadIdx.x, lane = t & 63;
+  const int64_t row = blockIdx.x;
+  const int part = blockIdx.y;
+  const int64_t pos = pos0 + row;
+  const bool active = 8 * t < HD;
+  const int e0 = active ? 8 * t : 0;
+  const int h = e0 / D, d0 = e0 % D;
+  const uint16_t* src = qkv + row * 3 * HD + (int64_t)part * HD;
+  const u32x4 raw = *reinterpret_cast<const u32x4*>(src + e0);
+  const uint32_t rw[4] = {raw.x, raw.y, raw.z, raw.w};
+  float o[8];
+  if (part < 2) {
+    const uint16_t* nw = part == 0 ? qn_w : kn_w;
+    const u32x4 wv = *reinterpret_cast<const u32x4*>(nw + e0);
+    const u32x4 cv = *reinterpret_cast<const u32x4*>(cos_tab + pos * D + d0);
+    const u32x4 sv = *reinterpret_cast<const u32x4*>(sin_tab + pos * D + d0);
+    float ssq = active ? ssq_f16x8(raw, 0.0f) : 0.0f;
+    ssq = wave_sum(ssq);
+    if (lane == 0) red[t >> 6] = ssq;
+    __syncthreads();
+    float tot = 0.0f;
+    for (int w = 0; w < (int)(blockDim.x >> 6); ++w) tot += red[w];
+    const float rstd = 1.0f / sqrtf(tot / (float)HD + eps);
+    const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
+    const uint32_t cw[4] = {cv.x, cv.y, cv.z, cv.w};
+    const uint32_t sw[4] = {sv.x, sv.y, sv.z, sv.w};
+    const bool first = d0 < D / 2;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint16_t xb = (uint16_t)(rw[i / 2] >> (16 * (i & 1)));
+      const uint16_t wb = (uint16_t)(ww[i / 2] >> (16 * (i & 1)));
+      const float xn = h2f(f2h(h2f(f2h(h2f(xb) * rstd)) * h2f(wb)));
+      const float xs = __shfl_xor(xn, D / 16, 64);
+      const float c = h2f((uint16_t)(cw[i / 2] >> (16 * (i & 1))));
+      const float sn = h2f((uint16_t)(sw[i / 2] >> (16 * (i & 1))));
+      const float xr = first ? -xs : xs;
+      {
+        // Three roundings; without this pragma the compiler narrows the
+        // products to fp16 multiplies and contracts one of them with the add
+        // into a single-rounding fma.
+#pragma clang fp contract(off)
+        o[i] = h2f(f2h(h2f(f2h(xn * c)) + h2f(f2h(xr * sn))));
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = h2f((uint16_t)(rw[i / 2] >> (16 * (i & 1))));
+  }
+  uint32_t packed[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) packed[i] = (uint32_t)f2h(o[2 * i]) | ((uint32_t)f2h(o[2 * i + 1]) << 16);
+  const u32x4 ov = (u32x4){packed[0], packed[1], packed[2], packed[3]};
+  if (part == 0) {
+    if (active) *reinterpret_cast<u32x4*>(q_out + row * HD + e0) = ov;
+    return;
+  }
+  // KV-INT8 row of this head: amax over the head's D/8 threads
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(o[i]));
+#pragma unroll
+  for (int d = 1; d < D / 8; d <<= 1) amax = fmaxf(amax, __shfl_xor(amax, d, 64));
+  const float sc = amax > 0.0f ? amax / 127.0f : 1.0f;
+  uint32_t cw2[2] = {0u, 0u};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float qv = rintf(o[i] / sc);
+    qv = fminf(fmaxf(qv, -127.0f), 127.0f);
+    cw2[i / 4] |= ((uint32_t)(uint8_t)(int8_t)(int)qv) << (8 * (i % 4));
+  }
+  if (!active) return;
+  int8_t* cdst = (part == 1 ? kc : vc) + (int64_t)h * code_head_stride + pos * D + d0;
+  *reinterpret_cast<uint2*>(cdst) = make_uint2(cw2[0], cw2[1]);
+  uint16_t* fdst = part == 1 ? k_f16 : v_f16;
+  if (fdst) *reinterpret_cast<u32x4*>(fdst + (int64_t)h * f16_head_stride + pos * D + d0) = ov;
+  if (d0 == 0) (part == 1 ? ks : vs)[(int64_t)h * s_len + pos] = f2h(sc);
 }
 
 }  // namespace
@@ -248,10 +325,9 @@ extern "C" int lemoq_qk_norm_rope_kv_i8(const uint16_t* qkv, int64_t heads, int6
   const dim3 grid((unsigned)(3 * heads));
   hipStream_t st = lemoq_stream(stream);
 #define LEMOQ_QK_CASE(EE)                                                                       \
-  hipLaunchKernelGGL((qk_norm_rope_kv_kernel<EE, false>), grid, dim3(64), 0, st, qkv,           \
-                     (int)heads, q_norm_w, k_norm_w, eps, cos_tab, sin_tab, pos, (int64_t)0,   \
-                     q_out, kc, ks, vc, vs, code_head_stride, s_len, k_f16, v_f16,              \
-                     f16_head_stride, k_rot_out);
+  hipLaunchKernelGGL((qk_norm_rope_kv_kernel<EE>), grid, dim3(64), 0, st, qkv, (int)heads,     \
+                     q_norm_w, k_norm_w, eps, cos_tab, sin_tab, pos, q_out, kc, ks, vc, vs,    \
+                     code_head_stride, s_len, k_f16, v_f16, f16_head_stride, k_rot_out);
   switch (head_dim) {
     case 64: LEMOQ_QK_CASE(1) break;
     case 128: LEMOQ_QK_CASE(2) break;
@@ -279,18 +355,25 @@ extern "C" int lemoq_qk_norm_rope_kv_i8_rows(const uint16_t* qkv, int64_t rows, 
   if (s_len <= 0 || code_head_stride < s_len * head_dim) return LEMOQ_ERR_SHAPE;
   if ((k_f16 || v_f16) && f16_head_stride < s_len * head_dim) return LEMOQ_ERR_SHAPE;
   // every row's slot must exist: the cos/sin tables and the caches hold s_len positions
-  if (rows <= 0 || rows > 65535 || pos0 < 0 || pos0 + rows > s_len) return LEMOQ_ERR_SHAPE;
-  const dim3 grid((unsigned)(3 * heads), (unsigned)rows);
+  if (rows <= 0 || rows > 0x7fffffffLL || pos0 < 0 || pos0 + rows > s_len) return LEMOQ_ERR_SHAPE;
+  const int64_t HD = heads * head_dim;
+  if (HD % 8 != 0 || HD / 8 > 1024) return LEMOQ_ERR_SHAPE;
+  if (!lemoq_aligned16(q_norm_w) || !lemoq_aligned16(k_norm_w) || !lemoq_aligned16(cos_tab) ||
+      !lemoq_aligned16(sin_tab) || !lemoq_aligned16(q_out) || (k_f16 && !lemoq_aligned16(k_f16)) ||
+      (v_f16 && !lemoq_aligned16(v_f16)) || (reinterpret_cast<uintptr_t>(kc) & 7u) ||
+      (reinterpret_cast<uintptr_t>(vc) & 7u) || code_head_stride % 8 != 0 || f16_head_stride % 8 != 0)
+    return LEMOQ_ERR_ALIGN;
+  const unsigned threads = (unsigned)(((HD / 8) + 63) / 64 * 64);
+  const dim3 grid((unsigned)rows, 3u);
   hipStream_t st = lemoq_stream(stream);
-#define LEMOQ_QK_ROWS_CASE(EE)                                                                  \
-  hipLaunchKernelGGL((qk_norm_rope_kv_kernel<EE, true>), grid, dim3(64), 0, st, qkv,            \
-                     (int)heads, q_norm_w, k_norm_w, eps, cos_tab, sin_tab,                     \
-                     (const int64_t*)nullptr, pos0, q_out, kc, ks, vc, vs, code_head_stride,    \
-                     s_len, k_f16, v_f16, f16_head_stride, (uint16_t*)nullptr);
+#define LEMOQ_QK_ROWS_CASE(DD)                                                                  \
+  hipLaunchKernelGGL((qk_rows_kernel<DD>), grid, dim3(threads), 0, st, qkv, (int)HD, q_norm_w,   \
+                     k_norm_w, eps, cos_tab, sin_tab, pos0, q_out, kc, ks, vc, vs,              \
+                     code_head_stride, s_len, k_f16, v_f16, f16_head_stride);
   switch (head_dim) {
-    case 64: LEMOQ_QK_ROWS_CASE(1) break;
-    case 128: LEMOQ_QK_ROWS_CASE(2) break;
-    default: LEMOQ_QK_ROWS_CASE(4) break;
+    case 64: LEMOQ_QK_ROWS_CASE(64) break;
+    case 128: LEMOQ_QK_ROWS_CASE(128) break;
+    default: LEMOQ_QK_ROWS_CASE(256) break;
   }
 #undef LEMOQ_QK_ROWS_CASE
   LEMOQ_CHECK_LAUNCH();
