@@ -12,8 +12,9 @@ Printed: ONE JSON line on stdout.  ``value`` is ms/token at ``--ctx`` (wall
 clock over exactly ``--steps`` replays, synchronised on both sides, after
 ``--warmup`` replays); the line also carries the second context, the step's
 HBM roofline fraction, per-kernel cold timings, the dominant kernel's roofline
-(``roofline``) and the CPU oracle's ms/token on this host (``cpu_baseline``).
-Progress goes to stderr.
+(``roofline``), the CPU oracle's ms/token on this host (``cpu_baseline``) and,
+per context, the batched prefill's TTFT with E2E-32/128 beside the
+reference's published values (``prefill``).  Progress goes to stderr.
 
 ``--mode kernels`` runs only the weights + isolated kernel timings.
 ``--mode traffic`` is the short form profiled under ``rocprofv3 --pmc``: a
@@ -22,6 +23,10 @@ a synthetic KV cache at ``--ctx`` (no prefill); it prints the dispatch plan.
 ``--summarize-pmc FETCH_CSV WRITE_CSV PLAN_JSON`` (CPU only) turns the two
 counter passes into per-kernel HBM bytes per launch: profiles/traffic.json,
 which fills ``roofline.traffic``, and a markdown table beside it.
+``--mode prefill`` times only the batched prefill (TTFT) at ``--ctx`` (and
+``--ctx2``); ``--summarize-prefill TRACE_CSV --ctx T`` (CPU only) turns a
+``rocprofv3 --kernel-trace`` of it into a per-kernel table with each kernel's
+FLOP rate against the MI355X dense fp16 matrix peak.
 """
 
 from __future__ import annotations
@@ -41,7 +46,11 @@ for _p in (REPO, PKG):
 
 METRIC = "ms/token decode step, OLMoE-shape w8a16+KV-INT8 @ctx1024/4096; % HBM roofline"
 HBM_PEAK_GBS = 8000.0  # MI355X published HBM3E bandwidth
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X published dense fp16 matrix peak
 REFERENCE_RTX5090_MS = {"1024": 1.4602, "4096": 1.6075}  # README_EN.md:71 (not this hardware)
+# Canonical-cell TTFT p50 and E2E-32 of the reference (RESULTS.md:136-141, RTX 5090, not this hardware).
+REFERENCE_RTX5090_TTFT_MS = {"1024": 84.4366, "4096": 158.3072}
+REFERENCE_RTX5090_E2E32_MS = {"1024": 131.16, "4096": 209.75}
 KV_BYTES_PER_TOKEN_LAYER = 16 * (128 + 2) * 2  # 16 heads x (128 codes + fp16 scale) x (K, V)
 
 
@@ -65,8 +74,10 @@ def parse_args(argv=None):
     ap.add_argument("--cpu-budget-s", type=float, default=20.0)
     ap.add_argument("--cpu-check-steps", type=int, default=32)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--mode", choices=("full", "kernels", "traffic"), default="full")
+    ap.add_argument("--mode", choices=("full", "kernels", "traffic", "prefill"), default="full")
     ap.add_argument("--summarize-pmc", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "PLAN_JSON"))
+    ap.add_argument("--summarize-prefill", metavar="KERNEL_TRACE_CSV",
+                    help="per-kernel table of the prefills in a rocprofv3 kernel trace of --mode prefill at --ctx")
     ap.add_argument("--profiles-dir", default=os.path.join(REPO, "profiles"))
     return ap.parse_args(argv)
 
@@ -216,14 +227,33 @@ def kernel_table(torch, hip, w, sess, flusher, reps: int) -> dict:
 # ---------------------------------------------------------------------------
 # decode timing
 # ---------------------------------------------------------------------------
+def measure_prefill(torch, sess, warmup: int = 2, timed: int = 7) -> dict:
+    """TTFT as the reference measures it (``_measure_static_prefill``,
+    ``benchmarks/runner.py:1045-1064``): wall time of a whole prefill (cache
+    reset, the batched forward of the prompt, greedy pick of the seed token)
+    between device synchronisations; ``warmup`` untimed, p50 of ``timed``.
+    Leaves the session prefilled."""
+    for _ in range(warmup):
+        sess.prefill()
+    torch.cuda.synchronize()
+    samples = []
+    for _ in range(timed):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        sess.prefill()
+        torch.cuda.synchronize()
+        samples.append((time.perf_counter() - t0) * 1e3)
+    samples.sort()
+    return {"p50": samples[len(samples) // 2], "min": samples[0], "max": samples[-1], "runs": timed}
+
+
 def time_decode(torch, w, ctx: int, steps: int, warmup: int, extra: int):
     from lemoq.model.olmoe import DecodeSession
 
     sess = DecodeSession(w, [1] * ctx, max_new_tokens=warmup + 2 * steps + extra + 4)
     sess.capture()
-    t = time.time()
-    sess.prefill()
-    log("ctx %d: prefill (%d graph replays) %.2fs" % (ctx, ctx, time.time() - t))
+    ttft = measure_prefill(torch, sess)
+    log("ctx %d: batched prefill (TTFT) p50 %.3f ms over %d runs" % (ctx, ttft["p50"], ttft["runs"]))
     for _ in range(warmup):
         sess.graph.replay()
     torch.cuda.synchronize()
@@ -260,6 +290,7 @@ def time_decode(torch, w, ctx: int, steps: int, warmup: int, extra: int):
         "launches_per_step": sess.launches_per_step,
         "step_ms_p50": p50,
         "step_ms_p99": p99,
+        "ttft": ttft,
     }
     log("ctx %d: %.4f ms/token wall, %.4f device, %d steps; per-step p50 %.4f p99 %.4f ms"
         % (ctx, res["ms_per_token"], res["device_ms_per_token"], steps, p50, p99))
@@ -499,6 +530,9 @@ def main(argv=None) -> int:
         r = summarize_pmc(*args.summarize_pmc, out_dir=args.profiles_dir)
         print(r["table"])
         return 0
+    if args.summarize_prefill:
+        print(summarize_prefill(args.summarize_prefill, args.ctx))
+        return 0
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (the batch-1 decode "
@@ -532,6 +566,19 @@ def main(argv=None) -> int:
         cal = copy_calibration(torch, _hip, flusher)
         kt = kernel_table(torch, _hip, w, sess, flusher, args.kernel_reps)
         print(json.dumps({"mode": "traffic", "ctx": args.ctx, "calibration": cal, "kernels": kt}))
+        return 0
+
+    if args.mode == "prefill":
+        from lemoq.model.olmoe import DecodeSession
+
+        res = {"mode": "prefill"}
+        for ctx in [c for c in (args.ctx, args.ctx2) if c]:
+            sess = DecodeSession(w, [1] * ctx, max_new_tokens=2)
+            sess.capture()
+            res["ctx%d" % ctx] = measure_prefill(torch, sess)
+            log("ctx %d: TTFT p50 %.3f ms" % (ctx, res["ctx%d" % ctx]["p50"]))
+            del sess
+        print(json.dumps(res))
         return 0
 
     if args.mode == "kernels":
@@ -618,6 +665,7 @@ def main(argv=None) -> int:
     }
     line["attention_configs"] = cfg
     line["step_ms_p50"], line["step_ms_p99"] = r1["step_ms_p50"], r1["step_ms_p99"]
+    line["prefill"] = _prefill_summary(r1, r2)
     if r2 is not None:
         line["ctx2"] = r2
         line["ms_per_token_ctx%d" % args.ctx2] = r2["ms_per_token"]
@@ -628,6 +676,88 @@ def main(argv=None) -> int:
     print(json.dumps(line))
     sys.stdout.flush()
     return 0
+
+
+# Launch order of one batched prefill (lemoq.model.prefill.prefill_prompt):
+# gather, 16 x [12 launches], final norm, lm_head GEMM, then the greedy pick.
+PREFILL_LAYER_ROLES = ("rmsnorm (input)", "gemm_w8 qkv", "qk_rows (q/k norm, RoPE, KV-INT8)", "attn_prefill",
+                       "gemm_w8 o_proj (+residual)", "rmsnorm (post-attention)", "gemm_f16 router",
+                       "route_topk", "moe_prefill_sort", "moe_prefill_gate_up", "moe_prefill_down",
+                       "moe_prefill_combine (+residual)")
+
+
+def prefill_flops(role: str, T: int, shape=None) -> float:
+    """Algorithmic FLOPs of one launch of a prefill role at prompt length T (OLMoE-1B-7B)."""
+    H, NH, D, E, K, F, V = 2048, 16, 128, 64, 8, 1024, 50304
+    return {
+        "gemm_w8 qkv": 2.0 * T * 3 * NH * D * H,
+        "gemm_w8 o_proj (+residual)": 2.0 * T * H * NH * D,
+        "gemm_f16 router": 2.0 * T * E * H,
+        "attn_prefill": 4.0 * NH * D * T * (T + 1) / 2,
+        "moe_prefill_gate_up": 2.0 * T * K * 2 * F * H,
+        "moe_prefill_down": 2.0 * T * K * H * F,
+        "gemm_w8 lm_head (last row)": 2.0 * V * H,
+    }.get(role, 0.0)
+
+
+def summarize_prefill(trace_csv: str, ctx: int) -> str:
+    """Markdown table of the prefills found in a rocprofv3 kernel trace: each prefill
+    starts at a gather_rows dispatch; roles follow PREFILL_LAYER_ROLES."""
+    import csv as _csv
+
+    rows = sorted(_csv.DictReader(open(trace_csv)), key=lambda r: int(r["Start_Timestamp"]))
+    starts = [i for i, r in enumerate(rows) if "gather_rows_kernel" in r["Kernel_Name"]]
+    per_role: dict = {}
+    n_layers = 16
+    total = []
+    for st in starts:
+        seq = rows[st: st + 1 + 12 * n_layers + 3]
+        if len(seq) < 1 + 12 * n_layers + 3:
+            continue
+        roles = ["gather_rows"] + [PREFILL_LAYER_ROLES[j % 12] for j in range(12 * n_layers)] + [
+            "rmsnorm (final)", "gemm_w8 lm_head (last row)", "argmax_advance"]
+        for role, r in zip(roles, seq):
+            per_role.setdefault(role, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-3)
+        total.append((int(seq[-1]["End_Timestamp"]) - int(seq[0]["Start_Timestamp"])) * 1e-3)
+    n = len(total)
+    if not n:
+        return "no complete prefill found in %s" % trace_csv
+    out = ["| role | launches per prefill | avg us | ms per prefill | share %% | GFLOP per launch | TF/s | %% of %.0f TF/s |"
+           % MFMA_F16_PEAK_TFLOPS, "|---|---|---|---|---|---|---|---|"]
+    span = sum(total) / n
+    busy = sum(sum(v) for v in per_role.values()) / n
+    for role, v in sorted(per_role.items(), key=lambda kv: -sum(kv[1])):
+        launches = len(v) // n
+        avg = sum(v) / len(v)
+        fl = prefill_flops(role, ctx)
+        tf = fl / (avg * 1e-6) / 1e12 if fl else 0.0
+        out.append("| %s | %d | %.2f | %.3f | %.1f | %s | %s | %s |" % (
+            role, launches, avg, sum(v) / n / 1e3, 100.0 * sum(v) / n / busy, "%.2f" % (fl / 1e9) if fl else "-",
+            "%.1f" % tf if fl else "-", "%.1f" % (100 * tf / MFMA_F16_PEAK_TFLOPS) if fl else "-"))
+    out.append("")
+    out.append("%d prefills of %d tokens; kernel time %.3f ms per prefill, first launch start to last launch "
+               "end %.3f ms (the gaps are launch and host overhead)." % (n, ctx, busy / 1e3, span / 1e3))
+    return "\n".join(out)
+
+
+def _prefill_summary(*runs) -> dict:
+    """TTFT p50 and E2E(N) = TTFT + N x per-token (the reference's composition,
+    RESULTS.md:133-141) per context, beside the reference's published values."""
+    out = {}
+    for r in runs:
+        if r is None:
+            continue
+        c = str(r["ctx"])
+        ttft = r["ttft"]["p50"]
+        out["ctx" + c] = {
+            "ttft_ms_p50": ttft,
+            "ttft_ms_min": r["ttft"]["min"],
+            "e2e_32_ms": ttft + 32 * r["ms_per_token"],
+            "e2e_128_ms": ttft + 128 * r["ms_per_token"],
+            "reference_rtx5090_ttft_ms": REFERENCE_RTX5090_TTFT_MS.get(c),
+            "reference_rtx5090_e2e_32_ms": REFERENCE_RTX5090_E2E32_MS.get(c),
+        }
+    return out
 
 
 class _Cap:

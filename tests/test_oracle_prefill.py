@@ -168,3 +168,20 @@ def test_prefill_kv_cache_layout_matches_the_stepped_cache():
     for li in range(SHAPE.layers):
         assert torch.equal(kv[li]["kc"][:, N_POS:], torch.zeros_like(kv[li]["kc"][:, N_POS:]))
         assert torch.equal(kv[li]["ks"][:, N_POS:], torch.ones_like(kv[li]["ks"][:, N_POS:]))
+
+
+def test_separate_arm_weight_is_one_rounding_of_the_exact_product():
+    """code (8 bits) x fp16 scale (11 significant bits) fits fp32 exactly, so the reference's
+    ``dequantized_weight(dtype=fp16)`` (fp32 product, then ``.to(fp16)``) rounds once."""
+    g = torch.Generator().manual_seed(21)
+    codes = torch.randint(-128, 128, (64, 256), generator=g, dtype=torch.int8)
+    scale = (torch.rand((64, 2), generator=g) * 1e-2 + 1e-5).to(torch.float16)
+    w32 = ops.dequant_w8(codes, scale, 128)
+    w64 = codes.double() * scale.double().repeat_interleave(128, 1)
+    assert torch.equal(w32.double(), w64)
+    assert torch.equal(ops.dequant_weight_f16(codes, scale, 128), w64.to(torch.float16))
+    # and the separate arm differs from the fused arm's single fp32 rounding of the sum
+    x = torch.randn((3, 256), generator=g).to(torch.float16)
+    sep = ops.linear_separate_w8(x, codes, scale, 128).double()
+    ref = x.double() @ w64.t()
+    assert float((sep - ref).abs().max()) < 2e-2 * float(ref.abs().max())
