@@ -428,6 +428,15 @@ int lemoq_gemm_w8(const uint16_t* x, int64_t M, int64_t K, int64_t x_ld, const i
 int lemoq_gemm_f16(const uint16_t* x, int64_t M, int64_t K, int64_t x_ld, const uint16_t* w,
                    int64_t N, uint16_t* y, int64_t y_ld, void* stream);
 
+/* lemoq_gemm_f16 for narrow outputs (the 64-expert router): K is cut into
+ * `splits` ranges (K % (64 * splits) == 0, splits <= 64), each range's fp32
+ * partial goes to workspace ((splits, M, N) fp32, 16-byte aligned, caller-
+ * owned), and a second launch sums the partials in range order and rounds
+ * once to fp16.  splits == 1 is lemoq_gemm_f16 (workspace unused). */
+int lemoq_gemm_f16_splitk(const uint16_t* x, int64_t M, int64_t K, int64_t x_ld, const uint16_t* w,
+                          int64_t N, uint16_t* y, int64_t y_ld, int64_t splits, float* workspace,
+                          void* stream);
+
 /* Embedding lookup of several tokens (HF embed_tokens on the prompt):
  * dst[r] = src[ids[r]] for r < rows, a zero row for an id outside
  * [0, n_rows).  src (n_rows, H) fp16, dst (rows, H); H % 8 == 0, 16-byte

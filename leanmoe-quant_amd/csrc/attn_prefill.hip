@@ -15,8 +15,11 @@
 // probabilities are already the B operand of O^T = V^T P^T (with the key
 // order of that register layout used for the k index of both operands).
 //
-// A block of NW waves (32*NW queries) shares key tiles of KT = 8192 / D keys
-// staged in LDS: K row-major, V transposed (V^T rows of KT keys).  The tile
+// A block of NW waves shares key tiles of KT = 8192 / D keys staged in LDS:
+// K row-major, V transposed (V^T rows of KT keys).  Each wave owns 32
+// queries; with a key split KS = 2, two waves own the same 32 queries and
+// take the two halves of every tile, and their online-softmax states are
+// merged through LDS at the end (more blocks for short prompts).  The tile
 // after the current one is loaded into registers before the current one is
 // used (V as 4-key x 8-dim sub-blocks, transposed in registers so the LDS
 // writes are 8 bytes wide) and written to the other half of a double buffer;
@@ -30,12 +33,15 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 __device__ __forceinline__ h8v h8_of(const u32x4 v) { return __builtin_bit_cast(h8v, v); }
 
-template <int D, int NW>
+template <int D, int NW, int KS = 1>
 struct AttnGeom {
   static constexpr int THREADS = 64 * NW;
-  static constexpr int QB = 32 * NW;               // queries per block
+  static constexpr int QG = NW / KS;               // query fragments per block
+  static constexpr int QB = 32 * QG;               // queries per block
   static constexpr int KT = 8192 / D;              // keys per tile
   static constexpr int NS = KT / 32;               // S fragments per tile
+  static constexpr int NSW = NS / KS;              // S fragments per wave per tile
+  static_assert(NS % KS == 0 && NW % KS == 0, "key split");
   static constexpr int DF = D / 32;                // output fragments
   static constexpr int KP = D + 8;                 // K tile row pitch (fp16)
   static constexpr int VP = KT + 8;                // V^T row pitch (fp16)
@@ -51,10 +57,9 @@ struct AttnStage {
   u32x4 v[G::V_CH][4];
 };
 
-template <int D, int NW>
-__device__ __forceinline__ void attn_load(AttnStage<AttnGeom<D, NW>>& st, const uint16_t* __restrict__ kh,
+template <int D, class G>
+__device__ __forceinline__ void attn_load(AttnStage<G>& st, const uint16_t* __restrict__ kh,
                                           const uint16_t* __restrict__ vh, int64_t k0, int64_t T, int t) {
-  using G = AttnGeom<D, NW>;
 #pragma unroll
   for (int i = 0; i < G::K_CH; ++i) {
     const int c = t + G::THREADS * i;
@@ -75,9 +80,8 @@ __device__ __forceinline__ void attn_load(AttnStage<AttnGeom<D, NW>>& st, const 
   }
 }
 
-template <int D, int NW>
-__device__ __forceinline__ void attn_store(const AttnStage<AttnGeom<D, NW>>& st, uint16_t* buf, int t) {
-  using G = AttnGeom<D, NW>;
+template <int D, class G>
+__device__ __forceinline__ void attn_store(const AttnStage<G>& st, uint16_t* buf, int t) {
   uint16_t* ks = buf;
   uint16_t* vt = buf + G::KT * G::KP;
 #pragma unroll
@@ -106,19 +110,20 @@ __device__ __forceinline__ void attn_store(const AttnStage<AttnGeom<D, NW>>& st,
   }
 }
 
-template <int D, int NW>
+template <int D, int NW, int KS>
 __device__ __forceinline__ void attn_prefill_body(
     const uint16_t* __restrict__ q, int64_t q_ld, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, int64_t kv_head_stride, int64_t T, float qk_scale,
     uint16_t* __restrict__ out, int64_t out_ld) {
-  using G = AttnGeom<D, NW>;
+  using G = AttnGeom<D, NW, KS>;
   __shared__ __align__(16) uint16_t lds[2 * G::HALF];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int half = lane >> 5, l32 = lane & 31;
+  const int qfrag = wave % G::QG, kpart = wave / G::QG;  // kpart: which NSW-fragment slice of each tile
   const int h = blockIdx.y;
   const int64_t nqb = (T + G::QB - 1) / G::QB;
   const int64_t q0 = (nqb - 1 - (int64_t)blockIdx.x) * G::QB;
-  const int64_t qw = q0 + 32 * wave;
+  const int64_t qw = q0 + 32 * qfrag;
   const int64_t qi = qw + l32;
   const int64_t qc = qi < T ? qi : T - 1;
 
@@ -143,47 +148,48 @@ __device__ __forceinline__ void attn_prefill_body(
   const int64_t kend = T < q0 + G::QB ? T : q0 + G::QB;
   const int64_t ntile = (kend + G::KT - 1) / G::KT;
   AttnStage<G> st;
-  attn_load<D, NW>(st, kh, vh, 0, T, t);
-  attn_store<D, NW>(st, lds, t);
+  attn_load<D, G>(st, kh, vh, 0, T, t);
+  attn_store<D, G>(st, lds, t);
   __syncthreads();
   for (int64_t it = 0; it < ntile; ++it) {
     const int64_t k0 = it * G::KT;
     const int64_t kn = (it + 1 < ntile ? it + 1 : it) * G::KT;  // clamped prefetch
-    attn_load<D, NW>(st, kh, vh, kn, T, t);
+    attn_load<D, G>(st, kh, vh, kn, T, t);
     const uint16_t* ks = lds + (it & 1) * G::HALF;
     const uint16_t* vt = ks + G::KT * G::KP;
-    if (k0 <= qw) {  // wave-uniform: the tile holds a key at or before every query of the wave
-      f32x16 s[G::NS];
+    const int64_t kw = k0 + 32 * G::NSW * kpart;  // first key of this wave's slice of the tile
+    if (kw <= qw) {  // wave-uniform: the slice holds a key at or before every query of the wave
+      f32x16 s[G::NSW];
 #pragma unroll
-      for (int sf = 0; sf < G::NS; ++sf) s[sf] = (f32x16){};
-      // the NS accumulation chains are interleaved (independent neighbours)
+      for (int sf = 0; sf < G::NSW; ++sf) s[sf] = (f32x16){};
+      // the NSW accumulation chains are interleaved (independent neighbours)
 #pragma unroll
       for (int j = 0; j < G::DF; ++j)
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-          for (int sf = 0; sf < G::NS; ++sf) {
-            const uint16_t* kp = ks + (32 * sf + l32) * G::KP + 32 * j + 16 * half + 8 * hh;
+          for (int sf = 0; sf < G::NSW; ++sf) {
+            const uint16_t* kp = ks + (32 * (G::NSW * kpart + sf) + l32) * G::KP + 32 * j + 16 * half + 8 * hh;
             s[sf] = __builtin_amdgcn_mfma_f32_32x32x16_f16(h8_of(*reinterpret_cast<const u32x4*>(kp)), qf[j][hh],
                                                            s[sf], 0, 0, 0);
           }
       float mx = -INFINITY;
 #pragma unroll
-      for (int sf = 0; sf < G::NS; ++sf)
+      for (int sf = 0; sf < G::NSW; ++sf)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int64_t key = k0 + 32 * sf + 8 * (r / 4) + 4 * half + (r % 4);
+          const int64_t key = kw + 32 * sf + 8 * (r / 4) + 4 * half + (r % 4);
           s[sf][r] = (key <= qi && key < T) ? s[sf][r] * qk_scale : -INFINITY;
           mx = fmaxf(mx, s[sf][r]);
         }
       mx = fmaxf(mx, xor32_get(mx, lane));
-      // key k0 <= qw <= qi is valid for every query of the wave, so mn is finite
+      // key kw <= qw <= qi is valid for every query of the wave, so mn is finite
       const float mn = fmaxf(m, mx);
       const float alpha = exp2f(m - mn);
       float ps = 0.0f;
-      h8v pb[2 * G::NS];
+      h8v pb[2 * G::NSW];
 #pragma unroll
-      for (int sf = 0; sf < G::NS; ++sf) {
+      for (int sf = 0; sf < G::NSW; ++sf) {
         uint32_t pk[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -204,8 +210,8 @@ __device__ __forceinline__ void attn_prefill_body(
           for (int r = 0; r < 16; ++r) o[f][r] *= alpha;
       }
 #pragma unroll
-      for (int qq = 0; qq < 2 * G::NS; ++qq) {
-        const int kb = 32 * (qq / 2) + 16 * (qq % 2);
+      for (int qq = 0; qq < 2 * G::NSW; ++qq) {
+        const int kb = 32 * (G::NSW * kpart + qq / 2) + 16 * (qq % 2);
 #pragma unroll
         for (int f = 0; f < G::DF; ++f) {
           const uint16_t* vp = vt + (32 * f + l32) * G::VP + 4 * half + kb;
@@ -216,10 +222,36 @@ __device__ __forceinline__ void attn_prefill_body(
         }
       }
     }
-    attn_store<D, NW>(st, lds + ((it + 1) & 1) * G::HALF, t);
+    attn_store<D, G>(st, lds + ((it + 1) & 1) * G::HALF, t);
     __syncthreads();
   }
 
+  if constexpr (KS == 2) {
+    // Merge the two key slices of each query fragment (the loop ended on a
+    // barrier, so the tile buffers are free): slice 1 publishes m, its lane's
+    // partial l and o, transposed so consecutive lanes hit consecutive banks;
+    // slice 0 combines in a fixed order.
+    constexpr int NV = 16 * G::DF + 2;
+    float* mrg = reinterpret_cast<float*>(lds) + qfrag * NV * 64;
+    if (kpart == 1) {
+      mrg[lane] = m;
+      mrg[64 + lane] = l;
+#pragma unroll
+      for (int f = 0; f < G::DF; ++f)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mrg[(2 + 16 * f + r) * 64 + lane] = o[f][r];
+    }
+    __syncthreads();
+    if (kpart == 1) return;
+    const float mb = mrg[lane], lb = mrg[64 + lane];
+    const float mm = fmaxf(m, mb);  // m is finite: slice 0 always holds key 0 for this fragment
+    const float fa = exp2f(m - mm), fb = exp2f(mb - mm);
+    l = l * fa + lb * fb;
+#pragma unroll
+    for (int f = 0; f < G::DF; ++f)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[f][r] = o[f][r] * fa + mrg[(2 + 16 * f + r) * 64 + lane] * fb;
+  }
   const float lt = l + xor32_get(l, lane);
   const float inv = 1.0f / lt;
   if (qi >= T) return;
@@ -236,43 +268,50 @@ __device__ __forceinline__ void attn_prefill_body(
 
 // Two waves per SIMD need at most 256 registers a lane: met without spills
 // for head_dim <= 128 with 4-wave blocks (two blocks fit the LDS of a CU).
-template <int D, int NW>
+template <int D, int NW, int KS>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) void attn_prefill_kernel_occ2(
     const uint16_t* __restrict__ q, int64_t q_ld, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, int64_t kv_head_stride, int64_t T, float qk_scale,
     uint16_t* __restrict__ out, int64_t out_ld) {
-  attn_prefill_body<D, NW>(q, q_ld, k, v, kv_head_stride, T, qk_scale, out, out_ld);
+  attn_prefill_body<D, NW, KS>(q, q_ld, k, v, kv_head_stride, T, qk_scale, out, out_ld);
 }
 
-template <int D, int NW>
+template <int D, int NW, int KS>
 __global__ __launch_bounds__(64 * NW) void attn_prefill_kernel(
     const uint16_t* __restrict__ q, int64_t q_ld, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, int64_t kv_head_stride, int64_t T, float qk_scale,
     uint16_t* __restrict__ out, int64_t out_ld) {
-  attn_prefill_body<D, NW>(q, q_ld, k, v, kv_head_stride, T, qk_scale, out, out_ld);
+  attn_prefill_body<D, NW, KS>(q, q_ld, k, v, kv_head_stride, T, qk_scale, out, out_ld);
 }
 
-template <int D, int NW>
+template <int D, int NW, int KS>
 void launch_attn(const uint16_t* q, int64_t q_ld, const uint16_t* k, const uint16_t* v, int64_t kv_head_stride,
                  int64_t T, int64_t heads, float qk_scale, uint16_t* out, int64_t out_ld, hipStream_t st) {
-  const int64_t nqb = (T + 32 * NW - 1) / (32 * NW);
+  constexpr int QB = 32 * NW / KS;
+  const int64_t nqb = (T + QB - 1) / QB;
   const dim3 grid((unsigned)nqb, (unsigned)heads);
   if constexpr (D <= 128 && NW == 4)
-    hipLaunchKernelGGL((attn_prefill_kernel_occ2<D, NW>), grid, dim3(64 * NW), 0, st, q, q_ld, k, v,
+    hipLaunchKernelGGL((attn_prefill_kernel_occ2<D, NW, KS>), grid, dim3(64 * NW), 0, st, q, q_ld, k, v,
                        kv_head_stride, T, qk_scale, out, out_ld);
   else
-    hipLaunchKernelGGL((attn_prefill_kernel<D, NW>), grid, dim3(64 * NW), 0, st, q, q_ld, k, v, kv_head_stride,
-                       T, qk_scale, out, out_ld);
+    hipLaunchKernelGGL((attn_prefill_kernel<D, NW, KS>), grid, dim3(64 * NW), 0, st, q, q_ld, k, v,
+                       kv_head_stride, T, qk_scale, out, out_ld);
 }
 
 template <int D>
 void launch_attn_d(const uint16_t* q, int64_t q_ld, const uint16_t* k, const uint16_t* v, int64_t kv_head_stride,
                    int64_t T, int64_t heads, float qk_scale, uint16_t* out, int64_t out_ld, hipStream_t st) {
-  // 4 waves per block once that still gives a block per compute unit
-  if (((T + 127) / 128) * heads >= 256)
-    launch_attn<D, 4>(q, q_ld, k, v, kv_head_stride, T, heads, qk_scale, out, out_ld, st);
-  else
-    launch_attn<D, 2>(q, q_ld, k, v, kv_head_stride, T, heads, qk_scale, out, out_ld, st);
+  // 128 queries per 4-wave block once that gives two blocks per compute unit;
+  // below that, 64 queries per block with each tile's keys split between
+  // wave pairs (twice the blocks, half the keys per wave).
+  if constexpr (D > 128) {  // one 32-key fragment per tile: nothing to split
+    launch_attn<D, 4, 1>(q, q_ld, k, v, kv_head_stride, T, heads, qk_scale, out, out_ld, st);
+  } else {
+    if (((T + 127) / 128) * heads >= 512)
+      launch_attn<D, 4, 1>(q, q_ld, k, v, kv_head_stride, T, heads, qk_scale, out, out_ld, st);
+    else
+      launch_attn<D, 4, 2>(q, q_ld, k, v, kv_head_stride, T, heads, qk_scale, out, out_ld, st);
+  }
 }
 
 }  // namespace

@@ -35,6 +35,8 @@ struct GemmArgs {
   int64_t y_ld;
   const uint16_t* resid;   // optional fp16 residual (M, resid_ld)
   int64_t resid_ld;
+  int splits;              // K ranges (blockIdx.y); > 1 writes fp32 partials
+  float* part;             // (splits, M, N) fp32 partials when splits > 1
 };
 
 template <bool W8, int BM, int BN>
@@ -46,6 +48,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
   const int64_t nbm = (a.M + BM - 1) / BM, nbn = (a.N + BN - 1) / BN;
   const int64_t tile = xcd_tile(blockIdx.x, nbm * nbn);
   const int64_t m0 = (tile % nbm) * BM, n0 = (tile / nbm) * BN;
+  const int z = blockIdx.y;
+  const int64_t klen = a.K / a.splits, kb = z * klen;  // this block's K range
 
   Sources<TL, W8> src;
 #pragma unroll
@@ -53,7 +57,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
     int64_t m = m0 + TL::a_row(t, i);
     m = m < a.M ? m : a.M - 1;
     const int64_t row = a.x_rows ? (int64_t)a.x_rows[m] : m;
-    src.a[i] = a.x + row * a.x_ld + TL::a_col(t, i);
+    src.a[i] = a.x + row * a.x_ld + kb + TL::a_col(t, i);
   }
   if constexpr (W8) {
     const int64_t ng = a.K / a.group;
@@ -61,15 +65,15 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
     for (int i = 0; i < TL::B8_CH; ++i) {
       int64_t n = n0 + TL::b8_row(t, i);
       n = n < a.N ? n : a.N - 1;
-      src.bc[i] = a.codes + n * a.K + TL::b8_col(t, i);
-      src.bs[i] = a.scale + n * ng;
+      src.bc[i] = a.codes + n * a.K + kb + TL::b8_col(t, i);
+      src.bs[i] = a.scale + n * ng + kb / a.group;
     }
   } else {
 #pragma unroll
     for (int i = 0; i < TL::B16_CH; ++i) {
       int64_t n = n0 + TL::b16_row(t, i);
       n = n < a.N ? n : a.N - 1;
-      src.bw[i] = a.w16 + n * a.K + TL::b16_col(t, i);
+      src.bw[i] = a.w16 + n * a.K + kb + TL::b16_col(t, i);
     }
   }
   const int wm = wave >> 1, wn = wave & 1;
@@ -77,7 +81,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
 #pragma unroll
   for (int j = 0; j < TL::FN; ++j) b_row0[j] = wn * (BN / 2) + 32 * j;
   Acc<TL::FM, TL::FN> acc;
-  block_mainloop<TL, W8>(acc, src, a.K, a.group, lds, wm * (BM / 2), b_row0);
+  block_mainloop<TL, W8>(acc, src, klen, a.group, lds, wm * (BM / 2), b_row0);
 
 #pragma unroll
   for (int i = 0; i < TL::FM; ++i)
@@ -88,6 +92,10 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
       for (int r = 0; r < 16; ++r) {
         const int64_t m = m0 + wm * (BM / 2) + 32 * i + acc_row(r, half);
         if (m >= a.M || n >= a.N) continue;
+        if (a.part) {
+          a.part[((int64_t)z * a.M + m) * a.N + n] = acc.v[i][j][r];
+          continue;
+        }
         uint16_t o = f2h(acc.v[i][j][r]);
         if (a.resid) o = hadd_round(h2f(o), a.resid[m * a.resid_ld + n]);
         a.y16[m * a.y_ld + n] = o;
@@ -95,8 +103,32 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
     }
 }
 
+// Split-K finish: y = fp16(sum over z of part[z]) in z order (+ residual).
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ part, int splits, int64_t M,
+                                                           int64_t N, uint16_t* __restrict__ y, int64_t y_ld,
+                                                           const uint16_t* __restrict__ resid, int64_t resid_ld) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= M * N) return;
+  const int64_t m = idx / N, n = idx - m * N;
+  float v = 0.0f;
+  for (int z = 0; z < splits; ++z) v += part[z * M * N + idx];
+  uint16_t o = f2h(v);
+  if (resid) o = hadd_round(h2f(o), resid[m * resid_ld + n]);
+  y[m * y_ld + n] = o;
+}
+
 template <bool W8>
 int launch_tiles(const GemmArgs& a, hipStream_t st) {
+  if (a.splits > 1) {  // small grids: 64 x 64 tiles, one K range per blockIdx.y, then the ordered sum
+    const int64_t tiles = ((a.M + 63) / 64) * ((a.N + 63) / 64);
+    hipLaunchKernelGGL((gemm_kernel<W8, 64, 64>), dim3((unsigned)tiles, (unsigned)a.splits), dim3(256), 0, st, a);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return (int)e;
+    const int64_t n = a.M * a.N;
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a.part, a.splits,
+                       a.M, a.N, a.y16, a.y_ld, a.resid, a.resid_ld);
+    LEMOQ_CHECK_LAUNCH();
+  }
   const int64_t big = ((a.M + 127) / 128) * ((a.N + 127) / 128);
   if (big >= 256) {
     hipLaunchKernelGGL((gemm_kernel<W8, 128, 128>), dim3((unsigned)big), dim3(256), 0, st, a);
@@ -118,6 +150,9 @@ int check_gemm(const GemmArgs& a) {
   if (a.K % 64 != 0 || a.x_ld < a.K || a.x_ld % 8 != 0 || a.y_ld < a.N) return LEMOQ_ERR_SHAPE;
   if (a.codes && (a.group <= 0 || a.group % 64 != 0 || a.K % a.group != 0)) return LEMOQ_ERR_UNSUPPORTED;
   if (a.resid && a.resid_ld < a.N) return LEMOQ_ERR_SHAPE;
+  if (a.splits < 1 || a.splits > 64 || a.K % (64LL * a.splits) != 0) return LEMOQ_ERR_SHAPE;
+  if (a.splits > 1 && (!a.part || (a.codes && (a.K / a.splits) % a.group != 0) || a.M * a.N > (1LL << 31)))
+    return a.part ? LEMOQ_ERR_SHAPE : LEMOQ_ERR_NULL;
   if (!lemoq_aligned16(a.x) || (a.codes && !lemoq_aligned16(a.codes)) || (a.w16 && !lemoq_aligned16(a.w16)))
     return LEMOQ_ERR_ALIGN;
   return LEMOQ_OK;
@@ -134,6 +169,7 @@ extern "C" int lemoq_gemm_w8(const uint16_t* x, int64_t M, int64_t K, int64_t x_
   a.codes = codes; a.scale = scale; a.w16 = nullptr; a.group = (int)group;
   a.y16 = y; a.y_ld = y_ld;
   a.resid = residual; a.resid_ld = residual_ld;
+  a.splits = 1; a.part = nullptr;
   if (!y || !codes) return LEMOQ_ERR_NULL;
   const int rc = check_gemm(a);
   if (rc != LEMOQ_OK) return rc;
@@ -147,7 +183,26 @@ extern "C" int lemoq_gemm_f16(const uint16_t* x, int64_t M, int64_t K, int64_t x
   a.codes = nullptr; a.scale = nullptr; a.w16 = w; a.group = 0;
   a.y16 = y; a.y_ld = y_ld;
   a.resid = nullptr; a.resid_ld = 0;
+  a.splits = 1; a.part = nullptr;
   if (!y || !w) return LEMOQ_ERR_NULL;
+  const int rc = check_gemm(a);
+  if (rc != LEMOQ_OK) return rc;
+  return launch_gemm(a, lemoq_stream(stream));
+}
+
+extern "C" int lemoq_gemm_f16_splitk(const uint16_t* x, int64_t M, int64_t K, int64_t x_ld, const uint16_t* w,
+                                     int64_t N, uint16_t* y, int64_t y_ld, int64_t splits, float* workspace,
+                                     void* stream) {
+  GemmArgs a{};
+  a.x = x; a.x_ld = x_ld; a.x_rows = nullptr; a.M = M; a.N = N; a.K = K;
+  a.codes = nullptr; a.scale = nullptr; a.w16 = w; a.group = 0;
+  a.y16 = y; a.y_ld = y_ld;
+  a.resid = nullptr; a.resid_ld = 0;
+  a.splits = (int)(splits < 1 ? 1 : (splits > 64 ? 65 : splits));
+  a.part = workspace;
+  if (!y || !w) return LEMOQ_ERR_NULL;
+  if (splits < 1 || splits > 64) return LEMOQ_ERR_SHAPE;
+  if (splits > 1 && !lemoq_aligned16(workspace)) return workspace ? LEMOQ_ERR_ALIGN : LEMOQ_ERR_NULL;
   const int rc = check_gemm(a);
   if (rc != LEMOQ_OK) return rc;
   return launch_gemm(a, lemoq_stream(stream));

@@ -186,8 +186,11 @@ def dequant_gemm_separate(
     return y
 
 
-def linear_f16(x: Any, weight: Any) -> Any:
-    """``fp16(x (M, K) @ weight (N, K).T)`` with fp32 accumulation (``F.linear`` in fp16)."""
+def linear_f16(x: Any, weight: Any, *, splits: int = 1) -> Any:
+    """``fp16(x (M, K) @ weight (N, K).T)`` with fp32 accumulation (``F.linear`` in fp16).
+
+    ``splits`` > 1 cuts K into that many ranges summed in order (``lemoq_gemm_f16_splitk``):
+    more blocks for narrow outputs such as the 64-expert router."""
     import torch  # noqa: PLC0415
 
     if weight.dim() != 2 or weight.dtype != torch.float16 or not weight.is_contiguous():
@@ -200,6 +203,13 @@ def linear_f16(x: Any, weight: Any) -> Any:
     y = torch.empty((M, N), dtype=torch.float16, device=x.device)
     _hip.require_rocm(x, weight, what="linear_f16")
     if M == 0 or N == 0:
+        return y
+    if splits > 1:
+        if K % (64 * splits) != 0:
+            raise ValueError("K=%d is not a multiple of 64 * splits (%d)" % (K, splits))
+        ws = torch.empty((splits, M, N), dtype=torch.float32, device=x.device)
+        _hip.call("lemoq_gemm_f16_splitk", _hip.ptr(x), M, K, K, _hip.ptr(weight), N, _hip.ptr(y), N, int(splits),
+                  _hip.ptr(ws), _hip.stream_of(x.device))
         return y
     _hip.call("lemoq_gemm_f16", _hip.ptr(x), M, K, K, _hip.ptr(weight), N, _hip.ptr(y), N,
               _hip.stream_of(x.device))

@@ -65,5 +65,9 @@ def test_argument_rejection_happens_before_any_launch():
     assert lib.lemoq_gemm_w8(fake, 4, 128, 128, None, fake, fake, 64, 16, fake, 64, None, 0, None) == -3
     assert lib.lemoq_gemm_w8(fake, 4, 128, 128, None, fake + 8, fake, 64, 128, fake, 64, None, 0, None) == -4
     assert lib.lemoq_gemm_f16(fake, 4, 128, 64, fake, 64, fake, 64, None) == -2
+    # split-K: K not a multiple of 64 * splits, a missing workspace, too many splits
+    assert lib.lemoq_gemm_f16_splitk(fake, 4, 192, 192, fake, 64, fake, 64, 2, fake, None) == -2
+    assert lib.lemoq_gemm_f16_splitk(fake, 4, 256, 256, fake, 64, fake, 64, 2, None, None) == -1
+    assert lib.lemoq_gemm_f16_splitk(fake, 4, 256, 256, fake, 64, fake, 64, 65, fake, None) == -2
     with pytest.raises(ValueError):
         _hip.call("lemoq_gemv_w8", None, 1, 16, None, None, 16, 16, 16, None, 1, None)

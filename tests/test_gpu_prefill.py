@@ -103,15 +103,18 @@ def test_qk_norm_rope_rows_vs_oracle(D, dev):
         assert (codes[:, T:] == 0).all() and (scales[:, T:] == 1).all()
 
 
-ATTN_CASES = [(1, 128), (7, 64), (64, 128), (129, 128), (300, 256), (2048, 128)]
+# (T, head_dim, heads).  Fewer than 512 blocks of 128 queries take the key-split
+# kernel (64 queries per block, each tile's keys split between wave pairs); the
+# (777, 128, 80) and (300, 64, 200) cases take the unsplit one.
+ATTN_CASES = [(1, 128, 3), (7, 64, 3), (64, 128, 3), (129, 128, 3), (300, 256, 3), (2048, 128, 2),
+              (777, 128, 80), (300, 64, 200)]
 
 
-@pytest.mark.parametrize("T,D", ATTN_CASES, ids=["T%d-D%d" % c for c in ATTN_CASES])
-def test_attn_prefill_vs_fp64(T, D, dev):
+@pytest.mark.parametrize("T,D,NH", ATTN_CASES, ids=["T%d-D%d-H%d" % c for c in ATTN_CASES])
+def test_attn_prefill_vs_fp64(T, D, NH, dev):
     from lemoq import _hip
 
-    print("case: attn_prefill T=%d D=%d" % (T, D), flush=True)
-    NH = 3 if T < 1000 else 2
+    print("case: attn_prefill T=%d D=%d heads=%d" % (T, D, NH), flush=True)
     S = T + 5
     g = torch.Generator().manual_seed(T * 7 + D)
     q = torch.randn((T, NH, D), generator=g).to(torch.float16)

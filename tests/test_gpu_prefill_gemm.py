@@ -110,6 +110,19 @@ def test_gemm_f16_vs_oracle(m, n, k, dev):
     _assert_linear(got, ref, x.double().abs() @ w.double().abs().t(), "gemm_f16 %dx%dx%d" % (m, n, k))
 
 
+@pytest.mark.parametrize("m,n,k,splits", [(1024, 64, 2048, 8), (5, 64, 2048, 4), (3, 50, 128, 2), (70, 64, 2048, 1)])
+def test_gemm_f16_splitk_vs_oracle(m, n, k, splits, dev):
+    from lemoq.kernels.dequant_gemm import linear_f16
+
+    print("case: gemm_f16 split-K m=%d n=%d k=%d splits=%d" % (m, n, k, splits), flush=True)
+    w = randn(n, k, seed=n + k + splits, std=0.02).to(torch.float16)
+    x = randn(m, k, seed=m + 9).to(torch.float16)
+    got = linear_f16(x.to(dev), w.to(dev), splits=splits)
+    torch.cuda.synchronize()
+    ref = ops.linear_f16(x, w)
+    _assert_linear(got, ref, x.double().abs() @ w.double().abs().t(), "gemm_f16 split %d" % splits)
+
+
 def test_quant_linear_dispatch(dev):
     """One row takes the fused GEMV, several rows the separate-arm GEMM (as the reference's forward)."""
     from lemoq.kernels.dequant_gemm import dequant_gemm_fused, dequant_gemm_separate
