@@ -679,11 +679,17 @@ def main(argv=None) -> int:
 
 
 # Launch order of one batched prefill (lemoq.model.prefill.prefill_prompt):
-# gather, 16 x [12 launches], final norm, lm_head GEMM, then the greedy pick.
-PREFILL_LAYER_ROLES = ("rmsnorm (input)", "gemm_w8 qkv", "qk_rows (q/k norm, RoPE, KV-INT8)", "attn_prefill",
-                       "gemm_w8 o_proj (+residual)", "rmsnorm (post-attention)", "gemm_f16 router",
-                       "route_topk", "moe_prefill_sort", "moe_prefill_gate_up", "moe_prefill_down",
-                       "moe_prefill_combine (+residual)")
+# gather, 16 x [13 launches], final norm, lm_head GEMM, then the greedy pick;
+# each role with the kernel-name fragment its dispatch must carry.
+PREFILL_LAYER_ROLES = (("rmsnorm (input)", "rmsnorm_kernel"), ("gemm_w8 qkv", "gemm_kernel<true"),
+                       ("qk_rows (q/k norm, RoPE, KV-INT8)", "qk_rows_kernel"), ("attn_prefill", "attn_prefill_kernel"),
+                       ("gemm_w8 o_proj (+residual)", "gemm_kernel<true"), ("rmsnorm (post-attention)", "rmsnorm_kernel"),
+                       ("gemm_f16 router (split-K partials)", "gemm_kernel<false"),
+                       ("router split-K sum", "splitk_reduce_kernel"), ("route_topk", "route_topk_kernel"),
+                       ("moe_prefill_sort", "moe_sort_kernel"), ("moe_prefill_gate_up", "moe_gate_up_kernel"),
+                       ("moe_prefill_down", "moe_down_kernel"), ("moe_prefill_combine (+residual)", "moe_combine_kernel"))
+PREFILL_TAIL_ROLES = (("rmsnorm (final)", "rmsnorm_kernel"), ("gemm_w8 lm_head (last row)", "gemm_kernel<true"),
+                      ("argmax_advance", "argmax_advance_kernel"))
 
 
 def prefill_flops(role: str, T: int, shape=None) -> float:
@@ -692,7 +698,7 @@ def prefill_flops(role: str, T: int, shape=None) -> float:
     return {
         "gemm_w8 qkv": 2.0 * T * 3 * NH * D * H,
         "gemm_w8 o_proj (+residual)": 2.0 * T * H * NH * D,
-        "gemm_f16 router": 2.0 * T * E * H,
+        "gemm_f16 router (split-K partials)": 2.0 * T * E * H,
         "attn_prefill": 4.0 * NH * D * T * (T + 1) / 2,
         "moe_prefill_gate_up": 2.0 * T * K * 2 * F * H,
         "moe_prefill_down": 2.0 * T * K * H * F,
@@ -705,18 +711,23 @@ def summarize_prefill(trace_csv: str, ctx: int) -> str:
     starts at a gather_rows dispatch; roles follow PREFILL_LAYER_ROLES."""
     import csv as _csv
 
-    rows = sorted(_csv.DictReader(open(trace_csv)), key=lambda r: int(r["Start_Timestamp"]))
+    # the library's own dispatches only (torch's fills and copies run between them)
+    rows = sorted((r for r in _csv.DictReader(open(trace_csv))
+                   if not r["Kernel_Name"].startswith("__amd_rocclr") and "at::native" not in r["Kernel_Name"]),
+                  key=lambda r: int(r["Start_Timestamp"]))
     starts = [i for i, r in enumerate(rows) if "gather_rows_kernel" in r["Kernel_Name"]]
     per_role: dict = {}
     n_layers = 16
+    roles = [("gather_rows", "gather_rows_kernel")] + list(PREFILL_LAYER_ROLES) * n_layers + list(PREFILL_TAIL_ROLES)
     total = []
     for st in starts:
-        seq = rows[st: st + 1 + 12 * n_layers + 3]
-        if len(seq) < 1 + 12 * n_layers + 3:
+        seq = rows[st: st + len(roles)]
+        if len(seq) < len(roles):
             continue
-        roles = ["gather_rows"] + [PREFILL_LAYER_ROLES[j % 12] for j in range(12 * n_layers)] + [
-            "rmsnorm (final)", "gemm_w8 lm_head (last row)", "argmax_advance"]
-        for role, r in zip(roles, seq):
+        for (role, frag), r in zip(roles, seq):
+            if frag not in r["Kernel_Name"]:
+                raise ValueError("prefill launch order changed: %r where %s (%s) was expected"
+                                 % (r["Kernel_Name"][:80], role, frag))
             per_role.setdefault(role, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-3)
         total.append((int(seq[-1]["End_Timestamp"]) - int(seq[0]["Start_Timestamp"])) * 1e-3)
     n = len(total)
