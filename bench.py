@@ -23,7 +23,12 @@ a synthetic KV cache at ``--ctx`` (no prefill); it prints the dispatch plan.
 ``--summarize-pmc FETCH_CSV WRITE_CSV PLAN_JSON`` (CPU only) turns the two
 counter passes into per-kernel HBM bytes per launch: profiles/traffic.json,
 which fills ``roofline.traffic``, and a markdown table beside it.
-``--mode prefill`` times only the batched prefill (TTFT) at ``--ctx`` (and
+``--summarize-trace TRACE_CSV`` (CPU only) splits a ``rocprofv3
+--kernel-trace`` of a full run per kernel into the graph's launches and the
+kernel table's cold isolated launches (the latter are what ``roofline`` and
+``kernels`` time).  ``--mode step`` prefills ``--ctx`` once and replays the step ``--warmup`` +
+``--steps`` times (nothing else: the form profiled for the in-graph kernel
+times).  ``--mode prefill`` times only the batched prefill (TTFT) at ``--ctx`` (and
 ``--ctx2``); ``--summarize-prefill TRACE_CSV --ctx T`` (CPU only) turns a
 ``rocprofv3 --kernel-trace`` of it into a per-kernel table with each kernel's
 FLOP rate against the MI355X dense fp16 matrix peak.
@@ -74,10 +79,13 @@ def parse_args(argv=None):
     ap.add_argument("--cpu-budget-s", type=float, default=20.0)
     ap.add_argument("--cpu-check-steps", type=int, default=32)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--mode", choices=("full", "kernels", "traffic", "prefill"), default="full")
+    ap.add_argument("--mode", choices=("full", "kernels", "traffic", "prefill", "step"), default="full")
     ap.add_argument("--summarize-pmc", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "PLAN_JSON"))
     ap.add_argument("--summarize-prefill", metavar="KERNEL_TRACE_CSV",
                     help="per-kernel table of the prefills in a rocprofv3 kernel trace of --mode prefill at --ctx")
+    ap.add_argument("--summarize-trace", metavar="KERNEL_TRACE_CSV",
+                    help="per-kernel table of a rocprofv3 kernel trace of a full bench run: in-graph launches "
+                         "and the cold isolated launches of the kernel table, separately")
     ap.add_argument("--profiles-dir", default=os.path.join(REPO, "profiles"))
     return ap.parse_args(argv)
 
@@ -533,6 +541,9 @@ def main(argv=None) -> int:
     if args.summarize_prefill:
         print(summarize_prefill(args.summarize_prefill, args.ctx))
         return 0
+    if args.summarize_trace:
+        print(summarize_trace(args.summarize_trace))
+        return 0
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (the batch-1 decode "
@@ -566,6 +577,20 @@ def main(argv=None) -> int:
         cal = copy_calibration(torch, _hip, flusher)
         kt = kernel_table(torch, _hip, w, sess, flusher, args.kernel_reps)
         print(json.dumps({"mode": "traffic", "ctx": args.ctx, "calibration": cal, "kernels": kt}))
+        return 0
+
+    if args.mode == "step":
+        from lemoq.model.olmoe import DecodeSession
+
+        sess = DecodeSession(w, [1] * args.ctx, max_new_tokens=args.warmup + args.steps + 1)
+        sess.capture()
+        sess.prefill()
+        sess.replay(args.warmup)
+        t0 = time.perf_counter()
+        sess.replay(args.steps)
+        ms = (time.perf_counter() - t0) * 1e3 / args.steps
+        log("ctx %d: %d replays, %.4f ms/token" % (args.ctx, args.steps, ms))
+        print(json.dumps({"mode": "step", "ctx": args.ctx, "steps": args.steps, "ms_per_token": ms}))
         return 0
 
     if args.mode == "prefill":
@@ -748,6 +773,52 @@ def summarize_prefill(trace_csv: str, ctx: int) -> str:
     out.append("")
     out.append("%d prefills of %d tokens; kernel time %.3f ms per prefill, first launch start to last launch "
                "end %.3f ms (the gaps are launch and host overhead)." % (n, ctx, busy / 1e3, span / 1e3))
+    return "\n".join(out)
+
+
+def _short_kernel(name: str) -> str:
+    n = name.replace("(anonymous namespace)::", "").replace("void ", "")
+    n = n.split("(")[0] if "<" not in n else n[: n.rfind(">") + 1]
+    return n
+
+
+def summarize_trace(trace_csv: str) -> str:
+    """Per-kernel durations of a rocprofv3 kernel trace of a full bench run, split
+    into the cold isolated launches of the kernel table and all other launches
+    (the graph replays and prefills).  A kernel-table pass is the run of
+    dispatches after a cache flush (``read_probe_kernel``) made of the first two
+    kernel names of the run (one kernel, or a kernel pair such as lm_head +
+    argmax or split + merge); the flushes of the bandwidth probe, followed by a
+    prefill (``gather_rows_kernel``), start no pass."""
+    import csv as _csv
+
+    rows = sorted((r for r in _csv.DictReader(open(trace_csv))
+                   if not r["Kernel_Name"].startswith("__amd_rocclr") and "at::native" not in r["Kernel_Name"]),
+                  key=lambda r: int(r["Start_Timestamp"]))
+    iso = set()
+    for i, r in enumerate(rows):
+        if "read_probe_kernel" not in r["Kernel_Name"] or i + 1 >= len(rows):
+            continue
+        first = rows[i + 1]["Kernel_Name"]
+        if "read_probe_kernel" in first or "gather_rows_kernel" in first:
+            continue
+        names = {first}
+        if i + 2 < len(rows) and "read_probe_kernel" not in rows[i + 2]["Kernel_Name"]:
+            names.add(rows[i + 2]["Kernel_Name"])
+        j = i + 1
+        while j < len(rows) and rows[j]["Kernel_Name"] in names:
+            iso.add(j)
+            j += 1
+    stats: dict = {}
+    for i, r in enumerate(rows):
+        d = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-3
+        e = stats.setdefault(_short_kernel(r["Kernel_Name"]), {"graph": [], "iso": []})
+        e["iso" if i in iso else "graph"].append(d)
+    out = ["| kernel | in-graph / other launches | avg us | isolated cold launches | avg us |", "|---|---|---|---|---|"]
+    for name, e in sorted(stats.items(), key=lambda kv: -(sum(kv[1]["graph"]) + sum(kv[1]["iso"]))):
+        g, c = e["graph"], e["iso"]
+        out.append("| %s | %d | %s | %d | %s |" % (name[:100], len(g), "%.2f" % (sum(g) / len(g)) if g else "-",
+                                                    len(c), "%.2f" % (sum(c) / len(c)) if c else "-"))
     return "\n".join(out)
 
 
