@@ -198,10 +198,10 @@ extern "C" int lemoq_gemm_f16_splitk(const uint16_t* x, int64_t M, int64_t K, in
   a.codes = nullptr; a.scale = nullptr; a.w16 = w; a.group = 0;
   a.y16 = y; a.y_ld = y_ld;
   a.resid = nullptr; a.resid_ld = 0;
-  a.splits = (int)(splits < 1 ? 1 : (splits > 64 ? 65 : splits));
-  a.part = workspace;
   if (!y || !w) return LEMOQ_ERR_NULL;
   if (splits < 1 || splits > 64) return LEMOQ_ERR_SHAPE;
+  a.splits = (int)splits;
+  a.part = workspace;
   if (splits > 1 && !lemoq_aligned16(workspace)) return workspace ? LEMOQ_ERR_ALIGN : LEMOQ_ERR_NULL;
   const int rc = check_gemm(a);
   if (rc != LEMOQ_OK) return rc;
