@@ -24,12 +24,14 @@ sys.path.insert(0, REPO)
 
 from oracle import ops  # noqa: E402
 from oracle import quant as oq  # noqa: E402
-from oracle.olmoe import OracleDecoder, Shape, random_host_weights  # noqa: E402
+from oracle.olmoe import OracleDecoder, Shape, oracle_prefill, random_host_weights  # noqa: E402
 
 TINY = Shape(hidden=256, heads=2, head_dim=128, layers=2, num_experts=4, top_k=2, ffn=128, vocab=512)
 TINY_SEED = 20261201
 TINY_PROMPT = [1, 7, 300, 42, 5, 5, 99, 1]
 TINY_STEPS = 8
+PREFILL_PROMPT_LEN = 24
+PREFILL_STEPS = 6
 
 
 def rtn_fixture() -> dict:
@@ -75,9 +77,26 @@ def tiny_decode_fixture() -> dict:
             "logits": torch.stack(logits).numpy(), "seed": np.array(TINY_SEED, dtype=np.int64)}
 
 
+def tiny_prefill_fixture() -> dict:
+    """The batched prefill of a 24-token prompt (``oracle_prefill``: last-position logits and every
+    layer's KV-INT8 rows), then greedy decode steps from that cache."""
+    hw = random_host_weights(TINY, seed=TINY_SEED)
+    prompt = np.random.default_rng(4).integers(0, TINY.vocab, PREFILL_PROMPT_LEN).astype(np.int64)
+    S = PREFILL_PROMPT_LEN + PREFILL_STEPS
+    logits, kv = oracle_prefill(hw, prompt, S)
+    od = OracleDecoder(hw, S, kv=kv)
+    seed = od.greedy(logits)
+    tokens, step_logits = od.run([], PREFILL_STEPS, start_pos=PREFILL_PROMPT_LEN, seed_token=seed)
+    T = PREFILL_PROMPT_LEN
+    return {"prompt": prompt, "logits": logits.numpy(), "seed": np.array(TINY_SEED, dtype=np.int64),
+            "kc": np.stack([c["kc"][:, :T].numpy() for c in kv]), "ks": np.stack([c["ks"][:, :T].numpy() for c in kv]),
+            "vc": np.stack([c["vc"][:, :T].numpy() for c in kv]), "vs": np.stack([c["vs"][:, :T].numpy() for c in kv]),
+            "tokens": np.array(tokens, dtype=np.int64), "step_logits": torch.stack(step_logits).numpy()}
+
+
 def main() -> None:
     fixtures = {"rtn_w8": rtn_fixture(), "kv_int8": kv_fixture(), "routing": route_fixture(),
-                "tiny_decode": tiny_decode_fixture()}
+                "tiny_decode": tiny_decode_fixture(), "tiny_prefill": tiny_prefill_fixture()}
     for name, arrays in fixtures.items():
         path = os.path.join(HERE, name + ".npz")
         np.savez_compressed(path, **arrays)
