@@ -174,16 +174,32 @@ __device__ __forceinline__ void attn_prefill_body(
                                                            s[sf], 0, 0, 0);
           }
       float mx = -INFINITY;
+      // Masks are needed only where the slice reaches past the wave's first
+      // query or past the prompt (wave-uniform test); there the key offset
+      // from this lane's query fits 32 bits.
+      const int64_t kend_w = kw + 32 * G::NSW;
+      if (kend_w - 1 <= qw && kend_w <= T) {
 #pragma unroll
-      for (int sf = 0; sf < G::NSW; ++sf)
+        for (int sf = 0; sf < G::NSW; ++sf)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int64_t key = kw + 32 * sf + 8 * (r / 4) + 4 * half + (r % 4);
-          s[sf][r] = (key <= qi && key < T) ? s[sf][r] * qk_scale : -INFINITY;
-          mx = fmaxf(mx, s[sf][r]);
-        }
+          for (int r = 0; r < 16; ++r) {
+            s[sf][r] *= qk_scale;
+            mx = fmaxf(mx, s[sf][r]);
+          }
+      } else {
+        const int lim = (int)((T < qi + 1 ? T : qi + 1) - kw);  // keys kw + j with j < lim are valid
+#pragma unroll
+        for (int sf = 0; sf < G::NSW; ++sf)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int j = 32 * sf + 8 * (r / 4) + 4 * half + (r % 4);
+            s[sf][r] = j < lim ? s[sf][r] * qk_scale : -INFINITY;
+            mx = fmaxf(mx, s[sf][r]);
+          }
+      }
       mx = fmaxf(mx, xor32_get(mx, lane));
-      // key kw <= qw <= qi is valid for every query of the wave, so mn is finite
+      // key kw <= qw <= qi is valid for every query of a wave with stored outputs
+      // (qw < T), so mn is finite there; waves wholly past the prompt store nothing
       const float mn = fmaxf(m, mx);
       const float alpha = exp2f(m - mn);
       float ps = 0.0f;
@@ -267,7 +283,7 @@ __device__ __forceinline__ void attn_prefill_body(
 }
 
 // Two waves per SIMD need at most 256 registers a lane: met without spills
-// for head_dim <= 128 with 4-wave blocks (two blocks fit the LDS of a CU).
+// for head_dim 128 with 4-wave blocks (two blocks fit the LDS of a CU).
 template <int D, int NW, int KS>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) void attn_prefill_kernel_occ2(
     const uint16_t* __restrict__ q, int64_t q_ld, const uint16_t* __restrict__ k,
@@ -290,7 +306,7 @@ void launch_attn(const uint16_t* q, int64_t q_ld, const uint16_t* k, const uint1
   constexpr int QB = 32 * NW / KS;
   const int64_t nqb = (T + QB - 1) / QB;
   const dim3 grid((unsigned)nqb, (unsigned)heads);
-  if constexpr (D <= 128 && NW == 4)
+  if constexpr (D == 128 && NW == 4)
     hipLaunchKernelGGL((attn_prefill_kernel_occ2<D, NW, KS>), grid, dim3(64 * NW), 0, st, q, q_ld, k, v,
                        kv_head_stride, T, qk_scale, out, out_ld);
   else
