@@ -69,5 +69,19 @@ def test_argument_rejection_happens_before_any_launch():
     assert lib.lemoq_gemm_f16_splitk(fake, 4, 192, 192, fake, 64, fake, 64, 2, fake, None) == -2
     assert lib.lemoq_gemm_f16_splitk(fake, 4, 256, 256, fake, 64, fake, 64, 2, None, None) == -1
     assert lib.lemoq_gemm_f16_splitk(fake, 4, 256, 256, fake, 64, fake, 64, 65, fake, None) == -2
+    # prefill entry points
+    assert lib.lemoq_gather_rows(fake, 10, 12, fake, 3, fake, None) == -2            # H % 8
+    assert lib.lemoq_gather_rows(fake, 10, 16, fake, 3, fake + 8, None) == -4        # dst alignment
+    assert lib.lemoq_attn_prefill_f16(fake, 256, fake, fake, 256 * 8, 8, 2, 96, 1.0, fake, 256, None) == -3
+    assert lib.lemoq_attn_prefill_f16(fake, 256, fake, fake, 128 * 4, 8, 2, 128, 1.0, fake, 256, None) == -2
+    assert lib.lemoq_qk_norm_rope_kv_i8_rows(fake, 10, 2, 128, fake, fake, 1e-5, fake, fake, 5, fake, fake, fake,
+                                             fake, fake, 16 * 128, 12, None, None, 0, None) == -2  # rows past s_len
+    assert lib.lemoq_moe_prefill_max_tiles(8192, 64) == 8192 // 128 + 64
+    assert lib.lemoq_moe_prefill_sort(fake, fake, 4097, 8, 64, fake, fake, fake, fake, fake, 10 ** 6, None) == -3
+    assert lib.lemoq_moe_prefill_sort(fake, fake, 16, 8, 300, fake, fake, fake, fake, fake, 10 ** 6, None) == -2
+    assert lib.lemoq_moe_prefill_sort(fake, fake, 16, 8, 64, fake, fake, fake, fake, fake, 10, None) == -2
+    assert lib.lemoq_moe_prefill_gate_up(fake, 2048, fake, fake, 64, fake, fake, 1000, 128, fake, None) == -2
+    assert lib.lemoq_moe_prefill_down(fake, 1024, fake, fake, fake, 64, fake + 4, fake, 2048, 128, fake, None) == -4
+    assert lib.lemoq_moe_prefill_combine(fake, fake, 4, 9, 2048, None, fake, None) == -2
     with pytest.raises(ValueError):
         _hip.call("lemoq_gemv_w8", None, 1, 16, None, None, 16, 16, 16, None, 1, None)
