@@ -163,6 +163,7 @@ def kernel_table(torch, hip, w, sess, flusher, reps: int) -> dict:
         "tw": sess.top_w.clone(),
         "act": sess.act.clone(),
         "xn": torch.empty((H,), dtype=torch.float16, device=dev),
+        "h2": torch.empty((H,), dtype=torch.float16, device=dev),
         "lg": torch.empty((E,), dtype=torch.float16, device=dev),
         "tok": torch.zeros((1,), dtype=torch.int64, device=dev),
         "pos": torch.zeros((1,), dtype=torch.int64, device=dev),
@@ -201,19 +202,33 @@ def kernel_table(torch, hip, w, sess, flusher, reps: int) -> dict:
                                qk_scale, P(sess.part_m), P(sess.part_l), P(sess.part_acc), st())
          for i in range(nl)],
         ["attn_split_fused_i8_kernel"])
-    add("attn_merge", s.heads * ns * (D + 2) * 4 + HD * 2,
-        [lambda: hip.call("lemoq_attn_merge", P(sess.part_m), P(sess.part_l), P(sess.part_acc), s.heads, ns, D,
-                          P(sess.attn), st())] * nl,
-        ["attn_merge_kernel"])
-    add("gemv_w8 o_proj (+residual)", w8(H, HD) + HD * 2 + 2 * H * 2,
-        [lambda i=i: hip.call("lemoq_gemv_w8_fused", P(sess.attn), None, 0, None, s.eps, None,
-                               P(L[i].o_codes), P(L[i].o_scale), H, HD, g, P(scratch["h"]), P(scratch["y"]), st())
-         for i in range(nl)],
-        ["gemv_w8_kernel"])
-    add("router_logits", E * H * 2 + 3 * H * 2 + E * 2,
-        [lambda i=i: hip.call("lemoq_router_logits", P(scratch["h"]), P(L[i].ln_post), s.eps, H, P(L[i].router), E,
-                               P(scratch["xn"]), P(scratch["lg"]), st()) for i in range(nl)],
-        ["router_logits_kernel"])
+    if sess.attn_output_fused:
+        npart = HD // 512
+        add("attn_merge_o_proj_w8", w8(H, HD) + s.heads * ns * (D + 2) * 4 + npart * H * 4,
+            [lambda i=i: hip.call("lemoq_attn_merge_o_proj_w8", P(sess.part_m), P(sess.part_l), P(sess.part_acc),
+                                   s.heads, ns, D, P(L[i].o_codes), P(L[i].o_scale), H, g, P(sess.o_part), st())
+             for i in range(nl)],
+            ["merge_oproj_kernel"])
+        add("router_logits_resid", E * H * 2 + npart * H * 4 + 4 * H * 2 + E * 2,
+            [lambda i=i: hip.call("lemoq_router_logits_resid", P(sess.o_part), npart, P(scratch["h"]),
+                                   P(L[i].ln_post), s.eps, H, P(L[i].router), E, P(scratch["h2"]), P(scratch["xn"]),
+                                   P(scratch["lg"]), st()) for i in range(nl)],
+            ["router_resid_kernel"])
+    else:
+        add("attn_merge", s.heads * ns * (D + 2) * 4 + HD * 2,
+            [lambda: hip.call("lemoq_attn_merge", P(sess.part_m), P(sess.part_l), P(sess.part_acc), s.heads, ns, D,
+                              P(sess.attn), st())] * nl,
+            ["attn_merge_kernel"])
+        add("gemv_w8 o_proj (+residual)", w8(H, HD) + HD * 2 + 2 * H * 2,
+            [lambda i=i: hip.call("lemoq_gemv_w8_fused", P(sess.attn), None, 0, None, s.eps, None,
+                                   P(L[i].o_codes), P(L[i].o_scale), H, HD, g, P(scratch["h"]), P(scratch["y"]),
+                                   st())
+             for i in range(nl)],
+            ["gemv_w8_kernel"])
+        add("router_logits", E * H * 2 + 3 * H * 2 + E * 2,
+            [lambda i=i: hip.call("lemoq_router_logits", P(scratch["h"]), P(L[i].ln_post), s.eps, H, P(L[i].router),
+                                   E, P(scratch["xn"]), P(scratch["lg"]), st()) for i in range(nl)],
+            ["router_logits_kernel"])
     add("gemv_w8 lm_head + argmax (2 launches)", w8(s.vocab, H) + 2 * H * 2 + s.vocab * 2,
         [lambda: hip.call("lemoq_lm_head_argmax_w8", P(scratch["h"]), P(w.final_norm), s.eps, P(w.lm_codes),
                           P(w.lm_scale), s.vocab, H, g, P(scratch["y"]), P(sess.am_val), P(sess.am_idx),

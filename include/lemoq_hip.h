@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define LEMOQ_ABI_VERSION 2
+#define LEMOQ_ABI_VERSION 3
 
 enum {
   LEMOQ_OK = 0,
@@ -193,6 +193,25 @@ int lemoq_attn_merge(const float* m, const float* l, const float* acc,
                      int64_t heads, int64_t num_splits, int64_t head_dim,
                      uint16_t* out, void* stream);
 
+/* LSE merge fused into the w8 o_proj GEMV, split over groups of 4 heads (no
+ * reference counterpart as one call: it joins _attn_combine_kernel
+ * (src/lemoq/kernels/_attn_triton.py:168-206) and the o_proj QuantLinear of
+ * the attention forward (src/lemoq/kernels/attn_decode.py:1015, fused GEMV
+ * arm src/lemoq/quant/linear.py:431-434)).  Block column g merges heads
+ * 4g..4g+3 with the arithmetic of lemoq_attn_merge (bit-identical fp16
+ * attention output) and writes
+ *   part[g][n] = sum over input features k in [512g, 512g+512) of
+ *                scale[n][k/group] * code[n][k] * attn[k]   (fp32),
+ * so that o = fp16(sum_g part[g]) is the o_proj output.  head_dim == 128,
+ * heads % 4 == 0, num_splits <= 64, N % 32 == 0, group % 16 == 0.
+ *   m, l (heads, num_splits); acc (heads, num_splits, 128) fp32;
+ *   codes (N, heads*128) int8; scale (N, heads*128/group) fp16;
+ *   part (heads/4, N) fp32. */
+int lemoq_attn_merge_o_proj_w8(const float* m, const float* l, const float* acc,
+                               int64_t heads, int64_t num_splits, int64_t head_dim,
+                               const int8_t* codes, const uint16_t* scale, int64_t N,
+                               int64_t group, float* part, void* stream);
+
 /* ---------------------------------------------------------------------------
  * A10 — RMSNorm, HF rounding points: y = fp16(fp16(x*rsqrt(mean(x^2)+eps)) * w).
  * Replaces rms_norm_fused (src/lemoq/kernels/rmsnorm.py:102-163, kernel
@@ -266,6 +285,21 @@ int lemoq_route_topk(const void* logits, int logits_is_f16, int64_t T, int64_t E
 int lemoq_router_logits(const uint16_t* h, const uint16_t* norm_w, float eps, int64_t hidden,
                         const uint16_t* router_w, int64_t E, uint16_t* xn_out,
                         uint16_t* logits_out, void* stream);
+
+/* Router logits after the o_proj partials of lemoq_attn_merge_o_proj_w8 (no
+ * reference counterpart as one call: the fp16 residual add after o_proj
+ * (transformers OlmoeDecoderLayer.forward), post_attention_layernorm
+ * (rms_norm_fused, src/lemoq/kernels/rmsnorm.py:102-163) and the router
+ * F.linear of moe_static._route (src/lemoq/kernels/moe_static.py:267)):
+ *   o = fp16(sum_g part[g]) (g ascending), h_out = fp16(o + h),
+ *   xn = rmsnorm(h_out, norm_w) (xn_out, nullable; block 0 writes it and
+ *   h_out), logits (E) = fp16(xn @ router_w^T) with fp32 accumulation.
+ * hidden in {2048, 4096}, n_part in {1, 2, 4, 8}; part (n_part, hidden) fp32;
+ * 16-byte aligned pointers; h_out must not overlap h or part. */
+int lemoq_router_logits_resid(const float* part, int64_t n_part, const uint16_t* h,
+                              const uint16_t* norm_w, float eps, int64_t hidden,
+                              const uint16_t* router_w, int64_t E, uint16_t* h_out,
+                              uint16_t* xn_out, uint16_t* logits, void* stream);
 
 /* Router of one token, fused: xn = rmsnorm(h, norm_w) (written to xn_out),
  * logits = fp16(xn @ router_w^T) with fp32 accumulation (the F.linear of
@@ -399,6 +433,13 @@ typedef struct LemoqOlmoeStep {
   float* am_val;                 /* (am_len) argmax partials */
   int32_t* am_idx;               /* (am_len) */
   int64_t am_len;                /* >= lemoq_lm_head_argmax_parts(vocab) */
+  /* Fused attention-output path (merge + o_proj, then residual + norm +
+   * router in the next launch), used when both are non-NULL and the shapes
+   * allow it (head_dim 128, heads % 4 == 0, num_splits <= 64, hidden 2048
+   * or 4096, heads*128/512 partial rows in {1, 2, 4, 8}); otherwise the step
+   * runs lemoq_attn_merge, the o_proj GEMV and lemoq_router_logits. */
+  float* o_part;                 /* (heads*D/512, H) o_proj partial sums */
+  uint16_t* h_mid;               /* (H) residual after attention */
 } LemoqOlmoeStep;
 
 int lemoq_olmoe_decode_step(const LemoqOlmoeStep* step, void* stream);

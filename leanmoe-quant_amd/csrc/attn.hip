@@ -146,20 +146,13 @@ __global__ __launch_bounds__(64) void attn_merge_wave_kernel(const float* __rest
 #pragma unroll
   for (int j = 0; j < NSMAX; ++j) a[j] = ah[(int64_t)(j < NS ? j : NS - 1) * D];
   LEMOQ_LOADS_ISSUED();
-  const float mj = lane < NS ? mraw : -INFINITY;  // selects, not branches
-  const float lj = lane < NS ? lraw : 0.0f;
-  float M = wave_max(mj);
-  if (!(M > -INFINITY)) M = 0.0f;  // every split empty: out = 0
-  const float wj = exp2f(mj - M);
-  const float den = wave_sum(lj * wj);
-  float num = 0.0f;
-#pragma unroll
-  for (int j = 0; j < NSMAX; ++j) num += a[j] * lane_f(wj, j);
+  float den;
+  const float wj = lemoq_attn::lse_weight(mraw, lraw, lane, NS, den);
   // Unconditional store: a lane with t >= D read the clamped column D - 1,
   // so it writes lane D-1's value to out[D-1] (identical bits).  A store
   // under `t < D` would let the compiler sink the acc loads and the sum into
   // the branch, after the reductions, costing a second memory round trip.
-  out[(int64_t)h * D + tc] = f2h(den > 0.0f ? num / den : num);
+  out[(int64_t)h * D + tc] = lemoq_attn::lse_out<NSMAX>(a, wj, den);
 }
 
 template <bool I8>

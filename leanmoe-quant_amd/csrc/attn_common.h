@@ -223,4 +223,30 @@ __device__ __forceinline__ void finish_split(SoftmaxState<S::EPL>& st, float* wm
   }
 }
 
+// LSE merge of the NS split partials of one head by one wave (the merge of
+// _attn_merge_kernel, src/lemoq/kernels/_attn_triton.py of the reference).
+// Lane j < NS holds split j's running max m_j and sum l_j (other lanes any
+// valid value).  Returns w_j = 2^(m_j - M) in lane j (0 for j >= NS) and sets
+// den = sum_j l_j w_j (wave-uniform), M = max_j m_j, or 0 when every split is
+// empty.
+__device__ __forceinline__ float lse_weight(float mraw, float lraw, int lane, int NS, float& den) {
+  const float mj = lane < NS ? mraw : -INFINITY;  // selects, not branches
+  const float lj = lane < NS ? lraw : 0.0f;
+  float M = wave_max(mj);
+  if (!(M > -INFINITY)) M = 0.0f;  // every split empty: out = 0
+  const float wj = exp2f(mj - M);
+  den = wave_sum(lj * wj);
+  return wj;
+}
+
+// fp16(num / den) with num = sum_j a[j] w_j in split order (w_j read from
+// lane j; slots j >= NS carry weight 0 and add exactly nothing).
+template <int NSMAX>
+__device__ __forceinline__ uint16_t lse_out(const float (&a)[NSMAX], float wj, float den) {
+  float num = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NSMAX; ++j) num += a[j] * lane_f(wj, j);
+  return f2h(den > 0.0f ? num / den : num);
+}
+
 }  // namespace lemoq_attn

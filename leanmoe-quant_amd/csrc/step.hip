@@ -2,17 +2,21 @@
 // canonical cell (w8a16 attention + experts, W8 lm_head, KV-INT8 cache) on a
 // stream, ready to be captured into a hipGraph by the caller.
 //
-// Per layer (7 launches):
+// Per layer (6 launches):
 //   1 gemv_w8_fused   input RMSNorm (+ embedding gather on layer 0) -> packed q|k|v
 //   2 attn_split_fused q_norm/k_norm, RoPE at *pos, KV-INT8 write of slot *pos,
 //                     split-KV partials over [0, *pos]
-//   3 attn_merge      LSE merge of the partials
-//   4 gemv_w8_fused   o_proj, residual add in the epilogue
-//   5 router_logits   post-attention RMSNorm + router GEMV -> fp16 logits
+//   3 attn_merge_o_proj  LSE merge of each block's 4 heads + their share of
+//                     o_proj -> fp32 partial sums per head group
+//   4 router_logits_resid  o = fp16(sum of partials), h_mid = fp16(o + h),
+//                     post-attention RMSNorm + router GEMV -> fp16 logits
 //                     (one wave per expert row)
-//   6 moe_gate_up_w8  softmax/top-k of the logits in every wave, then gate/up
+//   5 moe_gate_up_w8  softmax/top-k of the logits in every wave, then gate/up
 //                     + SiLU of the 8 selected experts (stores ids, weights)
-//   7 moe_down_w8     down projection x routing weight + residual add
+//   6 moe_down_w8     down projection x routing weight + residual (h_mid) -> h
+// Shapes outside the fused attention-output path (or a step without o_part /
+// h_mid) run 3-4 as three launches: attn_merge, the o_proj GEMV with the
+// residual add in its epilogue, router_logits.
 // then final RMSNorm + lm_head GEMV with per-block argmax partials, and the
 // greedy selection that writes the next token and advances *pos / *filled.
 //
@@ -41,6 +45,14 @@ extern "C" int lemoq_olmoe_decode_step(const LemoqOlmoeStep* p, void* stream) {
       p->num_splits <= 0 || p->vocab <= 0)
     return LEMOQ_ERR_SHAPE;
   const int64_t S = p->max_seq;
+  // Fused attention-output path: the shape rules of lemoq_attn_merge_o_proj_w8
+  // and lemoq_router_logits_resid, checked once so that a step never enqueues
+  // part of a layer before an argument is rejected.
+  const int64_t n_part = HD / 512;
+  const bool fused_o = p->o_part && p->h_mid && D == 128 && p->heads % 4 == 0 &&
+                       p->num_splits <= 64 && (H == 2048 || H == 4096) &&
+                       (n_part == 1 || n_part == 2 || n_part == 4 || n_part == 8) &&
+                       p->group % 16 == 0 && HD % p->group == 0;
   for (int64_t L = 0; L < p->num_layers; ++L) {
     const LemoqOlmoeLayer& w = p->layers[L];
     const bool first = L == 0;
@@ -54,22 +66,34 @@ extern "C" int lemoq_olmoe_decode_step(const LemoqOlmoeStep* p, void* stream) {
                                         p->cos_tab, p->sin_tab, p->pos, w.kc, w.ks, w.vc, w.vs,
                                         S * D, S, p->num_splits, p->qk_scale, p->part_m,
                                         p->part_l, p->part_acc, stream));
-    // 3. LSE merge of the partials.
-    LEMOQ_TRY(lemoq_attn_merge(p->part_m, p->part_l, p->part_acc, p->heads, p->num_splits, D,
-                               p->attn, stream));
-    // 4. o_proj; h = fp16(fp16(o) + h).
-    LEMOQ_TRY(lemoq_gemv_w8_fused(p->attn, nullptr, 0, nullptr, p->eps, nullptr, w.o_codes,
-                                  w.o_scale, H, HD, p->group, p->h, p->h, stream));
-    // 5. post-attention RMSNorm + router logits.
-    LEMOQ_TRY(lemoq_router_logits(p->h, w.ln_post, p->eps, H, w.router, p->num_experts, p->xn,
-                                  p->router_logits, stream));
-    // 6-7. routing + grouped MoE; h = fp16(fp16(moe) + h).
+    if (fused_o) {
+      // 3. LSE merge + o_proj partials per group of 4 heads.
+      LEMOQ_TRY(lemoq_attn_merge_o_proj_w8(p->part_m, p->part_l, p->part_acc, p->heads,
+                                           p->num_splits, D, w.o_codes, w.o_scale, H, p->group,
+                                           p->o_part, stream));
+      // 4. h_mid = fp16(fp16(o) + h); post-attention RMSNorm + router logits.
+      LEMOQ_TRY(lemoq_router_logits_resid(p->o_part, n_part, p->h, w.ln_post, p->eps, H,
+                                          w.router, p->num_experts, p->h_mid, p->xn,
+                                          p->router_logits, stream));
+    } else {
+      // 3. LSE merge of the partials.
+      LEMOQ_TRY(lemoq_attn_merge(p->part_m, p->part_l, p->part_acc, p->heads, p->num_splits, D,
+                                 p->attn, stream));
+      // 4. o_proj; h = fp16(fp16(o) + h).
+      LEMOQ_TRY(lemoq_gemv_w8_fused(p->attn, nullptr, 0, nullptr, p->eps, nullptr, w.o_codes,
+                                    w.o_scale, H, HD, p->group, p->h, p->h, stream));
+      // 4b. post-attention RMSNorm + router logits.
+      LEMOQ_TRY(lemoq_router_logits(p->h, w.ln_post, p->eps, H, w.router, p->num_experts, p->xn,
+                                    p->router_logits, stream));
+    }
+    // 5-6. routing + grouped MoE; h = fp16(fp16(moe) + residual).
     LEMOQ_TRY(lemoq_moe_gate_up_w8_routed(p->xn, w.gu_codes, w.gu_scale, p->router_logits,
                                           p->top_k, (int)p->norm_topk_prob, p->num_experts,
                                           p->ffn, H, p->group, p->act, p->top_i, p->top_w,
                                           stream));
     LEMOQ_TRY(lemoq_moe_down_w8(p->act, w.dn_codes, w.dn_scale, p->top_i, p->top_w, p->top_k,
-                                p->num_experts, H, p->ffn, p->group, p->h, p->h, stream));
+                                p->num_experts, H, p->ffn, p->group, fused_o ? p->h_mid : p->h,
+                                p->h, stream));
   }
   // Final norm + W8 lm_head with argmax partials, then greedy selection and step advance.
   return lemoq_lm_head_argmax_w8(p->h, p->final_norm, p->eps, p->lm_codes, p->lm_scale, p->vocab,

@@ -19,7 +19,7 @@ LIB_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib")
 LIB_NAME = "liblemoq_hip.so"
 LIB_PATH = os.path.join(LIB_DIR, LIB_NAME)
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -102,6 +102,8 @@ class LemoqOlmoeStep(ctypes.Structure):
         ("am_val", _P),
         ("am_idx", _P),
         ("am_len", _I64),
+        ("o_part", _P),
+        ("h_mid", _P),
     ]
 
 
@@ -120,6 +122,8 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         _I,
         [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P],
     ),
+    "lemoq_attn_merge_o_proj_w8": (_I, [_P, _P, _P, _I64, _I64, _I64, _P, _P, _I64, _I64, _P, _P]),
+    "lemoq_router_logits_resid": (_I, [_P, _I64, _P, _P, _F, _I64, _P, _I64, _P, _P, _P, _P]),
     "lemoq_attn_split_f16": (
         _I,
         [_P, _P, _P, _I64, _P, _I64, _I64, _I64, _F, _P, _P, _P, _P],

@@ -270,6 +270,11 @@ class DecodeSession:
         n_parts = int(_hip.load().lemoq_lm_head_argmax_parts(s.vocab))
         self.am_val = torch.zeros((n_parts,), dtype=torch.float32, device=dev)
         self.am_idx = torch.zeros((n_parts,), dtype=torch.int32, device=dev)
+        # o_proj partial sums per group of 4 heads and the residual after
+        # attention (the step's fused merge + o_proj path; unused by shapes it
+        # does not cover, which run merge, o_proj and router as three launches)
+        self.o_part = torch.zeros((max(1, HD // 512), s.hidden), dtype=torch.float32, device=dev)
+        self.h_mid = torch.zeros((s.hidden,), **f16)
 
         P = _hip.ptr
         self._layer_structs = (_hip.LemoqOlmoeLayer * s.layers)()
@@ -300,7 +305,8 @@ class DecodeSession:
         st.prompt, st.prompt_len = P(self.prompt), self.ctx
         st.history, st.history_len = P(self.history), int(self.history.numel())
         for name in ("h", "xn", "qkv", "q_rot", "attn", "part_m", "part_l", "part_acc",
-                     "router_logits", "top_w", "top_i", "act", "logits", "am_val", "am_idx"):
+                     "router_logits", "top_w", "top_i", "act", "logits", "am_val", "am_idx", "o_part",
+                     "h_mid"):
             setattr(st, name, P(getattr(self, name)))
         st.am_len = n_parts
         self._step = st
@@ -346,9 +352,19 @@ class DecodeSession:
         return self.logits
 
     @property
+    def attn_output_fused(self) -> bool:
+        """Whether the step runs merge + o_proj as one launch and the residual add
+        in the router launch (the shape rule of csrc/step.hip)."""
+        s = self.shape
+        HD = s.heads * s.head_dim
+        return (bool(self._step.o_part) and bool(self._step.h_mid) and s.head_dim == 128 and s.heads % 4 == 0
+                and self.num_splits <= 64 and s.hidden in (2048, 4096) and HD // 512 in (1, 2, 4, 8)
+                and s.group_size % 16 == 0 and HD % s.group_size == 0)
+
+    @property
     def launches_per_step(self) -> int:
         """Kernel launches in one captured step (see csrc/step.hip)."""
-        return 7 * self.shape.layers + 2
+        return (6 if self.attn_output_fused else 7) * self.shape.layers + 2
 
     def capture(self) -> dict[str, Any]:
         """Capture one decode step into a hipGraph (state is untouched by the capture)."""

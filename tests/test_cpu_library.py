@@ -83,5 +83,20 @@ def test_argument_rejection_happens_before_any_launch():
     assert lib.lemoq_moe_prefill_gate_up(fake, 2048, fake, fake, 64, fake, fake, 1000, 128, fake, None) == -2
     assert lib.lemoq_moe_prefill_down(fake, 1024, fake, fake, fake, 64, fake + 4, fake, 2048, 128, fake, None) == -4
     assert lib.lemoq_moe_prefill_combine(fake, fake, 4, 9, 2048, None, fake, None) == -2
+    # fused merge + o_proj: head_dim 64 and 6 heads unsupported, N % 32, too many splits, misaligned codes
+    assert lib.lemoq_attn_merge_o_proj_w8(fake, fake, fake, 16, 16, 64, fake, fake, 2048, 128, fake, None) == -3
+    assert lib.lemoq_attn_merge_o_proj_w8(fake, fake, fake, 6, 16, 128, fake, fake, 2048, 128, fake, None) == -3
+    assert lib.lemoq_attn_merge_o_proj_w8(fake, fake, fake, 16, 16, 128, fake, fake, 2040, 128, fake, None) == -2
+    assert lib.lemoq_attn_merge_o_proj_w8(fake, fake, fake, 16, 65, 128, fake, fake, 2048, 128, fake, None) == -2
+    assert lib.lemoq_attn_merge_o_proj_w8(fake, fake, fake, 16, 16, 128, fake + 4, fake, 2048, 128, fake, None) == -4
+    assert lib.lemoq_attn_merge_o_proj_w8(None, fake, fake, 16, 16, 128, fake, fake, 2048, 128, fake, None) == -1
+    # router after the partials: hidden 1024 and 3 partial rows unsupported, h_out overlapping h
+    rr = lambda part, npart, h, hidden, h_out: lib.lemoq_router_logits_resid(  # noqa: E731
+        part, npart, h, fake, 1e-5, hidden, fake, 64, h_out, fake, fake, None)
+    assert rr(fake, 4, 1 << 20, 1024, 1 << 21) == -3
+    assert rr(fake, 3, 1 << 20, 2048, 1 << 21) == -3
+    assert rr(fake, 4, 1 << 20, 2048, (1 << 20) + 2048) == -2
+    assert rr(fake + 4, 4, 1 << 20, 2048, 1 << 21) == -4
+    assert rr(fake, 4, 1 << 20, 2048, None) == -1
     with pytest.raises(ValueError):
         _hip.call("lemoq_gemv_w8", None, 1, 16, None, None, 16, 16, 16, None, 1, None)

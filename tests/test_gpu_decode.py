@@ -133,3 +133,35 @@ def test_prompt_tokens_are_fed_then_greedy_takes_over(dev):
     tokens, _ = oracle.run(prompt, 3)
     sess.replay(3)
     assert sess.generated() == tokens
+
+
+def test_fused_attention_output_path_matches_three_launches(dev):
+    """At the OLMoE shape the step runs merge + o_proj as one launch and the
+    residual add in the router launch (lemoq_attn_merge_o_proj_w8,
+    lemoq_router_logits_resid).  With o_part unset the same step runs
+    lemoq_attn_merge, the o_proj GEMV and lemoq_router_logits.  Both orders of
+    the o_proj fp32 sum must give the same step to fp16 rounding: per step
+    logits KL < 1e-4 and the same greedy token unless the top-2 margin is
+    below twice the logit difference."""
+    print("case: fused vs three-launch attention output, OLMoE shape, 4 layers", flush=True)
+    shape = OlmoeShape(**{**OLMOE_1B_7B.__dict__, "layers": 4})
+    w = OlmoeW8Weights.random(shape, seed=11, device=dev)
+    sess = DecodeSession(w, [3] * 200, max_new_tokens=8, num_splits=None)
+    sess.prefill()
+    o_part = sess._step.o_part
+    assert o_part
+    for _ in range(4):
+        p, tok = sess.position, int(sess.token.item())
+        sess._step.o_part = None
+        sess.decode_eager()
+        ref = sess.logits_cpu()
+        sess._step.o_part = o_part
+        sess.set_position(p, tok)
+        sess.decode_eager()
+        got = sess.logits_cpu()
+        diff = float((got.float() - ref.float()).abs().max())
+        kl = _kl(ref, got)
+        print("pos %d diff %.2e kl %.1e margin %.2e" % (p, diff, kl, _margin(ref)))
+        assert kl < 1e-4, kl
+        if int(torch.argmax(got.float())) != int(torch.argmax(ref.float())):
+            assert _margin(ref) <= 2 * diff

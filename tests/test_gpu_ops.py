@@ -534,6 +534,97 @@ def test_attn_merge_vs_oracle(ns, D, dev):
     assert_close(got, ref, what="merge ns=%d D=%d" % (ns, D))
 
 
+def _merge_inputs(heads, ns, D, seed):
+    g = torch.Generator().manual_seed(seed)
+    m = (torch.rand((heads, ns), generator=g) * 40 - 20).float()
+    l = torch.rand((heads, ns), generator=g).float() * 10 + 0.1
+    acc = torch.randn((heads, ns, D), generator=g).float() * l.unsqueeze(-1)
+    empty = torch.rand((heads, ns), generator=g) < 0.3
+    empty[1] = True  # one head with every split empty -> attention output 0
+    m[empty], l[empty], acc[empty] = float("-inf"), 0.0, 0.0
+    return m, l, acc
+
+
+@pytest.mark.parametrize("ns", [1, 5, 16, 17, 64])
+@pytest.mark.parametrize("heads", [16, 4, 8, 32])
+def test_merge_o_proj_partials(ns, heads, dev):
+    """lemoq_attn_merge_o_proj_w8 (merge fused into o_proj, split over groups of
+    4 heads).  Its merge is lemoq_attn_merge's, so each partial row g must equal
+    the fp64 product of the dequantised columns [512g, 512g+512) with the
+    merged fp16 attention output of lemoq_attn_merge, to fp32 summation error;
+    fp16(sum of partials) is the o_proj output (oracle: LSE merge in fp64, then
+    the w8 linear)."""
+    from lemoq import _hip
+
+    D, N, group = 128, 2048, 128
+    HD = heads * D
+    m, l, acc = _merge_inputs(heads, ns, D, seed=ns * 7 + heads)
+    w = randn(N, HD, seed=900 + heads, std=0.02)
+    codes, scale = _q8(w, group)
+    md, ld, ad, cd, sd = (t.to(dev) for t in (m, l, acc, codes, scale))
+    part = torch.full((heads // 4, N), float("nan"), dtype=torch.float32, device=dev)
+    attn = torch.empty((HD,), dtype=torch.float16, device=dev)
+    st = _hip.stream_of(dev)
+    _hip.call("lemoq_attn_merge_o_proj_w8", _hip.ptr(md), _hip.ptr(ld), _hip.ptr(ad), heads, ns, D, _hip.ptr(cd),
+              _hip.ptr(sd), N, group, _hip.ptr(part), st)
+    _hip.call("lemoq_attn_merge", _hip.ptr(md), _hip.ptr(ld), _hip.ptr(ad), heads, ns, D, _hip.ptr(attn), st)
+    torch.cuda.synchronize()
+    p = part.cpu().double()
+    assert torch.isfinite(p).all()
+    wd = ops.dequant_w8(codes, scale, group).double()  # (N, HD), the fp16-rounded weights
+    a = attn.cpu().double()
+    for gi in range(heads // 4):
+        cols = slice(512 * gi, 512 * gi + 512)
+        ref = wd[:, cols] @ a[cols]
+        err = (p[gi] - ref).abs().max().item()
+        assert err <= 1e-5 * (wd[:, cols].abs() @ a[cols].abs()).max().item() + 1e-7, (gi, err)
+    got = p.sum(0).to(torch.float16)
+    a_ref = ops.merge_splits(m.double(), l.double(), acc.double()).reshape(-1).to(torch.float16)
+    ref = ops.dequant_gemm_separate(a_ref.reshape(1, -1), codes, scale, group).reshape(-1)
+    assert_close(got, ref, what="merge+o_proj ns=%d heads=%d" % (ns, heads))
+
+
+@pytest.mark.parametrize("H,n_part", [(2048, 4), (2048, 1), (2048, 2), (2048, 8), (4096, 4)])
+@pytest.mark.parametrize("E", [64, 8, 100])
+def test_router_logits_resid_vs_oracle(H, n_part, E, dev):
+    """lemoq_router_logits_resid: h' = fp16(fp16(sum of partials) + h) must be
+    bit-exact against the same fp32 sum and fp16 add on the CPU; xn and the
+    logits against the oracle's RMSNorm and router linear (the bounds of the
+    lemoq_router_logits test), and the routing of the logits must give the
+    oracle's expert ids."""
+    from lemoq import _hip
+
+    gen = torch.Generator().manual_seed(H + n_part * 10 + E)
+    part = torch.randn((n_part, H), generator=gen).float() * 0.5
+    h = randn(H, seed=E + 1).to(torch.float16)
+    ln = (torch.rand(H, generator=gen) + 0.5).to(torch.float16)
+    rw = randn(E, H, seed=E + 2, std=0.02).to(torch.float16)
+    pd, hd, lnd, rwd = part.to(dev), h.to(dev), ln.to(dev), rw.to(dev)
+    h_out = torch.empty(H, dtype=torch.float16, device=dev)
+    xn = torch.empty(H, dtype=torch.float16, device=dev)
+    lg = torch.empty(E, dtype=torch.float16, device=dev)
+    _hip.call("lemoq_router_logits_resid", _hip.ptr(pd), n_part, _hip.ptr(hd), _hip.ptr(lnd), 1e-5, H,
+              _hip.ptr(rwd), E, _hip.ptr(h_out), _hip.ptr(xn), _hip.ptr(lg), _hip.stream_of(dev))
+    torch.cuda.synchronize()
+    o = part[0].clone()
+    for gi in range(1, n_part):
+        o = o + part[gi]  # fp32, group order
+    h_mid = o.to(torch.float16) + h  # torch's fp16 add: one rounding
+    assert torch.equal(h_out.cpu(), h_mid)
+    xn_ref = ops.rms_norm(h_mid, ln, 1e-5)
+    assert max_abs(xn.cpu(), xn_ref) <= 2e-3
+    rlg, _, rti = ops.route(xn_ref.reshape(1, H), rw, min(8, E), True)
+    assert max_abs(lg.cpu(), rlg.reshape(-1)) <= 2e-3
+    # the step's other router on h' gives the same fp16 outputs
+    xn2 = torch.empty_like(xn)
+    lg2 = torch.empty_like(lg)
+    hm = h_mid.to(dev)
+    _hip.call("lemoq_router_logits", _hip.ptr(hm), _hip.ptr(lnd), 1e-5, H, _hip.ptr(rwd), E, _hip.ptr(xn2),
+              _hip.ptr(lg2), _hip.stream_of(dev))
+    torch.cuda.synchronize()
+    assert max_abs(xn.cpu(), xn2.cpu()) <= 2e-3 and max_abs(lg.cpu(), lg2.cpu()) <= 2e-3
+
+
 def test_warm_entry_points_run_before_capture(dev):
     """The reference's warm() hooks (one real launch, then sync) exist with the
     same signatures and run on the device."""
