@@ -361,7 +361,7 @@ int lemoq_attn_split_fused_i8(const uint16_t* qkv, int64_t heads, int64_t head_d
  * _set_step_inputs, :655-678).  next = argmax(logits[0:n]) (first index on
  * ties), or prompt[*pos + 1] while *pos + 1 < prompt_len; then
  * *token = next, history[*pos + 1] = next (when *pos + 1 < history_len),
- * *pos += 1, *filled = *pos + 1.
+ * *pos += 1, *filled = *pos + 1.  0 < n < 2^31.
  * ------------------------------------------------------------------------- */
 int lemoq_argmax_advance(const uint16_t* logits, int64_t n, int64_t* token,
                          int64_t* pos, int32_t* filled, const int64_t* prompt,

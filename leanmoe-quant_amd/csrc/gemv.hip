@@ -308,7 +308,52 @@ GemvArgs make_args(const uint16_t* x, int64_t x_ld, const int64_t* x_row_index, 
 // Ties resolve to the lowest row; NaN never wins; all -inf/NaN -> row 0.
 // Then: next = argmax, or prompt[*pos + 1] while *pos + 1 < prompt_len;
 // *token = next, history[*pos + 1] = next, *pos += 1, *filled = *pos + 1.
+// *pos and the prompt token it selects are loaded at entry, around the first
+// pass of candidates, so the advance at the end waits on no memory; the wave
+// reductions are DPP (largest value, then the lowest row among the lanes
+// holding it).  n < 2^31.
 // ---------------------------------------------------------------------------
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+__device__ __forceinline__ int wave_min_i32(int v) {
+  v = min(v, dpp_i<LEMOQ_DPP_QUAD_1032>(v));
+  v = min(v, dpp_i<LEMOQ_DPP_QUAD_2301>(v));
+  v = min(v, dpp_i<LEMOQ_DPP_ROW_HALF_MIRROR>(v));
+  v = min(v, dpp_i<LEMOQ_DPP_ROW_MIRROR>(v));
+  return min(min(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+             min(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+}
+
+constexpr int kArgmaxPass = 8;  // candidate loads per thread per pass, all issued before comparing
+
+template <bool PARTIALS>
+__device__ __forceinline__ void argmax_load_pass(const uint16_t* __restrict__ logits,
+                                                 const float* __restrict__ pv,
+                                                 const int32_t* __restrict__ pi, int64_t n,
+                                                 int64_t base, int tid, float (&v)[kArgmaxPass],
+                                                 int (&ix)[kArgmaxPass]) {
+#pragma unroll
+  for (int j = 0; j < kArgmaxPass; ++j) {
+    const int64_t i = base + (int64_t)j * 1024 + tid;
+    const int64_t ic = i < n ? i : n - 1;  // clamped: every load is valid and unconditional
+    v[j] = PARTIALS ? pv[ic] : h2f(logits[ic]);
+    const int raw = PARTIALS ? pi[ic] : (int)ic;
+    ix[j] = i < n ? raw : -1;
+  }
+}
+
+__device__ __forceinline__ void argmax_fold_pass(const float (&v)[kArgmaxPass],
+                                                 const int (&ix)[kArgmaxPass], float& bv, int& bi) {
+#pragma unroll
+  for (int j = 0; j < kArgmaxPass; ++j)
+    if (ix[j] >= 0 && (v[j] > bv || (v[j] == bv && ix[j] < bi))) {
+      bv = v[j];
+      bi = ix[j];
+    }
+}
+
 template <bool PARTIALS>
 __global__ __launch_bounds__(1024) void argmax_advance_kernel(
     const uint16_t* __restrict__ logits, const float* __restrict__ pv,
@@ -316,60 +361,43 @@ __global__ __launch_bounds__(1024) void argmax_advance_kernel(
     int64_t* __restrict__ pos, int32_t* __restrict__ filled, const int64_t* __restrict__ prompt,
     int64_t prompt_len, int64_t* __restrict__ history, int64_t history_len) {
   __shared__ float bvs[16];
-  __shared__ int64_t bis[16];
+  __shared__ int bis[16];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t p = pos[0];
+  float v[kArgmaxPass];
+  int ix[kArgmaxPass];
+  argmax_load_pass<PARTIALS>(logits, pv, pi, n, 0, tid, v, ix);
+  LEMOQ_LOADS_ISSUED();
+  // The prompt token of position p + 1 (a valid address whether or not it is used).
+  const bool feed = prompt && p + 1 >= 0 && p + 1 < prompt_len;
+  const int64_t ptok = prompt ? prompt[feed ? p + 1 : 0] : 0;
   float bv = -INFINITY;
-  int64_t bi = INT64_MAX;
-  // Passes of 8 loads per thread, all issued (addresses clamped into [0, n))
-  // before any comparison, so a pass waits on memory once.  The result does
-  // not depend on the visiting order: ties go to the lowest index.
-  constexpr int B = 8;
-  for (int64_t base = 0; base < n; base += (int64_t)B * 1024) {
-    float v[B];
-    int64_t ix[B];
-#pragma unroll
-    for (int j = 0; j < B; ++j) {
-      const int64_t i = base + (int64_t)j * 1024 + tid;
-      const int64_t ic = i < n ? i : n - 1;
-      v[j] = PARTIALS ? pv[ic] : h2f(logits[ic]);
-      ix[j] = PARTIALS ? (int64_t)pi[ic] : ic;
-      if (i >= n) ix[j] = -1;
-    }
-#pragma unroll
-    for (int j = 0; j < B; ++j) {
-      if (ix[j] >= 0 && (v[j] > bv || (v[j] == bv && ix[j] < bi))) {
-        bv = v[j];
-        bi = ix[j];
-      }
-    }
+  int bi = 0x7fffffff;
+  argmax_fold_pass(v, ix, bv, bi);
+  for (int64_t base = (int64_t)kArgmaxPass * 1024; base < n; base += (int64_t)kArgmaxPass * 1024) {
+    argmax_load_pass<PARTIALS>(logits, pv, pi, n, base, tid, v, ix);
+    argmax_fold_pass(v, ix, bv, bi);
   }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const float ov = __shfl_xor(bv, o, 64);
-    const int64_t oi = __shfl_xor(bi, o, 64);
-    if (ov > bv || (ov == bv && oi < bi)) {
-      bv = ov;
-      bi = oi;
-    }
-  }
+  // NaN is never held (every comparison with it is false), so the wave max is
+  // a real value or -inf; lanes holding it offer their lowest row.
+  const float M = wave_max(bv);
+  const int I = wave_min_i32(bv == M ? bi : 0x7fffffff);
   if (lane == 0) {
-    bvs[wave] = bv;
-    bis[wave] = bi;
+    bvs[wave] = M;
+    bis[wave] = I;
   }
   __syncthreads();
   if (tid == 0) {
-    float v = bvs[0];
-    int64_t idx = bis[0];
+    float bm = bvs[0];
+    int idx = bis[0];
     for (int w = 1; w < 16; ++w) {
-      if (bvs[w] > v || (bvs[w] == v && bis[w] < idx)) {
-        v = bvs[w];
+      if (bvs[w] > bm || (bvs[w] == bm && bis[w] < idx)) {
+        bm = bvs[w];
         idx = bis[w];
       }
     }
-    if (idx == INT64_MAX || idx < 0) idx = 0;  // every logit was -inf or NaN
-    const int64_t p = pos[0];
-    int64_t next = idx;
-    if (prompt && p + 1 >= 0 && p + 1 < prompt_len) next = prompt[p + 1];
+    if (idx == 0x7fffffff || idx < 0) idx = 0;  // every logit was -inf or NaN
+    const int64_t next = feed ? ptok : (int64_t)idx;
     token[0] = next;
     if (history && p + 1 >= 0 && p + 1 < history_len) history[p + 1] = next;
     pos[0] = p + 1;
@@ -712,7 +740,7 @@ extern "C" int lemoq_argmax_advance(const uint16_t* logits, int64_t n, int64_t* 
                                     int64_t prompt_len, int64_t* history, int64_t history_len,
                                     void* stream) {
   if (!logits || !token || !pos || !filled) return LEMOQ_ERR_NULL;
-  if (n <= 0) return LEMOQ_ERR_SHAPE;
+  if (n <= 0 || n > 0x7ffffffeLL) return LEMOQ_ERR_SHAPE;
   hipLaunchKernelGGL((argmax_advance_kernel<false>), dim3(1), dim3(1024), 0, lemoq_stream(stream),
                      logits, nullptr, nullptr, n, token, pos, filled, prompt, prompt_len, history,
                      history_len);

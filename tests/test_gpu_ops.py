@@ -625,6 +625,106 @@ def test_router_logits_resid_vs_oracle(H, n_part, E, dev):
     assert max_abs(xn.cpu(), xn2.cpu()) <= 2e-3 and max_abs(lg.cpu(), lg2.cpu()) <= 2e-3
 
 
+def _advance(hip, dev, logits, pos, prompt=None, history_len=64):
+    """One lemoq_argmax_advance; returns (token, pos, filled, history)."""
+    ld = logits.to(dev)
+    tok = torch.full((1,), -7, dtype=torch.int64, device=dev)
+    pd = torch.tensor([pos], dtype=torch.int64, device=dev)
+    fd = torch.zeros((1,), dtype=torch.int32, device=dev)
+    hist = torch.full((history_len,), -5, dtype=torch.int64, device=dev)
+    pr = torch.tensor(prompt, dtype=torch.int64, device=dev) if prompt is not None else None
+    hip.call("lemoq_argmax_advance", hip.ptr(ld), logits.numel(), hip.ptr(tok), hip.ptr(pd), hip.ptr(fd),
+             hip.ptr(pr) if pr is not None else None, len(prompt) if prompt is not None else 0, hip.ptr(hist),
+             history_len, hip.stream_of(dev))
+    torch.cuda.synchronize()
+    return int(tok.item()), int(pd.item()), int(fd.item()), hist.cpu()
+
+
+def _first_argmax(x: torch.Tensor) -> int:
+    """Lowest index of the largest non-NaN value (0 when there is none)."""
+    v = x.float().clone()
+    v[torch.isnan(v)] = float("-inf")
+    m = v.max()
+    return int(torch.nonzero(v == m)[0]) if m > float("-inf") or (v == m).any() else 0
+
+
+@pytest.mark.parametrize("n", [1, 5, 1023, 8192, 8195, 50304])
+def test_argmax_advance_ties_nan_and_passes(n, dev):
+    """Greedy selection of lemoq_argmax_advance (the device form of the
+    reference's logits.argmax(), cudagraph.py:759-762): lowest index on ties,
+    NaN never selected, all -inf -> 0; n spans one and several passes of
+    8 x 1024 candidates."""
+    from lemoq import _hip
+
+    g = torch.Generator().manual_seed(n)
+    x = torch.randn(n, generator=g).to(torch.float16)
+    tok, p, f, hist = _advance(_hip, dev, x, 9)
+    assert tok == _first_argmax(x) and p == 10 and f == 11 and int(hist[10]) == tok
+    if n >= 5:
+        y = x.clone()
+        top = float(y.float().max()) + 1.0
+        y[n - 1] = top
+        y[n // 2] = top
+        y[1] = float("nan")
+        tok, _, _, _ = _advance(_hip, dev, y, 0)
+        assert tok == n // 2 if n // 2 < n - 1 else tok == n - 1
+        assert tok == _first_argmax(y)
+    z = torch.full((n,), float("-inf"), dtype=torch.float16)
+    assert _advance(_hip, dev, z, 0)[0] == 0
+    z[n - 1] = float("nan")
+    assert _advance(_hip, dev, z, 0)[0] == 0
+    if n >= 3:
+        z[n - 2] = -60000.0
+        assert _advance(_hip, dev, z, 0)[0] == n - 2
+
+
+def test_argmax_advance_prompt_feed_and_history_bounds(dev):
+    """While pos + 1 < prompt_len the next token is prompt[pos + 1], after that
+    the argmax; history[pos + 1] is written only inside history_len."""
+    from lemoq import _hip
+
+    x = torch.zeros(100, dtype=torch.float16)
+    x[42] = 3.0
+    prompt = [11, 12, 13, 14]
+    assert _advance(_hip, dev, x, 0, prompt)[0] == 12
+    assert _advance(_hip, dev, x, 2, prompt)[0] == 14
+    assert _advance(_hip, dev, x, 3, prompt)[0] == 42
+    tok, p, f, hist = _advance(_hip, dev, x, 7, history_len=8)  # pos + 1 == history_len: no write
+    assert tok == 42 and p == 8 and f == 9 and (hist == -5).all()
+
+
+@pytest.mark.parametrize("N", [50304, 1000, 37])
+def test_lm_head_argmax_partials(N, dev):
+    """lemoq_lm_head_argmax_w8: the fp16 logits of the w8 GEMV (final RMSNorm in
+    the prologue) against the oracle, and the selected token equal to the
+    lowest-index argmax of the GPU's own logits (the partial reduction must not
+    change the selection)."""
+    from lemoq import _hip
+
+    H, group = 2048, 128
+    w = randn(N, H, seed=N, std=0.02)
+    codes, scale = _q8(w, group)
+    x = randn(H, seed=N + 1).to(torch.float16)
+    nw = (torch.rand(H, generator=torch.Generator().manual_seed(N)) + 0.5).to(torch.float16)
+    xd, nd, cd, sd = x.to(dev), nw.to(dev), codes.to(dev), scale.to(dev)
+    parts = int(_hip.load().lemoq_lm_head_argmax_parts(N))
+    pv = torch.empty(parts, dtype=torch.float32, device=dev)
+    pi = torch.empty(parts, dtype=torch.int32, device=dev)
+    logits = torch.empty(N, dtype=torch.float16, device=dev)
+    tok = torch.zeros(1, dtype=torch.int64, device=dev)
+    pos = torch.zeros(1, dtype=torch.int64, device=dev)
+    fill = torch.zeros(1, dtype=torch.int32, device=dev)
+    _hip.call("lemoq_lm_head_argmax_w8", _hip.ptr(xd), _hip.ptr(nd), 1e-5, _hip.ptr(cd), _hip.ptr(sd), N, H, group,
+              _hip.ptr(logits), _hip.ptr(pv), _hip.ptr(pi), parts, _hip.ptr(tok), _hip.ptr(pos), _hip.ptr(fill),
+              None, 0, None, 0, _hip.stream_of(dev))
+    torch.cuda.synchronize()
+    lg = logits.cpu()
+    ref = ops.dequant_gemm_separate(ops.rms_norm(x, nw, 1e-5).reshape(1, -1), codes, scale, group).reshape(-1)
+    assert_close(lg, ref, what="lm_head N=%d" % N)
+    assert int(tok.item()) == _first_argmax(lg)
+    assert int(pos.item()) == 1 and int(fill.item()) == 2
+
+
 def test_warm_entry_points_run_before_capture(dev):
     """The reference's warm() hooks (one real launch, then sync) exist with the
     same signatures and run on the device."""
