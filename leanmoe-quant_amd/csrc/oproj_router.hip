@@ -52,12 +52,26 @@ struct MergeOprojArgs {
 // 512 g + 16 (l % 32) of row 2i + l / 32 for i = 0..3 (a row slice is 512
 // bytes, two rows per wave load).  Every load is issued at entry: the four
 // weight slices and their scales first, then the merge inputs.
+//
+// Blocks are dispatched round-robin over the 8 XCDs (each with its own L2).
+// With G = heads / 4 groups and R = N / 32 row blocks, linear block b goes to
+// XCD b % 8; when G divides 8 and R * G is a multiple of 8, the blocks of XCD
+// c all take head group c % G, so each L2 fetches one group's 33 KB of split
+// partials instead of every group's.
 template <int NSMAX>
 __global__ __launch_bounds__(256) void merge_oproj_kernel(const MergeOprojArgs a) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int half = lane >> 5, l32 = lane & 31;
-  const int g = blockIdx.y;
-  const int64_t row0 = (int64_t)blockIdx.x * MO_ROWS + wave * MO_ROWS_WAVE;
+  const int G = gridDim.y, R = gridDim.x;
+  const int b = blockIdx.x + R * blockIdx.y;
+  int g = blockIdx.y, rb = blockIdx.x;
+  if (8 % G == 0 && (R * G) % 8 == 0) {
+    const int xcd = b % 8, k = b / 8;  // k-th block on this XCD, k < R * G / 8
+    const int per = 8 / G;             // XCDs per head group
+    g = xcd % G;
+    rb = (xcd / G) + per * k;          // XCDs of one group interleave its row blocks
+  }
+  const int64_t row0 = (int64_t)rb * MO_ROWS + wave * MO_ROWS_WAVE;
   const int k0 = g * MO_COLS + 16 * l32;
   const int ngroups = a.HD / a.group;
   u32x4 c[4];
