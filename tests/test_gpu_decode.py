@@ -20,6 +20,10 @@ from oracle.olmoe import OracleDecoder
 pytestmark = pytest.mark.gpu
 
 TINY = OlmoeShape(hidden=512, heads=4, head_dim=128, layers=2, num_experts=8, top_k=2, ffn=256, vocab=1024)
+# hidden 2048, 16 heads: the step takes the fused attention-output path (merge + o_proj over
+# 4-head groups, residual in the router launch); TINY takes the three-launch path.
+TINY_FUSED = OlmoeShape(hidden=2048, heads=16, head_dim=128, layers=2, num_experts=8, top_k=2, ffn=256,
+                        vocab=1024)
 
 
 def _kl(p_logits, q_logits) -> float:
@@ -79,6 +83,16 @@ def _check_steps(toks, gl, rl, *, rel=2e-2):
 def test_tiny_model_32_steps_match_oracle(norm, dev):
     print("case: tiny model, 32 steps, norm_topk_prob=%s" % norm, flush=True)
     toks, gl, rl = _teacher_forced(TINY, [1] * 16, 32, 3, dev, norm_topk_prob=norm)
+    _check_steps(toks, gl, rl)
+
+
+@pytest.mark.parametrize("norm", [False, True])
+def test_fused_path_model_32_steps_match_oracle(norm, dev):
+    print("case: hidden-2048 test model (fused attention output), 32 steps, norm_topk_prob=%s" % norm,
+          flush=True)
+    w = OlmoeW8Weights.random(TINY_FUSED, seed=4, device=dev)
+    assert DecodeSession(w, [1] * 4, max_new_tokens=1).attn_output_fused
+    toks, gl, rl = _teacher_forced(TINY_FUSED, [1] * 40, 32, 4, dev, norm_topk_prob=norm)
     _check_steps(toks, gl, rl)
 
 
