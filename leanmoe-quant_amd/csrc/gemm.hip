@@ -39,9 +39,9 @@ struct GemmArgs {
   float* part;             // (splits, M, N) fp32 partials when splits > 1
 };
 
-template <bool W8, int BM, int BN>
-__global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
-  using TL = Tile<BM, BN>;
+template <bool W8, int BM, int BN, int WM = 2>
+__global__ __launch_bounds__(128 * WM) void gemm_kernel(const GemmArgs a) {
+  using TL = Tile<BM, BN, WM, 2>;
   __shared__ __align__(16) uint16_t lds[TL::LDS_ELEMS];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int half = lane >> 5, l32 = lane & 31;
@@ -76,12 +76,12 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
       src.bw[i] = a.w16 + n * a.K + kb + TL::b16_col(t, i);
     }
   }
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave >> 1, wn = wave & 1;  // WM x 2 waves
   int b_row0[TL::FN];
 #pragma unroll
   for (int j = 0; j < TL::FN; ++j) b_row0[j] = wn * (BN / 2) + 32 * j;
   Acc<TL::FM, TL::FN> acc;
-  block_mainloop<TL, W8>(acc, src, klen, a.group, lds, wm * (BM / 2), b_row0);
+  block_mainloop<TL, W8>(acc, src, klen, a.group, lds, wm * (BM / WM), b_row0);
 
 #pragma unroll
   for (int i = 0; i < TL::FM; ++i)
@@ -90,7 +90,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
       const int64_t n = n0 + wn * (BN / 2) + 32 * j + l32;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int64_t m = m0 + wm * (BM / 2) + 32 * i + acc_row(r, half);
+        const int64_t m = m0 + wm * (BM / WM) + 32 * i + acc_row(r, half);
         if (m >= a.M || n >= a.N) continue;
         if (a.part) {
           a.part[((int64_t)z * a.M + m) * a.N + n] = acc.v[i][j][r];
@@ -129,12 +129,19 @@ int launch_tiles(const GemmArgs& a, hipStream_t st) {
                        a.M, a.N, a.y16, a.y_ld, a.resid, a.resid_ld);
     LEMOQ_CHECK_LAUNCH();
   }
-  const int64_t big = ((a.M + 127) / 128) * ((a.N + 127) / 128);
-  if (big >= 256) {
-    hipLaunchKernelGGL((gemm_kernel<W8, 128, 128>), dim3((unsigned)big), dim3(256), 0, st, a);
+  // Measured on the OLMoE linears (qkv, o_proj at 1024 and 4096 rows): 256 x 128 tiles of 8
+  // waves (each wave 64 x 64, the B tile shared by 4 row waves) are fastest while they give
+  // at least 192 blocks; then 128 x 128 (8 waves of 32 x 64) from 256 blocks; below that the
+  // grid is too small and 64 x 64 tiles of 4 waves fill the chip best.
+  const int64_t t256 = ((a.M + 255) / 256) * ((a.N + 127) / 128);
+  const int64_t t128 = ((a.M + 127) / 128) * ((a.N + 127) / 128);
+  if (t256 >= 192) {
+    hipLaunchKernelGGL((gemm_kernel<W8, 256, 128, 4>), dim3((unsigned)t256), dim3(512), 0, st, a);
+  } else if (t128 >= 256) {
+    hipLaunchKernelGGL((gemm_kernel<W8, 128, 128, 4>), dim3((unsigned)t128), dim3(512), 0, st, a);
   } else {
-    const int64_t small = ((a.M + 63) / 64) * ((a.N + 127) / 128);
-    hipLaunchKernelGGL((gemm_kernel<W8, 64, 128>), dim3((unsigned)small), dim3(256), 0, st, a);
+    const int64_t small = ((a.M + 63) / 64) * ((a.N + 63) / 64);
+    hipLaunchKernelGGL((gemm_kernel<W8, 64, 64>), dim3((unsigned)small), dim3(256), 0, st, a);
   }
   LEMOQ_CHECK_LAUNCH();
 }
@@ -146,7 +153,7 @@ int launch_gemm(const GemmArgs& a, hipStream_t st) {
 int check_gemm(const GemmArgs& a) {
   if (!a.x || (!a.codes && !a.w16) || (a.codes && !a.scale) || !a.y16) return LEMOQ_ERR_NULL;
   if (a.M <= 0 || a.N <= 0 || a.K <= 0 || a.M > (1LL << 24) || a.N > (1LL << 24)) return LEMOQ_ERR_SHAPE;
-  if (((a.M + 63) / 64) * ((a.N + 127) / 128) > 0x7fffffffLL) return LEMOQ_ERR_SHAPE;
+  if (((a.M + 63) / 64) * ((a.N + 63) / 64) > 0x7fffffffLL) return LEMOQ_ERR_SHAPE;
   if (a.K % 64 != 0 || a.x_ld < a.K || a.x_ld % 8 != 0 || a.y_ld < a.N) return LEMOQ_ERR_SHAPE;
   if (a.codes && (a.group <= 0 || a.group % 64 != 0 || a.K % a.group != 0)) return LEMOQ_ERR_UNSUPPORTED;
   if (a.resid && a.resid_ld < a.N) return LEMOQ_ERR_SHAPE;

@@ -1,6 +1,6 @@
 // Matrix-core main loop shared by the multi-token (prefill) GEMMs.
 //
-// A block of 4 waves (2 x 2) computes a BM x BN tile of Y = X W^T with
+// A block of WM x WN waves computes a BM x BN tile of Y = X W^T with
 // v_mfma_f32_32x32x16_f16; X rows fp16, W rows either w8 (int8 codes + fp16
 // per-group scales, dequantised to fp16(code * scale) once per block as the
 // tile is written to LDS) or fp16.  K advances in stages of 64: the global
@@ -52,25 +52,31 @@ __device__ __forceinline__ void dequant16(const u32x4 c, uint32_t s2, u32x4& lo,
   hi = (u32x4){o[4], o[5], o[6], o[7]};
 }
 
-// Tile geometry of a BM x BN block (BM, BN in {64, 128}).
-template <int BM_, int BN_>
+// Tile geometry of a BM x BN block computed by WM x WN waves (each wave a
+// (BM / WM) x (BN / WN) sub-tile of 32 x 32 fragments).  Every thread of the
+// block stages A_CH 16-byte A chunks and B8_CH (w8) or B16_CH (fp16) B
+// chunks per stage.
+template <int BM_, int BN_, int WM_ = 2, int WN_ = 2>
 struct Tile {
-  static constexpr int BM = BM_, BN = BN_;
-  static constexpr int FM = BM / 64, FN = BN / 64;   // 32 x 32 fragments per wave
-  static constexpr int A_CH = BM * (BK / 8) / 256;   // 16-byte A chunks per thread per stage
-  static constexpr int B16_CH = BN * (BK / 8) / 256; // fp16 B chunks per thread
-  static constexpr int B8_CH = BN * (BK / 16) / 256; // w8 B chunks (16 codes) per thread
+  static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_;
+  static constexpr int NT = 64 * WM * WN;                 // threads per block
+  static constexpr int FM = BM / WM / 32, FN = BN / WN / 32;
+  static constexpr int A_CH = BM * (BK / 8) / NT;   // 16-byte A chunks per thread per stage
+  static constexpr int B16_CH = BN * (BK / 8) / NT; // fp16 B chunks per thread
+  static constexpr int B8_CH = BN * (BK / 16) / NT; // w8 B chunks (16 codes) per thread
   static constexpr int LDS_HALF = (BM + BN) * LDS_PITCH;  // fp16 per buffer
   static constexpr int LDS_ELEMS = 2 * LDS_HALF;
-  static_assert(BM % 64 == 0 && BN % 64 == 0 && B8_CH >= 1, "tile sizes");
-  // Thread t's A chunk i: tile row (t + 256 i) / 8, column 8 * ((t + 256 i) % 8).
-  __device__ static int a_row(int t, int i) { return (t + 256 * i) >> 3; }
-  __device__ static int a_col(int t, int i) { return 8 * ((t + 256 * i) & 7); }
-  __device__ static int b16_row(int t, int i) { return (t + 256 * i) >> 3; }
-  __device__ static int b16_col(int t, int i) { return 8 * ((t + 256 * i) & 7); }
-  // w8 chunk: 16 codes; tile row (t + 256 i) / 4, column 16 * ((t + 256 i) % 4).
-  __device__ static int b8_row(int t, int i) { return (t + 256 * i) >> 2; }
-  __device__ static int b8_col(int t, int i) { return 16 * ((t + 256 * i) & 3); }
+  static_assert(FM >= 1 && FN >= 1 && A_CH >= 1 && B8_CH >= 1 && BM * (BK / 8) % NT == 0 &&
+                    BN * (BK / 16) % NT == 0,
+                "tile sizes");
+  // Thread t's A chunk i: tile row (t + NT i) / 8, column 8 * ((t + NT i) % 8).
+  __device__ static int a_row(int t, int i) { return (t + NT * i) >> 3; }
+  __device__ static int a_col(int t, int i) { return 8 * ((t + NT * i) & 7); }
+  __device__ static int b16_row(int t, int i) { return (t + NT * i) >> 3; }
+  __device__ static int b16_col(int t, int i) { return 8 * ((t + NT * i) & 7); }
+  // w8 chunk: 16 codes; tile row (t + NT i) / 4, column 16 * ((t + NT i) % 4).
+  __device__ static int b8_row(int t, int i) { return (t + NT * i) >> 2; }
+  __device__ static int b8_col(int t, int i) { return 16 * ((t + NT * i) & 3); }
 };
 
 template <int FM, int FN>

@@ -161,9 +161,14 @@ struct GroupedArgs {
 // Grouped GEMM blocks: a 1-D grid over (column block nb, tile mt) numbered
 // nb-major, so consecutive blocks take consecutive tiles of the same column
 // block (usually the same expert, i.e. the same weight tile), and each XCD
-// takes a contiguous range of them.  Block tile 128 pairs x 128 weight rows
-// (the stage pipeline of gemm_core.h).
-using GTile = Tile<128, 128>;
+// takes a contiguous range of them.  Block tile 128 pairs x BN weight rows,
+// 2 x WN waves of 64 x 64 (the stage pipeline of gemm_core.h).
+#ifndef LEMOQ_MOE_WN
+#define LEMOQ_MOE_WN 4  // column waves per grouped block (2: 128 weight rows, 4: 256)
+#endif
+constexpr int MOE_WN = LEMOQ_MOE_WN;
+template <int WN>
+using GTile = Tile<128, 64 * WN, 2, WN>;
 
 __device__ __forceinline__ bool grouped_tile(const GroupedArgs& a, int64_t ncol_blocks, int64_t max_tiles,
                                              int64_t& nb, int& e, int64_t& rs, int64_t& re) {
@@ -176,39 +181,43 @@ __device__ __forceinline__ bool grouped_tile(const GroupedArgs& a, int64_t ncol_
   return e >= 0;
 }
 
-// 2. gate_up: the block's 128 weight rows are 64 gate rows (act columns
-// n0 .. n0+63) and the 64 matching up rows, so wave (wm, wn) pairs gate rows
-// 32 wn .. 32 wn + 31 (fragment 0) with the same up rows (fragment 1).
-__global__ __launch_bounds__(256) void moe_gate_up_kernel(const GroupedArgs a, int64_t max_tiles) {
-  __shared__ __align__(16) uint16_t lds[GTile::LDS_ELEMS];
+// 2. gate_up: the block's 64 WN weight rows are AC = 32 WN gate rows (act
+// columns n0 .. n0 + AC - 1) and the AC matching up rows, so wave (wm, wn)
+// pairs gate rows 32 wn .. 32 wn + 31 (fragment 0) with the same up rows
+// (fragment 1).
+template <int WN>
+__global__ __launch_bounds__(128 * WN) void moe_gate_up_kernel(const GroupedArgs a, int64_t max_tiles) {
+  using TL = GTile<WN>;
+  constexpr int AC = 32 * WN;  // act columns per block
+  __shared__ __align__(16) uint16_t lds[TL::LDS_ELEMS];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int half = lane >> 5, l32 = lane & 31;
   const int64_t F = a.N;
   int64_t nb, rs, re;
   int e;
-  if (!grouped_tile(a, (F + 63) / 64, max_tiles, nb, e, rs, re)) return;  // block-uniform
-  const int64_t n0 = nb * 64;
-  Sources<GTile, true> src;
+  if (!grouped_tile(a, (F + AC - 1) / AC, max_tiles, nb, e, rs, re)) return;  // block-uniform
+  const int64_t n0 = nb * AC;
+  Sources<TL, true> src;
 #pragma unroll
-  for (int i = 0; i < GTile::A_CH; ++i) {
-    int64_t m = rs + GTile::a_row(t, i);
+  for (int i = 0; i < TL::A_CH; ++i) {
+    int64_t m = rs + TL::a_row(t, i);
     m = m < re ? m : re - 1;
-    src.a[i] = a.x + (int64_t)a.pair_tok[m] * a.K + GTile::a_col(t, i);
+    src.a[i] = a.x + (int64_t)a.pair_tok[m] * a.K + TL::a_col(t, i);
   }
   const int64_t ng = a.K / a.group;
 #pragma unroll
-  for (int i = 0; i < GTile::B8_CH; ++i) {
-    const int r = GTile::b8_row(t, i);
-    int64_t n = n0 + (r & 63);
+  for (int i = 0; i < TL::B8_CH; ++i) {
+    const int r = TL::b8_row(t, i);
+    int64_t n = n0 + (r & (AC - 1));
     n = n < F ? n : F - 1;
-    const int64_t row = (int64_t)e * 2 * F + (r < 64 ? n : F + n);
-    src.bc[i] = a.codes + row * a.K + GTile::b8_col(t, i);
+    const int64_t row = (int64_t)e * 2 * F + (r < AC ? n : F + n);
+    src.bc[i] = a.codes + row * a.K + TL::b8_col(t, i);
     src.bs[i] = a.scale + row * ng;
   }
-  const int wm = wave >> 1, wn = wave & 1;
-  const int b_row0[2] = {32 * wn, 64 + 32 * wn};
+  const int wm = wave / WN, wn = wave % WN;
+  const int b_row0[2] = {32 * wn, AC + 32 * wn};
   Acc<2, 2> acc;
-  block_mainloop<GTile, true>(acc, src, a.K, a.group, lds, 64 * wm, b_row0);
+  block_mainloop<TL, true>(acc, src, a.K, a.group, lds, 64 * wm, b_row0);
   const int64_t n = n0 + 32 * wn + l32;
 #pragma unroll
   for (int i = 0; i < 2; ++i)
@@ -223,36 +232,39 @@ __global__ __launch_bounds__(256) void moe_gate_up_kernel(const GroupedArgs a, i
     }
 }
 
-// 3. down: 128 pairs x 128 hidden columns per block.
-__global__ __launch_bounds__(256) void moe_down_kernel(const GroupedArgs a, int64_t max_tiles) {
-  __shared__ __align__(16) uint16_t lds[GTile::LDS_ELEMS];
+// 3. down: 128 pairs x 64 WN hidden columns per block.
+template <int WN>
+__global__ __launch_bounds__(128 * WN) void moe_down_kernel(const GroupedArgs a, int64_t max_tiles) {
+  using TL = GTile<WN>;
+  constexpr int NC = 64 * WN;  // output columns per block
+  __shared__ __align__(16) uint16_t lds[TL::LDS_ELEMS];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int half = lane >> 5, l32 = lane & 31;
   const int64_t H = a.N;
   int64_t nb, rs, re;
   int e;
-  if (!grouped_tile(a, (H + 127) / 128, max_tiles, nb, e, rs, re)) return;  // block-uniform
-  const int64_t n0 = nb * 128;
-  Sources<GTile, true> src;
+  if (!grouped_tile(a, (H + NC - 1) / NC, max_tiles, nb, e, rs, re)) return;  // block-uniform
+  const int64_t n0 = nb * NC;
+  Sources<TL, true> src;
 #pragma unroll
-  for (int i = 0; i < GTile::A_CH; ++i) {
-    int64_t m = rs + GTile::a_row(t, i);
+  for (int i = 0; i < TL::A_CH; ++i) {
+    int64_t m = rs + TL::a_row(t, i);
     m = m < re ? m : re - 1;
-    src.a[i] = a.x + m * a.K + GTile::a_col(t, i);
+    src.a[i] = a.x + m * a.K + TL::a_col(t, i);
   }
   const int64_t ng = a.K / a.group;
 #pragma unroll
-  for (int i = 0; i < GTile::B8_CH; ++i) {
-    int64_t n = n0 + GTile::b8_row(t, i);
+  for (int i = 0; i < TL::B8_CH; ++i) {
+    int64_t n = n0 + TL::b8_row(t, i);
     n = n < H ? n : H - 1;
     const int64_t row = (int64_t)e * H + n;
-    src.bc[i] = a.codes + row * a.K + GTile::b8_col(t, i);
+    src.bc[i] = a.codes + row * a.K + TL::b8_col(t, i);
     src.bs[i] = a.scale + row * ng;
   }
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WN, wn = wave % WN;
   const int b_row0[2] = {64 * wn, 64 * wn + 32};
   Acc<2, 2> acc;
-  block_mainloop<GTile, true>(acc, src, a.K, a.group, lds, 64 * wm, b_row0);
+  block_mainloop<TL, true>(acc, src, a.K, a.group, lds, 64 * wm, b_row0);
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -367,10 +379,10 @@ extern "C" int lemoq_moe_prefill_gate_up(const uint16_t* x, int64_t H, const int
   GroupedArgs a{};
   a.x = x; a.pair_tok = pair_tok; a.tiles = tiles; a.codes = gu_codes; a.scale = gu_scale;
   a.K = H; a.N = F; a.group = (int)group; a.y = act;
-  const int64_t blocks = ((F + 63) / 64) * max_tiles;
+  const int64_t blocks = ((F + 32 * MOE_WN - 1) / (32 * MOE_WN)) * max_tiles;
   if (blocks > 0x7fffffffLL) return LEMOQ_ERR_SHAPE;
-  hipLaunchKernelGGL(moe_gate_up_kernel, dim3((unsigned)blocks), dim3(256), 0, lemoq_stream(stream), a,
-                     max_tiles);
+  hipLaunchKernelGGL(moe_gate_up_kernel<MOE_WN>, dim3((unsigned)blocks), dim3(128 * MOE_WN), 0,
+                     lemoq_stream(stream), a, max_tiles);
   LEMOQ_CHECK_LAUNCH();
 }
 
@@ -384,10 +396,10 @@ extern "C" int lemoq_moe_prefill_down(const uint16_t* act, int64_t F, const int3
   GroupedArgs a{};
   a.x = act; a.pair_src = pair_src; a.pair_w = pair_w; a.tiles = tiles; a.codes = dn_codes;
   a.scale = dn_scale; a.K = F; a.N = H; a.group = (int)group; a.y = y;
-  const int64_t blocks = ((H + 127) / 128) * max_tiles;
+  const int64_t blocks = ((H + 64 * MOE_WN - 1) / (64 * MOE_WN)) * max_tiles;
   if (blocks > 0x7fffffffLL) return LEMOQ_ERR_SHAPE;
-  hipLaunchKernelGGL(moe_down_kernel, dim3((unsigned)blocks), dim3(256), 0, lemoq_stream(stream), a,
-                     max_tiles);
+  hipLaunchKernelGGL(moe_down_kernel<MOE_WN>, dim3((unsigned)blocks), dim3(128 * MOE_WN), 0,
+                     lemoq_stream(stream), a, max_tiles);
   LEMOQ_CHECK_LAUNCH();
 }
 
