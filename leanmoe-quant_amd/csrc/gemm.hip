@@ -129,15 +129,15 @@ int launch_tiles(const GemmArgs& a, hipStream_t st) {
                        a.M, a.N, a.y16, a.y_ld, a.resid, a.resid_ld);
     LEMOQ_CHECK_LAUNCH();
   }
-  // Measured on the OLMoE linears (qkv, o_proj at 1024 and 4096 rows): 256 x 128 tiles of 8
+  // Measured on the OLMoE linears (qkv, o_proj at 1 to 4096 rows): 256 x 128 tiles of 8
   // waves (each wave 64 x 64, the B tile shared by 4 row waves) are fastest while they give
-  // at least 192 blocks; then 128 x 128 (8 waves of 32 x 64) from 256 blocks; below that the
-  // grid is too small and 64 x 64 tiles of 4 waves fill the chip best.
+  // at least 192 blocks; then 128 x 128 (8 waves of 32 x 64) from 256 blocks; below that, and
+  // for fewer rows than a tile (padding rows cost matrix work), 64 x 64 tiles of 4 waves.
   const int64_t t256 = ((a.M + 255) / 256) * ((a.N + 127) / 128);
   const int64_t t128 = ((a.M + 127) / 128) * ((a.N + 127) / 128);
-  if (t256 >= 192) {
+  if (a.M >= 256 && t256 >= 192) {
     hipLaunchKernelGGL((gemm_kernel<W8, 256, 128, 4>), dim3((unsigned)t256), dim3(512), 0, st, a);
-  } else if (t128 >= 256) {
+  } else if (a.M >= 128 && t128 >= 256) {
     hipLaunchKernelGGL((gemm_kernel<W8, 128, 128, 4>), dim3((unsigned)t128), dim3(512), 0, st, a);
   } else {
     const int64_t small = ((a.M + 63) / 64) * ((a.N + 63) / 64);
