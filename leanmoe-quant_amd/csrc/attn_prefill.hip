@@ -48,6 +48,10 @@ struct AttnGeom {
   static constexpr int K_CH = KT * D / 8 / THREADS;        // 16-byte K chunks per thread
   static constexpr int V_CH = (KT / 4) * (D / 8) / THREADS;  // 4 x 8 V sub-blocks per thread
   static constexpr int HALF = KT * KP + D * VP;    // fp16 per LDS buffer
+  // V^T row r keeps its 16-byte key chunk c at chunk c ^ vswz(r): the stores
+  // (8 bytes to rows 8 dq + 2 w) then spread over all banks instead of two.
+  static constexpr int VCH = KT / 8;               // 16-byte key chunks per V^T row
+  __device__ static int vswz(int r) { return (r >> 4) & (VCH - 1); }
   static_assert(K_CH >= 1 && V_CH >= 1, "tile split");
 };
 
@@ -104,8 +108,9 @@ __device__ __forceinline__ void attn_store(const AttnStage<G>& st, uint16_t* buf
                                   __builtin_amdgcn_perm(v3[w], v2[w], 0x05040100u));
       const uint2 hi = make_uint2(__builtin_amdgcn_perm(v1[w], v0[w], 0x07060302u),
                                   __builtin_amdgcn_perm(v3[w], v2[w], 0x07060302u));
-      *reinterpret_cast<uint2*>(vt + (8 * dq + 2 * w) * G::VP + 4 * kq) = lo;
-      *reinterpret_cast<uint2*>(vt + (8 * dq + 2 * w + 1) * G::VP + 4 * kq) = hi;
+      const int r0 = 8 * dq + 2 * w, r1 = r0 + 1;
+      *reinterpret_cast<uint2*>(vt + r0 * G::VP + 8 * ((kq >> 1) ^ G::vswz(r0)) + 4 * (kq & 1)) = lo;
+      *reinterpret_cast<uint2*>(vt + r1 * G::VP + 8 * ((kq >> 1) ^ G::vswz(r1)) + 4 * (kq & 1)) = hi;
     }
   }
 }
@@ -230,9 +235,10 @@ __device__ __forceinline__ void attn_prefill_body(
         const int kb = 32 * (G::NSW * kpart + qq / 2) + 16 * (qq % 2);
 #pragma unroll
         for (int f = 0; f < G::DF; ++f) {
-          const uint16_t* vp = vt + (32 * f + l32) * G::VP + 4 * half + kb;
-          const uint2 a0 = *reinterpret_cast<const uint2*>(vp);
-          const uint2 a1 = *reinterpret_cast<const uint2*>(vp + 8);
+          const int vr = 32 * f + l32, sw = G::vswz(vr);  // keys kb + 4 half and kb + 8 + 4 half
+          const uint16_t* vp = vt + vr * G::VP + 4 * half;
+          const uint2 a0 = *reinterpret_cast<const uint2*>(vp + 8 * ((kb >> 3) ^ sw));
+          const uint2 a1 = *reinterpret_cast<const uint2*>(vp + 8 * (((kb >> 3) + 1) ^ sw));
           o[f] = __builtin_amdgcn_mfma_f32_32x32x16_f16(h8_of((u32x4){a0.x, a0.y, a1.x, a1.y}), pb[qq], o[f], 0,
                                                         0, 0);
         }
