@@ -33,6 +33,13 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 __device__ __forceinline__ h8v h8_of(const u32x4 v) { return __builtin_bit_cast(h8v, v); }
 
+// 2^x by v_exp_f32 alone, for the softmax numerators and the running-max
+// rescale.  Results below 2^-126 flush to 0 where exp2f returns denormals; p
+// is rounded to fp16 (smallest subnormal 2^-24) before P.V and every running
+// sum it enters is >= 1, so no output changes.  exp2f's denormal path costs
+// four more instructions per score.
+__device__ __forceinline__ float exp2_flush(float x) { return __builtin_amdgcn_exp2f(x); }
+
 template <int D, int NW, int KS = 1>
 struct AttnGeom {
   static constexpr int THREADS = 64 * NW;
@@ -206,7 +213,7 @@ __device__ __forceinline__ void attn_prefill_body(
       // key kw <= qw <= qi is valid for every query of a wave with stored outputs
       // (qw < T), so mn is finite there; waves wholly past the prompt store nothing
       const float mn = fmaxf(m, mx);
-      const float alpha = exp2f(m - mn);
+      const float alpha = exp2_flush(m - mn);
       float ps = 0.0f;
       h8v pb[2 * G::NSW];
 #pragma unroll
@@ -214,9 +221,10 @@ __device__ __forceinline__ void attn_prefill_body(
         uint32_t pk[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          const float p0 = exp2f(s[sf][2 * i] - mn), p1 = exp2f(s[sf][2 * i + 1] - mn);
+          const float p0 = exp2_flush(s[sf][2 * i] - mn), p1 = exp2_flush(s[sf][2 * i + 1] - mn);
           ps += p0 + p1;
-          pk[i] = (uint32_t)f2h(p0) | ((uint32_t)f2h(p1) << 16);
+          const f16x2 hp = {(f16)p0, (f16)p1};  // one v_cvt_pk_f16_f32 (round to nearest even)
+          pk[i] = __builtin_bit_cast(uint32_t, hp);
         }
         pb[2 * sf] = h8_of((u32x4){pk[0], pk[1], pk[2], pk[3]});
         pb[2 * sf + 1] = h8_of((u32x4){pk[4], pk[5], pk[6], pk[7]});
