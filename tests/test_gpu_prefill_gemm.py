@@ -55,6 +55,8 @@ SHAPES = [
     (37, 100, 128),      # ragged M and N, one group
     (257, 2048, 1024),   # expert down width
     (1, 50304, 2048),    # lm_head on the last prompt row
+    (2000, 2048, 256),   # 128 x 128 tiles of 8 waves (>= 256 of them, < 192 of 256 x 128), ragged M
+    (1100, 6100, 512),   # 256 x 128 tiles of 8 waves, ragged M and N
 ]
 
 
