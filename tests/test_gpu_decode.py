@@ -24,6 +24,10 @@ TINY = OlmoeShape(hidden=512, heads=4, head_dim=128, layers=2, num_experts=8, to
 # 4-head groups, residual in the router launch); TINY takes the three-launch path.
 TINY_FUSED = OlmoeShape(hidden=2048, heads=16, head_dim=128, layers=2, num_experts=8, top_k=2, ffn=256,
                         vocab=1024)
+# 8 heads (attention width 1024 != hidden 2048: two partial rows) and, at a
+# 1200-slot cache, more than 16 splits per head (the 64-split merge instance)
+NARROW_FUSED = OlmoeShape(hidden=2048, heads=8, head_dim=128, layers=2, num_experts=8, top_k=2, ffn=256,
+                          vocab=1024)
 
 
 def _kl(p_logits, q_logits) -> float:
@@ -86,13 +90,17 @@ def test_tiny_model_32_steps_match_oracle(norm, dev):
     _check_steps(toks, gl, rl)
 
 
-@pytest.mark.parametrize("norm", [False, True])
-def test_fused_path_model_32_steps_match_oracle(norm, dev):
-    print("case: hidden-2048 test model (fused attention output), 32 steps, norm_topk_prob=%s" % norm,
-          flush=True)
-    w = OlmoeW8Weights.random(TINY_FUSED, seed=4, device=dev)
-    assert DecodeSession(w, [1] * 4, max_new_tokens=1).attn_output_fused
-    toks, gl, rl = _teacher_forced(TINY_FUSED, [1] * 40, 32, 4, dev, norm_topk_prob=norm)
+@pytest.mark.parametrize("shape,ctx,norm", [("tiny", 40, False), ("tiny", 40, True), ("narrow", 1200, False)])
+def test_fused_path_model_32_steps_match_oracle(shape, ctx, norm, dev):
+    print("case: %s fused-path test model, ctx %d, 32 steps, norm_topk_prob=%s" % (shape, ctx, norm), flush=True)
+    sh = TINY_FUSED if shape == "tiny" else NARROW_FUSED
+    w = OlmoeW8Weights.random(sh, seed=4, device=dev)
+    probe = DecodeSession(w, [1] * ctx, max_new_tokens=32)
+    assert probe.attn_output_fused
+    if shape == "narrow":
+        assert probe.num_splits > 16, probe.num_splits
+    del probe
+    toks, gl, rl = _teacher_forced(sh, [1] * ctx, 32, 4, dev, norm_topk_prob=norm)
     _check_steps(toks, gl, rl)
 
 
