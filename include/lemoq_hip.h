@@ -277,6 +277,16 @@ int lemoq_route_topk(const void* logits, int logits_is_f16, int64_t T, int64_t E
                      int64_t row_stride, int64_t top_k, int norm_topk_prob,
                      float* top_w, int64_t* top_i, void* stream);
 
+/* lemoq_route_topk on the logits lemoq_gemm_f16_splitk would produce from
+ * `partials` ((splits, T, E) fp32, its workspace): each logit is the fp16
+ * rounding of the partials summed in range order from 0, as that entry's
+ * second launch computes it, so the routing is identical while the sum and
+ * the routing share one launch (prefill's router, the same F.linear and
+ * routing_softmax_topk as lemoq_route_topk).  1 <= splits <= 64. */
+int lemoq_route_topk_splitk(const float* partials, int64_t splits, int64_t T, int64_t E,
+                            int64_t top_k, int norm_topk_prob, float* top_w, int64_t* top_i,
+                            void* stream);
+
 /* Router logits of one token: xn = rmsnorm(h, norm_w) (xn_out, nullable),
  * logits_out (E) = fp16(xn @ router_w^T), fp32 accumulation (the F.linear of
  * moe_static._route, src/lemoq/kernels/moe_static.py:267).  One wave per
@@ -473,7 +483,9 @@ int lemoq_gemm_f16(const uint16_t* x, int64_t M, int64_t K, int64_t x_ld, const 
  * `splits` ranges (K % (64 * splits) == 0, splits <= 64), each range's fp32
  * partial goes to workspace ((splits, M, N) fp32, 16-byte aligned, caller-
  * owned), and a second launch sums the partials in range order and rounds
- * once to fp16.  splits == 1 is lemoq_gemm_f16 (workspace unused). */
+ * once to fp16.  splits == 1 is lemoq_gemm_f16 (workspace unused).  With
+ * splits > 1, y == NULL leaves the partials in workspace and skips the sum
+ * (lemoq_route_topk_splitk finishes them). */
 int lemoq_gemm_f16_splitk(const uint16_t* x, int64_t M, int64_t K, int64_t x_ld, const uint16_t* w,
                           int64_t N, uint16_t* y, int64_t y_ld, int64_t splits, float* workspace,
                           void* stream);

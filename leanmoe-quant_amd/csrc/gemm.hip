@@ -124,6 +124,7 @@ int launch_tiles(const GemmArgs& a, hipStream_t st) {
     hipLaunchKernelGGL((gemm_kernel<W8, 64, 64>), dim3((unsigned)tiles, (unsigned)a.splits), dim3(256), 0, st, a);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
+    if (!a.y16) return LEMOQ_OK;  // partials only: the consumer sums them
     const int64_t n = a.M * a.N;
     hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a.part, a.splits,
                        a.M, a.N, a.y16, a.y_ld, a.resid, a.resid_ld);
@@ -151,10 +152,11 @@ int launch_gemm(const GemmArgs& a, hipStream_t st) {
 }
 
 int check_gemm(const GemmArgs& a) {
-  if (!a.x || (!a.codes && !a.w16) || (a.codes && !a.scale) || !a.y16) return LEMOQ_ERR_NULL;
+  if (!a.x || (!a.codes && !a.w16) || (a.codes && !a.scale) || (!a.y16 && (a.splits == 1 || a.resid)))
+    return LEMOQ_ERR_NULL;
   if (a.M <= 0 || a.N <= 0 || a.K <= 0 || a.M > (1LL << 24) || a.N > (1LL << 24)) return LEMOQ_ERR_SHAPE;
   if (((a.M + 63) / 64) * ((a.N + 63) / 64) > 0x7fffffffLL) return LEMOQ_ERR_SHAPE;
-  if (a.K % 64 != 0 || a.x_ld < a.K || a.x_ld % 8 != 0 || a.y_ld < a.N) return LEMOQ_ERR_SHAPE;
+  if (a.K % 64 != 0 || a.x_ld < a.K || a.x_ld % 8 != 0 || (a.y16 && a.y_ld < a.N)) return LEMOQ_ERR_SHAPE;
   if (a.codes && (a.group <= 0 || a.group % 64 != 0 || a.K % a.group != 0)) return LEMOQ_ERR_UNSUPPORTED;
   if (a.resid && a.resid_ld < a.N) return LEMOQ_ERR_SHAPE;
   if (a.splits < 1 || a.splits > 64 || a.K % (64LL * a.splits) != 0) return LEMOQ_ERR_SHAPE;
@@ -205,7 +207,7 @@ extern "C" int lemoq_gemm_f16_splitk(const uint16_t* x, int64_t M, int64_t K, in
   a.codes = nullptr; a.scale = nullptr; a.w16 = w; a.group = 0;
   a.y16 = y; a.y_ld = y_ld;
   a.resid = nullptr; a.resid_ld = 0;
-  if (!y || !w) return LEMOQ_ERR_NULL;
+  if ((!y && splits == 1) || !w) return LEMOQ_ERR_NULL;
   if (splits < 1 || splits > 64) return LEMOQ_ERR_SHAPE;
   a.splits = (int)splits;
   a.part = workspace;

@@ -564,9 +564,14 @@ int launch_router_logits(hipStream_t st, const uint16_t* h, const uint16_t* norm
 }
 
 // Routing of T tokens, one wave per token (values per lane PL = ceil(E/64)).
+// Logit kinds: fp32, fp16, or `splits` fp32 split-K partial planes of T x
+// stride (the logit is fp16(sum of the planes in order, from 0), the finish
+// of lemoq_gemm_f16_splitk, so routing the partials equals routing its output).
+constexpr int kLogitsF32 = 0, kLogitsF16 = 1, kLogitsSplitK = 2;
+
 template <int PL>
-__global__ __launch_bounds__(256) void route_topk_kernel(const void* __restrict__ logits, int f16,
-                                                         int64_t T, int E, int64_t stride,
+__global__ __launch_bounds__(256) void route_topk_kernel(const void* __restrict__ logits, int kind,
+                                                         int64_t T, int E, int64_t stride, int splits,
                                                          int top_k, int norm,
                                                          float* __restrict__ top_w32,
                                                          uint16_t* __restrict__ top_w16,
@@ -579,8 +584,15 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const void* __restrict_
   for (int i = 0; i < PL; ++i) {
     const int idx = lane + 64 * i;
     if (idx < E) {
-      z[i] = f16 ? h2f(reinterpret_cast<const uint16_t*>(logits)[t * stride + idx])
-                 : reinterpret_cast<const float*>(logits)[t * stride + idx];
+      if (kind == kLogitsSplitK) {
+        const float* pp = reinterpret_cast<const float*>(logits) + t * stride + idx;
+        float v = 0.0f;
+        for (int zz = 0; zz < splits; ++zz) v += pp[(int64_t)zz * T * stride];
+        z[i] = h2f(f2h(v));
+      } else {
+        z[i] = kind == kLogitsF16 ? h2f(reinterpret_cast<const uint16_t*>(logits)[t * stride + idx])
+                                  : reinterpret_cast<const float*>(logits)[t * stride + idx];
+      }
     } else {
       z[i] = -INFINITY;
     }
@@ -595,16 +607,16 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const void* __restrict_
   }
 }
 
-int launch_route(hipStream_t st, const void* logits, int f16, int64_t T, int64_t E,
+int launch_route(hipStream_t st, const void* logits, int kind, int64_t T, int64_t E,
                  int64_t stride, int64_t top_k, int norm, float* w32, uint16_t* w16,
-                 int64_t* ids) {
+                 int64_t* ids, int splits = 1) {
   const int64_t blocks = (T + 3) / 4;
   if (blocks > 0x7fffffffLL) return LEMOQ_ERR_SHAPE;
   const int pl = (int)((E + 63) / 64);
 #define LEMOQ_ROUTE_CASE(PP)                                                                    \
   if (pl <= PP) {                                                                               \
     hipLaunchKernelGGL((route_topk_kernel<PP>), dim3((unsigned)blocks), dim3(256), 0, st,      \
-                       logits, f16, T, (int)E, stride, (int)top_k, norm, w32, w16, ids);        \
+                       logits, kind, T, (int)E, stride, splits, (int)top_k, norm, w32, w16, ids); \
     LEMOQ_CHECK_LAUNCH();                                                                       \
   }
   LEMOQ_ROUTE_CASE(1)
@@ -703,8 +715,19 @@ extern "C" int lemoq_route_topk(const void* logits, int logits_is_f16, int64_t T
   if (T < 0 || E <= 0 || E > 1024 || top_k <= 0 || top_k > E || top_k > 64 || row_stride < E)
     return LEMOQ_ERR_SHAPE;
   if (T == 0) return LEMOQ_OK;
-  return launch_route(lemoq_stream(stream), logits, logits_is_f16 ? 1 : 0, T, E, row_stride, top_k,
-                      norm_topk_prob ? 1 : 0, top_w, nullptr, top_i);
+  return launch_route(lemoq_stream(stream), logits, logits_is_f16 ? kLogitsF16 : kLogitsF32, T, E, row_stride,
+                      top_k, norm_topk_prob ? 1 : 0, top_w, nullptr, top_i);
+}
+
+extern "C" int lemoq_route_topk_splitk(const float* partials, int64_t splits, int64_t T, int64_t E,
+                                       int64_t top_k, int norm_topk_prob, float* top_w, int64_t* top_i,
+                                       void* stream) {
+  if (!partials || !top_w || !top_i) return LEMOQ_ERR_NULL;
+  if (T < 0 || E <= 0 || E > 1024 || top_k <= 0 || top_k > E || top_k > 64 || splits < 1 || splits > 64)
+    return LEMOQ_ERR_SHAPE;
+  if (T == 0) return LEMOQ_OK;
+  return launch_route(lemoq_stream(stream), partials, kLogitsSplitK, T, E, E, top_k, norm_topk_prob ? 1 : 0,
+                      top_w, nullptr, top_i, (int)splits);
 }
 
 extern "C" int lemoq_router_logits(const uint16_t* h, const uint16_t* norm_w, float eps,

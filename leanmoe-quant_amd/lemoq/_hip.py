@@ -142,6 +142,7 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "lemoq_kv_write_i8": (_I, [_P, _P, _I64, _I64, _P, _P, _P, _P, _I64, _I64, _P, _P]),
     "lemoq_kv_quantize_rows": (_I, [_P, _I64, _I64, _P, _P, _P]),
     "lemoq_route_topk": (_I, [_P, _I, _I64, _I64, _I64, _I64, _I, _P, _P, _P]),
+    "lemoq_route_topk_splitk": (_I, [_P, _I64, _I64, _I64, _I64, _I, _P, _P, _P]),
     "lemoq_router_topk_fused": (
         _I,
         [_P, _P, _F, _I64, _P, _I64, _I64, _I, _P, _P, _P, _P, _P, _P],

@@ -17,7 +17,8 @@ KV cache + INT8 bulk   KV-INT8 rows are what kv_int8_bulk_quantize gives)
 sdpa causal attention  ``lemoq_attn_prefill_f16``
 o_proj + residual      ``lemoq_gemm_w8`` with the residual in its epilogue
 post_attention norm    ``lemoq_rmsnorm``
-router F.linear        ``lemoq_gemm_f16_splitk``; ``lemoq_route_topk``
+router F.linear +      ``lemoq_gemm_f16_splitk`` (fp32 partials only);
+routing_softmax_topk   ``lemoq_route_topk_splitk`` (sums the partials, then routes)
 _prefill_forward       ``lemoq_moe_prefill_sort`` / ``_gate_up`` / ``_down`` /
 (moe_static.py:329)    ``_combine`` (the combine adds the residual)
 final norm, lm_head    ``lemoq_rmsnorm`` + ``lemoq_gemm_w8`` on the last row
@@ -110,8 +111,14 @@ def prefill_prompt(weights: Any, tokens: Any, kv: list, cos_tab: Any, sin_tab: A
         _hip.call("lemoq_gemm_w8", P(attn), T, HD, HD, None, P(L.o_codes), P(L.o_scale), H, g, P(h), H, P(h), H,
                   st)
         _hip.call("lemoq_rmsnorm", P(h), T, H, P(L.ln_post), float(s.eps), P(xn), st)
-        _hip.call("lemoq_gemm_f16_splitk", P(xn), T, H, H, P(L.router), E, P(rlog), E, rsplit, P(rws), st)
-        _hip.call("lemoq_route_topk", P(rlog), 1, T, E, E, K, int(bool(s.norm_topk_prob)), P(top_w), P(top_i), st)
+        if rsplit > 1:  # partials only; the routing launch sums them as the GEMM's finish would
+            _hip.call("lemoq_gemm_f16_splitk", P(xn), T, H, H, P(L.router), E, None, E, rsplit, P(rws), st)
+            _hip.call("lemoq_route_topk_splitk", P(rws), rsplit, T, E, K, int(bool(s.norm_topk_prob)), P(top_w),
+                      P(top_i), st)
+        else:
+            _hip.call("lemoq_gemm_f16_splitk", P(xn), T, H, H, P(L.router), E, P(rlog), E, 1, P(rws), st)
+            _hip.call("lemoq_route_topk", P(rlog), 1, T, E, E, K, int(bool(s.norm_topk_prob)), P(top_w), P(top_i),
+                      st)
         _hip.call("lemoq_moe_prefill_sort", P(top_i), P(top_w), T, K, E, P(pair_tok), P(pair_src), P(pair_w),
                   P(expert_off), P(tiles), max_tiles, st)
         _hip.call("lemoq_moe_prefill_gate_up", P(xn), H, P(pair_tok), P(tiles), max_tiles, P(L.gu_codes),

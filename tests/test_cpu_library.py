@@ -69,6 +69,12 @@ def test_argument_rejection_happens_before_any_launch():
     assert lib.lemoq_gemm_f16_splitk(fake, 4, 192, 192, fake, 64, fake, 64, 2, fake, None) == -2
     assert lib.lemoq_gemm_f16_splitk(fake, 4, 256, 256, fake, 64, fake, 64, 2, None, None) == -1
     assert lib.lemoq_gemm_f16_splitk(fake, 4, 256, 256, fake, 64, fake, 64, 65, fake, None) == -2
+    # partials only (y NULL) needs splits > 1; the routing of partials bounds splits and E
+    assert lib.lemoq_gemm_f16_splitk(fake, 4, 256, 256, fake, 64, None, 64, 1, fake, None) == -1
+    assert lib.lemoq_route_topk_splitk(fake, 65, 4, 64, 8, 0, fake, fake, None) == -2
+    assert lib.lemoq_route_topk_splitk(fake, 0, 4, 64, 8, 0, fake, fake, None) == -2
+    assert lib.lemoq_route_topk_splitk(fake, 4, 4, 2000, 8, 0, fake, fake, None) == -2
+    assert lib.lemoq_route_topk_splitk(None, 4, 4, 64, 8, 0, fake, fake, None) == -1
     # prefill entry points
     assert lib.lemoq_gather_rows(fake, 10, 12, fake, 3, fake, None) == -2            # H % 8
     assert lib.lemoq_gather_rows(fake, 10, 16, fake, 3, fake + 8, None) == -4        # dst alignment

@@ -140,3 +140,37 @@ def test_quant_linear_dispatch(dev):
     assert y7.shape == (1, 7, 1024)
     assert torch.equal(y7.reshape(7, 1024), dequant_gemm_separate(x7.reshape(7, 2048), lin.packed, lin.scale,
                                                                   group_size=128))
+
+
+@pytest.mark.parametrize("m,n,k,splits,top_k,norm", [(1000, 64, 2048, 8, 8, False), (37, 64, 2048, 4, 8, True),
+                                                     (1, 16, 256, 2, 4, False), (300, 128, 4096, 8, 8, True)])
+def test_route_topk_of_splitk_partials(m, n, k, splits, top_k, norm, dev):
+    """The router's partials-only split-K GEMM followed by the routing that sums them gives the
+    same ids and weights, bit for bit, as the GEMM's own finish followed by lemoq_route_topk, and
+    the oracle's routing of the oracle's logits."""
+    from lemoq import _hip
+
+    print("case: route_topk_splitk m=%d n=%d k=%d splits=%d" % (m, n, k, splits), flush=True)
+    w = randn(n, k, seed=3 * n + k, std=0.05).to(torch.float16)
+    x = randn(m, k, seed=m + 11).to(torch.float16)
+    xd, wd = x.to(dev), w.to(dev)
+    P, st = _hip.ptr, _hip.stream_of(dev)
+    ws = torch.full((splits, m, n), float("nan"), dtype=torch.float32, device=dev)
+    logits = torch.empty((m, n), dtype=torch.float16, device=dev)
+    tw = [torch.empty((m, top_k), dtype=torch.float32, device=dev) for _ in range(2)]
+    ti = [torch.full((m, top_k), -1, dtype=torch.int64, device=dev) for _ in range(2)]
+    _hip.call("lemoq_gemm_f16_splitk", P(xd), m, k, k, P(wd), n, P(logits), n, splits, P(ws), st)
+    _hip.call("lemoq_route_topk", P(logits), 1, m, n, n, top_k, int(norm), P(tw[0]), P(ti[0]), st)
+    ws.fill_(float("nan"))
+    _hip.call("lemoq_gemm_f16_splitk", P(xd), m, k, k, P(wd), n, None, n, splits, P(ws), st)
+    _hip.call("lemoq_route_topk_splitk", P(ws), splits, m, n, top_k, int(norm), P(tw[1]), P(ti[1]), st)
+    torch.cuda.synchronize()
+    assert not torch.isnan(ws).any()  # every partial was written by the partials-only launch
+    assert torch.equal(ti[0].cpu(), ti[1].cpu())
+    assert torch.equal(tw[0].cpu(), tw[1].cpu())
+    # the oracle's routing of its own logits, where no two probabilities are within rounding
+    ref16 = ops.linear_f16(x, w)
+    rw, ri = ops.route_logits(ref16, top_k, norm)
+    same = (ri == ti[1].cpu()).all(dim=-1)
+    assert float(same.float().mean()) > 0.97, "ids agree on %.3f of rows" % float(same.float().mean())
+    torch.testing.assert_close(tw[1].cpu()[same], rw[same], rtol=2e-2, atol=2e-3)
