@@ -719,17 +719,29 @@ def main(argv=None) -> int:
 
 
 # Launch order of one batched prefill (lemoq.model.prefill.prefill_prompt):
-# gather, 16 x [13 launches], final norm, lm_head GEMM, then the greedy pick;
-# each role with the kernel-name fragment its dispatch must carry.
-PREFILL_LAYER_ROLES = (("rmsnorm (input)", "rmsnorm_kernel"), ("gemm_w8 qkv", "gemm_kernel<true"),
+# gather, layer 0's input norm, 16 x [11 launches] (each layer's combine but the
+# last also writes the next layer's input norm), final norm, lm_head GEMM, then
+# the greedy pick; each role with the kernel-name fragment its dispatch must carry.
+PREFILL_HEAD_ROLES = (("gather_rows", "gather_rows_kernel"), ("rmsnorm (input, layer 0)", "rmsnorm_kernel"))
+PREFILL_LAYER_ROLES = (("gemm_w8 qkv", "gemm_kernel<true"),
                        ("qk_rows (q/k norm, RoPE, KV-INT8)", "qk_rows_kernel"), ("attn_prefill", "attn_prefill_kernel"),
                        ("gemm_w8 o_proj (+residual)", "gemm_kernel<true"), ("rmsnorm (post-attention)", "rmsnorm_kernel"),
                        ("gemm_f16 router (split-K partials)", "gemm_kernel<false"),
-                       ("router split-K sum", "splitk_reduce_kernel"), ("route_topk", "route_topk_kernel"),
+                       ("route_topk (+ split-K sum)", "route_topk_kernel"),
                        ("moe_prefill_sort", "moe_sort_kernel"), ("moe_prefill_gate_up", "moe_gate_up_kernel"),
-                       ("moe_prefill_down", "moe_down_kernel"), ("moe_prefill_combine (+residual)", "moe_combine_kernel"))
+                       ("moe_prefill_down", "moe_down_kernel"))
+PREFILL_COMBINE_NORM = ("moe_prefill_combine (+residual, next input norm)", "moe_combine_kernel<true")
+PREFILL_COMBINE_LAST = ("moe_prefill_combine (+residual)", "moe_combine_kernel<false")
 PREFILL_TAIL_ROLES = (("rmsnorm (final)", "rmsnorm_kernel"), ("gemm_w8 lm_head (last row)", "gemm_kernel<true"),
                       ("argmax_advance", "argmax_advance_kernel"))
+
+
+def prefill_roles(n_layers: int = 16) -> list:
+    roles = list(PREFILL_HEAD_ROLES)
+    for li in range(n_layers):
+        roles += list(PREFILL_LAYER_ROLES)
+        roles.append(PREFILL_COMBINE_NORM if li + 1 < n_layers else PREFILL_COMBINE_LAST)
+    return roles + list(PREFILL_TAIL_ROLES)
 
 
 def prefill_flops(role: str, T: int, shape=None) -> float:
@@ -757,8 +769,7 @@ def summarize_prefill(trace_csv: str, ctx: int) -> str:
                   key=lambda r: int(r["Start_Timestamp"]))
     starts = [i for i, r in enumerate(rows) if "gather_rows_kernel" in r["Kernel_Name"]]
     per_role: dict = {}
-    n_layers = 16
-    roles = [("gather_rows", "gather_rows_kernel")] + list(PREFILL_LAYER_ROLES) * n_layers + list(PREFILL_TAIL_ROLES)
+    roles = prefill_roles(16)
     total = []
     for st in starts:
         seq = rows[st: st + len(roles)]

@@ -566,6 +566,14 @@ int lemoq_moe_prefill_down(const uint16_t* act, int64_t F, const int32_t* pair_s
 int lemoq_moe_prefill_combine(const uint16_t* y, const int64_t* top_i, int64_t T, int64_t top_k,
                               int64_t H, const uint16_t* residual, uint16_t* out, void* stream);
 
+/* lemoq_moe_prefill_combine, and in the same launch xn_out[t] = the RMSNorm
+ * of out[t] with norm_w (the next decoder layer's input_layernorm, rounded as
+ * lemoq_rmsnorm rounds it, bit for bit).  H <= 8192; xn_out (T, H) must not
+ * overlap y, residual or out. */
+int lemoq_moe_prefill_combine_norm(const uint16_t* y, const int64_t* top_i, int64_t T, int64_t top_k,
+                                   int64_t H, const uint16_t* residual, uint16_t* out,
+                                   const uint16_t* norm_w, float eps, uint16_t* xn_out, void* stream);
+
 /* ---------------------------------------------------------------------------
  * Measurement: read n_bytes (multiple of 16, 16-byte aligned) once with
  * nontemporal 16-byte loads.  The buffer is cut into contiguous shares of

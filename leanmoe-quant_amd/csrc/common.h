@@ -59,6 +59,36 @@ __device__ __forceinline__ float wave_sum(float v) {
   v += dpp_f<LEMOQ_DPP_ROW_MIRROR>(v);
   return (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48));
 }
+// Block-wide sum over 256 threads (4 waves); every thread gets the total.
+__device__ __forceinline__ float block_sum_256(float v, float* red) {
+  v = wave_sum(v);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  const float t = red[0] + red[1] + red[2] + red[3];
+  __syncthreads();
+  return t;
+}
+
+// One row of RMSNorm by a 256-thread block, with the rounding points of HF
+// OlmoeRMSNorm.forward (src/lemoq/kernels/rmsnorm.py:184-202): fp32 mean of
+// squares (thread t sums columns t, t + 256, ... in order, then the block
+// sum), x * rstd rounded to fp16, then the fp16 product with the weight.
+// xr may point to global memory or LDS; the result does not depend on which.
+__device__ __forceinline__ void rmsnorm_row_256(const uint16_t* xr, int H, const uint16_t* __restrict__ w,
+                                                float eps, uint16_t* __restrict__ yr, float* red) {
+  float ssq = 0.0f;
+  for (int i = threadIdx.x; i < H; i += 256) {
+    const float a = h2f(xr[i]);
+    ssq += a * a;
+  }
+  const float tot = block_sum_256(ssq, red);
+  const float rstd = 1.0f / sqrtf(tot / (float)H + eps);
+  for (int i = threadIdx.x; i < H; i += 256) {
+    const uint16_t nh = f2h(h2f(xr[i]) * rstd);
+    yr[i] = f2h(h2f(nh) * h2f(w[i]));
+  }
+}
+
 __device__ __forceinline__ float wave_max(float v) {
   v = fmaxf(v, dpp_f<LEMOQ_DPP_QUAD_1032>(v));
   v = fmaxf(v, dpp_f<LEMOQ_DPP_QUAD_2301>(v));

@@ -284,12 +284,22 @@ __global__ __launch_bounds__(128 * WN) void moe_down_kernel(const GroupedArgs a,
 
 // 4. combine: one block per token, 8 columns per thread.  The slot loop has a
 // fixed trip count of 8 (slots past top_k read slot 0 and are not added), so
-// all of a thread's loads are issued before the first add.
+// all of a thread's loads are issued before the first add.  NORM: the block
+// also keeps its output row in LDS and writes the next layer's input
+// RMSNorm of it (the same row function as the plain norm kernel, so xn is
+// bit-identical to a separate norm launch).
+constexpr int kCombineNormMaxH = 8192;
+
+template <bool NORM>
 __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __restrict__ y,
                                                           const int64_t* __restrict__ top_i,
                                                           int top_k, int64_t H,
                                                           const uint16_t* __restrict__ resid,
-                                                          uint16_t* __restrict__ out) {
+                                                          uint16_t* __restrict__ out,
+                                                          const uint16_t* __restrict__ norm_w, float eps,
+                                                          uint16_t* __restrict__ xn) {
+  __shared__ __align__(16) uint16_t row[NORM ? kCombineNormMaxH : 8];
+  __shared__ float red[4];
   const int64_t t = blockIdx.x;
   int64_t ids[8];
 #pragma unroll
@@ -342,6 +352,11 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __rest
       ow[i] = (uint32_t)lo | ((uint32_t)hi << 16);
     }
     *reinterpret_cast<u32x4*>(out + t * H + c) = (u32x4){ow[0], ow[1], ow[2], ow[3]};
+    if constexpr (NORM) *reinterpret_cast<u32x4*>(row + c) = (u32x4){ow[0], ow[1], ow[2], ow[3]};
+  }
+  if constexpr (NORM) {
+    __syncthreads();
+    rmsnorm_row_256(row, (int)H, norm_w, eps, xn + t * H, red);
   }
 }
 
@@ -409,7 +424,30 @@ extern "C" int lemoq_moe_prefill_combine(const uint16_t* y, const int64_t* top_i
   if (T <= 0 || T > 0x7fffffffLL || top_k <= 0 || top_k > 8 || H <= 0 || H % 8 != 0) return LEMOQ_ERR_SHAPE;
   if (!lemoq_aligned16(y) || !lemoq_aligned16(out) || (residual && !lemoq_aligned16(residual)))
     return LEMOQ_ERR_ALIGN;
-  hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)T), dim3(256), 0, lemoq_stream(stream), y, top_i,
-                     (int)top_k, H, residual, out);
+  hipLaunchKernelGGL(moe_combine_kernel<false>, dim3((unsigned)T), dim3(256), 0, lemoq_stream(stream), y, top_i,
+                     (int)top_k, H, residual, out, nullptr, 0.0f, nullptr);
+  LEMOQ_CHECK_LAUNCH();
+}
+
+extern "C" int lemoq_moe_prefill_combine_norm(const uint16_t* y, const int64_t* top_i, int64_t T, int64_t top_k,
+                                              int64_t H, const uint16_t* residual, uint16_t* out,
+                                              const uint16_t* norm_w, float eps, uint16_t* xn_out, void* stream) {
+  if (!y || !top_i || !out || !norm_w || !xn_out) return LEMOQ_ERR_NULL;
+  if (T <= 0 || T > 0x7fffffffLL || top_k <= 0 || top_k > 8 || H <= 0 || H % 8 != 0 || H > kCombineNormMaxH)
+    return LEMOQ_ERR_SHAPE;
+  if (!lemoq_aligned16(y) || !lemoq_aligned16(out) || (residual && !lemoq_aligned16(residual)))
+    return LEMOQ_ERR_ALIGN;
+  // xn_out must not overlap the rows the block reads (y, the residual) or writes (out)
+  const uintptr_t xa = (uintptr_t)xn_out, xb = xa + (uintptr_t)(T * H * 2);
+  const uintptr_t oa = (uintptr_t)out, ob = oa + (uintptr_t)(T * H * 2);
+  if (xa < ob && oa < xb) return LEMOQ_ERR_SHAPE;
+  if (residual) {
+    const uintptr_t ra = (uintptr_t)residual, rb = ra + (uintptr_t)(T * H * 2);
+    if (xa < rb && ra < xb) return LEMOQ_ERR_SHAPE;
+  }
+  const uintptr_t ya = (uintptr_t)y, yb = ya + (uintptr_t)(T * top_k * H * 2);
+  if (xa < yb && ya < xb) return LEMOQ_ERR_SHAPE;
+  hipLaunchKernelGGL(moe_combine_kernel<true>, dim3((unsigned)T), dim3(256), 0, lemoq_stream(stream), y, top_i,
+                     (int)top_k, H, residual, out, norm_w, eps, xn_out);
   LEMOQ_CHECK_LAUNCH();
 }

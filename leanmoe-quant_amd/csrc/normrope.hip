@@ -11,34 +11,12 @@
 
 namespace {
 
-// Block-wide sum over 256 threads (4 waves).
-__device__ __forceinline__ float block_sum_256(float v, float* red) {
-  v = wave_sum(v);
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-  __syncthreads();
-  const float t = red[0] + red[1] + red[2] + red[3];
-  __syncthreads();
-  return t;
-}
-
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict__ x, int H,
                                                       const uint16_t* __restrict__ w, float eps,
                                                       uint16_t* __restrict__ y) {
   __shared__ float red[4];
   const int64_t r = blockIdx.x;
-  const uint16_t* xr = x + r * H;
-  uint16_t* yr = y + r * H;
-  float ssq = 0.0f;
-  for (int i = threadIdx.x; i < H; i += 256) {
-    const float a = h2f(xr[i]);
-    ssq += a * a;
-  }
-  const float tot = block_sum_256(ssq, red);
-  const float rstd = 1.0f / sqrtf(tot / (float)H + eps);
-  for (int i = threadIdx.x; i < H; i += 256) {
-    const uint16_t nh = f2h(h2f(xr[i]) * rstd);
-    yr[i] = f2h(h2f(nh) * h2f(w[i]));
-  }
+  rmsnorm_row_256(x + r * H, H, w, eps, y + r * H, red);
 }
 
 // Embedding rows of several tokens: dst[r] = src[ids[r]] (a zero row for an

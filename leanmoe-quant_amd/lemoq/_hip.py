@@ -187,6 +187,7 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "lemoq_moe_prefill_gate_up": (_I, [_P, _I64, _P, _P, _I64, _P, _P, _I64, _I64, _P, _P]),
     "lemoq_moe_prefill_down": (_I, [_P, _I64, _P, _P, _P, _I64, _P, _P, _I64, _I64, _P, _P]),
     "lemoq_moe_prefill_combine": (_I, [_P, _P, _I64, _I64, _I64, _P, _P, _P]),
+    "lemoq_moe_prefill_combine_norm": (_I, [_P, _P, _I64, _I64, _I64, _P, _P, _P, _F, _P, _P]),
 }
 
 

@@ -10,7 +10,8 @@ with the HIP kernels, one layer at a time:
 HF / reference         here (C-ABI entry point)
 =====================  ==========================================================
 embed_tokens           ``lemoq_gather_rows``
-input_layernorm        ``lemoq_rmsnorm`` (the fused RMSNorm, any row count)
+input_layernorm        ``lemoq_rmsnorm`` (the fused RMSNorm, any row count) for layer 0;
+                       the previous layer's ``lemoq_moe_prefill_combine_norm`` after
 q/k/v_proj             ``lemoq_gemm_w8`` (QuantLinear separate arm, linear.py:471-480)
 q_norm, k_norm, RoPE,  ``lemoq_qk_norm_rope_kv_i8_rows`` (HF RoPE rounding; the
 KV cache + INT8 bulk   KV-INT8 rows are what kv_int8_bulk_quantize gives)
@@ -20,7 +21,8 @@ post_attention norm    ``lemoq_rmsnorm``
 router F.linear +      ``lemoq_gemm_f16_splitk`` (fp32 partials only);
 routing_softmax_topk   ``lemoq_route_topk_splitk`` (sums the partials, then routes)
 _prefill_forward       ``lemoq_moe_prefill_sort`` / ``_gate_up`` / ``_down`` /
-(moe_static.py:329)    ``_combine`` (the combine adds the residual)
+(moe_static.py:329)    ``_combine`` (the combine adds the residual; ``_combine_norm``
+                       also writes the next layer's input norm)
 final norm, lm_head    ``lemoq_rmsnorm`` + ``lemoq_gemm_w8`` on the last row
 =====================  ==========================================================
 
@@ -100,8 +102,10 @@ def prefill_prompt(weights: Any, tokens: Any, kv: list, cos_tab: Any, sin_tab: A
     qk_scale = float((1.0 / math.sqrt(D)) * LOG2E)
 
     _hip.call("lemoq_gather_rows", P(weights.embed), s.vocab, H, P(tokens), T, P(h), st)
-    for L, c in zip(weights.layers, kv):
-        _hip.call("lemoq_rmsnorm", P(h), T, H, P(L.ln_in), float(s.eps), P(xn), st)
+    _hip.call("lemoq_rmsnorm", P(h), T, H, P(weights.layers[0].ln_in), float(s.eps), P(xn), st)
+    n_layers = len(weights.layers)
+    for li, (L, c) in enumerate(zip(weights.layers, kv)):
+        # xn holds this layer's input norm: the previous layer's combine wrote it
         _hip.call("lemoq_gemm_w8", P(xn), T, H, H, None, P(L.qkv_codes), P(L.qkv_scale), 3 * HD, g,
                   P(qkv), 3 * HD, None, 0, st)
         _hip.call("lemoq_qk_norm_rope_kv_i8_rows", P(qkv), T, NH, D, P(L.q_norm), P(L.k_norm), float(s.eps),
@@ -125,7 +129,11 @@ def prefill_prompt(weights: Any, tokens: Any, kv: list, cos_tab: Any, sin_tab: A
                   P(L.gu_scale), F, g, P(act), st)
         _hip.call("lemoq_moe_prefill_down", P(act), F, P(pair_src), P(pair_w), P(tiles), max_tiles,
                   P(L.dn_codes), P(L.dn_scale), H, g, P(ybuf), st)
-        _hip.call("lemoq_moe_prefill_combine", P(ybuf), P(top_i), T, K, H, P(h), P(h), st)
+        if li + 1 < n_layers:
+            _hip.call("lemoq_moe_prefill_combine_norm", P(ybuf), P(top_i), T, K, H, P(h), P(h),
+                      P(weights.layers[li + 1].ln_in), float(s.eps), P(xn), st)
+        else:
+            _hip.call("lemoq_moe_prefill_combine", P(ybuf), P(top_i), T, K, H, P(h), P(h), st)
     last = h[T - 1:]
     _hip.call("lemoq_rmsnorm", P(last), 1, H, P(weights.final_norm), float(s.eps), P(xn), st)
     _hip.call("lemoq_gemm_w8", P(xn), 1, H, H, None, P(weights.lm_codes), P(weights.lm_scale), s.vocab, g,

@@ -89,6 +89,12 @@ def test_argument_rejection_happens_before_any_launch():
     assert lib.lemoq_moe_prefill_gate_up(fake, 2048, fake, fake, 64, fake, fake, 1000, 128, fake, None) == -2
     assert lib.lemoq_moe_prefill_down(fake, 1024, fake, fake, fake, 64, fake + 4, fake, 2048, 128, fake, None) == -4
     assert lib.lemoq_moe_prefill_combine(fake, fake, 4, 9, 2048, None, fake, None) == -2
+    # combine + next norm: H past the LDS row, xn overlapping out, a missing norm weight
+    cn = lambda T, H, out, w, xn: lib.lemoq_moe_prefill_combine_norm(  # noqa: E731
+        1 << 24, fake, T, 8, H, None, out, w, 1e-5, xn, None)
+    assert cn(4, 8200, 1 << 20, fake, 1 << 22) == -2
+    assert cn(4, 2048, 1 << 20, fake, (1 << 20) + 4096) == -2
+    assert cn(4, 2048, 1 << 20, None, 1 << 22) == -1
     # fused merge + o_proj: head_dim 64 and 6 heads unsupported, N % 32, too many splits, misaligned codes
     assert lib.lemoq_attn_merge_o_proj_w8(fake, fake, fake, 16, 16, 64, fake, fake, 2048, 128, fake, None) == -3
     assert lib.lemoq_attn_merge_o_proj_w8(fake, fake, fake, 6, 16, 128, fake, fake, 2048, 128, fake, None) == -3

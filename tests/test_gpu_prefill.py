@@ -215,6 +215,41 @@ def test_moe_prefill_vs_oracle(T, H, F, E, K, skew, dev):
     assert_close(out.cpu(), ref, what="moe_prefill T=%d" % T)
 
 
+COMBINE_NORM_CASES = [(1, 2048, 8, True), (77, 2048, 8, True), (513, 4096, 2, True), (40, 8192, 8, False),
+                      (9, 264, 4, True)]
+
+
+@pytest.mark.parametrize("T,H,K,with_resid", COMBINE_NORM_CASES,
+                         ids=["T%d-H%d-k%d%s" % (c[0], c[1], c[2], "-resid" if c[3] else "")
+                              for c in COMBINE_NORM_CASES])
+def test_moe_combine_norm_equals_combine_then_rmsnorm(T, H, K, with_resid, dev):
+    """The combine that also writes the next layer's input norm gives the plain combine's rows and
+    lemoq_rmsnorm's norm of them, bit for bit; the norm also against the oracle's RMSNorm."""
+    from lemoq import _hip
+
+    print("case: combine_norm T=%d H=%d k=%d resid=%s" % (T, H, K, with_resid), flush=True)
+    P, st = _hip.ptr, _hip.stream_of(dev)
+    gen = torch.Generator().manual_seed(T * H + K)
+    y = (torch.randn((T * K, H), generator=gen) * 0.5).to(torch.float16).to(dev)
+    top_i = torch.stack([torch.randperm(64, generator=gen)[:K] for _ in range(T)]).to(torch.int64).to(dev)
+    resid = (torch.randn((T, H), generator=gen) * 2.0).to(torch.float16).to(dev)
+    w = (1.0 + 0.1 * torch.randn((H,), generator=gen)).to(torch.float16).to(dev)
+    eps = 1e-5
+    out_a = resid.clone()
+    out_b = resid.clone()
+    xn_a = torch.full((T, H), 7.0, dtype=torch.float16, device=dev)
+    xn_b = torch.full((T, H), 9.0, dtype=torch.float16, device=dev)
+    rp = P(out_a) if with_resid else None
+    _hip.call("lemoq_moe_prefill_combine", P(y), P(top_i), T, K, H, rp, P(out_a), st)
+    _hip.call("lemoq_rmsnorm", P(out_a), T, H, P(w), eps, P(xn_a), st)
+    rp = P(out_b) if with_resid else None
+    _hip.call("lemoq_moe_prefill_combine_norm", P(y), P(top_i), T, K, H, rp, P(out_b), P(w), eps, P(xn_b), st)
+    torch.cuda.synchronize()
+    assert torch.equal(out_a.cpu(), out_b.cpu())
+    assert torch.equal(xn_a.cpu(), xn_b.cpu())
+    assert_close(xn_b.cpu(), ops.rms_norm(out_b.cpu(), w.cpu(), eps), what="combine_norm T=%d H=%d" % (T, H))
+
+
 def _prefill_vs_oracle(shape, prompt, seed, steps, dev):
     from lemoq.model.olmoe import DecodeSession, OlmoeW8Weights
 
