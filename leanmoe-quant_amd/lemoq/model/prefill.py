@@ -84,9 +84,10 @@ def prefill_prompt(weights: Any, tokens: Any, kv: list, cos_tab: Any, sin_tab: A
     k16 = torch.empty((NH, S, D), **f16)
     v16 = torch.empty((NH, S, D), **f16)
     attn = torch.empty((T, HD), **f16)
-    rlog = torch.empty((T, E), **f16)
     # the router's 64 outputs give few output tiles: K is cut into up to 8 ranges
+    # whose fp32 partials the routing launch sums; fp16 logits only without a split
     rsplit = next(sp for sp in (8, 4, 2, 1) if H % (64 * sp) == 0)
+    rlog = torch.empty((T, E), **f16) if rsplit == 1 else None
     rws = torch.empty((rsplit, T, E), dtype=torch.float32, device=dev)
     top_w = torch.empty((T, K), dtype=torch.float32, device=dev)
     top_i = torch.empty((T, K), dtype=torch.int64, device=dev)
