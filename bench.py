@@ -146,7 +146,10 @@ def time_cold(torch, flusher, launches, reps: int) -> dict:
 # ---------------------------------------------------------------------------
 # isolated kernels of the step (the same entry points the step executor calls)
 # ---------------------------------------------------------------------------
-def kernel_table(torch, hip, w, sess, flusher, reps: int) -> dict:
+READ_FLOOR = "read floor (gate/up bytes, read only)"
+
+
+def kernel_table(torch, hip, w, sess, flusher, reps: int, floors: bool = True) -> dict:
     s = w.shape
     H, HD, D, F, E, K, g = s.hidden, s.heads * s.head_dim, s.head_dim, s.ffn, s.num_experts, s.top_k, s.group_size
     P, st = hip.ptr, hip.stream_of
@@ -170,6 +173,9 @@ def kernel_table(torch, hip, w, sess, flusher, reps: int) -> dict:
         "fill": torch.zeros((1,), dtype=torch.int32, device=dev),
         "ids2": sess.top_i.clone(),
         "tw2": sess.top_w.clone(),
+        "act2": sess.act.clone(),
+        "fixed_ids": torch.arange(K, dtype=torch.int64, device=dev) * (E // K),
+        "probe": torch.empty((1024,), dtype=torch.int32, device=dev),
     }
     kv = sess.kv
     qk_scale = (1.0 / math.sqrt(D)) * 1.4426950408889634
@@ -183,6 +189,20 @@ def kernel_table(torch, hip, w, sess, flusher, reps: int) -> dict:
                                P(sess.router_logits), K, int(s.norm_topk_prob), E, F, H, g, P(scratch["act"]),
                                P(scratch["ids"]), P(scratch["tw"]), st()) for i in range(nl)],
         ["moe_gate_up_kernel"])
+    if floors:
+        # The same launch given the ids (no routing before the weight loads), and a launch that only
+        # reads the same number of bytes: the single-launch read floor the routed kernel is held to.
+        # (Left out of the traffic pass, whose cache flushes are read_probe dispatches too.)
+        add("moe_gate_up_w8 (ids given)", K * w8(2 * F, H) + H * 2 + K * 8 + K * F * 2,
+            [lambda i=i: hip.call("lemoq_moe_gate_up_w8", P(scratch["h"]), P(L[i].gu_codes), P(L[i].gu_scale),
+                                   P(scratch["fixed_ids"]), K, E, F, H, g, P(scratch["act2"]), st())
+             for i in range(nl)],
+            ["moe_gate_up_kernel"])
+        gu_bytes = (K * w8(2 * F, H) + H * 2 + E * 2 + K * F * 2) // 16 * 16
+        add(READ_FLOOR, gu_bytes,
+            [lambda i=i: hip.call("lemoq_read_probe", P(L[i].gu_codes), gu_bytes, P(scratch["probe"]), 1024, st())
+             for i in range(nl)],
+            ["read_probe_kernel"])
     add("moe_down_w8", K * w8(H, F) + K * F * 2 + 3 * H * 2,
         [lambda i=i: hip.call("lemoq_moe_down_w8", P(scratch["act"]), P(L[i].dn_codes), P(L[i].dn_scale),
                                P(scratch["ids"]), P(scratch["tw"]), K, E, H, F, g, P(scratch["h"]),
@@ -590,7 +610,7 @@ def main(argv=None) -> int:
         sess = DecodeSession(w, [1] * args.ctx, max_new_tokens=2)
         synthetic_cache(torch, sess, sess.ctx + 1)
         cal = copy_calibration(torch, _hip, flusher)
-        kt = kernel_table(torch, _hip, w, sess, flusher, args.kernel_reps)
+        kt = kernel_table(torch, _hip, w, sess, flusher, args.kernel_reps, floors=False)
         print(json.dumps({"mode": "traffic", "ctx": args.ctx, "calibration": cal, "kernels": kt}))
         return 0
 
@@ -699,6 +719,9 @@ def main(argv=None) -> int:
             "traffic": traffic,
             "bytes_per_launch": dom["bytes"],
             "avg_us": dom["avg_us"],
+            # a launch that only reads the same bytes, timed the same way (cold, 64 launches)
+            "read_floor_avg_us": kt[READ_FLOOR]["avg_us"],
+            "frac_of_read_floor": kt[READ_FLOOR]["avg_us"] / dom["avg_us"],
         },
         "kernels": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()
                         if kk != "dispatch_kernels"} for k, v in kt.items()},
