@@ -18,7 +18,7 @@ Contents (each function cites the reference file:line it restates):
 * ``oracle.olmoe``  — the full decode step on the CPU (HF OLMoE decoder math
   with the reference's patched operators), and a seeded tiny-model init.
 
-How each function is pinned (golden vectors, closed forms, brute force,
-independent restatements, HF transformers) is listed per function in
-DESIGN.md and exercised by ``tests/test_oracle_*.py``.
+Each function is pinned by golden vectors, closed forms, brute force,
+independent restatements or HF transformers; ``tests/test_oracle_*.py``
+hold those checks, each test naming the function and the check it applies.
 """
