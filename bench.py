@@ -203,6 +203,14 @@ def kernel_table(torch, hip, w, sess, flusher, reps: int, floors: bool = True) -
             [lambda i=i: hip.call("lemoq_read_probe", P(L[i].gu_codes), gu_bytes, P(scratch["probe"]), 1024, st())
              for i in range(nl)],
             ["read_probe_kernel"])
+        # the same floor at the down and qkv launches' byte counts (each layer's gate/up codes
+        # serve as 16 distinct source buffers)
+        for label, nb in (("down", K * w8(H, F) + K * F * 2 + 3 * H * 2), ("qkv", w8(3 * HD, H) + 2 * H * 2 + 3 * HD * 2)):
+            nb16 = nb // 16 * 16
+            add("read floor (%s bytes, read only)" % label, nb16,
+                [lambda i=i, nb16=nb16: hip.call("lemoq_read_probe", P(L[i].gu_codes), nb16, P(scratch["probe"]),
+                                                 1024, st()) for i in range(nl)],
+                ["read_probe_kernel"])
     add("moe_down_w8", K * w8(H, F) + K * F * 2 + 3 * H * 2,
         [lambda i=i: hip.call("lemoq_moe_down_w8", P(scratch["act"]), P(L[i].dn_codes), P(L[i].dn_scale),
                                P(scratch["ids"]), P(scratch["tw"]), K, E, H, F, g, P(scratch["h"]),
