@@ -8,13 +8,17 @@ split-KV attention, one graph per step): seeded random weights, prompt of
 captured hipGraph.  The reference quotes this as ms/token at ctx 1024 and 4096
 (README_EN.md:66-71 of LeanMoE-Quant, RTX 5090).
 
-Printed: ONE JSON line on stdout.  ``value`` is ms/token at ``--ctx`` (wall
-clock over exactly ``--steps`` replays, synchronised on both sides, after
-``--warmup`` replays); the line also carries the second context, the step's
-HBM roofline fraction, per-kernel cold timings, the dominant kernel's roofline
-(``roofline``), the CPU oracle's ms/token on this host (``cpu_baseline``) and,
-per context, the batched prefill's TTFT with E2E-32/128 beside the
-reference's published values (``prefill``).  Progress goes to stderr.
+Printed: ONE JSON line on stdout.  ``value`` is ms/token at ``--ctx``: the p50
+of ``--steps`` per-step times (an event between consecutive replays, after
+``--warmup`` replays), the reference's timing convention; ``ms_per_step_mean``
+is the wall clock over exactly ``--steps`` back-to-back replays, synchronised on
+both sides.  The line also carries the second context, the step's HBM roofline
+fraction, per-kernel cold timings, the dominant kernel's roofline
+(``roofline``), the CPU path on this host (``cpu_baseline``: the oracle's
+ms/token p50/p99 on all threads and on one, at both contexts, and the C1-C4
+operators' microseconds beside the GPU's) and, per context, the batched
+prefill's TTFT with E2E-32/128 beside the reference's published values
+(``prefill``).  Progress goes to stderr.
 
 ``--mode kernels`` runs only the weights + isolated kernel timings.
 ``--mode traffic`` is the short form profiled under ``rocprofv3 --pmc``: a
@@ -76,8 +80,12 @@ def parse_args(argv=None):
     ap.add_argument("--ctx2", type=int, default=4096, help="second context (0: skip)")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--kernel-reps", type=int, default=4)
-    ap.add_argument("--cpu-budget-s", type=float, default=20.0)
-    ap.add_argument("--cpu-check-steps", type=int, default=32)
+    ap.add_argument("--cpu-check-steps", type=int, default=32,
+                    help="GPU steps checked against the CPU oracle (also its first timed steps)")
+    ap.add_argument("--cpu-warmup", type=int, default=5, help="untimed CPU oracle steps / op calls")
+    ap.add_argument("--cpu-timed", type=int, default=20, help="timed CPU oracle steps / op calls (all threads)")
+    ap.add_argument("--cpu-timed-1t", type=int, default=20, help="timed CPU oracle steps on one thread")
+    ap.add_argument("--no-cpu-ops", action="store_true", help="skip the per-operator CPU timings (C1-C4)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--mode", choices=("full", "kernels", "traffic", "prefill", "step"), default="full")
     ap.add_argument("--summarize-pmc", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "PLAN_JSON"))
@@ -230,6 +238,20 @@ def kernel_table(torch, hip, w, sess, flusher, reps: int, floors: bool = True) -
                                qk_scale, P(sess.part_m), P(sess.part_l), P(sess.part_acc), st())
          for i in range(nl)],
         ["attn_split_fused_i8_kernel"])
+    if sess.attn_output_fused and int(hip.load().lemoq_attn_layer_check(s.heads, D, sess.num_splits, H, g, E)) == 0:
+        npart = HD // 512
+        attn_bytes = KV_BYTES_PER_TOKEN_LAYER * filled + 3 * HD * 2 + 2 * HD * 2 + 2 * D * 2
+        add("attn_layer_i8 (attention + merge/o_proj + router, 1 launch)",
+            attn_bytes + w8(H, HD) + E * H * 2 + 4 * H * 2 + E * 2,
+            [lambda i=i: hip.call("lemoq_attn_layer_i8", P(sess.qkv), s.heads, D, P(L[i].q_norm), P(L[i].k_norm),
+                                   s.eps, P(sess.cos_tab), P(sess.sin_tab), P(sess.pos), P(kv[i]["kc"]),
+                                   P(kv[i]["ks"]), P(kv[i]["vc"]), P(kv[i]["vs"]), S * D, S, ns, qk_scale,
+                                   P(sess.part_m), P(sess.part_l), P(sess.part_acc), P(L[i].o_codes),
+                                   P(L[i].o_scale), H, g, P(sess.o_part), P(scratch["h"]), P(L[i].ln_post),
+                                   P(L[i].router), E, P(scratch["h2"]), P(scratch["xn"]), P(scratch["lg"]),
+                                   P(sess.sync), 200_000, st())
+             for i in range(nl)],
+            ["attn_layer_kernel"])
     if sess.attn_output_fused:
         npart = HD // 512
         add("attn_merge_o_proj_w8", w8(H, HD) + s.heads * ns * (D + 2) * 4 + npart * H * 4,
@@ -305,16 +327,14 @@ def time_decode(torch, w, ctx: int, steps: int, warmup: int, extra: int):
     sess.capture()
     ttft = measure_prefill(torch, sess)
     log("ctx %d: batched prefill (TTFT) p50 %.3f ms over %d runs" % (ctx, ttft["p50"], ttft["runs"]))
-    for _ in range(warmup):
-        sess.graph.replay()
-    torch.cuda.synchronize()
+    sess.replay(warmup)
     filled0 = int(sess.filled.item())
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     e0.record()
     for _ in range(steps):
-        sess.graph.replay()
+        sess.replay(1, synchronize=False)
     e1.record()
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3
@@ -323,7 +343,7 @@ def time_decode(torch, w, ctx: int, steps: int, warmup: int, extra: int):
     evs = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
     evs[0].record()
     for i in range(steps):
-        sess.graph.replay()
+        sess.replay(1, synchronize=False)
         evs[i + 1].record()
     torch.cuda.synchronize()
     per = sorted(evs[i].elapsed_time(evs[i + 1]) for i in range(steps))
@@ -348,64 +368,233 @@ def time_decode(torch, w, ctx: int, steps: int, warmup: int, extra: int):
     return sess, res
 
 
-def cpu_baseline(torch, w, cap, gpu_tokens, gpu_logits, budget_s: float, max_steps: int, snap) -> dict:
-    """The CPU oracle (torch, this host's cores) decoding from the GPU's KV snapshot,
-    teacher-forced on the GPU's tokens so every step compares the same input."""
+def _p50_p99(samples: list) -> tuple:
+    s = sorted(samples)
+    return s[len(s) // 2], s[min(len(s) - 1, int(round(0.99 * (len(s) - 1))))]
+
+
+def _pad_kv(torch, kv: list, slots: int) -> list:
+    """Host KV-INT8 snapshot widened to ``slots`` cache slots (the CPU oracle keeps
+    stepping past the GPU session's capacity); new slots hold code 0, scale 1."""
+    out = []
+    for layer in kv:
+        d = {}
+        for name, t in layer.items():
+            S = int(t.shape[1])
+            if S >= slots:
+                d[name] = t
+                continue
+            shape = list(t.shape)
+            shape[1] = slots
+            fill = 1.0 if name in ("ks", "vs") else 0
+            big = torch.full(shape, fill, dtype=t.dtype)
+            big[:, :S] = t
+            d[name] = big
+        out.append(d)
+    return out
+
+
+def _oracle_steps(od, first_token: int, pos: int, n: int, forced: list) -> tuple:
+    """n oracle decode steps from (first_token, pos); step i consumes forced[i] when
+    given, else the oracle's own greedy token.  Returns (ms per step, logits)."""
+    times, logits, tok = [], [], int(first_token)
+    for i in range(n):
+        if i < len(forced):
+            tok = int(forced[i])
+        t = time.perf_counter()
+        lg = od.step(tok, pos + i)
+        times.append(1e3 * (time.perf_counter() - t))
+        logits.append(lg)
+        tok = od.greedy(lg)
+    return times, logits
+
+
+def cpu_baseline(torch, host, snap, gpu_tokens, gpu_logits, *, warmup: int, timed: int, timed_1t: int,
+                 snap2=None) -> dict:
+    """The CPU path (the torch-CPU oracle restating the reference's ``backend="oracle"``
+    operators and the HF glue) on this host's cores: the full decode step from the GPU's
+    KV snapshot, teacher-forced on the GPU's greedy tokens (the parity check of every
+    bench run), ``warmup`` untimed + ``timed`` timed steps, p50 / p99 per step
+    (``benchmarks/timing.py:19-69`` of the reference), on all threads and on one."""
     from oracle.olmoe import OracleDecoder
 
     kv, token, pos = snap
+    n_all = warmup + timed
+    slots = pos + max(n_all, len(gpu_logits)) + warmup + timed_1t + 2
+    if snap2 is not None:
+        slots = max(slots, snap2[2] + n_all + 2)
     t = time.time()
-    host = w.to_host()
-    od = OracleDecoder(host, cap.max_seq, kv=kv)
-    log("cpu oracle ready in %.1fs (%d threads)" % (time.time() - t, torch.get_num_threads()))
+    od = OracleDecoder(host, slots, kv=_pad_kv(torch, kv, slots))
+    threads = torch.get_num_threads()
+    log("cpu oracle ready in %.1fs (%d threads)" % (time.time() - t, threads))
     seq = [token] + list(gpu_tokens)
-    times, agree, flips, max_kl, max_diff = [], 0, [], 0.0, 0.0
-    n = 0
-    for i in range(min(max_steps, len(gpu_logits))):
-        t = time.perf_counter()
-        lg = od.step(seq[i], pos + i)
-        times.append(time.perf_counter() - t)
-        ref, got = lg.double(), gpu_logits[i].double()
-        p, q = torch.log_softmax(ref, -1), torch.log_softmax(got, -1)
+    n = max(n_all, len(gpu_logits))
+    times, logits = _oracle_steps(od, token, pos, n, seq)
+    agree, flips, max_kl, max_diff = 0, [], 0.0, 0.0
+    for i, got in enumerate(gpu_logits):
+        ref, g = logits[i].double(), got.double()
+        p, q = torch.log_softmax(ref, -1), torch.log_softmax(g, -1)
         kl = float((p.exp() * (p - q)).sum())
-        diff = float((ref - got).abs().max())
+        diff = float((ref - g).abs().max())
         top = torch.topk(ref, 2).values
-        margin = float(top[0] - top[1])
-        if int(torch.argmax(ref)) == int(torch.argmax(got)):
+        if int(torch.argmax(ref)) == int(torch.argmax(g)):
             agree += 1
         else:
-            flips.append({"step": i, "margin": margin, "logit_diff": diff})
+            flips.append({"step": i, "margin": float(top[0] - top[1]), "logit_diff": diff})
         max_kl, max_diff = max(max_kl, kl), max(max_diff, diff)
-        n += 1
-        if sum(times) > budget_s:
-            break
-    timed = times[1:] if len(times) > 1 else times  # first step warms the allocator
-    ms = 1e3 * sum(timed) / len(timed)
-    # One thread: two more steps (the second timed), the same oracle state.
-    threads = torch.get_num_threads()
+    t_all = times[warmup:]
+    p50, p99 = _p50_p99(t_all)
+    log("cpu oracle ctx %d: p50 %.1f p99 %.1f ms/token on %d threads (%d timed after %d warmup)"
+        % (pos, p50, p99, threads, len(t_all), warmup))
+    # one thread: the same oracle keeps decoding (its own greedy tokens) from where it stopped
     torch.set_num_threads(1)
     try:
-        od.step(seq[n], pos + n)
-        t = time.perf_counter()
-        od.step(seq[n + 1] if n + 1 < len(seq) else seq[n], pos + n + 1)
-        ms_1t = 1e3 * (time.perf_counter() - t)
+        t1, _ = _oracle_steps(od, od.greedy(logits[-1]), pos + n, warmup + timed_1t, [])
     finally:
         torch.set_num_threads(threads)
-    log("cpu oracle: %.1f ms/token on %d threads, %.1f ms/token on 1 thread" % (ms, threads, ms_1t))
-    return {
-        "value": ms,
+    p50_1t, p99_1t = _p50_p99(t1[warmup:])
+    log("cpu oracle: p50 %.1f p99 %.1f ms/token on 1 thread (%d timed after %d warmup)"
+        % (p50_1t, p99_1t, timed_1t, warmup))
+    res = {
+        "value": p50,
         "unit": "ms/token",
         "cores": int(threads),
-        "value_1thread": ms_1t,
+        "stat": "p50",
+        "p99": p99,
+        "mean": sum(t_all) / len(t_all),
+        "warmup": warmup,
+        "timed": len(t_all),
+        "value_1thread": p50_1t,
+        "p99_1thread": p99_1t,
+        "timed_1thread": timed_1t,
         "cpu_model": _cpu_model(),
         "kind": "port",
-        "sample": "%d decode steps of the full OLMoE-1B-7B-shaped w8a16+KV-INT8 model by the torch-CPU oracle "
-                  "from the GPU's KV snapshot at position %d, fed the GPU's greedy tokens (first step untimed)"
-                  % (n, pos),
+        "sample": "%d decode steps (%d warmup) of the full OLMoE-1B-7B-shaped w8a16+KV-INT8 model by the "
+                  "torch-CPU oracle from the GPU's KV snapshot at position %d, fed the GPU's greedy tokens; "
+                  "then %d steps (%d warmup) on one thread" % (n, warmup, pos, warmup + timed_1t, warmup),
         "host_cpu_count": os.cpu_count(),
-        "parity": {"steps": n, "argmax_agree": agree, "near_tie_flips": flips, "max_kl": max_kl,
+        "parity": {"steps": len(gpu_logits), "argmax_agree": agree, "flips": flips, "max_kl": max_kl,
                    "max_logit_diff": max_diff},
     }
+    if snap2 is not None:
+        kv2, token2, pos2 = snap2
+        od.kv = _pad_kv(torch, kv2, slots)
+        t2, _ = _oracle_steps(od, token2, pos2, n_all, [])
+        a, b = _p50_p99(t2[warmup:])
+        res["ctx2"] = {"position": pos2, "p50": a, "p99": b, "timed": timed, "warmup": warmup}
+        log("cpu oracle ctx %d: p50 %.1f p99 %.1f ms/token on %d threads" % (pos2, a, b, threads))
+    return res
+
+
+def cpu_ops_baseline(torch, host, *, warmup: int, timed: int, seed: int = 0) -> dict:
+    """C1-C4 of BASELINE.json as single operators of the reference's CPU path (the
+    torch oracle backend, ``moe_grouped_quant.py:476-477,520-523``, ``attn_decode.py:581-586``,
+    ``reference.py:50-60``; dense GEMVs dequantise the weight on every call as that
+    oracle does), p50 / p99 microseconds per call on this host's threads.  C1 uses the
+    model's layer-0 router and experts with norm_topk_prob=True; x ~ N(0, 1)."""
+    from oracle import ops
+    from oracle import quant as oq
+
+    s = host.shape
+    g = s.group_size
+    L0 = host.layers[0]
+    gen = torch.Generator().manual_seed(seed)
+    x = torch.randn((1, s.hidden), generator=gen).to(torch.float16)
+    gamma = (torch.rand((s.hidden,), generator=gen) + 0.5).to(torch.float16)
+    D, NH = s.head_dim, s.heads
+    HD = NH * D
+
+    def timeit(fn) -> dict:
+        ts = []
+        for i in range(warmup + timed):
+            t = time.perf_counter()
+            fn()
+            if i >= warmup:
+                ts.append(1e6 * (time.perf_counter() - t))
+        a, b = _p50_p99(ts)
+        return {"cpu_us_p50": a, "cpu_us_p99": b}
+
+    def c1():
+        _, tw, ti = ops.route(x, L0.router, s.top_k, True)
+        ops.grouped_moe_w8(x.reshape(-1), L0.gu_codes, L0.gu_scale, L0.dn_codes, L0.dn_scale, g,
+                           ti.reshape(-1), tw.reshape(-1))
+
+    out = {"C1 grouped MoE (router + top-8 of 64, w8 gate/up + down)": timeit(c1)}
+    for ctx in (1024, 4096):
+        q = torch.randn((NH, D), generator=gen).to(torch.float16)
+        k = torch.randn((NH, ctx, D), generator=gen).to(torch.float16)
+        v = torch.randn((NH, ctx, D), generator=gen).to(torch.float16)
+        out["C2 split-KV fp16 attention ctx %d" % ctx] = timeit(
+            lambda: ops.split_kv_oracle(q, k, v, ctx, num_splits=ctx // 256).to(torch.float16))
+    for ctx in (4096, 16384):
+        q = torch.randn((NH, D), generator=gen).to(torch.float16)
+        kc, ks = oq.kv_quantize_rows(torch.randn((NH * ctx, D), generator=gen).to(torch.float16).numpy())
+        vc, vs = oq.kv_quantize_rows(torch.randn((NH * ctx, D), generator=gen).to(torch.float16).numpy())
+        kc, vc = torch.from_numpy(kc).reshape(NH, ctx, D), torch.from_numpy(vc).reshape(NH, ctx, D)
+        ks, vs = torch.from_numpy(ks).reshape(NH, ctx), torch.from_numpy(vs).reshape(NH, ctx)
+        out["C3 KV-INT8 attention ctx %d" % ctx] = timeit(
+            lambda: ops.int8_attention_folded(q, kc, ks, vc, vs, ctx).to(torch.float16))
+    xn = ops.rms_norm(x.reshape(-1), gamma, s.eps)
+    out["C4 RMSNorm 2048"] = timeit(lambda: ops.rms_norm(x.reshape(-1), gamma, s.eps))
+    out["C4 qkv w8 GEMV 6144x2048"] = timeit(
+        lambda: ops.dequant_gemm_separate(xn.reshape(1, -1), L0.qkv_codes, L0.qkv_scale, g, out_dtype=torch.float16))
+    qkv = ops.dequant_gemm_separate(xn.reshape(1, -1), L0.qkv_codes, L0.qkv_scale, g, out_dtype=torch.float16)
+    cos, sin = ops.rotary_cos_sin(torch.tensor([4096]), D, s.rope_theta)
+
+    def qk_norm_rope():
+        qn = ops.rms_norm(qkv[0, :HD], L0.q_norm, s.eps).reshape(NH, D)
+        kn = ops.rms_norm(qkv[0, HD:2 * HD], L0.k_norm, s.eps).reshape(NH, D)
+        ops.rope_fused(qn, cos[0], sin[0])
+        ops.rope_fused(kn, cos[0], sin[0])
+
+    out["C4 q/k RMSNorm + RoPE"] = timeit(qk_norm_rope)
+    a = torch.randn((1, HD), generator=gen).to(torch.float16)
+    out["C4 o_proj w8 GEMV 2048x2048"] = timeit(
+        lambda: ops.dequant_gemm_separate(a, L0.o_codes, L0.o_scale, g, out_dtype=torch.float16))
+    out["C4 lm_head w8 GEMV 50304x2048"] = timeit(
+        lambda: ops.dequant_gemm_separate(xn.reshape(1, -1), host.lm_codes, host.lm_scale, g, out_dtype=torch.float16))
+    for name, r in out.items():
+        log("cpu op %-52s p50 %10.1f us  p99 %10.1f us" % (name, r["cpu_us_p50"], r["cpu_us_p99"]))
+    return out
+
+
+def attach_gpu_op_times(ops_cpu: dict, kt: dict, cfg: dict) -> dict:
+    """The GPU microseconds (isolated, cold) of the kernels that compute each CPU operator."""
+    def kavg(*names):
+        try:
+            return sum(kt[n]["avg_us"] for n in names)
+        except KeyError:
+            return None
+
+    def cavg(prefix):
+        for k, v in cfg.items():
+            if k.startswith(prefix):
+                return v["avg_us"]
+        return None
+
+    qkv = [k for k in kt if k.startswith("gemv_w8 qkv")]
+    oproj = [k for k in kt if k.startswith("attn_merge_o_proj") or k.startswith("gemv_w8 o_proj")]
+    router = [k for k in kt if k.startswith("router_logits")]
+    lm = [k for k in kt if k.startswith("gemv_w8 lm_head")]
+    gpu = {
+        "C1": (kavg(*(router + ["moe_gate_up_w8_routed", "moe_down_w8"])),
+               "router logits + routed gate/up + down launches"),
+        "C2 split-KV fp16 attention ctx 1024": (cavg("attn_f16 ctx 1024"), "split + merge"),
+        "C2 split-KV fp16 attention ctx 4096": (cavg("attn_f16 ctx 4096"), "split + merge"),
+        "C3 KV-INT8 attention ctx 4096": (cavg("attn_i8 ctx 4096"), "split + merge"),
+        "C3 KV-INT8 attention ctx 16384": (cavg("attn_i8 ctx 16384"), "split + merge"),
+        "C4 RMSNorm 2048": (None, "fused into the qkv GEMV prologue"),
+        "C4 qkv w8 GEMV 6144x2048": (kavg(*qkv), "qkv GEMV with the input RMSNorm in its prologue"),
+        "C4 q/k RMSNorm + RoPE": (None, "fused into the attention launch"),
+        "C4 o_proj w8 GEMV 2048x2048": (kavg(*oproj), "o_proj GEMV (with the attention merge when fused)"),
+        "C4 lm_head w8 GEMV 50304x2048": (kavg(*lm), "lm_head GEMV + greedy argmax (2 launches)"),
+    }
+    for name, r in ops_cpu.items():
+        key = "C1" if name.startswith("C1") else name
+        us, what = gpu.get(key, (None, ""))
+        r["gpu_us"] = us
+        r["gpu_kernels"] = what
+    return ops_cpu
 
 
 # ---------------------------------------------------------------------------
@@ -673,29 +862,39 @@ def main(argv=None) -> int:
         check_tokens = [int(t) for t in sess.history[p0 + 1: p0 + 1 + check_n].tolist()]
     kt = kernel_table(torch, _hip, w, sess, flusher, args.kernel_reps)
     cfg = attention_configs(torch, _hip, flusher, args.kernel_reps)
-    cap = _Cap(sess.max_seq)
     del sess
     r2 = None
+    snap2 = None
     if args.ctx2:
         s2, r2 = time_decode(torch, w, args.ctx2, args.steps, args.warmup, 0)
+        if check_n:
+            snap2 = (s2.kv_cpu(), int(s2.token.item()), s2.position)
         del s2
     torch.cuda.synchronize()
 
     cpu = None
     if check_n:
-        cpu = cpu_baseline(torch, w, cap, check_tokens, check_logits, args.cpu_budget_s, check_n, snap)
+        host = w.to_host()
+        cpu = cpu_baseline(torch, host, snap, check_tokens, check_logits, warmup=args.cpu_warmup,
+                           timed=args.cpu_timed, timed_1t=args.cpu_timed_1t, snap2=snap2)
+        if not args.no_cpu_ops:
+            cpu["ops"] = attach_gpu_op_times(
+                cpu_ops_baseline(torch, host, warmup=args.cpu_warmup, timed=args.cpu_timed, seed=args.seed), kt, cfg)
+        del host
 
     dom_name = "moe_gate_up_w8_routed"
     dom = kt[dom_name]
     traffic = _traffic_from_profiles(dom_name)
     line = {
         "metric": METRIC,
-        "value": r1["ms_per_token"],
+        "value": r1["step_ms_p50"],
         "unit": "ms/token",
+        "stat": "p50 of per-step times (an event between replays), the reference's timing convention",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": r1["ms_per_token"],
+        "ms_per_step": r1["step_ms_p50"],
+        "ms_per_step_mean": r1["ms_per_token"],
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
@@ -897,13 +1096,6 @@ def _prefill_summary(*runs) -> dict:
             "reference_rtx5090_e2e_32_ms": REFERENCE_RTX5090_E2E32_MS.get(c),
         }
     return out
-
-
-class _Cap:
-    """Stand-in carrying the cache capacity the CPU oracle needs."""
-
-    def __init__(self, max_seq: int) -> None:
-        self.max_seq = max_seq
 
 
 def _traffic_from_profiles(kernel: str):

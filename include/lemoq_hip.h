@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define LEMOQ_ABI_VERSION 3
+#define LEMOQ_ABI_VERSION 4
 
 enum {
   LEMOQ_OK = 0,
@@ -39,6 +39,17 @@ enum {
   LEMOQ_ERR_UNSUPPORTED = -3, /* a valid request this build does not cover   */
   LEMOQ_ERR_ALIGN = -4        /* a pointer is not 16-byte aligned            */
 };
+
+/* Cross-workgroup synchronisation of the fused launches (lemoq_attn_layer_i8
+ * and the decode step that uses it).  The caller owns a workspace of
+ * LEMOQ_SYNC_WORDS uint32 words, 256-byte aligned and zero before the first
+ * launch (lemoq_sync_reset); every successful launch leaves it zero again.
+ * Word 0 is the status: a wait that gives up (its time limit expires, or
+ * another workgroup already failed) ORs LEMOQ_SYNC_TIMEOUT_BIT into it and its
+ * workgroup returns, so the launch always completes; its outputs are then
+ * invalid and the workspace must be reset before the next launch. */
+#define LEMOQ_SYNC_WORDS 8192
+#define LEMOQ_SYNC_TIMEOUT_BIT 1u
 
 /* Human-readable name of a status returned by any lemoq_* call. */
 const char* lemoq_status_string(int status);
@@ -311,6 +322,42 @@ int lemoq_router_logits_resid(const float* part, int64_t n_part, const uint16_t*
                               const uint16_t* router_w, int64_t E, uint16_t* h_out,
                               uint16_t* xn_out, uint16_t* logits, void* stream);
 
+/* A14/A16 + A8 + A3 — the attention half of one decoder layer as ONE launch
+ * (no single reference counterpart: it joins, per layer, the patched
+ * attention forward _decode_forward_impl, src/lemoq/kernels/attn_decode.py:
+ * 836-1017, its o_proj QuantLinear, src/lemoq/quant/linear.py:446-469, the
+ * residual add of the HF decoder layer, the post-attention rms_norm_fused,
+ * src/lemoq/kernels/rmsnorm.py:102-163, and the router F.linear of
+ * moe_static._route, src/lemoq/kernels/moe_static.py:262-283).  Computes what
+ * lemoq_attn_split_fused_i8, then lemoq_attn_merge_o_proj_w8, then
+ * lemoq_router_logits_resid compute, bit for bit, with the arguments of those
+ * three calls (m, l, acc and o_part are the intermediate workspaces):
+ * heads * num_splits workgroups hand results to each other inside the launch
+ * through `sync` (LEMOQ_SYNC_WORDS words, see above); `timeout_us` bounds
+ * each wait.  head_dim 128, heads % 4 == 0, hidden in {2048, 4096},
+ * heads * 128 / 512 in {1, 2, 4, 8}, num_splits <= 64,
+ * ceil(num_experts / 4) <= heads * num_splits, and every workgroup resident at
+ * once (lemoq_attn_layer_check).  Returns LEMOQ_ERR_UNSUPPORTED where the
+ * three calls must be used instead. */
+int lemoq_attn_layer_i8(const uint16_t* qkv, int64_t heads, int64_t head_dim,
+                        const uint16_t* q_norm_w, const uint16_t* k_norm_w, float eps,
+                        const uint16_t* cos_tab, const uint16_t* sin_tab, const int64_t* pos,
+                        int8_t* kc, uint16_t* ks, int8_t* vc, uint16_t* vs,
+                        int64_t code_head_stride, int64_t s_len, int64_t num_splits,
+                        float qk_scale, float* m, float* l, float* acc,
+                        const int8_t* o_codes, const uint16_t* o_scale, int64_t hidden,
+                        int64_t group, float* o_part, const uint16_t* h,
+                        const uint16_t* post_norm_w, const uint16_t* router_w,
+                        int64_t num_experts, uint16_t* h_out, uint16_t* xn_out,
+                        uint16_t* logits, uint32_t* sync, int64_t timeout_us, void* stream);
+/* LEMOQ_OK when lemoq_attn_layer_i8 covers the shape on the current device
+ * (shape rules and co-residency), else the status it would return. */
+int lemoq_attn_layer_check(int64_t heads, int64_t head_dim, int64_t num_splits, int64_t hidden,
+                           int64_t group, int64_t num_experts);
+/* Zero a sync workspace (LEMOQ_SYNC_WORDS words) with a fill kernel on `stream`
+ * (graph-safe: no memset node). */
+int lemoq_sync_reset(uint32_t* sync, void* stream);
+
 /* Router of one token, fused: xn = rmsnorm(h, norm_w) (written to xn_out),
  * logits = fp16(xn @ router_w^T) with fp32 accumulation (the F.linear of
  * moe_static._route, src/lemoq/kernels/moe_static.py:262-283), then the
@@ -450,6 +497,13 @@ typedef struct LemoqOlmoeStep {
    * runs lemoq_attn_merge, the o_proj GEMV and lemoq_router_logits. */
   float* o_part;                 /* (heads*D/512, H) o_proj partial sums */
   uint16_t* h_mid;               /* (H) residual after attention */
+  /* With `sync` non-NULL (LEMOQ_SYNC_WORDS words, zeroed beforehand) and the
+   * fused path's shapes covered by lemoq_attn_layer_check, each layer's
+   * attention half (split attention, merge + o_proj, residual + norm +
+   * router) is ONE launch, lemoq_attn_layer_i8, with waits bounded by
+   * sync_timeout_us; otherwise the launches above. */
+  uint32_t* sync;
+  int64_t sync_timeout_us;
 } LemoqOlmoeStep;
 
 int lemoq_olmoe_decode_step(const LemoqOlmoeStep* step, void* stream);

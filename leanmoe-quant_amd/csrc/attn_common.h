@@ -15,6 +15,7 @@
 #pragma once
 
 #include "common.h"
+#include "sync.h"
 
 namespace lemoq_attn {
 
@@ -183,8 +184,9 @@ __device__ __forceinline__ void fold_tokens(SoftmaxState<S::EPL>& st, const TokB
 // End of a split block: sum the token groups of each wave (the running max is
 // wave-uniform), merge the NW wave states through LDS in wave order, and
 // write the block's (m, l, acc[D]) partial; m = -inf for an empty split
-// (l = 0, acc = 0).  wm/wl hold NW floats, wacc NW * D.
-template <class S, int NW, int D>
+// (l = 0, acc = 0).  wm/wl hold NW floats, wacc NW * D.  COHERENT: the partial
+// is stored with coherent stores, for a consumer in the same launch (sync.h).
+template <class S, int NW, int D, bool COHERENT = false>
 __device__ __forceinline__ void finish_split(SoftmaxState<S::EPL>& st, float* wm, float* wl,
                                              float* wacc, int lane, int wave, int tl, int dl,
                                              int64_t pidx, float* __restrict__ m_out,
@@ -215,10 +217,10 @@ __device__ __forceinline__ void finish_split(SoftmaxState<S::EPL>& st, float* wm
         den += wl[w] * f;
       }
     }
-    acc_out[pidx * D + t] = num;
+    lemoq_sync::store_f32<COHERENT>(acc_out + pidx * D + t, num);
     if (t == 0) {
-      m_out[pidx] = M;
-      l_out[pidx] = den;
+      lemoq_sync::store_f32<COHERENT>(m_out + pidx, M);
+      lemoq_sync::store_f32<COHERENT>(l_out + pidx, den);
     }
   }
 }

@@ -2,7 +2,13 @@
 // canonical cell (w8a16 attention + experts, W8 lm_head, KV-INT8 cache) on a
 // stream, ready to be captured into a hipGraph by the caller.
 //
-// Per layer (6 launches):
+// Per layer, with a sync workspace and the shapes lemoq_attn_layer_check
+// covers (4 launches):
+//   1 gemv_w8_fused   input RMSNorm (+ embedding gather on layer 0) -> packed q|k|v
+//   2 attn_layer_i8   2-4 below as ONE launch whose workgroups hand results to
+//                     each other through the sync workspace (attn_layer.hip)
+//   3 moe_gate_up_w8, 4 moe_down_w8 as 5-6 below.
+// Otherwise (6 launches):
 //   1 gemv_w8_fused   input RMSNorm (+ embedding gather on layer 0) -> packed q|k|v
 //   2 attn_split_fused q_norm/k_norm, RoPE at *pos, KV-INT8 write of slot *pos,
 //                     split-KV partials over [0, *pos]
@@ -20,6 +26,10 @@
 // then final RMSNorm + lm_head GEMV with per-block argmax partials, and the
 // greedy selection that writes the next token and advances *pos / *filled.
 //
+// Every shape and buffer rule of every launch is checked before the first
+// launch is enqueued, so a rejected step leaves the cache and buffers as they
+// were.
+//
 // The layer order and rounding points restate the HF OLMoE decoder layer
 // (transformers OlmoeDecoderLayer/OlmoeModel, called by the reference through
 // StaticCacheDecodeSession, benchmarks/cudagraph.py:720-737) with the
@@ -33,26 +43,101 @@
     if (rc__) return rc__;    \
   } while (0)
 
-extern "C" int lemoq_olmoe_decode_step(const LemoqOlmoeStep* p, void* stream) {
+namespace {
+
+bool a16(const void* p) { return lemoq_aligned16(p); }
+
+bool overlaps(const void* x, int64_t nx, const void* y, int64_t ny) {
+  const char* p = static_cast<const char*>(x);
+  const char* q = static_cast<const char*>(y);
+  return p < q + ny && q < p + nx;
+}
+
+// A w8 GEMV launch of the step: its weights' shape rules (gemv.hip).
+int check_gemv(int64_t N, int64_t K, int64_t group) {
+  if (N <= 0 || K <= 0) return LEMOQ_ERR_SHAPE;
+  if (K > 8192 || K % 16 != 0 || K % group != 0) return LEMOQ_ERR_UNSUPPORTED;
+  if ((N + 7) / 8 > 0x7fffffffLL) return LEMOQ_ERR_SHAPE;
+  return LEMOQ_OK;
+}
+
+enum AttnPath { kAttnLayer, kAttnFusedOut, kAttnThree };
+
+// Every rule of every launch of the step, before anything is enqueued.
+int validate(const LemoqOlmoeStep* p, AttnPath* path) {
   if (!p || !p->layers) return LEMOQ_ERR_NULL;
   if (!p->embed || !p->final_norm || !p->lm_codes || !p->lm_scale || !p->cos_tab ||
       !p->sin_tab || !p->token || !p->pos || !p->filled || !p->h || !p->xn || !p->qkv ||
       !p->q_rot || !p->attn || !p->part_m || !p->part_l || !p->part_acc || !p->top_w ||
       !p->top_i || !p->act || !p->logits || !p->router_logits || !p->am_val || !p->am_idx)
     return LEMOQ_ERR_NULL;
-  const int64_t H = p->hidden, HD = p->heads * p->head_dim, D = p->head_dim;
-  if (H <= 0 || p->heads <= 0 || D <= 0 || p->num_layers <= 0 || p->max_seq <= 0 ||
-      p->num_splits <= 0 || p->vocab <= 0)
+  const int64_t H = p->hidden, D = p->head_dim, HD = p->heads * p->head_dim, E = p->num_experts;
+  const int64_t F = p->ffn, K = p->top_k, g = p->group, S = p->max_seq, ns = p->num_splits;
+  if (H <= 0 || p->heads <= 0 || D <= 0 || p->num_layers <= 0 || S <= 0 || ns <= 0 ||
+      p->vocab <= 0 || E <= 0 || F <= 0 || K <= 0)
     return LEMOQ_ERR_SHAPE;
-  const int64_t S = p->max_seq;
-  // Fused attention-output path: the shape rules of lemoq_attn_merge_o_proj_w8
-  // and lemoq_router_logits_resid, checked once so that a step never enqueues
-  // part of a layer before an argument is rejected.
+  if (g <= 0 || g % 16 != 0) return LEMOQ_ERR_UNSUPPORTED;
+  // qkv and lm_head GEMVs (K = H), o_proj (K = HD) on the unfused path
+  LEMOQ_TRY(check_gemv(3 * HD, H, g));
+  LEMOQ_TRY(check_gemv(p->vocab, H, g));
+  if (p->vocab > 0x7ffffffeLL) return LEMOQ_ERR_SHAPE;
+  if (p->am_len < lemoq_lm_head_argmax_parts(p->vocab)) return LEMOQ_ERR_SHAPE;
+  if (!a16(p->lm_codes)) return LEMOQ_ERR_ALIGN;
+  // split-KV attention (attn_fused.hip)
+  if (D != 64 && D != 128 && D != 256) return LEMOQ_ERR_UNSUPPORTED;
+  if (p->heads > 65535 || HD > 65536 || ns > 65535) return LEMOQ_ERR_SHAPE;
+  if (!a16(p->qkv)) return LEMOQ_ERR_ALIGN;
+  // routed gate/up and down (moe.hip)
+  if (K > 64 || K > E) return LEMOQ_ERR_SHAPE;
+  if (E > 256) return LEMOQ_ERR_UNSUPPORTED;
+  if (F > 8192 || F % 16 != 0 || F % g != 0) return LEMOQ_ERR_UNSUPPORTED;
+  if (E * 2 * F * H >= ((int64_t)1 << 40)) return LEMOQ_ERR_SHAPE;
+  if (!a16(p->xn) || !a16(p->act)) return LEMOQ_ERR_ALIGN;
+  for (int64_t L = 0; L < p->num_layers; ++L) {
+    const LemoqOlmoeLayer& w = p->layers[L];
+    if (!w.ln_in || !w.ln_post || !w.q_norm || !w.k_norm || !w.qkv_codes || !w.qkv_scale ||
+        !w.o_codes || !w.o_scale || !w.router || !w.gu_codes || !w.gu_scale || !w.dn_codes ||
+        !w.dn_scale || !w.kc || !w.ks || !w.vc || !w.vs)
+      return LEMOQ_ERR_NULL;
+    if (!a16(w.qkv_codes) || !a16(w.o_codes) || !a16(w.gu_codes) || !a16(w.dn_codes) || !a16(w.kc) ||
+        !a16(w.vc) || !a16(w.router) || !a16(w.ln_post))
+      return LEMOQ_ERR_ALIGN;
+  }
+  // the attention-output half: one fused launch, two launches, or three
   const int64_t n_part = HD / 512;
-  const bool fused_o = p->o_part && p->h_mid && D == 128 && p->heads % 4 == 0 &&
-                       p->num_splits <= 64 && (H == 2048 || H == 4096) &&
-                       (n_part == 1 || n_part == 2 || n_part == 4 || n_part == 8) &&
-                       p->group % 16 == 0 && HD % p->group == 0;
+  const bool fused_o = p->o_part && p->h_mid && D == 128 && p->heads % 4 == 0 && ns <= 64 &&
+                       (H == 2048 || H == 4096) &&
+                       (n_part == 1 || n_part == 2 || n_part == 4 || n_part == 8) && HD % g == 0 &&
+                       H % 32 == 0 && E <= 4 * 65535;
+  if (fused_o) {
+    if (!a16(p->o_part) || !a16(p->h_mid) || !a16(p->h)) return LEMOQ_ERR_ALIGN;
+    if (overlaps(p->h_mid, H * 2, p->h, H * 2) || overlaps(p->h_mid, H * 2, p->o_part, n_part * H * 4))
+      return LEMOQ_ERR_SHAPE;
+    *path = kAttnFusedOut;
+    if (p->sync) {
+      if (p->sync_timeout_us < 0) return LEMOQ_ERR_SHAPE;
+      if ((reinterpret_cast<uintptr_t>(p->sync) & 255u) != 0) return LEMOQ_ERR_ALIGN;
+      if (lemoq_attn_layer_check(p->heads, D, ns, H, g, E) == LEMOQ_OK) *path = kAttnLayer;
+    }
+  } else {
+    LEMOQ_TRY(check_gemv(H, HD, g));
+    if (ns > 1024 || D > 256) return LEMOQ_ERR_SHAPE;
+    if (H > 8192 || H % 16 != 0) return LEMOQ_ERR_UNSUPPORTED;
+    if (E > 65536) return LEMOQ_ERR_SHAPE;
+    if (!a16(p->attn)) return LEMOQ_ERR_ALIGN;
+    *path = kAttnThree;
+  }
+  return LEMOQ_OK;
+}
+
+}  // namespace
+
+extern "C" int lemoq_olmoe_decode_step(const LemoqOlmoeStep* p, void* stream) {
+  AttnPath path = kAttnThree;
+  LEMOQ_TRY(validate(p, &path));
+  const int64_t H = p->hidden, HD = p->heads * p->head_dim, D = p->head_dim;
+  const int64_t S = p->max_seq;
+  const int64_t n_part = HD / 512;
   for (int64_t L = 0; L < p->num_layers; ++L) {
     const LemoqOlmoeLayer& w = p->layers[L];
     const bool first = L == 0;
@@ -61,38 +146,49 @@ extern "C" int lemoq_olmoe_decode_step(const LemoqOlmoeStep* p, void* stream) {
     LEMOQ_TRY(lemoq_gemv_w8_fused(first ? p->embed : p->h, first ? p->token : nullptr, p->vocab,
                                   w.ln_in, p->eps, first ? p->h : nullptr, w.qkv_codes,
                                   w.qkv_scale, 3 * HD, H, p->group, nullptr, p->qkv, stream));
-    // 2. q/k norm, RoPE, KV-INT8 write at slot *pos, split-KV partials.
-    LEMOQ_TRY(lemoq_attn_split_fused_i8(p->qkv, p->heads, D, w.q_norm, w.k_norm, p->eps,
-                                        p->cos_tab, p->sin_tab, p->pos, w.kc, w.ks, w.vc, w.vs,
-                                        S * D, S, p->num_splits, p->qk_scale, p->part_m,
-                                        p->part_l, p->part_acc, stream));
-    if (fused_o) {
-      // 3. LSE merge + o_proj partials per group of 4 heads.
-      LEMOQ_TRY(lemoq_attn_merge_o_proj_w8(p->part_m, p->part_l, p->part_acc, p->heads,
-                                           p->num_splits, D, w.o_codes, w.o_scale, H, p->group,
-                                           p->o_part, stream));
-      // 4. h_mid = fp16(fp16(o) + h); post-attention RMSNorm + router logits.
-      LEMOQ_TRY(lemoq_router_logits_resid(p->o_part, n_part, p->h, w.ln_post, p->eps, H,
-                                          w.router, p->num_experts, p->h_mid, p->xn,
-                                          p->router_logits, stream));
+    if (path == kAttnLayer) {
+      // 2-4 as one launch: attention, merge + o_proj, residual + norm + router.
+      LEMOQ_TRY(lemoq_attn_layer_i8(p->qkv, p->heads, D, w.q_norm, w.k_norm, p->eps, p->cos_tab,
+                                    p->sin_tab, p->pos, w.kc, w.ks, w.vc, w.vs, S * D, S,
+                                    p->num_splits, p->qk_scale, p->part_m, p->part_l, p->part_acc,
+                                    w.o_codes, w.o_scale, H, p->group, p->o_part, p->h, w.ln_post,
+                                    w.router, p->num_experts, p->h_mid, p->xn, p->router_logits,
+                                    p->sync, p->sync_timeout_us, stream));
     } else {
-      // 3. LSE merge of the partials.
-      LEMOQ_TRY(lemoq_attn_merge(p->part_m, p->part_l, p->part_acc, p->heads, p->num_splits, D,
-                                 p->attn, stream));
-      // 4. o_proj; h = fp16(fp16(o) + h).
-      LEMOQ_TRY(lemoq_gemv_w8_fused(p->attn, nullptr, 0, nullptr, p->eps, nullptr, w.o_codes,
-                                    w.o_scale, H, HD, p->group, p->h, p->h, stream));
-      // 4b. post-attention RMSNorm + router logits.
-      LEMOQ_TRY(lemoq_router_logits(p->h, w.ln_post, p->eps, H, w.router, p->num_experts, p->xn,
-                                    p->router_logits, stream));
+      // 2. q/k norm, RoPE, KV-INT8 write at slot *pos, split-KV partials.
+      LEMOQ_TRY(lemoq_attn_split_fused_i8(p->qkv, p->heads, D, w.q_norm, w.k_norm, p->eps,
+                                          p->cos_tab, p->sin_tab, p->pos, w.kc, w.ks, w.vc, w.vs,
+                                          S * D, S, p->num_splits, p->qk_scale, p->part_m,
+                                          p->part_l, p->part_acc, stream));
+      if (path == kAttnFusedOut) {
+        // 3. LSE merge + o_proj partials per group of 4 heads.
+        LEMOQ_TRY(lemoq_attn_merge_o_proj_w8(p->part_m, p->part_l, p->part_acc, p->heads,
+                                             p->num_splits, D, w.o_codes, w.o_scale, H, p->group,
+                                             p->o_part, stream));
+        // 4. h_mid = fp16(fp16(o) + h); post-attention RMSNorm + router logits.
+        LEMOQ_TRY(lemoq_router_logits_resid(p->o_part, n_part, p->h, w.ln_post, p->eps, H,
+                                            w.router, p->num_experts, p->h_mid, p->xn,
+                                            p->router_logits, stream));
+      } else {
+        // 3. LSE merge of the partials.
+        LEMOQ_TRY(lemoq_attn_merge(p->part_m, p->part_l, p->part_acc, p->heads, p->num_splits, D,
+                                   p->attn, stream));
+        // 4. o_proj; h = fp16(fp16(o) + h).
+        LEMOQ_TRY(lemoq_gemv_w8_fused(p->attn, nullptr, 0, nullptr, p->eps, nullptr, w.o_codes,
+                                      w.o_scale, H, HD, p->group, p->h, p->h, stream));
+        // 4b. post-attention RMSNorm + router logits.
+        LEMOQ_TRY(lemoq_router_logits(p->h, w.ln_post, p->eps, H, w.router, p->num_experts, p->xn,
+                                      p->router_logits, stream));
+      }
     }
+    const bool resid_mid = path != kAttnThree;
     // 5-6. routing + grouped MoE; h = fp16(fp16(moe) + residual).
     LEMOQ_TRY(lemoq_moe_gate_up_w8_routed(p->xn, w.gu_codes, w.gu_scale, p->router_logits,
                                           p->top_k, (int)p->norm_topk_prob, p->num_experts,
                                           p->ffn, H, p->group, p->act, p->top_i, p->top_w,
                                           stream));
     LEMOQ_TRY(lemoq_moe_down_w8(p->act, w.dn_codes, w.dn_scale, p->top_i, p->top_w, p->top_k,
-                                p->num_experts, H, p->ffn, p->group, fused_o ? p->h_mid : p->h,
+                                p->num_experts, H, p->ffn, p->group, resid_mid ? p->h_mid : p->h,
                                 p->h, stream));
   }
   // Final norm + W8 lm_head with argmax partials, then greedy selection and step advance.

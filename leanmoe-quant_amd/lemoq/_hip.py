@@ -19,7 +19,10 @@ LIB_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib")
 LIB_NAME = "liblemoq_hip.so"
 LIB_PATH = os.path.join(LIB_DIR, LIB_NAME)
 
-ABI_VERSION = 3
+ABI_VERSION = 4
+# include/lemoq_hip.h: the fused launches' sync workspace and its status bit
+SYNC_WORDS = 8192
+SYNC_TIMEOUT_BIT = 1
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -104,6 +107,8 @@ class LemoqOlmoeStep(ctypes.Structure):
         ("am_len", _I64),
         ("o_part", _P),
         ("h_mid", _P),
+        ("sync", _P),
+        ("sync_timeout_us", _I64),
     ]
 
 
@@ -169,6 +174,15 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         [_P, _I64, _I64, _P, _P, _F, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _F, _P, _P, _P, _P],
     ),
 
+    "lemoq_attn_layer_i8": (
+        _I,
+        [
+            _P, _I64, _I64, _P, _P, _F, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _F, _P, _P, _P,
+            _P, _P, _I64, _I64, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _I64, _P,
+        ],
+    ),
+    "lemoq_attn_layer_check": (_I, [_I64, _I64, _I64, _I64, _I64, _I64]),
+    "lemoq_sync_reset": (_I, [_P, _P]),
     "lemoq_moe_gate_up_w8_routed": (
         _I,
         [_P, _P, _P, _P, _I64, _I, _I64, _I64, _I64, _I64, _P, _P, _P, _P],

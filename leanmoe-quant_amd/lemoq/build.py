@@ -48,21 +48,48 @@ def sources() -> list[str]:
     return sorted(glob.glob(os.path.join(CSRC, "*.hip")))
 
 
-def build_library(verbose: bool = False) -> str:
-    """Compile csrc/*.hip -> lemoq/_lib/liblemoq_hip.so; returns the path."""
+_NOISE = "is not a recognized feature for this target"
+
+
+def _run(cmd: list[str]) -> str:
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    err = "\n".join(line for line in proc.stderr.splitlines() if _NOISE not in line)
+    if proc.returncode != 0:
+        raise RuntimeError("hipcc failed (%d):\n%s\n%s" % (proc.returncode, " ".join(cmd), err))
+    return err
+
+
+def build_library(verbose: bool = False, jobs: int | None = None) -> str:
+    """Compile csrc/*.hip -> lemoq/_lib/liblemoq_hip.so; returns the path.
+
+    Each source compiles to an object in a scratch directory (in parallel, one
+    hipcc per source), then one hipcc links the shared library."""
+    import concurrent.futures
+    import shutil
+    import tempfile
+
     os.makedirs(LIB_DIR, exist_ok=True)
     tmp = LIB_PATH + ".tmp%d" % os.getpid()
-    cmd = [hipcc(), *HIPCC_FLAGS, "-I" + INCLUDE, "-I" + CSRC, *sources(), "-o", tmp]
-    proc = subprocess.run(cmd, capture_output=True, text=True)
-    noise = "is not a recognized feature for this target"
-    err = "\n".join(line for line in proc.stderr.splitlines() if noise not in line)
-    if proc.returncode != 0:
+    work = tempfile.mkdtemp(prefix="lemoq_build_")
+    compile_flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+    try:
+        srcs = sources()
+        objs = [os.path.join(work, os.path.basename(src) + ".o") for src in srcs]
+        cmds = [[hipcc(), *compile_flags, "-c", "-I" + INCLUDE, "-I" + CSRC, src, "-o", obj]
+                for src, obj in zip(srcs, objs)]
+        n = jobs or min(len(cmds), max(1, os.cpu_count() or 1))
+        with concurrent.futures.ThreadPoolExecutor(max_workers=n) as pool:
+            errs = list(pool.map(_run, cmds))
+        errs.append(_run([hipcc(), "--offload-arch=" + OFFLOAD_ARCH, "-shared", "-fPIC", *objs, "-o", tmp]))
+        if verbose:
+            text = "\n".join(e for e in errs if e.strip())
+            if text:
+                sys.stderr.write(text + "\n")
+        os.replace(tmp, LIB_PATH)
+    finally:
+        shutil.rmtree(work, ignore_errors=True)
         if os.path.exists(tmp):
             os.remove(tmp)
-        raise RuntimeError("hipcc failed (%d):\n%s\n%s" % (proc.returncode, " ".join(cmd), err))
-    if verbose and err.strip():
-        sys.stderr.write(err + "\n")
-    os.replace(tmp, LIB_PATH)
     return LIB_PATH
 
 

@@ -157,7 +157,14 @@ def quantize_state_dict(sd: Mapping[str, Any], shape: OlmoeShape, *, device: Any
             dn_scale=dn_s.reshape(s.num_experts, s.hidden, s.ffn // g),
         ))
     embed = check(_get(sd, "embed_tokens.weight"), (s.vocab, s.hidden), "embed_tokens")
-    lm = embed if tie_word_embeddings or "lm_head.weight" not in sd else sd["lm_head.weight"]
+    if tie_word_embeddings:
+        lm = embed
+    elif "lm_head.weight" in sd:
+        lm = check(sd["lm_head.weight"], (s.vocab, s.hidden), "lm_head")
+    else:
+        # an untied checkpoint without its lm_head would silently decode with the
+        # embedding as the output projection: refuse it instead
+        raise KeyError("lm_head.weight is missing and tie_word_embeddings is False")
     lm_c, lm_s = quant(lm, s.vocab, s.hidden, "lm_head")
     return OlmoeW8Weights(shape=s, embed=f16(embed), final_norm=f16(check(_get(sd, "norm.weight"), (s.hidden,), "norm")),
                           lm_codes=lm_c, lm_scale=lm_s, layers=layers)

@@ -47,6 +47,11 @@ LOG2E = 1.4426950408889634
 # with the split count (2.5 us at 8 splits, 2.9 at 16, 3.6 at 32).
 STEP_SLOTS_PER_SPLIT = 64
 STEP_MAX_SPLITS = 64
+# Time limit of each cross-workgroup wait inside the fused attention-layer
+# launch; a healthy wait takes microseconds.
+SYNC_TIMEOUT_US = 200_000
+# Whether the step runs each layer's attention half as one launch by default.
+ATTENTION_ONE_LAUNCH_DEFAULT = False
 
 
 def step_num_splits(max_seq: int, heads: int, compute_units: int = 256) -> int:
@@ -209,6 +214,7 @@ class DecodeSession:
         *,
         max_new_tokens: int,
         num_splits: int | None = None,
+        attention_one_launch: bool | None = None,
     ) -> None:
         from lemoq.kernels.attn_decode import resolve_num_splits  # noqa: PLC0415
         from lemoq.kernels.rope import rotary_cos_sin  # noqa: PLC0415
@@ -275,6 +281,12 @@ class DecodeSession:
         # does not cover, which run merge, o_proj and router as three launches)
         self.o_part = torch.zeros((max(1, HD // 512), s.hidden), dtype=torch.float32, device=dev)
         self.h_mid = torch.zeros((s.hidden,), **f16)
+        # Counters and status word of the fused attention-layer launch (its
+        # workgroups hand results to each other inside the launch); zero
+        # between launches.  256-byte aligned (one counter per line).
+        self.sync = torch.zeros((_hip.SYNC_WORDS,), dtype=torch.int32, device=dev)
+        if self.sync.data_ptr() % 256 != 0:
+            raise RuntimeError("sync workspace is not 256-byte aligned")
 
         P = _hip.ptr
         self._layer_structs = (_hip.LemoqOlmoeLayer * s.layers)()
@@ -309,9 +321,15 @@ class DecodeSession:
                      "h_mid"):
             setattr(st, name, P(getattr(self, name)))
         st.am_len = n_parts
+        # The attention half of each layer as one launch (lemoq_attn_layer_i8)
+        # where the shape allows it; None takes the measured default.
+        one = ATTENTION_ONE_LAUNCH_DEFAULT if attention_one_launch is None else bool(attention_one_launch)
+        st.sync = P(self.sync) if one else None
+        st.sync_timeout_us = SYNC_TIMEOUT_US
         self._step = st
         self.graph: Any = None
         self.stream: Any = None
+        self._host_pos = 0
         self.reset()
 
     # ------------------------------------------------------------------ state
@@ -322,7 +340,17 @@ class DecodeSession:
         self.filled.fill_(1)
         self.history.zero_()
         self.history[:1].copy_(self.prompt[:1])
+        self.sync.zero_()
+        self._host_pos = 0
         torch.cuda.synchronize(self.device)
+
+    def check_sync_status(self) -> None:
+        """Raise if a cross-workgroup wait of a fused launch gave up since the last
+        reset (the step's outputs are then invalid; ``reset()`` clears it)."""
+        st = int(self.sync[0].item())
+        if st != 0:
+            raise RuntimeError("a fused launch's cross-workgroup wait timed out (status 0x%x); "
+                               "the step's results are invalid, reset() the session" % st)
 
     def set_position(self, position: int, token: int | None = None) -> None:
         """Move the decode position (graph-safe: only device scalars change)."""
@@ -332,9 +360,13 @@ class DecodeSession:
         self.filled.fill_(int(position) + 1)
         if token is not None:
             self.token.fill_(int(token))
+        self._host_pos = int(position)
 
     @property
     def position(self) -> int:
+        """The device's decode position (synchronises); equals the host-side count
+        the capacity check uses, which every step enqueued through this session
+        advances."""
         return int(self.pos.item())
 
     # ------------------------------------------------------------------ steps
@@ -342,14 +374,29 @@ class DecodeSession:
         _hip.call("lemoq_olmoe_decode_step", ctypes.byref(self._step), _hip.stream_of(self.device))
 
     def _check_room(self, n: int) -> None:
-        if self.position + n > self.max_seq:
-            raise RuntimeError("decode position would exceed the cache capacity %d" % self.max_seq)
+        """Refuse, before anything is enqueued, a step that would run past the last
+        cache slot (the device would attend over nothing and keep advancing).  Uses
+        the host-side position, so it needs no device synchronisation."""
+        if n < 0 or self._host_pos + n > self.max_seq:
+            raise RuntimeError("decode position %d + %d steps would exceed the cache capacity %d"
+                               % (self._host_pos, n, self.max_seq))
 
     def decode_eager(self) -> Any:
         """One step without the graph; returns the step's fp16 logits (device)."""
         self._check_room(1)
         self._enqueue_step()
+        self._host_pos += 1
         return self.logits
+
+    @property
+    def attn_layer_fused(self) -> bool:
+        """Whether each layer's attention half runs as one launch (lemoq_attn_layer_i8)."""
+        s = self.shape
+        if not (self._step.sync and self.attn_output_fused):
+            return False
+        rc = _hip.load().lemoq_attn_layer_check(s.heads, s.head_dim, self.num_splits, s.hidden, s.group_size,
+                                                s.num_experts)
+        return int(rc) == 0
 
     @property
     def attn_output_fused(self) -> bool:
@@ -364,7 +411,8 @@ class DecodeSession:
     @property
     def launches_per_step(self) -> int:
         """Kernel launches in one captured step (see csrc/step.hip)."""
-        return (6 if self.attn_output_fused else 7) * self.shape.layers + 2
+        per_layer = 4 if self.attn_layer_fused else (6 if self.attn_output_fused else 7)
+        return per_layer * self.shape.layers + 2
 
     def capture(self) -> dict[str, Any]:
         """Capture one decode step into a hipGraph (state is untouched by the capture)."""
@@ -383,11 +431,14 @@ class DecodeSession:
         """Replay the captured step ``n`` times back to back; returns the last logits."""
         if self.graph is None:
             raise RuntimeError("capture() must succeed before replay()")
-        self._check_room(n) if synchronize else None
-        for _ in range(int(n)):
+        n = int(n)
+        self._check_room(n)
+        for _ in range(n):
             self.graph.replay()
+        self._host_pos += n
         if synchronize:
             torch.cuda.synchronize(self.device)
+            self.check_sync_status()
         return self.logits
 
     def prefill(self, mode: str = "batched") -> int:
@@ -404,7 +455,7 @@ class DecodeSession:
             self.capture()
         self.reset()
         if mode == "stepped":
-            self.replay(self.ctx)
+            self.replay(self.ctx)  # advances the host-side position to ctx
         elif mode == "batched":
             from lemoq.model.prefill import prefill_prompt  # noqa: PLC0415
 
@@ -416,6 +467,7 @@ class DecodeSession:
                       _hip.ptr(self.pos), _hip.ptr(self.filled), _hip.ptr(self.prompt), self.ctx,
                       _hip.ptr(self.history), int(self.history.numel()), _hip.stream_of(self.device))
             torch.cuda.synchronize(self.device)
+            self._host_pos = self.ctx
         else:
             raise ValueError("prefill mode must be 'batched' or 'stepped', got %r" % (mode,))
         return int(self.token.item())
@@ -427,6 +479,7 @@ class DecodeSession:
 
     def logits_cpu(self) -> Any:
         torch.cuda.synchronize(self.device)
+        self.check_sync_status()
         return self.logits.detach().to("cpu").clone()
 
     def kv_cpu(self) -> list[dict[str, Any]]:

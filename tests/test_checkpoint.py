@@ -197,3 +197,18 @@ def test_tied_embeddings_and_shape_errors(tmp_path):
     missing = {k: v for k, v in sd.items() if "layers.1.self_attn.o_proj" not in k}
     with pytest.raises(KeyError):
         ck.quantize_state_dict(missing, shape, device="cpu", quantizer=_rtn)
+
+
+def test_untied_checkpoint_without_lm_head_is_refused(saved):
+    """An untied checkpoint whose lm_head is missing must not fall back to the embedding."""
+    d, _, _ = saved
+    sd = ck.read_hf_state(d)
+    with open(os.path.join(d, "config.json")) as f:
+        shape = ck.shape_from_hf_config(json.load(f))
+    assert "lm_head.weight" in sd
+    no_lm = {k: v for k, v in sd.items() if k != "lm_head.weight"}
+    with pytest.raises(KeyError):
+        ck.quantize_state_dict(no_lm, shape, device="cpu", quantizer=_rtn, tie_word_embeddings=False)
+    tied = ck.quantize_state_dict(no_lm, shape, device="cpu", quantizer=_rtn, tie_word_embeddings=True)
+    c, _ = _rtn(sd["model.embed_tokens.weight"].float(), 128)
+    assert torch.equal(tied.lm_codes, c)

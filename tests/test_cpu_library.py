@@ -112,3 +112,68 @@ def test_argument_rejection_happens_before_any_launch():
     assert rr(fake, 4, 1 << 20, 2048, None) == -1
     with pytest.raises(ValueError):
         _hip.call("lemoq_gemv_w8", None, 1, 16, None, None, 16, 16, 16, None, 1, None)
+
+
+def _fake_step(**over):
+    """A LemoqOlmoeStep at the OLMoE shape whose pointers are aligned fakes (never
+    dereferenced: these cases are rejected before anything is launched)."""
+    from lemoq import _hip
+
+    layers = (_hip.LemoqOlmoeLayer * 2)()
+    addr = [1 << 24]
+
+    def nxt():
+        addr[0] += 1 << 16
+        return addr[0]
+
+    for L in layers:
+        for name, _ in _hip.LemoqOlmoeLayer._fields_:
+            setattr(L, name, nxt())
+    st = _hip.LemoqOlmoeStep()
+    shape = dict(hidden=2048, heads=16, head_dim=128, ffn=1024, num_experts=64, top_k=8, vocab=50304, group=128,
+                 num_layers=2, max_seq=1100, num_splits=16, norm_topk_prob=0)
+    for k, v in shape.items():
+        setattr(st, k, v)
+    st.eps, st.qk_scale = 1e-5, 0.1
+    st.layers = ctypes.cast(layers, ctypes.POINTER(_hip.LemoqOlmoeLayer))
+    for name, typ in _hip.LemoqOlmoeStep._fields_:
+        if typ is ctypes.c_void_p:
+            setattr(st, name, nxt())
+    st.prompt_len, st.history_len = 4, 1200
+    st.am_len = int(_hip.load().lemoq_lm_head_argmax_parts(50304))
+    st.sync = None
+    st.sync_timeout_us = 1000
+    for k, v in over.items():
+        setattr(st, k, v)
+    return st, layers
+
+
+def test_decode_step_rejects_before_any_launch():
+    """Every rule of every launch of the step is checked before the first launch
+    (so a rejected step leaves the KV cache and buffers untouched).  Each case
+    below would otherwise be rejected by a launch in the middle of the step
+    (the routed gate/up, the down projection, the lm_head argmax, the merge);
+    a negative status proves nothing was enqueued: on this GPU-less host a
+    launch attempt would return a positive HIP error instead."""
+    from lemoq import _hip
+
+    lib = _hip.load()
+    step = lambda **over: lib.lemoq_olmoe_decode_step(ctypes.byref(_fake_step(**over)[0]), None)  # noqa: E731
+    parts = int(lib.lemoq_lm_head_argmax_parts(50304))
+    assert step(am_len=parts - 1) == -2                    # lm_head argmax partials (last launch)
+    assert step(num_experts=300) == -3                      # routed gate/up: > 256 experts
+    assert step(top_k=65) == -2                             # gate/up / down: top_k > 64
+    assert step(ffn=1000) == -3                             # down: ffn % 16
+    assert step(group=8) == -3                              # every GEMV: group % 16
+    assert step(head_dim=96) == -3                          # attention: head_dim
+    assert step(act=(1 << 30) + 8) == -4                    # down: act alignment
+    st, layers = _fake_step()
+    layers[1].dn_codes = (1 << 30) + 4                      # layer 1's down codes misaligned
+    assert lib.lemoq_olmoe_decode_step(ctypes.byref(st), None) == -4
+    st, layers = _fake_step()
+    layers[1].router = None                                 # layer 1's router missing
+    assert lib.lemoq_olmoe_decode_step(ctypes.byref(st), None) == -1
+    assert step(sync=(1 << 30) + 64) == -4                  # the fused layer's sync workspace alignment
+    assert step(sync=1 << 30, sync_timeout_us=-1) == -2
+    # unfused attention-output path (no o_part): merge split bound
+    assert step(o_part=None, num_splits=2000) == -2
