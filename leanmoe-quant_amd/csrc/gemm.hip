@@ -210,7 +210,9 @@ extern "C" int lemoq_gemm_f16_splitk(const uint16_t* x, int64_t M, int64_t K, in
   if ((!y && splits == 1) || !w) return LEMOQ_ERR_NULL;
   if (splits < 1 || splits > 64) return LEMOQ_ERR_SHAPE;
   a.splits = (int)splits;
-  a.part = workspace;
+  // one split is lemoq_gemm_f16: the workspace is not used (a non-null part
+  // would make the kernel write partials instead of y)
+  a.part = splits > 1 ? workspace : nullptr;
   if (splits > 1 && !lemoq_aligned16(workspace)) return workspace ? LEMOQ_ERR_ALIGN : LEMOQ_ERR_NULL;
   const int rc = check_gemm(a);
   if (rc != LEMOQ_OK) return rc;

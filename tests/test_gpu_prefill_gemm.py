@@ -142,6 +142,27 @@ def test_quant_linear_dispatch(dev):
                                                                   group_size=128))
 
 
+def test_gemm_f16_splitk_one_split_ignores_the_workspace(dev):
+    """splits == 1 is lemoq_gemm_f16: a workspace passed anyway must stay unused and y must be written."""
+    from lemoq import _hip
+
+    print("case: gemm_f16 split-K with one split and a workspace", flush=True)
+    m, n, k = 5, 64, 512
+    w = randn(n, k, seed=77, std=0.05).to(torch.float16)
+    x = randn(m, k, seed=78).to(torch.float16)
+    ws = torch.full((1, m, n), float("nan"), dtype=torch.float32, device=dev)
+    y = torch.full((m, n), float("nan"), dtype=torch.float16, device=dev)
+    y1 = torch.full((m, n), float("nan"), dtype=torch.float16, device=dev)
+    xd, wd = x.to(dev), w.to(dev)
+    P, st = _hip.ptr, _hip.stream_of(dev)
+    _hip.call("lemoq_gemm_f16_splitk", P(xd), m, k, k, P(wd), n, P(y), n, 1, P(ws), st)
+    _hip.call("lemoq_gemm_f16", P(xd), m, k, k, P(wd), n, P(y1), n, st)
+    torch.cuda.synchronize()
+    assert torch.isnan(ws).all()
+    assert torch.equal(y.cpu().view(torch.int16), y1.cpu().view(torch.int16))
+    _assert_linear(y, ops.linear_f16(x, w), x.double().abs() @ w.double().abs().t(), "gemm_f16 split 1")
+
+
 @pytest.mark.parametrize("m,n,k,splits,top_k,norm", [(1000, 64, 2048, 8, 8, False), (37, 64, 2048, 4, 8, True),
                                                      (1, 16, 256, 2, 4, False), (300, 128, 4096, 8, 8, True)])
 def test_route_topk_of_splitk_partials(m, n, k, splits, top_k, norm, dev):
