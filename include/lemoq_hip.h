@@ -17,7 +17,9 @@
  *   - Return value: 0 on success; a negative LEMOQ_ERR_* code when the
  *     arguments are rejected before anything is launched; a positive value is
  *     the hipError_t reported by the launch.  lemoq_status_string() names it.
- *   - All entry points are stateless and reentrant.
+ *   - All entry points are stateless and reentrant, except
+ *     lemoq_gemm_f16_splitk_noalloc, whose calls on one device share a fixed
+ *     library-owned array (see its declaration).
  *
  * Reference interfaces replaced are cited as path:line into LeanMoE-Quant.
  */
@@ -37,7 +39,8 @@ enum {
   LEMOQ_ERR_NULL = -1,        /* a required pointer is NULL                  */
   LEMOQ_ERR_SHAPE = -2,       /* a size is out of range or inconsistent      */
   LEMOQ_ERR_UNSUPPORTED = -3, /* a valid request this build does not cover   */
-  LEMOQ_ERR_ALIGN = -4        /* a pointer is not 16-byte aligned            */
+  LEMOQ_ERR_ALIGN = -4,       /* a pointer is not 16-byte aligned            */
+  LEMOQ_ERR_CAPACITY = -5     /* larger than a fixed capacity of the library */
 };
 
 /* Cross-workgroup synchronisation of the fused launches (lemoq_attn_layer_i8
@@ -543,6 +546,21 @@ int lemoq_gemm_f16(const uint16_t* x, int64_t M, int64_t K, int64_t x_ld, const 
 int lemoq_gemm_f16_splitk(const uint16_t* x, int64_t M, int64_t K, int64_t x_ld, const uint16_t* w,
                           int64_t N, uint16_t* y, int64_t y_ld, int64_t splits, float* workspace,
                           void* stream);
+
+/* lemoq_gemm_f16_splitk for callers that cannot allocate (code under hipGraph
+ * capture, serving loops, harnesses that forbid hipMalloc): no reference
+ * counterpart.  The split partials go to a fixed device array of
+ * LEMOQ_SPLITK_SCRATCH_FLOATS floats (16 MiB) that the library holds on each
+ * device it runs on until the process ends; the call itself allocates
+ * nothing.  Requires y (the partials cannot be left for the caller) and
+ * splits * M * N <= LEMOQ_SPLITK_SCRATCH_FLOATS when splits > 1, else returns
+ * LEMOQ_ERR_CAPACITY before launching.  All calls on one device share the
+ * array: calls that overlap in time on one device (other streams, other
+ * threads) race and must be serialised by the caller.  Same results as
+ * lemoq_gemm_f16_splitk bit for bit. */
+#define LEMOQ_SPLITK_SCRATCH_FLOATS (4 << 20)
+int lemoq_gemm_f16_splitk_noalloc(const uint16_t* x, int64_t M, int64_t K, int64_t x_ld, const uint16_t* w,
+                                  int64_t N, uint16_t* y, int64_t y_ld, int64_t splits, void* stream);
 
 /* Embedding lookup of several tokens (HF embed_tokens on the prompt):
  * dst[r] = src[ids[r]] for r < rows, a zero row for an id outside

@@ -18,6 +18,8 @@
 // columns beyond M/N are clamped on load and not stored.
 #include "gemm_core.h"
 
+#include <mutex>
+
 namespace {
 
 using namespace lemoq_gemm;
@@ -194,6 +196,66 @@ extern "C" int lemoq_gemm_f16(const uint16_t* x, int64_t M, int64_t K, int64_t x
   a.resid = nullptr; a.resid_ld = 0;
   a.splits = 1; a.part = nullptr;
   if (!y || !w) return LEMOQ_ERR_NULL;
+  const int rc = check_gemm(a);
+  if (rc != LEMOQ_OK) return rc;
+  return launch_gemm(a, lemoq_stream(stream));
+}
+
+// ---------------------------------------------------------------------------
+// lemoq_gemm_f16_splitk_noalloc: the same launches with the split partials in
+// a fixed device array instead of a caller workspace, so the call allocates
+// nothing.  The array's host-side name is not a device address: its address
+// on each device comes from hipGetSymbolAddress, taken once per device (with
+// that device current) on the first call there, and only that pointer is
+// handed to the kernels.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) float scratch[LEMOQ_SPLITK_SCRATCH_FLOATS];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+float* g_scratch_ptr[kMaxDevices] = {};
+
+// This device's copy of `scratch` (looked up once per device).
+int scratch_ptr(float** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxDevices) return LEMOQ_ERR_UNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    if (!p) return LEMOQ_ERR_NULL;
+    g_scratch_ptr[dev] = static_cast<float*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return LEMOQ_OK;
+}
+
+}  // namespace
+
+extern "C" int lemoq_gemm_f16_splitk_noalloc(const uint16_t* x, int64_t M, int64_t K, int64_t x_ld,
+                                             const uint16_t* w, int64_t N, uint16_t* y, int64_t y_ld,
+                                             int64_t splits, void* stream) {
+  GemmArgs a{};
+  a.x = x; a.x_ld = x_ld; a.x_rows = nullptr; a.M = M; a.N = N; a.K = K;
+  a.codes = nullptr; a.scale = nullptr; a.w16 = w; a.group = 0;
+  a.y16 = y; a.y_ld = y_ld;
+  a.resid = nullptr; a.resid_ld = 0;
+  // y is required: the partials stay in the library's array, which the caller cannot read
+  if (!y || !w) return LEMOQ_ERR_NULL;
+  if (splits < 1 || splits > 64) return LEMOQ_ERR_SHAPE;
+  if (M <= 0 || N <= 0 || M > (1LL << 24) || N > (1LL << 24)) return LEMOQ_ERR_SHAPE;
+  if (splits > 1 && M * N > LEMOQ_SPLITK_SCRATCH_FLOATS / splits) return LEMOQ_ERR_CAPACITY;
+  a.splits = (int)splits;
+  a.part = nullptr;
+  if (splits > 1) {
+    const int rc = scratch_ptr(&a.part);
+    if (rc != LEMOQ_OK) return rc;
+  }
   const int rc = check_gemm(a);
   if (rc != LEMOQ_OK) return rc;
   return launch_gemm(a, lemoq_stream(stream));

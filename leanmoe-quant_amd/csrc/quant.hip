@@ -180,6 +180,7 @@ extern "C" const char* lemoq_status_string(int status) {
     case LEMOQ_ERR_SHAPE: return "a size is out of range or inconsistent";
     case LEMOQ_ERR_UNSUPPORTED: return "the request is not supported by this build";
     case LEMOQ_ERR_ALIGN: return "a pointer is not 16-byte aligned";
+    case LEMOQ_ERR_CAPACITY: return "the request exceeds a fixed capacity of the library";
     default: break;
   }
   if (status > 0) return hipGetErrorString((hipError_t)status);

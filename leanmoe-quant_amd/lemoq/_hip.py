@@ -190,6 +190,7 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "lemoq_gemm_w8": (_I, [_P, _I64, _I64, _I64, _P, _P, _P, _I64, _I64, _P, _I64, _P, _I64, _P]),
     "lemoq_gemm_f16": (_I, [_P, _I64, _I64, _I64, _P, _I64, _P, _I64, _P]),
     "lemoq_gemm_f16_splitk": (_I, [_P, _I64, _I64, _I64, _P, _I64, _P, _I64, _I64, _P, _P]),
+    "lemoq_gemm_f16_splitk_noalloc": (_I, [_P, _I64, _I64, _I64, _P, _I64, _P, _I64, _I64, _P]),
     "lemoq_gather_rows": (_I, [_P, _I64, _I64, _P, _I64, _P, _P]),
     "lemoq_qk_norm_rope_kv_i8_rows": (
         _I,
