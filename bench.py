@@ -88,6 +88,8 @@ def parse_args(argv=None):
     ap.add_argument("--no-cpu-ops", action="store_true", help="skip the per-operator CPU timings (C1-C4)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--mode", choices=("full", "kernels", "traffic", "prefill", "step"), default="full")
+    ap.add_argument("--one-launch", choices=("default", "none", "attn", "moe", "both"), default="default",
+                    help="run each layer's attention half and/or MoE as one launch (default: the session's default)")
     ap.add_argument("--summarize-pmc", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "PLAN_JSON"))
     ap.add_argument("--summarize-prefill", metavar="KERNEL_TRACE_CSV",
                     help="per-kernel table of the prefills in a rocprofv3 kernel trace of --mode prefill at --ctx")
@@ -320,10 +322,10 @@ def measure_prefill(torch, sess, warmup: int = 2, timed: int = 7) -> dict:
     return {"p50": samples[len(samples) // 2], "min": samples[0], "max": samples[-1], "runs": timed}
 
 
-def time_decode(torch, w, ctx: int, steps: int, warmup: int, extra: int):
+def time_decode(torch, w, ctx: int, steps: int, warmup: int, extra: int, one_launch: dict | None = None):
     from lemoq.model.olmoe import DecodeSession
 
-    sess = DecodeSession(w, [1] * ctx, max_new_tokens=warmup + 2 * steps + extra + 4)
+    sess = DecodeSession(w, [1] * ctx, max_new_tokens=warmup + 2 * steps + extra + 4, **(one_launch or {}))
     sess.capture()
     ttft = measure_prefill(torch, sess)
     log("ctx %d: batched prefill (TTFT) p50 %.3f ms over %d runs" % (ctx, ttft["p50"], ttft["runs"]))
@@ -764,6 +766,14 @@ def summarize_pmc(fetch_csv: str, write_csv: str, plan_json: str, out_dir: str) 
     return {"table": "\n".join(lines), "data": out}
 
 
+def _one_launch(args) -> dict:
+    """DecodeSession keyword arguments for --one-launch."""
+    if args.one_launch == "default":
+        return {}
+    return {"attention_one_launch": args.one_launch in ("attn", "both"),
+            "moe_one_launch": args.one_launch in ("moe", "both")}
+
+
 def main(argv=None) -> int:
     args = parse_args(argv)
     if args.summarize_pmc:
@@ -814,7 +824,7 @@ def main(argv=None) -> int:
     if args.mode == "step":
         from lemoq.model.olmoe import DecodeSession
 
-        sess = DecodeSession(w, [1] * args.ctx, max_new_tokens=args.warmup + args.steps + 1)
+        sess = DecodeSession(w, [1] * args.ctx, max_new_tokens=args.warmup + args.steps + 1, **_one_launch(args))
         sess.capture()
         sess.prefill()
         sess.replay(args.warmup)
@@ -822,7 +832,8 @@ def main(argv=None) -> int:
         sess.replay(args.steps)
         ms = (time.perf_counter() - t0) * 1e3 / args.steps
         log("ctx %d: %d replays, %.4f ms/token" % (args.ctx, args.steps, ms))
-        print(json.dumps({"mode": "step", "ctx": args.ctx, "steps": args.steps, "ms_per_token": ms}))
+        print(json.dumps({"mode": "step", "ctx": args.ctx, "steps": args.steps, "ms_per_token": ms,
+                          "one_launch": args.one_launch, "launches_per_step": sess.launches_per_step}))
         return 0
 
     if args.mode == "prefill":
@@ -849,7 +860,7 @@ def main(argv=None) -> int:
         return 0
 
     check_n = 0 if args.no_cpu else max(1, args.cpu_check_steps)
-    sess, r1 = time_decode(torch, w, args.ctx, args.steps, args.warmup, check_n)
+    sess, r1 = time_decode(torch, w, args.ctx, args.steps, args.warmup, check_n, _one_launch(args))
     snap = None
     check_tokens: list[int] = []
     check_logits = []
@@ -866,7 +877,7 @@ def main(argv=None) -> int:
     r2 = None
     snap2 = None
     if args.ctx2:
-        s2, r2 = time_decode(torch, w, args.ctx2, args.steps, args.warmup, 0)
+        s2, r2 = time_decode(torch, w, args.ctx2, args.steps, args.warmup, 0, _one_launch(args))
         if check_n:
             snap2 = (s2.kv_cpu(), int(s2.token.item()), s2.position)
         del s2

@@ -51,7 +51,7 @@ enum {
  * another workgroup already failed) ORs LEMOQ_SYNC_TIMEOUT_BIT into it and its
  * workgroup returns, so the launch always completes; its outputs are then
  * invalid and the workspace must be reset before the next launch. */
-#define LEMOQ_SYNC_WORDS 8192
+#define LEMOQ_SYNC_WORDS 16384
 #define LEMOQ_SYNC_TIMEOUT_BIT 1u
 
 /* Human-readable name of a status returned by any lemoq_* call. */
@@ -357,6 +357,30 @@ int lemoq_attn_layer_i8(const uint16_t* qkv, int64_t heads, int64_t head_dim,
  * (shape rules and co-residency), else the status it would return. */
 int lemoq_attn_layer_check(int64_t heads, int64_t head_dim, int64_t num_splits, int64_t hidden,
                            int64_t group, int64_t num_experts);
+/* A4 + A5 + A6 — the grouped MoE of one decoder layer as ONE launch (no
+ * single reference counterpart: it joins _gate_up_act_kernel_q and
+ * _down_sum_kernel_q of grouped_moe_forward_quant, src/lemoq/kernels/
+ * _grouped_triton.py:249-398, with the routing of moe_static._route,
+ * src/lemoq/kernels/moe_static.py:262-283, and the residual add of the HF
+ * decoder layer).  Computes what lemoq_moe_gate_up_w8_routed followed by
+ * lemoq_moe_down_w8 (with `residual`) compute, bit for bit: act (top_k, F)
+ * fp16 and ypart (top_k, H) fp32 are its intermediate workspaces, top_i /
+ * top_w receive the routing.  top_k * 32 workgroups hand results to each
+ * other through `sync` (LEMOQ_SYNC_WORDS words, see above; this launch uses
+ * lines 64 and up, lemoq_attn_layer_i8 lines below 64); `timeout_us` bounds
+ * each wait.  This build covers hidden 2048, ffn 1024, E <= 64, top_k <= 16,
+ * with every workgroup resident at once (lemoq_moe_layer_check); otherwise it
+ * returns LEMOQ_ERR_UNSUPPORTED and the two launches must be used. */
+int lemoq_moe_layer_w8(const uint16_t* x, const int8_t* gu_codes, const uint16_t* gu_scale,
+                       const int8_t* dn_codes, const uint16_t* dn_scale,
+                       const uint16_t* router_logits, int64_t top_k, int norm_topk_prob,
+                       int64_t num_experts, int64_t ffn, int64_t hidden, int64_t group,
+                       uint16_t* act, float* ypart, const uint16_t* residual, uint16_t* out,
+                       int64_t* top_i, uint16_t* top_w, uint32_t* sync, int64_t timeout_us,
+                       void* stream);
+/* LEMOQ_OK when lemoq_moe_layer_w8 covers the shape on the current device. */
+int lemoq_moe_layer_check(int64_t top_k, int64_t num_experts, int64_t ffn, int64_t hidden,
+                          int64_t group);
 /* Zero a sync workspace (LEMOQ_SYNC_WORDS words) with a fill kernel on `stream`
  * (graph-safe: no memset node). */
 int lemoq_sync_reset(uint32_t* sync, void* stream);
@@ -500,13 +524,15 @@ typedef struct LemoqOlmoeStep {
    * runs lemoq_attn_merge, the o_proj GEMV and lemoq_router_logits. */
   float* o_part;                 /* (heads*D/512, H) o_proj partial sums */
   uint16_t* h_mid;               /* (H) residual after attention */
-  /* With `sync` non-NULL (LEMOQ_SYNC_WORDS words, zeroed beforehand) and the
-   * fused path's shapes covered by lemoq_attn_layer_check, each layer's
-   * attention half (split attention, merge + o_proj, residual + norm +
-   * router) is ONE launch, lemoq_attn_layer_i8, with waits bounded by
-   * sync_timeout_us; otherwise the launches above. */
+  /* Workspace of the one-launch paths (LEMOQ_SYNC_WORDS words, zeroed
+   * beforehand; see one_launch) and the time limit of their waits. */
   uint32_t* sync;
   int64_t sync_timeout_us;
+  /* With `sync` non-NULL: bit 0 runs each layer's attention half as one launch
+   * (lemoq_attn_layer_i8), bit 1 its MoE as one launch (lemoq_moe_layer_w8,
+   * which also needs moe_part), each where its check covers the shape. */
+  int64_t one_launch;
+  float* moe_part;               /* (top_k, H) fp32 MoE partials */
 } LemoqOlmoeStep;
 
 int lemoq_olmoe_decode_step(const LemoqOlmoeStep* step, void* stream);

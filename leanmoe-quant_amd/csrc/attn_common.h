@@ -152,14 +152,18 @@ __device__ __forceinline__ void fold_tokens(SoftmaxState<S::EPL>& st, const TokB
   for (int u = 1; u < S::U; ++u) mx = fmaxf(mx, sc[u]);
   mx = wave_max(mx);
   const float m_new = fmaxf(st.m, mx);
-  if (m_new == -INFINITY) return;  // no valid token in this block (wave-uniform)
-  const float alpha = exp2f(st.m - m_new);
+  // No valid token so far (m_new == -inf, wave-uniform): fold against 0
+  // instead, which keeps the state at (m = -inf, l = 0, acc = 0) -- what an
+  // early return would keep -- without a branch (at the join of a branch the
+  // compiler waits for every load in flight, the token blocks ahead included).
+  const float m_ref = m_new == -INFINITY ? 0.0f : m_new;
+  const float alpha = exp2f(st.m - m_ref);
   st.l *= alpha;
 #pragma unroll
   for (int e = 0; e < S::EPL; ++e) st.acc[e] *= alpha;
 #pragma unroll
   for (int u = 0; u < S::U; ++u) {
-    const float p = exp2f(sc[u] - m_new);  // 0 for masked loads (sc = -inf)
+    const float p = exp2f(sc[u] - m_ref);  // 0 for masked loads (sc = -inf)
     st.l += p;
     const uint32_t w[4] = {b.v[u].x, b.v[u].y, b.v[u].z, b.v[u].w};
     if constexpr (S::INT8) {

@@ -208,7 +208,8 @@ extern "C" int lemoq_attn_layer_check(int64_t heads, int64_t head_dim, int64_t n
     return LEMOQ_ERR_SHAPE;
   const int64_t G = heads * num_splits;
   if (num_experts <= 0 || (num_experts + 3) / 4 > G) return LEMOQ_ERR_SHAPE;
-  if (1 + heads + kTileLines + 1 > LEMOQ_SYNC_WORDS / lemoq_sync::kLineWords) return LEMOQ_ERR_SHAPE;
+  // lines 1 .. heads + 17; lemoq_moe_layer_w8 uses lines 64 and up
+  if (1 + heads + kTileLines + 1 > 64) return LEMOQ_ERR_SHAPE;
   // every workgroup resident at once
   int device = 0;
   if (hipGetDevice(&device) != hipSuccess) return LEMOQ_ERR_UNSUPPORTED;

@@ -2,12 +2,13 @@
 // canonical cell (w8a16 attention + experts, W8 lm_head, KV-INT8 cache) on a
 // stream, ready to be captured into a hipGraph by the caller.
 //
-// Per layer, with a sync workspace and the shapes lemoq_attn_layer_check
-// covers (4 launches):
+// Per layer, with a sync workspace, one_launch bit 0 and the shapes
+// lemoq_attn_layer_check covers (4 launches):
 //   1 gemv_w8_fused   input RMSNorm (+ embedding gather on layer 0) -> packed q|k|v
 //   2 attn_layer_i8   2-4 below as ONE launch whose workgroups hand results to
 //                     each other through the sync workspace (attn_layer.hip)
 //   3 moe_gate_up_w8, 4 moe_down_w8 as 5-6 below.
+// With one_launch bit 1, 5-6 run as ONE launch too (moe_layer_w8).
 // Otherwise (6 launches):
 //   1 gemv_w8_fused   input RMSNorm (+ embedding gather on layer 0) -> packed q|k|v
 //   2 attn_split_fused q_norm/k_norm, RoPE at *pos, KV-INT8 write of slot *pos,
@@ -64,7 +65,7 @@ int check_gemv(int64_t N, int64_t K, int64_t group) {
 enum AttnPath { kAttnLayer, kAttnFusedOut, kAttnThree };
 
 // Every rule of every launch of the step, before anything is enqueued.
-int validate(const LemoqOlmoeStep* p, AttnPath* path) {
+int validate(const LemoqOlmoeStep* p, AttnPath* path, bool* moe_one) {
   if (!p || !p->layers) return LEMOQ_ERR_NULL;
   if (!p->embed || !p->final_norm || !p->lm_codes || !p->lm_scale || !p->cos_tab ||
       !p->sin_tab || !p->token || !p->pos || !p->filled || !p->h || !p->xn || !p->qkv ||
@@ -114,11 +115,9 @@ int validate(const LemoqOlmoeStep* p, AttnPath* path) {
     if (overlaps(p->h_mid, H * 2, p->h, H * 2) || overlaps(p->h_mid, H * 2, p->o_part, n_part * H * 4))
       return LEMOQ_ERR_SHAPE;
     *path = kAttnFusedOut;
-    if (p->sync) {
-      if (p->sync_timeout_us < 0) return LEMOQ_ERR_SHAPE;
-      if ((reinterpret_cast<uintptr_t>(p->sync) & 255u) != 0) return LEMOQ_ERR_ALIGN;
-      if (lemoq_attn_layer_check(p->heads, D, ns, H, g, E) == LEMOQ_OK) *path = kAttnLayer;
-    }
+    if (p->sync && (p->one_launch & 1) &&
+        lemoq_attn_layer_check(p->heads, D, ns, H, g, E) == LEMOQ_OK)
+      *path = kAttnLayer;
   } else {
     LEMOQ_TRY(check_gemv(H, HD, g));
     if (ns > 1024 || D > 256) return LEMOQ_ERR_SHAPE;
@@ -127,6 +126,14 @@ int validate(const LemoqOlmoeStep* p, AttnPath* path) {
     if (!a16(p->attn)) return LEMOQ_ERR_ALIGN;
     *path = kAttnThree;
   }
+  if (p->sync) {
+    if (p->sync_timeout_us < 0) return LEMOQ_ERR_SHAPE;
+    if ((reinterpret_cast<uintptr_t>(p->sync) & 255u) != 0) return LEMOQ_ERR_ALIGN;
+  }
+  // the MoE as one launch (moe_layer.hip)
+  *moe_one = p->sync && (p->one_launch & 2) && p->moe_part &&
+             lemoq_moe_layer_check(K, E, F, H, g) == LEMOQ_OK;
+  if (*moe_one && !a16(p->moe_part)) return LEMOQ_ERR_ALIGN;
   return LEMOQ_OK;
 }
 
@@ -134,7 +141,8 @@ int validate(const LemoqOlmoeStep* p, AttnPath* path) {
 
 extern "C" int lemoq_olmoe_decode_step(const LemoqOlmoeStep* p, void* stream) {
   AttnPath path = kAttnThree;
-  LEMOQ_TRY(validate(p, &path));
+  bool moe_one = false;
+  LEMOQ_TRY(validate(p, &path, &moe_one));
   const int64_t H = p->hidden, HD = p->heads * p->head_dim, D = p->head_dim;
   const int64_t S = p->max_seq;
   const int64_t n_part = HD / 512;
@@ -181,15 +189,21 @@ extern "C" int lemoq_olmoe_decode_step(const LemoqOlmoeStep* p, void* stream) {
                                       p->router_logits, stream));
       }
     }
-    const bool resid_mid = path != kAttnThree;
+    const uint16_t* resid = path != kAttnThree ? p->h_mid : p->h;
     // 5-6. routing + grouped MoE; h = fp16(fp16(moe) + residual).
-    LEMOQ_TRY(lemoq_moe_gate_up_w8_routed(p->xn, w.gu_codes, w.gu_scale, p->router_logits,
-                                          p->top_k, (int)p->norm_topk_prob, p->num_experts,
-                                          p->ffn, H, p->group, p->act, p->top_i, p->top_w,
-                                          stream));
-    LEMOQ_TRY(lemoq_moe_down_w8(p->act, w.dn_codes, w.dn_scale, p->top_i, p->top_w, p->top_k,
-                                p->num_experts, H, p->ffn, p->group, resid_mid ? p->h_mid : p->h,
-                                p->h, stream));
+    if (moe_one) {
+      LEMOQ_TRY(lemoq_moe_layer_w8(p->xn, w.gu_codes, w.gu_scale, w.dn_codes, w.dn_scale,
+                                   p->router_logits, p->top_k, (int)p->norm_topk_prob,
+                                   p->num_experts, p->ffn, H, p->group, p->act, p->moe_part, resid,
+                                   p->h, p->top_i, p->top_w, p->sync, p->sync_timeout_us, stream));
+    } else {
+      LEMOQ_TRY(lemoq_moe_gate_up_w8_routed(p->xn, w.gu_codes, w.gu_scale, p->router_logits,
+                                            p->top_k, (int)p->norm_topk_prob, p->num_experts,
+                                            p->ffn, H, p->group, p->act, p->top_i, p->top_w,
+                                            stream));
+      LEMOQ_TRY(lemoq_moe_down_w8(p->act, w.dn_codes, w.dn_scale, p->top_i, p->top_w, p->top_k,
+                                  p->num_experts, H, p->ffn, p->group, resid, p->h, stream));
+    }
   }
   // Final norm + W8 lm_head with argmax partials, then greedy selection and step advance.
   return lemoq_lm_head_argmax_w8(p->h, p->final_norm, p->eps, p->lm_codes, p->lm_scale, p->vocab,

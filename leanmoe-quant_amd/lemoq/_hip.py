@@ -21,7 +21,7 @@ LIB_PATH = os.path.join(LIB_DIR, LIB_NAME)
 
 ABI_VERSION = 4
 # include/lemoq_hip.h: the fused launches' sync workspace and its status bit
-SYNC_WORDS = 8192
+SYNC_WORDS = 16384
 SYNC_TIMEOUT_BIT = 1
 
 _P = ctypes.c_void_p
@@ -109,6 +109,8 @@ class LemoqOlmoeStep(ctypes.Structure):
         ("h_mid", _P),
         ("sync", _P),
         ("sync_timeout_us", _I64),
+        ("one_launch", _I64),
+        ("moe_part", _P),
     ]
 
 
@@ -183,6 +185,11 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     ),
     "lemoq_attn_layer_check": (_I, [_I64, _I64, _I64, _I64, _I64, _I64]),
     "lemoq_sync_reset": (_I, [_P, _P]),
+    "lemoq_moe_layer_w8": (
+        _I,
+        [_P, _P, _P, _P, _P, _P, _I64, _I, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _I64, _P],
+    ),
+    "lemoq_moe_layer_check": (_I, [_I64, _I64, _I64, _I64, _I64]),
     "lemoq_moe_gate_up_w8_routed": (
         _I,
         [_P, _P, _P, _P, _I64, _I, _I64, _I64, _I64, _I64, _P, _P, _P, _P],

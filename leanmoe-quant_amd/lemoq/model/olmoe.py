@@ -50,8 +50,10 @@ STEP_MAX_SPLITS = 64
 # Time limit of each cross-workgroup wait inside the fused attention-layer
 # launch; a healthy wait takes microseconds.
 SYNC_TIMEOUT_US = 200_000
-# Whether the step runs each layer's attention half as one launch by default.
+# Whether the step runs each layer's attention half / its MoE as one launch
+# by default.
 ATTENTION_ONE_LAUNCH_DEFAULT = False
+MOE_ONE_LAUNCH_DEFAULT = False
 
 
 def step_num_splits(max_seq: int, heads: int, compute_units: int = 256) -> int:
@@ -215,6 +217,7 @@ class DecodeSession:
         max_new_tokens: int,
         num_splits: int | None = None,
         attention_one_launch: bool | None = None,
+        moe_one_launch: bool | None = None,
     ) -> None:
         from lemoq.kernels.attn_decode import resolve_num_splits  # noqa: PLC0415
         from lemoq.kernels.rope import rotary_cos_sin  # noqa: PLC0415
@@ -321,11 +324,16 @@ class DecodeSession:
                      "h_mid"):
             setattr(st, name, P(getattr(self, name)))
         st.am_len = n_parts
-        # The attention half of each layer as one launch (lemoq_attn_layer_i8)
-        # where the shape allows it; None takes the measured default.
-        one = ATTENTION_ONE_LAUNCH_DEFAULT if attention_one_launch is None else bool(attention_one_launch)
-        st.sync = P(self.sync) if one else None
+        # The attention half and the MoE of each layer as one launch each
+        # (lemoq_attn_layer_i8, lemoq_moe_layer_w8) where the shape allows it;
+        # None takes the measured default.
+        one_attn = ATTENTION_ONE_LAUNCH_DEFAULT if attention_one_launch is None else bool(attention_one_launch)
+        one_moe = MOE_ONE_LAUNCH_DEFAULT if moe_one_launch is None else bool(moe_one_launch)
+        self.moe_part = torch.zeros((s.top_k, s.hidden), dtype=torch.float32, device=dev)
+        st.sync = P(self.sync) if (one_attn or one_moe) else None
         st.sync_timeout_us = SYNC_TIMEOUT_US
+        st.one_launch = (1 if one_attn else 0) | (2 if one_moe else 0)
+        st.moe_part = P(self.moe_part)
         self._step = st
         self.graph: Any = None
         self.stream: Any = None
@@ -389,10 +397,19 @@ class DecodeSession:
         return self.logits
 
     @property
+    def moe_layer_fused(self) -> bool:
+        """Whether each layer's MoE runs as one launch (lemoq_moe_layer_w8)."""
+        s = self.shape
+        if not (self._step.sync and (self._step.one_launch & 2) and self._step.moe_part):
+            return False
+        rc = _hip.load().lemoq_moe_layer_check(s.top_k, s.num_experts, s.ffn, s.hidden, s.group_size)
+        return int(rc) == 0
+
+    @property
     def attn_layer_fused(self) -> bool:
         """Whether each layer's attention half runs as one launch (lemoq_attn_layer_i8)."""
         s = self.shape
-        if not (self._step.sync and self.attn_output_fused):
+        if not (self._step.sync and (self._step.one_launch & 1) and self.attn_output_fused):
             return False
         rc = _hip.load().lemoq_attn_layer_check(s.heads, s.head_dim, self.num_splits, s.hidden, s.group_size,
                                                 s.num_experts)
@@ -412,6 +429,8 @@ class DecodeSession:
     def launches_per_step(self) -> int:
         """Kernel launches in one captured step (see csrc/step.hip)."""
         per_layer = 4 if self.attn_layer_fused else (6 if self.attn_output_fused else 7)
+        if self.moe_layer_fused:
+            per_layer -= 1
         return per_layer * self.shape.layers + 2
 
     def capture(self) -> dict[str, Any]:

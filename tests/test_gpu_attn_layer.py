@@ -30,7 +30,7 @@ from oracle import quant as oq
 pytestmark = pytest.mark.gpu
 
 LOG2E = 1.4426950408889634
-SYNC_WORDS = 8192
+SYNC_WORDS = 16384  # LEMOQ_SYNC_WORDS
 
 
 def _inputs(heads, D, S, H, E, seed):

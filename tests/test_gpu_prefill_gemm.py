@@ -189,9 +189,26 @@ def test_route_topk_of_splitk_partials(m, n, k, splits, top_k, norm, dev):
     assert not torch.isnan(ws).any()  # every partial was written by the partials-only launch
     assert torch.equal(ti[0].cpu(), ti[1].cpu())
     assert torch.equal(tw[0].cpu(), tw[1].cpu())
-    # the oracle's routing of its own logits, where no two probabilities are within rounding
+    # 1. Given the same logits the routing is exact: the oracle's routing of the
+    #    GPU's own fp16 logits selects the same ids, in the same order, on every row.
+    got16 = logits.cpu()
+    rw_g, ri_g = ops.route_logits(got16, top_k, norm)
+    assert torch.equal(ri_g, ti[0].cpu()), "routing of identical logits differs"
+    torch.testing.assert_close(tw[0].cpu(), rw_g, rtol=1e-5, atol=1e-6)
+    # 2. Against the oracle's own logits (the fp64 product rounded once), the
+    #    GPU's fp32-accumulated logits may sit one fp16 step away.  A row may then
+    #    route differently only where two of the oracle's first top_k + 1 logits
+    #    (sorted) are within that measured logit error of each other; every
+    #    other row must select exactly the oracle's ids.
     ref16 = ops.linear_f16(x, w)
     rw, ri = ops.route_logits(ref16, top_k, norm)
+    err = float((got16.double() - ref16.double()).abs().max())
+    srt = torch.sort(ref16.double(), dim=-1, descending=True).values[:, : top_k + 1]
+    close = (srt[:, :-1] - srt[:, 1:]).min(dim=-1).values <= err
     same = (ri == ti[1].cpu()).all(dim=-1)
-    assert float(same.float().mean()) > 0.97, "ids agree on %.3f of rows" % float(same.float().mean())
+    excused = int((~same & close).sum())
+    print("rows %d, logit error %.2e, rows with a gap <= error %d, excused id differences %d"
+          % (m, err, int(close.sum()), excused))
+    assert bool((same | close).all()), "ids differ on a row with no near-tie: %s" % (
+        torch.nonzero(~(same | close)).flatten()[:8].tolist())
     torch.testing.assert_close(tw[1].cpu()[same], rw[same], rtol=2e-2, atol=2e-3)
