@@ -19,7 +19,9 @@ the per-token scales: ``score = ((q.c_k)*QK_SCALE)*ks``,
 
 from __future__ import annotations
 
+import copy
 import math
+from dataclasses import dataclass
 from typing import Any
 
 from lemoq import _hip
@@ -29,6 +31,7 @@ __all__ = [
     "LENGTH_CHANGE_GATE",
     "LOG2E",
     "PARITY_GATE",
+    "SplitPlan",
     "attn_decode_available",
     "attn_decode_forward",
     "attn_decode_forward_int8",
@@ -39,8 +42,9 @@ __all__ = [
     "warm",
 ]
 
-LOG2E = 1.4426950408889634
+LOG2E = 1.0 / math.log(2.0)
 
+# Frozen acceptance gates: their values are part of the operator contract.
 PARITY_GATE = {
     "tol_atol": 1e-3,
     "tol_rtol": 1e-3,
@@ -60,6 +64,9 @@ ATTN_CONFIGS: dict[str, Any] = {"num_splits": None}
 
 SUPPORTED_HEAD_DIMS = (64, 128, 256)
 
+# Threads per split block of lemoq_attn_split_{f16,i8} (four 64-lane waves).
+SPLIT_BLOCK_THREADS = 256
+
 
 def attn_decode_available() -> bool:
     try:
@@ -71,77 +78,104 @@ def attn_decode_available() -> bool:
 
 
 def merged_config(config: dict[str, Any] | None = None) -> dict[str, Any]:
-    cfg = {k: dict(v) if isinstance(v, dict) else v for k, v in ATTN_CONFIGS.items()}
-    for key, value in (config or {}).items():
-        if isinstance(value, dict) and isinstance(cfg.get(key), dict):
-            cfg[key].update(value)
-        else:
-            cfg[key] = value
-    return cfg
+    """A fresh copy of ``ATTN_CONFIGS`` with the call's overrides laid on top
+    (one level deep: a dict value updates the default dict of the same key)."""
+    out = copy.deepcopy(ATTN_CONFIGS)
+    for key, value in dict(config or {}).items():
+        base = out.get(key)
+        out[key] = {**base, **value} if isinstance(base, dict) and isinstance(value, dict) else value
+    return out
 
 
-def resolve_num_splits(num_splits: int | None, *, heads: int, device: Any = None) -> int:
-    """``None`` -> ``ceil(CUs / heads)`` of the device (1 when no device is visible)."""
-    if num_splits is not None:
-        if int(num_splits) < 1:
-            raise ValueError("num_splits must be >= 1")
-        return int(num_splits)
-    cus = None
+def _device_cu_count(device: Any) -> int:
+    """Compute units of ``device`` (default: device 0); 0 when no GPU is visible."""
     try:
         import torch  # noqa: PLC0415
 
-        if torch.cuda.is_available():
-            idx = device if device is not None else 0
-            cus = int(torch.cuda.get_device_properties(idx).multi_processor_count)
+        if not torch.cuda.is_available():
+            return 0
+        return int(torch.cuda.get_device_properties(0 if device is None else device).multi_processor_count)
     except Exception:  # noqa: BLE001
-        cus = None
-    if not cus:
-        return 1
-    return max(1, -(-cus // max(1, int(heads))))
+        return 0
 
 
-def launch_plan(*, heads: int, head_dim: int, num_splits: int, **_: Any) -> dict[str, Any]:
-    """Grid and partial-buffer shapes (pure host arithmetic)."""
-    if heads < 1 or head_dim < 1:
-        raise ValueError("heads and head_dim must be positive")
-    if head_dim & (head_dim - 1):
-        raise ValueError("head_dim must be a power of two, got %r" % (head_dim,))
-    if num_splits < 1:
+def resolve_num_splits(num_splits: int | None, *, heads: int, device: Any = None) -> int:
+    """An explicit count is kept (it must be >= 1).  ``None`` spreads one head's
+    splits over the device: ``ceil(CUs / heads)``, so heads x splits covers
+    every CU once; 1 where no device is visible."""
+    if num_splits is None:
+        cus = _device_cu_count(device)
+        return max(1, math.ceil(cus / max(1, int(heads)))) if cus else 1
+    n = int(num_splits)
+    if n < 1:
         raise ValueError("num_splits must be >= 1")
-    return {
-        "heads": int(heads),
-        "head_dim": int(head_dim),
-        "num_splits": int(num_splits),
-        "kernel_count": 2,
-        "split": {
-            "grid": (int(num_splits), int(heads)),
-            "block": 256,
-            "m_shape": (int(heads), int(num_splits)),
-            "l_shape": (int(heads), int(num_splits)),
-            "acc_shape": (int(heads), int(num_splits), int(head_dim)),
-            "dtype": "float32",
-        },
-        "combine": {"grid": (int(heads),), "out_shape": (1, int(heads), 1, int(head_dim))},
-    }
+    return n
+
+
+def _is_pow2(n: int) -> bool:
+    return n >= 1 and not n & (n - 1)
+
+
+@dataclass(frozen=True)
+class SplitPlan:
+    """Host-side geometry of one decode-attention call: the split launch is a
+    (num_splits, heads) grid that writes fp32 partials m, l (heads, num_splits)
+    and acc (heads, num_splits, head_dim); the merge launch is one block per
+    head writing the (1, heads, 1, head_dim) output."""
+
+    heads: int
+    head_dim: int
+    num_splits: int
+
+    def __post_init__(self) -> None:
+        if min(self.heads, self.head_dim) < 1:
+            raise ValueError("heads and head_dim must be positive")
+        if not _is_pow2(self.head_dim):
+            raise ValueError("head_dim must be a power of two, got %r" % (self.head_dim,))
+        if self.num_splits < 1:
+            raise ValueError("num_splits must be >= 1")
+
+    def as_dict(self) -> dict[str, Any]:
+        hs = (self.heads, self.num_splits)
+        return {
+            "heads": self.heads,
+            "head_dim": self.head_dim,
+            "num_splits": self.num_splits,
+            "kernel_count": 2,
+            "split": {"grid": hs[::-1], "block": SPLIT_BLOCK_THREADS, "m_shape": hs, "l_shape": hs,
+                      "acc_shape": hs + (self.head_dim,), "dtype": "float32"},
+            "combine": {"grid": (self.heads,), "out_shape": (1, self.heads, 1, self.head_dim)},
+        }
+
+
+def launch_plan(*, heads: int, head_dim: int, num_splits: int, block_n: int | None = None,
+                block_d: int | None = None) -> dict[str, Any]:
+    """Grid and partial-buffer shapes, pure host arithmetic.  ``block_n`` /
+    ``block_d`` (the reference's tile sizes) are validated as the reference
+    does (a power of two; ``block_d >= head_dim``) and otherwise unused: the HIP
+    kernels' tiles are fixed."""
+    if block_n is not None and not _is_pow2(int(block_n)):
+        raise ValueError("block_n must be a power of two, got %r" % (block_n,))
+    if block_d is not None and int(block_d) < int(head_dim):
+        raise ValueError("block_d must not be smaller than head_dim")
+    return SplitPlan(int(heads), int(head_dim), int(num_splits)).as_dict()
 
 
 def judge_length_change(
     *, correct_err: float, stale_err: float, gate: dict[str, Any] | None = None
 ) -> dict[str, Any]:
-    """K4 verdict: PASS/FAIL only when the stale answer is far from the correct one."""
-    gate = LENGTH_CHANGE_GATE if gate is None else gate
-    correct_err = float(correct_err)
-    stale_err = float(stale_err)
-    discriminating = stale_err >= float(gate["discriminant_min"])
-    correct = correct_err < float(gate["correct_err_max"])
-    verdict = "INCONCLUSIVE" if not discriminating else ("PASS" if correct else "FAIL")
-    return {
-        "verdict": verdict,
-        "correct_err": correct_err,
-        "stale_err": stale_err,
-        "discriminating": bool(discriminating),
-        "gate": dict(gate),
-    }
+    """Verdict of the length-change check.  The check only discriminates when the
+    stale answer (length N) is far from the true one at length M; without that it
+    is INCONCLUSIVE, never PASS.  With it, PASS iff the replayed answer's error is
+    under ``correct_err_max``."""
+    g = dict(LENGTH_CHANGE_GATE if gate is None else gate)
+    errs = {"correct_err": float(correct_err), "stale_err": float(stale_err)}
+    discriminating = errs["stale_err"] >= float(g["discriminant_min"])
+    if not discriminating:
+        verdict = "INCONCLUSIVE"
+    else:
+        verdict = "PASS" if errs["correct_err"] < float(g["correct_err_max"]) else "FAIL"
+    return {"verdict": verdict, **errs, "discriminating": discriminating, "gate": g}
 
 
 def _filled_tensor(filled_len: Any, *, device: Any, seq_len: int) -> Any:

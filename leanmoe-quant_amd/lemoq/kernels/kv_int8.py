@@ -29,24 +29,39 @@ __all__ = [
 ]
 
 
-def kv_int8_rows_applicable(k_new: Any, v_new: Any) -> bool:
-    """Row guard of the write path: ROCm fp16 (1, H, 1, D) contiguous rows, D a power of two."""
+def _row_guard_failure(k_new: Any, v_new: Any) -> str | None:
+    """The first rule that the k/v rows break, or None when the int8 write path
+    takes them: two ROCm-resident fp16 tensors of one (1, H, 1, D) shape, both
+    contiguous, with D a power of two (the per-row reduction of the kernel)."""
     import torch  # noqa: PLC0415
 
-    if not (torch.is_tensor(k_new) and torch.is_tensor(v_new)):
-        return False
-    if not (k_new.is_cuda and v_new.is_cuda):
-        return False
-    if k_new.dtype is not torch.float16 or v_new.dtype is not torch.float16:
-        return False
-    if k_new.shape != v_new.shape or k_new.dim() != 4 or k_new.shape[0] != 1:
-        return False
-    if k_new.shape[2] != 1:
-        return False
-    if not (k_new.is_contiguous() and v_new.is_contiguous()):
-        return False
-    dim = int(k_new.shape[-1])
-    return dim >= 1 and (dim & (dim - 1)) == 0
+    pair = (k_new, v_new)
+    if not all(torch.is_tensor(t) for t in pair):
+        return "k/v are not tensors"
+    if not all(t.is_cuda for t in pair):
+        return "k/v are not on the GPU"
+    if any(t.dtype is not torch.float16 for t in pair):
+        return "k/v are not fp16"
+    shape = tuple(k_new.shape)
+    if tuple(v_new.shape) != shape or len(shape) != 4 or shape[0] != 1 or shape[2] != 1:
+        return "k/v are not one (1, H, 1, D) shape"
+    if not all(t.is_contiguous() for t in pair):
+        return "k/v are not contiguous"
+    d = shape[3]
+    if d < 1 or d & (d - 1):
+        return "head_dim %d is not a power of two" % d
+    return None
+
+
+def kv_int8_rows_applicable(k_new: Any, v_new: Any) -> bool:
+    """Row guard of the write path; callers fall back to the fp16 write when False."""
+    return _row_guard_failure(k_new, v_new) is None
+
+
+def _require_rows(k_new: Any, v_new: Any, what: str) -> None:
+    why = _row_guard_failure(k_new, v_new)
+    if why is not None:
+        raise RuntimeError("%s: row guard failed (%s); check kv_int8_rows_applicable first" % (what, why))
 
 
 def quantize_per_token_int8(x: Any) -> tuple[Any, Any]:
@@ -101,17 +116,15 @@ def kv_int8_bulk_quantize(cache_keys: Any, cache_values: Any, filled: Any = None
 
 
 def kv_int8_init_buffers(layer_keys: Any, layer_values: Any, filled: Any = None) -> dict[str, Any]:
-    bufs = kv_int8_bulk_quantize(layer_keys, layer_values, filled)
-    bufs["initialized"] = True
-    return bufs
+    """A layer's int8 mirror of its fp16 cache, marked ``initialized``."""
+    return {**kv_int8_bulk_quantize(layer_keys, layer_values, filled), "initialized": True}
 
 
 def kv_int8_cache_write(bufs: dict[str, Any], k_new: Any, v_new: Any, pos: Any) -> None:
     """Quantize the new (1,H,1,D) k/v rows into slot ``pos`` (device int64 tensor)."""
     import torch  # noqa: PLC0415
 
-    if not kv_int8_rows_applicable(k_new, v_new):
-        raise RuntimeError("kv_int8_cache_write: row guard failed (need ROCm fp16 (1,H,1,D) rows)")
+    _require_rows(k_new, v_new, "kv_int8_cache_write")
     kc = bufs["kc"]
     if (
         kc.dim() != 4
@@ -148,14 +161,17 @@ def kv_int8_write(
     """Quantize (1,H,1,D) k/v rows into (1,H,1,D) int8 codes + (1,H,1) fp16 scales."""
     import torch  # noqa: PLC0415
 
-    if not kv_int8_rows_applicable(k_new, v_new):
-        raise RuntimeError("kv_int8_write: row guard failed (need ROCm fp16 (1,H,1,D) rows)")
+    _require_rows(k_new, v_new, "kv_int8_write")
     heads, dim = int(k_new.shape[1]), int(k_new.shape[-1])
-    if k_codes is None:
-        k_codes = torch.empty((1, heads, 1, dim), dtype=torch.int8, device=k_new.device)
-        k_scale = torch.empty((1, heads, 1), dtype=torch.float16, device=k_new.device)
-        v_codes = torch.empty((1, heads, 1, dim), dtype=torch.int8, device=v_new.device)
-        v_scale = torch.empty((1, heads, 1), dtype=torch.float16, device=v_new.device)
+    given = (k_codes, k_scale, v_codes, v_scale)
+    if all(t is None for t in given):
+        # one allocation each for the codes and the scales of both rows
+        codes = torch.empty((2, 1, heads, 1, dim), dtype=torch.int8, device=k_new.device)
+        scales = torch.empty((2, 1, heads, 1), dtype=torch.float16, device=k_new.device)
+        k_codes, v_codes = codes.unbind(0)
+        k_scale, v_scale = scales.unbind(0)
+    elif any(t is None for t in given):
+        raise ValueError("kv_int8_write: pass all four outputs or none")
     _hip.require_rocm(k_codes, k_scale, v_codes, v_scale, what="kv_int8_write")
     _hip.call(
         "lemoq_kv_write_i8",

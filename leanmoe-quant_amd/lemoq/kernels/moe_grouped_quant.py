@@ -25,6 +25,7 @@ product path.
 
 from __future__ import annotations
 
+import dataclasses
 from dataclasses import dataclass
 from typing import Any
 
@@ -77,33 +78,29 @@ class QuantFusedExperts:
     def hidden(self) -> int:
         return int(self.packed_gate_up.shape[-1]) * (8 // int(self.bits))
 
+    # The four device tensors, in the order they are laid out in HBM.
+    _TENSORS = ("packed_gate_up", "scale_gate_up", "packed_down", "scale_down")
+
     def nbytes(self) -> int:
-        total = 0
-        for t in (self.packed_gate_up, self.scale_gate_up, self.packed_down, self.scale_down):
-            total += int(t.numel()) * int(t.element_size())
-        return total
+        """Bytes of codes and scales together (what one full pass over every
+        expert reads)."""
+        return sum(getattr(self, f).numel() * getattr(self, f).element_size() for f in self._TENSORS)
 
     def to(self, device: Any = None, dtype: Any = None) -> "QuantFusedExperts":
-        """Move to a device; a dtype change is refused (it would undo the quantisation)."""
+        """Copy to ``device`` (contiguous).  Codes stay int8 and scales fp16, so a
+        dtype is refused, also when passed positionally as ``to(torch.float32)``:
+        converting would undo the quantisation."""
         import torch  # noqa: PLC0415
 
-        if isinstance(device, torch.dtype):
+        if dtype is None and isinstance(device, torch.dtype):
             device, dtype = None, device
         if dtype is not None:
-            raise ValueError(
-                "QuantFusedExperts does not convert dtype (codes stay int8, scales fp16); "
-                "got dtype=%r — re-quantize instead" % (dtype,)
-            )
+            raise ValueError("QuantFusedExperts keeps int8 codes and fp16 scales; dtype=%r refused "
+                             "(quantize again for another precision)" % (dtype,))
         if device is None:
             return self
-        return QuantFusedExperts(
-            packed_gate_up=self.packed_gate_up.to(device=device).contiguous(),
-            scale_gate_up=self.scale_gate_up.to(device=device).contiguous(),
-            packed_down=self.packed_down.to(device=device).contiguous(),
-            scale_down=self.scale_down.to(device=device).contiguous(),
-            bits=self.bits,
-            group_size=self.group_size,
-        )
+        moved = {f: getattr(self, f).to(device=device).contiguous() for f in self._TENSORS}
+        return dataclasses.replace(self, **moved)
 
 
 def quantize_fused_experts(fused: Any, *, bits: int = 8, group_size: int = 128) -> QuantFusedExperts:

@@ -25,24 +25,23 @@ class PackedQKV:
     out_features: int
     group_size: int
 
-    def project(self, x: Any) -> tuple[Any, Any, Any]:
+    def _packed_rows(self, x: Any) -> Any:
+        """The one GEMV/GEMM launch: ``(M, in)`` rows -> ``(M, 3*out)``, q | k | v."""
         from lemoq.kernels.dequant_gemm import dequant_gemm_fused  # noqa: PLC0415
 
-        flat = x.reshape(-1, self.in_features)
-        if not flat.is_contiguous():
-            flat = flat.contiguous()
-        y = dequant_gemm_fused(
-            flat, self.packed, self.scale, None, group_size=self.group_size, bits=8,
-            symmetric=True, out_dtype=x.dtype,
-        )
-        y = y.reshape(*x.shape[:-1], 3, self.out_features)
-        return y[..., 0, :], y[..., 1, :], y[..., 2, :]
+        rows = x.reshape(-1, self.in_features).contiguous()
+        return dequant_gemm_fused(rows, self.packed, self.scale, None, group_size=self.group_size,
+                                  bits=8, symmetric=True, out_dtype=x.dtype)
+
+    def project(self, x: Any) -> tuple[Any, Any, Any]:
+        """``(..., in)`` -> q, k, v of shape ``(..., out)`` each: views of one
+        packed output, no copies."""
+        y = self._packed_rows(x).view(*x.shape[:-1], 3, self.out_features)
+        return tuple(y.unbind(-2))
 
     def combined(self, x: Any) -> Any:
-        import torch  # noqa: PLC0415
-
-        q, k, v = self.project(x)
-        return torch.cat((q, k, v), dim=-1)
+        """The packed ``(..., 3*out)`` output itself."""
+        return self._packed_rows(x).view(*x.shape[:-1], 3 * self.out_features)
 
 
 def pack_qkv(q: Any, k: Any, v: Any) -> PackedQKV:

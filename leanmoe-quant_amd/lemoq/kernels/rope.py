@@ -86,16 +86,18 @@ def apply_rotary_pos_emb_fused(
 
 
 def warm(*, heads: int = 16, kv_heads: int = 4, head_dim: int = 128, device: Any = None) -> None:
-    """One real launch before graph capture (same signature and defaults as the
-    reference's ``rope.warm``, src/lemoq/kernels/rope.py:206): loads the HIP
-    library and runs ``apply_rotary_pos_emb_fused`` on (1, heads, 1, head_dim) q
-    and (1, kv_heads, 1, head_dim) k with (1, 1, head_dim) cos/sin, then syncs."""
+    """One real launch before graph capture, with the reference's signature and
+    defaults (src/lemoq/kernels/rope.py:206): rotates (1, heads, 1, head_dim) q
+    and (1, kv_heads, 1, head_dim) k by the angles of position 1 at base 10000
+    (the (1, 1, head_dim) cos/sin of a real decode step), then synchronises."""
     import torch  # noqa: PLC0415
 
-    dev = device if device is not None else torch.device("cuda")
-    q = torch.randn(1, heads, 1, head_dim, dtype=torch.float16, device=dev)
-    k = torch.randn(1, kv_heads, 1, head_dim, dtype=torch.float16, device=dev)
-    cos = torch.randn(1, 1, head_dim, dtype=torch.float16, device=dev)
-    sin = torch.randn(1, 1, head_dim, dtype=torch.float16, device=dev)
+    dev = torch.device(device if device is not None else "cuda")
+    half = head_dim // 2
+    inv_freq = 10000.0 ** (-torch.arange(half, dtype=torch.float32) / half)
+    ang = torch.cat((inv_freq, inv_freq)).view(1, 1, head_dim)
+    cos, sin = (f(ang).to(dev, torch.float16) for f in (torch.cos, torch.sin))
+    q = torch.ones((1, heads, 1, head_dim), dtype=torch.float16, device=dev)
+    k = torch.ones((1, kv_heads, 1, head_dim), dtype=torch.float16, device=dev)
     apply_rotary_pos_emb_fused(q, k, cos, sin)
     torch.cuda.synchronize(dev)
