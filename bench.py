@@ -896,6 +896,7 @@ def main(argv=None) -> int:
     dom_name = "moe_gate_up_w8_routed"
     dom = kt[dom_name]
     traffic = _traffic_from_profiles(dom_name)
+    in_graph_us = _in_graph_from_profiles(DOM_DISPATCH)
     line = {
         "metric": METRIC,
         "value": r1["step_ms_p50"],
@@ -940,6 +941,10 @@ def main(argv=None) -> int:
             # a launch that only reads the same bytes, timed the same way (cold, 64 launches)
             "read_floor_avg_us": kt[READ_FLOOR]["avg_us"],
             "frac_of_read_floor": kt[READ_FLOOR]["avg_us"] / dom["avg_us"],
+            # the same kernel as it runs inside the step's graph replays
+            "in_graph_avg_us": in_graph_us,
+            "frac_in_graph": (dom["bytes"] / (in_graph_us * 1e-6) / 1e9 / HBM_PEAK_GBS) if in_graph_us else None,
+            "in_graph_source": BENCH_TRACE + " (rocprofv3 --kernel-trace of this bench command)" if in_graph_us else None,
         },
         "kernels": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()
                         if kk != "dispatch_kernels"} for k, v in kt.items()},
@@ -1107,6 +1112,27 @@ def _prefill_summary(*runs) -> dict:
             "reference_rtx5090_e2e_32_ms": REFERENCE_RTX5090_E2E32_MS.get(c),
         }
     return out
+
+
+# The roofline kernel's dispatch name in a rocprofv3 kernel trace.
+DOM_DISPATCH = "moe_gate_up_kernel<2, 2, 1, true>"
+BENCH_TRACE = os.path.join("profiles", "bench_kernel_trace.md")
+
+
+def _in_graph_from_profiles(dispatch: str):
+    """Average duration (us) of ``dispatch`` inside the graph replays, from the
+    committed rocprofv3 kernel trace of this bench command (the table written by
+    ``--summarize-trace``), or None.  Events time a whole replay, not one of its
+    nodes, so the in-graph duration of one kernel comes from the profiler."""
+    try:
+        with open(os.path.join(REPO, BENCH_TRACE)) as f:
+            for line in f:
+                cells = [c.strip() for c in line.strip().strip("|").split("|")]
+                if len(cells) == 5 and cells[0] == dispatch and cells[2] != "-":
+                    return float(cells[2])
+    except (OSError, ValueError):
+        pass
+    return None
 
 
 def _traffic_from_profiles(kernel: str):

@@ -89,7 +89,8 @@ __device__ __forceinline__ void attn_split_fused_block(const AttnSplitArgs& a, i
   float* wl = sm.wl;
   float* wacc = sm.wacc;
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // wave from a scalar register: the branches on it below are scalar branches
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int dl = lane % T::LPT, tl = lane / T::LPT;
   const int HD = a.heads * D;
   const int64_t cap = a.s_len;
@@ -98,57 +99,71 @@ __device__ __forceinline__ void attn_split_fused_block(const AttnSplitArgs& a, i
   const uint16_t* ksh = a.ks + (int64_t)h * cap;
   const uint16_t* vsh = a.vs + (int64_t)h * cap;
 
-  const int64_t pos = a.pos[0];
-  const bool pos_ok = pos >= 0 && pos < cap;
-  const int64_t n_tot = pos_ok ? pos + 1 : 0;  // attention over tokens [0, pos]
-  const int64_t chunk = (n_tot + a.ns - 1) / a.ns;
-  const int64_t start = (int64_t)sp * chunk;
-  const int64_t end = start + chunk < n_tot ? start + chunk : n_tot;
-  const bool owns_new = pos_ok && start <= pos && pos < end;
-  const int64_t cend = owns_new ? pos : end;  // cached tokens [start, cend)
+  const int64_t pos = a.pos[0];  // a scalar load, issued first
 
-  // The first token block is issued unconditionally (slots clamped into
-  // [0, max(cend, 1)), folds masked by cend): a load under a branch lets the
-  // compiler unpack its bytes right after the issue, which waits on it before
-  // the prologue below could overlap it.  (Issuing more blocks up front,
-  // 2 or 4, measured slower: the prologue's wait then covers them too.)
-  lemoq_attn::TokBlock<T> ta, tb;
-  int64_t base = start + (int64_t)wave * BLK;
-  const int64_t lim = cend > 0 ? cend : 1;
-  lemoq_attn::issue_tokens<T>(ta, kb, vb, ksh, vsh, base, lim, tl, dl, D);
-
-  if (wave == 0 || (owns_new && wave < 3)) {
-    // Prologue: wave 0 -> q (every block), wave 1 -> new k (normed, rotated,
-    // quantised), wave 2 -> new v (quantised).  Element i of a lane is
-    // d = lane + 64 i, so for D >= 128 a lane holds both rotate_half partners
-    // (d and d + D/2) and RoPE needs no cross-lane exchange; for D = 64 the
-    // partner is lane ^ 32.  Every prologue load (the lane's values, norm
-    // weight, cos/sin row, and the whole q or k row for the sum of squares)
-    // is issued as raw bits before any of them is used, so the prologue waits
-    // on memory once.
-    constexpr int QV = 8;  // 16-byte row slices per lane held in registers (rows <= 4096)
-    const int which = wave;
-    const uint16_t* src = a.qkv + (int64_t)which * HD;
-    uint16_t ob[EPL], wb[EPL], cb[EPL], sb[EPL];
-    u32x4 qrow[QV];
+  // Issue order.  The vector loads of a wave retire in issue order, so what
+  // is needed first is issued first: the prologue rows that do not depend on
+  // *pos (q, or the new k / v, and the norm weights) go out before *pos has
+  // arrived; then the cos/sin row at *pos; then the first token block.  The
+  // q norm thus overlaps the token loads instead of waiting behind them.
+  // Waves 1 and 2 load the new k / v rows in every block (only the block that
+  // holds *pos uses them: *pos is not known yet).
+  constexpr int QV = 8;  // 16-byte row slices per lane held in registers (rows <= 4096)
+  const bool pro_wave = wave < 3;
+  const int which = wave;
+  const uint16_t* src = a.qkv + (int64_t)which * HD;
+  // 16-bit values held one per 32-bit register: packing two into one register
+  // would make the compiler wait for both loads inside the branch.
+  uint32_t ob[EPL], wb[EPL], cb[EPL], sb[EPL];
+  u32x4 qrow[QV];
+  if (pro_wave) {
 #pragma unroll
     for (int i = 0; i < EPL; ++i) ob[i] = src[h * D + lane + 64 * i];
     if (which < 2) {
       const uint16_t* nw = which == 0 ? a.qn_w : a.kn_w;
-      const int64_t prow = pos_ok ? pos : 0;
 #pragma unroll
       for (int j = 0; j < QV; ++j) {
         const int i = lane * 8 + j * 64 * 8;
         qrow[j] = *reinterpret_cast<const u32x4*>(src + (i < HD ? i : 0));  // masked below
       }
 #pragma unroll
-      for (int i = 0; i < EPL; ++i) {
-        wb[i] = nw[h * D + lane + 64 * i];
-        cb[i] = a.cos_tab[prow * D + lane + 64 * i];
-        sb[i] = a.sin_tab[prow * D + lane + 64 * i];
-      }
+      for (int i = 0; i < EPL; ++i) wb[i] = nw[h * D + lane + 64 * i];
     }
-    LEMOQ_LOADS_ISSUED();
+  }
+
+  // (cap < 2^31, checked on the host: the split arithmetic is 32-bit.)
+  const bool pos_ok = pos >= 0 && pos < cap;
+  const uint32_t n_tot = pos_ok ? (uint32_t)pos + 1u : 0u;  // attention over tokens [0, pos]
+  const uint32_t chunk = (n_tot + (uint32_t)a.ns - 1u) / (uint32_t)a.ns;
+  const int64_t start = (int64_t)sp * chunk;
+  const int64_t end = start + chunk < n_tot ? start + chunk : (int64_t)n_tot;
+  const bool owns_new = pos_ok && start <= pos && pos < end;
+  const int64_t cend = owns_new ? pos : end;  // cached tokens [start, cend)
+
+  if (pro_wave && which < 2) {
+    const int64_t prow = pos_ok ? pos : 0;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      cb[i] = a.cos_tab[prow * D + lane + 64 * i];
+      sb[i] = a.sin_tab[prow * D + lane + 64 * i];
+    }
+  }
+  // The first token block is issued unconditionally (slots clamped into
+  // [0, max(cend, 1)), folds masked by cend): a load under a branch lets the
+  // compiler unpack its bytes right after the issue, which would wait on it
+  // before the prologue below could overlap it.
+  lemoq_attn::TokBlock<T> ta, tb;
+  int64_t base = start + (int64_t)wave * BLK;
+  const int64_t lim = cend > 0 ? cend : 1;
+  lemoq_attn::issue_tokens<T>(ta, kb, vb, ksh, vsh, base, lim, tl, dl, D);
+  LEMOQ_LOADS_ISSUED();
+
+  if (wave == 0 || (owns_new && wave < 3)) {
+    // Prologue: wave 0 -> q (every block), wave 1 -> new k (normed, rotated,
+    // quantised), wave 2 -> new v (quantised).  Element i of a lane is
+    // d = lane + 64 i, so for D >= 128 a lane holds both rotate_half partners
+    // (d and d + D/2) and RoPE needs no cross-lane exchange; for D = 64 the
+    // partner is lane ^ 32.
     float o[EPL];
 #pragma unroll
     for (int i = 0; i < EPL; ++i) o[i] = h2f(ob[i]);
@@ -206,20 +221,24 @@ __device__ __forceinline__ void attn_split_fused_block(const AttnSplitArgs& a, i
   lemoq_attn::SoftmaxState<T::EPL> st;
   lemoq_attn::softmax_init(st);
 
-  // Two token blocks in flight: fold one while the next one loads.  The
-  // next block is issued unconditionally (clamped; at the end it re-reads
-  // the split's last slot, an L2 hit) for the reason given above.
+  // Two token blocks in flight: fold one while the next one loads.  The next
+  // block is issued only when the wave has one (a wave-uniform branch): a
+  // load of nothing would still have to retire before the block's closing
+  // barrier.
   while (base < cend) {
     int64_t nb = base + STRIDE;
-    lemoq_attn::issue_tokens<T>(tb, kb, vb, ksh, vsh, nb, lim, tl, dl, D);
+    bool more = nb < cend;
+    if (more) lemoq_attn::issue_tokens<T>(tb, kb, vb, ksh, vsh, nb, lim, tl, dl, D);
     LEMOQ_LOADS_ISSUED();
     lemoq_attn::fold_tokens<T>(st, ta, qx, base, cend, tl, lane, a.qk_scale);
+    if (!more) break;
     base = nb;
-    if (base >= cend) break;
     nb = base + STRIDE;
-    lemoq_attn::issue_tokens<T>(ta, kb, vb, ksh, vsh, nb, lim, tl, dl, D);
+    more = nb < cend;
+    if (more) lemoq_attn::issue_tokens<T>(ta, kb, vb, ksh, vsh, nb, lim, tl, dl, D);
     LEMOQ_LOADS_ISSUED();
     lemoq_attn::fold_tokens<T>(st, tb, qx, base, cend, tl, lane, a.qk_scale);
+    if (!more) break;
     base = nb;
   }
   if (wave == NW - 1 && owns_new) {

@@ -28,7 +28,8 @@ extern "C" int lemoq_attn_split_fused_i8(const uint16_t* qkv, int64_t heads, int
   if (head_dim != 64 && head_dim != 128 && head_dim != 256) return LEMOQ_ERR_UNSUPPORTED;
   if (heads <= 0 || heads > 65535 || heads * head_dim > 65536) return LEMOQ_ERR_SHAPE;
   if (num_splits <= 0 || num_splits > 65535) return LEMOQ_ERR_SHAPE;
-  if (s_len <= 0 || code_head_stride < s_len * head_dim) return LEMOQ_ERR_SHAPE;
+  if (s_len <= 0 || s_len >= (int64_t(1) << 31) || code_head_stride < s_len * head_dim)
+    return LEMOQ_ERR_SHAPE;
   if (!lemoq_aligned16(qkv) || !lemoq_aligned16(kc) || !lemoq_aligned16(vc) ||
       code_head_stride % 16 != 0)
     return LEMOQ_ERR_ALIGN;
@@ -59,9 +60,9 @@ extern "C" int lemoq_attn_split_fused_i8(const uint16_t* qkv, int64_t heads, int
   // cache slots with 16 splits (against 8 and 16 waves, 1 and 4 loads).
   const dim3 block(64 * 4);
   switch (head_dim) {
-    case 64: hipLaunchKernelGGL((attn_split_fused_i8_kernel<64, 4, 2>), grid, block, 0, st, a); break;
-    case 128: hipLaunchKernelGGL((attn_split_fused_i8_kernel<128, 4, 2>), grid, block, 0, st, a); break;
-    default: hipLaunchKernelGGL((attn_split_fused_i8_kernel<256, 4, 2>), grid, block, 0, st, a); break;
+    case 64: hipLaunchKernelGGL((attn_split_fused_i8_kernel<64, 4, 3>), grid, block, 0, st, a); break;
+    case 128: hipLaunchKernelGGL((attn_split_fused_i8_kernel<128, 4, 3>), grid, block, 0, st, a); break;
+    default: hipLaunchKernelGGL((attn_split_fused_i8_kernel<256, 4, 3>), grid, block, 0, st, a); break;
   }
   LEMOQ_CHECK_LAUNCH();
 }

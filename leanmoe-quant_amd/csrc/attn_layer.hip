@@ -111,7 +111,7 @@ __global__ __launch_bounds__(256) void attn_layer_kernel(const LayerArgs a) {
 
   // A: split block (sp, h).
   const int h = b / ns, sp = b % ns;
-  lemoq_attn_fused::attn_split_fused_block<128, 4, 2, true>(a.at, sp, h, sm);
+  lemoq_attn_fused::attn_split_fused_block<128, 4, 3, true>(a.at, sp, h, sm);
   publish(line(a, 1 + h));
 
   // B: o_proj tiles b, b + G, ...
@@ -244,7 +244,8 @@ extern "C" int lemoq_attn_layer_i8(const uint16_t* qkv, int64_t heads, int64_t h
       !logits || !sync)
     return LEMOQ_ERR_NULL;
   if (timeout_us < 0) return LEMOQ_ERR_SHAPE;
-  if (s_len <= 0 || code_head_stride < s_len * head_dim) return LEMOQ_ERR_SHAPE;
+  if (s_len <= 0 || s_len >= (int64_t(1) << 31) || code_head_stride < s_len * head_dim)
+    return LEMOQ_ERR_SHAPE;
   const int rc = lemoq_attn_layer_check(heads, head_dim, num_splits, hidden, group, num_experts);
   if (rc) return rc;
   const int64_t HD = heads * head_dim;

@@ -86,7 +86,7 @@ int validate(const LemoqOlmoeStep* p, AttnPath* path, bool* moe_one) {
   if (!a16(p->lm_codes)) return LEMOQ_ERR_ALIGN;
   // split-KV attention (attn_fused.hip)
   if (D != 64 && D != 128 && D != 256) return LEMOQ_ERR_UNSUPPORTED;
-  if (p->heads > 65535 || HD > 65536 || ns > 65535) return LEMOQ_ERR_SHAPE;
+  if (p->heads > 65535 || HD > 65536 || ns > 65535 || S >= ((int64_t)1 << 31)) return LEMOQ_ERR_SHAPE;
   if (!a16(p->qkv)) return LEMOQ_ERR_ALIGN;
   // routed gate/up and down (moe.hip)
   if (K > 64 || K > E) return LEMOQ_ERR_SHAPE;

@@ -74,3 +74,22 @@ def test_summary_rejects_dispatches_out_of_plan(tmp_path):
     with pytest.raises(SystemExit, match="gemv_w8_kernel.*expects moe_gate_up_kernel"):
         bench.summarize_pmc(str(tmp_path / "f.csv"), str(tmp_path / "w.csv"), str(tmp_path / "plan.json"),
                             str(tmp_path / "out"))
+
+
+def test_in_graph_duration_read_from_trace_table(tmp_path, monkeypatch):
+    """roofline.in_graph_avg_us comes from the committed kernel-trace table: the
+    row of the dispatch name, its in-graph column; absent rows or files give None."""
+    prof = tmp_path / "profiles"
+    prof.mkdir()
+    (prof / "bench_kernel_trace.md").write_text(
+        "# trace\n\n| kernel | in-graph / other launches | avg us | isolated cold launches | avg us |\n"
+        "|---|---|---|---|---|\n"
+        "| moe_gate_up_kernel<4> | 288 | 242.14 | 0 | - |\n"
+        "| moe_gate_up_kernel<2, 2, 1, true> | 2720 | 8.30 | 64 | 7.96 |\n"
+        "| attn_split_kernel<128, true> | 0 | - | 128 | 11.84 |\n")
+    monkeypatch.setattr(bench, "REPO", str(tmp_path))
+    assert bench._in_graph_from_profiles("moe_gate_up_kernel<2, 2, 1, true>") == 8.30
+    assert bench._in_graph_from_profiles("attn_split_kernel<128, true>") is None   # no in-graph launches
+    assert bench._in_graph_from_profiles("moe_down_kernel<1, 4, true>") is None
+    monkeypatch.setattr(bench, "REPO", str(tmp_path / "missing"))
+    assert bench._in_graph_from_profiles("moe_gate_up_kernel<2, 2, 1, true>") is None
