@@ -83,7 +83,7 @@ __global__ __launch_bounds__(128 * WM) void gemm_kernel(const GemmArgs a) {
 #pragma unroll
   for (int j = 0; j < TL::FN; ++j) b_row0[j] = wn * (BN / 2) + 32 * j;
   Acc<TL::FM, TL::FN> acc;
-  block_mainloop<TL, W8>(acc, src, klen, a.group, lds, wm * (BM / WM), b_row0);
+  block_mainloop2<TL, W8>(acc, src, klen, a.group, lds, wm * (BM / WM), b_row0);
 
 #pragma unroll
   for (int i = 0; i < TL::FM; ++i)

@@ -217,7 +217,7 @@ __global__ __launch_bounds__(128 * WN) void moe_gate_up_kernel(const GroupedArgs
   const int wm = wave / WN, wn = wave % WN;
   const int b_row0[2] = {32 * wn, AC + 32 * wn};
   Acc<2, 2> acc;
-  block_mainloop<TL, true>(acc, src, a.K, a.group, lds, 64 * wm, b_row0);
+  block_mainloop2<TL, true>(acc, src, a.K, a.group, lds, 64 * wm, b_row0);
   const int64_t n = n0 + 32 * wn + l32;
 #pragma unroll
   for (int i = 0; i < 2; ++i)
@@ -264,7 +264,7 @@ __global__ __launch_bounds__(128 * WN) void moe_down_kernel(const GroupedArgs a,
   const int wm = wave / WN, wn = wave % WN;
   const int b_row0[2] = {64 * wn, 64 * wn + 32};
   Acc<2, 2> acc;
-  block_mainloop<TL, true>(acc, src, a.K, a.group, lds, 64 * wm, b_row0);
+  block_mainloop2<TL, true>(acc, src, a.K, a.group, lds, 64 * wm, b_row0);
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
