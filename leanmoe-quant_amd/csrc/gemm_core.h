@@ -266,141 +266,6 @@ __device__ __forceinline__ void block_mainloop(Acc<TL::FM, TL::FN>& acc, const S
   }
 }
 
-// ---------------------------------------------------------------------------
-// Direct-B main loop (w8 only).  A block of 4 waves computes a BM x (4 * 32 FN)
-// tile; wave w owns all BM rows and the FN 32-row weight fragments whose
-// rows are given per lane by the caller (b_codes / b_scale).  Only X goes
-// through LDS (double-buffered, BM x BK per stage, one barrier per stage).
-// Each wave loads its own weight rows straight from global memory in the
-// operand layout of v_mfma_f32_32x32x16_f16 (lane l: row l % 32 of the
-// fragment, the 16 codes 32 c + 16 (l / 32) .. + 15 of 32-wide chunk c) and
-// dequantises them in registers with dequant16.  The weight rows of a block
-// are disjoint across its waves, so every code is read and dequantised once
-// per block, as in block_mainloop, but without the LDS round trip, and a
-// wave issues FM x FN x 4 matrix ops per stage for (FM + 0) fragment reads
-// from LDS.  The k-values each instruction sees and the order of the matrix
-// ops per accumulator are those of block_mainloop, so the results are
-// bit-identical to it.
-// ---------------------------------------------------------------------------
-template <int BM_, int FN_>
-struct DTile {
-  static constexpr int BM = BM_, FN = FN_, FM = BM / 32;
-  static constexpr int NT = 256;                         // 4 waves
-  static constexpr int A_CH = BM * (BK / 8) / NT;        // 16-byte X chunks per thread per stage
-  static constexpr int LDS_HALF = BM * LDS_PITCH;        // fp16 per buffer
-  static constexpr int LDS_ELEMS = 2 * LDS_HALF;
-  static_assert(BM % 32 == 0 && A_CH >= 1 && BM * (BK / 8) % NT == 0, "tile sizes");
-  __device__ static int a_row(int t, int i) { return (t + NT * i) >> 3; }
-  __device__ static int a_col(int t, int i) { return 8 * ((t + NT * i) & 7); }
-};
-
-// The lane's raw weight codes of one stage: fragment j, chunk c.
-template <int FN>
-struct BRaw {
-  u32x4 v[FN][BK / 32];
-  uint16_t s[FN];
-};
-
-template <int FN>
-__device__ __forceinline__ void b_issue(BRaw<FN>& r, const int8_t* const (&bc)[FN],
-                                        const uint16_t* const (&bs)[FN], int64_t k0, int sidx, int half) {
-#pragma unroll
-  for (int j = 0; j < FN; ++j) {
-#pragma unroll
-    for (int c = 0; c < BK / 32; ++c)
-      r.v[j][c] = *reinterpret_cast<const u32x4*>(bc[j] + k0 + 32 * c + 16 * half);
-    r.s[j] = bs[j][sidx];
-  }
-}
-
-template <class TL>
-__device__ __forceinline__ void a_issue(u32x4 (&st)[TL::A_CH], const uint16_t* const (&src)[TL::A_CH], int64_t k0) {
-#pragma unroll
-  for (int i = 0; i < TL::A_CH; ++i) st[i] = *reinterpret_cast<const u32x4*>(src[i] + k0);
-}
-
-template <class TL>
-__device__ __forceinline__ void a_store(const u32x4 (&st)[TL::A_CH], uint16_t* buf, int t) {
-#pragma unroll
-  for (int i = 0; i < TL::A_CH; ++i)
-    *reinterpret_cast<u32x4*>(buf + TL::a_row(t, i) * LDS_PITCH + TL::a_col(t, i)) = st[i];
-}
-
-template <class TL>
-__device__ __forceinline__ void stage_mma_direct(Acc<TL::FM, TL::FN>& acc, const uint16_t* As,
-                                                 const BRaw<TL::FN>& r, int l32, int half) {
-#pragma unroll
-  for (int c = 0; c < BK / 32; ++c) {
-    u32x4 b[TL::FN][2];
-#pragma unroll
-    for (int j = 0; j < TL::FN; ++j) dequant16(r.v[j][c], (uint32_t)r.s[j] * 0x10001u, b[j][0], b[j][1]);
-#pragma unroll
-    for (int i = 0; i < TL::FM; ++i) {
-      const uint16_t* p = As + (32 * i + l32) * LDS_PITCH + 32 * c + 16 * half;
-      const u32x4 a0 = *reinterpret_cast<const u32x4*>(p);
-      const u32x4 a1 = *reinterpret_cast<const u32x4*>(p + 8);
-#pragma unroll
-      for (int j = 0; j < TL::FN; ++j) {
-        acc.v[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(h8_of(a0), h8_of(b[j][0]), acc.v[i][j], 0, 0, 0);
-        acc.v[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(h8_of(a1), h8_of(b[j][1]), acc.v[i][j], 0, 0, 0);
-      }
-    }
-  }
-}
-
-// Whole K loop (K % 64 == 0, group % 64 == 0); lds holds TL::LDS_ELEMS fp16.
-// The weight codes of stage s + 1 are in flight while stage s is computed
-// (two register sets, ping-pong), as are the X chunks of stage s + 1.
-template <class TL>
-__device__ __forceinline__ void block_mainloop_direct(Acc<TL::FM, TL::FN>& acc,
-                                                      const uint16_t* const (&asrc)[TL::A_CH],
-                                                      const int8_t* const (&bc)[TL::FN],
-                                                      const uint16_t* const (&bs)[TL::FN], int64_t K, int group,
-                                                      uint16_t* lds) {
-  const int t = threadIdx.x, lane = t & 63;
-  const int half = lane >> 5, l32 = lane & 31;
-#pragma unroll
-  for (int i = 0; i < TL::FM; ++i)
-#pragma unroll
-    for (int j = 0; j < TL::FN; ++j) acc.v[i][j] = (f32x16){};
-  const int nst = (int)(K / BK);
-  const int spg = group / BK;
-  const int last_sidx = (nst - 1) / spg;
-  int gi = 0, gc = 0;  // scale index and stage within the group of the next stage to issue
-  u32x4 ast[TL::A_CH];
-  BRaw<TL::FN> r0, r1;
-  a_issue<TL>(ast, asrc, 0);
-  b_issue<TL::FN>(r0, bc, bs, 0, 0, half);
-  a_store<TL>(ast, lds, t);
-  __syncthreads();
-  if (++gc == spg) gc = 0, ++gi;  // stage 1
-  for (int s = 0; s < nst; s += 2) {
-    // stage s: X in buffer 0, codes in r0
-    {
-      const bool more = s + 1 < nst;
-      const int64_t kn = (int64_t)(more ? s + 1 : s) * BK;
-      a_issue<TL>(ast, asrc, kn);
-      b_issue<TL::FN>(r1, bc, bs, kn, more ? gi : last_sidx, half);
-      stage_mma_direct<TL>(acc, lds, r0, l32, half);
-      a_store<TL>(ast, lds + TL::LDS_HALF, t);
-      __syncthreads();
-      if (++gc == spg) gc = 0, ++gi;
-      if (!more) break;
-    }
-    // stage s + 1: X in buffer 1, codes in r1
-    {
-      const bool more = s + 2 < nst;
-      const int64_t kn = (int64_t)(more ? s + 2 : s + 1) * BK;
-      a_issue<TL>(ast, asrc, kn);
-      b_issue<TL::FN>(r0, bc, bs, kn, more ? gi : last_sidx, half);
-      stage_mma_direct<TL>(acc, lds + TL::LDS_HALF, r1, l32, half);
-      a_store<TL>(ast, lds, t);
-      __syncthreads();
-      if (++gc == spg) gc = 0, ++gi;
-    }
-  }
-}
-
 // Row (within the 32-row fragment) of accumulator register r in lane half `half`.
 __device__ __forceinline__ int acc_row(int r, int half) { return 8 * (r / 4) + 4 * half + (r % 4); }
 
