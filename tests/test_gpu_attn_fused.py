@@ -98,6 +98,12 @@ def _fused_path(hip, dev, qkv, qn, kn, cache, cos, sin, pos, heads, D, S, ns=4, 
     # the decode step's 16 splits: 4-wave blocks (<= 128 slots per split) and 8-wave blocks
     (16, 128, 1100, 1060, 16), (16, 128, 1100, 70, 16), (16, 128, 1100, 15, 16), (16, 128, 4200, 4132, 16),
     (16, 128, 4200, 300, 16), (4, 256, 1024, 1000, 16), (8, 64, 2048, 2047, 16),
+    # round boundaries of the token loop: a wave block is 3 loads (24 tokens at D 128, 48 at
+    # D 64, 12 at D 256) and a round of 4 waves 4x that; splits of exactly one round, one round
+    # plus a token, two rounds plus a token, and of one or two wave blocks' worth
+    (16, 128, 1600, 1535, 16), (16, 128, 1600, 1536, 16), (16, 128, 3200, 3072, 16),
+    (16, 128, 1100, 383, 16), (16, 128, 1100, 384, 16), (8, 64, 3200, 3071, 16), (8, 64, 3200, 3072, 16),
+    (4, 256, 1100, 767, 16), (4, 256, 1100, 768, 16),
 ])
 def test_fused_attention_equals_split_path_and_oracle(heads, D, S, pos, ns, dev):
     from lemoq import _hip
