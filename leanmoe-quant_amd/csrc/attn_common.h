@@ -185,27 +185,77 @@ __device__ __forceinline__ void fold_tokens(SoftmaxState<S::EPL>& st, const TokB
   st.m = m_new;
 }
 
+// Pair sums across lane halves (gfx950 v_permlane32_swap) and across the rows
+// of each half (v_permlane16_swap), for two values x, y per lane: lanes 0-31
+// get x + x of lane ^ 32 and lanes 32-63 get y + y of lane ^ 32 (rows: even
+// rows x, odd rows y, partner lane ^ 16).  One swap exchanges both: lanes 0-31
+// receive the partner's x, lanes 32-63 the partner's y.  The lane's own value
+// and the partner's are selected by lane and added, as in xor16_get /
+// xor32_get: adding the swap's two results directly is miscompiled (the
+// compiler adds the first result to itself).
+__device__ __forceinline__ float halves_pair_sum(float x, float y, int lane) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x),
+                                                  __builtin_bit_cast(uint32_t, y), false, false);
+  const bool lo = lane < 32;
+  return (lo ? x : y) + __builtin_bit_cast(float, lo ? r[1] : r[0]);
+}
+__device__ __forceinline__ float rows_pair_sum(float x, float y, int lane) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, x),
+                                                  __builtin_bit_cast(uint32_t, y), false, false);
+  const bool even = (lane & 16) == 0;
+  return (even ? x : y) + __builtin_bit_cast(float, even ? r[1] : r[0]);
+}
+
 // End of a split block: sum the token groups of each wave (the running max is
 // wave-uniform), merge the NW wave states through LDS in wave order, and
 // write the block's (m, l, acc[D]) partial; m = -inf for an empty split
 // (l = 0, acc = 0).  wm/wl hold NW floats, wacc NW * D.  COHERENT: the partial
 // is stored with coherent stores, for a consumer in the same launch (sync.h).
+//
+// The EPL accumulators of a lane are summed over its token group (the lanes
+// sharing lane % LPT, partners lane ^ LPT, ^ 2 LPT, ... ^ 32) as a reduce-
+// scatter: the pair sum across halves keeps elements [0, EPL/2) in the lower
+// half and [EPL/2, EPL) in the upper, the pair sum across rows halves them
+// again (LPT <= 16), and row rotations (LPT 4, 8) finish the sum.  A lane ends
+// with V = EPL / 2 (or 4) fully summed elements instead of all EPL, and one
+// lane of each group of duplicates writes them to LDS.
 template <class S, int NW, int D, bool COHERENT = false>
 __device__ __forceinline__ void finish_split(SoftmaxState<S::EPL>& st, float* wm, float* wl,
                                              float* wacc, int lane, int wave, int tl, int dl,
                                              int64_t pidx, float* __restrict__ m_out,
                                              float* __restrict__ l_out,
                                              float* __restrict__ acc_out) {
-  st.l = groups_total<S::LPT>(st.l, lane);
+  constexpr int G = S::LPT, E = S::EPL;
+  constexpr bool X16 = G <= 16;            // the row pair is a partner too
+  constexpr int V = X16 ? E / 4 : E / 2;   // elements per lane after the scatter
+  static_assert(G <= 32 && V >= 1, "token groups of 4, 8, 16 or 32 lanes");
+  st.l = groups_total<G>(st.l, lane);
+  float h[E / 2];
 #pragma unroll
-  for (int e = 0; e < S::EPL; ++e) st.acc[e] = groups_total<S::LPT>(st.acc[e], lane);
+  for (int i = 0; i < E / 2; ++i) h[i] = halves_pair_sum(st.acc[i], st.acc[i + E / 2], lane);
+  float v[V];
+  if constexpr (X16) {
+#pragma unroll
+    for (int i = 0; i < V; ++i) v[i] = rows_pair_sum(h[i], h[i + V], lane);
+  } else {
+#pragma unroll
+    for (int i = 0; i < V; ++i) v[i] = h[i];
+  }
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    if (G == 4) v[i] += dpp_f<LEMOQ_DPP_ROW_ROR4>(v[i]);
+    if (G <= 8) v[i] += dpp_f<LEMOQ_DPP_ROW_ROR8>(v[i]);
+  }
   if (lane == 0) {
     wm[wave] = st.m;
     wl[wave] = st.l;
   }
-  if (tl == 0) {
+  // lanes whose in-row token bits are zero hold distinct element ranges
+  if (G > 16 || (lane & 15) < G) {
+    const int base = ((lane & 32) ? E / 2 : 0) + ((X16 && (lane & 16)) ? E / 4 : 0);
+    float* dst = wacc + wave * D + dl * E + base;
 #pragma unroll
-    for (int e = 0; e < S::EPL; ++e) wacc[wave * D + dl * S::EPL + e] = st.acc[e];
+    for (int i = 0; i < V; ++i) dst[i] = v[i];
   }
   __syncthreads();
   for (int t = threadIdx.x; t < D; t += 64 * NW) {
