@@ -651,7 +651,8 @@ int lemoq_moe_prefill_gate_up(const uint16_t* x, int64_t H, const int32_t* pair_
                               void* stream);
 
 /* y[pair_src] (H) = fp16(fp16(act @ w_down^T) * pair_w) for each sorted pair.
- * dn_codes (E, H, F) int8; dn_scale (E, H, F/group) fp16; y (T*top_k, H). */
+ * dn_codes (E, H, F) int8; dn_scale (E, H, F/group) fp16; y (T*top_k, H), 16-byte
+ * aligned (the rows are written in 16-byte chunks). */
 int lemoq_moe_prefill_down(const uint16_t* act, int64_t F, const int32_t* pair_src,
                            const uint16_t* pair_w, const int32_t* tiles, int64_t max_tiles,
                            const int8_t* dn_codes, const uint16_t* dn_scale, int64_t H,

@@ -232,12 +232,24 @@ __global__ __launch_bounds__(128 * WN) void moe_gate_up_kernel(const GroupedArgs
     }
 }
 
-// 3. down: 128 pairs x 64 WN hidden columns per block.
+// 3. down: 128 pairs x 64 WN hidden columns per block.  The epilogue goes
+// through LDS: the waves write fp16(acc) into the (then idle) stage buffers
+// as a 128 x 64 WN row-major tile, and the block writes each pair's row
+// segment with 16-byte stores, scaled by its routing weight on the way out:
+// fp16(fp16(y) * w), the same two roundings as per element.  The pair's
+// output row and weight are loaded before the K loop (threads 0..127, one
+// pair each) and parked in LDS for the epilogue.
 template <int WN>
 __global__ __launch_bounds__(128 * WN) void moe_down_kernel(const GroupedArgs a, int64_t max_tiles) {
   using TL = GTile<WN>;
-  constexpr int NC = 64 * WN;  // output columns per block
+  constexpr int NC = 64 * WN;       // output columns per block
+  constexpr int OP = NC + 8;        // output tile pitch in LDS (fp16)
+  constexpr int CPR = NC / 8;       // 16-byte chunks per output row
+  constexpr int RPI = TL::NT / CPR; // rows written per pass of the block
+  static_assert(TILE_ROWS * OP <= TL::LDS_ELEMS && TL::NT % CPR == 0, "down output tile");
   __shared__ __align__(16) uint16_t lds[TL::LDS_ELEMS];
+  __shared__ int32_t row_dst[TILE_ROWS];
+  __shared__ float row_w[TILE_ROWS];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int half = lane >> 5, l32 = lane & 31;
   const int64_t H = a.N;
@@ -245,6 +257,13 @@ __global__ __launch_bounds__(128 * WN) void moe_down_kernel(const GroupedArgs a,
   int e;
   if (!grouped_tile(a, (H + NC - 1) / NC, max_tiles, nb, e, rs, re)) return;  // block-uniform
   const int64_t n0 = nb * NC;
+  const int rows = (int)(re - rs);  // 1 .. TILE_ROWS
+  int32_t my_dst = 0;
+  uint16_t my_w = 0;
+  if (t < rows) {
+    my_dst = a.pair_src[rs + t];
+    my_w = a.pair_w[rs + t];
+  }
   Sources<TL, true> src;
 #pragma unroll
   for (int i = 0; i < TL::A_CH; ++i) {
@@ -265,21 +284,35 @@ __global__ __launch_bounds__(128 * WN) void moe_down_kernel(const GroupedArgs a,
   const int b_row0[2] = {64 * wn, 64 * wn + 32};
   Acc<2, 2> acc;
   block_mainloop2<TL, true>(acc, src, a.K, a.group, lds, 64 * wm, b_row0);
+  __syncthreads();  // every wave has read its last stage from LDS
+  if (t < TILE_ROWS) {
+    row_dst[t] = my_dst;
+    row_w[t] = h2f(my_w);
+  }
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int64_t m = rs + 64 * wm + 32 * i + acc_row(r, half);
-      if (m >= re) continue;
-      const float w = h2f(a.pair_w[m]);
-      uint16_t* dst = a.y + (int64_t)a.pair_src[m] * H;
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int64_t n = n0 + 64 * wn + 32 * j + l32;
-        if (n >= H) continue;
-        dst[n] = f2h(h2f(f2h(acc.v[i][j][r])) * w);
-      }
+      for (int r = 0; r < 16; ++r)
+        lds[(64 * wm + 32 * i + acc_row(r, half)) * OP + 64 * wn + 32 * j + l32] = f2h(acc.v[i][j][r]);
+  __syncthreads();
+  const int c8 = (t % CPR) * 8;
+  const int64_t n = n0 + c8;
+  if (n >= H) return;  // N % 32 == 0: a chunk is wholly inside or outside
+  for (int row = t / CPR; row < rows; row += RPI) {
+    const u32x4 v = *reinterpret_cast<const u32x4*>(lds + row * OP + c8);
+    const float w = row_w[row];
+    const uint32_t in[4] = {v.x, v.y, v.z, v.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint16_t lo = f2h(h2f((uint16_t)(in[q] & 0xFFFFu)) * w);
+      const uint16_t hi = f2h(h2f((uint16_t)(in[q] >> 16)) * w);
+      o[q] = (uint32_t)lo | ((uint32_t)hi << 16);
     }
+    *reinterpret_cast<u32x4*>(a.y + (int64_t)row_dst[row] * H + n) = (u32x4){o[0], o[1], o[2], o[3]};
+  }
 }
 
 // 4. combine: one block per token, 8 columns per thread.  The slot loop has a
@@ -407,7 +440,7 @@ extern "C" int lemoq_moe_prefill_down(const uint16_t* act, int64_t F, const int3
                                       int64_t group, uint16_t* y, void* stream) {
   if (!act || !pair_src || !pair_w || !tiles || !dn_codes || !dn_scale || !y) return LEMOQ_ERR_NULL;
   if (!grouped_shape_ok(F, H, group) || max_tiles <= 0 || max_tiles > (1LL << 20)) return LEMOQ_ERR_SHAPE;
-  if (!lemoq_aligned16(act) || !lemoq_aligned16(dn_codes)) return LEMOQ_ERR_ALIGN;
+  if (!lemoq_aligned16(act) || !lemoq_aligned16(dn_codes) || !lemoq_aligned16(y)) return LEMOQ_ERR_ALIGN;
   GroupedArgs a{};
   a.x = act; a.pair_src = pair_src; a.pair_w = pair_w; a.tiles = tiles; a.codes = dn_codes;
   a.scale = dn_scale; a.K = F; a.N = H; a.group = (int)group; a.y = y;
