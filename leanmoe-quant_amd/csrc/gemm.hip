@@ -15,7 +15,10 @@
 //
 // Rows: X row m may be gathered (x_rows[m]); the output is fp16 rows with an
 // optional fp16 residual added in one rounding (torch's fp16 add).  Rows and
-// columns beyond M/N are clamped on load and not stored.
+// columns beyond M/N are clamped on load and not stored.  When the output
+// (and residual) rows are 16-byte aligned, the block stages its fp16 tile in
+// LDS and writes whole row segments in 16-byte chunks; otherwise each lane
+// stores its own elements.
 #include "gemm_core.h"
 
 #include <mutex>
@@ -39,6 +42,7 @@ struct GemmArgs {
   int64_t resid_ld;
   int splits;              // K ranges (blockIdx.y); > 1 writes fp32 partials
   float* part;             // (splits, M, N) fp32 partials when splits > 1
+  int row_out;             // fp16 rows written as 16-byte chunks (set by the host)
 };
 
 template <bool W8, int BM, int BN, int WM = 2>
@@ -85,6 +89,44 @@ __global__ __launch_bounds__(128 * WM) void gemm_kernel(const GemmArgs a) {
   Acc<TL::FM, TL::FN> acc;
   block_mainloop2<TL, W8>(acc, src, klen, a.group, lds, wm * (BM / WM), b_row0);
 
+  if (a.row_out) {  // block-uniform
+    // fp16(acc) into the (then idle) stage buffers as a BM x BN row-major
+    // tile, then each row segment goes out in 16-byte chunks with the
+    // residual added per chunk: the same roundings as the per-element path.
+    constexpr int OP = BN + 8, CPR = BN / 8, RPI = TL::NT / CPR;
+    static_assert(BM * OP <= TL::LDS_ELEMS && TL::NT % CPR == 0, "output tile");
+    __syncthreads();  // every wave has read its last stage from LDS
+#pragma unroll
+    for (int i = 0; i < TL::FM; ++i)
+#pragma unroll
+      for (int j = 0; j < TL::FN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          lds[(wm * (BM / WM) + 32 * i + acc_row(r, half)) * OP + wn * (BN / 2) + 32 * j + l32] =
+              f2h(acc.v[i][j][r]);
+    __syncthreads();
+    const int c8 = (t % CPR) * 8;
+    const int64_t n = n0 + c8;
+    if (n >= a.N) return;  // N % 8 == 0: a chunk is wholly inside or outside
+    const int rows = (int)(a.M - m0 < BM ? a.M - m0 : BM);
+    for (int row = t / CPR; row < rows; row += RPI) {
+      u32x4 v = *reinterpret_cast<const u32x4*>(lds + row * OP + c8);
+      if (a.resid) {
+        const u32x4 rv = *reinterpret_cast<const u32x4*>(a.resid + (m0 + row) * a.resid_ld + n);
+        const uint32_t in[4] = {v.x, v.y, v.z, v.w}, ri[4] = {rv.x, rv.y, rv.z, rv.w};
+        uint32_t o[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint16_t lo = hadd_round(h2f((uint16_t)(in[q] & 0xFFFFu)), (uint16_t)(ri[q] & 0xFFFFu));
+          const uint16_t hi = hadd_round(h2f((uint16_t)(in[q] >> 16)), (uint16_t)(ri[q] >> 16));
+          o[q] = (uint32_t)lo | ((uint32_t)hi << 16);
+        }
+        v = (u32x4){o[0], o[1], o[2], o[3]};
+      }
+      *reinterpret_cast<u32x4*>(a.y16 + (m0 + row) * a.y_ld + n) = v;
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < TL::FM; ++i)
 #pragma unroll
@@ -149,7 +191,10 @@ int launch_tiles(const GemmArgs& a, hipStream_t st) {
   LEMOQ_CHECK_LAUNCH();
 }
 
-int launch_gemm(const GemmArgs& a, hipStream_t st) {
+int launch_gemm(GemmArgs a, hipStream_t st) {
+  // 16-byte row stores need 16-byte aligned rows of the output (and residual)
+  a.row_out = a.splits == 1 && a.y16 && lemoq_aligned16(a.y16) && a.y_ld % 8 == 0 && a.N % 8 == 0 &&
+              (!a.resid || (lemoq_aligned16(a.resid) && a.resid_ld % 8 == 0));
   return a.codes ? launch_tiles<true>(a, st) : launch_tiles<false>(a, st);
 }
 

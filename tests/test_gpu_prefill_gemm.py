@@ -99,6 +99,42 @@ def test_gemm_w8_gather_and_residual(dev):
     assert_close(y.cpu(), ref, what="gather+residual")
 
 
+@pytest.mark.parametrize("m,n,k", [(1100, 6144, 256), (2000, 2048, 256), (77, 512, 1024)],
+                         ids=["256x128-tiles", "128x128-tiles", "64x64-tiles"])
+def test_gemm_w8_row_stores_equal_element_stores(m, n, k, dev):
+    """16-byte aligned output rows are staged in LDS and written as 16-byte
+    chunks; an output one element off that alignment takes the per-element
+    stores.  Both give the same bytes, with and without the residual, into a
+    strided output (y_ld > N) whose pad columns stay untouched."""
+    from lemoq import _hip
+
+    print("case: gemm_w8 row vs element stores m=%d n=%d k=%d" % (m, n, k), flush=True)
+    codes, scale = _q8(randn(n, k, seed=51, std=0.02), 128)
+    x = randn(m, k, seed=52).to(torch.float16)
+    resid = randn(m, n, seed=53).to(torch.float16)
+    xd, cd, sd = x.to(dev), codes.to(dev), scale.to(dev)
+    P, st = _hip.ptr, _hip.stream_of(dev)
+    ld = n + 8
+    outs = {}
+    for off in (0, 1):  # 0: 16-byte aligned rows; 1: one fp16 element off
+        for with_resid in (False, True):
+            buf = torch.full((m * ld + 16,), float("nan"), dtype=torch.float16, device=dev)
+            y = buf[off:off + m * ld].view(m, ld)
+            rbuf = torch.zeros((m * ld + 16,), dtype=torch.float16, device=dev)
+            r = rbuf[off:off + m * ld].view(m, ld)
+            r[:, :n] = resid.to(dev)
+            _hip.call("lemoq_gemm_w8", P(xd), m, k, k, None, P(cd), P(sd), n, 128, P(y), ld,
+                      P(r) if with_resid else None, ld, st)
+            torch.cuda.synchronize()
+            assert bool(torch.isnan(y[:, n:]).all()), "pad columns written"
+            outs[(off, with_resid)] = y[:, :n].cpu()
+    for with_resid in (False, True):
+        assert torch.equal(outs[(0, with_resid)], outs[(1, with_resid)]), with_resid
+    ref = ops.linear_separate_w8(x, codes, scale, 128)
+    assert_close(outs[(0, False)], ref, what="row stores vs oracle")
+    assert_close(outs[(0, True)], (ref.float() + resid.float()).to(torch.float16), what="row stores + residual")
+
+
 @pytest.mark.parametrize("m,n,k", [(1024, 64, 2048), (5, 64, 2048), (3, 50, 64)])
 def test_gemm_f16_vs_oracle(m, n, k, dev):
     from lemoq.kernels.dequant_gemm import linear_f16
