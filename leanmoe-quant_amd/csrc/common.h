@@ -89,6 +89,59 @@ __device__ __forceinline__ void rmsnorm_row_256(const uint16_t* xr, int H, const
   }
 }
 
+// The same RMSNorm on a row held in registers: thread t of the 256 owns the
+// 16-byte chunks at columns 8 (t + 256 i), i < RN_CHUNKS, those below H
+// (H % 8 == 0, H <= 2048 * RN_CHUNKS, rows and w 16-byte aligned).  Thread t
+// sums its chunks' squares in column order, then the block sum; every caller
+// of this function on the same row gets the same bits.
+constexpr int RN_CHUNKS = 4;
+__device__ __forceinline__ void rmsnorm_chunks(const u32x4 (&x)[RN_CHUNKS], int H, const uint16_t* __restrict__ w,
+                                               float eps, uint16_t* __restrict__ yr, float* red) {
+  const int c0 = 8 * (int)threadIdx.x;
+  u32x4 wv[RN_CHUNKS];
+#pragma unroll
+  for (int i = 0; i < RN_CHUNKS; ++i)
+    if (c0 + 2048 * i < H) wv[i] = *reinterpret_cast<const u32x4*>(w + c0 + 2048 * i);
+  float ssq = 0.0f;
+#pragma unroll
+  for (int i = 0; i < RN_CHUNKS; ++i) {
+    if (c0 + 2048 * i >= H) continue;
+    const uint32_t q[4] = {x[i].x, x[i].y, x[i].z, x[i].w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float a = h2f((uint16_t)(q[k] & 0xFFFFu)), b = h2f((uint16_t)(q[k] >> 16));
+      ssq += a * a;
+      ssq += b * b;
+    }
+  }
+  const float tot = block_sum_256(ssq, red);
+  const float rstd = 1.0f / sqrtf(tot / (float)H + eps);
+#pragma unroll
+  for (int i = 0; i < RN_CHUNKS; ++i) {
+    if (c0 + 2048 * i >= H) continue;
+    const uint32_t q[4] = {x[i].x, x[i].y, x[i].z, x[i].w};
+    const uint32_t g[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
+    uint32_t o[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint16_t na = f2h(h2f((uint16_t)(q[k] & 0xFFFFu)) * rstd);
+      const uint16_t nb = f2h(h2f((uint16_t)(q[k] >> 16)) * rstd);
+      const uint16_t ya = f2h(h2f(na) * h2f((uint16_t)(g[k] & 0xFFFFu)));
+      const uint16_t yb = f2h(h2f(nb) * h2f((uint16_t)(g[k] >> 16)));
+      o[k] = (uint32_t)ya | ((uint32_t)yb << 16);
+    }
+    *reinterpret_cast<u32x4*>(yr + c0 + 2048 * i) = (u32x4){o[0], o[1], o[2], o[3]};
+  }
+}
+
+// The chunks of rmsnorm_chunks from a row in global memory or LDS.
+__device__ __forceinline__ void rmsnorm_load_chunks(const uint16_t* xr, int H, u32x4 (&x)[RN_CHUNKS]) {
+  const int c0 = 8 * (int)threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < RN_CHUNKS; ++i)
+    if (c0 + 2048 * i < H) x[i] = *reinterpret_cast<const u32x4*>(xr + c0 + 2048 * i);
+}
+
 __device__ __forceinline__ float wave_max(float v) {
   v = fmaxf(v, dpp_f<LEMOQ_DPP_QUAD_1032>(v));
   v = fmaxf(v, dpp_f<LEMOQ_DPP_QUAD_2301>(v));

@@ -317,10 +317,13 @@ __global__ __launch_bounds__(128 * WN) void moe_down_kernel(const GroupedArgs a,
 
 // 4. combine: one block per token, 8 columns per thread.  The slot loop has a
 // fixed trip count of 8 (slots past top_k read slot 0 and are not added), so
-// all of a thread's loads are issued before the first add.  NORM: the block
-// also keeps its output row in LDS and writes the next layer's input
-// RMSNorm of it (the same row function as the plain norm kernel, so xn is
-// bit-identical to a separate norm launch).
+// all of a thread's loads are issued before the first add.  (Loading the
+// slots in slot order before the ids arrive, then reordering them through a
+// 32 KB LDS stage, was slower: the stage caps the blocks per CU.)  NORM: the
+// block keeps its output row in LDS and writes the next layer's input
+// RMSNorm of it with the norm kernel's own row function (rmsnorm_chunks), so
+// xn is bit-identical to a separate norm launch.  (Holding the row in
+// registers instead raised the kernel to 93 registers and cost occupancy.)
 constexpr int kCombineNormMaxH = 8192;
 
 template <bool NORM>
@@ -384,12 +387,15 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __rest
       const uint16_t hi = resid ? hadd_round(acc[2 * i + 1], (uint16_t)(rw[i] >> 16)) : f2h(acc[2 * i + 1]);
       ow[i] = (uint32_t)lo | ((uint32_t)hi << 16);
     }
-    *reinterpret_cast<u32x4*>(out + t * H + c) = (u32x4){ow[0], ow[1], ow[2], ow[3]};
-    if constexpr (NORM) *reinterpret_cast<u32x4*>(row + c) = (u32x4){ow[0], ow[1], ow[2], ow[3]};
+    const u32x4 o4 = (u32x4){ow[0], ow[1], ow[2], ow[3]};
+    *reinterpret_cast<u32x4*>(out + t * H + c) = o4;
+    if constexpr (NORM) *reinterpret_cast<u32x4*>(row + c) = o4;
   }
   if constexpr (NORM) {
-    __syncthreads();
-    rmsnorm_row_256(row, (int)H, norm_w, eps, xn + t * H, red);
+    // each thread reads back only the chunks it wrote: no barrier needed
+    u32x4 ox[RN_CHUNKS];
+    rmsnorm_load_chunks(row, (int)H, ox);
+    rmsnorm_chunks(ox, (int)H, norm_w, eps, xn + t * H, red);
   }
 }
 

@@ -11,12 +11,21 @@
 
 namespace {
 
+// VEC: rows held as 16-byte chunks in registers (H % 8 == 0, H <= 8192,
+// x, w, y 16-byte aligned): one read of the row, 16-byte stores.
+template <bool VEC>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict__ x, int H,
                                                       const uint16_t* __restrict__ w, float eps,
                                                       uint16_t* __restrict__ y) {
   __shared__ float red[4];
   const int64_t r = blockIdx.x;
-  rmsnorm_row_256(x + r * H, H, w, eps, y + r * H, red);
+  if constexpr (VEC) {
+    u32x4 xv[RN_CHUNKS];
+    rmsnorm_load_chunks(x + r * H, H, xv);
+    rmsnorm_chunks(xv, H, w, eps, y + r * H, red);
+  } else {
+    rmsnorm_row_256(x + r * H, H, w, eps, y + r * H, red);
+  }
 }
 
 // Embedding rows of several tokens: dst[r] = src[ids[r]] (a zero row for an
@@ -255,8 +264,14 @@ extern "C" int lemoq_rmsnorm(const uint16_t* x, int64_t rows, int64_t hidden, co
   if (rows < 0 || hidden <= 0 || hidden > 8192) return LEMOQ_ERR_SHAPE;
   if (rows == 0) return LEMOQ_OK;
   if (rows > 0x7fffffffLL) return LEMOQ_ERR_SHAPE;
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)rows), dim3(256), 0, lemoq_stream(stream), x,
-                     (int)hidden, w, eps, y);
+  const bool vec = hidden % 8 == 0 && hidden <= 2048 * RN_CHUNKS && lemoq_aligned16(x) && lemoq_aligned16(w) &&
+                   lemoq_aligned16(y);
+  if (vec)
+    hipLaunchKernelGGL(rmsnorm_kernel<true>, dim3((unsigned)rows), dim3(256), 0, lemoq_stream(stream), x,
+                       (int)hidden, w, eps, y);
+  else
+    hipLaunchKernelGGL(rmsnorm_kernel<false>, dim3((unsigned)rows), dim3(256), 0, lemoq_stream(stream), x,
+                       (int)hidden, w, eps, y);
   LEMOQ_CHECK_LAUNCH();
 }
 
