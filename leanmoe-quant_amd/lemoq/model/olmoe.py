@@ -336,6 +336,8 @@ class DecodeSession:
         st.moe_part = P(self.moe_part)
         self._step = st
         self.graph: Any = None
+        self.graph_multi: Any = None  # steps_per_graph decode steps in one graph (capture(steps_per_graph=K))
+        self.steps_per_graph = 1
         self.stream: Any = None
         self._host_pos = 0
         self.reset()
@@ -433,26 +435,51 @@ class DecodeSession:
             per_layer -= 1
         return per_layer * self.shape.layers + 2
 
-    def capture(self) -> dict[str, Any]:
-        """Capture one decode step into a hipGraph (state is untouched by the capture)."""
-        if self.graph is not None:
-            return {"capture_success": True, "launches_per_step": self.launches_per_step}
-        self.stream = torch.cuda.Stream(device=self.device)
-        self.stream.wait_stream(torch.cuda.current_stream(self.device))
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, stream=self.stream):
-            self._enqueue_step()
-        torch.cuda.synchronize(self.device)
-        self.graph = graph
-        return {"capture_success": True, "launches_per_step": self.launches_per_step}
+    def capture(self, steps_per_graph: int = 1) -> dict[str, Any]:
+        """Capture one decode step into a hipGraph (state is untouched by the capture).
+
+        ``steps_per_graph`` K > 1 also captures K steps back to back into a second
+        graph, which ``replay`` then uses for whole groups of K steps.  Each step
+        reads and advances the device's position and token, so a K-step replay
+        computes exactly what K one-step replays do, with one graph launch instead
+        of K (the multi-step replay of SURVEY's next steps; the reference replays
+        one step per graph, ``benchmarks/cudagraph.py:751-766``).
+        """
+        k = int(steps_per_graph)
+        if k < 1:
+            raise ValueError("steps_per_graph must be >= 1, got %d" % k)
+        if self.graph is None:
+            self.stream = torch.cuda.Stream(device=self.device)
+            self.stream.wait_stream(torch.cuda.current_stream(self.device))
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=self.stream):
+                self._enqueue_step()
+            torch.cuda.synchronize(self.device)
+            self.graph = graph
+        if k > 1 and (self.graph_multi is None or self.steps_per_graph != k):
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=self.stream):
+                for _ in range(k):
+                    self._enqueue_step()
+            torch.cuda.synchronize(self.device)
+            self.graph_multi = graph
+            self.steps_per_graph = k
+        return {"capture_success": True, "launches_per_step": self.launches_per_step,
+                "steps_per_graph": self.steps_per_graph if self.graph_multi is not None else 1}
 
     def replay(self, n: int = 1, *, synchronize: bool = True) -> Any:
-        """Replay the captured step ``n`` times back to back; returns the last logits."""
+        """Replay the captured step ``n`` times back to back; returns the last logits.
+
+        With a multi-step graph (``capture(steps_per_graph=K)``), ``n // K``
+        replays of it run first, then ``n % K`` one-step replays."""
         if self.graph is None:
             raise RuntimeError("capture() must succeed before replay()")
         n = int(n)
         self._check_room(n)
-        for _ in range(n):
+        k = self.steps_per_graph if self.graph_multi is not None else 1
+        for _ in range(n // k if k > 1 else 0):
+            self.graph_multi.replay()
+        for _ in range(n % k if k > 1 else n):
             self.graph.replay()
         self._host_pos += n
         if synchronize:

@@ -240,6 +240,53 @@ def test_graph_replay_equals_eager_step_bitwise(dev):
     assert torch.equal(sess.logits_cpu(), g_logits)
 
 
+def _kv_equal(a, b) -> bool:
+    return all(torch.equal(x[n], y[n]) for x, y in zip(a, b) for n in x)
+
+
+@pytest.mark.parametrize("prefill_mode", ["batched", "stepped"])
+def test_multi_step_graph_equals_one_step_replays_bitwise(prefill_mode, dev):
+    """capture(steps_per_graph=4): replay(11) runs two 4-step graph launches and
+    three one-step launches; tokens, last logits, position and the whole KV-INT8
+    cache equal those of 11 one-step replays of a second session, bit for bit.
+    The stepped prefill feeds the prompt through the 4-step graph as well."""
+    print("case: multi-step graph, prefill %s" % prefill_mode, flush=True)
+    w = OlmoeW8Weights.random(TINY, seed=7, device=dev)
+    prompt = [1, 5, 17, 300, 2, 999, 42, 7, 11]
+    a = DecodeSession(w, prompt, max_new_tokens=12, num_splits=4)
+    b = DecodeSession(w, prompt, max_new_tokens=12, num_splits=4)
+    info = a.capture(steps_per_graph=4)
+    assert info["steps_per_graph"] == 4
+    assert a.prefill(mode=prefill_mode) == b.prefill(mode=prefill_mode)
+    a.replay(11)
+    for _ in range(11):
+        b.replay(1)
+    assert a.position == b.position == len(prompt) + 11
+    assert a.generated() == b.generated()
+    assert torch.equal(a.logits_cpu(), b.logits_cpu())
+    assert _kv_equal(a.kv_cpu(), b.kv_cpu())
+    with pytest.raises(RuntimeError):
+        a.replay(2)  # past the capacity: refused before anything is enqueued
+
+
+def test_c5_multi_step_graph_equals_one_step_replays_bitwise(c5_model, dev):
+    """The same at the full OLMoE shape after the ctx-1024 batched prefill: two
+    8-step graph launches against 16 one-step replays."""
+    w, _ = c5_model
+    print("case: C5 multi-step graph, ctx 1024", flush=True)
+    a, seed_a = _c5_session(w, 1024)
+    b, seed_b = _c5_session(w, 1024)
+    assert seed_a == seed_b
+    a.capture(steps_per_graph=8)
+    a.replay(16)
+    for _ in range(16):
+        b.replay(1)
+    assert a.position == b.position == 1024 + 16
+    assert a.generated() == b.generated()
+    assert torch.equal(a.logits_cpu(), b.logits_cpu())
+    assert _kv_equal(a.kv_cpu(), b.kv_cpu())
+
+
 def test_prompt_tokens_are_fed_then_greedy_takes_over(dev):
     print("case: prompt feed", flush=True)
     w = OlmoeW8Weights.random(TINY, seed=6, device=dev)
