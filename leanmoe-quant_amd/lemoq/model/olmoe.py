@@ -442,8 +442,8 @@ class DecodeSession:
         graph, which ``replay`` then uses for whole groups of K steps.  Each step
         reads and advances the device's position and token, so a K-step replay
         computes exactly what K one-step replays do, with one graph launch instead
-        of K (the multi-step replay of SURVEY's next steps; the reference replays
-        one step per graph, ``benchmarks/cudagraph.py:751-766``).
+        of K (the reference replays one step per graph and synchronises after
+        each, ``benchmarks/cudagraph.py:751-766``).
         """
         k = int(steps_per_graph)
         if k < 1:
