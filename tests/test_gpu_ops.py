@@ -434,6 +434,29 @@ def test_rmsnorm_vs_hf_formula(rows, H, dev):
     assert (got.double() - ref.double()).abs().gt(0).float().mean() < 0.01
 
 
+@pytest.mark.parametrize("rows,H,offset", [(3, 1003, 0), (4, 2048, 1), (2, 8192, 0)],
+                         ids=["odd-width", "misaligned-rows", "widest"])
+def test_rmsnorm_element_path_and_widest_rows(rows, H, offset, dev):
+    """Rows that are not 16-byte chunks (odd width, or an input one element off
+    alignment) take the per-element path; 8192-wide rows are the 16-byte path's
+    widest.  Both against the oracle's RMSNorm."""
+    from lemoq import _hip
+
+    print("case: rmsnorm rows=%d H=%d offset=%d" % (rows, H, offset), flush=True)
+    x = randn(rows, H, seed=H + offset).to(torch.float16)
+    w = (torch.rand(H, generator=torch.Generator().manual_seed(H + 2)) + 0.5).to(torch.float16)
+    xbuf = torch.zeros(rows * H + 8, dtype=torch.float16, device=dev)
+    xd = xbuf[offset:offset + rows * H].view(rows, H)
+    xd.copy_(x.to(dev))
+    y = torch.empty((rows, H), dtype=torch.float16, device=dev)
+    wd = w.to(dev)
+    _hip.call("lemoq_rmsnorm", _hip.ptr(xd), rows, H, _hip.ptr(wd), 1e-5, _hip.ptr(y), _hip.stream_of(dev))
+    got = y.cpu()
+    ref = ops.rms_norm(x, w, 1e-5)
+    assert_close(got, ref, rtol=1e-3, atol=1e-3, what="rmsnorm H=%d offset=%d" % (H, offset))
+    assert (got.double() - ref.double()).abs().gt(0).float().mean() < 0.01
+
+
 @pytest.mark.parametrize("pos", [0, 1, 1024, 4096])
 def test_rope_fused_vs_oracle(pos, dev):
     from lemoq.kernels.rope import apply_rotary_pos_emb_fused, rotary_cos_sin
