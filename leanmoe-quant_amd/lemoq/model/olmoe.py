@@ -345,6 +345,11 @@ class DecodeSession:
     # ------------------------------------------------------------------ state
     def reset(self) -> None:
         """Back to position 0 with the first prompt token (cache slots are overwritten as it runs)."""
+        self._reset_device_state()
+        torch.cuda.synchronize(self.device)
+
+    def _reset_device_state(self) -> None:
+        """The device side of ``reset``, enqueued on the current stream (no synchronisation)."""
         self.token.copy_(self.prompt[:1])
         self.pos.zero_()
         self.filled.fill_(1)
@@ -352,7 +357,6 @@ class DecodeSession:
         self.history[:1].copy_(self.prompt[:1])
         self.sync.zero_()
         self._host_pos = 0
-        torch.cuda.synchronize(self.device)
 
     def check_sync_status(self) -> None:
         """Raise if a cross-workgroup wait of a fused launch gave up since the last
@@ -499,7 +503,9 @@ class DecodeSession:
         """
         if self.graph is None:
             self.capture()
-        self.reset()
+        # stream order keeps the reset ahead of the prefill's launches; the
+        # seed token's read below synchronises once at the end
+        self._reset_device_state()
         if mode == "stepped":
             self.replay(self.ctx)  # advances the host-side position to ctx
         elif mode == "batched":
@@ -512,7 +518,6 @@ class DecodeSession:
             _hip.call("lemoq_argmax_advance", _hip.ptr(self.logits), self.shape.vocab, _hip.ptr(self.token),
                       _hip.ptr(self.pos), _hip.ptr(self.filled), _hip.ptr(self.prompt), self.ctx,
                       _hip.ptr(self.history), int(self.history.numel()), _hip.stream_of(self.device))
-            torch.cuda.synchronize(self.device)
             self._host_pos = self.ctx
         else:
             raise ValueError("prefill mode must be 'batched' or 'stepped', got %r" % (mode,))
