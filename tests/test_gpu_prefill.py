@@ -105,9 +105,12 @@ def test_qk_norm_rope_rows_vs_oracle(D, dev):
 
 # (T, head_dim, heads).  Fewer than 512 blocks of 128 queries take the key-split
 # kernel (64 queries per block, each tile's keys split between wave pairs); the
-# (777, 128, 80) and (300, 64, 200) cases take the unsplit one.
+# (777, 128, 80), (300, 64, 200) and (2048, 128, 32) cases take the unsplit one
+# on the paired grid (an even number of heads; 2048 x 32 heads is 512 blocks,
+# the whole grid resident as at ctx 4096 with 16 heads), (1024, 128, 65) on the
+# two-dimensional grid (an odd number of heads).
 ATTN_CASES = [(1, 128, 3), (7, 64, 3), (64, 128, 3), (129, 128, 3), (300, 256, 3), (2048, 128, 2),
-              (777, 128, 80), (300, 64, 200)]
+              (777, 128, 80), (300, 64, 200), (2048, 128, 32), (1024, 128, 65)]
 
 
 @pytest.mark.parametrize("T,D,NH", ATTN_CASES, ids=["T%d-D%d-H%d" % c for c in ATTN_CASES])
