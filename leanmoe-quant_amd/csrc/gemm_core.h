@@ -4,11 +4,10 @@
 // v_mfma_f32_32x32x16_f16; X rows fp16, W rows either w8 (int8 codes + fp16
 // per-group scales, dequantised to fp16(code * scale) once per block as the
 // tile is written to LDS) or fp16.  K advances in stages of 64: the global
-// loads of stage s+1 are issued into registers before the matrix ops of stage
-// s, then written to the other half of a double-buffered LDS tile; one
-// barrier per stage.  Loads are never under a branch: the prefetch of the
-// stage after the last re-reads the last stage (clamped k) into the unused
-// buffer.
+// loads of a stage are issued into registers two stages ahead, then written
+// to the other half of a double-buffered LDS tile while the current stage's
+// matrix ops run; one barrier per stage.  Loads are never under a branch: the
+// prefetches past the last stage re-read the last stage (clamped k).
 //
 // Operand layout of v_mfma_f32_32x32x16_f16 (verified on the device): lane l
 // holds row (A) / column (B) l % 32 and 8 k-values of the lane half l / 32;
@@ -143,100 +142,65 @@ __device__ __forceinline__ void stage_store(const Staged<TL, W8>& st, uint16_t* 
   }
 }
 
-// The matrix ops of one stage for a wave: A fragments at tile rows
-// a_row0 + 32 i, B fragments at tile rows b_row0[j].
+// A wave's fragments of one stage: for each 32-k chunk c, A fragments at
+// tile rows a_row0 + 32 i and B fragments at tile rows b_row0[j], two 16-byte
+// LDS reads each.
 template <class TL>
-__device__ __forceinline__ void stage_mma(Acc<TL::FM, TL::FN>& acc, const uint16_t* buf, int a_row0,
-                                          const int (&b_row0)[TL::FN], int l32, int half) {
+struct Frags {
+  u32x4 a[BK / 32][TL::FM][2], b[BK / 32][TL::FN][2];
+};
+
+template <class TL>
+__device__ __forceinline__ void stage_frags(Frags<TL>& f, const uint16_t* buf, int a_row0,
+                                            const int (&b_row0)[TL::FN], int l32, int half) {
   const uint16_t* As = buf;
   const uint16_t* Bs = buf + TL::BM * LDS_PITCH;
 #pragma unroll
   for (int c = 0; c < BK / 32; ++c) {
-    u32x4 a[TL::FM][2], b[TL::FN][2];
 #pragma unroll
     for (int i = 0; i < TL::FM; ++i) {
       const uint16_t* p = As + (a_row0 + 32 * i + l32) * LDS_PITCH + 32 * c + 16 * half;
-      a[i][0] = *reinterpret_cast<const u32x4*>(p);
-      a[i][1] = *reinterpret_cast<const u32x4*>(p + 8);
+      f.a[c][i][0] = *reinterpret_cast<const u32x4*>(p);
+      f.a[c][i][1] = *reinterpret_cast<const u32x4*>(p + 8);
     }
 #pragma unroll
     for (int j = 0; j < TL::FN; ++j) {
       const uint16_t* p = Bs + (b_row0[j] + l32) * LDS_PITCH + 32 * c + 16 * half;
-      b[j][0] = *reinterpret_cast<const u32x4*>(p);
-      b[j][1] = *reinterpret_cast<const u32x4*>(p + 8);
+      f.b[c][j][0] = *reinterpret_cast<const u32x4*>(p);
+      f.b[c][j][1] = *reinterpret_cast<const u32x4*>(p + 8);
     }
+  }
+}
+
+template <class TL>
+__device__ __forceinline__ void stage_mfma(Acc<TL::FM, TL::FN>& acc, const Frags<TL>& f) {
+#pragma unroll
+  for (int c = 0; c < BK / 32; ++c)
 #pragma unroll
     for (int i = 0; i < TL::FM; ++i)
 #pragma unroll
       for (int j = 0; j < TL::FN; ++j) {
-        acc.v[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(h8_of(a[i][0]), h8_of(b[j][0]), acc.v[i][j], 0, 0, 0);
-        acc.v[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(h8_of(a[i][1]), h8_of(b[j][1]), acc.v[i][j], 0, 0, 0);
+        acc.v[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(h8_of(f.a[c][i][0]), h8_of(f.b[c][j][0]), acc.v[i][j], 0, 0, 0);
+        acc.v[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(h8_of(f.a[c][i][1]), h8_of(f.b[c][j][1]), acc.v[i][j], 0, 0, 0);
       }
-  }
 }
 
-// Whole K loop of a block, global loads two stages ahead: while stage s is
-// computed from LDS, the loads of stage s + 1 wait in one register set
-// (issued a stage earlier) to be written to LDS, and those of stage s + 2
-// are in flight into the other.  One barrier per stage as in block_mainloop,
-// which it computes bit for bit.  It holds twice the staging registers; on
-// the MoE grouped GEMMs (gfx950, 8 waves, 244 registers, two waves per SIMD)
-// it takes 393-417 us against 412-530 us for one stage ahead, whose time
-// varied more from box to box.
+// Whole K loop of a block, global loads two stages ahead.  Stage s sits in
+// one LDS buffer, the loads of stage s + 1 in one register set (issued a
+// stage earlier) and those of stage s + 2 go into the other.  A stage body:
+// the wave reads all its fragments of stage s from LDS, writes stage s + 1
+// (dequantised) to the other buffer, issues the loads of stage s + 2, then
+// runs its matrix ops; one barrier per stage.  With the fragment reads and
+// the stores ahead of the matrix ops the compiler places the dequantisation
+// and the LDS writes between the matrix ops, and the matrix ops no longer
+// wait on fragment reads issued in the middle of the stage: the grouped
+// gate/up GEMM at the ctx-4096 shape went from 435-480 to 405-440 us with
+// bit-identical outputs.  Loads two stages ahead instead of one took the
+// same GEMM from 412-530 to 393-417 us (gfx950, 8 waves, two per SIMD).
 template <class TL, bool W8>
 __device__ __forceinline__ void block_mainloop2(Acc<TL::FM, TL::FN>& acc, const Sources<TL, W8>& src,
                                                 int64_t K, int group, uint16_t* lds, int a_row0,
                                                 const int (&b_row0)[TL::FN]) {
-  const int t = threadIdx.x, lane = t & 63;
-  const int half = lane >> 5, l32 = lane & 31;
-#pragma unroll
-  for (int i = 0; i < TL::FM; ++i)
-#pragma unroll
-    for (int j = 0; j < TL::FN; ++j) acc.v[i][j] = (f32x16){};
-  const int nst = (int)(K / BK);
-  const int spg = W8 ? group / BK : 1;
-  auto sidx_of = [&](int p) { return W8 ? p / spg : 0; };  // outside the loop only
-  int gi = 0, gc = 0;  // scale index and stage within the group of stage p (advanced below)
-  auto advance = [&]() {
-    if (++gc == spg) gc = 0, ++gi;
-  };
-  const int last = nst - 1;
-  const int last_sidx = sidx_of(last);
-  Staged<TL, W8> s0, s1;
-  stage_load<TL, W8>(s0, src, 0, 0);
-  advance();  // stage 1
-  stage_load<TL, W8>(s1, src, (int64_t)(1 < nst ? 1 : 0) * BK, 1 < nst ? gi : 0);
-  advance();  // stage 2
-  stage_store<TL, W8>(s0, lds, t);
-  __syncthreads();
-  for (int s = 0; s < nst; s += 2) {
-    // stage s in LDS buffer 0, s1 holds stage s + 1
-    {
-      const bool more = s + 2 < nst;
-      stage_load<TL, W8>(s0, src, (int64_t)(more ? s + 2 : last) * BK, more ? gi : last_sidx);
-      advance();
-      stage_mma<TL>(acc, lds, a_row0, b_row0, l32, half);
-      stage_store<TL, W8>(s1, lds + TL::LDS_HALF, t);
-      __syncthreads();
-    }
-    if (s + 1 >= nst) break;
-    // stage s + 1 in LDS buffer 1, s0 holds stage s + 2
-    {
-      const bool more = s + 3 < nst;
-      stage_load<TL, W8>(s1, src, (int64_t)(more ? s + 3 : last) * BK, more ? gi : last_sidx);
-      advance();
-      stage_mma<TL>(acc, lds + TL::LDS_HALF, a_row0, b_row0, l32, half);
-      stage_store<TL, W8>(s0, lds, t);
-      __syncthreads();
-    }
-  }
-}
-
-// Whole K loop of a block.  K % 64 == 0; lds holds TL::LDS_ELEMS fp16.
-template <class TL, bool W8>
-__device__ __forceinline__ void block_mainloop(Acc<TL::FM, TL::FN>& acc, const Sources<TL, W8>& src,
-                                               int64_t K, int group, uint16_t* lds, int a_row0,
-                                               const int (&b_row0)[TL::FN]) {
   const int t = threadIdx.x, lane = t & 63;
   const int half = lane >> 5, l32 = lane & 31;
 #pragma unroll
@@ -248,21 +212,43 @@ __device__ __forceinline__ void block_mainloop(Acc<TL::FM, TL::FN>& acc, const S
   // loop would cost about a hundred scalar instructions per stage.
   const int nst = (int)(K / BK);
   const int spg = W8 ? group / BK : 1;
-  const int last_sidx = W8 ? (nst - 1) / spg : 0;  // the clamped prefetch re-reads stage nst - 1
-  int gi = 0, gc = 0;                              // scale index and stage within the group
-  Staged<TL, W8> st;
-  stage_load<TL, W8>(st, src, 0, 0);
-  stage_store<TL, W8>(st, lds, t);
-  __syncthreads();
-  if (++gc == spg) gc = 0, ++gi;                   // now at stage 1
-  for (int s = 0; s < nst; ++s) {
-    const bool more = s + 1 < nst;
-    const int64_t kn = (int64_t)(more ? s + 1 : s) * BK;  // clamped prefetch
-    stage_load<TL, W8>(st, src, kn, more ? gi : last_sidx);
-    stage_mma<TL>(acc, lds + (s & 1) * TL::LDS_HALF, a_row0, b_row0, l32, half);
-    stage_store<TL, W8>(st, lds + ((s + 1) & 1) * TL::LDS_HALF, t);
-    __syncthreads();
+  int gi = 0, gc = 0;  // scale index and stage within the group of the next stage loaded
+  auto advance = [&]() {
     if (++gc == spg) gc = 0, ++gi;
+  };
+  const int last = nst - 1;
+  const int last_sidx = W8 ? last / spg : 0;  // the clamped prefetch re-reads stage nst - 1
+  Staged<TL, W8> s0, s1;
+  stage_load<TL, W8>(s0, src, 0, 0);
+  advance();  // stage 1
+  stage_load<TL, W8>(s1, src, (int64_t)(1 < nst ? 1 : 0) * BK, 1 < nst ? gi : 0);
+  advance();  // stage 2
+  stage_store<TL, W8>(s0, lds, t);
+  __syncthreads();
+  for (int s = 0; s < nst; s += 2) {
+    // stage s in LDS buffer 0, s1 holds stage s + 1
+    {
+      const bool more = s + 2 < nst;
+      Frags<TL> f;
+      stage_frags<TL>(f, lds, a_row0, b_row0, l32, half);
+      stage_store<TL, W8>(s1, lds + TL::LDS_HALF, t);
+      stage_load<TL, W8>(s0, src, (int64_t)(more ? s + 2 : last) * BK, more ? gi : last_sidx);
+      advance();
+      stage_mfma<TL>(acc, f);
+      __syncthreads();
+    }
+    if (s + 1 >= nst) break;
+    // stage s + 1 in LDS buffer 1, s0 holds stage s + 2
+    {
+      const bool more = s + 3 < nst;
+      Frags<TL> f;
+      stage_frags<TL>(f, lds + TL::LDS_HALF, a_row0, b_row0, l32, half);
+      stage_store<TL, W8>(s0, lds, t);
+      stage_load<TL, W8>(s1, src, (int64_t)(more ? s + 3 : last) * BK, more ? gi : last_sidx);
+      advance();
+      stage_mfma<TL>(acc, f);
+      __syncthreads();
+    }
   }
 }
 
