@@ -585,9 +585,19 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const void* __restrict_
     const int idx = lane + 64 * i;
     if (idx < E) {
       if (kind == kLogitsSplitK) {
+        // The planes' loads are all issued before the first add (a load per
+        // loop trip would make each plane one more dependent memory round
+        // trip); the sum stays in plane order from 0.
         const float* pp = reinterpret_cast<const float*>(logits) + t * stride + idx;
+        constexpr int NP = 8;
+        float pv[NP];
+#pragma unroll
+        for (int zz = 0; zz < NP; ++zz) pv[zz] = zz < splits ? pp[(int64_t)zz * T * stride] : 0.0f;
         float v = 0.0f;
-        for (int zz = 0; zz < splits; ++zz) v += pp[(int64_t)zz * T * stride];
+#pragma unroll
+        for (int zz = 0; zz < NP; ++zz)
+          if (zz < splits) v += pv[zz];
+        for (int zz = NP; zz < splits; ++zz) v += pp[(int64_t)zz * T * stride];
         z[i] = h2f(f2h(v));
       } else {
         z[i] = kind == kLogitsF16 ? h2f(reinterpret_cast<const uint16_t*>(logits)[t * stride + idx])

@@ -46,6 +46,7 @@ constexpr int MAX_EXPERTS = 255;  // expert ids are bytes; 255 marks an invalid 
 // ---------------------------------------------------------------------------
 constexpr int SORT_THREADS = 1024;
 constexpr int SORT_WAVES = SORT_THREADS / 64;
+constexpr int RUN4 = (MAX_PAIRS / 4 + SORT_THREADS - 1) / SORT_THREADS;  // words of 4 pairs per thread, at most
 
 __global__ __launch_bounds__(SORT_THREADS) void moe_sort_kernel(const int64_t* __restrict__ top_i,
                                                                 const float* __restrict__ top_w, int P,
@@ -58,16 +59,34 @@ __global__ __launch_bounds__(SORT_THREADS) void moe_sort_kernel(const int64_t* _
   __shared__ int whist[SORT_WAVES][256];
   __shared__ int hist[256];
   __shared__ int wave_tot[SORT_WAVES];
-  __shared__ int s_off, s_toff;
+  __shared__ int ex_off[257], ex_toff[257];  // exclusive prefixes over the experts; [256] the totals
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int me = blockIdx.x;
+  // Each thread owns a run of at most RUN4 words of 4 pairs (placement below).
+  const int P4 = (P + 3) / 4;
+  const int chunk4 = (P4 + SORT_THREADS - 1) / SORT_THREADS;
+  const int beg4 = min(P4, tid * chunk4), end4 = min(P4, beg4 + chunk4);
   for (int i = lane; i < 256; i += 64) whist[wave][i] = 0;
   __syncthreads();
-  for (int p = tid; p < P; p += SORT_THREADS) {
-    const int64_t e = top_i[p];
-    const bool ok = e >= 0 && e < E;
-    ids[p] = ok ? (uint8_t)e : (uint8_t)255;
-    if (ok) atomicAdd(&whist[wave][(int)e], 1);
+  // The ids are loaded 8 per thread at a time (a load per loop trip would
+  // make each of the thread's P / 1024 ids one more dependent memory round
+  // trip).
+  constexpr int IB = 8;
+  for (int j0 = 0; SORT_THREADS * j0 < P; j0 += IB) {
+    int64_t ev[IB];
+#pragma unroll
+    for (int j = 0; j < IB; ++j) {
+      const int p = tid + SORT_THREADS * (j0 + j);
+      ev[j] = p < P ? top_i[p] : -1;
+    }
+#pragma unroll
+    for (int j = 0; j < IB; ++j) {
+      const int p = tid + SORT_THREADS * (j0 + j);
+      if (p >= P) break;
+      const bool ok = ev[j] >= 0 && ev[j] < E;
+      ids[p] = ok ? (uint8_t)ev[j] : (uint8_t)255;
+      if (ok) atomicAdd(&whist[wave][(int)ev[j]], 1);
+    }
   }
   // pad the byte array to a multiple of 4 with invalid ids
   if (tid < 4 && P + tid < ((P + 3) & ~3)) ids[P + tid] = 255;
@@ -79,44 +98,56 @@ __global__ __launch_bounds__(SORT_THREADS) void moe_sort_kernel(const int64_t* _
     hist[tid] = c;
   }
   __syncthreads();
-  if (tid == 0) {
-    int off = 0, toff = 0;
-    for (int e = 0; e < me; ++e) {
-      off += hist[e];
-      toff += (hist[e] + TILE_ROWS - 1) / TILE_ROWS;
+  // Exclusive prefix sums over the experts of the pair counts and of the tile
+  // counts, by wave 0 (lane l owns experts 4l .. 4l + 3): one wave scan
+  // instead of a serial loop over the experts.
+  if (wave == 0) {
+    int c[4], tc[4], cs = 0, ts = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int e = 4 * lane + j;
+      c[j] = e < E ? hist[e] : 0;
+      tc[j] = (c[j] + TILE_ROWS - 1) / TILE_ROWS;
+      cs += c[j];
+      ts += tc[j];
     }
-    s_off = off;
-    s_toff = toff;
-    if (me == 0) {
-      int o = 0, t = 0;
-      for (int e = 0; e < E; ++e) {
-        expert_off[e] = o;
-        o += hist[e];
-        t += (hist[e] + TILE_ROWS - 1) / TILE_ROWS;
-      }
-      expert_off[E] = o;
-      for (int i = t; i < max_tiles; ++i) tiles[4 * i] = -1;
+    int ci = cs, ti = ts;  // inclusive scans over the lanes
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int a = __shfl_up(ci, d, 64), b = __shfl_up(ti, d, 64);
+      if (lane >= d) ci += a, ti += b;
     }
+    int o = ci - cs, t = ti - ts;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      ex_off[4 * lane + j] = o;
+      ex_toff[4 * lane + j] = t;
+      o += c[j];
+      t += tc[j];
+    }
+    if (lane == 63) ex_off[256] = o, ex_toff[256] = t;  // totals
   }
   __syncthreads();
-  const int cnt = hist[me], off = s_off;
+  if (me == 0) {
+    for (int e = tid; e <= E; e += SORT_THREADS) expert_off[e] = ex_off[e < E ? e : 256];
+    for (int i = ex_toff[256] + tid; i < max_tiles; i += SORT_THREADS) tiles[4 * i] = -1;
+  }
+  const int cnt = hist[me], off = ex_off[me];
   const int ntiles = (cnt + TILE_ROWS - 1) / TILE_ROWS;
   for (int i = tid; i < ntiles; i += SORT_THREADS) {
-    int32_t* t = tiles + 4 * (s_toff + i);
+    int32_t* t = tiles + 4 * (ex_toff[me] + i);
     t[0] = me;
     t[1] = off + i * TILE_ROWS;
     t[2] = off + min(cnt, (i + 1) * TILE_ROWS);
     t[3] = 0;
   }
-  // runs of a multiple of 4 pairs per thread
-  const int P4 = (P + 3) / 4;
-  const int chunk4 = (P4 + SORT_THREADS - 1) / SORT_THREADS;
-  const int beg4 = min(P4, tid * chunk4), end4 = min(P4, beg4 + chunk4);
   const uint32_t* ids4 = reinterpret_cast<const uint32_t*>(ids);
   const uint32_t mev = (uint32_t)me * 0x01010101u;
   int c = 0;
-  for (int i = beg4; i < end4; ++i) {
-    const uint32_t x = ids4[i] ^ mev;  // a zero byte marks a match
+#pragma unroll
+  for (int i = 0; i < RUN4; ++i) {
+    if (beg4 + i >= end4) break;
+    const uint32_t x = ids4[beg4 + i] ^ mev;  // a zero byte marks a match
 #pragma unroll
     for (int b = 0; b < 4; ++b) c += ((x >> (8 * b)) & 0xFFu) == 0u;
   }
@@ -130,15 +161,28 @@ __global__ __launch_bounds__(SORT_THREADS) void moe_sort_kernel(const int64_t* _
   __syncthreads();
   int pos = off + incl - c;
   for (int w = 0; w < wave; ++w) pos += wave_tot[w];
-  for (int i = beg4; i < end4; ++i) {
-    const uint32_t x = ids4[i] ^ mev;
+  // The routing weights of the run's matches are all loaded before the first
+  // store (one load per matching pair, issued back to back).
+  uint32_t xm[RUN4];
+  float wrun[4 * RUN4];
+#pragma unroll
+  for (int i = 0; i < RUN4; ++i) {
+    xm[i] = beg4 + i < end4 ? ids4[beg4 + i] ^ mev : 0xFFFFFFFFu;
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
-      if (((x >> (8 * b)) & 0xFFu) != 0u) continue;
-      const int p = 4 * i + b;
+      const bool hit = ((xm[i] >> (8 * b)) & 0xFFu) == 0u;
+      wrun[4 * i + b] = hit ? top_w[4 * (beg4 + i) + b] : 0.0f;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < RUN4; ++i) {
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      if (((xm[i] >> (8 * b)) & 0xFFu) != 0u) continue;
+      const int p = 4 * (beg4 + i) + b;
       pair_tok[pos] = p / top_k;
       pair_src[pos] = p;
-      pair_w[pos] = f2h(top_w[p]);
+      pair_w[pos] = f2h(wrun[4 * i + b]);
       ++pos;
     }
   }

@@ -200,7 +200,8 @@ def test_gemm_f16_splitk_one_split_ignores_the_workspace(dev):
 
 
 @pytest.mark.parametrize("m,n,k,splits,top_k,norm", [(1000, 64, 2048, 8, 8, False), (37, 64, 2048, 4, 8, True),
-                                                     (1, 16, 256, 2, 4, False), (300, 128, 4096, 8, 8, True)])
+                                                     (1, 16, 256, 2, 4, False), (300, 128, 4096, 8, 8, True),
+                                                     (50, 64, 3072, 12, 8, False)])
 def test_route_topk_of_splitk_partials(m, n, k, splits, top_k, norm, dev):
     """The router's partials-only split-K GEMM followed by the routing that sums them gives the
     same ids and weights, bit for bit, as the GEMM's own finish followed by lemoq_route_topk, and
