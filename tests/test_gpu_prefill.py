@@ -218,6 +218,59 @@ def test_moe_prefill_vs_oracle(T, H, F, E, K, skew, dev):
     assert_close(out.cpu(), ref, what="moe_prefill T=%d" % T)
 
 
+SORT_CASES = [(4096, 8, 64, "uniform"), (4096, 8, 64, "bench"), (1537, 3, 64, "uniform"), (2500, 8, 200, "skew"),
+              (1, 1, 4, "uniform")]
+
+
+@pytest.mark.parametrize("T,K,E,kind", SORT_CASES, ids=["T%d-k%d-E%d-%s" % c for c in SORT_CASES])
+def test_moe_sort_exact(T, K, E, kind, dev):
+    """The expert sort at the largest pair counts (several id batches per thread, the whole
+    byte table in LDS) and ragged ones (pairs not a multiple of 4): the stable order, the
+    fp16 routing weights, the expert offsets and the tile table, exactly.  "bench" routes
+    every token to the same K experts (the bench's repeated prompt), "skew" half of them."""
+    from lemoq import _hip
+
+    print("case: moe_sort T=%d K=%d E=%d %s" % (T, K, E, kind), flush=True)
+    g = torch.Generator().manual_seed(T * K + E)
+    if kind == "bench":
+        ti = torch.arange(K, dtype=torch.int64).repeat(T, 1) * 3 % E
+    else:
+        ti = torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(T)]).to(torch.int64)
+        if kind == "skew":
+            ti[: T // 2] = torch.arange(K, dtype=torch.int64)
+    tw = torch.rand((T, K), generator=g)
+    pairs = T * K
+    lib = _hip.load()
+    mt = int(lib.lemoq_moe_prefill_max_tiles(pairs, E))
+    i32 = dict(dtype=torch.int32, device=dev)
+    pair_tok, pair_src = torch.full((pairs,), -5, **i32), torch.full((pairs,), -5, **i32)
+    pair_w = torch.empty((pairs,), dtype=torch.float16, device=dev)
+    expert_off = torch.full((E + 1,), -5, **i32)
+    tiles = torch.full((mt, 4), -7, **i32)
+    P, st = _hip.ptr, _hip.stream_of(dev)
+    tid, twd = ti.to(dev), tw.to(dev)
+    _hip.call("lemoq_moe_prefill_sort", P(tid), P(twd), T, K, E, P(pair_tok), P(pair_src), P(pair_w),
+              P(expert_off), P(tiles), mt, st)
+    torch.cuda.synchronize()
+    flat = ti.reshape(-1)
+    order = torch.from_numpy(np.argsort(flat.numpy(), kind="stable")).to(torch.int64)
+    assert torch.equal(pair_src.cpu().to(torch.int64), order)
+    assert torch.equal(pair_tok.cpu().to(torch.int64), order // K)
+    assert torch.equal(pair_w.cpu(), tw.reshape(-1)[order].to(torch.float16))
+    counts = torch.bincount(flat, minlength=E)
+    assert expert_off.cpu().tolist() == [0] + torch.cumsum(counts, 0).tolist()
+    tl = tiles.cpu()
+    live = tl[tl[:, 0] >= 0]
+    assert int((tl[:, 0] == -1).sum()) == mt - live.shape[0]
+    assert live.shape[0] == int(((counts + 127) // 128).sum())
+    sorted_ids = flat[order]
+    covered = torch.zeros((pairs,), dtype=torch.int64)
+    for e_, b, en, _ in live.tolist():
+        assert 0 < en - b <= 128 and int(sorted_ids[b]) == e_ and int(sorted_ids[en - 1]) == e_
+        covered[b:en] += 1
+    assert bool((covered == 1).all())
+
+
 COMBINE_NORM_CASES = [(1, 2048, 8, True), (77, 2048, 8, True), (513, 4096, 2, True), (40, 8192, 8, False),
                       (9, 264, 4, True)]
 
