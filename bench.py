@@ -993,8 +993,9 @@ def main(argv=None) -> int:
 
 # Launch order of one batched prefill (lemoq.model.prefill.prefill_prompt):
 # gather, layer 0's input norm, 16 x [11 launches] (each layer's combine but the
-# last also writes the next layer's input norm), final norm, lm_head GEMM, then
-# the greedy pick; each role with the kernel-name fragment its dispatch must carry.
+# last also writes the next layer's input norm), the lm_head GEMV of the last row
+# (final norm in its prologue), then the greedy pick; each role with the
+# kernel-name fragment its dispatch must carry.
 PREFILL_HEAD_ROLES = (("gather_rows", "gather_rows_kernel"), ("rmsnorm (input, layer 0)", "rmsnorm_kernel"))
 PREFILL_LAYER_ROLES = (("gemm_w8 qkv", "gemm_kernel<true"),
                        ("qk_rows (q/k norm, RoPE, KV-INT8)", "qk_rows_kernel"), ("attn_prefill", "attn_prefill_kernel"),
@@ -1005,7 +1006,7 @@ PREFILL_LAYER_ROLES = (("gemm_w8 qkv", "gemm_kernel<true"),
                        ("moe_prefill_down", "moe_down_kernel"))
 PREFILL_COMBINE_NORM = ("moe_prefill_combine (+residual, next input norm)", "moe_combine_kernel<true")
 PREFILL_COMBINE_LAST = ("moe_prefill_combine (+residual)", "moe_combine_kernel<false")
-PREFILL_TAIL_ROLES = (("rmsnorm (final)", "rmsnorm_kernel"), ("gemm_w8 lm_head (last row)", "gemm_kernel<true"),
+PREFILL_TAIL_ROLES = (("gemv_w8 lm_head (last row, + final norm)", "gemv_w8_kernel"),
                       ("argmax_advance", "argmax_advance_kernel"))
 
 
@@ -1027,7 +1028,7 @@ def prefill_flops(role: str, T: int, shape=None) -> float:
         "attn_prefill": 4.0 * NH * D * T * (T + 1) / 2,
         "moe_prefill_gate_up": 2.0 * T * K * 2 * F * H,
         "moe_prefill_down": 2.0 * T * K * H * F,
-        "gemm_w8 lm_head (last row)": 2.0 * V * H,
+        "gemv_w8 lm_head (last row, + final norm)": 2.0 * V * H,
     }.get(role, 0.0)
 
 

@@ -125,6 +125,19 @@ int lemoq_lm_head_argmax_w8(const uint16_t* x, const uint16_t* norm_w, float eps
                             int32_t* part_idx, int64_t part_len, int64_t* token, int64_t* pos,
                             int32_t* filled, const int64_t* prompt, int64_t prompt_len,
                             int64_t* history, int64_t history_len, void* stream);
+/* The same two launches with the lm_head arithmetic of the multi-token
+ * QuantLinear arm (src/lemoq/quant/linear.py:420-434, :365-395): each weight
+ * rounded to fp16(code * scale) before fp32 dot products, as the prefill's
+ * F.linear over the dequantised lm_head computes the last position's logits
+ * (the prefill forward, benchmarks/cudagraph.py:578-599), followed by the
+ * greedy pick of the seed token.  Arguments and errors as
+ * lemoq_lm_head_argmax_w8. */
+int lemoq_lm_head_argmax_w8_dq(const uint16_t* x, const uint16_t* norm_w, float eps,
+                               const int8_t* codes, const uint16_t* scale, int64_t N, int64_t K,
+                               int64_t group, uint16_t* logits, float* part_val,
+                               int32_t* part_idx, int64_t part_len, int64_t* token, int64_t* pos,
+                               int32_t* filled, const int64_t* prompt, int64_t prompt_len,
+                               int64_t* history, int64_t history_len, void* stream);
 /* Number of argmax partials lemoq_lm_head_argmax_w8 writes for N rows. */
 int64_t lemoq_lm_head_argmax_parts(int64_t N);
 

@@ -335,6 +335,31 @@ __device__ __forceinline__ float w8_row_dot(const W8Tile<R, KCH>& t, int r, cons
   return a;
 }
 
+// sum_j x_j . fp16(codes_j * scale_j) for row r of the tile: the weights
+// rounded to fp16 first, as a multi-token linear's dequantise-then-GEMM does
+// (fp16(code * scale) with one rounding: the code is exact in fp16 and the
+// fp16 multiply rounds the product once), then fp32 dot products.
+template <int R, int KCH>
+__device__ __forceinline__ float w8_row_dot_dq(const W8Tile<R, KCH>& t, int r, const XChunk (&xc)[KCH]) {
+  float a = 0.0f;
+  const f16x2 bias = {(f16)1152.0f, (f16)1152.0f};
+#pragma unroll
+  for (int j = 0; j < KCH; ++j) {
+    if (!((t.ok >> (r * KCH + j)) & 1u)) continue;
+    const f16x2 sc = as_h2((uint32_t)t.s[r][j] * 0x10001u);
+    const uint32_t cw[4] = {t.c[r][j].x, t.c[r][j].y, t.c[r][j].z, t.c[r][j].w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t u = cw[i] ^ 0x80808080u;
+      const f16x2 wlo = (as_h2(__builtin_amdgcn_perm(0x64646464u, u, 0x04020400u)) - bias) * sc;
+      const f16x2 whi = (as_h2(__builtin_amdgcn_perm(0x64646464u, u, 0x04030401u)) - bias) * sc;
+      a = __builtin_amdgcn_fdot2(wlo, xc[j].a[i], a, false);
+      a = __builtin_amdgcn_fdot2(whi, xc[j].b[i], a, false);
+    }
+  }
+  return a;
+}
+
 // The activation slice of one lane: 16 fp16 values per 1 KB chunk, raw bits.
 template <int KCH>
 struct XRaw {

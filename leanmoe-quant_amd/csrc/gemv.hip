@@ -42,6 +42,7 @@ struct GemvArgs {
 
 constexpr int kArgmaxPlain = 0;
 constexpr int kArgmaxPartials = 1;
+constexpr int kArgmaxPartialsDq = 2;  // as kArgmaxPartials, weights rounded to fp16 before the dot
 template <int KCH, int R, int MODE, bool EXACT>
 __global__ __launch_bounds__(256) void gemv_w8_kernel(const GemvArgs a) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -159,7 +160,8 @@ __global__ __launch_bounds__(256) void gemv_w8_kernel(const GemvArgs a) {
 
   float acc[R];
 #pragma unroll
-  for (int r = 0; r < R; ++r) acc[r] = wave_sum(w8_row_dot<R, KCH>(t, r, xc));
+  for (int r = 0; r < R; ++r)
+    acc[r] = wave_sum(MODE == kArgmaxPartialsDq ? w8_row_dot_dq<R, KCH>(t, r, xc) : w8_row_dot<R, KCH>(t, r, xc));
 
   if (MODE == kArgmaxPlain) {
     if (lane < R) {
@@ -688,13 +690,13 @@ extern "C" int lemoq_gemv_w8_fused(const uint16_t* x_src, const int64_t* x_row_i
       1);
 }
 
-extern "C" int lemoq_lm_head_argmax_w8(const uint16_t* x, const uint16_t* norm_w, float eps,
-                                       const int8_t* codes, const uint16_t* scale, int64_t N,
-                                       int64_t K, int64_t group, uint16_t* logits,
-                                       float* part_val, int32_t* part_idx, int64_t part_len,
-                                       int64_t* token, int64_t* pos, int32_t* filled,
-                                       const int64_t* prompt, int64_t prompt_len,
-                                       int64_t* history, int64_t history_len, void* stream) {
+namespace {
+template <int MODE>
+int lm_head_argmax(const uint16_t* x, const uint16_t* norm_w, float eps, const int8_t* codes,
+                   const uint16_t* scale, int64_t N, int64_t K, int64_t group, uint16_t* logits,
+                   float* part_val, int32_t* part_idx, int64_t part_len, int64_t* token, int64_t* pos,
+                   int32_t* filled, const int64_t* prompt, int64_t prompt_len, int64_t* history,
+                   int64_t history_len, void* stream) {
   if (!x || !codes || !scale || !logits || !part_val || !part_idx || !token || !pos || !filled)
     return LEMOQ_ERR_NULL;
   if (N <= 0 || N > 0x7ffffffeLL) return LEMOQ_ERR_SHAPE;
@@ -705,12 +707,37 @@ extern "C" int lemoq_lm_head_argmax_w8(const uint16_t* x, const uint16_t* norm_w
   a.am_val = part_val;
   a.am_idx = part_idx;
   hipStream_t st = lemoq_stream(stream);
-  const int rc = gemv_dispatch<kArgmaxPartials>(st, a, 1);
+  const int rc = gemv_dispatch<MODE>(st, a, 1);
   if (rc) return rc;
   hipLaunchKernelGGL((argmax_advance_kernel<true>), dim3(1), dim3(1024), 0, st, nullptr, part_val,
                      part_idx, blocks, token, pos, filled, prompt, prompt_len, history,
                      history_len);
   LEMOQ_CHECK_LAUNCH();
+}
+}  // namespace
+
+extern "C" int lemoq_lm_head_argmax_w8(const uint16_t* x, const uint16_t* norm_w, float eps,
+                                       const int8_t* codes, const uint16_t* scale, int64_t N,
+                                       int64_t K, int64_t group, uint16_t* logits,
+                                       float* part_val, int32_t* part_idx, int64_t part_len,
+                                       int64_t* token, int64_t* pos, int32_t* filled,
+                                       const int64_t* prompt, int64_t prompt_len,
+                                       int64_t* history, int64_t history_len, void* stream) {
+  return lm_head_argmax<kArgmaxPartials>(x, norm_w, eps, codes, scale, N, K, group, logits, part_val,
+                                         part_idx, part_len, token, pos, filled, prompt, prompt_len,
+                                         history, history_len, stream);
+}
+
+extern "C" int lemoq_lm_head_argmax_w8_dq(const uint16_t* x, const uint16_t* norm_w, float eps,
+                                          const int8_t* codes, const uint16_t* scale, int64_t N,
+                                          int64_t K, int64_t group, uint16_t* logits,
+                                          float* part_val, int32_t* part_idx, int64_t part_len,
+                                          int64_t* token, int64_t* pos, int32_t* filled,
+                                          const int64_t* prompt, int64_t prompt_len,
+                                          int64_t* history, int64_t history_len, void* stream) {
+  return lm_head_argmax<kArgmaxPartialsDq>(x, norm_w, eps, codes, scale, N, K, group, logits, part_val,
+                                           part_idx, part_len, token, pos, filled, prompt, prompt_len,
+                                           history, history_len, stream);
 }
 
 extern "C" int64_t lemoq_lm_head_argmax_parts(int64_t N) {

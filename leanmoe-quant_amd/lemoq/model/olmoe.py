@@ -511,13 +511,11 @@ class DecodeSession:
         elif mode == "batched":
             from lemoq.model.prefill import prefill_prompt  # noqa: PLC0415
 
-            prefill_prompt(self.weights, self.prompt, self.kv, self.cos_tab, self.sin_tab, self.max_seq,
-                           self.logits)
             self.history[: self.ctx].copy_(self.prompt)
             self.pos.fill_(self.ctx - 1)
-            _hip.call("lemoq_argmax_advance", _hip.ptr(self.logits), self.shape.vocab, _hip.ptr(self.token),
-                      _hip.ptr(self.pos), _hip.ptr(self.filled), _hip.ptr(self.prompt), self.ctx,
-                      _hip.ptr(self.history), int(self.history.numel()), _hip.stream_of(self.device))
+            prefill_prompt(self.weights, self.prompt, self.kv, self.cos_tab, self.sin_tab, self.max_seq,
+                           self.logits, step={"token": self.token, "pos": self.pos, "filled": self.filled,
+                                              "history": self.history})
             self._host_pos = self.ctx
         else:
             raise ValueError("prefill mode must be 'batched' or 'stepped', got %r" % (mode,))

@@ -23,11 +23,13 @@ routing_softmax_topk   ``lemoq_route_topk_splitk`` (sums the partials, then rout
 _prefill_forward       ``lemoq_moe_prefill_sort`` / ``_gate_up`` / ``_down`` /
 (moe_static.py:329)    ``_combine`` (the combine adds the residual; ``_combine_norm``
                        also writes the next layer's input norm)
-final norm, lm_head    ``lemoq_rmsnorm`` + ``lemoq_gemm_w8`` on the last row
+final norm, lm_head,   ``lemoq_lm_head_argmax_w8_dq`` on the last row: the final
+greedy pick            norm in the GEMV's prologue, weights rounded to fp16 before
+                       the dot (the separate arm's arithmetic), then the argmax
 =====================  ==========================================================
 
 The KV-INT8 cache slots 0..T-1 of every layer are written; the logits of the
-last prompt position land in ``logits``.  All launches go on torch's current
+last prompt position land in ``logits`` and their greedy pick in ``step["token"]``.  All launches go on torch's current
 stream; scratch tensors are allocated per call (prefill is eager, as in the
 reference).
 """
@@ -49,12 +51,15 @@ PREFILL_MAX_PAIRS = 32768
 
 
 def prefill_prompt(weights: Any, tokens: Any, kv: list, cos_tab: Any, sin_tab: Any, max_seq: int,
-                   logits: Any) -> None:
+                   logits: Any, step: dict | None = None) -> None:
     """Prefill ``tokens`` (int64 (T,) on the device) at positions 0..T-1.
 
     ``kv``: per layer the KV-INT8 cache dict (kc (heads, S, D) int8, ks (heads, S)
     fp16, vc, vs) with S = ``max_seq``; ``cos_tab``/``sin_tab`` (S, D) fp16;
-    ``logits`` (vocab,) fp16 receives the last position's logits.
+    ``logits`` (vocab,) fp16 receives the last position's logits.  ``step``: the
+    decode session's device state that the greedy pick advances, as
+    ``lemoq_argmax_advance`` does (``token``, ``pos`` holding T - 1, ``filled``,
+    ``history``; the prompt is ``tokens``); scratch buffers when None.
     """
     s = weights.shape
     dev = weights.device
@@ -135,10 +140,17 @@ def prefill_prompt(weights: Any, tokens: Any, kv: list, cos_tab: Any, sin_tab: A
                       P(weights.layers[li + 1].ln_in), float(s.eps), P(xn), st)
         else:
             _hip.call("lemoq_moe_prefill_combine", P(ybuf), P(top_i), T, K, H, P(h), P(h), st)
-    last = h[T - 1:]
-    _hip.call("lemoq_rmsnorm", P(last), 1, H, P(weights.final_norm), float(s.eps), P(xn), st)
-    _hip.call("lemoq_gemm_w8", P(xn), 1, H, H, None, P(weights.lm_codes), P(weights.lm_scale), s.vocab, g,
-              P(logits), s.vocab, None, 0, st)
+    if step is None:
+        step = {"token": torch.zeros((1,), dtype=torch.int64, device=dev),
+                "pos": torch.full((1,), T - 1, dtype=torch.int64, device=dev),
+                "filled": torch.zeros((1,), dtype=torch.int32, device=dev),
+                "history": torch.zeros((T + 1,), dtype=torch.int64, device=dev)}
+    parts = int(lib.lemoq_lm_head_argmax_parts(s.vocab))
+    part_val = torch.empty((parts,), dtype=torch.float32, device=dev)
+    part_idx = torch.empty((parts,), dtype=torch.int32, device=dev)
+    _hip.call("lemoq_lm_head_argmax_w8_dq", P(h[T - 1:]), P(weights.final_norm), float(s.eps), P(weights.lm_codes),
+              P(weights.lm_scale), s.vocab, H, g, P(logits), P(part_val), P(part_idx), parts, P(step["token"]),
+              P(step["pos"]), P(step["filled"]), P(tokens), T, P(step["history"]), int(step["history"].numel()), st)
     # The scratch tensors are released when this returns; the caching allocator
     # hands their memory only to later work on this same stream, which runs
     # after these kernels.

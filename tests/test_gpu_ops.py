@@ -748,6 +748,48 @@ def test_lm_head_argmax_partials(N, dev):
     assert int(pos.item()) == 1 and int(fill.item()) == 2
 
 
+@pytest.mark.parametrize("N", [50304, 1000, 37])
+def test_lm_head_argmax_dequant_first(N, dev):
+    """lemoq_lm_head_argmax_w8_dq (the prefill's last row): the weights rounded to
+    fp16(code * scale) before the dot, as the separate arm's F.linear over the
+    dequantised lm_head.  Logits within one fp16 step of the fp64 product with those
+    fp16 weights (plus fp32 accumulation), the token the lowest-index argmax of the
+    GPU's logits, and the step advanced as lemoq_argmax_advance does."""
+    from lemoq import _hip
+
+    H, group = 2048, 128
+    w = randn(N, H, seed=N + 5, std=0.02)
+    codes, scale = _q8(w, group)
+    x = randn(H, seed=N + 6).to(torch.float16)
+    nw = (torch.rand(H, generator=torch.Generator().manual_seed(N + 7)) + 0.5).to(torch.float16)
+    xd, nd, cd, sd = x.to(dev), nw.to(dev), codes.to(dev), scale.to(dev)
+    parts = int(_hip.load().lemoq_lm_head_argmax_parts(N))
+    pv = torch.empty(parts, dtype=torch.float32, device=dev)
+    pi = torch.empty(parts, dtype=torch.int32, device=dev)
+    logits = torch.empty(N, dtype=torch.float16, device=dev)
+    tok = torch.zeros(1, dtype=torch.int64, device=dev)
+    pos = torch.full((1,), 4, dtype=torch.int64, device=dev)
+    fill = torch.zeros(1, dtype=torch.int32, device=dev)
+    hist = torch.full((8,), -5, dtype=torch.int64, device=dev)
+    prompt = torch.arange(5, dtype=torch.int64, device=dev)
+    _hip.call("lemoq_lm_head_argmax_w8_dq", _hip.ptr(xd), _hip.ptr(nd), 1e-5, _hip.ptr(cd), _hip.ptr(sd), N, H,
+              group, _hip.ptr(logits), _hip.ptr(pv), _hip.ptr(pi), parts, _hip.ptr(tok), _hip.ptr(pos),
+              _hip.ptr(fill), _hip.ptr(prompt), 5, _hip.ptr(hist), 8, _hip.stream_of(dev))
+    torch.cuda.synchronize()
+    lg = logits.cpu()
+    xn = ops.rms_norm(x, nw, 1e-5)
+    ref = ops.dequant_gemm_separate(xn.reshape(1, -1), codes, scale, group).reshape(-1)
+    assert_close(lg, ref, what="lm_head dq N=%d" % N)
+    w16 = (codes.float() * scale.float().repeat_interleave(group, dim=1)).to(torch.float16)
+    exact = (w16.double() @ xn.double()).reshape(-1)
+    ulp = torch.finfo(torch.float16).eps * exact.abs().clamp_min(2.0 ** -14)
+    allow = ulp + 3e-5 * (w16.double().abs() @ xn.double().abs()).reshape(-1)
+    assert bool(((lg.double() - exact).abs() <= allow).all()), "dq logits beyond one fp16 step"
+    assert int(tok.item()) == _first_argmax(lg)
+    assert int(pos.item()) == 5 and int(fill.item()) == 6
+    assert int(hist[5].item()) == int(tok.item())
+
+
 def test_warm_entry_points_run_before_capture(dev):
     """The reference's warm() hooks (one real launch, then sync) exist with the
     same signatures and run on the device."""
