@@ -992,8 +992,9 @@ def main(argv=None) -> int:
 
 
 # Launch order of one batched prefill (lemoq.model.prefill.prefill_prompt):
-# gather, layer 0's input norm, 16 x [11 launches] (each layer's combine but the
-# last also writes the next layer's input norm), the lm_head GEMV of the last row
+# gather, layer 0's input norm, 15 x [11 launches] (each combine also writes the
+# next layer's input norm), the last layer (qkv and KV rows for every position,
+# then 10 launches on the last row), the lm_head GEMV of the last row
 # (final norm in its prologue), then the greedy pick; each role with the
 # kernel-name fragment its dispatch must carry.
 PREFILL_HEAD_ROLES = (("gather_rows", "gather_rows_kernel"), ("rmsnorm (input, layer 0)", "rmsnorm_kernel"))
@@ -1005,17 +1006,29 @@ PREFILL_LAYER_ROLES = (("gemm_w8 qkv", "gemm_kernel<true"),
                        ("moe_prefill_sort", "moe_sort_kernel"), ("moe_prefill_gate_up", "moe_gate_up_kernel"),
                        ("moe_prefill_down", "moe_down_kernel"))
 PREFILL_COMBINE_NORM = ("moe_prefill_combine (+residual, next input norm)", "moe_combine_kernel<true")
-PREFILL_COMBINE_LAST = ("moe_prefill_combine (+residual)", "moe_combine_kernel<false")
+# the last layer: its qkv and KV rows for every position, the rest for the last row only
+PREFILL_LAST_LAYER_ROLES = (("gemm_w8 qkv", "gemm_kernel<true"),
+                            ("qk_rows (q/k norm, RoPE, KV-INT8)", "qk_rows_kernel"),
+                            ("last row: attention split-KV", "attn_split_kernel"),
+                            ("last row: attention merge", "attn_merge"),
+                            ("last row: o_proj (+residual)", "gemm_kernel<true"),
+                            ("last row: post norm", "rmsnorm_kernel"),
+                            ("last row: router (split-K partials)", "gemm_kernel<false"),
+                            ("last row: route_topk", "route_topk_kernel"),
+                            ("last row: moe sort", "moe_sort_kernel"),
+                            ("last row: moe gate_up", "moe_gate_up_kernel"),
+                            ("last row: moe down", "moe_down_kernel"),
+                            ("last row: moe combine (+residual)", "moe_combine_kernel<false"))
 PREFILL_TAIL_ROLES = (("gemv_w8 lm_head (last row, + final norm)", "gemv_w8_kernel"),
                       ("argmax_advance", "argmax_advance_kernel"))
 
 
 def prefill_roles(n_layers: int = 16) -> list:
     roles = list(PREFILL_HEAD_ROLES)
-    for li in range(n_layers):
+    for _ in range(n_layers - 1):
         roles += list(PREFILL_LAYER_ROLES)
-        roles.append(PREFILL_COMBINE_NORM if li + 1 < n_layers else PREFILL_COMBINE_LAST)
-    return roles + list(PREFILL_TAIL_ROLES)
+        roles.append(PREFILL_COMBINE_NORM)
+    return roles + list(PREFILL_LAST_LAYER_ROLES) + list(PREFILL_TAIL_ROLES)
 
 
 def prefill_flops(role: str, T: int, shape=None) -> float:

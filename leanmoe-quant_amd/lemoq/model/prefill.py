@@ -15,7 +15,10 @@ input_layernorm        ``lemoq_rmsnorm`` (the fused RMSNorm, any row count) for 
 q/k/v_proj             ``lemoq_gemm_w8`` (QuantLinear separate arm, linear.py:471-480)
 q_norm, k_norm, RoPE,  ``lemoq_qk_norm_rope_kv_i8_rows`` (HF RoPE rounding; the
 KV cache + INT8 bulk   KV-INT8 rows are what kv_int8_bulk_quantize gives)
-sdpa causal attention  ``lemoq_attn_prefill_f16``
+sdpa causal attention  ``lemoq_attn_prefill_f16``; in the last layer only the last
+                       query: ``lemoq_attn_split_f16`` + ``lemoq_attn_merge`` (nothing
+                       after the last layer reads another position, so its
+                       attention, o_proj, norm, router and MoE run on that row)
 o_proj + residual      ``lemoq_gemm_w8`` with the residual in its epilogue
 post_attention norm    ``lemoq_rmsnorm``
 router F.linear +      ``lemoq_gemm_f16_splitk`` (fp32 partials only);
@@ -117,6 +120,10 @@ def prefill_prompt(weights: Any, tokens: Any, kv: list, cos_tab: Any, sin_tab: A
         _hip.call("lemoq_qk_norm_rope_kv_i8_rows", P(qkv), T, NH, D, P(L.q_norm), P(L.k_norm), float(s.eps),
                   P(cos_tab), P(sin_tab), 0, P(q), P(c["kc"]), P(c["ks"]), P(c["vc"]), P(c["vs"]), S * D, S,
                   P(k16), P(v16), S * D, st)
+        if li + 1 == n_layers and T > 1:
+            _last_layer_last_row(L, T, q, k16, v16, h, xn, attn, rws, rsplit, rlog, top_w, top_i, pair_tok,
+                                 pair_src, pair_w, expert_off, tiles, act, ybuf, s, S, qk_scale, lib, st)
+            break
         _hip.call("lemoq_attn_prefill_f16", P(q), HD, P(k16), P(v16), S * D, T, NH, D, qk_scale, P(attn), HD, st)
         _hip.call("lemoq_gemm_w8", P(attn), T, HD, HD, None, P(L.o_codes), P(L.o_scale), H, g, P(h), H, P(h), H,
                   st)
@@ -154,3 +161,50 @@ def prefill_prompt(weights: Any, tokens: Any, kv: list, cos_tab: Any, sin_tab: A
     # The scratch tensors are released when this returns; the caching allocator
     # hands their memory only to later work on this same stream, which runs
     # after these kernels.
+
+
+def _last_layer_last_row(L: Any, T: int, q: Any, k16: Any, v16: Any, h: Any, xn: Any, attn: Any, rws: Any,
+                         rsplit: int, rlog: Any, top_w: Any, top_i: Any, pair_tok: Any, pair_src: Any, pair_w: Any,
+                         expert_off: Any, tiles: Any, act: Any, ybuf: Any, s: Any, S: int, qk_scale: float,
+                         lib: Any, st: Any) -> None:
+    """The last layer after its KV rows are written, for the last position only.
+
+    Nothing after the last layer reads another position: the prefill returns the
+    last position's logits and its greedy pick, and every layer's KV-INT8 rows are
+    already in the cache.  So the last layer's attention runs for the one query at
+    T - 1 over keys 0..T-1 (the decode split-KV fp16 kernel and its merge, on the
+    fp16 K/V rows the prologue just wrote), and o_proj + residual, the post norm,
+    the router and the MoE block (sort, grouped gate/up and down, combine) run on
+    that row with the same kernels as the other layers.
+    """
+    P = _hip.ptr
+    H, NH, D, E, K, F = s.hidden, s.heads, s.head_dim, s.num_experts, s.top_k, s.ffn
+    HD, g, dev = NH * D, s.group_size, q.device
+    from lemoq.model.olmoe import step_num_splits  # noqa: PLC0415
+
+    ns = step_num_splits(T, NH)
+    m = torch.empty((NH * ns,), dtype=torch.float32, device=dev)
+    ls = torch.empty_like(m)
+    acc = torch.empty((NH * ns * D,), dtype=torch.float32, device=dev)
+    filled = torch.full((1,), T, dtype=torch.int32, device=dev)
+    hl = h[T - 1:]
+    _hip.call("lemoq_attn_split_f16", P(q[T - 1:]), P(k16), P(v16), S * D, P(filled), NH, D, ns, qk_scale, P(m),
+              P(ls), P(acc), st)
+    _hip.call("lemoq_attn_merge", P(m), P(ls), P(acc), NH, ns, D, P(attn), st)
+    _hip.call("lemoq_gemm_w8", P(attn), 1, HD, HD, None, P(L.o_codes), P(L.o_scale), H, g, P(hl), H, P(hl), H, st)
+    _hip.call("lemoq_rmsnorm", P(hl), 1, H, P(L.ln_post), float(s.eps), P(xn), st)
+    norm = int(bool(s.norm_topk_prob))
+    if rsplit > 1:
+        _hip.call("lemoq_gemm_f16_splitk", P(xn), 1, H, H, P(L.router), E, None, E, rsplit, P(rws), st)
+        _hip.call("lemoq_route_topk_splitk", P(rws), rsplit, 1, E, K, norm, P(top_w), P(top_i), st)
+    else:
+        _hip.call("lemoq_gemm_f16_splitk", P(xn), 1, H, H, P(L.router), E, P(rlog), E, 1, P(rws), st)
+        _hip.call("lemoq_route_topk", P(rlog), 1, 1, E, E, K, norm, P(top_w), P(top_i), st)
+    mt = int(lib.lemoq_moe_prefill_max_tiles(K, E))
+    _hip.call("lemoq_moe_prefill_sort", P(top_i), P(top_w), 1, K, E, P(pair_tok), P(pair_src), P(pair_w),
+              P(expert_off), P(tiles), mt, st)
+    _hip.call("lemoq_moe_prefill_gate_up", P(xn), H, P(pair_tok), P(tiles), mt, P(L.gu_codes), P(L.gu_scale), F, g,
+              P(act), st)
+    _hip.call("lemoq_moe_prefill_down", P(act), F, P(pair_src), P(pair_w), P(tiles), mt, P(L.dn_codes),
+              P(L.dn_scale), H, g, P(ybuf), st)
+    _hip.call("lemoq_moe_prefill_combine", P(ybuf), P(top_i), 1, K, H, P(hl), P(hl), st)
