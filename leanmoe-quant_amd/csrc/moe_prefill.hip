@@ -211,6 +211,7 @@ struct GroupedArgs {
 #define LEMOQ_MOE_WN 4  // column waves per grouped block (2: 128 weight rows, 4: 256)
 #endif
 constexpr int MOE_WN = LEMOQ_MOE_WN;
+constexpr int64_t kSmallTiles = 16;  // tile tables this small run 64-row blocks (WN = 1)
 template <int WN>
 using GTile = Tile<128, 64 * WN, 2, WN>;
 
@@ -477,6 +478,15 @@ extern "C" int lemoq_moe_prefill_gate_up(const uint16_t* x, int64_t H, const int
   GroupedArgs a{};
   a.x = x; a.pair_tok = pair_tok; a.tiles = tiles; a.codes = gu_codes; a.scale = gu_scale;
   a.K = H; a.N = F; a.group = (int)group; a.y = act;
+  // A table of at most 16 tiles (e.g. one token's top_k experts, passed with
+  // max_tiles = top_k) leaves most CUs idle with 256 weight rows per block:
+  // 64 rows per block there (the same arithmetic per element).
+  if (max_tiles <= kSmallTiles) {
+    const int64_t blocks = ((F + 31) / 32) * max_tiles;
+    hipLaunchKernelGGL(moe_gate_up_kernel<1>, dim3((unsigned)blocks), dim3(128), 0, lemoq_stream(stream), a,
+                       max_tiles);
+    LEMOQ_CHECK_LAUNCH();
+  }
   const int64_t blocks = ((F + 32 * MOE_WN - 1) / (32 * MOE_WN)) * max_tiles;
   if (blocks > 0x7fffffffLL) return LEMOQ_ERR_SHAPE;
   hipLaunchKernelGGL(moe_gate_up_kernel<MOE_WN>, dim3((unsigned)blocks), dim3(128 * MOE_WN), 0,
@@ -494,6 +504,12 @@ extern "C" int lemoq_moe_prefill_down(const uint16_t* act, int64_t F, const int3
   GroupedArgs a{};
   a.x = act; a.pair_src = pair_src; a.pair_w = pair_w; a.tiles = tiles; a.codes = dn_codes;
   a.scale = dn_scale; a.K = F; a.N = H; a.group = (int)group; a.y = y;
+  if (max_tiles <= kSmallTiles) {  // as in lemoq_moe_prefill_gate_up
+    const int64_t blocks = ((H + 63) / 64) * max_tiles;
+    hipLaunchKernelGGL(moe_down_kernel<1>, dim3((unsigned)blocks), dim3(128), 0, lemoq_stream(stream), a,
+                       max_tiles);
+    LEMOQ_CHECK_LAUNCH();
+  }
   const int64_t blocks = ((H + 64 * MOE_WN - 1) / (64 * MOE_WN)) * max_tiles;
   if (blocks > 0x7fffffffLL) return LEMOQ_ERR_SHAPE;
   hipLaunchKernelGGL(moe_down_kernel<MOE_WN>, dim3((unsigned)blocks), dim3(128 * MOE_WN), 0,

@@ -203,8 +203,10 @@ def _last_layer_last_row(L: Any, T: int, q: Any, k16: Any, v16: Any, h: Any, xn:
     mt = int(lib.lemoq_moe_prefill_max_tiles(K, E))
     _hip.call("lemoq_moe_prefill_sort", P(top_i), P(top_w), 1, K, E, P(pair_tok), P(pair_src), P(pair_w),
               P(expert_off), P(tiles), mt, st)
-    _hip.call("lemoq_moe_prefill_gate_up", P(xn), H, P(pair_tok), P(tiles), mt, P(L.gu_codes), P(L.gu_scale), F, g,
+    # one token meets each of its top_k experts once: the sort's live tiles are
+    # the first top_k entries of the table (the rest marked unused)
+    _hip.call("lemoq_moe_prefill_gate_up", P(xn), H, P(pair_tok), P(tiles), K, P(L.gu_codes), P(L.gu_scale), F, g,
               P(act), st)
-    _hip.call("lemoq_moe_prefill_down", P(act), F, P(pair_src), P(pair_w), P(tiles), mt, P(L.dn_codes),
+    _hip.call("lemoq_moe_prefill_down", P(act), F, P(pair_src), P(pair_w), P(tiles), K, P(L.dn_codes),
               P(L.dn_scale), H, g, P(ybuf), st)
     _hip.call("lemoq_moe_prefill_combine", P(ybuf), P(top_i), 1, K, H, P(hl), P(hl), st)

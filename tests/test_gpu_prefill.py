@@ -271,6 +271,45 @@ def test_moe_sort_exact(T, K, E, kind, dev):
     assert bool((covered == 1).all())
 
 
+@pytest.mark.parametrize("T,K", [(1, 8), (2, 8), (1, 2)])
+def test_moe_prefill_small_table_blocks_equal_wide_blocks(T, K, dev):
+    """A tile table of at most 16 entries runs 64-weight-row blocks (the last prompt row's MoE,
+    called with max_tiles = its live tiles); the same sort output through the 256-row blocks
+    (the full table) gives identical act and y bytes."""
+    from lemoq import _hip
+
+    H, F, E = 2048, 1024, 64
+    print("case: moe small table T=%d K=%d" % (T, K), flush=True)
+    x, router, gu_c, gu_s, dn_c, dn_s = _moe_case(T, H, F, E, K, 91 + T + K, dev)
+    g = torch.Generator().manual_seed(T * 31 + K)
+    ti = torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(T)]).to(torch.int64)
+    tw = torch.rand((T, K), generator=g)
+    pairs = T * K
+    mt = int(_hip.load().lemoq_moe_prefill_max_tiles(pairs, E))
+    live = len(set(ti.reshape(-1).tolist()))  # one tile per expert here (under 128 pairs)
+    assert live <= 16 < mt
+    P, st = _hip.ptr, _hip.stream_of(dev)
+    i32 = dict(dtype=torch.int32, device=dev)
+    pair_tok, pair_src = torch.empty((pairs,), **i32), torch.empty((pairs,), **i32)
+    pair_w = torch.empty((pairs,), dtype=torch.float16, device=dev)
+    expert_off, tiles = torch.empty((E + 1,), **i32), torch.empty((mt, 4), **i32)
+    xd, gcd, gsd, dcd, dsd = x.to(dev), gu_c.to(dev), gu_s.to(dev), dn_c.to(dev), dn_s.to(dev)
+    _hip.call("lemoq_moe_prefill_sort", P(ti.to(dev)), P(tw.to(dev)), T, K, E, P(pair_tok), P(pair_src), P(pair_w),
+              P(expert_off), P(tiles), mt, st)
+    outs = []
+    for m in (live, mt):
+        act = torch.full((pairs, F), 3.0, dtype=torch.float16, device=dev)
+        y = torch.full((pairs, H), 5.0, dtype=torch.float16, device=dev)
+        _hip.call("lemoq_moe_prefill_gate_up", P(xd), H, P(pair_tok), P(tiles), m, P(gcd), P(gsd), F, 128, P(act), st)
+        _hip.call("lemoq_moe_prefill_down", P(act), F, P(pair_src), P(pair_w), P(tiles), m, P(dcd), P(dsd), H, 128,
+                  P(y), st)
+        outs.append((act.cpu(), y.cpu()))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0][0].view(torch.int16), outs[1][0].view(torch.int16))
+    assert torch.equal(outs[0][1].view(torch.int16), outs[1][1].view(torch.int16))
+    assert not torch.isnan(outs[0][1].float()).any()
+
+
 COMBINE_NORM_CASES = [(1, 2048, 8, True), (77, 2048, 8, True), (513, 4096, 2, True), (40, 8192, 8, False),
                       (9, 264, 4, True)]
 
