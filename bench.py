@@ -509,7 +509,7 @@ def cpu_baseline(torch, host, snap, gpu_tokens, gpu_logits, *, warmup: int, time
 
 
 def cpu_ops_baseline(torch, host, *, warmup: int, timed: int, seed: int = 0) -> dict:
-    """C1-C4 of BASELINE.json as single operators of the reference's CPU path (the
+    """Benchmark configs C1-C4 as single operators of the reference's CPU path (the
     torch oracle backend, ``moe_grouped_quant.py:476-477,520-523``, ``attn_decode.py:581-586``,
     ``reference.py:50-60``; dense GEMVs dequantise the weight on every call as that
     oracle does), p50 / p99 microseconds per call on this host's threads.  C1 uses the
@@ -632,10 +632,10 @@ def _cpu_model() -> str:
 
 
 # ---------------------------------------------------------------------------
-# BASELINE attention configs as isolated kernels (fp16 and KV-INT8 split-KV)
+# The benchmark's attention configs as isolated kernels (fp16 and KV-INT8 split-KV)
 # ---------------------------------------------------------------------------
 def attention_configs(torch, hip, flusher, reps: int) -> dict:
-    """Split-KV decode attention at the BASELINE shapes, cold, 16 layers' worth of
+    """Split-KV decode attention at the benchmark's shapes, cold, 16 layers' worth of
     caches per pass (split kernel + LSE merge, chunks of 256 cache slots):
     fp16 K/V at ctx 1024 and 4096, KV-INT8 at 4096 and 16384.  Algorithmic
     bytes: fp16 4 * 16 * ctx * 128; int8 4160 * ctx; plus q and partials."""

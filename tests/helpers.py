@@ -4,7 +4,7 @@ from __future__ import annotations
 
 import torch
 
-# BASELINE.json north_star tolerance for fp16 GEMV and attention outputs.
+# The north-star tolerance for fp16 GEMV and attention outputs (rtol 2e-2, atol 2e-3).
 RTOL = 2e-2
 ATOL = 2e-3
 # The reference's frozen kernel gate (src/lemoq/kernels/moe_grouped.py:64-72).

@@ -7,7 +7,7 @@ and the CPU oracle:
 
 The KV-INT8 bytes written must equal the unfused path's bit for bit (both are
 pinned to the oracle's per-token quantiser); attention outputs must match
-within the BASELINE fp16 tolerance (rtol 2e-2 / atol 2e-3).  Cases mirror the
+within the fp16 tolerance rtol 2e-2 / atol 2e-3.  Cases mirror the
 reference's length boundaries (tests/test_fusion_adversarial.py:72-85,
 tests/test_attn_decode.py:83-149 of LeanMoE-Quant): first token, block edges,
 several split counts, long caches, a NaN-poisoned tail that must never be read.

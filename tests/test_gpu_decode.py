@@ -1,6 +1,6 @@
 """GPU parity of the whole decode step (A17/A18) against the CPU oracle.
 
-The BASELINE gates for the full step: identical greedy tokens over 32 steps
+The gates of the decode-step target: identical greedy tokens over 32 steps
 and logits KL < 0.01, here per step, plus the reference session's own gate
 that the captured graph and the eager step agree exactly
 (benchmarks/cudagraph.py:298-339 of LeanMoE-Quant: KL 0, identical tokens).
@@ -8,8 +8,8 @@ The oracle decodes from the GPU's KV-INT8 cache after prefill (the cache
 bytes themselves are pinned bit-exactly by the KV write tests), so every
 compared step runs the same inputs through both implementations.
 
-The full OLMoE-1B-7B shape is gated at the contexts BASELINE config C5 quotes
-(1024 and 4096): the batched prefill of ``[1] * ctx``, then 32 graph replays
+The full OLMoE-1B-7B shape is gated at the contexts the full-step benchmark
+uses (1024 and 4096): the batched prefill of ``[1] * ctx``, then 32 graph replays
 (greedy) and 32 teacher-forced replays of a seeded random token sequence,
 each step against the oracle.  The greedy token must equal the oracle's
 argmax; the only exception is an exact fp16 tie between the two tokens in
@@ -79,7 +79,7 @@ def _ulp16(v: float) -> float:
 
 
 def _check_steps(toks, gl, rl, *, rel=2e-2, strict=False):
-    """Per step: logits KL < 0.01 (the BASELINE gate for the full step), max
+    """Per step: logits KL < 0.01 (the gate for the full step), max
     |diff| below ``rel`` of the largest logit, and the GPU's greedy token is the
     oracle's argmax.  A flip is excused only at an exact fp16 tie of the two
     tokens in either logits vector (index order alone decides there); without
@@ -137,7 +137,7 @@ def test_olmoe_shape_32_greedy_steps_match_oracle(dev):
 
 
 # ---------------------------------------------------------------------------
-# BASELINE config C5 at its own contexts: OLMoE-1B-7B shape, prompt of ctx
+# The full-step benchmark at its own contexts: OLMoE-1B-7B shape, prompt of ctx
 # ones, batched prefill (the bench's path), 32 replays of the captured step.
 # ---------------------------------------------------------------------------
 C5_STEPS = 32

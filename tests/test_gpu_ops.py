@@ -49,7 +49,7 @@ def test_dequant_gemm_fused_vs_fp64(m, k, dev):
     assert got32.dtype == torch.float32
     baseline = ops.dequant_gemm_separate(x, codes, scale, group)
     assert_gate(got32.cpu(), ref64, baseline, what="gemv fp32 m=%d k=%d" % (m, k))
-    # fp16 output (the decode path): BASELINE tolerance against fp64
+    # fp16 output (the decode path): rtol 2e-2 / atol 2e-3 against fp64
     got = dequant_gemm_fused(x.to(dev), codes.to(dev), scale.to(dev), None, group_size=group,
                              bits=8, out_dtype=torch.float16)
     assert_close(got.cpu(), ref64, what="gemv fp16 m=%d k=%d" % (m, k))

@@ -8,7 +8,7 @@ in fp64 from the same fp16 weight and rounds once to fp16; the kernel
 accumulates in fp32, so every output lies within one fp16 ulp of the oracle
 plus an fp32 accumulation allowance of 3e-5 * sum|x||w| (the worst case for
 K = 2048 is 2048 * 2^-24 = 1.2e-4; observed errors are far below the
-allowance).  The BASELINE tolerance (rtol 2e-2, atol 2e-3) is checked as well.
+allowance).  The fp16 output tolerance of the decode-step target (rtol 2e-2, atol 2e-3) is checked as well.
 Shapes: the OLMoE prefill linears (qkv 6144 x 2048, o_proj 2048 x 2048, one
 expert's gate_up 2048 x 2048 and down 2048 x 1024, router 64 x 2048, lm_head
 50304 x 2048 for the last row), ragged M and N, row gather and residual.

@@ -5,8 +5,8 @@ in their previous tests: ``QuantLinear`` and ``quantize_fused_experts``.
   oracle, as the reference's K1 gate does (``tests/test_kernel_parity.py:134-220``):
   its buffers equal the oracle's RTN of the same weight bit for bit; one token
   (the fused arm, ``_fused_forward`` ``:446-469``) is within the K1 gate of the
-  fp64 product (error <= 1.5 x the fp32 separate arm's) and the BASELINE
-  tolerance; seven tokens (the separate arm, ``:471-480``: fp16 dequantised
+  fp64 product (error <= 1.5 x the fp32 separate arm's) and the fp16
+  tolerance rtol 2e-2 / atol 2e-3; seven tokens (the separate arm, ``:471-480``: fp16 dequantised
   weight, ``F.linear``) lie within one fp16 ulp of the fp64 product of the fp16
   weight plus the fp32 accumulation allowance 3e-5 * sum|x||w|.
 * ``quantize_fused_experts`` on the device (reference
