@@ -54,7 +54,7 @@ PREFILL_MAX_PAIRS = 32768
 
 
 def prefill_prompt(weights: Any, tokens: Any, kv: list, cos_tab: Any, sin_tab: Any, max_seq: int,
-                   logits: Any, step: dict | None = None) -> None:
+                   logits: Any, step: dict | None = None, last_row_only: bool = True) -> None:
     """Prefill ``tokens`` (int64 (T,) on the device) at positions 0..T-1.
 
     ``kv``: per layer the KV-INT8 cache dict (kc (heads, S, D) int8, ks (heads, S)
@@ -63,6 +63,8 @@ def prefill_prompt(weights: Any, tokens: Any, kv: list, cos_tab: Any, sin_tab: A
     decode session's device state that the greedy pick advances, as
     ``lemoq_argmax_advance`` does (``token``, ``pos`` holding T - 1, ``filled``,
     ``history``; the prompt is ``tokens``); scratch buffers when None.
+    ``last_row_only``: run the last layer after its KV rows on the last position
+    only (the default; False runs it on every position, as the other layers).
     """
     s = weights.shape
     dev = weights.device
@@ -120,7 +122,7 @@ def prefill_prompt(weights: Any, tokens: Any, kv: list, cos_tab: Any, sin_tab: A
         _hip.call("lemoq_qk_norm_rope_kv_i8_rows", P(qkv), T, NH, D, P(L.q_norm), P(L.k_norm), float(s.eps),
                   P(cos_tab), P(sin_tab), 0, P(q), P(c["kc"]), P(c["ks"]), P(c["vc"]), P(c["vs"]), S * D, S,
                   P(k16), P(v16), S * D, st)
-        if li + 1 == n_layers and T > 1:
+        if li + 1 == n_layers and T > 1 and last_row_only:
             _last_layer_last_row(L, T, q, k16, v16, h, xn, attn, rws, rsplit, rlog, top_w, top_i, pair_tok,
                                  pair_src, pair_w, expert_off, tiles, act, ybuf, s, S, qk_scale, lib, st)
             break

@@ -419,3 +419,44 @@ def test_prefill_modes_agree_on_the_canonical_prompt(dev):
     if a != b:
         top = torch.topk(lb, 2).values
         assert float(top[0] - top[1]) <= 2 * diff
+
+
+@pytest.mark.parametrize("T", [2, 300, 1024])
+def test_prefill_last_layer_on_the_last_row_only(T, dev):
+    """The last layer run on the last position only (after its KV rows are written for every
+    position) against the same layer run on every position: identical KV-INT8 caches (the rows
+    come from the same launches), the last logits within the fp16 tolerance of each other and
+    the same seed token unless the two top logits are within that difference."""
+    from lemoq.kernels.rope import rotary_cos_sin
+    from lemoq.model.olmoe import OlmoeShape, OlmoeW8Weights
+    from lemoq.model.prefill import prefill_prompt
+
+    print("case: prefill last row only T=%d" % T, flush=True)
+    shape = OlmoeShape(hidden=512, heads=4, head_dim=128, layers=3, num_experts=16, top_k=4, ffn=256, vocab=4096)
+    w = OlmoeW8Weights.random(shape, seed=T, device=dev)
+    S = T + 8
+    cos, sin = (t.to(dev).contiguous() for t in rotary_cos_sin(torch.arange(S), shape.head_dim, shape.rope_theta))
+    g = torch.Generator().manual_seed(T)
+    tokens = torch.randint(0, shape.vocab, (T,), generator=g).to(torch.int64).to(dev)
+    outs = []
+    for last_only in (True, False):
+        kv = [{"kc": torch.zeros((shape.heads, S, shape.head_dim), dtype=torch.int8, device=dev),
+               "ks": torch.zeros((shape.heads, S), dtype=torch.float16, device=dev),
+               "vc": torch.zeros((shape.heads, S, shape.head_dim), dtype=torch.int8, device=dev),
+               "vs": torch.zeros((shape.heads, S), dtype=torch.float16, device=dev)} for _ in range(shape.layers)]
+        logits = torch.empty((shape.vocab,), dtype=torch.float16, device=dev)
+        step = {"token": torch.zeros((1,), dtype=torch.int64, device=dev),
+                "pos": torch.full((1,), T - 1, dtype=torch.int64, device=dev),
+                "filled": torch.zeros((1,), dtype=torch.int32, device=dev),
+                "history": torch.zeros((S,), dtype=torch.int64, device=dev)}
+        prefill_prompt(w, tokens, kv, cos, sin, S, logits, step=step, last_row_only=last_only)
+        torch.cuda.synchronize()
+        outs.append((kv, logits.cpu(), int(step["token"].item())))
+    (kv_a, lg_a, tok_a), (kv_b, lg_b, tok_b) = outs
+    for la, lb in zip(kv_a, kv_b):
+        for name in ("kc", "ks", "vc", "vs"):
+            assert torch.equal(la[name].cpu(), lb[name].cpu()), name
+    assert_close(lg_a, lg_b, what="last logits T=%d" % T)
+    if tok_a != tok_b:
+        top = torch.topk(lg_b.float(), 2).values
+        assert float(top[0] - top[1]) <= float((lg_a.float() - lg_b.float()).abs().max())
