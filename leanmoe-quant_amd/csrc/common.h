@@ -15,9 +15,22 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 // ---------------------------------------------------------------------------
 // fp16 <-> fp32.  The f32->f16 conversion is v_cvt_f16_f32 (round to nearest
 // even), the same rounding as torch's `.half()` / `.to(torch.float16)`.
+//
+// f2h first pins its argument as an fp32 register value.  Without that, the
+// compiler (fp-contract=fast, hipcc's default) folds the fp32 multiply or fma
+// that produced the argument and the conversion into one mixed-precision op
+// (v_fma_mixlo_f16), which rounds the exact product once to fp16, where the
+// reference rounds it to fp32 first and then to fp16 (`(x * rstd).to(fp16)`
+// in fp32 arithmetic).  The two differ when the fp32 rounding lands the
+// product on an fp16 rounding tie: rare, but enough to move single elements
+// of a normalised row by one fp16 ulp, and the fold is applied to some
+// elements of a row and not to others depending on the surrounding code.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float h2f(uint16_t b) { return (float)__builtin_bit_cast(f16, b); }
-__device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (f16)f); }
+__device__ __forceinline__ uint16_t f2h(float f) {
+  __asm__("" : "+v"(f));
+  return __builtin_bit_cast(uint16_t, (f16)f);
+}
 // fp16 + fp16 with one rounding, as torch adds two fp16 tensors.
 __device__ __forceinline__ uint16_t hadd_round(float a_f16_exact, uint16_t b) {
   return f2h(a_f16_exact + h2f(b));
