@@ -92,6 +92,8 @@ def parse_args(argv=None):
     ap.add_argument("--mode", choices=("full", "kernels", "traffic", "prefill", "step"), default="full")
     ap.add_argument("--one-launch", choices=("default", "none", "attn", "moe", "both"), default="default",
                     help="run each layer's attention half and/or MoE as one launch (default: the session's default)")
+    ap.add_argument("--down-qkv", choices=("default", "on", "off"), default="default",
+                    help="each layer's down projection and the next layer's q|k|v as one launch")
     ap.add_argument("--summarize-pmc", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "PLAN_JSON"))
     ap.add_argument("--summarize-prefill", metavar="KERNEL_TRACE_CSV",
                     help="per-kernel table of the prefills in a rocprofv3 kernel trace of --mode prefill at --ctx")
@@ -791,10 +793,13 @@ def summarize_pmc(fetch_csv: str, write_csv: str, plan_json: str, out_dir: str) 
 
 def _one_launch(args) -> dict:
     """DecodeSession keyword arguments for --one-launch."""
-    if args.one_launch == "default":
-        return {}
-    return {"attention_one_launch": args.one_launch in ("attn", "both"),
-            "moe_one_launch": args.one_launch in ("moe", "both")}
+    kw: dict = {}
+    if args.one_launch != "default":
+        kw = {"attention_one_launch": args.one_launch in ("attn", "both"),
+              "moe_one_launch": args.one_launch in ("moe", "both")}
+    if args.down_qkv != "default":
+        kw["down_qkv_fused"] = args.down_qkv == "on"
+    return kw
 
 
 def main(argv=None) -> int:

@@ -394,6 +394,36 @@ int lemoq_moe_layer_w8(const uint16_t* x, const int8_t* gu_codes, const uint16_t
 /* LEMOQ_OK when lemoq_moe_layer_w8 covers the shape on the current device. */
 int lemoq_moe_layer_check(int64_t top_k, int64_t num_experts, int64_t ffn, int64_t hidden,
                           int64_t group);
+/* A5 + A7 + A10 — the down projection of decoder layer L and the input
+ * RMSNorm + packed q|k|v GEMV of layer L+1 as ONE launch (no single reference
+ * counterpart: it joins _down_sum_kernel_q of grouped_moe_forward_quant,
+ * src/lemoq/kernels/_grouped_triton.py:334-398, the residual add of the HF
+ * decoder layer, rms_norm_fused, src/lemoq/kernels/rmsnorm.py:102-163, and
+ * the PackedQKV projection, src/lemoq/kernels/packed_qkv.py).  Computes what
+ * lemoq_moe_down_w8(act, dn_codes, dn_scale, ids, top_w, top_k, num_experts,
+ * hidden, ffn, group, residual, h_out) followed by
+ * lemoq_gemv_w8_fused(h_out, NULL, 0, norm_w, eps, NULL, qkv_codes,
+ * qkv_scale, n_qkv, hidden, group, NULL, qkv_out) compute, bit for bit.  The
+ * workgroups publish h to each other through `ll` (hidden / 2 64-bit words,
+ * 256-byte aligned) with a flag unique to the launch, taken from the launch
+ * counter sync[1]; sync[0] is a status word that a wait exceeding
+ * `timeout_us` ORs LEMOQ_SYNC_TIMEOUT_BIT into (the q|k|v output is then
+ * invalid).  `ll` and sync[1] must be zeroed together when first allocated
+ * (and may be zeroed together again, never one alone), and `ll` is written by
+ * this function only.  This build covers hidden 2048, ffn 1024, top_k <= 8,
+ * n_qkv a multiple of 1024 up to 8192, with every workgroup resident at once
+ * (lemoq_moe_down_qkv_check); otherwise it returns LEMOQ_ERR_UNSUPPORTED and
+ * the two launches must be used. */
+int lemoq_moe_down_qkv_w8(const uint16_t* act, const int8_t* dn_codes, const uint16_t* dn_scale,
+                          const int64_t* ids, const uint16_t* top_w, int64_t top_k,
+                          int64_t num_experts, int64_t hidden, int64_t ffn, int64_t group,
+                          const uint16_t* residual, uint16_t* h_out, const uint16_t* norm_w,
+                          float eps, const int8_t* qkv_codes, const uint16_t* qkv_scale,
+                          int64_t n_qkv, uint16_t* qkv_out, uint64_t* ll, uint32_t* sync,
+                          int64_t timeout_us, void* stream);
+/* LEMOQ_OK when lemoq_moe_down_qkv_w8 covers the shape on the current device. */
+int lemoq_moe_down_qkv_check(int64_t top_k, int64_t hidden, int64_t ffn, int64_t group,
+                             int64_t n_qkv);
 /* Zero a sync workspace (LEMOQ_SYNC_WORDS words) with a fill kernel on `stream`
  * (graph-safe: no memset node). */
 int lemoq_sync_reset(uint32_t* sync, void* stream);

@@ -137,6 +137,16 @@ int validate(const LemoqOlmoeStep* p, AttnPath* path, bool* moe_one) {
   return LEMOQ_OK;
 }
 
+// The down -> next q|k|v hand-off (down_qkv.hip) takes its status and launch
+// counter from sync words 0 and 1 and its buffer from 32 KB into the sync
+// workspace (the one-launch MoE, which it excludes, uses that range too).
+constexpr int64_t kLLOffsetWords = 8192;
+bool use_down_qkv(const LemoqOlmoeStep* p, bool moe_one) {
+  if (!p->sync || !(p->one_launch & 4) || moe_one || p->num_layers < 2) return false;
+  if (kLLOffsetWords + p->hidden > LEMOQ_SYNC_WORDS) return false;
+  return lemoq_moe_down_qkv_check(p->top_k, p->hidden, p->ffn, p->group, 3 * p->heads * p->head_dim) == LEMOQ_OK;
+}
+
 }  // namespace
 
 extern "C" int lemoq_olmoe_decode_step(const LemoqOlmoeStep* p, void* stream) {
@@ -146,14 +156,18 @@ extern "C" int lemoq_olmoe_decode_step(const LemoqOlmoeStep* p, void* stream) {
   const int64_t H = p->hidden, HD = p->heads * p->head_dim, D = p->head_dim;
   const int64_t S = p->max_seq;
   const int64_t n_part = HD / 512;
+  const bool dq = use_down_qkv(p, moe_one);
+  uint64_t* ll = dq ? reinterpret_cast<uint64_t*>(p->sync + kLLOffsetWords) : nullptr;
   for (int64_t L = 0; L < p->num_layers; ++L) {
     const LemoqOlmoeLayer& w = p->layers[L];
     const bool first = L == 0;
     // 1. input RMSNorm + packed qkv projection.  Layer 0 gathers the
     //    embedding row of *token and block 0 stores it as the residual.
-    LEMOQ_TRY(lemoq_gemv_w8_fused(first ? p->embed : p->h, first ? p->token : nullptr, p->vocab,
-                                  w.ln_in, p->eps, first ? p->h : nullptr, w.qkv_codes,
-                                  w.qkv_scale, 3 * HD, H, p->group, nullptr, p->qkv, stream));
+    //    (With the fused down launch, layers >= 1 got q|k|v from it.)
+    if (first || !dq)
+      LEMOQ_TRY(lemoq_gemv_w8_fused(first ? p->embed : p->h, first ? p->token : nullptr, p->vocab,
+                                    w.ln_in, p->eps, first ? p->h : nullptr, w.qkv_codes,
+                                    w.qkv_scale, 3 * HD, H, p->group, nullptr, p->qkv, stream));
     if (path == kAttnLayer) {
       // 2-4 as one launch: attention, merge + o_proj, residual + norm + router.
       LEMOQ_TRY(lemoq_attn_layer_i8(p->qkv, p->heads, D, w.q_norm, w.k_norm, p->eps, p->cos_tab,
@@ -201,8 +215,17 @@ extern "C" int lemoq_olmoe_decode_step(const LemoqOlmoeStep* p, void* stream) {
                                             p->top_k, (int)p->norm_topk_prob, p->num_experts,
                                             p->ffn, H, p->group, p->act, p->top_i, p->top_w,
                                             stream));
-      LEMOQ_TRY(lemoq_moe_down_w8(p->act, w.dn_codes, w.dn_scale, p->top_i, p->top_w, p->top_k,
-                                  p->num_experts, H, p->ffn, p->group, resid, p->h, stream));
+      if (dq && L + 1 < p->num_layers) {
+        // 6 + next layer's 1 as one launch.
+        const LemoqOlmoeLayer& nx = p->layers[L + 1];
+        LEMOQ_TRY(lemoq_moe_down_qkv_w8(p->act, w.dn_codes, w.dn_scale, p->top_i, p->top_w, p->top_k,
+                                        p->num_experts, H, p->ffn, p->group, resid, p->h, nx.ln_in,
+                                        p->eps, nx.qkv_codes, nx.qkv_scale, 3 * HD, p->qkv,
+                                        ll, p->sync, p->sync_timeout_us, stream));
+      } else {
+        LEMOQ_TRY(lemoq_moe_down_w8(p->act, w.dn_codes, w.dn_scale, p->top_i, p->top_w, p->top_k,
+                                    p->num_experts, H, p->ffn, p->group, resid, p->h, stream));
+      }
     }
   }
   // Final norm + W8 lm_head with argmax partials, then greedy selection and step advance.

@@ -194,6 +194,12 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         [_P, _P, _P, _P, _P, _P, _I64, _I, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _I64, _P],
     ),
     "lemoq_moe_layer_check": (_I, [_I64, _I64, _I64, _I64, _I64]),
+    "lemoq_moe_down_qkv_w8": (
+        _I,
+        [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _F, _P, _P, _I64, _P, _P, _P, _I64,
+         _P],
+    ),
+    "lemoq_moe_down_qkv_check": (_I, [_I64, _I64, _I64, _I64, _I64]),
     "lemoq_moe_gate_up_w8_routed": (
         _I,
         [_P, _P, _P, _P, _I64, _I, _I64, _I64, _I64, _I64, _P, _P, _P, _P],

@@ -7,8 +7,11 @@
 
 For the decode shape (one fp16 token) the whole router is one HIP kernel
 (``lemoq_router_topk_fused``: GEMV with fp32 accumulation and a single fp16
-rounding of each logit, then softmax/top-k).  More tokens use ATen's
-``F.linear`` on the device (as the reference does) and the HIP top-k.
+rounding of each logit, then softmax/top-k).  Several fp16 tokens run the
+router linear as ``lemoq_gemm_f16`` (``lemoq.kernels.dequant_gemm.linear_f16``:
+fp32 accumulation, one fp16 rounding, F.linear's contract in fp16) and then
+the HIP top-k; other dtypes or widths (hidden % 64 != 0) use ATen's
+``F.linear`` on the device, as the reference does, before the HIP top-k.
 """
 
 from __future__ import annotations
@@ -75,6 +78,16 @@ def _route(x: Any, router_weight: Any, *, top_k: int, norm_topk_prob: bool):
         return logits, top_w, top_i
     from lemoq.kernels.routing import routing_softmax_topk  # noqa: PLC0415
 
-    logits = F.linear(x, router_weight)
+    if x.dtype == torch.float16 and router_weight.dtype == torch.float16 and hidden % 64 == 0:
+        from lemoq.kernels.dequant_gemm import linear_f16  # noqa: PLC0415
+
+        xc, wc = x.contiguous(), router_weight.contiguous()
+        if xc.data_ptr() % 16:
+            xc = xc.clone()
+        if wc.data_ptr() % 16:
+            wc = wc.clone()
+        logits = linear_f16(xc, wc)
+    else:
+        logits = F.linear(x, router_weight)
     top_w, top_i = routing_softmax_topk(logits, top_k=top_k, norm_topk_prob=norm_topk_prob)
     return logits, top_w.to(x.dtype), top_i

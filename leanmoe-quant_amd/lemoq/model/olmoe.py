@@ -54,6 +54,7 @@ SYNC_TIMEOUT_US = 200_000
 # by default.
 ATTENTION_ONE_LAUNCH_DEFAULT = False
 MOE_ONE_LAUNCH_DEFAULT = False
+DOWN_QKV_FUSED_DEFAULT = False
 
 
 def step_num_splits(max_seq: int, heads: int, compute_units: int = 256) -> int:
@@ -218,6 +219,7 @@ class DecodeSession:
         num_splits: int | None = None,
         attention_one_launch: bool | None = None,
         moe_one_launch: bool | None = None,
+        down_qkv_fused: bool | None = None,
     ) -> None:
         from lemoq.kernels.attn_decode import resolve_num_splits  # noqa: PLC0415
         from lemoq.kernels.rope import rotary_cos_sin  # noqa: PLC0415
@@ -330,9 +332,10 @@ class DecodeSession:
         one_attn = ATTENTION_ONE_LAUNCH_DEFAULT if attention_one_launch is None else bool(attention_one_launch)
         one_moe = MOE_ONE_LAUNCH_DEFAULT if moe_one_launch is None else bool(moe_one_launch)
         self.moe_part = torch.zeros((s.top_k, s.hidden), dtype=torch.float32, device=dev)
-        st.sync = P(self.sync) if (one_attn or one_moe) else None
+        dq = DOWN_QKV_FUSED_DEFAULT if down_qkv_fused is None else bool(down_qkv_fused)
+        st.sync = P(self.sync) if (one_attn or one_moe or dq) else None
         st.sync_timeout_us = SYNC_TIMEOUT_US
-        st.one_launch = (1 if one_attn else 0) | (2 if one_moe else 0)
+        st.one_launch = (1 if one_attn else 0) | (2 if one_moe else 0) | (4 if dq else 0)
         st.moe_part = P(self.moe_part)
         self._step = st
         self.graph: Any = None
@@ -422,6 +425,18 @@ class DecodeSession:
         return int(rc) == 0
 
     @property
+    def down_qkv_fused(self) -> bool:
+        """Whether each layer's down projection and the next layer's q|k|v run as one
+        launch (lemoq_moe_down_qkv_w8; the buffer rule of csrc/step.hip)."""
+        s = self.shape
+        if not (self._step.sync and (self._step.one_launch & 4)) or self.moe_layer_fused or s.layers < 2:
+            return False
+        if 8192 + s.hidden > _hip.SYNC_WORDS:
+            return False
+        rc = _hip.load().lemoq_moe_down_qkv_check(s.top_k, s.hidden, s.ffn, s.group_size, s.qkv_rows)
+        return int(rc) == 0
+
+    @property
     def attn_output_fused(self) -> bool:
         """Whether the step runs merge + o_proj as one launch and the residual add
         in the router launch (the shape rule of csrc/step.hip)."""
@@ -437,7 +452,8 @@ class DecodeSession:
         per_layer = 4 if self.attn_layer_fused else (6 if self.attn_output_fused else 7)
         if self.moe_layer_fused:
             per_layer -= 1
-        return per_layer * self.shape.layers + 2
+        fused_dq = self.shape.layers - 1 if self.down_qkv_fused else 0
+        return per_layer * self.shape.layers + 2 - fused_dq
 
     def capture(self, steps_per_graph: int = 1) -> dict[str, Any]:
         """Capture one decode step into a hipGraph (state is untouched by the capture).
@@ -491,7 +507,7 @@ class DecodeSession:
             self.check_sync_status()
         return self.logits
 
-    def prefill(self, mode: str = "batched") -> int:
+    def prefill(self, mode: str = "batched", *, kv_f16: list | None = None) -> int:
         """Fill the KV-INT8 cache with the prompt and seed the first decode token; returns it.
 
         ``mode="batched"`` (default) is the reference's prefill: one multi-token
@@ -500,6 +516,8 @@ class DecodeSession:
         then the greedy pick of the last position's logits (``lemoq_argmax_advance``).
         ``mode="stepped"`` feeds the prompt through the captured decode step, one
         replay per position (decode numerics for every prompt token).
+        ``kv_f16`` (batched only): a list that receives per layer the fp16 k and v
+        rows the cache bytes were quantised from (see ``prefill_prompt``).
         """
         if self.graph is None:
             self.capture()
@@ -515,7 +533,7 @@ class DecodeSession:
             self.pos.fill_(self.ctx - 1)
             prefill_prompt(self.weights, self.prompt, self.kv, self.cos_tab, self.sin_tab, self.max_seq,
                            self.logits, step={"token": self.token, "pos": self.pos, "filled": self.filled,
-                                              "history": self.history})
+                                              "history": self.history}, kv_f16=kv_f16)
             self._host_pos = self.ctx
         else:
             raise ValueError("prefill mode must be 'batched' or 'stepped', got %r" % (mode,))

@@ -54,7 +54,8 @@ PREFILL_MAX_PAIRS = 32768
 
 
 def prefill_prompt(weights: Any, tokens: Any, kv: list, cos_tab: Any, sin_tab: Any, max_seq: int,
-                   logits: Any, step: dict | None = None, last_row_only: bool = True) -> None:
+                   logits: Any, step: dict | None = None, last_row_only: bool = True,
+                   kv_f16: list | None = None) -> None:
     """Prefill ``tokens`` (int64 (T,) on the device) at positions 0..T-1.
 
     ``kv``: per layer the KV-INT8 cache dict (kc (heads, S, D) int8, ks (heads, S)
@@ -65,6 +66,9 @@ def prefill_prompt(weights: Any, tokens: Any, kv: list, cos_tab: Any, sin_tab: A
     ``history``; the prompt is ``tokens``); scratch buffers when None.
     ``last_row_only``: run the last layer after its KV rows on the last position
     only (the default; False runs it on every position, as the other layers).
+    ``kv_f16``: when a list, receives per layer copies of the fp16 k (after k_norm
+    and RoPE) and v rows that were quantised into the cache, each (heads, T, D)
+    (for parity checks of the KV bytes against their inputs).
     """
     s = weights.shape
     dev = weights.device
@@ -122,6 +126,8 @@ def prefill_prompt(weights: Any, tokens: Any, kv: list, cos_tab: Any, sin_tab: A
         _hip.call("lemoq_qk_norm_rope_kv_i8_rows", P(qkv), T, NH, D, P(L.q_norm), P(L.k_norm), float(s.eps),
                   P(cos_tab), P(sin_tab), 0, P(q), P(c["kc"]), P(c["ks"]), P(c["vc"]), P(c["vs"]), S * D, S,
                   P(k16), P(v16), S * D, st)
+        if kv_f16 is not None:
+            kv_f16.append((k16[:, :T].clone(), v16[:, :T].clone()))
         if li + 1 == n_layers and T > 1 and last_row_only:
             _last_layer_last_row(L, T, q, k16, v16, h, xn, attn, rws, rsplit, rlog, top_w, top_i, pair_tok,
                                  pair_src, pair_w, expert_off, tiles, act, ybuf, s, S, qk_scale, lib, st)

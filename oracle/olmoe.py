@@ -216,7 +216,8 @@ class OracleDecoder:
         return tokens, all_logits
 
 
-def oracle_prefill(weights: Any, tokens: Any, max_seq: int, *, all_logits: bool = False):
+def oracle_prefill(weights: Any, tokens: Any, max_seq: int, *, all_logits: bool = False,
+                   kv_f16: list | None = None, kv_layers: int | None = None):
     """The reference's prefill of the prompt ``tokens`` (positions 0..T-1) on the CPU.
 
     ``StaticCacheDecodeSession.prefill`` (``benchmarks/cudagraph.py:578-599``) runs the
@@ -240,7 +241,10 @@ def oracle_prefill(weights: Any, tokens: Any, max_seq: int, *, all_logits: bool 
 
     Returns ``(logits, kv)``: fp16 logits of the last position (``(T, vocab)`` with
     ``all_logits``), and per layer the KV-INT8 cache dict (kc, ks, vc, vs) of ``max_seq``
-    slots with slots 0..T-1 filled (the rest codes 0, scales 1).
+    slots with slots 0..T-1 filled (the rest codes 0, scales 1).  ``kv_f16``, when a
+    list, receives per layer the fp16 k (after k_norm and RoPE) and v rows that were
+    quantised, each (heads, T, D).  ``kv_layers`` stops after that many layers' KV rows
+    (logits are then None).
     """
     s, w = weights.shape, weights
     toks = torch.as_tensor(tokens, dtype=torch.int64).reshape(-1)
@@ -273,6 +277,10 @@ def oracle_prefill(weights: Any, tokens: Any, max_seq: int, *, all_logits: bool 
             cache[name + "c"][:, :T, :] = torch.from_numpy(codes).reshape(T, NH, D).transpose(0, 1)
             cache[name + "s"][:, :T] = torch.from_numpy(scales).reshape(T, NH).transpose(0, 1)
         kv_out.append(cache)
+        if kv_f16 is not None:
+            kv_f16.append((k.transpose(0, 1).contiguous(), v.transpose(0, 1).contiguous()))
+        if kv_layers is not None and len(kv_out) >= kv_layers:
+            return None, kv_out
         attn = ops.causal_attention(q, k, v).to(torch.float16).reshape(T, HD)
         h = r + ops.linear_separate_w8(attn, L.o_codes, L.o_scale, g)
         r = h

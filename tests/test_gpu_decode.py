@@ -23,8 +23,9 @@ import math
 import pytest
 import torch
 
+from helpers import kv_rows_vs_oracle
 from lemoq.model.olmoe import OLMOE_1B_7B, DecodeSession, OlmoeShape, OlmoeW8Weights
-from oracle.olmoe import OracleDecoder
+from oracle.olmoe import OracleDecoder, oracle_prefill
 
 pytestmark = pytest.mark.gpu
 
@@ -153,9 +154,10 @@ def c5_model(dev):
     return w, oracle
 
 
-def _c5_session(w, ctx):
-    sess = DecodeSession(w, [1] * ctx, max_new_tokens=C5_STEPS, num_splits=None)
-    seed_tok = sess.prefill()
+def _c5_session(w, ctx, kv_f16=None, max_new_tokens=C5_STEPS, prompt=None):
+    sess = DecodeSession(w, [1] * ctx if prompt is None else prompt, max_new_tokens=max_new_tokens,
+                         num_splits=None)
+    seed_tok = sess.prefill(kv_f16=kv_f16)
     return sess, seed_tok
 
 
@@ -164,12 +166,31 @@ def test_c5_greedy_32_steps_match_oracle(ctx, c5_model, dev):
     """32 greedy graph replays after the batched prefill; each step's logits and
     argmax against the oracle stepping the GPU's tokens from the GPU's KV-INT8
     snapshot (so the two token sequences are identical exactly when every
-    step's argmax agrees)."""
+    step's argmax agrees).  The prefill itself is pinned too: layer 0's KV
+    bytes against the oracle's prefill of the same prompt, and the seed token
+    against the oracle's prefill of the one-token prompt [1] (with a prompt of
+    identical tokens every cached v row of a layer is the same vector, so the
+    attention of every position returns it whatever the scores, and the last
+    position's hidden state is that of the one-token prompt up to the fp32
+    rounding of the softmax normalisation): equal unless the oracle's top-2
+    margin is within the logits' difference."""
     w, oracle = c5_model
     print("case: C5 greedy, ctx %d, %d steps" % (ctx, C5_STEPS), flush=True)
-    sess, seed_tok = _c5_session(w, ctx)
+    rows = []
+    sess, seed_tok = _c5_session(w, ctx, kv_f16=rows)
     assert sess.position == ctx
-    oracle.kv = sess.kv_cpu()
+    seed_logits = sess.logits_cpu()
+    kv = sess.kv_cpu()
+    ref_rows = []
+    _, ref_kv = oracle_prefill(oracle.w, [1] * ctx, sess.max_seq, kv_f16=ref_rows, kv_layers=1)
+    kv_rows_vs_oracle("C5 ctx %d layer 0" % ctx, kv[0], rows[0], ref_kv[0], ref_rows[0], ctx)
+    ref_seed, _ = oracle_prefill(oracle.w, [1], 8)
+    diff = float((seed_logits.double() - ref_seed.double()).abs().max())
+    ra = int(torch.argmax(ref_seed.float()))
+    print("seed token gpu %d oracle %d, max|diff| %.2e, oracle margin %.2e" % (seed_tok, ra, diff, _margin(ref_seed)))
+    assert diff <= 2e-2 * float(ref_seed.float().abs().max())
+    assert seed_tok == ra or _margin(ref_seed) <= 2 * diff
+    oracle.kv = kv
     gl = []
     for _ in range(C5_STEPS):
         sess.replay(1)
@@ -201,14 +222,55 @@ def test_c5_random_tokens_32_steps_match_oracle(ctx, c5_model, dev):
     _check_steps(toks + [-1], gl, rl, strict=True)
 
 
-def test_c5_graph_replay_equals_eager_bitwise(c5_model, dev):
+def test_c5_random_prompt_1024_greedy_and_forced_match_oracle(c5_model, dev):
+    """A non-degenerate state at the full shape: a seeded random 1024-token prompt
+    (every cached row differs, so the decode attention's scores over the prompt
+    decide its output), batched prefill, then 32 greedy replays and 32
+    teacher-forced replays of seeded random tokens, each step against the oracle
+    continuing from the GPU's KV-INT8 snapshot (strict argmax rule).  Layer 0's
+    prompt KV bytes are pinned against the oracle's prefill."""
+    w, oracle = c5_model
+    ctx = 1024
+    print("case: C5 random prompt, ctx %d, %d greedy + %d forced steps" % (ctx, C5_STEPS, C5_STEPS), flush=True)
+    prompt = torch.randint(0, OLMOE_1B_7B.vocab, (ctx,), generator=torch.Generator().manual_seed(77)).tolist()
+    rows = []
+    sess, seed_tok = _c5_session(w, ctx, kv_f16=rows, max_new_tokens=2 * C5_STEPS + 1, prompt=prompt)
+    kv = sess.kv_cpu()
+    ref_rows = []
+    _, ref_kv = oracle_prefill(oracle.w, prompt, sess.max_seq, kv_f16=ref_rows, kv_layers=1)
+    kv_rows_vs_oracle("random prompt layer 0", kv[0], rows[0], ref_kv[0], ref_rows[0], ctx)
+    oracle.kv = kv
+    gl = []
+    for _ in range(C5_STEPS):
+        sess.replay(1)
+        gl.append(sess.logits_cpu())
+    toks = [int(t) for t in sess.history[ctx: ctx + C5_STEPS + 1].tolist()]
+    assert toks[0] == seed_tok
+    rl = [oracle.step(toks[i], ctx + i) for i in range(C5_STEPS)]
+    print("gpu greedy tokens:", toks)
+    _check_steps(toks, gl, rl, strict=True)
+    forced = torch.randint(0, OLMOE_1B_7B.vocab, (C5_STEPS,), generator=torch.Generator().manual_seed(78)).tolist()
+    gl, rl = [], []
+    for i, t in enumerate(forced):
+        pos = ctx + C5_STEPS + i
+        sess.token.fill_(int(t))
+        sess.replay(1)
+        gl.append(sess.logits_cpu())
+        rl.append(oracle.step(int(t), pos))
+    _check_steps(forced + [-1], gl, rl, strict=True)
+    assert sess.position == ctx + 2 * C5_STEPS
+
+
+@pytest.mark.parametrize("ctx,positions", [(1024, 4), (4096, 8)])
+def test_c5_graph_replay_equals_eager_bitwise(ctx, positions, c5_model, dev):
     """The reference session's own gate (benchmarks/cudagraph.py:298-339): the
     captured step and the eager step give identical logits and tokens, here at
-    the full OLMoE shape after the ctx-1024 batched prefill, over 4 positions."""
+    the full OLMoE shape after the batched prefill at both benchmark contexts
+    (at ctx 4096 the step runs 8-wave attention blocks over 256-slot splits)."""
     w, _ = c5_model
-    print("case: C5 graph vs eager, ctx 1024", flush=True)
-    sess, _ = _c5_session(w, 1024)
-    for _ in range(4):
+    print("case: C5 graph vs eager, ctx %d, %d positions" % (ctx, positions), flush=True)
+    sess, _ = _c5_session(w, ctx, max_new_tokens=positions + 1)
+    for _ in range(positions):
         p, tok = sess.position, int(sess.token.item())
         sess.replay(1)
         g_logits, g_next = sess.logits_cpu(), int(sess.token.item())

@@ -149,6 +149,30 @@ def test_fused_router_vs_oracle(norm, dev):
         assert tw.dtype == torch.float16 and ti.dtype == torch.int64
 
 
+@pytest.mark.parametrize("T", [2, 7, 64])
+@pytest.mark.parametrize("norm", [False, True])
+def test_route_several_tokens_vs_oracle(T, norm, dev):
+    """``_route`` on several fp16 tokens (the prefill shape) runs the router linear
+    as lemoq_gemm_f16 and the HIP top-k: logits against the oracle's F.linear
+    (one fp16 rounding of an fp32 dot; the order may move a value by one ulp),
+    the ids bit-exact against the oracle's top-k of the GPU's own logits (ties
+    -> lowest index), so a near-tied pair cannot excuse a wrong selection, and
+    the weights within 1e-3 (fp32 softmax, then fp16)."""
+    from lemoq.kernels.moe_static import _route
+
+    print("case: _route T=%d norm=%s" % (T, norm), flush=True)
+    x = randn(T, 2048, seed=300 + T).to(torch.float16)
+    rw = randn(64, 2048, seed=400 + T, std=0.02).to(torch.float16)
+    lg, tw, ti = _route(x.to(dev), rw.to(dev), top_k=8, norm_topk_prob=norm)
+    rlg, _, _ = ops.route(x, rw, 8, norm)
+    assert lg.shape == (T, 64) and tw.shape == (T, 8) and ti.shape == (T, 8)
+    assert max_abs(lg.cpu(), rlg) <= 2e-3
+    gw, gi = ops.route_logits(lg.cpu(), 8, norm)
+    assert np.array_equal(ti.cpu().numpy(), gi.numpy())
+    assert torch.allclose(tw.cpu().float(), gw.float(), atol=1e-3, rtol=0)
+    assert tw.dtype == torch.float16 and ti.dtype == torch.int64
+
+
 @pytest.mark.parametrize("norm", [False, True])
 @pytest.mark.parametrize("E", [64, 8, 100])
 def test_router_logits_then_routed_gate_up_vs_oracle(norm, E, dev):

@@ -32,7 +32,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import assert_close, randn
+from helpers import assert_close, kv_rows_vs_oracle, randn
 from oracle import ops
 from oracle import quant as oq
 from oracle.olmoe import OracleDecoder, oracle_prefill
@@ -350,11 +350,13 @@ def _prefill_vs_oracle(shape, prompt, seed, steps, dev):
 
     w = OlmoeW8Weights.random(shape, seed=seed, device=dev)
     sess = DecodeSession(w, prompt, max_new_tokens=steps, num_splits=None)
-    seed_tok = sess.prefill()
+    rows = []
+    seed_tok = sess.prefill(kv_f16=rows)
     logits = sess.logits_cpu()
     kv = sess.kv_cpu()
     hw = w.to_host()
-    ref, ref_kv = oracle_prefill(hw, prompt, sess.max_seq)
+    ref_rows = []
+    ref, ref_kv = oracle_prefill(hw, prompt, sess.max_seq, kv_f16=ref_rows)
     ref64, got64 = ref.double(), logits.double()
     p, q = torch.log_softmax(ref64, -1), torch.log_softmax(got64, -1)
     kl = float((p.exp() * (p - q)).sum())
@@ -366,9 +368,10 @@ def _prefill_vs_oracle(shape, prompt, seed, steps, dev):
         top = torch.topk(ref64, 2).values
         assert float(top[0] - top[1]) <= 2 * diff
     T = len(prompt)
-    for name in ("kc", "vc"):
-        a, b = kv[0][name][:, :T].int(), ref_kv[0][name][:, :T].int()
-        assert int((a - b).abs().max()) <= 1, name
+    assert len(rows) == len(ref_rows) == shape.layers
+    for li in range(shape.layers):
+        kv_rows_vs_oracle("prefill T=%d layer %d" % (T, li), kv[li], rows[li], ref_kv[li], ref_rows[li], T,
+                          rows_close=li == 0)
     assert sess.position == T and sess.generated() == [seed_tok]
     # decode from the prefilled cache, checked step by step against the CPU decoder on the same cache
     gl = []

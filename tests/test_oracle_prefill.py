@@ -185,3 +185,30 @@ def test_separate_arm_weight_is_one_rounding_of_the_exact_product():
     sep = ops.linear_separate_w8(x, codes, scale, 128).double()
     ref = x.double() @ w64.t()
     assert float((sep - ref).abs().max()) < 2e-2 * float(ref.abs().max())
+
+
+def test_prefill_kv_rows_hook_matches_the_cache_and_stops_early():
+    """``oracle_prefill(kv_f16=...)`` hands out the fp16 rows its cache bytes were
+    quantised from (the GPU parity tests compare the GPU's rows and bytes with
+    them), and ``kv_layers`` stops after that many layers with the same bytes."""
+    import numpy as np
+
+    from oracle import quant as oq
+
+    w = random_host_weights(SHAPE, seed=5)
+    toks = [3, 17, 17, 42, 9, 3, 60]
+    rows = []
+    _, kv = oracle_prefill(w, toks, 12, kv_f16=rows)
+    assert len(rows) == SHAPE.layers
+    T = len(toks)
+    for li, (k16, v16) in enumerate(rows):
+        assert k16.shape == (SHAPE.heads, T, SHAPE.head_dim) and k16.dtype == torch.float16
+        for name, r in (("k", k16), ("v", v16)):
+            c, s = oq.kv_quantize_rows(r.reshape(-1, SHAPE.head_dim).numpy())
+            assert np.array_equal(kv[li][name + "c"][:, :T].reshape(-1, SHAPE.head_dim).numpy(), c)
+            assert np.array_equal(kv[li][name + "s"][:, :T].reshape(-1).numpy().view(np.uint16), s.view(np.uint16))
+    rows1 = []
+    lg, kv1 = oracle_prefill(w, toks, 12, kv_f16=rows1, kv_layers=1)
+    assert lg is None and len(kv1) == 1 and len(rows1) == 1
+    assert all(torch.equal(kv1[0][n], kv[0][n]) for n in ("kc", "ks", "vc", "vs"))
+    assert torch.equal(rows1[0][0], rows[0][0]) and torch.equal(rows1[0][1], rows[0][1])
