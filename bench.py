@@ -90,10 +90,6 @@ def parse_args(argv=None):
     ap.add_argument("--no-cpu-ops", action="store_true", help="skip the per-operator CPU timings (C1-C4)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--mode", choices=("full", "kernels", "traffic", "prefill", "step"), default="full")
-    ap.add_argument("--one-launch", choices=("default", "none", "attn", "moe", "both"), default="default",
-                    help="run each layer's attention half and/or MoE as one launch (default: the session's default)")
-    ap.add_argument("--down-qkv", choices=("default", "on", "off"), default="default",
-                    help="each layer's down projection and the next layer's q|k|v as one launch")
     ap.add_argument("--summarize-pmc", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "PLAN_JSON"))
     ap.add_argument("--summarize-prefill", metavar="KERNEL_TRACE_CSV",
                     help="per-kernel table of the prefills in a rocprofv3 kernel trace of --mode prefill at --ctx")
@@ -244,20 +240,6 @@ def kernel_table(torch, hip, w, sess, flusher, reps: int, floors: bool = True) -
                                qk_scale, P(sess.part_m), P(sess.part_l), P(sess.part_acc), st())
          for i in range(nl)],
         ["attn_split_fused_i8_kernel"])
-    if sess.attn_output_fused and int(hip.load().lemoq_attn_layer_check(s.heads, D, sess.num_splits, H, g, E)) == 0:
-        npart = HD // 512
-        attn_bytes = KV_BYTES_PER_TOKEN_LAYER * filled + 3 * HD * 2 + 2 * HD * 2 + 2 * D * 2
-        add("attn_layer_i8 (attention + merge/o_proj + router, 1 launch)",
-            attn_bytes + w8(H, HD) + E * H * 2 + 4 * H * 2 + E * 2,
-            [lambda i=i: hip.call("lemoq_attn_layer_i8", P(sess.qkv), s.heads, D, P(L[i].q_norm), P(L[i].k_norm),
-                                   s.eps, P(sess.cos_tab), P(sess.sin_tab), P(sess.pos), P(kv[i]["kc"]),
-                                   P(kv[i]["ks"]), P(kv[i]["vc"]), P(kv[i]["vs"]), S * D, S, ns, qk_scale,
-                                   P(sess.part_m), P(sess.part_l), P(sess.part_acc), P(L[i].o_codes),
-                                   P(L[i].o_scale), H, g, P(sess.o_part), P(scratch["h"]), P(L[i].ln_post),
-                                   P(L[i].router), E, P(scratch["h2"]), P(scratch["xn"]), P(scratch["lg"]),
-                                   P(sess.sync), 200_000, st())
-             for i in range(nl)],
-            ["attn_layer_kernel"])
     if sess.attn_output_fused:
         npart = HD // 512
         add("attn_merge_o_proj_w8", w8(H, HD) + s.heads * ns * (D + 2) * 4 + npart * H * 4,
@@ -329,12 +311,11 @@ def measure_prefill(torch, sess, warmup: int = 2, timed: int = 7) -> dict:
 MULTI_STEPS = 8  # decode steps per graph of the multi-step measurement
 
 
-def time_decode(torch, w, ctx: int, steps: int, warmup: int, extra: int, one_launch: dict | None = None):
+def time_decode(torch, w, ctx: int, steps: int, warmup: int, extra: int):
     from lemoq.model.olmoe import DecodeSession
 
     groups = max(8, steps // MULTI_STEPS)
-    sess = DecodeSession(w, [1] * ctx, max_new_tokens=warmup + 2 * steps + groups * MULTI_STEPS + extra + 4,
-                         **(one_launch or {}))
+    sess = DecodeSession(w, [1] * ctx, max_new_tokens=warmup + 2 * steps + groups * MULTI_STEPS + extra + 4)
     sess.capture()
     ttft = measure_prefill(torch, sess)
     log("ctx %d: batched prefill (TTFT) p50 %.3f ms over %d runs" % (ctx, ttft["p50"], ttft["runs"]))
@@ -791,17 +772,6 @@ def summarize_pmc(fetch_csv: str, write_csv: str, plan_json: str, out_dir: str) 
     return {"table": "\n".join(lines), "data": out}
 
 
-def _one_launch(args) -> dict:
-    """DecodeSession keyword arguments for --one-launch."""
-    kw: dict = {}
-    if args.one_launch != "default":
-        kw = {"attention_one_launch": args.one_launch in ("attn", "both"),
-              "moe_one_launch": args.one_launch in ("moe", "both")}
-    if args.down_qkv != "default":
-        kw["down_qkv_fused"] = args.down_qkv == "on"
-    return kw
-
-
 def main(argv=None) -> int:
     args = parse_args(argv)
     if args.summarize_pmc:
@@ -852,7 +822,7 @@ def main(argv=None) -> int:
     if args.mode == "step":
         from lemoq.model.olmoe import DecodeSession
 
-        sess = DecodeSession(w, [1] * args.ctx, max_new_tokens=args.warmup + args.steps + 1, **_one_launch(args))
+        sess = DecodeSession(w, [1] * args.ctx, max_new_tokens=args.warmup + args.steps + 1)
         sess.capture()
         sess.prefill()
         sess.replay(args.warmup)
@@ -861,7 +831,7 @@ def main(argv=None) -> int:
         ms = (time.perf_counter() - t0) * 1e3 / args.steps
         log("ctx %d: %d replays, %.4f ms/token" % (args.ctx, args.steps, ms))
         print(json.dumps({"mode": "step", "ctx": args.ctx, "steps": args.steps, "ms_per_token": ms,
-                          "one_launch": args.one_launch, "launches_per_step": sess.launches_per_step}))
+                          "launches_per_step": sess.launches_per_step}))
         return 0
 
     if args.mode == "prefill":
@@ -888,7 +858,7 @@ def main(argv=None) -> int:
         return 0
 
     check_n = 0 if args.no_cpu else max(1, args.cpu_check_steps)
-    sess, r1 = time_decode(torch, w, args.ctx, args.steps, args.warmup, check_n, _one_launch(args))
+    sess, r1 = time_decode(torch, w, args.ctx, args.steps, args.warmup, check_n)
     snap = None
     check_tokens: list[int] = []
     check_logits = []
@@ -905,7 +875,7 @@ def main(argv=None) -> int:
     r2 = None
     snap2 = None
     if args.ctx2:
-        s2, r2 = time_decode(torch, w, args.ctx2, args.steps, args.warmup, 0, _one_launch(args))
+        s2, r2 = time_decode(torch, w, args.ctx2, args.steps, args.warmup, 0)
         if check_n:
             snap2 = (s2.kv_cpu(), int(s2.token.item()), s2.position)
         del s2

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define LEMOQ_ABI_VERSION 4
+#define LEMOQ_ABI_VERSION 5
 
 enum {
   LEMOQ_OK = 0,
@@ -42,17 +42,6 @@ enum {
   LEMOQ_ERR_ALIGN = -4,       /* a pointer is not 16-byte aligned            */
   LEMOQ_ERR_CAPACITY = -5     /* larger than a fixed capacity of the library */
 };
-
-/* Cross-workgroup synchronisation of the fused launches (lemoq_attn_layer_i8
- * and the decode step that uses it).  The caller owns a workspace of
- * LEMOQ_SYNC_WORDS uint32 words, 256-byte aligned and zero before the first
- * launch (lemoq_sync_reset); every successful launch leaves it zero again.
- * Word 0 is the status: a wait that gives up (its time limit expires, or
- * another workgroup already failed) ORs LEMOQ_SYNC_TIMEOUT_BIT into it and its
- * workgroup returns, so the launch always completes; its outputs are then
- * invalid and the workspace must be reset before the next launch. */
-#define LEMOQ_SYNC_WORDS 16384
-#define LEMOQ_SYNC_TIMEOUT_BIT 1u
 
 /* Human-readable name of a status returned by any lemoq_* call. */
 const char* lemoq_status_string(int status);
@@ -338,95 +327,6 @@ int lemoq_router_logits_resid(const float* part, int64_t n_part, const uint16_t*
                               const uint16_t* router_w, int64_t E, uint16_t* h_out,
                               uint16_t* xn_out, uint16_t* logits, void* stream);
 
-/* A14/A16 + A8 + A3 — the attention half of one decoder layer as ONE launch
- * (no single reference counterpart: it joins, per layer, the patched
- * attention forward _decode_forward_impl, src/lemoq/kernels/attn_decode.py:
- * 836-1017, its o_proj QuantLinear, src/lemoq/quant/linear.py:446-469, the
- * residual add of the HF decoder layer, the post-attention rms_norm_fused,
- * src/lemoq/kernels/rmsnorm.py:102-163, and the router F.linear of
- * moe_static._route, src/lemoq/kernels/moe_static.py:262-283).  Computes what
- * lemoq_attn_split_fused_i8, then lemoq_attn_merge_o_proj_w8, then
- * lemoq_router_logits_resid compute, bit for bit, with the arguments of those
- * three calls (m, l, acc and o_part are the intermediate workspaces):
- * heads * num_splits workgroups hand results to each other inside the launch
- * through `sync` (LEMOQ_SYNC_WORDS words, see above); `timeout_us` bounds
- * each wait.  head_dim 128, heads % 4 == 0, hidden in {2048, 4096},
- * heads * 128 / 512 in {1, 2, 4, 8}, num_splits <= 64,
- * ceil(num_experts / 4) <= heads * num_splits, and every workgroup resident at
- * once (lemoq_attn_layer_check).  Returns LEMOQ_ERR_UNSUPPORTED where the
- * three calls must be used instead. */
-int lemoq_attn_layer_i8(const uint16_t* qkv, int64_t heads, int64_t head_dim,
-                        const uint16_t* q_norm_w, const uint16_t* k_norm_w, float eps,
-                        const uint16_t* cos_tab, const uint16_t* sin_tab, const int64_t* pos,
-                        int8_t* kc, uint16_t* ks, int8_t* vc, uint16_t* vs,
-                        int64_t code_head_stride, int64_t s_len, int64_t num_splits,
-                        float qk_scale, float* m, float* l, float* acc,
-                        const int8_t* o_codes, const uint16_t* o_scale, int64_t hidden,
-                        int64_t group, float* o_part, const uint16_t* h,
-                        const uint16_t* post_norm_w, const uint16_t* router_w,
-                        int64_t num_experts, uint16_t* h_out, uint16_t* xn_out,
-                        uint16_t* logits, uint32_t* sync, int64_t timeout_us, void* stream);
-/* LEMOQ_OK when lemoq_attn_layer_i8 covers the shape on the current device
- * (shape rules and co-residency), else the status it would return. */
-int lemoq_attn_layer_check(int64_t heads, int64_t head_dim, int64_t num_splits, int64_t hidden,
-                           int64_t group, int64_t num_experts);
-/* A4 + A5 + A6 — the grouped MoE of one decoder layer as ONE launch (no
- * single reference counterpart: it joins _gate_up_act_kernel_q and
- * _down_sum_kernel_q of grouped_moe_forward_quant, src/lemoq/kernels/
- * _grouped_triton.py:249-398, with the routing of moe_static._route,
- * src/lemoq/kernels/moe_static.py:262-283, and the residual add of the HF
- * decoder layer).  Computes what lemoq_moe_gate_up_w8_routed followed by
- * lemoq_moe_down_w8 (with `residual`) compute, bit for bit: act (top_k, F)
- * fp16 and ypart (top_k, H) fp32 are its intermediate workspaces, top_i /
- * top_w receive the routing.  top_k * 32 workgroups hand results to each
- * other through `sync` (LEMOQ_SYNC_WORDS words, see above; this launch uses
- * lines 64 and up, lemoq_attn_layer_i8 lines below 64); `timeout_us` bounds
- * each wait.  This build covers hidden 2048, ffn 1024, E <= 64, top_k <= 16,
- * with every workgroup resident at once (lemoq_moe_layer_check); otherwise it
- * returns LEMOQ_ERR_UNSUPPORTED and the two launches must be used. */
-int lemoq_moe_layer_w8(const uint16_t* x, const int8_t* gu_codes, const uint16_t* gu_scale,
-                       const int8_t* dn_codes, const uint16_t* dn_scale,
-                       const uint16_t* router_logits, int64_t top_k, int norm_topk_prob,
-                       int64_t num_experts, int64_t ffn, int64_t hidden, int64_t group,
-                       uint16_t* act, float* ypart, const uint16_t* residual, uint16_t* out,
-                       int64_t* top_i, uint16_t* top_w, uint32_t* sync, int64_t timeout_us,
-                       void* stream);
-/* LEMOQ_OK when lemoq_moe_layer_w8 covers the shape on the current device. */
-int lemoq_moe_layer_check(int64_t top_k, int64_t num_experts, int64_t ffn, int64_t hidden,
-                          int64_t group);
-/* A5 + A7 + A10 — the down projection of decoder layer L and the input
- * RMSNorm + packed q|k|v GEMV of layer L+1 as ONE launch (no single reference
- * counterpart: it joins _down_sum_kernel_q of grouped_moe_forward_quant,
- * src/lemoq/kernels/_grouped_triton.py:334-398, the residual add of the HF
- * decoder layer, rms_norm_fused, src/lemoq/kernels/rmsnorm.py:102-163, and
- * the PackedQKV projection, src/lemoq/kernels/packed_qkv.py).  Computes what
- * lemoq_moe_down_w8(act, dn_codes, dn_scale, ids, top_w, top_k, num_experts,
- * hidden, ffn, group, residual, h_out) followed by
- * lemoq_gemv_w8_fused(h_out, NULL, 0, norm_w, eps, NULL, qkv_codes,
- * qkv_scale, n_qkv, hidden, group, NULL, qkv_out) compute, bit for bit.  The
- * workgroups publish h to each other through `ll` (hidden / 2 64-bit words,
- * 256-byte aligned) with a flag unique to the launch, taken from the launch
- * counter sync[1]; sync[0] is a status word that a wait exceeding
- * `timeout_us` ORs LEMOQ_SYNC_TIMEOUT_BIT into (the q|k|v output is then
- * invalid).  `ll` and sync[1] must be zeroed together when first allocated
- * (and may be zeroed together again, never one alone), and `ll` is written by
- * this function only.  This build covers hidden 2048, ffn 1024, top_k <= 8,
- * n_qkv a multiple of 1024 up to 8192, with every workgroup resident at once
- * (lemoq_moe_down_qkv_check); otherwise it returns LEMOQ_ERR_UNSUPPORTED and
- * the two launches must be used. */
-int lemoq_moe_down_qkv_w8(const uint16_t* act, const int8_t* dn_codes, const uint16_t* dn_scale,
-                          const int64_t* ids, const uint16_t* top_w, int64_t top_k,
-                          int64_t num_experts, int64_t hidden, int64_t ffn, int64_t group,
-                          const uint16_t* residual, uint16_t* h_out, const uint16_t* norm_w,
-                          float eps, const int8_t* qkv_codes, const uint16_t* qkv_scale,
-                          int64_t n_qkv, uint16_t* qkv_out, uint64_t* ll, uint32_t* sync,
-                          int64_t timeout_us, void* stream);
-/* LEMOQ_OK when lemoq_moe_down_qkv_w8 covers the shape on the current device. */
-int lemoq_moe_down_qkv_check(int64_t top_k, int64_t hidden, int64_t ffn, int64_t group,
-                             int64_t n_qkv);
-/* Zero a sync workspace (LEMOQ_SYNC_WORDS words) with a fill kernel on `stream`
- * (graph-safe: no memset node). */
-int lemoq_sync_reset(uint32_t* sync, void* stream);
 
 /* Router of one token, fused: xn = rmsnorm(h, norm_w) (written to xn_out),
  * logits = fp16(xn @ router_w^T) with fp32 accumulation (the F.linear of
@@ -567,15 +467,6 @@ typedef struct LemoqOlmoeStep {
    * runs lemoq_attn_merge, the o_proj GEMV and lemoq_router_logits. */
   float* o_part;                 /* (heads*D/512, H) o_proj partial sums */
   uint16_t* h_mid;               /* (H) residual after attention */
-  /* Workspace of the one-launch paths (LEMOQ_SYNC_WORDS words, zeroed
-   * beforehand; see one_launch) and the time limit of their waits. */
-  uint32_t* sync;
-  int64_t sync_timeout_us;
-  /* With `sync` non-NULL: bit 0 runs each layer's attention half as one launch
-   * (lemoq_attn_layer_i8), bit 1 its MoE as one launch (lemoq_moe_layer_w8,
-   * which also needs moe_part), each where its check covers the shape. */
-  int64_t one_launch;
-  float* moe_part;               /* (top_k, H) fp32 MoE partials */
 } LemoqOlmoeStep;
 
 int lemoq_olmoe_decode_step(const LemoqOlmoeStep* step, void* stream);

@@ -15,7 +15,6 @@
 #pragma once
 
 #include "common.h"
-#include "sync.h"
 
 namespace lemoq_attn {
 
@@ -209,8 +208,7 @@ __device__ __forceinline__ float rows_pair_sum(float x, float y, int lane) {
 // End of a split block: sum the token groups of each wave (the running max is
 // wave-uniform), merge the NW wave states through LDS in wave order, and
 // write the block's (m, l, acc[D]) partial; m = -inf for an empty split
-// (l = 0, acc = 0).  wm/wl hold NW floats, wacc NW * D.  COHERENT: the partial
-// is stored with coherent stores, for a consumer in the same launch (sync.h).
+// (l = 0, acc = 0).  wm/wl hold NW floats, wacc NW * D.
 //
 // The EPL accumulators of a lane are summed over its token group (the lanes
 // sharing lane % LPT, partners lane ^ LPT, ^ 2 LPT, ... ^ 32) as a reduce-
@@ -219,7 +217,7 @@ __device__ __forceinline__ float rows_pair_sum(float x, float y, int lane) {
 // again (LPT <= 16), and row rotations (LPT 4, 8) finish the sum.  A lane ends
 // with V = EPL / 2 (or 4) fully summed elements instead of all EPL, and one
 // lane of each group of duplicates writes them to LDS.
-template <class S, int NW, int D, bool COHERENT = false>
+template <class S, int NW, int D>
 __device__ __forceinline__ void finish_split(SoftmaxState<S::EPL>& st, float* wm, float* wl,
                                              float* wacc, int lane, int wave, int tl, int dl,
                                              int64_t pidx, float* __restrict__ m_out,
@@ -271,10 +269,10 @@ __device__ __forceinline__ void finish_split(SoftmaxState<S::EPL>& st, float* wm
         den += wl[w] * f;
       }
     }
-    lemoq_sync::store_f32<COHERENT>(acc_out + pidx * D + t, num);
+    acc_out[pidx * D + t] = num;
     if (t == 0) {
-      lemoq_sync::store_f32<COHERENT>(m_out + pidx, M);
-      lemoq_sync::store_f32<COHERENT>(l_out + pidx, den);
+      m_out[pidx] = M;
+      l_out[pidx] = den;
     }
   }
 }

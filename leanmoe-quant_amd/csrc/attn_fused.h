@@ -1,7 +1,6 @@
 // The split-KV block of the fused per-layer attention over the KV-INT8 cache
 // (q_norm/k_norm, RoPE, KV-INT8 write of the new token, online softmax over
-// the block's cached tokens), shared by the standalone launch
-// (attn_fused.hip) and the fused attention-layer launch (attn_layer.hip).
+// the block's cached tokens), launched by attn_fused.hip.
 //
 // attn_split_fused_i8: grid (num_splits, heads), 4 waves per block.  Block
 // (s, h) covers tokens [s*c, min((s+1)*c, n)) of head h with n = *pos + 1 and
@@ -74,7 +73,7 @@ struct AttnFusedSmem {
   float wacc[NW * D];
 };
 
-template <int D, int NW_, int U_, bool COHERENT>
+template <int D, int NW_, int U_>
 __device__ __forceinline__ void attn_split_fused_block(const AttnSplitArgs& a, int sp, int h,
                                                        AttnFusedSmem<D, NW_>& sm) {
   using S = HeadShape<D, NW_, U_>;
@@ -254,7 +253,7 @@ __device__ __forceinline__ void attn_split_fused_block(const AttnSplitArgs& a, i
     }
     lemoq_attn::fold_tokens<T>(st, nbk, qx, 0, 1, tl, lane, a.qk_scale);
   }
-  lemoq_attn::finish_split<T, NW, D, COHERENT>(st, wm, wl, wacc, lane, wave, tl, dl,
+  lemoq_attn::finish_split<T, NW, D>(st, wm, wl, wacc, lane, wave, tl, dl,
                                                (int64_t)h * a.ns + sp, a.m_out, a.l_out, a.acc_out);
 }
 

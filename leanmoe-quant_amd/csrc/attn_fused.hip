@@ -9,7 +9,7 @@ using lemoq_attn_fused::AttnSplitArgs;
 template <int D, int NW_ = 8, int U_ = 4>
 __global__ __launch_bounds__(64 * NW_) void attn_split_fused_i8_kernel(const AttnSplitArgs a) {
   __shared__ lemoq_attn_fused::AttnFusedSmem<D, NW_> sm;
-  lemoq_attn_fused::attn_split_fused_block<D, NW_, U_, false>(a, blockIdx.x, blockIdx.y, sm);
+  lemoq_attn_fused::attn_split_fused_block<D, NW_, U_>(a, blockIdx.x, blockIdx.y, sm);
 }
 
 }  // namespace

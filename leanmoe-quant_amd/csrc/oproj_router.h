@@ -1,7 +1,6 @@
 // Device parts of the attention-output half of a decode layer (merge + o_proj
-// per head group, residual + post-attention norm + router), shared by the
-// standalone launches (oproj_router.hip) and the fused attention-layer
-// launch (attn_layer.hip).
+// per head group, residual + post-attention norm + router), launched by
+// oproj_router.hip.
 //
 //   lemoq_attn_merge_o_proj_w8   the LSE merge of the split-KV partials fused
 //                                into the w8 o_proj GEMV, split over groups of
@@ -86,24 +85,23 @@ __device__ __forceinline__ void oproj_issue(const MergeOprojArgs& a, int g, int 
 }
 
 // Merge the tile's 4 heads into LDS (xs: 512 fp16) and write its partial
-// sums.  COHERENT: the split partials are read, and the o_proj partials
-// written, with coherent accesses (producer and consumer in one launch).
-template <int NSMAX, bool COHERENT>
+// sums.
+template <int NSMAX>
 __device__ __forceinline__ void oproj_finish(const MergeOprojArgs& a, const OprojTile& t, uint16_t* xs) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l32 = lane & 31;
   const int NS = a.NS;
   const int64_t hh = (int64_t)t.g * MO_HEADS + wave;
   const int jl = lane < NS ? lane : NS - 1;
-  const float mraw = lemoq_sync::load_f32<COHERENT>(a.m + hh * NS + jl);
-  const float lraw = lemoq_sync::load_f32<COHERENT>(a.l + hh * NS + jl);
+  const float mraw = a.m[hh * NS + jl];
+  const float lraw = a.l[hh * NS + jl];
   const float* ah = a.acc + hh * NS * MO_D + lane;
   float a0[NSMAX], a1[NSMAX];
 #pragma unroll
   for (int j = 0; j < NSMAX; ++j) {
     const int64_t o = (int64_t)(j < NS ? j : NS - 1) * MO_D;
-    a0[j] = lemoq_sync::load_f32<COHERENT>(ah + o);
-    a1[j] = lemoq_sync::load_f32<COHERENT>(ah + o + 64);
+    a0[j] = ah[o];
+    a1[j] = ah[o + 64];
   }
   LEMOQ_LOADS_ISSUED();
 
@@ -129,7 +127,7 @@ __device__ __forceinline__ void oproj_finish(const MergeOprojArgs& a, const Opro
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf)
       if (lane == 2 * i + hf) out = tot[i][hf];
-  if (lane < MO_ROWS_WAVE) lemoq_sync::store_f32<COHERENT>(a.part + (int64_t)t.g * a.N + t.row0 + lane, out);
+  if (lane < MO_ROWS_WAVE) a.part[(int64_t)t.g * a.N + t.row0 + lane] = out;
 }
 
 // Block (x, g) of the standalone launch -> o_proj tile (rb, g).  Blocks are
@@ -197,8 +195,8 @@ __device__ __forceinline__ void router_issue(const RouterResidArgs& a, int blk, 
 
 // o = fp16(sum of the NP partial rows), h' = fp16(o + h), the norm and the
 // router logits of block `blk`'s 4 experts.  xs: KCH * 1024 fp16 of LDS, red: 4
-// floats.  COHERENT: the partials are read with coherent loads.
-template <int KCH, int NP, bool COHERENT>
+// floats.
+template <int KCH, int NP>
 __device__ __forceinline__ void router_finish(const RouterResidArgs& a, int blk, const RouterPre<KCH>& p,
                                               uint16_t* xs, float* red) {
   constexpr int NV = KCH / 2;
@@ -210,8 +208,8 @@ __device__ __forceinline__ void router_finish(const RouterResidArgs& a, int blk,
     const int off = (i * 256 + threadIdx.x) * 8;
 #pragma unroll
     for (int g = 0; g < NP; ++g) {
-      pv[i][g][0] = lemoq_sync::load_16<COHERENT>(a.part + (int64_t)g * a.H + off);
-      pv[i][g][1] = lemoq_sync::load_16<COHERENT>(a.part + (int64_t)g * a.H + off + 4);
+      pv[i][g][0] = *reinterpret_cast<const u32x4*>(a.part + (int64_t)g * a.H + off);
+      pv[i][g][1] = *reinterpret_cast<const u32x4*>(a.part + (int64_t)g * a.H + off + 4);
     }
   }
   LEMOQ_LOADS_ISSUED();

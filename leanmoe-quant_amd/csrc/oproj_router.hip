@@ -15,7 +15,7 @@ __global__ __launch_bounds__(256) void merge_oproj_kernel(const MergeOprojArgs a
   OprojTile t;
   oproj_issue(a, g, rb, t);
   LEMOQ_LOADS_ISSUED();  // the weight stream first, then the merge inputs
-  oproj_finish<NSMAX, false>(a, t, xs);
+  oproj_finish<NSMAX>(a, t, xs);
 }
 
 template <int KCH, int NP>
@@ -24,7 +24,7 @@ __global__ __launch_bounds__(256) void router_resid_kernel(const RouterResidArgs
   __shared__ float red[4];
   RouterPre<KCH> p;
   router_issue<KCH>(a, blockIdx.x, p);
-  router_finish<KCH, NP, false>(a, blockIdx.x, p, xs, red);
+  router_finish<KCH, NP>(a, blockIdx.x, p, xs, red);
 }
 
 bool overlaps(const void* a, int64_t na, const void* b, int64_t nb) {

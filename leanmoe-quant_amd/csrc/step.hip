@@ -2,14 +2,7 @@
 // canonical cell (w8a16 attention + experts, W8 lm_head, KV-INT8 cache) on a
 // stream, ready to be captured into a hipGraph by the caller.
 //
-// Per layer, with a sync workspace, one_launch bit 0 and the shapes
-// lemoq_attn_layer_check covers (4 launches):
-//   1 gemv_w8_fused   input RMSNorm (+ embedding gather on layer 0) -> packed q|k|v
-//   2 attn_layer_i8   2-4 below as ONE launch whose workgroups hand results to
-//                     each other through the sync workspace (attn_layer.hip)
-//   3 moe_gate_up_w8, 4 moe_down_w8 as 5-6 below.
-// With one_launch bit 1, 5-6 run as ONE launch too (moe_layer_w8).
-// Otherwise (6 launches):
+// Per layer (6 launches):
 //   1 gemv_w8_fused   input RMSNorm (+ embedding gather on layer 0) -> packed q|k|v
 //   2 attn_split_fused q_norm/k_norm, RoPE at *pos, KV-INT8 write of slot *pos,
 //                     split-KV partials over [0, *pos]
@@ -62,10 +55,10 @@ int check_gemv(int64_t N, int64_t K, int64_t group) {
   return LEMOQ_OK;
 }
 
-enum AttnPath { kAttnLayer, kAttnFusedOut, kAttnThree };
+enum AttnPath { kAttnFusedOut, kAttnThree };
 
 // Every rule of every launch of the step, before anything is enqueued.
-int validate(const LemoqOlmoeStep* p, AttnPath* path, bool* moe_one) {
+int validate(const LemoqOlmoeStep* p, AttnPath* path) {
   if (!p || !p->layers) return LEMOQ_ERR_NULL;
   if (!p->embed || !p->final_norm || !p->lm_codes || !p->lm_scale || !p->cos_tab ||
       !p->sin_tab || !p->token || !p->pos || !p->filled || !p->h || !p->xn || !p->qkv ||
@@ -115,9 +108,6 @@ int validate(const LemoqOlmoeStep* p, AttnPath* path, bool* moe_one) {
     if (overlaps(p->h_mid, H * 2, p->h, H * 2) || overlaps(p->h_mid, H * 2, p->o_part, n_part * H * 4))
       return LEMOQ_ERR_SHAPE;
     *path = kAttnFusedOut;
-    if (p->sync && (p->one_launch & 1) &&
-        lemoq_attn_layer_check(p->heads, D, ns, H, g, E) == LEMOQ_OK)
-      *path = kAttnLayer;
   } else {
     LEMOQ_TRY(check_gemv(H, HD, g));
     if (ns > 1024 || D > 256) return LEMOQ_ERR_SHAPE;
@@ -126,107 +116,58 @@ int validate(const LemoqOlmoeStep* p, AttnPath* path, bool* moe_one) {
     if (!a16(p->attn)) return LEMOQ_ERR_ALIGN;
     *path = kAttnThree;
   }
-  if (p->sync) {
-    if (p->sync_timeout_us < 0) return LEMOQ_ERR_SHAPE;
-    if ((reinterpret_cast<uintptr_t>(p->sync) & 255u) != 0) return LEMOQ_ERR_ALIGN;
-  }
-  // the MoE as one launch (moe_layer.hip)
-  *moe_one = p->sync && (p->one_launch & 2) && p->moe_part &&
-             lemoq_moe_layer_check(K, E, F, H, g) == LEMOQ_OK;
-  if (*moe_one && !a16(p->moe_part)) return LEMOQ_ERR_ALIGN;
   return LEMOQ_OK;
-}
-
-// The down -> next q|k|v hand-off (down_qkv.hip) takes its status and launch
-// counter from sync words 0 and 1 and its buffer from 32 KB into the sync
-// workspace (the one-launch MoE, which it excludes, uses that range too).
-constexpr int64_t kLLOffsetWords = 8192;
-bool use_down_qkv(const LemoqOlmoeStep* p, bool moe_one) {
-  if (!p->sync || !(p->one_launch & 4) || moe_one || p->num_layers < 2) return false;
-  if (kLLOffsetWords + p->hidden > LEMOQ_SYNC_WORDS) return false;
-  return lemoq_moe_down_qkv_check(p->top_k, p->hidden, p->ffn, p->group, 3 * p->heads * p->head_dim) == LEMOQ_OK;
 }
 
 }  // namespace
 
 extern "C" int lemoq_olmoe_decode_step(const LemoqOlmoeStep* p, void* stream) {
   AttnPath path = kAttnThree;
-  bool moe_one = false;
-  LEMOQ_TRY(validate(p, &path, &moe_one));
+  LEMOQ_TRY(validate(p, &path));
   const int64_t H = p->hidden, HD = p->heads * p->head_dim, D = p->head_dim;
   const int64_t S = p->max_seq;
   const int64_t n_part = HD / 512;
-  const bool dq = use_down_qkv(p, moe_one);
-  uint64_t* ll = dq ? reinterpret_cast<uint64_t*>(p->sync + kLLOffsetWords) : nullptr;
   for (int64_t L = 0; L < p->num_layers; ++L) {
     const LemoqOlmoeLayer& w = p->layers[L];
     const bool first = L == 0;
     // 1. input RMSNorm + packed qkv projection.  Layer 0 gathers the
     //    embedding row of *token and block 0 stores it as the residual.
-    //    (With the fused down launch, layers >= 1 got q|k|v from it.)
-    if (first || !dq)
-      LEMOQ_TRY(lemoq_gemv_w8_fused(first ? p->embed : p->h, first ? p->token : nullptr, p->vocab,
-                                    w.ln_in, p->eps, first ? p->h : nullptr, w.qkv_codes,
-                                    w.qkv_scale, 3 * HD, H, p->group, nullptr, p->qkv, stream));
-    if (path == kAttnLayer) {
-      // 2-4 as one launch: attention, merge + o_proj, residual + norm + router.
-      LEMOQ_TRY(lemoq_attn_layer_i8(p->qkv, p->heads, D, w.q_norm, w.k_norm, p->eps, p->cos_tab,
-                                    p->sin_tab, p->pos, w.kc, w.ks, w.vc, w.vs, S * D, S,
-                                    p->num_splits, p->qk_scale, p->part_m, p->part_l, p->part_acc,
-                                    w.o_codes, w.o_scale, H, p->group, p->o_part, p->h, w.ln_post,
-                                    w.router, p->num_experts, p->h_mid, p->xn, p->router_logits,
-                                    p->sync, p->sync_timeout_us, stream));
+    LEMOQ_TRY(lemoq_gemv_w8_fused(first ? p->embed : p->h, first ? p->token : nullptr, p->vocab,
+                                  w.ln_in, p->eps, first ? p->h : nullptr, w.qkv_codes,
+                                  w.qkv_scale, 3 * HD, H, p->group, nullptr, p->qkv, stream));
+    // 2. q/k norm, RoPE, KV-INT8 write at slot *pos, split-KV partials.
+    LEMOQ_TRY(lemoq_attn_split_fused_i8(p->qkv, p->heads, D, w.q_norm, w.k_norm, p->eps,
+                                        p->cos_tab, p->sin_tab, p->pos, w.kc, w.ks, w.vc, w.vs,
+                                        S * D, S, p->num_splits, p->qk_scale, p->part_m,
+                                        p->part_l, p->part_acc, stream));
+    if (path == kAttnFusedOut) {
+      // 3. LSE merge + o_proj partials per group of 4 heads.
+      LEMOQ_TRY(lemoq_attn_merge_o_proj_w8(p->part_m, p->part_l, p->part_acc, p->heads,
+                                           p->num_splits, D, w.o_codes, w.o_scale, H, p->group,
+                                           p->o_part, stream));
+      // 4. h_mid = fp16(fp16(o) + h); post-attention RMSNorm + router logits.
+      LEMOQ_TRY(lemoq_router_logits_resid(p->o_part, n_part, p->h, w.ln_post, p->eps, H,
+                                          w.router, p->num_experts, p->h_mid, p->xn,
+                                          p->router_logits, stream));
     } else {
-      // 2. q/k norm, RoPE, KV-INT8 write at slot *pos, split-KV partials.
-      LEMOQ_TRY(lemoq_attn_split_fused_i8(p->qkv, p->heads, D, w.q_norm, w.k_norm, p->eps,
-                                          p->cos_tab, p->sin_tab, p->pos, w.kc, w.ks, w.vc, w.vs,
-                                          S * D, S, p->num_splits, p->qk_scale, p->part_m,
-                                          p->part_l, p->part_acc, stream));
-      if (path == kAttnFusedOut) {
-        // 3. LSE merge + o_proj partials per group of 4 heads.
-        LEMOQ_TRY(lemoq_attn_merge_o_proj_w8(p->part_m, p->part_l, p->part_acc, p->heads,
-                                             p->num_splits, D, w.o_codes, w.o_scale, H, p->group,
-                                             p->o_part, stream));
-        // 4. h_mid = fp16(fp16(o) + h); post-attention RMSNorm + router logits.
-        LEMOQ_TRY(lemoq_router_logits_resid(p->o_part, n_part, p->h, w.ln_post, p->eps, H,
-                                            w.router, p->num_experts, p->h_mid, p->xn,
-                                            p->router_logits, stream));
-      } else {
-        // 3. LSE merge of the partials.
-        LEMOQ_TRY(lemoq_attn_merge(p->part_m, p->part_l, p->part_acc, p->heads, p->num_splits, D,
-                                   p->attn, stream));
-        // 4. o_proj; h = fp16(fp16(o) + h).
-        LEMOQ_TRY(lemoq_gemv_w8_fused(p->attn, nullptr, 0, nullptr, p->eps, nullptr, w.o_codes,
-                                      w.o_scale, H, HD, p->group, p->h, p->h, stream));
-        // 4b. post-attention RMSNorm + router logits.
-        LEMOQ_TRY(lemoq_router_logits(p->h, w.ln_post, p->eps, H, w.router, p->num_experts, p->xn,
-                                      p->router_logits, stream));
-      }
+      // 3. LSE merge of the partials.
+      LEMOQ_TRY(lemoq_attn_merge(p->part_m, p->part_l, p->part_acc, p->heads, p->num_splits, D,
+                                 p->attn, stream));
+      // 4. o_proj; h = fp16(fp16(o) + h).
+      LEMOQ_TRY(lemoq_gemv_w8_fused(p->attn, nullptr, 0, nullptr, p->eps, nullptr, w.o_codes,
+                                    w.o_scale, H, HD, p->group, p->h, p->h, stream));
+      // 4b. post-attention RMSNorm + router logits.
+      LEMOQ_TRY(lemoq_router_logits(p->h, w.ln_post, p->eps, H, w.router, p->num_experts, p->xn,
+                                    p->router_logits, stream));
     }
-    const uint16_t* resid = path != kAttnThree ? p->h_mid : p->h;
+    const uint16_t* resid = path == kAttnFusedOut ? p->h_mid : p->h;
     // 5-6. routing + grouped MoE; h = fp16(fp16(moe) + residual).
-    if (moe_one) {
-      LEMOQ_TRY(lemoq_moe_layer_w8(p->xn, w.gu_codes, w.gu_scale, w.dn_codes, w.dn_scale,
-                                   p->router_logits, p->top_k, (int)p->norm_topk_prob,
-                                   p->num_experts, p->ffn, H, p->group, p->act, p->moe_part, resid,
-                                   p->h, p->top_i, p->top_w, p->sync, p->sync_timeout_us, stream));
-    } else {
-      LEMOQ_TRY(lemoq_moe_gate_up_w8_routed(p->xn, w.gu_codes, w.gu_scale, p->router_logits,
-                                            p->top_k, (int)p->norm_topk_prob, p->num_experts,
-                                            p->ffn, H, p->group, p->act, p->top_i, p->top_w,
-                                            stream));
-      if (dq && L + 1 < p->num_layers) {
-        // 6 + next layer's 1 as one launch.
-        const LemoqOlmoeLayer& nx = p->layers[L + 1];
-        LEMOQ_TRY(lemoq_moe_down_qkv_w8(p->act, w.dn_codes, w.dn_scale, p->top_i, p->top_w, p->top_k,
-                                        p->num_experts, H, p->ffn, p->group, resid, p->h, nx.ln_in,
-                                        p->eps, nx.qkv_codes, nx.qkv_scale, 3 * HD, p->qkv,
-                                        ll, p->sync, p->sync_timeout_us, stream));
-      } else {
-        LEMOQ_TRY(lemoq_moe_down_w8(p->act, w.dn_codes, w.dn_scale, p->top_i, p->top_w, p->top_k,
-                                    p->num_experts, H, p->ffn, p->group, resid, p->h, stream));
-      }
-    }
+    LEMOQ_TRY(lemoq_moe_gate_up_w8_routed(p->xn, w.gu_codes, w.gu_scale, p->router_logits,
+                                          p->top_k, (int)p->norm_topk_prob, p->num_experts,
+                                          p->ffn, H, p->group, p->act, p->top_i, p->top_w,
+                                          stream));
+    LEMOQ_TRY(lemoq_moe_down_w8(p->act, w.dn_codes, w.dn_scale, p->top_i, p->top_w, p->top_k,
+                                p->num_experts, H, p->ffn, p->group, resid, p->h, stream));
   }
   // Final norm + W8 lm_head with argmax partials, then greedy selection and step advance.
   return lemoq_lm_head_argmax_w8(p->h, p->final_norm, p->eps, p->lm_codes, p->lm_scale, p->vocab,

@@ -19,10 +19,7 @@ LIB_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib")
 LIB_NAME = "liblemoq_hip.so"
 LIB_PATH = os.path.join(LIB_DIR, LIB_NAME)
 
-ABI_VERSION = 4
-# include/lemoq_hip.h: the fused launches' sync workspace and its status bit
-SYNC_WORDS = 16384
-SYNC_TIMEOUT_BIT = 1
+ABI_VERSION = 5
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -107,10 +104,6 @@ class LemoqOlmoeStep(ctypes.Structure):
         ("am_len", _I64),
         ("o_part", _P),
         ("h_mid", _P),
-        ("sync", _P),
-        ("sync_timeout_us", _I64),
-        ("one_launch", _I64),
-        ("moe_part", _P),
     ]
 
 
@@ -180,26 +173,6 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         [_P, _I64, _I64, _P, _P, _F, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _F, _P, _P, _P, _P],
     ),
 
-    "lemoq_attn_layer_i8": (
-        _I,
-        [
-            _P, _I64, _I64, _P, _P, _F, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _F, _P, _P, _P,
-            _P, _P, _I64, _I64, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _I64, _P,
-        ],
-    ),
-    "lemoq_attn_layer_check": (_I, [_I64, _I64, _I64, _I64, _I64, _I64]),
-    "lemoq_sync_reset": (_I, [_P, _P]),
-    "lemoq_moe_layer_w8": (
-        _I,
-        [_P, _P, _P, _P, _P, _P, _I64, _I, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _I64, _P],
-    ),
-    "lemoq_moe_layer_check": (_I, [_I64, _I64, _I64, _I64, _I64]),
-    "lemoq_moe_down_qkv_w8": (
-        _I,
-        [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _F, _P, _P, _I64, _P, _P, _P, _I64,
-         _P],
-    ),
-    "lemoq_moe_down_qkv_check": (_I, [_I64, _I64, _I64, _I64, _I64]),
     "lemoq_moe_gate_up_w8_routed": (
         _I,
         [_P, _P, _P, _P, _I64, _I, _I64, _I64, _I64, _I64, _P, _P, _P, _P],

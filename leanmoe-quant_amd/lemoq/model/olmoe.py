@@ -47,14 +47,6 @@ LOG2E = 1.4426950408889634
 # with the split count (2.5 us at 8 splits, 2.9 at 16, 3.6 at 32).
 STEP_SLOTS_PER_SPLIT = 64
 STEP_MAX_SPLITS = 64
-# Time limit of each cross-workgroup wait inside the fused attention-layer
-# launch; a healthy wait takes microseconds.
-SYNC_TIMEOUT_US = 200_000
-# Whether the step runs each layer's attention half / its MoE as one launch
-# by default.
-ATTENTION_ONE_LAUNCH_DEFAULT = False
-MOE_ONE_LAUNCH_DEFAULT = False
-DOWN_QKV_FUSED_DEFAULT = False
 
 
 def step_num_splits(max_seq: int, heads: int, compute_units: int = 256) -> int:
@@ -217,9 +209,6 @@ class DecodeSession:
         *,
         max_new_tokens: int,
         num_splits: int | None = None,
-        attention_one_launch: bool | None = None,
-        moe_one_launch: bool | None = None,
-        down_qkv_fused: bool | None = None,
     ) -> None:
         from lemoq.kernels.attn_decode import resolve_num_splits  # noqa: PLC0415
         from lemoq.kernels.rope import rotary_cos_sin  # noqa: PLC0415
@@ -286,12 +275,6 @@ class DecodeSession:
         # does not cover, which run merge, o_proj and router as three launches)
         self.o_part = torch.zeros((max(1, HD // 512), s.hidden), dtype=torch.float32, device=dev)
         self.h_mid = torch.zeros((s.hidden,), **f16)
-        # Counters and status word of the fused attention-layer launch (its
-        # workgroups hand results to each other inside the launch); zero
-        # between launches.  256-byte aligned (one counter per line).
-        self.sync = torch.zeros((_hip.SYNC_WORDS,), dtype=torch.int32, device=dev)
-        if self.sync.data_ptr() % 256 != 0:
-            raise RuntimeError("sync workspace is not 256-byte aligned")
 
         P = _hip.ptr
         self._layer_structs = (_hip.LemoqOlmoeLayer * s.layers)()
@@ -326,17 +309,6 @@ class DecodeSession:
                      "h_mid"):
             setattr(st, name, P(getattr(self, name)))
         st.am_len = n_parts
-        # The attention half and the MoE of each layer as one launch each
-        # (lemoq_attn_layer_i8, lemoq_moe_layer_w8) where the shape allows it;
-        # None takes the measured default.
-        one_attn = ATTENTION_ONE_LAUNCH_DEFAULT if attention_one_launch is None else bool(attention_one_launch)
-        one_moe = MOE_ONE_LAUNCH_DEFAULT if moe_one_launch is None else bool(moe_one_launch)
-        self.moe_part = torch.zeros((s.top_k, s.hidden), dtype=torch.float32, device=dev)
-        dq = DOWN_QKV_FUSED_DEFAULT if down_qkv_fused is None else bool(down_qkv_fused)
-        st.sync = P(self.sync) if (one_attn or one_moe or dq) else None
-        st.sync_timeout_us = SYNC_TIMEOUT_US
-        st.one_launch = (1 if one_attn else 0) | (2 if one_moe else 0) | (4 if dq else 0)
-        st.moe_part = P(self.moe_part)
         self._step = st
         self.graph: Any = None
         self.graph_multi: Any = None  # steps_per_graph decode steps in one graph (capture(steps_per_graph=K))
@@ -358,16 +330,7 @@ class DecodeSession:
         self.filled.fill_(1)
         self.history.zero_()
         self.history[:1].copy_(self.prompt[:1])
-        self.sync.zero_()
         self._host_pos = 0
-
-    def check_sync_status(self) -> None:
-        """Raise if a cross-workgroup wait of a fused launch gave up since the last
-        reset (the step's outputs are then invalid; ``reset()`` clears it)."""
-        st = int(self.sync[0].item())
-        if st != 0:
-            raise RuntimeError("a fused launch's cross-workgroup wait timed out (status 0x%x); "
-                               "the step's results are invalid, reset() the session" % st)
 
     def set_position(self, position: int, token: int | None = None) -> None:
         """Move the decode position (graph-safe: only device scalars change)."""
@@ -406,37 +369,6 @@ class DecodeSession:
         return self.logits
 
     @property
-    def moe_layer_fused(self) -> bool:
-        """Whether each layer's MoE runs as one launch (lemoq_moe_layer_w8)."""
-        s = self.shape
-        if not (self._step.sync and (self._step.one_launch & 2) and self._step.moe_part):
-            return False
-        rc = _hip.load().lemoq_moe_layer_check(s.top_k, s.num_experts, s.ffn, s.hidden, s.group_size)
-        return int(rc) == 0
-
-    @property
-    def attn_layer_fused(self) -> bool:
-        """Whether each layer's attention half runs as one launch (lemoq_attn_layer_i8)."""
-        s = self.shape
-        if not (self._step.sync and (self._step.one_launch & 1) and self.attn_output_fused):
-            return False
-        rc = _hip.load().lemoq_attn_layer_check(s.heads, s.head_dim, self.num_splits, s.hidden, s.group_size,
-                                                s.num_experts)
-        return int(rc) == 0
-
-    @property
-    def down_qkv_fused(self) -> bool:
-        """Whether each layer's down projection and the next layer's q|k|v run as one
-        launch (lemoq_moe_down_qkv_w8; the buffer rule of csrc/step.hip)."""
-        s = self.shape
-        if not (self._step.sync and (self._step.one_launch & 4)) or self.moe_layer_fused or s.layers < 2:
-            return False
-        if 8192 + s.hidden > _hip.SYNC_WORDS:
-            return False
-        rc = _hip.load().lemoq_moe_down_qkv_check(s.top_k, s.hidden, s.ffn, s.group_size, s.qkv_rows)
-        return int(rc) == 0
-
-    @property
     def attn_output_fused(self) -> bool:
         """Whether the step runs merge + o_proj as one launch and the residual add
         in the router launch (the shape rule of csrc/step.hip)."""
@@ -449,11 +381,8 @@ class DecodeSession:
     @property
     def launches_per_step(self) -> int:
         """Kernel launches in one captured step (see csrc/step.hip)."""
-        per_layer = 4 if self.attn_layer_fused else (6 if self.attn_output_fused else 7)
-        if self.moe_layer_fused:
-            per_layer -= 1
-        fused_dq = self.shape.layers - 1 if self.down_qkv_fused else 0
-        return per_layer * self.shape.layers + 2 - fused_dq
+        per_layer = 6 if self.attn_output_fused else 7
+        return per_layer * self.shape.layers + 2
 
     def capture(self, steps_per_graph: int = 1) -> dict[str, Any]:
         """Capture one decode step into a hipGraph (state is untouched by the capture).
@@ -504,7 +433,6 @@ class DecodeSession:
         self._host_pos += n
         if synchronize:
             torch.cuda.synchronize(self.device)
-            self.check_sync_status()
         return self.logits
 
     def prefill(self, mode: str = "batched", *, kv_f16: list | None = None) -> int:
@@ -546,7 +474,6 @@ class DecodeSession:
 
     def logits_cpu(self) -> Any:
         torch.cuda.synchronize(self.device)
-        self.check_sync_status()
         return self.logits.detach().to("cpu").clone()
 
     def kv_cpu(self) -> list[dict[str, Any]]:

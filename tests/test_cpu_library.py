@@ -141,8 +141,6 @@ def _fake_step(**over):
             setattr(st, name, nxt())
     st.prompt_len, st.history_len = 4, 1200
     st.am_len = int(_hip.load().lemoq_lm_head_argmax_parts(50304))
-    st.sync = None
-    st.sync_timeout_us = 1000
     for k, v in over.items():
         setattr(st, k, v)
     return st, layers
@@ -173,7 +171,5 @@ def test_decode_step_rejects_before_any_launch():
     st, layers = _fake_step()
     layers[1].router = None                                 # layer 1's router missing
     assert lib.lemoq_olmoe_decode_step(ctypes.byref(st), None) == -1
-    assert step(sync=(1 << 30) + 64) == -4                  # the fused layer's sync workspace alignment
-    assert step(sync=1 << 30, sync_timeout_us=-1) == -2
     # unfused attention-output path (no o_part): merge split bound
     assert step(o_part=None, num_splits=2000) == -2

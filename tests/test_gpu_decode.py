@@ -393,65 +393,3 @@ def test_fused_attention_output_path_matches_three_launches(dev):
         assert kl < 1e-4, kl
         if int(torch.argmax(got.float())) != int(torch.argmax(ref.float())):
             assert _margin(ref) <= 2 * diff
-
-
-def test_attn_layer_step_equals_two_launch_step_bitwise(dev):
-    """At the OLMoE shape the step runs each layer's attention half as one launch
-    (lemoq_attn_layer_i8, workgroups handing results over inside the launch).
-    Without the sync workspace the same step runs it as split attention, merge
-    + o_proj, and residual + norm + router launches.  The arithmetic is the
-    same, so the logits, the token and the KV-INT8 cache must be identical."""
-    print("case: one-launch attention half vs three launches, OLMoE shape, 4 layers, ctx 1024", flush=True)
-    shape = OlmoeShape(**{**OLMOE_1B_7B.__dict__, "layers": 4})
-    w = OlmoeW8Weights.random(shape, seed=12, device=dev)
-    sess = DecodeSession(w, [2] * 1024, max_new_tokens=8, num_splits=None, attention_one_launch=True)
-    assert sess.attn_layer_fused and sess.launches_per_step == 4 * 4 + 2
-    sess.prefill()
-    sync = sess._step.sync
-    for _ in range(4):
-        p, tok = sess.position, int(sess.token.item())
-        sess._step.sync = None
-        sess.decode_eager()
-        ref, ref_tok = sess.logits_cpu(), int(sess.token.item())
-        ref_kv = [{k: v.clone() for k, v in kv.items()} for kv in sess.kv_cpu()]
-        sess._step.sync = sync
-        sess.set_position(p, tok)
-        sess.decode_eager()
-        got = sess.logits_cpu()
-        assert torch.equal(got.view(torch.int16), ref.view(torch.int16)), p
-        assert int(sess.token.item()) == ref_tok
-        for a, b in zip(sess.kv_cpu(), ref_kv):
-            for k in a:
-                assert torch.equal(a[k].view(torch.uint8) if a[k].dtype == torch.int8 else a[k].view(torch.int16),
-                                   b[k].view(torch.uint8) if b[k].dtype == torch.int8 else b[k].view(torch.int16)), k
-        assert int(torch.count_nonzero(sess.sync)) == 0
-
-
-def test_moe_one_launch_step_equals_two_launch_step_bitwise(dev):
-    """With the MoE of each layer as one launch (lemoq_moe_layer_w8) the step's
-    logits, token and KV-INT8 cache equal the two-launch step's bit for bit."""
-    print("case: one-launch MoE vs two launches, OLMoE shape, 4 layers, ctx 1024", flush=True)
-    shape = OlmoeShape(**{**OLMOE_1B_7B.__dict__, "layers": 4})
-    w = OlmoeW8Weights.random(shape, seed=13, device=dev)
-    sess = DecodeSession(w, [3] * 1024, max_new_tokens=8, num_splits=None, moe_one_launch=True,
-                         attention_one_launch=False)
-    assert sess.moe_layer_fused and sess.launches_per_step == 5 * 4 + 2
-    sess.prefill()
-    sync = sess._step.sync
-    for _ in range(4):
-        p, tok = sess.position, int(sess.token.item())
-        sess._step.sync = None
-        sess.decode_eager()
-        ref, ref_tok = sess.logits_cpu(), int(sess.token.item())
-        ref_kv = sess.kv_cpu()
-        sess._step.sync = sync
-        sess.set_position(p, tok)
-        sess.decode_eager()
-        got = sess.logits_cpu()
-        assert torch.equal(got.view(torch.int16), ref.view(torch.int16)), p
-        assert int(sess.token.item()) == ref_tok
-        for a, b in zip(sess.kv_cpu(), ref_kv):
-            for k in a:
-                assert torch.equal(a[k].view(torch.uint8) if a[k].dtype == torch.int8 else a[k].view(torch.int16),
-                                   b[k].view(torch.uint8) if b[k].dtype == torch.int8 else b[k].view(torch.int16)), k
-        assert int(torch.count_nonzero(sess.sync)) == 0
