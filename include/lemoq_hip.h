@@ -232,7 +232,10 @@ int lemoq_attn_merge_o_proj_w8(const float* m, const float* l, const float* acc,
  * A10 — RMSNorm, HF rounding points: y = fp16(fp16(x*rsqrt(mean(x^2)+eps)) * w).
  * Replaces rms_norm_fused (src/lemoq/kernels/rmsnorm.py:102-163, kernel
  * :173-202).  x, y (rows, hidden) fp16 contiguous; w (hidden,) fp16;
- * hidden <= 8192.
+ * hidden <= 8192.  Rows with hidden % 8 == 0 and x, w, y 16-byte aligned are
+ * read in 16-byte chunks; other rows one element per thread, which sums the
+ * squares in another fp32 order, so the two can differ by an fp16 ulp on the
+ * same row (the rounding points are the same).
  * ------------------------------------------------------------------------- */
 int lemoq_rmsnorm(const uint16_t* x, int64_t rows, int64_t hidden,
                   const uint16_t* w, float eps, uint16_t* y, void* stream);
@@ -601,8 +604,10 @@ int lemoq_moe_prefill_combine(const uint16_t* y, const int64_t* top_i, int64_t T
 
 /* lemoq_moe_prefill_combine, and in the same launch xn_out[t] = the RMSNorm
  * of out[t] with norm_w (the next decoder layer's input_layernorm, rounded as
- * lemoq_rmsnorm rounds it, bit for bit).  H <= 8192; xn_out (T, H) must not
- * overlap y, residual or out. */
+ * lemoq_rmsnorm rounds it on 16-byte aligned rows, bit for bit: the same sum
+ * order of the squares).  H <= 8192; norm_w and xn_out 16-byte aligned too
+ * (the norm reads and writes 16-byte chunks); xn_out (T, H) must not overlap
+ * y, residual or out. */
 int lemoq_moe_prefill_combine_norm(const uint16_t* y, const int64_t* top_i, int64_t T, int64_t top_k,
                                    int64_t H, const uint16_t* residual, uint16_t* out,
                                    const uint16_t* norm_w, float eps, uint16_t* xn_out, void* stream);

@@ -534,7 +534,9 @@ extern "C" int lemoq_moe_prefill_combine_norm(const uint16_t* y, const int64_t* 
   if (!y || !top_i || !out || !norm_w || !xn_out) return LEMOQ_ERR_NULL;
   if (T <= 0 || T > 0x7fffffffLL || top_k <= 0 || top_k > 8 || H <= 0 || H % 8 != 0 || H > kCombineNormMaxH)
     return LEMOQ_ERR_SHAPE;
-  if (!lemoq_aligned16(y) || !lemoq_aligned16(out) || (residual && !lemoq_aligned16(residual)))
+  // the row norm reads norm_w and writes xn_out in 16-byte chunks too
+  if (!lemoq_aligned16(y) || !lemoq_aligned16(out) || (residual && !lemoq_aligned16(residual)) ||
+      !lemoq_aligned16(norm_w) || !lemoq_aligned16(xn_out))
     return LEMOQ_ERR_ALIGN;
   // xn_out must not overlap the rows the block reads (y, the residual) or writes (out)
   const uintptr_t xa = (uintptr_t)xn_out, xb = xa + (uintptr_t)(T * H * 2);

@@ -95,6 +95,8 @@ def test_argument_rejection_happens_before_any_launch():
     assert cn(4, 8200, 1 << 20, fake, 1 << 22) == -2
     assert cn(4, 2048, 1 << 20, fake, (1 << 20) + 4096) == -2
     assert cn(4, 2048, 1 << 20, None, 1 << 22) == -1
+    assert cn(4, 2048, 1 << 20, fake + 2, 1 << 22) == -4      # norm weight misaligned
+    assert cn(4, 2048, 1 << 20, fake, (1 << 22) + 8) == -4    # xn_out misaligned
     # fused merge + o_proj: head_dim 64 and 6 heads unsupported, N % 32, too many splits, misaligned codes
     assert lib.lemoq_attn_merge_o_proj_w8(fake, fake, fake, 16, 16, 64, fake, fake, 2048, 128, fake, None) == -3
     assert lib.lemoq_attn_merge_o_proj_w8(fake, fake, fake, 6, 16, 128, fake, fake, 2048, 128, fake, None) == -3
