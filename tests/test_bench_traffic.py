@@ -93,3 +93,32 @@ def test_in_graph_duration_read_from_trace_table(tmp_path, monkeypatch):
     assert bench._in_graph_from_profiles("moe_down_kernel<1, 4, true>") is None
     monkeypatch.setattr(bench, "REPO", str(tmp_path / "missing"))
     assert bench._in_graph_from_profiles("moe_gate_up_kernel<2, 2, 1, true>") is None
+
+
+def test_summarize_step_timeline(tmp_path):
+    """bench.py --summarize-step on a synthetic kernel trace of two whole decode
+    steps (16 layers x 6 launches + lm_head + argmax, each kernel 2 us with a
+    1 us gap) plus a prefill seed pick (argmax alone): two steps, span and busy
+    time of each, per-kernel averages."""
+    path = tmp_path / "trace.csv"
+    names = [k for _, k in bench.STEP_LAYER_KERNELS] * 16 + [k for _, k in bench.STEP_TAIL_KERNELS]
+    rows, t = [], 1000
+    rows.append(("void (anonymous namespace)::argmax_advance_kernel<true>(args)", t, t + 2000))  # prefill seed pick
+    t += 5000
+    for _ in range(2):
+        for n in names:
+            rows.append(("void (anonymous namespace)::%s(args)" % n.replace("<", "<").strip(), t, t + 2000))
+            t += 3000
+    with open(path, "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=["Kernel_Name", "Start_Timestamp", "End_Timestamp"])
+        w.writeheader()
+        for n, a, b in rows:
+            w.writerow({"Kernel_Name": n, "Start_Timestamp": a, "End_Timestamp": b})
+    out = bench.summarize_step(str(path))
+    per_step = 16 * 6 + 2
+    assert out.startswith("2 whole steps of %d launches" % per_step)
+    span = (per_step - 1) * 3.0 + 2.0
+    assert "step span p50 %.1f us" % span in out
+    assert "kernel busy time p50 %.1f us" % (per_step * 2.0) in out
+    assert "| qkv (+ input RMSNorm) | 16 | 2.00 |" in out
+    assert "| argmax + advance | 1 | 2.00 |" in out
