@@ -239,7 +239,9 @@ def kernel_table(torch, hip, w, sess, flusher, reps: int, floors: bool = True) -
         [lambda i=i: hip.call("lemoq_attn_split_fused_i8", P(sess.qkv), s.heads, D, P(L[i].q_norm),
                                P(L[i].k_norm), s.eps, P(sess.cos_tab), P(sess.sin_tab), P(sess.pos),
                                P(kv[i]["kc"]), P(kv[i]["ks"]), P(kv[i]["vc"]), P(kv[i]["vs"]), S * D, S, ns,
-                               qk_scale, P(sess.part_m), P(sess.part_l), P(sess.part_acc), st())
+                               qk_scale, P(sess.part_m), P(sess.part_l), P(sess.part_acc),
+                               math.inf if s.clip_qkv is None else s.clip_qkv,
+                               st())
          for i in range(nl)],
         ["attn_split_fused_i8_kernel"])
     if sess.attn_output_fused:

@@ -352,8 +352,11 @@ int lemoq_router_topk_fused(const uint16_t* h, const uint16_t* norm_w, float eps
  * the new k and v rows KV-INT8-quantised to slot *pos (same arithmetic as
  * lemoq_kv_write_i8).  k_f16/v_f16 (nullable): also copy the fp16 rows into an
  * fp16 cache at h*f16_head_stride + (*pos)*D.  k_rot_out (nullable): the
- * fp16 rotated k row, for tests.  Replaces the sequence at
- * src/lemoq/kernels/attn_decode.py:882-987.
+ * fp16 rotated k row, for tests.  clip_qkv: HF OLMoE's clip_qkv, applied as
+ * the reference applies it (src/lemoq/kernels/attn_decode.py:903-907, after
+ * q_norm/k_norm, before RoPE, and to v): values beyond +-clip_qkv become
+ * +-fp16(clip_qkv), NaN stays; +INFINITY disables it; a negative or NaN bound
+ * is rejected.  Replaces the sequence at src/lemoq/kernels/attn_decode.py:882-987.
  * ------------------------------------------------------------------------- */
 int lemoq_qk_norm_rope_kv_i8(const uint16_t* qkv, int64_t heads, int64_t head_dim,
                              const uint16_t* q_norm_w, const uint16_t* k_norm_w,
@@ -363,7 +366,7 @@ int lemoq_qk_norm_rope_kv_i8(const uint16_t* qkv, int64_t heads, int64_t head_di
                              uint16_t* vs, int64_t code_head_stride, int64_t s_len,
                              uint16_t* k_f16, uint16_t* v_f16,
                              int64_t f16_head_stride, uint16_t* k_rot_out,
-                             void* stream);
+                             float clip_qkv, void* stream);
 
 /* A16 fused (no reference counterpart as one call: it joins the q_norm/k_norm,
  * RoPE, KV-INT8 write and split-KV int8 attention sequence of
@@ -372,7 +375,7 @@ int lemoq_qk_norm_rope_kv_i8(const uint16_t* qkv, int64_t heads, int64_t head_di
  * n = *pos + 1, c = ceil(n/num_splits).  From the packed q|k|v row, q and the
  * new k are RMS-normed over heads*D and rotated at *pos; the block holding
  * *pos quantises the new k and v to KV-INT8 and writes them to slot *pos
- * (same arithmetic and bytes as lemoq_qk_norm_rope_kv_i8).  Writes the
+ * (same arithmetic, clip_qkv included, and bytes as lemoq_qk_norm_rope_kv_i8).  Writes the
  * partials m, l (heads, num_splits) and acc (heads, num_splits, D) of
  * lemoq_attn_split_i8 over tokens [0, *pos]; merge them with
  * lemoq_attn_merge.  D in {64, 128, 256}. */
@@ -382,7 +385,7 @@ int lemoq_attn_split_fused_i8(const uint16_t* qkv, int64_t heads, int64_t head_d
                               const int64_t* pos, int8_t* kc, uint16_t* ks, int8_t* vc,
                               uint16_t* vs, int64_t code_head_stride, int64_t s_len,
                               int64_t num_splits, float qk_scale, float* m, float* l, float* acc,
-                              void* stream);
+                              float clip_qkv, void* stream);
 
 /* ---------------------------------------------------------------------------
  * A17 — greedy selection and step advance on the device (replaces the host
@@ -431,6 +434,7 @@ typedef struct LemoqOlmoeStep {
   int64_t hidden, heads, head_dim, ffn, num_experts, top_k, vocab, group;
   int64_t num_layers, max_seq, num_splits, norm_topk_prob;
   float eps, qk_scale;
+  float clip_qkv;                /* HF clip_qkv (+INFINITY: none); see lemoq_qk_norm_rope_kv_i8 */
   /* weights */
   const LemoqOlmoeLayer* layers; /* host array of num_layers entries */
   const uint16_t* embed;         /* (vocab, H) fp16 */
@@ -541,14 +545,15 @@ int lemoq_gather_rows(const uint16_t* src, int64_t n_rows, int64_t H, const int6
  * kv_int8_bulk_quantize, src/lemoq/kernels/kv_int8.py:127-162, gives for the
  * fp16 cache rows); k_f16/v_f16 (nullable) fp16 copies at
  * h*f16_head_stride + pos*D for the prefill attention.  pos0 + rows <= s_len;
- * cos_tab/sin_tab hold s_len rows. */
+ * cos_tab/sin_tab hold s_len rows.  clip_qkv as for lemoq_qk_norm_rope_kv_i8. */
 int lemoq_qk_norm_rope_kv_i8_rows(const uint16_t* qkv, int64_t rows, int64_t heads,
                                   int64_t head_dim, const uint16_t* q_norm_w,
                                   const uint16_t* k_norm_w, float eps, const uint16_t* cos_tab,
                                   const uint16_t* sin_tab, int64_t pos0, uint16_t* q_out,
                                   int8_t* kc, uint16_t* ks, int8_t* vc, uint16_t* vs,
                                   int64_t code_head_stride, int64_t s_len, uint16_t* k_f16,
-                                  uint16_t* v_f16, int64_t f16_head_stride, void* stream);
+                                  uint16_t* v_f16, int64_t f16_head_stride, float clip_qkv,
+                                  void* stream);
 
 /* Causal attention over T prompt rows (HF OlmoeAttention with sdpa, the
  * reference's multi-token path, src/lemoq/kernels/attn_decode.py:836-1017):

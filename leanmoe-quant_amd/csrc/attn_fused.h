@@ -47,6 +47,7 @@ struct AttnSplitArgs {
   int heads;
   int ns;
   float qk_scale;  // softmax scale * log2(e)
+  float clip;      // clip_qkv bound (+inf: none)
   float* m_out;    // (heads, ns)
   float* l_out;    // (heads, ns)
   float* acc_out;  // (heads, ns, D)
@@ -163,9 +164,14 @@ __device__ __forceinline__ void attn_split_fused_block(const AttnSplitArgs& a, i
     // d = lane + 64 i, so for D >= 128 a lane holds both rotate_half partners
     // (d and d + D/2) and RoPE needs no cross-lane exchange; for D = 64 the
     // partner is lane ^ 32.
+    const float clip16 = h2f(f2h(a.clip));
     float o[EPL];
 #pragma unroll
     for (int i = 0; i < EPL; ++i) o[i] = h2f(ob[i]);
+    if (which == 2) {
+#pragma unroll
+      for (int i = 0; i < EPL; ++i) o[i] = clip_qkv(o[i], a.clip, clip16);
+    }
     if (which < 2) {
       // Same sum-of-squares order as lemoq_qk_norm_rope_kv_i8 (slices
       // lane*8 + 512 j, ssq_f16x8), so both write identical KV bytes.
@@ -178,7 +184,8 @@ __device__ __forceinline__ void attn_split_fused_block(const AttnSplitArgs& a, i
       const float rstd = 1.0f / sqrtf(wave_sum(ssq) / (float)HD + a.eps);
       float xn[EPL];
 #pragma unroll
-      for (int i = 0; i < EPL; ++i) xn[i] = h2f(f2h(h2f(f2h(o[i] * rstd)) * h2f(wb[i])));
+      for (int i = 0; i < EPL; ++i)
+        xn[i] = clip_qkv(h2f(f2h(h2f(f2h(o[i] * rstd)) * h2f(wb[i]))), a.clip, clip16);
 #pragma unroll
       for (int i = 0; i < EPL; ++i) {
         const bool first = EPL == 1 ? lane < 32 : i < EPL / 2;  // d < D/2

@@ -21,13 +21,14 @@ extern "C" int lemoq_attn_split_fused_i8(const uint16_t* qkv, int64_t heads, int
                                          uint16_t* ks, int8_t* vc, uint16_t* vs,
                                          int64_t code_head_stride, int64_t s_len,
                                          int64_t num_splits, float qk_scale, float* m, float* l,
-                                         float* acc, void* stream) {
+                                         float* acc, float clip_qkv, void* stream) {
   if (!qkv || !q_norm_w || !k_norm_w || !cos_tab || !sin_tab || !pos || !kc || !ks || !vc || !vs ||
       !m || !l || !acc)
     return LEMOQ_ERR_NULL;
   if (head_dim != 64 && head_dim != 128 && head_dim != 256) return LEMOQ_ERR_UNSUPPORTED;
   if (heads <= 0 || heads > 65535 || heads * head_dim > 65536) return LEMOQ_ERR_SHAPE;
   if (num_splits <= 0 || num_splits > 65535) return LEMOQ_ERR_SHAPE;
+  if (!(clip_qkv >= 0.0f)) return LEMOQ_ERR_SHAPE;  // negative or NaN bound
   if (s_len <= 0 || s_len >= (int64_t(1) << 31) || code_head_stride < s_len * head_dim)
     return LEMOQ_ERR_SHAPE;
   if (!lemoq_aligned16(qkv) || !lemoq_aligned16(kc) || !lemoq_aligned16(vc) ||
@@ -50,6 +51,7 @@ extern "C" int lemoq_attn_split_fused_i8(const uint16_t* qkv, int64_t heads, int
   a.heads = (int)heads;
   a.ns = (int)num_splits;
   a.qk_scale = qk_scale;
+  a.clip = clip_qkv;
   a.m_out = m;
   a.l_out = l;
   a.acc_out = acc;

@@ -36,6 +36,14 @@ __device__ __forceinline__ uint16_t hadd_round(float a_f16_exact, uint16_t b) {
   return f2h(a_f16_exact + h2f(b));
 }
 
+// HF OLMoE's clip_qkv on one fp16 value (torch's clamp_(min=-c, max=c) of
+// the normed q, the normed k and the raw v rows): a value above c becomes
+// c16 = fp16(c), below -c becomes -c16, NaN passes through (both comparisons
+// are false).  c = +inf leaves every value as it is.
+__device__ __forceinline__ float clip_qkv(float x, float c, float c16) {
+  return x > c ? c16 : (x < -c ? -c16 : x);
+}
+
 // Reinterpret a dword as an fp16 pair.  Takes the dword BY VALUE on purpose:
 // clang's __builtin_bit_cast applied directly to an ext_vector element
 // (e.g. `__builtin_bit_cast(f16x2, v.y)` for a u32x4 v) reads element .x

@@ -85,8 +85,9 @@ __global__ __launch_bounds__(64) void qk_norm_rope_kv_kernel(
     uint16_t* __restrict__ q_out, int8_t* __restrict__ kc, uint16_t* __restrict__ ks,
     int8_t* __restrict__ vc, uint16_t* __restrict__ vs, int64_t code_head_stride, int64_t s_len,
     uint16_t* __restrict__ k_f16, uint16_t* __restrict__ v_f16, int64_t f16_head_stride,
-    uint16_t* __restrict__ k_rot_out) {
+    uint16_t* __restrict__ k_rot_out, float clip) {
   constexpr int D = 64 * EPL;
+  const float clip16 = h2f(f2h(clip));
   const int lane = threadIdx.x;
   const int which = blockIdx.x / heads;  // 0 q, 1 k, 2 v
   const int h = blockIdx.x - which * heads;
@@ -120,7 +121,7 @@ __global__ __launch_bounds__(64) void qk_norm_rope_kv_kernel(
     const float rstd = 1.0f / sqrtf(wave_sum(ssq) / (float)HD + eps);
     float xn[EPL];
 #pragma unroll
-    for (int i = 0; i < EPL; ++i) xn[i] = h2f(f2h(h2f(f2h(xv[i] * rstd)) * wv[i]));
+    for (int i = 0; i < EPL; ++i) xn[i] = clip_qkv(h2f(f2h(h2f(f2h(xv[i] * rstd)) * wv[i])), clip, clip16);
     const bool first = lane < 32;  // d < D/2
 #pragma unroll
     for (int i = 0; i < EPL; ++i) {
@@ -139,7 +140,7 @@ __global__ __launch_bounds__(64) void qk_norm_rope_kv_kernel(
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < EPL; ++i) o[i] = xv[i];
+    for (int i = 0; i < EPL; ++i) o[i] = clip_qkv(xv[i], clip, clip16);
   }
   if (!pos_ok) return;
   // KV-INT8 quantisation of this head's row.
@@ -176,8 +177,9 @@ __global__ __launch_bounds__(1024) void qk_rows_kernel(
     const uint16_t* __restrict__ sin_tab, int64_t pos0, uint16_t* __restrict__ q_out,
     int8_t* __restrict__ kc, uint16_t* __restrict__ ks, int8_t* __restrict__ vc,
     uint16_t* __restrict__ vs, int64_t code_head_stride, int64_t s_len, uint16_t* __restrict__ k_f16,
-    uint16_t* __restrict__ v_f16, int64_t f16_head_stride) {
+    uint16_t* __restrict__ v_f16, int64_t f16_head_stride, float clip) {
   __shared__ float red[16];
+  const float clip16 = h2f(f2h(clip));
   const int t = threadIdx.x, lane = t & 63;
   const int64_t row = blockIdx.x;
   const int part = blockIdx.y;
@@ -209,7 +211,7 @@ __global__ __launch_bounds__(1024) void qk_rows_kernel(
     for (int i = 0; i < 8; ++i) {
       const uint16_t xb = (uint16_t)(rw[i / 2] >> (16 * (i & 1)));
       const uint16_t wb = (uint16_t)(ww[i / 2] >> (16 * (i & 1)));
-      const float xn = h2f(f2h(h2f(f2h(h2f(xb) * rstd)) * h2f(wb)));
+      const float xn = clip_qkv(h2f(f2h(h2f(f2h(h2f(xb) * rstd)) * h2f(wb))), clip, clip16);
       const float xs = __shfl_xor(xn, D / 16, 64);
       const float c = h2f((uint16_t)(cw[i / 2] >> (16 * (i & 1))));
       const float sn = h2f((uint16_t)(sw[i / 2] >> (16 * (i & 1))));
@@ -224,7 +226,7 @@ __global__ __launch_bounds__(1024) void qk_rows_kernel(
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) o[i] = h2f((uint16_t)(rw[i / 2] >> (16 * (i & 1))));
+    for (int i = 0; i < 8; ++i) o[i] = clip_qkv(h2f((uint16_t)(rw[i / 2] >> (16 * (i & 1)))), clip, clip16);
   }
   uint32_t packed[4];
 #pragma unroll
@@ -306,12 +308,13 @@ extern "C" int lemoq_qk_norm_rope_kv_i8(const uint16_t* qkv, int64_t heads, int6
                                         uint16_t* vs, int64_t code_head_stride, int64_t s_len,
                                         uint16_t* k_f16, uint16_t* v_f16,
                                         int64_t f16_head_stride, uint16_t* k_rot_out,
-                                        void* stream) {
+                                        float clip_qkv, void* stream) {
   if (!qkv || !q_norm_w || !k_norm_w || !cos_tab || !sin_tab || !pos || !q_out || !kc || !ks ||
       !vc || !vs)
     return LEMOQ_ERR_NULL;
   if (heads <= 0 || heads > 4096 || heads * head_dim > 65536) return LEMOQ_ERR_SHAPE;
   if (head_dim != 64 && head_dim != 128 && head_dim != 256) return LEMOQ_ERR_UNSUPPORTED;
+  if (!(clip_qkv >= 0.0f)) return LEMOQ_ERR_SHAPE;  // negative or NaN bound
   if (!lemoq_aligned16(qkv)) return LEMOQ_ERR_ALIGN;
   if (s_len <= 0 || code_head_stride < s_len * head_dim) return LEMOQ_ERR_SHAPE;
   if ((k_f16 || v_f16) && f16_head_stride < s_len * head_dim) return LEMOQ_ERR_SHAPE;
@@ -320,7 +323,7 @@ extern "C" int lemoq_qk_norm_rope_kv_i8(const uint16_t* qkv, int64_t heads, int6
 #define LEMOQ_QK_CASE(EE)                                                                       \
   hipLaunchKernelGGL((qk_norm_rope_kv_kernel<EE>), grid, dim3(64), 0, st, qkv, (int)heads,     \
                      q_norm_w, k_norm_w, eps, cos_tab, sin_tab, pos, q_out, kc, ks, vc, vs,    \
-                     code_head_stride, s_len, k_f16, v_f16, f16_head_stride, k_rot_out);
+                     code_head_stride, s_len, k_f16, v_f16, f16_head_stride, k_rot_out, clip_qkv);
   switch (head_dim) {
     case 64: LEMOQ_QK_CASE(1) break;
     case 128: LEMOQ_QK_CASE(2) break;
@@ -338,12 +341,13 @@ extern "C" int lemoq_qk_norm_rope_kv_i8_rows(const uint16_t* qkv, int64_t rows, 
                                              uint16_t* ks, int8_t* vc, uint16_t* vs,
                                              int64_t code_head_stride, int64_t s_len,
                                              uint16_t* k_f16, uint16_t* v_f16,
-                                             int64_t f16_head_stride, void* stream) {
+                                             int64_t f16_head_stride, float clip_qkv, void* stream) {
   if (!qkv || !q_norm_w || !k_norm_w || !cos_tab || !sin_tab || !q_out || !kc || !ks || !vc ||
       !vs)
     return LEMOQ_ERR_NULL;
   if (heads <= 0 || heads > 4096 || heads * head_dim > 65536) return LEMOQ_ERR_SHAPE;
   if (head_dim != 64 && head_dim != 128 && head_dim != 256) return LEMOQ_ERR_UNSUPPORTED;
+  if (!(clip_qkv >= 0.0f)) return LEMOQ_ERR_SHAPE;  // negative or NaN bound
   if (!lemoq_aligned16(qkv)) return LEMOQ_ERR_ALIGN;
   if (s_len <= 0 || code_head_stride < s_len * head_dim) return LEMOQ_ERR_SHAPE;
   if ((k_f16 || v_f16) && f16_head_stride < s_len * head_dim) return LEMOQ_ERR_SHAPE;
@@ -362,7 +366,7 @@ extern "C" int lemoq_qk_norm_rope_kv_i8_rows(const uint16_t* qkv, int64_t rows, 
 #define LEMOQ_QK_ROWS_CASE(DD)                                                                  \
   hipLaunchKernelGGL((qk_rows_kernel<DD>), grid, dim3(threads), 0, st, qkv, (int)HD, q_norm_w,   \
                      k_norm_w, eps, cos_tab, sin_tab, pos0, q_out, kc, ks, vc, vs,              \
-                     code_head_stride, s_len, k_f16, v_f16, f16_head_stride);
+                     code_head_stride, s_len, k_f16, v_f16, f16_head_stride, clip_qkv);
   switch (head_dim) {
     case 64: LEMOQ_QK_ROWS_CASE(64) break;
     case 128: LEMOQ_QK_ROWS_CASE(128) break;

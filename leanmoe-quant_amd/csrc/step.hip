@@ -71,6 +71,7 @@ int validate(const LemoqOlmoeStep* p, AttnPath* path) {
       p->vocab <= 0 || E <= 0 || F <= 0 || K <= 0)
     return LEMOQ_ERR_SHAPE;
   if (g <= 0 || g % 16 != 0) return LEMOQ_ERR_UNSUPPORTED;
+  if (!(p->clip_qkv >= 0.0f)) return LEMOQ_ERR_SHAPE;  // negative or NaN clip_qkv
   // qkv and lm_head GEMVs (K = H), o_proj (K = HD) on the unfused path
   LEMOQ_TRY(check_gemv(3 * HD, H, g));
   LEMOQ_TRY(check_gemv(p->vocab, H, g));
@@ -139,7 +140,7 @@ extern "C" int lemoq_olmoe_decode_step(const LemoqOlmoeStep* p, void* stream) {
     LEMOQ_TRY(lemoq_attn_split_fused_i8(p->qkv, p->heads, D, w.q_norm, w.k_norm, p->eps,
                                         p->cos_tab, p->sin_tab, p->pos, w.kc, w.ks, w.vc, w.vs,
                                         S * D, S, p->num_splits, p->qk_scale, p->part_m,
-                                        p->part_l, p->part_acc, stream));
+                                        p->part_l, p->part_acc, p->clip_qkv, stream));
     if (path == kAttnFusedOut) {
       // 3. LSE merge + o_proj partials per group of 4 heads.
       LEMOQ_TRY(lemoq_attn_merge_o_proj_w8(p->part_m, p->part_l, p->part_acc, p->heads,

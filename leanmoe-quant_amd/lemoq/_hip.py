@@ -72,6 +72,7 @@ class LemoqOlmoeStep(ctypes.Structure):
         ("norm_topk_prob", _I64),
         ("eps", _F),
         ("qk_scale", _F),
+        ("clip_qkv", _F),
         ("layers", ctypes.POINTER(LemoqOlmoeLayer)),
         ("embed", _P),
         ("final_norm", _P),
@@ -151,7 +152,7 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         _I,
         [
             _P, _I64, _I64, _P, _P, _F, _P, _P, _P, _P, _P, _P, _P, _P,
-            _I64, _I64, _P, _P, _I64, _P, _P,
+            _I64, _I64, _P, _P, _I64, _P, _F, _P,
         ],
     ),
     "lemoq_argmax_advance": (_I, [_P, _I64, _P, _P, _P, _P, _I64, _P, _I64, _P]),
@@ -170,9 +171,8 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "lemoq_router_logits": (_I, [_P, _P, _F, _I64, _P, _I64, _P, _P, _P]),
     "lemoq_attn_split_fused_i8": (
         _I,
-        [_P, _I64, _I64, _P, _P, _F, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _F, _P, _P, _P, _P],
+        [_P, _I64, _I64, _P, _P, _F, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _F, _P, _P, _P, _F, _P],
     ),
-
     "lemoq_moe_gate_up_w8_routed": (
         _I,
         [_P, _P, _P, _P, _I64, _I, _I64, _I64, _I64, _I64, _P, _P, _P, _P],
@@ -184,7 +184,7 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "lemoq_gather_rows": (_I, [_P, _I64, _I64, _P, _I64, _P, _P]),
     "lemoq_qk_norm_rope_kv_i8_rows": (
         _I,
-        [_P, _I64, _I64, _I64, _P, _P, _F, _P, _P, _I64, _P, _P, _P, _P, _P, _I64, _I64, _P, _P, _I64, _P],
+        [_P, _I64, _I64, _I64, _P, _P, _F, _P, _P, _I64, _P, _P, _P, _P, _P, _I64, _I64, _P, _P, _I64, _F, _P],
     ),
     "lemoq_attn_prefill_f16": (_I, [_P, _I64, _P, _P, _I64, _I64, _I64, _I64, _F, _P, _I64, _P]),
     "lemoq_moe_prefill_max_tiles": (_I64, [_I64, _I64]),

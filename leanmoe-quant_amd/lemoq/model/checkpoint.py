@@ -50,8 +50,6 @@ def shape_from_hf_config(cfg: Mapping[str, Any], *, group_size: int = 128) -> Ol
     kv_heads = int(cfg.get("num_key_value_heads") or heads)
     if kv_heads != heads:
         raise NotImplementedError("grouped-query attention (num_key_value_heads != num_attention_heads)")
-    if cfg.get("clip_qkv") is not None:
-        raise NotImplementedError("clip_qkv is not supported by the decode step")
     hidden = int(cfg["hidden_size"])
     head_dim = int(cfg.get("head_dim") or hidden // heads)
     theta = cfg.get("rope_theta")
@@ -70,6 +68,7 @@ def shape_from_hf_config(cfg: Mapping[str, Any], *, group_size: int = 128) -> Ol
         rope_theta=float(theta),
         norm_topk_prob=bool(cfg.get("norm_topk_prob", False)),
         group_size=int(group_size),
+        clip_qkv=None if cfg.get("clip_qkv") is None else float(cfg["clip_qkv"]),
     )
 
 

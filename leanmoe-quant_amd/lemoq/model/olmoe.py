@@ -70,6 +70,9 @@ class OlmoeShape:
     norm_topk_prob: bool = False
     group_size: int = 128
     init_std: float = 0.02
+    # HF OLMoE's clip_qkv: the normed q, the normed k and v are clamped to
+    # +-clip_qkv before RoPE (None: no clamp)
+    clip_qkv: float | None = None
 
     @property
     def qkv_rows(self) -> int:
@@ -296,6 +299,7 @@ class DecodeSession:
         st.vocab, st.group, st.num_layers = s.vocab, s.group_size, s.layers
         st.max_seq, st.num_splits, st.norm_topk_prob = S, self.num_splits, int(bool(s.norm_topk_prob))
         st.eps = float(s.eps)
+        st.clip_qkv = math.inf if s.clip_qkv is None else float(s.clip_qkv)
         st.qk_scale = float((1.0 / math.sqrt(D)) * LOG2E)
         st.layers = ctypes.cast(self._layer_structs, ctypes.POINTER(_hip.LemoqOlmoeLayer))
         st.embed, st.final_norm = P(weights.embed), P(weights.final_norm)

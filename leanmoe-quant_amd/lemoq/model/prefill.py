@@ -125,7 +125,7 @@ def prefill_prompt(weights: Any, tokens: Any, kv: list, cos_tab: Any, sin_tab: A
                   P(qkv), 3 * HD, None, 0, st)
         _hip.call("lemoq_qk_norm_rope_kv_i8_rows", P(qkv), T, NH, D, P(L.q_norm), P(L.k_norm), float(s.eps),
                   P(cos_tab), P(sin_tab), 0, P(q), P(c["kc"]), P(c["ks"]), P(c["vc"]), P(c["vs"]), S * D, S,
-                  P(k16), P(v16), S * D, st)
+                  P(k16), P(v16), S * D, math.inf if s.clip_qkv is None else float(s.clip_qkv), st)
         if kv_f16 is not None:
             kv_f16.append((k16[:, :T].clone(), v16[:, :T].clone()))
         if li + 1 == n_layers and T > 1 and last_row_only:

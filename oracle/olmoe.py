@@ -48,6 +48,7 @@ class Shape:
     norm_topk_prob: bool = False
     group_size: int = 128
     init_std: float = 0.02
+    clip_qkv: float | None = None
 
 
 @dataclass
@@ -170,6 +171,7 @@ class OracleDecoder:
             q, k, v = qkv[:HD], qkv[HD : 2 * HD], qkv[2 * HD :]
             q = ops.rms_norm(q, L.q_norm, s.eps)
             k = ops.rms_norm(k, L.k_norm, s.eps)
+            q, k, v = ops.clip_qkv(q, k, v, getattr(s, "clip_qkv", None))
             q = ops.rope_fused(q.reshape(NH, D), cos, sin)
             k = ops.rope_fused(k.reshape(NH, D), cos, sin)
             self._quant_into(kv["kc"], kv["ks"], pos, k)
@@ -265,6 +267,7 @@ def oracle_prefill(weights: Any, tokens: Any, max_seq: int, *, all_logits: bool 
         q = ops.rms_norm(qkv[:, :HD], L.q_norm, s.eps).reshape(T, NH, D)
         k = ops.rms_norm(qkv[:, HD:2 * HD], L.k_norm, s.eps).reshape(T, NH, D)
         v = qkv[:, 2 * HD:].reshape(T, NH, D)
+        q, k, v = ops.clip_qkv(q, k, v, getattr(s, "clip_qkv", None))
         q, k = ops.rope_hf(q, k, cos, sin)
         cache = {
             "kc": torch.zeros((NH, max_seq, D), dtype=torch.int8),

@@ -87,6 +87,17 @@ def rms_norm(x: Any, weight: Any, eps: float) -> torch.Tensor:
     return weight * h.to(dt)
 
 
+def clip_qkv(q: Any, k: Any, v: Any, clip: float | None):
+    """HF OLMoE's ``clip_qkv`` (``OlmoeAttention.forward``; the reference's glue,
+    ``src/lemoq/kernels/attn_decode.py:903-907``): ``clamp_(min=-clip, max=clip)``
+    of the normed q, the normed k and v in their dtype, after q_norm/k_norm and
+    before RoPE; ``None`` leaves them as they are."""
+    if clip is None:
+        return q, k, v
+    c = float(clip)
+    return q.clamp(min=-c, max=c), k.clamp(min=-c, max=c), v.clamp(min=-c, max=c)
+
+
 def rotary_cos_sin(positions: Any, head_dim: int, theta: float = 10000.0):
     """HF ``OlmoeRotaryEmbedding`` (default rope): fp32 freqs, cos/sin cast to fp16."""
     pos = torch.as_tensor(positions, dtype=torch.int64).reshape(-1)

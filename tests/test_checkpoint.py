@@ -88,8 +88,8 @@ def test_shape_from_config(saved):
     assert s.rope_theta == 10000.0 and s.eps == 1e-5 and s.norm_topk_prob is False
     with pytest.raises(NotImplementedError):
         ck.shape_from_hf_config({**cfg, "num_key_value_heads": 1})
-    with pytest.raises(NotImplementedError):
-        ck.shape_from_hf_config({**cfg, "clip_qkv": 8.0})
+    assert ck.shape_from_hf_config({**cfg, "clip_qkv": 8.0}).clip_qkv == 8.0
+    assert ck.shape_from_hf_config({**cfg, "clip_qkv": None}).clip_qkv is None
 
 
 def test_loaded_checkpoint_decodes_like_hf(saved):

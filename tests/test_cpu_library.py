@@ -4,6 +4,7 @@ symbol include/lemoq_hip.h declares, with the status strings of the header."""
 from __future__ import annotations
 
 import ctypes
+import math
 import os
 import re
 
@@ -81,7 +82,14 @@ def test_argument_rejection_happens_before_any_launch():
     assert lib.lemoq_attn_prefill_f16(fake, 256, fake, fake, 256 * 8, 8, 2, 96, 1.0, fake, 256, None) == -3
     assert lib.lemoq_attn_prefill_f16(fake, 256, fake, fake, 128 * 4, 8, 2, 128, 1.0, fake, 256, None) == -2
     assert lib.lemoq_qk_norm_rope_kv_i8_rows(fake, 10, 2, 128, fake, fake, 1e-5, fake, fake, 5, fake, fake, fake,
-                                             fake, fake, 16 * 128, 12, None, None, 0, None) == -2  # rows past s_len
+                                             fake, fake, 16 * 128, 12, None, None, 0, math.inf, None) == -2  # rows past s_len
+    for bad in (-1.0, math.nan):  # clip_qkv must be >= 0 (+inf disables it)
+        assert lib.lemoq_qk_norm_rope_kv_i8_rows(fake, 10, 2, 128, fake, fake, 1e-5, fake, fake, 0, fake, fake,
+                                                 fake, fake, fake, 16 * 128, 12, None, None, 0, bad, None) == -2
+        assert lib.lemoq_qk_norm_rope_kv_i8(fake, 2, 128, fake, fake, 1e-5, fake, fake, fake, fake, fake, fake,
+                                            fake, fake, 16 * 128, 12, None, None, 0, None, bad, None) == -2
+        assert lib.lemoq_attn_split_fused_i8(fake, 16, 128, fake, fake, 1e-5, fake, fake, fake, fake, fake, fake,
+                                             fake, 1100 * 128, 1100, 16, 0.1, fake, fake, fake, bad, None) == -2
     assert lib.lemoq_moe_prefill_max_tiles(8192, 64) == 8192 // 128 + 64
     assert lib.lemoq_moe_prefill_sort(fake, fake, 4097, 8, 64, fake, fake, fake, fake, fake, 10 ** 6, None) == -3
     assert lib.lemoq_moe_prefill_sort(fake, fake, 16, 8, 300, fake, fake, fake, fake, fake, 10 ** 6, None) == -2
@@ -136,7 +144,7 @@ def _fake_step(**over):
                  num_layers=2, max_seq=1100, num_splits=16, norm_topk_prob=0)
     for k, v in shape.items():
         setattr(st, k, v)
-    st.eps, st.qk_scale = 1e-5, 0.1
+    st.eps, st.qk_scale, st.clip_qkv = 1e-5, 0.1, math.inf
     st.layers = ctypes.cast(layers, ctypes.POINTER(_hip.LemoqOlmoeLayer))
     for name, typ in _hip.LemoqOlmoeStep._fields_:
         if typ is ctypes.c_void_p:
@@ -167,6 +175,7 @@ def test_decode_step_rejects_before_any_launch():
     assert step(group=8) == -3                              # every GEMV: group % 16
     assert step(head_dim=96) == -3                          # attention: head_dim
     assert step(act=(1 << 30) + 8) == -4                    # down: act alignment
+    assert step(clip_qkv=-1.0) == -2 and step(clip_qkv=math.nan) == -2  # attention: clip_qkv bound
     st, layers = _fake_step()
     layers[1].dn_codes = (1 << 30) + 4                      # layer 1's down codes misaligned
     assert lib.lemoq_olmoe_decode_step(ctypes.byref(st), None) == -4

@@ -17,6 +17,7 @@ from __future__ import annotations
 
 import math
 
+import numpy as np
 import pytest
 import torch
 
@@ -48,7 +49,7 @@ def _to(dev, cache):
     return {n: t.clone().to(dev) for n, t in cache.items()}
 
 
-def _split_path(hip, dev, qkv, qn, kn, cache, cos, sin, pos, heads, D, S, ns):
+def _split_path(hip, dev, qkv, qn, kn, cache, cos, sin, pos, heads, D, S, ns, clip=math.inf):
     c = _to(dev, cache)
     q_rot = torch.empty((heads * D,), dtype=torch.float16, device=dev)
     posd = torch.tensor([pos], dtype=torch.int64, device=dev)
@@ -60,7 +61,7 @@ def _split_path(hip, dev, qkv, qn, kn, cache, cos, sin, pos, heads, D, S, ns):
     P, st = hip.ptr, hip.stream_of(dev)
     qkvd, qnd, knd, cosd, sind = (t.to(dev) for t in (qkv, qn, kn, cos, sin))
     hip.call("lemoq_qk_norm_rope_kv_i8", P(qkvd), heads, D, P(qnd), P(knd), 1e-5, P(cosd), P(sind), P(posd),
-             P(q_rot), P(c["kc"]), P(c["ks"]), P(c["vc"]), P(c["vs"]), S * D, S, None, None, 0, None, st)
+             P(q_rot), P(c["kc"]), P(c["ks"]), P(c["vc"]), P(c["vs"]), S * D, S, None, None, 0, None, clip, st)
     qk_scale = (1.0 / math.sqrt(D)) * LOG2E
     hip.call("lemoq_attn_split_i8", P(q_rot), P(c["kc"]), P(c["ks"]), P(c["vc"]), P(c["vs"]), S * D, S,
              P(filled), heads, D, ns, qk_scale, P(m), P(l), P(acc), st)
@@ -74,7 +75,7 @@ def _merge(hip, dev, m, l, acc, heads, ns, D):
     return out
 
 
-def _fused_path(hip, dev, qkv, qn, kn, cache, cos, sin, pos, heads, D, S, ns=4, raw=False):
+def _fused_path(hip, dev, qkv, qn, kn, cache, cos, sin, pos, heads, D, S, ns=4, raw=False, clip=math.inf):
     c = _to(dev, cache)
     posd = torch.tensor([pos], dtype=torch.int64, device=dev)
     m = torch.full((heads * ns,), float("nan"), dtype=torch.float32, device=dev)
@@ -84,7 +85,7 @@ def _fused_path(hip, dev, qkv, qn, kn, cache, cos, sin, pos, heads, D, S, ns=4, 
     qkvd, qnd, knd, cosd, sind = (t.to(dev) for t in (qkv, qn, kn, cos, sin))
     qk_scale = (1.0 / math.sqrt(D)) * LOG2E
     hip.call("lemoq_attn_split_fused_i8", P(qkvd), heads, D, P(qnd), P(knd), 1e-5, P(cosd), P(sind), P(posd),
-             P(c["kc"]), P(c["ks"]), P(c["vc"]), P(c["vs"]), S * D, S, ns, qk_scale, P(m), P(l), P(acc), st)
+             P(c["kc"]), P(c["ks"]), P(c["vc"]), P(c["vs"]), S * D, S, ns, qk_scale, P(m), P(l), P(acc), clip, st)
     if raw:
         return m, l, acc, {n: t.cpu() for n, t in c.items()}
     out = _merge(hip, dev, m, l, acc, heads, ns, D)
@@ -151,3 +152,39 @@ def test_fused_attention_position_outside_cache_writes_nothing(dev):
     assert (out == 0).all()
 
 
+
+
+@pytest.mark.parametrize("heads,D,S,pos,ns,clip", [
+    (16, 128, 1100, 0, 16, 0.8), (16, 128, 1100, 700, 16, 0.8), (8, 64, 700, 511, 4, 1.3),
+    (4, 256, 300, 257, 5, 0.5), (16, 128, 1100, 300, 16, 0.0),
+])
+def test_fused_attention_clip_qkv(heads, D, S, pos, ns, clip, dev):
+    """HF OLMoE's clip_qkv (the reference's glue clamps the normed q/k and v,
+    ``src/lemoq/kernels/attn_decode.py:903-907``): the fused launch and the
+    unfused q/k norm + RoPE launch write the same KV bytes, their q and v match
+    the oracle's clamp, and the bound changes the output (it is not ignored)."""
+    from lemoq import _hip
+
+    print("case: clip heads=%d D=%d S=%d pos=%d ns=%d clip=%g" % (heads, D, S, pos, ns, clip), flush=True)
+    qkv, qn, kn, cache, cos, sin = _state(heads, D, S, pos + 1, seed=pos + D + 7)
+    HD = heads * D
+    out_s, cache_s, q_rot = _split_path(_hip, dev, qkv, qn, kn, cache, cos, sin, pos, heads, D, S, ns=16, clip=clip)
+    out_f, cache_f = _fused_path(_hip, dev, qkv, qn, kn, cache, cos, sin, pos, heads, D, S, ns=ns, clip=clip)
+    for n in ("kc", "ks", "vc", "vs"):
+        assert torch.equal(cache_f[n], cache_s[n]), n
+    assert_close(out_f, out_s, what="fused vs split")
+    qn_, kn_ = (ops.rms_norm(qkv[a:a + HD], w, 1e-5).reshape(heads, D) for a, w in ((0, qn), (HD, kn)))
+    qc, kc_, vc_ = ops.clip_qkv(qn_, kn_, qkv[2 * HD:].reshape(heads, D), clip)
+    clamped = float((qc != qn_).double().mean())
+    assert clamped > (0.99 if clip == 0.0 else 0.05), clamped  # the bound bites
+    q = ops.rope_fused(qc, cos[pos], sin[pos])
+    assert_close(q_rot, q.reshape(-1), rtol=2e-3, atol=2e-3, what="clipped q_norm+rope")
+    # v is stored unrotated: its codes and scale are the oracle's quantisation of the clamped row, bit for bit
+    vcodes, vscale = oq.kv_quantize_rows(vc_.numpy())
+    assert np.array_equal(cache_f["vc"][:, pos].numpy(), vcodes)
+    assert np.array_equal(cache_f["vs"][:, pos].numpy().view(np.uint16), vscale.view(np.uint16))
+    ref = ops.int8_attention_folded(q, cache_s["kc"], cache_s["ks"], cache_s["vc"], cache_s["vs"], pos + 1)
+    assert_close(out_f.reshape(heads, D), ref, what="clipped fused vs oracle")
+    if clip > 0.0:
+        out_n, _ = _fused_path(_hip, dev, qkv, qn, kn, cache, cos, sin, pos, heads, D, S, ns=ns)
+        assert not torch.equal(out_n, out_f)

@@ -114,6 +114,22 @@ def test_tiny_model_32_steps_match_oracle(norm, dev):
     _check_steps(toks, gl, rl)
 
 
+@pytest.mark.parametrize("shape", ["tiny", "tiny_fused"])
+def test_clip_qkv_model_32_steps_match_oracle(shape, dev):
+    """HF OLMoE's clip_qkv (the reference clamps the normed q/k and v when the
+    config sets it, ``src/lemoq/kernels/attn_decode.py:903-907``): 32 teacher-
+    forced steps against the oracle with the same clamp; the clamp changes the
+    logits (a step that ignored it would not match)."""
+    print("case: %s model with clip_qkv 0.8, 32 steps" % shape, flush=True)
+    base = TINY if shape == "tiny" else TINY_FUSED
+    sh = OlmoeShape(**{**base.__dict__, "clip_qkv": 0.8})
+    toks, gl, rl = _teacher_forced(sh, [1] * 40, 32, 5, dev)
+    _check_steps(toks, gl, rl)
+    _, gl0, _ = _teacher_forced(base, [1] * 40, 1, 5, dev)
+    d = float((gl0[0].float() - gl[0].float()).abs().max())
+    assert d > 0.05 * float(gl[0].float().abs().max()), d
+
+
 @pytest.mark.parametrize("shape,ctx,norm", [("tiny", 40, False), ("tiny", 40, True), ("narrow", 1200, False)])
 def test_fused_path_model_32_steps_match_oracle(shape, ctx, norm, dev):
     print("case: %s fused-path test model, ctx %d, 32 steps, norm_topk_prob=%s" % (shape, ctx, norm), flush=True)

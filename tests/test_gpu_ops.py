@@ -536,7 +536,7 @@ def test_qk_norm_rope_kv_fused_prologue(dev):
     pos_d = torch.tensor([pos], device=dev)
     _hip.call("lemoq_qk_norm_rope_kv_i8", P(qkv_d), NH, D, P(qn_d), P(kn_d), 1e-5, P(cos_d), P(sin_d),
               P(pos_d), P(q_out), P(kc), P(ks), P(vc), P(vs), S * D, S, P(kf), P(vf), S * D, P(k_rot),
-              _hip.stream_of(dev))
+              math.inf, _hip.stream_of(dev))
     torch.cuda.synchronize()
     q_ref = ops.rope_fused(ops.rms_norm(qkv[:HD], qn, 1e-5).reshape(NH, D), cos[pos], sin[pos])
     k_ref = ops.rope_fused(ops.rms_norm(qkv[HD:2 * HD], kn, 1e-5).reshape(NH, D), cos[pos], sin[pos])

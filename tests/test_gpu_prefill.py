@@ -58,11 +58,13 @@ def test_gather_rows(dev):
         assert torch.equal(got[r], ref), r
 
 
-@pytest.mark.parametrize("D", [64, 128])
-def test_qk_norm_rope_rows_vs_oracle(D, dev):
+@pytest.mark.parametrize("D,clip", [(64, math.inf), (128, math.inf), (128, 0.7)])
+def test_qk_norm_rope_rows_vs_oracle(D, clip, dev):
+    """With ``clip`` finite, HF OLMoE's clip_qkv clamps the normed q/k and v
+    before RoPE (``src/lemoq/kernels/attn_decode.py:903-907``)."""
     from lemoq import _hip
 
-    print("case: qk_norm_rope rows D=%d" % D, flush=True)
+    print("case: qk_norm_rope rows D=%d clip=%g" % (D, clip), flush=True)
     T, NH, S = 37, 4, 50
     HD = NH * D
     qkv = randn(T, 3 * HD, seed=D).to(torch.float16)
@@ -78,10 +80,15 @@ def test_qk_norm_rope_rows_vs_oracle(D, dev):
     qkv_d, qn_d, kn_d, cos_d, sin_d = (t.to(dev) for t in (qkv, qn, kn, cos, sin))
     P = _hip.ptr
     _hip.call("lemoq_qk_norm_rope_kv_i8_rows", P(qkv_d), T, NH, D, P(qn_d), P(kn_d), 1e-5, P(cos_d), P(sin_d), 0,
-              P(q_out), P(kc), P(ks), P(vc), P(vs), S * D, S, P(kf), P(vf), S * D, _hip.stream_of(dev))
+              P(q_out), P(kc), P(ks), P(vc), P(vs), S * D, S, P(kf), P(vf), S * D, clip, _hip.stream_of(dev))
     torch.cuda.synchronize()
     q = ops.rms_norm(qkv[:, :HD], qn, 1e-5).reshape(T, NH, D)
     k = ops.rms_norm(qkv[:, HD:2 * HD], kn, 1e-5).reshape(T, NH, D)
+    v = qkv[:, 2 * HD:].reshape(T, NH, D)
+    if math.isfinite(clip):
+        q0 = q
+        q, k, v = ops.clip_qkv(q, k, v, clip)
+        assert float((q != q0).double().mean()) > 0.2  # the bound bites
     c, s_ = cos[:T].unsqueeze(1), sin[:T].unsqueeze(1)
     q_ref, k_ref = ops.rope_hf(q, k, c, s_)
     q_got = q_out.cpu().reshape(T, NH, D)
@@ -93,7 +100,6 @@ def test_qk_norm_rope_rows_vs_oracle(D, dev):
     exact_fused = float((q_got == fused_q).double().mean())
     print("q exact vs HF rope %.4f, vs single-rounding rope %.4f" % (exact, exact_fused))
     assert exact >= 0.97 and exact > exact_fused
-    v = qkv[:, 2 * HD:].reshape(T, NH, D)
     assert torch.equal(vf[:, :T].cpu().transpose(0, 1), v)
     for codes, scales, rows in ((kc, ks, k_got), (vc, vs, v)):
         rc, rs = oq.kv_quantize_rows(rows.reshape(T * NH, D).numpy())
@@ -394,6 +400,19 @@ def test_prefill_session_tiny(dev):
     print("case: prefill session tiny", flush=True)
     shape = OlmoeShape(hidden=512, heads=4, head_dim=128, layers=2, num_experts=8, top_k=2, ffn=256, vocab=1024)
     prompt = [int(t) for t in torch.randint(0, 1024, (45,), generator=torch.Generator().manual_seed(8))]
+    _prefill_vs_oracle(shape, prompt, 3, 6, dev)
+
+
+def test_prefill_session_clip_qkv(dev):
+    """A model with HF OLMoE's clip_qkv set: the batched prefill (rows kernel)
+    and the decode steps after it (fused attention launch) against the oracles
+    with the same clamp."""
+    from lemoq.model.olmoe import OlmoeShape
+
+    print("case: prefill session tiny, clip_qkv 0.8", flush=True)
+    shape = OlmoeShape(hidden=512, heads=4, head_dim=128, layers=2, num_experts=8, top_k=2, ffn=256, vocab=1024,
+                       clip_qkv=0.8)
+    prompt = [int(t) for t in torch.randint(0, 1024, (45,), generator=torch.Generator().manual_seed(18))]
     _prefill_vs_oracle(shape, prompt, 3, 6, dev)
 
 

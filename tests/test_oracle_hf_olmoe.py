@@ -48,8 +48,8 @@ def _hf_model(hw):
     from transformers.utils import logging as hf_logging
 
     hf_logging.set_verbosity_error()
-    s = SHAPE
-    cfg = OlmoeConfig(vocab_size=s.vocab, hidden_size=s.hidden, intermediate_size=s.ffn,
+    s = hw.shape
+    cfg = OlmoeConfig(clip_qkv=s.clip_qkv, vocab_size=s.vocab, hidden_size=s.hidden, intermediate_size=s.ffn,
                       num_hidden_layers=s.layers, num_attention_heads=s.heads, num_key_value_heads=s.heads,
                       num_experts=s.num_experts, num_experts_per_tok=s.top_k, norm_topk_prob=s.norm_topk_prob,
                       rms_norm_eps=s.eps, rope_theta=s.rope_theta, max_position_embeddings=64,
@@ -110,6 +110,47 @@ def _stats(ref, out):
 def _passes(ref, out):
     kl, rel = _stats(ref, out)
     return kl < MED_KL and rel < MED_REL, (kl, rel)
+
+
+# clip_qkv small enough to clamp a large share of the normed q/k and of v
+SHAPE_CLIP = Shape(**{**SHAPE.__dict__, "clip_qkv": 0.6})
+
+
+def test_oracle_clip_qkv_matches_hf_olmoe():
+    """HF OLMoE's clip_qkv (after q_norm/k_norm, before RoPE, and on v; the
+    reference's glue at src/lemoq/kernels/attn_decode.py:903-907): the oracle
+    with the clamp passes the same gate against HF with ``clip_qkv`` set; the
+    oracle without it, or clamping before the norms, fails it."""
+    hw = random_host_weights(SHAPE_CLIP, seed=8)
+    toks = torch.randint(0, SHAPE.vocab, (N_POS,), generator=torch.Generator().manual_seed(108))
+    with torch.no_grad():
+        ref = _hf_model(hw)(toks[None]).logits[0]
+    # the clamp must bite: a large share of the oracle's first-layer q values lie beyond it
+    L = hw.layers[0]
+    xn = ops.rms_norm(hw.embed[toks], L.ln_in, SHAPE.eps)
+    q = ops.rms_norm(ops.linear_separate_w8(xn, L.qkv_codes, L.qkv_scale, SHAPE.group_size)[:, :256], L.q_norm,
+                     SHAPE.eps)
+    assert float((q.float().abs() > 0.6).float().mean()) > 0.2
+    ok, (kl, rel) = _passes(ref, _oracle_logits(hw, toks))
+    assert ok, "with the clamp: median KL %.3e, median rel %.4f" % (kl, rel)
+    hw_none = random_host_weights(SHAPE, seed=8)  # same tensors, no clamp in the oracle
+    ok, (kl, rel) = _passes(ref, _oracle_logits(hw_none, toks))
+    assert not ok, "without the clamp the gate still passed (KL %.3e, rel %.4f)" % (kl, rel)
+    orig_norm, orig_clip = ops.rms_norm, ops.clip_qkv
+    targets = [L.q_norm for L in hw.layers] + [L.k_norm for L in hw.layers]
+    try:
+        # planted: q and k clamped before q_norm / k_norm instead of after (v as before)
+        def norm_of_clipped(x, w, eps):
+            if any(w is t for t in targets):
+                x = x.clamp(min=-0.6, max=0.6)
+            return orig_norm(x, w, eps)
+
+        ops.rms_norm = norm_of_clipped
+        ops.clip_qkv = lambda q, k, v, c: (q, k, v.clamp(min=-c, max=c))
+        ok, (kl, rel) = _passes(ref, _oracle_logits(hw, toks))
+    finally:
+        ops.rms_norm, ops.clip_qkv = orig_norm, orig_clip
+    assert not ok, "clamping before the norms still passed (KL %.3e, rel %.4f)" % (kl, rel)
 
 
 @pytest.mark.parametrize("seed", [5, 6, 7])

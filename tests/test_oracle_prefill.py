@@ -63,6 +63,23 @@ def test_oracle_prefill_matches_hf_olmoe(seed):
     assert ok, "median KL %.3e, median rel %.4f" % (kl, rel)
 
 
+def test_oracle_prefill_clip_qkv_matches_hf_olmoe():
+    """The prefill oracle with HF OLMoE's clip_qkv set (0.6, which clamps a large
+    share of the normed q/k and of v) against HF's full forward with the same
+    config, and without its clamp it fails the gate."""
+    from oracle.olmoe import Shape
+
+    shape = Shape(**{**SHAPE.__dict__, "clip_qkv": 0.6})
+    hw = random_host_weights(shape, seed=9)
+    toks = torch.randint(0, SHAPE.vocab, (N_POS,), generator=torch.Generator().manual_seed(109))
+    with torch.no_grad():
+        ref = _hf_model(hw)(toks[None]).logits[0]
+    ok, (kl, rel) = _passes(ref, hw, toks)
+    assert ok, "median KL %.3e, median rel %.4f" % (kl, rel)
+    ok, (kl, rel) = _passes(ref, random_host_weights(SHAPE, seed=9), toks)
+    assert not ok, "without the clamp the gate still passed (KL %.3e, rel %.4f)" % (kl, rel)
+
+
 def _plant_rope_sign():
     orig = ops.rope_hf
     return "rope_hf", lambda q, k, c, s: orig(q, k, c, -s)
