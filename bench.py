@@ -89,6 +89,7 @@ def parse_args(argv=None):
     ap.add_argument("--cpu-timed-1t", type=int, default=20, help="timed CPU oracle steps on one thread")
     ap.add_argument("--no-cpu-ops", action="store_true", help="skip the per-operator CPU timings (C1-C4)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-formats", action="store_true", help="skip the weight-format GEMV timings")
     ap.add_argument("--mode", choices=("full", "kernels", "traffic", "prefill", "step"), default="full")
     ap.add_argument("--summarize-pmc", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "PLAN_JSON"))
     ap.add_argument("--summarize-prefill", metavar="KERNEL_TRACE_CSV",
@@ -723,6 +724,53 @@ def attention_configs(torch, hip, flusher, reps: int) -> dict:
     return out
 
 
+def format_gemvs(torch, hip, flusher, reps: int) -> dict:
+    """The decode GEMV over each weight format of the dense dequant operator
+    (w8 / w8 asymmetric / w4 / w4 asymmetric / MXFP4), at the qkv, o_proj and
+    lm_head shapes, cold (16 weight copies per pass, caches flushed), one token
+    in, fp16 out.  Algorithmic bytes: codes + scales (+ zero points) + x + y."""
+    dev = flusher.buf.device
+    K, copies = 2048, 16
+    P, st = hip.ptr, hip.stream_of
+    x = torch.randn((1, K), device=dev).to(torch.float16)
+    out = {}
+    for fname, fmt, bits, asym in (("w8", 0, 8, False), ("w8_asym", 1, 8, True), ("w4", 2, 4, False),
+                                   ("w4_asym", 3, 4, True), ("mxfp4", 4, 4, False)):
+        group = 32 if fmt == 4 else 128
+        for shape, N in (("qkv", 6144), ("o_proj", 2048), ("lm_head", 50304)):
+            ng = K // group
+            row_bytes = K if bits == 8 else K // 2
+            y = torch.empty((1, N), dtype=torch.float16, device=dev)
+            ws = []
+            for _ in range(copies):
+                codes = torch.randint(0, 256, (N, row_bytes), dtype=torch.uint8, device=dev)
+                if fmt == 4:
+                    scale = torch.randint(118, 125, (N, ng), dtype=torch.uint8, device=dev)
+                else:
+                    scale = (torch.rand((N, ng), device=dev) * 0.01 + 1e-3).to(torch.float16)
+                zero = torch.randint(0, 16, (N, ng), device=dev).to(torch.float16) if asym else None
+                ws.append((codes, scale, zero))
+            if fmt == 0:
+                fns = [lambda c=c: hip.call("lemoq_gemv_w8", P(x), 1, K, P(c[0]), P(c[1]), N, K, group, P(y), 1, st())
+                       for c in ws]
+            else:
+                fns = [lambda c=c: hip.call("lemoq_gemv_q", P(x), 1, K, P(c[0]), fmt, P(c[1]),
+                                            P(c[2]) if c[2] is not None else None, 0, N, K, group, P(y), 1, st())
+                       for c in ws]
+            nbytes = N * row_bytes + N * ng * (1 if fmt == 4 else 2) * (2 if asym else 1) + K * 2 + N * 2
+            fns[0]()
+            r = time_cold(torch, flusher, fns, reps)
+            name = "%s %s %dx%d" % (fname, shape, N, K)
+            r["bytes"] = int(nbytes)
+            r["gbs"] = nbytes / (r["avg_us"] * 1e-6) / 1e9
+            r["frac_of_peak"] = r["gbs"] / HBM_PEAK_GBS
+            out[name] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in r.items()}
+            log("format %-28s %8.2f us avg  %7.1f GB/s" % (name, r["avg_us"], r["gbs"]))
+            del ws, fns
+            torch.cuda.synchronize()
+    return out
+
+
 # HBM traffic from two rocprofv3 --pmc passes
 # ---------------------------------------------------------------------------
 COPY_BYTES = 512 << 20  # calibration copy: larger than the 256 MB Infinity Cache
@@ -928,6 +976,7 @@ def main(argv=None) -> int:
         check_tokens = [int(t) for t in sess.history[p0 + 1: p0 + 1 + check_n].tolist()]
     kt = kernel_table(torch, _hip, w, sess, flusher, args.kernel_reps)
     cfg = attention_configs(torch, _hip, flusher, args.kernel_reps)
+    fmts = None if args.no_formats else format_gemvs(torch, _hip, flusher, args.kernel_reps)
     del sess
     r2 = None
     snap2 = None
@@ -1008,6 +1057,8 @@ def main(argv=None) -> int:
                         if kk != "dispatch_kernels"} for k, v in kt.items()},
     }
     line["attention_configs"] = cfg
+    if fmts is not None:
+        line["weight_formats"] = fmts
     line["step_ms_p50"], line["step_ms_p99"] = r1["step_ms_p50"], r1["step_ms_p99"]
     gk = "ms_per_token_graph%d" % MULTI_STEPS
     line[gk] = r1[gk]  # MULTI_STEPS steps per graph launch (not the headline)

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define LEMOQ_ABI_VERSION 5
+#define LEMOQ_ABI_VERSION 6
 
 enum {
   LEMOQ_OK = 0,
@@ -63,6 +63,85 @@ int lemoq_abi_version(void);
 int lemoq_rtn_quantize_w8(const float* w, int64_t rows, int64_t cols, int64_t group,
                           int8_t* codes, uint16_t* scale_f16, float* scale_f32,
                           void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Weight formats of the dense dequant operator (the `bits`, `symmetric`,
+ * `zero` and `mxfp4` arguments of dequant_gemm_fused,
+ * src/lemoq/kernels/_dequant_triton.py:155-293, and the schemes of
+ * QuantLinear, src/lemoq/quant/linear.py:76-89):
+ *   LEMOQ_QFMT_W8       int8 codes, w = c * s                 (N, padded_k) bytes
+ *   LEMOQ_QFMT_W8_ASYM  uint8 codes, w = (c - z) * s          (N, padded_k) bytes
+ *   LEMOQ_QFMT_W4       int4 codes (-8..7), w = c * s         (N, padded_k / 2)
+ *   LEMOQ_QFMT_W4_ASYM  uint4 codes (0..15), w = (c - z) * s  (N, padded_k / 2)
+ *   LEMOQ_QFMT_MXFP4    E2M1 codes (bit 3 sign, bits 2..0 the magnitude
+ *                       0, 0.5, 1, 1.5, 2, 3, 4, 6), w = e2m1(c) * 2^(X - 127)
+ *                       with X the E8M0 scale byte of each 32 codes  (N, padded_k / 2)
+ * 4-bit codes are two per byte, the even column in the low nibble
+ * (src/lemoq/quant/pack.py:21-37).  Scales and zero points are per (row,
+ * group of `group` codes along k): fp16 (scale_is_f32 = 0) or fp32, the zero
+ * points of the same type; MXFP4 scales are uint8 E8M0 bytes with group 32 and
+ * no zero point.
+ * ------------------------------------------------------------------------- */
+enum {
+  LEMOQ_QFMT_W8 = 0,
+  LEMOQ_QFMT_W8_ASYM = 1,
+  LEMOQ_QFMT_W4 = 2,
+  LEMOQ_QFMT_W4_ASYM = 3,
+  LEMOQ_QFMT_MXFP4 = 4
+};
+
+/* Per-group RTN at 4 or 8 bits, symmetric or asymmetric.  Replaces
+ * lemoq.quant.rtn.quantize_rtn (src/lemoq/quant/rtn.py:38-99) and, for 4
+ * bits, pack.pack_4bit of its padded codes (src/lemoq/quant/pack.py:21-37).
+ * w (rows, cols) fp32; padded = ceil(cols / group) * group (group even at 4
+ * bits).  codes: (rows, padded) int8 (8-bit symmetric) or uint8 (8-bit
+ * asymmetric), or (rows, padded / 2) packed bytes (4-bit).  Per (row, group),
+ * each output that is non-NULL: scale_f16 / scale_f32 and zero_f16 / zero_f32
+ * (zero 0 when symmetric).  Symmetric: s = absmax / qmax (1 for an all-zero
+ * group), c = clamp(rint(w / s), -qmax - 1, qmax), qmax = 2^(bits-1) - 1.
+ * Asymmetric, over the real columns only: s = (max - min) / qmax (1 when
+ * max == min), z = rint(-min / s), c = clamp(rint(w / s) + z, 0, qmax),
+ * qmax = 2^bits - 1.  fp32 arithmetic, IEEE division, round half to even. */
+int lemoq_rtn_quantize(const float* w, int64_t rows, int64_t cols, int64_t group, int bits,
+                       int symmetric, uint8_t* codes, uint16_t* scale_f16, float* scale_f32,
+                       uint16_t* zero_f16, float* zero_f32, void* stream);
+
+/* MXFP4 quantiser.  Replaces lemoq.quant.mxfp4.quantize_mxfp4
+ * (src/lemoq/quant/mxfp4.py:50-102).  w (rows, cols) fp32; columns padded
+ * with zeros to nblk * 32.  codes_packed (rows, nblk * 16) bytes,
+ * scale_e8m0 (rows, nblk).  Per block: X = clamp(floor(log2(amax)) - 2, -127,
+ * 127) (-127 for an all-zero block; log2 rounded to fp32 as torch's is),
+ * byte X + 127; v = w / 2^X; the magnitude code is the first nearest of
+ * {0, 0.5, 1, 1.5, 2, 3, 4, 6} to min(|v|, 6); the sign bit is v < 0. */
+int lemoq_mxfp4_quantize(const float* w, int64_t rows, int64_t cols, uint8_t* codes_packed,
+                         uint8_t* scale_e8m0, void* stream);
+
+/* Decode GEMV over any LEMOQ_QFMT_* weight: y (M, N) = x (M, K) @ w^T with w
+ * as above in fp32 and fp32 accumulation (the fused arm,
+ * src/lemoq/kernels/_dequant_triton.py:313-463), y fp16 (y_is_f16) or fp32.
+ * x fp16 contiguous, columns past K read as 0.  K <= padded_k <= 8192,
+ * padded_k % group == 0, group % 16 == 0 (8-bit) or % 32 == 0 (4-bit; 32 for
+ * MXFP4), 1 <= M <= 65535, qweight 16-byte aligned.  zero is required by the
+ * asymmetric formats and ignored otherwise. */
+int lemoq_gemv_q(const uint16_t* x, int64_t M, int64_t K, const void* qweight, int fmt,
+                 const void* scale, const void* zero, int scale_is_f32, int64_t N,
+                 int64_t padded_k, int64_t group, void* y, int y_is_f16, void* stream);
+
+/* Dense weight of any LEMOQ_QFMT_* format: w[n][k] for k < k_out, computed
+ * in fp32 and stored as fp32 (w_is_f32) or rounded once to fp16, rows ld_w
+ * elements apart.  Replaces QuantLinear.dequantized_weight
+ * (src/lemoq/quant/linear.py:365-395) and mxfp4.dequantize_packed
+ * (src/lemoq/quant/mxfp4.py:105-122).  Same format rules as lemoq_gemv_q;
+ * 1 <= k_out <= padded_k and ld_w >= k_out. */
+int lemoq_dequant_q(const void* qweight, int fmt, const void* scale, const void* zero,
+                    int scale_is_f32, int64_t N, int64_t padded_k, int64_t group, void* w,
+                    int64_t ld_w, int64_t k_out, int w_is_f32, void* stream);
+
+/* Per-token symmetric int8 fake quantisation of fp16 activations (x, y
+ * (rows, D), may alias), the w8a8 scheme's QuantLinear._fake_quant_activation
+ * (src/lemoq/quant/linear.py:398-414): fp32 absmax per row, s = absmax / 127
+ * (1 when 0), q = clamp(rint(x / s), -128, 127), y = fp16(q * s). */
+int lemoq_fake_quant_rows(const uint16_t* x, int64_t rows, int64_t D, uint16_t* y, void* stream);
 
 /* ---------------------------------------------------------------------------
  * A7/A8/A9 — w8 symmetric dense GEMV (dequant in registers, fp32 accumulate).

@@ -1,0 +1,662 @@
+// Weight formats of the reference's dense dequant operator beyond 8-bit
+// symmetric: 8-bit asymmetric (uint8 codes + zero point), 4-bit symmetric
+// (int4) and asymmetric (uint4 + zero point), both two codes per byte with the
+// low nibble first, and MXFP4 (E2M1 codes, two per byte, one E8M0 byte scale
+// per 32 codes).  For each: the decode GEMV (the fused arm of
+// dequant_gemm_fused, src/lemoq/kernels/_dequant_triton.py:155-293, kernel
+// :313-463), the dequantisation to a dense weight (QuantLinear's separate arm,
+// src/lemoq/quant/linear.py:365-395, and mxfp4.dequantize_packed,
+// src/lemoq/quant/mxfp4.py:105-122), and the quantisers (rtn.quantize_rtn,
+// src/lemoq/quant/rtn.py:38-99 with pack.pack_4bit, src/lemoq/quant/pack.py:21-37;
+// mxfp4.quantize_mxfp4, src/lemoq/quant/mxfp4.py:50-102).
+//
+// GEMV layout (as the w8 GEMV): a 256-thread block is 4 waves, wave w of block
+// b owns rows (4b + w) * R ... + R - 1; lane l reads bytes [1024 j + 16 l, +16)
+// of chunk j of a packed row (16 codes at 8 bits, 32 at 4 bits), the group
+// scale (and zero point) of that slice, and the matching slice of x, all
+// issued before any arithmetic.  Codes become exact fp16 values in registers:
+//   8-bit: byte permutes against 0x64 (fp16 1024 + u) and one packed subtract;
+//   4-bit int: nibble masks, then the same permutes and subtract;
+//   E2M1: v_cvt_scalef32_pk_f16_fp4 at scale 1.0 (the values 0 .. 6 and their
+//   negatives are exact in fp16; the E8M0 scale is applied in fp32 afterwards).
+// v_dot2_f32_f16 forms the products with x exactly in fp32 and accumulates in
+// fp32.  Per slice: acc += s * (sum c x - z * sum x), which is the reference's
+// sum over k of ((c - z) * s) * x in another fp32 summation order.
+#include "common.h"
+
+namespace {
+
+constexpr bool qf_4bit(int f) {
+  return f == LEMOQ_QFMT_W4 || f == LEMOQ_QFMT_W4_ASYM || f == LEMOQ_QFMT_MXFP4;
+}
+constexpr bool qf_asym(int f) { return f == LEMOQ_QFMT_W8_ASYM || f == LEMOQ_QFMT_W4_ASYM; }
+constexpr int qf_slice_codes(int f) { return qf_4bit(f) ? 32 : 16; }  // codes per 16-byte slice
+
+// E8M0 byte -> 2^(X - 127) as fp32, exactly as exp2(X - 127.0) in fp32:
+// X = 0 is the subnormal 2^-127, X = 255 overflows to +inf.
+__device__ __forceinline__ float e8m0_value(uint32_t X) {
+  return X == 0u ? __builtin_bit_cast(float, 0x00400000u) : __builtin_bit_cast(float, X << 23);
+}
+
+template <int FMT, bool S32>
+__device__ __forceinline__ uint32_t load_scale_raw(const void* p, int64_t i) {
+  if (FMT == LEMOQ_QFMT_MXFP4) return reinterpret_cast<const uint8_t*>(p)[i];
+  if (S32) return reinterpret_cast<const uint32_t*>(p)[i];
+  return reinterpret_cast<const uint16_t*>(p)[i];
+}
+
+template <int FMT, bool S32>
+__device__ __forceinline__ float scale_value(uint32_t raw) {
+  if (FMT == LEMOQ_QFMT_MXFP4) return e8m0_value(raw);
+  return S32 ? __builtin_bit_cast(float, raw) : h2f((uint16_t)raw);
+}
+
+// Unsigned 8-bit codes (0 .. 255) x 16 activations: as dot16_i8 without the
+// sign flip (fp16 1024 + u, minus 1024).
+__device__ __forceinline__ float dot16_u8(const u32x4 c, const XChunk& xc, float acc) {
+  const uint32_t cw[4] = {c.x, c.y, c.z, c.w};
+  const f16x2 bias = {(f16)1024.0f, (f16)1024.0f};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const f16x2 clo = as_h2(__builtin_amdgcn_perm(0x64646464u, cw[i], 0x04020400u)) - bias;
+    const f16x2 chi = as_h2(__builtin_amdgcn_perm(0x64646464u, cw[i], 0x04030401u)) - bias;
+    acc = __builtin_amdgcn_fdot2(clo, xc.a[i], acc, false);
+    acc = __builtin_amdgcn_fdot2(chi, xc.b[i], acc, false);
+  }
+  return acc;
+}
+
+// 32 packed 4-bit codes (16 bytes; byte b of dword d holds codes 8d + 2b in
+// its low nibble and 8d + 2b + 1 in its high nibble) x 32 activations given as
+// two XChunks (x[0, 16) and x[16, 32)).  SIGNED: int4 -8 .. 7 (xor 8 gives the
+// offset-binary nibble n + 8, minus 1032); else uint4 0 .. 15 (minus 1024).
+// Low nibbles of a dword are the codes (8d, 8d+2, 8d+4, 8d+6), high nibbles
+// (8d+1, 8d+3, 8d+5, 8d+7): the (x0, x2) / (x1, x3) pairs of XChunk.
+template <bool SIGNED>
+__device__ __forceinline__ float dot32_i4(const u32x4 c, const XChunk& x0, const XChunk& x1, float acc) {
+  const uint32_t cw[4] = {c.x, c.y, c.z, c.w};
+  const f16x2 bias = SIGNED ? (f16x2){(f16)1032.0f, (f16)1032.0f} : (f16x2){(f16)1024.0f, (f16)1024.0f};
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const uint32_t t = SIGNED ? cw[d] ^ 0x88888888u : cw[d];
+    const uint32_t lo = t & 0x0F0F0F0Fu, hi = (t >> 4) & 0x0F0F0F0Fu;
+    const XChunk& xc = d < 2 ? x0 : x1;
+    const int i0 = 2 * (d & 1);
+    const f16x2 p0 = as_h2(__builtin_amdgcn_perm(0x64646464u, lo, 0x04010400u)) - bias;  // 8d, 8d+2
+    const f16x2 p1 = as_h2(__builtin_amdgcn_perm(0x64646464u, lo, 0x04030402u)) - bias;  // 8d+4, 8d+6
+    const f16x2 p2 = as_h2(__builtin_amdgcn_perm(0x64646464u, hi, 0x04010400u)) - bias;  // 8d+1, 8d+3
+    const f16x2 p3 = as_h2(__builtin_amdgcn_perm(0x64646464u, hi, 0x04030402u)) - bias;  // 8d+5, 8d+7
+    acc = __builtin_amdgcn_fdot2(p0, xc.a[i0], acc, false);
+    acc = __builtin_amdgcn_fdot2(p1, xc.a[i0 + 1], acc, false);
+    acc = __builtin_amdgcn_fdot2(p2, xc.b[i0], acc, false);
+    acc = __builtin_amdgcn_fdot2(p3, xc.b[i0 + 1], acc, false);
+  }
+  return acc;
+}
+
+// 32 E2M1 codes x 32 activations in natural pairs (xw[m] = x[2m] | x[2m+1] << 16).
+// The conversion puts the low nibble of the selected byte in element 0
+// (checked on the device for all 256 bytes).
+__device__ __forceinline__ float dot32_fp4(const u32x4 c, const uint32_t (&xw)[16], float acc) {
+  const uint32_t cw[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    acc = __builtin_amdgcn_fdot2(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(cw[d], 1.0f, 0), as_h2(xw[4 * d + 0]),
+                                 acc, false);
+    acc = __builtin_amdgcn_fdot2(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(cw[d], 1.0f, 1), as_h2(xw[4 * d + 1]),
+                                 acc, false);
+    acc = __builtin_amdgcn_fdot2(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(cw[d], 1.0f, 2), as_h2(xw[4 * d + 2]),
+                                 acc, false);
+    acc = __builtin_amdgcn_fdot2(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(cw[d], 1.0f, 3), as_h2(xw[4 * d + 3]),
+                                 acc, false);
+  }
+  return acc;
+}
+
+struct GemvQArgs {
+  const uint16_t* x;
+  int64_t x_ld;
+  int K;                  // activation width (<= codes per row)
+  const uint8_t* codes;   // (N, row_bytes) packed rows
+  int row_bytes;
+  const void* scale;      // (N, ngroups): fp16 / fp32 / E8M0 bytes
+  const void* zero;       // (N, ngroups), same type as scale (asymmetric formats)
+  int64_t N;
+  int ngroups;
+  int group;              // codes per group
+  void* y;
+  int64_t y_ld;
+  int y_f16;
+};
+
+// Activation slice of one lane for chunk j: NV values from k0, zero at or past K.
+template <int NV>
+__device__ __forceinline__ void xq_load(uint32_t (&w)[NV / 2], const uint16_t* __restrict__ xr, int K, int k0,
+                                        bool vec) {
+  if (vec && k0 + NV <= K) {
+#pragma unroll
+    for (int q = 0; q < NV / 8; ++q) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(xr + k0 + 8 * q);
+      w[4 * q + 0] = v.x;
+      w[4 * q + 1] = v.y;
+      w[4 * q + 2] = v.z;
+      w[4 * q + 3] = v.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < NV / 2; ++i) {
+      const int e = k0 + 2 * i;
+      const uint32_t lo = e < K ? xr[e] : 0u;
+      const uint32_t hi = e + 1 < K ? xr[e + 1] : 0u;
+      w[i] = lo | (hi << 16);
+    }
+  }
+}
+
+// 16 values in natural pairs (8 dwords) -> XChunk (dot order of dot16_*).
+__device__ __forceinline__ void xchunk_of(const uint32_t* w, XChunk& xc) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t lo = w[2 * i], hi = w[2 * i + 1];
+    xc.a[i] = as_h2((lo & 0xFFFFu) | (hi << 16));
+    xc.b[i] = as_h2((lo >> 16) | (hi & 0xFFFF0000u));
+  }
+}
+
+template <int FMT, int KCH, int R, bool S32>
+__global__ __launch_bounds__(256) void gemv_q_kernel(const GemvQArgs a) {
+  constexpr int NV = qf_slice_codes(FMT);
+  constexpr int CPC = 64 * NV;  // codes per 1 KB chunk
+  constexpr bool ASYM = qf_asym(FMT);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t m = blockIdx.y;
+  const int64_t row0 = ((int64_t)blockIdx.x * 4 + wave) * R;
+
+  u32x4 c[R][KCH];
+  uint32_t sraw[R][KCH], zraw[R][KCH];
+  uint32_t ok = 0u;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int64_t row = row0 + r;
+#pragma unroll
+    for (int j = 0; j < KCH; ++j) {
+      const int off = 1024 * j + 16 * lane;
+      const bool in = row < a.N && off < a.row_bytes;
+      const int64_t rr = in ? row : 0;
+      const int oo = in ? off : 0;
+      c[r][j] = load_stream16(reinterpret_cast<const int8_t*>(a.codes) + rr * a.row_bytes + oo);
+      const int64_t si = rr * a.ngroups + (oo / 16) * NV / a.group;
+      sraw[r][j] = load_scale_raw<FMT, S32>(a.scale, si);
+      zraw[r][j] = ASYM ? load_scale_raw<FMT, S32>(a.zero, si) : 0u;
+      ok |= (in ? 1u : 0u) << (r * KCH + j);
+    }
+  }
+  const uint16_t* xr = a.x + m * a.x_ld;
+  const bool vec = ((reinterpret_cast<uintptr_t>(xr) & 15u) == 0) && ((a.K & 7) == 0);
+  uint32_t xw[KCH][NV / 2];
+#pragma unroll
+  for (int j = 0; j < KCH; ++j) xq_load<NV>(xw[j], xr, a.K, j * CPC + lane * NV, vec);
+  LEMOQ_LOADS_ISSUED();
+
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+#pragma unroll
+  for (int j = 0; j < KCH; ++j) {
+    float xs = 0.0f;  // sum of the slice's activations (zero-point term)
+    if (ASYM) {
+      const f16x2 one = {(f16)1.0f, (f16)1.0f};
+#pragma unroll
+      for (int i = 0; i < NV / 2; ++i) xs = __builtin_amdgcn_fdot2(as_h2(xw[j][i]), one, xs, false);
+    }
+    XChunk x0, x1;
+    if (FMT != LEMOQ_QFMT_MXFP4) {
+      xchunk_of(&xw[j][0], x0);
+      if (NV == 32) xchunk_of(&xw[j][8], x1);
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float d;
+      if constexpr (FMT == LEMOQ_QFMT_W8) d = dot16_i8(c[r][j], x0, 0.0f);
+      else if constexpr (FMT == LEMOQ_QFMT_W8_ASYM) d = dot16_u8(c[r][j], x0, 0.0f);
+      else if constexpr (FMT == LEMOQ_QFMT_W4) d = dot32_i4<true>(c[r][j], x0, x1, 0.0f);
+      else if constexpr (FMT == LEMOQ_QFMT_W4_ASYM) d = dot32_i4<false>(c[r][j], x0, x1, 0.0f);
+      else d = dot32_fp4(c[r][j], xw[j], 0.0f);
+      if (ASYM) d = fmaf(-scale_value<FMT, S32>(zraw[r][j]), xs, d);
+      const bool use = (ok >> (r * KCH + j)) & 1u;
+      acc[r] = use ? fmaf(scale_value<FMT, S32>(sraw[r][j]), d, acc[r]) : acc[r];
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
+  if (lane < R) {
+    float v = acc[0];
+#pragma unroll
+    for (int r = 1; r < R; ++r)
+      if (lane == r) v = acc[r];
+    const int64_t n = row0 + lane;
+    if (n < a.N) {
+      if (a.y_f16)
+        reinterpret_cast<uint16_t*>(a.y)[m * a.y_ld + n] = f2h(v);
+      else
+        reinterpret_cast<float*>(a.y)[m * a.y_ld + n] = v;
+    }
+  }
+}
+
+constexpr int kGemvQRows = 2;  // rows per wave, as the w8 GEMV
+
+template <int FMT, bool S32>
+int launch_gemv_q(int kch, dim3 grid, hipStream_t st, const GemvQArgs& a) {
+  switch (kch) {
+    case 1: hipLaunchKernelGGL((gemv_q_kernel<FMT, 1, kGemvQRows, S32>), grid, dim3(256), 0, st, a); break;
+    case 2: hipLaunchKernelGGL((gemv_q_kernel<FMT, 2, kGemvQRows, S32>), grid, dim3(256), 0, st, a); break;
+    case 4: hipLaunchKernelGGL((gemv_q_kernel<FMT, 4, kGemvQRows, S32>), grid, dim3(256), 0, st, a); break;
+    case 8:
+      if constexpr (!qf_4bit(FMT)) {
+        hipLaunchKernelGGL((gemv_q_kernel<FMT, 8, kGemvQRows, S32>), grid, dim3(256), 0, st, a);
+        break;
+      }
+      return LEMOQ_ERR_UNSUPPORTED;
+    default: return LEMOQ_ERR_UNSUPPORTED;
+  }
+  LEMOQ_CHECK_LAUNCH();
+}
+
+template <int FMT>
+int launch_gemv_q_fmt(bool s32, int kch, dim3 grid, hipStream_t st, const GemvQArgs& a) {
+  if constexpr (FMT == LEMOQ_QFMT_MXFP4) return launch_gemv_q<FMT, false>(kch, grid, st, a);
+  else return s32 ? launch_gemv_q<FMT, true>(kch, grid, st, a) : launch_gemv_q<FMT, false>(kch, grid, st, a);
+}
+
+// Shape rules shared by the GEMV and the dequantisation.  Returns 0 or a
+// LEMOQ_ERR_* status.
+int check_format(int fmt, const void* qweight, const void* scale, const void* zero, int scale_is_f32,
+                 int64_t N, int64_t padded_k, int64_t group) {
+  if (fmt < LEMOQ_QFMT_W8 || fmt > LEMOQ_QFMT_MXFP4) return LEMOQ_ERR_UNSUPPORTED;
+  if (!qweight || !scale) return LEMOQ_ERR_NULL;
+  const bool asym = fmt == LEMOQ_QFMT_W8_ASYM || fmt == LEMOQ_QFMT_W4_ASYM;
+  if (asym && !zero) return LEMOQ_ERR_NULL;
+  if (fmt == LEMOQ_QFMT_MXFP4 && (group != 32 || scale_is_f32 || zero)) return LEMOQ_ERR_UNSUPPORTED;
+  if (N <= 0 || N > 0x7fffffffLL || padded_k <= 0 || group <= 0) return LEMOQ_ERR_SHAPE;
+  const int nv = (fmt == LEMOQ_QFMT_W8 || fmt == LEMOQ_QFMT_W8_ASYM) ? 16 : 32;
+  if (group % nv != 0 || padded_k % group != 0 || padded_k > 8192) return LEMOQ_ERR_UNSUPPORTED;
+  if (!lemoq_aligned16(qweight)) return LEMOQ_ERR_ALIGN;
+  return LEMOQ_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Dequantisation to a dense weight, one thread per 16-byte slice of codes:
+// w = c * s (symmetric), (c - z) * s (asymmetric), e2m1(c) * 2^(X - 127)
+// (MXFP4), each in fp32 as the reference's separate arm computes it, then
+// stored as fp32 or rounded once to fp16 (`.to(dtype)`).  Columns at or past
+// k_out are not written.
+// ---------------------------------------------------------------------------
+struct DequantQArgs {
+  const uint8_t* codes;
+  int row_bytes;
+  const void* scale;
+  const void* zero;
+  int64_t N;
+  int ngroups;
+  int group;
+  void* w;
+  int64_t ld;
+  int k_out;
+};
+
+template <int FMT, bool S32, bool OUT32>
+__global__ __launch_bounds__(256) void dequant_q_kernel(const DequantQArgs a) {
+  constexpr int NV = qf_slice_codes(FMT);
+  const int64_t spr = a.row_bytes / 16;  // slices per row
+  const int64_t sl = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (sl >= a.N * spr) return;
+  const int64_t row = sl / spr;
+  const int k0 = (int)(sl - row * spr) * NV;
+  if (k0 >= a.k_out) return;
+  const u32x4 c = *reinterpret_cast<const u32x4*>(a.codes + row * a.row_bytes + (k0 / NV) * 16);
+  const int64_t si = row * a.ngroups + k0 / a.group;
+  const float s = scale_value<FMT, S32>(load_scale_raw<FMT, S32>(a.scale, si));
+  const float z = qf_asym(FMT) ? scale_value<FMT, S32>(load_scale_raw<FMT, S32>(a.zero, si)) : 0.0f;
+  const uint32_t cw[4] = {c.x, c.y, c.z, c.w};
+  float v[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    float code;
+    if (NV == 16) {
+      const uint32_t b = (cw[i >> 2] >> (8 * (i & 3))) & 0xFFu;
+      code = FMT == LEMOQ_QFMT_W8 ? (float)(int)(int8_t)b : (float)b;
+    } else {
+      const uint32_t nib = (cw[i >> 3] >> (4 * (i & 7))) & 0xFu;
+      if (FMT == LEMOQ_QFMT_W4) code = (float)((int)(nib ^ 8u) - 8);
+      else if (FMT == LEMOQ_QFMT_W4_ASYM) code = (float)nib;
+      else code = 0.0f;  // MXFP4 below
+    }
+    v[i] = code;
+  }
+  if (FMT == LEMOQ_QFMT_MXFP4) {
+#pragma unroll
+    for (int d = 0; d < 4; ++d)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        f16x2 p;
+        switch (b) {
+          case 0: p = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(cw[d], 1.0f, 0); break;
+          case 1: p = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(cw[d], 1.0f, 1); break;
+          case 2: p = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(cw[d], 1.0f, 2); break;
+          default: p = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(cw[d], 1.0f, 3); break;
+        }
+        v[8 * d + 2 * b] = (float)p[0];
+        v[8 * d + 2 * b + 1] = (float)p[1];
+      }
+  }
+#pragma unroll
+  for (int i = 0; i < NV; ++i) v[i] = qf_asym(FMT) ? (v[i] - z) * s : v[i] * s;
+  if (OUT32) {
+    float* dst = reinterpret_cast<float*>(a.w) + row * a.ld + k0;
+    for (int i = 0; i < NV && k0 + i < a.k_out; ++i) dst[i] = v[i];
+  } else {
+    uint16_t* dst = reinterpret_cast<uint16_t*>(a.w) + row * a.ld + k0;
+    const bool vec = k0 + NV <= a.k_out && ((reinterpret_cast<uintptr_t>(dst) & 15u) == 0);
+    if (vec) {
+#pragma unroll
+      for (int q = 0; q < NV / 8; ++q) {
+        uint32_t o[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          o[i] = (uint32_t)f2h(v[8 * q + 2 * i]) | ((uint32_t)f2h(v[8 * q + 2 * i + 1]) << 16);
+        *reinterpret_cast<u32x4*>(dst + 8 * q) = (u32x4){o[0], o[1], o[2], o[3]};
+      }
+    } else {
+      for (int i = 0; i < NV && k0 + i < a.k_out; ++i) dst[i] = f2h(v[i]);
+    }
+  }
+}
+
+template <int FMT, bool S32>
+int launch_dequant_q2(bool out32, dim3 grid, hipStream_t st, const DequantQArgs& a) {
+  if (out32)
+    hipLaunchKernelGGL((dequant_q_kernel<FMT, S32, true>), grid, dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL((dequant_q_kernel<FMT, S32, false>), grid, dim3(256), 0, st, a);
+  LEMOQ_CHECK_LAUNCH();
+}
+
+template <int FMT>
+int launch_dequant_q(bool s32, bool out32, dim3 grid, hipStream_t st, const DequantQArgs& a) {
+  if constexpr (FMT == LEMOQ_QFMT_MXFP4) return launch_dequant_q2<FMT, false>(out32, grid, st, a);
+  else return s32 ? launch_dequant_q2<FMT, true>(out32, grid, st, a) : launch_dequant_q2<FMT, false>(out32, grid, st, a);
+}
+
+// ---------------------------------------------------------------------------
+// Per-group RTN at 4 or 8 bits, symmetric or asymmetric, one wave per
+// (row, group) (src/lemoq/quant/rtn.py:58-87):
+//   symmetric:  s = absmax / qmax (1 when absmax == 0), c = clamp(rint(w / s),
+//               -(qmax + 1), qmax), zero 0;
+//   asymmetric: over the real columns only (the zero padding of the last
+//               group is left out of min / max), gmax / gmin (0 when not
+//               finite), s = (gmax - gmin) / qmax (1 when the range is 0),
+//               z = rint(-gmin / s), c = clamp(rint(w / s) + z, 0, qmax).
+// All in fp32 with IEEE division and round-half-even.  4-bit codes are packed
+// two per byte, the even column in the low nibble (pack.pack_4bit).
+// ---------------------------------------------------------------------------
+template <int BITS, bool SYM>
+__global__ __launch_bounds__(256) void rtn_q_kernel(const float* __restrict__ w, int64_t rows, int64_t cols,
+                                                    int64_t group, int64_t ngroups, uint8_t* __restrict__ codes,
+                                                    int64_t code_ld, uint16_t* __restrict__ s16,
+                                                    float* __restrict__ s32, uint16_t* __restrict__ z16,
+                                                    float* __restrict__ z32) {
+  constexpr float QMAX = SYM ? (float)((1 << (BITS - 1)) - 1) : (float)((1 << BITS) - 1);
+  const int lane = threadIdx.x & 63;
+  const int64_t gid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (gid >= rows * ngroups) return;
+  const int64_t row = gid / ngroups;
+  const int64_t k0 = (gid - row * ngroups) * group;
+  const float* wr = w + row * cols;
+  float s, z = 0.0f;
+  if (SYM) {
+    float amax = 0.0f;
+    for (int64_t i = lane; i < group; i += 64) {
+      const int64_t k = k0 + i;
+      amax = fmaxf(amax, fabsf(k < cols ? wr[k] : 0.0f));
+    }
+    amax = wave_max(amax);
+    s = amax > 0.0f ? amax / QMAX : 1.0f;
+  } else {
+    float gmax = -INFINITY, gmin = INFINITY;
+    for (int64_t i = lane; i < group; i += 64) {
+      const int64_t k = k0 + i;
+      if (k < cols) {
+        gmax = fmaxf(gmax, wr[k]);
+        gmin = fminf(gmin, wr[k]);
+      }
+    }
+    gmax = wave_max(gmax);
+    gmin = -wave_max(-gmin);
+    if (!__builtin_isfinite(gmax)) gmax = 0.0f;
+    if (!__builtin_isfinite(gmin)) gmin = 0.0f;
+    const float rng = gmax - gmin;
+    s = rng > 0.0f ? rng / QMAX : 1.0f;
+    z = rintf(-gmin / s);
+  }
+  const float lo = SYM ? -(QMAX + 1.0f) : 0.0f;
+  if (BITS == 8) {
+    for (int64_t i = lane; i < group; i += 64) {
+      const int64_t k = k0 + i;
+      float q = rintf((k < cols ? wr[k] : 0.0f) / s);
+      if (!SYM) q = q + z;
+      q = fminf(fmaxf(q, lo), QMAX);
+      codes[row * code_ld + k] = SYM ? (uint8_t)(int8_t)(int)q : (uint8_t)(int)q;
+    }
+  } else {
+    for (int64_t i = 2 * lane; i < group; i += 128) {  // a pair of columns per byte
+      const int64_t k = k0 + i;
+      float q0 = rintf((k < cols ? wr[k] : 0.0f) / s);
+      float q1 = rintf((k + 1 < cols ? wr[k + 1] : 0.0f) / s);
+      if (!SYM) {
+        q0 = q0 + z;
+        q1 = q1 + z;
+      }
+      q0 = fminf(fmaxf(q0, lo), QMAX);
+      q1 = fminf(fmaxf(q1, lo), QMAX);
+      const uint32_t b = ((uint32_t)(int)q0 & 0xFu) | (((uint32_t)(int)q1 & 0xFu) << 4);
+      codes[row * code_ld + k / 2] = (uint8_t)b;
+    }
+  }
+  if (lane == 0) {
+    if (s16) s16[gid] = f2h(s);
+    if (s32) s32[gid] = s;
+    if (z16) z16[gid] = f2h(z);
+    if (z32) z32[gid] = z;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// MXFP4 quantiser (src/lemoq/quant/mxfp4.py:50-102), two blocks of 32 columns
+// per wave (lanes 0-31 and 32-63), columns past `cols` read as 0:
+//   X = clamp(floor(log2(amax)) - 2, -127, 127), X = -127 for an all-zero
+//   block; the scale byte is X + 127;
+//   v = w / 2^X (exact: a power-of-two scaling), m = min(|v|, 6);
+//   the magnitude code is the first index of the smallest |m - M[i]| over
+//   M = {0, 0.5, 1, 1.5, 2, 3, 4, 6} (ties go to the smaller magnitude);
+//   code = (v < 0) << 3 | index; two codes per byte, even column low.
+// log2 follows torch's fp32 log2 (the correctly rounded value, which is what
+// the floor sees: amax one ulp below 2^k gives k, not k - 1): the double
+// log2 rounded to fp32.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void mxfp4_quant_kernel(const float* __restrict__ w, int64_t rows, int64_t cols,
+                                                          int64_t nblk, uint8_t* __restrict__ codes,
+                                                          uint8_t* __restrict__ scales) {
+  const int lane = threadIdx.x & 63;
+  const int64_t blk = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 2 + (lane >> 5);
+  const bool live = blk < rows * nblk;
+  const int64_t b = live ? blk : 0;
+  const int64_t row = b / nblk, bi = b - row * nblk;
+  const int64_t col = bi * 32 + (lane & 31);
+  const float v = (live && col < cols) ? w[row * cols + col] : 0.0f;
+  const float amax = group_max<32>(fabsf(v));
+  float X = -127.0f;
+  if (amax > 0.0f) X = fminf(fmaxf(floorf((float)log2((double)amax)) - 2.0f, -127.0f), 127.0f);
+  const float nv = ldexpf(v, -(int)X);
+  const float mag = fminf(fabsf(nv), 6.0f);
+  const float M[8] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f};
+  int idx = 0;
+  float best = fabsf(mag - M[0]);
+#pragma unroll
+  for (int i = 1; i < 8; ++i) {
+    const float d = fabsf(mag - M[i]);
+    if (d < best) {
+      best = d;
+      idx = i;
+    }
+  }
+  const uint32_t code = (nv < 0.0f ? 8u : 0u) | (uint32_t)idx;
+  const uint32_t hi = (uint32_t)__shfl_xor((int)code, 1, LEMOQ_WAVE);
+  if (live && (lane & 1) == 0) codes[row * nblk * 16 + (bi * 32 + (lane & 31)) / 2] = (uint8_t)(code | (hi << 4));
+  if (live && (lane & 31) == 0) scales[b] = (uint8_t)(int)(X + 127.0f);
+}
+
+// ---------------------------------------------------------------------------
+// Per-token symmetric int8 fake quantisation of activations (the w8a8
+// scheme's QuantLinear._fake_quant_activation, src/lemoq/quant/linear.py:398-414),
+// one wave per row: fp32 absmax, s = absmax / 127 (1 when 0),
+// q = clamp(rint(x / s), -128, 127), y = fp16(q * s) (fp32 product, one rounding).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void fake_quant_rows_kernel(const uint16_t* __restrict__ x, int64_t rows,
+                                                              int D, uint16_t* __restrict__ y) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const uint16_t* xr = x + r * D;
+  uint16_t* yr = y + r * D;
+  float amax = 0.0f;
+  for (int d = lane; d < D; d += 64) amax = fmaxf(amax, fabsf(h2f(xr[d])));
+  amax = wave_max(amax);
+  const float s = amax > 0.0f ? amax / 127.0f : 1.0f;
+  for (int d = lane; d < D; d += 64) {
+    const float q = fminf(fmaxf(rintf(h2f(xr[d]) / s), -128.0f), 127.0f);
+    yr[d] = f2h(q * s);
+  }
+}
+
+}  // namespace
+
+extern "C" int lemoq_fake_quant_rows(const uint16_t* x, int64_t rows, int64_t D, uint16_t* y, void* stream) {
+  if (!x || !y) return LEMOQ_ERR_NULL;
+  if (rows < 0 || D <= 0 || D > 0x7fffffffLL) return LEMOQ_ERR_SHAPE;
+  if (rows == 0) return LEMOQ_OK;
+  const int64_t blocks = (rows + 3) / 4;
+  if (blocks > 0x7fffffffLL) return LEMOQ_ERR_SHAPE;
+  hipLaunchKernelGGL(fake_quant_rows_kernel, dim3((unsigned)blocks), dim3(256), 0, lemoq_stream(stream), x, rows,
+                     (int)D, y);
+  LEMOQ_CHECK_LAUNCH();
+}
+
+extern "C" int lemoq_gemv_q(const uint16_t* x, int64_t M, int64_t K, const void* qweight, int fmt,
+                            const void* scale, const void* zero, int scale_is_f32, int64_t N,
+                            int64_t padded_k, int64_t group, void* y, int y_is_f16, void* stream) {
+  if (!x || !y) return LEMOQ_ERR_NULL;
+  const int rc = check_format(fmt, qweight, scale, zero, scale_is_f32, N, padded_k, group);
+  if (rc) return rc;
+  if (M <= 0 || M > 65535 || K <= 0 || K > padded_k) return LEMOQ_ERR_SHAPE;
+  GemvQArgs a;
+  a.x = x;
+  a.x_ld = K;
+  a.K = (int)K;
+  a.codes = reinterpret_cast<const uint8_t*>(qweight);
+  const bool four = qf_4bit(fmt);
+  a.row_bytes = (int)(four ? padded_k / 2 : padded_k);
+  a.scale = scale;
+  a.zero = zero;
+  a.N = N;
+  a.ngroups = (int)(padded_k / group);
+  a.group = (int)group;
+  a.y = y;
+  a.y_ld = N;
+  a.y_f16 = y_is_f16 ? 1 : 0;
+  const int64_t chunks = (a.row_bytes + 1023) / 1024;
+  const int kch = chunks <= 1 ? 1 : (chunks <= 2 ? 2 : (chunks <= 4 ? 4 : 8));
+  const int64_t blocks = (N + 4 * kGemvQRows - 1) / (4 * kGemvQRows);
+  const dim3 grid((unsigned)blocks, (unsigned)M);
+  hipStream_t st = lemoq_stream(stream);
+  const bool s32 = scale_is_f32 != 0;
+  switch (fmt) {
+    case LEMOQ_QFMT_W8: return launch_gemv_q_fmt<LEMOQ_QFMT_W8>(s32, kch, grid, st, a);
+    case LEMOQ_QFMT_W8_ASYM: return launch_gemv_q_fmt<LEMOQ_QFMT_W8_ASYM>(s32, kch, grid, st, a);
+    case LEMOQ_QFMT_W4: return launch_gemv_q_fmt<LEMOQ_QFMT_W4>(s32, kch, grid, st, a);
+    case LEMOQ_QFMT_W4_ASYM: return launch_gemv_q_fmt<LEMOQ_QFMT_W4_ASYM>(s32, kch, grid, st, a);
+    default: return launch_gemv_q_fmt<LEMOQ_QFMT_MXFP4>(false, kch, grid, st, a);
+  }
+}
+
+extern "C" int lemoq_dequant_q(const void* qweight, int fmt, const void* scale, const void* zero,
+                               int scale_is_f32, int64_t N, int64_t padded_k, int64_t group, void* w,
+                               int64_t ld_w, int64_t k_out, int w_is_f32, void* stream) {
+  if (!w) return LEMOQ_ERR_NULL;
+  const int rc = check_format(fmt, qweight, scale, zero, scale_is_f32, N, padded_k, group);
+  if (rc) return rc;
+  if (k_out <= 0 || k_out > padded_k || ld_w < k_out) return LEMOQ_ERR_SHAPE;
+  DequantQArgs a;
+  a.codes = reinterpret_cast<const uint8_t*>(qweight);
+  a.row_bytes = (int)(qf_4bit(fmt) ? padded_k / 2 : padded_k);
+  a.scale = scale;
+  a.zero = zero;
+  a.N = N;
+  a.ngroups = (int)(padded_k / group);
+  a.group = (int)group;
+  a.w = w;
+  a.ld = ld_w;
+  a.k_out = (int)k_out;
+  const int64_t slices = N * (a.row_bytes / 16);
+  const int64_t blocks = (slices + 255) / 256;
+  if (blocks > 0x7fffffffLL) return LEMOQ_ERR_SHAPE;
+  const dim3 grid((unsigned)blocks);
+  hipStream_t st = lemoq_stream(stream);
+  const bool s32 = scale_is_f32 != 0, o32 = w_is_f32 != 0;
+  switch (fmt) {
+    case LEMOQ_QFMT_W8: return launch_dequant_q<LEMOQ_QFMT_W8>(s32, o32, grid, st, a);
+    case LEMOQ_QFMT_W8_ASYM: return launch_dequant_q<LEMOQ_QFMT_W8_ASYM>(s32, o32, grid, st, a);
+    case LEMOQ_QFMT_W4: return launch_dequant_q<LEMOQ_QFMT_W4>(s32, o32, grid, st, a);
+    case LEMOQ_QFMT_W4_ASYM: return launch_dequant_q<LEMOQ_QFMT_W4_ASYM>(s32, o32, grid, st, a);
+    default: return launch_dequant_q<LEMOQ_QFMT_MXFP4>(false, o32, grid, st, a);
+  }
+}
+
+extern "C" int lemoq_rtn_quantize(const float* w, int64_t rows, int64_t cols, int64_t group, int bits,
+                                  int symmetric, uint8_t* codes, uint16_t* scale_f16, float* scale_f32,
+                                  uint16_t* zero_f16, float* zero_f32, void* stream) {
+  if (!w || !codes) return LEMOQ_ERR_NULL;
+  if (bits != 4 && bits != 8) return LEMOQ_ERR_UNSUPPORTED;
+  if (rows < 0 || cols <= 0 || group <= 0 || (bits == 4 && group % 2 != 0)) return LEMOQ_ERR_SHAPE;
+  if (rows == 0) return LEMOQ_OK;
+  const int64_t ngroups = (cols + group - 1) / group;
+  const int64_t padded = ngroups * group;
+  const int64_t code_ld = bits == 4 ? padded / 2 : padded;
+  const int64_t blocks = (rows * ngroups + 3) / 4;
+  if (blocks > 0x7fffffffLL) return LEMOQ_ERR_SHAPE;
+  hipStream_t st = lemoq_stream(stream);
+  const dim3 grid((unsigned)blocks);
+#define LEMOQ_RTN_CASE(B, S)                                                                         \
+  hipLaunchKernelGGL((rtn_q_kernel<B, S>), grid, dim3(256), 0, st, w, rows, cols, group, ngroups, codes, \
+                     code_ld, scale_f16, scale_f32, zero_f16, zero_f32)
+  if (bits == 8 && symmetric) LEMOQ_RTN_CASE(8, true);
+  else if (bits == 8) LEMOQ_RTN_CASE(8, false);
+  else if (symmetric) LEMOQ_RTN_CASE(4, true);
+  else LEMOQ_RTN_CASE(4, false);
+#undef LEMOQ_RTN_CASE
+  LEMOQ_CHECK_LAUNCH();
+}
+
+extern "C" int lemoq_mxfp4_quantize(const float* w, int64_t rows, int64_t cols, uint8_t* codes_packed,
+                                    uint8_t* scale_e8m0, void* stream) {
+  if (!w || !codes_packed || !scale_e8m0) return LEMOQ_ERR_NULL;
+  if (rows < 0 || cols <= 0) return LEMOQ_ERR_SHAPE;
+  if (rows == 0) return LEMOQ_OK;
+  const int64_t nblk = (cols + 31) / 32;
+  const int64_t waves = (rows * nblk + 1) / 2;
+  const int64_t blocks = (waves + 3) / 4;
+  if (blocks > 0x7fffffffLL) return LEMOQ_ERR_SHAPE;
+  hipLaunchKernelGGL(mxfp4_quant_kernel, dim3((unsigned)blocks), dim3(256), 0, lemoq_stream(stream), w, rows,
+                     cols, nblk, codes_packed, scale_e8m0);
+  LEMOQ_CHECK_LAUNCH();
+}

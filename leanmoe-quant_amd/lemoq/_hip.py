@@ -19,7 +19,7 @@ LIB_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib")
 LIB_NAME = "liblemoq_hip.so"
 LIB_PATH = os.path.join(LIB_DIR, LIB_NAME)
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -113,6 +113,11 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "lemoq_status_string": (ctypes.c_char_p, [_I]),
     "lemoq_abi_version": (_I, []),
     "lemoq_rtn_quantize_w8": (_I, [_P, _I64, _I64, _I64, _P, _P, _P, _P]),
+    "lemoq_rtn_quantize": (_I, [_P, _I64, _I64, _I64, _I, _I, _P, _P, _P, _P, _P, _P]),
+    "lemoq_mxfp4_quantize": (_I, [_P, _I64, _I64, _P, _P, _P]),
+    "lemoq_gemv_q": (_I, [_P, _I64, _I64, _P, _I, _P, _P, _I, _I64, _I64, _I64, _P, _I, _P]),
+    "lemoq_dequant_q": (_I, [_P, _I, _P, _P, _I, _I64, _I64, _I64, _P, _I64, _I64, _I, _P]),
+    "lemoq_fake_quant_rows": (_I, [_P, _I64, _I64, _P, _P]),
     "lemoq_gemv_w8": (_I, [_P, _I64, _I64, _P, _P, _I64, _I64, _I64, _P, _I, _P]),
     "lemoq_gemv_w8_fused": (
         _I,

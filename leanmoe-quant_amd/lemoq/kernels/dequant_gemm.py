@@ -1,15 +1,17 @@
-"""w8 dense GEMV with in-register dequantisation (``lemoq_gemv_w8``), and the
-multi-token w8 / fp16 linears on the matrix cores (``lemoq_gemm_w8``,
-``lemoq_gemm_f16``).
+"""Dense dequant GEMV (``lemoq_gemv_w8``, ``lemoq_gemv_q``) and the multi-token
+linears on the matrix cores (``lemoq_gemm_w8``, ``lemoq_gemm_f16``).
 
 Replaces ``dequant_gemm_fused`` of the reference
-(``src/lemoq/kernels/_dequant_triton.py:155-293``) for the branch the decode
-hot path uses: 8-bit symmetric codes (int8), fp16 per-group scales along the
-input dimension, ``zero=None``.  Same contract: ``y = x @ dequant(qweight).T``
-with fp32 accumulation and a single rounding to ``out_dtype`` (fp32 by
-default), contiguous inputs required, boundaries raise instead of computing
-something wrong.  The 4-bit, asymmetric and MXFP4 branches are outside the
-decode path and raise ``NotImplementedError``.
+(``src/lemoq/kernels/_dequant_triton.py:155-293``) for every weight format it
+takes: 8-bit symmetric (int8) and asymmetric (uint8 + zero point), 4-bit
+symmetric and asymmetric (two codes per byte), and MXFP4 (E2M1 codes + E8M0
+byte scales per 32).  Same contract: ``y = x @ dequant(qweight).T`` with fp32
+dequantisation and accumulation and a single rounding to ``out_dtype`` (fp32
+by default), contiguous inputs required, the same argument checks (and
+exception types) before anything runs.  Activations are fp16 (the decode
+path's type); fp32 activations raise ``NotImplementedError``.  The 8-bit
+symmetric branch with fp16 scales runs the decode step's GEMV; the others run
+``lemoq_gemv_q``.
 """
 
 from __future__ import annotations
@@ -39,6 +41,63 @@ def fused_available() -> bool:
         return False
 
 
+def _check_format(qweight: Any, scale: Any, zero: Any, group_size: int, bits: int | None, symmetric: bool,
+                  mxfp4: bool) -> tuple[int, int, int]:
+    """The reference's argument rules (``_dequant_triton.py:200-249``); returns
+    (bits, padded_in, format id)."""
+    import torch  # noqa: PLC0415
+
+    from lemoq.quant.formats import format_id  # noqa: PLC0415
+
+    if qweight.dim() != 2:
+        raise ValueError("qweight must be 2-D (N, P), got %r" % (tuple(qweight.shape),))
+    if scale.dim() != 2:
+        raise ValueError("scale must be 2-D (N, n_groups), got %r" % (tuple(scale.shape),))
+    N, packed_in = int(qweight.shape[0]), int(qweight.shape[1])
+    n_groups = int(scale.shape[1])
+    if int(scale.shape[0]) != N:
+        raise ValueError("scale has %d rows, qweight has %d" % (int(scale.shape[0]), N))
+    if bits is None:
+        bits = 4 if qweight.dtype == torch.uint8 else 8
+    bits = int(bits)
+    if bits not in (4, 8):
+        raise NotImplementedError("fused dequant-GEMM implements 4/8-bit, got %d" % bits)
+    if mxfp4:
+        if bits != 4:
+            raise ValueError("mxfp4 is 4-bit E2M1 only, got bits=%r" % bits)
+        if int(group_size) != 32:
+            raise ValueError("the mxfp4 block is fixed at 32 (OCP MX), got group_size=%d" % int(group_size))
+        if scale.dtype != torch.uint8:
+            raise ValueError("mxfp4 scales must be uint8 E8M0 bytes, got %s" % scale.dtype)
+        if not symmetric or zero is not None:
+            raise ValueError("mxfp4 has no zero point (E2M1 carries its sign): symmetric=True and zero=None")
+    padded_in = n_groups * int(group_size)
+    expect_packed = padded_in if bits == 8 else padded_in // 2
+    if packed_in != expect_packed:
+        raise ValueError("qweight width %d != %d implied by n_groups * group_size (and bits)"
+                         % (packed_in, expect_packed))
+    if not symmetric and zero is None:
+        raise ValueError("asymmetric quantisation needs a zero point")
+    if bits == 4 and int(group_size) % 2 != 0:
+        raise ValueError("4-bit needs an even group_size, got %d" % int(group_size))
+    expected = torch.uint8 if (bits == 4 or not symmetric) else torch.int8
+    if qweight.dtype != expected:
+        raise ValueError("%d-bit qweight must be %s, got %s" % (bits, expected, qweight.dtype))
+    if not mxfp4 and scale.dtype not in (torch.float16, torch.float32):
+        raise ValueError("scale must be fp16 or fp32, got %s" % scale.dtype)
+    if zero is not None and tuple(zero.shape) != tuple(scale.shape):
+        raise ValueError("zero must have the shape of scale, got %r" % (tuple(zero.shape),))
+    for name, tensor in (("qweight", qweight), ("scale", scale), ("zero", zero)):
+        if tensor is not None and not tensor.is_contiguous():
+            raise ValueError("%s must be contiguous" % name)
+    step = 16 if bits == 8 else 32
+    if int(group_size) % step != 0 or padded_in > MAX_PADDED_K:
+        raise NotImplementedError(
+            "the HIP GEMV needs group_size %% %d == 0 and padded_in <= %d (got group %d, padded %d)"
+            % (step, MAX_PADDED_K, int(group_size), padded_in))
+    return bits, padded_in, format_id(bits, symmetric, mxfp4)
+
+
 def dequant_gemm_fused(
     x: Any,
     qweight: Any,
@@ -52,73 +111,42 @@ def dequant_gemm_fused(
     config: dict[str, Any] | None = None,
     mxfp4: bool = False,
 ) -> Any:
-    """``y (M, N) = x (M, K) @ dequant(qweight (N, P), scale (N, n_groups)).T``."""
+    """``y (M, N) = x (M, K) @ dequant(qweight (N, P), scale (N, n_groups), zero).T``."""
     import torch  # noqa: PLC0415
+
+    from lemoq.quant.formats import QFMT_W8, scale_zero_args  # noqa: PLC0415
 
     del config
     if x.dim() != 2:
         raise ValueError("x must be 2-D (M, K), got %r" % (tuple(x.shape),))
-    if qweight.dim() != 2:
-        raise ValueError("qweight must be 2-D (N, P), got %r" % (tuple(qweight.shape),))
-    if scale.dim() != 2:
-        raise ValueError("scale must be 2-D (N, n_groups), got %r" % (tuple(scale.shape),))
+    bits, padded_in, fmt = _check_format(qweight, scale, zero, group_size, bits, symmetric, mxfp4)
     M, K = int(x.shape[0]), int(x.shape[1])
-    N, packed_in = int(qweight.shape[0]), int(qweight.shape[1])
-    n_groups = int(scale.shape[1])
-    if int(scale.shape[0]) != N:
-        raise ValueError("scale has %d rows, qweight has %d" % (int(scale.shape[0]), N))
-    if bits is None:
-        bits = 4 if qweight.dtype == torch.uint8 else 8
-    bits = int(bits)
-    if bits not in (4, 8):
-        raise NotImplementedError("fused dequant-GEMM implements 4/8-bit, got %d" % bits)
-    if mxfp4 or bits != 8 or not symmetric or zero is not None:
-        raise NotImplementedError(
-            "the HIP build implements the 8-bit symmetric (zero=None) branch only"
-        )
-    padded_in = n_groups * int(group_size)
-    if packed_in != padded_in:
-        raise ValueError(
-            "qweight width %d != n_groups*group_size %d" % (packed_in, padded_in)
-        )
+    N = int(qweight.shape[0])
     if K > padded_in:
         raise ValueError("K=%d exceeds padded_in=%d" % (K, padded_in))
-    if qweight.dtype != torch.int8:
-        raise ValueError("8-bit symmetric qweight must be int8, got %s" % qweight.dtype)
     if x.dtype != torch.float16:
-        raise NotImplementedError("x must be fp16 (the w8a16 path), got %s" % x.dtype)
-    if scale.dtype != torch.float16:
-        raise NotImplementedError("scale must be fp16, got %s" % scale.dtype)
+        raise NotImplementedError("x must be fp16 (the w8a16 / w4a16 decode path), got %s" % x.dtype)
+    if not x.is_contiguous():
+        raise ValueError("x must be contiguous")
     if out_dtype is None:
         out_dtype = torch.float32
     if out_dtype not in (torch.float32, torch.float16):
         raise NotImplementedError("out_dtype must be fp32 or fp16, got %s" % out_dtype)
-    for name, tensor in (("x", x), ("qweight", qweight), ("scale", scale)):
-        if not tensor.is_contiguous():
-            raise ValueError("%s must be contiguous" % name)
-    if int(group_size) % 16 != 0 or padded_in % 16 != 0 or padded_in > MAX_PADDED_K:
-        raise NotImplementedError(
-            "HIP GEMV needs group_size %% 16 == 0 and padded_in <= %d (got group %d, padded %d)"
-            % (MAX_PADDED_K, int(group_size), padded_in)
-        )
-    _hip.require_rocm(x, qweight, scale, what="dequant_gemm_fused")
+    zero_arg = None if symmetric else zero
+    scale_arg, zero_arg, s32 = scale_zero_args(scale, zero_arg)
+    _hip.require_rocm(x, qweight, scale_arg, what="dequant_gemm_fused")
     y = torch.empty((M, N), dtype=out_dtype, device=x.device)
     if M == 0 or N == 0:
         return y
-    _hip.call(
-        "lemoq_gemv_w8",
-        _hip.ptr(x),
-        M,
-        K,
-        _hip.ptr(qweight),
-        _hip.ptr(scale),
-        N,
-        padded_in,
-        int(group_size),
-        _hip.ptr(y),
-        1 if out_dtype == torch.float16 else 0,
-        _hip.stream_of(x.device),
-    )
+    y16 = 1 if out_dtype == torch.float16 else 0
+    st = _hip.stream_of(x.device)
+    if fmt == QFMT_W8 and not s32:
+        _hip.call("lemoq_gemv_w8", _hip.ptr(x), M, K, _hip.ptr(qweight), _hip.ptr(scale_arg), N, padded_in,
+                  int(group_size), _hip.ptr(y), y16, st)
+    else:
+        _hip.call("lemoq_gemv_q", _hip.ptr(x), M, K, _hip.ptr(qweight), fmt, _hip.ptr(scale_arg),
+                  _hip.ptr(zero_arg) if zero_arg is not None else None, s32, N, padded_in, int(group_size),
+                  _hip.ptr(y), y16, st)
     return y
 
 
@@ -148,6 +176,7 @@ def dequant_gemm_separate(
     bits: int = 8,
     symmetric: bool = True,
     residual: Any = None,
+    mxfp4: bool = False,
 ) -> Any:
     """``y (M, N) = fp16(x @ fp16(dequant(qweight)).T)`` on the matrix cores.
 
@@ -157,12 +186,16 @@ def dequant_gemm_separate(
     weight: each code is dequantised to ``fp16(code * scale)`` in registers,
     products accumulate in fp32, the output is rounded to fp16 once.  With
     ``residual`` (M, N) fp16, ``y = fp16(y + residual)``.  K must equal the
-    padded width (a multiple of 64 and of ``group_size``).
+    padded width (a multiple of 64 and of ``group_size``).  The other weight
+    formats (4-bit, asymmetric, MXFP4, fp32 scales) dequantise the weight to
+    fp16 first (``lemoq_dequant_q``, the reference arm's materialised weight)
+    and run the fp16 GEMM; they take no residual.
     """
     import torch  # noqa: PLC0415
 
-    if bits != 8 or not symmetric or zero is not None:
-        raise NotImplementedError("the HIP build implements the 8-bit symmetric (zero=None) branch only")
+    if mxfp4 or bits != 8 or not symmetric or zero is not None or scale.dtype != torch.float16:
+        return _separate_dense(x, qweight, scale, zero, group_size=group_size, bits=bits, symmetric=symmetric,
+                               residual=residual, mxfp4=mxfp4)
     if qweight.dim() != 2 or qweight.dtype != torch.int8 or not qweight.is_contiguous():
         raise ValueError("qweight must be contiguous int8 (N, K)")
     N, K = int(qweight.shape[0]), int(qweight.shape[1])
@@ -184,6 +217,26 @@ def dequant_gemm_separate(
               _hip.ptr(y), N, _hip.ptr(residual) if residual is not None else None, N,
               _hip.stream_of(x.device))
     return y
+
+
+def _separate_dense(x: Any, qweight: Any, scale: Any, zero: Any, *, group_size: int, bits: int, symmetric: bool,
+                    residual: Any, mxfp4: bool) -> Any:
+    """Separate arm for the formats the w8 matrix-core GEMM does not read:
+    fp16 ``dequantized_weight`` (``src/lemoq/quant/linear.py:365-395``), then
+    ``F.linear`` in fp16 with fp32 accumulation (``lemoq_gemm_f16``)."""
+    from lemoq.quant.formats import dequantize  # noqa: PLC0415
+
+    import torch  # noqa: PLC0415
+
+    if residual is not None:
+        raise NotImplementedError("the dequantise-then-GEMM arm takes no residual")
+    bits, padded_in, fmt = _check_format(qweight, scale, zero, group_size, bits, symmetric, mxfp4)
+    if padded_in % 64 != 0:
+        raise NotImplementedError("the fp16 GEMM needs padded_in % 64 == 0, got %d" % padded_in)
+    _check_rows(x, padded_in, "dequant_gemm_separate")
+    w = dequantize(qweight, scale, None if symmetric else zero, fmt=fmt, group_size=group_size, k_out=padded_in,
+                   dtype=torch.float16)
+    return linear_f16(x, w)
 
 
 def linear_f16(x: Any, weight: Any, *, splits: int = 1) -> Any:

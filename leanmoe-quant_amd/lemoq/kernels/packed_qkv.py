@@ -57,6 +57,8 @@ def pack_qkv(q: Any, k: Any, v: Any) -> PackedQKV:
             raise NotImplementedError("packed q/k/v supports w8 only (%s)" % role)
         if m.zero is not None:
             raise NotImplementedError("packed q/k/v supports symmetric weights only (%s)" % role)
+        if getattr(m, "act_bits", None) is not None:
+            raise NotImplementedError("packed q/k/v supports fp16 activations only (%s is w8a8)" % role)
         if m.bias is not None:
             raise NotImplementedError("packed q/k/v does not support biased projections (%s)" % role)
     shape = {

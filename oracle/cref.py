@@ -33,6 +33,10 @@ def load():
         lib.oracle_rtn_w8.restype = None
         lib.oracle_kv_quant_rows.argtypes = [P, I64, I64, P, P]
         lib.oracle_kv_quant_rows.restype = None
+        lib.oracle_rtn.argtypes = [P, I64, I64, I64, ctypes.c_int, ctypes.c_int, P, P, P]
+        lib.oracle_rtn.restype = None
+        lib.oracle_mxfp4.argtypes = [P, I64, I64, P, P]
+        lib.oracle_mxfp4.restype = None
         lib.oracle_f32_to_f16.argtypes = [ctypes.c_float]
         lib.oracle_f32_to_f16.restype = ctypes.c_uint16
         _lib = lib
@@ -65,3 +69,27 @@ def f32_to_f16(values: np.ndarray) -> np.ndarray:
     v = np.asarray(values, dtype=np.float32).reshape(-1)
     out = np.array([lib.oracle_f32_to_f16(float(t)) for t in v], dtype=np.uint16)
     return out.view(np.float16).reshape(np.shape(values))
+
+
+def rtn(w: np.ndarray, group: int, bits: int, symmetric: bool):
+    """Codes (int32, rows x padded), scale and zero (float32) of ``oracle_rtn``."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    rows, cols = w.shape
+    ng = -(-cols // group)
+    codes = np.zeros((rows, ng * group), dtype=np.int32)
+    s32 = np.zeros((rows, ng), dtype=np.float32)
+    z32 = np.zeros((rows, ng), dtype=np.float32)
+    load().oracle_rtn(w.ctypes.data, rows, cols, group, bits, 1 if symmetric else 0, codes.ctypes.data,
+                      s32.ctypes.data, z32.ctypes.data)
+    return codes, s32, z32
+
+
+def mxfp4(w: np.ndarray):
+    """Unpacked E2M1 codes (rows x nblk*32) and E8M0 scale bytes of ``oracle_mxfp4``."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    rows, cols = w.shape
+    nblk = -(-cols // 32)
+    codes = np.zeros((rows, nblk * 32), dtype=np.uint8)
+    scales = np.zeros((rows, nblk), dtype=np.uint8)
+    load().oracle_mxfp4(w.ctypes.data, rows, cols, codes.ctypes.data, scales.ctypes.data)
+    return codes, scales

@@ -120,6 +120,24 @@ def test_argument_rejection_happens_before_any_launch():
     assert rr(fake, 4, 1 << 20, 2048, (1 << 20) + 2048) == -2
     assert rr(fake + 4, 4, 1 << 20, 2048, 1 << 21) == -4
     assert rr(fake, 4, 1 << 20, 2048, None) == -1
+    # weight formats: unknown format, MXFP4 with fp32 scales / group 64 / a zero point, missing zero point,
+    # group not a multiple of the 16-byte slice, padded_k past 8192, misaligned codes, K > padded_k
+    gq = lambda fmt, zero, s32, pk, g, codes=fake, M=1, K=128: lib.lemoq_gemv_q(  # noqa: E731
+        fake, M, K, codes, fmt, fake, zero, s32, 64, pk, g, fake, 1, None)
+    assert gq(5, None, 0, 128, 128) == -3
+    assert gq(4, None, 1, 128, 32) == -3 and gq(4, None, 0, 128, 64) == -3 and gq(4, fake, 0, 128, 32) == -3
+    assert gq(1, None, 0, 128, 128) == -1 and gq(3, None, 0, 128, 128) == -1
+    assert gq(2, None, 0, 128, 16) == -3 and gq(0, None, 0, 128, 8) == -3
+    assert gq(2, None, 0, 16384, 128) == -3
+    assert gq(2, None, 0, 128, 128, codes=fake + 8) == -4
+    assert gq(0, None, 0, 128, 128, K=256) == -2 and gq(0, None, 0, 128, 128, M=0) == -2
+    assert gq(4, None, 0, 128, 32, M=70000) == -2
+    assert lib.lemoq_dequant_q(fake, 2, fake, None, 0, 64, 128, 128, fake, 100, 129, 0, None) == -2  # k_out > padded
+    assert lib.lemoq_dequant_q(fake, 2, fake, None, 0, 64, 128, 128, fake, 100, 120, 0, None) == -2  # ld < k_out
+    assert lib.lemoq_rtn_quantize(fake, 4, 130, 7, 4, 1, fake, None, None, None, None, None) == -2   # odd group at 4 bits
+    assert lib.lemoq_rtn_quantize(fake, 4, 130, 128, 6, 1, fake, None, None, None, None, None) == -3
+    assert lib.lemoq_mxfp4_quantize(fake, 4, 0, fake, fake, None) == -2
+    assert lib.lemoq_fake_quant_rows(fake, 4, 0, fake, None) == -2
     with pytest.raises(ValueError):
         _hip.call("lemoq_gemv_w8", None, 1, 16, None, None, 16, 16, 16, None, 1, None)
 

@@ -1,0 +1,273 @@
+"""GPU parity of the weight formats beyond 8-bit symmetric (8-bit asymmetric,
+4-bit symmetric / asymmetric, MXFP4) and of the w8a8 activation fake-quant,
+through the C-ABI wrappers.
+
+- Quantisers (``lemoq_rtn_quantize``, ``lemoq_mxfp4_quantize``): codes,
+  scales and zero points bit-exact to the oracle (``oracle.quant``), on the
+  reference's case grid (``tests/test_quant_oracle.py:104-146``,
+  ``tests/test_mxfp4.py``) and edge values (all-zero, largest and smallest
+  normal weights, amax just below powers of two).
+- Dequantisation (``lemoq_dequant_q``): fp32 weights bit-exact to the
+  oracle's ``dequant_tile`` / ``mxfp4_dequantize`` (every E2M1 code at several
+  scales, the -0 of code 8 included), fp16 weights their single rounding.
+- Decode GEMV (``lemoq_gemv_q`` through ``dequant_gemm_fused``): the
+  reference's K1 gate (``tests/test_kernel_parity.py:134-227``,
+  ``tests/test_mxfp4_gpu.py``): within atol / rtol 1e-3 of the separate
+  reference ``x @ dequant(w).T`` in fp32, and the A6 conjunction against an
+  fp64 oracle (the kernel's error at most 1.5x the separate reference's).
+  Cases: m = 1 and 4, K = 2048 / 256 / 500 / 50, groups 32-128, fp16 and fp32
+  scales.
+- ``QuantLinear`` per scheme, one token (fused arm) and several (separate arm).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import randn
+from oracle import quant as oq
+
+pytestmark = pytest.mark.gpu
+
+TOL = dict(atol=1e-3, rtol=1e-3)
+
+
+def _bits16(a) -> np.ndarray:
+    return np.asarray(a).astype(np.float16).view(np.uint16)
+
+
+def _rtn_vs_oracle(w: torch.Tensor, bits: int, group: int, sym: bool, dev):
+    from lemoq.quant.rtn import quantize_rtn
+
+    got = quantize_rtn(w.to(dev), bits=bits, group_size=group, symmetric=sym)
+    ref = oq.rtn_quantize(w.numpy(), bits, group, sym)
+    codes = got["codes_padded"].cpu().numpy().astype(np.int32)
+    assert np.array_equal(codes, ref["codes_padded"]), "codes"
+    assert np.array_equal(got["scale"].cpu().numpy(), ref["scale"]), "scale"
+    assert np.array_equal(got["zero"].cpu().numpy(), ref["zero"]), "zero"
+    assert np.array_equal(got["scale_f16"].cpu().numpy().view(np.uint16), _bits16(ref["scale"])), "scale fp16"
+    assert np.array_equal(got["zero_f16"].cpu().numpy().view(np.uint16), _bits16(ref["zero"])), "zero fp16"
+    if bits == 4:
+        assert np.array_equal(got["packed"].cpu().numpy(), oq.pack_4bit(ref["codes_padded"])), "packed bytes"
+    return got, ref
+
+
+RTN_CASES = [(4, 128, True), (4, 32, True), (8, 64, True), (8, 128, True), (4, 128, False), (4, 64, False),
+             (8, 128, False), (8, 32, False)]
+
+
+@pytest.mark.parametrize("bits,group,sym", RTN_CASES)
+@pytest.mark.parametrize("shape,seed", [((64, 2048), 0), ((64, 500), 1), ((3, 130), 7), ((1, 1), 2026)])
+def test_rtn_quantize_bit_exact(bits, group, sym, shape, seed, dev):
+    print("case: rtn bits=%d group=%d sym=%s shape=%s" % (bits, group, sym, shape), flush=True)
+    _rtn_vs_oracle(randn(*shape, seed=seed, std=0.05), bits, group, sym, dev)
+
+
+@pytest.mark.parametrize("fill", [0.0, float(np.finfo(np.float32).max), float(np.finfo(np.float32).tiny)],
+                         ids=["zeros", "finfo_max", "finfo_tiny"])
+@pytest.mark.parametrize("bits,group,sym", [(4, 128, True), (8, 32, True), (4, 128, False), (8, 32, False)])
+def test_rtn_quantize_edge_values(fill, bits, group, sym, dev):
+    print("case: rtn edge fill=%g bits=%d sym=%s" % (fill, bits, sym), flush=True)
+    _rtn_vs_oracle(torch.full((16, 40), fill), bits, group, sym, dev)
+
+
+def _mx_edge_rows() -> np.ndarray:
+    rows = []
+    for k in range(-20, 21):
+        a = np.float32(2.0 ** k)
+        for _ in range(5):
+            a = np.nextafter(a, np.float32(0))
+            blk = np.zeros(32, np.float32)
+            blk[3], blk[7] = a, -a * np.float32(0.3)
+            rows.append(blk)
+    ties = np.zeros(32, np.float32)
+    ties[:8] = [0.25, -0.25, 1.25, 2.5, -3.5, 5.0, 0.75, -1.75]
+    rows.append(ties)
+    return np.stack(rows)
+
+
+@pytest.mark.parametrize("which", ["random", "wide", "padded", "edges", "zeros", "tiny"])
+def test_mxfp4_quantize_bit_exact(which, dev):
+    from lemoq.quant.mxfp4 import quantize_mxfp4
+
+    print("case: mxfp4 quantize %s" % which, flush=True)
+    w = {
+        "random": lambda: randn(64, 256, seed=0, std=0.3).numpy(),
+        "wide": lambda: randn(512, 2048, seed=3, std=0.05).numpy(),
+        "padded": lambda: randn(4, 50, seed=3, std=0.2).numpy(),
+        "edges": _mx_edge_rows,
+        "zeros": lambda: np.zeros((2, 70), np.float32),
+        "tiny": lambda: (randn(8, 64, seed=5, std=1.0) * 1e-30).numpy(),
+    }[which]()
+    got = quantize_mxfp4(torch.from_numpy(w).to(dev))
+    ref = oq.mxfp4_quantize(w)
+    assert got["padded_in"] == ref["padded_in"]
+    assert np.array_equal(got["scales"].cpu().numpy(), ref["scales"]), "scale bytes"
+    assert np.array_equal(got["codes_packed"].cpu().numpy(), ref["codes_packed"]), "codes"
+
+
+@pytest.mark.parametrize("bits,group,sym", RTN_CASES)
+@pytest.mark.parametrize("scale_dtype", [torch.float16, torch.float32])
+def test_dequant_bit_exact(bits, group, sym, scale_dtype, dev):
+    from lemoq.quant.formats import dequantize, format_id
+
+    print("case: dequant bits=%d group=%d sym=%s scale %s" % (bits, group, sym, scale_dtype), flush=True)
+    w = randn(40, 300, seed=bits * group, std=0.05)
+    q = oq.rtn_quantize(w.numpy(), bits, group, sym)
+    scale = torch.from_numpy(q["scale"]).to(scale_dtype)
+    zero = torch.from_numpy(q["zero"]).to(scale_dtype)
+    codes = q["codes_padded"]
+    packed = torch.from_numpy(oq.pack_4bit(codes) if bits == 4 else
+                              codes.astype(np.int8 if sym else np.uint8))
+    ref = oq.dequant_tile(codes, scale.float().numpy(), zero.float().numpy(), group, sym, in_features=300)
+    fmt = format_id(bits, sym)
+    got32 = dequantize(packed.to(dev), scale.to(dev), None if sym else zero.to(dev), fmt=fmt, group_size=group,
+                       k_out=300, dtype=torch.float32).cpu().numpy()
+    assert np.array_equal(got32.view(np.uint32), ref.view(np.uint32))
+    got16 = dequantize(packed.to(dev), scale.to(dev), None if sym else zero.to(dev), fmt=fmt, group_size=group,
+                       k_out=300, dtype=torch.float16).cpu().numpy()
+    assert np.array_equal(got16.view(np.uint16), _bits16(ref))
+
+
+def test_mxfp4_dequant_every_code_and_scale(dev):
+    """All 16 E2M1 codes (code 8 is -0) at scale bytes 0, 1, 100, 126, 127, 128,
+    200, 254: fp32 bit-exact to the oracle, fp16 its one rounding."""
+    from lemoq.quant.mxfp4 import dequantize_packed
+
+    print("case: mxfp4 dequant table", flush=True)
+    codes = np.tile(np.arange(16, dtype=np.uint8), (8, 4))  # 8 rows x 64 codes
+    scales = np.repeat(np.array([[0], [1], [100], [126], [127], [128], [200], [254]], np.uint8), 2, axis=1)
+    packed = oq.pack_4bit(codes)
+    ref = oq.mxfp4_dequantize(packed, scales, 64)
+    got = dequantize_packed(torch.from_numpy(packed).to(dev), torch.from_numpy(scales).to(dev), 64,
+                            dtype=torch.float32).cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    got16 = dequantize_packed(torch.from_numpy(packed).to(dev), torch.from_numpy(scales).to(dev), 64,
+                              dtype=torch.float16).cpu().numpy()
+    assert np.array_equal(got16.view(np.uint16), _bits16(ref))
+
+
+def _gemv_case(m, k, n, bits, group, sym, *, scale_dtype=torch.float16, mxfp4=False, seed=0, dev="cuda"):
+    """The reference's K1 gate for one case; returns (err_kernel, err_ref)."""
+    from lemoq.kernels.dequant_gemm import dequant_gemm_fused
+
+    g = torch.Generator().manual_seed(seed)
+    x = (torch.randn(m, k, generator=g) * 0.5).to(torch.float16)
+    w = torch.randn(n, k, generator=g) * 0.05
+    if mxfp4:
+        q = oq.mxfp4_quantize(w.numpy())
+        packed = torch.from_numpy(q["codes_packed"])
+        scale = torch.from_numpy(q["scales"])
+        zero = None
+        w_ref = torch.from_numpy(oq.mxfp4_dequantize(q["codes_packed"], q["scales"], k))
+        w64 = w_ref.double()
+        group = 32
+    else:
+        q = oq.rtn_quantize(w.numpy(), bits, group, sym)
+        codes = q["codes_padded"]
+        packed = torch.from_numpy(oq.pack_4bit(codes) if bits == 4 else codes.astype(np.int8 if sym else np.uint8))
+        scale = torch.from_numpy(q["scale"]).to(scale_dtype)
+        zero = torch.from_numpy(q["zero"]).to(scale_dtype)
+        w_ref = torch.from_numpy(oq.dequant_tile(codes, scale.float().numpy(), zero.float().numpy(), group, sym,
+                                                 in_features=k))
+        w64 = torch.from_numpy(oq.dequant_tile(codes, q["scale"], q["zero"], group, sym, in_features=k)).double()
+    ref = x.float() @ w_ref.T  # the separate reference (fp32)
+    got = dequant_gemm_fused(x.to(dev), packed.to(dev), scale.to(dev),
+                             None if (sym or mxfp4) else zero.to(dev), group_size=group,
+                             bits=4 if mxfp4 else bits, symmetric=sym, out_dtype=torch.float32,
+                             mxfp4=mxfp4).cpu()
+    assert torch.allclose(got, ref, **TOL), float((got - ref).abs().max())
+    oracle = x.double() @ w64.T
+    err_ref = float((ref.double() - oracle).abs().max())
+    err_got = float((got.double() - oracle).abs().max())
+    assert err_got <= 1.5 * err_ref + 1e-9, (err_got, err_ref)
+    return err_got, err_ref
+
+
+GEMV_CASES = [
+    # (m, k, n, bits, group, sym, scale dtype): the reference's K1 grid plus the asymmetric formats
+    (1, 2048, 2048, 8, 128, True, torch.float16), (1, 2048, 2048, 4, 128, True, torch.float16),
+    (4, 256, 512, 8, 128, True, torch.float16), (4, 256, 512, 4, 128, True, torch.float16),
+    (1, 512, 256, 8, 128, True, torch.float32), (1, 512, 256, 4, 128, True, torch.float32),
+    (1, 500, 256, 8, 128, True, torch.float16), (1, 500, 256, 4, 128, True, torch.float16),
+    (1, 1024, 512, 8, 64, True, torch.float16), (1, 1024, 512, 4, 32, True, torch.float16),
+    (1, 2048, 2048, 8, 128, False, torch.float16), (1, 2048, 2048, 4, 128, False, torch.float16),
+    (4, 256, 512, 8, 128, False, torch.float16), (4, 256, 512, 4, 64, False, torch.float16),
+    (1, 500, 256, 4, 128, False, torch.float32), (1, 8192, 64, 4, 128, True, torch.float16),
+    (1, 8192, 64, 8, 128, False, torch.float16), (3, 4096, 300, 4, 128, False, torch.float16),
+]
+
+
+@pytest.mark.parametrize("m,k,n,bits,group,sym,sd", GEMV_CASES)
+def test_gemv_formats_k1_gate(m, k, n, bits, group, sym, sd, dev):
+    print("case: gemv m=%d k=%d n=%d bits=%d group=%d sym=%s scale %s" % (m, k, n, bits, group, sym, sd),
+          flush=True)
+    _gemv_case(m, k, n, bits, group, sym, scale_dtype=sd, seed=m * k + n + bits, dev=dev)
+
+
+@pytest.mark.parametrize("m,k,n,seed", [(1, 256, 128, 0), (4, 256, 128, 1), (1, 50, 128, 2), (1, 2048, 512, 3),
+                                        (1, 2048, 2048, 7), (2, 8192, 96, 9)])
+def test_gemv_mxfp4_k1_gate(m, k, n, seed, dev):
+    print("case: gemv mxfp4 m=%d k=%d n=%d" % (m, k, n), flush=True)
+    _gemv_case(m, k, n, 4, 32, True, mxfp4=True, seed=seed, dev=dev)
+
+
+def test_gemv_w8_sym_fp32_scale_equals_fp16_path_on_exact_scales(dev):
+    """The generic kernel (fp32 scales) and the decode step's w8 GEMV (fp16
+    scales) on the same fp16-representable scales: equal up to the fp32 order."""
+    from lemoq.kernels.dequant_gemm import dequant_gemm_fused
+
+    print("case: w8 fp32-scale vs fp16-scale paths", flush=True)
+    x = randn(1, 2048, seed=1, std=0.5).to(torch.float16).to(dev)
+    q = oq.rtn_quantize(randn(1024, 2048, seed=2, std=0.05).numpy(), 8, 128, True)
+    codes = torch.from_numpy(q["codes_padded"].astype(np.int8)).to(dev)
+    s16 = torch.from_numpy(q["scale"]).half().to(dev)
+    a = dequant_gemm_fused(x, codes, s16, group_size=128, bits=8)
+    b = dequant_gemm_fused(x, codes, s16.float(), group_size=128, bits=8)
+    assert torch.allclose(a, b, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("scheme,sym", [("w4a16", True), ("w4a16", False), ("w8a16", False), ("mxfp4", True),
+                                        ("w8a8", True), ("w8a16", True)])
+def test_quant_linear_schemes(scheme, sym, dev):
+    """One token through the fused arm and five through the separate arm, each
+    against its reference: fused = x @ dequant(w).T in fp32 (K1 tolerance),
+    separate = fp16(x @ fp16(dequant(w)).T) (fp16 GEMM tolerance); w8a8 also
+    checks the per-token fake-quant bit for bit."""
+    from lemoq.quant.linear import QuantLinear
+
+    print("case: QuantLinear %s sym=%s" % (scheme, sym), flush=True)
+    w = randn(384, 512, seed=31, std=0.05)
+    bias = randn(384, seed=32, std=0.1).to(torch.float16)
+    ql = QuantLinear(w.to(dev), group_size=128, bias=bias.to(dev), scheme=scheme, symmetric=sym)
+    if scheme == "mxfp4":
+        assert ql.group_size == 32 and ql.scale.dtype == torch.uint8 and ql.zero is None
+        q = oq.mxfp4_quantize(w.numpy())
+        assert np.array_equal(ql.packed.cpu().numpy(), q["codes_packed"])
+        wdq = oq.mxfp4_dequantize(q["codes_packed"], q["scales"], 512)
+    else:
+        bits = 4 if scheme == "w4a16" else 8
+        q = oq.rtn_quantize(w.numpy(), bits, 128, sym)
+        wdq = oq.dequant_tile(q["codes_padded"], q["scale"].astype(np.float16).astype(np.float32),
+                              q["zero"].astype(np.float16).astype(np.float32), 128, sym, in_features=512)
+    wdq_t = torch.from_numpy(wdq)
+    assert np.array_equal(ql.dequantized_weight().cpu().numpy().view(np.uint32), wdq.view(np.uint32))
+    for T in (1, 5):
+        x = randn(T, 512, seed=33 + T, std=0.5).to(torch.float16)
+        xin = x
+        if scheme == "w8a8":  # per-token int8 fake quant (src/lemoq/quant/linear.py:398-414)
+            xf = x.float()
+            amax = xf.abs().amax(-1, keepdim=True)
+            s = torch.where(amax > 0, amax / 127.0, torch.ones_like(amax))
+            xin = ((xf / s).round().clamp(-128, 127) * s).to(torch.float16)
+            got_fq = ql._fake_quant_activation(x.to(dev)).cpu()
+            assert torch.equal(got_fq.view(torch.int16), xin.view(torch.int16))
+        y = ql(x.to(dev)).cpu()
+        if T == 1:
+            ref = (xin.float() @ wdq_t.T + bias.float())
+            assert torch.allclose(y.float(), ref, atol=2e-3, rtol=2e-3), float((y.float() - ref).abs().max())
+        else:
+            ref = (xin.double() @ wdq_t.half().double().T).half().float() + bias.float()
+            assert torch.allclose(y.float(), ref, atol=3e-3, rtol=3e-3), float((y.float() - ref).abs().max())
