@@ -252,6 +252,21 @@ int lemoq_moe_down_w8(const uint16_t* act, const int8_t* codes,
                       int64_t hidden, int64_t ffn, int64_t group,
                       const uint16_t* residual, uint16_t* out, void* stream);
 
+/* A4/A5 on 4-bit symmetric experts (the BITS=4 branch of the same kernels,
+ * src/lemoq/kernels/_grouped_triton.py:235-398, and of
+ * quantize_fused_experts(bits=4), src/lemoq/kernels/moe_grouped_quant.py:191-244).
+ * codes are int4 (-8..7) packed two per byte, the even column in the low
+ * nibble: gate/up (E, 2F, H/2), down (E, H, F/2); scales fp16 per group of
+ * `group` codes.  Arguments, outputs and numerics as the 8-bit entry points;
+ * hidden and ffn <= 8192, multiples of 32 and of group, group % 32 == 0. */
+int lemoq_moe_gate_up_w4(const uint16_t* x, const uint8_t* codes, const uint16_t* scale,
+                         const int64_t* ids, int64_t top_k, int64_t num_experts, int64_t ffn,
+                         int64_t hidden, int64_t group, uint16_t* act, void* stream);
+int lemoq_moe_down_w4(const uint16_t* act, const uint8_t* codes, const uint16_t* scale,
+                      const int64_t* ids, const uint16_t* top_w, int64_t top_k,
+                      int64_t num_experts, int64_t hidden, int64_t ffn, int64_t group,
+                      const uint16_t* residual, uint16_t* out, void* stream);
+
 /* ---------------------------------------------------------------------------
  * A14/A15 — split-KV decode attention (flash-decoding), batch 1, q_len 1.
  * Partials: m, l (heads, num_splits) fp32 and acc (heads, num_splits, D) fp32;

@@ -1,16 +1,17 @@
-"""Grouped MoE decode on w8 weights: gate/up + SiLU and down + weighted sum.
+"""Grouped MoE decode on w8 (and 4-bit) weights: gate/up + SiLU and down + weighted sum.
 
 Operator surface of the reference's ``src/lemoq/kernels/moe_grouped_quant.py``:
 
 * ``QuantFusedExperts`` (``:72-188``) — packed codes + per-group fp16 scales,
   ``packed_gate_up`` (E, 2F, H) int8 with gate rows [0, F) and up rows [F, 2F),
   ``packed_down`` (E, H, F) int8, ``scale_gate_up`` (E, 2F, H/g),
-  ``scale_down`` (E, H, F/g), groups along the last (K) dimension.
-* ``quantize_fused_experts`` (``:191-244``) — RTN w8 of the fused fp weights
-  (on the device, ``lemoq_rtn_quantize_w8``).
+  ``scale_down`` (E, H, F/g), groups along the last (K) dimension; at
+  ``bits=4`` the codes are int4 packed two per byte (uint8, last dim halved).
+* ``quantize_fused_experts`` (``:191-244``) — RTN w8 or w4 of the fused fp
+  weights (on the device, ``lemoq_rtn_quantize``).
 * ``grouped_moe_forward_quant`` (``:411-559``) — ``(H,)`` token + ``(K,)`` expert
   ids + ``(K,)`` routing weights -> ``(H,)``; two HIP launches
-  (``lemoq_moe_gate_up_w8``, ``lemoq_moe_down_w8``), the reference's SPLIT_K
+  (``lemoq_moe_gate_up_w8``, ``lemoq_moe_down_w8``; ``_w4`` at 4 bits), the reference's SPLIT_K
   reduction kernel is folded into the down kernel's fixed-order epilogue.
 * ``static_moe_forward_grouped_quant`` (``:562-601``) — the MoE block glue with
   ``_route``.
@@ -86,8 +87,40 @@ class QuantFusedExperts:
         expert reads)."""
         return sum(getattr(self, f).numel() * getattr(self, f).element_size() for f in self._TENSORS)
 
+    def _dequant_rows(self, codes: Any, scale: Any, rows: int, width: int, dtype: Any) -> Any:
+        """(rows, width) weights of stacked packed rows, ``code * scale`` in fp32
+        (``lemoq_dequant_q``), rounded once to ``dtype`` when given
+        (``src/lemoq/kernels/moe_grouped_quant.py:145-157``)."""
+        import torch  # noqa: PLC0415
+
+        from lemoq.quant.formats import QFMT_W4, QFMT_W8, dequantize  # noqa: PLC0415
+
+        out = dtype if dtype in (torch.float16, torch.float32) else torch.float32
+        w = dequantize(codes.reshape(rows, -1), scale.reshape(rows, -1), None,
+                       fmt=QFMT_W8 if int(self.bits) == 8 else QFMT_W4, group_size=int(self.group_size),
+                       k_out=width, dtype=out)
+        return w if dtype is None or dtype == out else w.to(dtype)
+
+    def dequant_gate_up(self, dtype: Any = None) -> Any:
+        e, rows = int(self.packed_gate_up.shape[0]), int(self.packed_gate_up.shape[1])
+        return self._dequant_rows(self.packed_gate_up, self.scale_gate_up, e * rows, self.hidden,
+                                  dtype).reshape(e, rows, self.hidden)
+
+    def dequant_down(self, dtype: Any = None) -> Any:
+        e, rows = int(self.packed_down.shape[0]), int(self.packed_down.shape[1])
+        return self._dequant_rows(self.packed_down, self.scale_down, e * rows, self.ffn, dtype).reshape(
+            e, rows, self.ffn)
+
+    def dequant_gate_up_expert(self, index: int, dtype: Any = None) -> Any:
+        """One expert's (2F, H) gate/up weight (without dequantising the others)."""
+        return self._dequant_rows(self.packed_gate_up[index], self.scale_gate_up[index], 2 * self.ffn, self.hidden,
+                                  dtype)
+
+    def dequant_down_expert(self, index: int, dtype: Any = None) -> Any:
+        return self._dequant_rows(self.packed_down[index], self.scale_down[index], self.hidden, self.ffn, dtype)
+
     def to(self, device: Any = None, dtype: Any = None) -> "QuantFusedExperts":
-        """Copy to ``device`` (contiguous).  Codes stay int8 and scales fp16, so a
+        """Copy to ``device`` (contiguous).  Codes keep their storage type and scales fp16, so a
         dtype is refused, also when passed positionally as ``to(torch.float32)``:
         converting would undo the quantisation."""
         import torch  # noqa: PLC0415
@@ -104,15 +137,16 @@ class QuantFusedExperts:
 
 
 def quantize_fused_experts(fused: Any, *, bits: int = 8, group_size: int = 128) -> QuantFusedExperts:
-    """RTN-quantize ``fused.gate_up`` (E, 2F, H) and ``fused.down`` (E, H, F) on the device."""
+    """RTN-quantize ``fused.gate_up`` (E, 2F, H) and ``fused.down`` (E, H, F) on the
+    device, symmetric, 8-bit (int8 codes) or 4-bit (int4 codes packed two per byte)."""
     from lemoq.quant import rtn  # noqa: PLC0415
 
     if bits not in (4, 8):
         raise NotImplementedError("grouped quantization implements 4/8-bit, got %r" % (bits,))
-    if bits != 8:
-        raise NotImplementedError("the HIP build implements 8-bit experts only")
     if group_size <= 0:
         raise ValueError("group_size must be > 0")
+    if bits == 4 and group_size % 2 != 0:
+        raise ValueError("4-bit packing needs an even group_size, got %d" % group_size)
     gate_up, down = fused.gate_up, fused.down
     hidden = int(gate_up.shape[2])
     ffn = int(down.shape[2])
@@ -122,16 +156,17 @@ def quantize_fused_experts(fused: Any, *, bits: int = 8, group_size: int = 128) 
                 "%s=%d is not divisible by group_size=%d (the grouped path does not pad)"
                 % (name, dim, group_size)
             )
-    q_gu = rtn.quantize_rtn(gate_up.reshape(-1, hidden), bits=8, group_size=group_size)
-    q_d = rtn.quantize_rtn(down.reshape(-1, ffn), bits=8, group_size=group_size)
+    q_gu = rtn.quantize_rtn(gate_up.reshape(-1, hidden), bits=bits, group_size=group_size)
+    q_d = rtn.quantize_rtn(down.reshape(-1, ffn), bits=bits, group_size=group_size)
     e, rows_gu = int(gate_up.shape[0]), int(gate_up.shape[1])
     rows_d = int(down.shape[1])
+    per = 1 if bits == 8 else 2  # codes per stored byte
     return QuantFusedExperts(
-        packed_gate_up=q_gu["codes_padded"].reshape(e, rows_gu, hidden).contiguous(),
+        packed_gate_up=q_gu["packed"].reshape(e, rows_gu, hidden // per).contiguous(),
         scale_gate_up=q_gu["scale_f16"].reshape(e, rows_gu, hidden // group_size).contiguous(),
-        packed_down=q_d["codes_padded"].reshape(e, rows_d, ffn).contiguous(),
+        packed_down=q_d["packed"].reshape(e, rows_d, ffn // per).contiguous(),
         scale_down=q_d["scale_f16"].reshape(e, rows_d, ffn // group_size).contiguous(),
-        bits=8,
+        bits=int(bits),
         group_size=int(group_size),
     )
 
@@ -161,13 +196,17 @@ def quant_launch_plan(
 
     Pure host arithmetic (testable without a GPU), as the reference's
     ``quant_launch_plan`` (``moe_grouped_quant.py:289-379``).  Checks, always:
-    bits == 8, contiguous tensors, hidden/ffn divisible by group_size; with
-    ``for_kernel``: group_size % 16 == 0 and hidden, ffn <= 8192 (a lane's
-    16 codes never straddle a group; one row fits the register tiling).
+    bits 4 or 8 with codes stored as int8 / packed uint8, contiguous tensors,
+    hidden/ffn divisible by group_size; with ``for_kernel``: group_size a
+    multiple of a lane's slice (16 codes at 8 bits, 32 at 4) and hidden, ffn
+    <= 8192 (a slice never straddles a group; one row fits the register tiling).
     """
+    import torch  # noqa: PLC0415
+
     del config
-    if int(q.bits) != 8:
-        raise NotImplementedError("grouped path implements 8-bit only, got %d" % int(q.bits))
+    bits = int(q.bits)
+    if bits not in (4, 8):
+        raise NotImplementedError("grouped path implements 4/8-bit, got %d" % bits)
     if top_k <= 0:
         raise ValueError("top_k must be > 0")
     e = int(q.packed_gate_up.shape[0])
@@ -183,10 +222,14 @@ def quant_launch_plan(
             raise ValueError("%s must be contiguous" % name)
         if int(tensor.numel()) >= _MAX_OFFSET:
             raise ValueError("%s is too large" % name)
-    if tuple(q.packed_down.shape) != (e, hidden, ffn):
+    per = 8 // bits  # codes per stored byte
+    want = torch.int8 if bits == 8 else torch.uint8
+    if q.packed_gate_up.dtype != want or q.packed_down.dtype != want:
+        raise ValueError("%d-bit codes must be %s" % (bits, want))
+    if tuple(q.packed_down.shape) != (e, hidden, ffn // per):
         raise ValueError(
-            "packed_down must be (E=%d, H=%d, F=%d), got %r"
-            % (e, hidden, ffn, tuple(q.packed_down.shape))
+            "packed_down must be (E=%d, H=%d, F/%d=%d), got %r"
+            % (e, hidden, per, ffn // per, tuple(q.packed_down.shape))
         )
     group = int(q.group_size)
     for name, dim in (("hidden", hidden), ("ffn", ffn)):
@@ -212,13 +255,17 @@ def quant_launch_plan(
             "out_shape": (hidden,),
         },
         "kernel_count": 2,
-        "quant": {"bits": 8, "group_size": group, "for_kernel": bool(for_kernel)},
+        "quant": {"bits": bits, "group_size": group, "for_kernel": bool(for_kernel)},
+        "kernels": ("lemoq_moe_gate_up_w8", "lemoq_moe_down_w8") if bits == 8 else
+                   ("lemoq_moe_gate_up_w4", "lemoq_moe_down_w4"),
     }
     if for_kernel:
-        if group % 16 != 0:
-            raise ValueError("group_size=%d must be a multiple of 16 for the HIP kernels" % group)
-        if hidden > 8192 or ffn > 8192 or hidden % 16 or ffn % 16:
-            raise NotImplementedError("hidden and ffn must be multiples of 16 and <= 8192")
+        step = 16 if bits == 8 else 32  # codes per 16-byte lane slice
+        if group % step != 0:
+            raise ValueError("group_size=%d must be a multiple of %d for the %d-bit HIP kernels"
+                             % (group, step, bits))
+        if hidden > 8192 or ffn > 8192 or hidden % step or ffn % step:
+            raise NotImplementedError("hidden and ffn must be multiples of %d and <= 8192" % step)
         if int(top_k) > 64:
             raise NotImplementedError("top_k <= 64 is supported")
     return plan
@@ -294,7 +341,7 @@ def grouped_moe_forward_quant(
     act = torch.empty(plan["gate_up_act"]["act_shape"], dtype=torch.float16, device=dev)
     out = torch.empty((hidden,), dtype=torch.float16, device=dev)
     _hip.call(
-        "lemoq_moe_gate_up_w8",
+        plan["kernels"][0],
         _hip.ptr(xf),
         _hip.ptr(q.packed_gate_up),
         _hip.ptr(q.scale_gate_up),
@@ -308,7 +355,7 @@ def grouped_moe_forward_quant(
         st,
     )
     _hip.call(
-        "lemoq_moe_down_w8",
+        plan["kernels"][1],
         _hip.ptr(act),
         _hip.ptr(q.packed_down),
         _hip.ptr(q.scale_down),
@@ -338,7 +385,7 @@ def grouped_gate_up_act_quant(x: Any, q: QuantFusedExperts, ids: Any) -> Any:
     _hip.require_rocm(xf, idx, q.packed_gate_up, q.scale_gate_up, what="grouped_gate_up_act_quant")
     act = torch.empty(plan["gate_up_act"]["act_shape"], dtype=torch.float16, device=xf.device)
     _hip.call(
-        "lemoq_moe_gate_up_w8",
+        plan["kernels"][0],
         _hip.ptr(xf),
         _hip.ptr(q.packed_gate_up),
         _hip.ptr(q.scale_gate_up),

@@ -18,6 +18,11 @@ through the C-ABI wrappers.
   Cases: m = 1 and 4, K = 2048 / 256 / 500 / 50, groups 32-128, fp16 and fp32
   scales.
 - ``QuantLinear`` per scheme, one token (fused arm) and several (separate arm).
+- 4-bit grouped MoE (``lemoq_moe_gate_up_w4`` / ``lemoq_moe_down_w4`` through
+  ``grouped_moe_forward_quant``): ``quantize_fused_experts(bits=4)`` bit-exact
+  to the oracle's RTN and packing, the output against the oracle's grouped
+  MoE on the unpacked codes and the fp64 closed form, the residual add and an
+  out-of-range expert id.
 """
 
 from __future__ import annotations
@@ -271,3 +276,88 @@ def test_quant_linear_schemes(scheme, sym, dev):
         else:
             ref = (xin.double() @ wdq_t.half().double().T).half().float() + bias.float()
             assert torch.allclose(y.float(), ref, atol=3e-3, rtol=3e-3), float((y.float() - ref).abs().max())
+
+
+# ---------------------------------------------------------------------------
+# 4-bit grouped MoE (grouped_moe_forward_quant on QuantFusedExperts(bits=4))
+# ---------------------------------------------------------------------------
+def _q4_experts(E, F, H, group, seed, dev):
+    """fp experts quantised on the device with bits=4; checked bit for bit
+    against the oracle's 4-bit RTN and packing, row block by row block."""
+    from lemoq.kernels.moe_grouped_quant import FusedExperts, quantize_fused_experts
+
+    gu = randn(E, 2 * F, H, seed=seed, std=0.02)
+    dn = randn(E, H, F, seed=seed + 1, std=0.02)
+    q = quantize_fused_experts(FusedExperts(gu.to(dev), dn.to(dev)), bits=4, group_size=group)
+    assert q.bits == 4 and q.packed_gate_up.dtype == torch.uint8
+    assert tuple(q.packed_gate_up.shape) == (E, 2 * F, H // 2) and tuple(q.packed_down.shape) == (E, H, F // 2)
+    out = []
+    for w, packed, scale in ((gu, q.packed_gate_up, q.scale_gate_up), (dn, q.packed_down, q.scale_down)):
+        ref = oq.rtn_quantize(w.reshape(-1, w.shape[-1]).numpy(), 4, group, True)
+        assert np.array_equal(packed.cpu().reshape(-1, w.shape[-1] // 2).numpy(), oq.pack_4bit(ref["codes_padded"]))
+        assert np.array_equal(scale.cpu().reshape(-1, w.shape[-1] // group).numpy().view(np.uint16),
+                              _bits16(ref["scale"]))
+        out.append(torch.from_numpy(ref["codes_padded"].astype(np.int8)).reshape(w.shape))
+        out.append(scale.cpu())
+    return q, out  # out: int8 codes (-8..7) and fp16 scales of gate/up and down
+
+
+@pytest.mark.parametrize("E,F,H,K,group", [(64, 1024, 2048, 8, 128), (8, 256, 512, 2, 128), (4, 256, 512, 2, 32),
+                                           (16, 128, 1024, 4, 64)])
+def test_grouped_moe_w4_vs_oracle_and_fp64(E, F, H, K, group, dev):
+    """The reference's quantised grouped gate (``tests/test_kernel_parity.py:230-282``,
+    8- and 4-bit): the oracle's grouped MoE on the unpacked int4 codes (same
+    arithmetic as at 8 bits) and the fp64 closed form with the fp16 act
+    rounding point."""
+    from helpers import assert_close
+    from lemoq.kernels.moe_grouped_quant import grouped_moe_forward_quant
+    from oracle import ops
+
+    print("case: grouped moe w4 E=%d F=%d H=%d K=%d group=%d" % (E, F, H, K, group), flush=True)
+    q, (gc, gs, dc, ds) = _q4_experts(E, F, H, group, seed=E + F + group, dev=dev)
+    x = randn(H, seed=3).to(torch.float16)
+    ids = torch.randperm(E, generator=torch.Generator().manual_seed(4))[:K]
+    w = torch.softmax(randn(K, seed=5), 0).to(torch.float16)
+    got = grouped_moe_forward_quant(x.to(dev), q, ids.to(dev), w.to(dev)).cpu()
+    ref, act_ref = ops.grouped_moe_w8(x, gc, gs, dc, ds, group, ids, w)
+    gu64 = torch.stack([ops.dequant_w8(gc[e], gs[e], group) for e in ids.tolist()]).double()
+    g = gu64[:, :F] @ x.double()
+    u = gu64[:, F:] @ x.double()
+    act64 = (g * torch.sigmoid(g) * u).to(torch.float16).double()
+    dn64 = torch.stack([ops.dequant_w8(dc[e], ds[e], group) for e in ids.tolist()]).double()
+    out64 = ((dn64 @ act64.unsqueeze(-1)).squeeze(-1) * w.double().unsqueeze(1)).sum(0)
+    assert_close(got, out64, what="moe w4 vs fp64")
+    assert_close(got, ref, what="moe w4 vs oracle")
+
+
+def test_grouped_moe_w4_reference_case_residual_and_invalid_id(dev):
+    """E=4, F=256, H=512, ids (0, 2), weights (0.7, 0.3) as the reference's gate;
+    the residual add keeps the fp16 rounding point; an out-of-range expert id
+    contributes nothing."""
+    from lemoq.kernels.moe_grouped_quant import grouped_moe_forward_quant
+
+    print("case: grouped moe w4 reference case", flush=True)
+    q, _ = _q4_experts(4, 256, 512, 128, seed=0, dev=dev)
+    x = (randn(512, seed=1) * 0.5).to(torch.float16).to(dev)
+    ids = torch.tensor([0, 2], dtype=torch.int64, device=dev)
+    wts = torch.tensor([0.7, 0.3], dtype=torch.float16, device=dev)
+    y = grouped_moe_forward_quant(x, q, ids, wts)
+    resid = randn(512, seed=2).to(torch.float16).to(dev)
+    assert torch.equal(grouped_moe_forward_quant(x, q, ids, wts, residual=resid), y + resid)
+    one = grouped_moe_forward_quant(x, q, ids[:1], wts[:1])
+    bad = grouped_moe_forward_quant(x, q, torch.tensor([0, 99], device=dev), wts)
+    assert torch.equal(bad, one)
+
+
+def test_quant_fused_experts_w4_dequant_bit_exact(dev):
+    from lemoq.kernels.moe_grouped_quant import FusedExperts, quantize_fused_experts
+
+    print("case: QuantFusedExperts w4 dequant", flush=True)
+    gu = randn(3, 256, 512, seed=11, std=0.02)
+    dn = randn(3, 512, 128, seed=12, std=0.02)
+    q = quantize_fused_experts(FusedExperts(gu.to(dev), dn.to(dev)), bits=4, group_size=64)
+    for got, w, k in ((q.dequant_gate_up_expert(1), gu[1], 512), (q.dequant_down_expert(2), dn[2], 128)):
+        r = oq.rtn_quantize(w.numpy(), 4, 64, True)
+        ref = oq.dequant_tile(r["codes_padded"], r["scale"].astype(np.float16).astype(np.float32), None, 64, True)
+        assert np.array_equal(got.cpu().numpy().view(np.uint32), ref.view(np.uint32))
+    assert tuple(q.dequant_gate_up(torch.float16).shape) == (3, 256, 512)

@@ -85,3 +85,26 @@ def test_pack_4bit_torch_matches_the_reference_convention():
     with pytest.raises(ValueError):
         pack_4bit(torch.zeros((2, 3), dtype=torch.int32))
     assert bit_cost(2 * 130, 4, 128, in_features=130)["scale_bytes"] == 2 * 2 * 2  # 2 rows x 2 groups x 2 B
+
+
+def test_grouped_launch_plan_4bit_shapes():
+    """Host-side plan of the 4-bit grouped MoE: packed widths halved, uint8 codes,
+    group a multiple of the 32-code lane slice."""
+    from lemoq.kernels.moe_grouped_quant import QuantFusedExperts, quant_launch_plan
+
+    E, F, H, g = 8, 256, 512, 64
+    q = QuantFusedExperts(torch.zeros((E, 2 * F, H // 2), dtype=torch.uint8),
+                          torch.ones((E, 2 * F, H // g), dtype=torch.float16),
+                          torch.zeros((E, H, F // 2), dtype=torch.uint8),
+                          torch.ones((E, H, F // g), dtype=torch.float16), bits=4, group_size=g)
+    assert q.hidden == H and q.ffn == F
+    plan = quant_launch_plan(q, top_k=2)
+    assert plan["kernels"] == ("lemoq_moe_gate_up_w4", "lemoq_moe_down_w4") and plan["quant"]["bits"] == 4
+    bad = QuantFusedExperts(q.packed_gate_up.to(torch.int8), q.scale_gate_up, q.packed_down, q.scale_down, bits=4,
+                            group_size=g)
+    with pytest.raises(ValueError, match="uint8"):
+        quant_launch_plan(bad, top_k=2)
+    g16 = QuantFusedExperts(q.packed_gate_up, torch.ones((E, 2 * F, H // 16), dtype=torch.float16),
+                            q.packed_down, torch.ones((E, H, F // 16), dtype=torch.float16), bits=4, group_size=16)
+    with pytest.raises(ValueError, match="multiple of 32"):
+        quant_launch_plan(g16, top_k=2)
