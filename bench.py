@@ -727,8 +727,9 @@ def attention_configs(torch, hip, flusher, reps: int) -> dict:
 def format_gemvs(torch, hip, flusher, reps: int) -> dict:
     """The decode GEMV over each weight format of the dense dequant operator
     (w8 / w8 asymmetric / w4 / w4 asymmetric / MXFP4), at the qkv, o_proj and
-    lm_head shapes, cold (16 weight copies per pass, caches flushed), one token
-    in, fp16 out.  Algorithmic bytes: codes + scales (+ zero points) + x + y."""
+    lm_head shapes, and the grouped MoE on 8- and 4-bit experts, cold (16
+    weight copies per pass, caches flushed), one token in, fp16 out.
+    Algorithmic bytes: codes + scales (+ zero points) + activations in and out."""
     dev = flusher.buf.device
     K, copies = 2048, 16
     P, st = hip.ptr, hip.stream_of
@@ -768,6 +769,46 @@ def format_gemvs(torch, hip, flusher, reps: int) -> dict:
             log("format %-28s %8.2f us avg  %7.1f GB/s" % (name, r["avg_us"], r["gbs"]))
             del ws, fns
             torch.cuda.synchronize()
+    # the grouped MoE of one token at the OLMoE shape (64 experts, top-8, F 1024, H 2048),
+    # 8-bit and 4-bit experts, ids given, 16 expert sets per pass
+    E, F, H, top_k, group = 64, 1024, 2048, 8, 128
+    ids = torch.randperm(E, device=dev)[:top_k].to(torch.int64)
+    tw = torch.full((top_k,), 0.125, dtype=torch.float16, device=dev)
+    xh = torch.randn((H,), device=dev).to(torch.float16)
+    act = torch.empty((top_k, F), dtype=torch.float16, device=dev)
+    yo = torch.empty((H,), dtype=torch.float16, device=dev)
+    for bits in (8, 4):
+        per = 8 // bits
+        sets = []
+        for _ in range(copies):
+            dt = torch.int8 if bits == 8 else torch.uint8
+            gu = torch.randint(-128 if bits == 8 else 0, 128 if bits == 8 else 256, (E, 2 * F, H // per), dtype=dt,
+                               device=dev)
+            dn = torch.randint(-128 if bits == 8 else 0, 128 if bits == 8 else 256, (E, H, F // per), dtype=dt,
+                               device=dev)
+            gs = (torch.rand((E, 2 * F, H // group), device=dev) * 0.01).to(torch.float16)
+            ds = (torch.rand((E, H, F // group), device=dev) * 0.01).to(torch.float16)
+            sets.append((gu, gs, dn, ds))
+        gname, dname = ("lemoq_moe_gate_up_w8", "lemoq_moe_down_w8") if bits == 8 else (
+            "lemoq_moe_gate_up_w4", "lemoq_moe_down_w4")
+        for part, fn_of, nbytes in (
+            ("gate_up", lambda c: (lambda: hip.call(gname, P(xh), P(c[0]), P(c[1]), P(ids), top_k, E, F, H, group,
+                                                    P(act), st())),
+             top_k * 2 * F * (H // per + (H // group) * 2) + H * 2 + top_k * F * 2),
+            ("down", lambda c: (lambda: hip.call(dname, P(act), P(c[2]), P(c[3]), P(ids), P(tw), top_k, E, H, F, group,
+                                                 None, P(yo), st())),
+             top_k * H * (F // per + (F // group) * 2) + top_k * F * 2 + H * 2)):
+            fns = [fn_of(c) for c in sets]
+            fns[0]()
+            r = time_cold(torch, flusher, fns, reps)
+            name = "w%d moe %s (%d of %d experts)" % (bits, part, top_k, E)
+            r["bytes"] = int(nbytes)
+            r["gbs"] = nbytes / (r["avg_us"] * 1e-6) / 1e9
+            r["frac_of_peak"] = r["gbs"] / HBM_PEAK_GBS
+            out[name] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in r.items()}
+            log("format %-28s %8.2f us avg  %7.1f GB/s" % (name, r["avg_us"], r["gbs"]))
+        del sets
+        torch.cuda.synchronize()
     return out
 
 

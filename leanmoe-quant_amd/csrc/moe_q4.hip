@@ -12,7 +12,8 @@
 // down grid ceil(H / R) blocks of 8 waves walking the slots, then a
 // fixed-order sum of partial * top_w and the optional fp16 residual add.
 // Lane l reads bytes [1024 j + 16 l, +16) of chunk j of a packed row (32
-// codes) and the matching 32 activations; codes become exact fp16 values
+// codes; rows shorter than 1 KB, such as down's 512 bytes at ffn 1024: bytes
+// [512 j + 8 l, +8), 16 codes) and the matching activations; codes become exact fp16 values
 // (nibble masks, byte permutes against 0x64, one packed subtract) dotted with
 // v_dot2_f32_f16.
 #include "qformat.h"
@@ -21,16 +22,32 @@ namespace {
 
 using namespace lemoq_qf;
 
-// One packed row tile of R rows: KCH 16-byte slices per row and their scales.
-template <int R, int KCH>
+// One packed row tile of R rows: KCH slices of SB bytes per row (SB = 16:
+// lane l reads bytes [1024 j + 16 l, +16), 32 codes; SB = 8, for rows shorter
+// than 1 KB: bytes [512 j + 8 l, +8), 16 codes, so all 64 lanes load) and
+// their scales.
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+template <int SB>
+struct Slice;
+template <>
+struct Slice<16> {
+  u32x4 v;
+};
+template <>
+struct Slice<8> {
+  u32x2 v;
+};
+
+template <int R, int KCH, int SB>
 struct Q4Tile {
-  u32x4 c[R][KCH];
+  Slice<SB> c[R][KCH];
   uint16_t s[R][KCH];
   uint32_t ok;
 };
 
-template <int R, int KCH>
-__device__ __forceinline__ void q4_issue(Q4Tile<R, KCH>& t, const uint8_t* __restrict__ codes,
+template <int R, int KCH, int SB>
+__device__ __forceinline__ void q4_issue(Q4Tile<R, KCH, SB>& t, const uint8_t* __restrict__ codes,
                                          const uint16_t* __restrict__ scale, int64_t row0, int64_t nrows,
                                          int row_bytes, int ngroups, int group, int lane) {
   t.ok = 0u;
@@ -39,50 +56,79 @@ __device__ __forceinline__ void q4_issue(Q4Tile<R, KCH>& t, const uint8_t* __res
     const int64_t row = row0 + r;
 #pragma unroll
     for (int j = 0; j < KCH; ++j) {
-      const int off = 1024 * j + 16 * lane;
+      const int off = 64 * SB * j + SB * lane;
       const bool in = row < nrows && off < row_bytes;
       const int64_t rr = in ? row : 0;
       const int oo = in ? off : 0;
-      t.c[r][j] = load_stream16(reinterpret_cast<const int8_t*>(codes) + rr * row_bytes + oo);
+      const uint8_t* p = codes + rr * row_bytes + oo;
+      if constexpr (SB == 16)
+        t.c[r][j].v = load_stream16(reinterpret_cast<const int8_t*>(p));
+      else
+        t.c[r][j].v = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
       t.s[r][j] = scale[rr * ngroups + (oo * 2) / group];
       t.ok |= (in ? 1u : 0u) << (r * KCH + j);
     }
   }
 }
 
-template <int KCH>
+template <int KCH, int SB>
 struct X4 {
-  XChunk a[KCH], b[KCH];  // activations [2048 j + 32 l, +16) and [+16, +32)
+  XChunk a[KCH], b[KCH];  // activations of the slice: [0, 16) and (SB = 16) [16, 32)
 };
 
-template <int KCH>
-__device__ __forceinline__ void x4_load(uint32_t (&w)[KCH][16], const uint16_t* __restrict__ x, int n, int lane) {
+template <int KCH, int SB>
+__device__ __forceinline__ void x4_load(uint32_t (&w)[KCH][SB], const uint16_t* __restrict__ x, int n, int lane) {
   const bool vec = ((reinterpret_cast<uintptr_t>(x) & 15u) == 0) && ((n & 7) == 0);
 #pragma unroll
-  for (int j = 0; j < KCH; ++j) xq_load<32>(w[j], x, n, 2048 * j + 32 * lane, vec);
+  for (int j = 0; j < KCH; ++j) xq_load<2 * SB>(w[j], x, n, 128 * SB * j + 2 * SB * lane, vec);
 }
 
-template <int KCH>
-__device__ __forceinline__ void x4_chunks(const uint32_t (&w)[KCH][16], X4<KCH>& x) {
+template <int KCH, int SB>
+__device__ __forceinline__ void x4_chunks(const uint32_t (&w)[KCH][SB], X4<KCH, SB>& x) {
 #pragma unroll
   for (int j = 0; j < KCH; ++j) {
     xchunk_of(&w[j][0], x.a[j]);
-    xchunk_of(&w[j][8], x.b[j]);
+    if constexpr (SB == 16) xchunk_of(&w[j][8], x.b[j]);
   }
 }
 
-template <int R, int KCH>
-__device__ __forceinline__ float q4_row_dot(const Q4Tile<R, KCH>& t, int r, const X4<KCH>& x) {
+// 16 packed int4 codes (two dwords) x 16 activations: dword d holds codes
+// 8d .. 8d+7, the layout dot32_i4 reads from each of its four dwords.
+__device__ __forceinline__ float dot16_i4(const u32x2 c, const XChunk& x, float acc) {
+  const uint32_t cw[2] = {c.x, c.y};
+  const f16x2 bias = {(f16)1032.0f, (f16)1032.0f};
+#pragma unroll
+  for (int d = 0; d < 2; ++d) {
+    const uint32_t t = cw[d] ^ 0x88888888u;
+    const uint32_t lo = t & 0x0F0F0F0Fu, hi = (t >> 4) & 0x0F0F0F0Fu;
+    const int i0 = 2 * d;
+    const f16x2 p0 = as_h2(__builtin_amdgcn_perm(0x64646464u, lo, 0x04010400u)) - bias;
+    const f16x2 p1 = as_h2(__builtin_amdgcn_perm(0x64646464u, lo, 0x04030402u)) - bias;
+    const f16x2 p2 = as_h2(__builtin_amdgcn_perm(0x64646464u, hi, 0x04010400u)) - bias;
+    const f16x2 p3 = as_h2(__builtin_amdgcn_perm(0x64646464u, hi, 0x04030402u)) - bias;
+    acc = __builtin_amdgcn_fdot2(p0, x.a[i0], acc, false);
+    acc = __builtin_amdgcn_fdot2(p1, x.a[i0 + 1], acc, false);
+    acc = __builtin_amdgcn_fdot2(p2, x.b[i0], acc, false);
+    acc = __builtin_amdgcn_fdot2(p3, x.b[i0 + 1], acc, false);
+  }
+  return acc;
+}
+
+template <int R, int KCH, int SB>
+__device__ __forceinline__ float q4_row_dot(const Q4Tile<R, KCH, SB>& t, int r, const X4<KCH, SB>& x) {
   float a = 0.0f;
 #pragma unroll
   for (int j = 0; j < KCH; ++j) {
     const float sc = ((t.ok >> (r * KCH + j)) & 1u) ? h2f(t.s[r][j]) : 0.0f;
-    a = fmaf(sc, dot32_i4<true>(t.c[r][j], x.a[j], x.b[j], 0.0f), a);
+    float d;
+    if constexpr (SB == 16) d = dot32_i4<true>(t.c[r][j].v, x.a[j], x.b[j], 0.0f);
+    else d = dot16_i4(t.c[r][j].v, x.a[j], 0.0f);
+    a = fmaf(sc, d, a);
   }
   return a;
 }
 
-template <int KCH, int R>
+template <int KCH, int R, int SB>
 __global__ __launch_bounds__(256) void moe_gate_up_q4_kernel(const uint16_t* __restrict__ x,
                                                              const uint8_t* __restrict__ codes,
                                                              const uint16_t* __restrict__ scale,
@@ -91,25 +137,25 @@ __global__ __launch_bounds__(256) void moe_gate_up_q4_kernel(const uint16_t* __r
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int slot = blockIdx.y;
   const int64_t e = ids[slot];
-  uint32_t xw[KCH][16];
-  x4_load<KCH>(xw, x, H, lane);
+  uint32_t xw[KCH][SB];
+  x4_load<KCH, SB>(xw, x, H, lane);
   const bool ev = e >= 0 && e < E;
   const int n0 = (blockIdx.x * 4 + wave) * R;
   const int ng = H / group;
   const int rb = H / 2;
   const int64_t ebase = (ev ? e : 0) * (int64_t)(2 * F);
   const int64_t nrows = ev ? (int64_t)F : 0;  // an invalid expert id yields a zero row
-  Q4Tile<R, KCH> tg, tu;
-  q4_issue<R, KCH>(tg, codes + ebase * rb, scale + ebase * ng, n0, nrows, rb, ng, group, lane);
-  q4_issue<R, KCH>(tu, codes + (ebase + F) * rb, scale + (ebase + F) * ng, n0, nrows, rb, ng, group, lane);
+  Q4Tile<R, KCH, SB> tg, tu;
+  q4_issue<R, KCH, SB>(tg, codes + ebase * rb, scale + ebase * ng, n0, nrows, rb, ng, group, lane);
+  q4_issue<R, KCH, SB>(tu, codes + (ebase + F) * rb, scale + (ebase + F) * ng, n0, nrows, rb, ng, group, lane);
   LEMOQ_LOADS_ISSUED();
-  X4<KCH> xc;
-  x4_chunks<KCH>(xw, xc);
+  X4<KCH, SB> xc;
+  x4_chunks<KCH, SB>(xw, xc);
   float g[R], u[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    g[r] = wave_sum(q4_row_dot<R, KCH>(tg, r, xc));
-    u[r] = wave_sum(q4_row_dot<R, KCH>(tu, r, xc));
+    g[r] = wave_sum(q4_row_dot<R, KCH, SB>(tg, r, xc));
+    u[r] = wave_sum(q4_row_dot<R, KCH, SB>(tu, r, xc));
   }
   if (lane < R) {
     float gv = g[0], uv = u[0];
@@ -128,7 +174,7 @@ __global__ __launch_bounds__(256) void moe_gate_up_q4_kernel(const uint16_t* __r
   }
 }
 
-template <int KCH, int R>
+template <int KCH, int R, int SB>
 __global__ __launch_bounds__(512) void moe_down_q4_kernel(
     const uint16_t* __restrict__ act, const uint8_t* __restrict__ codes, const uint16_t* __restrict__ scale,
     const int64_t* __restrict__ ids, const uint16_t* __restrict__ top_w, int top_k, int E, int H, int F,
@@ -144,18 +190,19 @@ __global__ __launch_bounds__(512) void moe_down_q4_kernel(
   for (int slot = wave; slot < top_k; slot += 8) {
     const int64_t e = ids[slot];
     const float wslot = h2f(top_w[slot]);
-    uint32_t aw[KCH][16];
-    x4_load<KCH>(aw, act + (int64_t)slot * F, F, lane);
+    uint32_t aw[KCH][SB];
+    x4_load<KCH, SB>(aw, act + (int64_t)slot * F, F, lane);
     const bool ev = e >= 0 && e < E;
     const int64_t ebase = (ev ? e : 0) * (int64_t)H;
-    Q4Tile<R, KCH> tl;
-    q4_issue<R, KCH>(tl, codes + ebase * rb, scale + ebase * ng, n0, ev ? (int64_t)H : 0, rb, ng, group, lane);
+    Q4Tile<R, KCH, SB> tl;
+    q4_issue<R, KCH, SB>(tl, codes + ebase * rb, scale + ebase * ng, n0, ev ? (int64_t)H : 0, rb, ng, group,
+                         lane);
     LEMOQ_LOADS_ISSUED();
-    X4<KCH> xc;
-    x4_chunks<KCH>(aw, xc);
+    X4<KCH, SB> xc;
+    x4_chunks<KCH, SB>(aw, xc);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const float v = wave_sum(q4_row_dot<R, KCH>(tl, r, xc));
+      const float v = wave_sum(q4_row_dot<R, KCH, SB>(tl, r, xc));
       if (lane == 0) part[slot][r] = ev ? v * wslot : 0.0f;
     }
   }
@@ -172,9 +219,16 @@ __global__ __launch_bounds__(512) void moe_down_q4_kernel(
   }
 }
 
-int kch4_of(int64_t k) {  // 1 KB chunks of a packed 4-bit row of k codes
-  const int64_t c = (k / 2 + 1023) / 1024;
-  return c <= 1 ? 1 : (c <= 2 ? 2 : 4);
+// Slice bytes and 1 KB (SB = 16) or 512 B (SB = 8) chunks of a packed row of
+// k 4-bit codes: rows shorter than 1 KB take 8-byte slices so every lane loads.
+struct Q4Geom {
+  int sb, kch;
+};
+Q4Geom q4_geom(int64_t k) {
+  const int64_t rb = k / 2;
+  if (rb < 1024) return {8, 1};
+  const int64_t c = (rb + 1023) / 1024;
+  return {16, c <= 1 ? 1 : (c <= 2 ? 2 : 4)};
 }
 
 }  // namespace
@@ -192,11 +246,14 @@ extern "C" int lemoq_moe_gate_up_w4(const uint16_t* x, const uint8_t* codes, con
   const dim3 grid((unsigned)((ffn + 4 * R - 1) / (4 * R)), (unsigned)top_k);
   hipStream_t st = lemoq_stream(stream);
   const int E = (int)num_experts, F = (int)ffn, H = (int)hidden, g = (int)group;
-  switch (kch4_of(hidden)) {
-    case 1: hipLaunchKernelGGL((moe_gate_up_q4_kernel<1, R>), grid, dim3(256), 0, st, x, codes, scale, ids, E, F, H, g, act); break;
-    case 2: hipLaunchKernelGGL((moe_gate_up_q4_kernel<2, R>), grid, dim3(256), 0, st, x, codes, scale, ids, E, F, H, g, act); break;
-    default: hipLaunchKernelGGL((moe_gate_up_q4_kernel<4, R>), grid, dim3(256), 0, st, x, codes, scale, ids, E, F, H, g, act); break;
-  }
+  const Q4Geom geo = q4_geom(hidden);
+#define LEMOQ_GU4(KK, SS) \
+  hipLaunchKernelGGL((moe_gate_up_q4_kernel<KK, R, SS>), grid, dim3(256), 0, st, x, codes, scale, ids, E, F, H, g, act)
+  if (geo.sb == 8) LEMOQ_GU4(1, 8);
+  else if (geo.kch == 1) LEMOQ_GU4(1, 16);
+  else if (geo.kch == 2) LEMOQ_GU4(2, 16);
+  else LEMOQ_GU4(4, 16);
+#undef LEMOQ_GU4
   LEMOQ_CHECK_LAUNCH();
 }
 
@@ -214,10 +271,14 @@ extern "C" int lemoq_moe_down_w4(const uint16_t* act, const uint8_t* codes, cons
   const dim3 grid((unsigned)((hidden + R - 1) / R));
   hipStream_t st = lemoq_stream(stream);
   const int K = (int)top_k, E = (int)num_experts, H = (int)hidden, F = (int)ffn, g = (int)group;
-  switch (kch4_of(ffn)) {
-    case 1: hipLaunchKernelGGL((moe_down_q4_kernel<1, R>), grid, dim3(512), 0, st, act, codes, scale, ids, top_w, K, E, H, F, g, residual, out); break;
-    case 2: hipLaunchKernelGGL((moe_down_q4_kernel<2, R>), grid, dim3(512), 0, st, act, codes, scale, ids, top_w, K, E, H, F, g, residual, out); break;
-    default: hipLaunchKernelGGL((moe_down_q4_kernel<4, R>), grid, dim3(512), 0, st, act, codes, scale, ids, top_w, K, E, H, F, g, residual, out); break;
-  }
+  const Q4Geom geo = q4_geom(ffn);
+#define LEMOQ_DN4(KK, SS)                                                                                 \
+  hipLaunchKernelGGL((moe_down_q4_kernel<KK, R, SS>), grid, dim3(512), 0, st, act, codes, scale, ids, top_w, K, \
+                     E, H, F, g, residual, out)
+  if (geo.sb == 8) LEMOQ_DN4(1, 8);
+  else if (geo.kch == 1) LEMOQ_DN4(1, 16);
+  else if (geo.kch == 2) LEMOQ_DN4(2, 16);
+  else LEMOQ_DN4(4, 16);
+#undef LEMOQ_DN4
   LEMOQ_CHECK_LAUNCH();
 }
