@@ -50,8 +50,8 @@ def rms_norm_fused(
     if H > MAX_HIDDEN:
         raise NotImplementedError("H=%d exceeds the block limit %d" % (H, MAX_HIDDEN))
     out_dtype = x.dtype if out_dtype is None else out_dtype
-    if out_dtype != torch.float16:
-        raise NotImplementedError("out_dtype must be fp16")
+    if out_dtype not in (torch.float16, torch.float32, torch.float64):
+        raise NotImplementedError("out_dtype must be fp16, fp32 or fp64, got %s" % out_dtype)
     _hip.require_rocm(x, weight, what="rms_norm_fused")
     y = torch.empty_like(x)
     M = int(x.numel()) // H if H else 0
@@ -60,7 +60,9 @@ def rms_norm_fused(
             "lemoq_rmsnorm", _hip.ptr(x), M, H, _hip.ptr(weight), float(eps), _hip.ptr(y),
             _hip.stream_of(x.device),
         )
-    return y
+    # The reference stores the kernel's fp16 product into an out_dtype buffer
+    # (src/lemoq/kernels/rmsnorm.py:147-160): a wider dtype holds the same values.
+    return y if out_dtype == torch.float16 else y.to(out_dtype)
 
 
 def warm(x: Any, weight: Any, eps: float, **kwargs: Any) -> None:

@@ -2,8 +2,8 @@
 device RTN kernel (``load_hf_olmoe(..., device="cuda")``) gives bit-exactly
 the codes and scales of the CPU oracle's RTN, decodes greedily in a captured
 graph in step with the CPU oracle (per-step KL < 0.01, identical tokens
-except at near-ties), and reloaded from the packed format decodes bitwise
-identically."""
+except at near-ties), also with HF OLMoE's clip_qkv set in the config, and
+reloaded from the packed format decodes bitwise identically."""
 
 from __future__ import annotations
 
@@ -27,8 +27,7 @@ def _rtn(w, g):
     return torch.from_numpy(q["codes_padded"]), torch.from_numpy(q["scale_f16"])
 
 
-@pytest.fixture(scope="module")
-def ckpt_dir(tmp_path_factory):
+def _write_ckpt(tmp_path_factory, clip_qkv=None):
     from transformers import OlmoeConfig, OlmoeForCausalLM
     from transformers.utils import logging as hf_logging
 
@@ -38,7 +37,7 @@ def ckpt_dir(tmp_path_factory):
                       num_attention_heads=2, num_key_value_heads=2, num_experts=8, num_experts_per_tok=2,
                       norm_topk_prob=False, rms_norm_eps=1e-5, rope_theta=10000.0, max_position_embeddings=64,
                       tie_word_embeddings=False, eos_token_id=None, pad_token_id=None, bos_token_id=None,
-                      initializer_range=0.05)
+                      initializer_range=0.05, clip_qkv=clip_qkv)
     m = OlmoeForCausalLM(cfg)
     with torch.no_grad():
         for n, p in m.named_parameters():
@@ -47,6 +46,17 @@ def ckpt_dir(tmp_path_factory):
     d = str(tmp_path_factory.mktemp("olmoe_gpu_ckpt"))
     m.save_pretrained(d, safe_serialization=True)
     return d
+
+
+@pytest.fixture(scope="module")
+def ckpt_dir(tmp_path_factory):
+    return _write_ckpt(tmp_path_factory)
+
+
+@pytest.fixture(scope="module")
+def ckpt_dir_clip(tmp_path_factory):
+    """The same model with HF OLMoE's clip_qkv set (0.4 clamps a good share of q/k/v)."""
+    return _write_ckpt(tmp_path_factory, clip_qkv=0.4)
 
 
 def test_device_rtn_load_is_bit_exact_to_the_oracle(ckpt_dir, dev):
@@ -63,9 +73,11 @@ def test_device_rtn_load_is_bit_exact_to_the_oracle(ckpt_dir, dev):
         assert torch.equal(a.view(torch.uint8), b.view(torch.uint8)), name
 
 
-def test_loaded_checkpoint_decodes_with_the_oracle(ckpt_dir, dev, tmp_path):
-    print("case: loaded checkpoint decode", flush=True)
-    w = ck.load_hf_olmoe(ckpt_dir, device=dev)
+@pytest.mark.parametrize("clip", [False, True], ids=["plain", "clip_qkv"])
+def test_loaded_checkpoint_decodes_with_the_oracle(clip, ckpt_dir, ckpt_dir_clip, dev, tmp_path):
+    print("case: loaded checkpoint decode (clip_qkv %s)" % clip, flush=True)
+    w = ck.load_hf_olmoe(ckpt_dir_clip if clip else ckpt_dir, device=dev)
+    assert w.shape.clip_qkv == (0.4 if clip else None)
     prompt, steps = [5, 77, 300, 12], 12
     sess = DecodeSession(w, prompt, max_new_tokens=steps, num_splits=None)
     sess.prefill()
@@ -93,6 +105,7 @@ def test_loaded_checkpoint_decodes_with_the_oracle(ckpt_dir, dev, tmp_path):
     # packed format: saved, reloaded onto the device, the same graph step bit for bit
     ck.save_packed(w, str(tmp_path))
     w2 = ck.load_packed(str(tmp_path), device=dev)
+    assert w2.shape == w.shape  # clip_qkv travels with the shape
     s2 = DecodeSession(w2, prompt, max_new_tokens=steps, num_splits=None)
     s2.prefill()
     s2.replay(steps)

@@ -458,6 +458,18 @@ def test_rmsnorm_vs_hf_formula(rows, H, dev):
     assert (got.double() - ref.double()).abs().gt(0).float().mean() < 0.01
 
 
+def test_rmsnorm_out_dtype_widens_the_fp16_result(dev):
+    """out_dtype fp32: the same fp16 values in an fp32 buffer, as the reference
+    stores its fp16 product into an out_dtype tensor (rmsnorm.py:147-160)."""
+    from lemoq.kernels.rmsnorm import rms_norm_fused
+
+    x = randn(4, 2048, seed=7).to(torch.float16).to(dev)
+    w = (torch.rand(2048, generator=torch.Generator().manual_seed(8)) + 0.5).to(torch.float16).to(dev)
+    y16 = rms_norm_fused(x, w, 1e-5)
+    y32 = rms_norm_fused(x, w, 1e-5, out_dtype=torch.float32)
+    assert y32.dtype == torch.float32 and torch.equal(y32, y16.float())
+
+
 @pytest.mark.parametrize("rows,H,offset", [(3, 1003, 0), (4, 2048, 1), (2, 8192, 0)],
                          ids=["odd-width", "misaligned-rows", "widest"])
 def test_rmsnorm_element_path_and_widest_rows(rows, H, offset, dev):
