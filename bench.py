@@ -63,6 +63,9 @@ REFERENCE_RTX5090_MS = {"1024": 1.4602, "4096": 1.6075}  # README_EN.md:71 (not 
 REFERENCE_RTX5090_TTFT_MS = {"1024": 84.4366, "4096": 158.3072}
 REFERENCE_RTX5090_E2E32_MS = {"1024": 131.16, "4096": 209.75}
 KV_BYTES_PER_TOKEN_LAYER = 16 * (128 + 2) * 2  # 16 heads x (128 codes + fp16 scale) x (K, V)
+KV_F16_BYTES_PER_TOKEN_LAYER = 16 * 128 * 2 * 2  # 16 heads x 128 fp16 values x (K, V)
+# the reference's cell with KV-INT8 off (EXP-p5-01-kv-int8.md:140-143; RTX 5090, not this hardware)
+REFERENCE_RTX5090_KV_F16_MS = {"1024": 1.4689, "4096": 1.71798}
 
 
 def log(msg: str) -> None:
@@ -90,6 +93,7 @@ def parse_args(argv=None):
     ap.add_argument("--no-cpu-ops", action="store_true", help="skip the per-operator CPU timings (C1-C4)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-formats", action="store_true", help="skip the weight-format GEMV timings")
+    ap.add_argument("--no-kv-fp16", action="store_true", help="skip the fp16-cache (KV-INT8 off) step timing")
     ap.add_argument("--mode", choices=("full", "kernels", "traffic", "prefill", "step"), default="full")
     ap.add_argument("--summarize-pmc", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "PLAN_JSON"))
     ap.add_argument("--summarize-prefill", metavar="KERNEL_TRACE_CSV",
@@ -426,6 +430,29 @@ def time_decode(torch, w, ctx: int, steps: int, warmup: int, extra: int):
         % (ctx, res["ms_per_token"], res["device_ms_per_token"], steps, p50, p99, MULTI_STEPS,
            res["ms_per_token_graph%d" % MULTI_STEPS], groups))
     return sess, res
+
+
+def time_kv_fp16(torch, w, ctx: int, steps: int, warmup: int, read_bw: float) -> dict:
+    """The step over the fp16 cache (the reference's cell with KV-INT8 off): the
+    same repeated timing as the headline (3 repeats x ``steps`` replays from the
+    prefilled state of ``[1] * ctx``), and its bytes with fp16 KV rows."""
+    from lemoq.model.olmoe import DecodeSession
+
+    sess = DecodeSession(w, [1] * ctx, max_new_tokens=max(warmup, 5) + max(steps, 20) + 4, kv_cache="fp16")
+    sess.capture()
+    sess.prefill()
+    rep = measure_repeats(torch, sess, warmup=max(warmup, 5), timed=max(steps, 20), repeats=3)
+    ms = sorted(rep["wall_ms"])[1]
+    dev_ms = sorted(rep["event_ms"])[1]
+    filled_avg = ctx + 1 + (rep["timed"] - 1) / 2.0
+    nbytes = w.shape.weight_bytes_per_token() + KV_F16_BYTES_PER_TOKEN_LAYER * w.shape.layers * filled_avg
+    launches = sess.launches_per_step
+    del sess
+    res = {"ms_per_token_repeats_p50": ms, "device_ms_per_token": dev_ms, "wall_spread": rep["wall_spread"],
+           "step_bytes": int(nbytes), "step_hbm_frac_of_measured": nbytes / (dev_ms * 1e-3) / 1e9 / read_bw,
+           "launches_per_step": launches}
+    log("ctx %d fp16 cache: %.4f ms/token (repeats p50), device %.4f" % (ctx, ms, dev_ms))
+    return res
 
 
 def _p50_p99(samples: list) -> tuple:
@@ -1018,6 +1045,12 @@ def main(argv=None) -> int:
     kt = kernel_table(torch, _hip, w, sess, flusher, args.kernel_reps)
     cfg = attention_configs(torch, _hip, flusher, args.kernel_reps)
     fmts = None if args.no_formats else format_gemvs(torch, _hip, flusher, args.kernel_reps)
+    kv16 = None
+    if not args.no_kv_fp16:
+        del sess  # its caches: the fp16-cache sessions take their own
+        sess = None
+        kv16 = {str(c): time_kv_fp16(torch, w, c, args.steps, args.warmup, read_bw)
+                for c in (args.ctx, args.ctx2) if c}
     del sess
     r2 = None
     snap2 = None
@@ -1100,6 +1133,11 @@ def main(argv=None) -> int:
     line["attention_configs"] = cfg
     if fmts is not None:
         line["weight_formats"] = fmts
+    if kv16 is not None:
+        kv16["reference_rtx5090_ms_per_token"] = REFERENCE_RTX5090_KV_F16_MS
+        kv16["what"] = ("the same step over the fp16 cache (DecodeSession(kv_cache='fp16'): the reference's cell "
+                        "with KV-INT8 off), prompt ctx x token 1, timed as the headline")
+        line["kv_fp16"] = kv16
     line["step_ms_p50"], line["step_ms_p99"] = r1["step_ms_p50"], r1["step_ms_p99"]
     gk = "ms_per_token_graph%d" % MULTI_STEPS
     line[gk] = r1[gk]  # MULTI_STEPS steps per graph launch (not the headline)

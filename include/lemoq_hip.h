@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define LEMOQ_ABI_VERSION 6
+#define LEMOQ_ABI_VERSION 7
 
 enum {
   LEMOQ_OK = 0,
@@ -481,6 +481,23 @@ int lemoq_attn_split_fused_i8(const uint16_t* qkv, int64_t heads, int64_t head_d
                               int64_t num_splits, float qk_scale, float* m, float* l, float* acc,
                               float clip_qkv, void* stream);
 
+/* A16 fused over the fp16 cache (KV-INT8 off): the q_norm/k_norm, RoPE,
+ * kv_direct_write and fp16 split-KV attention sequence of
+ * src/lemoq/kernels/attn_decode.py:882-948,999-1008 (kv_direct.py:110-137,
+ * _attn_triton.py:30-99) for one decode token.  As lemoq_attn_split_fused_i8,
+ * except that the block holding *pos writes the rotated k row and the v row
+ * as fp16 to slot *pos of kc / vc ((heads, head_stride) fp16, head_stride >=
+ * s_len*D elements, 16-byte aligned rows) -- the bits lemoq_qk_norm_rope_kv_i8
+ * gives for them -- and the partials are those of lemoq_attn_split_f16 over
+ * tokens [0, *pos] (the same arithmetic; the token order within a split may
+ * differ, so the sums agree to fp32 rounding). */
+int lemoq_attn_split_fused_f16(const uint16_t* qkv, int64_t heads, int64_t head_dim,
+                               const uint16_t* q_norm_w, const uint16_t* k_norm_w, float eps,
+                               const uint16_t* cos_tab, const uint16_t* sin_tab,
+                               const int64_t* pos, uint16_t* kc, uint16_t* vc, int64_t head_stride,
+                               int64_t s_len, int64_t num_splits, float qk_scale, float* m, float* l,
+                               float* acc, float clip_qkv, void* stream);
+
 /* ---------------------------------------------------------------------------
  * A17 — greedy selection and step advance on the device (replaces the host
  * `logits.argmax().item()` of StaticCacheDecodeSession.replay,
@@ -501,7 +518,10 @@ int lemoq_argmax_advance(const uint16_t* logits, int64_t n, int64_t* token,
  * caller captures it into a hipGraph.  Replaces the captured
  * model(token, ...) forward of StaticCacheDecodeSession.capture
  * (benchmarks/cudagraph.py:680-737) for the canonical w8a16 + W8 lm_head +
- * KV-INT8 cell.  All buffers are caller-owned; see LemoqOlmoeStep.
+ * KV-INT8 cell, or, with kv_fp16 set, the same cell with KV-INT8 off (the
+ * fp16 StaticCache written by kv_direct_write and read by the fp16 split-KV
+ * attention, src/lemoq/kernels/attn_decode.py:930-948,999-1008).  All buffers are
+ * caller-owned; see LemoqOlmoeStep.
  * ------------------------------------------------------------------------- */
 typedef struct LemoqOlmoeLayer {
   const uint16_t* ln_in;     /* (H)                */
@@ -517,10 +537,10 @@ typedef struct LemoqOlmoeLayer {
   const uint16_t* gu_scale;  /* (E, 2F, H/g)       */
   const int8_t* dn_codes;    /* (E, H, F)          */
   const uint16_t* dn_scale;  /* (E, H, F/g)        */
-  int8_t* kc;                /* (heads, S, D)      */
-  uint16_t* ks;              /* (heads, S)         */
-  int8_t* vc;                /* (heads, S, D)      */
-  uint16_t* vs;              /* (heads, S)         */
+  int8_t* kc;                /* (heads, S, D) int8; fp16 rows when kv_fp16 */
+  uint16_t* ks;              /* (heads, S); unused (may be NULL) when kv_fp16 */
+  int8_t* vc;                /* (heads, S, D) int8; fp16 rows when kv_fp16 */
+  uint16_t* vs;              /* (heads, S); unused (may be NULL) when kv_fp16 */
 } LemoqOlmoeLayer;
 
 typedef struct LemoqOlmoeStep {
@@ -568,6 +588,9 @@ typedef struct LemoqOlmoeStep {
    * runs lemoq_attn_merge, the o_proj GEMV and lemoq_router_logits. */
   float* o_part;                 /* (heads*D/512, H) o_proj partial sums */
   uint16_t* h_mid;               /* (H) residual after attention */
+  /* Cache kind: 0 = KV-INT8 (kc/vc int8 codes, ks/vs fp16 scales), 1 = fp16
+   * rows (kc/vc point to (heads, S, D) fp16; lemoq_attn_split_fused_f16). */
+  int64_t kv_fp16;
 } LemoqOlmoeStep;
 
 int lemoq_olmoe_decode_step(const LemoqOlmoeStep* step, void* stream);
@@ -638,7 +661,9 @@ int lemoq_gather_rows(const uint16_t* src, int64_t n_rows, int64_t H, const int6
  * D); KV-INT8 rows into slots pos0 .. pos0+rows-1 (the values
  * kv_int8_bulk_quantize, src/lemoq/kernels/kv_int8.py:127-162, gives for the
  * fp16 cache rows); k_f16/v_f16 (nullable) fp16 copies at
- * h*f16_head_stride + pos*D for the prefill attention.  pos0 + rows <= s_len;
+ * h*f16_head_stride + pos*D for the prefill attention.  With kc, ks, vc and
+ * vs all NULL no KV-INT8 rows are written and k_f16/v_f16 (then required)
+ * are the fp16 cache itself (KV-INT8 off).  pos0 + rows <= s_len;
  * cos_tab/sin_tab hold s_len rows.  clip_qkv as for lemoq_qk_norm_rope_kv_i8. */
 int lemoq_qk_norm_rope_kv_i8_rows(const uint16_t* qkv, int64_t rows, int64_t heads,
                                   int64_t head_dim, const uint16_t* q_norm_w,

@@ -1,8 +1,8 @@
-// The split-KV block of the fused per-layer attention over the KV-INT8 cache
-// (q_norm/k_norm, RoPE, KV-INT8 write of the new token, online softmax over
-// the block's cached tokens), launched by attn_fused.hip.
+// The split-KV block of the fused per-layer attention over the KV-INT8 or the
+// fp16 cache (q_norm/k_norm, RoPE, the cache write of the new token, online
+// softmax over the block's cached tokens), launched by attn_fused.hip.
 //
-// attn_split_fused_i8: grid (num_splits, heads), 4 waves per block.  Block
+// attn_split_fused_i8 / _f16: grid (num_splits, heads), 4 waves per block.  Block
 // (s, h) covers tokens [s*c, min((s+1)*c, n)) of head h with n = *pos + 1 and
 // c = ceil(n / num_splits) (the reference's split rule,
 // src/lemoq/kernels/attn_decode.py:295-354), and does in one launch what the
@@ -10,18 +10,22 @@
 //   - q_norm over all heads*D values of q (HF rounding points) and RoPE at
 //     *pos for head h (wave 0, every block: the 4 KB row is L2-resident);
 //   - in the one block whose range holds *pos: k_norm + RoPE of the new k and
-//     the KV-INT8 quantisation of the new k and v rows (waves 1 and 2),
-//     written to slot *pos of the cache and kept in LDS;
-//   - the online softmax over its cached tokens with the per-token scales
-//     folded in (score = ((q.c) * qk_scale) * ks, acc += (p * vs) * c,
-//     l += p), the new token folded from LDS (never read back from the slot
-//     just written), and the block's (m, l, acc[D]) partial.
+//     the cache write of the new k and v rows (waves 1 and 2): their KV-INT8
+//     quantisation, or the fp16 rows as they are (the reference's
+//     kv_direct_write, src/lemoq/kernels/kv_direct.py:110-137, when KV-INT8
+//     is off), written to slot *pos of the cache and kept in LDS;
+//   - the online softmax over its cached tokens, for KV-INT8 with the
+//     per-token scales folded in (score = ((q.c) * qk_scale) * ks,
+//     acc += (p * vs) * c, l += p), the new token folded from LDS (never read
+//     back from the slot just written), and the block's (m, l, acc[D])
+//     partial.
 // The LSE merge of the partials is lemoq_attn_merge.  Each wave keeps two
 // blocks of token loads in flight (double buffering); the token groups of a
 // wave are summed with DPP row rotations and the gfx950 cross-row swaps.
 //
 // Arithmetic restates _attn_split_kernel_int8
-// (src/lemoq/kernels/_attn_triton.py:102-165), the KV write
+// (src/lemoq/kernels/_attn_triton.py:102-165) and, for fp16 rows,
+// _attn_split_kernel (:30-99), the KV write
 // (src/lemoq/kernels/kv_int8.py:196-216), _rope_one_kernel
 // (src/lemoq/kernels/rope.py:101-123) and the HF q_norm/k_norm RMSNorm.
 #pragma once
@@ -38,11 +42,11 @@ struct AttnSplitArgs {
   const uint16_t* cos_tab;  // (s_len, D) fp16
   const uint16_t* sin_tab;  // (s_len, D) fp16
   const int64_t* pos;       // device scalar
-  int8_t* kc;
-  uint16_t* ks;
-  int8_t* vc;
+  void* kc;                 // (heads, code_head_stride) int8 codes, or fp16 rows
+  uint16_t* ks;             // (heads, s_len) fp16 scales (KV-INT8 only)
+  void* vc;
   uint16_t* vs;
-  int64_t code_head_stride;  // >= s_len * D
+  int64_t code_head_stride;  // elements, >= s_len * D
   int64_t s_len;
   int heads;
   int ns;
@@ -53,37 +57,38 @@ struct AttnSplitArgs {
   float* acc_out;  // (heads, ns, D)
 };
 
-template <int D, int NW_ = 8, int U_ = 4>
+template <int D, bool I8, int NW_ = 8, int U_ = 4>
 struct HeadShape {
-  using T = lemoq_attn::TokShape<D, true, U_>;  // KV-INT8 token rows
-  static constexpr int LPT = T::LPT;    // lanes per cached token row (16 codes per lane)
+  using T = lemoq_attn::TokShape<D, I8, U_>;  // KV-INT8 or fp16 token rows
+  static constexpr int LPT = T::LPT;    // lanes per cached token row (16 bytes per lane)
   static constexpr int BLK = T::BLK;    // tokens per wave token block
   static constexpr int NW = NW_;        // waves per block
   static constexpr int EPL = D / 64;    // prologue elements per lane
   static_assert(NW >= 3, "waves 0..2 carry the q and new k/v prologue");
 };
 
-// LDS of one split block.
-template <int D, int NW>
+// LDS of one split block (the new k / v rows as the cache holds them: EB
+// bytes per element).
+template <int D, int NW, int EB>
 struct AttnFusedSmem {
   alignas(16) uint16_t q_s[D];
-  alignas(16) int8_t knew_s[D];
-  alignas(16) int8_t vnew_s[D];
+  alignas(16) uint8_t knew_s[D * EB];
+  alignas(16) uint8_t vnew_s[D * EB];
   float kvs_s[2];
   float wm[NW], wl[NW];
   float wacc[NW * D];
 };
 
-template <int D, int NW_, int U_>
+template <int D, bool I8, int NW_, int U_>
 __device__ __forceinline__ void attn_split_fused_block(const AttnSplitArgs& a, int sp, int h,
-                                                       AttnFusedSmem<D, NW_>& sm) {
-  using S = HeadShape<D, NW_, U_>;
+                                                       AttnFusedSmem<D, NW_, I8 ? 1 : 2>& sm) {
+  using S = HeadShape<D, I8, NW_, U_>;
   using T = typename S::T;
-  constexpr int BLK = S::BLK, NW = S::NW, EPL = S::EPL;
+  constexpr int BLK = S::BLK, NW = S::NW, EPL = S::EPL, EB = T::EB;
   constexpr int STRIDE = NW * BLK;
   uint16_t* q_s = sm.q_s;
-  int8_t* knew_s = sm.knew_s;
-  int8_t* vnew_s = sm.vnew_s;
+  uint8_t* knew_s = sm.knew_s;
+  uint8_t* vnew_s = sm.vnew_s;
   float* kvs_s = sm.kvs_s;
   float* wm = sm.wm;
   float* wl = sm.wl;
@@ -94,10 +99,10 @@ __device__ __forceinline__ void attn_split_fused_block(const AttnSplitArgs& a, i
   const int dl = lane % T::LPT, tl = lane / T::LPT;
   const int HD = a.heads * D;
   const int64_t cap = a.s_len;
-  const uint8_t* kb = reinterpret_cast<const uint8_t*>(a.kc + (int64_t)h * a.code_head_stride);
-  const uint8_t* vb = reinterpret_cast<const uint8_t*>(a.vc + (int64_t)h * a.code_head_stride);
-  const uint16_t* ksh = a.ks + (int64_t)h * cap;
-  const uint16_t* vsh = a.vs + (int64_t)h * cap;
+  const uint8_t* kb = static_cast<const uint8_t*>(a.kc) + (int64_t)h * a.code_head_stride * EB;
+  const uint8_t* vb = static_cast<const uint8_t*>(a.vc) + (int64_t)h * a.code_head_stride * EB;
+  const uint16_t* ksh = I8 ? a.ks + (int64_t)h * cap : nullptr;  // read only for KV-INT8
+  const uint16_t* vsh = I8 ? a.vs + (int64_t)h * cap : nullptr;
 
   const int64_t pos = a.pos[0];  // a scalar load, issued first
 
@@ -197,6 +202,17 @@ __device__ __forceinline__ void attn_split_fused_block(const AttnSplitArgs& a, i
     if (which == 0) {
 #pragma unroll
       for (int i = 0; i < EPL; ++i) q_s[lane + 64 * i] = f2h(o[i]);
+    } else if constexpr (!I8) {
+      // fp16 cache: the rotated k / the (clipped) v row as it is
+      uint16_t* lds = reinterpret_cast<uint16_t*>(which == 1 ? knew_s : vnew_s);
+      uint16_t* dst = static_cast<uint16_t*>(which == 1 ? a.kc : a.vc) + (int64_t)h * a.code_head_stride +
+                      pos * D;
+#pragma unroll
+      for (int i = 0; i < EPL; ++i) {
+        const uint16_t b = f2h(o[i]);
+        lds[lane + 64 * i] = b;
+        dst[lane + 64 * i] = b;
+      }
     } else {
       float amax = 0.0f;
 #pragma unroll
@@ -204,8 +220,8 @@ __device__ __forceinline__ void attn_split_fused_block(const AttnSplitArgs& a, i
       amax = wave_max(amax);
       const float s = amax > 0.0f ? amax / 127.0f : 1.0f;
       const uint16_t s16 = f2h(s);
-      int8_t* lds = which == 1 ? knew_s : vnew_s;
-      int8_t* dst = (which == 1 ? a.kc : a.vc) + (int64_t)h * a.code_head_stride + pos * D;
+      int8_t* lds = reinterpret_cast<int8_t*>(which == 1 ? knew_s : vnew_s);
+      int8_t* dst = static_cast<int8_t*>(which == 1 ? a.kc : a.vc) + (int64_t)h * a.code_head_stride + pos * D;
 #pragma unroll
       for (int i = 0; i < EPL; ++i) {
         float qv = rintf(o[i] / s);
@@ -222,8 +238,8 @@ __device__ __forceinline__ void attn_split_fused_block(const AttnSplitArgs& a, i
   }
   __syncthreads();
 
-  lemoq_attn::QSlice<true> qx;
-  load_xchunk(q_s + dl * 16, qx.x);
+  lemoq_attn::QSlice<I8> qx;
+  lemoq_attn::load_q<T>(qx, q_s, dl);
   lemoq_attn::SoftmaxState<T::EPL> st;
   lemoq_attn::softmax_init(st);
 
@@ -255,8 +271,10 @@ __device__ __forceinline__ void attn_split_fused_block(const AttnSplitArgs& a, i
     for (int u = 0; u < T::U; ++u) {
       nbk.k[u] = *reinterpret_cast<const u32x4*>(knew_s + dl * 16);
       nbk.v[u] = *reinterpret_cast<const u32x4*>(vnew_s + dl * 16);
-      nbk.ks[u] = f2h(kvs_s[0]);
-      nbk.vs[u] = f2h(kvs_s[1]);
+      if constexpr (I8) {
+        nbk.ks[u] = f2h(kvs_s[0]);
+        nbk.vs[u] = f2h(kvs_s[1]);
+      }
     }
     lemoq_attn::fold_tokens<T>(st, nbk, qx, 0, 1, tl, lane, a.qk_scale);
   }

@@ -236,6 +236,11 @@ __global__ __launch_bounds__(1024) void qk_rows_kernel(
     if (active) *reinterpret_cast<u32x4*>(q_out + row * HD + e0) = ov;
     return;
   }
+  uint16_t* fdst = part == 1 ? k_f16 : v_f16;
+  if (!kc) {  // fp16 cache only (no KV-INT8 rows): a grid-uniform branch
+    if (active) *reinterpret_cast<u32x4*>(fdst + (int64_t)h * f16_head_stride + pos * D + d0) = ov;
+    return;
+  }
   // KV-INT8 row of this head: amax over the head's D/8 threads
   float amax = 0.0f;
 #pragma unroll
@@ -253,7 +258,6 @@ __global__ __launch_bounds__(1024) void qk_rows_kernel(
   if (!active) return;
   int8_t* cdst = (part == 1 ? kc : vc) + (int64_t)h * code_head_stride + pos * D + d0;
   *reinterpret_cast<uint2*>(cdst) = make_uint2(cw2[0], cw2[1]);
-  uint16_t* fdst = part == 1 ? k_f16 : v_f16;
   if (fdst) *reinterpret_cast<u32x4*>(fdst + (int64_t)h * f16_head_stride + pos * D + d0) = ov;
   if (d0 == 0) (part == 1 ? ks : vs)[(int64_t)h * s_len + pos] = f2h(sc);
 }
@@ -342,14 +346,15 @@ extern "C" int lemoq_qk_norm_rope_kv_i8_rows(const uint16_t* qkv, int64_t rows, 
                                              int64_t code_head_stride, int64_t s_len,
                                              uint16_t* k_f16, uint16_t* v_f16,
                                              int64_t f16_head_stride, float clip_qkv, void* stream) {
-  if (!qkv || !q_norm_w || !k_norm_w || !cos_tab || !sin_tab || !q_out || !kc || !ks || !vc ||
-      !vs)
-    return LEMOQ_ERR_NULL;
+  if (!qkv || !q_norm_w || !k_norm_w || !cos_tab || !sin_tab || !q_out) return LEMOQ_ERR_NULL;
+  // KV-INT8 rows (all four buffers), or, with none of them, the fp16 rows only
+  const bool i8 = kc || ks || vc || vs;
+  if (i8 ? (!kc || !ks || !vc || !vs) : (!k_f16 || !v_f16)) return LEMOQ_ERR_NULL;
   if (heads <= 0 || heads > 4096 || heads * head_dim > 65536) return LEMOQ_ERR_SHAPE;
   if (head_dim != 64 && head_dim != 128 && head_dim != 256) return LEMOQ_ERR_UNSUPPORTED;
   if (!(clip_qkv >= 0.0f)) return LEMOQ_ERR_SHAPE;  // negative or NaN bound
   if (!lemoq_aligned16(qkv)) return LEMOQ_ERR_ALIGN;
-  if (s_len <= 0 || code_head_stride < s_len * head_dim) return LEMOQ_ERR_SHAPE;
+  if (s_len <= 0 || (i8 && code_head_stride < s_len * head_dim)) return LEMOQ_ERR_SHAPE;
   if ((k_f16 || v_f16) && f16_head_stride < s_len * head_dim) return LEMOQ_ERR_SHAPE;
   // every row's slot must exist: the cos/sin tables and the caches hold s_len positions
   if (rows <= 0 || rows > 0x7fffffffLL || pos0 < 0 || pos0 + rows > s_len) return LEMOQ_ERR_SHAPE;

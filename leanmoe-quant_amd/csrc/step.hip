@@ -1,11 +1,12 @@
 // Native decode-step executor: enqueues one whole OLMoE decode step of the
-// canonical cell (w8a16 attention + experts, W8 lm_head, KV-INT8 cache) on a
-// stream, ready to be captured into a hipGraph by the caller.
+// canonical cell (w8a16 attention + experts, W8 lm_head, KV-INT8 cache; or the
+// fp16 cache with kv_fp16) on a stream, ready to be captured into a hipGraph
+// by the caller.
 //
 // Per layer (6 launches):
 //   1 gemv_w8_fused   input RMSNorm (+ embedding gather on layer 0) -> packed q|k|v
-//   2 attn_split_fused q_norm/k_norm, RoPE at *pos, KV-INT8 write of slot *pos,
-//                     split-KV partials over [0, *pos]
+//   2 attn_split_fused q_norm/k_norm, RoPE at *pos, KV-INT8 (or fp16) write of
+//                     slot *pos, split-KV partials over [0, *pos]
 //   3 attn_merge_o_proj  LSE merge of each block's 4 heads + their share of
 //                     o_proj -> fp32 partial sums per head group
 //   4 router_logits_resid  o = fp16(sum of partials), h_mid = fp16(o + h),
@@ -60,6 +61,7 @@ enum AttnPath { kAttnFusedOut, kAttnThree };
 // Every rule of every launch of the step, before anything is enqueued.
 int validate(const LemoqOlmoeStep* p, AttnPath* path) {
   if (!p || !p->layers) return LEMOQ_ERR_NULL;
+  if (p->kv_fp16 != 0 && p->kv_fp16 != 1) return LEMOQ_ERR_SHAPE;
   if (!p->embed || !p->final_norm || !p->lm_codes || !p->lm_scale || !p->cos_tab ||
       !p->sin_tab || !p->token || !p->pos || !p->filled || !p->h || !p->xn || !p->qkv ||
       !p->q_rot || !p->attn || !p->part_m || !p->part_l || !p->part_acc || !p->top_w ||
@@ -92,7 +94,7 @@ int validate(const LemoqOlmoeStep* p, AttnPath* path) {
     const LemoqOlmoeLayer& w = p->layers[L];
     if (!w.ln_in || !w.ln_post || !w.q_norm || !w.k_norm || !w.qkv_codes || !w.qkv_scale ||
         !w.o_codes || !w.o_scale || !w.router || !w.gu_codes || !w.gu_scale || !w.dn_codes ||
-        !w.dn_scale || !w.kc || !w.ks || !w.vc || !w.vs)
+        !w.dn_scale || !w.kc || !w.vc || (!p->kv_fp16 && (!w.ks || !w.vs)))
       return LEMOQ_ERR_NULL;
     if (!a16(w.qkv_codes) || !a16(w.o_codes) || !a16(w.gu_codes) || !a16(w.dn_codes) || !a16(w.kc) ||
         !a16(w.vc) || !a16(w.router) || !a16(w.ln_post))
@@ -136,11 +138,19 @@ extern "C" int lemoq_olmoe_decode_step(const LemoqOlmoeStep* p, void* stream) {
     LEMOQ_TRY(lemoq_gemv_w8_fused(first ? p->embed : p->h, first ? p->token : nullptr, p->vocab,
                                   w.ln_in, p->eps, first ? p->h : nullptr, w.qkv_codes,
                                   w.qkv_scale, 3 * HD, H, p->group, nullptr, p->qkv, stream));
-    // 2. q/k norm, RoPE, KV-INT8 write at slot *pos, split-KV partials.
-    LEMOQ_TRY(lemoq_attn_split_fused_i8(p->qkv, p->heads, D, w.q_norm, w.k_norm, p->eps,
-                                        p->cos_tab, p->sin_tab, p->pos, w.kc, w.ks, w.vc, w.vs,
-                                        S * D, S, p->num_splits, p->qk_scale, p->part_m,
-                                        p->part_l, p->part_acc, p->clip_qkv, stream));
+    // 2. q/k norm, RoPE, cache write at slot *pos, split-KV partials.
+    if (p->kv_fp16)
+      LEMOQ_TRY(lemoq_attn_split_fused_f16(p->qkv, p->heads, D, w.q_norm, w.k_norm, p->eps,
+                                           p->cos_tab, p->sin_tab, p->pos,
+                                           reinterpret_cast<uint16_t*>(w.kc),
+                                           reinterpret_cast<uint16_t*>(w.vc), S * D, S,
+                                           p->num_splits, p->qk_scale, p->part_m, p->part_l,
+                                           p->part_acc, p->clip_qkv, stream));
+    else
+      LEMOQ_TRY(lemoq_attn_split_fused_i8(p->qkv, p->heads, D, w.q_norm, w.k_norm, p->eps,
+                                          p->cos_tab, p->sin_tab, p->pos, w.kc, w.ks, w.vc, w.vs,
+                                          S * D, S, p->num_splits, p->qk_scale, p->part_m,
+                                          p->part_l, p->part_acc, p->clip_qkv, stream));
     if (path == kAttnFusedOut) {
       // 3. LSE merge + o_proj partials per group of 4 heads.
       LEMOQ_TRY(lemoq_attn_merge_o_proj_w8(p->part_m, p->part_l, p->part_acc, p->heads,

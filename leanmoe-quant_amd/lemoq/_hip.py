@@ -19,7 +19,7 @@ LIB_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib")
 LIB_NAME = "liblemoq_hip.so"
 LIB_PATH = os.path.join(LIB_DIR, LIB_NAME)
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -105,6 +105,7 @@ class LemoqOlmoeStep(ctypes.Structure):
         ("am_len", _I64),
         ("o_part", _P),
         ("h_mid", _P),
+        ("kv_fp16", _I64),
     ]
 
 
@@ -179,6 +180,10 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "lemoq_attn_split_fused_i8": (
         _I,
         [_P, _I64, _I64, _P, _P, _F, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _F, _P, _P, _P, _F, _P],
+    ),
+    "lemoq_attn_split_fused_f16": (
+        _I,
+        [_P, _I64, _I64, _P, _P, _F, _P, _P, _P, _P, _P, _I64, _I64, _I64, _F, _P, _P, _P, _F, _P],
     ),
     "lemoq_moe_gate_up_w8_routed": (
         _I,

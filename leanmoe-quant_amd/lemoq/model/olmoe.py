@@ -1,4 +1,4 @@
-"""OLMoE decode-step module on the HIP kernels: weights, KV-INT8 cache, session.
+"""OLMoE decode-step module on the HIP kernels: weights, KV cache, session.
 
 This replaces the reference's HF-patched model + ``StaticCacheDecodeSession``
 (``benchmarks/cudagraph.py:511-820``) for the canonical cell
@@ -11,7 +11,9 @@ This replaces the reference's HF-patched model + ``StaticCacheDecodeSession``
 * ``OlmoeW8Weights.random(shape, seed)`` — seeded random init generated and
   RTN-w8-quantized on the device (attention q|k|v packed row-wise, o_proj,
   experts, lm_head); router, embedding and norm weights stay fp16.
-* ``DecodeSession`` — fixed-address KV-INT8 cache and step buffers, the step
+* ``DecodeSession`` — fixed-address KV cache (KV-INT8, or fp16 rows with
+  ``kv_cache="fp16"``: the same cell with KV-INT8 off, ``attn_decode.py:930-948,
+  999-1008``) and step buffers, the step
   enqueued by one native call (``lemoq_olmoe_decode_step``), captured once
   into a hipGraph (``torch.cuda.CUDAGraph``) and replayed.  Greedy selection
   and the position advance run on the device, so consecutive replays need no
@@ -22,7 +24,8 @@ This replaces the reference's HF-patched model + ``StaticCacheDecodeSession``
 Layout in HBM (per layer): ``qkv_codes`` (3*heads*D, H) int8 with fp16 scales
 (3*heads*D, H/g); ``o_codes`` (H, heads*D); ``gu_codes`` (E, 2F, H) and
 ``dn_codes`` (E, H, F) int8 with per-group fp16 scales; ``kc``/``vc`` (heads, S, D)
-int8 and ``ks``/``vs`` (heads, S) fp16 for S = max_seq cache slots.
+int8 and ``ks``/``vs`` (heads, S) fp16 for S = max_seq cache slots (the fp16
+cache: ``k``/``v`` (heads, S, D) fp16).
 """
 
 from __future__ import annotations
@@ -36,9 +39,12 @@ import torch
 
 from lemoq import _hip
 
-__all__ = ["OlmoeShape", "OLMOE_1B_7B", "OlmoeW8Weights", "LayerW8", "DecodeSession"]
+__all__ = ["OlmoeShape", "OLMOE_1B_7B", "OlmoeW8Weights", "LayerW8", "DecodeSession", "KV_CACHE_KINDS"]
 
 LOG2E = 1.4426950408889634
+# The decode cache kinds: "int8" (KV-INT8 codes + fp16 per-token scales, the
+# canonical cell) and "fp16" (the rows as they are: the cell with KV-INT8 off).
+KV_CACHE_KINDS = ("int8", "fp16")
 # Split-KV blocks per head of the step's attention: one block per 64 cache
 # slots, at least 2, and at most one wave of blocks over the chip
 # (heads * splits <= compute units; 16 splits per head for OLMoE's 16 heads on
@@ -196,13 +202,15 @@ class OlmoeW8Weights:
 
 
 class DecodeSession:
-    """Static-shape decode session over a KV-INT8 cache, captured as one hipGraph step.
+    """Static-shape decode session over a KV cache, captured as one hipGraph step.
 
     Mirrors ``StaticCacheDecodeSession`` (``benchmarks/cudagraph.py:511-820``):
     ``prefill()``, ``capture()``, ``replay()``, ``decode_eager()``,
     ``set_position()``, ``logits_cpu()``, ``reset()``.  ``prompt_ids`` is a 1-D
     sequence of token ids (the canonical prompt is ``ctx`` ones); the cache has
-    ``ctx + max_new_tokens`` slots.
+    ``ctx + max_new_tokens`` slots.  ``kv_cache``: ``"int8"`` (KV-INT8, the
+    canonical cell) or ``"fp16"`` (KV-INT8 off: the attention reads the fp16
+    rows the step writes, as the reference does without its int8 mirror).
     """
 
     def __init__(
@@ -212,6 +220,7 @@ class DecodeSession:
         *,
         max_new_tokens: int,
         num_splits: int | None = None,
+        kv_cache: str = "int8",
     ) -> None:
         from lemoq.kernels.attn_decode import resolve_num_splits  # noqa: PLC0415
         from lemoq.kernels.rope import rotary_cos_sin  # noqa: PLC0415
@@ -226,6 +235,9 @@ class DecodeSession:
             raise ValueError("prompt token ids must lie in [0, vocab)")
         if max_new_tokens < 1:
             raise ValueError("max_new_tokens must be >= 1")
+        if kv_cache not in KV_CACHE_KINDS:
+            raise ValueError("kv_cache must be one of %s, got %r" % (KV_CACHE_KINDS, kv_cache))
+        self.kv_cache = kv_cache
         self.weights = weights
         self.shape = s
         self.device = dev
@@ -241,6 +253,10 @@ class DecodeSession:
         f16 = dict(dtype=torch.float16, device=dev)
         self.kv = []
         for _ in range(s.layers):
+            if kv_cache == "fp16":
+                self.kv.append({"k": torch.zeros((s.heads, S, D), **f16),
+                                "v": torch.zeros((s.heads, S, D), **f16)})
+                continue
             self.kv.append(
                 {
                     "kc": torch.zeros((s.heads, S, D), **i8),
@@ -291,8 +307,11 @@ class DecodeSession:
                 if not t.is_contiguous() or t.device != dev:
                     raise ValueError("layer %d weight %s must be contiguous on %s" % (i, name, dev))
                 setattr(ls, name, P(t))
-            for name in ("kc", "ks", "vc", "vs"):
-                setattr(ls, name, P(kv[name]))
+            if kv_cache == "fp16":  # fp16 rows behind kc / vc, no scales
+                ls.kc, ls.vc, ls.ks, ls.vs = P(kv["k"]), P(kv["v"]), None, None
+            else:
+                for name in ("kc", "ks", "vc", "vs"):
+                    setattr(ls, name, P(kv[name]))
         st = _hip.LemoqOlmoeStep()
         st.hidden, st.heads, st.head_dim = s.hidden, s.heads, s.head_dim
         st.ffn, st.num_experts, st.top_k = s.ffn, s.num_experts, s.top_k
@@ -313,6 +332,7 @@ class DecodeSession:
                      "h_mid"):
             setattr(st, name, P(getattr(self, name)))
         st.am_len = n_parts
+        st.kv_fp16 = int(kv_cache == "fp16")
         self._step = st
         self.graph: Any = None
         self.graph_multi: Any = None  # steps_per_graph decode steps in one graph (capture(steps_per_graph=K))
@@ -440,7 +460,7 @@ class DecodeSession:
         return self.logits
 
     def prefill(self, mode: str = "batched", *, kv_f16: list | None = None) -> int:
-        """Fill the KV-INT8 cache with the prompt and seed the first decode token; returns it.
+        """Fill the KV cache with the prompt and seed the first decode token; returns it.
 
         ``mode="batched"`` (default) is the reference's prefill: one multi-token
         forward (``lemoq.model.prefill.prefill_prompt``, the path of
@@ -481,6 +501,7 @@ class DecodeSession:
         return self.logits.detach().to("cpu").clone()
 
     def kv_cpu(self) -> list[dict[str, Any]]:
-        """Host copy of every layer's KV-INT8 cache (for the CPU oracle)."""
+        """Host copy of every layer's KV cache (for the CPU oracle): kc/ks/vc/vs for
+        KV-INT8, k/v for the fp16 cache."""
         torch.cuda.synchronize(self.device)
         return [{k: v.detach().to("cpu").clone() for k, v in kv.items()} for kv in self.kv]

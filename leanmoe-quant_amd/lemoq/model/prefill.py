@@ -59,7 +59,9 @@ def prefill_prompt(weights: Any, tokens: Any, kv: list, cos_tab: Any, sin_tab: A
     """Prefill ``tokens`` (int64 (T,) on the device) at positions 0..T-1.
 
     ``kv``: per layer the KV-INT8 cache dict (kc (heads, S, D) int8, ks (heads, S)
-    fp16, vc, vs) with S = ``max_seq``; ``cos_tab``/``sin_tab`` (S, D) fp16;
+    fp16, vc, vs), or the fp16 cache dict (k, v (heads, S, D) fp16: KV-INT8 off,
+    the rows written as they are), with S = ``max_seq``; ``cos_tab``/``sin_tab``
+    (S, D) fp16;
     ``logits`` (vocab,) fp16 receives the last position's logits.  ``step``: the
     decode session's device state that the greedy pick advances, as
     ``lemoq_argmax_advance`` does (``token``, ``pos`` holding T - 1, ``filled``,
@@ -67,8 +69,8 @@ def prefill_prompt(weights: Any, tokens: Any, kv: list, cos_tab: Any, sin_tab: A
     ``last_row_only``: run the last layer after its KV rows on the last position
     only (the default; False runs it on every position, as the other layers).
     ``kv_f16``: when a list, receives per layer copies of the fp16 k (after k_norm
-    and RoPE) and v rows that were quantised into the cache, each (heads, T, D)
-    (for parity checks of the KV bytes against their inputs).
+    and RoPE) and v rows that were written (or quantised) into the cache, each
+    (heads, T, D) (for parity checks of the KV bytes against their inputs).
     """
     s = weights.shape
     dev = weights.device
@@ -95,8 +97,10 @@ def prefill_prompt(weights: Any, tokens: Any, kv: list, cos_tab: Any, sin_tab: A
     xn = torch.empty((T, H), **f16)
     qkv = torch.empty((T, 3 * HD), **f16)
     q = torch.empty((T, HD), **f16)
-    k16 = torch.empty((NH, S, D), **f16)
-    v16 = torch.empty((NH, S, D), **f16)
+    fp16_cache = "k" in kv[0]
+    if not fp16_cache:  # fp16 rows for the prompt's attention, then quantised into the cache
+        k16 = torch.empty((NH, S, D), **f16)
+        v16 = torch.empty((NH, S, D), **f16)
     attn = torch.empty((T, HD), **f16)
     # the router's 64 outputs give few output tiles: K is cut into up to 8 ranges
     # whose fp32 partials the routing launch sums; fp16 logits only without a split
@@ -123,8 +127,13 @@ def prefill_prompt(weights: Any, tokens: Any, kv: list, cos_tab: Any, sin_tab: A
         # xn holds this layer's input norm: the previous layer's combine wrote it
         _hip.call("lemoq_gemm_w8", P(xn), T, H, H, None, P(L.qkv_codes), P(L.qkv_scale), 3 * HD, g,
                   P(qkv), 3 * HD, None, 0, st)
+        if fp16_cache:  # the cache is the attention's k/v (no KV-INT8 rows)
+            k16, v16 = c["k"], c["v"]
+            i8 = (None, None, None, None)
+        else:
+            i8 = (P(c["kc"]), P(c["ks"]), P(c["vc"]), P(c["vs"]))
         _hip.call("lemoq_qk_norm_rope_kv_i8_rows", P(qkv), T, NH, D, P(L.q_norm), P(L.k_norm), float(s.eps),
-                  P(cos_tab), P(sin_tab), 0, P(q), P(c["kc"]), P(c["ks"]), P(c["vc"]), P(c["vs"]), S * D, S,
+                  P(cos_tab), P(sin_tab), 0, P(q), *i8, S * D, S,
                   P(k16), P(v16), S * D, math.inf if s.clip_qkv is None else float(s.clip_qkv), st)
         if kv_f16 is not None:
             kv_f16.append((k16[:, :T].clone(), v16[:, :T].clone()))

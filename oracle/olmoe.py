@@ -8,7 +8,10 @@ as patched by the reference's canonical cell:
 * packed q|k|v via the fused w8 GEMV (``src/lemoq/kernels/packed_qkv.py:78-96``);
   q_norm/k_norm over heads*D, fused RoPE (``rope.py:154-203``);
 * KV-INT8 write of the new row then split-KV INT8 attention over
-  ``[0, pos+1)`` (``attn_decode.py:952-1000``, ``kv_int8.py:223-257``);
+  ``[0, pos+1)`` (``attn_decode.py:952-1000``, ``kv_int8.py:223-257``); or, with
+  ``kv_cache="fp16"`` (KV-INT8 off), the fp16 row written as it is
+  (``kv_direct_write``, ``attn_decode.py:930-948``) and the fp16 split-KV
+  attention over ``[0, pos+1)`` (``attn_decode.py:999-1008``);
 * o_proj, fp16 residual add; post-attention norm; ``_route``; grouped w8 MoE
   (``moe_grouped_quant.py:562-601``); fp16 residual add;
 * final norm, W8 lm_head; greedy argmax (first index on ties).
@@ -117,9 +120,11 @@ def random_host_weights(shape: Shape, seed: int = 0) -> HostWeights:
 
 
 class OracleDecoder:
-    """CPU decode step with its own KV-INT8 cache of ``max_seq`` slots."""
+    """CPU decode step with its own KV cache of ``max_seq`` slots: KV-INT8 (kc, ks,
+    vc, vs per layer) or, with ``kv_cache="fp16"``, fp16 rows (k, v per layer).  A
+    ``kv`` list given in either form sets the kind."""
 
-    def __init__(self, weights: Any, max_seq: int, *, kv: list | None = None) -> None:
+    def __init__(self, weights: Any, max_seq: int, *, kv: list | None = None, kv_cache: str = "int8") -> None:
         self.w = weights
         s = weights.shape
         self.s = s
@@ -130,6 +135,19 @@ class OracleDecoder:
         self.lm_w = ops.dequant_w8(weights.lm_codes, weights.lm_scale, g)
         cos, sin = ops.rotary_cos_sin(torch.arange(self.max_seq), s.head_dim, s.rope_theta)
         self.cos, self.sin = cos, sin
+        if kv is not None:
+            kv_cache = "fp16" if "k" in kv[0] else "int8"
+        if kv_cache not in ("int8", "fp16"):
+            raise ValueError("kv_cache must be 'int8' or 'fp16', got %r" % (kv_cache,))
+        self.kv_cache = kv_cache
+        if kv is None and kv_cache == "fp16":
+            kv = [
+                {
+                    "k": torch.zeros((s.heads, self.max_seq, s.head_dim), dtype=torch.float16),
+                    "v": torch.zeros((s.heads, self.max_seq, s.head_dim), dtype=torch.float16),
+                }
+                for _ in range(s.layers)
+            ]
         if kv is None:
             kv = [
                 {
@@ -174,10 +192,16 @@ class OracleDecoder:
             q, k, v = ops.clip_qkv(q, k, v, getattr(s, "clip_qkv", None))
             q = ops.rope_fused(q.reshape(NH, D), cos, sin)
             k = ops.rope_fused(k.reshape(NH, D), cos, sin)
-            self._quant_into(kv["kc"], kv["ks"], pos, k)
-            self._quant_into(kv["vc"], kv["vs"], pos, v.reshape(NH, D))
-            attn = ops.int8_attention_folded(q, kv["kc"], kv["ks"], kv["vc"], kv["vs"], pos + 1,
-                                             scale=qk_scale).to(torch.float16).reshape(-1)
+            if self.kv_cache == "fp16":
+                kv["k"][:, pos, :] = k
+                kv["v"][:, pos, :] = v.reshape(NH, D)
+                attn = ops.split_kv_oracle(q, kv["k"], kv["v"], pos + 1, num_splits=1,
+                                           scale=qk_scale).to(torch.float16).reshape(-1)
+            else:
+                self._quant_into(kv["kc"], kv["ks"], pos, k)
+                self._quant_into(kv["vc"], kv["vs"], pos, v.reshape(NH, D))
+                attn = ops.int8_attention_folded(q, kv["kc"], kv["ks"], kv["vc"], kv["vs"], pos + 1,
+                                                 scale=qk_scale).to(torch.float16).reshape(-1)
             o = self._linear(attn, self.o_w[li])
             h = r + o
             r = h
@@ -219,7 +243,7 @@ class OracleDecoder:
 
 
 def oracle_prefill(weights: Any, tokens: Any, max_seq: int, *, all_logits: bool = False,
-                   kv_f16: list | None = None, kv_layers: int | None = None):
+                   kv_f16: list | None = None, kv_layers: int | None = None, kv_cache: str = "int8"):
     """The reference's prefill of the prompt ``tokens`` (positions 0..T-1) on the CPU.
 
     ``StaticCacheDecodeSession.prefill`` (``benchmarks/cudagraph.py:578-599``) runs the
@@ -238,12 +262,14 @@ def oracle_prefill(weights: Any, tokens: Any, max_seq: int, *, all_logits: bool 
       (``moe_static.py:262-283,329-371``) -> ``ops.linear_f16``, ``ops.route_logits``,
       ``ops.moe_prefill_w8``;
     * the KV-INT8 cache is the bulk quantisation of the fp16 k/v rows
-      (``kv_int8.py:127-162``) -> ``oracle.quant.kv_quantize_rows``;
+      (``kv_int8.py:127-162``) -> ``oracle.quant.kv_quantize_rows``; with
+      ``kv_cache="fp16"`` (KV-INT8 off) the cache holds those fp16 rows;
     * logits: final norm and the W8 lm_head (separate arm: T > 1 rows reach it).
 
     Returns ``(logits, kv)``: fp16 logits of the last position (``(T, vocab)`` with
     ``all_logits``), and per layer the KV-INT8 cache dict (kc, ks, vc, vs) of ``max_seq``
-    slots with slots 0..T-1 filled (the rest codes 0, scales 1).  ``kv_f16``, when a
+    slots with slots 0..T-1 filled (the rest codes 0, scales 1), or the fp16 cache dict
+    (k, v; the rest zeros).  ``kv_f16``, when a
     list, receives per layer the fp16 k (after k_norm and RoPE) and v rows that were
     quantised, each (heads, T, D).  ``kv_layers`` stops after that many layers' KV rows
     (logits are then None).
@@ -269,16 +295,24 @@ def oracle_prefill(weights: Any, tokens: Any, max_seq: int, *, all_logits: bool 
         v = qkv[:, 2 * HD:].reshape(T, NH, D)
         q, k, v = ops.clip_qkv(q, k, v, getattr(s, "clip_qkv", None))
         q, k = ops.rope_hf(q, k, cos, sin)
-        cache = {
-            "kc": torch.zeros((NH, max_seq, D), dtype=torch.int8),
-            "ks": torch.ones((NH, max_seq), dtype=torch.float16),
-            "vc": torch.zeros((NH, max_seq, D), dtype=torch.int8),
-            "vs": torch.ones((NH, max_seq), dtype=torch.float16),
-        }
-        for name, rows in (("k", k), ("v", v)):
-            codes, scales = oq.kv_quantize_rows(rows.reshape(T * NH, D).numpy())
-            cache[name + "c"][:, :T, :] = torch.from_numpy(codes).reshape(T, NH, D).transpose(0, 1)
-            cache[name + "s"][:, :T] = torch.from_numpy(scales).reshape(T, NH).transpose(0, 1)
+        if kv_cache == "fp16":
+            cache = {
+                "k": torch.zeros((NH, max_seq, D), dtype=torch.float16),
+                "v": torch.zeros((NH, max_seq, D), dtype=torch.float16),
+            }
+            cache["k"][:, :T, :] = k.transpose(0, 1)
+            cache["v"][:, :T, :] = v.transpose(0, 1)
+        else:
+            cache = {
+                "kc": torch.zeros((NH, max_seq, D), dtype=torch.int8),
+                "ks": torch.ones((NH, max_seq), dtype=torch.float16),
+                "vc": torch.zeros((NH, max_seq, D), dtype=torch.int8),
+                "vs": torch.ones((NH, max_seq), dtype=torch.float16),
+            }
+            for name, rows in (("k", k), ("v", v)):
+                codes, scales = oq.kv_quantize_rows(rows.reshape(T * NH, D).numpy())
+                cache[name + "c"][:, :T, :] = torch.from_numpy(codes).reshape(T, NH, D).transpose(0, 1)
+                cache[name + "s"][:, :T] = torch.from_numpy(scales).reshape(T, NH).transpose(0, 1)
         kv_out.append(cache)
         if kv_f16 is not None:
             kv_f16.append((k.transpose(0, 1).contiguous(), v.transpose(0, 1).contiguous()))

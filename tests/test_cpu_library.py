@@ -90,6 +90,30 @@ def test_argument_rejection_happens_before_any_launch():
                                             fake, fake, 16 * 128, 12, None, None, 0, None, bad, None) == -2
         assert lib.lemoq_attn_split_fused_i8(fake, 16, 128, fake, fake, 1e-5, fake, fake, fake, fake, fake, fake,
                                              fake, 1100 * 128, 1100, 16, 0.1, fake, fake, fake, bad, None) == -2
+        assert lib.lemoq_attn_split_fused_f16(fake, 16, 128, fake, fake, 1e-5, fake, fake, fake, fake, fake,
+                                              1100 * 128, 1100, 16, 0.1, fake, fake, fake, bad, None) == -2
+    f16 = lambda *a: lib.lemoq_attn_split_fused_f16(fake, *a)  # noqa: E731
+    assert f16(16, 128, fake, fake, 1e-5, fake, fake, fake, None, fake, 1100 * 128, 1100, 16, 0.1, fake, fake,
+               fake, math.inf, None) == -1                                          # no k cache
+    assert f16(16, 96, fake, fake, 1e-5, fake, fake, fake, fake, fake, 1100 * 96, 1100, 16, 0.1, fake, fake,
+               fake, math.inf, None) == -3                                          # head_dim
+    assert f16(16, 128, fake, fake, 1e-5, fake, fake, fake, fake, fake, 1000 * 128, 1100, 16, 0.1, fake, fake,
+               fake, math.inf, None) == -2                                          # head stride < s_len * D
+    assert f16(16, 128, fake, fake, 1e-5, fake, fake, fake, fake + 2, fake, 1100 * 128, 1100, 16, 0.1, fake, fake,
+               fake, math.inf, None) == -4                                          # k cache alignment
+    assert f16(16, 128, fake, fake, 1e-5, fake, fake, fake, fake, fake, 1100 * 128 + 4, 1100, 16, 0.1, fake,
+               fake, fake, math.inf, None) == -4                                    # rows 16-byte aligned
+    # the prefill rows: all four KV-INT8 buffers, or none of them and both fp16 caches
+    rows = lambda kc, ks, kf, vf: lib.lemoq_qk_norm_rope_kv_i8_rows(  # noqa: E731
+        fake, 10, 2, 128, fake, fake, 1e-5, fake, fake, 20, fake, kc, ks, fake, fake, 16 * 128, 12, kf, vf,
+        16 * 128, math.inf, None)
+    assert rows(fake, None, None, None) == -1                                       # half the KV-INT8 buffers
+    assert lib.lemoq_qk_norm_rope_kv_i8_rows(fake, 10, 2, 128, fake, fake, 1e-5, fake, fake, 20, fake, None,
+                                             None, None, None, 16 * 128, 12, fake, None, 16 * 128, math.inf,
+                                             None) == -1                            # fp16 only: v cache missing
+    assert lib.lemoq_qk_norm_rope_kv_i8_rows(fake, 10, 2, 128, fake, fake, 1e-5, fake, fake, 20, fake, None,
+                                             None, None, None, 0, 12, fake, fake, 16 * 128, math.inf,
+                                             None) == -2                            # fp16 only: rows past s_len
     assert lib.lemoq_moe_prefill_max_tiles(8192, 64) == 8192 // 128 + 64
     assert lib.lemoq_moe_prefill_sort(fake, fake, 4097, 8, 64, fake, fake, fake, fake, fake, 10 ** 6, None) == -3
     assert lib.lemoq_moe_prefill_sort(fake, fake, 16, 8, 300, fake, fake, fake, fake, fake, 10 ** 6, None) == -2
@@ -202,3 +226,12 @@ def test_decode_step_rejects_before_any_launch():
     assert lib.lemoq_olmoe_decode_step(ctypes.byref(st), None) == -1
     # unfused attention-output path (no o_part): merge split bound
     assert step(o_part=None, num_splits=2000) == -2
+    # cache kind: 0 or 1 only; the fp16 cache needs no scales, KV-INT8 does
+    assert step(kv_fp16=2) == -2
+    st, layers = _fake_step(kv_fp16=1)
+    layers[0].ks = layers[0].vs = None                      # no scales: fine for fp16 rows,
+    st.h_mid = st.h                                         # so the rule after the layers rejects
+    assert lib.lemoq_olmoe_decode_step(ctypes.byref(st), None) == -2
+    st, layers = _fake_step()
+    layers[0].ks = None                                     # KV-INT8 without its scales
+    assert lib.lemoq_olmoe_decode_step(ctypes.byref(st), None) == -1

@@ -225,3 +225,44 @@ def test_planted_oracle_mistake_fails_the_hf_gate(mistake, monkeypatch):
     monkeypatch.setattr(ops, name, fn)
     ok, (kl, rel) = _passes(ref, _oracle_logits(hw, toks))
     assert not ok, "%s went unnoticed: median KL %.3e, median rel %.4f" % (mistake, kl, rel)
+
+
+# ---------------------------------------------------------------------------
+# The fp16 cache (KV-INT8 off): the new k (normed, rotated) and v rows are
+# written as they are and the fp16 split-KV attention reads [0, pos + 1)
+# (src/lemoq/kernels/attn_decode.py:930-948,999-1008).  HF keeps its cache in
+# the model's dtype, so the same gate holds, and without the KV-INT8 rounding
+# the oracle sits closer to HF than the KV-INT8 oracle does.
+def _oracle_logits_fp16(hw, toks):
+    o = OracleDecoder(hw, max_seq=N_POS + 4, kv_cache="fp16")
+    return torch.stack([o.step(int(t), p).double() for p, t in enumerate(toks)])
+
+
+@pytest.mark.parametrize("seed", [5, 6, 7])
+def test_oracle_fp16_cache_decoder_matches_hf_olmoe(seed):
+    hw, toks, ref = _case(seed)
+    ok, (kl, rel) = _passes(ref, _oracle_logits_fp16(hw, toks))
+    assert ok, "median KL %.3e, median rel %.4f" % (kl, rel)
+    kl8, _ = _stats(ref, _oracle_logits(hw, toks))
+    assert kl <= kl8, "fp16 cache KL %.3e above the KV-INT8 cache's %.3e" % (kl, kl8)
+
+
+def _plant_kv_fp16(kind):
+    def plant(hw):
+        orig = ops.split_kv_oracle
+
+        def attend(q, k, v, filled, **kw):
+            if kind == "new_token_dropped":  # attends over [0, pos) only
+                return orig(q, k, v, filled - 1, **kw) if filled > 1 else orig(q, k, v, filled, **kw)
+            return orig(q, v, k, filled, **kw)  # k and v exchanged
+        return "split_kv_oracle", attend
+    return plant
+
+
+@pytest.mark.parametrize("mistake", ["new_token_dropped", "k_v_swapped"])
+def test_planted_fp16_cache_mistake_fails_the_hf_gate(mistake, monkeypatch):
+    hw, toks, ref = _case(5)
+    name, fn = _plant_kv_fp16(mistake)(hw)
+    monkeypatch.setattr(ops, name, fn)
+    ok, (kl, rel) = _passes(ref, _oracle_logits_fp16(hw, toks))
+    assert not ok, "%s went unnoticed: median KL %.3e, median rel %.4f" % (mistake, kl, rel)

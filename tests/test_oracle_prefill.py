@@ -229,3 +229,30 @@ def test_prefill_kv_rows_hook_matches_the_cache_and_stops_early():
     assert lg is None and len(kv1) == 1 and len(rows1) == 1
     assert all(torch.equal(kv1[0][n], kv[0][n]) for n in ("kc", "ks", "vc", "vs"))
     assert torch.equal(rows1[0][0], rows[0][0]) and torch.equal(rows1[0][1], rows[0][1])
+
+
+def test_prefill_fp16_cache_holds_the_rows_of_the_int8_cache():
+    """``oracle_prefill(kv_cache="fp16")`` keeps the fp16 k/v rows that the KV-INT8
+    prefill quantises (``kv_f16``) at the same slots, zeros past the prompt, and its
+    last logits match HF under the same gate; the fp16-cache decoder stepped over the
+    prompt writes layer 0's rows at the same slots: within 0.5% of the rows' largest
+    value (measured 0.06-0.13%: the fused against the separate linear arm and RoPE
+    rounding), while rows one slot apart differ by over 100%."""
+    hw, toks, ref = _case(6)
+    rows: list = []
+    _, kv8 = oracle_prefill(hw, toks, N_POS + 4, kv_f16=rows)
+    logits, kv = oracle_prefill(hw, toks, N_POS + 4, kv_cache="fp16", all_logits=True)
+    for li in range(SHAPE.layers):
+        assert torch.equal(kv[li]["k"][:, :N_POS], rows[li][0])
+        assert torch.equal(kv[li]["v"][:, :N_POS], rows[li][1])
+        assert not kv[li]["k"][:, N_POS:].any() and not kv[li]["v"][:, N_POS:].any()
+    kl, rel = _stats(ref, logits.double())
+    assert kl < MED_KL and rel < MED_REL, (kl, rel)
+    o = OracleDecoder(hw, N_POS + 4, kv_cache="fp16")
+    for p, t in enumerate(toks):
+        o.step(int(t), p)
+    for name in ("k", "v"):
+        a, b = kv[0][name][:, :N_POS].double(), o.kv[0][name][:, :N_POS].double()
+        top = float(a.abs().max())
+        assert float((a - b).abs().max()) <= 5e-3 * top, name
+        assert float((a[:, 1:] - b[:, :-1]).abs().max()) > 0.5 * top, name
