@@ -357,14 +357,15 @@ def time_decode(torch, w, ctx: int, steps: int, warmup: int, extra: int):
     from lemoq.model.olmoe import DecodeSession
 
     groups = max(8, steps // MULTI_STEPS)
-    sess = DecodeSession(w, [1] * ctx, max_new_tokens=warmup + 2 * steps + groups * MULTI_STEPS + extra + 4)
+    sess = DecodeSession(w, [1] * ctx, max_new_tokens=warmup + 2 * steps + groups * MULTI_STEPS + extra + 4,
+                         kv_cache="int8")
     sess.capture()
     ttft = measure_prefill(torch, sess)
     log("ctx %d: batched prefill (TTFT) p50 %.3f ms over %d runs" % (ctx, ttft["p50"], ttft["runs"]))
     # TTFT on a seeded random prompt too: tokens route to all 64 experts, so the
     # prefill streams every expert's weights (with ctx ones all rows pick the same 8)
     rnd = DecodeSession(w, torch.randint(0, w.shape.vocab, (ctx,), generator=torch.Generator().manual_seed(ctx)),
-                        max_new_tokens=2)
+                        max_new_tokens=2, kv_cache="int8")
     rnd.capture()
     ttft_rnd = measure_prefill(torch, rnd)
     del rnd
@@ -985,7 +986,7 @@ def main(argv=None) -> int:
     if args.mode == "traffic":
         from lemoq.model.olmoe import DecodeSession
 
-        sess = DecodeSession(w, [1] * args.ctx, max_new_tokens=2)
+        sess = DecodeSession(w, [1] * args.ctx, max_new_tokens=2, kv_cache="int8")
         synthetic_cache(torch, sess, sess.ctx + 1)
         cal = copy_calibration(torch, _hip, flusher)
         kt = kernel_table(torch, _hip, w, sess, flusher, args.kernel_reps, floors=False)
@@ -995,7 +996,7 @@ def main(argv=None) -> int:
     if args.mode == "step":
         from lemoq.model.olmoe import DecodeSession
 
-        sess = DecodeSession(w, [1] * args.ctx, max_new_tokens=args.warmup + args.steps + 1)
+        sess = DecodeSession(w, [1] * args.ctx, max_new_tokens=args.warmup + args.steps + 1, kv_cache="int8")
         sess.capture()
         sess.prefill()
         sess.replay(args.warmup)
@@ -1012,7 +1013,7 @@ def main(argv=None) -> int:
 
         res = {"mode": "prefill"}
         for ctx in [c for c in (args.ctx, args.ctx2) if c]:
-            sess = DecodeSession(w, [1] * ctx, max_new_tokens=2)
+            sess = DecodeSession(w, [1] * ctx, max_new_tokens=2, kv_cache="int8")
             sess.capture()
             res["ctx%d" % ctx] = measure_prefill(torch, sess)
             log("ctx %d: TTFT p50 %.3f ms" % (ctx, res["ctx%d" % ctx]["p50"]))
@@ -1023,7 +1024,7 @@ def main(argv=None) -> int:
     if args.mode == "kernels":
         from lemoq.model.olmoe import DecodeSession
 
-        sess = DecodeSession(w, [1] * args.ctx, max_new_tokens=2)
+        sess = DecodeSession(w, [1] * args.ctx, max_new_tokens=2, kv_cache="int8")
         sess.capture()
         sess.prefill()
         kt = kernel_table(torch, _hip, w, sess, flusher, args.kernel_reps)
@@ -1133,6 +1134,11 @@ def main(argv=None) -> int:
     line["attention_configs"] = cfg
     if fmts is not None:
         line["weight_formats"] = fmts
+    from lemoq.kernels.fusion_switches import fusion_payload_fields  # noqa: PLC0415
+
+    # the reference records its switches in every payload; here all are the fused form, and the
+    # headline runs the KV-INT8 cache whatever LEMOQ_KV_INT8 says (the fp16 cache is `kv_fp16`)
+    line["fusion_switches"] = fusion_payload_fields()
     if kv16 is not None:
         kv16["reference_rtx5090_ms_per_token"] = REFERENCE_RTX5090_KV_F16_MS
         kv16["what"] = ("the same step over the fp16 cache (DecodeSession(kv_cache='fp16'): the reference's cell "

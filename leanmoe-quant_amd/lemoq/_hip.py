@@ -219,6 +219,25 @@ def library_available() -> bool:
     return os.path.exists(LIB_PATH)
 
 
+def unavailable_reason() -> str | None:
+    """Why the HIP operators cannot run here, or None when they can (the library is
+    built, loads with this ABI, and a ROCm device is visible).  Never raises."""
+    if not os.path.exists(LIB_PATH):
+        return "lemoq HIP library not built (%s missing)" % LIB_PATH
+    try:
+        load()
+    except Exception as exc:  # noqa: BLE001
+        return "lemoq HIP library does not load: %s" % exc
+    try:
+        import torch  # noqa: PLC0415
+
+        if not torch.cuda.is_available() or torch.version.hip is None:
+            return "no ROCm device is visible"
+    except Exception as exc:  # noqa: BLE001
+        return "torch is unavailable (%s)" % type(exc).__name__
+    return None
+
+
 def load() -> ctypes.CDLL:
     """Load (once) and type the C-ABI library.  Raises when it is missing."""
     global _LIB

@@ -21,7 +21,7 @@ from typing import Any
 from lemoq import _hip
 
 __all__ = ["DEQUANT_GEMM_CONFIGS", "dequant_gemm_fused", "dequant_gemm_separate", "linear_f16",
-           "fused_available", "warm"]
+           "fused_available", "unavailable_reason", "warm"]
 
 # The HIP kernel's tiling is chosen inside the library from N (rows per wave)
 # and K (1 KB chunks per row); no tunables are exposed.  Kept for call-site
@@ -29,6 +29,11 @@ __all__ = ["DEQUANT_GEMM_CONFIGS", "dequant_gemm_fused", "dequant_gemm_separate"
 DEQUANT_GEMM_CONFIGS: dict[str, dict[str, int]] = {"dequant_gemm": {}}
 
 MAX_PADDED_K = 8192
+
+
+def unavailable_reason() -> str | None:
+    """Why ``fused_available()`` is False, or None when it is True."""
+    return _hip.unavailable_reason()
 
 
 def fused_available() -> bool:

@@ -35,6 +35,7 @@ from lemoq import _hip
 __all__ = [
     "FusedExperts",
     "QuantFusedExperts",
+    "dequantize_fused_experts",
     "grouped_moe_forward_quant",
     "quant_launch_plan",
     "quantize_fused_experts",
@@ -179,6 +180,14 @@ def quantized_grouped_available() -> bool:
         return _hip.library_available() and bool(torch.cuda.is_available())
     except Exception:  # noqa: BLE001
         return False
+
+
+def dequantize_fused_experts(q: "QuantFusedExperts", dtype: Any = None) -> FusedExperts:
+    """``QuantFusedExperts`` -> ``FusedExperts`` with the dense weights (fp32, or
+    ``dtype``), dequantised on the device (``QuantFusedExperts.dequant_gate_up`` /
+    ``dequant_down``), as the reference's ``dequantize_fused_experts``
+    (``moe_grouped_quant.py:247-254``)."""
+    return FusedExperts(gate_up=q.dequant_gate_up(dtype=dtype), down=q.dequant_down(dtype=dtype))
 
 
 def _cdiv(a: int, b: int) -> int:

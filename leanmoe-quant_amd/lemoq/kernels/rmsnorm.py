@@ -13,10 +13,15 @@ from typing import Any
 
 from lemoq import _hip
 
-__all__ = ["RMSNORM_CONFIG", "rms_norm_fused", "fused_available", "warm"]
+__all__ = ["RMSNORM_CONFIG", "rms_norm_fused", "fused_available", "unavailable_reason", "warm"]
 
 RMSNORM_CONFIG: dict[str, int] = {}
 MAX_HIDDEN = 8192
+
+
+def unavailable_reason() -> str | None:
+    """Why ``fused_available()`` is False, or None when it is True."""
+    return _hip.unavailable_reason()
 
 
 def fused_available() -> bool:

@@ -210,7 +210,9 @@ class DecodeSession:
     sequence of token ids (the canonical prompt is ``ctx`` ones); the cache has
     ``ctx + max_new_tokens`` slots.  ``kv_cache``: ``"int8"`` (KV-INT8, the
     canonical cell) or ``"fp16"`` (KV-INT8 off: the attention reads the fp16
-    rows the step writes, as the reference does without its int8 mirror).
+    rows the step writes, as the reference does without its int8 mirror);
+    None follows the reference's ``kv_int8`` switch (``LEMOQ_KV_INT8``, on by
+    default; ``lemoq.kernels.fusion_switches``).
     """
 
     def __init__(
@@ -220,7 +222,7 @@ class DecodeSession:
         *,
         max_new_tokens: int,
         num_splits: int | None = None,
-        kv_cache: str = "int8",
+        kv_cache: str | None = None,
     ) -> None:
         from lemoq.kernels.attn_decode import resolve_num_splits  # noqa: PLC0415
         from lemoq.kernels.rope import rotary_cos_sin  # noqa: PLC0415
@@ -235,6 +237,11 @@ class DecodeSession:
             raise ValueError("prompt token ids must lie in [0, vocab)")
         if max_new_tokens < 1:
             raise ValueError("max_new_tokens must be >= 1")
+        from lemoq.kernels.fusion_switches import require_built  # noqa: PLC0415
+
+        switches = require_built()  # refuses a switch set to an arm this build does not have
+        if kv_cache is None:  # the reference's kv_int8 switch (LEMOQ_KV_INT8, default on)
+            kv_cache = "int8" if switches["kv_int8"] else "fp16"
         if kv_cache not in KV_CACHE_KINDS:
             raise ValueError("kv_cache must be one of %s, got %r" % (KV_CACHE_KINDS, kv_cache))
         self.kv_cache = kv_cache

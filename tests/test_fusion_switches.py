@@ -1,0 +1,43 @@
+"""The fusion-switch mirror (``lemoq.kernels.fusion_switches``, the reference's
+``src/lemoq/kernels/fusion_switches.py``): the same switch names, defaults and
+environment overrides; every switch reports its requested state, and a switch
+set to an arm this build does not have is refused, never ignored.  CPU only."""
+
+from __future__ import annotations
+
+import pytest
+
+from lemoq.kernels import fusion_switches as fs
+
+
+def test_names_defaults_and_overrides_match_the_reference():
+    assert sorted(fs.ENV_VARS) == sorted(["fused_rope", "fused_route", "skip_mask_fill", "packed_qkv",
+                                          "kv_direct_write", "lm_head_w8", "kv_int8"])
+    assert fs.ENV_VARS["kv_int8"] == "LEMOQ_KV_INT8" and fs.ENV_VARS["lm_head_w8"] == "LEMOQ_LMHEAD_W8"
+    assert fs.fusion_states({}) == {n: True for n in fs.ENV_VARS}
+    assert fs.fusion_enabled("kv_int8", {"LEMOQ_KV_INT8": "0"}) is False
+    assert fs.fusion_enabled("kv_int8", {"LEMOQ_KV_INT8": "1"}) is True
+    assert fs.fusion_enabled("packed_qkv", {"LEMOQ_PACKED_QKV": "yes"}) is False  # only "1" is on
+    assert fs.fusion_payload_fields({}) == fs.fusion_states({})
+    with pytest.raises(KeyError):
+        fs.fusion_enabled("fused_moe")
+
+
+def test_only_built_arms_are_accepted():
+    assert fs.require_built({})["kv_int8"] is True
+    assert fs.require_built({"LEMOQ_KV_INT8": "0"})["kv_int8"] is False  # the fp16 cache is built
+    with pytest.raises(NotImplementedError, match="packed_qkv"):
+        fs.require_built({"LEMOQ_PACKED_QKV": "0"})
+    with pytest.raises(NotImplementedError, match="LEMOQ_FUSED_ROPE, LEMOQ_LMHEAD_W8"):
+        fs.require_built({"LEMOQ_LMHEAD_W8": "0", "LEMOQ_FUSED_ROPE": "0"})
+
+
+def test_unavailable_reason_names_the_missing_device_here():
+    import torch
+
+    from lemoq.kernels import dequant_gemm, rmsnorm
+
+    reason = rmsnorm.unavailable_reason()
+    assert (reason is None) == rmsnorm.fused_available()
+    if not torch.cuda.is_available():
+        assert reason and dequant_gemm.unavailable_reason() == reason

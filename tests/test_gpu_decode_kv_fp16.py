@@ -181,7 +181,18 @@ def test_c5_fp16_cache_graph_replay_equals_eager_bitwise(ctx, positions, c5_fp16
         assert int(sess.token.item()) == g_next
 
 
-def test_kv_cache_kind_is_checked(dev):
+def test_kv_cache_kind_is_checked(dev, monkeypatch):
+    """An unknown kind is refused; with no kind given the session follows the
+    reference's kv_int8 switch (LEMOQ_KV_INT8), and a switch set to an arm this
+    build does not have (the unfused q|k|v projections) is refused."""
     w = OlmoeW8Weights.random(TINY, seed=1, device=dev)
     with pytest.raises(ValueError):
         DecodeSession(w, [1, 2], max_new_tokens=2, kv_cache="bf16")
+    assert DecodeSession(w, [1, 2], max_new_tokens=2).kv_cache == "int8"
+    monkeypatch.setenv("LEMOQ_KV_INT8", "0")
+    s = DecodeSession(w, [1, 2], max_new_tokens=2)
+    assert s.kv_cache == "fp16" and set(s.kv[0]) == {"k", "v"}
+    assert DecodeSession(w, [1, 2], max_new_tokens=2, kv_cache="int8").kv_cache == "int8"  # explicit wins
+    monkeypatch.setenv("LEMOQ_PACKED_QKV", "0")
+    with pytest.raises(NotImplementedError, match="packed_qkv"):
+        DecodeSession(w, [1, 2], max_new_tokens=2)

@@ -361,3 +361,9 @@ def test_quant_fused_experts_w4_dequant_bit_exact(dev):
         ref = oq.dequant_tile(r["codes_padded"], r["scale"].astype(np.float16).astype(np.float32), None, 64, True)
         assert np.array_equal(got.cpu().numpy().view(np.uint32), ref.view(np.uint32))
     assert tuple(q.dequant_gate_up(torch.float16).shape) == (3, 256, 512)
+    # the module-level form (the reference's dequantize_fused_experts) is the same dequantisation
+    from lemoq.kernels.moe_grouped_quant import dequantize_fused_experts
+
+    f = dequantize_fused_experts(q)
+    assert torch.equal(f.gate_up[1], q.dequant_gate_up_expert(1)) and torch.equal(f.down[2], q.dequant_down_expert(2))
+    assert dequantize_fused_experts(q, torch.float16).down.dtype == torch.float16
