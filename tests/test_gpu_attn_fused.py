@@ -96,7 +96,7 @@ def _fused_path(hip, dev, qkv, qn, kn, cache, cos, sin, pos, heads, D, S, ns=4, 
     (16, 128, 1100, 0, 3), (16, 128, 1100, 1, 3), (16, 128, 1100, 63, 3), (16, 128, 1100, 64, 8),
     (16, 128, 1100, 1024, 3), (16, 128, 1100, 1024, 1), (16, 128, 4200, 4095, 8), (8, 64, 700, 511, 2),
     (4, 256, 300, 257, 5), (16, 128, 1100, 5, 8),
-    # the decode step's 16 splits: 4-wave blocks (<= 128 slots per split) and 8-wave blocks
+    # the decode step's 16 splits: splits of one token round per wave and of several
     (16, 128, 1100, 1060, 16), (16, 128, 1100, 70, 16), (16, 128, 1100, 15, 16), (16, 128, 4200, 4132, 16),
     (16, 128, 4200, 300, 16), (4, 256, 1024, 1000, 16), (8, 64, 2048, 2047, 16),
     # round boundaries of the token loop: a wave block is 3 loads (24 tokens at D 128, 48 at

@@ -282,7 +282,7 @@ def test_c5_graph_replay_equals_eager_bitwise(ctx, positions, c5_model, dev):
     """The reference session's own gate (benchmarks/cudagraph.py:298-339): the
     captured step and the eager step give identical logits and tokens, here at
     the full OLMoE shape after the batched prefill at both benchmark contexts
-    (at ctx 4096 the step runs 8-wave attention blocks over 256-slot splits)."""
+    (at ctx 4096 every attention block loops over a 256-slot split)."""
     w, _ = c5_model
     print("case: C5 graph vs eager, ctx %d, %d positions" % (ctx, positions), flush=True)
     sess, _ = _c5_session(w, ctx, max_new_tokens=positions + 1)
