@@ -127,6 +127,14 @@ int lemoq_gemv_q(const uint16_t* x, int64_t M, int64_t K, const void* qweight, i
                  const void* scale, const void* zero, int scale_is_f32, int64_t N,
                  int64_t padded_k, int64_t group, void* y, int y_is_f16, void* stream);
 
+/* lemoq_gemv_q on fp32 activations (the reference's dequant_gemm_fused takes
+ * x fp16 or fp32, src/lemoq/kernels/_dequant_triton.py:252-253): the codes
+ * become fp32 values and meet x in fp32 FMAs, fp32 accumulation.  Same
+ * arguments and rules, x (M, K) fp32 contiguous. */
+int lemoq_gemv_q_x32(const float* x, int64_t M, int64_t K, const void* qweight, int fmt,
+                     const void* scale, const void* zero, int scale_is_f32, int64_t N,
+                     int64_t padded_k, int64_t group, void* y, int y_is_f16, void* stream);
+
 /* Dense weight of any LEMOQ_QFMT_* format: w[n][k] for k < k_out, computed
  * in fp32 and stored as fp32 (w_is_f32) or rounded once to fp16, rows ld_w
  * elements apart.  Replaces QuantLinear.dequantized_weight

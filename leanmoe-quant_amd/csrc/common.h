@@ -50,6 +50,7 @@ __device__ __forceinline__ float clip_qkv(float x, float c, float c16) {
 // instead (observed with the ROCm 7.2 clang for gfx950), so vector elements
 // must first be copied to a scalar, which this parameter does.
 __device__ __forceinline__ f16x2 as_h2(uint32_t v) { return __builtin_bit_cast(f16x2, v); }
+__device__ __forceinline__ float as_f32(uint32_t v) { return __builtin_bit_cast(float, v); }  // same rule
 
 // ---------------------------------------------------------------------------
 // Wave-level reductions, deterministic (fixed combination order).

@@ -212,6 +212,177 @@ int launch_gemv_q_fmt(bool s32, int kch, dim3 grid, hipStream_t st, const GemvQA
   else return s32 ? launch_gemv_q<FMT, true>(kch, grid, st, a) : launch_gemv_q<FMT, false>(kch, grid, st, a);
 }
 
+// ---------------------------------------------------------------------------
+// The same GEMV on fp32 activations (the reference's dequant_gemm_fused takes
+// x in fp16 or fp32, src/lemoq/kernels/_dequant_triton.py:252-253).  fp32 x
+// cannot enter v_dot2_f32_f16, so each code becomes an fp32 value (exact: 8-bit
+// and 4-bit integers, E2M1's 0 .. 6) and is multiplied with x in fp32 FMAs;
+// per slice acc += s * (sum c x - z * sum x) as above.  The load order is the
+// fp16 kernel's: every code slice, scale and x slice before any arithmetic.
+// ---------------------------------------------------------------------------
+template <int FMT>
+__device__ __forceinline__ void codes_to_f32(const u32x4 c, float (&v)[qf_slice_codes(FMT)]) {
+  const uint32_t cw[4] = {c.x, c.y, c.z, c.w};
+  if constexpr (FMT == LEMOQ_QFMT_MXFP4) {
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      const f16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(cw[d], 1.0f, 0);
+      const f16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(cw[d], 1.0f, 1);
+      const f16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(cw[d], 1.0f, 2);
+      const f16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(cw[d], 1.0f, 3);
+      v[8 * d + 0] = (float)p0[0];
+      v[8 * d + 1] = (float)p0[1];
+      v[8 * d + 2] = (float)p1[0];
+      v[8 * d + 3] = (float)p1[1];
+      v[8 * d + 4] = (float)p2[0];
+      v[8 * d + 5] = (float)p2[1];
+      v[8 * d + 6] = (float)p3[0];
+      v[8 * d + 7] = (float)p3[1];
+    }
+  } else if constexpr (qf_4bit(FMT)) {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      const uint32_t nib = (cw[i >> 3] >> (4 * (i & 7))) & 0xFu;
+      v[i] = FMT == LEMOQ_QFMT_W4 ? (float)((int)(nib ^ 8u) - 8) : (float)nib;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const uint32_t b = (cw[i >> 2] >> (8 * (i & 3))) & 0xFFu;
+      v[i] = FMT == LEMOQ_QFMT_W8 ? (float)(int)(int8_t)b : (float)b;
+    }
+  }
+}
+
+struct GemvQ32Args {
+  const float* x;
+  int64_t x_ld;
+  int K;
+  const uint8_t* codes;
+  int row_bytes;
+  const void* scale;
+  const void* zero;
+  int64_t N;
+  int ngroups;
+  int group;
+  void* y;
+  int64_t y_ld;
+  int y_f16;
+};
+
+template <int FMT, int KCH, int R, bool S32>
+__global__ __launch_bounds__(256) void gemv_q_x32_kernel(const GemvQ32Args a) {
+  constexpr int NV = qf_slice_codes(FMT);
+  constexpr int CPC = 64 * NV;
+  constexpr bool ASYM = qf_asym(FMT);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t m = blockIdx.y;
+  const int64_t row0 = ((int64_t)blockIdx.x * 4 + wave) * R;
+
+  u32x4 c[R][KCH];
+  uint32_t sraw[R][KCH], zraw[R][KCH];
+  uint32_t ok = 0u;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int64_t row = row0 + r;
+#pragma unroll
+    for (int j = 0; j < KCH; ++j) {
+      const int off = 1024 * j + 16 * lane;
+      const bool in = row < a.N && off < a.row_bytes;
+      const int64_t rr = in ? row : 0;
+      const int oo = in ? off : 0;
+      c[r][j] = load_stream16(reinterpret_cast<const int8_t*>(a.codes) + rr * a.row_bytes + oo);
+      const int64_t si = rr * a.ngroups + (oo / 16) * NV / a.group;
+      sraw[r][j] = load_scale_raw<FMT, S32>(a.scale, si);
+      zraw[r][j] = ASYM ? load_scale_raw<FMT, S32>(a.zero, si) : 0u;
+      ok |= (in ? 1u : 0u) << (r * KCH + j);
+    }
+  }
+  // x: the lane's NV consecutive fp32 values of each chunk, zero past K
+  const float* xr = a.x + m * a.x_ld;
+  const bool vec = ((reinterpret_cast<uintptr_t>(xr) & 15u) == 0) && ((a.K & 3) == 0);
+  float xv[KCH][NV];
+#pragma unroll
+  for (int j = 0; j < KCH; ++j) {
+    const int k0 = j * CPC + lane * NV;
+    if (vec && k0 + NV <= a.K) {
+#pragma unroll
+      for (int q = 0; q < NV / 4; ++q) {
+        const u32x4 w = *reinterpret_cast<const u32x4*>(xr + k0 + 4 * q);
+        xv[j][4 * q + 0] = as_f32(w.x);
+        xv[j][4 * q + 1] = as_f32(w.y);
+        xv[j][4 * q + 2] = as_f32(w.z);
+        xv[j][4 * q + 3] = as_f32(w.w);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < NV; ++i) xv[j][i] = k0 + i < a.K ? xr[k0 + i] : 0.0f;
+    }
+  }
+  LEMOQ_LOADS_ISSUED();
+
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+#pragma unroll
+  for (int j = 0; j < KCH; ++j) {
+    float xs = 0.0f;
+    if (ASYM) {
+#pragma unroll
+      for (int i = 0; i < NV; ++i) xs += xv[j][i];
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float cv[NV];
+      codes_to_f32<FMT>(c[r][j], cv);
+      float d = 0.0f;
+#pragma unroll
+      for (int i = 0; i < NV; ++i) d = fmaf(cv[i], xv[j][i], d);
+      if (ASYM) d = fmaf(-scale_value<FMT, S32>(zraw[r][j]), xs, d);
+      const bool use = (ok >> (r * KCH + j)) & 1u;
+      acc[r] = use ? fmaf(scale_value<FMT, S32>(sraw[r][j]), d, acc[r]) : acc[r];
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
+  if (lane < R) {
+    float v = acc[0];
+#pragma unroll
+    for (int r = 1; r < R; ++r)
+      if (lane == r) v = acc[r];
+    const int64_t n = row0 + lane;
+    if (n < a.N) {
+      if (a.y_f16)
+        reinterpret_cast<uint16_t*>(a.y)[m * a.y_ld + n] = f2h(v);
+      else
+        reinterpret_cast<float*>(a.y)[m * a.y_ld + n] = v;
+    }
+  }
+}
+
+template <int FMT, bool S32>
+int launch_gemv_q_x32(int kch, dim3 grid, hipStream_t st, const GemvQ32Args& a) {
+  switch (kch) {
+    case 1: hipLaunchKernelGGL((gemv_q_x32_kernel<FMT, 1, kGemvQRows, S32>), grid, dim3(256), 0, st, a); break;
+    case 2: hipLaunchKernelGGL((gemv_q_x32_kernel<FMT, 2, kGemvQRows, S32>), grid, dim3(256), 0, st, a); break;
+    case 4: hipLaunchKernelGGL((gemv_q_x32_kernel<FMT, 4, kGemvQRows, S32>), grid, dim3(256), 0, st, a); break;
+    case 8:
+      if constexpr (!qf_4bit(FMT)) {
+        hipLaunchKernelGGL((gemv_q_x32_kernel<FMT, 8, kGemvQRows, S32>), grid, dim3(256), 0, st, a);
+        break;
+      }
+      return LEMOQ_ERR_UNSUPPORTED;
+    default: return LEMOQ_ERR_UNSUPPORTED;
+  }
+  LEMOQ_CHECK_LAUNCH();
+}
+
+template <int FMT>
+int launch_gemv_q_x32_fmt(bool s32, int kch, dim3 grid, hipStream_t st, const GemvQ32Args& a) {
+  if constexpr (FMT == LEMOQ_QFMT_MXFP4) return launch_gemv_q_x32<FMT, false>(kch, grid, st, a);
+  else return s32 ? launch_gemv_q_x32<FMT, true>(kch, grid, st, a) : launch_gemv_q_x32<FMT, false>(kch, grid, st, a);
+}
+
 // Shape rules shared by the GEMV and the dequantisation.  Returns 0 or a
 // LEMOQ_ERR_* status.
 int check_format(int fmt, const void* qweight, const void* scale, const void* zero, int scale_is_f32,
@@ -529,6 +700,42 @@ extern "C" int lemoq_gemv_q(const uint16_t* x, int64_t M, int64_t K, const void*
     case LEMOQ_QFMT_W4: return launch_gemv_q_fmt<LEMOQ_QFMT_W4>(s32, kch, grid, st, a);
     case LEMOQ_QFMT_W4_ASYM: return launch_gemv_q_fmt<LEMOQ_QFMT_W4_ASYM>(s32, kch, grid, st, a);
     default: return launch_gemv_q_fmt<LEMOQ_QFMT_MXFP4>(false, kch, grid, st, a);
+  }
+}
+
+extern "C" int lemoq_gemv_q_x32(const float* x, int64_t M, int64_t K, const void* qweight, int fmt,
+                                const void* scale, const void* zero, int scale_is_f32, int64_t N,
+                                int64_t padded_k, int64_t group, void* y, int y_is_f16, void* stream) {
+  if (!x || !y) return LEMOQ_ERR_NULL;
+  const int rc = check_format(fmt, qweight, scale, zero, scale_is_f32, N, padded_k, group);
+  if (rc) return rc;
+  if (M <= 0 || M > 65535 || K <= 0 || K > padded_k) return LEMOQ_ERR_SHAPE;
+  GemvQ32Args a;
+  a.x = x;
+  a.x_ld = K;
+  a.K = (int)K;
+  a.codes = reinterpret_cast<const uint8_t*>(qweight);
+  a.row_bytes = (int)(qf_4bit(fmt) ? padded_k / 2 : padded_k);
+  a.scale = scale;
+  a.zero = zero;
+  a.N = N;
+  a.ngroups = (int)(padded_k / group);
+  a.group = (int)group;
+  a.y = y;
+  a.y_ld = N;
+  a.y_f16 = y_is_f16 ? 1 : 0;
+  const int64_t chunks = (a.row_bytes + 1023) / 1024;
+  const int kch = chunks <= 1 ? 1 : (chunks <= 2 ? 2 : (chunks <= 4 ? 4 : 8));
+  const int64_t blocks = (N + 4 * kGemvQRows - 1) / (4 * kGemvQRows);
+  const dim3 grid((unsigned)blocks, (unsigned)M);
+  hipStream_t st = lemoq_stream(stream);
+  const bool s32 = scale_is_f32 != 0;
+  switch (fmt) {
+    case LEMOQ_QFMT_W8: return launch_gemv_q_x32_fmt<LEMOQ_QFMT_W8>(s32, kch, grid, st, a);
+    case LEMOQ_QFMT_W8_ASYM: return launch_gemv_q_x32_fmt<LEMOQ_QFMT_W8_ASYM>(s32, kch, grid, st, a);
+    case LEMOQ_QFMT_W4: return launch_gemv_q_x32_fmt<LEMOQ_QFMT_W4>(s32, kch, grid, st, a);
+    case LEMOQ_QFMT_W4_ASYM: return launch_gemv_q_x32_fmt<LEMOQ_QFMT_W4_ASYM>(s32, kch, grid, st, a);
+    default: return launch_gemv_q_x32_fmt<LEMOQ_QFMT_MXFP4>(false, kch, grid, st, a);
   }
 }
 

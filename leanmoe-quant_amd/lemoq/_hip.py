@@ -117,6 +117,7 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "lemoq_rtn_quantize": (_I, [_P, _I64, _I64, _I64, _I, _I, _P, _P, _P, _P, _P, _P]),
     "lemoq_mxfp4_quantize": (_I, [_P, _I64, _I64, _P, _P, _P]),
     "lemoq_gemv_q": (_I, [_P, _I64, _I64, _P, _I, _P, _P, _I, _I64, _I64, _I64, _P, _I, _P]),
+    "lemoq_gemv_q_x32": (_I, [_P, _I64, _I64, _P, _I, _P, _P, _I, _I64, _I64, _I64, _P, _I, _P]),
     "lemoq_dequant_q": (_I, [_P, _I, _P, _P, _I, _I64, _I64, _I64, _P, _I64, _I64, _I, _P]),
     "lemoq_fake_quant_rows": (_I, [_P, _I64, _I64, _P, _P]),
     "lemoq_moe_gate_up_w4": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P]),

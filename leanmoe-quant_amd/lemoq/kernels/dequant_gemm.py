@@ -116,7 +116,12 @@ def dequant_gemm_fused(
     config: dict[str, Any] | None = None,
     mxfp4: bool = False,
 ) -> Any:
-    """``y (M, N) = x (M, K) @ dequant(qweight (N, P), scale (N, n_groups), zero).T``."""
+    """``y (M, N) = x (M, K) @ dequant(qweight (N, P), scale (N, n_groups), zero).T``.
+
+    x fp16 (``lemoq_gemv_w8`` / ``lemoq_gemv_q``: exact fp16 codes, fp16 x fp16
+    products in fp32) or fp32 (``lemoq_gemv_q_x32``: fp32 products), fp32
+    accumulation either way; the reference's ``_dequant_gemm_kernel``
+    (``_dequant_triton.py:313-463``) in another fp32 summation order."""
     import torch  # noqa: PLC0415
 
     from lemoq.quant.formats import QFMT_W8, scale_zero_args  # noqa: PLC0415
@@ -129,8 +134,8 @@ def dequant_gemm_fused(
     N = int(qweight.shape[0])
     if K > padded_in:
         raise ValueError("K=%d exceeds padded_in=%d" % (K, padded_in))
-    if x.dtype != torch.float16:
-        raise NotImplementedError("x must be fp16 (the w8a16 / w4a16 decode path), got %s" % x.dtype)
+    if x.dtype not in (torch.float16, torch.float32):
+        raise NotImplementedError("x must be fp16 or fp32, got %s" % x.dtype)
     if not x.is_contiguous():
         raise ValueError("x must be contiguous")
     if out_dtype is None:
@@ -145,7 +150,11 @@ def dequant_gemm_fused(
         return y
     y16 = 1 if out_dtype == torch.float16 else 0
     st = _hip.stream_of(x.device)
-    if fmt == QFMT_W8 and not s32:
+    if x.dtype == torch.float32:
+        _hip.call("lemoq_gemv_q_x32", _hip.ptr(x), M, K, _hip.ptr(qweight), fmt, _hip.ptr(scale_arg),
+                  _hip.ptr(zero_arg) if zero_arg is not None else None, s32, N, padded_in, int(group_size),
+                  _hip.ptr(y), y16, st)
+    elif fmt == QFMT_W8 and not s32:
         _hip.call("lemoq_gemv_w8", _hip.ptr(x), M, K, _hip.ptr(qweight), _hip.ptr(scale_arg), N, padded_in,
                   int(group_size), _hip.ptr(y), y16, st)
     else:
@@ -198,6 +207,9 @@ def dequant_gemm_separate(
     """
     import torch  # noqa: PLC0415
 
+    if x.dtype == torch.float32:  # the fp32 arm: F.linear on the fp32 dequantised weight
+        return _separate_f32(x, qweight, scale, zero, group_size=group_size, bits=bits, symmetric=symmetric,
+                             residual=residual, mxfp4=mxfp4)
     if mxfp4 or bits != 8 or not symmetric or zero is not None or scale.dtype != torch.float16:
         return _separate_dense(x, qweight, scale, zero, group_size=group_size, bits=bits, symmetric=symmetric,
                                residual=residual, mxfp4=mxfp4)
@@ -222,6 +234,24 @@ def dequant_gemm_separate(
               _hip.ptr(y), N, _hip.ptr(residual) if residual is not None else None, N,
               _hip.stream_of(x.device))
     return y
+
+
+def _separate_f32(x: Any, qweight: Any, scale: Any, zero: Any, *, group_size: int, bits: int, symmetric: bool,
+                  residual: Any, mxfp4: bool) -> Any:
+    """Separate arm on fp32 activations: the reference's ``dequantized_weight(dtype=
+    fp32)`` then ``F.linear`` in fp32 (``src/lemoq/quant/linear.py:365-395,480``).
+    The fp32 weight is ``code * scale`` exactly as the fused arm forms it, so
+    the fp32-activation GEMV over the M rows (``lemoq_gemv_q_x32``) computes
+    the same products, accumulated in fp32 in another order; fp32 output."""
+    import torch  # noqa: PLC0415
+
+    if residual is not None:
+        raise NotImplementedError("the fp32 arm takes no residual")
+    bits, padded_in, _ = _check_format(qweight, scale, zero, group_size, bits, symmetric, mxfp4)
+    if x.dim() != 2 or int(x.shape[1]) > padded_in:
+        raise ValueError("dequant_gemm_separate: x must be (M, K <= %d), got %r" % (padded_in, tuple(x.shape)))
+    return dequant_gemm_fused(x, qweight, scale, zero, group_size=group_size, bits=bits, symmetric=symmetric,
+                              out_dtype=torch.float32, mxfp4=mxfp4)
 
 
 def _separate_dense(x: Any, qweight: Any, scale: Any, zero: Any, *, group_size: int, bits: int, symmetric: bool,

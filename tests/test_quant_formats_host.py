@@ -54,8 +54,8 @@ def test_format_argument_rejections():
     with pytest.raises(NotImplementedError, match="group_size"):  # 4-bit groups must be whole 16-byte slices
         dequant_gemm_fused(x, torch.zeros((64, 128), dtype=torch.uint8), torch.ones((64, 16), dtype=torch.float16),
                            None, group_size=16, bits=4)
-    with pytest.raises(NotImplementedError, match="fp16"):
-        dequant_gemm_fused(x.float(), torch.zeros((64, 128), dtype=torch.uint8), s, None, group_size=128, bits=4)
+    with pytest.raises(NotImplementedError, match="fp16 or fp32"):  # fp32 x is taken, bf16 is not
+        dequant_gemm_fused(x.bfloat16(), torch.zeros((64, 128), dtype=torch.uint8), s, None, group_size=128, bits=4)
     # bits inferred from the code dtype: uint8 -> 4-bit
     with pytest.raises(ValueError, match="width"):
         dequant_gemm_fused(x, torch.zeros((64, 256), dtype=torch.uint8), s, None, group_size=128)
