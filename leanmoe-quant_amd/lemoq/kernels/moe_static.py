@@ -20,7 +20,34 @@ from typing import Any
 
 from lemoq import _hip
 
-__all__ = ["_route"]
+__all__ = ["FusedExperts", "_route", "fuse_experts"]
+
+
+def fuse_experts(experts: Any):
+    """Stack a list of per-expert MLPs (``gate_proj`` / ``up_proj`` / ``down_proj``
+    linears, HF OLMoE 4.x's ``OlmoeSparseMoeBlock.experts``) into the packed
+    layout: ``gate_up`` (E, 2F, H) with the gate rows first, ``down`` (E, H, F),
+    as the reference's ``fuse_experts`` (``moe_static.py:106-122``).  Call once,
+    outside capture; the stacked copies are new tensors on the experts' device."""
+    import torch  # noqa: PLC0415
+
+    from lemoq.kernels.moe_grouped_quant import FusedExperts  # noqa: PLC0415
+
+    layers = list(experts)
+    if not layers:
+        raise ValueError("experts is empty")
+    gate = torch.stack([e.gate_proj.weight.detach() for e in layers])
+    up = torch.stack([e.up_proj.weight.detach() for e in layers])
+    down = torch.stack([e.down_proj.weight.detach() for e in layers])
+    return FusedExperts(gate_up=torch.cat([gate, up], dim=1).contiguous(), down=down.contiguous())
+
+
+def __getattr__(name: str) -> Any:
+    if name == "FusedExperts":  # the container lives with the quantised one
+        from lemoq.kernels.moe_grouped_quant import FusedExperts  # noqa: PLC0415
+
+        return FusedExperts
+    raise AttributeError(name)
 
 
 def _route(x: Any, router_weight: Any, *, top_k: int, norm_topk_prob: bool):

@@ -5,8 +5,13 @@ the three symmetric w8 ``QuantLinear`` weights are concatenated along the output
 dimension and projected with one ``dequant_gemm_fused`` call.  The layout is
 row-local (each output row reads only its own codes and scales), so every
 packed row equals the single-projection row bit for bit.
-``pack_qkv(q_proj, k_proj, v_proj)`` replaces ``install_packed_qkv`` (which
-patched HF modules; this build owns its decode module).
+``pack_qkv(q_proj, k_proj, v_proj)`` builds one; ``install_packed_qkv(model)``
+attaches one to every attention module of a model (a module with ``q_proj``,
+``k_proj`` and ``v_proj``, as ``_lemoq_packed_qkv``, the reference's attribute),
+``packed_qkv_installed`` / ``remove_packed_qkv`` count and drop them
+(``:104-170``), and ``packed_qkv_enabled`` / ``packed_qkv_applicable`` are the
+reference's switch and preconditions (``:40-58``).  This build's own decode step
+packs q|k|v in its weights (``OlmoeW8Weights.qkv_codes``).
 """
 
 from __future__ import annotations
@@ -14,7 +19,54 @@ from __future__ import annotations
 from dataclasses import dataclass
 from typing import Any
 
-__all__ = ["PackedQKV", "pack_qkv"]
+__all__ = ["PackedQKV", "install_packed_qkv", "pack_qkv", "packed_qkv_applicable", "packed_qkv_enabled",
+           "packed_qkv_installed", "remove_packed_qkv"]
+
+_ATTR = "_lemoq_packed_qkv"
+
+
+def packed_qkv_enabled() -> bool:
+    """The ``packed_qkv`` fusion switch (``LEMOQ_PACKED_QKV``)."""
+    from lemoq.kernels.fusion_switches import fusion_enabled  # noqa: PLC0415
+
+    return fusion_enabled("packed_qkv")
+
+
+def packed_qkv_applicable(attn: Any, quantized: bool) -> bool:
+    """The two preconditions: the attention kernel cell and quantised projections
+    (fp16 q/k/v are plain linears: nothing to pack; not applicable means no-op)."""
+    return str(attn) == "kernel" and bool(quantized)
+
+
+def _attention_modules(model: Any) -> list:
+    return [m for m in model.modules() if all(hasattr(m, n) for n in ("q_proj", "k_proj", "v_proj"))]
+
+
+def install_packed_qkv(model: Any) -> int:
+    """Attach a ``PackedQKV`` to every attention module of ``model``; returns how
+    many.  Run after quantisation and before graph capture (it allocates).
+    Raises when no module has q/k/v projections, or one is not packable."""
+    mods = _attention_modules(model)
+    if not mods:
+        raise RuntimeError("no attention module (q_proj, k_proj, v_proj) found")
+    for m in mods:
+        setattr(m, _ATTR, pack_qkv(m.q_proj, m.k_proj, m.v_proj))
+    return len(mods)
+
+
+def packed_qkv_installed(model: Any) -> int:
+    """How many attention modules carry a packed q/k/v state."""
+    return sum(1 for m in _attention_modules(model) if getattr(m, _ATTR, None) is not None)
+
+
+def remove_packed_qkv(model: Any) -> int:
+    """Drop the packed states (A/B arms in one process); returns how many."""
+    n = 0
+    for m in _attention_modules(model):
+        if getattr(m, _ATTR, None) is not None:
+            delattr(m, _ATTR)
+            n += 1
+    return n
 
 
 @dataclass

@@ -41,3 +41,36 @@ def test_unavailable_reason_names_the_missing_device_here():
     assert (reason is None) == rmsnorm.fused_available()
     if not torch.cuda.is_available():
         assert reason and dequant_gemm.unavailable_reason() == reason
+
+
+def test_packed_qkv_switch_and_preconditions():
+    from lemoq.kernels.packed_qkv import install_packed_qkv, packed_qkv_applicable, packed_qkv_enabled
+    from torch import nn
+
+    assert packed_qkv_enabled() is True
+    assert packed_qkv_applicable("kernel", True) and not packed_qkv_applicable("sdpa", True)
+    assert not packed_qkv_applicable("kernel", False)
+    with pytest.raises(RuntimeError, match="no attention module"):
+        install_packed_qkv(nn.Linear(4, 4))
+
+
+def test_fuse_experts_stacks_gate_rows_first():
+    """moe_static.fuse_experts (the reference's ``moe_static.py:106-122``): gate rows
+    then up rows per expert, down as (E, H, F); host tensors stay host tensors."""
+    import torch
+    from torch import nn
+
+    from lemoq.kernels.moe_static import FusedExperts, fuse_experts
+
+    class _E(nn.Module):
+        def __init__(self, i):
+            super().__init__()
+            self.gate_proj, self.up_proj, self.down_proj = nn.Linear(8, 4), nn.Linear(8, 4), nn.Linear(4, 8)
+            for lin, off in ((self.gate_proj, 0), (self.up_proj, 100), (self.down_proj, 200)):
+                nn.init.constant_(lin.weight, float(i + off))
+
+    f = fuse_experts([_E(0), _E(1), _E(2)])
+    assert isinstance(f, FusedExperts) and tuple(f.gate_up.shape) == (3, 8, 8) and tuple(f.down.shape) == (3, 8, 4)
+    assert float(f.gate_up[2, 0, 0]) == 2.0 and float(f.gate_up[2, 4, 0]) == 102.0 and float(f.down[1, 0, 0]) == 201.0
+    with pytest.raises(ValueError):
+        fuse_experts([])

@@ -123,3 +123,23 @@ def test_fp32_activations_through_both_arms(scheme, sym, dev):
         ref = x.double() @ w64.T
         assert torch.allclose(y.double().cpu(), ref, rtol=2e-2, atol=2e-3), float((y.double().cpu() - ref).abs().max())
         assert float((y.double().cpu() - ref).abs().max()) < 1e-4  # fp32 products, fp32 sums
+
+
+def test_install_packed_qkv_over_a_quantised_model(dev):
+    """install_packed_qkv (the reference's ``packed_qkv.py:104-170``) on the
+    quantised tree: one packed state per attention module, its projection
+    bitwise equal to the three QuantLinear calls; counted and removed."""
+    from lemoq.kernels.packed_qkv import install_packed_qkv, packed_qkv_installed, remove_packed_qkv
+
+    print("case: install_packed_qkv", flush=True)
+    m = _model(dev)
+    with pytest.raises(ValueError, match="quantized q_proj"):
+        install_packed_qkv(m)  # plain linears: refused, not silently three calls
+    quantize_model(m, SchemeSpec.from_flags("w8a16", 128))
+    assert install_packed_qkv(m) == 2 and packed_qkv_installed(m) == 2
+    at = m.model.layers[1].self_attn
+    x = torch.randn(1, H, device=dev).to(torch.float16)
+    q, k, v = at._lemoq_packed_qkv.project(x)
+    for got, proj in ((q, at.q_proj), (k, at.k_proj), (v, at.v_proj)):
+        assert torch.equal(got, proj(x))
+    assert remove_packed_qkv(m) == 2 and packed_qkv_installed(m) == 0
