@@ -322,35 +322,22 @@ MULTI_STEPS = 8  # decode steps per graph of the multi-step measurement
 
 def measure_repeats(torch, sess, *, warmup: int, timed: int, repeats: int) -> dict:
     """The reference's repeated graph timing (``measure_graph_gap``,
-    ``benchmarks/cudagraph.py:420-495``): each repeat starts from the same
-    prefilled state (position and seed token restored, outside the timed
-    window), replays ``warmup`` steps untimed, restores the state again, then
-    times ``timed`` replays with host wall time and device events; returns
-    the per-repeat ms/token of both and their spread ((max - min) / min).
-    The KV slots past the prompt are rewritten by each repeat's own steps, so
-    every repeat decodes the same positions from the same cache."""
-    pos0, tok0 = sess.position, int(sess.token.item())
-    wall, event = [], []
-    for _ in range(repeats):
-        sess.set_position(pos0, tok0)
-        sess.replay(warmup, synchronize=False)
-        torch.cuda.synchronize()
-        sess.set_position(pos0, tok0)
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        e0.record()
-        t0 = time.perf_counter()
-        for _ in range(timed):
-            sess.replay(1, synchronize=False)
-        e1.record()
-        torch.cuda.synchronize()
-        wall.append((time.perf_counter() - t0) * 1e3 / timed)
-        event.append(e0.elapsed_time(e1) / timed)
-    sess.set_position(pos0, tok0)
-    return {"warmup": warmup, "timed": timed, "wall_ms": wall, "event_ms": event,
+    ``benchmarks/cudagraph.py:420-495``), run by ``lemoq.model.graph_session``:
+    each repeat starts from the same prefilled state (position and seed token
+    restored, outside the timed window), replays ``warmup`` steps untimed,
+    restores the state again, then times ``timed`` replays with host wall time
+    and device events; returns the per-repeat ms/token of both and their spread
+    ((max - min) / min).  The KV slots past the prompt are rewritten by each
+    repeat's own steps, so every repeat decodes the same positions from the
+    same cache."""
+    from lemoq.model.graph_session import measure_graph_gap  # noqa: PLC0415
+
+    gap = measure_graph_gap(sess, warmup=warmup, timed=timed, repeats=repeats)
+    wall, event = gap["stats"]["wall"]["samples"], gap["stats"]["gpu_event"]["samples"]
+    return {"warmup": gap["warmup"], "timed": gap["timed"], "wall_ms": wall, "event_ms": event,
             "wall_spread": (max(wall) - min(wall)) / min(wall),
             "event_spread": (max(event) - min(event)) / min(event),
-            "method": "perf_counter wall + device events around `timed` replays, per repeat"}
+            "host_share_pct": gap["host_share_pct"], "method": gap["method"]}
 
 
 def time_decode(torch, w, ctx: int, steps: int, warmup: int, extra: int):
@@ -370,6 +357,13 @@ def time_decode(torch, w, ctx: int, steps: int, warmup: int, extra: int):
     ttft_rnd = measure_prefill(torch, rnd)
     del rnd
     log("ctx %d: batched prefill of a random prompt (TTFT) p50 %.3f ms" % (ctx, ttft_rnd["p50"]))
+    # the reference's per-cell gate (benchmarks/cudagraph.py:298-339): eager steps against graph
+    # replays from the prefilled state, KL <= 1e-5 and identical tokens; state restored after
+    from lemoq.model.graph_session import graph_correctness  # noqa: PLC0415
+
+    gate = graph_correctness(sess, steps=8)
+    log("ctx %d: graph == eager gate %s (KL %.1e, bitwise %s)" % (ctx, "PASS" if gate["passed"] else "FAIL",
+                                                                   gate["kl"], gate["bitwise"]))
     repeats = measure_repeats(torch, sess, warmup=max(warmup, 5), timed=max(steps, 20), repeats=3)
     log("ctx %d: %d repeats x %d replays from the prefilled state: event ms/token %s (spread %.2f%%)"
         % (ctx, len(repeats["event_ms"]), repeats["timed"], ", ".join("%.4f" % v for v in repeats["event_ms"]),
@@ -422,6 +416,8 @@ def time_decode(torch, w, ctx: int, steps: int, warmup: int, extra: int):
         "ttft": ttft,
         "ttft_random_prompt": ttft_rnd,
         "repeats": repeats,
+        "graph_gate": {k: gate[k] for k in ("kl", "top1_agreement", "seed_token_match", "token_sequence_match",
+                                            "bitwise", "passed", "steps")},
         # the reference's per-token figure: p50 over the repeats of the wall-clock
         # mean per replay (runner.py:984, gap["stats"]["wall"]["p50"])
         "ms_per_token_repeats_p50": sorted(repeats["wall_ms"])[len(repeats["wall_ms"]) // 2],
@@ -1150,6 +1146,7 @@ def main(argv=None) -> int:
     line["prefill"] = _prefill_summary(r1, r2)
     # the reference's repeated timing: 3 repeats x >= 20 replays from the same prefilled state
     line["repeats"] = {"ctx%d" % r["ctx"]: r["repeats"] for r in (r1, r2) if r is not None}
+    line["graph_gate"] = {"ctx%d" % r["ctx"]: r["graph_gate"] for r in (r1, r2) if r is not None}
     if r2 is not None:
         line["ctx2"] = r2
         # the headline statistic at the second context

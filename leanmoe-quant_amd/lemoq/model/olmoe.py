@@ -346,6 +346,7 @@ class DecodeSession:
         self.steps_per_graph = 1
         self.stream: Any = None
         self._host_pos = 0
+        self._seed_token: int | None = None
         self.reset()
 
     # ------------------------------------------------------------------ state
@@ -496,7 +497,36 @@ class DecodeSession:
             self._host_pos = self.ctx
         else:
             raise ValueError("prefill mode must be 'batched' or 'stepped', got %r" % (mode,))
+        self._seed_token = int(self.token.item())
+        return self._seed_token
+
+    @property
+    def seed_token_id(self) -> int:
+        """The first decode token, chosen by ``prefill()`` (synchronises)."""
+        if self._seed_token is None:
+            raise RuntimeError("prefill must run before reading the seed token")
+        return self._seed_token
+
+    def next_token_cpu(self) -> int:
+        """The token the next step consumes: the greedy pick of the last step (synchronises)."""
         return int(self.token.item())
+
+    def replay_at_position(self, position: int, *, synchronize: bool = True) -> Any:
+        """Replay the captured step at ``position`` (with the token already in
+        place), as the reference's ``replay_at_position``; returns the logits."""
+        p = int(position)
+        if p < 0 or p >= self.max_seq:
+            raise RuntimeError("position %d outside the cache capacity %d" % (p, self.max_seq))
+        self.pos.fill_(p)
+        self.filled.fill_(p + 1)
+        self._host_pos = p
+        return self.replay(1, synchronize=synchronize)
+
+    def buffer_addresses(self) -> tuple[int, ...]:
+        """Device addresses of the fixed step inputs and outputs (token, position,
+        filled length, logits, history): they never move after construction, which
+        is what lets one captured graph serve every step."""
+        return tuple(int(t.data_ptr()) for t in (self.token, self.pos, self.filled, self.logits, self.history))
 
     def generated(self) -> list[int]:
         """Tokens chosen after the prompt so far (device history -> host)."""

@@ -196,3 +196,31 @@ def test_kv_cache_kind_is_checked(dev, monkeypatch):
     monkeypatch.setenv("LEMOQ_PACKED_QKV", "0")
     with pytest.raises(NotImplementedError, match="packed_qkv"):
         DecodeSession(w, [1, 2], max_new_tokens=2)
+
+
+@pytest.mark.parametrize("kv", ["int8", "fp16"])
+def test_graph_session_gate_timing_and_accessors(kv, dev):
+    """``lemoq.model.graph_session`` over a prefilled session: the reference's
+    graph-against-eager gate passes bit for bit, the repeated timing leaves the
+    session where it was, and the reference's accessors agree with the state."""
+    from lemoq.model.graph_session import graph_correctness, measure_graph_gap
+
+    print("case: graph_session gate + timing, %s cache" % kv, flush=True)
+    w = OlmoeW8Weights.random(TINY_FUSED, seed=3, device=dev)
+    prompt = torch.randint(0, TINY_FUSED.vocab, (40,), generator=torch.Generator().manual_seed(4)).tolist()
+    sess = DecodeSession(w, prompt, max_new_tokens=64, kv_cache=kv)
+    addrs = sess.buffer_addresses()
+    seed = sess.prefill()
+    assert sess.seed_token_id == seed == sess.next_token_cpu()
+    rep = graph_correctness(sess, steps=8)
+    assert rep["passed"] and rep["bitwise"] and rep["kl"] == 0.0 and rep["seed_token"] == seed
+    assert sess.position == 40 and sess.next_token_cpu() == seed  # state restored
+    gap = measure_graph_gap(sess, warmup=5, timed=20, repeats=2)
+    assert gap["kernels_per_call"] == sess.launches_per_step and 0 < gap["gpu_p50_ms"] <= gap["wall_p50_ms"] * 1.05
+    assert gap["host_share_pct"] is not None and sess.position == 40
+    a = sess.replay_at_position(40).clone()
+    assert sess.position == 41 and sess.next_token_cpu() == int(torch.argmax(a.float()))
+    sess.token.fill_(seed)  # the replay consumed the seed token and advanced it
+    b = sess.replay_at_position(40).clone()
+    assert torch.equal(a, b) and sess.position == 41
+    assert sess.buffer_addresses() == addrs
