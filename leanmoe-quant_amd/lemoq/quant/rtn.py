@@ -23,7 +23,7 @@ from typing import Any
 
 from lemoq import _hip
 
-__all__ = ["qmax_for", "quantize_rtn", "dequantize_rtn"]
+__all__ = ["qmax_for", "quantize_rtn", "dequantize_rtn", "quantization_error"]
 
 
 def qmax_for(bits: int, symmetric: bool = True) -> int:
@@ -114,3 +114,18 @@ def dequantize_rtn(q: dict[str, Any], dtype: Any = None) -> Any:
                    fmt=format_id(q["bits"], q["symmetric"]), group_size=q["group_size"], k_out=q["shape"][1],
                    dtype=torch.float32)
     return w.to(dtype) if dtype is not None else w
+
+
+def quantization_error(weight: Any, q: dict[str, Any]) -> dict[str, float]:
+    """Error of a quantisation against its weight (the reference's report,
+    ``src/lemoq/quant/rtn.py:117-132``): max and mean absolute error, the max
+    relative to the weight's absmax, and the SNR in dB (signal power over error
+    power, each floored at 1e-12)."""
+    w = weight.float()
+    diff = w - dequantize_rtn(q)
+    top = float(w.abs().max()) or 1.0
+    err_pow = float((diff * diff).mean()) or 1e-12
+    sig_pow = float((w * w).mean()) or 1e-12
+    return {"max_abs_err": float(diff.abs().max()), "mean_abs_err": float(diff.abs().mean()),
+            "max_rel_err_vs_absmax": float(diff.abs().max()) / top,
+            "snr_db": 10.0 * math.log10(sig_pow / err_pow)}

@@ -390,3 +390,32 @@ def test_quant_fused_experts_w4_dequant_bit_exact(dev):
     f = dequantize_fused_experts(q)
     assert torch.equal(f.gate_up[1], q.dequant_gate_up_expert(1)) and torch.equal(f.down[2], q.dequant_down_expert(2))
     assert dequantize_fused_experts(q, torch.float16).down.dtype == torch.float16
+
+
+@pytest.mark.parametrize("bits,sym", [(8, True), (8, False), (4, True), (4, False)])
+def test_quantize_linear_api_and_quantization_error(bits, sym, dev):
+    """``lemoq.quant.quantize_linear`` / ``dequantize_reference`` (the reference's
+    ``api.py:91-171``) on the device: the dequantised weight is the oracle's
+    dequantisation bit for bit, also when rebuilt from the unpacked codes alone;
+    ``rtn.quantization_error`` reports errors within the rounding bound."""
+    import lemoq.quant as lq
+    from lemoq.quant.rtn import quantization_error
+
+    print("case: quantize_linear bits=%d sym=%s" % (bits, sym), flush=True)
+    w = randn(96, 300, seed=bits + (0 if sym else 1), std=0.05)
+    ql = lq.quantize_linear(w.to(dev), bits=bits, group_size=64, symmetric=sym)
+    assert ql.shape == (96, 300) and ql.meta["padded_in"] == 320 and ql.scheme == "rtn"
+    got = lq.dequantize_reference(ql).cpu()
+    r = oq.rtn_quantize(w.numpy(), bits, 64, sym)
+    ref = oq.dequant_tile(r["codes_padded"], r["scale"], r["zero"], 64, sym, in_features=300)
+    assert np.array_equal(got.numpy().view(np.uint32), ref.view(np.uint32))
+    bare = lq.QuantizedLinear(codes=ql.codes, scale=ql.scale, zero=ql.zero, bits=bits, group_size=64, symmetric=sym,
+                              scheme="rtn", shape=ql.shape, meta={"n_groups": 5, "padded_in": 320})
+    assert torch.equal(lq.dequantize_reference(bare), lq.dequantize_reference(ql))
+    q = {"packed": ql.meta["packed"], "scale": ql.scale, "zero": ql.zero, "bits": bits, "group_size": 64,
+         "symmetric": sym, "shape": ql.shape}
+    e = quantization_error(w.to(dev), q)
+    step = float(ql.scale.max())
+    assert e["max_abs_err"] <= (0.5 if sym else 1.0) * step * (1 + 1e-5) and e["mean_abs_err"] < e["max_abs_err"]
+    assert e["snr_db"] > (30.0 if bits == 8 else 10.0)
+    assert e["max_rel_err_vs_absmax"] == pytest.approx(e["max_abs_err"] / float(w.abs().max()), rel=1e-5)
