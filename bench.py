@@ -94,6 +94,8 @@ def parse_args(argv=None):
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-formats", action="store_true", help="skip the weight-format GEMV timings")
     ap.add_argument("--no-kv-fp16", action="store_true", help="skip the fp16-cache (KV-INT8 off) step timing")
+    ap.add_argument("--kv-cache", choices=("int8", "fp16"), default="int8",
+                    help="--mode step: the decode cache kind (fp16 = the cell with KV-INT8 off)")
     ap.add_argument("--mode", choices=("full", "kernels", "traffic", "prefill", "step"), default="full")
     ap.add_argument("--summarize-pmc", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "PLAN_JSON"))
     ap.add_argument("--summarize-prefill", metavar="KERNEL_TRACE_CSV",
@@ -249,6 +251,19 @@ def kernel_table(torch, hip, w, sess, flusher, reps: int, floors: bool = True) -
                                st())
          for i in range(nl)],
         ["attn_split_fused_i8_kernel"])
+    # the same attention launch over the fp16 cache (KV-INT8 off): 16 layers' worth of fp16 rows
+    # with the same filled length, random values
+    kv16 = [(torch.randn((s.heads, S, D), device=dev).to(torch.float16),
+             torch.randn((s.heads, S, D), device=dev).to(torch.float16)) for _ in range(nl)]
+    add("attn_split_fused_f16 (filled=%d)" % filled,
+        KV_F16_BYTES_PER_TOKEN_LAYER * filled + 3 * HD * 2 + 2 * HD * 2 + 2 * D * 2 + s.heads * ns * (D + 2) * 4,
+        [lambda i=i: hip.call("lemoq_attn_split_fused_f16", P(sess.qkv), s.heads, D, P(L[i].q_norm),
+                               P(L[i].k_norm), s.eps, P(sess.cos_tab), P(sess.sin_tab), P(sess.pos),
+                               P(kv16[i][0]), P(kv16[i][1]), S * D, S, ns, qk_scale, P(sess.part_m),
+                               P(sess.part_l), P(sess.part_acc), math.inf if s.clip_qkv is None else s.clip_qkv,
+                               st())
+         for i in range(nl)],
+        ["attn_split_fused_f16_kernel"])
     if sess.attn_output_fused:
         npart = HD // 512
         add("attn_merge_o_proj_w8", w8(H, HD) + s.heads * ns * (D + 2) * 4 + npart * H * 4,
@@ -992,7 +1007,7 @@ def main(argv=None) -> int:
     if args.mode == "step":
         from lemoq.model.olmoe import DecodeSession
 
-        sess = DecodeSession(w, [1] * args.ctx, max_new_tokens=args.warmup + args.steps + 1, kv_cache="int8")
+        sess = DecodeSession(w, [1] * args.ctx, max_new_tokens=args.warmup + args.steps + 1, kv_cache=args.kv_cache)
         sess.capture()
         sess.prefill()
         sess.replay(args.warmup)
@@ -1000,8 +1015,8 @@ def main(argv=None) -> int:
         sess.replay(args.steps)
         ms = (time.perf_counter() - t0) * 1e3 / args.steps
         log("ctx %d: %d replays, %.4f ms/token" % (args.ctx, args.steps, ms))
-        print(json.dumps({"mode": "step", "ctx": args.ctx, "steps": args.steps, "ms_per_token": ms,
-                          "launches_per_step": sess.launches_per_step}))
+        print(json.dumps({"mode": "step", "ctx": args.ctx, "kv_cache": args.kv_cache, "steps": args.steps,
+                          "ms_per_token": ms, "launches_per_step": sess.launches_per_step}))
         return 0
 
     if args.mode == "prefill":
@@ -1309,7 +1324,7 @@ def summarize_trace(trace_csv: str) -> str:
 # The decode step's kernels in launch order (csrc/step.hip): per layer, then the lm_head pair.
 STEP_LAYER_KERNELS = [
     ("qkv (+ input RMSNorm)", "gemv_w8_kernel<2, 2, 0, true>"),
-    ("attention split (+ q/k norm, RoPE, KV-INT8 write)", "attn_split_fused_i8_kernel"),
+    ("attention split (+ q/k norm, RoPE, cache write)", "attn_split_fused_"),  # the _i8 or _f16 kernel
     ("merge + o_proj", "merge_oproj_kernel"),
     ("residual + norm + router", "router_resid_kernel"),
     ("gate/up (+ routing)", "moe_gate_up_kernel<2, 2, 1, true>"),
