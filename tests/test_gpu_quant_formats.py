@@ -218,12 +218,14 @@ def test_gemv_formats_k1_gate(m, k, n, bits, group, sym, sd, dev):
     _gemv_case(m, k, n, bits, group, sym, scale_dtype=sd, seed=m * k + n + bits, dev=dev)
 
 
-@pytest.mark.parametrize("m,k,n,bits,group,sym,sd", GEMV_CASES[::2] + [(1, 8192, 64, 8, 128, True, torch.float16),
-                                                                       (1, 4098, 40, 8, 64, True, torch.float16)])
+@pytest.mark.parametrize("m,k,n,bits,group,sym,sd", GEMV_CASES + [(1, 8192, 64, 8, 128, True, torch.float16),
+                                                                  (1, 4098, 40, 8, 64, True, torch.float16),
+                                                                  (2, 4098, 40, 4, 64, False, torch.float16)])
 def test_gemv_formats_fp32_activations_k1_gate(m, k, n, bits, group, sym, sd, dev):
     """The reference's operator takes fp32 x as well (``_dequant_triton.py:252``):
-    the fp32-activation kernel against the fp32 separate reference and fp64, with
-    K values that leave a ragged tail (500, 4098) and the widest rows (8192)."""
+    the fp32-activation kernel against the fp32 separate reference and fp64 on
+    every case of the fp16 grid, plus K values that leave a ragged tail (4098,
+    whose x rows also miss the 16-byte vector path) and the widest rows (8192)."""
     print("case: gemv fp32 x m=%d k=%d n=%d bits=%d group=%d sym=%s scale %s" % (m, k, n, bits, group, sym, sd),
           flush=True)
     _gemv_case(m, k, n, bits, group, sym, scale_dtype=sd, seed=m * k + n + bits + 1, dev=dev, x32=True)
