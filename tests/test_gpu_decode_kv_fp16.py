@@ -224,3 +224,30 @@ def test_graph_session_gate_timing_and_accessors(kv, dev):
     b = sess.replay_at_position(40).clone()
     assert torch.equal(a, b) and sess.position == 41
     assert sess.buffer_addresses() == addrs
+
+
+@pytest.mark.parametrize("kv", ["int8", "fp16"])
+def test_head_dim_64_model_match_oracle(kv, dev):
+    """A model with 64-wide heads (8 heads, hidden 512): the step's attention
+    instances for D = 64 and the three-launch attention-output path, batched
+    prefill of a random prompt, 32 greedy steps against the oracle from the
+    GPU's cache, with either cache kind."""
+    from lemoq.model.olmoe import OlmoeShape
+
+    print("case: head_dim 64 model, %s cache" % kv, flush=True)
+    sh = OlmoeShape(hidden=512, heads=8, head_dim=64, layers=2, num_experts=8, top_k=2, ffn=256, vocab=1024)
+    w = OlmoeW8Weights.random(sh, seed=21, device=dev)
+    ctx = 70
+    prompt = torch.randint(0, sh.vocab, (ctx,), generator=torch.Generator().manual_seed(22)).tolist()
+    sess = DecodeSession(w, prompt, max_new_tokens=STEPS, kv_cache=kv)
+    assert not sess.attn_output_fused
+    seed = sess.prefill()
+    oracle = OracleDecoder(w.to_host(), sess.max_seq, kv=sess.kv_cpu())
+    gl = []
+    for _ in range(STEPS):
+        sess.replay(1)
+        gl.append(sess.logits_cpu())
+    toks = [int(t) for t in sess.history[ctx: ctx + STEPS + 1].tolist()]
+    assert toks[0] == seed
+    rl = [oracle.step(toks[i], ctx + i) for i in range(STEPS)]
+    _check_steps(toks, gl, rl)
