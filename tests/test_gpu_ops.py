@@ -288,6 +288,57 @@ def test_grouped_moe_vs_fp64(E, F, H, K, dev):
     assert_close(got, ref, what="moe vs oracle")
 
 
+def _moe_fp64(x, gc, gs, dc, ds, ids, w, F):
+    gu64 = torch.stack([ops.dequant_w8(gc[e], gs[e], 128) for e in ids.tolist()]).double()
+    g, u = gu64[:, :F] @ x.double(), gu64[:, F:] @ x.double()
+    act64 = (g * torch.sigmoid(g) * u).to(torch.float16).double()
+    dn64 = torch.stack([ops.dequant_w8(dc[e], ds[e], 128) for e in ids.tolist()]).double()
+    return ((dn64 @ act64.unsqueeze(-1)).squeeze(-1) * w.double().unsqueeze(1)).sum(0)
+
+
+@pytest.mark.parametrize("E,F,H,K", [(64, 1024, 2048, 8), (8, 256, 512, 4)])
+def test_grouped_moe_degenerate_routing_all_slots_same_expert(E, F, H, K, dev):
+    """Every slot routed to one expert (the reference's
+    tests/test_moe_grouped.py:139-153): the slots' gate/up and down rows are
+    the same rows, summed over the slots in fixed order with their own weights."""
+    from lemoq.kernels.moe_grouped_quant import QuantFusedExperts, grouped_moe_forward_quant
+
+    gc, gs, dc, ds = _experts(E, F, H, 128, seed=E + 3 * F)
+    q = QuantFusedExperts(gc.to(dev), gs.to(dev), dc.to(dev), ds.to(dev), bits=8, group_size=128)
+    x = randn(H, seed=41).to(torch.float16)
+    for e in (0, E - 1, E // 3):
+        ids = torch.full((K,), e, dtype=torch.int64)
+        w = torch.softmax(randn(K, seed=42 + e), 0).to(torch.float16)
+        got = grouped_moe_forward_quant(x.to(dev), q, ids.to(dev), w.to(dev)).cpu()
+        ref, _ = ops.grouped_moe_w8(x, gc, gs, dc, ds, 128, ids, w)
+        assert_close(got, _moe_fp64(x, gc, gs, dc, ds, ids, w, F), what="expert %d x%d vs fp64" % (e, K))
+        assert_close(got, ref, what="expert %d x%d vs oracle" % (e, K))
+        # one slot with the summed weight gives the same answer up to the fp16
+        # rounding of that sum and of the output
+        one = grouped_moe_forward_quant(x.to(dev), q, ids[:1].to(dev),
+                                        w.float().sum().reshape(1).to(torch.float16).to(dev)).cpu()
+        assert_close(got, one, rtol=5e-3, atol=1e-3, what="expert %d: x%d against one slot" % (e, K))
+
+
+def test_grouped_moe_across_random_routings(dev):
+    """Twelve seeded routings at one shape, each against the fp64 closed form
+    and the oracle (the reference's tests/test_moe_grouped.py:123-137)."""
+    from lemoq.kernels.moe_grouped_quant import QuantFusedExperts, grouped_moe_forward_quant
+
+    E, F, H, K = 32, 256, 1024, 8
+    gc, gs, dc, ds = _experts(E, F, H, 128, seed=51)
+    q = QuantFusedExperts(gc.to(dev), gs.to(dev), dc.to(dev), ds.to(dev), bits=8, group_size=128)
+    for s in range(12):
+        g = torch.Generator().manual_seed(600 + s)
+        x = (torch.randn(H, generator=g) * (0.5 + s / 4)).to(torch.float16)
+        ids = torch.randperm(E, generator=g)[:K] if s % 3 else torch.randint(0, E, (K,), generator=g)
+        w = torch.softmax(torch.randn(K, generator=g), 0).to(torch.float16)
+        got = grouped_moe_forward_quant(x.to(dev), q, ids.to(dev), w.to(dev)).cpu()
+        ref, _ = ops.grouped_moe_w8(x, gc, gs, dc, ds, 128, ids, w)
+        assert_close(got, _moe_fp64(x, gc, gs, dc, ds, ids, w, F), what="routing %d vs fp64" % s)
+        assert_close(got, ref, what="routing %d vs oracle" % s)
+
+
 def test_grouped_moe_linear_in_weights_and_residual(dev):
     from lemoq.kernels.moe_grouped_quant import QuantFusedExperts, grouped_moe_forward_quant
 

@@ -128,3 +128,69 @@ def test_kv_direct_write_bitwise(dev):
 
     write_kv_slot(keys0, values0, 5, k, v)
     assert torch.equal(layer.keys, keys0) and torch.equal(layer.values, values0)
+
+
+def test_kv_direct_write_stream_sentinels_and_graph(dev):
+    """The reference's tests/test_kv_direct_write.py:100-147 on the device: a
+    stream of positions 0..7 over two layers against the slot contract, the
+    sentinel tail and the neighbouring slots untouched, the buffers kept (same
+    addresses), a position outside the cache writing nothing, and the write
+    captured once in a graph and replayed with the position advanced on the
+    device between replays."""
+    from types import SimpleNamespace
+
+    from lemoq.kernels.kv_direct import kv_direct_write
+    from oracle.ops import write_kv_slot
+
+    H, S, D, L = 16, 16, 128, 2
+    sentinel = torch.tensor(-7.25, dtype=torch.float16)
+    layers = [SimpleNamespace(keys=torch.full((1, H, S, D), float(sentinel), dtype=torch.float16, device=dev),
+                              values=torch.full((1, H, S, D), float(sentinel), dtype=torch.float16, device=dev))
+              for _ in range(L)]
+    ref = [(l.keys.cpu(), l.values.cpu()) for l in layers]
+    addrs = [(l.keys.data_ptr(), l.values.data_ptr()) for l in layers]
+    pos = torch.zeros(1, dtype=torch.int64, device=dev)
+
+    def kv(li, t):
+        return (randn(1, H, 1, D, seed=100 * li + 2 * t).to(torch.float16),
+                randn(1, H, 1, D, seed=100 * li + 2 * t + 1).to(torch.float16))
+
+    for t in range(8):
+        pos.fill_(t)
+        for li, layer in enumerate(layers):
+            k, v = kv(li, t)
+            kv_direct_write(layer, k.to(dev), v.to(dev), pos)
+            write_kv_slot(ref[li][0], ref[li][1], t, k, v)
+        for li, layer in enumerate(layers):
+            assert torch.equal(layer.keys.cpu(), ref[li][0]) and torch.equal(layer.values.cpu(), ref[li][1]), (li, t)
+    for li, layer in enumerate(layers):
+        assert (layer.keys.cpu()[:, :, 8:] == sentinel).all() and (layer.values.cpu()[:, :, 8:] == sentinel).all()
+        assert (layer.keys.data_ptr(), layer.values.data_ptr()) == addrs[li]
+
+    # a position outside [0, S) writes nothing
+    before = layers[0].keys.clone(), layers[0].values.clone()
+    k, v = kv(0, 99)
+    for bad in (S, S + 5, -1):
+        pos.fill_(bad)
+        kv_direct_write(layers[0], k.to(dev), v.to(dev), pos)
+    assert torch.equal(layers[0].keys, before[0]) and torch.equal(layers[0].values, before[1])
+
+    # one captured write, replayed at positions 9..12 set on the device
+    k, v = kv(1, 50)
+    kd, vd = k.to(dev), v.to(dev)
+    pos.fill_(9)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        kv_direct_write(layers[1], kd, vd, pos)  # warm-up outside the capture
+    s.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        kv_direct_write(layers[1], kd, vd, pos)
+    for t in range(9, 13):
+        pos.fill_(t)
+        g.replay()
+        torch.cuda.synchronize()
+        write_kv_slot(ref[1][0], ref[1][1], t, k, v)
+        assert torch.equal(layers[1].keys.cpu(), ref[1][0]) and torch.equal(layers[1].values.cpu(), ref[1][1]), t
+    assert (layers[1].keys.cpu()[:, :, 13:] == sentinel).all() and (layers[1].keys.cpu()[:, :, 8] == sentinel).all()

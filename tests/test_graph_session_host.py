@@ -41,6 +41,21 @@ def test_gate_predicate():
         assert not graph_correctness_passed({**ok, k: v}), (k, v)
 
 
+def test_nonfinite_logits_fail_the_gate():
+    """A NaN or infinite candidate logit gives a non-finite KL, which the gate
+    refuses (the reference's tests/test_cudagraph.py:328-342)."""
+    a = [torch.randn(40, generator=torch.Generator().manual_seed(10 + i)) for i in range(3)]
+    for bad in (float("nan"), float("inf")):
+        b = [x.clone() for x in a]
+        b[1][7] = bad
+        r = compare_logits(a, b)
+        assert not math.isfinite(r["kl"])
+        assert not graph_correctness_passed({**r, "seed_token_match": True, "token_sequence_match": True})
+    # mixed dtypes and shapes of one step's logits are compared as fp32 rows
+    r = compare_logits([x.reshape(1, 1, -1).half() for x in a], [x.double() for x in a])
+    assert r["top1_agreement"] == 1.0 and 0.0 <= r["kl"] < 1e-6
+
+
 def test_summarize_matches_numpy_percentiles():
     xs = [0.5, 0.51, 0.49, 0.52, 0.50, 0.7]
     s = summarize(xs)
