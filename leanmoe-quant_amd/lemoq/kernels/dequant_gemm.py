@@ -8,10 +8,11 @@ symmetric and asymmetric (two codes per byte), and MXFP4 (E2M1 codes + E8M0
 byte scales per 32).  Same contract: ``y = x @ dequant(qweight).T`` with fp32
 dequantisation and accumulation and a single rounding to ``out_dtype`` (fp32
 by default), contiguous inputs required, the same argument checks (and
-exception types) before anything runs.  Activations are fp16 (the decode
-path's type); fp32 activations raise ``NotImplementedError``.  The 8-bit
-symmetric branch with fp16 scales runs the decode step's GEMV; the others run
-``lemoq_gemv_q``.
+exception types) before anything runs.  fp16 activations (the decode path's
+type): the 8-bit symmetric branch with fp16 scales runs the decode step's GEMV,
+the others ``lemoq_gemv_q``.  fp32 activations run ``lemoq_gemv_q_x32`` for
+every format (fp32 products); other activation dtypes raise
+``NotImplementedError``.
 """
 
 from __future__ import annotations
