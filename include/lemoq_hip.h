@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define LEMOQ_ABI_VERSION 7
+#define LEMOQ_ABI_VERSION 8
 
 enum {
   LEMOQ_OK = 0,
@@ -126,6 +126,16 @@ int lemoq_mxfp4_quantize(const float* w, int64_t rows, int64_t cols, uint8_t* co
 int lemoq_gemv_q(const uint16_t* x, int64_t M, int64_t K, const void* qweight, int fmt,
                  const void* scale, const void* zero, int scale_is_f32, int64_t N,
                  int64_t padded_k, int64_t group, void* y, int y_is_f16, void* stream);
+
+/* lemoq_gemv_q with the fp16 residual add of the decoder layer after o_proj
+ * (transformers OlmoeDecoderLayer.forward, the `residual + hidden_states` of
+ * fp16 tensors): y (M, N) fp16 = fp16(fp16(x @ w^T) + residual), one rounding
+ * of each.  residual (M, N) fp16 is y itself or apart from it (a partial
+ * overlap returns LEMOQ_ERR_SHAPE).  Used by the 4-bit decode step. */
+int lemoq_gemv_q_residual(const uint16_t* x, int64_t M, int64_t K, const void* qweight, int fmt,
+                          const void* scale, const void* zero, int scale_is_f32, int64_t N,
+                          int64_t padded_k, int64_t group, const uint16_t* residual, uint16_t* y,
+                          void* stream);
 
 /* lemoq_gemv_q on fp32 activations (the reference's dequant_gemm_fused takes
  * x fp16 or fp32, src/lemoq/kernels/_dequant_triton.py:252-253): the codes
@@ -270,6 +280,14 @@ int lemoq_moe_down_w8(const uint16_t* act, const int8_t* codes,
 int lemoq_moe_gate_up_w4(const uint16_t* x, const uint8_t* codes, const uint16_t* scale,
                          const int64_t* ids, int64_t top_k, int64_t num_experts, int64_t ffn,
                          int64_t hidden, int64_t group, uint16_t* act, void* stream);
+/* Routed form of lemoq_moe_gate_up_w4, as lemoq_moe_gate_up_w8_routed: the
+ * router's fp16 logits (E) in place of ids, routing in every block (ties ->
+ * lowest index), the selected ids and fp16 weights stored to top_i / top_w.
+ * E <= 256, top_k <= 64.  Used by the 4-bit decode step. */
+int lemoq_moe_gate_up_w4_routed(const uint16_t* x, const uint8_t* codes, const uint16_t* scale,
+                                const uint16_t* router_logits, int64_t top_k, int norm_topk_prob,
+                                int64_t num_experts, int64_t ffn, int64_t hidden, int64_t group,
+                                uint16_t* act, int64_t* top_i, uint16_t* top_w, void* stream);
 int lemoq_moe_down_w4(const uint16_t* act, const uint8_t* codes, const uint16_t* scale,
                       const int64_t* ids, const uint16_t* top_w, int64_t top_k,
                       int64_t num_experts, int64_t hidden, int64_t ffn, int64_t group,
@@ -599,6 +617,22 @@ typedef struct LemoqOlmoeStep {
   /* Cache kind: 0 = KV-INT8 (kc/vc int8 codes, ks/vs fp16 scales), 1 = fp16
    * rows (kc/vc point to (heads, S, D) fp16; lemoq_attn_split_fused_f16). */
   int64_t kv_fp16;
+  /* Attention and expert weight bits: 8 (the layer's codes as declared
+   * above) or 4 (the reference's w4a16 cell: 4-bit symmetric codes packed two
+   * per byte, the even column in the low nibble, so qkv_codes (3*heads*D,
+   * H/2), o_codes (H, heads*D/2), gu_codes (E, 2F, H/2), dn_codes (E, H, F/2);
+   * scales as above; group % 32 == 0).  A 4-bit step runs 8 launches per
+   * layer: lemoq_rmsnorm, lemoq_gemv_q (q|k|v), the fused attention,
+   * lemoq_attn_merge, lemoq_gemv_q_residual (o_proj + residual into h),
+   * lemoq_router_logits, lemoq_moe_gate_up_w4_routed, lemoq_moe_down_w4
+   * (+ residual into h); layer 0 first gathers the embedding row into h
+   * (lemoq_gather_rows). */
+  int64_t weight_bits;
+  /* fp16 lm_head (vocab, H), or NULL for the W8 lm_head of lm_codes /
+   * lm_scale.  With it the step ends with lemoq_router_logits (final norm +
+   * fp16 GEMV) and lemoq_argmax_advance; the reference keeps the lm_head in
+   * fp16 in every cell but w8a16 with its lm_head switch on. */
+  const uint16_t* lm_f16;
 } LemoqOlmoeStep;
 
 int lemoq_olmoe_decode_step(const LemoqOlmoeStep* step, void* stream);

@@ -8,7 +8,9 @@
 //
 // Same structure and numerics as the 8-bit kernels (moe.hip): gate/up grid
 // (ceil(F / (4R)), top_k), wave w of block b computes the R gate rows and the
-// R matching up rows of expert ids[slot] and writes act = fp16(silu(g) * u);
+// R matching up rows of expert ids[slot] and writes act = fp16(silu(g) * u)
+// (the routed form takes the router's fp16 logits and routes in every block,
+// as moe.hip's routed 8-bit kernel does);
 // down grid ceil(H / R) blocks of 8 waves walking the slots, then a
 // fixed-order sum of partial * top_w and the optional fp16 residual add.
 // Lane l reads bytes [1024 j + 16 l, +16) of chunk j of a packed row (32
@@ -128,17 +130,68 @@ __device__ __forceinline__ float q4_row_dot(const Q4Tile<R, KCH, SB>& t, int r, 
   return a;
 }
 
-template <int KCH, int R, int SB>
-__global__ __launch_bounds__(256) void moe_gate_up_q4_kernel(const uint16_t* __restrict__ x,
-                                                             const uint8_t* __restrict__ codes,
-                                                             const uint16_t* __restrict__ scale,
-                                                             const int64_t* __restrict__ ids, int E, int F, int H,
-                                                             int group, uint16_t* __restrict__ act) {
+struct Q4GateUpArgs {
+  const uint16_t* x;
+  const uint8_t* codes;
+  const uint16_t* scale;
+  const int64_t* ids;      // plain form
+  const uint16_t* logits;  // routed form: (E) fp16 router logits
+  int top_k;
+  int norm;
+  int64_t* ids_out;        // routed form: selected ids (top_k)
+  uint16_t* w_out;         // routed form: fp16 routing weights (top_k)
+  int E, F, H, group;
+  uint16_t* act;
+};
+
+// PL = 0: ids given; PL > 0: routed from E <= 64 * PL logits, as the 8-bit
+// routed kernel (moe.hip): wave 0 of every block runs the softmax and the
+// argmax rounds up to its slot's rank (wave_route), block (0, 0) runs all
+// top_k rounds and stores the ids and fp16 weights for the down kernel.
+template <int KCH, int R, int SB, int PL>
+__global__ __launch_bounds__(256) void moe_gate_up_q4_kernel(const Q4GateUpArgs a) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int slot = blockIdx.y;
-  const int64_t e = ids[slot];
+  const uint16_t* __restrict__ x = a.x;
+  const uint8_t* __restrict__ codes = a.codes;
+  const uint16_t* __restrict__ scale = a.scale;
+  const int E = a.E, F = a.F, H = a.H, group = a.group;
+  uint16_t* __restrict__ act = a.act;
+  int64_t e = 0;
+  constexpr int PZ = PL > 0 ? PL : 1;
+  float z[PZ];
+  if constexpr (PL > 0) {
+    // Unconditional loads (index clamped, value masked after the load).
+#pragma unroll
+    for (int i = 0; i < PL; ++i) {
+      const int idx = lane + 64 * i;
+      const float v = h2f(a.logits[idx < E ? idx : E - 1]);
+      z[i] = idx < E ? v : -INFINITY;
+    }
+  } else {
+    e = a.ids[slot];
+  }
   uint32_t xw[KCH][SB];
   x4_load<KCH, SB>(xw, x, H, lane);
+  if constexpr (PL > 0) {
+    __shared__ int sel_id[64];
+    if (wave == 0) {
+      const bool publish = blockIdx.x == 0 && slot == 0;
+      const int rounds = publish ? a.top_k : slot + 1;
+      int id;
+      float w;
+      wave_route<PZ>(z, E, a.top_k, a.norm != 0, id, w, rounds);
+      if (lane < rounds) {
+        sel_id[lane] = id;
+        if (publish) {
+          a.ids_out[lane] = (int64_t)id;
+          a.w_out[lane] = f2h(w);
+        }
+      }
+    }
+    __syncthreads();
+    e = sel_id[slot];
+  }
   const bool ev = e >= 0 && e < E;
   const int n0 = (blockIdx.x * 4 + wave) * R;
   const int ng = H / group;
@@ -233,28 +286,82 @@ Q4Geom q4_geom(int64_t k) {
 
 }  // namespace
 
-extern "C" int lemoq_moe_gate_up_w4(const uint16_t* x, const uint8_t* codes, const uint16_t* scale,
-                                    const int64_t* ids, int64_t top_k, int64_t num_experts, int64_t ffn,
-                                    int64_t hidden, int64_t group, uint16_t* act, void* stream) {
-  if (!x || !codes || !scale || !ids || !act) return LEMOQ_ERR_NULL;
+namespace {
+
+int check_gate_up_q4(const uint16_t* x, const uint8_t* codes, const uint16_t* scale, const void* sel,
+                     const uint16_t* act, int64_t top_k, int64_t num_experts, int64_t ffn, int64_t hidden,
+                     int64_t group) {
+  if (!x || !codes || !scale || !sel || !act) return LEMOQ_ERR_NULL;
   if (top_k <= 0 || top_k > 65535 || num_experts <= 0 || ffn <= 0 || hidden <= 0) return LEMOQ_ERR_SHAPE;
   if (hidden > 8192 || hidden % 32 != 0 || group <= 0 || group % 32 != 0 || hidden % group != 0)
     return LEMOQ_ERR_UNSUPPORTED;
   if (num_experts * 2 * ffn * hidden >= (int64_t)1 << 40) return LEMOQ_ERR_SHAPE;
   if (!lemoq_aligned16(codes)) return LEMOQ_ERR_ALIGN;
+  return LEMOQ_OK;
+}
+
+template <int PL>
+int launch_gate_up_q4(hipStream_t st, const Q4GateUpArgs& a) {
   constexpr int R = 2;
-  const dim3 grid((unsigned)((ffn + 4 * R - 1) / (4 * R)), (unsigned)top_k);
-  hipStream_t st = lemoq_stream(stream);
-  const int E = (int)num_experts, F = (int)ffn, H = (int)hidden, g = (int)group;
-  const Q4Geom geo = q4_geom(hidden);
-#define LEMOQ_GU4(KK, SS) \
-  hipLaunchKernelGGL((moe_gate_up_q4_kernel<KK, R, SS>), grid, dim3(256), 0, st, x, codes, scale, ids, E, F, H, g, act)
+  const dim3 grid((unsigned)((a.F + 4 * R - 1) / (4 * R)), (unsigned)a.top_k);
+  const Q4Geom geo = q4_geom(a.H);
+#define LEMOQ_GU4(KK, SS) hipLaunchKernelGGL((moe_gate_up_q4_kernel<KK, R, SS, PL>), grid, dim3(256), 0, st, a)
   if (geo.sb == 8) LEMOQ_GU4(1, 8);
   else if (geo.kch == 1) LEMOQ_GU4(1, 16);
   else if (geo.kch == 2) LEMOQ_GU4(2, 16);
   else LEMOQ_GU4(4, 16);
 #undef LEMOQ_GU4
   LEMOQ_CHECK_LAUNCH();
+}
+
+Q4GateUpArgs make_gate_up_q4(const uint16_t* x, const uint8_t* codes, const uint16_t* scale, int64_t top_k,
+                             int64_t E, int64_t F, int64_t H, int64_t group, uint16_t* act) {
+  Q4GateUpArgs a;
+  a.x = x;
+  a.codes = codes;
+  a.scale = scale;
+  a.ids = nullptr;
+  a.logits = nullptr;
+  a.top_k = (int)top_k;
+  a.norm = 0;
+  a.ids_out = nullptr;
+  a.w_out = nullptr;
+  a.E = (int)E;
+  a.F = (int)F;
+  a.H = (int)H;
+  a.group = (int)group;
+  a.act = act;
+  return a;
+}
+
+}  // namespace
+
+extern "C" int lemoq_moe_gate_up_w4(const uint16_t* x, const uint8_t* codes, const uint16_t* scale,
+                                    const int64_t* ids, int64_t top_k, int64_t num_experts, int64_t ffn,
+                                    int64_t hidden, int64_t group, uint16_t* act, void* stream) {
+  const int rc = check_gate_up_q4(x, codes, scale, ids, act, top_k, num_experts, ffn, hidden, group);
+  if (rc) return rc;
+  Q4GateUpArgs a = make_gate_up_q4(x, codes, scale, top_k, num_experts, ffn, hidden, group, act);
+  a.ids = ids;
+  return launch_gate_up_q4<0>(lemoq_stream(stream), a);
+}
+
+extern "C" int lemoq_moe_gate_up_w4_routed(const uint16_t* x, const uint8_t* codes, const uint16_t* scale,
+                                           const uint16_t* router_logits, int64_t top_k, int norm_topk_prob,
+                                           int64_t num_experts, int64_t ffn, int64_t hidden, int64_t group,
+                                           uint16_t* act, int64_t* top_i, uint16_t* top_w, void* stream) {
+  const int rc = check_gate_up_q4(x, codes, scale, router_logits, act, top_k, num_experts, ffn, hidden, group);
+  if (rc) return rc;
+  if (!top_i || !top_w) return LEMOQ_ERR_NULL;
+  if (top_k > 64 || top_k > num_experts) return LEMOQ_ERR_SHAPE;
+  if (num_experts > 256) return LEMOQ_ERR_UNSUPPORTED;
+  Q4GateUpArgs a = make_gate_up_q4(x, codes, scale, top_k, num_experts, ffn, hidden, group, act);
+  a.logits = router_logits;
+  a.norm = norm_topk_prob ? 1 : 0;
+  a.ids_out = top_i;
+  a.w_out = top_w;
+  hipStream_t st = lemoq_stream(stream);
+  return num_experts <= 64 ? launch_gate_up_q4<1>(st, a) : launch_gate_up_q4<4>(st, a);
 }
 
 extern "C" int lemoq_moe_down_w4(const uint16_t* act, const uint8_t* codes, const uint16_t* scale,

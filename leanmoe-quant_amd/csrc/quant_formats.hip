@@ -101,6 +101,7 @@ struct GemvQArgs {
   void* y;
   int64_t y_ld;
   int y_f16;
+  const uint16_t* residual;  // (M, N) fp16 with ld y_ld, or NULL: y = fp16(fp16(acc) + residual)
 };
 
 template <int FMT, int KCH, int R, bool S32>
@@ -176,7 +177,9 @@ __global__ __launch_bounds__(256) void gemv_q_kernel(const GemvQArgs a) {
       if (lane == r) v = acc[r];
     const int64_t n = row0 + lane;
     if (n < a.N) {
-      if (a.y_f16)
+      if (a.residual)  // the fp16 residual add after the projection (one rounding of the fp16 sum)
+        reinterpret_cast<uint16_t*>(a.y)[m * a.y_ld + n] = hadd_round(h2f(f2h(v)), a.residual[m * a.y_ld + n]);
+      else if (a.y_f16)
         reinterpret_cast<uint16_t*>(a.y)[m * a.y_ld + n] = f2h(v);
       else
         reinterpret_cast<float*>(a.y)[m * a.y_ld + n] = v;
@@ -666,9 +669,42 @@ extern "C" int lemoq_fake_quant_rows(const uint16_t* x, int64_t rows, int64_t D,
   LEMOQ_CHECK_LAUNCH();
 }
 
+namespace {
+
+int gemv_q_common(const uint16_t* x, int64_t M, int64_t K, const void* qweight, int fmt, const void* scale,
+                  const void* zero, int scale_is_f32, int64_t N, int64_t padded_k, int64_t group, void* y,
+                  int y_is_f16, const uint16_t* residual, void* stream);
+
+}  // namespace
+
 extern "C" int lemoq_gemv_q(const uint16_t* x, int64_t M, int64_t K, const void* qweight, int fmt,
                             const void* scale, const void* zero, int scale_is_f32, int64_t N,
                             int64_t padded_k, int64_t group, void* y, int y_is_f16, void* stream) {
+  return gemv_q_common(x, M, K, qweight, fmt, scale, zero, scale_is_f32, N, padded_k, group, y, y_is_f16,
+                       nullptr, stream);
+}
+
+extern "C" int lemoq_gemv_q_residual(const uint16_t* x, int64_t M, int64_t K, const void* qweight, int fmt,
+                                     const void* scale, const void* zero, int scale_is_f32, int64_t N,
+                                     int64_t padded_k, int64_t group, const uint16_t* residual, uint16_t* y,
+                                     void* stream) {
+  if (!residual || !y) return LEMOQ_ERR_NULL;
+  // residual is y itself (each element read, then written, by one lane) or apart from it
+  if (M > 0 && N > 0 && residual != y) {
+    const char* r = reinterpret_cast<const char*>(residual);
+    const char* o = reinterpret_cast<const char*>(y);
+    const int64_t nb = M * N * 2;
+    if (r < o + nb && o < r + nb) return LEMOQ_ERR_SHAPE;
+  }
+  return gemv_q_common(x, M, K, qweight, fmt, scale, zero, scale_is_f32, N, padded_k, group, y, 1, residual,
+                       stream);
+}
+
+namespace {
+
+int gemv_q_common(const uint16_t* x, int64_t M, int64_t K, const void* qweight, int fmt, const void* scale,
+                  const void* zero, int scale_is_f32, int64_t N, int64_t padded_k, int64_t group, void* y,
+                  int y_is_f16, const uint16_t* residual, void* stream) {
   if (!x || !y) return LEMOQ_ERR_NULL;
   const int rc = check_format(fmt, qweight, scale, zero, scale_is_f32, N, padded_k, group);
   if (rc) return rc;
@@ -688,6 +724,7 @@ extern "C" int lemoq_gemv_q(const uint16_t* x, int64_t M, int64_t K, const void*
   a.y = y;
   a.y_ld = N;
   a.y_f16 = y_is_f16 ? 1 : 0;
+  a.residual = residual;
   const int64_t chunks = (a.row_bytes + 1023) / 1024;
   const int kch = chunks <= 1 ? 1 : (chunks <= 2 ? 2 : (chunks <= 4 ? 4 : 8));
   const int64_t blocks = (N + 4 * kGemvQRows - 1) / (4 * kGemvQRows);
@@ -702,6 +739,8 @@ extern "C" int lemoq_gemv_q(const uint16_t* x, int64_t M, int64_t K, const void*
     default: return launch_gemv_q_fmt<LEMOQ_QFMT_MXFP4>(false, kch, grid, st, a);
   }
 }
+
+}  // namespace
 
 extern "C" int lemoq_gemv_q_x32(const float* x, int64_t M, int64_t K, const void* qweight, int fmt,
                                 const void* scale, const void* zero, int scale_is_f32, int64_t N,

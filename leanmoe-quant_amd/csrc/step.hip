@@ -21,6 +21,15 @@
 // then final RMSNorm + lm_head GEMV with per-block argmax partials, and the
 // greedy selection that writes the next token and advances *pos / *filled.
 //
+// 4-bit weights (weight_bits 4, the reference's w4a16 cell) run 8 launches per
+// layer from the operators of the 4-bit formats: input RMSNorm, the 4-bit
+// q|k|v GEMV, the same fused attention, the LSE merge, the 4-bit o_proj GEMV
+// with the residual add, router logits (post-attention norm + router), the
+// routed 4-bit gate/up and the 4-bit down with the residual add; layer 0
+// first gathers the embedding row.  An fp16 lm_head (lm_f16, the reference's
+// lm_head in every cell but w8a16 with its lm_head switch on) ends the step
+// with the final norm + fp16 GEMV and the greedy selection over the logits.
+//
 // Every shape and buffer rule of every launch is checked before the first
 // launch is enqueued, so a rejected step leaves the cache and buffers as they
 // were.
@@ -56,17 +65,19 @@ int check_gemv(int64_t N, int64_t K, int64_t group) {
   return LEMOQ_OK;
 }
 
-enum AttnPath { kAttnFusedOut, kAttnThree };
+enum AttnPath { kAttnFusedOut, kAttnThree, kAttnW4 };
 
 // Every rule of every launch of the step, before anything is enqueued.
 int validate(const LemoqOlmoeStep* p, AttnPath* path) {
   if (!p || !p->layers) return LEMOQ_ERR_NULL;
   if (p->kv_fp16 != 0 && p->kv_fp16 != 1) return LEMOQ_ERR_SHAPE;
-  if (!p->embed || !p->final_norm || !p->lm_codes || !p->lm_scale || !p->cos_tab ||
-      !p->sin_tab || !p->token || !p->pos || !p->filled || !p->h || !p->xn || !p->qkv ||
-      !p->q_rot || !p->attn || !p->part_m || !p->part_l || !p->part_acc || !p->top_w ||
-      !p->top_i || !p->act || !p->logits || !p->router_logits || !p->am_val || !p->am_idx)
+  if (!p->embed || !p->final_norm || !p->cos_tab || !p->sin_tab || !p->token || !p->pos ||
+      !p->filled || !p->h || !p->xn || !p->qkv || !p->q_rot || !p->attn || !p->part_m ||
+      !p->part_l || !p->part_acc || !p->top_w || !p->top_i || !p->act || !p->logits ||
+      !p->router_logits)
     return LEMOQ_ERR_NULL;
+  // the W8 lm_head and its argmax partials (not read with an fp16 lm_head)
+  if (!p->lm_f16 && (!p->lm_codes || !p->lm_scale || !p->am_val || !p->am_idx)) return LEMOQ_ERR_NULL;
   const int64_t H = p->hidden, D = p->head_dim, HD = p->heads * p->head_dim, E = p->num_experts;
   const int64_t F = p->ffn, K = p->top_k, g = p->group, S = p->max_seq, ns = p->num_splits;
   if (H <= 0 || p->heads <= 0 || D <= 0 || p->num_layers <= 0 || S <= 0 || ns <= 0 ||
@@ -74,12 +85,26 @@ int validate(const LemoqOlmoeStep* p, AttnPath* path) {
     return LEMOQ_ERR_SHAPE;
   if (g <= 0 || g % 16 != 0) return LEMOQ_ERR_UNSUPPORTED;
   if (!(p->clip_qkv >= 0.0f)) return LEMOQ_ERR_SHAPE;  // negative or NaN clip_qkv
-  // qkv and lm_head GEMVs (K = H), o_proj (K = HD) on the unfused path
+  if (p->weight_bits != 8 && p->weight_bits != 4) return LEMOQ_ERR_UNSUPPORTED;
+  const bool w4 = p->weight_bits == 4;
+  // qkv GEMV (K = H), o_proj (K = HD) on the unfused path
   LEMOQ_TRY(check_gemv(3 * HD, H, g));
-  LEMOQ_TRY(check_gemv(p->vocab, H, g));
   if (p->vocab > 0x7ffffffeLL) return LEMOQ_ERR_SHAPE;
-  if (p->am_len < lemoq_lm_head_argmax_parts(p->vocab)) return LEMOQ_ERR_SHAPE;
-  if (!a16(p->lm_codes)) return LEMOQ_ERR_ALIGN;
+  if (p->lm_f16) {  // final norm + fp16 lm_head (lemoq_router_logits), then the greedy pick
+    if (p->vocab > 65536 || H > 8192 || H % 16 != 0) return LEMOQ_ERR_UNSUPPORTED;
+    if (!a16(p->lm_f16) || !a16(p->h) || !a16(p->final_norm) || !a16(p->xn)) return LEMOQ_ERR_ALIGN;
+  } else {
+    LEMOQ_TRY(check_gemv(p->vocab, H, g));
+    if (p->am_len < lemoq_lm_head_argmax_parts(p->vocab)) return LEMOQ_ERR_SHAPE;
+    if (!a16(p->lm_codes)) return LEMOQ_ERR_ALIGN;
+  }
+  if (w4) {
+    // 4-bit GEMVs (lemoq_gemv_q rules), routed gate/up and down (moe_q4.hip),
+    // row norm, gather, merge and router logits of the 4-bit layer
+    if (g % 32 != 0 || HD > 8192 || HD % g != 0 || H % 32 != 0 || F % 32 != 0) return LEMOQ_ERR_UNSUPPORTED;
+    if (ns > 1024) return LEMOQ_ERR_SHAPE;
+    if (!a16(p->h) || !a16(p->embed) || !a16(p->attn)) return LEMOQ_ERR_ALIGN;
+  }
   // split-KV attention (attn_fused.hip)
   if (D != 64 && D != 128 && D != 256) return LEMOQ_ERR_UNSUPPORTED;
   if (p->heads > 65535 || HD > 65536 || ns > 65535 || S >= ((int64_t)1 << 31)) return LEMOQ_ERR_SHAPE;
@@ -99,6 +124,10 @@ int validate(const LemoqOlmoeStep* p, AttnPath* path) {
     if (!a16(w.qkv_codes) || !a16(w.o_codes) || !a16(w.gu_codes) || !a16(w.dn_codes) || !a16(w.kc) ||
         !a16(w.vc) || !a16(w.router) || !a16(w.ln_post))
       return LEMOQ_ERR_ALIGN;
+  }
+  if (w4) {
+    *path = kAttnW4;
+    return LEMOQ_OK;
   }
   // the attention-output half: one fused launch, two launches, or three
   const int64_t n_part = HD / 512;
@@ -124,11 +153,68 @@ int validate(const LemoqOlmoeStep* p, AttnPath* path) {
 
 }  // namespace
 
+namespace {
+
+// Split-KV attention of one layer: q/k norm, RoPE, cache write at slot *pos,
+// partials over [0, *pos].
+int enqueue_attention(const LemoqOlmoeStep* p, const LemoqOlmoeLayer& w, void* stream) {
+  const int64_t D = p->head_dim, S = p->max_seq;
+  if (p->kv_fp16)
+    return lemoq_attn_split_fused_f16(p->qkv, p->heads, D, w.q_norm, w.k_norm, p->eps, p->cos_tab, p->sin_tab,
+                                      p->pos, reinterpret_cast<uint16_t*>(w.kc),
+                                      reinterpret_cast<uint16_t*>(w.vc), S * D, S, p->num_splits, p->qk_scale,
+                                      p->part_m, p->part_l, p->part_acc, p->clip_qkv, stream);
+  return lemoq_attn_split_fused_i8(p->qkv, p->heads, D, w.q_norm, w.k_norm, p->eps, p->cos_tab, p->sin_tab,
+                                   p->pos, w.kc, w.ks, w.vc, w.vs, S * D, S, p->num_splits, p->qk_scale,
+                                   p->part_m, p->part_l, p->part_acc, p->clip_qkv, stream);
+}
+
+// Final norm + lm_head and the greedy selection / step advance.
+int enqueue_head(const LemoqOlmoeStep* p, void* stream) {
+  const int64_t H = p->hidden;
+  if (p->lm_f16) {
+    LEMOQ_TRY(lemoq_router_logits(p->h, p->final_norm, p->eps, H, p->lm_f16, p->vocab, p->xn, p->logits,
+                                  stream));
+    return lemoq_argmax_advance(p->logits, p->vocab, p->token, p->pos, p->filled, p->prompt, p->prompt_len,
+                                p->history, p->history_len, stream);
+  }
+  return lemoq_lm_head_argmax_w8(p->h, p->final_norm, p->eps, p->lm_codes, p->lm_scale, p->vocab, H,
+                                 p->group, p->logits, p->am_val, p->am_idx, p->am_len, p->token, p->pos,
+                                 p->filled, p->prompt, p->prompt_len, p->history, p->history_len, stream);
+}
+
+// One layer on 4-bit weights (8 launches, 9 on layer 0).
+int enqueue_layer_w4(const LemoqOlmoeStep* p, const LemoqOlmoeLayer& w, bool first, void* stream) {
+  const int64_t H = p->hidden, HD = p->heads * p->head_dim, g = p->group;
+  if (first) LEMOQ_TRY(lemoq_gather_rows(p->embed, p->vocab, H, p->token, 1, p->h, stream));
+  LEMOQ_TRY(lemoq_rmsnorm(p->h, 1, H, w.ln_in, p->eps, p->xn, stream));
+  LEMOQ_TRY(lemoq_gemv_q(p->xn, 1, H, w.qkv_codes, LEMOQ_QFMT_W4, w.qkv_scale, nullptr, 0, 3 * HD, H, g,
+                         p->qkv, 1, stream));
+  LEMOQ_TRY(enqueue_attention(p, w, stream));
+  LEMOQ_TRY(lemoq_attn_merge(p->part_m, p->part_l, p->part_acc, p->heads, p->num_splits, p->head_dim,
+                             p->attn, stream));
+  // o_proj; h = fp16(fp16(o) + h)
+  LEMOQ_TRY(lemoq_gemv_q_residual(p->attn, 1, HD, w.o_codes, LEMOQ_QFMT_W4, w.o_scale, nullptr, 0, H, HD, g,
+                                  p->h, p->h, stream));
+  LEMOQ_TRY(lemoq_router_logits(p->h, w.ln_post, p->eps, H, w.router, p->num_experts, p->xn,
+                                p->router_logits, stream));
+  LEMOQ_TRY(lemoq_moe_gate_up_w4_routed(p->xn, reinterpret_cast<const uint8_t*>(w.gu_codes), w.gu_scale,
+                                        p->router_logits, p->top_k, (int)p->norm_topk_prob, p->num_experts,
+                                        p->ffn, H, g, p->act, p->top_i, p->top_w, stream));
+  return lemoq_moe_down_w4(p->act, reinterpret_cast<const uint8_t*>(w.dn_codes), w.dn_scale, p->top_i, p->top_w,
+                           p->top_k, p->num_experts, H, p->ffn, g, p->h, p->h, stream);
+}
+
+}  // namespace
+
 extern "C" int lemoq_olmoe_decode_step(const LemoqOlmoeStep* p, void* stream) {
   AttnPath path = kAttnThree;
   LEMOQ_TRY(validate(p, &path));
+  if (path == kAttnW4) {
+    for (int64_t L = 0; L < p->num_layers; ++L) LEMOQ_TRY(enqueue_layer_w4(p, p->layers[L], L == 0, stream));
+    return enqueue_head(p, stream);
+  }
   const int64_t H = p->hidden, HD = p->heads * p->head_dim, D = p->head_dim;
-  const int64_t S = p->max_seq;
   const int64_t n_part = HD / 512;
   for (int64_t L = 0; L < p->num_layers; ++L) {
     const LemoqOlmoeLayer& w = p->layers[L];
@@ -139,18 +225,7 @@ extern "C" int lemoq_olmoe_decode_step(const LemoqOlmoeStep* p, void* stream) {
                                   w.ln_in, p->eps, first ? p->h : nullptr, w.qkv_codes,
                                   w.qkv_scale, 3 * HD, H, p->group, nullptr, p->qkv, stream));
     // 2. q/k norm, RoPE, cache write at slot *pos, split-KV partials.
-    if (p->kv_fp16)
-      LEMOQ_TRY(lemoq_attn_split_fused_f16(p->qkv, p->heads, D, w.q_norm, w.k_norm, p->eps,
-                                           p->cos_tab, p->sin_tab, p->pos,
-                                           reinterpret_cast<uint16_t*>(w.kc),
-                                           reinterpret_cast<uint16_t*>(w.vc), S * D, S,
-                                           p->num_splits, p->qk_scale, p->part_m, p->part_l,
-                                           p->part_acc, p->clip_qkv, stream));
-    else
-      LEMOQ_TRY(lemoq_attn_split_fused_i8(p->qkv, p->heads, D, w.q_norm, w.k_norm, p->eps,
-                                          p->cos_tab, p->sin_tab, p->pos, w.kc, w.ks, w.vc, w.vs,
-                                          S * D, S, p->num_splits, p->qk_scale, p->part_m,
-                                          p->part_l, p->part_acc, p->clip_qkv, stream));
+    LEMOQ_TRY(enqueue_attention(p, w, stream));
     if (path == kAttnFusedOut) {
       // 3. LSE merge + o_proj partials per group of 4 heads.
       LEMOQ_TRY(lemoq_attn_merge_o_proj_w8(p->part_m, p->part_l, p->part_acc, p->heads,
@@ -180,9 +255,6 @@ extern "C" int lemoq_olmoe_decode_step(const LemoqOlmoeStep* p, void* stream) {
     LEMOQ_TRY(lemoq_moe_down_w8(p->act, w.dn_codes, w.dn_scale, p->top_i, p->top_w, p->top_k,
                                 p->num_experts, H, p->ffn, p->group, resid, p->h, stream));
   }
-  // Final norm + W8 lm_head with argmax partials, then greedy selection and step advance.
-  return lemoq_lm_head_argmax_w8(p->h, p->final_norm, p->eps, p->lm_codes, p->lm_scale, p->vocab,
-                                 H, p->group, p->logits, p->am_val, p->am_idx, p->am_len,
-                                 p->token, p->pos, p->filled, p->prompt, p->prompt_len,
-                                 p->history, p->history_len, stream);
+  // Final norm + lm_head (W8 with argmax partials, or fp16), then greedy selection and step advance.
+  return enqueue_head(p, stream);
 }

@@ -19,7 +19,7 @@ LIB_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib")
 LIB_NAME = "liblemoq_hip.so"
 LIB_PATH = os.path.join(LIB_DIR, LIB_NAME)
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -106,6 +106,8 @@ class LemoqOlmoeStep(ctypes.Structure):
         ("o_part", _P),
         ("h_mid", _P),
         ("kv_fp16", _I64),
+        ("weight_bits", _I64),
+        ("lm_f16", _P),
     ]
 
 
@@ -121,6 +123,9 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "lemoq_dequant_q": (_I, [_P, _I, _P, _P, _I, _I64, _I64, _I64, _P, _I64, _I64, _I, _P]),
     "lemoq_fake_quant_rows": (_I, [_P, _I64, _I64, _P, _P]),
     "lemoq_moe_gate_up_w4": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P]),
+    "lemoq_moe_gate_up_w4_routed": (
+        _I, [_P, _P, _P, _P, _I64, _I, _I64, _I64, _I64, _I64, _P, _P, _P, _P]),
+    "lemoq_gemv_q_residual": (_I, [_P, _I64, _I64, _P, _I, _P, _P, _I, _I64, _I64, _I64, _P, _P, _P]),
     "lemoq_moe_down_w4": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P]),
     "lemoq_gemv_w8": (_I, [_P, _I64, _I64, _P, _P, _I64, _I64, _I64, _P, _I, _P]),
     "lemoq_gemv_w8_fused": (

@@ -17,6 +17,8 @@ Restates the reference's byte model (``benchmarks/bytes.py:182-411``:
   (The reference's payload still counts KV-INT8 as fp16; this model counts
   what is read.)
 * ``attainment = bytes / seconds / bandwidth``.
+* 4-bit weights (the w4a16 cell: attention and experts at 4 bits, router and
+  lm_head fp16) cost ``rows*in_f/2`` code bytes plus the same scales.
 
 Pinned by the reference's anchors (tests/test_bytes.py:39-79 of LeanMoE-Quant):
 fp16 ``[W]`` = 2,357,723,136 B; fp16 KV read = 134,217,728 B at ctx 1024 and
@@ -34,7 +36,8 @@ __all__ = ["WeightBits", "weight_budget", "kv_read_bytes", "step_bytes", "attain
 
 @dataclass(frozen=True)
 class WeightBits:
-    """Storage of each weight family: 16 (fp16) or 8 (int8 codes + fp16 group scales)."""
+    """Storage of each weight family: 16 (fp16), or 8 / 4 (codes + fp16 group scales;
+    4-bit codes two per byte)."""
 
     attention: int = 8
     experts: int = 8
@@ -44,11 +47,14 @@ class WeightBits:
 
 
 def _matrix_bytes(rows: int, in_f: int, bits: int, group: int) -> int:
+    """fp16 bytes, or packed codes (``params * bits // 8``) plus one fp16 scale per
+    row and group along the input dimension (the reference's ``_quantized_bytes``,
+    ``benchmarks/bytes.py:141-171``)."""
     if bits == 16:
         return rows * in_f * 2
-    if bits == 8:
-        return rows * in_f + rows * (-(-in_f // group)) * 2
-    raise ValueError("bits must be 8 or 16, got %r" % (bits,))
+    if bits in (4, 8):
+        return rows * in_f * bits // 8 + rows * (-(-in_f // group)) * 2
+    raise ValueError("bits must be 4, 8 or 16, got %r" % (bits,))
 
 
 def weight_budget(shape: Any, bits: WeightBits | None = None) -> dict[str, Any]:

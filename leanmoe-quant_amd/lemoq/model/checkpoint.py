@@ -181,17 +181,23 @@ def load_hf_olmoe(path: str, device: Any = "cuda", *, group_size: int = 128,
 
 
 def save_packed(w: OlmoeW8Weights, path: str) -> None:
-    """Write the packed weights (safetensors) and their shape (JSON) to ``path``."""
+    """Write the packed weights (safetensors) and their shape, code width and
+    lm_head kind (JSON) to ``path``."""
     from safetensors.torch import save_file  # noqa: PLC0415
 
     os.makedirs(path, exist_ok=True)
-    tensors = {"embed": w.embed, "final_norm": w.final_norm, "lm_codes": w.lm_codes, "lm_scale": w.lm_scale}
+    tensors = {"embed": w.embed, "final_norm": w.final_norm}
+    if w.lm_f16 is not None:
+        tensors["lm_f16"] = w.lm_f16
+    else:
+        tensors.update(lm_codes=w.lm_codes, lm_scale=w.lm_scale)
     for i, L in enumerate(w.layers):
         for f in fields(LayerW8):
             tensors["layers.%d.%s" % (i, f.name)] = getattr(L, f.name)
     save_file({k: v.detach().to("cpu").contiguous() for k, v in tensors.items()}, os.path.join(path, PACKED_TENSORS))
     with open(os.path.join(path, PACKED_META), "w") as f:
-        json.dump({"format": _FORMAT, "shape": asdict(w.shape)}, f, indent=1, sort_keys=True)
+        json.dump({"format": _FORMAT, "shape": asdict(w.shape), "bits": int(w.bits),
+                   "lm_head": "fp16" if w.lm_f16 is not None else "w8"}, f, indent=1, sort_keys=True)
 
 
 def load_packed(path: str, device: Any = "cuda") -> OlmoeW8Weights:
@@ -208,5 +214,11 @@ def load_packed(path: str, device: Any = "cuda") -> OlmoeW8Weights:
     on = lambda x: x.to(dev).contiguous()  # noqa: E731
     layers = [LayerW8(**{f.name: on(t["layers.%d.%s" % (i, f.name)]) for f in fields(LayerW8)})
               for i in range(shape.layers)]
+    bits, lm_head = int(meta.get("bits", 8)), meta.get("lm_head", "w8")  # files without them: the w8a16 cell
+    if bits not in (4, 8) or lm_head not in ("w8", "fp16"):
+        raise ValueError("unknown packed weights: bits %r, lm_head %r" % (bits, lm_head))
+    if lm_head == "fp16":
+        return OlmoeW8Weights(shape=shape, embed=on(t["embed"]), final_norm=on(t["final_norm"]), lm_codes=None,
+                              lm_scale=None, layers=layers, bits=bits, lm_f16=on(t["lm_f16"]))
     return OlmoeW8Weights(shape=shape, embed=on(t["embed"]), final_norm=on(t["final_norm"]), lm_codes=on(t["lm_codes"]),
-                          lm_scale=on(t["lm_scale"]), layers=layers)
+                          lm_scale=on(t["lm_scale"]), layers=layers, bits=bits)

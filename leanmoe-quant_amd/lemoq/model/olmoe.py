@@ -11,6 +11,10 @@ This replaces the reference's HF-patched model + ``StaticCacheDecodeSession``
 * ``OlmoeW8Weights.random(shape, seed)`` — seeded random init generated and
   RTN-w8-quantized on the device (attention q|k|v packed row-wise, o_proj,
   experts, lm_head); router, embedding and norm weights stay fp16.
+  ``random(..., bits=4, lm_head="fp16")`` gives the reference's w4a16 cell
+  (``--bit-width w4a16``, ``benchmarks/runner.py:451-482``): attention and
+  experts as 4-bit symmetric codes packed two per byte, the lm_head in fp16
+  (``runner.py:393-412``).
 * ``DecodeSession`` — fixed-address KV cache (KV-INT8, or fp16 rows with
   ``kv_cache="fp16"``: the same cell with KV-INT8 off, ``attn_decode.py:930-948,
   999-1008``) and step buffers, the step
@@ -120,12 +124,20 @@ class LayerW8:
 
 @dataclass
 class OlmoeW8Weights:
+    """The decode step's weights.  ``bits`` is the code width of attention and
+    experts: 8 (int8 codes, the canonical w8a16 cell) or 4 (4-bit symmetric
+    codes packed two per byte, the even column in the low nibble: the w4a16
+    cell).  ``lm_f16`` is an fp16 lm_head (vocab, H) in place of ``lm_codes`` /
+    ``lm_scale`` (which are then None)."""
+
     shape: OlmoeShape
     embed: Any
     final_norm: Any
     lm_codes: Any
     lm_scale: Any
     layers: list[LayerW8] = field(default_factory=list)
+    bits: int = 8
+    lm_f16: Any = None
 
     @property
     def device(self) -> Any:
@@ -133,7 +145,7 @@ class OlmoeW8Weights:
 
     def to_host(self) -> "OlmoeW8Weights":
         """Copy every tensor to the CPU (the form the CPU oracle consumes)."""
-        cpu = lambda t: t.detach().to("cpu")  # noqa: E731
+        cpu = lambda t: None if t is None else t.detach().to("cpu")  # noqa: E731
         return OlmoeW8Weights(
             shape=self.shape,
             embed=cpu(self.embed),
@@ -141,20 +153,38 @@ class OlmoeW8Weights:
             lm_codes=cpu(self.lm_codes),
             lm_scale=cpu(self.lm_scale),
             layers=[LayerW8(**{f.name: cpu(getattr(L, f.name)) for f in fields(LayerW8)}) for L in self.layers],
+            bits=self.bits,
+            lm_f16=cpu(self.lm_f16),
         )
 
+    def weight_bits(self) -> Any:
+        """The byte model's storage of each weight family (``lemoq.bytes.WeightBits``)."""
+        from lemoq.bytes import WeightBits  # noqa: PLC0415
+
+        return WeightBits(attention=self.bits, experts=self.bits, lm_head=16 if self.lm_f16 is not None else 8,
+                          group_size=self.shape.group_size)
+
     @classmethod
-    def random(cls, shape: OlmoeShape = OLMOE_1B_7B, *, seed: int = 0, device: Any = "cuda") -> "OlmoeW8Weights":
-        """Seeded random init on the device, RTN-w8-quantized by the HIP kernel.
+    def random(cls, shape: OlmoeShape = OLMOE_1B_7B, *, seed: int = 0, device: Any = "cuda", bits: int = 8,
+               lm_head: str = "w8") -> "OlmoeW8Weights":
+        """Seeded random init on the device, RTN-quantized by the HIP kernel.
 
         Linear, expert, router and embedding weights ~ N(0, init_std) (the HF
         ``_init_weights`` distribution); norm weights ~ U(0.5, 1.5) so that a
         mixed-up norm weight changes the answer.  Generation order is fixed:
         embedding, then per layer (ln_in, ln_post, q_norm, k_norm, q|k|v, o,
-        router, gate_up, down), then final norm, lm_head.
+        router, gate_up, down), then final norm, lm_head.  ``bits`` 8 or 4
+        (attention and experts; RTN symmetric, groups of ``group_size``);
+        ``lm_head`` "w8" (RTN w8) or "fp16".
         """
         from lemoq.quant import rtn  # noqa: PLC0415
 
+        if bits not in (4, 8):
+            raise ValueError("bits must be 4 or 8, got %r" % (bits,))
+        if lm_head not in ("w8", "fp16"):
+            raise ValueError("lm_head must be 'w8' or 'fp16', got %r" % (lm_head,))
+        if bits == 4 and shape.group_size % 32 != 0:
+            raise ValueError("4-bit weights need group_size % 32 == 0, got %d" % shape.group_size)
         dev = torch.device(device)
         _hip.require_rocm(torch.empty(0, device=dev), what="OlmoeW8Weights.random")
         gen = torch.Generator(device=dev)
@@ -169,9 +199,17 @@ class OlmoeW8Weights:
         def gamma(n: int) -> Any:
             return (torch.rand((n,), generator=gen, device=dev, dtype=torch.float32) + 0.5).to(torch.float16)
 
-        def q8(w: Any) -> tuple[Any, Any]:
+        def q8_lm(w: Any) -> tuple[Any, Any]:
             q = rtn.quantize_rtn(w, bits=8, group_size=g)
             return q["codes_padded"], q["scale_f16"]
+
+        def q8(w: Any) -> tuple[Any, Any]:  # attention and experts at `bits`
+            if bits == 8:
+                return q8_lm(w)
+            q = rtn.quantize_rtn(w, bits=4, group_size=g)
+            return q["packed"], q["scale_f16"]
+
+        per = 8 // bits  # codes per byte
 
         embed = normal(s.vocab, s.hidden).to(torch.float16)
         layers = []
@@ -190,15 +228,20 @@ class OlmoeW8Weights:
                 LayerW8(
                     ln_in=ln_in, ln_post=ln_post, q_norm=qn, k_norm=kn,
                     qkv_codes=qkv_c, qkv_scale=qkv_s, o_codes=o_c, o_scale=o_s, router=router,
-                    gu_codes=gu_c.reshape(s.num_experts, 2 * s.ffn, s.hidden),
+                    gu_codes=gu_c.reshape(s.num_experts, 2 * s.ffn, s.hidden // per),
                     gu_scale=gu_s.reshape(s.num_experts, 2 * s.ffn, s.hidden // g),
-                    dn_codes=dn_c.reshape(s.num_experts, s.hidden, s.ffn),
+                    dn_codes=dn_c.reshape(s.num_experts, s.hidden, s.ffn // per),
                     dn_scale=dn_s.reshape(s.num_experts, s.hidden, s.ffn // g),
                 )
             )
         final_norm = gamma(s.hidden)
-        lm_c, lm_s = q8(normal(s.vocab, s.hidden))
-        return cls(shape=s, embed=embed, final_norm=final_norm, lm_codes=lm_c, lm_scale=lm_s, layers=layers)
+        lm = normal(s.vocab, s.hidden)
+        if lm_head == "fp16":
+            return cls(shape=s, embed=embed, final_norm=final_norm, lm_codes=None, lm_scale=None, layers=layers,
+                       bits=bits, lm_f16=lm.to(torch.float16))
+        lm_c, lm_s = q8_lm(lm)
+        return cls(shape=s, embed=embed, final_norm=final_norm, lm_codes=lm_c, lm_scale=lm_s, layers=layers,
+                   bits=bits)
 
 
 class DecodeSession:
@@ -212,7 +255,11 @@ class DecodeSession:
     canonical cell) or ``"fp16"`` (KV-INT8 off: the attention reads the fp16
     rows the step writes, as the reference does without its int8 mirror);
     None follows the reference's ``kv_int8`` switch (``LEMOQ_KV_INT8``, on by
-    default; ``lemoq.kernels.fusion_switches``).
+    default; ``lemoq.kernels.fusion_switches``).  The step follows the weights:
+    4-bit attention and experts (``weights.bits == 4``, the w4a16 cell) and an
+    fp16 lm_head (``weights.lm_f16``) run the step's 4-bit layer and fp16
+    lm_head; their prompt is prefilled through the step (``prefill(mode=
+    "stepped")``), since the batched prefill runs W8 weights.
     """
 
     def __init__(
@@ -329,7 +376,15 @@ class DecodeSession:
         st.qk_scale = float((1.0 / math.sqrt(D)) * LOG2E)
         st.layers = ctypes.cast(self._layer_structs, ctypes.POINTER(_hip.LemoqOlmoeLayer))
         st.embed, st.final_norm = P(weights.embed), P(weights.final_norm)
-        st.lm_codes, st.lm_scale = P(weights.lm_codes), P(weights.lm_scale)
+        if weights.lm_f16 is not None:
+            if not weights.lm_f16.is_contiguous() or weights.lm_f16.device != dev:
+                raise ValueError("lm_f16 must be contiguous on %s" % dev)
+            st.lm_f16, st.lm_codes, st.lm_scale = P(weights.lm_f16), None, None
+        else:
+            st.lm_codes, st.lm_scale, st.lm_f16 = P(weights.lm_codes), P(weights.lm_scale), None
+        if weights.bits not in (4, 8):
+            raise ValueError("weights.bits must be 4 or 8, got %r" % (weights.bits,))
+        st.weight_bits = int(weights.bits)
         st.cos_tab, st.sin_tab = P(self.cos_tab), P(self.sin_tab)
         st.token, st.pos, st.filled = P(self.token), P(self.pos), P(self.filled)
         st.prompt, st.prompt_len = P(self.prompt), self.ctx
@@ -403,16 +458,21 @@ class DecodeSession:
     @property
     def attn_output_fused(self) -> bool:
         """Whether the step runs merge + o_proj as one launch and the residual add
-        in the router launch (the shape rule of csrc/step.hip)."""
+        in the router launch (the shape rule of csrc/step.hip; 8-bit weights only)."""
         s = self.shape
         HD = s.heads * s.head_dim
-        return (bool(self._step.o_part) and bool(self._step.h_mid) and s.head_dim == 128 and s.heads % 4 == 0
+        return (self.weights.bits == 8 and bool(self._step.o_part) and bool(self._step.h_mid)
+                and s.head_dim == 128 and s.heads % 4 == 0
                 and self.num_splits <= 64 and s.hidden in (2048, 4096) and HD // 512 in (1, 2, 4, 8)
                 and s.group_size % 16 == 0 and HD % s.group_size == 0)
 
     @property
     def launches_per_step(self) -> int:
-        """Kernel launches in one captured step (see csrc/step.hip)."""
+        """Kernel launches in one captured step (see csrc/step.hip): 6 or 7 per
+        8-bit layer, 8 per 4-bit layer plus layer 0's embedding gather, and the
+        lm_head and greedy selection."""
+        if self.weights.bits == 4:
+            return 8 * self.shape.layers + 1 + 2
         per_layer = 6 if self.attn_output_fused else 7
         return per_layer * self.shape.layers + 2
 
@@ -477,8 +537,15 @@ class DecodeSession:
         ``mode="stepped"`` feeds the prompt through the captured decode step, one
         replay per position (decode numerics for every prompt token).
         ``kv_f16`` (batched only): a list that receives per layer the fp16 k and v
-        rows the cache bytes were quantised from (see ``prefill_prompt``).
+        rows the cache bytes were quantised from (see ``prefill_prompt``).  The
+        batched prefill runs W8 weights and the W8 lm_head; other weights raise
+        ``NotImplementedError`` there and prefill with ``mode="stepped"``.
         """
+        if mode not in ("batched", "stepped"):
+            raise ValueError("prefill mode must be 'batched' or 'stepped', got %r" % (mode,))
+        if mode == "batched" and (self.weights.bits != 8 or self.weights.lm_f16 is not None):
+            raise NotImplementedError("the batched prefill runs W8 weights and the W8 lm_head; prefill 4-bit "
+                                      "or fp16-lm_head weights with mode='stepped'")
         if self.graph is None:
             self.capture()
         # stream order keeps the reset ahead of the prefill's launches; the
@@ -495,8 +562,6 @@ class DecodeSession:
                            self.logits, step={"token": self.token, "pos": self.pos, "filled": self.filled,
                                               "history": self.history}, kv_f16=kv_f16)
             self._host_pos = self.ctx
-        else:
-            raise ValueError("prefill mode must be 'batched' or 'stepped', got %r" % (mode,))
         self._seed_token = int(self.token.item())
         return self._seed_token
 

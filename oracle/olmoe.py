@@ -18,7 +18,13 @@ as patched by the reference's canonical cell:
 
 Weights come as plain CPU tensors with the same field names as
 ``lemoq.model.olmoe.OlmoeW8Weights``.  Static weights (q|k|v, o, lm_head) are
-dequantised once; experts are dequantised when selected.
+dequantised once; experts are dequantised when selected.  ``bits`` 4 (the
+reference's w4a16 cell: 4-bit symmetric codes of attention and experts,
+packed two per byte, the even column in the low nibble) unpacks the codes
+with ``oracle.quant.unpack_4bit`` first and computes ``code * scale`` as for
+8 bits; ``lm_f16`` (the reference's fp16 lm_head of every cell but w8a16 with
+its lm_head switch on, ``benchmarks/runner.py:393-412``) replaces the W8
+lm_head by an fp16 ``F.linear`` (fp32 accumulation, one fp16 rounding).
 """
 
 from __future__ import annotations
@@ -79,10 +85,16 @@ class HostWeights:
     lm_codes: Any
     lm_scale: Any
     layers: list = field(default_factory=list)
+    bits: int = 8          # attention and expert code width (4: packed two per byte)
+    lm_f16: Any = None     # fp16 lm_head (vocab, H) in place of lm_codes / lm_scale
 
 
-def random_host_weights(shape: Shape, seed: int = 0) -> HostWeights:
-    """Seeded CPU init for tiny CPU-only oracle tests (numpy RTN; not the device generator)."""
+def random_host_weights(shape: Shape, seed: int = 0, *, bits: int = 8, lm_head: str = "w8") -> HostWeights:
+    """Seeded CPU init for tiny CPU-only oracle tests (numpy RTN; not the device
+    generator).  ``bits`` 4 quantises attention and experts to packed 4-bit
+    symmetric codes; ``lm_head`` "fp16" keeps the lm_head in fp16."""
+    if bits not in (4, 8) or lm_head not in ("w8", "fp16"):
+        raise ValueError("bits must be 4 or 8 and lm_head 'w8' or 'fp16'")
     g = torch.Generator().manual_seed(seed)
     s = shape
     HD = s.heads * s.head_dim
@@ -93,9 +105,15 @@ def random_host_weights(shape: Shape, seed: int = 0) -> HostWeights:
     def gamma(n: int) -> Any:
         return (torch.rand((n,), generator=g, dtype=torch.float32) + 0.5).to(torch.float16)
 
-    def q8(w: Any):
+    def q8_lm(w: Any):
         q = oq.rtn_quantize_w8(w.numpy(), s.group_size)
         return torch.from_numpy(q["codes_padded"]), torch.from_numpy(q["scale_f16"])
+
+    def q8(w: Any):
+        if bits == 8:
+            return q8_lm(w)
+        q = oq.rtn_quantize(w.numpy(), bits=4, group_size=s.group_size, symmetric=True)
+        return torch.from_numpy(oq.pack_4bit(q["codes_padded"])), torch.from_numpy(q["scale_f16"])
 
     embed = normal(s.vocab, s.hidden).to(torch.float16)
     layers = []
@@ -106,17 +124,39 @@ def random_host_weights(shape: Shape, seed: int = 0) -> HostWeights:
         router = normal(s.num_experts, s.hidden).to(torch.float16)
         gu_c, gu_s = q8(normal(s.num_experts * 2 * s.ffn, s.hidden))
         dn_c, dn_s = q8(normal(s.num_experts * s.hidden, s.ffn))
+        per = 8 // bits  # codes per byte
         layers.append(HostLayer(
             ln_in=ln_in, ln_post=ln_post, q_norm=qn, k_norm=kn, qkv_codes=qkv_c, qkv_scale=qkv_s,
             o_codes=o_c, o_scale=o_s, router=router,
-            gu_codes=gu_c.reshape(s.num_experts, 2 * s.ffn, s.hidden),
+            gu_codes=gu_c.reshape(s.num_experts, 2 * s.ffn, s.hidden // per),
             gu_scale=gu_s.reshape(s.num_experts, 2 * s.ffn, s.hidden // s.group_size),
-            dn_codes=dn_c.reshape(s.num_experts, s.hidden, s.ffn),
+            dn_codes=dn_c.reshape(s.num_experts, s.hidden, s.ffn // per),
             dn_scale=dn_s.reshape(s.num_experts, s.hidden, s.ffn // s.group_size),
         ))
     final_norm = gamma(s.hidden)
-    lm_c, lm_s = q8(normal(s.vocab, s.hidden))
-    return HostWeights(shape=s, embed=embed, final_norm=final_norm, lm_codes=lm_c, lm_scale=lm_s, layers=layers)
+    lm = normal(s.vocab, s.hidden)
+    if lm_head == "fp16":
+        return HostWeights(shape=s, embed=embed, final_norm=final_norm, lm_codes=None, lm_scale=None,
+                           layers=layers, bits=bits, lm_f16=lm.to(torch.float16))
+    lm_c, lm_s = q8_lm(lm)
+    return HostWeights(shape=s, embed=embed, final_norm=final_norm, lm_codes=lm_c, lm_scale=lm_s, layers=layers,
+                       bits=bits)
+
+
+def unpacked_codes(codes: Any, bits: int) -> Any:
+    """The codes as int8 values: 8-bit codes as they are, 4-bit ones unpacked
+    (``oracle.quant.unpack_4bit``, signed, low nibble first)."""
+    if int(bits) == 8:
+        return codes
+    return torch.from_numpy(oq.unpack_4bit(codes.numpy(), signed=True))
+
+
+def lm_head_weight(weights: Any) -> Any:
+    """The lm_head as fp32 values: the fp16 lm_head, or the W8 one dequantised."""
+    lm_f16 = getattr(weights, "lm_f16", None)
+    if lm_f16 is not None:
+        return lm_f16.to(torch.float32)
+    return ops.dequant_w8(weights.lm_codes, weights.lm_scale, weights.shape.group_size)
 
 
 class OracleDecoder:
@@ -130,9 +170,12 @@ class OracleDecoder:
         self.s = s
         self.max_seq = int(max_seq)
         g = s.group_size
-        self.qkv_w = [ops.dequant_w8(L.qkv_codes, L.qkv_scale, g) for L in weights.layers]
-        self.o_w = [ops.dequant_w8(L.o_codes, L.o_scale, g) for L in weights.layers]
-        self.lm_w = ops.dequant_w8(weights.lm_codes, weights.lm_scale, g)
+        self.bits = int(getattr(weights, "bits", 8))
+        if self.bits not in (4, 8):
+            raise ValueError("weights.bits must be 4 or 8")
+        self.qkv_w = [ops.dequant_w8(unpacked_codes(L.qkv_codes, self.bits), L.qkv_scale, g) for L in weights.layers]
+        self.o_w = [ops.dequant_w8(unpacked_codes(L.o_codes, self.bits), L.o_scale, g) for L in weights.layers]
+        self.lm_w = lm_head_weight(weights)
         cos, sin = ops.rotary_cos_sin(torch.arange(self.max_seq), s.head_dim, s.rope_theta)
         self.cos, self.sin = cos, sin
         if kv is not None:
@@ -207,8 +250,14 @@ class OracleDecoder:
             r = h
             xn = ops.rms_norm(h, L.ln_post, s.eps)
             logits_r, top_w, top_i = ops.route(xn.reshape(1, -1), L.router, s.top_k, s.norm_topk_prob)
-            moe, act = ops.grouped_moe_w8(xn, L.gu_codes, L.gu_scale, L.dn_codes, L.dn_scale,
-                                          s.group_size, top_i.reshape(-1), top_w.reshape(-1))
+            ids = top_i.reshape(-1)
+            if self.bits == 8:
+                moe, act = ops.grouped_moe_w8(xn, L.gu_codes, L.gu_scale, L.dn_codes, L.dn_scale,
+                                              s.group_size, ids, top_w.reshape(-1))
+            else:  # the selected experts' codes unpacked; slot i reads row i of them
+                moe, act = ops.grouped_moe_w8(xn, unpacked_codes(L.gu_codes[ids], 4), L.gu_scale[ids],
+                                              unpacked_codes(L.dn_codes[ids], 4), L.dn_scale[ids],
+                                              s.group_size, torch.arange(ids.numel()), top_w.reshape(-1))
             h = r + moe
             if keep_trace:
                 self.trace.setdefault("top_i", []).append(top_i.reshape(-1).clone())
@@ -275,6 +324,8 @@ def oracle_prefill(weights: Any, tokens: Any, max_seq: int, *, all_logits: bool 
     (logits are then None).
     """
     s, w = weights.shape, weights
+    if int(getattr(weights, "bits", 8)) != 8 or getattr(weights, "lm_f16", None) is not None:
+        raise NotImplementedError("oracle_prefill restates the w8a16 cell's prefill (W8 weights and lm_head)")
     toks = torch.as_tensor(tokens, dtype=torch.int64).reshape(-1)
     T = int(toks.numel())
     NH, D = s.heads, s.head_dim

@@ -76,3 +76,22 @@ def test_step_split_rule():
         for heads in (1, 2, 16, 64, 300):
             ns = step_num_splits(S, heads, 256)
             assert ns >= 1 and (heads * ns <= 256 or ns == 1)
+
+
+def test_w4a16_cell_bytes():
+    """The w4a16 cell (attention + experts at 4 bits, router and lm_head fp16):
+    the reference's anchors (tests/test_bytes.py:88-105 of LeanMoE-Quant) -- the
+    fp16 lm_head streams 103,022,592 x 2 bytes and the whole [W] shrinks by less
+    than 4x against fp16 -- and the per-call figures the 4-bit kernels move."""
+    bits = WeightBits(attention=4, experts=4, lm_head=16)
+    w = weight_budget(OLMOE_1B_7B, bits)
+    by = {it["name"]: it["bytes"] for it in w["items"]}
+    assert by["lm_head"] == 103_022_592 * 2
+    assert 2.5 < weight_budget(OLMOE_1B_7B, FP16)["total_bytes"] / w["total_bytes"] < 4.0
+    # per layer: q|k|v 6144 x 1024 codes + 6144 x 16 scales, o_proj 2048 x 1024 + 2048 x 16,
+    # 8 experts x (2048 x 1024 + 2048 x 16 gate/up, 2048 x 512 + 2048 x 8 down)
+    assert by["attention"] == 16 * ((6144 * 1024 + 6144 * 32) + (2048 * 1024 + 2048 * 32))
+    assert by["experts(top-k)"] == 16 * 8 * ((2048 * 1024 + 2048 * 32) + (2048 * 512 + 2048 * 16))
+    assert w["total_bytes"] == by["attention"] + by["experts(top-k)"] + by["lm_head"] + by["router"]
+    with pytest.raises(ValueError):
+        weight_budget(OLMOE_1B_7B, WeightBits(attention=3))

@@ -212,3 +212,34 @@ def test_untied_checkpoint_without_lm_head_is_refused(saved):
     tied = ck.quantize_state_dict(no_lm, shape, device="cpu", quantizer=_rtn, tie_word_embeddings=True)
     c, _ = _rtn(sd["model.embed_tokens.weight"].float(), 128)
     assert torch.equal(tied.lm_codes, c)
+
+
+def test_packed_round_trip_of_4bit_weights_with_fp16_lm_head(tmp_path):
+    """The w4a16 cell's weights (4-bit attention and experts packed two per byte,
+    fp16 lm_head) keep their code width and lm_head kind through save/load, bit
+    for bit; a file without the two keys reads as the w8a16 cell."""
+    from dataclasses import asdict
+
+    from lemoq.model.olmoe import OlmoeShape, OlmoeW8Weights
+    from oracle.olmoe import Shape, random_host_weights
+
+    small = Shape(hidden=256, heads=2, head_dim=128, layers=2, num_experts=4, top_k=2, ffn=128, vocab=64)
+    hw = random_host_weights(small, seed=3, bits=4, lm_head="fp16")
+    w = OlmoeW8Weights(shape=OlmoeShape(**asdict(small)), embed=hw.embed, final_norm=hw.final_norm, lm_codes=None,
+                       lm_scale=None, layers=[LayerW8(**{f.name: getattr(L, f.name) for f in fields(LayerW8)})
+                                              for L in hw.layers], bits=4, lm_f16=hw.lm_f16)
+    ck.save_packed(w, str(tmp_path))
+    w2 = ck.load_packed(str(tmp_path), device="cpu")
+    assert (w2.bits, w2.lm_codes, w2.lm_scale) == (4, None, None)
+    assert torch.equal(w2.lm_f16, w.lm_f16) and w2.layers[0].gu_codes.shape == (4, 256, 128)
+    for i, (la, lb) in enumerate(zip(w.layers, w2.layers)):
+        for f in fields(LayerW8):
+            assert torch.equal(getattr(la, f.name), getattr(lb, f.name)), (i, f.name)
+    with open(os.path.join(str(tmp_path), ck.PACKED_META)) as f:
+        meta = json.load(f)
+    assert (meta["bits"], meta["lm_head"]) == (4, "fp16")
+    meta["bits"] = 3
+    with open(os.path.join(str(tmp_path), ck.PACKED_META), "w") as f:
+        json.dump(meta, f)
+    with pytest.raises(ValueError):
+        ck.load_packed(str(tmp_path), device="cpu")

@@ -162,6 +162,18 @@ def test_argument_rejection_happens_before_any_launch():
     assert lib.lemoq_rtn_quantize(fake, 4, 130, 128, 6, 1, fake, None, None, None, None, None) == -3
     assert lib.lemoq_mxfp4_quantize(fake, 4, 0, fake, fake, None) == -2
     assert lib.lemoq_fake_quant_rows(fake, 4, 0, fake, None) == -2
+    # o_proj + residual of the 4-bit step: residual required; y itself or apart from it
+    gr = lambda res, y, M=1, N=64: lib.lemoq_gemv_q_residual(  # noqa: E731
+        fake, M, 128, fake, 2, fake, None, 0, N, 128, 128, res, y, None)
+    assert gr(None, 1 << 22) == -1 and gr(1 << 22, None) == -1
+    assert gr(1 << 22, (1 << 22) + 64) == -2                # partial overlap
+    assert gr(1 << 22, 1 << 23, N=64, M=0) == -2            # then the GEMV's own rules
+    # routed 4-bit gate/up: ids/weights outputs, top_k <= min(64, E), E <= 256, 4-bit groups
+    gu = lambda E=64, K=8, g=128, ti=fake, tw=fake: lib.lemoq_moe_gate_up_w4_routed(  # noqa: E731
+        fake, fake, fake, fake, K, 0, E, 1024, 2048, g, fake, ti, tw, None)
+    assert gu(ti=None) == -1 and gu(tw=None) == -1
+    assert gu(K=65, E=128) == -2 and gu(E=4, K=8) == -2
+    assert gu(E=300) == -3 and gu(g=16) == -3
     with pytest.raises(ValueError):
         _hip.call("lemoq_gemv_w8", None, 1, 16, None, None, 16, 16, 16, None, 1, None)
 
@@ -193,6 +205,7 @@ def _fake_step(**over):
             setattr(st, name, nxt())
     st.prompt_len, st.history_len = 4, 1200
     st.am_len = int(_hip.load().lemoq_lm_head_argmax_parts(50304))
+    st.weight_bits, st.lm_f16 = 8, None  # the w8a16 cell with the W8 lm_head
     for k, v in over.items():
         setattr(st, k, v)
     return st, layers
@@ -235,3 +248,16 @@ def test_decode_step_rejects_before_any_launch():
     st, layers = _fake_step()
     layers[0].ks = None                                     # KV-INT8 without its scales
     assert lib.lemoq_olmoe_decode_step(ctypes.byref(st), None) == -1
+    # weight bits 8 or 4; the 4-bit layer's GEMV / MoE rules; the fp16 lm_head's
+    assert step(weight_bits=0) == -3 and step(weight_bits=5) == -3
+    assert step(weight_bits=4, group=16) == -3              # 4-bit groups of 32
+    assert step(weight_bits=4, ffn=1008) == -3              # 4-bit down: ffn % 32
+    assert step(weight_bits=4, num_splits=2000) == -2       # the merge of the 4-bit layer
+    assert step(weight_bits=4, attn=(1 << 30) + 8) == -4    # merge output / o_proj input alignment
+    assert step(weight_bits=4, num_experts=300) == -3       # routed 4-bit gate/up: > 256 experts
+    big = 1 << 30
+    assert step(lm_f16=big, vocab=70000) == -3              # fp16 lm_head: vocab <= 65536 rows
+    assert step(lm_f16=big + 8) == -4                       # fp16 lm_head alignment
+    # with an fp16 lm_head the W8 lm_head and its partials may be absent (a later rule rejects)
+    assert step(lm_f16=big, lm_codes=None, am_val=None, am_idx=None, am_len=0, top_k=65) == -2
+    assert step(lm_codes=None) == -1 and step(am_idx=None) == -1

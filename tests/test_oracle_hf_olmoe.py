@@ -32,7 +32,7 @@ import pytest
 import torch
 
 from oracle import ops
-from oracle.olmoe import OracleDecoder, Shape, random_host_weights
+from oracle.olmoe import OracleDecoder, Shape, lm_head_weight, random_host_weights, unpacked_codes
 
 transformers = pytest.importorskip("transformers")
 
@@ -59,7 +59,7 @@ def _hf_model(hw):
     g, HD, E = s.group_size, s.heads * s.head_dim, s.num_experts
 
     def dq(codes, scale):
-        return ops.dequant_w8(codes, scale, g).double()
+        return ops.dequant_w8(unpacked_codes(codes, getattr(hw, "bits", 8)), scale, g).double()
 
     with torch.no_grad():
         m.model.embed_tokens.weight.copy_(hw.embed.double())
@@ -78,7 +78,7 @@ def _hf_model(hw):
             layer.mlp.experts.gate_up_proj.copy_(torch.stack([dq(L.gu_codes[e], L.gu_scale[e]) for e in range(E)]))
             layer.mlp.experts.down_proj.copy_(torch.stack([dq(L.dn_codes[e], L.dn_scale[e]) for e in range(E)]))
         m.model.norm.weight.copy_(hw.final_norm.double())
-        m.lm_head.weight.copy_(dq(hw.lm_codes, hw.lm_scale))
+        m.lm_head.weight.copy_(lm_head_weight(hw).double())
     return m
 
 
@@ -266,3 +266,40 @@ def test_planted_fp16_cache_mistake_fails_the_hf_gate(mistake, monkeypatch):
     monkeypatch.setattr(ops, name, fn)
     ok, (kl, rel) = _passes(ref, _oracle_logits_fp16(hw, toks))
     assert not ok, "%s went unnoticed: median KL %.3e, median rel %.4f" % (mistake, kl, rel)
+
+
+# ---------------------------------------------------------------------------
+# The reference's w4a16 cell: attention and experts as 4-bit symmetric codes
+# (packed two per byte), the lm_head in fp16 (benchmarks/runner.py:393-412,
+# 451-482).  HF is loaded with the same unpacked, dequantised weights and the
+# fp16 lm_head, so the same gate applies; a planted nibble-order mistake in the
+# unpacking (high nibble first) fails it.
+@pytest.mark.parametrize("seed", [5, 6])
+def test_oracle_w4_fp16_lm_head_matches_hf_olmoe(seed):
+    hw = random_host_weights(SHAPE, seed=seed, bits=4, lm_head="fp16")
+    assert hw.layers[0].qkv_codes.shape[1] == SHAPE.hidden // 2 and hw.lm_codes is None
+    toks = torch.randint(0, SHAPE.vocab, (N_POS,), generator=torch.Generator().manual_seed(seed + 300))
+    with torch.no_grad():
+        ref = _hf_model(hw)(toks[None]).logits[0]
+    ok, (kl, rel) = _passes(ref, _oracle_logits(hw, toks))
+    assert ok, "median KL %.3e, median rel %.4f" % (kl, rel)
+
+
+def test_planted_nibble_order_fails_the_w4_hf_gate(monkeypatch):
+    import oracle.olmoe as om
+
+    hw = random_host_weights(SHAPE, seed=5, bits=4, lm_head="fp16")
+    toks = torch.randint(0, SHAPE.vocab, (N_POS,), generator=torch.Generator().manual_seed(305))
+    with torch.no_grad():
+        ref = _hf_model(hw)(toks[None]).logits[0]
+    orig = om.unpacked_codes
+
+    def swapped(codes, bits):
+        u = orig(codes, bits)
+        if int(bits) != 4:
+            return u
+        return u.reshape(*u.shape[:-1], -1, 2).flip(-1).reshape(u.shape)  # high nibble first
+
+    monkeypatch.setattr(om, "unpacked_codes", swapped)
+    ok, (kl, rel) = _passes(ref, _oracle_logits(hw, toks))
+    assert not ok, "a swapped nibble order went unnoticed: median KL %.3e, median rel %.4f" % (kl, rel)
