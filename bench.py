@@ -96,6 +96,12 @@ def parse_args(argv=None):
     ap.add_argument("--no-kv-fp16", action="store_true", help="skip the fp16-cache (KV-INT8 off) step timing")
     ap.add_argument("--kv-cache", choices=("int8", "fp16"), default="int8",
                     help="--mode step: the decode cache kind (fp16 = the cell with KV-INT8 off)")
+    ap.add_argument("--weights", choices=("w8a16", "w4a16"), default="w8a16",
+                    help="--mode step: the cell's weights (w4a16: 4-bit attention and experts, fp16 lm_head; "
+                         "its prompt is fed through the step)")
+    ap.add_argument("--no-w4a16", action="store_true", help="skip the w4a16-cell step timing")
+    ap.add_argument("--summarize-last", type=int, default=0,
+                    help="--summarize-step: keep only the last N whole steps (0: all)")
     ap.add_argument("--mode", choices=("full", "kernels", "traffic", "prefill", "step"), default="full")
     ap.add_argument("--summarize-pmc", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "PLAN_JSON"))
     ap.add_argument("--summarize-prefill", metavar="KERNEL_TRACE_CSV",
@@ -464,6 +470,34 @@ def time_kv_fp16(torch, w, ctx: int, steps: int, warmup: int, read_bw: float) ->
            "step_bytes": int(nbytes), "step_hbm_frac_of_measured": nbytes / (dev_ms * 1e-3) / 1e9 / read_bw,
            "launches_per_step": launches}
     log("ctx %d fp16 cache: %.4f ms/token (repeats p50), device %.4f" % (ctx, ms, dev_ms))
+    return res
+
+
+def time_w4a16(torch, shape, seed: int, dev, ctx: int, steps: int, warmup: int, read_bw: float) -> dict:
+    """The reference's w4a16 cell (4-bit attention and experts, router and lm_head
+    fp16, KV-INT8; ``--bit-width w4a16``, benchmarks/runner.py:393-412,451-482) on
+    the same shape: the prompt ``[1] * ctx`` fed through the step (the batched
+    prefill runs W8 weights), then the headline's repeated timing, and the
+    cell's bytes per step (``lemoq.bytes`` at 4 bits)."""
+    from lemoq.bytes import step_bytes
+    from lemoq.model.olmoe import DecodeSession, OlmoeW8Weights
+
+    w4 = OlmoeW8Weights.random(shape, seed=seed, device=dev, bits=4, lm_head="fp16")
+    sess = DecodeSession(w4, [1] * ctx, max_new_tokens=max(warmup, 5) + max(steps, 20) + 4, kv_cache="int8")
+    sess.capture()
+    sess.prefill(mode="stepped")
+    rep = measure_repeats(torch, sess, warmup=max(warmup, 5), timed=max(steps, 20), repeats=3)
+    ms = sorted(rep["wall_ms"])[1]
+    dev_ms = sorted(rep["event_ms"])[1]
+    filled_avg = ctx + 1 + (rep["timed"] - 1) / 2.0
+    nbytes = step_bytes(shape, 0, bits=w4.weight_bits()) + KV_BYTES_PER_TOKEN_LAYER * shape.layers * filled_avg
+    launches = sess.launches_per_step
+    del sess, w4
+    torch.cuda.empty_cache()
+    res = {"ms_per_token_repeats_p50": ms, "device_ms_per_token": dev_ms, "wall_spread": rep["wall_spread"],
+           "step_bytes": int(nbytes), "step_hbm_frac_of_measured": nbytes / (dev_ms * 1e-3) / 1e9 / read_bw,
+           "launches_per_step": launches}
+    log("ctx %d w4a16: %.4f ms/token (repeats p50), device %.4f" % (ctx, ms, dev_ms))
     return res
 
 
@@ -967,7 +1001,7 @@ def main(argv=None) -> int:
         print(summarize_trace(args.summarize_trace))
         return 0
     if args.summarize_step:
-        print(summarize_step(args.summarize_step))
+        print(summarize_step(args.summarize_step, last=args.summarize_last))
         return 0
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -1005,18 +1039,23 @@ def main(argv=None) -> int:
         return 0
 
     if args.mode == "step":
-        from lemoq.model.olmoe import DecodeSession
+        from lemoq.model.olmoe import DecodeSession, OlmoeW8Weights
 
+        w4 = args.weights == "w4a16"
+        if w4:
+            del w
+            torch.cuda.empty_cache()
+            w = OlmoeW8Weights.random(OLMOE_1B_7B, seed=args.seed, device=dev, bits=4, lm_head="fp16")
         sess = DecodeSession(w, [1] * args.ctx, max_new_tokens=args.warmup + args.steps + 1, kv_cache=args.kv_cache)
         sess.capture()
-        sess.prefill()
+        sess.prefill(mode="stepped" if w4 else "batched")
         sess.replay(args.warmup)
         t0 = time.perf_counter()
         sess.replay(args.steps)
         ms = (time.perf_counter() - t0) * 1e3 / args.steps
         log("ctx %d: %d replays, %.4f ms/token" % (args.ctx, args.steps, ms))
-        print(json.dumps({"mode": "step", "ctx": args.ctx, "kv_cache": args.kv_cache, "steps": args.steps,
-                          "ms_per_token": ms, "launches_per_step": sess.launches_per_step}))
+        print(json.dumps({"mode": "step", "ctx": args.ctx, "kv_cache": args.kv_cache, "weights": args.weights,
+                          "steps": args.steps, "ms_per_token": ms, "launches_per_step": sess.launches_per_step}))
         return 0
 
     if args.mode == "prefill":
@@ -1063,6 +1102,12 @@ def main(argv=None) -> int:
         sess = None
         kv16 = {str(c): time_kv_fp16(torch, w, c, args.steps, args.warmup, read_bw)
                 for c in (args.ctx, args.ctx2) if c}
+    w4a16 = None
+    if not args.no_w4a16:
+        del sess
+        sess = None
+        w4a16 = {str(c): time_w4a16(torch, OLMOE_1B_7B, args.seed, dev, c, args.steps, args.warmup, read_bw)
+                 for c in (args.ctx, args.ctx2) if c}
     del sess
     r2 = None
     snap2 = None
@@ -1155,6 +1200,12 @@ def main(argv=None) -> int:
         kv16["what"] = ("the same step over the fp16 cache (DecodeSession(kv_cache='fp16'): the reference's cell "
                         "with KV-INT8 off), prompt ctx x token 1, timed as the headline")
         line["kv_fp16"] = kv16
+    if w4a16 is not None:
+        w4a16["what"] = ("the reference's w4a16 cell on the same shape: attention and experts as 4-bit symmetric RTN "
+                         "codes (g128), router and lm_head fp16, KV-INT8 (OlmoeW8Weights.random(bits=4, "
+                         "lm_head='fp16')); prompt ctx x token 1 fed through the step, timed as the headline; the "
+                         "reference publishes no w4a16 latency (its accuracy gate fails, RESULTS.md:166)")
+        line["w4a16"] = w4a16
     line["step_ms_p50"], line["step_ms_p99"] = r1["step_ms_p50"], r1["step_ms_p99"]
     gk = "ms_per_token_graph%d" % MULTI_STEPS
     line[gk] = r1[gk]  # MULTI_STEPS steps per graph launch (not the headline)
@@ -1334,18 +1385,41 @@ STEP_TAIL_KERNELS = [("lm_head (+ final norm, argmax partials)", "gemv_w8_kernel
                      ("argmax + advance", "argmax_advance_kernel<true>")]
 
 
-def summarize_step(trace_csv: str) -> str:
+# The 4-bit step (--weights w4a16) by position: layer 0's embedding gather, then per
+# layer the 7 launches below, then the fp16 lm_head and the greedy pick.  The router
+# and the fp16 lm_head are one kernel instance, so the launches are told apart by
+# their place in the step.
+STEP_W4_LAYER = ["qkv GEMV (4-bit, + input RMSNorm)", "attention split (+ q/k norm, RoPE, cache write)",
+                 "LSE merge", "o_proj GEMV (4-bit, + residual)", "router (+ post-attention norm)",
+                 "gate/up (4-bit, + routing)", "down (4-bit, + residual)"]
+STEP_W4_HEAD = ["lm_head fp16 (+ final norm)", "argmax + advance"]
+STEP_W4_END = "argmax_advance_kernel<false>"
+
+
+def _w4_roles() -> list:
+    """Role of each launch of a whole 4-bit step, by position."""
+    roles = ["embedding gather"]
+    for _ in range(16):
+        roles += STEP_W4_LAYER
+    return roles + STEP_W4_HEAD
+
+
+def summarize_step(trace_csv: str, last: int = 0) -> str:
     """Per-kernel durations of the decode step's graph replays in a rocprofv3
     kernel trace of ``bench.py --mode step``, and the step's timeline: each step
     is the run of the step's kernels ending with the argmax launch; its span is
     first start to last end, its busy time the sum of its kernels' durations,
     and the rest of the span is the time between kernels (launch and dispatch
-    gaps inside the graph)."""
+    gaps inside the graph).  ``last`` keeps only the last N whole steps (the
+    4-bit step's prompt is fed through the step itself).  A trace of the 4-bit
+    step (``--weights w4a16``) is recognised by its argmax kernel."""
     import csv as _csv
 
+    all_rows = list(_csv.DictReader(open(trace_csv)))
+    if any(STEP_W4_END in _short_kernel(r["Kernel_Name"]) for r in all_rows):
+        return _summarize_step_w4(all_rows, last, trace_csv)
     names = [k for _, k in STEP_LAYER_KERNELS + STEP_TAIL_KERNELS]
-    rows = sorted((r for r in _csv.DictReader(open(trace_csv))
-                   if any(n in _short_kernel(r["Kernel_Name"]) for n in names)),
+    rows = sorted((r for r in all_rows if any(n in _short_kernel(r["Kernel_Name"]) for n in names)),
                   key=lambda r: int(r["Start_Timestamp"]))
     steps, cur = [], []
     for r in rows:
@@ -1355,19 +1429,53 @@ def summarize_step(trace_csv: str) -> str:
             cur = []
     per_step = len(STEP_LAYER_KERNELS) * 16 + len(STEP_TAIL_KERNELS)
     steps = [st for st in steps if len(st) == per_step]  # whole 16-layer steps only (the prefill's seed pick is not)
+    if last > 0:
+        steps = steps[-last:]
     if not steps:
         return "no whole decode steps in %s" % trace_csv
+    labels = [lbl for lbl, _ in STEP_LAYER_KERNELS + STEP_TAIL_KERNELS]
+
+    def role(i, r):
+        return next(lbl for lbl, k in STEP_LAYER_KERNELS + STEP_TAIL_KERNELS if k in _short_kernel(r["Kernel_Name"]))
+
+    return _step_table(steps, per_step, labels, role)
+
+
+def _summarize_step_w4(all_rows: list, last: int, trace_csv: str) -> str:
+    """``summarize_step`` of the 4-bit step: every dispatch between two greedy
+    picks is one step (the graph holds nothing else), roles by position."""
+    rows = sorted(all_rows, key=lambda r: int(r["Start_Timestamp"]))
+    steps, cur = [], []
+    for r in rows:
+        cur.append(r)
+        if STEP_W4_END in _short_kernel(r["Kernel_Name"]):
+            steps.append(cur)
+            cur = []
+    roles = _w4_roles()
+    per_step = len(roles)
+    # a chunk may start with other dispatches before the step (the first one after
+    # the session's set-up): keep its last per_step launches when they open with the gather
+    steps = [st[-per_step:] for st in steps
+             if len(st) >= per_step and "gather_rows_kernel" in _short_kernel(st[-per_step]["Kernel_Name"])]
+    if last > 0:
+        steps = steps[-last:]
+    if not steps:
+        return "no whole 4-bit decode steps in %s" % trace_csv
+    labels = ["embedding gather"] + STEP_W4_LAYER + STEP_W4_HEAD
+    return _step_table(steps, per_step, labels, lambda i, r: roles[i])
+
+
+def _step_table(steps: list, per_step: int, labels: list, role) -> str:
     dur: dict = {}
     spans, busy = [], []
     for st in steps:
         t0, t1 = int(st[0]["Start_Timestamp"]), int(st[-1]["End_Timestamp"])
         spans.append((t1 - t0) * 1e-3)
         b = 0.0
-        for r in st:
+        for i, r in enumerate(st):
             d = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-3
             b += d
-            key = next(lbl for lbl, k in STEP_LAYER_KERNELS + STEP_TAIL_KERNELS if k in _short_kernel(r["Kernel_Name"]))
-            dur.setdefault(key, []).append(d)
+            dur.setdefault(role(i, r), []).append(d)
         busy.append(b)
     spans.sort()
     busy.sort()
@@ -1378,7 +1486,7 @@ def summarize_step(trace_csv: str) -> str:
                100.0 * (spans[n // 2] - busy[n // 2]) / spans[n // 2]), "",
            "| kernel | launches per step | avg us | p50 us | min us | max us | us per step |", "|---|---|---|---|---|---|---|"]
     tot = 0.0
-    for lbl, _ in STEP_LAYER_KERNELS + STEP_TAIL_KERNELS:
+    for lbl in labels:
         v = sorted(dur.get(lbl, []))
         if not v:
             continue

@@ -127,6 +127,19 @@ int lemoq_gemv_q(const uint16_t* x, int64_t M, int64_t K, const void* qweight, i
                  const void* scale, const void* zero, int scale_is_f32, int64_t N,
                  int64_t padded_k, int64_t group, void* y, int y_is_f16, void* stream);
 
+/* lemoq_gemv_q of the RMSNorm of x (the decoder layer's input norm before the
+ * packed q|k|v projection, rms_norm_fused then dequant_gemm_fused,
+ * src/lemoq/kernels/rmsnorm.py:102-163, _dequant_triton.py:155-293): each
+ * wave normalises the row it holds, xn = fp16(fp16(x * rsqrt(mean(x^2) + eps))
+ * * norm_w) with an fp32 mean over K (lemoq_rmsnorm's rounding points; the
+ * fp32 sum of squares runs in another order, so an element may differ from
+ * lemoq_rmsnorm's by one fp16 ulp), then y = xn @ w^T as lemoq_gemv_q.
+ * norm_w (K) fp16; fp16 or E8M0 scales only (scale_is_f32 returns
+ * LEMOQ_ERR_UNSUPPORTED); eps >= 0.  Used by the 4-bit decode step. */
+int lemoq_gemv_q_rmsnorm(const uint16_t* x, int64_t M, int64_t K, const uint16_t* norm_w, float eps,
+                         const void* qweight, int fmt, const void* scale, const void* zero, int scale_is_f32,
+                         int64_t N, int64_t padded_k, int64_t group, void* y, int y_is_f16, void* stream);
+
 /* lemoq_gemv_q with the fp16 residual add of the decoder layer after o_proj
  * (transformers OlmoeDecoderLayer.forward, the `residual + hidden_states` of
  * fp16 tensors): y (M, N) fp16 = fp16(fp16(x @ w^T) + residual), one rounding
@@ -621,8 +634,8 @@ typedef struct LemoqOlmoeStep {
    * above) or 4 (the reference's w4a16 cell: 4-bit symmetric codes packed two
    * per byte, the even column in the low nibble, so qkv_codes (3*heads*D,
    * H/2), o_codes (H, heads*D/2), gu_codes (E, 2F, H/2), dn_codes (E, H, F/2);
-   * scales as above; group % 32 == 0).  A 4-bit step runs 8 launches per
-   * layer: lemoq_rmsnorm, lemoq_gemv_q (q|k|v), the fused attention,
+   * scales as above; group % 32 == 0).  A 4-bit step runs 7 launches per
+   * layer: lemoq_gemv_q_rmsnorm (input norm + q|k|v), the fused attention,
    * lemoq_attn_merge, lemoq_gemv_q_residual (o_proj + residual into h),
    * lemoq_router_logits, lemoq_moe_gate_up_w4_routed, lemoq_moe_down_w4
    * (+ residual into h); layer 0 first gathers the embedding row into h

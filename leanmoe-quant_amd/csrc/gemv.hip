@@ -356,29 +356,74 @@ __device__ __forceinline__ void argmax_fold_pass(const float (&v)[kArgmaxPass],
     }
 }
 
-template <bool PARTIALS>
+// fp16 logits with n % 8 == 0 and a 16-byte aligned row: 8 candidates per
+// 16-byte load, kArgmaxPass loads per thread per pass (65536 candidates a pass,
+// a 50304-row vocabulary in one).
+__device__ __forceinline__ void argmax_load_pass_vec(const uint16_t* __restrict__ logits, int64_t nv,
+                                                     int64_t vbase, int tid, u32x4 (&w)[kArgmaxPass]) {
+#pragma unroll
+  for (int j = 0; j < kArgmaxPass; ++j) {
+    const int64_t q = vbase + (int64_t)j * 1024 + tid;
+    w[j] = *reinterpret_cast<const u32x4*>(logits + (q < nv ? q : nv - 1) * 8);  // clamped, unconditional
+  }
+}
+
+__device__ __forceinline__ void argmax_fold_pass_vec(const u32x4 (&w)[kArgmaxPass], int64_t nv, int64_t vbase,
+                                                     int tid, float& bv, int& bi) {
+#pragma unroll
+  for (int j = 0; j < kArgmaxPass; ++j) {
+    const int64_t q = vbase + (int64_t)j * 1024 + tid;
+    if (q >= nv) continue;
+    const uint32_t h[4] = {w[j].x, w[j].y, w[j].z, w[j].w};
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float v = h2f((uint16_t)(h[k >> 1] >> (16 * (k & 1))));
+      const int i = (int)(q * 8 + k);
+      if (v > bv || (v == bv && i < bi)) {
+        bv = v;
+        bi = i;
+      }
+    }
+  }
+}
+
+template <bool PARTIALS, bool VEC = false>
 __global__ __launch_bounds__(1024) void argmax_advance_kernel(
     const uint16_t* __restrict__ logits, const float* __restrict__ pv,
     const int32_t* __restrict__ pi, int64_t n, int64_t* __restrict__ token,
     int64_t* __restrict__ pos, int32_t* __restrict__ filled, const int64_t* __restrict__ prompt,
     int64_t prompt_len, int64_t* __restrict__ history, int64_t history_len) {
+  static_assert(!(PARTIALS && VEC), "the vector form reads fp16 logits");
   __shared__ float bvs[16];
   __shared__ int bis[16];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t p = pos[0];
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
   float v[kArgmaxPass];
   int ix[kArgmaxPass];
-  argmax_load_pass<PARTIALS>(logits, pv, pi, n, 0, tid, v, ix);
+  u32x4 w[kArgmaxPass];
+  const int64_t nv = n / 8;
+  if constexpr (VEC)
+    argmax_load_pass_vec(logits, nv, 0, tid, w);
+  else
+    argmax_load_pass<PARTIALS>(logits, pv, pi, n, 0, tid, v, ix);
   LEMOQ_LOADS_ISSUED();
   // The prompt token of position p + 1 (a valid address whether or not it is used).
   const bool feed = prompt && p + 1 >= 0 && p + 1 < prompt_len;
   const int64_t ptok = prompt ? prompt[feed ? p + 1 : 0] : 0;
-  float bv = -INFINITY;
-  int bi = 0x7fffffff;
-  argmax_fold_pass(v, ix, bv, bi);
-  for (int64_t base = (int64_t)kArgmaxPass * 1024; base < n; base += (int64_t)kArgmaxPass * 1024) {
-    argmax_load_pass<PARTIALS>(logits, pv, pi, n, base, tid, v, ix);
+  if constexpr (VEC) {
+    argmax_fold_pass_vec(w, nv, 0, tid, bv, bi);
+    for (int64_t vb = (int64_t)kArgmaxPass * 1024; vb < nv; vb += (int64_t)kArgmaxPass * 1024) {
+      argmax_load_pass_vec(logits, nv, vb, tid, w);
+      argmax_fold_pass_vec(w, nv, vb, tid, bv, bi);
+    }
+  } else {
     argmax_fold_pass(v, ix, bv, bi);
+    for (int64_t base = (int64_t)kArgmaxPass * 1024; base < n; base += (int64_t)kArgmaxPass * 1024) {
+      argmax_load_pass<PARTIALS>(logits, pv, pi, n, base, tid, v, ix);
+      argmax_fold_pass(v, ix, bv, bi);
+    }
   }
   // NaN is never held (every comparison with it is false), so the wave max is
   // a real value or -inf; lanes holding it offer their lowest row.
@@ -801,8 +846,13 @@ extern "C" int lemoq_argmax_advance(const uint16_t* logits, int64_t n, int64_t* 
                                     void* stream) {
   if (!logits || !token || !pos || !filled) return LEMOQ_ERR_NULL;
   if (n <= 0 || n > 0x7ffffffeLL) return LEMOQ_ERR_SHAPE;
-  hipLaunchKernelGGL((argmax_advance_kernel<false>), dim3(1), dim3(1024), 0, lemoq_stream(stream),
-                     logits, nullptr, nullptr, n, token, pos, filled, prompt, prompt_len, history,
-                     history_len);
+  if (n % 8 == 0 && lemoq_aligned16(logits))
+    hipLaunchKernelGGL((argmax_advance_kernel<false, true>), dim3(1), dim3(1024), 0, lemoq_stream(stream),
+                       logits, nullptr, nullptr, n, token, pos, filled, prompt, prompt_len, history,
+                       history_len);
+  else
+    hipLaunchKernelGGL((argmax_advance_kernel<false, false>), dim3(1), dim3(1024), 0, lemoq_stream(stream),
+                       logits, nullptr, nullptr, n, token, pos, filled, prompt, prompt_len, history,
+                       history_len);
   LEMOQ_CHECK_LAUNCH();
 }

@@ -102,9 +102,40 @@ struct GemvQArgs {
   int64_t y_ld;
   int y_f16;
   const uint16_t* residual;  // (M, N) fp16 with ld y_ld, or NULL: y = fp16(fp16(acc) + residual)
+  const uint16_t* norm_w;    // (K) fp16 RMSNorm weight of x, or NULL: x as it is
+  float eps;
 };
 
-template <int FMT, int KCH, int R, bool S32>
+// HF RMSNorm of the row the wave holds (lane slices of NV values per chunk,
+// zero past K), in place: x := fp16(fp16(x * rsqrt(mean(x^2) + eps)) * w) with
+// an fp32 mean over K values -- the rounding points of rms_norm_fused and of
+// the other norm prologues (x_rmsnorm).
+template <int KCH, int NV>
+__device__ __forceinline__ void xq_rmsnorm(uint32_t (&xw)[KCH][NV / 2], const uint32_t (&nw)[KCH][NV / 2], int K,
+                                           float eps) {
+  float ssq = 0.0f;
+#pragma unroll
+  for (int j = 0; j < KCH; ++j)
+#pragma unroll
+    for (int i = 0; i < NV / 2; ++i) {
+      const float a = h2f((uint16_t)(xw[j][i] & 0xFFFFu)), b = h2f((uint16_t)(xw[j][i] >> 16));
+      ssq = fmaf(a, a, ssq);
+      ssq = fmaf(b, b, ssq);
+    }
+  const float rstd = 1.0f / sqrtf(wave_sum(ssq) / (float)K + eps);
+#pragma unroll
+  for (int j = 0; j < KCH; ++j)
+#pragma unroll
+    for (int i = 0; i < NV / 2; ++i) {
+      const uint16_t a = f2h(h2f((uint16_t)(xw[j][i] & 0xFFFFu)) * rstd);
+      const uint16_t b = f2h(h2f((uint16_t)(xw[j][i] >> 16)) * rstd);
+      const uint16_t ya = f2h(h2f(a) * h2f((uint16_t)(nw[j][i] & 0xFFFFu)));
+      const uint16_t yb = f2h(h2f(b) * h2f((uint16_t)(nw[j][i] >> 16)));
+      xw[j][i] = (uint32_t)ya | ((uint32_t)yb << 16);
+    }
+}
+
+template <int FMT, int KCH, int R, bool S32, bool NORM = false>
 __global__ __launch_bounds__(256) void gemv_q_kernel(const GemvQArgs a) {
   constexpr int NV = qf_slice_codes(FMT);
   constexpr int CPC = 64 * NV;  // codes per 1 KB chunk
@@ -137,7 +168,15 @@ __global__ __launch_bounds__(256) void gemv_q_kernel(const GemvQArgs a) {
   uint32_t xw[KCH][NV / 2];
 #pragma unroll
   for (int j = 0; j < KCH; ++j) xq_load<NV>(xw[j], xr, a.K, j * CPC + lane * NV, vec);
+  constexpr int NWV = NORM ? KCH : 1;
+  uint32_t nw[NWV][NV / 2];
+  if constexpr (NORM) {  // the norm weight's slices, laid out as x's
+    const bool vw = ((reinterpret_cast<uintptr_t>(a.norm_w) & 15u) == 0) && ((a.K & 7) == 0);
+#pragma unroll
+    for (int j = 0; j < KCH; ++j) xq_load<NV>(nw[j], a.norm_w, a.K, j * CPC + lane * NV, vw);
+  }
   LEMOQ_LOADS_ISSUED();
+  if constexpr (NORM) xq_rmsnorm<KCH, NV>(xw, nw, a.K, a.eps);
 
   float acc[R];
 #pragma unroll
@@ -192,15 +231,15 @@ __global__ __launch_bounds__(256) void gemv_q_kernel(const GemvQArgs a) {
 #endif
 constexpr int kGemvQRows = LEMOQ_GEMVQ_ROWS;
 
-template <int FMT, bool S32>
+template <int FMT, bool S32, bool NORM>
 int launch_gemv_q(int kch, dim3 grid, hipStream_t st, const GemvQArgs& a) {
   switch (kch) {
-    case 1: hipLaunchKernelGGL((gemv_q_kernel<FMT, 1, kGemvQRows, S32>), grid, dim3(256), 0, st, a); break;
-    case 2: hipLaunchKernelGGL((gemv_q_kernel<FMT, 2, kGemvQRows, S32>), grid, dim3(256), 0, st, a); break;
-    case 4: hipLaunchKernelGGL((gemv_q_kernel<FMT, 4, kGemvQRows, S32>), grid, dim3(256), 0, st, a); break;
+    case 1: hipLaunchKernelGGL((gemv_q_kernel<FMT, 1, kGemvQRows, S32, NORM>), grid, dim3(256), 0, st, a); break;
+    case 2: hipLaunchKernelGGL((gemv_q_kernel<FMT, 2, kGemvQRows, S32, NORM>), grid, dim3(256), 0, st, a); break;
+    case 4: hipLaunchKernelGGL((gemv_q_kernel<FMT, 4, kGemvQRows, S32, NORM>), grid, dim3(256), 0, st, a); break;
     case 8:
       if constexpr (!qf_4bit(FMT)) {
-        hipLaunchKernelGGL((gemv_q_kernel<FMT, 8, kGemvQRows, S32>), grid, dim3(256), 0, st, a);
+        hipLaunchKernelGGL((gemv_q_kernel<FMT, 8, kGemvQRows, S32, NORM>), grid, dim3(256), 0, st, a);
         break;
       }
       return LEMOQ_ERR_UNSUPPORTED;
@@ -209,10 +248,13 @@ int launch_gemv_q(int kch, dim3 grid, hipStream_t st, const GemvQArgs& a) {
   LEMOQ_CHECK_LAUNCH();
 }
 
+// The RMSNorm prologue is instantiated for fp16 (or E8M0) scales only.
 template <int FMT>
 int launch_gemv_q_fmt(bool s32, int kch, dim3 grid, hipStream_t st, const GemvQArgs& a) {
-  if constexpr (FMT == LEMOQ_QFMT_MXFP4) return launch_gemv_q<FMT, false>(kch, grid, st, a);
-  else return s32 ? launch_gemv_q<FMT, true>(kch, grid, st, a) : launch_gemv_q<FMT, false>(kch, grid, st, a);
+  if (a.norm_w) return s32 ? LEMOQ_ERR_UNSUPPORTED : launch_gemv_q<FMT, false, true>(kch, grid, st, a);
+  if constexpr (FMT == LEMOQ_QFMT_MXFP4) return launch_gemv_q<FMT, false, false>(kch, grid, st, a);
+  else
+    return s32 ? launch_gemv_q<FMT, true, false>(kch, grid, st, a) : launch_gemv_q<FMT, false, false>(kch, grid, st, a);
 }
 
 // ---------------------------------------------------------------------------
@@ -673,7 +715,8 @@ namespace {
 
 int gemv_q_common(const uint16_t* x, int64_t M, int64_t K, const void* qweight, int fmt, const void* scale,
                   const void* zero, int scale_is_f32, int64_t N, int64_t padded_k, int64_t group, void* y,
-                  int y_is_f16, const uint16_t* residual, void* stream);
+                  int y_is_f16, const uint16_t* residual, void* stream, const uint16_t* norm_w = nullptr,
+                  float eps = 0.0f);
 
 }  // namespace
 
@@ -682,6 +725,17 @@ extern "C" int lemoq_gemv_q(const uint16_t* x, int64_t M, int64_t K, const void*
                             int64_t padded_k, int64_t group, void* y, int y_is_f16, void* stream) {
   return gemv_q_common(x, M, K, qweight, fmt, scale, zero, scale_is_f32, N, padded_k, group, y, y_is_f16,
                        nullptr, stream);
+}
+
+extern "C" int lemoq_gemv_q_rmsnorm(const uint16_t* x, int64_t M, int64_t K, const uint16_t* norm_w, float eps,
+                                    const void* qweight, int fmt, const void* scale, const void* zero,
+                                    int scale_is_f32, int64_t N, int64_t padded_k, int64_t group, void* y,
+                                    int y_is_f16, void* stream) {
+  if (!norm_w) return LEMOQ_ERR_NULL;
+  if (!(eps >= 0.0f)) return LEMOQ_ERR_SHAPE;  // negative or NaN eps
+  if (scale_is_f32) return LEMOQ_ERR_UNSUPPORTED;  // the norm prologue takes fp16 (or E8M0) scales
+  return gemv_q_common(x, M, K, qweight, fmt, scale, zero, scale_is_f32, N, padded_k, group, y, y_is_f16,
+                       nullptr, stream, norm_w, eps);
 }
 
 extern "C" int lemoq_gemv_q_residual(const uint16_t* x, int64_t M, int64_t K, const void* qweight, int fmt,
@@ -704,7 +758,7 @@ namespace {
 
 int gemv_q_common(const uint16_t* x, int64_t M, int64_t K, const void* qweight, int fmt, const void* scale,
                   const void* zero, int scale_is_f32, int64_t N, int64_t padded_k, int64_t group, void* y,
-                  int y_is_f16, const uint16_t* residual, void* stream) {
+                  int y_is_f16, const uint16_t* residual, void* stream, const uint16_t* norm_w, float eps) {
   if (!x || !y) return LEMOQ_ERR_NULL;
   const int rc = check_format(fmt, qweight, scale, zero, scale_is_f32, N, padded_k, group);
   if (rc) return rc;
@@ -725,6 +779,8 @@ int gemv_q_common(const uint16_t* x, int64_t M, int64_t K, const void* qweight, 
   a.y_ld = N;
   a.y_f16 = y_is_f16 ? 1 : 0;
   a.residual = residual;
+  a.norm_w = norm_w;
+  a.eps = eps;
   const int64_t chunks = (a.row_bytes + 1023) / 1024;
   const int kch = chunks <= 1 ? 1 : (chunks <= 2 ? 2 : (chunks <= 4 ? 4 : 8));
   const int64_t blocks = (N + 4 * kGemvQRows - 1) / (4 * kGemvQRows);

@@ -21,9 +21,9 @@
 // then final RMSNorm + lm_head GEMV with per-block argmax partials, and the
 // greedy selection that writes the next token and advances *pos / *filled.
 //
-// 4-bit weights (weight_bits 4, the reference's w4a16 cell) run 8 launches per
-// layer from the operators of the 4-bit formats: input RMSNorm, the 4-bit
-// q|k|v GEMV, the same fused attention, the LSE merge, the 4-bit o_proj GEMV
+// 4-bit weights (weight_bits 4, the reference's w4a16 cell) run 7 launches per
+// layer from the operators of the 4-bit formats: the 4-bit q|k|v GEMV with the
+// input RMSNorm in its prologue, the same fused attention, the LSE merge, the 4-bit o_proj GEMV
 // with the residual add, router logits (post-attention norm + router), the
 // routed 4-bit gate/up and the 4-bit down with the residual add; layer 0
 // first gathers the embedding row.  An fp16 lm_head (lm_f16, the reference's
@@ -183,13 +183,13 @@ int enqueue_head(const LemoqOlmoeStep* p, void* stream) {
                                  p->filled, p->prompt, p->prompt_len, p->history, p->history_len, stream);
 }
 
-// One layer on 4-bit weights (8 launches, 9 on layer 0).
+// One layer on 4-bit weights (7 launches, 8 on layer 0).
 int enqueue_layer_w4(const LemoqOlmoeStep* p, const LemoqOlmoeLayer& w, bool first, void* stream) {
   const int64_t H = p->hidden, HD = p->heads * p->head_dim, g = p->group;
   if (first) LEMOQ_TRY(lemoq_gather_rows(p->embed, p->vocab, H, p->token, 1, p->h, stream));
-  LEMOQ_TRY(lemoq_rmsnorm(p->h, 1, H, w.ln_in, p->eps, p->xn, stream));
-  LEMOQ_TRY(lemoq_gemv_q(p->xn, 1, H, w.qkv_codes, LEMOQ_QFMT_W4, w.qkv_scale, nullptr, 0, 3 * HD, H, g,
-                         p->qkv, 1, stream));
+  // input RMSNorm (in every wave) + packed q|k|v
+  LEMOQ_TRY(lemoq_gemv_q_rmsnorm(p->h, 1, H, w.ln_in, p->eps, w.qkv_codes, LEMOQ_QFMT_W4, w.qkv_scale, nullptr, 0,
+                                 3 * HD, H, g, p->qkv, 1, stream));
   LEMOQ_TRY(enqueue_attention(p, w, stream));
   LEMOQ_TRY(lemoq_attn_merge(p->part_m, p->part_l, p->part_acc, p->heads, p->num_splits, p->head_dim,
                              p->attn, stream));

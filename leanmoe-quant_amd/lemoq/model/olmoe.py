@@ -469,10 +469,10 @@ class DecodeSession:
     @property
     def launches_per_step(self) -> int:
         """Kernel launches in one captured step (see csrc/step.hip): 6 or 7 per
-        8-bit layer, 8 per 4-bit layer plus layer 0's embedding gather, and the
+        8-bit layer, 7 per 4-bit layer plus layer 0's embedding gather, and the
         lm_head and greedy selection."""
         if self.weights.bits == 4:
-            return 8 * self.shape.layers + 1 + 2
+            return 7 * self.shape.layers + 1 + 2
         per_layer = 6 if self.attn_output_fused else 7
         return per_layer * self.shape.layers + 2
 

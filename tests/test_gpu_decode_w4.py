@@ -105,7 +105,7 @@ def test_tiny_model_matches_oracle(bits, lm_head, kv, dev):
     ctx = 40
     prompt = torch.randint(0, TINY.vocab, (ctx,), generator=torch.Generator().manual_seed(32)).tolist()
     sess = DecodeSession(w, prompt, max_new_tokens=STEPS, kv_cache=kv)
-    assert sess.launches_per_step == (8 * TINY.layers + 3 if bits == 4 else 7 * TINY.layers + 2)
+    assert sess.launches_per_step == (7 * TINY.layers + 3 if bits == 4 else 7 * TINY.layers + 2)
     with pytest.raises(NotImplementedError):
         sess.prefill()  # the batched prefill runs W8 weights and the W8 lm_head
     seed = sess.prefill(mode="stepped")
@@ -146,7 +146,7 @@ def test_olmoe_shape_w4a16_random_prompt(dev):
     ctx = 192
     prompt = torch.randint(0, OLMOE_1B_7B.vocab, (ctx,), generator=torch.Generator().manual_seed(42)).tolist()
     sess = DecodeSession(w, prompt, max_new_tokens=24)
-    assert sess.launches_per_step == 8 * 16 + 3
+    assert sess.launches_per_step == 7 * 16 + 3
     sess.prefill(mode="stepped")
     pos0, tok0 = sess.position, sess.next_token_cpu()
     kv0 = sess.kv_cpu()
