@@ -1385,12 +1385,12 @@ STEP_TAIL_KERNELS = [("lm_head (+ final norm, argmax partials)", "gemv_w8_kernel
                      ("argmax + advance", "argmax_advance_kernel<true>")]
 
 
-# The 4-bit step (--weights w4a16) by position: layer 0's embedding gather, then per
-# layer the 7 launches below, then the fp16 lm_head and the greedy pick.  The router
-# and the fp16 lm_head are one kernel instance, so the launches are told apart by
-# their place in the step.
-STEP_W4_LAYER = ["qkv GEMV (4-bit, + input RMSNorm)", "attention split (+ q/k norm, RoPE, cache write)",
-                 "LSE merge", "o_proj GEMV (4-bit, + residual)", "router (+ post-attention norm)",
+# The 4-bit step (--weights w4a16) at the OLMoE shape by position: layer 0's embedding
+# gather, then per layer the 6 launches below, then the fp16 lm_head and the greedy
+# pick (told apart by their place in the step, as the lm_head runs the router's
+# kernel).
+STEP_W4_LAYER = ["qkv (4-bit, + input RMSNorm)", "attention split (+ q/k norm, RoPE, cache write)",
+                 "merge + o_proj (4-bit)", "residual + norm + router",
                  "gate/up (4-bit, + routing)", "down (4-bit, + residual)"]
 STEP_W4_HEAD = ["lm_head fp16 (+ final norm)", "argmax + advance"]
 STEP_W4_END = "argmax_advance_kernel<false>"

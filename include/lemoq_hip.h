@@ -360,6 +360,14 @@ int lemoq_attn_merge_o_proj_w8(const float* m, const float* l, const float* acc,
                                int64_t heads, int64_t num_splits, int64_t head_dim,
                                const int8_t* codes, const uint16_t* scale, int64_t N,
                                int64_t group, float* part, void* stream);
+/* The same on 4-bit symmetric codes (the w4a16 cell's o_proj, the 4-bit
+ * branch of dequant_gemm_fused, src/lemoq/kernels/_dequant_triton.py:155-293):
+ * codes (N, heads*128/2) packed two per byte, the even column in the low
+ * nibble; group % 32 == 0.  Used by the 4-bit decode step. */
+int lemoq_attn_merge_o_proj_w4(const float* m, const float* l, const float* acc,
+                               int64_t heads, int64_t num_splits, int64_t head_dim,
+                               const uint8_t* codes, const uint16_t* scale, int64_t N,
+                               int64_t group, float* part, void* stream);
 
 /* ---------------------------------------------------------------------------
  * A10 — RMSNorm, HF rounding points: y = fp16(fp16(x*rsqrt(mean(x^2)+eps)) * w).
@@ -634,12 +642,14 @@ typedef struct LemoqOlmoeStep {
    * above) or 4 (the reference's w4a16 cell: 4-bit symmetric codes packed two
    * per byte, the even column in the low nibble, so qkv_codes (3*heads*D,
    * H/2), o_codes (H, heads*D/2), gu_codes (E, 2F, H/2), dn_codes (E, H, F/2);
-   * scales as above; group % 32 == 0).  A 4-bit step runs 7 launches per
-   * layer: lemoq_gemv_q_rmsnorm (input norm + q|k|v), the fused attention,
-   * lemoq_attn_merge, lemoq_gemv_q_residual (o_proj + residual into h),
-   * lemoq_router_logits, lemoq_moe_gate_up_w4_routed, lemoq_moe_down_w4
-   * (+ residual into h); layer 0 first gathers the embedding row into h
-   * (lemoq_gather_rows). */
+   * scales as above; group % 32 == 0).  A 4-bit step runs 6 launches per
+   * layer on the fused attention-output path (the shape rule below):
+   * lemoq_gemv_q_rmsnorm (input norm + q|k|v), the fused attention,
+   * lemoq_attn_merge_o_proj_w4, lemoq_router_logits_resid,
+   * lemoq_moe_gate_up_w4_routed, lemoq_moe_down_w4 (+ residual); otherwise 7,
+   * with lemoq_attn_merge, lemoq_gemv_q_residual (o_proj + residual into h)
+   * and lemoq_router_logits in place of the middle two.  Layer 0 first gathers
+   * the embedding row into h (lemoq_gather_rows). */
   int64_t weight_bits;
   /* fp16 lm_head (vocab, H), or NULL for the W8 lm_head of lm_codes /
    * lm_scale.  With it the step ends with lemoq_router_logits (final norm +

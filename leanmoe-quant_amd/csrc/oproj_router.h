@@ -10,7 +10,8 @@
 //                                the fp16 attention output is bit-identical),
 //                                then dots its 32 output rows with them and
 //                                writes fp32 partial sums, one row of partials
-//                                per head group.
+//                                per head group.  lemoq_attn_merge_o_proj_w4 is
+//                                the same on 4-bit codes (the w4a16 cell).
 //   lemoq_router_logits_resid    o = fp16(sum of the partials in group order),
 //                                h' = fp16(o + h) (the residual add after
 //                                o_proj), xn = RMSNorm(h') (post-attention
@@ -27,6 +28,7 @@
 #pragma once
 
 #include "attn_common.h"
+#include "qformat.h"
 
 namespace lemoq_oproj {
 
@@ -41,7 +43,7 @@ struct MergeOprojArgs {
   const float* l;    // (heads, NS) running sum per split
   const float* acc;  // (heads, NS, 128) unnormalised outputs per split
   int NS;
-  const int8_t* codes;    // (N, HD)
+  const int8_t* codes;    // (N, HD) int8, or (N, HD / 2) packed 4-bit codes
   const uint16_t* scale;  // (N, HD / group)
   int64_t N;
   int HD;
@@ -84,14 +86,38 @@ __device__ __forceinline__ void oproj_issue(const MergeOprojArgs& a, int g, int 
   }
 }
 
-// Merge the tile's 4 heads into LDS (xs: 512 fp16) and write its partial
-// sums.
-template <int NSMAX>
-__device__ __forceinline__ void oproj_finish(const MergeOprojArgs& a, const OprojTile& t, uint16_t* xs) {
+// 4-bit codes (two per byte): a row slice of 512 features is 256 bytes, so one
+// wave load covers 4 rows: lane l reads the 32 codes at feature 512 g +
+// 32 (l % 16) of row 4i + l / 16 for i = 0, 1.
+struct OprojTileQ4 {
+  u32x4 c[2];
+  uint16_t s[2];
+  int64_t row0;
+  int g;
+};
+
+__device__ __forceinline__ void oproj_issue_q4(const MergeOprojArgs& a, int g, int rb, OprojTileQ4& t) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int l32 = lane & 31;
+  const int q = lane >> 4, l16 = lane & 15;
+  t.g = g;
+  t.row0 = (int64_t)rb * MO_ROWS + wave * MO_ROWS_WAVE;
+  const int k0 = g * MO_COLS + 32 * l16;
+  const int row_bytes = a.HD / 2, ngroups = a.HD / a.group;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int64_t row = t.row0 + 4 * i + q;
+    t.c[i] = load_stream16(a.codes + row * row_bytes + k0 / 2);
+    t.s[i] = a.scale[row * ngroups + k0 / a.group];
+  }
+}
+
+// The LSE merge of the block's 4 heads into LDS (xs: 512 fp16), one wave per
+// head (lane holds dims lane and lane + 64).
+template <int NSMAX>
+__device__ __forceinline__ void oproj_merge(const MergeOprojArgs& a, int g, uint16_t* xs) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int NS = a.NS;
-  const int64_t hh = (int64_t)t.g * MO_HEADS + wave;
+  const int64_t hh = (int64_t)g * MO_HEADS + wave;
   const int jl = lane < NS ? lane : NS - 1;
   const float mraw = a.m[hh * NS + jl];
   const float lraw = a.l[hh * NS + jl];
@@ -110,6 +136,40 @@ __device__ __forceinline__ void oproj_finish(const MergeOprojArgs& a, const Opro
   xs[wave * MO_D + lane] = lemoq_attn::lse_out<NSMAX>(a0, wj, den);
   xs[wave * MO_D + 64 + lane] = lemoq_attn::lse_out<NSMAX>(a1, wj, den);
   __syncthreads();
+}
+
+// Merge, then the 4-bit tile's partial sums (rows 4i + r in lanes 16r .. 16r + 15).
+template <int NSMAX>
+__device__ __forceinline__ void oproj_finish_q4(const MergeOprojArgs& a, const OprojTileQ4& t, uint16_t* xs) {
+  oproj_merge<NSMAX>(a, t.g, xs);
+  const int lane = threadIdx.x & 63, l16 = lane & 15;
+  XChunk x0, x1;
+  load_xchunk(xs + 32 * l16, x0);
+  load_xchunk(xs + 32 * l16 + 16, x1);
+  float tot[2][4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    float v = h2f(t.s[i]) * lemoq_qf::dot32_i4<true>(t.c[i], x0, x1, 0.0f);
+    v = lemoq_attn::group_sum_lanes<16>(v, lane);  // every lane holds its 16-lane row's total
+#pragma unroll
+    for (int r = 0; r < 4; ++r) tot[i][r] = lane_f(v, 16 * r);
+  }
+  float out = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (lane == 4 * i + r) out = tot[i][r];
+  if (lane < MO_ROWS_WAVE) a.part[(int64_t)t.g * a.N + t.row0 + lane] = out;
+}
+
+// Merge the tile's 4 heads into LDS (xs: 512 fp16) and write its partial
+// sums.
+template <int NSMAX>
+__device__ __forceinline__ void oproj_finish(const MergeOprojArgs& a, const OprojTile& t, uint16_t* xs) {
+  oproj_merge<NSMAX>(a, t.g, xs);
+  const int lane = threadIdx.x & 63;
+  const int l32 = lane & 31;
 
   XChunk xc;
   load_xchunk(xs + 16 * l32, xc);

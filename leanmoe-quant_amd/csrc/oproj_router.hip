@@ -18,6 +18,17 @@ __global__ __launch_bounds__(256) void merge_oproj_kernel(const MergeOprojArgs a
   oproj_finish<NSMAX>(a, t, xs);
 }
 
+template <int NSMAX>
+__global__ __launch_bounds__(256) void merge_oproj_q4_kernel(const MergeOprojArgs a) {
+  __shared__ __align__(16) uint16_t xs[MO_COLS];
+  int g, rb;
+  oproj_tile_of_block(g, rb);
+  OprojTileQ4 t;
+  oproj_issue_q4(a, g, rb, t);
+  LEMOQ_LOADS_ISSUED();  // the weight stream first, then the merge inputs
+  oproj_finish_q4<NSMAX>(a, t, xs);
+}
+
 template <int KCH, int NP>
 __global__ __launch_bounds__(256) void router_resid_kernel(const RouterResidArgs a) {
   __shared__ __align__(16) uint16_t xs[KCH * 1024];
@@ -35,17 +46,19 @@ bool overlaps(const void* a, int64_t na, const void* b, int64_t nb) {
 
 }  // namespace
 
-extern "C" int lemoq_attn_merge_o_proj_w8(const float* m, const float* l, const float* acc,
-                                          int64_t heads, int64_t num_splits, int64_t head_dim,
-                                          const int8_t* codes, const uint16_t* scale, int64_t N,
-                                          int64_t group, float* part, void* stream) {
+namespace {
+
+int merge_oproj(const float* m, const float* l, const float* acc, int64_t heads, int64_t num_splits,
+                int64_t head_dim, const int8_t* codes, const uint16_t* scale, int64_t N, int64_t group, float* part,
+                void* stream, int bits) {
   if (!m || !l || !acc || !codes || !scale || !part) return LEMOQ_ERR_NULL;
   if (heads <= 0 || num_splits <= 0 || N <= 0 || group <= 0) return LEMOQ_ERR_SHAPE;
   if (head_dim != MO_D || heads % MO_HEADS != 0) return LEMOQ_ERR_UNSUPPORTED;
   if (num_splits > 64 || N % MO_ROWS != 0 || N / MO_ROWS > 0x7fffffff || heads / MO_HEADS > 65535)
     return LEMOQ_ERR_SHAPE;
   const int64_t HD = heads * head_dim;
-  if (group % 16 != 0 || HD % group != 0 || HD > 0x7fffffff) return LEMOQ_ERR_SHAPE;
+  // a lane's slice (16 codes at 8 bits, 32 at 4) lies inside one scale group
+  if (group % (bits == 4 ? 32 : 16) != 0 || HD % group != 0 || HD > 0x7fffffff) return LEMOQ_ERR_SHAPE;
   if (!lemoq_aligned16(codes)) return LEMOQ_ERR_ALIGN;
   MergeOprojArgs a;
   a.m = m;
@@ -60,11 +73,35 @@ extern "C" int lemoq_attn_merge_o_proj_w8(const float* m, const float* l, const 
   a.part = part;
   const dim3 grid((unsigned)(N / MO_ROWS), (unsigned)(heads / MO_HEADS));
   hipStream_t st = lemoq_stream(stream);
-  if (num_splits <= 16)
-    hipLaunchKernelGGL((merge_oproj_kernel<16>), grid, dim3(256), 0, st, a);
-  else
-    hipLaunchKernelGGL((merge_oproj_kernel<64>), grid, dim3(256), 0, st, a);
+  if (bits == 4) {
+    if (num_splits <= 16)
+      hipLaunchKernelGGL((merge_oproj_q4_kernel<16>), grid, dim3(256), 0, st, a);
+    else
+      hipLaunchKernelGGL((merge_oproj_q4_kernel<64>), grid, dim3(256), 0, st, a);
+  } else {
+    if (num_splits <= 16)
+      hipLaunchKernelGGL((merge_oproj_kernel<16>), grid, dim3(256), 0, st, a);
+    else
+      hipLaunchKernelGGL((merge_oproj_kernel<64>), grid, dim3(256), 0, st, a);
+  }
   LEMOQ_CHECK_LAUNCH();
+}
+
+}  // namespace
+
+extern "C" int lemoq_attn_merge_o_proj_w8(const float* m, const float* l, const float* acc,
+                                          int64_t heads, int64_t num_splits, int64_t head_dim,
+                                          const int8_t* codes, const uint16_t* scale, int64_t N,
+                                          int64_t group, float* part, void* stream) {
+  return merge_oproj(m, l, acc, heads, num_splits, head_dim, codes, scale, N, group, part, stream, 8);
+}
+
+extern "C" int lemoq_attn_merge_o_proj_w4(const float* m, const float* l, const float* acc,
+                                          int64_t heads, int64_t num_splits, int64_t head_dim,
+                                          const uint8_t* codes, const uint16_t* scale, int64_t N,
+                                          int64_t group, float* part, void* stream) {
+  return merge_oproj(m, l, acc, heads, num_splits, head_dim, reinterpret_cast<const int8_t*>(codes), scale, N,
+                     group, part, stream, 4);
 }
 
 extern "C" int lemoq_router_logits_resid(const float* part, int64_t n_part, const uint16_t* h,

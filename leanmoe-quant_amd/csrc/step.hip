@@ -21,12 +21,12 @@
 // then final RMSNorm + lm_head GEMV with per-block argmax partials, and the
 // greedy selection that writes the next token and advances *pos / *filled.
 //
-// 4-bit weights (weight_bits 4, the reference's w4a16 cell) run 7 launches per
-// layer from the operators of the 4-bit formats: the 4-bit q|k|v GEMV with the
-// input RMSNorm in its prologue, the same fused attention, the LSE merge, the 4-bit o_proj GEMV
-// with the residual add, router logits (post-attention norm + router), the
-// routed 4-bit gate/up and the 4-bit down with the residual add; layer 0
-// first gathers the embedding row.  An fp16 lm_head (lm_f16, the reference's
+// 4-bit weights (weight_bits 4, the reference's w4a16 cell) run the same
+// layer on 4-bit kernels: the q|k|v GEMV with the input RMSNorm in its
+// prologue, the same fused attention, merge + 4-bit o_proj (or, off the fused
+// shape rule, the merge, the 4-bit o_proj GEMV with the residual add and the
+// router logits), the routed 4-bit gate/up and the 4-bit down with the
+// residual add; layer 0 first gathers the embedding row.  An fp16 lm_head (lm_f16, the reference's
 // lm_head in every cell but w8a16 with its lm_head switch on) ends the step
 // with the final norm + fp16 GEMV and the greedy selection over the logits.
 //
@@ -65,7 +65,7 @@ int check_gemv(int64_t N, int64_t K, int64_t group) {
   return LEMOQ_OK;
 }
 
-enum AttnPath { kAttnFusedOut, kAttnThree, kAttnW4 };
+enum AttnPath { kAttnFusedOut, kAttnThree };
 
 // Every rule of every launch of the step, before anything is enqueued.
 int validate(const LemoqOlmoeStep* p, AttnPath* path) {
@@ -125,11 +125,8 @@ int validate(const LemoqOlmoeStep* p, AttnPath* path) {
         !a16(w.vc) || !a16(w.router) || !a16(w.ln_post))
       return LEMOQ_ERR_ALIGN;
   }
-  if (w4) {
-    *path = kAttnW4;
-    return LEMOQ_OK;
-  }
-  // the attention-output half: one fused launch, two launches, or three
+  // the attention-output half: two launches (merge + o_proj, residual + norm +
+  // router) or three (merge, o_proj with the residual, norm + router)
   const int64_t n_part = HD / 512;
   const bool fused_o = p->o_part && p->h_mid && D == 128 && p->heads % 4 == 0 && ns <= 64 &&
                        (H == 2048 || H == 4096) &&
@@ -141,7 +138,7 @@ int validate(const LemoqOlmoeStep* p, AttnPath* path) {
       return LEMOQ_ERR_SHAPE;
     *path = kAttnFusedOut;
   } else {
-    LEMOQ_TRY(check_gemv(H, HD, g));
+    LEMOQ_TRY(check_gemv(H, HD, g));  // the o_proj GEMV (w8, or the 4-bit rules checked above)
     if (ns > 1024 || D > 256) return LEMOQ_ERR_SHAPE;
     if (H > 8192 || H % 16 != 0) return LEMOQ_ERR_UNSUPPORTED;
     if (E > 65536) return LEMOQ_ERR_SHAPE;
@@ -183,26 +180,38 @@ int enqueue_head(const LemoqOlmoeStep* p, void* stream) {
                                  p->filled, p->prompt, p->prompt_len, p->history, p->history_len, stream);
 }
 
-// One layer on 4-bit weights (7 launches, 8 on layer 0).
-int enqueue_layer_w4(const LemoqOlmoeStep* p, const LemoqOlmoeLayer& w, bool first, void* stream) {
+// One layer on 4-bit weights: 6 launches on the fused attention-output path,
+// 7 otherwise (one more on layer 0, the embedding gather).
+int enqueue_layer_w4(const LemoqOlmoeStep* p, const LemoqOlmoeLayer& w, bool first, AttnPath path, void* stream) {
   const int64_t H = p->hidden, HD = p->heads * p->head_dim, g = p->group;
   if (first) LEMOQ_TRY(lemoq_gather_rows(p->embed, p->vocab, H, p->token, 1, p->h, stream));
   // input RMSNorm (in every wave) + packed q|k|v
   LEMOQ_TRY(lemoq_gemv_q_rmsnorm(p->h, 1, H, w.ln_in, p->eps, w.qkv_codes, LEMOQ_QFMT_W4, w.qkv_scale, nullptr, 0,
                                  3 * HD, H, g, p->qkv, 1, stream));
   LEMOQ_TRY(enqueue_attention(p, w, stream));
-  LEMOQ_TRY(lemoq_attn_merge(p->part_m, p->part_l, p->part_acc, p->heads, p->num_splits, p->head_dim,
-                             p->attn, stream));
-  // o_proj; h = fp16(fp16(o) + h)
-  LEMOQ_TRY(lemoq_gemv_q_residual(p->attn, 1, HD, w.o_codes, LEMOQ_QFMT_W4, w.o_scale, nullptr, 0, H, HD, g,
-                                  p->h, p->h, stream));
-  LEMOQ_TRY(lemoq_router_logits(p->h, w.ln_post, p->eps, H, w.router, p->num_experts, p->xn,
-                                p->router_logits, stream));
+  if (path == kAttnFusedOut) {
+    // LSE merge + 4-bit o_proj partials per group of 4 heads; h_mid = fp16(fp16(o) + h),
+    // post-attention RMSNorm + router logits
+    LEMOQ_TRY(lemoq_attn_merge_o_proj_w4(p->part_m, p->part_l, p->part_acc, p->heads, p->num_splits,
+                                         p->head_dim, reinterpret_cast<const uint8_t*>(w.o_codes), w.o_scale, H,
+                                         g, p->o_part, stream));
+    LEMOQ_TRY(lemoq_router_logits_resid(p->o_part, HD / 512, p->h, w.ln_post, p->eps, H, w.router,
+                                        p->num_experts, p->h_mid, p->xn, p->router_logits, stream));
+  } else {
+    LEMOQ_TRY(lemoq_attn_merge(p->part_m, p->part_l, p->part_acc, p->heads, p->num_splits, p->head_dim,
+                               p->attn, stream));
+    // o_proj; h = fp16(fp16(o) + h)
+    LEMOQ_TRY(lemoq_gemv_q_residual(p->attn, 1, HD, w.o_codes, LEMOQ_QFMT_W4, w.o_scale, nullptr, 0, H, HD, g,
+                                    p->h, p->h, stream));
+    LEMOQ_TRY(lemoq_router_logits(p->h, w.ln_post, p->eps, H, w.router, p->num_experts, p->xn,
+                                  p->router_logits, stream));
+  }
+  const uint16_t* resid = path == kAttnFusedOut ? p->h_mid : p->h;
   LEMOQ_TRY(lemoq_moe_gate_up_w4_routed(p->xn, reinterpret_cast<const uint8_t*>(w.gu_codes), w.gu_scale,
                                         p->router_logits, p->top_k, (int)p->norm_topk_prob, p->num_experts,
                                         p->ffn, H, g, p->act, p->top_i, p->top_w, stream));
   return lemoq_moe_down_w4(p->act, reinterpret_cast<const uint8_t*>(w.dn_codes), w.dn_scale, p->top_i, p->top_w,
-                           p->top_k, p->num_experts, H, p->ffn, g, p->h, p->h, stream);
+                           p->top_k, p->num_experts, H, p->ffn, g, resid, p->h, stream);
 }
 
 }  // namespace
@@ -210,8 +219,9 @@ int enqueue_layer_w4(const LemoqOlmoeStep* p, const LemoqOlmoeLayer& w, bool fir
 extern "C" int lemoq_olmoe_decode_step(const LemoqOlmoeStep* p, void* stream) {
   AttnPath path = kAttnThree;
   LEMOQ_TRY(validate(p, &path));
-  if (path == kAttnW4) {
-    for (int64_t L = 0; L < p->num_layers; ++L) LEMOQ_TRY(enqueue_layer_w4(p, p->layers[L], L == 0, stream));
+  if (p->weight_bits == 4) {
+    for (int64_t L = 0; L < p->num_layers; ++L)
+      LEMOQ_TRY(enqueue_layer_w4(p, p->layers[L], L == 0, path, stream));
     return enqueue_head(p, stream);
   }
   const int64_t H = p->hidden, HD = p->heads * p->head_dim, D = p->head_dim;

@@ -458,23 +458,21 @@ class DecodeSession:
     @property
     def attn_output_fused(self) -> bool:
         """Whether the step runs merge + o_proj as one launch and the residual add
-        in the router launch (the shape rule of csrc/step.hip; 8-bit weights only)."""
+        in the router launch (the shape rule of csrc/step.hip)."""
         s = self.shape
         HD = s.heads * s.head_dim
-        return (self.weights.bits == 8 and bool(self._step.o_part) and bool(self._step.h_mid)
+        return (bool(self._step.o_part) and bool(self._step.h_mid)
                 and s.head_dim == 128 and s.heads % 4 == 0
                 and self.num_splits <= 64 and s.hidden in (2048, 4096) and HD // 512 in (1, 2, 4, 8)
                 and s.group_size % 16 == 0 and HD % s.group_size == 0)
 
     @property
     def launches_per_step(self) -> int:
-        """Kernel launches in one captured step (see csrc/step.hip): 6 or 7 per
-        8-bit layer, 7 per 4-bit layer plus layer 0's embedding gather, and the
-        lm_head and greedy selection."""
-        if self.weights.bits == 4:
-            return 7 * self.shape.layers + 1 + 2
+        """Kernel launches in one captured step (see csrc/step.hip): 6 per layer
+        on the fused attention-output path, 7 otherwise, one more for a 4-bit
+        step's embedding gather, and the lm_head and greedy selection."""
         per_layer = 6 if self.attn_output_fused else 7
-        return per_layer * self.shape.layers + 2
+        return per_layer * self.shape.layers + 2 + (1 if self.weights.bits == 4 else 0)
 
     def capture(self, steps_per_graph: int = 1) -> dict[str, Any]:
         """Capture one decode step into a hipGraph (state is untouched by the capture).

@@ -125,20 +125,19 @@ def test_summarize_step_timeline(tmp_path):
 
 
 def test_summarize_step_timeline_of_the_4bit_step(tmp_path):
-    """The 4-bit step (bench.py --mode step --weights w4a16): 115 launches told
-    apart by position (the router and the fp16 lm_head share one kernel
-    instance); the prompt's steps come first and --summarize-last keeps the
-    decode steps.  Synthetic trace: 3 prompt steps (1 us kernels) and 2 decode
+    """The 4-bit step (bench.py --mode step --weights w4a16): 99 launches told
+    apart by position (the lm_head runs the router's kernel); the prompt's steps
+    come first and --summarize-last keeps the decode steps.  Synthetic trace: 3 prompt steps (1 us kernels) and 2 decode
     steps (role i lasts i + 1 us), 1 us gaps."""
     path = tmp_path / "trace_w4.csv"
     layer = ["gemv_q_kernel<2, 1, 2, false, true>", "attn_split_fused_i8_kernel<128, 4, 3>",
-             "attn_merge_wave_kernel<16>", "gemv_q_kernel<2, 1, 2, false, false>", "router_logits_kernel<2, true>",
+             "merge_oproj_q4_kernel<16>", "router_resid_kernel<2, 4>",
              "moe_gate_up_q4_kernel<1, 2, 16, 1>", "moe_down_q4_kernel<1, 4, 8>"]
     step = ["gather_rows_kernel"] + layer * 16 + ["router_logits_kernel<2, true>", "argmax_advance_kernel<false>"]
     rows, t = [("void at::native::fill_kernel(args)", 0, 500)], 1000
     for s in range(5):
         for i, n in enumerate(step):
-            d = 1000 if s < 3 else 1000 * (1 + (0 if i == 0 else 1 + (i - 1) % 7 if i <= 112 else 8 + (i - 113)))
+            d = 1000 if s < 3 else 1000 * (1 + (0 if i == 0 else 1 + (i - 1) % 6 if i <= 96 else 7 + (i - 97)))
             rows.append(("void (anonymous namespace)::%s(args)" % n, t, t + d))
             t += d + 1000
     with open(path, "w", newline="") as f:
@@ -147,10 +146,10 @@ def test_summarize_step_timeline_of_the_4bit_step(tmp_path):
         for n, a, b in rows:
             w.writerow({"Kernel_Name": n, "Start_Timestamp": a, "End_Timestamp": b})
     out = bench.summarize_step(str(path), last=2)
-    assert out.startswith("2 whole steps of 115 launches"), out
+    assert out.startswith("2 whole steps of 99 launches"), out
     assert "| embedding gather | 1 | 1.00 |" in out
-    assert "| qkv GEMV (4-bit, + input RMSNorm) | 16 | 2.00 |" in out
-    assert "| o_proj GEMV (4-bit, + residual) | 16 | 5.00 |" in out
-    assert "| router (+ post-attention norm) | 16 | 6.00 |" in out
-    assert "| lm_head fp16 (+ final norm) | 1 | 9.00 |" in out and "| argmax + advance | 1 | 10.00 |" in out
-    assert bench.summarize_step(str(path)).startswith("5 whole steps of 115 launches")
+    assert "| qkv (4-bit, + input RMSNorm) | 16 | 2.00 |" in out
+    assert "| merge + o_proj (4-bit) | 16 | 4.00 |" in out
+    assert "| residual + norm + router | 16 | 5.00 |" in out
+    assert "| lm_head fp16 (+ final norm) | 1 | 8.00 |" in out and "| argmax + advance | 1 | 9.00 |" in out
+    assert bench.summarize_step(str(path)).startswith("5 whole steps of 99 launches")

@@ -105,7 +105,8 @@ def test_tiny_model_matches_oracle(bits, lm_head, kv, dev):
     ctx = 40
     prompt = torch.randint(0, TINY.vocab, (ctx,), generator=torch.Generator().manual_seed(32)).tolist()
     sess = DecodeSession(w, prompt, max_new_tokens=STEPS, kv_cache=kv)
-    assert sess.launches_per_step == (7 * TINY.layers + 3 if bits == 4 else 7 * TINY.layers + 2)
+    assert not sess.attn_output_fused  # hidden 512: merge, o_proj (+ residual), router as three launches
+    assert sess.launches_per_step == 7 * TINY.layers + 2 + (bits == 4)
     with pytest.raises(NotImplementedError):
         sess.prefill()  # the batched prefill runs W8 weights and the W8 lm_head
     seed = sess.prefill(mode="stepped")
@@ -116,6 +117,30 @@ def test_tiny_model_matches_oracle(bits, lm_head, kv, dev):
         gl.append(sess.logits_cpu())
     toks = [int(t) for t in sess.history[ctx: ctx + STEPS + 1].tolist()]
     assert toks[0] == seed
+    rl = [oracle.step(toks[i], ctx + i) for i in range(STEPS)]
+    _check_steps(toks, gl, rl)
+
+
+@pytest.mark.parametrize("kv", ["int8", "fp16"])
+def test_tiny_fused_shape_w4_matches_oracle(kv, dev):
+    """Hidden 2048 and 16 heads at 2 layers: the 4-bit layer's fused attention
+    output (merge + 4-bit o_proj, residual + norm + router); 32 greedy steps
+    against the oracle from the GPU's cache."""
+    from test_gpu_decode import TINY_FUSED
+
+    print("case: tiny fused-shape w4a16 model, kv %s" % kv, flush=True)
+    w = _weights(TINY_FUSED, 4, "fp16", 36, dev)
+    ctx = 40
+    prompt = torch.randint(0, TINY_FUSED.vocab, (ctx,), generator=torch.Generator().manual_seed(37)).tolist()
+    sess = DecodeSession(w, prompt, max_new_tokens=STEPS, kv_cache=kv)
+    assert sess.attn_output_fused and sess.launches_per_step == 6 * TINY_FUSED.layers + 3
+    sess.prefill(mode="stepped")
+    oracle = OracleDecoder(w.to_host(), sess.max_seq, kv=sess.kv_cpu())
+    gl = []
+    for _ in range(STEPS):
+        sess.replay(1)
+        gl.append(sess.logits_cpu())
+    toks = [int(t) for t in sess.history[ctx: ctx + STEPS + 1].tolist()]
     rl = [oracle.step(toks[i], ctx + i) for i in range(STEPS)]
     _check_steps(toks, gl, rl)
 
@@ -146,7 +171,7 @@ def test_olmoe_shape_w4a16_random_prompt(dev):
     ctx = 192
     prompt = torch.randint(0, OLMOE_1B_7B.vocab, (ctx,), generator=torch.Generator().manual_seed(42)).tolist()
     sess = DecodeSession(w, prompt, max_new_tokens=24)
-    assert sess.launches_per_step == 7 * 16 + 3
+    assert sess.attn_output_fused and sess.launches_per_step == 6 * 16 + 3
     sess.prefill(mode="stepped")
     pos0, tok0 = sess.position, sess.next_token_cpu()
     kv0 = sess.kv_cpu()

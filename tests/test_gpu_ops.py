@@ -657,26 +657,33 @@ def _merge_inputs(heads, ns, D, seed):
 
 @pytest.mark.parametrize("ns", [1, 5, 16, 17, 64])
 @pytest.mark.parametrize("heads", [16, 4, 8, 32])
-def test_merge_o_proj_partials(ns, heads, dev):
-    """lemoq_attn_merge_o_proj_w8 (merge fused into o_proj, split over groups of
-    4 heads).  Its merge is lemoq_attn_merge's, so each partial row g must equal
-    the fp64 product of the dequantised columns [512g, 512g+512) with the
-    merged fp16 attention output of lemoq_attn_merge, to fp32 summation error;
-    fp16(sum of partials) is the o_proj output (oracle: LSE merge in fp64, then
-    the w8 linear)."""
+@pytest.mark.parametrize("bits", [8, 4])
+def test_merge_o_proj_partials(ns, heads, bits, dev):
+    """lemoq_attn_merge_o_proj_w8 / _w4 (merge fused into o_proj, split over
+    groups of 4 heads; int8 or packed 4-bit codes).  Its merge is
+    lemoq_attn_merge's, so each partial row g must equal the fp64 product of the
+    dequantised columns [512g, 512g+512) with the merged fp16 attention output of
+    lemoq_attn_merge, to fp32 summation error; fp16(sum of partials) is the
+    o_proj output (oracle: LSE merge in fp64, then the linear)."""
     from lemoq import _hip
 
     D, N, group = 128, 2048, 128
     HD = heads * D
     m, l, acc = _merge_inputs(heads, ns, D, seed=ns * 7 + heads)
     w = randn(N, HD, seed=900 + heads, std=0.02)
-    codes, scale = _q8(w, group)
-    md, ld, ad, cd, sd = (t.to(dev) for t in (m, l, acc, codes, scale))
+    if bits == 8:
+        codes, scale = _q8(w, group)
+        stored = codes
+    else:
+        q = oq.rtn_quantize(w.numpy(), bits=4, group_size=group, symmetric=True)
+        codes = torch.from_numpy(q["codes_padded"].astype(np.int8))  # unpacked, for the oracle
+        stored, scale = torch.from_numpy(oq.pack_4bit(q["codes_padded"])), torch.from_numpy(q["scale_f16"])
+    md, ld, ad, cd, sd = (t.to(dev) for t in (m, l, acc, stored, scale))
     part = torch.full((heads // 4, N), float("nan"), dtype=torch.float32, device=dev)
     attn = torch.empty((HD,), dtype=torch.float16, device=dev)
     st = _hip.stream_of(dev)
-    _hip.call("lemoq_attn_merge_o_proj_w8", _hip.ptr(md), _hip.ptr(ld), _hip.ptr(ad), heads, ns, D, _hip.ptr(cd),
-              _hip.ptr(sd), N, group, _hip.ptr(part), st)
+    _hip.call("lemoq_attn_merge_o_proj_w%d" % bits, _hip.ptr(md), _hip.ptr(ld), _hip.ptr(ad), heads, ns, D,
+              _hip.ptr(cd), _hip.ptr(sd), N, group, _hip.ptr(part), st)
     _hip.call("lemoq_attn_merge", _hip.ptr(md), _hip.ptr(ld), _hip.ptr(ad), heads, ns, D, _hip.ptr(attn), st)
     torch.cuda.synchronize()
     p = part.cpu().double()
