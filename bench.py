@@ -1382,26 +1382,23 @@ STEP_LAYER_KERNELS = [
     ("down (+ residual)", "moe_down_kernel<1, 4, true>"),
 ]
 STEP_TAIL_KERNELS = [("lm_head (+ final norm, argmax partials)", "gemv_w8_kernel<2, 2, 1, true>"),
-                     ("argmax + advance", "argmax_advance_kernel<true>")]
+                     ("argmax + advance", "argmax_advance_kernel<true")]  # <true, false>: over the partials
 
 
-# The 4-bit step (--weights w4a16) at the OLMoE shape by position: layer 0's embedding
-# gather, then per layer the 6 launches below, then the fp16 lm_head and the greedy
-# pick (told apart by their place in the step, as the lm_head runs the router's
-# kernel).
+# The 4-bit step (--weights w4a16) at the OLMoE shape by position: per layer the 6
+# launches below (layer 0's q|k|v GEMV gathers the embedding row), then the fp16
+# lm_head and the greedy pick (told apart by their place in the step, as the
+# lm_head runs the router's kernel).
 STEP_W4_LAYER = ["qkv (4-bit, + input RMSNorm)", "attention split (+ q/k norm, RoPE, cache write)",
                  "merge + o_proj (4-bit)", "residual + norm + router",
                  "gate/up (4-bit, + routing)", "down (4-bit, + residual)"]
 STEP_W4_HEAD = ["lm_head fp16 (+ final norm)", "argmax + advance"]
-STEP_W4_END = "argmax_advance_kernel<false>"
+STEP_W4_END = "argmax_advance_kernel<false"  # over the fp16 logits (<false, true>: 16-byte loads)
 
 
 def _w4_roles() -> list:
     """Role of each launch of a whole 4-bit step, by position."""
-    roles = ["embedding gather"]
-    for _ in range(16):
-        roles += STEP_W4_LAYER
-    return roles + STEP_W4_HEAD
+    return STEP_W4_LAYER * 16 + STEP_W4_HEAD
 
 
 def summarize_step(trace_csv: str, last: int = 0) -> str:
@@ -1424,7 +1421,7 @@ def summarize_step(trace_csv: str, last: int = 0) -> str:
     steps, cur = [], []
     for r in rows:
         cur.append(r)
-        if "argmax_advance_kernel<true>" in _short_kernel(r["Kernel_Name"]):
+        if "argmax_advance_kernel<true" in _short_kernel(r["Kernel_Name"]):
             steps.append(cur)
             cur = []
     per_step = len(STEP_LAYER_KERNELS) * 16 + len(STEP_TAIL_KERNELS)
@@ -1454,14 +1451,15 @@ def _summarize_step_w4(all_rows: list, last: int, trace_csv: str) -> str:
     roles = _w4_roles()
     per_step = len(roles)
     # a chunk may start with other dispatches before the step (the first one after
-    # the session's set-up): keep its last per_step launches when they open with the gather
+    # the session's set-up): keep its last per_step launches when they open with
+    # the q|k|v GEMV (layer 0 gathers the embedding row inside it)
     steps = [st[-per_step:] for st in steps
-             if len(st) >= per_step and "gather_rows_kernel" in _short_kernel(st[-per_step]["Kernel_Name"])]
+             if len(st) >= per_step and "gemv_q_kernel<" in _short_kernel(st[-per_step]["Kernel_Name"])]
     if last > 0:
         steps = steps[-last:]
     if not steps:
         return "no whole 4-bit decode steps in %s" % trace_csv
-    labels = ["embedding gather"] + STEP_W4_LAYER + STEP_W4_HEAD
+    labels = STEP_W4_LAYER + STEP_W4_HEAD
     return _step_table(steps, per_step, labels, lambda i, r: roles[i])
 
 

@@ -129,16 +129,24 @@ int lemoq_gemv_q(const uint16_t* x, int64_t M, int64_t K, const void* qweight, i
 
 /* lemoq_gemv_q of the RMSNorm of x (the decoder layer's input norm before the
  * packed q|k|v projection, rms_norm_fused then dequant_gemm_fused,
- * src/lemoq/kernels/rmsnorm.py:102-163, _dequant_triton.py:155-293): each
- * wave normalises the row it holds, xn = fp16(fp16(x * rsqrt(mean(x^2) + eps))
- * * norm_w) with an fp32 mean over K (lemoq_rmsnorm's rounding points; the
- * fp32 sum of squares runs in another order, so an element may differ from
- * lemoq_rmsnorm's by one fp16 ulp), then y = xn @ w^T as lemoq_gemv_q.
- * norm_w (K) fp16; fp16 or E8M0 scales only (scale_is_f32 returns
- * LEMOQ_ERR_UNSUPPORTED); eps >= 0.  Used by the 4-bit decode step. */
-int lemoq_gemv_q_rmsnorm(const uint16_t* x, int64_t M, int64_t K, const uint16_t* norm_w, float eps,
-                         const void* qweight, int fmt, const void* scale, const void* zero, int scale_is_f32,
-                         int64_t N, int64_t padded_k, int64_t group, void* y, int y_is_f16, void* stream);
+ * src/lemoq/kernels/rmsnorm.py:102-163, _dequant_triton.py:155-293):
+ * xn = fp16(fp16(x * rsqrt(mean(x^2) + eps)) * norm_w) with an fp32 mean over
+ * K (lemoq_rmsnorm's rounding points; the fp32 sum of squares runs in another
+ * order, so an element may differ from lemoq_rmsnorm's by one fp16 ulp), then
+ * y = xn @ w^T as lemoq_gemv_q.  Rows that fill the kernel's 1 KB code chunks
+ * exactly with K a multiple of 2048 (4-bit K 2048 / 4096 / 8192, 8-bit K 2048
+ * / 4096 / 8192), x and norm_w 16-byte aligned, normalise once per block
+ * (LDS); other rows in every wave.  With x_row_index (a device int64, M == 1)
+ * the row is x[*x_row_index] of x_rows (the embedding gather of layer 0; an
+ * index outside reads as a zero row); x_copy (nullable, needs the per-block
+ * form, else LEMOQ_ERR_UNSUPPORTED) receives the raw row, written by block 0
+ * (the residual stream).  norm_w (K) fp16; fp16 or E8M0 scales only
+ * (scale_is_f32 returns LEMOQ_ERR_UNSUPPORTED); eps >= 0.  Used by the 4-bit
+ * decode step. */
+int lemoq_gemv_q_rmsnorm(const uint16_t* x, const int64_t* x_row_index, int64_t x_rows, int64_t M, int64_t K,
+                         const uint16_t* norm_w, float eps, uint16_t* x_copy, const void* qweight, int fmt,
+                         const void* scale, const void* zero, int scale_is_f32, int64_t N, int64_t padded_k,
+                         int64_t group, void* y, int y_is_f16, void* stream);
 
 /* lemoq_gemv_q with the fp16 residual add of the decoder layer after o_proj
  * (transformers OlmoeDecoderLayer.forward, the `residual + hidden_states` of
@@ -644,12 +652,14 @@ typedef struct LemoqOlmoeStep {
    * H/2), o_codes (H, heads*D/2), gu_codes (E, 2F, H/2), dn_codes (E, H, F/2);
    * scales as above; group % 32 == 0).  A 4-bit step runs 6 launches per
    * layer on the fused attention-output path (the shape rule below):
-   * lemoq_gemv_q_rmsnorm (input norm + q|k|v), the fused attention,
+   * lemoq_gemv_q_rmsnorm (input norm + q|k|v; layer 0 gathers the embedding
+   * row and stores it to h), the fused attention,
    * lemoq_attn_merge_o_proj_w4, lemoq_router_logits_resid,
    * lemoq_moe_gate_up_w4_routed, lemoq_moe_down_w4 (+ residual); otherwise 7,
    * with lemoq_attn_merge, lemoq_gemv_q_residual (o_proj + residual into h)
-   * and lemoq_router_logits in place of the middle two.  Layer 0 first gathers
-   * the embedding row into h (lemoq_gather_rows). */
+   * and lemoq_router_logits in place of the middle two.  (When the q|k|v
+   * GEMV's rows do not take its per-block norm, layer 0 first gathers the
+   * embedding row into h with lemoq_gather_rows.) */
   int64_t weight_bits;
   /* fp16 lm_head (vocab, H), or NULL for the W8 lm_head of lm_codes /
    * lm_scale.  With it the step ends with lemoq_router_logits (final norm +

@@ -104,6 +104,13 @@ struct GemvQArgs {
   const uint16_t* residual;  // (M, N) fp16 with ld y_ld, or NULL: y = fp16(fp16(acc) + residual)
   const uint16_t* norm_w;    // (K) fp16 RMSNorm weight of x, or NULL: x as it is
   float eps;
+  // RMSNorm instances only: x row *x_row_index of x_rows (M == 1; an index
+  // outside reads as a zero row), the raw row copied to x_copy by block 0, and
+  // the norm computed once per block through LDS (block_norm) or in every wave
+  const int64_t* x_row_index;
+  int64_t x_rows;
+  uint16_t* x_copy;
+  int block_norm;
 };
 
 // HF RMSNorm of the row the wave holds (lane slices of NV values per chunk,
@@ -135,17 +142,12 @@ __device__ __forceinline__ void xq_rmsnorm(uint32_t (&xw)[KCH][NV / 2], const ui
     }
 }
 
-template <int FMT, int KCH, int R, bool S32, bool NORM = false>
-__global__ __launch_bounds__(256) void gemv_q_kernel(const GemvQArgs a) {
+// The wave's R rows x KCH chunks of codes, their scales (and zero points).
+template <int FMT, int KCH, int R, bool S32>
+__device__ __forceinline__ uint32_t gemv_q_issue(const GemvQArgs& a, int64_t row0, int lane, u32x4 (&c)[R][KCH],
+                                                 uint32_t (&sraw)[R][KCH], uint32_t (&zraw)[R][KCH]) {
   constexpr int NV = qf_slice_codes(FMT);
-  constexpr int CPC = 64 * NV;  // codes per 1 KB chunk
   constexpr bool ASYM = qf_asym(FMT);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t m = blockIdx.y;
-  const int64_t row0 = ((int64_t)blockIdx.x * 4 + wave) * R;
-
-  u32x4 c[R][KCH];
-  uint32_t sraw[R][KCH], zraw[R][KCH];
   uint32_t ok = 0u;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
@@ -163,20 +165,120 @@ __global__ __launch_bounds__(256) void gemv_q_kernel(const GemvQArgs a) {
       ok |= (in ? 1u : 0u) << (r * KCH + j);
     }
   }
-  const uint16_t* xr = a.x + m * a.x_ld;
-  const bool vec = ((reinterpret_cast<uintptr_t>(xr) & 15u) == 0) && ((a.K & 7) == 0);
+  return ok;
+}
+
+template <int FMT, int KCH, int R, bool S32, bool NORM = false>
+__global__ __launch_bounds__(256) void gemv_q_kernel(const GemvQArgs a) {
+  constexpr int NV = qf_slice_codes(FMT);
+  constexpr int CPC = 64 * NV;  // codes per 1 KB chunk
+  constexpr bool ASYM = qf_asym(FMT);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t m = blockIdx.y;
+  const int64_t row0 = ((int64_t)blockIdx.x * 4 + wave) * R;
+
+  u32x4 c[R][KCH];
+  uint32_t sraw[R][KCH], zraw[R][KCH];
+  uint32_t ok = 0u;
   uint32_t xw[KCH][NV / 2];
+  if constexpr (!NORM) {
+    ok = gemv_q_issue<FMT, KCH, R, S32>(a, row0, lane, c, sraw, zraw);
+    const uint16_t* xr = a.x + m * a.x_ld;
+    const bool vec = ((reinterpret_cast<uintptr_t>(xr) & 15u) == 0) && ((a.K & 7) == 0);
 #pragma unroll
-  for (int j = 0; j < KCH; ++j) xq_load<NV>(xw[j], xr, a.K, j * CPC + lane * NV, vec);
-  constexpr int NWV = NORM ? KCH : 1;
-  uint32_t nw[NWV][NV / 2];
-  if constexpr (NORM) {  // the norm weight's slices, laid out as x's
-    const bool vw = ((reinterpret_cast<uintptr_t>(a.norm_w) & 15u) == 0) && ((a.K & 7) == 0);
+    for (int j = 0; j < KCH; ++j) xq_load<NV>(xw[j], xr, a.K, j * CPC + lane * NV, vec);
+    LEMOQ_LOADS_ISSUED();
+  } else {
+    // RMSNorm prologue.  The row and the norm weight are loaded first (the
+    // memory counter retires in order, so the norm waits only for them while
+    // the weight codes stream in).  Rows that fill the chunks exactly, K a
+    // multiple of 2048: once per block (8 values a thread, an LDS reduction,
+    // the normalised row in LDS); otherwise in every wave from its slices.
+    bool x_ok = true;
+    const uint16_t* xr = a.x + m * a.x_ld;
+    if (a.x_row_index) {
+      const int64_t r = a.x_row_index[0];
+      x_ok = r >= 0 && r < a.x_rows;  // an index outside the table reads as a zero row
+      xr = a.x + (x_ok ? r : 0) * a.x_ld;
+    }
+    constexpr int BNV = (KCH * CPC) % 2048 == 0 ? (KCH * CPC) / 2048 : 1;  // u32x4 a thread, block form
+    constexpr bool kBlockForm = (KCH * CPC) % 2048 == 0;
+    if (kBlockForm && a.block_norm) {
+      __shared__ __align__(16) uint16_t xs[KCH * CPC];
+      __shared__ float red[4];
+      u32x4 rv[BNV], wv[BNV];
 #pragma unroll
-    for (int j = 0; j < KCH; ++j) xq_load<NV>(nw[j], a.norm_w, a.K, j * CPC + lane * NV, vw);
+      for (int i = 0; i < BNV; ++i) {
+        const int off = (i * 256 + threadIdx.x) * 8;
+        rv[i] = *reinterpret_cast<const u32x4*>(xr + off);
+        wv[i] = *reinterpret_cast<const u32x4*>(a.norm_w + off);
+      }
+      ok = gemv_q_issue<FMT, KCH, R, S32>(a, row0, lane, c, sraw, zraw);
+      LEMOQ_LOADS_ISSUED();
+      float ssq = 0.0f;
+#pragma unroll
+      for (int i = 0; i < BNV; ++i) {
+        if (!x_ok) rv[i] = (u32x4){0u, 0u, 0u, 0u};
+        const uint32_t q[4] = {rv[i].x, rv[i].y, rv[i].z, rv[i].w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const float x0 = h2f((uint16_t)(q[k] & 0xFFFFu)), x1 = h2f((uint16_t)(q[k] >> 16));
+          ssq = fmaf(x0, x0, ssq);
+          ssq = fmaf(x1, x1, ssq);
+        }
+        if (a.x_copy && blockIdx.x == 0 && m == 0)
+          *reinterpret_cast<u32x4*>(a.x_copy + (i * 256 + threadIdx.x) * 8) = rv[i];
+      }
+      ssq = wave_sum(ssq);
+      if (lane == 0) red[wave] = ssq;
+      __syncthreads();
+      const float rstd = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)a.K + a.eps);
+#pragma unroll
+      for (int i = 0; i < BNV; ++i) {
+        const uint32_t q[4] = {rv[i].x, rv[i].y, rv[i].z, rv[i].w};
+        const uint32_t g[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
+        uint32_t o[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const uint16_t n0 = f2h(h2f((uint16_t)(q[k] & 0xFFFFu)) * rstd);
+          const uint16_t n1 = f2h(h2f((uint16_t)(q[k] >> 16)) * rstd);
+          const uint16_t y0 = f2h(h2f(n0) * h2f((uint16_t)(g[k] & 0xFFFFu)));
+          const uint16_t y1 = f2h(h2f(n1) * h2f((uint16_t)(g[k] >> 16)));
+          o[k] = (uint32_t)y0 | ((uint32_t)y1 << 16);
+        }
+        *reinterpret_cast<u32x4*>(xs + (i * 256 + threadIdx.x) * 8) = (u32x4){o[0], o[1], o[2], o[3]};
+      }
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < KCH; ++j)
+#pragma unroll
+        for (int q = 0; q < NV / 8; ++q) {
+          const u32x4 v = *reinterpret_cast<const u32x4*>(xs + j * CPC + lane * NV + 8 * q);
+          xw[j][4 * q + 0] = v.x;
+          xw[j][4 * q + 1] = v.y;
+          xw[j][4 * q + 2] = v.z;
+          xw[j][4 * q + 3] = v.w;
+        }
+    } else {
+      const bool vec = ((reinterpret_cast<uintptr_t>(xr) & 15u) == 0) && ((a.K & 7) == 0);
+      const bool vw = ((reinterpret_cast<uintptr_t>(a.norm_w) & 15u) == 0) && ((a.K & 7) == 0);
+      uint32_t nw[KCH][NV / 2];
+#pragma unroll
+      for (int j = 0; j < KCH; ++j) {
+        xq_load<NV>(xw[j], xr, a.K, j * CPC + lane * NV, vec);
+        xq_load<NV>(nw[j], a.norm_w, a.K, j * CPC + lane * NV, vw);
+      }
+      ok = gemv_q_issue<FMT, KCH, R, S32>(a, row0, lane, c, sraw, zraw);
+      LEMOQ_LOADS_ISSUED();
+      if (!x_ok) {
+#pragma unroll
+        for (int j = 0; j < KCH; ++j)
+#pragma unroll
+          for (int i = 0; i < NV / 2; ++i) xw[j][i] = 0u;
+      }
+      xq_rmsnorm<KCH, NV>(xw, nw, a.K, a.eps);
+    }
   }
-  LEMOQ_LOADS_ISSUED();
-  if constexpr (NORM) xq_rmsnorm<KCH, NV>(xw, nw, a.K, a.eps);
 
   float acc[R];
 #pragma unroll
@@ -713,10 +815,17 @@ extern "C" int lemoq_fake_quant_rows(const uint16_t* x, int64_t rows, int64_t D,
 
 namespace {
 
+struct NormOpts {
+  const uint16_t* norm_w;
+  float eps;
+  const int64_t* x_row_index;
+  int64_t x_rows;
+  uint16_t* x_copy;
+};
+
 int gemv_q_common(const uint16_t* x, int64_t M, int64_t K, const void* qweight, int fmt, const void* scale,
                   const void* zero, int scale_is_f32, int64_t N, int64_t padded_k, int64_t group, void* y,
-                  int y_is_f16, const uint16_t* residual, void* stream, const uint16_t* norm_w = nullptr,
-                  float eps = 0.0f);
+                  int y_is_f16, const uint16_t* residual, void* stream, const NormOpts* norm = nullptr);
 
 }  // namespace
 
@@ -727,15 +836,23 @@ extern "C" int lemoq_gemv_q(const uint16_t* x, int64_t M, int64_t K, const void*
                        nullptr, stream);
 }
 
-extern "C" int lemoq_gemv_q_rmsnorm(const uint16_t* x, int64_t M, int64_t K, const uint16_t* norm_w, float eps,
+extern "C" int lemoq_gemv_q_rmsnorm(const uint16_t* x, const int64_t* x_row_index, int64_t x_rows, int64_t M,
+                                    int64_t K, const uint16_t* norm_w, float eps, uint16_t* x_copy,
                                     const void* qweight, int fmt, const void* scale, const void* zero,
                                     int scale_is_f32, int64_t N, int64_t padded_k, int64_t group, void* y,
                                     int y_is_f16, void* stream) {
-  if (!norm_w) return LEMOQ_ERR_NULL;
+  if (!norm_w || !x) return LEMOQ_ERR_NULL;
   if (!(eps >= 0.0f)) return LEMOQ_ERR_SHAPE;  // negative or NaN eps
   if (scale_is_f32) return LEMOQ_ERR_UNSUPPORTED;  // the norm prologue takes fp16 (or E8M0) scales
+  if (x_row_index && (M != 1 || x_rows <= 0)) return LEMOQ_ERR_SHAPE;
+  NormOpts o;
+  o.norm_w = norm_w;
+  o.eps = eps;
+  o.x_row_index = x_row_index;
+  o.x_rows = x_row_index ? x_rows : 0;
+  o.x_copy = x_copy;
   return gemv_q_common(x, M, K, qweight, fmt, scale, zero, scale_is_f32, N, padded_k, group, y, y_is_f16,
-                       nullptr, stream, norm_w, eps);
+                       nullptr, stream, &o);
 }
 
 extern "C" int lemoq_gemv_q_residual(const uint16_t* x, int64_t M, int64_t K, const void* qweight, int fmt,
@@ -758,7 +875,7 @@ namespace {
 
 int gemv_q_common(const uint16_t* x, int64_t M, int64_t K, const void* qweight, int fmt, const void* scale,
                   const void* zero, int scale_is_f32, int64_t N, int64_t padded_k, int64_t group, void* y,
-                  int y_is_f16, const uint16_t* residual, void* stream, const uint16_t* norm_w, float eps) {
+                  int y_is_f16, const uint16_t* residual, void* stream, const NormOpts* norm) {
   if (!x || !y) return LEMOQ_ERR_NULL;
   const int rc = check_format(fmt, qweight, scale, zero, scale_is_f32, N, padded_k, group);
   if (rc) return rc;
@@ -779,10 +896,19 @@ int gemv_q_common(const uint16_t* x, int64_t M, int64_t K, const void* qweight, 
   a.y_ld = N;
   a.y_f16 = y_is_f16 ? 1 : 0;
   a.residual = residual;
-  a.norm_w = norm_w;
-  a.eps = eps;
+  a.norm_w = norm ? norm->norm_w : nullptr;
+  a.eps = norm ? norm->eps : 0.0f;
+  a.x_row_index = norm ? norm->x_row_index : nullptr;
+  a.x_rows = norm ? norm->x_rows : 0;
+  a.x_copy = norm ? norm->x_copy : nullptr;
   const int64_t chunks = (a.row_bytes + 1023) / 1024;
   const int kch = chunks <= 1 ? 1 : (chunks <= 2 ? 2 : (chunks <= 4 ? 4 : 8));
+  // the block form of the norm: rows that fill the kernel's chunks exactly, a
+  // multiple of 2048 values, 16-byte aligned rows (x_copy needs it)
+  const int64_t cpc = 64 * (qf_4bit(fmt) ? 32 : 16);
+  a.block_norm = norm && K == kch * cpc && K % 2048 == 0 && lemoq_aligned16(x) && lemoq_aligned16(a.norm_w) &&
+                 (!a.x_copy || lemoq_aligned16(a.x_copy));
+  if (norm && a.x_copy && !a.block_norm) return LEMOQ_ERR_UNSUPPORTED;
   const int64_t blocks = (N + 4 * kGemvQRows - 1) / (4 * kGemvQRows);
   const dim3 grid((unsigned)blocks, (unsigned)M);
   hipStream_t st = lemoq_stream(stream);

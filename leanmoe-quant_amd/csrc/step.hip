@@ -180,13 +180,27 @@ int enqueue_head(const LemoqOlmoeStep* p, void* stream) {
                                  p->filled, p->prompt, p->prompt_len, p->history, p->history_len, stream);
 }
 
+// Whether the 4-bit q|k|v GEMV normalises once per block (lemoq_gemv_q_rmsnorm's
+// rule: 4-bit rows of H codes fill its 1 KB chunks exactly for H 2048, 4096,
+// 8192; the step's buffers are 16-byte aligned), which lets it gather layer
+// 0's embedding row itself.
+bool qkv_w4_block_norm(const LemoqOlmoeStep* p) {
+  const int64_t H = p->hidden;
+  return (H == 2048 || H == 4096 || H == 8192) && a16(p->embed) && a16(p->h) && a16(p->layers[0].ln_in);
+}
+
 // One layer on 4-bit weights: 6 launches on the fused attention-output path,
-// 7 otherwise (one more on layer 0, the embedding gather).
+// 7 otherwise (plus, on layer 0, the embedding gather when the q|k|v GEMV
+// cannot do it).
 int enqueue_layer_w4(const LemoqOlmoeStep* p, const LemoqOlmoeLayer& w, bool first, AttnPath path, void* stream) {
   const int64_t H = p->hidden, HD = p->heads * p->head_dim, g = p->group;
-  if (first) LEMOQ_TRY(lemoq_gather_rows(p->embed, p->vocab, H, p->token, 1, p->h, stream));
-  // input RMSNorm (in every wave) + packed q|k|v
-  LEMOQ_TRY(lemoq_gemv_q_rmsnorm(p->h, 1, H, w.ln_in, p->eps, w.qkv_codes, LEMOQ_QFMT_W4, w.qkv_scale, nullptr, 0,
+  // input RMSNorm + packed q|k|v; layer 0 gathers the embedding row of *token and
+  // stores it as the residual (in the GEMV when it takes the per-block norm)
+  const bool gather_in_gemv = qkv_w4_block_norm(p);
+  if (first && !gather_in_gemv) LEMOQ_TRY(lemoq_gather_rows(p->embed, p->vocab, H, p->token, 1, p->h, stream));
+  const bool g0 = first && gather_in_gemv;
+  LEMOQ_TRY(lemoq_gemv_q_rmsnorm(g0 ? p->embed : p->h, g0 ? p->token : nullptr, g0 ? p->vocab : 0, 1, H, w.ln_in,
+                                 p->eps, g0 ? p->h : nullptr, w.qkv_codes, LEMOQ_QFMT_W4, w.qkv_scale, nullptr, 0,
                                  3 * HD, H, g, p->qkv, 1, stream));
   LEMOQ_TRY(enqueue_attention(p, w, stream));
   if (path == kAttnFusedOut) {

@@ -126,7 +126,8 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "lemoq_moe_gate_up_w4_routed": (
         _I, [_P, _P, _P, _P, _I64, _I, _I64, _I64, _I64, _I64, _P, _P, _P, _P]),
     "lemoq_gemv_q_residual": (_I, [_P, _I64, _I64, _P, _I, _P, _P, _I, _I64, _I64, _I64, _P, _P, _P]),
-    "lemoq_gemv_q_rmsnorm": (_I, [_P, _I64, _I64, _P, _F, _P, _I, _P, _P, _I, _I64, _I64, _I64, _P, _I, _P]),
+    "lemoq_gemv_q_rmsnorm": (
+        _I, [_P, _P, _I64, _I64, _I64, _P, _F, _P, _P, _I, _P, _P, _I, _I64, _I64, _I64, _P, _I, _P]),
     "lemoq_attn_merge_o_proj_w4": (_I, [_P, _P, _P, _I64, _I64, _I64, _P, _P, _I64, _I64, _P, _P]),
     "lemoq_moe_down_w4": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P]),
     "lemoq_gemv_w8": (_I, [_P, _I64, _I64, _P, _P, _I64, _I64, _I64, _P, _I, _P]),

@@ -469,10 +469,12 @@ class DecodeSession:
     @property
     def launches_per_step(self) -> int:
         """Kernel launches in one captured step (see csrc/step.hip): 6 per layer
-        on the fused attention-output path, 7 otherwise, one more for a 4-bit
-        step's embedding gather, and the lm_head and greedy selection."""
+        on the fused attention-output path, 7 otherwise, the lm_head and greedy
+        selection, and for a 4-bit step whose q|k|v GEMV cannot gather the
+        embedding row itself (hidden not 2048 / 4096 / 8192) one gather."""
         per_layer = 6 if self.attn_output_fused else 7
-        return per_layer * self.shape.layers + 2 + (1 if self.weights.bits == 4 else 0)
+        gather = self.weights.bits == 4 and self.shape.hidden not in (2048, 4096, 8192)
+        return per_layer * self.shape.layers + 2 + int(gather)
 
     def capture(self, steps_per_graph: int = 1) -> dict[str, Any]:
         """Capture one decode step into a hipGraph (state is untouched by the capture).

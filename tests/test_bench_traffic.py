@@ -102,8 +102,9 @@ def test_summarize_step_timeline(tmp_path):
     time of each, per-kernel averages."""
     path = tmp_path / "trace.csv"
     names = [k for _, k in bench.STEP_LAYER_KERNELS] * 16 + [k for _, k in bench.STEP_TAIL_KERNELS]
+    names = [k + ", false>" if k.endswith("<true") else k for k in names]  # the kernel's full instance name
     rows, t = [], 1000
-    rows.append(("void (anonymous namespace)::argmax_advance_kernel<true>(args)", t, t + 2000))  # prefill seed pick
+    rows.append(("void (anonymous namespace)::argmax_advance_kernel<true, false>(args)", t, t + 2000))  # seed pick
     t += 5000
     for _ in range(2):
         for n in names:
@@ -125,7 +126,7 @@ def test_summarize_step_timeline(tmp_path):
 
 
 def test_summarize_step_timeline_of_the_4bit_step(tmp_path):
-    """The 4-bit step (bench.py --mode step --weights w4a16): 99 launches told
+    """The 4-bit step (bench.py --mode step --weights w4a16): 98 launches told
     apart by position (the lm_head runs the router's kernel); the prompt's steps
     come first and --summarize-last keeps the decode steps.  Synthetic trace: 3 prompt steps (1 us kernels) and 2 decode
     steps (role i lasts i + 1 us), 1 us gaps."""
@@ -133,11 +134,11 @@ def test_summarize_step_timeline_of_the_4bit_step(tmp_path):
     layer = ["gemv_q_kernel<2, 1, 2, false, true>", "attn_split_fused_i8_kernel<128, 4, 3>",
              "merge_oproj_q4_kernel<16>", "router_resid_kernel<2, 4>",
              "moe_gate_up_q4_kernel<1, 2, 16, 1>", "moe_down_q4_kernel<1, 4, 8>"]
-    step = ["gather_rows_kernel"] + layer * 16 + ["router_logits_kernel<2, true>", "argmax_advance_kernel<false>"]
+    step = layer * 16 + ["router_logits_kernel<2, true>", "argmax_advance_kernel<false, true>"]
     rows, t = [("void at::native::fill_kernel(args)", 0, 500)], 1000
     for s in range(5):
         for i, n in enumerate(step):
-            d = 1000 if s < 3 else 1000 * (1 + (0 if i == 0 else 1 + (i - 1) % 6 if i <= 96 else 7 + (i - 97)))
+            d = 1000 if s < 3 else 1000 * (1 + (i % 6 if i < 96 else 6 + (i - 96)))
             rows.append(("void (anonymous namespace)::%s(args)" % n, t, t + d))
             t += d + 1000
     with open(path, "w", newline="") as f:
@@ -146,10 +147,9 @@ def test_summarize_step_timeline_of_the_4bit_step(tmp_path):
         for n, a, b in rows:
             w.writerow({"Kernel_Name": n, "Start_Timestamp": a, "End_Timestamp": b})
     out = bench.summarize_step(str(path), last=2)
-    assert out.startswith("2 whole steps of 99 launches"), out
-    assert "| embedding gather | 1 | 1.00 |" in out
-    assert "| qkv (4-bit, + input RMSNorm) | 16 | 2.00 |" in out
-    assert "| merge + o_proj (4-bit) | 16 | 4.00 |" in out
-    assert "| residual + norm + router | 16 | 5.00 |" in out
-    assert "| lm_head fp16 (+ final norm) | 1 | 8.00 |" in out and "| argmax + advance | 1 | 9.00 |" in out
-    assert bench.summarize_step(str(path)).startswith("5 whole steps of 99 launches")
+    assert out.startswith("2 whole steps of 98 launches"), out
+    assert "| qkv (4-bit, + input RMSNorm) | 16 | 1.00 |" in out
+    assert "| merge + o_proj (4-bit) | 16 | 3.00 |" in out
+    assert "| residual + norm + router | 16 | 4.00 |" in out
+    assert "| lm_head fp16 (+ final norm) | 1 | 7.00 |" in out and "| argmax + advance | 1 | 8.00 |" in out
+    assert bench.summarize_step(str(path)).startswith("5 whole steps of 98 launches")

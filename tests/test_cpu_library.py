@@ -169,9 +169,11 @@ def test_argument_rejection_happens_before_any_launch():
     assert gr(1 << 22, (1 << 22) + 64) == -2                # partial overlap
     assert gr(1 << 22, 1 << 23, N=64, M=0) == -2            # then the GEMV's own rules
     # 4-bit q|k|v GEMV with the input norm: norm weight required, eps >= 0, fp16 scales only
-    gn = lambda nw=fake, eps=1e-5, s32=0: lib.lemoq_gemv_q_rmsnorm(  # noqa: E731
-        fake, 1, 128, nw, eps, fake, 2, fake, None, s32, 64, 128, 128, fake, 1, None)
+    gn = lambda nw=fake, eps=1e-5, s32=0, idx=None, M=1, K=128, copy=None: lib.lemoq_gemv_q_rmsnorm(  # noqa: E731
+        fake, idx, 10, M, K, nw, eps, copy, fake, 2, fake, None, s32, 64, K, 128, fake, 1, None)
     assert gn(nw=None) == -1 and gn(eps=-1.0) == -2 and gn(eps=math.nan) == -2 and gn(s32=1) == -3
+    assert gn(idx=fake, M=2) == -2                           # a gathered row is one row
+    assert gn(copy=fake) == -3                               # x_copy needs the per-block form (K 128: per wave)
     # routed 4-bit gate/up: ids/weights outputs, top_k <= min(64, E), E <= 256, 4-bit groups
     gu = lambda E=64, K=8, g=128, ti=fake, tw=fake: lib.lemoq_moe_gate_up_w4_routed(  # noqa: E731
         fake, fake, fake, fake, K, 0, E, 1024, 2048, g, fake, ti, tw, None)

@@ -61,6 +61,36 @@ def test_gemv_q_residual_equals_gemv_then_fp16_add(M, N, K, dev):
     assert torch.equal(out.cpu(), ref) and torch.equal(inplace.cpu(), ref)
 
 
+@pytest.mark.parametrize("K", [2048, 4096])
+def test_qkv_norm_gemv_gathers_the_embedding_row(K, dev):
+    """lemoq_gemv_q_rmsnorm with x_row_index (layer 0 of the 4-bit step: the
+    embedding row of the device token, normalised once per block): the outputs
+    equal those of the same call on the row itself, bit for bit; x_copy receives
+    the raw row; an index outside the table reads as a zero row (zero outputs,
+    zero copy)."""
+    print("case: 4-bit q|k|v GEMV with the gather, K %d" % K, flush=True)
+    P, st = _hip.ptr, _hip.stream_of(dev)
+    N, V = 768, 50
+    codes, scale = _q4(randn(N, K, seed=K + 1, std=0.02), dev)
+    embed = randn(V, K, seed=K + 2).to(torch.float16).to(dev)
+    nw = (torch.rand(K, generator=torch.Generator().manual_seed(K + 3)) + 0.5).to(torch.float16).to(dev)
+    for idx in (7, V - 1, V, -3):
+        tok = torch.tensor([idx], dtype=torch.int64, device=dev)
+        y = torch.empty(N, dtype=torch.float16, device=dev)
+        copy = torch.full((K,), 7.0, dtype=torch.float16, device=dev)
+        _hip.call("lemoq_gemv_q_rmsnorm", P(embed), P(tok), V, 1, K, P(nw), 1e-5, P(copy), P(codes), W4, P(scale),
+                  None, 0, N, K, 128, P(y), 1, st)
+        row = embed[idx].clone() if 0 <= idx < V else torch.zeros(K, dtype=torch.float16, device=dev)
+        y_ref = torch.empty_like(y)
+        _hip.call("lemoq_gemv_q_rmsnorm", P(row), None, 0, 1, K, P(nw), 1e-5, None, P(codes), W4, P(scale), None, 0,
+                  N, K, 128, P(y_ref), 1, st)
+        torch.cuda.synchronize()
+        assert torch.equal(copy, row), idx
+        assert torch.equal(y, y_ref), idx
+        if not 0 <= idx < V:
+            assert not y.any()
+
+
 @pytest.mark.parametrize("E,K,F,H,norm", [(64, 8, 1024, 2048, False), (8, 2, 256, 512, True),
                                           (200, 6, 128, 1024, False)])
 @pytest.mark.parametrize("ties", [False, True])
@@ -133,7 +163,7 @@ def test_tiny_fused_shape_w4_matches_oracle(kv, dev):
     ctx = 40
     prompt = torch.randint(0, TINY_FUSED.vocab, (ctx,), generator=torch.Generator().manual_seed(37)).tolist()
     sess = DecodeSession(w, prompt, max_new_tokens=STEPS, kv_cache=kv)
-    assert sess.attn_output_fused and sess.launches_per_step == 6 * TINY_FUSED.layers + 3
+    assert sess.attn_output_fused and sess.launches_per_step == 6 * TINY_FUSED.layers + 2
     sess.prefill(mode="stepped")
     oracle = OracleDecoder(w.to_host(), sess.max_seq, kv=sess.kv_cpu())
     gl = []
@@ -171,7 +201,7 @@ def test_olmoe_shape_w4a16_random_prompt(dev):
     ctx = 192
     prompt = torch.randint(0, OLMOE_1B_7B.vocab, (ctx,), generator=torch.Generator().manual_seed(42)).tolist()
     sess = DecodeSession(w, prompt, max_new_tokens=24)
-    assert sess.attn_output_fused and sess.launches_per_step == 6 * 16 + 3
+    assert sess.attn_output_fused and sess.launches_per_step == 6 * 16 + 2
     sess.prefill(mode="stepped")
     pos0, tok0 = sess.position, sess.next_token_cpu()
     kv0 = sess.kv_cpu()

@@ -125,11 +125,12 @@ def test_router_norm_output_bit_exact(dev):
     assert diff == 0, "%d elements differ from the oracle" % diff
 
 
-@pytest.mark.parametrize("K", [2048, 4096, 1024])
+@pytest.mark.parametrize("K", [2048, 4096, 1024, 3072])
 def test_gemv_q_norm_prologue_bit_exact(K, dev):
-    """lemoq_gemv_q_rmsnorm's per-wave RMSNorm (the 4-bit decode step's input
-    norm), observed through a 4-bit identity weight (code 1 on the diagonal,
-    scale 1), all rows in one launch (M rows)."""
+    """lemoq_gemv_q_rmsnorm's RMSNorm (the 4-bit decode step's input norm; the
+    per-block form at K 2048 / 4096, the per-wave form at 1024 / 3072),
+    observed through a 4-bit identity weight (code 1 on the diagonal, scale 1),
+    all rows in one launch (M rows)."""
     print("case: 4-bit gemv norm prologue rounding K=%d" % K, flush=True)
     rows = 256
     x, w = _rows(rows, K, K + 5)
@@ -139,8 +140,8 @@ def test_gemv_q_norm_prologue_bit_exact(K, dev):
     scale = torch.ones((K, K // 128), dtype=torch.float16)
     pd, sd, wd, xd = packed.to(dev), scale.to(dev), w.to(dev), x.to(dev)
     y = torch.empty((rows, K), dtype=torch.float16, device=dev)
-    _hip.call("lemoq_gemv_q_rmsnorm", _hip.ptr(xd), rows, K, _hip.ptr(wd), EPS, _hip.ptr(pd), 2, _hip.ptr(sd), None,
-              0, K, K, 128, _hip.ptr(y), 1, _hip.stream_of(dev))
+    _hip.call("lemoq_gemv_q_rmsnorm", _hip.ptr(xd), None, 0, rows, K, _hip.ptr(wd), EPS, None, _hip.ptr(pd), 2,
+              _hip.ptr(sd), None, 0, K, K, 128, _hip.ptr(y), 1, _hip.stream_of(dev))
     torch.cuda.synchronize()
     ref = ops.rms_norm(x, w, EPS)
     diff = int((_bits(y) != _bits(ref)).sum())
