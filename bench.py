@@ -97,8 +97,7 @@ def parse_args(argv=None):
     ap.add_argument("--kv-cache", choices=("int8", "fp16"), default="int8",
                     help="--mode step: the decode cache kind (fp16 = the cell with KV-INT8 off)")
     ap.add_argument("--weights", choices=("w8a16", "w4a16"), default="w8a16",
-                    help="--mode step: the cell's weights (w4a16: 4-bit attention and experts, fp16 lm_head; "
-                         "its prompt is fed through the step)")
+                    help="--mode step: the cell's weights (w4a16: 4-bit attention and experts, fp16 lm_head)")
     ap.add_argument("--no-w4a16", action="store_true", help="skip the w4a16-cell step timing")
     ap.add_argument("--summarize-last", type=int, default=0,
                     help="--summarize-step: keep only the last N whole steps (0: all)")
@@ -485,7 +484,7 @@ def time_w4a16(torch, shape, seed: int, dev, ctx: int, steps: int, warmup: int, 
     w4 = OlmoeW8Weights.random(shape, seed=seed, device=dev, bits=4, lm_head="fp16")
     sess = DecodeSession(w4, [1] * ctx, max_new_tokens=max(warmup, 5) + max(steps, 20) + 4, kv_cache="int8")
     sess.capture()
-    sess.prefill(mode="stepped")
+    ttft = measure_prefill(torch, sess)  # batched prefill of the ctx-ones prompt; leaves the session prefilled
     rep = measure_repeats(torch, sess, warmup=max(warmup, 5), timed=max(steps, 20), repeats=3)
     ms = sorted(rep["wall_ms"])[1]
     dev_ms = sorted(rep["event_ms"])[1]
@@ -496,8 +495,9 @@ def time_w4a16(torch, shape, seed: int, dev, ctx: int, steps: int, warmup: int, 
     torch.cuda.empty_cache()
     res = {"ms_per_token_repeats_p50": ms, "device_ms_per_token": dev_ms, "wall_spread": rep["wall_spread"],
            "step_bytes": int(nbytes), "step_hbm_frac_of_measured": nbytes / (dev_ms * 1e-3) / 1e9 / read_bw,
-           "launches_per_step": launches}
-    log("ctx %d w4a16: %.4f ms/token (repeats p50), device %.4f" % (ctx, ms, dev_ms))
+           "launches_per_step": launches, "ttft_ms_p50": ttft["p50"]}
+    log("ctx %d w4a16: %.4f ms/token (repeats p50), device %.4f, TTFT %.3f ms" % (ctx, ms, dev_ms,
+                                                                               ttft["p50"]))
     return res
 
 
@@ -1048,7 +1048,7 @@ def main(argv=None) -> int:
             w = OlmoeW8Weights.random(OLMOE_1B_7B, seed=args.seed, device=dev, bits=4, lm_head="fp16")
         sess = DecodeSession(w, [1] * args.ctx, max_new_tokens=args.warmup + args.steps + 1, kv_cache=args.kv_cache)
         sess.capture()
-        sess.prefill(mode="stepped" if w4 else "batched")
+        sess.prefill()
         sess.replay(args.warmup)
         t0 = time.perf_counter()
         sess.replay(args.steps)
@@ -1203,8 +1203,9 @@ def main(argv=None) -> int:
     if w4a16 is not None:
         w4a16["what"] = ("the reference's w4a16 cell on the same shape: attention and experts as 4-bit symmetric RTN "
                          "codes (g128), router and lm_head fp16, KV-INT8 (OlmoeW8Weights.random(bits=4, "
-                         "lm_head='fp16')); prompt ctx x token 1 fed through the step, timed as the headline; the "
-                         "reference publishes no w4a16 latency (its accuracy gate fails, RESULTS.md:166)")
+                         "lm_head='fp16')); batched prefill of ctx x token 1 (TTFT beside it), timed as the "
+                         "headline; the reference publishes no w4a16 latency (its accuracy gate fails, "
+                         "RESULTS.md:166)")
         line["w4a16"] = w4a16
     line["step_ms_p50"], line["step_ms_p99"] = r1["step_ms_p50"], r1["step_ms_p99"]
     gk = "ms_per_token_graph%d" % MULTI_STEPS

@@ -157,6 +157,25 @@ class OlmoeW8Weights:
             lm_f16=cpu(self.lm_f16),
         )
 
+    def int8_codes(self) -> "OlmoeW8Weights":
+        """The same weights with attention and expert codes as int8 (the batched
+        prefill's operand type): 8-bit weights as they are; 4-bit codes unpacked,
+        an exact re-encoding (code * scale is the same value), so the prefill's
+        fp16(code * scale) weights are the w4a16 cell's separate-arm weights.
+        Scales, norms, router, embedding and lm_head are shared, not copied."""
+        if self.bits == 8:
+            return self
+        from lemoq.quant.pack import unpack_4bit  # noqa: PLC0415
+
+        def layer(L: LayerW8) -> LayerW8:
+            codes = {n: unpack_4bit(getattr(L, n), signed=True).contiguous()
+                     for n in ("qkv_codes", "o_codes", "gu_codes", "dn_codes")}
+            return LayerW8(**{f.name: codes.get(f.name, getattr(L, f.name)) for f in fields(LayerW8)})
+
+        return OlmoeW8Weights(shape=self.shape, embed=self.embed, final_norm=self.final_norm, lm_codes=self.lm_codes,
+                              lm_scale=self.lm_scale, layers=[layer(L) for L in self.layers], bits=8,
+                              lm_f16=self.lm_f16)
+
     def weight_bits(self) -> Any:
         """The byte model's storage of each weight family (``lemoq.bytes.WeightBits``)."""
         from lemoq.bytes import WeightBits  # noqa: PLC0415
@@ -258,8 +277,7 @@ class DecodeSession:
     default; ``lemoq.kernels.fusion_switches``).  The step follows the weights:
     4-bit attention and experts (``weights.bits == 4``, the w4a16 cell) and an
     fp16 lm_head (``weights.lm_f16``) run the step's 4-bit layer and fp16
-    lm_head; their prompt is prefilled through the step (``prefill(mode=
-    "stepped")``), since the batched prefill runs W8 weights.
+    lm_head.
     """
 
     def __init__(
@@ -402,6 +420,7 @@ class DecodeSession:
         self.stream: Any = None
         self._host_pos = 0
         self._seed_token: int | None = None
+        self._prefill_weights: Any = None
         self.reset()
 
     # ------------------------------------------------------------------ state
@@ -537,15 +556,14 @@ class DecodeSession:
         ``mode="stepped"`` feeds the prompt through the captured decode step, one
         replay per position (decode numerics for every prompt token).
         ``kv_f16`` (batched only): a list that receives per layer the fp16 k and v
-        rows the cache bytes were quantised from (see ``prefill_prompt``).  The
-        batched prefill runs W8 weights and the W8 lm_head; other weights raise
-        ``NotImplementedError`` there and prefill with ``mode="stepped"``.
+        rows the cache bytes were quantised from (see ``prefill_prompt``).  4-bit
+        weights run the batched prefill on an int8 re-encoding of their codes
+        (``OlmoeW8Weights.int8_codes``, made once per session and kept: for the
+        OLMoE shape 6.7 GB beside the 4-bit weights), the separate arm's
+        arithmetic; an fp16 lm_head ends it with the fp16 GEMV of the last row.
         """
         if mode not in ("batched", "stepped"):
             raise ValueError("prefill mode must be 'batched' or 'stepped', got %r" % (mode,))
-        if mode == "batched" and (self.weights.bits != 8 or self.weights.lm_f16 is not None):
-            raise NotImplementedError("the batched prefill runs W8 weights and the W8 lm_head; prefill 4-bit "
-                                      "or fp16-lm_head weights with mode='stepped'")
         if self.graph is None:
             self.capture()
         # stream order keeps the reset ahead of the prefill's launches; the
@@ -556,9 +574,11 @@ class DecodeSession:
         elif mode == "batched":
             from lemoq.model.prefill import prefill_prompt  # noqa: PLC0415
 
+            if self._prefill_weights is None:  # 4-bit codes as int8 for the prefill GEMMs, once
+                self._prefill_weights = self.weights.int8_codes()
             self.history[: self.ctx].copy_(self.prompt)
             self.pos.fill_(self.ctx - 1)
-            prefill_prompt(self.weights, self.prompt, self.kv, self.cos_tab, self.sin_tab, self.max_seq,
+            prefill_prompt(self._prefill_weights, self.prompt, self.kv, self.cos_tab, self.sin_tab, self.max_seq,
                            self.logits, step={"token": self.token, "pos": self.pos, "filled": self.filled,
                                               "history": self.history}, kv_f16=kv_f16)
             self._host_pos = self.ctx

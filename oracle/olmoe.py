@@ -313,7 +313,10 @@ def oracle_prefill(weights: Any, tokens: Any, max_seq: int, *, all_logits: bool 
     * the KV-INT8 cache is the bulk quantisation of the fp16 k/v rows
       (``kv_int8.py:127-162``) -> ``oracle.quant.kv_quantize_rows``; with
       ``kv_cache="fp16"`` (KV-INT8 off) the cache holds those fp16 rows;
-    * logits: final norm and the W8 lm_head (separate arm: T > 1 rows reach it).
+    * logits: final norm and the W8 lm_head (separate arm: T > 1 rows reach it), or the
+      fp16 lm_head (``lm_f16``) as an fp16 ``F.linear``;
+    * 4-bit weights (``bits`` 4, the w4a16 cell): the codes unpacked, then the same
+      separate arm (``code * scale`` rounded to fp16).
 
     Returns ``(logits, kv)``: fp16 logits of the last position (``(T, vocab)`` with
     ``all_logits``), and per layer the KV-INT8 cache dict (kc, ks, vc, vs) of ``max_seq``
@@ -324,8 +327,7 @@ def oracle_prefill(weights: Any, tokens: Any, max_seq: int, *, all_logits: bool 
     (logits are then None).
     """
     s, w = weights.shape, weights
-    if int(getattr(weights, "bits", 8)) != 8 or getattr(weights, "lm_f16", None) is not None:
-        raise NotImplementedError("oracle_prefill restates the w8a16 cell's prefill (W8 weights and lm_head)")
+    bits = int(getattr(weights, "bits", 8))  # 4: the w4a16 cell, codes unpacked before the separate arm
     toks = torch.as_tensor(tokens, dtype=torch.int64).reshape(-1)
     T = int(toks.numel())
     NH, D = s.heads, s.head_dim
@@ -340,7 +342,7 @@ def oracle_prefill(weights: Any, tokens: Any, max_seq: int, *, all_logits: bool 
     for L in w.layers:
         r = h
         xn = ops.rms_norm(h, L.ln_in, s.eps)
-        qkv = ops.linear_separate_w8(xn, L.qkv_codes, L.qkv_scale, g)
+        qkv = ops.linear_separate_w8(xn, unpacked_codes(L.qkv_codes, bits), L.qkv_scale, g)
         q = ops.rms_norm(qkv[:, :HD], L.q_norm, s.eps).reshape(T, NH, D)
         k = ops.rms_norm(qkv[:, HD:2 * HD], L.k_norm, s.eps).reshape(T, NH, D)
         v = qkv[:, 2 * HD:].reshape(T, NH, D)
@@ -370,12 +372,15 @@ def oracle_prefill(weights: Any, tokens: Any, max_seq: int, *, all_logits: bool 
         if kv_layers is not None and len(kv_out) >= kv_layers:
             return None, kv_out
         attn = ops.causal_attention(q, k, v).to(torch.float16).reshape(T, HD)
-        h = r + ops.linear_separate_w8(attn, L.o_codes, L.o_scale, g)
+        h = r + ops.linear_separate_w8(attn, unpacked_codes(L.o_codes, bits), L.o_scale, g)
         r = h
         xn = ops.rms_norm(h, L.ln_post, s.eps)
         top_w, top_i = ops.route_logits(ops.linear_f16(xn, L.router), s.top_k, s.norm_topk_prob)
-        h = r + ops.moe_prefill_w8(xn, L.gu_codes, L.gu_scale, L.dn_codes, L.dn_scale, g, top_i,
-                                   top_w.to(torch.float16))
+        h = r + ops.moe_prefill_w8(xn, unpacked_codes(L.gu_codes, bits), L.gu_scale,
+                                   unpacked_codes(L.dn_codes, bits), L.dn_scale, g, top_i, top_w.to(torch.float16))
     rows = h if all_logits else h[-1:]
-    logits = ops.linear_separate_w8(ops.rms_norm(rows, w.final_norm, s.eps), w.lm_codes, w.lm_scale, g)
+    hn = ops.rms_norm(rows, w.final_norm, s.eps)
+    lm_f16 = getattr(w, "lm_f16", None)  # fp16 lm_head: F.linear in fp16
+    logits = ops.linear_f16(hn, lm_f16) if lm_f16 is not None else ops.linear_separate_w8(hn, w.lm_codes,
+                                                                                            w.lm_scale, g)
     return (logits if all_logits else logits[0]), kv_out

@@ -137,8 +137,6 @@ def test_tiny_model_matches_oracle(bits, lm_head, kv, dev):
     sess = DecodeSession(w, prompt, max_new_tokens=STEPS, kv_cache=kv)
     assert not sess.attn_output_fused  # hidden 512: merge, o_proj (+ residual), router as three launches
     assert sess.launches_per_step == 7 * TINY.layers + 2 + (bits == 4)
-    with pytest.raises(NotImplementedError):
-        sess.prefill()  # the batched prefill runs W8 weights and the W8 lm_head
     seed = sess.prefill(mode="stepped")
     oracle = OracleDecoder(w.to_host(), sess.max_seq, kv=sess.kv_cpu())
     gl = []
@@ -173,6 +171,50 @@ def test_tiny_fused_shape_w4_matches_oracle(kv, dev):
     toks = [int(t) for t in sess.history[ctx: ctx + STEPS + 1].tolist()]
     rl = [oracle.step(toks[i], ctx + i) for i in range(STEPS)]
     _check_steps(toks, gl, rl)
+
+
+@pytest.mark.parametrize("shape", ["tiny", "tiny_fused"])
+def test_batched_prefill_of_4bit_weights_matches_oracle(shape, dev):
+    """The batched prefill of the w4a16 cell (the prefill GEMMs on the int8
+    re-encoding of the 4-bit codes, the fp16 lm_head for the last row) against
+    the oracle's prefill of the same weights: last logits (KL < 0.01, max |diff|
+    within 2%), the seed token (near-ties aside), every layer's KV-INT8 bytes
+    (kv_rows_vs_oracle); then 8 decode steps against the oracle from the GPU's
+    cache."""
+    from helpers import kv_rows_vs_oracle
+    from oracle.olmoe import oracle_prefill
+    from test_gpu_decode import TINY_FUSED
+
+    print("case: batched prefill, 4-bit weights, %s" % shape, flush=True)
+    sh = TINY if shape == "tiny" else TINY_FUSED
+    w = _weights(sh, 4, "fp16", 38, dev)
+    T, steps = 48, 8
+    prompt = torch.randint(0, sh.vocab, (T,), generator=torch.Generator().manual_seed(39)).tolist()
+    sess = DecodeSession(w, prompt, max_new_tokens=steps)
+    rows = []
+    seed_tok = sess.prefill(kv_f16=rows)
+    logits, kv = sess.logits_cpu(), sess.kv_cpu()
+    hw = w.to_host()
+    ref_rows = []
+    ref, ref_kv = oracle_prefill(hw, prompt, sess.max_seq, kv_f16=ref_rows)
+    r64, g64 = ref.double(), logits.double()
+    p, q = torch.log_softmax(r64, -1), torch.log_softmax(g64, -1)
+    kl, diff = float((p.exp() * (p - q)).sum()), float((r64 - g64).abs().max())
+    print("prefill: KL %.2e, max|diff| %.3e" % (kl, diff))
+    assert kl < 1e-2 and diff <= 2e-2 * float(r64.abs().max())
+    if seed_tok != int(torch.argmax(r64)):
+        top = torch.topk(r64, 2).values
+        assert float(top[0] - top[1]) <= 2 * diff
+    for li in range(sh.layers):
+        kv_rows_vs_oracle("w4 prefill layer %d" % li, kv[li], rows[li], ref_kv[li], ref_rows[li], T,
+                          rows_close=li == 0)
+    gl = []
+    for _ in range(steps):
+        sess.replay(1)
+        gl.append(sess.logits_cpu())
+    toks = [int(t) for t in sess.history[T: T + steps + 1].tolist()]
+    oracle = OracleDecoder(hw, sess.max_seq, kv=kv)
+    _check_steps(toks, gl, [oracle.step(toks[i], T + i) for i in range(steps)])
 
 
 def test_tiny_model_prompt_steps_match_oracle_run(dev):

@@ -256,3 +256,23 @@ def test_prefill_fp16_cache_holds_the_rows_of_the_int8_cache():
         top = float(a.abs().max())
         assert float((a - b).abs().max()) <= 5e-3 * top, name
         assert float((a[:, 1:] - b[:, :-1]).abs().max()) > 0.5 * top, name
+
+
+@pytest.mark.parametrize("seed", [5, 6])
+def test_oracle_prefill_w4_fp16_lm_head_matches_hf_olmoe(seed):
+    """The w4a16 cell's prefill (4-bit codes unpacked before the separate arm, the
+    fp16 lm_head as an fp16 F.linear) against HF OlmoeForCausalLM in fp64 loaded
+    with the same dequantised weights and fp16 lm_head, with the prefill gate; its
+    KV-INT8 rows match the stepped 4-bit decoder's at the same slots."""
+    hw = random_host_weights(SHAPE, seed=seed, bits=4, lm_head="fp16")
+    toks = torch.randint(0, SHAPE.vocab, (N_POS,), generator=torch.Generator().manual_seed(seed + 400))
+    with torch.no_grad():
+        ref = _hf_model(hw)(toks[None]).logits[0]
+    ok, (kl, rel) = _passes(ref, hw, toks)
+    assert ok, "median KL %.3e, median rel %.4f" % (kl, rel)
+    _, kv = oracle_prefill(hw, toks, N_POS + 4)
+    dec = OracleDecoder(hw, N_POS + 4)
+    for p, t in enumerate(toks.tolist()):
+        dec.step(int(t), p)
+    diff = (kv[0]["kc"][:, :N_POS].int() - dec.kv[0]["kc"][:, :N_POS].int()).abs().max()
+    assert int(diff) <= 1  # layer 0: the same rows up to the separate / fused rounding (one code)
