@@ -575,15 +575,16 @@ int lemoq_argmax_advance(const uint16_t* logits, int64_t n, int64_t* token,
  * (benchmarks/cudagraph.py:680-737) for the canonical w8a16 + W8 lm_head +
  * KV-INT8 cell, or, with kv_fp16 set, the same cell with KV-INT8 off (the
  * fp16 StaticCache written by kv_direct_write and read by the fp16 split-KV
- * attention, src/lemoq/kernels/attn_decode.py:930-948,999-1008).  All buffers are
- * caller-owned; see LemoqOlmoeStep.
+ * attention, src/lemoq/kernels/attn_decode.py:930-948,999-1008), or, with
+ * weight_bits 4 and lm_f16, the w4a16 cell (benchmarks/runner.py:393-412,
+ * 451-482).  All buffers are caller-owned; see LemoqOlmoeStep.
  * ------------------------------------------------------------------------- */
 typedef struct LemoqOlmoeLayer {
   const uint16_t* ln_in;     /* (H)                */
   const uint16_t* ln_post;   /* (H)                */
   const uint16_t* q_norm;    /* (heads*D)          */
   const uint16_t* k_norm;    /* (heads*D)          */
-  const int8_t* qkv_codes;   /* (3*heads*D, H)     */
+  const int8_t* qkv_codes;   /* (3*heads*D, H); the code arrays are packed 4-bit at weight_bits 4 */
   const uint16_t* qkv_scale; /* (3*heads*D, H/g)   */
   const int8_t* o_codes;     /* (H, heads*D)       */
   const uint16_t* o_scale;   /* (H, heads*D/g)     */
