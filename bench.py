@@ -1388,13 +1388,14 @@ STEP_TAIL_KERNELS = [("lm_head (+ final norm, argmax partials)", "gemv_w8_kernel
 
 # The 4-bit step (--weights w4a16) at the OLMoE shape by position: per layer the 6
 # launches below (layer 0's q|k|v GEMV gathers the embedding row), then the fp16
-# lm_head and the greedy pick (told apart by their place in the step, as the
-# lm_head runs the router's kernel).
+# lm_head with the argmax partials and the greedy pick over them.  A trace of it
+# is recognised by its fp16 lm_head kernel.
 STEP_W4_LAYER = ["qkv (4-bit, + input RMSNorm)", "attention split (+ q/k norm, RoPE, cache write)",
                  "merge + o_proj (4-bit)", "residual + norm + router",
                  "gate/up (4-bit, + routing)", "down (4-bit, + residual)"]
-STEP_W4_HEAD = ["lm_head fp16 (+ final norm)", "argmax + advance"]
-STEP_W4_END = "argmax_advance_kernel<false"  # over the fp16 logits (<false, true>: 16-byte loads)
+STEP_W4_HEAD = ["lm_head fp16 (+ final norm, argmax partials)", "argmax + advance"]
+STEP_W4_MARK = "lm_head_f16_argmax_kernel<"
+STEP_W4_END = "argmax_advance_kernel<true"  # over the partials
 
 
 def _w4_roles() -> list:
@@ -1410,11 +1411,11 @@ def summarize_step(trace_csv: str, last: int = 0) -> str:
     and the rest of the span is the time between kernels (launch and dispatch
     gaps inside the graph).  ``last`` keeps only the last N whole steps (the
     4-bit step's prompt is fed through the step itself).  A trace of the 4-bit
-    step (``--weights w4a16``) is recognised by its argmax kernel."""
+    step (``--weights w4a16``) is recognised by its fp16 lm_head kernel."""
     import csv as _csv
 
     all_rows = list(_csv.DictReader(open(trace_csv)))
-    if any(STEP_W4_END in _short_kernel(r["Kernel_Name"]) for r in all_rows):
+    if any(STEP_W4_MARK in _short_kernel(r["Kernel_Name"]) for r in all_rows):
         return _summarize_step_w4(all_rows, last, trace_csv)
     names = [k for _, k in STEP_LAYER_KERNELS + STEP_TAIL_KERNELS]
     rows = sorted((r for r in all_rows if any(n in _short_kernel(r["Kernel_Name"]) for n in names)),
@@ -1452,10 +1453,12 @@ def _summarize_step_w4(all_rows: list, last: int, trace_csv: str) -> str:
     roles = _w4_roles()
     per_step = len(roles)
     # a chunk may start with other dispatches before the step (the first one after
-    # the session's set-up): keep its last per_step launches when they open with
-    # the q|k|v GEMV (layer 0 gathers the embedding row inside it)
+    # the session's set-up, or a batched prefill): keep its last per_step launches
+    # when they open with the q|k|v GEMV (layer 0 gathers the embedding row inside
+    # it) and close with the fp16 lm_head and the pick
     steps = [st[-per_step:] for st in steps
-             if len(st) >= per_step and "gemv_q_kernel<" in _short_kernel(st[-per_step]["Kernel_Name"])]
+             if len(st) >= per_step and "gemv_q_kernel<" in _short_kernel(st[-per_step]["Kernel_Name"])
+             and STEP_W4_MARK in _short_kernel(st[-2]["Kernel_Name"])]
     if last > 0:
         steps = steps[-last:]
     if not steps:

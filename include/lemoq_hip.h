@@ -245,6 +245,20 @@ int lemoq_lm_head_argmax_w8_dq(const uint16_t* x, const uint16_t* norm_w, float 
                                int32_t* part_idx, int64_t part_len, int64_t* token, int64_t* pos,
                                int32_t* filled, const int64_t* prompt, int64_t prompt_len,
                                int64_t* history, int64_t history_len, void* stream);
+/* The same two launches over an fp16 lm_head (the w4a16 cell keeps lm_head
+ * in fp16, benchmarks/runner.py:399-401 and src/lemoq/quant/linear.py:646-647,
+ * so its logits are a plain F.linear; the greedy pick of
+ * benchmarks/cudagraph.py:759-762).  weight (N, K)
+ * fp16 row-major; logits = fp16(rmsnorm(x, norm_w) . W[n]) with fp32
+ * accumulation, bit-identical to lemoq_router_logits over the same rows;
+ * part_len >= lemoq_lm_head_argmax_parts(N).  K % 16 == 0, K <= 8192;
+ * 16-byte aligned x, weight and norm_w (else LEMOQ_ERR_ALIGN). */
+int lemoq_lm_head_argmax_f16(const uint16_t* x, const uint16_t* norm_w, float eps,
+                             const uint16_t* weight, int64_t N, int64_t K, uint16_t* logits,
+                             float* part_val, int32_t* part_idx, int64_t part_len, int64_t* token,
+                             int64_t* pos, int32_t* filled, const int64_t* prompt,
+                             int64_t prompt_len, int64_t* history, int64_t history_len,
+                             void* stream);
 /* Number of argmax partials lemoq_lm_head_argmax_w8 writes for N rows. */
 int64_t lemoq_lm_head_argmax_parts(int64_t N);
 

@@ -43,6 +43,35 @@ struct GemvArgs {
 constexpr int kArgmaxPlain = 0;
 constexpr int kArgmaxPartials = 1;
 constexpr int kArgmaxPartialsDq = 2;  // as kArgmaxPartials, weights rounded to fp16 before the dot
+
+// Block epilogue of the argmax partials: each of the 4 waves brings its best
+// (fp16-rounded value, lowest row; -inf / 0x7fffffff when it has no row) and
+// thread 0 stores the block's best at blockIdx.x (ties -> lowest row; a block
+// without a valid row stores -inf / -1).  Every thread of the block calls it.
+__device__ __forceinline__ void block_argmax_partial(float bv, int bi, int wave, int lane, float* am_val,
+                                                     int32_t* am_idx) {
+  __shared__ float sv[4];
+  __shared__ int si[4];
+  if (lane == 0) {
+    sv[wave] = bv;
+    si[wave] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float v = sv[0];
+    int i = si[0];
+#pragma unroll
+    for (int w = 1; w < 4; ++w)
+      if (sv[w] > v || (sv[w] == v && si[w] < i)) {
+        v = sv[w];
+        i = si[w];
+      }
+    const bool none = i == 0x7fffffff;
+    am_val[blockIdx.x] = none ? -INFINITY : v;
+    am_idx[blockIdx.x] = none ? -1 : i;
+  }
+}
+
 template <int KCH, int R, int MODE, bool EXACT>
 __global__ __launch_bounds__(256) void gemv_w8_kernel(const GemvArgs a) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -197,26 +226,7 @@ __global__ __launch_bounds__(256) void gemv_w8_kernel(const GemvArgs a) {
         }
       }
     }
-    __shared__ float sv[4];
-    __shared__ int si[4];
-    if (lane == 0) {
-      sv[wave] = bv;
-      si[wave] = bi;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      float v = sv[0];
-      int i = si[0];
-#pragma unroll
-      for (int w = 1; w < 4; ++w)
-        if (sv[w] > v || (sv[w] == v && si[w] < i)) {
-          v = sv[w];
-          i = si[w];
-        }
-      const bool none = i == 0x7fffffff;  // no valid row in this block
-      a.am_val[blockIdx.x] = none ? -INFINITY : v;
-      a.am_idx[blockIdx.x] = none ? -1 : i;
-    }
+    block_argmax_partial(bv, bi, wave, lane, a.am_val, a.am_idx);
   }
 }
 
@@ -584,6 +594,59 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
   if (lane == 0 && e < E) logits_out[e] = f2h(acc);
 }
 
+// fp16 lm_head of one token with the argmax partials: wave w of block b owns
+// the 2 rows (4b + w)*2, +1, normalises x once for both (the router's
+// x_rmsnorm), and each row's logit is fp16(xn . W[n]) with the router
+// kernel's lane order and butterfly, so the logits equal
+// router_logits_kernel's bit for bit.  Each block stores its best (value,
+// lowest row) for argmax_advance_kernel<true>; the row count per block is
+// the W8 lm_head's, so lemoq_lm_head_argmax_parts(N) sizes both.
+template <int KCH, bool EXACT>
+__global__ __launch_bounds__(256) void lm_head_f16_argmax_kernel(
+    const uint16_t* __restrict__ h, const uint16_t* __restrict__ norm_w, float eps, int H,
+    const uint16_t* __restrict__ w, int64_t N, uint16_t* __restrict__ logits, float* __restrict__ am_val,
+    int32_t* __restrict__ am_idx) {
+  constexpr int R = 2;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t row0 = ((int64_t)blockIdx.x * 4 + wave) * R;
+  XRaw<KCH> xv, nw, wr[R];
+  x_issue<KCH, EXACT>(xv, h, H, true, lane);
+  if (norm_w) x_issue<KCH, EXACT>(nw, norm_w, H, true, lane);
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int64_t n = row0 + r < N ? row0 + r : N - 1;
+    x_issue<KCH, EXACT>(wr[r], w + n * H, H, true, lane);
+  }
+  LEMOQ_LOADS_ISSUED();
+  if (norm_w) x_rmsnorm<KCH>(xv, nw, H, eps);
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < KCH; ++j)
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const uint32_t ww[4] = {wr[r].v[j][q].x, wr[r].v[j][q].y, wr[r].v[j][q].z, wr[r].v[j][q].w};
+        const uint32_t xw[4] = {xv.v[j][q].x, xv.v[j][q].y, xv.v[j][q].z, xv.v[j][q].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc = __builtin_amdgcn_fdot2(as_h2(ww[i]), as_h2(xw[i]), acc, false);
+      }
+    const uint16_t o = f2h(wave_sum(acc));
+    const int64_t n = row0 + r;
+    if (n < N) {
+      if (lane == r) logits[n] = o;
+      const float v = h2f(o);
+      if (v > bv) {  // rows ascend: strict > keeps the lowest row on ties
+        bv = v;
+        bi = (int)n;
+      }
+    }
+  }
+  block_argmax_partial(bv, bi, wave, lane, am_val, am_idx);
+}
+
 int launch_router_logits(hipStream_t st, const uint16_t* h, const uint16_t* norm_w, float eps,
                          int64_t H, const uint16_t* rw, int64_t E, uint16_t* xn_out,
                          uint16_t* logits) {
@@ -783,6 +846,47 @@ extern "C" int lemoq_lm_head_argmax_w8_dq(const uint16_t* x, const uint16_t* nor
   return lm_head_argmax<kArgmaxPartialsDq>(x, norm_w, eps, codes, scale, N, K, group, logits, part_val,
                                            part_idx, part_len, token, pos, filled, prompt, prompt_len,
                                            history, history_len, stream);
+}
+
+extern "C" int lemoq_lm_head_argmax_f16(const uint16_t* x, const uint16_t* norm_w, float eps,
+                                        const uint16_t* weight, int64_t N, int64_t K, uint16_t* logits,
+                                        float* part_val, int32_t* part_idx, int64_t part_len,
+                                        int64_t* token, int64_t* pos, int32_t* filled,
+                                        const int64_t* prompt, int64_t prompt_len, int64_t* history,
+                                        int64_t history_len, void* stream) {
+  if (!x || !weight || !logits || !part_val || !part_idx || !token || !pos || !filled)
+    return LEMOQ_ERR_NULL;
+  if (K <= 0 || K > 8192 || K % 16 != 0) return LEMOQ_ERR_UNSUPPORTED;
+  if (N <= 0 || N > 0x7ffffffeLL) return LEMOQ_ERR_SHAPE;
+  const int64_t blocks = lemoq_lm_head_argmax_parts(N);
+  if (part_len < blocks) return LEMOQ_ERR_SHAPE;
+  if (!lemoq_aligned16(x) || !lemoq_aligned16(weight) || (norm_w && !lemoq_aligned16(norm_w)))
+    return LEMOQ_ERR_ALIGN;
+  hipStream_t st = lemoq_stream(stream);
+  const int kch = kch_pow2(K);
+  const bool exact = K == 1024 * kch;
+#define LEMOQ_LMF_CASE(KK)                                                                          \
+  case KK:                                                                                          \
+    if (exact)                                                                                      \
+      hipLaunchKernelGGL((lm_head_f16_argmax_kernel<KK, true>), dim3((unsigned)blocks), dim3(256), 0, st, x, \
+                         norm_w, eps, (int)K, weight, N, logits, part_val, part_idx);                \
+    else                                                                                            \
+      hipLaunchKernelGGL((lm_head_f16_argmax_kernel<KK, false>), dim3((unsigned)blocks), dim3(256), 0, st, x, \
+                         norm_w, eps, (int)K, weight, N, logits, part_val, part_idx);                \
+    break;
+  switch (kch) {
+    LEMOQ_LMF_CASE(1)
+    LEMOQ_LMF_CASE(2)
+    LEMOQ_LMF_CASE(4)
+    LEMOQ_LMF_CASE(8)
+    default: return LEMOQ_ERR_UNSUPPORTED;
+  }
+#undef LEMOQ_LMF_CASE
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  hipLaunchKernelGGL((argmax_advance_kernel<true>), dim3(1), dim3(1024), 0, st, nullptr, part_val, part_idx,
+                     blocks, token, pos, filled, prompt, prompt_len, history, history_len);
+  LEMOQ_CHECK_LAUNCH();
 }
 
 extern "C" int64_t lemoq_lm_head_argmax_parts(int64_t N) {

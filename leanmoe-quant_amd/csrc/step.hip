@@ -28,7 +28,8 @@
 // router logits), the routed 4-bit gate/up and the 4-bit down with the
 // residual add; layer 0 first gathers the embedding row.  An fp16 lm_head (lm_f16, the reference's
 // lm_head in every cell but w8a16 with its lm_head switch on) ends the step
-// with the final norm + fp16 GEMV and the greedy selection over the logits.
+// with the final norm + fp16 GEMV writing the argmax partials and the greedy
+// selection over them, the W8 head's two launches.
 //
 // Every shape and buffer rule of every launch is checked before the first
 // launch is enqueued, so a rejected step leaves the cache and buffers as they
@@ -76,8 +77,8 @@ int validate(const LemoqOlmoeStep* p, AttnPath* path) {
       !p->part_l || !p->part_acc || !p->top_w || !p->top_i || !p->act || !p->logits ||
       !p->router_logits)
     return LEMOQ_ERR_NULL;
-  // the W8 lm_head and its argmax partials (not read with an fp16 lm_head)
-  if (!p->lm_f16 && (!p->lm_codes || !p->lm_scale || !p->am_val || !p->am_idx)) return LEMOQ_ERR_NULL;
+  // the argmax partials (either lm_head) and the W8 lm_head (not read with an fp16 lm_head)
+  if (!p->am_val || !p->am_idx || (!p->lm_f16 && (!p->lm_codes || !p->lm_scale))) return LEMOQ_ERR_NULL;
   const int64_t H = p->hidden, D = p->head_dim, HD = p->heads * p->head_dim, E = p->num_experts;
   const int64_t F = p->ffn, K = p->top_k, g = p->group, S = p->max_seq, ns = p->num_splits;
   if (H <= 0 || p->heads <= 0 || D <= 0 || p->num_layers <= 0 || S <= 0 || ns <= 0 ||
@@ -90,12 +91,12 @@ int validate(const LemoqOlmoeStep* p, AttnPath* path) {
   // qkv GEMV (K = H), o_proj (K = HD) on the unfused path
   LEMOQ_TRY(check_gemv(3 * HD, H, g));
   if (p->vocab > 0x7ffffffeLL) return LEMOQ_ERR_SHAPE;
-  if (p->lm_f16) {  // final norm + fp16 lm_head (lemoq_router_logits), then the greedy pick
-    if (p->vocab > 65536 || H > 8192 || H % 16 != 0) return LEMOQ_ERR_UNSUPPORTED;
-    if (!a16(p->lm_f16) || !a16(p->h) || !a16(p->final_norm) || !a16(p->xn)) return LEMOQ_ERR_ALIGN;
+  if (p->am_len < lemoq_lm_head_argmax_parts(p->vocab)) return LEMOQ_ERR_SHAPE;
+  if (p->lm_f16) {  // final norm + fp16 lm_head with the argmax partials (lemoq_lm_head_argmax_f16)
+    if (H > 8192 || H % 16 != 0) return LEMOQ_ERR_UNSUPPORTED;
+    if (!a16(p->lm_f16) || !a16(p->h) || !a16(p->final_norm)) return LEMOQ_ERR_ALIGN;
   } else {
     LEMOQ_TRY(check_gemv(p->vocab, H, g));
-    if (p->am_len < lemoq_lm_head_argmax_parts(p->vocab)) return LEMOQ_ERR_SHAPE;
     if (!a16(p->lm_codes)) return LEMOQ_ERR_ALIGN;
   }
   if (w4) {
@@ -169,12 +170,10 @@ int enqueue_attention(const LemoqOlmoeStep* p, const LemoqOlmoeLayer& w, void* s
 // Final norm + lm_head and the greedy selection / step advance.
 int enqueue_head(const LemoqOlmoeStep* p, void* stream) {
   const int64_t H = p->hidden;
-  if (p->lm_f16) {
-    LEMOQ_TRY(lemoq_router_logits(p->h, p->final_norm, p->eps, H, p->lm_f16, p->vocab, p->xn, p->logits,
-                                  stream));
-    return lemoq_argmax_advance(p->logits, p->vocab, p->token, p->pos, p->filled, p->prompt, p->prompt_len,
-                                p->history, p->history_len, stream);
-  }
+  if (p->lm_f16)
+    return lemoq_lm_head_argmax_f16(p->h, p->final_norm, p->eps, p->lm_f16, p->vocab, H, p->logits, p->am_val,
+                                    p->am_idx, p->am_len, p->token, p->pos, p->filled, p->prompt, p->prompt_len,
+                                    p->history, p->history_len, stream);
   return lemoq_lm_head_argmax_w8(p->h, p->final_norm, p->eps, p->lm_codes, p->lm_scale, p->vocab, H,
                                  p->group, p->logits, p->am_val, p->am_idx, p->am_len, p->token, p->pos,
                                  p->filled, p->prompt, p->prompt_len, p->history, p->history_len, stream);

@@ -184,6 +184,10 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         _I,
         [_P, _P, _F, _P, _P, _I64, _I64, _I64, _P, _P, _P, _I64, _P, _P, _P, _P, _I64, _P, _I64, _P],
     ),
+    "lemoq_lm_head_argmax_f16": (
+        _I,
+        [_P, _P, _F, _P, _I64, _I64, _P, _P, _P, _I64, _P, _P, _P, _P, _I64, _P, _I64, _P],
+    ),
     "lemoq_lm_head_argmax_parts": (_I64, [_I64]),
     "lemoq_router_logits": (_I, [_P, _P, _F, _I64, _P, _I64, _P, _P, _P]),
     "lemoq_attn_split_fused_i8": (

@@ -169,18 +169,16 @@ def prefill_prompt(weights: Any, tokens: Any, kv: list, cos_tab: Any, sin_tab: A
                 "pos": torch.full((1,), T - 1, dtype=torch.int64, device=dev),
                 "filled": torch.zeros((1,), dtype=torch.int32, device=dev),
                 "history": torch.zeros((T + 1,), dtype=torch.int64, device=dev)}
-    lm_f16 = getattr(weights, "lm_f16", None)
-    if lm_f16 is not None:
-        # fp16 lm_head (F.linear in fp16 on the normed last row), then the greedy pick
-        xl = torch.empty((H,), dtype=torch.float16, device=dev)
-        _hip.call("lemoq_router_logits", P(h[T - 1:]), P(weights.final_norm), float(s.eps), H, P(lm_f16), s.vocab,
-                  P(xl), P(logits), st)
-        _hip.call("lemoq_argmax_advance", P(logits), s.vocab, P(step["token"]), P(step["pos"]), P(step["filled"]),
-                  P(tokens), T, P(step["history"]), int(step["history"].numel()), st)
-        return
     parts = int(lib.lemoq_lm_head_argmax_parts(s.vocab))
     part_val = torch.empty((parts,), dtype=torch.float32, device=dev)
     part_idx = torch.empty((parts,), dtype=torch.int32, device=dev)
+    lm_f16 = getattr(weights, "lm_f16", None)
+    if lm_f16 is not None:
+        # fp16 lm_head (F.linear in fp16 on the normed last row), then the greedy pick
+        _hip.call("lemoq_lm_head_argmax_f16", P(h[T - 1:]), P(weights.final_norm), float(s.eps), P(lm_f16), s.vocab,
+                  H, P(logits), P(part_val), P(part_idx), parts, P(step["token"]), P(step["pos"]), P(step["filled"]),
+                  P(tokens), T, P(step["history"]), int(step["history"].numel()), st)
+        return
     _hip.call("lemoq_lm_head_argmax_w8_dq", P(h[T - 1:]), P(weights.final_norm), float(s.eps), P(weights.lm_codes),
               P(weights.lm_scale), s.vocab, H, g, P(logits), P(part_val), P(part_idx), parts, P(step["token"]),
               P(step["pos"]), P(step["filled"]), P(tokens), T, P(step["history"]), int(step["history"].numel()), st)

@@ -127,14 +127,14 @@ def test_summarize_step_timeline(tmp_path):
 
 def test_summarize_step_timeline_of_the_4bit_step(tmp_path):
     """The 4-bit step (bench.py --mode step --weights w4a16): 98 launches told
-    apart by position (the lm_head runs the router's kernel); the prompt's steps
+    apart by position, the trace recognised by the fp16 lm_head kernel; the prompt's steps
     come first and --summarize-last keeps the decode steps.  Synthetic trace: 3 prompt steps (1 us kernels) and 2 decode
     steps (role i lasts i + 1 us), 1 us gaps."""
     path = tmp_path / "trace_w4.csv"
     layer = ["gemv_q_kernel<2, 1, 2, false, true>", "attn_split_fused_i8_kernel<128, 4, 3>",
              "merge_oproj_q4_kernel<16>", "router_resid_kernel<2, 4>",
              "moe_gate_up_q4_kernel<1, 2, 16, 1>", "moe_down_q4_kernel<1, 4, 8>"]
-    step = layer * 16 + ["router_logits_kernel<2, true>", "argmax_advance_kernel<false, true>"]
+    step = layer * 16 + ["lm_head_f16_argmax_kernel<2, true>", "argmax_advance_kernel<true, false>"]
     rows, t = [("void at::native::fill_kernel(args)", 0, 500)], 1000
     for s in range(5):
         for i, n in enumerate(step):
@@ -151,5 +151,6 @@ def test_summarize_step_timeline_of_the_4bit_step(tmp_path):
     assert "| qkv (4-bit, + input RMSNorm) | 16 | 1.00 |" in out
     assert "| merge + o_proj (4-bit) | 16 | 3.00 |" in out
     assert "| residual + norm + router | 16 | 4.00 |" in out
-    assert "| lm_head fp16 (+ final norm) | 1 | 7.00 |" in out and "| argmax + advance | 1 | 8.00 |" in out
+    assert "| lm_head fp16 (+ final norm, argmax partials) | 1 | 7.00 |" in out
+    assert "| argmax + advance | 1 | 8.00 |" in out
     assert bench.summarize_step(str(path)).startswith("5 whole steps of 98 launches")

@@ -262,8 +262,9 @@ def test_decode_step_rejects_before_any_launch():
     assert step(weight_bits=4, attn=(1 << 30) + 8) == -4    # merge output / o_proj input alignment
     assert step(weight_bits=4, num_experts=300) == -3       # routed 4-bit gate/up: > 256 experts
     big = 1 << 30
-    assert step(lm_f16=big, vocab=70000) == -3              # fp16 lm_head: vocab <= 65536 rows
+    assert step(lm_f16=big, am_len=parts - 1) == -2         # the fp16 lm_head writes the same partials
+    assert step(lm_f16=big, am_val=None) == -1
     assert step(lm_f16=big + 8) == -4                       # fp16 lm_head alignment
-    # with an fp16 lm_head the W8 lm_head and its partials may be absent (a later rule rejects)
-    assert step(lm_f16=big, lm_codes=None, am_val=None, am_idx=None, am_len=0, top_k=65) == -2
+    # with an fp16 lm_head the W8 lm_head may be absent (a later rule rejects)
+    assert step(lm_f16=big, lm_codes=None, lm_scale=None, top_k=65) == -2
     assert step(lm_codes=None) == -1 and step(am_idx=None) == -1

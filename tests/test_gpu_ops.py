@@ -884,6 +884,57 @@ def test_lm_head_argmax_dequant_first(N, dev):
     assert int(hist[5].item()) == int(tok.item())
 
 
+@pytest.mark.parametrize("N,H", [(50304, 2048), (1000, 2048), (37, 2048), (203, 1040)])
+def test_lm_head_argmax_f16(N, H, dev):
+    """lemoq_lm_head_argmax_f16 (the fp16 lm_head of the w4a16 cell): logits
+    bit-identical to lemoq_router_logits over the same rows (same lane order and
+    butterfly), within one fp16 step of the oracle's fp64 F.linear of the normed
+    row, the token the lowest-index argmax of those logits (a tie planted across
+    blocks: two identical winning rows), and the step advanced as
+    lemoq_argmax_advance does (prompt feed, history write)."""
+    from lemoq import _hip
+
+    w = randn(N, H, seed=N + 11, std=0.02)
+    x = randn(H, seed=N + 12).to(torch.float16)
+    nw = (torch.rand(H, generator=torch.Generator().manual_seed(N + 13)) + 0.5).to(torch.float16)
+    xn = ops.rms_norm(x, nw, 1e-5)
+    a, b = 3, N - 2  # different blocks (8 rows each) at every N here
+    w[a] = w[b] = 0.05 * torch.sign(xn.float())
+    w16 = w.to(torch.float16)
+    xd, nd, wd = x.to(dev), nw.to(dev), w16.to(dev)
+    parts = int(_hip.load().lemoq_lm_head_argmax_parts(N))
+    pv = torch.empty(parts, dtype=torch.float32, device=dev)
+    pi = torch.empty(parts, dtype=torch.int32, device=dev)
+    logits = torch.empty(N, dtype=torch.float16, device=dev)
+    ref_logits = torch.empty(N, dtype=torch.float16, device=dev)
+    tok = torch.zeros(1, dtype=torch.int64, device=dev)
+    fill = torch.zeros(1, dtype=torch.int32, device=dev)
+    hist = torch.full((8,), -5, dtype=torch.int64, device=dev)
+    prompt = torch.arange(100, 105, dtype=torch.int64, device=dev)
+    st = _hip.stream_of(dev)
+    toks = []
+    for p0 in (2, 4):  # inside the prompt (fed), then past it (argmax)
+        pos = torch.full((1,), p0, dtype=torch.int64, device=dev)
+        _hip.call("lemoq_lm_head_argmax_f16", _hip.ptr(xd), _hip.ptr(nd), 1e-5, _hip.ptr(wd), N, H, _hip.ptr(logits),
+                  _hip.ptr(pv), _hip.ptr(pi), parts, _hip.ptr(tok), _hip.ptr(pos), _hip.ptr(fill), _hip.ptr(prompt), 5,
+                  _hip.ptr(hist), 8, st)
+        torch.cuda.synchronize()
+        toks.append(int(tok.item()))
+        assert int(pos.item()) == p0 + 1 and int(fill.item()) == p0 + 2
+        assert int(hist[p0 + 1].item()) == toks[-1]
+    _hip.call("lemoq_router_logits", _hip.ptr(xd), _hip.ptr(nd), 1e-5, H, _hip.ptr(wd), N, None,
+              _hip.ptr(ref_logits), st)
+    torch.cuda.synchronize()
+    lg = logits.cpu()
+    assert torch.equal(lg.view(torch.int16), ref_logits.cpu().view(torch.int16)), "not the router kernel's logits"
+    exact = (w16.double() @ xn.double()).reshape(-1)
+    ulp = torch.finfo(torch.float16).eps * exact.abs().clamp_min(2.0 ** -14)
+    allow = ulp + 3e-5 * (w16.double().abs() @ xn.double().abs()).reshape(-1)
+    assert bool(((lg.double() - exact).abs() <= allow).all()), "fp16 lm_head logits beyond one fp16 step"
+    assert toks[0] == 103  # prompt[pos + 1] while pos + 1 < prompt_len
+    assert lg[a] == lg[b] and _first_argmax(lg) == a and toks[1] == a
+
+
 def test_warm_entry_points_run_before_capture(dev):
     """The reference's warm() hooks (one real launch, then sync) exist with the
     same signatures and run on the device."""
