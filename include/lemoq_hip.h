@@ -677,9 +677,10 @@ typedef struct LemoqOlmoeStep {
    * embedding row into h with lemoq_gather_rows.) */
   int64_t weight_bits;
   /* fp16 lm_head (vocab, H), or NULL for the W8 lm_head of lm_codes /
-   * lm_scale.  With it the step ends with lemoq_router_logits (final norm +
-   * fp16 GEMV) and lemoq_argmax_advance; the reference keeps the lm_head in
-   * fp16 in every cell but w8a16 with its lm_head switch on. */
+   * lm_scale.  With it the step ends with lemoq_lm_head_argmax_f16 (final
+   * norm + fp16 GEMV writing the argmax partials to am_val / am_idx, then
+   * the pick); the reference keeps the lm_head in fp16 in every cell but
+   * w8a16 with its lm_head switch on. */
   const uint16_t* lm_f16;
 } LemoqOlmoeStep;
 
